@@ -1,0 +1,37 @@
+"""axiom-compute_amd: MI355X (gfx950) Q4_0 / Q4_K_M dequant-matvec path.
+
+The package directory name contains a hyphen, so it is loaded by path; see
+`load()` in __graft_entry__.py and tests/conftest.py.  Everything here calls
+into libaxh.so (hand-written HIP kernels + C ABI runtime).
+"""
+from . import axh  # noqa: F401
+from .axh import (  # noqa: F401
+    BindingPlan,
+    DeviceBuffer,
+    DispatchError,
+    DispatchRequest,
+    HipContext,
+    HipContextOptions,
+    KernelHandle,
+    Variant,
+    builtin_code_object,
+    compiled_variants,
+    load_library,
+    validate_request,
+)
+
+__all__ = [
+    "axh",
+    "BindingPlan",
+    "DeviceBuffer",
+    "DispatchError",
+    "DispatchRequest",
+    "HipContext",
+    "HipContextOptions",
+    "KernelHandle",
+    "Variant",
+    "builtin_code_object",
+    "compiled_variants",
+    "load_library",
+    "validate_request",
+]

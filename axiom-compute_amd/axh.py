@@ -1,0 +1,481 @@
+"""Python mirror of the reference runtime surface over the axh C ABI.
+
+Names follow crates/axc-runtime of rudybear/axiom-compute:
+  VulkanContext::new / new_with_options  -> HipContext.new / new_with_options
+  VulkanContextOptions                   -> HipContextOptions
+  prepare_kernel -> KernelHandle         -> HipContext.prepare_kernel
+  dispatch_handle                        -> HipContext.dispatch_handle
+  dispatch(DispatchRequest)              -> HipContext.dispatch
+  DispatchError (25 variants)            -> DispatchError with .variant
+The Q4 hot path (resident device buffers, asynchronous launches) is exposed as
+HipContext.q4k_matvec / q4_0_matvec / q4k_dequant / q4_0_dequant.
+
+The product path is the HIP library libaxh.so next to this file: importing
+this module fails loudly when it has not been built; there is no fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+from pathlib import Path
+from typing import Iterable, Optional, Sequence
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = _HERE / "libaxh.so"
+HEADER_PATH = _HERE.parent / "include" / "axh.h"
+
+# status code -> reference DispatchError variant name (error.rs:27-195)
+VARIANTS = {
+    1: "VulkanEntryFailed",
+    2: "NoVulkanInstance",
+    3: "NoSupportedDevice",
+    4: "NoComputeQueue",
+    5: "DeviceCreationFailed",
+    6: "ShaderModuleCreationFailed",
+    7: "DescriptorSetLayoutFailed",
+    8: "DescriptorPoolFailed",
+    9: "PipelineLayoutFailed",
+    10: "PipelineCreationFailed",
+    11: "BufferAllocationFailed",
+    12: "MemoryMapFailed",
+    13: "NoCompatibleMemoryType",
+    14: "CommandBufferRecordFailed",
+    15: "QueueSubmitFailed",
+    16: "FenceTimeout",
+    17: "ReadbackFailed",
+    18: "BindingCountMismatch",
+    19: "PushConstantSizeMismatch",
+    20: "WorkgroupCountExceedsDeviceLimit",
+    21: "MetadataIoError",
+    22: "MetadataParseError",
+    23: "MetadataSchemaMismatch",
+    24: "PipelineCacheLoadFailed",
+    25: "StagingCopyFailed",
+    100: "InvalidArgument",
+}
+
+ACCESS_READ_ONLY, ACCESS_WRITE_ONLY, ACCESS_READ_WRITE = 0, 1, 2
+
+
+class DispatchError(RuntimeError):
+    """A non-zero axh_status; `.variant` is the reference variant name."""
+
+    def __init__(self, status: int, message: str):
+        self.status = int(status)
+        self.variant = VARIANTS.get(self.status, "Unknown")
+        super().__init__(f"{self.variant}: {message}")
+
+
+class _Options(ctypes.Structure):
+    _fields_ = [
+        ("code_object_cache_dir", ctypes.c_char_p),
+        ("device_index", ctypes.c_int32),
+        ("fence_timeout_ms", ctypes.c_uint64),
+    ]
+
+
+class _Plan(ctypes.Structure):
+    _fields_ = [
+        ("n_buffers", ctypes.c_uint32),
+        ("access", ctypes.POINTER(ctypes.c_uint8)),
+        ("push_constant_total_bytes", ctypes.c_uint32),
+        ("workgroup_size", ctypes.c_uint32 * 3),
+        ("dynamic_lds_bytes", ctypes.c_uint32),
+    ]
+
+
+class _Variant(ctypes.Structure):
+    _fields_ = [
+        ("rows_per_wave", ctypes.c_uint32),
+        ("waves_per_workgroup", ctypes.c_uint32),
+        ("prefetch", ctypes.c_uint32),
+    ]
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
+    """Load libaxh.so (raises ImportError if it has not been built)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise ImportError(f"{p} is missing: run __graft_entry__.build() (HIP path not built)")
+    lib = ctypes.CDLL(str(p))
+    c = ctypes
+    vp, sz, u32, u64, st = c.c_void_p, c.c_size_t, c.c_uint32, c.c_uint64, c.c_int
+    sigs = {
+        "axh_last_error": (c.c_char_p, []),
+        "axh_status_name": (c.c_char_p, [c.c_int]),
+        "axh_context_create": (st, [c.POINTER(_Options), c.POINTER(vp)]),
+        "axh_context_destroy": (None, [vp]),
+        "axh_context_device_name": (c.c_char_p, [vp]),
+        "axh_context_stream": (vp, [vp]),
+        "axh_context_max_workgroup_count": (None, [vp, c.POINTER(u32)]),
+        "axh_prepare_kernel": (st, [vp, vp, sz, c.POINTER(_Plan), u32, c.c_char_p, c.POINTER(vp)]),
+        "axh_kernel_retain": (None, [vp]),
+        "axh_kernel_release": (None, [vp]),
+        "axh_kernel_cache_key": (u64, [vp]),
+        "axh_kernel_pool_bytes": (u64, [vp, u32]),
+        "axh_dispatch_handle": (st, [vp, vp, c.POINTER(u32), c.POINTER(vp), c.POINTER(sz), sz,
+                                     c.POINTER(sz), sz, c.POINTER(vp), vp, sz]),
+        "axh_dispatch": (st, [vp, vp, sz, c.POINTER(_Plan), c.POINTER(u32), c.POINTER(vp),
+                              c.POINTER(sz), sz, c.POINTER(sz), sz, c.POINTER(vp), vp, sz,
+                              c.c_char_p]),
+        "axh_validate_request": (st, [c.POINTER(_Plan), c.POINTER(u32), sz, sz, sz,
+                                      c.POINTER(u32)]),
+        "axh_buffer_alloc": (st, [vp, sz, c.POINTER(vp)]),
+        "axh_buffer_free": (st, [vp, vp]),
+        "axh_upload": (st, [vp, vp, vp, sz]),
+        "axh_download": (st, [vp, vp, vp, sz]),
+        "axh_launch": (st, [vp, vp, c.POINTER(u32), c.POINTER(vp), sz, vp, sz, vp]),
+        "axh_synchronize": (st, [vp, vp]),
+        "axh_q4k_matvec": (st, [vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
+        "axh_q4_0_matvec": (st, [vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
+        "axh_q4k_dequant": (st, [vp, vp, vp, u64, vp]),
+        "axh_q4_0_dequant": (st, [vp, vp, vp, u64, vp]),
+        "axh_f16_widen": (st, [vp, vp, vp, u64, vp]),
+        "axh_q4k_matvec_variant_count": (u32, []),
+        "axh_q4k_matvec_variant_at": (st, [u32, c.POINTER(_Variant)]),
+        "axh_q4_0_matvec_variant_count": (u32, []),
+        "axh_q4_0_matvec_variant_at": (st, [u32, c.POINTER(_Variant)]),
+        "axh_builtin_code_object": (vp, [c.POINTER(sz)]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        msg = load_library().axh_last_error().decode(errors="replace")
+        raise DispatchError(status, msg)
+
+
+def status_name(status: int) -> str:
+    return load_library().axh_status_name(status).decode()
+
+
+def builtin_code_object() -> bytes:
+    """The embedded gfx950 code object holding every kernel of the library."""
+    lib = load_library()
+    n = ctypes.c_size_t()
+    p = lib.axh_builtin_code_object(ctypes.byref(n))
+    return ctypes.string_at(p, n.value)
+
+
+@dataclass
+class Variant:
+    """Strategy holes of the matvec kernels (0 = default)."""
+
+    rows_per_wave: int = 0
+    waves_per_workgroup: int = 0
+    prefetch: int = 0
+
+    def _c(self) -> _Variant:
+        return _Variant(self.rows_per_wave, self.waves_per_workgroup, self.prefetch)
+
+
+def compiled_variants(kind: str = "q4k") -> list[Variant]:
+    lib = load_library()
+    count = lib.axh_q4k_matvec_variant_count if kind == "q4k" else lib.axh_q4_0_matvec_variant_count
+    at = lib.axh_q4k_matvec_variant_at if kind == "q4k" else lib.axh_q4_0_matvec_variant_at
+    out = []
+    for i in range(count()):
+        v = _Variant()
+        _check(at(i, ctypes.byref(v)))
+        out.append(Variant(v.rows_per_wave, v.waves_per_workgroup, v.prefetch))
+    return out
+
+
+@dataclass
+class BindingPlan:
+    """ParamBindingPlan (crates/axc-hir/src/param.rs:119-126) + launch facts."""
+
+    buffers: Sequence[int]  # ACCESS_* per binding, in binding order
+    push_constant_total_bytes: int
+    workgroup_size: tuple = (64, 1, 1)
+    dynamic_lds_bytes: int = 0
+    _keep: list = field(default_factory=list, repr=False)
+
+    def _c(self) -> _Plan:
+        arr = (ctypes.c_uint8 * max(1, len(self.buffers)))(*self.buffers)
+        self._keep = [arr]
+        return _Plan(len(self.buffers), ctypes.cast(arr, ctypes.POINTER(ctypes.c_uint8)),
+                     self.push_constant_total_bytes,
+                     (ctypes.c_uint32 * 3)(*self.workgroup_size), self.dynamic_lds_bytes)
+
+
+def validate_request(plan: BindingPlan, workgroups, n_inputs: int, n_outputs: int,
+                     push_constant_bytes: int, max_workgroup_count=(0xFFFFFFFF,) * 3) -> None:
+    """Pure request validation (dispatch.rs:56-95); raises DispatchError."""
+    lib = load_library()
+    cp = plan._c()
+    wg = (ctypes.c_uint32 * 3)(*workgroups)
+    mx = (ctypes.c_uint32 * 3)(*max_workgroup_count)
+    _check(lib.axh_validate_request(ctypes.byref(cp), wg, n_inputs, n_outputs,
+                                    push_constant_bytes, mx))
+
+
+@dataclass
+class HipContextOptions:
+    """VulkanContextOptions (context.rs:76-109)."""
+
+    code_object_cache_dir: Optional[str] = None
+    physical_device_index: int = -1
+    fence_timeout_ms: int = 0
+
+
+@dataclass
+class DispatchRequest:
+    """DispatchRequest (dispatch.rs:33-50) with a code object in place of SPIR-V."""
+
+    code_object: bytes
+    binding_plan: BindingPlan
+    workgroups: tuple
+    inputs: Sequence[bytes]
+    output_sizes: Sequence[int]
+    push_constants: bytes
+    entry_point: str
+
+
+def _ptr(obj) -> int:
+    """Device address of a DeviceBuffer, a torch tensor or a raw int."""
+    if obj is None:
+        return 0
+    if isinstance(obj, int):
+        return obj
+    if hasattr(obj, "ptr"):
+        return int(obj.ptr)
+    if hasattr(obj, "data_ptr"):
+        return int(obj.data_ptr())
+    raise TypeError(f"not a device pointer: {type(obj)!r}")
+
+
+def _stream(s) -> Optional[int]:
+    if s is None:
+        return None
+    if isinstance(s, int):
+        return s
+    if hasattr(s, "cuda_stream"):
+        return int(s.cuda_stream)
+    raise TypeError(f"not a stream: {type(s)!r}")
+
+
+class KernelHandle:
+    """Reference-counted prepared kernel (KernelHandle, kernel_handle.rs:44-51)."""
+
+    def __init__(self, lib, raw: int):
+        self._lib = lib
+        self._raw = raw
+
+    @property
+    def raw(self) -> int:
+        return self._raw
+
+    def clone(self) -> "KernelHandle":
+        self._lib.axh_kernel_retain(self._raw)
+        return KernelHandle(self._lib, self._raw)
+
+    @property
+    def cache_key(self) -> int:
+        return int(self._lib.axh_kernel_cache_key(self._raw))
+
+    def pool_bytes(self, binding: int) -> int:
+        return int(self._lib.axh_kernel_pool_bytes(self._raw, binding))
+
+    def release(self) -> None:
+        if self._raw:
+            self._lib.axh_kernel_release(self._raw)
+            self._raw = 0
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+
+class DeviceBuffer:
+    """Device allocation owned by a context (freed on close/__del__)."""
+
+    def __init__(self, ctx: "HipContext", nbytes: int):
+        self._ctx = ctx
+        self.nbytes = int(nbytes)
+        p = ctypes.c_void_p()
+        _check(ctx._lib.axh_buffer_alloc(ctx._raw, self.nbytes, ctypes.byref(p)))
+        self.ptr = int(p.value)
+
+    def close(self) -> None:
+        if self.ptr and self._ctx._raw:
+            self._ctx._lib.axh_buffer_free(self._ctx._raw, self.ptr)
+        self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class HipContext:
+    """VulkanContext counterpart: one gfx950 device, one stream."""
+
+    def __init__(self, options: Optional[HipContextOptions] = None):
+        self._lib = load_library()
+        o = options or HipContextOptions()
+        co = _Options(o.code_object_cache_dir.encode() if o.code_object_cache_dir else None,
+                      o.physical_device_index, o.fence_timeout_ms)
+        raw = ctypes.c_void_p()
+        _check(self._lib.axh_context_create(ctypes.byref(co), ctypes.byref(raw)))
+        self._raw = int(raw.value)
+
+    @classmethod
+    def new(cls) -> "HipContext":
+        return cls(None)
+
+    @classmethod
+    def new_with_options(cls, options: HipContextOptions) -> "HipContext":
+        return cls(options)
+
+    @property
+    def raw(self) -> int:
+        return self._raw
+
+    @property
+    def device_name(self) -> str:
+        return self._lib.axh_context_device_name(self._raw).decode()
+
+    @property
+    def stream(self) -> int:
+        return int(self._lib.axh_context_stream(self._raw) or 0)
+
+    @property
+    def max_workgroup_count(self) -> tuple:
+        out = (ctypes.c_uint32 * 3)()
+        self._lib.axh_context_max_workgroup_count(self._raw, out)
+        return tuple(out)
+
+    def close(self) -> None:
+        if self._raw:
+            self._lib.axh_context_destroy(self._raw)
+            self._raw = 0
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- kernels -----------------------------------------------------------
+    def prepare_kernel(self, code_object: bytes, plan: BindingPlan, push_constant_bytes: int,
+                       entry: str) -> KernelHandle:
+        cp = plan._c()
+        buf = ctypes.create_string_buffer(bytes(code_object), len(code_object))
+        raw = ctypes.c_void_p()
+        _check(self._lib.axh_prepare_kernel(self._raw, buf, len(code_object), ctypes.byref(cp),
+                                            push_constant_bytes, entry.encode(),
+                                            ctypes.byref(raw)))
+        return KernelHandle(self._lib, int(raw.value))
+
+    def dispatch_handle(self, handle: KernelHandle, workgroups, inputs: Sequence[bytes],
+                        output_sizes: Sequence[int], push_constants: bytes) -> list:
+        n_in, n_out = len(inputs), len(output_sizes)
+        in_bufs = [bytes(b) for b in inputs]
+        in_ptrs = (ctypes.c_void_p * max(1, n_in))(
+            *[ctypes.cast(ctypes.c_char_p(b), ctypes.c_void_p) if b else None for b in in_bufs])
+        in_sz = (ctypes.c_size_t * max(1, n_in))(*[len(b) for b in in_bufs])
+        outs = [ctypes.create_string_buffer(max(1, int(s))) for s in output_sizes]
+        out_ptrs = (ctypes.c_void_p * max(1, n_out))(*[ctypes.addressof(o) for o in outs])
+        out_sz = (ctypes.c_size_t * max(1, n_out))(*[int(s) for s in output_sizes])
+        pc = bytes(push_constants)
+        pcb = ctypes.create_string_buffer(pc, max(1, len(pc)))
+        wg = (ctypes.c_uint32 * 3)(*workgroups)
+        _check(self._lib.axh_dispatch_handle(self._raw, handle.raw, wg, in_ptrs, in_sz, n_in,
+                                             out_sz, n_out, out_ptrs, pcb, len(pc)))
+        return [o.raw[: int(s)] for o, s in zip(outs, output_sizes)]
+
+    def dispatch(self, req: DispatchRequest) -> list:
+        validate_request(req.binding_plan, req.workgroups, len(req.inputs),
+                         len(req.output_sizes), len(req.push_constants),
+                         self.max_workgroup_count)
+        h = self.prepare_kernel(req.code_object, req.binding_plan,
+                                req.binding_plan.push_constant_total_bytes, req.entry_point)
+        try:
+            return self.dispatch_handle(h, req.workgroups, req.inputs, req.output_sizes,
+                                        req.push_constants)
+        finally:
+            h.release()
+
+    def launch(self, handle: KernelHandle, workgroups, buffers: Iterable, push_constants: bytes,
+               stream=None) -> None:
+        ptrs = [_ptr(b) for b in buffers]
+        arr = (ctypes.c_void_p * max(1, len(ptrs)))(*ptrs)
+        pc = bytes(push_constants)
+        pcb = ctypes.create_string_buffer(pc, max(1, len(pc)))
+        wg = (ctypes.c_uint32 * 3)(*workgroups)
+        _check(self._lib.axh_launch(self._raw, handle.raw, wg, arr, len(ptrs), pcb, len(pc),
+                                    _stream(stream)))
+
+    # ---- resident buffers --------------------------------------------------
+    def alloc(self, nbytes: int) -> DeviceBuffer:
+        return DeviceBuffer(self, nbytes)
+
+    def upload(self, dst, data) -> None:
+        mv = memoryview(data).cast("B")
+        buf = (ctypes.c_char * len(mv)).from_buffer_copy(mv) if mv.readonly else (
+            ctypes.c_char * len(mv)).from_buffer(mv)
+        _check(self._lib.axh_upload(self._raw, _ptr(dst), buf, len(mv)))
+
+    def download(self, src, nbytes: int) -> bytes:
+        out = ctypes.create_string_buffer(max(1, nbytes))
+        _check(self._lib.axh_download(self._raw, out, _ptr(src), nbytes))
+        return out.raw[:nbytes]
+
+    def synchronize(self, stream=None) -> None:
+        _check(self._lib.axh_synchronize(self._raw, _stream(stream)))
+
+    # ---- Q4 operations -----------------------------------------------------
+    def q4k_matvec(self, q, x, y, n_rows: int, sb_per_row: int,
+                   variant: Optional[Variant] = None, stream=None) -> None:
+        v = variant._c() if variant else None
+        _check(self._lib.axh_q4k_matvec(self._raw, _ptr(q), _ptr(x), _ptr(y), n_rows, sb_per_row,
+                                        ctypes.byref(v) if v else None, _stream(stream)))
+
+    def q4_0_matvec(self, q, x, y, n_rows: int, blocks_per_row: int,
+                    variant: Optional[Variant] = None, stream=None) -> None:
+        v = variant._c() if variant else None
+        _check(self._lib.axh_q4_0_matvec(self._raw, _ptr(q), _ptr(x), _ptr(y), n_rows,
+                                         blocks_per_row, ctypes.byref(v) if v else None,
+                                         _stream(stream)))
+
+    def q4k_dequant(self, q, w, n_superblocks: int, stream=None) -> None:
+        _check(self._lib.axh_q4k_dequant(self._raw, _ptr(q), _ptr(w), n_superblocks,
+                                         _stream(stream)))
+
+    def q4_0_dequant(self, q, w, n_blocks: int, stream=None) -> None:
+        _check(self._lib.axh_q4_0_dequant(self._raw, _ptr(q), _ptr(w), n_blocks, _stream(stream)))
+
+    def f16_widen(self, h, f, n: int, stream=None) -> None:
+        _check(self._lib.axh_f16_widen(self._raw, _ptr(h), _ptr(f), n, _stream(stream)))
+
+
+def header_functions(header: Path = HEADER_PATH) -> list[str]:
+    """Names of every function declared in include/axh.h."""
+    import re
+
+    text = header.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(axh_[a-z0-9_]+)\s*\(", text)))

@@ -1,0 +1,90 @@
+"""Build recipe for the gfx950 path (no cmake/ninja needed).
+
+1. csrc/kernels/*.hip -> gfx950 code objects (hipcc, device only, raw ELF)
+2. csrc/runtime/*.cpp + axh_embed.S -> libaxh.so (g++ against libamdhip64),
+   with the code objects embedded so the library is self-contained
+3. oracle/ -> oracle/liboracle.so (test infrastructure, gcc)
+
+Every step runs on a machine without a GPU.  Outputs stay in the source
+tree (libaxh.so next to this file, intermediates in _build/).
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+BUILD = PKG / "_build"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+HIPCC = str(ROCM / "bin" / "hipcc")
+LIB = PKG / "libaxh.so"
+
+# Packed-FP32 instructions stay off (hipcc flag for device code).
+HIP_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+KERNELS = ["q4_matvec"]
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(
+        ln for ln in proc.stdout.splitlines() if "packed-fp32-ops" not in ln
+    )
+    if proc.returncode != 0:
+        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
+
+
+def build_kernels() -> dict[str, Path]:
+    BUILD.mkdir(exist_ok=True)
+    cos = {}
+    for name in KERNELS:
+        src = PKG / "csrc" / "kernels" / f"{name}.hip"
+        out = BUILD / f"{name}.co"
+        _run([HIPCC, *HIP_FLAGS, "--offload-device-only", "--no-gpu-bundle-output",
+              "-I", str(PKG / "csrc" / "kernels"), "-o", str(out), str(src)])
+        cos[name] = out
+    return cos
+
+
+def build_runtime(cos: dict[str, Path]) -> Path:
+    rt = PKG / "csrc" / "runtime"
+    embed_o = BUILD / "axh_embed.o"
+    _run(["gcc", "-c", f'-DAXH_Q4_MATVEC_CO="{cos["q4_matvec"]}"', "-o", str(embed_o),
+          str(rt / "axh_embed.S")])
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([
+        "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
+        "-D__HIP_PLATFORM_AMD__", "-I", str(ROCM / "include"), "-I", str(ROOT / "include"),
+        "-I", str(rt),
+        str(rt / "axh_runtime.cpp"), str(rt / "axh_ops.cpp"), str(embed_o),
+        "-L", str(ROCM / "lib"), "-Wl,-rpath," + str(ROCM / "lib"), "-lamdhip64", "-pthread",
+        "-o", str(tmp),
+    ])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_oracle() -> Path:
+    _run(["make", "-s", "-C", str(ROOT / "oracle")])
+    return ROOT / "oracle" / "liboracle.so"
+
+
+def build_all() -> None:
+    cos = build_kernels()
+    build_runtime(cos)
+    build_oracle()
+
+
+if __name__ == "__main__":
+    build_all()
+    print(f"built {LIB}")
+    sys.exit(0)

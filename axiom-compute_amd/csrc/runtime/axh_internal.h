@@ -1,0 +1,84 @@
+// Internal types shared by the runtime (axh_runtime.cpp) and the Q4
+// operations (axh_ops.cpp).  Not part of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdint>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "axh.h"
+
+namespace axh {
+
+// Records `msg` as this thread's last error and returns `s`.
+axh_status fail(axh_status s, const std::string &msg);
+axh_status ok();
+
+struct LoadedModule {
+  hipModule_t module = nullptr;
+  int refs = 0;
+};
+
+// Device-side state shared by a context and every handle prepared on it, so
+// a handle may outlive the context that made it.
+struct Core {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string name;
+  uint32_t max_wg[3] = {0, 0, 0};
+  uint32_t max_lds = 0;
+  uint64_t fence_timeout_ms = 10000;
+  std::string cache_dir;
+
+  std::mutex staging_mu;
+  void *staging = nullptr; // pinned host memory
+  size_t staging_bytes = 0;
+
+  std::mutex cache_mu; // guards modules and kernels
+  std::unordered_map<uint64_t, LoadedModule> modules;
+  std::unordered_map<uint64_t, axh_kernel *> kernels; // non-owning
+
+  ~Core();
+};
+
+} // namespace axh
+
+struct axh_kernel {
+  std::atomic<int> refs{1};
+  std::shared_ptr<axh::Core> core;
+  uint64_t key = 0;
+  uint64_t module_hash = 0;
+  hipFunction_t fn = nullptr;
+  std::string entry;
+  std::vector<uint8_t> access;
+  uint32_t pc_bytes = 0;
+  uint32_t wg[3] = {1, 1, 1};
+  uint32_t lds = 0;
+  std::mutex mu;              // serialises dispatch_handle on this handle
+  std::vector<void *> pool;   // per-binding device buffers
+  std::vector<size_t> pool_bytes;
+};
+
+struct axh_context {
+  std::shared_ptr<axh::Core> core;
+  std::mutex ops_mu;
+  std::unordered_map<std::string, axh_kernel *> ops; // builtin kernels by entry name
+};
+
+namespace axh {
+// Launch `k` with explicit kernel arguments; `lds` overrides the plan's
+// dynamic LDS when non-zero.
+axh_status launch_raw(axh_kernel *k, const uint32_t grid[3], void *const *buffers, size_t n_buffers,
+                      const void *pc, size_t pc_bytes, uint32_t lds, hipStream_t stream);
+// Builtin kernel by entry name, prepared once per context.
+axh_status builtin_kernel(axh_context *ctx, const char *entry, uint32_t n_buffers,
+                          uint32_t pc_bytes, uint32_t wg_x, axh_kernel **out);
+hipStream_t pick_stream(axh_context *ctx, void *stream);
+uint64_t hash_bytes(const void *data, size_t n, uint64_t seed);
+} // namespace axh

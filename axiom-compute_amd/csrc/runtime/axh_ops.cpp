@@ -1,0 +1,248 @@
+// Q4_0 / Q4_K_M operations over resident device buffers: variant selection
+// (the strategy holes), LDS tile sizing, grid shape and launch of the
+// builtin gfx950 kernels in q4_matvec.hip.
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "axh_internal.h"
+
+// Code object embedded by axh_embed.S (.incbin of the gfx950 ELF).
+extern "C" const unsigned char axh_q4_matvec_co_begin[];
+extern "C" const unsigned char axh_q4_matvec_co_end[];
+
+namespace axh {
+
+namespace {
+
+struct RowsArgs {
+  uint32_t n_rows;
+  uint32_t units_per_row;
+  uint32_t tile_units;
+  uint32_t pad;
+};
+struct CountArgs {
+  uint32_t n_units;
+};
+
+struct MatvecVariant {
+  uint32_t rpw, nw, pf;
+};
+
+// Compiled instantiations of axh_q4k_matvec_r{rpw}_w{nw}_p{pf}; keep in sync
+// with the AXH_Q4K_MATVEC list in q4_matvec.hip.
+constexpr MatvecVariant kQ4kVariants[] = {
+    {1, 4, 2}, {1, 4, 4}, {1, 8, 4}, {1, 8, 8}, {1, 16, 4}, {2, 4, 2}, {2, 4, 4},
+    {2, 8, 2}, {2, 8, 4}, {2, 8, 7}, {4, 4, 2}, {4, 4, 4},  {4, 8, 2},
+};
+// axh_q4_0_matvec_r{rpw}_w{nw} (prefetch is not a hole for Q4_0).
+constexpr MatvecVariant kQ4_0Variants[] = {{1, 1, 1}, {1, 4, 1}, {2, 4, 1}, {4, 4, 1}};
+
+constexpr uint32_t kQ4kMaxTileSb = 128; // 128 * 1088 B = 136 KiB of LDS
+constexpr uint32_t kQ4_0MaxTileB = 1024; // 1024 * 132 B = 132 KiB of LDS
+
+} // namespace
+
+axh_status builtin_kernel(axh_context *ctx, const char *entry, uint32_t n_buffers,
+                          uint32_t pc_bytes, uint32_t wg_x, axh_kernel **out) {
+  std::lock_guard<std::mutex> lk(ctx->ops_mu);
+  auto it = ctx->ops.find(entry);
+  if (it != ctx->ops.end()) {
+    *out = it->second;
+    return AXH_OK;
+  }
+  static const uint8_t kAccess[3] = {AXH_ACCESS_READ_ONLY, AXH_ACCESS_READ_ONLY,
+                                     AXH_ACCESS_READ_WRITE};
+  uint8_t access[3] = {kAccess[0], kAccess[1], kAccess[2]};
+  if (n_buffers == 2) access[1] = AXH_ACCESS_READ_WRITE;
+  axh_binding_plan plan{};
+  plan.n_buffers = n_buffers;
+  plan.access = access;
+  plan.push_constant_total_bytes = pc_bytes;
+  plan.workgroup_size[0] = wg_x;
+  plan.workgroup_size[1] = 1;
+  plan.workgroup_size[2] = 1;
+  plan.dynamic_lds_bytes = 0;
+  size_t n = 0;
+  const void *co = axh_builtin_code_object(&n);
+  axh_kernel *k = nullptr;
+  axh_status s = axh_prepare_kernel(ctx, co, n, &plan, pc_bytes, entry, &k);
+  if (s != AXH_OK) return s;
+  ctx->ops.emplace(entry, k);
+  *out = k;
+  return AXH_OK;
+}
+
+static const MatvecVariant *find_variant(const MatvecVariant *table, size_t n,
+                                         const axh_q4_variant *v, MatvecVariant dflt) {
+  MatvecVariant want = dflt;
+  if (v) {
+    if (v->rows_per_wave) want.rpw = v->rows_per_wave;
+    if (v->waves_per_workgroup) want.nw = v->waves_per_workgroup;
+    if (v->prefetch) want.pf = v->prefetch;
+  }
+  for (size_t i = 0; i < n; ++i)
+    if (table[i].rpw == want.rpw && table[i].nw == want.nw && table[i].pf == want.pf)
+      return &table[i];
+  return nullptr;
+}
+
+// Default strategy per shape (chosen from on-device sweeps; any compiled
+// variant can be forced through axh_q4_variant).
+static MatvecVariant q4k_default(uint32_t n_rows, uint32_t nsb) {
+  (void)nsb;
+  if (n_rows >= 2048) return {2, 8, 4};
+  return {1, 4, 2};
+}
+
+static MatvecVariant q4_0_default(uint32_t n_rows, uint32_t nb) {
+  (void)nb;
+  if (n_rows >= 4096) return {2, 4, 1};
+  return {1, 1, 1};
+}
+
+static bool device_ptr_ok(const void *p) { return p != nullptr; }
+
+} // namespace axh
+
+using namespace axh;
+
+extern "C" {
+
+const void *axh_builtin_code_object(size_t *bytes) {
+  if (bytes) *bytes = (size_t)(axh_q4_matvec_co_end - axh_q4_matvec_co_begin);
+  return axh_q4_matvec_co_begin;
+}
+
+uint32_t axh_q4k_matvec_variant_count(void) {
+  return (uint32_t)(sizeof(kQ4kVariants) / sizeof(kQ4kVariants[0]));
+}
+
+axh_status axh_q4k_matvec_variant_at(uint32_t i, axh_q4_variant *out) {
+  if (!out || i >= axh_q4k_matvec_variant_count())
+    return fail(AXH_ERR_INVALID_ARGUMENT, "variant index out of range");
+  out->rows_per_wave = kQ4kVariants[i].rpw;
+  out->waves_per_workgroup = kQ4kVariants[i].nw;
+  out->prefetch = kQ4kVariants[i].pf;
+  return ok();
+}
+
+uint32_t axh_q4_0_matvec_variant_count(void) {
+  return (uint32_t)(sizeof(kQ4_0Variants) / sizeof(kQ4_0Variants[0]));
+}
+
+axh_status axh_q4_0_matvec_variant_at(uint32_t i, axh_q4_variant *out) {
+  if (!out || i >= axh_q4_0_matvec_variant_count())
+    return fail(AXH_ERR_INVALID_ARGUMENT, "variant index out of range");
+  out->rows_per_wave = kQ4_0Variants[i].rpw;
+  out->waves_per_workgroup = kQ4_0Variants[i].nw;
+  out->prefetch = kQ4_0Variants[i].pf;
+  return ok();
+}
+
+axh_status axh_q4k_matvec(axh_context *ctx, const void *q, const float *x, float *y,
+                          uint32_t n_rows, uint32_t sb_per_row, const axh_q4_variant *variant,
+                          void *stream) {
+  if (!ctx) return fail(AXH_ERR_INVALID_ARGUMENT, "ctx is NULL");
+  if (n_rows == 0) return ok();
+  if (!device_ptr_ok(y) || (sb_per_row && (!device_ptr_ok(q) || !device_ptr_ok(x))))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q, x and y must be device pointers");
+  if ((uint64_t)sb_per_row * 256u > 0xFFFFFFFFull)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "sb_per_row too large");
+  if (((uintptr_t)q & 15u) || ((uintptr_t)x & 15u))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q and x must be 16-byte aligned");
+  const MatvecVariant *v = find_variant(kQ4kVariants, axh_q4k_matvec_variant_count(), variant,
+                                        q4k_default(n_rows, sb_per_row));
+  if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_K matvec variant matches");
+  char name[64];
+  std::snprintf(name, sizeof(name), "axh_q4k_matvec_r%u_w%u_p%u", v->rpw, v->nw, v->pf);
+  axh_kernel *k = nullptr;
+  axh_status s = builtin_kernel(ctx, name, 3, sizeof(RowsArgs), v->nw * 64u, &k);
+  if (s != AXH_OK) return s;
+  uint32_t tile = (sb_per_row + 7u) & ~7u;
+  if (tile == 0) tile = 8;
+  if (tile > kQ4kMaxTileSb) tile = kQ4kMaxTileSb;
+  const uint32_t lds = tile * 1088u;
+  if (lds > ctx->core->max_lds)
+    return fail(AXH_ERR_PIPELINE_LAYOUT, "LDS tile exceeds the device limit");
+  RowsArgs a{n_rows, sb_per_row, tile, 0};
+  const uint32_t rows_per_wg = v->rpw * v->nw;
+  const uint32_t grid[3] = {(n_rows + rows_per_wg - 1) / rows_per_wg, 1, 1};
+  void *bufs[3] = {const_cast<void *>(q), const_cast<float *>(x), y};
+  hipSetDevice(ctx->core->device);
+  s = launch_raw(k, grid, bufs, 3, &a, sizeof(a), lds, pick_stream(ctx, stream));
+  return s == AXH_OK ? ok() : s;
+}
+
+axh_status axh_q4_0_matvec(axh_context *ctx, const void *q, const float *x, float *y,
+                           uint32_t n_rows, uint32_t blocks_per_row,
+                           const axh_q4_variant *variant, void *stream) {
+  if (!ctx) return fail(AXH_ERR_INVALID_ARGUMENT, "ctx is NULL");
+  if (n_rows == 0) return ok();
+  if (!device_ptr_ok(y) || (blocks_per_row && (!device_ptr_ok(q) || !device_ptr_ok(x))))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q, x and y must be device pointers");
+  if ((uint64_t)blocks_per_row * 32u > 0xFFFFFFFFull)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "blocks_per_row too large");
+  if (((uintptr_t)q & 3u) || ((uintptr_t)x & 15u))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q must be 4-byte and x 16-byte aligned");
+  MatvecVariant dflt = q4_0_default(n_rows, blocks_per_row);
+  axh_q4_variant vv{};
+  if (variant) vv = *variant;
+  vv.prefetch = 1;
+  const MatvecVariant *v = find_variant(kQ4_0Variants, axh_q4_0_matvec_variant_count(), &vv, dflt);
+  if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_0 matvec variant matches");
+  char name[64];
+  std::snprintf(name, sizeof(name), "axh_q4_0_matvec_r%u_w%u", v->rpw, v->nw);
+  axh_kernel *k = nullptr;
+  axh_status s = builtin_kernel(ctx, name, 3, sizeof(RowsArgs), v->nw * 64u, &k);
+  if (s != AXH_OK) return s;
+  uint32_t tile = (blocks_per_row + 127u) & ~127u;
+  if (tile == 0) tile = 128;
+  if (tile > kQ4_0MaxTileB) tile = kQ4_0MaxTileB;
+  const uint32_t lds = tile * 132u;
+  RowsArgs a{n_rows, blocks_per_row, tile, 0};
+  const uint32_t rows_per_wg = v->rpw * v->nw;
+  const uint32_t grid[3] = {(n_rows + rows_per_wg - 1) / rows_per_wg, 1, 1};
+  void *bufs[3] = {const_cast<void *>(q), const_cast<float *>(x), y};
+  hipSetDevice(ctx->core->device);
+  s = launch_raw(k, grid, bufs, 3, &a, sizeof(a), lds, pick_stream(ctx, stream));
+  return s == AXH_OK ? ok() : s;
+}
+
+static axh_status count_launch(axh_context *ctx, const char *name, const void *in, void *out,
+                               uint64_t n_threads, uint64_t n_units, void *stream) {
+  if (!ctx) return fail(AXH_ERR_INVALID_ARGUMENT, "ctx is NULL");
+  if (n_units == 0) return ok();
+  if (!in || !out) return fail(AXH_ERR_INVALID_ARGUMENT, "NULL device pointer");
+  if (n_units > 0xFFFFFFFFull || n_threads > (uint64_t)0xFFFFFFFFull * 256ull)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "too many units for one launch");
+  axh_kernel *k = nullptr;
+  axh_status s = builtin_kernel(ctx, name, 2, sizeof(CountArgs), 256, &k);
+  if (s != AXH_OK) return s;
+  CountArgs a{(uint32_t)n_units};
+  const uint32_t grid[3] = {(uint32_t)((n_threads + 255u) / 256u), 1, 1};
+  void *bufs[2] = {const_cast<void *>(in), out};
+  hipSetDevice(ctx->core->device);
+  s = launch_raw(k, grid, bufs, 2, &a, sizeof(a), 0, pick_stream(ctx, stream));
+  return s == AXH_OK ? ok() : s;
+}
+
+axh_status axh_q4k_dequant(axh_context *ctx, const void *q, float *w, uint64_t n_sb, void *stream) {
+  if (n_sb > (1ull << 28)) return fail(AXH_ERR_INVALID_ARGUMENT, "too many superblocks");
+  if (((uintptr_t)q & 15u) || ((uintptr_t)w & 15u))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q and w must be 16-byte aligned");
+  return count_launch(ctx, "axh_q4k_dequant", q, w, n_sb * 8u, n_sb, stream);
+}
+
+axh_status axh_q4_0_dequant(axh_context *ctx, const void *q, float *w, uint64_t n_blocks,
+                            void *stream) {
+  if (((uintptr_t)q & 1u) || ((uintptr_t)w & 3u))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q must be 2-byte and w 4-byte aligned");
+  return count_launch(ctx, "axh_q4_0_dequant", q, w, n_blocks, n_blocks, stream);
+}
+
+axh_status axh_f16_widen(axh_context *ctx, const uint16_t *h, float *f, uint64_t n, void *stream) {
+  return count_launch(ctx, "axh_f16_widen", h, f, n, n, stream);
+}
+
+} // extern "C"

@@ -1,0 +1,197 @@
+/*
+ * axh: C ABI of the MI355X (gfx950) Q4_0 / Q4_K_M dequant-matvec path.
+ *
+ * Drop-in boundary for rudybear/axiom-compute's runtime surface
+ * (crates/axc-runtime).  Plain pointers and sizes only; every call returns an
+ * axh_status and leaves a thread-local message readable with axh_last_error().
+ * Device pointers are HIP device addresses (from axh_buffer_alloc or any other
+ * HIP allocation on the context's device).  `stream` arguments are hipStream_t
+ * values passed as void*; NULL means the context's own stream.
+ */
+#ifndef AXH_H
+#define AXH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* One code per DispatchError variant (crates/axc-runtime/src/error.rs:27-195),
+ * in the reference's order, with the HIP failure each one stands for. */
+typedef enum axh_status {
+    AXH_OK = 0,
+    AXH_ERR_RUNTIME_LOAD = 1,                 /* VulkanEntryFailed: HIP runtime unusable        */
+    AXH_ERR_NO_INSTANCE = 2,                  /* NoVulkanInstance: hipInit failed               */
+    AXH_ERR_NO_SUPPORTED_DEVICE = 3,          /* NoSupportedDevice: no gfx950 device at index   */
+    AXH_ERR_NO_COMPUTE_QUEUE = 4,             /* NoComputeQueue: stream creation failed         */
+    AXH_ERR_DEVICE_CREATION = 5,              /* DeviceCreationFailed: hipSetDevice failed      */
+    AXH_ERR_MODULE_CREATION = 6,              /* ShaderModuleCreationFailed: hipModuleLoadData  */
+    AXH_ERR_DESCRIPTOR_SET_LAYOUT = 7,        /* DescriptorSetLayoutFailed: bad binding plan    */
+    AXH_ERR_DESCRIPTOR_POOL = 8,              /* DescriptorPoolFailed: kernarg assembly         */
+    AXH_ERR_PIPELINE_LAYOUT = 9,              /* PipelineLayoutFailed: plan/pc size disagree    */
+    AXH_ERR_PIPELINE_CREATION = 10,           /* PipelineCreationFailed: entry not in module    */
+    AXH_ERR_BUFFER_ALLOCATION = 11,           /* BufferAllocationFailed: hipMalloc              */
+    AXH_ERR_MEMORY_MAP = 12,                  /* MemoryMapFailed: pinned host allocation        */
+    AXH_ERR_NO_COMPATIBLE_MEMORY_TYPE = 13,   /* NoCompatibleMemoryType                         */
+    AXH_ERR_COMMAND_RECORD = 14,              /* CommandBufferRecordFailed: launch rejected     */
+    AXH_ERR_QUEUE_SUBMIT = 15,                /* QueueSubmitFailed: stream/event error          */
+    AXH_ERR_FENCE_TIMEOUT = 16,               /* FenceTimeout: completion wait timed out        */
+    AXH_ERR_READBACK = 17,                    /* ReadbackFailed: device-to-host copy            */
+    AXH_ERR_BINDING_COUNT_MISMATCH = 18,      /* BindingCountMismatch                           */
+    AXH_ERR_PUSH_CONSTANT_SIZE_MISMATCH = 19, /* PushConstantSizeMismatch                       */
+    AXH_ERR_WORKGROUP_COUNT_EXCEEDS_LIMIT = 20, /* WorkgroupCountExceedsDeviceLimit             */
+    AXH_ERR_METADATA_IO = 21,                 /* MetadataIoError                                */
+    AXH_ERR_METADATA_PARSE = 22,              /* MetadataParseError                             */
+    AXH_ERR_METADATA_SCHEMA_MISMATCH = 23,    /* MetadataSchemaMismatch                         */
+    AXH_ERR_CODE_OBJECT_CACHE_LOAD = 24,      /* PipelineCacheLoadFailed                        */
+    AXH_ERR_STAGING_COPY = 25,                /* StagingCopyFailed: host-to-device copy         */
+    AXH_ERR_INVALID_ARGUMENT = 100            /* no counterpart: null pointer or bad shape      */
+} axh_status;
+
+typedef struct axh_context axh_context;
+typedef struct axh_kernel axh_kernel;
+
+/* Thread-local description of the last failure on this thread ("" if none). */
+const char *axh_last_error(void);
+const char *axh_status_name(int status);
+
+/* ---- context ---------------------------------------------------------------
+ * Replaces VulkanContextOptions / VulkanContext::new_with_options
+ * (crates/axc-runtime/src/context.rs:76-109,175). */
+typedef struct axh_context_options {
+    const char *code_object_cache_dir; /* pipeline_cache_path; NULL = none         */
+    int32_t device_index;              /* physical_device_index; -1 = AXH_DEVICE_INDEX env or 0 */
+    uint64_t fence_timeout_ms;         /* 0 = AXH_FENCE_TIMEOUT_MS env or 10000 (dispatch.rs:26) */
+} axh_context_options;
+
+axh_status axh_context_create(const axh_context_options *opts, axh_context **out);
+/* Handles prepared on the context stay valid after this call
+ * (crates/axc-runtime/tests/kernel_handle_outlives_context.rs:24): the device
+ * state is released with the last handle. */
+void axh_context_destroy(axh_context *ctx);
+const char *axh_context_device_name(const axh_context *ctx);
+void *axh_context_stream(const axh_context *ctx);
+/* Device limit checked before any dispatch (dispatch.rs:85-93). */
+void axh_context_max_workgroup_count(const axh_context *ctx, uint32_t out[3]);
+
+/* ---- kernels ---------------------------------------------------------------
+ * Binding plan: ParamBindingPlan (crates/axc-hir/src/param.rs:119-126) plus
+ * the launch facts a HIP code object needs (KernelMetadata workgroup size,
+ * crates/axc-runtime/src/metadata.rs:45-68).  Kernel arguments are one
+ * pointer per buffer in binding order followed by one push-constant struct
+ * of push_constant_total_bytes passed by value. */
+enum { AXH_ACCESS_READ_ONLY = 0, AXH_ACCESS_WRITE_ONLY = 1, AXH_ACCESS_READ_WRITE = 2 };
+
+typedef struct axh_binding_plan {
+    uint32_t n_buffers;
+    const uint8_t *access;             /* n_buffers AXH_ACCESS_* values */
+    uint32_t push_constant_total_bytes;
+    uint32_t workgroup_size[3];        /* @workgroup(x, y, z) */
+    uint32_t dynamic_lds_bytes;        /* 0 for kernels whose LDS is static */
+} axh_binding_plan;
+
+/* prepare_kernel (context.rs:392-486): code object (HSACO/ELF or offload
+ * bundle for gfx950) + plan + entry -> handle.  Handles are cached per
+ * context by (code-object hash, plan, push-constant size, entry); a second
+ * prepare of the same key returns the cached handle with one more reference. */
+axh_status axh_prepare_kernel(axh_context *ctx, const void *code_object, size_t code_object_bytes,
+                              const axh_binding_plan *plan, uint32_t push_constant_bytes,
+                              const char *entry, axh_kernel **out);
+void axh_kernel_retain(axh_kernel *k);
+void axh_kernel_release(axh_kernel *k);
+uint64_t axh_kernel_cache_key(const axh_kernel *k);
+/* Bytes currently held by the handle's buffer pool for binding i (0 if none). */
+uint64_t axh_kernel_pool_bytes(const axh_kernel *k, uint32_t binding);
+
+/* dispatch_handle (context.rs:498-547): uploads each non-empty input into its
+ * binding's pooled device buffer (pool size round_up_pow2(max(in, out, 4)),
+ * grown only upward: kernel_handle.rs:295-393), launches workgroups, waits
+ * with the fence timeout and copies output_sizes[i] bytes of every binding
+ * into outputs[i] (skipped when output_sizes[i] == 0).  Validation happens
+ * before any device work (dispatch.rs:56-95).  Dispatches on one handle are
+ * serialised; different handles may dispatch concurrently. */
+axh_status axh_dispatch_handle(axh_context *ctx, axh_kernel *k, const uint32_t workgroups[3],
+                               const void *const *inputs, const size_t *input_sizes,
+                               size_t n_inputs, const size_t *output_sizes, size_t n_outputs,
+                               void *const *outputs, const void *push_constants,
+                               size_t push_constant_bytes);
+
+/* Legacy one-shot dispatch (DispatchRequest, dispatch.rs:33-50,109-132):
+ * validate, prepare, dispatch_handle, release. */
+axh_status axh_dispatch(axh_context *ctx, const void *code_object, size_t code_object_bytes,
+                        const axh_binding_plan *plan, const uint32_t workgroups[3],
+                        const void *const *inputs, const size_t *input_sizes, size_t n_inputs,
+                        const size_t *output_sizes, size_t n_outputs, void *const *outputs,
+                        const void *push_constants, size_t push_constant_bytes, const char *entry);
+
+/* Pure request validation (dispatch.rs:56-95), usable without a device. */
+axh_status axh_validate_request(const axh_binding_plan *plan, const uint32_t workgroups[3],
+                                size_t n_inputs, size_t n_outputs, size_t push_constant_bytes,
+                                const uint32_t max_workgroup_count[3]);
+
+/* ---- resident buffers and asynchronous launch ------------------------------
+ * The hot path: buffers stay in HBM between calls; launches are asynchronous
+ * on `stream`.  Uploads/downloads go through the context's pinned staging
+ * buffer with hipMemcpyAsync and return when the copy is complete. */
+axh_status axh_buffer_alloc(axh_context *ctx, size_t bytes, void **device_ptr);
+axh_status axh_buffer_free(axh_context *ctx, void *device_ptr);
+axh_status axh_upload(axh_context *ctx, void *device_dst, const void *host_src, size_t bytes);
+axh_status axh_download(axh_context *ctx, void *host_dst, const void *device_src, size_t bytes);
+axh_status axh_launch(axh_context *ctx, axh_kernel *k, const uint32_t workgroups[3],
+                      void *const *device_buffers, size_t n_buffers, const void *push_constants,
+                      size_t push_constant_bytes, void *stream);
+/* Waits for `stream` with the context's fence timeout (AXH_ERR_FENCE_TIMEOUT). */
+axh_status axh_synchronize(axh_context *ctx, void *stream);
+
+/* ---- Q4 dequant-matvec operations ------------------------------------------
+ * Strategy holes of the matvec kernels (the reference's @strategy surface,
+ * crates/axc-hir/src/hir.rs:62-68): rows_per_wave, waves_per_workgroup and
+ * prefetch (superblock iterations loaded ahead).  Zero fields pick defaults. */
+typedef struct axh_q4_variant {
+    uint32_t rows_per_wave;
+    uint32_t waves_per_workgroup;
+    uint32_t prefetch;
+} axh_q4_variant;
+
+/* y[r] = dot(row r of Q4_K_M matrix q, x) for r < n_rows, where each row is
+ * sb_per_row contiguous 144-byte superblocks and x holds sb_per_row*256 f32.
+ * Replaces prepare_kernel + dispatch_handle of examples/q4km_dequant_matvec.axc
+ * (its single output is the n_rows = 1 case), compared against
+ * q4km_dequant_matvec_cpu (crates/axc-driver/tests/common_helpers.rs:411-461). */
+axh_status axh_q4k_matvec(axh_context *ctx, const void *q, const float *x, float *y,
+                          uint32_t n_rows, uint32_t sb_per_row, const axh_q4_variant *variant,
+                          void *stream);
+/* Q4_0 counterpart: rows of blocks_per_row 18-byte blocks; x holds
+ * blocks_per_row*32 f32.  Replaces examples/q4_0_dequant_matvec.axc; compared
+ * against q4_0_dequant_matvec_cpu (crates/axc-driver/benches/common.rs:212-259). */
+axh_status axh_q4_0_matvec(axh_context *ctx, const void *q, const float *x, float *y,
+                           uint32_t n_rows, uint32_t blocks_per_row,
+                           const axh_q4_variant *variant, void *stream);
+/* Decode-only kernels, bit-exact with the reference's CPU dequantisation
+ * (common_helpers.rs:437-454; common.rs:229-253): w receives 256 (Q4_K) or
+ * 32 (Q4_0) f32 per unit in the reference's element order. */
+axh_status axh_q4k_dequant(axh_context *ctx, const void *q, float *w, uint64_t n_superblocks,
+                           void *stream);
+axh_status axh_q4_0_dequant(axh_context *ctx, const void *q, float *w, uint64_t n_blocks,
+                            void *stream);
+/* IEEE binary16 -> binary32 widening of n raw patterns (the ptr_read_u16_zext +
+ * f16_bits_to_f32 builtins, crates/axc-codegen/src/q4_0.rs:86-171). */
+axh_status axh_f16_widen(axh_context *ctx, const uint16_t *h, float *f, uint64_t n, void *stream);
+
+/* Number of compiled matvec variants and the i-th one (for the autotuner). */
+uint32_t axh_q4k_matvec_variant_count(void);
+axh_status axh_q4k_matvec_variant_at(uint32_t i, axh_q4_variant *out);
+uint32_t axh_q4_0_matvec_variant_count(void);
+axh_status axh_q4_0_matvec_variant_at(uint32_t i, axh_q4_variant *out);
+
+/* The built-in code object holding every kernel above, for callers that drive
+ * the generic prepare/dispatch API (e.g. the reference-contract kernels
+ * "q4km_dequant_matvec" and "q4_0_dequant_matvec"). */
+const void *axh_builtin_code_object(size_t *bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* AXH_H */

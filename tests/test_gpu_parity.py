@@ -1,0 +1,272 @@
+"""GPU parity of the HIP path against the CPU oracle (marked `gpu`).
+
+Bars: dequantised weights and the f16 decode bit-exact; matvec outputs under
+the row-wise tolerance criterion of oracle.matvec_tolerance_report (1e-3
+relative per well-conditioned row, condition-scaled bound on cancelling
+rows, 1e-3 norm-wise) plus the reference's own single-output check
+(rel < 1e-3, compile_q4km_dequant_matvec.rs:946-956).
+"""
+from __future__ import annotations
+
+import struct
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-3  # @equiv_fp_tol(1e-3), DESIGN.md:508-513 of the reference
+
+
+def _say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _to_dev(ctx, arr: np.ndarray):
+    b = ctx.alloc(arr.nbytes)
+    ctx.upload(b, arr)
+    return b
+
+
+def _run_q4k(ctx, q, x, rows, sb, variant=None):
+    dq, dx, dy = _to_dev(ctx, q), _to_dev(ctx, x), ctx.alloc(rows * 4)
+    ctx.q4k_matvec(dq, dx, dy, rows, sb, variant)
+    ctx.synchronize()
+    y = np.frombuffer(ctx.download(dy, rows * 4), dtype=np.float32).copy()
+    for b in (dq, dx, dy):
+        b.close()
+    return y
+
+
+def _run_q4_0(ctx, q, x, rows, nb, variant=None):
+    dq, dx, dy = _to_dev(ctx, q), _to_dev(ctx, x), ctx.alloc(rows * 4)
+    ctx.q4_0_matvec(dq, dx, dy, rows, nb, variant)
+    ctx.synchronize()
+    y = np.frombuffer(ctx.download(dy, rows * 4), dtype=np.float32).copy()
+    for b in (dq, dx, dy):
+        b.close()
+    return y
+
+
+def _check_q4k(y, q, x, rows, sb, what):
+    ref = O.q4k_matvec(q, x, rows, sb)
+    yf, absdot = O.q4k_matvec_f64(q, x, rows, sb)
+    rep = O.matvec_tolerance_report(y, ref, yf, absdot, sb * 256, REL_TOL)
+    _say(f"{what}: {rep}")
+    assert rep["ok"], f"{what}: {rep}"
+
+
+def _check_q4_0(y, q, x, rows, nb, what):
+    ref = O.q4_0_matvec(q, x, rows, nb)
+    yf, absdot = O.q4_0_matvec_f64(q, x, rows, nb)
+    rep = O.matvec_tolerance_report(y, ref, yf, absdot, nb * 32, REL_TOL)
+    _say(f"{what}: {rep}")
+    assert rep["ok"], f"{what}: {rep}"
+
+
+# ---- a3: f16 decode --------------------------------------------------------
+def test_f16_widen_exhaustive_matches_oracle(ctx):
+    _say("f16 widen: all 65536 patterns")
+    h = np.arange(65536, dtype=np.uint16)
+    dh, df = _to_dev(ctx, h), ctx.alloc(65536 * 4)
+    ctx.f16_widen(dh, df, 65536)
+    ctx.synchronize()
+    gpu = np.frombuffer(ctx.download(df, 65536 * 4), dtype=np.uint32)
+    ref = h.view(np.float16).astype(np.float32).view(np.uint32)
+    nan = np.isnan(h.view(np.float16))
+    assert np.array_equal(gpu[~nan], ref[~nan])
+    assert np.isnan(gpu[nan].view(np.float32)).all()
+    dh.close()
+    df.close()
+
+
+# ---- a1/a4/a5: bit-exact dequantisation -------------------------------------
+@pytest.mark.parametrize("rows,sb", [(1, 128), (4096, 16), (4096, 56)])
+def test_q4k_dequant_bit_exact(ctx, rows, sb):
+    _say(f"q4k dequant bit-exact {rows}x{sb * 256}")
+    n = rows * sb
+    q = O.gen_q4k_weights(11 + rows, n)
+    dq, dw = _to_dev(ctx, q), ctx.alloc(n * 256 * 4)
+    ctx.q4k_dequant(dq, dw, n)
+    ctx.synchronize()
+    gpu = np.frombuffer(ctx.download(dw, n * 256 * 4), dtype=np.uint32)
+    ref = O.q4k_dequant(q, n).view(np.uint32)
+    bad = np.flatnonzero(gpu != ref)
+    assert bad.size == 0, f"{bad.size} mismatching weights, first at {bad[:5]}"
+    dq.close()
+    dw.close()
+
+
+def test_q4k_dequant_bit_exact_lcg_fixture(ctx):
+    """Reference generator data (d in [0.1, 2], dmin in [0, 0.5])."""
+    q, _ = O.generate_q4km_test_data(512, 0xCAFEBABE)
+    dq, dw = _to_dev(ctx, q), ctx.alloc(512 * 256 * 4)
+    ctx.q4k_dequant(dq, dw, 512)
+    ctx.synchronize()
+    gpu = np.frombuffer(ctx.download(dw, 512 * 256 * 4), dtype=np.uint32)
+    assert np.array_equal(gpu, O.q4k_dequant(q, 512).view(np.uint32))
+    dq.close()
+    dw.close()
+
+
+@pytest.mark.parametrize("rows,nb", [(256, 128), (7, 129)])
+def test_q4_0_dequant_bit_exact(ctx, rows, nb):
+    _say(f"q4_0 dequant bit-exact {rows}x{nb * 32}")
+    n = rows * nb
+    q = O.gen_q4_0_weights(5 + rows, n)
+    dq, dw = _to_dev(ctx, q), ctx.alloc(n * 32 * 4)
+    ctx.q4_0_dequant(dq, dw, n)
+    ctx.synchronize()
+    gpu = np.frombuffer(ctx.download(dw, n * 32 * 4), dtype=np.uint32)
+    assert np.array_equal(gpu, O.q4_0_dequant(q, n).view(np.uint32))
+    dq.close()
+    dw.close()
+
+
+# ---- a6: Q4_K matvec at the BASELINE configurations ---------------------------
+@pytest.mark.parametrize(
+    "rows,sb,sigma",
+    [
+        (1, 128, 1.0),      # C2: 1 x 32768
+        (4096, 16, 1.0),    # C3: 4096 x 4096
+        (14336, 16, 1.0),   # C3: 14336 x 4096
+        (4096, 56, 0.5),    # C4: 4096 x 14336 (north star)
+    ],
+)
+def test_q4k_matvec_baseline_configs(ctx, rows, sb, sigma):
+    _say(f"q4k matvec {rows}x{sb * 256}")
+    q = O.gen_q4k_weights(1000 + rows + sb, rows * sb)
+    x = O.gen_normal_f32(2000 + sb, sb * 256, sigma)
+    y = _run_q4k(ctx, q, x, rows, sb)
+    _check_q4k(y, q, x, rows, sb, f"q4k {rows}x{sb * 256}")
+
+
+def test_q4k_matvec_output_head(ctx):
+    """C4 output head 128256 x 4096 (295 MB of weights)."""
+    rows, sb = 128256, 16
+    _say(f"q4k matvec head {rows}x{sb * 256}")
+    q = O.gen_q4k_weights(77, rows * sb)
+    x = O.gen_normal_f32(78, sb * 256, 0.5)
+    y = _run_q4k(ctx, q, x, rows, sb)
+    _check_q4k(y, q, x, rows, sb, "q4k head")
+
+
+def test_q4k_matvec_every_variant(ctx, axc):
+    rows, sb = 1000, 57  # ragged: rows and superblocks not multiples of the tiles
+    q = O.gen_q4k_weights(3, rows * sb)
+    x = O.gen_normal_f32(4, sb * 256)
+    for v in axc.compiled_variants("q4k"):
+        _say(f"q4k variant {v}")
+        y = _run_q4k(ctx, q, x, rows, sb, v)
+        _check_q4k(y, q, x, rows, sb, f"variant {v}")
+
+
+@pytest.mark.parametrize("rows,sb", [(1, 1), (3, 7), (5, 8), (9, 9), (65, 129), (2, 160), (33, 300)])
+def test_q4k_matvec_edge_shapes(ctx, rows, sb):
+    """Single superblock, ragged tails, and rows longer than one LDS tile."""
+    _say(f"q4k edge {rows}x{sb}")
+    q = O.gen_q4k_weights(rows * 31 + sb, rows * sb)
+    x = O.gen_normal_f32(rows + 5 * sb, sb * 256)
+    y = _run_q4k(ctx, q, x, rows, sb)
+    _check_q4k(y, q, x, rows, sb, f"q4k edge {rows}x{sb}")
+
+
+def test_q4k_matvec_zero_superblocks_gives_positive_zero(ctx):
+    """AT-1323: n_superblocks = 0 -> +0.0 (compile_q4km_dequant_matvec.rs:850-856)."""
+    dq, dx, dy = ctx.alloc(16), ctx.alloc(16), ctx.alloc(4 * 4)
+    ctx.upload(dy, np.full(4, 7.0, dtype=np.float32))
+    ctx.q4k_matvec(dq, dx, dy, 4, 0)
+    ctx.synchronize()
+    y = np.frombuffer(ctx.download(dy, 16), dtype=np.uint32)
+    assert (y == 0).all()
+
+
+def test_q4k_matvec_lcg_fixture_single_row(ctx):
+    """AT-1324/1331 data: generate_q4km_test_data(128, 0xDEADBEEF)."""
+    q, x = O.generate_q4km_test_data(128, 0xDEADBEEF)
+    y = _run_q4k(ctx, q, x, 1, 128)
+    cpu = O.q4k_dot(q, x, 128)
+    assert O.reference_rel_err(y[0], cpu) < REL_TOL
+
+
+# ---- a2: Q4_0 matvec ---------------------------------------------------------
+def test_q4_0_matvec_c1(ctx):
+    rows, nb = 256, 128
+    _say("q4_0 matvec C1 256x4096")
+    q = O.gen_q4_0_weights(42, rows * nb)
+    x = O.gen_normal_f32(43, nb * 32)
+    y = _run_q4_0(ctx, q, x, rows, nb)
+    _check_q4_0(y, q, x, rows, nb, "q4_0 C1")
+
+
+def test_q4_0_matvec_every_variant(ctx, axc):
+    rows, nb = 300, 130
+    q = O.gen_q4_0_weights(9, rows * nb)
+    x = O.gen_normal_f32(10, nb * 32)
+    for v in axc.compiled_variants("q4_0"):
+        _say(f"q4_0 variant {v}")
+        y = _run_q4_0(ctx, q, x, rows, nb, v)
+        _check_q4_0(y, q, x, rows, nb, f"q4_0 variant {v}")
+
+
+@pytest.mark.parametrize("rows,nb", [(1, 1), (2, 3), (3, 127), (4, 129), (5, 1025), (17, 2048)])
+def test_q4_0_matvec_edge_shapes(ctx, rows, nb):
+    _say(f"q4_0 edge {rows}x{nb}")
+    q = O.gen_q4_0_weights(rows * 13 + nb, rows * nb)
+    x = O.gen_normal_f32(rows + nb, nb * 32)
+    y = _run_q4_0(ctx, q, x, rows, nb)
+    _check_q4_0(y, q, x, rows, nb, f"q4_0 edge {rows}x{nb}")
+
+
+# ---- the reference kernel contract through prepare_kernel / dispatch_handle --
+def _plan(axc, pc):
+    return axc.BindingPlan(
+        buffers=[axc.axh.ACCESS_READ_ONLY, axc.axh.ACCESS_READ_ONLY, axc.axh.ACCESS_READ_WRITE],
+        push_constant_total_bytes=pc, workgroup_size=(64, 1, 1))
+
+
+def test_at_1324_q4km_dispatch_handle_matches_cpu_within_1e_3(ctx, axc):
+    """compile_q4km_dequant_matvec.rs:867-957 on the HIP runtime."""
+    n = 128
+    q, x = O.generate_q4km_test_data(n, 0xDEADBEEF)
+    cpu = O.q4k_dot(q, x, n)
+    co = axc.builtin_code_object()
+    h = ctx.prepare_kernel(co, _plan(axc, 4), 4, "q4km_dequant_matvec")
+    out = ctx.dispatch_handle(h, (1, 1, 1), [q.tobytes(), x.tobytes(), bytes(4)],
+                              [q.nbytes, x.nbytes, 4], struct.pack("<I", n))
+    gpu = struct.unpack("<f", out[2][:4])[0]
+    assert out[0] == q.tobytes() and out[1] == x.tobytes()
+    assert O.reference_rel_err(gpu, cpu) < REL_TOL, (gpu, float(cpu))
+    h.release()
+
+
+def test_at_918_q4_0_dispatch_matches_cpu_within_1e_3(ctx, axc):
+    """compile_q4_0_dequant_matvec.rs:437-537: 128 blocks, one output."""
+    nb = 128
+    q = O.gen_q4_0_weights(42, nb)
+    x = O.gen_normal_f32(42, nb * 32)
+    cpu = O.q4_0_dot(q, x, nb)
+    req = axc.DispatchRequest(
+        code_object=axc.builtin_code_object(), binding_plan=_plan(axc, 4), workgroups=(1, 1, 1),
+        inputs=[q.tobytes(), x.tobytes(), bytes(4)], output_sizes=[0, 0, 4],
+        push_constants=struct.pack("<I", nb), entry_point="q4_0_dequant_matvec")
+    out = ctx.dispatch(req)
+    assert out[0] == b"" and out[1] == b""
+    gpu = struct.unpack("<f", out[2])[0]
+    assert O.reference_rel_err(gpu, cpu) < REL_TOL, (gpu, float(cpu))
+
+
+@pytest.mark.parametrize("n", [1, 16, 17, 512])
+def test_q4km_reference_kernel_many_superblocks(ctx, axc, n):
+    """More superblocks than one 16-superblock LDS tile (512 = dispatch_q4km_512)."""
+    q, x = O.generate_q4km_test_data(n, 0xCAFEBABE)
+    cpu = O.q4k_dot(q, x, n)
+    h = ctx.prepare_kernel(axc.builtin_code_object(), _plan(axc, 4), 4, "q4km_dequant_matvec")
+    out = ctx.dispatch_handle(h, (1, 1, 1), [q.tobytes(), x.tobytes(), b""], [0, 0, 4],
+                              struct.pack("<I", n))
+    gpu = struct.unpack("<f", out[2])[0]
+    assert O.reference_rel_err(gpu, cpu) < REL_TOL, (n, gpu, float(cpu))
