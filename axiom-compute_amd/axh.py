@@ -89,6 +89,7 @@ class _Variant(ctypes.Structure):
         ("rows_per_wave", ctypes.c_uint32),
         ("waves_per_workgroup", ctypes.c_uint32),
         ("prefetch", ctypes.c_uint32),
+        ("nontemporal", ctypes.c_uint32),
     ]
 
 
@@ -177,9 +178,11 @@ class Variant:
     rows_per_wave: int = 0
     waves_per_workgroup: int = 0
     prefetch: int = 0
+    nontemporal: int = 0
 
     def _c(self) -> _Variant:
-        return _Variant(self.rows_per_wave, self.waves_per_workgroup, self.prefetch)
+        return _Variant(self.rows_per_wave, self.waves_per_workgroup, self.prefetch,
+                        self.nontemporal)
 
 
 def compiled_variants(kind: str = "q4k") -> list[Variant]:
@@ -190,7 +193,7 @@ def compiled_variants(kind: str = "q4k") -> list[Variant]:
     for i in range(count()):
         v = _Variant()
         _check(at(i, ctypes.byref(v)))
-        out.append(Variant(v.rows_per_wave, v.waves_per_workgroup, v.prefetch))
+        out.append(Variant(v.rows_per_wave, v.waves_per_workgroup, v.prefetch, v.nontemporal))
     return out
 
 

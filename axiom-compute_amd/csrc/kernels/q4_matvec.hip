@@ -48,25 +48,86 @@ struct CountArgs {
 //   d * (sc0 * 2^24 * alo + sc1 * 2^20 * ahi) - dmin * (m0 * hs_lo + m1 * hs_hi)
 // which is sum_i (d*sc*q_i - dmin*m) * x_i regrouped per sub-block.
 
+// One 16-element group of x (group gi of a tile: superblock slot gi/16,
+// r = gi%16 -> x[slot*256 + 16r .. +16], i.e. c = r/4, part = (r/2)%2, h = r%2).
+struct XGroup {
+  float4 v[4];
+};
+
+__device__ __forceinline__ void q4k_load_group(const float *__restrict__ x, uint32_t sb0,
+                                               uint32_t gi, XGroup &g) {
+  const float4 *src =
+      reinterpret_cast<const float4 *>(x + (size_t)(sb0 + (gi >> 4)) * 256u + 16u * (gi & 15u));
+  g.v[0] = src[0];
+  g.v[1] = src[1];
+  g.v[2] = src[2];
+  g.v[3] = src[3];
+}
+
+__device__ __forceinline__ void q4k_store_group(float *xs, float *hs, uint32_t gi,
+                                                const XGroup &g) {
+  const uint32_t slot = gi >> 4, r = gi & 15u;
+  const uint32_t c = r >> 2, part = (r >> 1) & 1u, h = r & 1u, k = 2u * c + h;
+  float *dst = xs + slot * 256u + part * 128u + 4u * k;
+  const uint32_t sw = (slot & 1u) * 32u;
+  *reinterpret_cast<float4 *>(dst + (0u ^ sw)) = g.v[0];
+  *reinterpret_cast<float4 *>(dst + (32u ^ sw)) = g.v[1];
+  *reinterpret_cast<float4 *>(dst + (64u ^ sw)) = g.v[2];
+  *reinterpret_cast<float4 *>(dst + (96u ^ sw)) = g.v[3];
+  const float4 a = g.v[0], b = g.v[1], cc = g.v[2], d = g.v[3];
+  const float s = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w)) +
+                  (((cc.x + cc.y) + (cc.z + cc.w)) + ((d.x + d.y) + (d.z + d.w)));
+  hs[slot * 16u + 2u * k + part] = s;
+}
+
 __device__ __forceinline__ void q4k_stage_tile(const float *__restrict__ x, float *xs, float *hs,
                                                uint32_t sb0, uint32_t n_sb, uint32_t tid,
                                                uint32_t nthreads) {
   const uint32_t ngroups = n_sb * 16u;
   for (uint32_t gi = tid; gi < ngroups; gi += nthreads) {
-    const uint32_t slot = gi >> 4, r = gi & 15u;
-    const uint32_t c = r >> 2, part = (r >> 1) & 1u, h = r & 1u, k = 2u * c + h;
-    const float4 *src = reinterpret_cast<const float4 *>(x + (size_t)(sb0 + slot) * 256u + 16u * r);
-    const float4 v0 = src[0], v1 = src[1], v2 = src[2], v3 = src[3];
-    float *dst = xs + slot * 256u + part * 128u + 4u * k;
-    const uint32_t sw = (slot & 1u) * 32u;
-    *reinterpret_cast<float4 *>(dst + (0u ^ sw)) = v0;
-    *reinterpret_cast<float4 *>(dst + (32u ^ sw)) = v1;
-    *reinterpret_cast<float4 *>(dst + (64u ^ sw)) = v2;
-    *reinterpret_cast<float4 *>(dst + (96u ^ sw)) = v3;
-    const float s = ((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w)) +
-                    (((v2.x + v2.y) + (v2.z + v2.w)) + ((v3.x + v3.y) + (v3.z + v3.w)));
-    hs[slot * 16u + 2u * k + part] = s;
+    XGroup g;
+    q4k_load_group(x, sb0, gi, g);
+    q4k_store_group(xs, hs, gi, g);
   }
+}
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte weight load; kNT marks it non-temporal (streamed once per call).
+template <bool kNT>
+__device__ __forceinline__ uint4 load16(const uint8_t *p) {
+  if constexpr (kNT) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+  } else {
+    return *reinterpret_cast<const uint4 *>(p);
+  }
+}
+
+// Raw buffer access (MUBUF) through a resource descriptor: 32-bit byte
+// offsets, and offsets past num_records read as zero in hardware.  The
+// compiler keeps these loads in program order relative to barriers.
+constexpr int kBufferFlags = 0x00020000; // dword3 of the V# for gfx9 (32-bit data)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                           kBufferFlags);
+}
+
+template <bool kNT>
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kNT ? 2 : 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4 buf_loadf4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  // Bit-cast the whole vector: a bit-cast of a single vector element drops
+  // the other three loaded dwords with this compiler.
+  const f32x4_t f =
+      __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+  return make_float4(f.x, f.y, f.z, f.w);
 }
 
 // Four qs bytes (one dword) of a lane's slice against four x values of each part.
@@ -86,24 +147,48 @@ __device__ __forceinline__ void q4k_dword(uint32_t w, float4 xl, float4 xh, floa
   ahi = __builtin_fmaf(hi_half_f16(dh), xh.w, ahi);
 }
 
-template <int RPW, int NW, int PF>
+// All global loads of this kernel are unconditional, with addresses clamped
+// into the row (the results for out-of-range slots are simply not used), so
+// the hardware's in-order load counter lets each iteration wait for exactly
+// its own data while later iterations' loads stay in flight.
+template <int RPW, int PF, bool kNT>
+__device__ __forceinline__ void q4k_load_iter(uint4 (&H)[PF][RPW], uint4 (&Qv)[PF][RPW], int p,
+                                              const uint8_t *const (&rowp)[RPW], uint32_t it,
+                                              uint32_t g, uint32_t k, uint32_t nsb) {
+  const uint32_t sb = min(it * 8u + g, nsb - 1u);
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const uint8_t *b = rowp[r] + (size_t)sb * kQ4kSbBytes;
+    H[p][r] = load16<kNT>(b - 16u * k);
+    Qv[p][r] = load16<kNT>(b + 16u);
+  }
+}
+
+template <int RPW, int NW, int PF, bool kNT, bool kMultiTile>
 __device__ __forceinline__ void q4k_matvec_body(const uint8_t *__restrict__ q,
                                                 const float *__restrict__ x, float *__restrict__ y,
                                                 uint32_t n_rows, uint32_t nsb, uint32_t tile_sb,
                                                 uint32_t block, float *lds) {
   const uint32_t tid = threadIdx.x;
-  const uint32_t lane = tid & 63u, wave = tid >> 6;
+  const uint32_t lane = tid & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t g = lane >> 3, k = lane & 7u, c = k >> 1;
   const uint32_t row0 = (block * NW + wave) * RPW;
+  if (nsb == 0) { // empty rows: the reference returns +0.0 (AT-1323)
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+      if (lane == 0 && row0 + r < n_rows) y[row0 + r] = 0.0f;
+    return;
+  }
   const size_t row_bytes = (size_t)nsb * kQ4kSbBytes;
-
   const uint8_t *rowp[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
     const uint32_t row = min(row0 + r, n_rows - 1u); // clamp: loads stay in bounds
     rowp[r] = q + (size_t)row * row_bytes + 16u * k;
   }
-  const uint32_t n_it = (nsb + 7u) >> 3;
+  // iterations padded to a multiple of PF: the extra ones hold no superblock
+  const uint32_t n_it = (((nsb + 7u) >> 3) + (PF - 1)) / PF * PF;
   const uint32_t it_per_tile = tile_sb >> 3;
   float *xs = lds;
   float *hs = lds + tile_sb * 256u;
@@ -113,78 +198,80 @@ __device__ __forceinline__ void q4k_matvec_body(const uint8_t *__restrict__ q,
 #pragma unroll
   for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
 
+  // Prologue: x for the first tile is requested before the weight prefetch so
+  // that waiting for x never waits on weights.
+  constexpr int kXR = 2; // x groups per thread loaded ahead of the weights
+  const uint32_t ngroups0 = min(tile_sb, nsb) * 16u;
+  XGroup xg[kXR];
 #pragma unroll
-  for (int p = 0; p < PF; ++p) {
-    const uint32_t sb = (uint32_t)p * 8u + g;
-    if ((uint32_t)p < n_it && sb < nsb) {
+  for (int i = 0; i < kXR; ++i)
+    q4k_load_group(x, 0u, min(tid + (uint32_t)i * (NW * 64u), ngroups0 - 1u), xg[i]);
+  __builtin_amdgcn_sched_barrier(0); // keep the x requests ahead of the weight requests
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) {
-        const uint8_t *b = rowp[r] + (size_t)sb * kQ4kSbBytes;
-        H[p][r] = *reinterpret_cast<const uint4 *>(b - 16u * k);
-        Qv[p][r] = *reinterpret_cast<const uint4 *>(b + 16u);
-      }
-    }
+  for (int p = 0; p < PF; ++p) q4k_load_iter<RPW, PF, kNT>(H, Qv, p, rowp, (uint32_t)p, g, k, nsb);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < kXR; ++i) {
+    const uint32_t gi = tid + (uint32_t)i * (NW * 64u);
+    if (gi < ngroups0) q4k_store_group(xs, hs, gi, xg[i]);
   }
+  for (uint32_t gi = tid + kXR * (NW * 64u); gi < ngroups0; gi += NW * 64u) {
+    XGroup gx;
+    q4k_load_group(x, 0u, gi, gx);
+    q4k_store_group(xs, hs, gi, gx);
+  }
+  __syncthreads();
 
-  uint32_t tile = 0xFFFFFFFFu;
+  uint32_t tile = 0;
   for (uint32_t it0 = 0; it0 < n_it; it0 += PF) {
 #pragma unroll
     for (int p = 0; p < PF; ++p) {
       const uint32_t it = it0 + (uint32_t)p;
-      if (it < n_it) {
+      if constexpr (kMultiTile) {
         const uint32_t t_it = it / it_per_tile;
-        if (t_it != tile) { // uniform across the workgroup
-          if (tile != 0xFFFFFFFFu) __syncthreads();
+        if (t_it != tile && t_it * tile_sb < nsb) { // uniform across the workgroup
+          __syncthreads();
           tile = t_it;
           const uint32_t sb0 = t_it * tile_sb;
           q4k_stage_tile(x, xs, hs, sb0, min(tile_sb, nsb - sb0), tid, NW * 64u);
           __syncthreads();
         }
-        const uint32_t sb = it * 8u + g;
-        if (sb < nsb) {
-          const uint32_t slot = sb - tile * tile_sb;
-          const float *xb = xs + slot * 256u + 4u * k;
-          const uint32_t sw = (slot & 1u) * 32u;
-          float4 xl[4], xh[4];
+      }
+      const uint32_t sb = it * 8u + g;
+      if (sb < nsb) {
+        const uint32_t slot = sb - tile * tile_sb;
+        const float *xb = xs + slot * 256u + 4u * k;
+        const uint32_t sw = (slot & 1u) * 32u;
+        float4 xl[4], xh[4];
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            xl[t] = *reinterpret_cast<const float4 *>(xb + ((uint32_t)(t * 32) ^ sw));
-            xh[t] = *reinterpret_cast<const float4 *>(xb + 128u + ((uint32_t)(t * 32) ^ sw));
-          }
-          const float2 hsum = *reinterpret_cast<const float2 *>(hs + slot * 16u + 2u * k);
-#pragma unroll
-          for (int r = 0; r < RPW; ++r) {
-            const uint4 hd = H[p][r];
-            const uint4 qv = Qv[p][r];
-            uint32_t scp, mp;
-            q4k_scale_min_pair(hd.y, hd.z, hd.w, c, &scp, &mp);
-            const float d = f16_to_f32(hd.x & 0xFFFFu);
-            const float dmin = f16_to_f32(hd.x >> 16);
-            float alo = 0.0f, ahi = 0.0f;
-            q4k_dword(qv.x, xl[0], xh[0], alo, ahi);
-            q4k_dword(qv.y, xl[1], xh[1], alo, ahi);
-            q4k_dword(qv.z, xl[2], xh[2], alo, ahi);
-            q4k_dword(qv.w, xl[3], xh[3], alo, ahi);
-            const float sc0 = (float)(scp & 0xFFu) * 16777216.0f; // 2^24
-            const float sc1 = (float)(scp >> 8) * 1048576.0f;     // 2^20
-            const float m0 = (float)(mp & 0xFFu), m1 = (float)(mp >> 8);
-            const float dot = __builtin_fmaf(sc0, alo, sc1 * ahi);
-            const float mins = __builtin_fmaf(m0, hsum.x, m1 * hsum.y);
-            acc[r] = __builtin_fmaf(d, dot, __builtin_fmaf(-dmin, mins, acc[r]));
-          }
+        for (int t = 0; t < 4; ++t) {
+          xl[t] = *reinterpret_cast<const float4 *>(xb + ((uint32_t)(t * 32) ^ sw));
+          xh[t] = *reinterpret_cast<const float4 *>(xb + 128u + ((uint32_t)(t * 32) ^ sw));
         }
-        // refill this prefetch slot with iteration it + PF
-        const uint32_t nit = it + PF;
-        const uint32_t nsb_i = nit * 8u + g;
-        if (nit < n_it && nsb_i < nsb) {
+        const float2 hsum = *reinterpret_cast<const float2 *>(hs + slot * 16u + 2u * k);
 #pragma unroll
-          for (int r = 0; r < RPW; ++r) {
-            const uint8_t *b = rowp[r] + (size_t)nsb_i * kQ4kSbBytes;
-            H[p][r] = *reinterpret_cast<const uint4 *>(b - 16u * k);
-            Qv[p][r] = *reinterpret_cast<const uint4 *>(b + 16u);
-          }
+        for (int r = 0; r < RPW; ++r) {
+          const uint4 hd = H[p][r];
+          const uint4 qv = Qv[p][r];
+          uint32_t scp, mp;
+          q4k_scale_min_pair(hd.y, hd.z, hd.w, c, &scp, &mp);
+          const float d = f16_to_f32(hd.x & 0xFFFFu);
+          const float dmin = f16_to_f32(hd.x >> 16);
+          float alo = 0.0f, ahi = 0.0f;
+          q4k_dword(qv.x, xl[0], xh[0], alo, ahi);
+          q4k_dword(qv.y, xl[1], xh[1], alo, ahi);
+          q4k_dword(qv.z, xl[2], xh[2], alo, ahi);
+          q4k_dword(qv.w, xl[3], xh[3], alo, ahi);
+          const float sc0 = (float)(scp & 0xFFu) * 16777216.0f; // 2^24
+          const float sc1 = (float)(scp >> 8) * 1048576.0f;     // 2^20
+          const float m0 = (float)(mp & 0xFFu), m1 = (float)(mp >> 8);
+          const float dot = __builtin_fmaf(sc0, alo, sc1 * ahi);
+          const float mins = __builtin_fmaf(m0, hsum.x, m1 * hsum.y);
+          acc[r] = __builtin_fmaf(d, dot, __builtin_fmaf(-dmin, mins, acc[r]));
         }
       }
+      // refill this prefetch slot with iteration it + PF (clamped, unconditional)
+      q4k_load_iter<RPW, PF, kNT>(H, Qv, p, rowp, it + PF, g, k, nsb);
     }
   }
 
@@ -195,29 +282,238 @@ __device__ __forceinline__ void q4k_matvec_body(const uint8_t *__restrict__ q,
   }
 }
 
-#define AXH_Q4K_MATVEC(RPW, NW, PF)                                                              \
+// Tiled kernel: rows longer than one LDS tile (x is re-staged per tile).
+#define AXH_Q4K_MATVEC_TILED(RPW, NW, PF)                                                        \
   extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
-      axh_q4k_matvec_r##RPW##_w##NW##_p##PF(const uint8_t *__restrict__ q,                       \
-                                            const float *__restrict__ x, float *__restrict__ y,  \
-                                            RowsArgs a) {                                        \
+      axh_q4k_matvec_tiled_r##RPW##_w##NW##_p##PF(const uint8_t *__restrict__ q,                 \
+                                                  const float *__restrict__ x,                   \
+                                                  float *__restrict__ y, RowsArgs a) {           \
     extern __shared__ float axh_lds_dyn[];                                                       \
-    q4k_matvec_body<RPW, NW, PF>(q, x, y, a.n_rows, a.units_per_row, a.tile_units, blockIdx.x,   \
-                                 axh_lds_dyn);                                                   \
+    if (a.units_per_row <= a.tile_units)                                                         \
+      q4k_matvec_body<RPW, NW, PF, false, false>(q, x, y, a.n_rows, a.units_per_row,             \
+                                                 a.tile_units, blockIdx.x, axh_lds_dyn);         \
+    else                                                                                         \
+      q4k_matvec_body<RPW, NW, PF, false, true>(q, x, y, a.n_rows, a.units_per_row,              \
+                                                a.tile_units, blockIdx.x, axh_lds_dyn);          \
   }
 
-AXH_Q4K_MATVEC(1, 4, 2)
-AXH_Q4K_MATVEC(1, 4, 4)
-AXH_Q4K_MATVEC(1, 8, 4)
-AXH_Q4K_MATVEC(1, 8, 8)
-AXH_Q4K_MATVEC(1, 16, 4)
-AXH_Q4K_MATVEC(2, 4, 2)
-AXH_Q4K_MATVEC(2, 4, 4)
-AXH_Q4K_MATVEC(2, 8, 2)
-AXH_Q4K_MATVEC(2, 8, 4)
-AXH_Q4K_MATVEC(2, 8, 7)
-AXH_Q4K_MATVEC(4, 4, 2)
-AXH_Q4K_MATVEC(4, 4, 4)
-AXH_Q4K_MATVEC(4, 8, 2)
+AXH_Q4K_MATVEC_TILED(1, 4, 2)
+AXH_Q4K_MATVEC_TILED(2, 8, 2)
+
+// ---------------------------------------------------------------------------
+// Persistent Q4_K matvec for rows that fit one LDS tile (<= 128 superblocks).
+//
+// Lane mapping: lane = 4*G + c with G = 8*half + s.  The two half-waves work
+// on two different row bundles (RPW consecutive rows each); in one iteration
+// half-wave `half` covers superblocks it*8 + s (s = 0..7) of its bundle, and
+// lane c (0..3) owns qs bytes [32c, 32c+32) of that superblock: its low
+// nibbles are sub-block 2c (weights 64c + i), its high nibbles sub-block 2c+1
+// (weights 64c + 32 + i), i = 0..31.  Per superblock a lane loads the 16-byte
+// header and two 16-byte qs slices.
+//
+// Each wave walks a flattened sequence (bundle pair, iteration): loads run PF
+// iterations ahead across bundle boundaries, so the load pipeline only
+// drains at the end of the wave's work.  x is staged once per workgroup.
+//
+// LDS: xs[sb*256 + part*128 + ((16t) ^ (16*(sb&3))) + 4c + e]
+//        = x[sb*256 + 64c + 32*part + 4t + e] * (part ? 2^20 : 2^24)
+//      ss[sb*8 + j] = sum of the 32 (unscaled) x of sub-block j
+// For fixed (t, part), 16 consecutive lanes read 64 distinct banks.  The
+// 2^24 / 2^20 factors cancel the f16-subnormal encoding of the nibbles, so
+//   sum_i (d*sc*q_i - dmin*m) * x_i = d*sc*sum_i q_i x_i - dmin*m*ss
+// needs no further scaling.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void q4k_flat_stage(const float *__restrict__ x, float *xs, float *ss,
+                                               uint32_t si, const float4 (&v)[8]) {
+  const uint32_t sb = si >> 3, j = si & 7u, c = j >> 1, part = j & 1u;
+  const float scale = part ? 1048576.0f : 16777216.0f;
+  float *dst = xs + sb * 256u + part * 128u + 4u * c;
+  const uint32_t sw = (sb & 3u) * 16u;
+  float sum = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const float4 a = v[t];
+    sum += (a.x + a.y) + (a.z + a.w);
+    *reinterpret_cast<float4 *>(dst + (((uint32_t)t * 16u) ^ sw)) =
+        make_float4(a.x * scale, a.y * scale, a.z * scale, a.w * scale);
+  }
+  ss[si] = sum;
+}
+
+__device__ __forceinline__ void q4k_flat_load_x(__amdgpu_buffer_rsrc_t xr, uint32_t si,
+                                                float4 (&v)[8]) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t) v[t] = buf_loadf4(xr, si * 128u + 16u * (uint32_t)t);
+}
+
+template <int RPW, int PF>
+struct Q4kFlatBuf {
+  uint4 h[PF][RPW], a[PF][RPW], b[PF][RPW];
+};
+
+// Loads of one iteration for the RPW rows of `bundle`.  Rows past the matrix
+// read zeros (buffer range check); superblocks past the row are never used.
+template <int RPW, int PF, bool kNT>
+__device__ __forceinline__ void q4k_flat_load(Q4kFlatBuf<RPW, PF> &B, int p,
+                                              __amdgpu_buffer_rsrc_t qr, uint32_t row_bytes,
+                                              uint32_t bundle, uint32_t it, uint32_t s,
+                                              uint32_t c) {
+  const uint32_t sb_off = (it * 8u + s) * (uint32_t)kQ4kSbBytes;
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const uint32_t off = (bundle * RPW + (uint32_t)r) * row_bytes + sb_off;
+    B.h[p][r] = buf_load16<kNT>(qr, off);
+    B.a[p][r] = buf_load16<kNT>(qr, off + 16u + 32u * c);
+    B.b[p][r] = buf_load16<kNT>(qr, off + 32u + 32u * c);
+  }
+}
+
+template <int RPW, int NW, int PF, bool kNT>
+__device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
+                                                const float *__restrict__ x,
+                                                float *__restrict__ y, uint32_t n_rows,
+                                                uint32_t nsb, float *lds) {
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63u;
+  // wave index as a scalar: every loop bound below is then wave-uniform
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t G = lane >> 2, half = G >> 3, s = G & 7u, c = lane & 3u;
+  const uint32_t total_waves = gridDim.x * NW;
+  const uint32_t W = blockIdx.x * NW + wave;
+  const uint32_t n_bundles = (n_rows + RPW - 1) / RPW;
+  const uint32_t n_pairs = (n_bundles + 1u) >> 1;
+  if (nsb == 0) { // empty rows: the reference returns +0.0 (AT-1323)
+    for (uint32_t r = W * 64u + lane; r < n_rows; r += total_waves * 64u) y[r] = 0.0f;
+    return;
+  }
+  const uint32_t n_my = W < n_pairs ? (n_pairs - 1u - W) / total_waves + 1u : 0u;
+  const uint32_t n_it = (nsb + 7u) >> 3;
+  const uint32_t total = (n_my * n_it + (PF - 1)) / PF * PF;
+  // The host guarantees n_rows * row_bytes < 2^32 for this kernel.
+  const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
+  const __amdgpu_buffer_rsrc_t qr = make_rsrc(q, n_rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, nsb * 1024u);
+  float *xs = lds;
+  float *ss = lds + nsb * 256u;
+
+  // Prologue: x requests first, then the weight prefetch, then the LDS writes
+  // (waiting for x never waits for the weights: loads retire in order).  One
+  // sub-block of x (32 floats) per thread: the host launches this kernel only
+  // when nsb * 8 <= NW * 64.
+  const uint32_t nsub = nsb * 8u;
+  const uint32_t my_sub = min(tid, nsub - 1u);
+  float4 xv[8];
+  q4k_flat_load_x(xr, my_sub, xv);
+  __builtin_amdgcn_sched_barrier(0);
+
+  Q4kFlatBuf<RPW, PF> B;
+  uint32_t l_pi = 0, l_it = 0; // load cursor: pair index (of this wave) and iteration
+#pragma unroll
+  for (int p = 0; p < PF; ++p) {
+    const uint32_t bundle = 2u * (W + l_pi * total_waves) + half;
+    q4k_flat_load<RPW, PF, kNT>(B, p, qr, row_bytes, bundle, l_it, s, c);
+    if (++l_it == n_it) { l_it = 0; ++l_pi; }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // Threads beyond nsub rewrite the last sub-block with the same values.
+  q4k_flat_stage(x, xs, ss, my_sub, xv);
+  __syncthreads();
+
+  float acc[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
+  uint32_t c_pi = 0, c_it = 0; // compute cursor
+  for (uint32_t j0 = 0; j0 < total; j0 += PF) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+      const uint32_t sb = c_it * 8u + s;
+      if (c_pi < n_my && sb < nsb) {
+        const float *xb = xs + sb * 256u + 4u * c;
+        const uint32_t sw = (sb & 3u) * 16u;
+        float4 xl[8], xh[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          xl[t] = *reinterpret_cast<const float4 *>(xb + (((uint32_t)t * 16u) ^ sw));
+          xh[t] = *reinterpret_cast<const float4 *>(xb + 128u + (((uint32_t)t * 16u) ^ sw));
+        }
+        const float2 sub = *reinterpret_cast<const float2 *>(ss + sb * 8u + 2u * c);
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+          const uint4 hd = B.h[p][r];
+          uint32_t scp, mp;
+          q4k_scale_min_pair(hd.y, hd.z, hd.w, c, &scp, &mp);
+          float alo = 0.0f, ahi = 0.0f;
+          q4k_dword(B.a[p][r].x, xl[0], xh[0], alo, ahi);
+          q4k_dword(B.a[p][r].y, xl[1], xh[1], alo, ahi);
+          q4k_dword(B.a[p][r].z, xl[2], xh[2], alo, ahi);
+          q4k_dword(B.a[p][r].w, xl[3], xh[3], alo, ahi);
+          q4k_dword(B.b[p][r].x, xl[4], xh[4], alo, ahi);
+          q4k_dword(B.b[p][r].y, xl[5], xh[5], alo, ahi);
+          q4k_dword(B.b[p][r].z, xl[6], xh[6], alo, ahi);
+          q4k_dword(B.b[p][r].w, xl[7], xh[7], alo, ahi);
+          const float dot = __builtin_fmaf((float)(scp & 0xFFu), alo, (float)(scp >> 8) * ahi);
+          const float mins = __builtin_fmaf((float)(mp & 0xFFu), sub.x, (float)(mp >> 8) * sub.y);
+          acc[r] = __builtin_fmaf(f16_to_f32(hd.x & 0xFFFFu), dot,
+                                  __builtin_fmaf(-f16_to_f32(hd.x >> 16), mins, acc[r]));
+        }
+      }
+      // refill this slot PF iterations ahead (unconditional)
+      {
+        const uint32_t bundle = 2u * (W + l_pi * total_waves) + half;
+        q4k_flat_load<RPW, PF, kNT>(B, p, qr, row_bytes, bundle, l_it, s, c);
+        if (++l_it == n_it) { l_it = 0; ++l_pi; }
+      }
+      if (++c_it == n_it) { // a bundle pair is complete: reduce and store
+        if (c_pi < n_my) {
+          const uint32_t bundle0 = 2u * (W + c_pi * total_waves);
+#pragma unroll
+          for (int r = 0; r < RPW; ++r) {
+            float v = acc[r];
+            v += dpp_mov<0xB1>(v);
+            v += dpp_mov<0x4E>(v);
+            v += dpp_mov<0x141>(v);
+            v += dpp_mov<0x140>(v);
+            const int vi = __builtin_bit_cast(int, v);
+            const float h0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 0)) +
+                             __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 16));
+            const float h1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 32)) +
+                             __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 48));
+            const uint32_t r0 = bundle0 * RPW + (uint32_t)r;
+            const uint32_t r1 = (bundle0 + 1u) * RPW + (uint32_t)r;
+            if (lane == 0 && r0 < n_rows) y[r0] = h0;
+            if (lane == 0 && r1 < n_rows) y[r1] = h1;
+            acc[r] = 0.0f;
+          }
+        }
+        c_it = 0;
+        ++c_pi;
+      }
+    }
+  }
+}
+
+#define AXH_Q4K_MATVEC_FLAT(RPW, NW, PF, NT)                                                     \
+  extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
+      axh_q4k_matvec_flat_r##RPW##_w##NW##_p##PF##_n##NT(const uint8_t *__restrict__ q,          \
+                                                         const float *__restrict__ x,            \
+                                                         float *__restrict__ y, RowsArgs a) {    \
+    extern __shared__ float axh_lds_dyn[];                                                       \
+    q4k_matvec_flat<RPW, NW, PF, NT != 0>(q, x, y, a.n_rows, a.units_per_row, axh_lds_dyn);     \
+  }
+
+AXH_Q4K_MATVEC_FLAT(1, 8, 2, 0)
+AXH_Q4K_MATVEC_FLAT(1, 8, 4, 0)
+AXH_Q4K_MATVEC_FLAT(1, 8, 7, 0)
+AXH_Q4K_MATVEC_FLAT(1, 16, 2, 0)
+AXH_Q4K_MATVEC_FLAT(1, 4, 7, 0)
+AXH_Q4K_MATVEC_FLAT(2, 4, 2, 0)
+AXH_Q4K_MATVEC_FLAT(2, 4, 4, 0)
+AXH_Q4K_MATVEC_FLAT(2, 8, 2, 0)
+AXH_Q4K_MATVEC_FLAT(2, 8, 4, 0)
+AXH_Q4K_MATVEC_FLAT(4, 4, 2, 0)
+AXH_Q4K_MATVEC_FLAT(1, 8, 7, 1)
+AXH_Q4K_MATVEC_FLAT(2, 4, 2, 1)
+AXH_Q4K_MATVEC_FLAT(2, 4, 4, 1)
 
 // Reference-compatible entry point: the contract of
 // examples/q4km_dequant_matvec.axc (bindings q=0, x=1, y=2; push constant
@@ -230,11 +526,10 @@ extern "C" __global__ void __launch_bounds__(64)
                         float *__restrict__ y, CountArgs a) {
   __shared__ float lds[kRefTileSb * 256 + kRefTileSb * 16];
   if (blockIdx.x != 0 || blockIdx.y != 0 || blockIdx.z != 0) return;
-  if (a.n_units == 0) {
-    if (threadIdx.x == 0) y[0] = 0.0f;
-    return;
-  }
-  q4k_matvec_body<1, 1, 2>(q, x, y, 1u, a.n_units, kRefTileSb, 0u, lds);
+  if (a.n_units <= kRefTileSb)
+    q4k_matvec_body<1, 1, 2, false, false>(q, x, y, 1u, a.n_units, kRefTileSb, 0u, lds);
+  else
+    q4k_matvec_body<1, 1, 2, false, true>(q, x, y, 1u, a.n_units, kRefTileSb, 0u, lds);
 }
 
 // ===========================================================================

@@ -33,6 +33,7 @@ struct Core {
   std::string name;
   uint32_t max_wg[3] = {0, 0, 0};
   uint32_t max_lds = 0;
+  uint32_t cu_count = 1;
   uint64_t fence_timeout_ms = 10000;
   std::string cache_dir;
 
@@ -69,6 +70,7 @@ struct axh_context {
   std::shared_ptr<axh::Core> core;
   std::mutex ops_mu;
   std::unordered_map<std::string, axh_kernel *> ops; // builtin kernels by entry name
+  std::unordered_map<uint64_t, uint32_t> occupancy;  // (kernel, lds) -> workgroups per CU
 };
 
 namespace axh {

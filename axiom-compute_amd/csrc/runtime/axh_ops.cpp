@@ -26,19 +26,22 @@ struct CountArgs {
 };
 
 struct MatvecVariant {
-  uint32_t rpw, nw, pf;
+  uint32_t rpw, nw, pf, nt;
 };
 
-// Compiled instantiations of axh_q4k_matvec_r{rpw}_w{nw}_p{pf}; keep in sync
-// with the AXH_Q4K_MATVEC list in q4_matvec.hip.
+// Compiled instantiations of axh_q4k_matvec_flat_r{rpw}_w{nw}_p{pf}_n{0|1}
+// (persistent kernel; nt: 1 = non-temporal weight loads, 2 = normal loads).
+// Keep in sync with the AXH_Q4K_MATVEC_FLAT list in q4_matvec.hip.
 constexpr MatvecVariant kQ4kVariants[] = {
-    {1, 4, 2}, {1, 4, 4}, {1, 8, 4}, {1, 8, 8}, {1, 16, 4}, {2, 4, 2}, {2, 4, 4},
-    {2, 8, 2}, {2, 8, 4}, {2, 8, 7}, {4, 4, 2}, {4, 4, 4},  {4, 8, 2},
+    {1, 8, 2, 2}, {1, 8, 4, 2}, {1, 8, 7, 2}, {1, 16, 2, 2},
+    {1, 4, 7, 2}, {2, 4, 2, 2}, {2, 4, 4, 2}, {2, 8, 2, 2},  {2, 8, 4, 2},
+    {4, 4, 2, 2}, {1, 8, 7, 1}, {2, 4, 2, 1}, {2, 4, 4, 1},
 };
-// axh_q4_0_matvec_r{rpw}_w{nw} (prefetch is not a hole for Q4_0).
-constexpr MatvecVariant kQ4_0Variants[] = {{1, 1, 1}, {1, 4, 1}, {2, 4, 1}, {4, 4, 1}};
+// axh_q4_0_matvec_r{rpw}_w{nw} (prefetch and cache policy are not holes for Q4_0).
+constexpr MatvecVariant kQ4_0Variants[] = {{1, 1, 1, 2}, {1, 4, 1, 2}, {2, 4, 1, 2}, {4, 4, 1, 2}};
 
-constexpr uint32_t kQ4kMaxTileSb = 128; // 128 * 1088 B = 136 KiB of LDS
+constexpr uint32_t kQ4kMaxTileSb = 128;   // tiled kernel: 128 * 1088 B = 136 KiB of LDS
+constexpr uint32_t kQ4kFlatMaxSb = 128;   // persistent kernel: 128 * 1056 B = 132 KiB of LDS
 constexpr uint32_t kQ4_0MaxTileB = 1024; // 1024 * 132 B = 132 KiB of LDS
 
 } // namespace
@@ -80,9 +83,11 @@ static const MatvecVariant *find_variant(const MatvecVariant *table, size_t n,
     if (v->rows_per_wave) want.rpw = v->rows_per_wave;
     if (v->waves_per_workgroup) want.nw = v->waves_per_workgroup;
     if (v->prefetch) want.pf = v->prefetch;
+    if (v->nontemporal) want.nt = v->nontemporal;
   }
   for (size_t i = 0; i < n; ++i)
-    if (table[i].rpw == want.rpw && table[i].nw == want.nw && table[i].pf == want.pf)
+    if (table[i].rpw == want.rpw && table[i].nw == want.nw && table[i].pf == want.pf &&
+        table[i].nt == want.nt)
       return &table[i];
   return nullptr;
 }
@@ -90,15 +95,18 @@ static const MatvecVariant *find_variant(const MatvecVariant *table, size_t n,
 // Default strategy per shape (chosen from on-device sweeps; any compiled
 // variant can be forced through axh_q4_variant).
 static MatvecVariant q4k_default(uint32_t n_rows, uint32_t nsb) {
-  (void)nsb;
-  if (n_rows >= 2048) return {2, 8, 4};
-  return {1, 4, 2};
+  (void)n_rows;
+  // The persistent kernel stages one 32-element sub-block of x per thread,
+  // so the workgroup must have at least nsb * 8 threads.
+  if (nsb * 8u <= 256u) return {2, 4, 2, 2};
+  if (nsb * 8u <= 512u) return {1, 8, 2, 2};
+  return {1, 16, 2, 2};
 }
 
 static MatvecVariant q4_0_default(uint32_t n_rows, uint32_t nb) {
   (void)nb;
-  if (n_rows >= 4096) return {2, 4, 1};
-  return {1, 1, 1};
+  if (n_rows >= 4096) return {2, 4, 1, 2};
+  return {1, 1, 1, 2};
 }
 
 static bool device_ptr_ok(const void *p) { return p != nullptr; }
@@ -124,6 +132,7 @@ axh_status axh_q4k_matvec_variant_at(uint32_t i, axh_q4_variant *out) {
   out->rows_per_wave = kQ4kVariants[i].rpw;
   out->waves_per_workgroup = kQ4kVariants[i].nw;
   out->prefetch = kQ4kVariants[i].pf;
+  out->nontemporal = kQ4kVariants[i].nt;
   return ok();
 }
 
@@ -137,7 +146,27 @@ axh_status axh_q4_0_matvec_variant_at(uint32_t i, axh_q4_variant *out) {
   out->rows_per_wave = kQ4_0Variants[i].rpw;
   out->waves_per_workgroup = kQ4_0Variants[i].nw;
   out->prefetch = kQ4_0Variants[i].pf;
+  out->nontemporal = kQ4_0Variants[i].nt;
   return ok();
+}
+
+// Workgroups of `k` resident per CU at `lds` bytes of dynamic LDS (cached).
+static uint32_t occupancy(axh_context *ctx, axh_kernel *k, uint32_t lds) {
+  const uint64_t key = ((uint64_t)(uintptr_t)k << 20) ^ lds;
+  {
+    std::lock_guard<std::mutex> lk(ctx->ops_mu);
+    auto it = ctx->occupancy.find(key);
+    if (it != ctx->occupancy.end()) return it->second;
+  }
+  int blocks = 0;
+  const int threads = (int)(k->wg[0] * k->wg[1] * k->wg[2]);
+  if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, k->fn, threads, lds) !=
+          hipSuccess ||
+      blocks < 1)
+    blocks = 1;
+  std::lock_guard<std::mutex> lk(ctx->ops_mu);
+  ctx->occupancy[key] = (uint32_t)blocks;
+  return (uint32_t)blocks;
 }
 
 axh_status axh_q4k_matvec(axh_context *ctx, const void *q, const float *x, float *y,
@@ -154,10 +183,36 @@ axh_status axh_q4k_matvec(axh_context *ctx, const void *q, const float *x, float
   const MatvecVariant *v = find_variant(kQ4kVariants, axh_q4k_matvec_variant_count(), variant,
                                         q4k_default(n_rows, sb_per_row));
   if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_K matvec variant matches");
+  hipSetDevice(ctx->core->device);
+  void *bufs[3] = {const_cast<void *>(q), const_cast<float *>(x), y};
+  const uint64_t q_bytes = (uint64_t)n_rows * sb_per_row * 144u;
+  const bool flat = sb_per_row >= 1 && sb_per_row <= kQ4kFlatMaxSb &&
+                    sb_per_row * 8u <= v->nw * 64u && q_bytes < 0xFFFFFFFFull;
   char name[64];
-  std::snprintf(name, sizeof(name), "axh_q4k_matvec_r%u_w%u_p%u", v->rpw, v->nw, v->pf);
   axh_kernel *k = nullptr;
-  axh_status s = builtin_kernel(ctx, name, 3, sizeof(RowsArgs), v->nw * 64u, &k);
+  axh_status s;
+  if (flat) {
+    std::snprintf(name, sizeof(name), "axh_q4k_matvec_flat_r%u_w%u_p%u_n%u", v->rpw, v->nw, v->pf,
+                  v->nt == 1 ? 1u : 0u);
+    s = builtin_kernel(ctx, name, 3, sizeof(RowsArgs), v->nw * 64u, &k);
+    if (s != AXH_OK) return s;
+    const uint32_t lds = sb_per_row * 1056u;
+    if (lds > ctx->core->max_lds)
+      return fail(AXH_ERR_PIPELINE_LAYOUT, "LDS tile exceeds the device limit");
+    // Each wave handles pairs of RPW-row bundles; the grid is persistent.
+    const uint32_t bundles = (n_rows + v->rpw - 1) / v->rpw;
+    const uint32_t pairs = (bundles + 1) / 2;
+    const uint32_t wgs_needed = (pairs + v->nw - 1) / v->nw;
+    const uint32_t resident = occupancy(ctx, k, lds) * ctx->core->cu_count;
+    const uint32_t grid[3] = {wgs_needed < resident ? wgs_needed : resident, 1, 1};
+    RowsArgs a{n_rows, sb_per_row, sb_per_row, 0};
+    s = launch_raw(k, grid, bufs, 3, &a, sizeof(a), lds, pick_stream(ctx, stream));
+    return s == AXH_OK ? ok() : s;
+  }
+  // Rows longer than one LDS tile, or matrices of 4 GiB and more.
+  const MatvecVariant tv = n_rows >= 2048 ? MatvecVariant{2, 8, 2, 2} : MatvecVariant{1, 4, 2, 2};
+  std::snprintf(name, sizeof(name), "axh_q4k_matvec_tiled_r%u_w%u_p%u", tv.rpw, tv.nw, tv.pf);
+  s = builtin_kernel(ctx, name, 3, sizeof(RowsArgs), tv.nw * 64u, &k);
   if (s != AXH_OK) return s;
   uint32_t tile = (sb_per_row + 7u) & ~7u;
   if (tile == 0) tile = 8;
@@ -166,10 +221,8 @@ axh_status axh_q4k_matvec(axh_context *ctx, const void *q, const float *x, float
   if (lds > ctx->core->max_lds)
     return fail(AXH_ERR_PIPELINE_LAYOUT, "LDS tile exceeds the device limit");
   RowsArgs a{n_rows, sb_per_row, tile, 0};
-  const uint32_t rows_per_wg = v->rpw * v->nw;
+  const uint32_t rows_per_wg = tv.rpw * tv.nw;
   const uint32_t grid[3] = {(n_rows + rows_per_wg - 1) / rows_per_wg, 1, 1};
-  void *bufs[3] = {const_cast<void *>(q), const_cast<float *>(x), y};
-  hipSetDevice(ctx->core->device);
   s = launch_raw(k, grid, bufs, 3, &a, sizeof(a), lds, pick_stream(ctx, stream));
   return s == AXH_OK ? ok() : s;
 }
@@ -189,6 +242,7 @@ axh_status axh_q4_0_matvec(axh_context *ctx, const void *q, const float *x, floa
   axh_q4_variant vv{};
   if (variant) vv = *variant;
   vv.prefetch = 1;
+  vv.nontemporal = 2;
   const MatvecVariant *v = find_variant(kQ4_0Variants, axh_q4_0_matvec_variant_count(), &vv, dflt);
   if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_0 matvec variant matches");
   char name[64];

@@ -265,6 +265,7 @@ axh_status axh_context_create(const axh_context_options *opts, axh_context **out
   core->max_wg[1] = (uint32_t)prop.maxGridSize[1];
   core->max_wg[2] = (uint32_t)prop.maxGridSize[2];
   core->max_lds = (uint32_t)prop.sharedMemPerBlock;
+  core->cu_count = prop.multiProcessorCount > 0 ? (uint32_t)prop.multiProcessorCount : 1u;
   uint64_t timeout = opts ? opts->fence_timeout_ms : 0;
   if (timeout == 0) {
     const char *env = std::getenv("AXH_FENCE_TIMEOUT_MS");

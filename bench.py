@@ -63,7 +63,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--variant", default="", help="rows_per_wave,waves,prefetch")
+    ap.add_argument("--variant", default="", help="rows_per_wave,waves,prefetch[,nontemporal]")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -80,8 +80,7 @@ def main() -> int:
     pkg = __graft_entry__.load_package()
     variant = None
     if args.variant:
-        r, w, p = (int(t) for t in args.variant.split(","))
-        variant = pkg.Variant(r, w, p)
+        variant = pkg.Variant(*(int(t) for t in args.variant.split(",")))
 
     rows, sb = ROWS, SB
     weight_bytes = rows * sb * 144

@@ -147,12 +147,14 @@ axh_status axh_synchronize(axh_context *ctx, void *stream);
 
 /* ---- Q4 dequant-matvec operations ------------------------------------------
  * Strategy holes of the matvec kernels (the reference's @strategy surface,
- * crates/axc-hir/src/hir.rs:62-68): rows_per_wave, waves_per_workgroup and
- * prefetch (superblock iterations loaded ahead).  Zero fields pick defaults. */
+ * crates/axc-hir/src/hir.rs:62-68): rows_per_wave, waves_per_workgroup,
+ * prefetch (superblock iterations loaded ahead) and nontemporal (weight-load
+ * cache policy).  Zero fields pick the defaults for the shape. */
 typedef struct axh_q4_variant {
     uint32_t rows_per_wave;
     uint32_t waves_per_workgroup;
     uint32_t prefetch;
+    uint32_t nontemporal; /* 1: weight loads bypass cache allocation; 2: force normal loads */
 } axh_q4_variant;
 
 /* y[r] = dot(row r of Q4_K_M matrix q, x) for r < n_rows, where each row is
