@@ -64,6 +64,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--variant", default="", help="rows_per_wave,waves,prefetch[,nontemporal]")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run device-to-device copies of the weight size (counter calibration)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -126,6 +128,14 @@ def main() -> int:
     total_ms = ev0.elapsed_time(ev1)
     us_per_call = total_ms * 1000.0 / args.steps
     gbs = weight_bytes / (us_per_call * 1e-6) / 1e9
+
+    if args.calibrate_copy:
+        # A plain copy of exactly weight_bytes, for scaling FETCH_SIZE/WRITE_SIZE.
+        src = torch.empty(weight_bytes, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
 
     cpu = cpu_baseline(O, q, x, rows, sb, args.cpu_seconds) if args.cpu_seconds > 0 else None
     out = {

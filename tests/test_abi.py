@@ -1,0 +1,131 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+the headers declare, and validates requests before touching a device
+(reference: crates/axc-runtime/src/dispatch.rs:56-95 and its unit tests at
+dispatch.rs:193,217; crates/axc-runtime/tests/dispatch_error_paths.rs)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _header_functions(path: Path) -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", path.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(axh_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_function(axc):
+    lib = axc.load_library()
+    names = []
+    for h in sorted((ROOT / "include").glob("*.h")):
+        names += _header_functions(h)
+    assert len(names) > 20
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_status_names_mirror_reference_dispatch_error_variants(axc):
+    expected = [
+        "VulkanEntryFailed", "NoVulkanInstance", "NoSupportedDevice", "NoComputeQueue",
+        "DeviceCreationFailed", "ShaderModuleCreationFailed", "DescriptorSetLayoutFailed",
+        "DescriptorPoolFailed", "PipelineLayoutFailed", "PipelineCreationFailed",
+        "BufferAllocationFailed", "MemoryMapFailed", "NoCompatibleMemoryType",
+        "CommandBufferRecordFailed", "QueueSubmitFailed", "FenceTimeout", "ReadbackFailed",
+        "BindingCountMismatch", "PushConstantSizeMismatch", "WorkgroupCountExceedsDeviceLimit",
+        "MetadataIoError", "MetadataParseError", "MetadataSchemaMismatch",
+        "PipelineCacheLoadFailed", "StagingCopyFailed",
+    ]  # error.rs:27-195, in order
+    assert [axc.axh.status_name(i) for i in range(1, 26)] == expected
+    assert axc.axh.status_name(0) == "Ok"
+    assert [axc.axh.VARIANTS[i] for i in range(1, 26)] == expected
+
+
+def _plan(axc, n=3, pc=4):
+    return axc.BindingPlan([axc.axh.ACCESS_READ_ONLY] * (n - 1) + [axc.axh.ACCESS_READ_WRITE],
+                           pc, (64, 1, 1))
+
+
+def test_validate_accepts_matching_request(axc):
+    axc.validate_request(_plan(axc), (1, 1, 1), 3, 3, 4, (65535, 65535, 65535))
+
+
+def test_validate_binding_count_mismatch_inputs(axc):
+    with pytest.raises(axc.DispatchError) as e:
+        axc.validate_request(_plan(axc), (1, 1, 1), 2, 3, 4)
+    assert e.value.variant == "BindingCountMismatch"
+    assert "expected 3, got 2" in str(e.value)
+
+
+def test_validate_binding_count_mismatch_outputs(axc):
+    with pytest.raises(axc.DispatchError) as e:
+        axc.validate_request(_plan(axc), (1, 1, 1), 3, 4, 4)
+    assert e.value.variant == "BindingCountMismatch"
+    assert "expected 3, got 4" in str(e.value)
+
+
+def test_validate_push_constant_size_mismatch(axc):
+    with pytest.raises(axc.DispatchError) as e:
+        axc.validate_request(_plan(axc, pc=4), (1, 1, 1), 3, 3, 8)
+    assert e.value.variant == "PushConstantSizeMismatch"
+    assert "expected 4 bytes, got 8" in str(e.value)
+
+
+def test_validate_workgroup_count_exceeds_limit(axc):
+    with pytest.raises(axc.DispatchError) as e:
+        axc.validate_request(_plan(axc), (70000, 1, 1), 3, 3, 4, (65535, 65535, 65535))
+    assert e.value.variant == "WorkgroupCountExceedsDeviceLimit"
+
+
+def test_validation_order_binding_before_push_constants(axc):
+    """Both wrong: the binding count is reported first (dispatch.rs:60-83)."""
+    with pytest.raises(axc.DispatchError) as e:
+        axc.validate_request(_plan(axc), (1, 1, 1), 1, 3, 99)
+    assert e.value.variant == "BindingCountMismatch"
+
+
+def test_builtin_code_object_holds_every_variant_kernel(axc):
+    co = axc.builtin_code_object()
+    assert co[:4] == b"\x7fELF"
+    for v in axc.compiled_variants("q4k"):
+        name = (f"axh_q4k_matvec_flat_r{v.rows_per_wave}_w{v.waves_per_workgroup}"
+                f"_p{v.prefetch}_n{1 if v.nontemporal == 1 else 0}")
+        assert name.encode() in co, name
+    for v in axc.compiled_variants("q4_0"):
+        name = f"axh_q4_0_matvec_r{v.rows_per_wave}_w{v.waves_per_workgroup}"
+        assert name.encode() in co, name
+    for name in ("q4km_dequant_matvec", "q4_0_dequant_matvec", "axh_q4k_dequant",
+                 "axh_q4_0_dequant", "axh_f16_widen", "axh_q4k_matvec_tiled_r2_w8_p2",
+                 "axh_q4k_matvec_tiled_r1_w4_p2"):
+        assert name.encode() in co, name
+
+
+def test_variant_index_out_of_range_is_typed_error(axc):
+    lib = axc.load_library()
+    v = axc.axh._Variant()
+    assert lib.axh_q4k_matvec_variant_at(10_000, ctypes.byref(v)) == 100
+    assert b"out of range" in lib.axh_last_error()
+
+
+def test_null_context_calls_fail_cleanly(axc):
+    lib = axc.load_library()
+    assert lib.axh_q4k_matvec(None, None, None, None, 1, 1, None, None) == 100
+    assert lib.axh_synchronize(None, None) == 100
+    assert lib.axh_upload(None, None, None, 0) == 100
+    lib.axh_context_destroy(None)  # no-op
+    lib.axh_kernel_release(None)   # no-op
+
+
+def test_context_without_gpu_reports_typed_error(axc):
+    """In a container without a GPU, context creation fails with a typed
+    status (no crash); on a GPU box it succeeds."""
+    try:
+        ctx = axc.HipContext.new()
+    except axc.DispatchError as e:
+        assert e.variant in ("NoVulkanInstance", "NoSupportedDevice")
+    else:
+        assert "gfx950" in ctx.device_name or ctx.device_name
+        ctx.close()
