@@ -131,8 +131,15 @@ def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
         "axh_buffer_free": (st, [vp, vp]),
         "axh_upload": (st, [vp, vp, vp, sz]),
         "axh_download": (st, [vp, vp, vp, sz]),
+        "axh_copy_device": (st, [vp, vp, vp, sz]),
         "axh_launch": (st, [vp, vp, c.POINTER(u32), c.POINTER(vp), sz, vp, sz, vp]),
         "axh_synchronize": (st, [vp, vp]),
+        "axh_device_synchronize": (st, [vp]),
+        "axh_event_create": (st, [vp, c.POINTER(vp)]),
+        "axh_event_record": (st, [vp, vp, vp]),
+        "axh_event_synchronize": (st, [vp, vp]),
+        "axh_event_elapsed_ms": (st, [vp, vp, c.POINTER(c.c_float)]),
+        "axh_event_destroy": (None, [vp]),
         "axh_q4k_matvec": (st, [vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
         "axh_q4_0_matvec": (st, [vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
         "axh_q4k_dequant": (st, [vp, vp, vp, u64, vp]),
@@ -249,7 +256,7 @@ class DispatchRequest:
 
 
 def _ptr(obj) -> int:
-    """Device address of a DeviceBuffer, a torch tensor or a raw int."""
+    """Device address of a DeviceBuffer, an object with data_ptr() or a raw int."""
     if obj is None:
         return 0
     if isinstance(obj, int):
@@ -262,13 +269,41 @@ def _ptr(obj) -> int:
 
 
 def _stream(s) -> Optional[int]:
+    """A hipStream_t of this library's HIP runtime, as an int (None = context stream)."""
     if s is None:
         return None
     if isinstance(s, int):
         return s
-    if hasattr(s, "cuda_stream"):
-        return int(s.cuda_stream)
-    raise TypeError(f"not a stream: {type(s)!r}")
+    raise TypeError(f"not a stream handle: {type(s)!r}")
+
+
+class Event:
+    """HIP event of the context's runtime (GPU timestamps on a stream)."""
+
+    def __init__(self, ctx: "HipContext"):
+        self._ctx = ctx
+        raw = ctypes.c_void_p()
+        _check(ctx._lib.axh_event_create(ctx._raw, ctypes.byref(raw)))
+        self._raw = int(raw.value)
+
+    def record(self, stream=None) -> None:
+        _check(self._ctx._lib.axh_event_record(self._ctx._raw, self._raw, _stream(stream)))
+
+    def synchronize(self) -> None:
+        _check(self._ctx._lib.axh_event_synchronize(self._ctx._raw, self._raw))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = ctypes.c_float()
+        _check(self._ctx._lib.axh_event_elapsed_ms(self._raw, end._raw, ctypes.byref(ms)))
+        return float(ms.value)
+
+    def __del__(self):
+        try:
+            if self._raw:
+                self._ctx._lib.axh_event_destroy(self._raw)
+                self._raw = 0
+        except Exception:
+            pass
 
 
 class KernelHandle:
@@ -447,8 +482,17 @@ class HipContext:
         _check(self._lib.axh_download(self._raw, out, _ptr(src), nbytes))
         return out.raw[:nbytes]
 
+    def copy_device(self, dst, src, nbytes: int) -> None:
+        _check(self._lib.axh_copy_device(self._raw, _ptr(dst), _ptr(src), nbytes))
+
     def synchronize(self, stream=None) -> None:
         _check(self._lib.axh_synchronize(self._raw, _stream(stream)))
+
+    def device_synchronize(self) -> None:
+        _check(self._lib.axh_device_synchronize(self._raw))
+
+    def event(self) -> "Event":
+        return Event(self)
 
     # ---- Q4 operations -----------------------------------------------------
     def q4k_matvec(self, q, x, y, n_rows: int, sb_per_row: int,

@@ -751,3 +751,11 @@ extern "C" __global__ void __launch_bounds__(256)
   const uint32_t i = blockIdx.x * 256u + threadIdx.x;
   if (i < a.n_units) f[i] = f16_to_f32(h[i]);
 }
+
+// Bounded busy wait (runtime tests of the completion timeout): sleeps
+// a.n_units times (about 3 us each) and then writes the count.  Always ends.
+extern "C" __global__ void __launch_bounds__(64) axh_spin(uint32_t *__restrict__ out,
+                                                          CountArgs a) {
+  for (uint32_t i = 0; i < a.n_units; ++i) __builtin_amdgcn_s_sleep(127);
+  if (threadIdx.x == 0 && blockIdx.x == 0) out[0] = a.n_units;
+}

@@ -579,6 +579,16 @@ axh_status axh_download(axh_context *ctx, void *dst, const void *src, size_t byt
   return s == AXH_OK ? ok() : s;
 }
 
+axh_status axh_copy_device(axh_context *ctx, void *dst, const void *src, size_t bytes) {
+  if (!ctx || (bytes && (!dst || !src))) return fail(AXH_ERR_INVALID_ARGUMENT, "NULL argument");
+  if (bytes == 0) return ok();
+  hipSetDevice(ctx->core->device);
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->core->stream);
+  if (e != hipSuccess) return fail(AXH_ERR_STAGING_COPY, hip_msg("hipMemcpyAsync", e));
+  axh_status s = wait_stream(*ctx->core, ctx->core->stream);
+  return s == AXH_OK ? ok() : s;
+}
+
 axh_status axh_launch(axh_context *ctx, axh_kernel *k, const uint32_t workgroups[3],
                       void *const *bufs, size_t n_buffers, const void *pc, size_t pc_bytes,
                       void *stream) {
@@ -597,6 +607,50 @@ axh_status axh_launch(axh_context *ctx, axh_kernel *k, const uint32_t workgroups
   hipSetDevice(ctx->core->device);
   axh_status s = launch_raw(k, workgroups, bufs, n_buffers, pc, pc_bytes, 0, pick_stream(ctx, stream));
   return s == AXH_OK ? ok() : s;
+}
+
+axh_status axh_device_synchronize(axh_context *ctx) {
+  if (!ctx) return fail(AXH_ERR_INVALID_ARGUMENT, "ctx is NULL");
+  hipSetDevice(ctx->core->device);
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return fail(AXH_ERR_QUEUE_SUBMIT, hip_msg("hipDeviceSynchronize", e));
+  return ok();
+}
+
+axh_status axh_event_create(axh_context *ctx, axh_event **out) {
+  if (!ctx || !out) return fail(AXH_ERR_INVALID_ARGUMENT, "NULL argument");
+  hipSetDevice(ctx->core->device);
+  hipEvent_t ev = nullptr;
+  hipError_t e = hipEventCreate(&ev);
+  if (e != hipSuccess) return fail(AXH_ERR_QUEUE_SUBMIT, hip_msg("hipEventCreate", e));
+  *out = reinterpret_cast<axh_event *>(ev);
+  return ok();
+}
+
+axh_status axh_event_record(axh_context *ctx, axh_event *ev, void *stream) {
+  if (!ctx || !ev) return fail(AXH_ERR_INVALID_ARGUMENT, "NULL argument");
+  hipError_t e = hipEventRecord(reinterpret_cast<hipEvent_t>(ev), pick_stream(ctx, stream));
+  if (e != hipSuccess) return fail(AXH_ERR_QUEUE_SUBMIT, hip_msg("hipEventRecord", e));
+  return ok();
+}
+
+axh_status axh_event_synchronize(axh_context *ctx, axh_event *ev) {
+  if (!ctx || !ev) return fail(AXH_ERR_INVALID_ARGUMENT, "NULL argument");
+  hipError_t e = hipEventSynchronize(reinterpret_cast<hipEvent_t>(ev));
+  if (e != hipSuccess) return fail(AXH_ERR_QUEUE_SUBMIT, hip_msg("hipEventSynchronize", e));
+  return ok();
+}
+
+axh_status axh_event_elapsed_ms(axh_event *start, axh_event *end, float *ms) {
+  if (!start || !end || !ms) return fail(AXH_ERR_INVALID_ARGUMENT, "NULL argument");
+  hipError_t e = hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start),
+                                     reinterpret_cast<hipEvent_t>(end));
+  if (e != hipSuccess) return fail(AXH_ERR_QUEUE_SUBMIT, hip_msg("hipEventElapsedTime", e));
+  return ok();
+}
+
+void axh_event_destroy(axh_event *ev) {
+  if (ev) hipEventDestroy(reinterpret_cast<hipEvent_t>(ev));
 }
 
 axh_status axh_synchronize(axh_context *ctx, void *stream) {

@@ -1,0 +1,478 @@
+// Strategy-hole autotuner: XXH3-64 variant ids, mixed-radix enumeration and
+// grid search with caller callbacks (crates/axc-optimize of
+// rudybear/axiom-compute), plus a HIP-timed sweep of the Q4_K matvec
+// variants built on the same grid search.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <numeric>
+#include <string>
+#include <vector>
+
+#include "axh_internal.h"
+#include "axh_tune.h"
+
+namespace axh {
+namespace {
+
+// ---------------------------------------------------------------------------
+// XXH3 64-bit, seed 0, default 192-byte secret (the published XXH3 algorithm;
+// variant ids must equal the reference's xxhash-rust xxh3_64).
+// ---------------------------------------------------------------------------
+constexpr uint64_t kP32_1 = 0x9E3779B1u, kP32_2 = 0x85EBCA77u, kP32_3 = 0xC2B2AE3Du;
+constexpr uint64_t kP64_1 = 0x9E3779B185EBCA87ull, kP64_2 = 0xC2B2AE3D27D4EB4Full,
+                   kP64_3 = 0x165667B19E3779F9ull, kP64_4 = 0x85EBCA77C2B2AE63ull,
+                   kP64_5 = 0x27D4EB2F165667C5ull;
+constexpr uint64_t kMx1 = 0x165667919E3779F9ull, kMx2 = 0x9FB21C651E98DF25ull;
+
+const uint8_t kSecret[192] = {
+    0xb8, 0xfe, 0x6c, 0x39, 0x23, 0xa4, 0x4b, 0xbe, 0x7c, 0x01, 0x81, 0x2c, 0xf7, 0x21, 0xad, 0x1c,
+    0xde, 0xd4, 0x6d, 0xe9, 0x83, 0x90, 0x97, 0xdb, 0x72, 0x40, 0xa4, 0xa4, 0xb7, 0xb3, 0x67, 0x1f,
+    0xcb, 0x79, 0xe6, 0x4e, 0xcc, 0xc0, 0xe5, 0x78, 0x82, 0x5a, 0xd0, 0x7d, 0xcc, 0xff, 0x72, 0x21,
+    0xb8, 0x08, 0x46, 0x74, 0xf7, 0x43, 0x24, 0x8e, 0xe0, 0x35, 0x90, 0xe6, 0x81, 0x3a, 0x26, 0x4c,
+    0x3c, 0x28, 0x52, 0xbb, 0x91, 0xc3, 0x00, 0xcb, 0x88, 0xd0, 0x65, 0x8b, 0x1b, 0x53, 0x2e, 0xa3,
+    0x71, 0x64, 0x48, 0x97, 0xa2, 0x0d, 0xf9, 0x4e, 0x38, 0x19, 0xef, 0x46, 0xa9, 0xde, 0xac, 0xd8,
+    0xa8, 0xfa, 0x76, 0x3f, 0xe3, 0x9c, 0x34, 0x3f, 0xf9, 0xdc, 0xbb, 0xc7, 0xc7, 0x0b, 0x4f, 0x1d,
+    0x8a, 0x51, 0xe0, 0x4b, 0xcd, 0xb4, 0x59, 0x31, 0xc8, 0x9f, 0x7e, 0xc9, 0xd9, 0x78, 0x73, 0x64,
+    0xea, 0xc5, 0xac, 0x83, 0x34, 0xd3, 0xeb, 0xc3, 0xc5, 0x81, 0xa0, 0xff, 0xfa, 0x13, 0x63, 0xeb,
+    0x17, 0x0d, 0xdd, 0x51, 0xb7, 0xf0, 0xda, 0x49, 0xd3, 0x16, 0x55, 0x26, 0x29, 0xd4, 0x68, 0x9e,
+    0x2b, 0x16, 0xbe, 0x58, 0x7d, 0x47, 0xa1, 0xfc, 0x8f, 0xf8, 0xb8, 0xd1, 0x7a, 0xd0, 0x31, 0xce,
+    0x45, 0xcb, 0x3a, 0x8f, 0x95, 0x16, 0x04, 0x28, 0xaf, 0xd7, 0xfb, 0xca, 0xbb, 0x4b, 0x40, 0x7e,
+};
+constexpr size_t kSecretLen = sizeof(kSecret);
+
+inline uint64_t rd64(const uint8_t *p) {
+  uint64_t v;
+  std::memcpy(&v, p, 8); // little-endian host (x86-64)
+  return v;
+}
+inline uint32_t rd32(const uint8_t *p) {
+  uint32_t v;
+  std::memcpy(&v, p, 4);
+  return v;
+}
+inline uint64_t rotl64(uint64_t v, int r) { return (v << r) | (v >> (64 - r)); }
+inline uint64_t bswap64(uint64_t v) { return __builtin_bswap64(v); }
+
+// low 64 bits XOR high 64 bits of the 128-bit product
+inline uint64_t mul_fold(uint64_t a, uint64_t b) {
+  const unsigned __int128 p = (unsigned __int128)a * b;
+  return (uint64_t)p ^ (uint64_t)(p >> 64);
+}
+
+inline uint64_t avalanche_xxh64(uint64_t h) {
+  h ^= h >> 33;
+  h *= kP64_2;
+  h ^= h >> 29;
+  h *= kP64_3;
+  h ^= h >> 32;
+  return h;
+}
+
+inline uint64_t avalanche_xxh3(uint64_t h) {
+  h ^= h >> 37;
+  h *= kMx1;
+  h ^= h >> 32;
+  return h;
+}
+
+inline uint64_t rrmxmx(uint64_t h, uint64_t len) {
+  h ^= rotl64(h, 49) ^ rotl64(h, 24);
+  h *= kMx2;
+  h ^= (h >> 35) + len;
+  h *= kMx2;
+  return h ^ (h >> 28);
+}
+
+inline uint64_t mix16(const uint8_t *in, const uint8_t *sec) {
+  return mul_fold(rd64(in) ^ rd64(sec), rd64(in + 8) ^ rd64(sec + 8));
+}
+
+inline void acc512(uint64_t acc[8], const uint8_t *in, const uint8_t *sec) {
+  for (int i = 0; i < 8; ++i) {
+    const uint64_t v = rd64(in + 8 * i);
+    const uint64_t k = v ^ rd64(sec + 8 * i);
+    acc[i ^ 1] += v;
+    acc[i] += (uint64_t)(uint32_t)k * (k >> 32);
+  }
+}
+
+uint64_t xxh3_long(const uint8_t *in, size_t len) {
+  uint64_t acc[8] = {kP32_3, kP64_1, kP64_2, kP64_3, kP64_4, kP32_2, kP64_5, kP32_1};
+  const size_t stripes_per_block = (kSecretLen - 64) / 8;
+  const size_t block = 64 * stripes_per_block;
+  const size_t n_blocks = (len - 1) / block;
+  for (size_t b = 0; b < n_blocks; ++b) {
+    for (size_t s = 0; s < stripes_per_block; ++s) acc512(acc, in + b * block + 64 * s, kSecret + 8 * s);
+    for (int i = 0; i < 8; ++i) { // scramble
+      uint64_t a = acc[i];
+      a ^= a >> 47;
+      a ^= rd64(kSecret + kSecretLen - 64 + 8 * i);
+      acc[i] = a * kP32_1;
+    }
+  }
+  const size_t stripes = ((len - 1) - block * n_blocks) / 64;
+  for (size_t s = 0; s < stripes; ++s) acc512(acc, in + n_blocks * block + 64 * s, kSecret + 8 * s);
+  acc512(acc, in + len - 64, kSecret + kSecretLen - 64 - 7);
+  uint64_t r = (uint64_t)len * kP64_1;
+  for (int i = 0; i < 4; ++i)
+    r += mul_fold(acc[2 * i] ^ rd64(kSecret + 11 + 16 * i), acc[2 * i + 1] ^ rd64(kSecret + 11 + 16 * i + 8));
+  return avalanche_xxh3(r);
+}
+
+uint64_t xxh3_64(const uint8_t *in, size_t len) {
+  if (len == 0) return avalanche_xxh64(rd64(kSecret + 56) ^ rd64(kSecret + 64));
+  if (len <= 3) {
+    const uint32_t combined = ((uint32_t)in[0] << 16) | ((uint32_t)in[len >> 1] << 24) |
+                              (uint32_t)in[len - 1] | ((uint32_t)len << 8);
+    const uint64_t flip = (uint64_t)(rd32(kSecret) ^ rd32(kSecret + 4));
+    return avalanche_xxh64((uint64_t)combined ^ flip);
+  }
+  if (len <= 8) {
+    const uint64_t flip = rd64(kSecret + 8) ^ rd64(kSecret + 16);
+    const uint64_t v = (uint64_t)rd32(in + len - 4) + ((uint64_t)rd32(in) << 32);
+    return rrmxmx(v ^ flip, len);
+  }
+  if (len <= 16) {
+    const uint64_t lo = rd64(in) ^ (rd64(kSecret + 24) ^ rd64(kSecret + 32));
+    const uint64_t hi = rd64(in + len - 8) ^ (rd64(kSecret + 40) ^ rd64(kSecret + 48));
+    return avalanche_xxh3((uint64_t)len + bswap64(lo) + hi + mul_fold(lo, hi));
+  }
+  if (len <= 128) {
+    uint64_t acc = (uint64_t)len * kP64_1;
+    if (len > 32) {
+      if (len > 64) {
+        if (len > 96) {
+          acc += mix16(in + 48, kSecret + 96);
+          acc += mix16(in + len - 64, kSecret + 112);
+        }
+        acc += mix16(in + 32, kSecret + 64);
+        acc += mix16(in + len - 48, kSecret + 80);
+      }
+      acc += mix16(in + 16, kSecret + 32);
+      acc += mix16(in + len - 32, kSecret + 48);
+    }
+    acc += mix16(in, kSecret);
+    acc += mix16(in + len - 16, kSecret + 16);
+    return avalanche_xxh3(acc);
+  }
+  if (len <= 240) {
+    uint64_t acc = (uint64_t)len * kP64_1;
+    const size_t rounds = len / 16;
+    for (size_t i = 0; i < 8; ++i) acc += mix16(in + 16 * i, kSecret + 16 * i);
+    acc = avalanche_xxh3(acc);
+    for (size_t i = 8; i < rounds; ++i) acc += mix16(in + 16 * i, kSecret + 16 * (i - 8) + 3);
+    acc += mix16(in + len - 16, kSecret + 136 - 17);
+    return avalanche_xxh3(acc);
+  }
+  return xxh3_long(in, len);
+}
+
+struct Sorted {
+  std::vector<uint32_t> order; // caller indices, by name
+  std::vector<uint64_t> radix;
+  uint64_t total = 0;
+};
+
+axh_status sort_holes(const axh_strategy_hole *holes, uint32_t n, Sorted &s) {
+  if (n == 0) return fail((axh_status)AXH_ERR_EMPTY_STRATEGY,
+                          "strategy map is empty (no holes to enumerate)");
+  if (!holes) return fail(AXH_ERR_INVALID_ARGUMENT, "holes is NULL");
+  s.order.resize(n);
+  std::iota(s.order.begin(), s.order.end(), 0u);
+  for (uint32_t i = 0; i < n; ++i)
+    if (!holes[i].name || !holes[i].candidates || holes[i].n_candidates == 0)
+      return fail(AXH_ERR_INVALID_ARGUMENT, "hole " + std::to_string(i) + " has no candidates");
+  std::sort(s.order.begin(), s.order.end(), [&](uint32_t a, uint32_t b) {
+    return std::strcmp(holes[a].name, holes[b].name) < 0;
+  });
+  for (uint32_t i = 1; i < n; ++i)
+    if (std::strcmp(holes[s.order[i - 1]].name, holes[s.order[i]].name) == 0)
+      return fail(AXH_ERR_INVALID_ARGUMENT,
+                  std::string("duplicate hole name '") + holes[s.order[i]].name + "'");
+  s.radix.resize(n);
+  s.total = 1;
+  for (uint32_t k = 0; k < n; ++k) {
+    s.radix[k] = holes[s.order[k]].n_candidates;
+    s.total = (s.total > UINT64_MAX / s.radix[k]) ? UINT64_MAX : s.total * s.radix[k];
+  }
+  return AXH_OK;
+}
+
+// Values (sorted-key order) and id of variant `ordinal`: the last key varies fastest.
+uint64_t variant_at(const axh_strategy_hole *holes, const Sorted &s, uint64_t ordinal,
+                    int64_t *values, std::vector<uint8_t> &enc) {
+  const uint32_t n = (uint32_t)s.order.size();
+  uint64_t rem = ordinal;
+  for (uint32_t k = n; k-- > 0;) {
+    const uint64_t idx = rem % s.radix[k];
+    rem /= s.radix[k];
+    values[k] = holes[s.order[k]].candidates[idx];
+  }
+  enc.clear();
+  for (uint32_t k = 0; k < n; ++k) {
+    const char *name = holes[s.order[k]].name;
+    const uint32_t len = (uint32_t)std::strlen(name);
+    uint8_t b[8];
+    std::memcpy(b, &len, 4);
+    enc.insert(enc.end(), b, b + 4);
+    enc.insert(enc.end(), name, name + len);
+    std::memcpy(b, &values[k], 8);
+    enc.insert(enc.end(), b, b + 8);
+  }
+  return xxh3_64(enc.data(), enc.size());
+}
+
+} // namespace
+} // namespace axh
+
+using namespace axh;
+
+extern "C" {
+
+uint64_t axh_xxh3_64(const void *data, size_t len) {
+  return xxh3_64(static_cast<const uint8_t *>(data), data ? len : 0);
+}
+
+axh_status axh_enumerate_strategy(const axh_strategy_hole *holes, uint32_t n_holes,
+                                  uint64_t *n_variants_out, uint32_t *sorted_hole_index_out,
+                                  int64_t *values_out, uint64_t *variant_ids_out,
+                                  uint64_t capacity) {
+  Sorted s;
+  axh_status st = sort_holes(holes, n_holes, s);
+  if (st != AXH_OK) return st;
+  if (n_variants_out) *n_variants_out = s.total;
+  if (sorted_hole_index_out)
+    for (uint32_t k = 0; k < n_holes; ++k) sorted_hole_index_out[k] = s.order[k];
+  if (capacity == 0 || (!values_out && !variant_ids_out)) return ok();
+  if (capacity < s.total)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "capacity " + std::to_string(capacity) + " < " +
+                                              std::to_string(s.total) + " variants");
+  std::vector<int64_t> vals(n_holes);
+  std::vector<uint8_t> enc;
+  for (uint64_t v = 0; v < s.total; ++v) {
+    const uint64_t id = variant_at(holes, s, v, vals.data(), enc);
+    if (values_out) std::memcpy(values_out + v * n_holes, vals.data(), 8 * n_holes);
+    if (variant_ids_out) variant_ids_out[v] = id;
+  }
+  return ok();
+}
+
+axh_status axh_grid_search(const axh_strategy_hole *holes, uint32_t n_holes,
+                           const axh_correctness_policy *policy, axh_correctness_fn correctness,
+                           axh_bench_fn bench, void *user, axh_variant_result *results,
+                           uint64_t capacity, axh_grid_search_result *out) {
+  if (n_holes == 0)
+    return fail((axh_status)AXH_ERR_NO_STRATEGY, "kernel has no @strategy annotation");
+  if (!bench || !out) return fail(AXH_ERR_INVALID_ARGUMENT, "bench and out are required");
+  Sorted s;
+  axh_status st = sort_holes(holes, n_holes, s);
+  if (st != AXH_OK)
+    return fail((axh_status)AXH_ERR_ENUMERATE_FAILED,
+                std::string("strategy enumeration failed: ") + axh_last_error());
+  if (!results || capacity < s.total)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "results must hold " + std::to_string(s.total) +
+                                              " variants");
+  const bool check = policy && policy->kind != AXH_POLICY_NONE && correctness;
+  std::vector<int64_t> vals(n_holes);
+  std::vector<uint8_t> enc;
+  char err[120];
+  for (uint64_t v = 0; v < s.total; ++v) {
+    axh_variant_result &r = results[v];
+    std::memset(&r, 0, sizeof(r));
+    r.ordinal = v;
+    r.variant_id = variant_at(holes, s, v, vals.data(), enc);
+    err[0] = 0;
+    if (check && correctness(user, v, vals.data(), n_holes, err, sizeof(err)) != 0) {
+      r.outcome = AXH_OUTCOME_CORRECTNESS_REJECTED;
+      std::snprintf(r.message, sizeof(r.message), "%s", err);
+      continue;
+    }
+    err[0] = 0;
+    if (bench(user, v, vals.data(), n_holes, &r.stats, err, sizeof(err)) != 0) {
+      r.outcome = AXH_OUTCOME_FAILED;
+      std::snprintf(r.message, sizeof(r.message), "%s", err);
+      continue;
+    }
+    r.outcome = AXH_OUTCOME_OK;
+  }
+  std::memset(out, 0, sizeof(*out));
+  out->n_results = s.total;
+  out->warned_large_product = s.total > AXH_CARTESIAN_WARN_THRESHOLD;
+  const axh_variant_result *best = nullptr;
+  for (uint64_t v = 0; v < s.total; ++v) // strict < keeps the lowest ordinal on ties
+    if (results[v].outcome == AXH_OUTCOME_OK &&
+        (!best || results[v].stats.median_ns < best->stats.median_ns))
+      best = &results[v];
+  if (!best) {
+    for (uint64_t fo = 0; fo < 4 && fo < s.total; ++fo) { // R3 fallback chain
+      out->winner_ordinal = fo;
+      out->winner_variant_id = results[fo].variant_id;
+      out->fallback_used = 1;
+      return ok();
+    }
+    return fail((axh_status)AXH_ERR_NO_SUCCESSFUL_VARIANTS, "no variant benchmarked successfully");
+  }
+  out->winner_ordinal = best->ordinal;
+  out->winner_variant_id = best->variant_id;
+  return ok();
+}
+
+// ---- HIP-timed sweep of the compiled Q4_K matvec variants ------------------
+namespace {
+struct Q4kTuneCtx {
+  axh_context *ctx;
+  const void *q;
+  const float *x;
+  float *y;
+  float *y_ref; // device scratch for the reference output
+  uint32_t n_rows, sb;
+  uint32_t samples;
+  double tol;
+  std::vector<float> ref_host;
+};
+
+// values in sorted key order: nontemporal, prefetch, rows_per_wave, waves_per_workgroup
+axh_q4_variant to_variant(const int64_t *v) {
+  axh_q4_variant r{};
+  r.nontemporal = (uint32_t)v[0];
+  r.prefetch = (uint32_t)v[1];
+  r.rows_per_wave = (uint32_t)v[2];
+  r.waves_per_workgroup = (uint32_t)v[3];
+  return r;
+}
+
+bool compiled(const axh_q4_variant &v) {
+  const uint32_t n = axh_q4k_matvec_variant_count();
+  for (uint32_t i = 0; i < n; ++i) {
+    axh_q4_variant c{};
+    axh_q4k_matvec_variant_at(i, &c);
+    if (c.rows_per_wave == v.rows_per_wave && c.waves_per_workgroup == v.waves_per_workgroup &&
+        c.prefetch == v.prefetch && c.nontemporal == v.nontemporal)
+      return true;
+  }
+  return false;
+}
+
+int tune_correct(void *user, uint64_t, const int64_t *vals, uint32_t, char *err, size_t cap) {
+  Q4kTuneCtx &t = *static_cast<Q4kTuneCtx *>(user);
+  const axh_q4_variant v = to_variant(vals);
+  if (!compiled(v)) {
+    std::snprintf(err, cap, "variant not compiled");
+    return 1;
+  }
+  if (axh_q4k_matvec(t.ctx, t.q, t.x, t.y, t.n_rows, t.sb, &v, nullptr) != AXH_OK ||
+      axh_synchronize(t.ctx, nullptr) != AXH_OK) {
+    std::snprintf(err, cap, "%s", axh_last_error());
+    return 1;
+  }
+  std::vector<float> got(t.n_rows);
+  if (axh_download(t.ctx, got.data(), t.y, 4u * t.n_rows) != AXH_OK) {
+    std::snprintf(err, cap, "%s", axh_last_error());
+    return 1;
+  }
+  if (t.tol == 0.0) {
+    if (std::memcmp(got.data(), t.ref_host.data(), 4u * t.n_rows) != 0) {
+      std::snprintf(err, cap, "output differs bitwise from the default variant");
+      return 1;
+    }
+    return 0;
+  }
+  double num = 0, den = 0;
+  for (uint32_t i = 0; i < t.n_rows; ++i) {
+    const double d = (double)got[i] - (double)t.ref_host[i];
+    num += d * d;
+    den += (double)t.ref_host[i] * t.ref_host[i];
+  }
+  if (std::sqrt(num) > t.tol * std::sqrt(den) + 1e-30) {
+    std::snprintf(err, cap, "norm-wise relative error %.3g > %.3g", std::sqrt(num / (den + 1e-300)),
+                  t.tol);
+    return 1;
+  }
+  return 0;
+}
+
+int tune_bench(void *user, uint64_t, const int64_t *vals, uint32_t, axh_sample_stats *out,
+               char *err, size_t cap) {
+  Q4kTuneCtx &t = *static_cast<Q4kTuneCtx *>(user);
+  const axh_q4_variant v = to_variant(vals);
+  if (!compiled(v)) {
+    std::snprintf(err, cap, "variant not compiled");
+    return 1;
+  }
+  hipStream_t s = t.ctx->core->stream;
+  std::vector<uint64_t> ns;
+  hipEvent_t e0, e1;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+    std::snprintf(err, cap, "hipEventCreate failed");
+    return 1;
+  }
+  for (uint32_t i = 0; i < 3; ++i) axh_q4k_matvec(t.ctx, t.q, t.x, t.y, t.n_rows, t.sb, &v, s);
+  const uint32_t reps = 20;
+  for (uint32_t smp = 0; smp < t.samples; ++smp) {
+    hipEventRecord(e0, s);
+    for (uint32_t i = 0; i < reps; ++i)
+      if (axh_q4k_matvec(t.ctx, t.q, t.x, t.y, t.n_rows, t.sb, &v, s) != AXH_OK) {
+        std::snprintf(err, cap, "%s", axh_last_error());
+        hipEventDestroy(e0);
+        hipEventDestroy(e1);
+        return 1;
+      }
+    hipEventRecord(e1, s);
+    if (axh_synchronize(t.ctx, nullptr) != AXH_OK) {
+      std::snprintf(err, cap, "%s", axh_last_error());
+      hipEventDestroy(e0);
+      hipEventDestroy(e1);
+      return 1;
+    }
+    float ms = 0;
+    hipEventElapsedTime(&ms, e0, e1);
+    ns.push_back((uint64_t)((double)ms * 1e6 / reps));
+  }
+  hipEventDestroy(e0);
+  hipEventDestroy(e1);
+  std::sort(ns.begin(), ns.end());
+  out->median_ns = ns[ns.size() / 2];
+  out->min_ns = ns.front();
+  out->max_ns = ns.back();
+  out->n_samples = (uint32_t)ns.size();
+  return 0;
+}
+} // namespace
+
+axh_status axh_q4k_matvec_autotune(axh_context *ctx, const void *q, const float *x, float *y,
+                                   uint32_t n_rows, uint32_t sb_per_row, uint32_t samples,
+                                   double tol, axh_q4_variant *best, uint64_t *best_median_ns) {
+  if (!ctx || !best || n_rows == 0 || sb_per_row == 0)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "autotune needs a context, a shape and an output");
+  // reference output from the default variant
+  axh_status st = axh_q4k_matvec(ctx, q, x, y, n_rows, sb_per_row, nullptr, nullptr);
+  if (st != AXH_OK) return st;
+  if ((st = axh_synchronize(ctx, nullptr)) != AXH_OK) return st;
+  Q4kTuneCtx t{ctx, q, x, y, nullptr, n_rows, sb_per_row, samples ? samples : 5, tol, {}};
+  t.ref_host.resize(n_rows);
+  if ((st = axh_download(ctx, t.ref_host.data(), y, 4u * n_rows)) != AXH_OK) return st;
+  const int64_t rpw[] = {1, 2, 4}, nw[] = {4, 8, 16}, pf[] = {2, 4, 7}, nt[] = {2, 1};
+  const axh_strategy_hole holes[] = {{"rows_per_wave", rpw, 3},
+                                     {"waves_per_workgroup", nw, 3},
+                                     {"prefetch", pf, 3},
+                                     {"nontemporal", nt, 2}};
+  uint64_t n = 0;
+  if ((st = axh_enumerate_strategy(holes, 4, &n, nullptr, nullptr, nullptr, 0)) != AXH_OK) return st;
+  std::vector<axh_variant_result> res(n);
+  axh_correctness_policy pol{AXH_POLICY_EQUIV_FP_TOL, 0};
+  axh_grid_search_result out{};
+  st = axh_grid_search(holes, 4, &pol, tune_correct, tune_bench, &t, res.data(), n, &out);
+  if (st != AXH_OK) return st;
+  if (out.fallback_used) return fail((axh_status)AXH_ERR_NO_SUCCESSFUL_VARIANTS, "no variant ran");
+  std::vector<int64_t> vals(4 * n);
+  axh_enumerate_strategy(holes, 4, &n, nullptr, vals.data(), nullptr, n);
+  *best = to_variant(&vals[4 * out.winner_ordinal]);
+  if (best_median_ns) *best_median_ns = res[out.winner_ordinal].stats.median_ns;
+  return ok();
+}
+
+} // extern "C"

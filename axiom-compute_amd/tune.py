@@ -1,0 +1,248 @@
+"""Python mirror of the autotuner surface (crates/axc-optimize) over axh_tune.h.
+
+  enumerate_strategy(holes) -> list[StrategyVariant]        (enumerator.rs:68-129)
+  grid_search(holes, policy, correctness_fn, bench_fn)       (grid_search.rs:158-283)
+  q4k_matvec_autotune(ctx, q, x, y, n_rows, sb_per_row)      (HIP-timed variant sweep)
+
+`holes` is a mapping name -> candidate list (source order; index 0 is the
+baseline), like StrategyHoles.map.  bench_fn(assignments) returns SampleStats
+or raises; correctness_fn(assignments) returns None or raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+from typing import Callable, Mapping, Optional, Sequence
+
+from . import axh as _axh
+
+CARTESIAN_WARN_THRESHOLD = 100
+
+
+class _Hole(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("candidates", ctypes.POINTER(ctypes.c_int64)),
+                ("n_candidates", ctypes.c_uint32)]
+
+
+class _Policy(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_uint32), ("ulp", ctypes.c_uint32)]
+
+
+class _Stats(ctypes.Structure):
+    _fields_ = [("median_ns", ctypes.c_uint64), ("min_ns", ctypes.c_uint64),
+                ("max_ns", ctypes.c_uint64), ("n_samples", ctypes.c_uint32)]
+
+
+class _Result(ctypes.Structure):
+    _fields_ = [("ordinal", ctypes.c_uint64), ("variant_id", ctypes.c_uint64),
+                ("outcome", ctypes.c_uint32), ("stats", _Stats), ("message", ctypes.c_char * 120)]
+
+
+class _Summary(ctypes.Structure):
+    _fields_ = [("winner_ordinal", ctypes.c_uint64), ("winner_variant_id", ctypes.c_uint64),
+                ("fallback_used", ctypes.c_uint32), ("warned_large_product", ctypes.c_uint32),
+                ("n_results", ctypes.c_uint64)]
+
+
+_BENCH = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64,
+                          ctypes.POINTER(ctypes.c_int64), ctypes.c_uint32,
+                          ctypes.POINTER(_Stats), ctypes.c_void_p, ctypes.c_size_t)
+_CORRECT = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64,
+                            ctypes.POINTER(ctypes.c_int64), ctypes.c_uint32,
+                            ctypes.c_void_p, ctypes.c_size_t)
+
+_configured = False
+
+
+def _lib():
+    global _configured
+    lib = _axh.load_library()
+    if not _configured:
+        c = ctypes
+        lib.axh_xxh3_64.restype = c.c_uint64
+        lib.axh_xxh3_64.argtypes = [c.c_void_p, c.c_size_t]
+        lib.axh_enumerate_strategy.restype = c.c_int
+        lib.axh_enumerate_strategy.argtypes = [c.POINTER(_Hole), c.c_uint32,
+                                               c.POINTER(c.c_uint64), c.POINTER(c.c_uint32),
+                                               c.POINTER(c.c_int64), c.POINTER(c.c_uint64),
+                                               c.c_uint64]
+        lib.axh_grid_search.restype = c.c_int
+        lib.axh_grid_search.argtypes = [c.POINTER(_Hole), c.c_uint32, c.POINTER(_Policy),
+                                        _CORRECT, _BENCH, c.c_void_p, c.POINTER(_Result),
+                                        c.c_uint64, c.POINTER(_Summary)]
+        lib.axh_q4k_matvec_autotune.restype = c.c_int
+        lib.axh_q4k_matvec_autotune.argtypes = [c.c_void_p, c.c_void_p, c.c_void_p, c.c_void_p,
+                                                c.c_uint32, c.c_uint32, c.c_uint32, c.c_double,
+                                                c.POINTER(_axh._Variant),
+                                                c.POINTER(c.c_uint64)]
+        _configured = True
+    return lib
+
+
+class TuneError(_axh.DispatchError):
+    NAMES = {40: "EmptyStrategy", 41: "UnknownHole", 42: "NoStrategy", 43: "EnumerateFailed",
+             44: "NoSuccessfulVariants"}
+
+    def __init__(self, status: int, message: str):
+        super().__init__(status, message)
+        self.variant = self.NAMES.get(self.status, self.variant)
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        raise TuneError(status, _lib().axh_last_error().decode(errors="replace"))
+
+
+def xxh3_64(data: bytes) -> int:
+    b = bytes(data)
+    return int(_lib().axh_xxh3_64(ctypes.c_char_p(b) if b else None, len(b)))
+
+
+@dataclass(frozen=True)
+class StrategyVariant:
+    ordinal: int
+    variant_id: int
+    assignments: dict
+
+
+@dataclass
+class SampleStats:
+    median_ns: int
+    min_ns: int
+    max_ns: int
+    n_samples: int
+
+
+@dataclass
+class CorrectnessPolicy:
+    """NONE, BIT_EXACT or EQUIV_FP_TOL(ulp) (grid_search.rs:55-66)."""
+
+    kind: int = 0
+    ulp: int = 0
+    NONE = 0
+    BIT_EXACT = 1
+    EQUIV_FP_TOL = 2
+
+
+@dataclass
+class VariantResult:
+    ordinal: int
+    variant_id: int
+    assignments: dict
+    outcome: str  # "Ok" | "Failed" | "CorrectnessRejected"
+    stats: Optional[SampleStats]
+    message: str
+
+
+@dataclass
+class GridSearchResult:
+    winner_ordinal: int
+    winner_variant_id: int
+    winner_assignments: dict
+    results: list
+    fallback_used: bool
+    warnings: list = field(default_factory=list)
+
+
+def _holes(holes: Mapping[str, Sequence[int]]):
+    names = list(holes)
+    keep = []
+    arr = (_Hole * max(1, len(names)))()
+    for i, n in enumerate(names):
+        cand = (ctypes.c_int64 * max(1, len(holes[n])))(*holes[n])
+        nb = n.encode()
+        keep += [cand, nb]
+        arr[i] = _Hole(nb, ctypes.cast(cand, ctypes.POINTER(ctypes.c_int64)), len(holes[n]))
+    return arr, names, keep
+
+
+def enumerate_strategy(holes: Mapping[str, Sequence[int]]) -> list:
+    arr, names, keep = _holes(holes)
+    lib = _lib()
+    n = ctypes.c_uint64()
+    order = (ctypes.c_uint32 * max(1, len(names)))()
+    _check(lib.axh_enumerate_strategy(arr, len(names), ctypes.byref(n), order, None, None, 0))
+    total = n.value
+    vals = (ctypes.c_int64 * max(1, total * len(names)))()
+    ids = (ctypes.c_uint64 * max(1, total))()
+    _check(lib.axh_enumerate_strategy(arr, len(names), ctypes.byref(n), order, vals, ids, total))
+    keys = [names[order[k]] for k in range(len(names))]
+    out = []
+    for v in range(total):
+        a = {keys[k]: int(vals[v * len(keys) + k]) for k in range(len(keys))}
+        out.append(StrategyVariant(v, int(ids[v]), a))
+    return out
+
+
+_OUTCOMES = {0: "Ok", 1: "Failed", 2: "CorrectnessRejected"}
+
+
+def grid_search(holes: Mapping[str, Sequence[int]], policy: CorrectnessPolicy,
+                correctness_fn: Optional[Callable[[dict], None]],
+                bench_fn: Callable[[dict], SampleStats]) -> GridSearchResult:
+    arr, names, keep = _holes(holes)
+    lib = _lib()
+    n_keys = len(names)
+    variants = enumerate_strategy(holes) if n_keys else []
+    keys = list(variants[0].assignments) if variants else []
+
+    def _assign(vals, nh):
+        return {keys[k]: int(vals[k]) for k in range(nh)}
+
+    def _write(buf, cap, msg):
+        raw = str(msg).encode(errors="replace")[: max(0, cap - 1)]
+        ctypes.memmove(buf, raw + b"\0", len(raw) + 1)
+
+    @_BENCH
+    def cb_bench(user, ordinal, vals, nh, out, err, cap):
+        try:
+            s = bench_fn(_assign(vals, nh))
+            out[0].median_ns, out[0].min_ns = s.median_ns, s.min_ns
+            out[0].max_ns, out[0].n_samples = s.max_ns, s.n_samples
+            return 0
+        except Exception as e:  # reported as BenchOutcome::Failed
+            _write(err, cap, e)
+            return 1
+
+    @_CORRECT
+    def cb_correct(user, ordinal, vals, nh, err, cap):
+        try:
+            correctness_fn(_assign(vals, nh))
+            return 0
+        except Exception as e:  # reported as CorrectnessRejected
+            _write(err, cap, e)
+            return 1
+
+    total = len(variants)
+    res = (_Result * max(1, total))()
+    summ = _Summary()
+    pol = _Policy(policy.kind, policy.ulp)
+    _check(lib.axh_grid_search(arr, n_keys, ctypes.byref(pol),
+                               cb_correct if correctness_fn else _CORRECT(),
+                               cb_bench, None, res, total, ctypes.byref(summ)))
+    results = []
+    for v in range(total):
+        r = res[v]
+        st = SampleStats(r.stats.median_ns, r.stats.min_ns, r.stats.max_ns, r.stats.n_samples)
+        results.append(VariantResult(int(r.ordinal), int(r.variant_id), variants[v].assignments,
+                                     _OUTCOMES[r.outcome], st if r.outcome == 0 else None,
+                                     r.message.decode(errors="replace")))
+    warnings = []
+    if summ.warned_large_product:
+        warnings.append(f"Cartesian product size {total} exceeds CARTESIAN_WARN_THRESHOLD "
+                        f"({CARTESIAN_WARN_THRESHOLD}); grid search may take a long time")
+    w = int(summ.winner_ordinal)
+    return GridSearchResult(w, int(summ.winner_variant_id), variants[w].assignments, results,
+                            bool(summ.fallback_used), warnings)
+
+
+def q4k_matvec_autotune(ctx, q, x, y, n_rows: int, sb_per_row: int, samples: int = 5,
+                        tol: float = 1e-3):
+    """Sweep the compiled Q4_K matvec variants on resident buffers; returns
+    (Variant, median ns per call)."""
+    v = _axh._Variant()
+    ns = ctypes.c_uint64()
+    _check(_lib().axh_q4k_matvec_autotune(ctx.raw, _axh._ptr(q), _axh._ptr(x), _axh._ptr(y),
+                                          n_rows, sb_per_row, samples, tol, ctypes.byref(v),
+                                          ctypes.byref(ns)))
+    return _axh.Variant(v.rows_per_wave, v.waves_per_workgroup, v.prefetch, v.nontemporal), int(ns.value)

@@ -74,7 +74,6 @@ def main() -> int:
         return 2
 
     import numpy as np
-    import torch
 
     import __graft_entry__
     from oracle import oracle as O
@@ -111,31 +110,30 @@ def main() -> int:
         print(json.dumps({"error": "parity failure", "report": rep}), file=sys.stderr)
         return 1
 
-    stream = torch.cuda.ExternalStream(ctx.stream)
+    # Timed region: K back-to-back calls on the context stream, bracketed by
+    # device synchronisation and HIP events recorded on that same stream.
     for i in range(args.warmup):
         ctx.q4k_matvec(copies[i % n_copies], dx, dy, rows, sb, variant)
-    ctx.synchronize()
-    torch.cuda.synchronize()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    ev0.record(stream)
+    ctx.device_synchronize()
+    ev0, ev1 = ctx.event(), ctx.event()
+    ev0.record()
     for i in range(args.steps):
         ctx.q4k_matvec(copies[i % n_copies], dx, dy, rows, sb, variant)
-    ev1.record(stream)
+    ev1.record()
     ev1.synchronize()
-    ctx.synchronize()
-    torch.cuda.synchronize()
-    total_ms = ev0.elapsed_time(ev1)
+    ctx.device_synchronize()
+    total_ms = ev0.elapsed_ms(ev1)
     us_per_call = total_ms * 1000.0 / args.steps
     gbs = weight_bytes / (us_per_call * 1e-6) / 1e9
 
     if args.calibrate_copy:
-        # A plain copy of exactly weight_bytes, for scaling FETCH_SIZE/WRITE_SIZE.
-        src = torch.empty(weight_bytes, dtype=torch.uint8, device="cuda")
-        dst = torch.empty_like(src)
+        # A plain copy of exactly weight_bytes (hipMemcpy device-to-device
+        # through the runtime's copy kernel), for scaling FETCH_SIZE/WRITE_SIZE.
+        dst = ctx.alloc(weight_bytes)
         for _ in range(10):
-            dst.copy_(src)
-        torch.cuda.synchronize()
+            ctx.copy_device(dst, copies[0], weight_bytes)
+        ctx.device_synchronize()
+        dst.close()
 
     cpu = cpu_baseline(O, q, x, rows, sb, args.cpu_seconds) if args.cpu_seconds > 0 else None
     out = {

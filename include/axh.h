@@ -139,11 +139,26 @@ axh_status axh_buffer_alloc(axh_context *ctx, size_t bytes, void **device_ptr);
 axh_status axh_buffer_free(axh_context *ctx, void *device_ptr);
 axh_status axh_upload(axh_context *ctx, void *device_dst, const void *host_src, size_t bytes);
 axh_status axh_download(axh_context *ctx, void *host_dst, const void *device_src, size_t bytes);
+/* Device-to-device copy on the context stream; returns when complete. */
+axh_status axh_copy_device(axh_context *ctx, void *device_dst, const void *device_src, size_t bytes);
 axh_status axh_launch(axh_context *ctx, axh_kernel *k, const uint32_t workgroups[3],
                       void *const *device_buffers, size_t n_buffers, const void *push_constants,
                       size_t push_constant_bytes, void *stream);
 /* Waits for `stream` with the context's fence timeout (AXH_ERR_FENCE_TIMEOUT). */
 axh_status axh_synchronize(axh_context *ctx, void *stream);
+/* Waits for all work on the context's device, without a timeout. */
+axh_status axh_device_synchronize(axh_context *ctx);
+
+/* ---- timing ----------------------------------------------------------------
+ * HIP events on the context's runtime, for timing launches on a stream
+ * (the reference times dispatches on the host only; GPU timestamps are the
+ * measurement this build reports). */
+typedef struct axh_event axh_event;
+axh_status axh_event_create(axh_context *ctx, axh_event **out);
+axh_status axh_event_record(axh_context *ctx, axh_event *ev, void *stream);
+axh_status axh_event_synchronize(axh_context *ctx, axh_event *ev);
+axh_status axh_event_elapsed_ms(axh_event *start, axh_event *end, float *ms);
+void axh_event_destroy(axh_event *ev);
 
 /* ---- Q4 dequant-matvec operations ------------------------------------------
  * Strategy holes of the matvec kernels (the reference's @strategy surface,

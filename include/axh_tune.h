@@ -1,0 +1,116 @@
+/*
+ * axh_tune: the @strategy-hole autotuner surface of rudybear/axiom-compute
+ * (crates/axc-optimize) over plain C types.  Holes are named integer
+ * candidate lists; a variant is one assignment; the caller's bench and
+ * correctness callbacks receive the assignment values (the HIP counterpart of
+ * the reference passing resolved SPIR-V to its BenchFn/CorrectnessFn).
+ */
+#ifndef AXH_TUNE_H
+#define AXH_TUNE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "axh.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes beyond axh_status for the autotuner (EnumerateError and
+ * GridSearchError, crates/axc-optimize/src/lib.rs:35-52). */
+enum {
+    AXH_ERR_EMPTY_STRATEGY = 40,          /* EnumerateError::EmptyStrategy        */
+    AXH_ERR_UNKNOWN_HOLE = 41,            /* EnumerateError::UnknownHole          */
+    AXH_ERR_NO_STRATEGY = 42,             /* GridSearchError::NoStrategy          */
+    AXH_ERR_ENUMERATE_FAILED = 43,        /* GridSearchError::EnumerateFailed     */
+    AXH_ERR_NO_SUCCESSFUL_VARIANTS = 44   /* GridSearchError::NoSuccessfulVariants */
+};
+
+/* CARTESIAN_WARN_THRESHOLD (crates/axc-optimize/src/enumerator.rs:42). */
+#define AXH_CARTESIAN_WARN_THRESHOLD 100u
+
+typedef struct axh_strategy_hole {
+    const char *name;          /* UTF-8 hole name                */
+    const int64_t *candidates; /* source order; [0] is the baseline */
+    uint32_t n_candidates;
+} axh_strategy_hole;
+
+/* XXH3 64-bit hash, seed 0 (the variant_id hash, xxhash-rust xxh3_64). */
+uint64_t axh_xxh3_64(const void *data, size_t len);
+
+/* enumerate_strategy (enumerator.rs:68-129).  Holes are ordered by name
+ * (byte-wise, as a BTreeMap); variants walk the mixed-radix product with the
+ * last key varying fastest; variant_id = xxh3_64 over, per key in order,
+ * u32le(len(name)) || name || i64le(value).
+ *   sorted_hole_index_out[k] = caller index of the k-th key (n_holes entries)
+ *   values_out[v * n_holes + k] = value of key k in variant v
+ *   variant_ids_out[v]
+ * With capacity 0 (or NULL outputs) only *n_variants_out is filled. */
+axh_status axh_enumerate_strategy(const axh_strategy_hole *holes, uint32_t n_holes,
+                                  uint64_t *n_variants_out, uint32_t *sorted_hole_index_out,
+                                  int64_t *values_out, uint64_t *variant_ids_out,
+                                  uint64_t capacity);
+
+/* CorrectnessPolicy (grid_search.rs:55-66). */
+enum { AXH_POLICY_NONE = 0, AXH_POLICY_BIT_EXACT = 1, AXH_POLICY_EQUIV_FP_TOL = 2 };
+typedef struct axh_correctness_policy {
+    uint32_t kind;
+    uint32_t ulp; /* EquivFpTol */
+} axh_correctness_policy;
+
+/* SampleStats (grid_search.rs:80-90). */
+typedef struct axh_sample_stats {
+    uint64_t median_ns, min_ns, max_ns;
+    uint32_t n_samples;
+} axh_sample_stats;
+
+/* BenchOutcome (grid_search.rs:93-101). */
+enum { AXH_OUTCOME_OK = 0, AXH_OUTCOME_FAILED = 1, AXH_OUTCOME_CORRECTNESS_REJECTED = 2 };
+
+/* Callbacks: return 0 on success; on failure write a message into err. */
+typedef int (*axh_bench_fn)(void *user, uint64_t ordinal, const int64_t *values, uint32_t n_holes,
+                            axh_sample_stats *out, char *err, size_t err_cap);
+typedef int (*axh_correctness_fn)(void *user, uint64_t ordinal, const int64_t *values,
+                                  uint32_t n_holes, char *err, size_t err_cap);
+
+typedef struct axh_variant_result {
+    uint64_t ordinal;
+    uint64_t variant_id;
+    uint32_t outcome;     /* AXH_OUTCOME_* */
+    axh_sample_stats stats; /* valid when outcome == AXH_OUTCOME_OK */
+    char message[120];    /* failure reason, if any */
+} axh_variant_result;
+
+typedef struct axh_grid_search_result {
+    uint64_t winner_ordinal;
+    uint64_t winner_variant_id;
+    uint32_t fallback_used;
+    uint32_t warned_large_product; /* product > AXH_CARTESIAN_WARN_THRESHOLD */
+    uint64_t n_results;
+} axh_grid_search_result;
+
+/* grid_search (grid_search.rs:158-283): for every variant in ordinal order,
+ * run correctness (if policy != NONE and a callback is given), then bench.
+ * Winner = minimum median_ns among OK variants (ties: lowest ordinal).  If
+ * none is OK, fall back to ordinal 0 (then 1, 2, 3) with fallback_used = 1.
+ * results must hold the full product (see axh_enumerate_strategy). */
+axh_status axh_grid_search(const axh_strategy_hole *holes, uint32_t n_holes,
+                           const axh_correctness_policy *policy, axh_correctness_fn correctness,
+                           axh_bench_fn bench, void *user, axh_variant_result *results,
+                           uint64_t capacity, axh_grid_search_result *out);
+
+/* Timed sweep of the compiled Q4_K matvec variants on resident buffers:
+ * each variant is checked against the default variant's output (relative
+ * 1e-3 norm-wise, or bit-exact when tol == 0) and timed over `samples`
+ * back-to-back calls with HIP events; the fastest passing variant is
+ * written to *best.  A wrapper of axh_grid_search whose holes are
+ * rows_per_wave, waves_per_workgroup, prefetch and nontemporal. */
+axh_status axh_q4k_matvec_autotune(axh_context *ctx, const void *q, const float *x, float *y,
+                                   uint32_t n_rows, uint32_t sb_per_row, uint32_t samples,
+                                   double tol, axh_q4_variant *best, uint64_t *best_median_ns);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* AXH_TUNE_H */

@@ -1,0 +1,200 @@
+"""GPU behaviour of the runtime boundary (marked `gpu`): handle cache, buffer
+pool growth, handle lifetime, typed errors on a live device, the completion
+timeout, concurrency, event timing and the autotuner.  Behaviour spec:
+crates/axc-runtime/tests (handle reuse, pow2 growth, error paths,
+kernel_handle_outlives_context.rs:24, amortisation) of the reference."""
+from __future__ import annotations
+
+import struct
+import sys
+import threading
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _plan(axc, n=3, pc=4, wg=64):
+    acc = [axc.axh.ACCESS_READ_ONLY] * (n - 1) + [axc.axh.ACCESS_READ_WRITE]
+    return axc.BindingPlan(acc, pc, (wg, 1, 1))
+
+
+def _q4km_handle(ctx, axc):
+    return ctx.prepare_kernel(axc.builtin_code_object(), _plan(axc), 4, "q4km_dequant_matvec")
+
+
+def test_prepare_twice_returns_cached_handle(ctx, axc):
+    h1 = _q4km_handle(ctx, axc)
+    h2 = _q4km_handle(ctx, axc)
+    assert h1.raw == h2.raw and h1.cache_key == h2.cache_key
+    h1.release()
+    # still alive through h2
+    q, x = O.generate_q4km_test_data(4, 0xDEADBEEF)
+    out = ctx.dispatch_handle(h2, (1, 1, 1), [q.tobytes(), x.tobytes(), b""], [0, 0, 4],
+                              struct.pack("<I", 4))
+    assert O.reference_rel_err(struct.unpack("<f", out[2])[0], O.q4k_dot(q, x, 4)) < 1e-3
+    h2.release()
+    h3 = _q4km_handle(ctx, axc)  # prepared again after the last release
+    assert h3.raw
+    h3.release()
+
+
+def test_buffer_pool_grows_to_pow2_and_never_shrinks(ctx, axc):
+    h = _q4km_handle(ctx, axc)
+    for n in (1, 2, 1):
+        q, x = O.generate_q4km_test_data(n, 7)
+        ctx.dispatch_handle(h, (1, 1, 1), [q.tobytes(), x.tobytes(), b""], [0, 0, 4],
+                            struct.pack("<I", n))
+    # n=2 sized the pools: q 288 -> 512, x 2048 -> 2048, y max(4,4) -> 4
+    assert (h.pool_bytes(0), h.pool_bytes(1), h.pool_bytes(2)) == (512, 2048, 4)
+    h.release()
+
+
+def test_handle_outlives_context(axc):
+    """AT-827: drop the context first, then the handle; no use after free."""
+    c = axc.HipContext.new()
+    h = _q4km_handle(c, axc)
+    q, x = O.generate_q4km_test_data(2, 1)
+    c.dispatch_handle(h, (1, 1, 1), [q.tobytes(), x.tobytes(), b""], [0, 0, 4],
+                      struct.pack("<I", 2))
+    c.close()
+    assert h.pool_bytes(0) == 512  # device state still valid through the handle
+    h.release()
+
+
+def test_dispatch_error_paths_on_device(ctx, axc):
+    h = _q4km_handle(ctx, axc)
+    with pytest.raises(axc.DispatchError) as e:
+        ctx.dispatch_handle(h, (1, 1, 1), [b"", b""], [0, 0, 4], struct.pack("<I", 0))
+    assert e.value.variant == "BindingCountMismatch"
+    with pytest.raises(axc.DispatchError) as e:
+        ctx.dispatch_handle(h, (1, 1, 1), [b"", b"", b""], [0, 0, 4], b"\0" * 8)
+    assert e.value.variant == "PushConstantSizeMismatch"
+    big = ctx.max_workgroup_count[0] + 1
+    if big <= 0xFFFFFFFF:
+        with pytest.raises(axc.DispatchError) as e:
+            ctx.dispatch_handle(h, (big, 1, 1), [b"", b"", b""], [0, 0, 4], struct.pack("<I", 0))
+        assert e.value.variant == "WorkgroupCountExceedsDeviceLimit"
+    h.release()
+
+
+def test_prepare_error_paths_on_device(ctx, axc):
+    with pytest.raises(axc.DispatchError) as e:
+        ctx.prepare_kernel(b"\x00" * 64, _plan(axc), 4, "q4km_dequant_matvec")
+    assert e.value.variant == "ShaderModuleCreationFailed"
+    with pytest.raises(axc.DispatchError) as e:
+        ctx.prepare_kernel(axc.builtin_code_object(), _plan(axc), 4, "no_such_entry")
+    assert e.value.variant == "PipelineCreationFailed"
+    with pytest.raises(axc.DispatchError) as e:
+        ctx.prepare_kernel(axc.builtin_code_object(), _plan(axc, pc=4), 8, "q4km_dequant_matvec")
+    assert e.value.variant == "PipelineLayoutFailed"
+
+
+def test_fence_timeout_is_reported_and_recoverable(axc):
+    """A bounded sleep kernel (~10 ms) against a 1 ms completion timeout."""
+    c = axc.HipContext.new_with_options(axc.HipContextOptions(fence_timeout_ms=1))
+    h = c.prepare_kernel(axc.builtin_code_object(),
+                         axc.BindingPlan([axc.axh.ACCESS_READ_WRITE], 4, (64, 1, 1)), 4, "axh_spin")
+    with pytest.raises(axc.DispatchError) as e:
+        c.dispatch_handle(h, (1, 1, 1), [b""], [4], struct.pack("<I", 3000))
+    assert e.value.variant == "FenceTimeout"
+    c.device_synchronize()  # unbounded wait: the bounded kernel ends by itself
+    h.release()
+    c.close()
+
+
+def test_spin_kernel_completes_within_default_timeout(ctx, axc):
+    h = ctx.prepare_kernel(axc.builtin_code_object(),
+                           axc.BindingPlan([axc.axh.ACCESS_READ_WRITE], 4, (64, 1, 1)), 4, "axh_spin")
+    out = ctx.dispatch_handle(h, (1, 1, 1), [b""], [4], struct.pack("<I", 10))
+    assert struct.unpack("<I", out[0])[0] == 10
+    h.release()
+
+
+@pytest.mark.parametrize("nbytes", [1, 4097, 70 * 1024 * 1024 + 3])
+def test_upload_download_round_trip(ctx, nbytes):
+    data = np.random.default_rng(nbytes).integers(0, 256, nbytes, dtype=np.uint8)
+    b = ctx.alloc(nbytes)
+    ctx.upload(b, data)
+    assert ctx.download(b, nbytes) == data.tobytes()
+    b.close()
+
+
+def test_concurrent_dispatch_on_two_handles(ctx, axc):
+    """Different handles dispatch in parallel; each handle serialises its own."""
+    co = axc.builtin_code_object()
+    h1 = ctx.prepare_kernel(co, _plan(axc), 4, "q4km_dequant_matvec")
+    h2 = ctx.prepare_kernel(co, _plan(axc), 4, "q4_0_dequant_matvec")
+    q1, x1 = O.generate_q4km_test_data(8, 3)
+    q2 = O.gen_q4_0_weights(4, 16)
+    x2 = O.gen_normal_f32(5, 16 * 32)
+    ref1, ref2 = O.q4k_dot(q1, x1, 8), O.q4_0_dot(q2, x2, 16)
+    errors = []
+
+    def worker(h, q, x, n, ref):
+        try:
+            for _ in range(30):
+                out = ctx.dispatch_handle(h, (1, 1, 1), [q.tobytes(), x.tobytes(), b""], [0, 0, 4],
+                                          struct.pack("<I", n))
+                if O.reference_rel_err(struct.unpack("<f", out[2])[0], ref) >= 1e-3:
+                    errors.append("mismatch")
+        except Exception as exc:  # surfaced below
+            errors.append(repr(exc))
+
+    ts = [threading.Thread(target=worker, args=(h1, q1, x1, 8, ref1)),
+          threading.Thread(target=worker, args=(h2, q2, x2, 16, ref2)),
+          threading.Thread(target=worker, args=(h1, q1, x1, 8, ref1))]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errors, errors[:3]
+    h1.release()
+    h2.release()
+
+
+def test_autotune_picks_a_compiled_variant(ctx, axc):
+    import importlib
+    tune = importlib.import_module("axiom_compute_amd.tune")
+    rows, sb = 2048, 16
+    _say("autotune 2048x4096")
+    q = O.gen_q4k_weights(61, rows * sb)
+    x = O.gen_normal_f32(62, sb * 256)
+    dq, dx, dy = ctx.alloc(q.nbytes), ctx.alloc(x.nbytes), ctx.alloc(rows * 4)
+    ctx.upload(dq, q)
+    ctx.upload(dx, x)
+    v, ns = tune.q4k_matvec_autotune(ctx, dq, dx, dy, rows, sb, samples=3)
+    assert ns > 0
+    assert v in axc.compiled_variants("q4k")
+    ctx.q4k_matvec(dq, dx, dy, rows, sb, v)
+    ctx.synchronize()
+    y = np.frombuffer(ctx.download(dy, rows * 4), dtype=np.float32)
+    ref = O.q4k_matvec(q, x, rows, sb)
+    yf, ad = O.q4k_matvec_f64(q, x, rows, sb)
+    assert O.matvec_tolerance_report(y, ref, yf, ad, sb * 256)["ok"]
+    for b in (dq, dx, dy):
+        b.close()
+
+
+def test_events_time_launches_on_the_context_stream(ctx, axc):
+    h = ctx.prepare_kernel(axc.builtin_code_object(),
+                           axc.BindingPlan([axc.axh.ACCESS_READ_WRITE], 4, (64, 1, 1)), 4, "axh_spin")
+    buf = ctx.alloc(4)
+    e0, e1 = ctx.event(), ctx.event()
+    e0.record()
+    ctx.launch(h, (1, 1, 1), [buf], struct.pack("<I", 300))  # ~1 ms of sleeps
+    e1.record()
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1)
+    assert 0.1 < ms < 100.0
+    assert struct.unpack("<I", ctx.download(buf, 4))[0] == 300
+    buf.close()
+    h.release()
