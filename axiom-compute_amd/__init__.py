@@ -16,6 +16,7 @@ from .axh import (  # noqa: F401
     Variant,
     builtin_code_object,
     compiled_variants,
+    q4k_matvec_kernel_name,
     load_library,
     validate_request,
 )
@@ -32,6 +33,7 @@ __all__ = [
     "Variant",
     "builtin_code_object",
     "compiled_variants",
+    "q4k_matvec_kernel_name",
     "load_library",
     "validate_request",
 ]

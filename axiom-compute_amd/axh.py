@@ -141,6 +141,7 @@ def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
         "axh_event_elapsed_ms": (st, [vp, vp, c.POINTER(c.c_float)]),
         "axh_event_destroy": (None, [vp]),
         "axh_q4k_matvec": (st, [vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
+        "axh_q4k_matvec_kernel_name": (st, [u32, u32, c.POINTER(_Variant), c.c_char_p, sz]),
         "axh_q4_0_matvec": (st, [vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
         "axh_q4k_dequant": (st, [vp, vp, vp, u64, vp]),
         "axh_q4_0_dequant": (st, [vp, vp, vp, u64, vp]),
@@ -190,6 +191,17 @@ class Variant:
     def _c(self) -> _Variant:
         return _Variant(self.rows_per_wave, self.waves_per_workgroup, self.prefetch,
                         self.nontemporal)
+
+
+def q4k_matvec_kernel_name(n_rows: int, sb_per_row: int,
+                           variant: Optional[Variant] = None) -> str:
+    """Entry point axh_q4k_matvec launches for this shape and variant."""
+    lib = load_library()
+    v = variant._c() if variant else None
+    buf = ctypes.create_string_buffer(64)
+    _check(lib.axh_q4k_matvec_kernel_name(n_rows, sb_per_row, ctypes.byref(v) if v else None,
+                                          buf, 64))
+    return buf.value.decode()
 
 
 def compiled_variants(kind: str = "q4k") -> list[Variant]:

@@ -169,6 +169,61 @@ static uint32_t occupancy(axh_context *ctx, axh_kernel *k, uint32_t lds) {
   return (uint32_t)blocks;
 }
 
+// The kernel, LDS bytes and shape arguments for one Q4_K matvec call.
+struct Q4kPlan {
+  char name[64];
+  uint32_t nw;      // waves per workgroup
+  uint32_t lds;     // dynamic LDS bytes
+  bool flat;        // persistent kernel (grid sized by occupancy)
+  uint32_t units;   // flat: workgroups needed; tiled: workgroups
+  RowsArgs args;
+};
+
+static axh_status plan_q4k(uint32_t n_rows, uint32_t sb_per_row, const axh_q4_variant *variant,
+                           Q4kPlan *p) {
+  const MatvecVariant *v = find_variant(kQ4kVariants, axh_q4k_matvec_variant_count(), variant,
+                                        q4k_default(n_rows, sb_per_row));
+  if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_K matvec variant matches");
+  const uint64_t q_bytes = (uint64_t)n_rows * sb_per_row * 144u;
+  p->flat = sb_per_row >= 1 && sb_per_row <= kQ4kFlatMaxSb &&
+            sb_per_row * 8u <= v->nw * 64u && q_bytes < 0xFFFFFFFFull;
+  if (p->flat) {
+    std::snprintf(p->name, sizeof(p->name), "axh_q4k_matvec_flat_r%u_w%u_p%u_n%u", v->rpw, v->nw,
+                  v->pf, v->nt == 1 ? 1u : 0u);
+    p->nw = v->nw;
+    p->lds = sb_per_row * 1056u;
+    // Each wave handles pairs of RPW-row bundles; the grid is persistent.
+    const uint32_t bundles = (n_rows + v->rpw - 1) / v->rpw;
+    const uint32_t pairs = (bundles + 1) / 2;
+    p->units = (pairs + v->nw - 1) / v->nw;
+    p->args = RowsArgs{n_rows, sb_per_row, sb_per_row, 0};
+    return ok();
+  }
+  // Rows longer than one LDS tile, or matrices of 4 GiB and more.
+  const MatvecVariant tv = n_rows >= 2048 ? MatvecVariant{2, 8, 2, 2} : MatvecVariant{1, 4, 2, 2};
+  std::snprintf(p->name, sizeof(p->name), "axh_q4k_matvec_tiled_r%u_w%u_p%u", tv.rpw, tv.nw, tv.pf);
+  uint32_t tile = (sb_per_row + 7u) & ~7u;
+  if (tile == 0) tile = 8;
+  if (tile > kQ4kMaxTileSb) tile = kQ4kMaxTileSb;
+  p->nw = tv.nw;
+  p->lds = tile * 1088u;
+  const uint32_t rows_per_wg = tv.rpw * tv.nw;
+  p->units = (n_rows + rows_per_wg - 1) / rows_per_wg;
+  p->args = RowsArgs{n_rows, sb_per_row, tile, 0};
+  return ok();
+}
+
+axh_status axh_q4k_matvec_kernel_name(uint32_t n_rows, uint32_t sb_per_row,
+                                      const axh_q4_variant *variant, char *buf, size_t cap) {
+  if (!buf || cap == 0) return fail(AXH_ERR_INVALID_ARGUMENT, "buf is NULL");
+  Q4kPlan p{};
+  axh_status s = plan_q4k(n_rows, sb_per_row, variant, &p);
+  if (s != AXH_OK) return s;
+  if (std::strlen(p.name) + 1 > cap) return fail(AXH_ERR_INVALID_ARGUMENT, "buf too small");
+  std::memcpy(buf, p.name, std::strlen(p.name) + 1);
+  return ok();
+}
+
 axh_status axh_q4k_matvec(axh_context *ctx, const void *q, const float *x, float *y,
                           uint32_t n_rows, uint32_t sb_per_row, const axh_q4_variant *variant,
                           void *stream) {
@@ -180,50 +235,22 @@ axh_status axh_q4k_matvec(axh_context *ctx, const void *q, const float *x, float
     return fail(AXH_ERR_INVALID_ARGUMENT, "sb_per_row too large");
   if (((uintptr_t)q & 15u) || ((uintptr_t)x & 15u))
     return fail(AXH_ERR_INVALID_ARGUMENT, "q and x must be 16-byte aligned");
-  const MatvecVariant *v = find_variant(kQ4kVariants, axh_q4k_matvec_variant_count(), variant,
-                                        q4k_default(n_rows, sb_per_row));
-  if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_K matvec variant matches");
-  hipSetDevice(ctx->core->device);
-  void *bufs[3] = {const_cast<void *>(q), const_cast<float *>(x), y};
-  const uint64_t q_bytes = (uint64_t)n_rows * sb_per_row * 144u;
-  const bool flat = sb_per_row >= 1 && sb_per_row <= kQ4kFlatMaxSb &&
-                    sb_per_row * 8u <= v->nw * 64u && q_bytes < 0xFFFFFFFFull;
-  char name[64];
-  axh_kernel *k = nullptr;
-  axh_status s;
-  if (flat) {
-    std::snprintf(name, sizeof(name), "axh_q4k_matvec_flat_r%u_w%u_p%u_n%u", v->rpw, v->nw, v->pf,
-                  v->nt == 1 ? 1u : 0u);
-    s = builtin_kernel(ctx, name, 3, sizeof(RowsArgs), v->nw * 64u, &k);
-    if (s != AXH_OK) return s;
-    const uint32_t lds = sb_per_row * 1056u;
-    if (lds > ctx->core->max_lds)
-      return fail(AXH_ERR_PIPELINE_LAYOUT, "LDS tile exceeds the device limit");
-    // Each wave handles pairs of RPW-row bundles; the grid is persistent.
-    const uint32_t bundles = (n_rows + v->rpw - 1) / v->rpw;
-    const uint32_t pairs = (bundles + 1) / 2;
-    const uint32_t wgs_needed = (pairs + v->nw - 1) / v->nw;
-    const uint32_t resident = occupancy(ctx, k, lds) * ctx->core->cu_count;
-    const uint32_t grid[3] = {wgs_needed < resident ? wgs_needed : resident, 1, 1};
-    RowsArgs a{n_rows, sb_per_row, sb_per_row, 0};
-    s = launch_raw(k, grid, bufs, 3, &a, sizeof(a), lds, pick_stream(ctx, stream));
-    return s == AXH_OK ? ok() : s;
-  }
-  // Rows longer than one LDS tile, or matrices of 4 GiB and more.
-  const MatvecVariant tv = n_rows >= 2048 ? MatvecVariant{2, 8, 2, 2} : MatvecVariant{1, 4, 2, 2};
-  std::snprintf(name, sizeof(name), "axh_q4k_matvec_tiled_r%u_w%u_p%u", tv.rpw, tv.nw, tv.pf);
-  s = builtin_kernel(ctx, name, 3, sizeof(RowsArgs), tv.nw * 64u, &k);
+  Q4kPlan p{};
+  axh_status s = plan_q4k(n_rows, sb_per_row, variant, &p);
   if (s != AXH_OK) return s;
-  uint32_t tile = (sb_per_row + 7u) & ~7u;
-  if (tile == 0) tile = 8;
-  if (tile > kQ4kMaxTileSb) tile = kQ4kMaxTileSb;
-  const uint32_t lds = tile * 1088u;
-  if (lds > ctx->core->max_lds)
+  if (p.lds > ctx->core->max_lds)
     return fail(AXH_ERR_PIPELINE_LAYOUT, "LDS tile exceeds the device limit");
-  RowsArgs a{n_rows, sb_per_row, tile, 0};
-  const uint32_t rows_per_wg = tv.rpw * tv.nw;
-  const uint32_t grid[3] = {(n_rows + rows_per_wg - 1) / rows_per_wg, 1, 1};
-  s = launch_raw(k, grid, bufs, 3, &a, sizeof(a), lds, pick_stream(ctx, stream));
+  hipSetDevice(ctx->core->device);
+  axh_kernel *k = nullptr;
+  s = builtin_kernel(ctx, p.name, 3, sizeof(RowsArgs), p.nw * 64u, &k);
+  if (s != AXH_OK) return s;
+  uint32_t grid[3] = {p.units, 1, 1};
+  if (p.flat) {
+    const uint32_t resident = occupancy(ctx, k, p.lds) * ctx->core->cu_count;
+    if (resident < grid[0]) grid[0] = resident;
+  }
+  void *bufs[3] = {const_cast<void *>(q), const_cast<float *>(x), y};
+  s = launch_raw(k, grid, bufs, 3, &p.args, sizeof(p.args), p.lds, pick_stream(ctx, stream));
   return s == AXH_OK ? ok() : s;
 }
 

@@ -13,6 +13,7 @@ import argparse
 import json
 import os
 import platform
+import re
 import sys
 import time
 from pathlib import Path
@@ -35,18 +36,26 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(O, q, x, rows, sb, budget_s: float) -> dict:
-    """The oracle (C restatement of q4km_dequant_matvec_cpu, one core) on the
-    full matrix, repeated for about `budget_s` seconds."""
-    weight_bytes = rows * sb * 144
-    O.q4k_matvec_single(q, x, rows, sb)  # warm caches / page in
+def _time_cpu(fn, budget_s: float):
+    fn()  # warm caches / page in
     n, t0 = 0, time.perf_counter()
     while True:
-        O.q4k_matvec_single(q, x, rows, sb)
+        fn()
         n += 1
         el = time.perf_counter() - t0
         if el >= budget_s:
-            break
+            return n, el
+
+
+def cpu_baseline(O, q, x, rows, sb, budget_s: float) -> dict:
+    """The oracle (C restatement of q4km_dequant_matvec_cpu: scalar, the
+    reference's order) on the full matrix for about `budget_s` seconds on one
+    core, then row-parallel over the host's cores for a quarter of that."""
+    weight_bytes = rows * sb * 144
+    n, el = _time_cpu(lambda: O.q4k_matvec_single(q, x, rows, sb), budget_s)
+    threads = max(1, min(os.cpu_count() or 1, 16))
+    nm, elm = _time_cpu(lambda: O.q4k_matvec(q, x, rows, sb, threads=threads),
+                        max(1.0, budget_s / 4))
     return {
         "value": round(weight_bytes * n / el / 1e9, 4),
         "unit": "GB/s",
@@ -54,7 +63,27 @@ def cpu_baseline(O, q, x, rows, sb, budget_s: float) -> dict:
         "kind": "port",
         "sample": f"{n} full {rows}x{sb * 256} Q4_K matvecs in {el:.1f}s, one thread "
                   f"({cpu_model()}, nproc={os.cpu_count()}); {el / n * 1e6:.0f} us/call",
+        "all_cores": {
+            "value": round(weight_bytes * nm / elm / 1e9, 4),
+            "cores": threads,
+            "sample": f"{nm} full matvecs in {elm:.1f}s, rows split over {threads} threads "
+                      f"(bit-identical to one thread); {elm / nm * 1e6:.0f} us/call",
+        },
     }
+
+
+def profiled_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of `kernel` at `workload`, as recorded by the
+    FETCH_SIZE / WRITE_SIZE counter summary under profiles/ (None if that
+    kernel has no recorded summary)."""
+    pat = re.compile(r"^traffic_per_launch kernel=(\S+) workload=(\S+) bytes=(\d+) "
+                     r"source=(\S+)")
+    for f in sorted((ROOT / "profiles").glob("*.md")):
+        for ln in f.read_text().splitlines():
+            m = pat.match(ln.strip().strip("`"))
+            if m and m.group(1) == kernel and m.group(2) == workload:
+                return int(m.group(3)), f"profiles/{f.name}"
+    return None, None
 
 
 def main() -> int:
@@ -126,6 +155,23 @@ def main() -> int:
     us_per_call = total_ms * 1000.0 / args.steps
     gbs = weight_bytes / (us_per_call * 1e-6) / 1e9
 
+    # Distribution: the same back-to-back stream cut into groups of 10 calls
+    # by events (an event between every call would add its own gap).
+    group = 10
+    n_groups = max(1, args.steps // group)
+    evs = [ctx.event() for _ in range(n_groups + 1)]
+    evs[0].record()
+    for g in range(n_groups):
+        for i in range(group):
+            ctx.q4k_matvec(copies[(g * group + i) % n_copies], dx, dy, rows, sb, variant)
+        evs[g + 1].record()
+    evs[-1].synchronize()
+    per_call = sorted(evs[g].elapsed_ms(evs[g + 1]) * 1000.0 / group for g in range(n_groups))
+    pct = {p: round(per_call[min(len(per_call) - 1, int(p / 100 * len(per_call)))], 3)
+           for p in (10, 50, 90)}
+    kernel = pkg.q4k_matvec_kernel_name(rows, sb, variant)
+    traffic, traffic_src = profiled_traffic(kernel, f"{rows}x{sb * 256}")
+
     if args.calibrate_copy:
         # A plain copy of exactly weight_bytes (hipMemcpy device-to-device
         # through the runtime's copy kernel), for scaling FETCH_SIZE/WRITE_SIZE.
@@ -145,6 +191,8 @@ def main() -> int:
         "warmup": args.warmup,
         "ms_per_step": round(total_ms / args.steps, 6),
         "us_per_call": round(us_per_call, 3),
+        "us_per_call_p10_p50_p90_of_10call_groups": [pct[10], pct[50], pct[90]],
+        "kernel": kernel,
         "pct_of_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
         "higher_is_better": True,
         "scaling": "weak",
@@ -170,7 +218,9 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
+            "algorithmic_bytes": weight_bytes,
         },
         "cpu_baseline": cpu,
     }

@@ -180,6 +180,12 @@ typedef struct axh_q4_variant {
 axh_status axh_q4k_matvec(axh_context *ctx, const void *q, const float *x, float *y,
                           uint32_t n_rows, uint32_t sb_per_row, const axh_q4_variant *variant,
                           void *stream);
+/* Name of the kernel axh_q4k_matvec launches for this shape and variant (the
+ * entry point profilers report), NUL-terminated into buf[cap].  No device
+ * work.  Counterpart of the kernel name the reference's BenchFn receives in
+ * place of SPIR-V (crates/axc-optimize/src/grid_search.rs:139-146). */
+axh_status axh_q4k_matvec_kernel_name(uint32_t n_rows, uint32_t sb_per_row,
+                                      const axh_q4_variant *variant, char *buf, size_t cap);
 /* Q4_0 counterpart: rows of blocks_per_row 18-byte blocks; x holds
  * blocks_per_row*32 f32.  Replaces examples/q4_0_dequant_matvec.axc; compared
  * against q4_0_dequant_matvec_cpu (crates/axc-driver/benches/common.rs:212-259). */

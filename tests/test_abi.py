@@ -103,6 +103,24 @@ def test_builtin_code_object_holds_every_variant_kernel(axc):
         assert name.encode() in co, name
 
 
+def test_kernel_selection_by_shape_and_variant(axc):
+    """The entry point axh_q4k_matvec launches (no device work): persistent
+    kernel while a row's x fits one workgroup's LDS, tiled kernel beyond."""
+    name = axc.q4k_matvec_kernel_name
+    assert name(4096, 56) == "axh_q4k_matvec_flat_r1_w8_p2_n0"
+    assert name(4096, 16) == "axh_q4k_matvec_flat_r2_w4_p2_n0"
+    assert name(4096, 128) == "axh_q4k_matvec_flat_r1_w16_p2_n0"
+    assert name(1, 1024) == "axh_q4k_matvec_tiled_r1_w4_p2"
+    assert name(4096, 1024) == "axh_q4k_matvec_tiled_r2_w8_p2"
+    assert name(4096, 56, axc.Variant(2, 4, 4, 1)) == "axh_q4k_matvec_tiled_r2_w8_p2"  # 56*8 > 4*64
+    assert name(4096, 16, axc.Variant(2, 4, 4, 1)) == "axh_q4k_matvec_flat_r2_w4_p4_n1"
+    co = axc.builtin_code_object()
+    for sb in (1, 16, 56, 128, 129, 4096):
+        assert name(64, sb).encode() in co
+    with pytest.raises(axc.DispatchError):
+        name(64, 16, axc.Variant(3, 4, 2, 2))
+
+
 def test_variant_index_out_of_range_is_typed_error(axc):
     lib = axc.load_library()
     v = axc.axh._Variant()
