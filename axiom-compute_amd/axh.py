@@ -179,7 +179,7 @@ def builtin_code_object() -> bytes:
     return ctypes.string_at(p, n.value)
 
 
-@dataclass
+@dataclass(frozen=True)
 class Variant:
     """Strategy holes of the matvec kernels (0 = default)."""
 

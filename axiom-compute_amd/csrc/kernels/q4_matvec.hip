@@ -315,26 +315,30 @@ AXH_Q4K_MATVEC_TILED(2, 8, 2)
 // iterations ahead across bundle boundaries, so the load pipeline only
 // drains at the end of the wave's work.  x is staged once per workgroup.
 //
-// LDS: xs[sb*256 + part*128 + ((16t) ^ (16*(sb&3))) + 4c + e]
+// LDS: xs[sb*272 + part*128 + 16t + 4c + e]
 //        = x[sb*256 + 64c + 32*part + 4t + e] * (part ? 2^20 : 2^24)
 //      ss[sb*8 + j] = sum of the 32 (unscaled) x of sub-block j
-// For fixed (t, part), 16 consecutive lanes read 64 distinct banks.  The
+// The 16-float pad per superblock puts superblocks s = 0..3 of an iteration on
+// different bank quarters: for fixed (t, part), 16 consecutive lanes read 64
+// distinct banks, and every read is the lane's base address plus an
+// immediate offset.  The
 // 2^24 / 2^20 factors cancel the f16-subnormal encoding of the nibbles, so
 //   sum_i (d*sc*q_i - dmin*m) * x_i = d*sc*sum_i q_i x_i - dmin*m*ss
 // needs no further scaling.
 // ---------------------------------------------------------------------------
+constexpr uint32_t kQ4kFlatSbFloats = 272; // LDS floats per superblock of x (256 + pad)
+
 __device__ __forceinline__ void q4k_flat_stage(const float *__restrict__ x, float *xs, float *ss,
                                                uint32_t si, const float4 (&v)[8]) {
   const uint32_t sb = si >> 3, j = si & 7u, c = j >> 1, part = j & 1u;
   const float scale = part ? 1048576.0f : 16777216.0f;
-  float *dst = xs + sb * 256u + part * 128u + 4u * c;
-  const uint32_t sw = (sb & 3u) * 16u;
+  float *dst = xs + sb * kQ4kFlatSbFloats + part * 128u + 4u * c;
   float sum = 0.0f;
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     const float4 a = v[t];
     sum += (a.x + a.y) + (a.z + a.w);
-    *reinterpret_cast<float4 *>(dst + (((uint32_t)t * 16u) ^ sw)) =
+    *reinterpret_cast<float4 *>(dst + (uint32_t)t * 16u) =
         make_float4(a.x * scale, a.y * scale, a.z * scale, a.w * scale);
   }
   ss[si] = sum;
@@ -368,7 +372,7 @@ __device__ __forceinline__ void q4k_flat_load(Q4kFlatBuf<RPW, PF> &B, int p,
   }
 }
 
-template <int RPW, int NW, int PF, bool kNT>
+template <int RPW, int NW, int PF, bool kNT, int XP>
 __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
                                                 const float *__restrict__ x,
                                                 float *__restrict__ y, uint32_t n_rows,
@@ -394,16 +398,20 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(q, n_rows * row_bytes);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, nsb * 1024u);
   float *xs = lds;
-  float *ss = lds + nsb * 256u;
+  float *ss = lds + nsb * kQ4kFlatSbFloats;
 
   // Prologue: x requests first, then the weight prefetch, then the LDS writes
-  // (waiting for x never waits for the weights: loads retire in order).  One
-  // sub-block of x (32 floats) per thread: the host launches this kernel only
-  // when nsb * 8 <= NW * 64.
+  // (waiting for x never waits for the weights: loads retire in order).  XP
+  // sub-blocks of x (32 floats each) per thread: the host launches this
+  // kernel only when nsb * 8 <= XP * NW * 64.
   const uint32_t nsub = nsb * 8u;
-  const uint32_t my_sub = min(tid, nsub - 1u);
-  float4 xv[8];
-  q4k_flat_load_x(xr, my_sub, xv);
+  uint32_t my_sub[XP];
+  float4 xv[XP][8];
+#pragma unroll
+  for (int k = 0; k < XP; ++k) {
+    my_sub[k] = min(tid + (uint32_t)k * (NW * 64u), nsub - 1u);
+    q4k_flat_load_x(xr, my_sub[k], xv[k]);
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   Q4kFlatBuf<RPW, PF> B;
@@ -416,7 +424,8 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
   }
   __builtin_amdgcn_sched_barrier(0);
   // Threads beyond nsub rewrite the last sub-block with the same values.
-  q4k_flat_stage(x, xs, ss, my_sub, xv);
+#pragma unroll
+  for (int k = 0; k < XP; ++k) q4k_flat_stage(x, xs, ss, my_sub[k], xv[k]);
   __syncthreads();
 
   float acc[RPW];
@@ -428,13 +437,12 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
     for (int p = 0; p < PF; ++p) {
       const uint32_t sb = c_it * 8u + s;
       if (c_pi < n_my && sb < nsb) {
-        const float *xb = xs + sb * 256u + 4u * c;
-        const uint32_t sw = (sb & 3u) * 16u;
+        const float *xb = xs + sb * kQ4kFlatSbFloats + 4u * c;
         float4 xl[8], xh[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-          xl[t] = *reinterpret_cast<const float4 *>(xb + (((uint32_t)t * 16u) ^ sw));
-          xh[t] = *reinterpret_cast<const float4 *>(xb + 128u + (((uint32_t)t * 16u) ^ sw));
+          xl[t] = *reinterpret_cast<const float4 *>(xb + (uint32_t)t * 16u);
+          xh[t] = *reinterpret_cast<const float4 *>(xb + 128u + (uint32_t)t * 16u);
         }
         const float2 sub = *reinterpret_cast<const float2 *>(ss + sb * 8u + 2u * c);
 #pragma unroll
@@ -498,7 +506,17 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
                                                          const float *__restrict__ x,            \
                                                          float *__restrict__ y, RowsArgs a) {    \
     extern __shared__ float axh_lds_dyn[];                                                       \
-    q4k_matvec_flat<RPW, NW, PF, NT != 0>(q, x, y, a.n_rows, a.units_per_row, axh_lds_dyn);     \
+    q4k_matvec_flat<RPW, NW, PF, NT != 0, 1>(q, x, y, a.n_rows, a.units_per_row, axh_lds_dyn);  \
+  }
+// Two staged x sub-blocks per thread (rows of up to 2 * NW * 8 superblocks).
+#define AXH_Q4K_MATVEC_FLAT_X2(RPW, NW, PF, NT)                                                  \
+  extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
+      axh_q4k_matvec_flat_r##RPW##_w##NW##_p##PF##_n##NT##_x2(const uint8_t *__restrict__ q,     \
+                                                              const float *__restrict__ x,       \
+                                                              float *__restrict__ y,             \
+                                                              RowsArgs a) {                      \
+    extern __shared__ float axh_lds_dyn[];                                                       \
+    q4k_matvec_flat<RPW, NW, PF, NT != 0, 2>(q, x, y, a.n_rows, a.units_per_row, axh_lds_dyn);  \
   }
 
 AXH_Q4K_MATVEC_FLAT(1, 8, 2, 0)
@@ -514,6 +532,222 @@ AXH_Q4K_MATVEC_FLAT(4, 4, 2, 0)
 AXH_Q4K_MATVEC_FLAT(1, 8, 7, 1)
 AXH_Q4K_MATVEC_FLAT(2, 4, 2, 1)
 AXH_Q4K_MATVEC_FLAT(2, 4, 4, 1)
+AXH_Q4K_MATVEC_FLAT_X2(1, 4, 2, 0)
+AXH_Q4K_MATVEC_FLAT_X2(1, 4, 4, 0)
+AXH_Q4K_MATVEC_FLAT_X2(2, 4, 2, 0)
+AXH_Q4K_MATVEC_FLAT_X2(2, 4, 4, 0)
+
+// ---------------------------------------------------------------------------
+// Column-slice Q4_K matvec: x held in VGPRs, rows streamed in batches.
+//
+// Thread t of the workgroup owns quarter t of every row: superblock sb = t/4,
+// c = t%4, i.e. qs bytes [32c, 32c+32) of that superblock, whose low nibbles
+// are weights 64c + i of sub-block 2c and high nibbles weights 64c + 32 + i of
+// sub-block 2c+1 (i = 0..31).  The workgroup has NW*64 >= 4*nsb threads;
+// threads past 4*nsb read zeros (buffer range check) and add 0.
+//
+// Each thread loads its 64 x values once, keeps them in VGPRs pre-scaled by
+// 2^24 (sub-block 2c) and 2^20 (sub-block 2c+1) for the f16-subnormal nibble
+// encoding, with the two unscaled sub-block sums for the dmin term.  No LDS
+// staging of x and no barrier before the first row.
+//
+// Rows go in batches of RB: workgroup g handles batches g, g + G, g + 2G, ...
+// (G = gridDim.x) and keeps the next batch's weights in flight while it
+// computes the current one.  Per row the 64 lane partials are summed with
+// DPP (all 16-lane rows, then row_bcast15/31 into lane 63); with NW > 1 the
+// wave sums meet in LDS (double-buffered by batch parity, one barrier per
+// batch).
+// ---------------------------------------------------------------------------
+template <int RB>
+struct Q4kColsBuf {
+  uint4 h[RB], a[RB], b[RB];
+};
+
+// Out-of-range offset for idle lanes and rows past the matrix: the buffer
+// range check returns zeros (the host keeps n_rows * row_bytes below it).
+constexpr uint32_t kQ4kColsOob = 0xFFFFFF00u;
+
+// `lane_off` is this lane's header offset within a row, or kQ4kColsOob for
+// an idle lane.
+template <int RB, bool kNT>
+__device__ __forceinline__ void q4k_cols_load(Q4kColsBuf<RB> &B, __amdgpu_buffer_rsrc_t qr,
+                                              uint32_t batch, uint32_t n_rows,
+                                              uint32_t row_bytes, uint32_t lane_off,
+                                              uint32_t c) {
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const uint32_t row = batch * RB + (uint32_t)r;
+    const uint32_t off =
+        (row < n_rows && lane_off != kQ4kColsOob) ? row * row_bytes + lane_off : kQ4kColsOob;
+    B.h[r] = buf_load16<kNT>(qr, off);
+    B.a[r] = buf_load16<kNT>(qr, off + 16u + 32u * c);
+    B.b[r] = buf_load16<kNT>(qr, off + 32u + 32u * c);
+  }
+}
+
+// Sum over the wave, valid in lane 63.
+__device__ __forceinline__ float wave_sum_to_lane63(float v) {
+  v += dpp_mov<0xB1>(v);  // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);  // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v); // row_half_mirror
+  v += dpp_mov<0x140>(v); // row_mirror: every lane holds its 16-lane row sum
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142,
+                                                             0xA, 0xF, false)); // row_bcast15
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143,
+                                                             0xC, 0xF, false)); // row_bcast31
+  return v;
+}
+
+template <int RB>
+__device__ __forceinline__ void q4k_cols_compute(const Q4kColsBuf<RB> &B, const float4 (&xl)[8],
+                                                 const float4 (&xh)[8], float s0, float s1,
+                                                 uint32_t c, float (&v)[RB]) {
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const uint4 hd = B.h[r];
+    uint32_t scp, mp;
+    q4k_scale_min_pair(hd.y, hd.z, hd.w, c, &scp, &mp);
+    float alo = 0.0f, ahi = 0.0f;
+    q4k_dword(B.a[r].x, xl[0], xh[0], alo, ahi);
+    q4k_dword(B.a[r].y, xl[1], xh[1], alo, ahi);
+    q4k_dword(B.a[r].z, xl[2], xh[2], alo, ahi);
+    q4k_dword(B.a[r].w, xl[3], xh[3], alo, ahi);
+    q4k_dword(B.b[r].x, xl[4], xh[4], alo, ahi);
+    q4k_dword(B.b[r].y, xl[5], xh[5], alo, ahi);
+    q4k_dword(B.b[r].z, xl[6], xh[6], alo, ahi);
+    q4k_dword(B.b[r].w, xl[7], xh[7], alo, ahi);
+    const float dot = __builtin_fmaf((float)(scp & 0xFFu), alo, (float)(scp >> 8) * ahi);
+    const float mins = __builtin_fmaf((float)(mp & 0xFFu), s0, (float)(mp >> 8) * s1);
+    v[r] = __builtin_fmaf(f16_to_f32(hd.x & 0xFFFFu), dot, -f16_to_f32(hd.x >> 16) * mins);
+  }
+}
+
+// Wave sums of the batch's rows -> y (through LDS when NW > 1).
+template <int RB, int NW>
+__device__ __forceinline__ void q4k_cols_finish(float (&v)[RB], float *red, uint32_t parity,
+                                                uint32_t batch, uint32_t n_rows, uint32_t tid,
+                                                uint32_t wave, float *__restrict__ y) {
+#pragma unroll
+  for (int r = 0; r < RB; ++r) v[r] = wave_sum_to_lane63(v[r]);
+  const uint32_t lane = tid & 63u;
+  if constexpr (NW == 1) {
+    if (lane == 63u) {
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const uint32_t row = batch * RB + (uint32_t)r;
+        if (row < n_rows) y[row] = v[r];
+      }
+    }
+  } else {
+    float *buf = red + parity * (RB * NW);
+    if (lane == 63u) {
+#pragma unroll
+      for (int r = 0; r < RB; ++r) buf[r * NW + wave] = v[r];
+    }
+    __syncthreads();
+    if (tid < (uint32_t)RB) {
+      float s = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) s += buf[tid * NW + w];
+      const uint32_t row = batch * RB + tid;
+      if (row < n_rows) y[row] = s;
+    }
+  }
+}
+
+template <int RB, int NW, bool kNT, bool kXFirst>
+__device__ __forceinline__ void q4k_matvec_cols(const uint8_t *__restrict__ q,
+                                                const float *__restrict__ x,
+                                                float *__restrict__ y, uint32_t n_rows,
+                                                uint32_t nsb, float *red) {
+  const uint32_t tid = threadIdx.x;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t G = gridDim.x;
+  const uint32_t n_batches = (n_rows + RB - 1) / RB;
+  uint32_t b = blockIdx.x;
+  if (nsb == 0) { // empty rows: the reference returns +0.0 (AT-1323)
+    for (uint32_t r = b * (NW * 64u) + tid; r < n_rows; r += G * (NW * 64u)) y[r] = 0.0f;
+    return;
+  }
+  if (b >= n_batches) return; // whole workgroup
+  const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
+  const __amdgpu_buffer_rsrc_t qr = make_rsrc(q, n_rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, nsb * 1024u);
+  const uint32_t nq = nsb * 4u;
+  const uint32_t c = tid & 3u;
+  // header offset of this lane's superblock within a row (idle lanes: out of range)
+  const uint32_t lane_off = tid < nq ? (tid >> 2) * (uint32_t)kQ4kSbBytes : kQ4kColsOob;
+  const uint32_t x_off = tid < nq ? tid * 256u : nsb * 1024u; // idle lanes read zeros
+
+  float4 xl[8], xh[8];
+  Q4kColsBuf<RB> B0, B1;
+  if constexpr (kXFirst) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      xl[t] = buf_loadf4(xr, x_off + 16u * (uint32_t)t);
+      xh[t] = buf_loadf4(xr, x_off + 128u + 16u * (uint32_t)t);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // B0 strictly before B1: the loop waits on B0 with B1 still in flight
+  q4k_cols_load<RB, kNT>(B0, qr, b, n_rows, row_bytes, lane_off, c);
+  __builtin_amdgcn_sched_barrier(0);
+  q4k_cols_load<RB, kNT>(B1, qr, b + G, n_rows, row_bytes, lane_off, c);
+  if constexpr (!kXFirst) {
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      xl[t] = buf_loadf4(xr, x_off + 16u * (uint32_t)t);
+      xh[t] = buf_loadf4(xr, x_off + 128u + 16u * (uint32_t)t);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    s0 += (xl[t].x + xl[t].y) + (xl[t].z + xl[t].w);
+    s1 += (xh[t].x + xh[t].y) + (xh[t].z + xh[t].w);
+    xl[t] = make_float4(xl[t].x * 16777216.0f, xl[t].y * 16777216.0f, xl[t].z * 16777216.0f,
+                        xl[t].w * 16777216.0f);
+    xh[t] = make_float4(xh[t].x * 1048576.0f, xh[t].y * 1048576.0f, xh[t].z * 1048576.0f,
+                        xh[t].w * 1048576.0f);
+  }
+
+  // Batches of this workgroup, padded to an even count: a padding batch has
+  // only out-of-range rows (zero loads, nothing stored).
+  const uint32_t n_mine = (n_batches - b + G - 1u) / G;
+  const uint32_t n_pad = (n_mine + 1u) & ~1u;
+  float v[RB];
+  uint32_t i = 0;
+  do { // n_pad >= 2: this workgroup has at least one batch
+    q4k_cols_compute<RB>(B0, xl, xh, s0, s1, c, v);
+    q4k_cols_load<RB, kNT>(B0, qr, b + 2u * G, n_rows, row_bytes, lane_off, c);
+    q4k_cols_finish<RB, NW>(v, red, 0u, b, n_rows, tid, wave, y);
+    q4k_cols_compute<RB>(B1, xl, xh, s0, s1, c, v);
+    q4k_cols_load<RB, kNT>(B1, qr, b + 3u * G, n_rows, row_bytes, lane_off, c);
+    q4k_cols_finish<RB, NW>(v, red, 1u, b + G, n_rows, tid, wave, y);
+    b += 2u * G;
+    i += 2u;
+  } while (i < n_pad);
+}
+
+#define AXH_Q4K_MATVEC_COLS(RB, NW, NT, XF)                                                       \
+  extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
+      axh_q4k_matvec_cols_r##RB##_w##NW##_n##NT##_x##XF(const uint8_t *__restrict__ q,           \
+                                                         const float *__restrict__ x,            \
+                                                         float *__restrict__ y, RowsArgs a) {    \
+    __shared__ float red[2 * RB * NW];                                                           \
+    q4k_matvec_cols<RB, NW, NT != 0, XF != 0>(q, x, y, a.n_rows, a.units_per_row, red);         \
+  }
+
+AXH_Q4K_MATVEC_COLS(4, 1, 0, 1)
+AXH_Q4K_MATVEC_COLS(4, 2, 0, 1)
+AXH_Q4K_MATVEC_COLS(4, 3, 0, 1)
+AXH_Q4K_MATVEC_COLS(4, 4, 0, 1)
+AXH_Q4K_MATVEC_COLS(4, 5, 0, 1)
+AXH_Q4K_MATVEC_COLS(4, 6, 0, 1)
+AXH_Q4K_MATVEC_COLS(4, 7, 0, 1)
+AXH_Q4K_MATVEC_COLS(4, 8, 0, 1)
 
 // Reference-compatible entry point: the contract of
 // examples/q4km_dequant_matvec.axc (bindings q=0, x=1, y=2; push constant

@@ -27,21 +27,24 @@ struct CountArgs {
 
 struct MatvecVariant {
   uint32_t rpw, nw, pf, nt;
+  uint32_t xp; // x sub-blocks staged per thread (1, or 2 for the _x2 kernels)
 };
 
-// Compiled instantiations of axh_q4k_matvec_flat_r{rpw}_w{nw}_p{pf}_n{0|1}
+// Compiled instantiations of axh_q4k_matvec_flat_r{rpw}_w{nw}_p{pf}_n{0|1}[_x2]
 // (persistent kernel; nt: 1 = non-temporal weight loads, 2 = normal loads).
-// Keep in sync with the AXH_Q4K_MATVEC_FLAT list in q4_matvec.hip.
+// Keep in sync with the AXH_Q4K_MATVEC_FLAT / _X2 lists in q4_matvec.hip.
 constexpr MatvecVariant kQ4kVariants[] = {
-    {1, 8, 2, 2}, {1, 8, 4, 2}, {1, 8, 7, 2}, {1, 16, 2, 2},
-    {1, 4, 7, 2}, {2, 4, 2, 2}, {2, 4, 4, 2}, {2, 8, 2, 2},  {2, 8, 4, 2},
-    {4, 4, 2, 2}, {1, 8, 7, 1}, {2, 4, 2, 1}, {2, 4, 4, 1},
+    {1, 8, 2, 2, 1}, {1, 8, 4, 2, 1}, {1, 8, 7, 2, 1}, {1, 16, 2, 2, 1}, {1, 4, 7, 2, 1},
+    {2, 4, 2, 2, 1}, {2, 4, 4, 2, 1}, {2, 8, 2, 2, 1}, {2, 8, 4, 2, 1},  {4, 4, 2, 2, 1},
+    {1, 8, 7, 1, 1}, {2, 4, 2, 1, 1}, {2, 4, 4, 1, 1}, {1, 4, 2, 2, 2},  {1, 4, 4, 2, 2},
+    {2, 4, 2, 2, 2}, {2, 4, 4, 2, 2},
 };
 // axh_q4_0_matvec_r{rpw}_w{nw} (prefetch and cache policy are not holes for Q4_0).
-constexpr MatvecVariant kQ4_0Variants[] = {{1, 1, 1, 2}, {1, 4, 1, 2}, {2, 4, 1, 2}, {4, 4, 1, 2}};
+constexpr MatvecVariant kQ4_0Variants[] = {
+    {1, 1, 1, 2, 1}, {1, 4, 1, 2, 1}, {2, 4, 1, 2, 1}, {4, 4, 1, 2, 1}};
 
 constexpr uint32_t kQ4kMaxTileSb = 128;   // tiled kernel: 128 * 1088 B = 136 KiB of LDS
-constexpr uint32_t kQ4kFlatMaxSb = 128;   // persistent kernel: 128 * 1056 B = 132 KiB of LDS
+constexpr uint32_t kQ4kFlatMaxSb = 128;   // persistent kernel: 128 * 1120 B = 140 KiB of LDS
 constexpr uint32_t kQ4_0MaxTileB = 1024; // 1024 * 132 B = 132 KiB of LDS
 
 } // namespace
@@ -76,8 +79,12 @@ axh_status builtin_kernel(axh_context *ctx, const char *entry, uint32_t n_buffer
   return AXH_OK;
 }
 
+// The compiled variant matching the requested holes (unset holes take the
+// default's value); among staging widths, the smallest one that holds
+// `min_xp` x sub-blocks per thread, else the widest.
 static const MatvecVariant *find_variant(const MatvecVariant *table, size_t n,
-                                         const axh_q4_variant *v, MatvecVariant dflt) {
+                                         const axh_q4_variant *v, MatvecVariant dflt,
+                                         uint32_t min_xp = 1) {
   MatvecVariant want = dflt;
   if (v) {
     if (v->rows_per_wave) want.rpw = v->rows_per_wave;
@@ -85,29 +92,44 @@ static const MatvecVariant *find_variant(const MatvecVariant *table, size_t n,
     if (v->prefetch) want.pf = v->prefetch;
     if (v->nontemporal) want.nt = v->nontemporal;
   }
-  for (size_t i = 0; i < n; ++i)
-    if (table[i].rpw == want.rpw && table[i].nw == want.nw && table[i].pf == want.pf &&
-        table[i].nt == want.nt)
-      return &table[i];
-  return nullptr;
+  const MatvecVariant *best = nullptr;
+  for (size_t i = 0; i < n; ++i) {
+    const MatvecVariant &t = table[i];
+    if (t.rpw != want.rpw || t.nw != want.nw || t.pf != want.pf || t.nt != want.nt) continue;
+    if (!best) {
+      best = &t;
+      continue;
+    }
+    const bool t_fits = t.xp >= min_xp, b_fits = best->xp >= min_xp;
+    if ((t_fits && (!b_fits || t.xp < best->xp)) || (!t_fits && !b_fits && t.xp > best->xp))
+      best = &t;
+  }
+  return best;
 }
 
 // Default strategy per shape (chosen from on-device sweeps; any compiled
 // variant can be forced through axh_q4_variant).
 static MatvecVariant q4k_default(uint32_t n_rows, uint32_t nsb) {
   (void)n_rows;
-  // The persistent kernel stages one 32-element sub-block of x per thread,
-  // so the workgroup must have at least nsb * 8 threads.
-  if (nsb * 8u <= 256u) return {2, 4, 2, 2};
-  if (nsb * 8u <= 512u) return {1, 8, 2, 2};
-  return {1, 16, 2, 2};
+  // The persistent kernel stages 32-element sub-blocks of x, one (or two for
+  // the _x2 kernels) per thread.
+  if (nsb * 8u <= 256u) return {2, 4, 2, 2, 1};
+  if (nsb * 8u <= 512u) return {1, 8, 2, 2, 1};
+  return {1, 16, 2, 2, 1};
 }
 
 static MatvecVariant q4_0_default(uint32_t n_rows, uint32_t nb) {
   (void)nb;
-  if (n_rows >= 4096) return {2, 4, 1, 2};
-  return {1, 1, 1, 2};
+  if (n_rows >= 4096) return {2, 4, 1, 2, 1};
+  return {1, 1, 1, 2, 1};
 }
+
+// Rows below this count (with at most kQ4kColsMaxSb superblocks) go to the
+// register-resident column-slice kernel, which splits each row across the
+// workgroup's waves; it wins where a call is latency-bound (few rows).
+constexpr uint32_t kQ4kColsMaxRows = 32;
+constexpr uint32_t kQ4kColsMaxSb = 128; // 4 * 128 lanes = 8 waves
+constexpr uint32_t kQ4kColsRb = 4;      // rows per batch of the compiled cols kernels
 
 static bool device_ptr_ok(const void *p) { return p != nullptr; }
 
@@ -122,18 +144,37 @@ const void *axh_builtin_code_object(size_t *bytes) {
   return axh_q4_matvec_co_begin;
 }
 
+// Distinct hole assignments of the Q4_K table (staging width is derived
+// from the shape, not a hole).
+static bool q4k_first_of_holes(size_t i) {
+  for (size_t k = 0; k < i; ++k)
+    if (kQ4kVariants[k].rpw == kQ4kVariants[i].rpw && kQ4kVariants[k].nw == kQ4kVariants[i].nw &&
+        kQ4kVariants[k].pf == kQ4kVariants[i].pf && kQ4kVariants[k].nt == kQ4kVariants[i].nt)
+      return false;
+  return true;
+}
+
 uint32_t axh_q4k_matvec_variant_count(void) {
-  return (uint32_t)(sizeof(kQ4kVariants) / sizeof(kQ4kVariants[0]));
+  uint32_t n = 0;
+  for (size_t i = 0; i < sizeof(kQ4kVariants) / sizeof(kQ4kVariants[0]); ++i)
+    n += q4k_first_of_holes(i) ? 1u : 0u;
+  return n;
 }
 
 axh_status axh_q4k_matvec_variant_at(uint32_t i, axh_q4_variant *out) {
-  if (!out || i >= axh_q4k_matvec_variant_count())
-    return fail(AXH_ERR_INVALID_ARGUMENT, "variant index out of range");
-  out->rows_per_wave = kQ4kVariants[i].rpw;
-  out->waves_per_workgroup = kQ4kVariants[i].nw;
-  out->prefetch = kQ4kVariants[i].pf;
-  out->nontemporal = kQ4kVariants[i].nt;
-  return ok();
+  if (!out) return fail(AXH_ERR_INVALID_ARGUMENT, "out is NULL");
+  uint32_t n = 0;
+  for (size_t k = 0; k < sizeof(kQ4kVariants) / sizeof(kQ4kVariants[0]); ++k) {
+    if (!q4k_first_of_holes(k)) continue;
+    if (n++ == i) {
+      out->rows_per_wave = kQ4kVariants[k].rpw;
+      out->waves_per_workgroup = kQ4kVariants[k].nw;
+      out->prefetch = kQ4kVariants[k].pf;
+      out->nontemporal = kQ4kVariants[k].nt;
+      return ok();
+    }
+  }
+  return fail(AXH_ERR_INVALID_ARGUMENT, "variant index out of range");
 }
 
 uint32_t axh_q4_0_matvec_variant_count(void) {
@@ -181,17 +222,33 @@ struct Q4kPlan {
 
 static axh_status plan_q4k(uint32_t n_rows, uint32_t sb_per_row, const axh_q4_variant *variant,
                            Q4kPlan *p) {
-  const MatvecVariant *v = find_variant(kQ4kVariants, axh_q4k_matvec_variant_count(), variant,
-                                        q4k_default(n_rows, sb_per_row));
-  if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_K matvec variant matches");
   const uint64_t q_bytes = (uint64_t)n_rows * sb_per_row * 144u;
+  if (!variant && n_rows < kQ4kColsMaxRows && sb_per_row >= 1 &&
+      sb_per_row <= kQ4kColsMaxSb) {
+    // Few rows: each row is split across NW waves (4 lanes per superblock).
+    const uint32_t nw = (sb_per_row * 4u + 63u) / 64u;
+    std::snprintf(p->name, sizeof(p->name), "axh_q4k_matvec_cols_r%u_w%u_n0_x1", kQ4kColsRb, nw);
+    p->nw = nw;
+    p->lds = 0;
+    p->flat = false;
+    p->units = (n_rows + kQ4kColsRb - 1) / kQ4kColsRb;
+    p->args = RowsArgs{n_rows, sb_per_row, sb_per_row, 0};
+    return ok();
+  }
+  const MatvecVariant dflt = q4k_default(n_rows, sb_per_row);
+  const uint32_t want_nw =
+      variant && variant->waves_per_workgroup ? variant->waves_per_workgroup : dflt.nw;
+  const uint32_t min_xp = (sb_per_row * 8u + want_nw * 64u - 1u) / (want_nw * 64u);
+  const MatvecVariant *v = find_variant(
+      kQ4kVariants, sizeof(kQ4kVariants) / sizeof(kQ4kVariants[0]), variant, dflt, min_xp);
+  if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_K matvec variant matches");
   p->flat = sb_per_row >= 1 && sb_per_row <= kQ4kFlatMaxSb &&
-            sb_per_row * 8u <= v->nw * 64u && q_bytes < 0xFFFFFFFFull;
+            sb_per_row * 8u <= v->xp * v->nw * 64u && q_bytes < 0xFFFFFFFFull;
   if (p->flat) {
-    std::snprintf(p->name, sizeof(p->name), "axh_q4k_matvec_flat_r%u_w%u_p%u_n%u", v->rpw, v->nw,
-                  v->pf, v->nt == 1 ? 1u : 0u);
+    std::snprintf(p->name, sizeof(p->name), "axh_q4k_matvec_flat_r%u_w%u_p%u_n%u%s", v->rpw,
+                  v->nw, v->pf, v->nt == 1 ? 1u : 0u, v->xp == 2 ? "_x2" : "");
     p->nw = v->nw;
-    p->lds = sb_per_row * 1056u;
+    p->lds = sb_per_row * 1120u; // 272 floats of x + 8 sums per superblock
     // Each wave handles pairs of RPW-row bundles; the grid is persistent.
     const uint32_t bundles = (n_rows + v->rpw - 1) / v->rpw;
     const uint32_t pairs = (bundles + 1) / 2;
@@ -200,7 +257,8 @@ static axh_status plan_q4k(uint32_t n_rows, uint32_t sb_per_row, const axh_q4_va
     return ok();
   }
   // Rows longer than one LDS tile, or matrices of 4 GiB and more.
-  const MatvecVariant tv = n_rows >= 2048 ? MatvecVariant{2, 8, 2, 2} : MatvecVariant{1, 4, 2, 2};
+  const MatvecVariant tv =
+      n_rows >= 2048 ? MatvecVariant{2, 8, 2, 2, 1} : MatvecVariant{1, 4, 2, 2, 1};
   std::snprintf(p->name, sizeof(p->name), "axh_q4k_matvec_tiled_r%u_w%u_p%u", tv.rpw, tv.nw, tv.pf);
   uint32_t tile = (sb_per_row + 7u) & ~7u;
   if (tile == 0) tile = 8;

@@ -90,10 +90,12 @@ def test_validation_order_binding_before_push_constants(axc):
 def test_builtin_code_object_holds_every_variant_kernel(axc):
     co = axc.builtin_code_object()
     assert co[:4] == b"\x7fELF"
-    for v in axc.compiled_variants("q4k"):
+    variants = axc.compiled_variants("q4k")
+    assert len(set(variants)) == len(variants)  # one entry per hole assignment
+    for v in variants:
         name = (f"axh_q4k_matvec_flat_r{v.rows_per_wave}_w{v.waves_per_workgroup}"
                 f"_p{v.prefetch}_n{1 if v.nontemporal == 1 else 0}")
-        assert name.encode() in co, name
+        assert name.encode() in co or (name + "_x2").encode() in co, name
     for v in axc.compiled_variants("q4_0"):
         name = f"axh_q4_0_matvec_r{v.rows_per_wave}_w{v.waves_per_workgroup}"
         assert name.encode() in co, name
@@ -114,9 +116,18 @@ def test_kernel_selection_by_shape_and_variant(axc):
     assert name(4096, 1024) == "axh_q4k_matvec_tiled_r2_w8_p2"
     assert name(4096, 56, axc.Variant(2, 4, 4, 1)) == "axh_q4k_matvec_tiled_r2_w8_p2"  # 56*8 > 4*64
     assert name(4096, 16, axc.Variant(2, 4, 4, 1)) == "axh_q4k_matvec_flat_r2_w4_p4_n1"
+    # two staged x sub-blocks per thread when one is not enough
+    assert name(4096, 56, axc.Variant(2, 4, 2, 2)) == "axh_q4k_matvec_flat_r2_w4_p2_n0_x2"
+    assert name(4096, 16, axc.Variant(2, 4, 2, 2)) == "axh_q4k_matvec_flat_r2_w4_p2_n0"
+    # few rows: the row is split across the workgroup's waves
+    assert name(1, 128) == "axh_q4k_matvec_cols_r4_w8_n0_x1"
+    assert name(8, 56) == "axh_q4k_matvec_cols_r4_w4_n0_x1"
+    assert name(31, 1) == "axh_q4k_matvec_cols_r4_w1_n0_x1"
+    assert name(32, 1) == "axh_q4k_matvec_flat_r2_w4_p2_n0"
     co = axc.builtin_code_object()
-    for sb in (1, 16, 56, 128, 129, 4096):
-        assert name(64, sb).encode() in co
+    for rows in (1, 31, 64):
+        for sb in (1, 16, 56, 128, 129, 4096):
+            assert name(rows, sb).encode() in co
     with pytest.raises(axc.DispatchError):
         name(64, 16, axc.Variant(3, 4, 2, 2))
 

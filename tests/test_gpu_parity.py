@@ -165,9 +165,11 @@ def test_q4k_matvec_every_variant(ctx, axc):
         _check_q4k(y, q, x, rows, sb, f"variant {v}")
 
 
-@pytest.mark.parametrize("rows,sb", [(1, 1), (3, 7), (5, 8), (9, 9), (65, 129), (2, 160), (33, 300)])
+@pytest.mark.parametrize("rows,sb", [(1, 1), (3, 7), (5, 8), (9, 9), (65, 129), (2, 160), (33, 300),
+                                     (31, 128), (17, 56), (4, 33), (30, 100), (32, 56)])
 def test_q4k_matvec_edge_shapes(ctx, rows, sb):
-    """Single superblock, ragged tails, and rows longer than one LDS tile."""
+    """Single superblock, ragged tails, rows longer than one LDS tile, and the
+    few-row shapes that split a row across 1..8 waves (every partial batch)."""
     _say(f"q4k edge {rows}x{sb}")
     q = O.gen_q4k_weights(rows * 31 + sb, rows * sb)
     x = O.gen_normal_f32(rows + 5 * sb, sb * 256)
