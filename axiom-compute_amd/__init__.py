@@ -16,6 +16,9 @@ from .axh import (  # noqa: F401
     Variant,
     builtin_code_object,
     compiled_variants,
+    compiled_matmul_variants,
+    MatmulVariant,
+    q4k_matmul_kernel_name,
     q4k_matvec_kernel_name,
     load_library,
     validate_request,
@@ -33,6 +36,9 @@ __all__ = [
     "Variant",
     "builtin_code_object",
     "compiled_variants",
+    "compiled_matmul_variants",
+    "MatmulVariant",
+    "q4k_matmul_kernel_name",
     "q4k_matvec_kernel_name",
     "load_library",
     "validate_request",

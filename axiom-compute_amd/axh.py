@@ -96,6 +96,11 @@ class _Variant(ctypes.Structure):
 _lib: Optional[ctypes.CDLL] = None
 
 
+class _MatmulVariant(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_uint32), ("waves_per_workgroup", ctypes.c_uint32),
+                ("col_tiles", ctypes.c_uint32), ("prefetch", ctypes.c_uint32)]
+
+
 def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
     """Load libaxh.so (raises ImportError if it has not been built)."""
     global _lib
@@ -142,6 +147,12 @@ def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
         "axh_event_destroy": (None, [vp]),
         "axh_q4k_matvec": (st, [vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
         "axh_q4k_matvec_kernel_name": (st, [u32, u32, c.POINTER(_Variant), c.c_char_p, sz]),
+        "axh_q4k_matmul_f16": (st, [vp, vp, vp, vp, u32, u32, u32, c.POINTER(_MatmulVariant),
+                                    vp]),
+        "axh_q4k_matmul_kernel_name": (st, [u32, u32, c.POINTER(_MatmulVariant), c.c_char_p,
+                                            sz]),
+        "axh_q4k_matmul_variant_count": (u32, []),
+        "axh_q4k_matmul_variant_at": (st, [u32, c.POINTER(_MatmulVariant)]),
         "axh_q4_0_matvec": (st, [vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
         "axh_q4k_dequant": (st, [vp, vp, vp, u64, vp]),
         "axh_q4_0_dequant": (st, [vp, vp, vp, u64, vp]),
@@ -201,6 +212,40 @@ def q4k_matvec_kernel_name(n_rows: int, sb_per_row: int,
     buf = ctypes.create_string_buffer(64)
     _check(lib.axh_q4k_matvec_kernel_name(n_rows, sb_per_row, ctypes.byref(v) if v else None,
                                           buf, 64))
+    return buf.value.decode()
+
+
+@dataclass(frozen=True)
+class MatmulVariant:
+    """Strategy holes of the batched matmul kernels (0 = default).  kind: 1
+    LDS-tiled, 2 register A, 3 K-split."""
+
+    kind: int = 0
+    waves_per_workgroup: int = 0
+    col_tiles: int = 0
+    prefetch: int = 0
+
+    def _c(self) -> _MatmulVariant:
+        return _MatmulVariant(self.kind, self.waves_per_workgroup, self.col_tiles, self.prefetch)
+
+
+def compiled_matmul_variants() -> list[MatmulVariant]:
+    lib = load_library()
+    out = []
+    for i in range(lib.axh_q4k_matmul_variant_count()):
+        v = _MatmulVariant()
+        _check(lib.axh_q4k_matmul_variant_at(i, ctypes.byref(v)))
+        out.append(MatmulVariant(v.kind, v.waves_per_workgroup, v.col_tiles, v.prefetch))
+    return out
+
+
+def q4k_matmul_kernel_name(n_rows: int, batch: int,
+                           variant: Optional[MatmulVariant] = None) -> str:
+    """Entry point axh_q4k_matmul_f16 launches for this shape and variant."""
+    lib = load_library()
+    v = variant._c() if variant else None
+    buf = ctypes.create_string_buffer(64)
+    _check(lib.axh_q4k_matmul_kernel_name(n_rows, batch, ctypes.byref(v) if v else None, buf, 64))
     return buf.value.decode()
 
 
@@ -519,6 +564,14 @@ class HipContext:
         _check(self._lib.axh_q4_0_matvec(self._raw, _ptr(q), _ptr(x), _ptr(y), n_rows,
                                          blocks_per_row, ctypes.byref(v) if v else None,
                                          _stream(stream)))
+
+    def q4k_matmul(self, q, x, y, n_rows: int, sb_per_row: int, batch: int,
+                   variant: Optional[MatmulVariant] = None, stream=None) -> None:
+        """y (batch x n_rows f32) = RN_f16(W) x (batch x K f16 vectors)."""
+        v = variant._c() if variant else None
+        _check(self._lib.axh_q4k_matmul_f16(self._raw, _ptr(q), _ptr(x), _ptr(y), n_rows,
+                                            sb_per_row, batch, ctypes.byref(v) if v else None,
+                                            _stream(stream)))
 
     def q4k_dequant(self, q, w, n_superblocks: int, stream=None) -> None:
         _check(self._lib.axh_q4k_dequant(self._raw, _ptr(q), _ptr(w), n_superblocks,

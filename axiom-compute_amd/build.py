@@ -31,7 +31,7 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
-KERNELS = ["q4_matvec"]
+KERNELS = ["q4_matvec", "q4_matmul"]
 
 
 def _run(cmd: list[str]) -> None:
@@ -58,7 +58,8 @@ def build_kernels() -> dict[str, Path]:
 def build_runtime(cos: dict[str, Path]) -> Path:
     rt = PKG / "csrc" / "runtime"
     embed_o = BUILD / "axh_embed.o"
-    _run(["gcc", "-c", f'-DAXH_Q4_MATVEC_CO="{cos["q4_matvec"]}"', "-o", str(embed_o),
+    _run(["gcc", "-c", f'-DAXH_Q4_MATVEC_CO="{cos["q4_matvec"]}"',
+          f'-DAXH_Q4_MATMUL_CO="{cos["q4_matmul"]}"', "-o", str(embed_o),
           str(rt / "axh_embed.S")])
     tmp = LIB.with_suffix(".so.tmp")
     _run([

@@ -1,0 +1,566 @@
+// gfx950 batched Q4_K_M matmul on MFMA: Y[b][r] = sum_k W[r][k] * X[b][k]
+// for a Q4_K_M weight matrix W (n_rows x K, K = 256 * sb_per_row, rows of
+// contiguous 144-byte superblocks) and `batch` f16 activation vectors X
+// (batch x K, each vector contiguous).  Y is f32, batch x n_rows (each
+// output vector contiguous).
+//
+// The reference has no batched kernel (its matvec produces one output); per
+// column b this is the reference dot product (q4km_dequant_matvec_cpu,
+// crates/axc-driver/tests/common_helpers.rs:411-461) with x_b widened from
+// f16, computed here with f16 weights: every weight is dequantised exactly as
+// the reference does it in f32 (w32 = RN_f32(d*sc*q - dmin*m),
+// common_helpers.rs:437-454) and then rounded once to f16 (RN_f16(w32)).
+// f16 x f16 products are exact in the f32 accumulators of the MFMA.
+//
+// Three kernel kinds (selected per batch size by the runtime):
+//   * LDS-tiled (axh_q4k_matmul_w{W}_n{NT}): a workgroup of W waves owns
+//     TM = 32*W rows and TN = 16*NT columns of Y; per 128-wide K step (half a
+//     superblock) every thread dequantises one quarter superblock (32 qs
+//     bytes = 64 weights) of one row into the LDS tile As[TM][128], the
+//     threads copy the X tile [TN][128] into LDS, and each wave runs
+//     v_mfma_f32_16x16x32_f16 over its 32 x TN sub-tile while the next
+//     step's global loads are in flight;
+//   * register-A (axh_q4k_matmul_rf_...): each lane dequantises exactly the
+//     A fragments it feeds the MFMA, X is double-buffered in LDS;
+//   * K-split (axh_q4k_matmul_ks_...): for small batches, the waves of a
+//     workgroup share one 32-row tile and split K, summing in LDS.
+// LDS rows are padded to 136 halves (272 bytes) so that 16 lanes reading
+// 16-byte fragments of 16 consecutive rows hit 64 distinct banks.
+#include "q4_common.h"
+
+using namespace axh;
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+struct MatmulArgs {
+  uint32_t n_rows;
+  uint32_t sb_per_row;
+  uint32_t batch;
+  uint32_t pad;
+};
+
+namespace {
+
+constexpr int kKStep = 128;   // K per LDS step (half a superblock)
+constexpr int kLd = 136;      // LDS row stride in halves (128 + 8 pad)
+constexpr uint32_t kOob = 0xFFFFFF00u; // out-of-range buffer offset: loads return zeros
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// RN_f16 of two f32 values, packed (lo = a).
+__device__ __forceinline__ uint32_t pack_f16(float a, float b) {
+  const half2_t h = __builtin_convertvector((f32x2_t){a, b}, half2_t);
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+// Four qs bytes (one dword) of a quarter: low nibbles are weights 4t..4t+3 of
+// the quarter's first sub-block, high nibbles the same of its second.  Each
+// weight is w32 = RN_f32(q * d1 - m1) through v_fma_mix_f32 with the nibble
+// as an f16 subnormal (q * 2^-24 or q * 2^-20) against d1 pre-scaled by 2^24
+// or 2^20, then RN_f16.  Outputs: lo = 4 f16 (2 dwords), hi = 4 f16.
+__device__ __forceinline__ void dequant_dword(uint32_t w, float d1s, float m1, float d2s, float m2,
+                                              uint32_t &lo01, uint32_t &lo23, uint32_t &hi01,
+                                              uint32_t &hi23) {
+  const uint32_t w8 = w >> 8;
+  const uint32_t a = w & 0x000F000Fu;   // bytes 0, 2 low nibbles
+  const uint32_t b = w8 & 0x000F000Fu;  // bytes 1, 3 low nibbles
+  const uint32_t ch = w & 0x00F000F0u;  // bytes 0, 2 high nibbles
+  const uint32_t dh = w8 & 0x00F000F0u; // bytes 1, 3 high nibbles
+  const float l0 = __builtin_fmaf(lo_half_f16(a), d1s, -m1);
+  const float l1 = __builtin_fmaf(lo_half_f16(b), d1s, -m1);
+  const float l2 = __builtin_fmaf(hi_half_f16(a), d1s, -m1);
+  const float l3 = __builtin_fmaf(hi_half_f16(b), d1s, -m1);
+  const float h0 = __builtin_fmaf(lo_half_f16(ch), d2s, -m2);
+  const float h1 = __builtin_fmaf(lo_half_f16(dh), d2s, -m2);
+  const float h2 = __builtin_fmaf(hi_half_f16(ch), d2s, -m2);
+  const float h3 = __builtin_fmaf(hi_half_f16(dh), d2s, -m2);
+  lo01 = pack_f16(l0, l1);
+  lo23 = pack_f16(l2, l3);
+  hi01 = pack_f16(h0, h1);
+  hi23 = pack_f16(h2, h3);
+}
+
+template <int W, int NT>
+__device__ __forceinline__ void q4k_matmul(const uint8_t *__restrict__ q,
+                                           const uint16_t *__restrict__ x,
+                                           float *__restrict__ y, const MatmulArgs a) {
+  constexpr int TM = 32 * W, TN = 16 * NT;
+  constexpr int kXChunks = TN * (kKStep / 8);        // 16-byte chunks of the X tile
+  constexpr int kXPer = (kXChunks + 64 * W - 1) / (64 * W);
+  __shared__ __attribute__((aligned(16))) _Float16 As[TM * kLd];
+  __shared__ __attribute__((aligned(16))) _Float16 Xs[TN * kLd];
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t n_rows = a.n_rows, nsb = a.sb_per_row, batch = a.batch;
+  const uint32_t m0 = blockIdx.x * TM, n0 = blockIdx.y * TN;
+  const uint32_t K = nsb * 256u;
+  const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
+  const __amdgpu_buffer_rsrc_t qr = rsrc(q, n_rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t xr = rsrc(x, batch * K * 2u);
+
+  // Dequantisation role: row m0 + drow, quarter dq of each 128-wide K step.
+  const uint32_t drow = tid >> 1, dq = tid & 1u;
+  const uint32_t grow = m0 + drow;
+  const uint32_t row_off = grow < n_rows ? grow * row_bytes : kOob;
+
+  f32x4_t acc[2][NT];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[i][j] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+
+  uint4 hd, qa, qb, xv[kXPer];
+  auto load_step = [&](uint32_t ks) {
+    const uint32_t sb = ks >> 1, c = 2u * (ks & 1u) + dq;
+    const uint32_t off = row_off == kOob ? kOob : row_off + sb * (uint32_t)kQ4kSbBytes;
+    hd = bload16(qr, off);
+    qa = bload16(qr, off == kOob ? kOob : off + 16u + 32u * c);
+    qb = bload16(qr, off == kOob ? kOob : off + 32u + 32u * c);
+#pragma unroll
+    for (int i = 0; i < kXPer; ++i) {
+      const uint32_t chunk = tid + (uint32_t)i * (64u * W);
+      const uint32_t n = chunk >> 4, kc = chunk & 15u, b = n0 + n;
+      const uint32_t xoff =
+          (chunk < (uint32_t)kXChunks && b < batch) ? (b * K + ks * kKStep + kc * 8u) * 2u : kOob;
+      xv[i] = bload16(xr, xoff);
+    }
+  };
+
+  const uint32_t n_steps = nsb * 2u;
+  load_step(0);
+  for (uint32_t ks = 0; ks < n_steps; ++ks) {
+    __syncthreads(); // the previous step's fragment reads are done
+    {
+      const uint32_t c = 2u * (ks & 1u) + dq;
+      uint32_t scp, mp;
+      q4k_scale_min_pair(hd.y, hd.z, hd.w, c, &scp, &mp);
+      const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
+      const float d1s = d * (float)(scp & 0xFFu) * 16777216.0f; // low nibbles: q * 2^-24
+      const float d2s = d * (float)(scp >> 8) * 1048576.0f;     // high nibbles: q * 2^-20
+      const float m1 = dmin * (float)(mp & 0xFFu), m2 = dmin * (float)(mp >> 8);
+      const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+      _Float16 *dst = As + drow * kLd + 64u * dq;
+#pragma unroll
+      for (int t = 0; t < 8; t += 2) {
+        uint32_t l0, l1, h0, h1, l2, l3, h2, h3;
+        dequant_dword(w[t], d1s, m1, d2s, m2, l0, l1, h0, h1);
+        dequant_dword(w[t + 1], d1s, m1, d2s, m2, l2, l3, h2, h3);
+        *reinterpret_cast<uint4 *>(dst + 4 * t) = make_uint4(l0, l1, l2, l3);
+        *reinterpret_cast<uint4 *>(dst + 32 + 4 * t) = make_uint4(h0, h1, h2, h3);
+      }
+#pragma unroll
+      for (int i = 0; i < kXPer; ++i) {
+        const uint32_t chunk = tid + (uint32_t)i * (64u * W);
+        if (chunk < (uint32_t)kXChunks)
+          *reinterpret_cast<uint4 *>(Xs + (chunk >> 4) * kLd + (chunk & 15u) * 8u) = xv[i];
+      }
+    }
+    __syncthreads();
+    if (ks + 1u < n_steps) load_step(ks + 1u); // in flight during the MFMAs
+    const uint32_t fr = lane & 15u, fk = 8u * (lane >> 4);
+#pragma unroll
+    for (int kk = 0; kk < kKStep / 32; ++kk) {
+      half8_t af[2], bf[NT];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        af[i] = *reinterpret_cast<const half8_t *>(As + (wave * 32u + 16u * i + fr) * kLd +
+                                                   32u * kk + fk);
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+        bf[j] = *reinterpret_cast<const half8_t *>(Xs + (16u * j + fr) * kLd + 32u * kk + fk);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // C fragment: lane holds column (lane % 16) and rows 4 * (lane / 16) + 0..3.
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const uint32_t b = n0 + 16u * j + (lane & 15u);
+      const uint32_t r0 = m0 + wave * 32u + 16u * i + 4u * (lane >> 4);
+      if (b >= batch) continue;
+      float *dst = y + (size_t)b * n_rows + r0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (r0 + e < n_rows) dst[e] = acc[i][j][e];
+    }
+}
+
+__device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+  const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b32(r, (int)off + 4, 0, 0);
+  return make_uint2(lo, hi);
+}
+
+// ---------------------------------------------------------------------------
+// Register-fragment variant.  Each lane dequantises exactly the A fragments
+// it feeds to v_mfma_f32_16x16x32_f16 (row lane%16 of a 16-row tile,
+// k = 32*kk + 8*(lane/16) + 0..7), so A never goes through LDS.  In a
+// 128-wide K step of superblock sb (half h = step%2) the lane reads, per
+// 16-row tile, the row's 16-byte header and the 8 qs bytes
+// [32c + 8g, 32c + 8g + 8) for c = 2h and 2h+1: low nibbles feed the
+// fragments of sub-blocks 2c (kk = 2(c-2h)), high nibbles those of 2c+1.
+// X fragments come straight from global memory (kXLds = false; every wave
+// reads the same lines through L1) or from a double-buffered LDS tile
+// filled by the whole workgroup (kXLds = true).  Loads run PF steps ahead
+// in a register ring.
+// ---------------------------------------------------------------------------
+template <int NT, int XPER, bool kXLds>
+struct RfStep {
+  uint4 hd[2];
+  uint2 qlo[2], qhi[2];
+  uint4 xv[kXLds ? XPER : 4 * NT];
+};
+
+template <int W, int NT, int PF, bool kXLds>
+__device__ __forceinline__ void q4k_matmul_rf(const uint8_t *__restrict__ q,
+                                              const uint16_t *__restrict__ x,
+                                              float *__restrict__ y, const MatmulArgs a) {
+  constexpr int TM = 32 * W, TN = 16 * NT;
+  constexpr int kXChunks = TN * (kKStep / 8);
+  constexpr int kXPer = (kXChunks + 64 * W - 1) / (64 * W);
+  __shared__ __attribute__((aligned(16))) _Float16 Xs[kXLds ? 2 * TN * kLd : 8];
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t n_rows = a.n_rows, nsb = a.sb_per_row, batch = a.batch;
+  const uint32_t m0 = blockIdx.x * TM, n0 = blockIdx.y * TN;
+  const uint32_t K = nsb * 256u;
+  const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
+  const __amdgpu_buffer_rsrc_t qr = rsrc(q, n_rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t xr = rsrc(x, batch * K * 2u);
+  const uint32_t fr = lane & 15u, g = lane >> 4;
+
+  uint32_t row_off[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t row = m0 + wave * 32u + 16u * (uint32_t)i + fr;
+    row_off[i] = row < n_rows ? row * row_bytes : kOob;
+  }
+  // X fragment / chunk offsets of step 0 (step ks adds ks * 256 bytes)
+  uint32_t xoff0[kXLds ? kXPer : NT];
+  if constexpr (kXLds) {
+#pragma unroll
+    for (int i = 0; i < kXPer; ++i) {
+      const uint32_t chunk = tid + (uint32_t)i * (64u * W);
+      const uint32_t n = chunk >> 4, kc = chunk & 15u, b = n0 + n;
+      xoff0[i] = (chunk < (uint32_t)kXChunks && b < batch) ? (b * K + kc * 8u) * 2u : kOob;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const uint32_t b = n0 + 16u * (uint32_t)j + fr;
+      xoff0[j] = b < batch ? (b * K + 8u * g) * 2u : kOob;
+    }
+  }
+
+  auto load_step = [&](RfStep<NT, kXPer, kXLds> &S, uint32_t ks) {
+    const uint32_t sb = ks >> 1, h = ks & 1u;
+    const bool live = ks < 2u * nsb;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t base = (row_off[i] == kOob || !live) ? kOob : row_off[i] + sb * 144u;
+      S.hd[i] = bload16(qr, base);
+      const uint32_t qo = 16u + 64u * h + 8u * g;
+      S.qlo[i] = bload8(qr, base == kOob ? kOob : base + qo);
+      S.qhi[i] = bload8(qr, base == kOob ? kOob : base + qo + 32u);
+    }
+    if constexpr (kXLds) {
+#pragma unroll
+      for (int i = 0; i < kXPer; ++i)
+        S.xv[i] = bload16(xr, (xoff0[i] == kOob || !live) ? kOob : xoff0[i] + ks * 256u);
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+          S.xv[kk * NT + j] =
+              bload16(xr, (xoff0[j] == kOob || !live) ? kOob : xoff0[j] + ks * 256u + 64u * kk);
+    }
+  };
+
+  f32x4_t acc[2][NT];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[i][j] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+
+  RfStep<NT, kXPer, kXLds> S[PF];
+#pragma unroll
+  for (int p = 0; p < PF; ++p) load_step(S[p], (uint32_t)p);
+
+  const uint32_t n_steps = (2u * nsb + PF - 1) / PF * PF;
+  for (uint32_t ks0 = 0; ks0 < n_steps; ks0 += PF) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+      const uint32_t ks = ks0 + (uint32_t)p;
+      const uint32_t h = ks & 1u;
+      // A fragments of this step: [tile][kk]
+      half8_t af[2][4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const uint4 hd = S[p].hd[i];
+        const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          const uint32_t c = 2u * h + (uint32_t)cc;
+          uint32_t scp, mp;
+          q4k_scale_min_pair(hd.y, hd.z, hd.w, c, &scp, &mp);
+          const float d1s = d * (float)(scp & 0xFFu) * 16777216.0f;
+          const float d2s = d * (float)(scp >> 8) * 1048576.0f;
+          const float m1 = dmin * (float)(mp & 0xFFu), m2 = dmin * (float)(mp >> 8);
+          const uint2 qw = cc == 0 ? S[p].qlo[i] : S[p].qhi[i];
+          uint32_t l0, l1, h0, h1, l2, l3, h2, h3;
+          dequant_dword(qw.x, d1s, m1, d2s, m2, l0, l1, h0, h1);
+          dequant_dword(qw.y, d1s, m1, d2s, m2, l2, l3, h2, h3);
+          af[i][2 * cc] = __builtin_bit_cast(half8_t, make_uint4(l0, l1, l2, l3));
+          af[i][2 * cc + 1] = __builtin_bit_cast(half8_t, make_uint4(h0, h1, h2, h3));
+        }
+      }
+      half8_t bfr[4][NT];
+      if constexpr (kXLds) {
+        _Float16 *xb = Xs + (ks & 1u) * (TN * kLd);
+#pragma unroll
+        for (int i = 0; i < kXPer; ++i) {
+          const uint32_t chunk = tid + (uint32_t)i * (64u * W);
+          if (chunk < (uint32_t)kXChunks)
+            *reinterpret_cast<uint4 *>(xb + (chunk >> 4) * kLd + (chunk & 15u) * 8u) = S[p].xv[i];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+          for (int j = 0; j < NT; ++j)
+            bfr[kk][j] = *reinterpret_cast<const half8_t *>(xb + (16u * j + fr) * kLd +
+                                                             32u * kk + 8u * g);
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+          for (int j = 0; j < NT; ++j)
+            bfr[kk][j] = __builtin_bit_cast(half8_t, S[p].xv[kk * NT + j]);
+      }
+      // refill this slot PF steps ahead (unconditional; past the end: zeros)
+      load_step(S[p], ks + (uint32_t)PF);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < NT; ++j)
+            acc[i][j] =
+                __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i][kk], bfr[kk][j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const uint32_t b = n0 + 16u * j + fr;
+      const uint32_t r0 = m0 + wave * 32u + 16u * i + 4u * g;
+      if (b >= batch) continue;
+      float *dst = y + (size_t)b * n_rows + r0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (r0 + e < n_rows) dst[e] = acc[i][j][e];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// K-split variant for small batches (memory- and dequant-bound): the KS waves
+// of a workgroup share one 32 x TN output tile and take interleaved K steps
+// (wave w: steps w, w + KS, ...), with register A fragments and X fragments
+// from global memory as in q4k_matmul_rf.  The KS partial tiles are summed in
+// LDS in wave order (deterministic) by wave 0.
+// ---------------------------------------------------------------------------
+template <int KS, int NT, int PF>
+__device__ __forceinline__ void q4k_matmul_ks(const uint8_t *__restrict__ q,
+                                              const uint16_t *__restrict__ x,
+                                              float *__restrict__ y, const MatmulArgs a) {
+  constexpr int TN = 16 * NT;
+  __shared__ __attribute__((aligned(16))) f32x4_t red[KS > 1 ? (KS - 1) * 2 * NT * 64 : 1];
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t n_rows = a.n_rows, nsb = a.sb_per_row, batch = a.batch;
+  const uint32_t m0 = blockIdx.x * 32u, n0 = blockIdx.y * TN;
+  const uint32_t K = nsb * 256u;
+  const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
+  const __amdgpu_buffer_rsrc_t qr = rsrc(q, n_rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t xr = rsrc(x, batch * K * 2u);
+  const uint32_t fr = lane & 15u, g = lane >> 4;
+  const uint32_t n_steps = 2u * nsb;
+
+  uint32_t row_off[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t row = m0 + 16u * (uint32_t)i + fr;
+    row_off[i] = row < n_rows ? row * row_bytes : kOob;
+  }
+  uint32_t xoff0[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const uint32_t b = n0 + 16u * (uint32_t)j + fr;
+    xoff0[j] = b < batch ? (b * K + 8u * g) * 2u : kOob;
+  }
+
+  auto load_step = [&](RfStep<NT, 1, false> &S, uint32_t ks) {
+    const uint32_t sb = ks >> 1, h = ks & 1u;
+    const bool live = ks < n_steps;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t base = (row_off[i] == kOob || !live) ? kOob : row_off[i] + sb * 144u;
+      S.hd[i] = bload16(qr, base);
+      const uint32_t qo = 16u + 64u * h + 8u * g;
+      S.qlo[i] = bload8(qr, base == kOob ? kOob : base + qo);
+      S.qhi[i] = bload8(qr, base == kOob ? kOob : base + qo + 32u);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+        S.xv[kk * NT + j] =
+            bload16(xr, (xoff0[j] == kOob || !live) ? kOob : xoff0[j] + ks * 256u + 64u * kk);
+  };
+
+  f32x4_t acc[2][NT];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[i][j] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+
+  RfStep<NT, 1, false> S[PF];
+#pragma unroll
+  for (int p = 0; p < PF; ++p) load_step(S[p], wave + (uint32_t)(p * KS));
+
+  const uint32_t my_steps = (n_steps + KS - 1u) / KS;
+  const uint32_t n_iter = (my_steps + PF - 1u) / PF * PF;
+  for (uint32_t j0 = 0; j0 < n_iter; j0 += PF) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+      const uint32_t ks = wave + (j0 + (uint32_t)p) * KS;
+      const uint32_t h = ks & 1u;
+      half8_t af[2][4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const uint4 hd = S[p].hd[i];
+        const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          const uint32_t c = 2u * h + (uint32_t)cc;
+          uint32_t scp, mp;
+          q4k_scale_min_pair(hd.y, hd.z, hd.w, c, &scp, &mp);
+          const float d1s = d * (float)(scp & 0xFFu) * 16777216.0f;
+          const float d2s = d * (float)(scp >> 8) * 1048576.0f;
+          const float m1 = dmin * (float)(mp & 0xFFu), m2 = dmin * (float)(mp >> 8);
+          const uint2 qw = cc == 0 ? S[p].qlo[i] : S[p].qhi[i];
+          uint32_t l0, l1, h0, h1, l2, l3, h2, h3;
+          dequant_dword(qw.x, d1s, m1, d2s, m2, l0, l1, h0, h1);
+          dequant_dword(qw.y, d1s, m1, d2s, m2, l2, l3, h2, h3);
+          af[i][2 * cc] = __builtin_bit_cast(half8_t, make_uint4(l0, l1, l2, l3));
+          af[i][2 * cc + 1] = __builtin_bit_cast(half8_t, make_uint4(h0, h1, h2, h3));
+        }
+      }
+      half8_t bfr[4][NT];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) bfr[kk][j] = __builtin_bit_cast(half8_t, S[p].xv[kk * NT + j]);
+      load_step(S[p], ks + (uint32_t)(PF * KS));
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < NT; ++j)
+            acc[i][j] =
+                __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i][kk], bfr[kk][j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  if constexpr (KS > 1) {
+    if (wave > 0) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) red[(((wave - 1u) * 2u + i) * NT + j) * 64u + lane] = acc[i][j];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (uint32_t w = 1; w < (uint32_t)KS; ++w)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] += red[(((w - 1u) * 2u + i) * NT + j) * 64u + lane];
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const uint32_t b = n0 + 16u * j + fr;
+      const uint32_t r0 = m0 + 16u * i + 4u * g;
+      if (b >= batch) continue;
+      float *dst = y + (size_t)b * n_rows + r0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (r0 + e < n_rows) dst[e] = acc[i][j][e];
+    }
+}
+
+} // namespace
+
+#define AXH_Q4K_MATMUL(W, NT)                                                                    \
+  extern "C" __global__ void __launch_bounds__(W * 64)                                           \
+      axh_q4k_matmul_w##W##_n##NT(const uint8_t *__restrict__ q, const uint16_t *__restrict__ x, \
+                                  float *__restrict__ y, MatmulArgs a) {                         \
+    q4k_matmul<W, NT>(q, x, y, a);                                                               \
+  }
+
+AXH_Q4K_MATMUL(1, 1)
+AXH_Q4K_MATMUL(2, 2)
+AXH_Q4K_MATMUL(4, 4)
+AXH_Q4K_MATMUL(4, 8)
+
+#define AXH_Q4K_MATMUL_RF(W, NT, PF, XL)                                                         \
+  extern "C" __global__ void __launch_bounds__(W * 64)                                           \
+      axh_q4k_matmul_rf_w##W##_n##NT##_p##PF##_x##XL(const uint8_t *__restrict__ q,             \
+                                                      const uint16_t *__restrict__ x,            \
+                                                      float *__restrict__ y, MatmulArgs a) {     \
+    q4k_matmul_rf<W, NT, PF, XL != 0>(q, x, y, a);                                               \
+  }
+
+AXH_Q4K_MATMUL_RF(4, 4, 2, 1)
+AXH_Q4K_MATMUL_RF(4, 8, 1, 1)
+
+#define AXH_Q4K_MATMUL_KS(KS, NT, PF)                                                            \
+  extern "C" __global__ void __launch_bounds__(KS * 64)                                          \
+      axh_q4k_matmul_ks_k##KS##_n##NT##_p##PF(const uint8_t *__restrict__ q,                     \
+                                              const uint16_t *__restrict__ x,                    \
+                                              float *__restrict__ y, MatmulArgs a) {             \
+    q4k_matmul_ks<KS, NT, PF>(q, x, y, a);                                                       \
+  }
+
+AXH_Q4K_MATMUL_KS(4, 1, 2)
+AXH_Q4K_MATMUL_KS(8, 1, 1)
+AXH_Q4K_MATMUL_KS(4, 2, 2)
+AXH_Q4K_MATMUL_KS(8, 2, 1)

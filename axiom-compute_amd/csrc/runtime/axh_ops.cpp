@@ -7,9 +7,11 @@
 
 #include "axh_internal.h"
 
-// Code object embedded by axh_embed.S (.incbin of the gfx950 ELF).
+// Code objects embedded by axh_embed.S (.incbin of the gfx950 ELFs).
 extern "C" const unsigned char axh_q4_matvec_co_begin[];
 extern "C" const unsigned char axh_q4_matvec_co_end[];
+extern "C" const unsigned char axh_q4_matmul_co_begin[];
+extern "C" const unsigned char axh_q4_matmul_co_end[];
 
 namespace axh {
 
@@ -24,6 +26,24 @@ struct RowsArgs {
 struct CountArgs {
   uint32_t n_units;
 };
+struct MatmulArgs {
+  uint32_t n_rows;
+  uint32_t sb_per_row;
+  uint32_t batch;
+  uint32_t pad;
+};
+
+// Compiled batched-matmul kernels (keep in sync with q4_matmul.hip):
+//   kind 1 (LDS-tiled)  axh_q4k_matmul_w{W}_n{NT}: W waves x 32 rows, NT 16-column tiles;
+//   kind 2 (register A) axh_q4k_matmul_rf_w{W}_n{NT}_p{PF}_x1;
+//   kind 3 (K-split)    axh_q4k_matmul_ks_k{W}_n{NT}_p{PF}: W waves split K of one 32-row tile.
+struct MatmulVariant {
+  uint32_t kind, w, nt, pf;
+};
+constexpr MatmulVariant kQ4kMatmulVariants[] = {
+    {1, 1, 1, 1}, {1, 2, 2, 1}, {1, 4, 4, 1}, {1, 4, 8, 1}, {2, 4, 4, 2},
+    {2, 4, 8, 1}, {3, 4, 1, 2}, {3, 8, 1, 1}, {3, 4, 2, 2}, {3, 8, 2, 1}};
+constexpr uint32_t kMatmulOob = 0xFFFFFF00u; // the kernels' out-of-range offset
 
 struct MatvecVariant {
   uint32_t rpw, nw, pf, nt;
@@ -71,6 +91,10 @@ axh_status builtin_kernel(axh_context *ctx, const char *entry, uint32_t n_buffer
   plan.dynamic_lds_bytes = 0;
   size_t n = 0;
   const void *co = axh_builtin_code_object(&n);
+  if (std::strncmp(entry, "axh_q4k_matmul_", 15) == 0) {
+    co = axh_q4_matmul_co_begin;
+    n = (size_t)(axh_q4_matmul_co_end - axh_q4_matmul_co_begin);
+  }
   axh_kernel *k = nullptr;
   axh_status s = axh_prepare_kernel(ctx, co, n, &plan, pc_bytes, entry, &k);
   if (s != AXH_OK) return s;
@@ -345,6 +369,102 @@ axh_status axh_q4_0_matvec(axh_context *ctx, const void *q, const float *x, floa
   void *bufs[3] = {const_cast<void *>(q), const_cast<float *>(x), y};
   hipSetDevice(ctx->core->device);
   s = launch_raw(k, grid, bufs, 3, &a, sizeof(a), lds, pick_stream(ctx, stream));
+  return s == AXH_OK ? ok() : s;
+}
+
+// Defaults from on-device sweeps at 14336 x 4096 (K-split while the batch
+// fits one or two 16-column tiles, LDS tiles in the middle, register A for
+// large batches).
+static MatmulVariant q4k_matmul_default(uint32_t n_rows, uint32_t batch) {
+  (void)n_rows;
+  if (batch <= 16) return {3, 8, 1, 1};
+  if (batch <= 32) return {3, 8, 2, 1};
+  if (batch <= 128) return {1, 4, 4, 1};
+  return {2, 4, 8, 1};
+}
+
+uint32_t axh_q4k_matmul_variant_count(void) {
+  return (uint32_t)(sizeof(kQ4kMatmulVariants) / sizeof(kQ4kMatmulVariants[0]));
+}
+
+axh_status axh_q4k_matmul_variant_at(uint32_t i, axh_q4_matmul_variant *out) {
+  if (!out || i >= axh_q4k_matmul_variant_count())
+    return fail(AXH_ERR_INVALID_ARGUMENT, "variant index out of range");
+  out->kind = kQ4kMatmulVariants[i].kind;
+  out->waves_per_workgroup = kQ4kMatmulVariants[i].w;
+  out->col_tiles = kQ4kMatmulVariants[i].nt;
+  out->prefetch = kQ4kMatmulVariants[i].pf;
+  return ok();
+}
+
+static axh_status plan_q4k_matmul(uint32_t n_rows, uint32_t batch,
+                                  const axh_q4_matmul_variant *variant, MatmulVariant *out,
+                                  char *name, size_t cap) {
+  MatmulVariant want = q4k_matmul_default(n_rows, batch);
+  if (variant) {
+    if (variant->kind) want.kind = variant->kind;
+    if (variant->waves_per_workgroup) want.w = variant->waves_per_workgroup;
+    if (variant->col_tiles) want.nt = variant->col_tiles;
+    if (variant->prefetch) want.pf = variant->prefetch;
+  }
+  for (const MatmulVariant &v : kQ4kMatmulVariants)
+    if (v.kind == want.kind && v.w == want.w && v.nt == want.nt && v.pf == want.pf) {
+      *out = v;
+      if (v.kind == 1)
+        std::snprintf(name, cap, "axh_q4k_matmul_w%u_n%u", v.w, v.nt);
+      else if (v.kind == 2)
+        std::snprintf(name, cap, "axh_q4k_matmul_rf_w%u_n%u_p%u_x1", v.w, v.nt, v.pf);
+      else
+        std::snprintf(name, cap, "axh_q4k_matmul_ks_k%u_n%u_p%u", v.w, v.nt, v.pf);
+      return ok();
+    }
+  return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_K matmul variant matches");
+}
+
+axh_status axh_q4k_matmul_kernel_name(uint32_t n_rows, uint32_t batch,
+                                      const axh_q4_matmul_variant *variant, char *buf,
+                                      size_t cap) {
+  if (!buf || cap == 0) return fail(AXH_ERR_INVALID_ARGUMENT, "buf is NULL");
+  MatmulVariant v{};
+  char name[64];
+  axh_status s = plan_q4k_matmul(n_rows, batch, variant, &v, name, sizeof(name));
+  if (s != AXH_OK) return s;
+  if (std::strlen(name) + 1 > cap) return fail(AXH_ERR_INVALID_ARGUMENT, "buf too small");
+  std::memcpy(buf, name, std::strlen(name) + 1);
+  return ok();
+}
+
+axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x, float *y,
+                              uint32_t n_rows, uint32_t sb_per_row, uint32_t batch,
+                              const axh_q4_matmul_variant *variant, void *stream) {
+  if (!ctx) return fail(AXH_ERR_INVALID_ARGUMENT, "ctx is NULL");
+  if (n_rows == 0 || batch == 0) return ok();
+  if (sb_per_row == 0)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "sb_per_row must be at least 1 for the matmul");
+  if (!device_ptr_ok(q) || !device_ptr_ok(x) || !device_ptr_ok(y))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q, x and y must be device pointers");
+  if (((uintptr_t)q & 15u) || ((uintptr_t)x & 15u) || ((uintptr_t)y & 3u))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q and x must be 16-byte and y 4-byte aligned");
+  const uint64_t q_bytes = (uint64_t)n_rows * sb_per_row * 144u;
+  const uint64_t x_bytes = (uint64_t)batch * sb_per_row * 256u * 2u;
+  if (q_bytes >= kMatmulOob || x_bytes >= kMatmulOob)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q and x must each be below 4 GiB - 256 B");
+  MatmulVariant v{};
+  char name[64];
+  axh_status s = plan_q4k_matmul(n_rows, batch, variant, &v, name, sizeof(name));
+  if (s != AXH_OK) return s;
+  const uint32_t tm = v.kind == 3 ? 32u : 32u * v.w, tn = 16u * v.nt;
+  const uint64_t gx = (n_rows + tm - 1) / tm, gy = (batch + tn - 1) / tn;
+  if (gx > ctx->core->max_wg[0] || gy > ctx->core->max_wg[1])
+    return fail(AXH_ERR_WORKGROUP_COUNT_EXCEEDS_LIMIT, "matmul grid exceeds the device limit");
+  hipSetDevice(ctx->core->device);
+  axh_kernel *k = nullptr;
+  s = builtin_kernel(ctx, name, 3, sizeof(MatmulArgs), v.w * 64u, &k);
+  if (s != AXH_OK) return s;
+  const uint32_t grid[3] = {(uint32_t)gx, (uint32_t)gy, 1};
+  void *bufs[3] = {const_cast<void *>(q), const_cast<uint16_t *>(x), y};
+  MatmulArgs a{n_rows, sb_per_row, batch, 0};
+  s = launch_raw(k, grid, bufs, 3, &a, sizeof(a), 0, pick_stream(ctx, stream));
   return s == AXH_OK ? ok() : s;
 }
 

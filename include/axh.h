@@ -209,6 +209,29 @@ axh_status axh_q4k_matvec_variant_at(uint32_t i, axh_q4_variant *out);
 uint32_t axh_q4_0_matvec_variant_count(void);
 axh_status axh_q4_0_matvec_variant_at(uint32_t i, axh_q4_variant *out);
 
+/* Batched Q4_K_M matmul on MFMA (f16 in, f32 accumulate):
+ *   y[b * n_rows + r] = sum_k RN_f16(w32[r][k]) * x[b * K + k],  K = 256 * sb_per_row,
+ * for b < batch, where w32 is the reference's f32 dequantisation
+ * (crates/axc-driver/tests/common_helpers.rs:437-454) and x holds `batch`
+ * contiguous f16 activation vectors.  Y is batch x n_rows f32.  The reference
+ * has no batched kernel (its matvec, examples/q4km_dequant_matvec.axc, is the
+ * batch = 1 case with f32 weights); multi-row matmul is roadmap there
+ * (ROADMAP.md:54-72).  q and x 16-byte aligned, each below 4 GiB. */
+typedef struct axh_q4_matmul_variant {
+    uint32_t kind;                /* 1 LDS-tiled, 2 register A, 3 K-split; 0 = default */
+    uint32_t waves_per_workgroup; /* kinds 1-2: 32 rows per wave; kind 3: waves splitting K */
+    uint32_t col_tiles;           /* 16-column MFMA tiles per workgroup */
+    uint32_t prefetch;            /* K steps in flight (kinds 2-3) */
+} axh_q4_matmul_variant;
+axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x, float *y,
+                              uint32_t n_rows, uint32_t sb_per_row, uint32_t batch,
+                              const axh_q4_matmul_variant *variant, void *stream);
+axh_status axh_q4k_matmul_kernel_name(uint32_t n_rows, uint32_t batch,
+                                      const axh_q4_matmul_variant *variant, char *buf,
+                                      size_t cap);
+uint32_t axh_q4k_matmul_variant_count(void);
+axh_status axh_q4k_matmul_variant_at(uint32_t i, axh_q4_matmul_variant *out);
+
 /* The built-in code object holding every kernel above, for callers that drive
  * the generic prepare/dispatch API (e.g. the reference-contract kernels
  * "q4km_dequant_matvec" and "q4_0_dequant_matvec"). */

@@ -158,3 +158,20 @@ def test_context_without_gpu_reports_typed_error(axc):
     else:
         assert "gfx950" in ctx.device_name or ctx.device_name
         ctx.close()
+
+
+def test_matmul_kernel_selection(axc):
+    name = axc.q4k_matmul_kernel_name
+    assert name(14336, 8) == "axh_q4k_matmul_ks_k8_n1_p1"
+    assert name(14336, 32) == "axh_q4k_matmul_ks_k8_n2_p1"
+    assert name(14336, 128) == "axh_q4k_matmul_w4_n4"
+    assert name(14336, 512) == "axh_q4k_matmul_rf_w4_n8_p1_x1"
+    assert name(14336, 512, axc.MatmulVariant(1, 2, 2, 1)) == "axh_q4k_matmul_w2_n2"
+    assert name(14336, 8, axc.MatmulVariant(3, 4, 1, 2)) == "axh_q4k_matmul_ks_k4_n1_p2"
+    with pytest.raises(axc.DispatchError):
+        name(14336, 8, axc.MatmulVariant(1, 3, 1, 1))
+    vs = axc.compiled_matmul_variants()
+    assert len(set(vs)) == len(vs) >= 6
+    assert {v.kind for v in vs} == {1, 2, 3}
+    for v in vs:
+        assert name(64, 64, v).startswith("axh_q4k_matmul_")

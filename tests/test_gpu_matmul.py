@@ -1,0 +1,156 @@
+"""Batched Q4_K_M matmul on MFMA (marked `gpu`): y_b = RN_f16(W) x_b for f16
+activation vectors x_b.  The reference has no batched kernel; per column it
+is the reference dot product (q4km_dequant_matvec_cpu,
+crates/axc-driver/tests/common_helpers.rs:411-461) with x widened from f16.
+
+Three checks, from tight to loose:
+  * one-hot activations pick single weights: y = RN_f16(w32) bit for bit
+    (pins the f16 weights against numpy's float16 rounding of the oracle's
+    bit-exact f32 dequantisation);
+  * against an f64 product of the same f16 weights: only f32 accumulation
+    error remains (norm-wise <= 1e-5);
+  * against the f32-weight oracle (the reference's arithmetic per column):
+    per row |dy| <= 2^-11 * sum|w*x| (f16 weight rounding) + 1e-5 * sum|w*x|,
+    and norm-wise <= 1e-3.
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _dev(ctx, arr):
+    b = ctx.alloc(max(arr.nbytes, 16))
+    ctx.upload(b, arr)
+    return b
+
+
+def _run(ctx, q, xh, rows, sb, batch, variant=None):
+    dq, dx, dy = _dev(ctx, q), _dev(ctx, xh), ctx.alloc(batch * rows * 4)
+    ctx.q4k_matmul(dq, dx, dy, rows, sb, batch, variant)
+    ctx.synchronize()
+    y = np.frombuffer(ctx.download(dy, batch * rows * 4), dtype=np.float32).reshape(batch, rows)
+    for b in (dq, dx, dy):
+        b.close()
+    return y.copy()
+
+
+def _inputs(seed, rows, sb, batch):
+    q = O.gen_q4k_weights(seed, rows * sb)
+    xh = O.gen_normal_f32(seed + 1, sb * 256 * batch).astype(np.float16)
+    return q, xh
+
+
+def _w32(q, rows, sb):
+    return O.q4k_dequant(q, rows * sb).reshape(rows, sb * 256)
+
+
+def _check(y, q, xh, rows, sb, batch, what, oracle_f32=True):
+    w32 = _w32(q, rows, sb)
+    w16 = w32.astype(np.float16).astype(np.float64)
+    xf = xh.astype(np.float64).reshape(batch, sb * 256)
+    ref16 = xf @ w16.T                              # batch x rows, f64
+    abs16 = np.abs(xf) @ np.abs(w16).T
+    err16 = np.linalg.norm(y - ref16) / max(np.linalg.norm(ref16), 1e-30)
+    worst = float(np.max(np.abs(y - ref16) / np.maximum(abs16, 1e-30)))
+    _say(f"{what}: vs f16-weight f64 ref norm {err16:.2e}, worst/sum|wx| {worst:.2e}")
+    assert err16 <= 1e-5, what
+    assert np.all(np.abs(y - ref16) <= 1e-5 * abs16 + 1e-30), what
+    # f32-weight reference (the reference's per-column arithmetic)
+    if oracle_f32:
+        ref = O.q4k_matmul_f16x(q, xh.view(np.uint16), rows, sb, batch).T  # batch x rows
+    else:
+        ref = xf @ w32.astype(np.float64).T
+    abs32 = np.abs(xf) @ np.abs(w32.astype(np.float64)).T
+    d = np.abs(y.astype(np.float64) - ref)
+    bound = (2.0 ** -11 + 1e-5) * abs32
+    norm = np.linalg.norm(y - ref) / max(np.linalg.norm(ref), 1e-30)
+    _say(f"{what}: vs f32-weight ref norm {norm:.2e}, max d/bound {float(np.max(d / bound)):.3f}")
+    assert np.all(d <= bound), what
+    assert norm <= 1e-3, what
+
+
+def test_one_hot_activations_give_rn_f16_weights_bit_exact(ctx):
+    rows, sb = 64, 1
+    batch = sb * 256
+    q = O.gen_q4k_weights(71, rows * sb)
+    xh = np.eye(batch, dtype=np.float16)  # x_b = e_b
+    y = _run(ctx, q, xh, rows, sb, batch)
+    w16 = _w32(q, rows, sb).astype(np.float16).astype(np.float32)
+    assert np.array_equal(y.view(np.uint32), w16.T.copy().view(np.uint32))
+
+
+def test_one_hot_lcg_fixture_weights(ctx):
+    """The reference's own generator (seed 0xDEADBEEF, 16 superblocks) as one row."""
+    q, _ = O.generate_q4km_test_data(16, 0xDEADBEEF)
+    batch = 256
+    for part in range(16):  # superblock `part` selected by one-hot vectors
+        xh = np.zeros((batch, 16 * 256), dtype=np.float16)
+        xh[np.arange(batch), part * 256 + np.arange(batch)] = 1.0
+        y = _run(ctx, q, xh, 1, 16, batch)
+        w16 = O.q4k_dequant(q, 16)[part * 256:(part + 1) * 256].astype(np.float16)
+        assert np.array_equal(y[:, 0].astype(np.float16).view(np.uint16), w16.view(np.uint16))
+
+
+@pytest.mark.parametrize("batch", [8, 32, 128, 512])
+def test_c5_down_projection_shapes(ctx, batch):
+    """14336 x 4096 weights, B f16 activations ~ N(0, 1)."""
+    rows, sb = 14336, 16
+    _say(f"matmul C5 batch {batch}")
+    q, xh = _inputs(500 + batch, rows, sb, batch)
+    y = _run(ctx, q, xh, rows, sb, batch)
+    _check(y, q, xh, rows, sb, batch, f"C5 B={batch}", oracle_f32=batch <= 32)
+
+
+@pytest.mark.parametrize("rows,sb,batch", [(1, 1, 1), (100, 1, 7), (33, 3, 17), (257, 2, 130),
+                                           (96, 5, 16), (31, 4, 33)])
+def test_edge_shapes(ctx, rows, sb, batch):
+    """Partial row and column tiles, single superblock, batch 1."""
+    _say(f"matmul edge {rows}x{sb * 256} B={batch}")
+    q, xh = _inputs(rows * 7 + sb * 3 + batch, rows, sb, batch)
+    y = _run(ctx, q, xh, rows, sb, batch)
+    _check(y, q, xh, rows, sb, batch, f"edge {rows}x{sb} B={batch}")
+
+
+def test_every_variant(ctx, axc):
+    rows, sb, batch = 200, 3, 40
+    q, xh = _inputs(91, rows, sb, batch)
+    for v in axc.compiled_matmul_variants():
+        _say(f"matmul variant {v}")
+        y = _run(ctx, q, xh, rows, sb, batch, v)
+        _check(y, q, xh, rows, sb, batch, f"variant {v}")
+
+
+def test_batch_one_matches_the_matvec_within_f16_weight_rounding(ctx):
+    rows, sb = 512, 16
+    q, xh = _inputs(93, rows, sb, 1)
+    y = _run(ctx, q, xh, rows, sb, 1)[0]
+    dq, dx, dy = _dev(ctx, q), _dev(ctx, xh.astype(np.float32)), ctx.alloc(rows * 4)
+    ctx.q4k_matvec(dq, dx, dy, rows, sb)
+    ctx.synchronize()
+    ymv = np.frombuffer(ctx.download(dy, rows * 4), dtype=np.float32)
+    for b in (dq, dx, dy):
+        b.close()
+    absd = np.abs(_w32(q, rows, sb).astype(np.float64)) @ np.abs(xh.astype(np.float64))
+    assert np.all(np.abs(y.astype(np.float64) - ymv) <= (2.0 ** -11 + 2e-5) * absd)
+
+
+def test_invalid_arguments_are_typed_errors(ctx, axc):
+    b = ctx.alloc(64)
+    with pytest.raises(axc.DispatchError):
+        ctx.q4k_matmul(b, b, b, 4, 0, 2)  # no superblocks
+    with pytest.raises(axc.DispatchError):
+        ctx.q4k_matmul(b, b, b, 4, 1, 2, axc.MatmulVariant(1, 3, 3, 1))  # not compiled
+    ctx.q4k_matmul(b, b, b, 0, 1, 2)  # empty: nothing to do
+    b.close()
