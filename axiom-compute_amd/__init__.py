@@ -10,6 +10,7 @@ from .axh import (  # noqa: F401
     DeviceBuffer,
     DispatchError,
     DispatchRequest,
+    Graph,
     HipContext,
     HipContextOptions,
     KernelHandle,
@@ -20,6 +21,7 @@ from .axh import (  # noqa: F401
     MatmulVariant,
     q4k_matmul_kernel_name,
     q4k_matvec_kernel_name,
+    q4_0_matvec_kernel_name,
     load_library,
     validate_request,
 )
@@ -30,6 +32,7 @@ __all__ = [
     "DeviceBuffer",
     "DispatchError",
     "DispatchRequest",
+    "Graph",
     "HipContext",
     "HipContextOptions",
     "KernelHandle",
@@ -40,6 +43,7 @@ __all__ = [
     "MatmulVariant",
     "q4k_matmul_kernel_name",
     "q4k_matvec_kernel_name",
+    "q4_0_matvec_kernel_name",
     "load_library",
     "validate_request",
 ]

@@ -146,7 +146,13 @@ def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
         "axh_event_elapsed_ms": (st, [vp, vp, c.POINTER(c.c_float)]),
         "axh_event_destroy": (None, [vp]),
         "axh_q4k_matvec": (st, [vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
+        "axh_capture_begin": (st, [vp]),
+        "axh_capture_end": (st, [vp, c.POINTER(vp)]),
+        "axh_graph_launch": (st, [vp, vp, vp]),
+        "axh_graph_node_count": (u64, [vp]),
+        "axh_graph_destroy": (None, [vp]),
         "axh_q4k_matvec_kernel_name": (st, [u32, u32, c.POINTER(_Variant), c.c_char_p, sz]),
+        "axh_q4_0_matvec_kernel_name": (st, [u32, u32, c.POINTER(_Variant), c.c_char_p, sz]),
         "axh_q4k_matmul_f16": (st, [vp, vp, vp, vp, u32, u32, u32, c.POINTER(_MatmulVariant),
                                     vp]),
         "axh_q4k_matmul_kernel_name": (st, [u32, u32, c.POINTER(_MatmulVariant), c.c_char_p,
@@ -246,6 +252,17 @@ def q4k_matmul_kernel_name(n_rows: int, batch: int,
     v = variant._c() if variant else None
     buf = ctypes.create_string_buffer(64)
     _check(lib.axh_q4k_matmul_kernel_name(n_rows, batch, ctypes.byref(v) if v else None, buf, 64))
+    return buf.value.decode()
+
+
+def q4_0_matvec_kernel_name(n_rows: int, blocks_per_row: int,
+                            variant: Optional[Variant] = None) -> str:
+    """Entry point axh_q4_0_matvec launches for this shape and variant."""
+    lib = load_library()
+    v = variant._c() if variant else None
+    buf = ctypes.create_string_buffer(64)
+    _check(lib.axh_q4_0_matvec_kernel_name(n_rows, blocks_per_row,
+                                           ctypes.byref(v) if v else None, buf, 64))
     return buf.value.decode()
 
 
@@ -359,6 +376,32 @@ class Event:
             if self._raw:
                 self._ctx._lib.axh_event_destroy(self._raw)
                 self._raw = 0
+        except Exception:
+            pass
+
+
+class Graph:
+    """Launches captured on a context stream, replayed with launch()."""
+
+    def __init__(self, ctx: "HipContext", raw: int):
+        self._ctx = ctx
+        self._raw = raw
+
+    @property
+    def node_count(self) -> int:
+        return int(self._ctx._lib.axh_graph_node_count(self._raw))
+
+    def launch(self, stream=None) -> None:
+        _check(self._ctx._lib.axh_graph_launch(self._ctx._raw, self._raw, _stream(stream)))
+
+    def close(self) -> None:
+        if self._raw:
+            self._ctx._lib.axh_graph_destroy(self._raw)
+            self._raw = 0
+
+    def __del__(self):
+        try:
+            self.close()
         except Exception:
             pass
 
@@ -550,6 +593,20 @@ class HipContext:
 
     def event(self) -> "Event":
         return Event(self)
+
+    def capture(self, fn) -> "Graph":
+        """Runs fn() with the context stream in capture mode and returns the
+        graph of the launches it issued."""
+        _check(self._lib.axh_capture_begin(self._raw))
+        g = ctypes.c_void_p()
+        try:
+            fn()
+        except BaseException:
+            if self._lib.axh_capture_end(self._raw, ctypes.byref(g)) == 0 and g.value:
+                self._lib.axh_graph_destroy(g)
+            raise
+        _check(self._lib.axh_capture_end(self._raw, ctypes.byref(g)))
+        return Graph(self, int(g.value))
 
     # ---- Q4 operations -----------------------------------------------------
     def q4k_matvec(self, q, x, y, n_rows: int, sb_per_row: int,

@@ -336,6 +336,26 @@ axh_status axh_q4k_matvec(axh_context *ctx, const void *q, const float *x, float
   return s == AXH_OK ? ok() : s;
 }
 
+static const MatvecVariant *pick_q4_0(uint32_t n_rows, uint32_t blocks_per_row,
+                                      const axh_q4_variant *variant) {
+  axh_q4_variant vv{};
+  if (variant) vv = *variant;
+  vv.prefetch = 1;
+  vv.nontemporal = 2;
+  return find_variant(kQ4_0Variants, axh_q4_0_matvec_variant_count(), &vv,
+                      q4_0_default(n_rows, blocks_per_row));
+}
+
+axh_status axh_q4_0_matvec_kernel_name(uint32_t n_rows, uint32_t blocks_per_row,
+                                       const axh_q4_variant *variant, char *buf, size_t cap) {
+  if (!buf || cap == 0) return fail(AXH_ERR_INVALID_ARGUMENT, "buf is NULL");
+  const MatvecVariant *v = pick_q4_0(n_rows, blocks_per_row, variant);
+  if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_0 matvec variant matches");
+  const int n = std::snprintf(buf, cap, "axh_q4_0_matvec_r%u_w%u", v->rpw, v->nw);
+  if (n < 0 || (size_t)n >= cap) return fail(AXH_ERR_INVALID_ARGUMENT, "buf too small");
+  return ok();
+}
+
 axh_status axh_q4_0_matvec(axh_context *ctx, const void *q, const float *x, float *y,
                            uint32_t n_rows, uint32_t blocks_per_row,
                            const axh_q4_variant *variant, void *stream) {
@@ -347,12 +367,7 @@ axh_status axh_q4_0_matvec(axh_context *ctx, const void *q, const float *x, floa
     return fail(AXH_ERR_INVALID_ARGUMENT, "blocks_per_row too large");
   if (((uintptr_t)q & 3u) || ((uintptr_t)x & 15u))
     return fail(AXH_ERR_INVALID_ARGUMENT, "q must be 4-byte and x 16-byte aligned");
-  MatvecVariant dflt = q4_0_default(n_rows, blocks_per_row);
-  axh_q4_variant vv{};
-  if (variant) vv = *variant;
-  vv.prefetch = 1;
-  vv.nontemporal = 2;
-  const MatvecVariant *v = find_variant(kQ4_0Variants, axh_q4_0_matvec_variant_count(), &vv, dflt);
+  const MatvecVariant *v = pick_q4_0(n_rows, blocks_per_row, variant);
   if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_0 matvec variant matches");
   char name[64];
   std::snprintf(name, sizeof(name), "axh_q4_0_matvec_r%u_w%u", v->rpw, v->nw);

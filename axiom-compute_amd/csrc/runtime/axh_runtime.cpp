@@ -653,6 +653,65 @@ void axh_event_destroy(axh_event *ev) {
   if (ev) hipEventDestroy(reinterpret_cast<hipEvent_t>(ev));
 }
 
+// ---- graph capture ----------------------------------------------------------
+// A captured sequence of launches on the context stream, replayed as one
+// hipGraphExec (no host work per kernel).  Only kernel launches are captured:
+// the operations of this library record no memset or copy nodes.
+struct axh_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  uint64_t n_nodes = 0;
+};
+
+axh_status axh_capture_begin(axh_context *ctx) {
+  if (!ctx) return fail(AXH_ERR_INVALID_ARGUMENT, "ctx is NULL");
+  hipSetDevice(ctx->core->device);
+  hipError_t e = hipStreamBeginCapture(ctx->core->stream, hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) return fail(AXH_ERR_COMMAND_RECORD, hip_msg("hipStreamBeginCapture", e));
+  return ok();
+}
+
+axh_status axh_capture_end(axh_context *ctx, axh_graph **out) {
+  if (!ctx || !out) return fail(AXH_ERR_INVALID_ARGUMENT, "NULL argument");
+  *out = nullptr;
+  hipSetDevice(ctx->core->device);
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(ctx->core->stream, &g);
+  if (e != hipSuccess || !g)
+    return fail(AXH_ERR_COMMAND_RECORD, hip_msg("hipStreamEndCapture", e));
+  hipGraphExec_t exec = nullptr;
+  e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    hipGraphDestroy(g);
+    return fail(AXH_ERR_COMMAND_RECORD, hip_msg("hipGraphInstantiate", e));
+  }
+  size_t n = 0;
+  hipGraphGetNodes(g, nullptr, &n);
+  auto *G = new axh_graph;
+  G->graph = g;
+  G->exec = exec;
+  G->n_nodes = n;
+  *out = G;
+  return ok();
+}
+
+axh_status axh_graph_launch(axh_context *ctx, axh_graph *g, void *stream) {
+  if (!ctx || !g) return fail(AXH_ERR_INVALID_ARGUMENT, "NULL argument");
+  hipSetDevice(ctx->core->device);
+  hipError_t e = hipGraphLaunch(g->exec, pick_stream(ctx, stream));
+  if (e != hipSuccess) return fail(AXH_ERR_QUEUE_SUBMIT, hip_msg("hipGraphLaunch", e));
+  return ok();
+}
+
+uint64_t axh_graph_node_count(const axh_graph *g) { return g ? g->n_nodes : 0; }
+
+void axh_graph_destroy(axh_graph *g) {
+  if (!g) return;
+  if (g->exec) hipGraphExecDestroy(g->exec);
+  if (g->graph) hipGraphDestroy(g->graph);
+  delete g;
+}
+
 axh_status axh_synchronize(axh_context *ctx, void *stream) {
   if (!ctx) return fail(AXH_ERR_INVALID_ARGUMENT, "ctx is NULL");
   hipSetDevice(ctx->core->device);

@@ -1,11 +1,21 @@
-"""Benchmark of the MI355X Q4_K_M dequant-matvec hot path.
+"""Benchmark of the MI355X Q4_0 / Q4_K_M dequant-matvec hot path.
 
-One step = one Q4_K_M matvec of the 4096 x 14336 down-projection (BASELINE
-config 4, the north-star shape) over weights already resident in HBM.
-Weights rotate over enough distinct copies (> 256 MiB) that every call reads
-HBM instead of the Infinity Cache.  Prints ONE JSON line.
+Default (the headline metric): one step = one Q4_K_M matvec of the
+4096 x 14336 down-projection over weights already
+resident in HBM.  Weights rotate over enough distinct copies (> 512 MiB)
+that every call reads HBM instead of the 256 MiB Infinity Cache.  Prints ONE
+JSON line.  Other BASELINE configs are measured with --workload:
 
-  python bench.py [--gpus 1] [--steps 200] [--warmup 20]
+  c1    Q4_0 matvec 256 x 4096                 (GB/s of weights)
+  c2    Q4_K matvec 1 x 32768                  (GB/s of weights)
+  c3    Q4_K matvec 4096 x 4096
+  c3b   Q4_K matvec 14336 x 4096
+  c4    Q4_K matvec 4096 x 14336               (default)
+  head  Q4_K matvec 128256 x 4096              (output head)
+  c5    Q4_K matmul 14336 x 4096, --batch B    (f16 activations; GB/s for B <= 32,
+                                                TFLOP/s for larger B)
+
+  python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--workload c4] [--batch 128]
 """
 from __future__ import annotations
 
@@ -21,9 +31,21 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
-ROWS, SB = 4096, 56     # 4096 x 14336 Q4_K_M
+HBM_PEAK_GBS = 8000.0        # MI355X published HBM3E bandwidth
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16 MFMA
 COPIES_MIN_BYTES = 512 << 20
+COPY_ALIGN = 256
+
+# name: (kind, rows, units per row, x sigma, config label)
+WORKLOADS = {
+    "c1": ("q4_0", 256, 128, 1.0, "config 1"),
+    "c2": ("q4k", 1, 128, 1.0, "config 2"),
+    "c3": ("q4k", 4096, 16, 1.0, "config 3"),
+    "c3b": ("q4k", 14336, 16, 1.0, "config 3"),
+    "c4": ("q4k", 4096, 56, 0.5, "config 4, down-projection"),
+    "head": ("q4k", 128256, 16, 1.0, "config 4, output head"),
+    "c5": ("matmul", 14336, 16, 1.0, "config 5"),
+}
 
 
 def cpu_model() -> str:
@@ -47,31 +69,6 @@ def _time_cpu(fn, budget_s: float):
             return n, el
 
 
-def cpu_baseline(O, q, x, rows, sb, budget_s: float) -> dict:
-    """The oracle (C restatement of q4km_dequant_matvec_cpu: scalar, the
-    reference's order) on the full matrix for about `budget_s` seconds on one
-    core, then row-parallel over the host's cores for a quarter of that."""
-    weight_bytes = rows * sb * 144
-    n, el = _time_cpu(lambda: O.q4k_matvec_single(q, x, rows, sb), budget_s)
-    threads = max(1, min(os.cpu_count() or 1, 16))
-    nm, elm = _time_cpu(lambda: O.q4k_matvec(q, x, rows, sb, threads=threads),
-                        max(1.0, budget_s / 4))
-    return {
-        "value": round(weight_bytes * n / el / 1e9, 4),
-        "unit": "GB/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": f"{n} full {rows}x{sb * 256} Q4_K matvecs in {el:.1f}s, one thread "
-                  f"({cpu_model()}, nproc={os.cpu_count()}); {el / n * 1e6:.0f} us/call",
-        "all_cores": {
-            "value": round(weight_bytes * nm / elm / 1e9, 4),
-            "cores": threads,
-            "sample": f"{nm} full matvecs in {elm:.1f}s, rows split over {threads} threads "
-                      f"(bit-identical to one thread); {elm / nm * 1e6:.0f} us/call",
-        },
-    }
-
-
 def profiled_traffic(kernel: str, workload: str):
     """HBM bytes per launch of `kernel` at `workload`, as recorded by the
     FETCH_SIZE / WRITE_SIZE counter summary under profiles/ (None if that
@@ -86,13 +83,154 @@ def profiled_traffic(kernel: str, workload: str):
     return None, None
 
 
+class Case:
+    """One workload: device buffers, the launch of step i, parity, CPU baseline."""
+
+    def __init__(self, pkg, O, np, ctx, name, batch, variant):
+        kind, rows, units, sigma, label = WORKLOADS[name]
+        self.kind, self.rows, self.units, self.label = kind, rows, units, label
+        self.ctx, self.O, self.np, self.pkg = ctx, O, np, pkg
+        self.batch = batch if kind == "matmul" else 1
+        unit_bytes = 18 if kind == "q4_0" else 144
+        self.cols = units * (32 if kind == "q4_0" else 256)
+        self.weight_bytes = rows * units * unit_bytes
+        seed = 20241 if name == "c4" else 30000 + rows + units
+        if kind == "q4_0":
+            self.q = O.gen_q4_0_weights(seed, rows * units)
+        else:
+            self.q = O.gen_q4k_weights(seed, rows * units)
+        if kind == "matmul":
+            self.x = O.gen_normal_f32(seed + 1, self.cols * self.batch, sigma).astype(np.float16)
+            self.y_bytes = self.batch * rows * 4
+        else:
+            self.x = O.gen_normal_f32(seed + 1, self.cols, sigma)
+            self.y_bytes = rows * 4
+        self.variant = variant
+        stride = -(-self.weight_bytes // COPY_ALIGN) * COPY_ALIGN
+        self.n_copies = max(2, -(-COPIES_MIN_BYTES // stride))
+        self.stride = stride
+        self.wbuf = ctx.alloc(stride * self.n_copies)
+        one = np.zeros(stride, dtype=np.uint8)
+        one[: self.weight_bytes] = self.q
+        ctx.upload(self.wbuf, np.tile(one, self.n_copies))
+        self.dx = ctx.alloc(self.x.nbytes)
+        ctx.upload(self.dx, self.x)
+        self.dy = ctx.alloc(self.y_bytes)
+
+    def launch(self, i: int) -> None:
+        w = self.wbuf.ptr + (i % self.n_copies) * self.stride
+        if self.kind == "q4k":
+            self.ctx.q4k_matvec(w, self.dx, self.dy, self.rows, self.units, self.variant)
+        elif self.kind == "q4_0":
+            self.ctx.q4_0_matvec(w, self.dx, self.dy, self.rows, self.units, self.variant)
+        else:
+            self.ctx.q4k_matmul(w, self.dx, self.dy, self.rows, self.units, self.batch,
+                                self.variant)
+
+    def kernel(self) -> str:
+        if self.kind == "q4k":
+            return self.pkg.q4k_matvec_kernel_name(self.rows, self.units, self.variant)
+        if self.kind == "q4_0":
+            return self.pkg.q4_0_matvec_kernel_name(self.rows, self.units, self.variant)
+        return self.pkg.q4k_matmul_kernel_name(self.rows, self.batch, self.variant)
+
+    def parity(self) -> dict:
+        """Checks this exact workload against the oracle before timing."""
+        np, O = self.np, self.O
+        self.launch(0)
+        self.ctx.synchronize()
+        y = np.frombuffer(self.ctx.download(self.dy, self.y_bytes), dtype=np.float32)
+        if self.kind == "q4k":
+            ref = O.q4k_matvec(self.q, self.x, self.rows, self.units)
+            yf, ad = O.q4k_matvec_f64(self.q, self.x, self.rows, self.units)
+            rep = O.matvec_tolerance_report(y, ref, yf, ad, self.cols)
+            return {k: rep[k] for k in ("ok", "rows_failed", "norm_rel_err",
+                                        "gpu_err_vs_f64_norm", "cpu_err_vs_f64_norm")}
+        if self.kind == "q4_0":
+            ref = O.q4_0_matvec(self.q, self.x, self.rows, self.units)
+            yf, ad = O.q4_0_matvec_f64(self.q, self.x, self.rows, self.units)
+            rep = O.matvec_tolerance_report(y, ref, yf, ad, self.cols)
+            return {k: rep[k] for k in ("ok", "rows_failed", "norm_rel_err",
+                                        "gpu_err_vs_f64_norm", "cpu_err_vs_f64_norm")}
+        # batched: against the f64 product of the same RN_f16 weights
+        w16 = O.q4k_dequant(self.q, self.rows * self.units).reshape(self.rows, self.cols)
+        w16 = w16.astype(np.float16).astype(np.float64)
+        xf = self.x.astype(np.float64).reshape(self.batch, self.cols)
+        ref = xf @ w16.T
+        yy = y.reshape(self.batch, self.rows)
+        err = float(np.linalg.norm(yy - ref) / max(np.linalg.norm(ref), 1e-30))
+        return {"ok": err <= 1e-5, "norm_rel_err_vs_f16_weight_f64": err}
+
+    def flops(self) -> float:
+        return 2.0 * self.rows * self.cols * self.batch
+
+    def cpu_baseline(self, budget_s: float, unit: str) -> dict:
+        """The oracle (scalar C restatement of the reference's CPU function, its
+        order) on this workload for about `budget_s` seconds on one core, then
+        row-parallel on the host's cores for a quarter of that.  The batched
+        case times a slice of rows (rows are independent) and scales up."""
+        O = self.O
+        threads = max(1, min(os.cpu_count() or 1, 16))
+        if self.kind == "q4k":
+            one = lambda: O.q4k_matvec_single(self.q, self.x, self.rows, self.units)
+            many = lambda: O.q4k_matvec(self.q, self.x, self.rows, self.units, threads=threads)
+            frac, what = 1.0, f"full {self.rows}x{self.cols} Q4_K matvecs"
+        elif self.kind == "q4_0":
+            one = lambda: O.q4_0_matvec(self.q, self.x, self.rows, self.units, threads=1)
+            many = lambda: O.q4_0_matvec(self.q, self.x, self.rows, self.units, threads=threads)
+            frac, what = 1.0, f"full {self.rows}x{self.cols} Q4_0 matvecs"
+        else:
+            sl = max(1, min(self.rows, 16384 // self.batch))
+            qs = self.q[: sl * self.units * 144]
+            xb = self.x.view(self.np.uint16)
+            one = lambda: O.q4k_matmul_f16x(qs, xb, sl, self.units, self.batch, threads=1)
+            many = lambda: O.q4k_matmul_f16x(qs, xb, sl, self.units, self.batch,
+                                             threads=threads)
+            frac = sl / self.rows
+            what = f"{sl}-row slices (of {self.rows}) of the B={self.batch} matmul"
+        n, el = _time_cpu(one, budget_s)
+        nm, elm = _time_cpu(many, max(1.0, budget_s / 4))
+        per_call, per_call_m = el / n / frac, elm / nm / frac
+
+        def rate(t):
+            if unit == "TFLOP/s":
+                return round(self.flops() / t / 1e12, 6)
+            return round(self.weight_bytes / t / 1e9, 4)
+
+        return {
+            "value": rate(per_call), "unit": unit, "cores": 1, "kind": "port",
+            "sample": f"{n} {what} in {el:.1f}s, one thread ({cpu_model()}, "
+                      f"nproc={os.cpu_count()}); {per_call * 1e6:.0f} us per full call",
+            "all_cores": {
+                "value": rate(per_call_m), "cores": threads,
+                "sample": f"{nm} in {elm:.1f}s over {threads} threads (bit-identical per row); "
+                          f"{per_call_m * 1e6:.0f} us per full call",
+            },
+        }
+
+    def close(self) -> None:
+        for b in (self.wbuf, self.dx, self.dy):
+            b.close()
+
+
+def parse_variant(pkg, kind: str, text: str):
+    if not text:
+        return None
+    vals = [int(t) for t in text.split(",")]
+    return pkg.MatmulVariant(*vals) if kind == "matmul" else pkg.Variant(*vals)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="c4", choices=sorted(WORKLOADS))
+    ap.add_argument("--batch", type=int, default=128, help="activation vectors (c5 only)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--variant", default="", help="rows_per_wave,waves,prefetch[,nontemporal]")
+    ap.add_argument("--variant", default="",
+                    help="matvec: rows_per_wave,waves,prefetch[,nontemporal]; "
+                         "c5: kind,waves,col_tiles,prefetch")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run device-to-device copies of the weight size (counter calibration)")
     args = ap.parse_args()
@@ -108,52 +246,44 @@ def main() -> int:
     from oracle import oracle as O
 
     pkg = __graft_entry__.load_package()
-    variant = None
-    if args.variant:
-        variant = pkg.Variant(*(int(t) for t in args.variant.split(",")))
-
-    rows, sb = ROWS, SB
-    weight_bytes = rows * sb * 144
-    q = O.gen_q4k_weights(20241, rows * sb)
-    x = O.gen_normal_f32(20242, sb * 256, 0.5)
-
+    kind = WORKLOADS[args.workload][0]
+    variant = parse_variant(pkg, kind, args.variant)
     ctx = pkg.HipContext.new()
-    n_copies = max(2, -(-COPIES_MIN_BYTES // weight_bytes))
-    copies = []
-    for _ in range(n_copies):
-        b = ctx.alloc(weight_bytes)
-        ctx.upload(b, q)
-        copies.append(b)
-    dx = ctx.alloc(x.nbytes)
-    ctx.upload(dx, x)
-    dy = ctx.alloc(rows * 4)
+    case = Case(pkg, O, np, ctx, args.workload, args.batch, variant)
 
-    # parity of this exact workload before timing
-    ctx.q4k_matvec(copies[0], dx, dy, rows, sb, variant)
-    ctx.synchronize()
-    y = np.frombuffer(ctx.download(dy, rows * 4), dtype=np.float32)
-    ref = O.q4k_matvec(q, x, rows, sb)
-    yf, absdot = O.q4k_matvec_f64(q, x, rows, sb)
-    rep = O.matvec_tolerance_report(y, ref, yf, absdot, sb * 256)
-    if not rep["ok"]:
-        print(json.dumps({"error": "parity failure", "report": rep}), file=sys.stderr)
+    par = case.parity()
+    if not par["ok"]:
+        print(json.dumps({"error": "parity failure", "report": par}), file=sys.stderr)
         return 1
 
-    # Timed region: K back-to-back calls on the context stream, bracketed by
-    # device synchronisation and HIP events recorded on that same stream.
+    # Timed region: K back-to-back calls launched from the host on the context
+    # stream, bracketed by device synchronisation and HIP events recorded on
+    # that same stream (the reported value).  The same K calls are then
+    # captured once into a HIP graph and replayed, for comparison.
     for i in range(args.warmup):
-        ctx.q4k_matvec(copies[i % n_copies], dx, dy, rows, sb, variant)
+        case.launch(i)
     ctx.device_synchronize()
     ev0, ev1 = ctx.event(), ctx.event()
     ev0.record()
     for i in range(args.steps):
-        ctx.q4k_matvec(copies[i % n_copies], dx, dy, rows, sb, variant)
+        case.launch(i)
     ev1.record()
     ev1.synchronize()
     ctx.device_synchronize()
     total_ms = ev0.elapsed_ms(ev1)
     us_per_call = total_ms * 1000.0 / args.steps
-    gbs = weight_bytes / (us_per_call * 1e-6) / 1e9
+    t = us_per_call * 1e-6
+
+    graph = ctx.capture(lambda: [case.launch(i) for i in range(args.steps)])
+    graph.launch()  # warm replay
+    ctx.device_synchronize()
+    ev0.record()
+    graph.launch()
+    ev1.record()
+    ev1.synchronize()
+    ctx.device_synchronize()
+    us_graph = ev0.elapsed_ms(ev1) * 1000.0 / args.steps
+    graph.close()
 
     # Distribution: the same back-to-back stream cut into groups of 10 calls
     # by events (an event between every call would add its own gap).
@@ -163,70 +293,90 @@ def main() -> int:
     evs[0].record()
     for g in range(n_groups):
         for i in range(group):
-            ctx.q4k_matvec(copies[(g * group + i) % n_copies], dx, dy, rows, sb, variant)
+            case.launch(g * group + i)
         evs[g + 1].record()
     evs[-1].synchronize()
     per_call = sorted(evs[g].elapsed_ms(evs[g + 1]) * 1000.0 / group for g in range(n_groups))
     pct = {p: round(per_call[min(len(per_call) - 1, int(p / 100 * len(per_call)))], 3)
            for p in (10, 50, 90)}
-    kernel = pkg.q4k_matvec_kernel_name(rows, sb, variant)
-    traffic, traffic_src = profiled_traffic(kernel, f"{rows}x{sb * 256}")
+    kernel = case.kernel()
+    shape = f"{case.rows}x{case.cols}" + (f"xB{case.batch}" if kind == "matmul" else "")
+    traffic, traffic_src = profiled_traffic(kernel, shape)
 
     if args.calibrate_copy:
-        # A plain copy of exactly weight_bytes (hipMemcpy device-to-device
+        # A plain copy of exactly the weight bytes (hipMemcpy device-to-device
         # through the runtime's copy kernel), for scaling FETCH_SIZE/WRITE_SIZE.
-        dst = ctx.alloc(weight_bytes)
+        dst = ctx.alloc(case.weight_bytes)
         for _ in range(10):
-            ctx.copy_device(dst, copies[0], weight_bytes)
+            ctx.copy_device(dst, case.wbuf, case.weight_bytes)
         ctx.device_synchronize()
         dst.close()
 
-    cpu = cpu_baseline(O, q, x, rows, sb, args.cpu_seconds) if args.cpu_seconds > 0 else None
+    mfma_bound = kind == "matmul" and case.batch > 32
+    if mfma_bound:
+        unit, peak = "TFLOP/s", MFMA_F16_PEAK_TFLOPS
+        value = case.flops() / t / 1e12
+        algo = case.flops()
+        metric = (f"Q4_K_M x f16 matmul TFLOP/s at {case.rows}x{case.cols}, B={case.batch}; "
+                  "us/call")
+    else:
+        unit, peak = "GB/s", HBM_PEAK_GBS
+        algo = case.weight_bytes
+        value = algo / t / 1e9
+        qname = "Q4_0" if kind == "q4_0" else "Q4_K_M"
+        if kind == "matmul":
+            metric = (f"Q4_K_M x f16 matmul weight-bytes HBM GB/s at {case.rows}x{case.cols}, "
+                      f"B={case.batch}; us/call")
+        else:
+            metric = f"{qname} matvec weight-bytes HBM GB/s (% of peak) at {shape}; us/call"
+
+    cpu = case.cpu_baseline(args.cpu_seconds, unit) if args.cpu_seconds > 0 else None
     out = {
-        "metric": "Q4_K_M matvec weight-bytes HBM GB/s (% of peak) at 4096x14336; us/call",
-        "value": round(gbs, 2),
-        "unit": "GB/s",
+        "metric": metric,
+        "value": round(value, 2),
+        "unit": unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(total_ms / args.steps, 6),
         "us_per_call": round(us_per_call, 3),
+        "timing": f"{args.steps} back-to-back calls launched from the host; the same calls "
+                  f"replayed from one HIP graph: {us_graph:.3f} us/call",
         "us_per_call_p10_p50_p90_of_10call_groups": [pct[10], pct[50], pct[90]],
         "kernel": kernel,
-        "pct_of_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+        "pct_of_peak": round(100.0 * value / peak, 2),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f16 in, f32 accumulate" if kind == "matmul" else "f32",
         "data": "synthetic",
         "config": {
-            "workload": "q4k_matvec 4096x14336 (Q4_K_M down-projection, config 4)",
-            "rows": rows,
-            "cols": sb * 256,
-            "weight_bytes": weight_bytes,
-            "x_bytes": sb * 256 * 4,
-            "y_bytes": rows * 4,
-            "weight_copies_rotated": n_copies,
+            "workload": f"{args.workload}: {kind} {shape} (BASELINE {case.label})",
+            "rows": case.rows,
+            "cols": case.cols,
+            "batch": case.batch,
+            "weight_bytes": case.weight_bytes,
+            "x_bytes": case.x.nbytes,
+            "y_bytes": case.y_bytes,
+            "weight_copies_rotated": case.n_copies,
             "variant": args.variant or "default",
             "parallelism": "single GPU",
         },
-        "parity": {k: rep[k] for k in ("rows_failed", "norm_rel_err", "gpu_err_vs_f64_norm",
-                                       "cpu_err_vs_f64_norm")},
+        "parity": par,
         "roofline": {
-            "bound": "hbm",
-            "achieved": round(gbs, 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "bound": "mfma" if mfma_bound else "hbm",
+            "achieved": round(value, 2),
+            "peak": peak,
+            "unit": unit,
+            "frac": round(value / peak, 4),
             "traffic": traffic,
             "traffic_source": traffic_src,
-            "algorithmic_bytes": weight_bytes,
+            "algorithmic_bytes" if not mfma_bound else "algorithmic_flops": algo,
         },
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
-    for b in copies + [dx, dy]:
-        b.close()
+    case.close()
     ctx.close()
     return 0
 

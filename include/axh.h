@@ -192,6 +192,8 @@ axh_status axh_q4k_matvec_kernel_name(uint32_t n_rows, uint32_t sb_per_row,
 axh_status axh_q4_0_matvec(axh_context *ctx, const void *q, const float *x, float *y,
                            uint32_t n_rows, uint32_t blocks_per_row,
                            const axh_q4_variant *variant, void *stream);
+axh_status axh_q4_0_matvec_kernel_name(uint32_t n_rows, uint32_t blocks_per_row,
+                                       const axh_q4_variant *variant, char *buf, size_t cap);
 /* Decode-only kernels, bit-exact with the reference's CPU dequantisation
  * (common_helpers.rs:437-454; common.rs:229-253): w receives 256 (Q4_K) or
  * 32 (Q4_0) f32 per unit in the reference's element order. */
@@ -202,6 +204,21 @@ axh_status axh_q4_0_dequant(axh_context *ctx, const void *q, float *w, uint64_t 
 /* IEEE binary16 -> binary32 widening of n raw patterns (the ptr_read_u16_zext +
  * f16_bits_to_f32 builtins, crates/axc-codegen/src/q4_0.rs:86-171). */
 axh_status axh_f16_widen(axh_context *ctx, const uint16_t *h, float *f, uint64_t n, void *stream);
+
+/* ---- graph capture -----------------------------------------------------------
+ * Records the launches issued on the context stream between begin and end
+ * (axh_q4k_matvec, axh_q4_0_matvec, axh_q4k_matmul_f16, axh_launch with a NULL
+ * stream) into a graph that replays them in order with no host work per
+ * kernel: the HIP counterpart of recording a Vulkan command buffer once and
+ * resubmitting it.  Launch each operation once before capturing it (its
+ * kernel is then prepared and cached).  No event, copy or synchronisation
+ * call may be made on the context stream while capturing. */
+typedef struct axh_graph axh_graph;
+axh_status axh_capture_begin(axh_context *ctx);
+axh_status axh_capture_end(axh_context *ctx, axh_graph **out);
+axh_status axh_graph_launch(axh_context *ctx, axh_graph *g, void *stream);
+uint64_t axh_graph_node_count(const axh_graph *g);
+void axh_graph_destroy(axh_graph *g);
 
 /* Number of compiled matvec variants and the i-th one (for the autotuner). */
 uint32_t axh_q4k_matvec_variant_count(void);

@@ -198,3 +198,44 @@ def test_events_time_launches_on_the_context_stream(ctx, axc):
     assert struct.unpack("<I", ctx.download(buf, 4))[0] == 300
     buf.close()
     h.release()
+
+
+def test_graph_replays_match_eager_results(ctx, axc):
+    """Captured matvec / Q4_0 / matmul launches replayed several times, with
+    eager work and synchronisation between replays; every replay is compared
+    bit for bit with the eager result."""
+    rows, sb, nb, batch = 300, 16, 128, 24
+    q = O.gen_q4k_weights(81, rows * sb)
+    x = O.gen_normal_f32(82, sb * 256)
+    q0 = O.gen_q4_0_weights(83, rows * nb)
+    x0 = O.gen_normal_f32(84, nb * 32)
+    xh = O.gen_normal_f32(85, sb * 256 * batch).astype(np.float16)
+    bufs = {}
+    for name, arr in (("q", q), ("x", x), ("q0", q0), ("x0", x0), ("xh", xh)):
+        bufs[name] = ctx.alloc(arr.nbytes)
+        ctx.upload(bufs[name], arr)
+    y1, y2, y3 = ctx.alloc(rows * 4), ctx.alloc(rows * 4), ctx.alloc(rows * batch * 4)
+
+    def ops():
+        ctx.q4k_matvec(bufs["q"], bufs["x"], y1, rows, sb)
+        ctx.q4_0_matvec(bufs["q0"], bufs["x0"], y2, rows, nb)
+        ctx.q4k_matmul(bufs["q"], bufs["xh"], y3, rows, sb, batch)
+
+    ops()  # eager (also prepares every kernel before capture)
+    ctx.synchronize()
+    eager = [ctx.download(b, n) for b, n in ((y1, rows * 4), (y2, rows * 4), (y3, rows * batch * 4))]
+    g = ctx.capture(ops)
+    assert g.node_count == 3
+    for rep in range(4):
+        for b, n in ((y1, rows * 4), (y2, rows * 4), (y3, rows * batch * 4)):
+            ctx.upload(b, np.full(n // 4, np.nan, dtype=np.float32))  # poison between replays
+        ctx.q4k_matvec(bufs["q"], bufs["x"], y1, rows, sb)  # eager work between replays
+        ctx.synchronize()
+        g.launch()
+        ctx.synchronize()
+        got = [ctx.download(b, n) for b, n in ((y1, rows * 4), (y2, rows * 4),
+                                                (y3, rows * batch * 4))]
+        assert got == eager, f"replay {rep}"
+    g.close()
+    for b in list(bufs.values()) + [y1, y2, y3]:
+        b.close()
