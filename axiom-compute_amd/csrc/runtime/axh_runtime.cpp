@@ -260,7 +260,9 @@ axh_status axh_context_create(const axh_context_options *opts, axh_context **out
 
   auto core = std::make_shared<Core>();
   core->device = index;
-  core->name = prop.name;
+  // The marketing name can be empty (it comes from a PCI id table that not
+  // every install ships); the architecture string is always there.
+  core->name = std::string(prop.name[0] ? prop.name : "AMD GPU") + " [" + prop.gcnArchName + "]";
   core->max_wg[0] = (uint32_t)prop.maxGridSize[0];
   core->max_wg[1] = (uint32_t)prop.maxGridSize[1];
   core->max_wg[2] = (uint32_t)prop.maxGridSize[2];

@@ -1,0 +1,81 @@
+"""Tuning tools on the device (marked `gpu`): bench_variant returns timings
+with a real correctness verdict for every Q4 kernel, grid_search ranks the
+compiled hole space and appends one history line (reference:
+crates/axc-driver/src/mcp/tools/bench_variant.rs:209-282,
+grid_search.rs:256-410)."""
+from __future__ import annotations
+
+import importlib
+import io
+import json
+import sys
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def mcp(axc):
+    return importlib.import_module("axiom_compute_amd.mcp")
+
+
+@pytest.mark.parametrize("kernel,shape", [
+    ("q4km_dequant_matvec", {"n_rows": 512, "units_per_row": 16}),
+    ("q4_0_dequant_matvec", {"n_rows": 256, "units_per_row": 128}),
+    ("q4k_matmul_f16", {"n_rows": 256, "units_per_row": 4, "batch": 24}),
+])
+def test_bench_variant_checks_every_kernel(mcp, tmp_path, kernel, shape):
+    _say(f"bench_variant {kernel} {shape}")
+    ctx = mcp.McpContext(history_dir=tmp_path)
+    r = mcp.bench_variant({"kernel": kernel, "shape": shape, "sample_count": 3,
+                           "launches_per_sample": 4}, ctx)
+    assert r["correctness"] == {"status": "ok"}, r["correctness"]
+    assert len(r["samples"]) == 3 and r["median_ns"] > 0
+    assert r["machine"]["device_name"]
+    assert r["kernel_entry"].startswith("axh_q4")
+
+
+def test_bench_variant_uncompiled_assignment_is_an_error(mcp, tmp_path):
+    ctx = mcp.McpContext(history_dir=tmp_path)
+    with pytest.raises(mcp.McpToolError) as e:
+        mcp.bench_variant({"kernel": "q4km_dequant_matvec",
+                           "shape": {"n_rows": 64, "units_per_row": 4}, "sample_count": 1,
+                           "assignments": {"rows_per_wave": 3}}, ctx)
+    assert e.value.code == mcp.DEVICE_UNAVAILABLE and e.value.category == "dispatch_failed"
+
+
+def test_grid_search_over_the_stdio_server(mcp, tmp_path):
+    """Two JSON-RPC calls through serve(): a grid search (some assignments are
+    not compiled and rank last as failures) and the history it appended."""
+    ctx = mcp.McpContext(history_dir=tmp_path)
+    shape = {"n_rows": 1024, "units_per_row": 16}
+    reqs = [
+        {"jsonrpc": "2.0", "id": 1, "method": "grid_search",
+         "params": {"kernel": "q4km_dequant_matvec", "shape": shape, "sample_count": 2,
+                    "holes_override": {"rows_per_wave": [1, 2, 3], "waves_per_workgroup": [4, 8],
+                                       "prefetch": [2], "nontemporal": [2]}}},
+        {"jsonrpc": "2.0", "id": 2, "method": "optimization_history",
+         "params": {"kernel": "q4km_dequant_matvec", "shape": shape}},
+    ]
+    out = io.StringIO()
+    mcp.serve(io.StringIO("\n".join(json.dumps(r) for r in reqs) + "\n"), out, ctx)
+    r1, r2 = [json.loads(ln) for ln in out.getvalue().splitlines()]
+    res = r1["result"]
+    assert len(res["ranked"]) == 6 and not res["fallback_used"]
+    ok = [r for r in res["ranked"] if r["median_ns"] is not None]
+    assert [r["median_ns"] for r in ok] == sorted(r["median_ns"] for r in ok)
+    assert all(r["outcome"] == "ok" for r in ok)
+    failed = [r for r in res["ranked"] if r["median_ns"] is None]
+    assert failed and all(r["assignments"]["rows_per_wave"] == 3 for r in failed)
+    assert res["ranked"][-1]["median_ns"] is None  # failures rank last
+    assert res["winner"]["variant_id"] == ok[0]["variant_id"]
+    entries = r2["result"]["entries"]
+    assert len(entries) == 1
+    assert entries[0]["grid_search"]["winner_variant_id"] == res["winner"]["variant_id"]
+    assert entries[0]["source_xxh3"] == r2["result"]["history_path"].split("/")[-1][:16]
