@@ -20,6 +20,7 @@ from .axh import (  # noqa: F401
     compiled_matmul_variants,
     MatmulVariant,
     q4k_matmul_kernel_name,
+    q4k_gate_up_kernel_name,
     q4k_matvec_kernel_name,
     q4_0_matvec_kernel_name,
     load_library,
@@ -42,6 +43,7 @@ __all__ = [
     "compiled_matmul_variants",
     "MatmulVariant",
     "q4k_matmul_kernel_name",
+    "q4k_gate_up_kernel_name",
     "q4k_matvec_kernel_name",
     "q4_0_matvec_kernel_name",
     "load_library",

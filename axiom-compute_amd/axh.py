@@ -153,6 +153,10 @@ def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
         "axh_graph_destroy": (None, [vp]),
         "axh_q4k_matvec_kernel_name": (st, [u32, u32, c.POINTER(_Variant), c.c_char_p, sz]),
         "axh_q4_0_matvec_kernel_name": (st, [u32, u32, c.POINTER(_Variant), c.c_char_p, sz]),
+        "axh_q4k_gate_up": (st, [vp, vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
+        "axh_q4k_gate_up_kernel_name": (st, [u32, u32, c.POINTER(_Variant), c.c_char_p, sz]),
+        "axh_q4k_gate_up_variant_count": (u32, []),
+        "axh_q4k_gate_up_variant_at": (st, [u32, c.POINTER(_Variant)]),
         "axh_q4k_matmul_f16": (st, [vp, vp, vp, vp, u32, u32, u32, c.POINTER(_MatmulVariant),
                                     vp]),
         "axh_q4k_matmul_kernel_name": (st, [u32, u32, c.POINTER(_MatmulVariant), c.c_char_p,
@@ -266,10 +270,27 @@ def q4_0_matvec_kernel_name(n_rows: int, blocks_per_row: int,
     return buf.value.decode()
 
 
-def compiled_variants(kind: str = "q4k") -> list[Variant]:
+def q4k_gate_up_kernel_name(n_rows: int, sb_per_row: int,
+                            variant: Optional[Variant] = None) -> str:
+    """Entry point axh_q4k_gate_up launches for this shape and variant."""
     lib = load_library()
-    count = lib.axh_q4k_matvec_variant_count if kind == "q4k" else lib.axh_q4_0_matvec_variant_count
-    at = lib.axh_q4k_matvec_variant_at if kind == "q4k" else lib.axh_q4_0_matvec_variant_at
+    v = variant._c() if variant else None
+    buf = ctypes.create_string_buffer(64)
+    _check(lib.axh_q4k_gate_up_kernel_name(n_rows, sb_per_row, ctypes.byref(v) if v else None,
+                                           buf, 64))
+    return buf.value.decode()
+
+
+def compiled_variants(kind: str = "q4k") -> list[Variant]:
+    """Compiled hole assignments of the "q4k" or "q4_0" matvec, or of the
+    fused "gate_up" kernel."""
+    lib = load_library()
+    if kind not in ("q4k", "q4_0", "gate_up"):
+        raise ValueError(f"unknown kernel family {kind!r}")
+    count = getattr(lib, f"axh_{kind}_matvec_variant_count" if kind != "gate_up"
+                    else "axh_q4k_gate_up_variant_count")
+    at = getattr(lib, f"axh_{kind}_matvec_variant_at" if kind != "gate_up"
+                 else "axh_q4k_gate_up_variant_at")
     out = []
     for i in range(count()):
         v = _Variant()
@@ -614,6 +635,14 @@ class HipContext:
         v = variant._c() if variant else None
         _check(self._lib.axh_q4k_matvec(self._raw, _ptr(q), _ptr(x), _ptr(y), n_rows, sb_per_row,
                                         ctypes.byref(v) if v else None, _stream(stream)))
+
+    def q4k_gate_up(self, q_gate, q_up, x, h, n_rows: int, sb_per_row: int,
+                    variant: Optional[Variant] = None, stream=None) -> None:
+        """h[r] = silu(q_gate[r] . x) * (q_up[r] . x), silu(g) = g / (1 + exp(-g))."""
+        v = variant._c() if variant else None
+        _check(self._lib.axh_q4k_gate_up(self._raw, _ptr(q_gate), _ptr(q_up), _ptr(x), _ptr(h),
+                                         n_rows, sb_per_row, ctypes.byref(v) if v else None,
+                                         _stream(stream)))
 
     def q4_0_matvec(self, q, x, y, n_rows: int, blocks_per_row: int,
                     variant: Optional[Variant] = None, stream=None) -> None:

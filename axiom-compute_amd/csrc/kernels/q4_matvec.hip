@@ -357,26 +357,42 @@ struct Q4kFlatBuf {
 
 // Loads of one iteration for the RPW rows of `bundle`.  Rows past the matrix
 // read zeros (buffer range check); superblocks past the row are never used.
-template <int RPW, int PF, bool kNT>
+// kDual (fused gate/up): a bundle is RPW/2 output rows, slots r < RPW/2 read
+// row bundle*RPW/2 + r of the first matrix and slots r >= RPW/2 the same row
+// of the second.
+template <int RPW, int PF, bool kNT, bool kDual>
 __device__ __forceinline__ void q4k_flat_load(Q4kFlatBuf<RPW, PF> &B, int p,
-                                              __amdgpu_buffer_rsrc_t qr, uint32_t row_bytes,
+                                              __amdgpu_buffer_rsrc_t qr,
+                                              __amdgpu_buffer_rsrc_t qr2, uint32_t row_bytes,
                                               uint32_t bundle, uint32_t it, uint32_t s,
                                               uint32_t c) {
+  constexpr int kRb = kDual ? RPW / 2 : RPW;
   const uint32_t sb_off = (it * 8u + s) * (uint32_t)kQ4kSbBytes;
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
-    const uint32_t off = (bundle * RPW + (uint32_t)r) * row_bytes + sb_off;
-    B.h[p][r] = buf_load16<kNT>(qr, off);
-    B.a[p][r] = buf_load16<kNT>(qr, off + 16u + 32u * c);
-    B.b[p][r] = buf_load16<kNT>(qr, off + 32u + 32u * c);
+    const __amdgpu_buffer_rsrc_t src = (kDual && r >= kRb) ? qr2 : qr;
+    const uint32_t off = (bundle * kRb + (uint32_t)(r % kRb)) * row_bytes + sb_off;
+    B.h[p][r] = buf_load16<kNT>(src, off);
+    B.a[p][r] = buf_load16<kNT>(src, off + 16u + 32u * c);
+    B.b[p][r] = buf_load16<kNT>(src, off + 32u + 32u * c);
   }
 }
 
-template <int RPW, int NW, int PF, bool kNT, int XP>
+// SiLU(g) * u, the SwiGLU combination of a gate and an up projection.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return g / (1.0f + expf(-g)) * u;
+}
+
+// kDual: y[r] = silu(W1[r].x) * (W2[r].x) for q = W1, q2 = W2 (same shape);
+// otherwise y = W1 x and q2 is unused.
+template <int RPW, int NW, int PF, bool kNT, int XP, bool kDual = false>
 __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
+                                                const uint8_t *__restrict__ q2,
                                                 const float *__restrict__ x,
                                                 float *__restrict__ y, uint32_t n_rows,
                                                 uint32_t nsb, float *lds) {
+  constexpr int kRb = kDual ? RPW / 2 : RPW; // output rows per bundle
+  static_assert(!kDual || RPW % 2 == 0, "the fused kernel pairs gate and up rows");
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   // wave index as a scalar: every loop bound below is then wave-uniform
@@ -384,7 +400,7 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
   const uint32_t G = lane >> 2, half = G >> 3, s = G & 7u, c = lane & 3u;
   const uint32_t total_waves = gridDim.x * NW;
   const uint32_t W = blockIdx.x * NW + wave;
-  const uint32_t n_bundles = (n_rows + RPW - 1) / RPW;
+  const uint32_t n_bundles = (n_rows + kRb - 1) / kRb;
   const uint32_t n_pairs = (n_bundles + 1u) >> 1;
   if (nsb == 0) { // empty rows: the reference returns +0.0 (AT-1323)
     for (uint32_t r = W * 64u + lane; r < n_rows; r += total_waves * 64u) y[r] = 0.0f;
@@ -396,6 +412,7 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
   // The host guarantees n_rows * row_bytes < 2^32 for this kernel.
   const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(q, n_rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t qr2 = kDual ? make_rsrc(q2, n_rows * row_bytes) : qr;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, nsb * 1024u);
   float *xs = lds;
   float *ss = lds + nsb * kQ4kFlatSbFloats;
@@ -425,7 +442,7 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
 #pragma unroll
   for (int p = 0; p < PF; ++p) {
     const uint32_t bundle = 2u * (W + l_pi * total_waves) + half;
-    q4k_flat_load<RPW, PF, kNT>(B, p, qr, row_bytes, bundle, l_it, s, c);
+    q4k_flat_load<RPW, PF, kNT, kDual>(B, p, qr, qr2, row_bytes, bundle, l_it, s, c);
     if (++l_it == n_it) { l_it = 0; ++l_pi; }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -474,12 +491,13 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
       // refill this slot PF iterations ahead (unconditional)
       {
         const uint32_t bundle = 2u * (W + l_pi * total_waves) + half;
-        q4k_flat_load<RPW, PF, kNT>(B, p, qr, row_bytes, bundle, l_it, s, c);
+        q4k_flat_load<RPW, PF, kNT, kDual>(B, p, qr, qr2, row_bytes, bundle, l_it, s, c);
         if (++l_it == n_it) { l_it = 0; ++l_pi; }
       }
       if (++c_it == n_it) { // a bundle pair is complete: reduce and store
         if (c_pi < n_my) {
           const uint32_t bundle0 = 2u * (W + c_pi * total_waves);
+          float h0[RPW], h1[RPW];
 #pragma unroll
           for (int r = 0; r < RPW; ++r) {
             float v = acc[r];
@@ -488,15 +506,20 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
             v += dpp_mov<0x141>(v);
             v += dpp_mov<0x140>(v);
             const int vi = __builtin_bit_cast(int, v);
-            const float h0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 0)) +
-                             __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 16));
-            const float h1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 32)) +
-                             __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 48));
-            const uint32_t r0 = bundle0 * RPW + (uint32_t)r;
-            const uint32_t r1 = (bundle0 + 1u) * RPW + (uint32_t)r;
-            if (lane == 0 && r0 < n_rows) y[r0] = h0;
-            if (lane == 0 && r1 < n_rows) y[r1] = h1;
+            h0[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 0)) +
+                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 16));
+            h1[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 32)) +
+                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 48));
             acc[r] = 0.0f;
+          }
+#pragma unroll
+          for (int r = 0; r < kRb; ++r) {
+            const uint32_t r0 = bundle0 * kRb + (uint32_t)r;
+            const uint32_t r1 = (bundle0 + 1u) * kRb + (uint32_t)r;
+            const float o0 = kDual ? silu_mul(h0[r], h0[(r + kRb) % RPW]) : h0[r];
+            const float o1 = kDual ? silu_mul(h1[r], h1[(r + kRb) % RPW]) : h1[r];
+            if (lane == 0 && r0 < n_rows) y[r0] = o0;
+            if (lane == 0 && r1 < n_rows) y[r1] = o1;
           }
         }
         c_it = 0;
@@ -512,7 +535,8 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
                                                          const float *__restrict__ x,            \
                                                          float *__restrict__ y, RowsArgs a) {    \
     extern __shared__ float axh_lds_dyn[];                                                       \
-    q4k_matvec_flat<RPW, NW, PF, NT != 0, 1>(q, x, y, a.n_rows, a.units_per_row, axh_lds_dyn);  \
+    q4k_matvec_flat<RPW, NW, PF, NT != 0, 1>(q, q, x, y, a.n_rows, a.units_per_row,             \
+                                               axh_lds_dyn);                                     \
   }
 // Two staged x sub-blocks per thread (rows of up to 2 * NW * 8 superblocks).
 #define AXH_Q4K_MATVEC_FLAT_X2(RPW, NW, PF, NT)                                                  \
@@ -522,8 +546,29 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
                                                               float *__restrict__ y,             \
                                                               RowsArgs a) {                      \
     extern __shared__ float axh_lds_dyn[];                                                       \
-    q4k_matvec_flat<RPW, NW, PF, NT != 0, 2>(q, x, y, a.n_rows, a.units_per_row, axh_lds_dyn);  \
+    q4k_matvec_flat<RPW, NW, PF, NT != 0, 2>(q, q, x, y, a.n_rows, a.units_per_row,             \
+                                               axh_lds_dyn);                                     \
   }
+
+// Fused SwiGLU gate/up projection: y[r] = silu(Wg[r].x) * (Wu[r].x), ROWS
+// output rows per bundle (2 * ROWS weight rows per lane group).
+#define AXH_Q4K_GATE_UP(ROWS, NW, PF, XP)                                                        \
+  extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
+      axh_q4k_gate_up_r##ROWS##_w##NW##_p##PF##_x##XP(                                           \
+          const uint8_t *__restrict__ qg, const uint8_t *__restrict__ qu,                        \
+          const float *__restrict__ x, float *__restrict__ y, RowsArgs a) {                      \
+    extern __shared__ float axh_lds_dyn[];                                                       \
+    q4k_matvec_flat<2 * ROWS, NW, PF, false, XP, true>(qg, qu, x, y, a.n_rows, a.units_per_row,  \
+                                                       axh_lds_dyn);                             \
+  }
+
+AXH_Q4K_GATE_UP(1, 4, 2, 1)
+AXH_Q4K_GATE_UP(1, 4, 4, 1)
+AXH_Q4K_GATE_UP(1, 8, 2, 1)
+AXH_Q4K_GATE_UP(2, 4, 2, 1)
+AXH_Q4K_GATE_UP(2, 8, 2, 1)
+AXH_Q4K_GATE_UP(1, 4, 2, 2)
+AXH_Q4K_GATE_UP(1, 8, 2, 2)
 
 AXH_Q4K_MATVEC_FLAT(1, 8, 2, 0)
 AXH_Q4K_MATVEC_FLAT(1, 8, 4, 0)

@@ -59,6 +59,13 @@ constexpr MatvecVariant kQ4kVariants[] = {
     {1, 8, 7, 1, 1}, {2, 4, 2, 1, 1}, {2, 4, 4, 1, 1}, {1, 4, 2, 2, 2},  {1, 4, 4, 2, 2},
     {2, 4, 2, 2, 2}, {2, 4, 4, 2, 2},
 };
+// axh_q4k_gate_up_r{rpw}_w{nw}_p{pf}_x{xp}: fused SwiGLU gate/up kernels, rpw
+// output rows per bundle (each lane group reads rpw gate and rpw up rows).
+// Keep in sync with the AXH_Q4K_GATE_UP list in q4_matvec.hip.
+constexpr MatvecVariant kGateUpVariants[] = {
+    {1, 4, 2, 2, 1}, {1, 4, 4, 2, 1}, {1, 8, 2, 2, 1}, {2, 4, 2, 2, 1},
+    {2, 8, 2, 2, 1}, {1, 4, 2, 2, 2}, {1, 8, 2, 2, 2},
+};
 // axh_q4_0_matvec_r{rpw}_w{nw} (prefetch and cache policy are not holes for Q4_0).
 constexpr MatvecVariant kQ4_0Variants[] = {
     {1, 1, 1, 2, 1}, {1, 4, 1, 2, 1}, {2, 4, 1, 2, 1}, {4, 4, 1, 2, 1}};
@@ -77,10 +84,11 @@ axh_status builtin_kernel(axh_context *ctx, const char *entry, uint32_t n_buffer
     *out = it->second;
     return AXH_OK;
   }
-  static const uint8_t kAccess[3] = {AXH_ACCESS_READ_ONLY, AXH_ACCESS_READ_ONLY,
-                                     AXH_ACCESS_READ_WRITE};
-  uint8_t access[3] = {kAccess[0], kAccess[1], kAccess[2]};
-  if (n_buffers == 2) access[1] = AXH_ACCESS_READ_WRITE;
+  // Inputs are read-only; the last binding is the output.
+  uint8_t access[4] = {AXH_ACCESS_READ_ONLY, AXH_ACCESS_READ_ONLY, AXH_ACCESS_READ_ONLY,
+                       AXH_ACCESS_READ_ONLY};
+  if (n_buffers == 0 || n_buffers > 4) return fail(AXH_ERR_INVALID_ARGUMENT, "bad binding count");
+  access[n_buffers - 1] = AXH_ACCESS_READ_WRITE;
   axh_binding_plan plan{};
   plan.n_buffers = n_buffers;
   plan.access = access;
@@ -168,37 +176,51 @@ const void *axh_builtin_code_object(size_t *bytes) {
   return axh_q4_matvec_co_begin;
 }
 
-// Distinct hole assignments of the Q4_K table (staging width is derived
-// from the shape, not a hole).
-static bool q4k_first_of_holes(size_t i) {
+// Distinct hole assignments of a persistent-kernel table (staging width is
+// derived from the shape, not a hole).
+static bool first_of_holes(const MatvecVariant *t, size_t i) {
   for (size_t k = 0; k < i; ++k)
-    if (kQ4kVariants[k].rpw == kQ4kVariants[i].rpw && kQ4kVariants[k].nw == kQ4kVariants[i].nw &&
-        kQ4kVariants[k].pf == kQ4kVariants[i].pf && kQ4kVariants[k].nt == kQ4kVariants[i].nt)
+    if (t[k].rpw == t[i].rpw && t[k].nw == t[i].nw && t[k].pf == t[i].pf && t[k].nt == t[i].nt)
       return false;
   return true;
 }
 
-uint32_t axh_q4k_matvec_variant_count(void) {
-  uint32_t n = 0;
-  for (size_t i = 0; i < sizeof(kQ4kVariants) / sizeof(kQ4kVariants[0]); ++i)
-    n += q4k_first_of_holes(i) ? 1u : 0u;
-  return n;
+static uint32_t count_holes(const MatvecVariant *t, size_t n) {
+  uint32_t c = 0;
+  for (size_t i = 0; i < n; ++i) c += first_of_holes(t, i) ? 1u : 0u;
+  return c;
 }
 
-axh_status axh_q4k_matvec_variant_at(uint32_t i, axh_q4_variant *out) {
+static axh_status holes_at(const MatvecVariant *t, size_t n, uint32_t i, axh_q4_variant *out) {
   if (!out) return fail(AXH_ERR_INVALID_ARGUMENT, "out is NULL");
-  uint32_t n = 0;
-  for (size_t k = 0; k < sizeof(kQ4kVariants) / sizeof(kQ4kVariants[0]); ++k) {
-    if (!q4k_first_of_holes(k)) continue;
-    if (n++ == i) {
-      out->rows_per_wave = kQ4kVariants[k].rpw;
-      out->waves_per_workgroup = kQ4kVariants[k].nw;
-      out->prefetch = kQ4kVariants[k].pf;
-      out->nontemporal = kQ4kVariants[k].nt;
+  uint32_t c = 0;
+  for (size_t k = 0; k < n; ++k) {
+    if (!first_of_holes(t, k)) continue;
+    if (c++ == i) {
+      out->rows_per_wave = t[k].rpw;
+      out->waves_per_workgroup = t[k].nw;
+      out->prefetch = t[k].pf;
+      out->nontemporal = t[k].nt;
       return ok();
     }
   }
   return fail(AXH_ERR_INVALID_ARGUMENT, "variant index out of range");
+}
+
+uint32_t axh_q4k_matvec_variant_count(void) {
+  return count_holes(kQ4kVariants, sizeof(kQ4kVariants) / sizeof(kQ4kVariants[0]));
+}
+
+axh_status axh_q4k_matvec_variant_at(uint32_t i, axh_q4_variant *out) {
+  return holes_at(kQ4kVariants, sizeof(kQ4kVariants) / sizeof(kQ4kVariants[0]), i, out);
+}
+
+uint32_t axh_q4k_gate_up_variant_count(void) {
+  return count_holes(kGateUpVariants, sizeof(kGateUpVariants) / sizeof(kGateUpVariants[0]));
+}
+
+axh_status axh_q4k_gate_up_variant_at(uint32_t i, axh_q4_variant *out) {
+  return holes_at(kGateUpVariants, sizeof(kGateUpVariants) / sizeof(kGateUpVariants[0]), i, out);
 }
 
 uint32_t axh_q4_0_matvec_variant_count(void) {
@@ -333,6 +355,80 @@ axh_status axh_q4k_matvec(axh_context *ctx, const void *q, const float *x, float
   }
   void *bufs[3] = {const_cast<void *>(q), const_cast<float *>(x), y};
   s = launch_raw(k, grid, bufs, 3, &p.args, sizeof(p.args), p.lds, pick_stream(ctx, stream));
+  return s == AXH_OK ? ok() : s;
+}
+
+// Fused gate/up: the persistent kernel only (x of a row fits LDS).
+static MatvecVariant gate_up_default(uint32_t n_rows, uint32_t nsb) {
+  (void)n_rows;
+  if (nsb * 8u <= 256u) return {1, 4, 2, 2, 1};
+  return {1, 8, 2, 2, 1};
+}
+
+static axh_status plan_gate_up(uint32_t n_rows, uint32_t sb_per_row,
+                               const axh_q4_variant *variant, Q4kPlan *p) {
+  if (sb_per_row == 0 || sb_per_row > kQ4kFlatMaxSb)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "gate/up: sb_per_row must be 1..128");
+  if ((uint64_t)n_rows * sb_per_row * 144u >= 0xFFFFFFFFull)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "gate/up: each matrix must be below 4 GiB");
+  if (variant && variant->nontemporal == 1)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "gate/up: no non-temporal variant is compiled");
+  const MatvecVariant dflt = gate_up_default(n_rows, sb_per_row);
+  const uint32_t want_nw =
+      variant && variant->waves_per_workgroup ? variant->waves_per_workgroup : dflt.nw;
+  const uint32_t min_xp = (sb_per_row * 8u + want_nw * 64u - 1u) / (want_nw * 64u);
+  const MatvecVariant *v =
+      find_variant(kGateUpVariants, sizeof(kGateUpVariants) / sizeof(kGateUpVariants[0]),
+                   variant, dflt, min_xp);
+  if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled gate/up variant matches");
+  if (sb_per_row * 8u > v->xp * v->nw * 64u)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "gate/up: row too long for this variant's x staging");
+  std::snprintf(p->name, sizeof(p->name), "axh_q4k_gate_up_r%u_w%u_p%u_x%u", v->rpw, v->nw,
+                v->pf, v->xp);
+  p->nw = v->nw;
+  p->lds = sb_per_row * 1120u;
+  p->flat = true;
+  const uint32_t bundles = (n_rows + v->rpw - 1) / v->rpw;
+  p->units = ((bundles + 1) / 2 + v->nw - 1) / v->nw;
+  p->args = RowsArgs{n_rows, sb_per_row, sb_per_row, 0};
+  return ok();
+}
+
+axh_status axh_q4k_gate_up_kernel_name(uint32_t n_rows, uint32_t sb_per_row,
+                                       const axh_q4_variant *variant, char *buf, size_t cap) {
+  if (!buf || cap == 0) return fail(AXH_ERR_INVALID_ARGUMENT, "buf is NULL");
+  Q4kPlan p{};
+  axh_status s = plan_gate_up(n_rows, sb_per_row, variant, &p);
+  if (s != AXH_OK) return s;
+  if (std::strlen(p.name) + 1 > cap) return fail(AXH_ERR_INVALID_ARGUMENT, "buf too small");
+  std::memcpy(buf, p.name, std::strlen(p.name) + 1);
+  return ok();
+}
+
+axh_status axh_q4k_gate_up(axh_context *ctx, const void *q_gate, const void *q_up,
+                           const float *x, float *h, uint32_t n_rows, uint32_t sb_per_row,
+                           const axh_q4_variant *variant, void *stream) {
+  if (!ctx) return fail(AXH_ERR_INVALID_ARGUMENT, "ctx is NULL");
+  if (n_rows == 0) return ok();
+  if (!device_ptr_ok(h) || !device_ptr_ok(q_gate) || !device_ptr_ok(q_up) || !device_ptr_ok(x))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q_gate, q_up, x and h must be device pointers");
+  if (((uintptr_t)q_gate & 15u) || ((uintptr_t)q_up & 15u) || ((uintptr_t)x & 15u))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q_gate, q_up and x must be 16-byte aligned");
+  Q4kPlan p{};
+  axh_status s = plan_gate_up(n_rows, sb_per_row, variant, &p);
+  if (s != AXH_OK) return s;
+  if (p.lds > ctx->core->max_lds)
+    return fail(AXH_ERR_PIPELINE_LAYOUT, "LDS tile exceeds the device limit");
+  hipSetDevice(ctx->core->device);
+  axh_kernel *k = nullptr;
+  s = builtin_kernel(ctx, p.name, 4, sizeof(RowsArgs), p.nw * 64u, &k);
+  if (s != AXH_OK) return s;
+  uint32_t grid[3] = {p.units, 1, 1};
+  const uint32_t resident = occupancy(ctx, k, p.lds) * ctx->core->cu_count;
+  if (resident < grid[0]) grid[0] = resident;
+  void *bufs[4] = {const_cast<void *>(q_gate), const_cast<void *>(q_up), const_cast<float *>(x),
+                   h};
+  s = launch_raw(k, grid, bufs, 4, &p.args, sizeof(p.args), p.lds, pick_stream(ctx, stream));
   return s == AXH_OK ? ok() : s;
 }
 

@@ -45,6 +45,9 @@ WORKLOADS = {
     "c4": ("q4k", 4096, 56, 0.5, "config 4, down-projection"),
     "head": ("q4k", 128256, 16, 1.0, "config 4, output head"),
     "c5": ("matmul", 14336, 16, 1.0, "config 5"),
+    # fused SwiGLU gate/up projections of a Llama-3-8B decode step (two
+    # 14336 x 4096 Q4_K_M matrices against one x)
+    "ffn": ("gate_up", 14336, 16, 0.5, "gate/up, fused"),
 }
 
 
@@ -95,8 +98,18 @@ class Case:
         self.cols = units * (32 if kind == "q4_0" else 256)
         self.weight_bytes = rows * units * unit_bytes
         seed = 20241 if name == "c4" else 30000 + rows + units
+        self.up_off = 0
         if kind == "q4_0":
             self.q = O.gen_q4_0_weights(seed, rows * units)
+        elif kind == "gate_up":
+            # gate rows, then the up rows at the next COPY_ALIGN boundary
+            self.qg = O.gen_q4k_weights(seed, rows * units)
+            self.qu = O.gen_q4k_weights(seed + 7, rows * units)
+            self.up_off = -(-self.weight_bytes // COPY_ALIGN) * COPY_ALIGN
+            self.q = np.zeros(self.up_off + self.weight_bytes, dtype=np.uint8)
+            self.q[: self.weight_bytes] = self.qg
+            self.q[self.up_off:] = self.qu
+            self.weight_bytes *= 2
         else:
             self.q = O.gen_q4k_weights(seed, rows * units)
         if kind == "matmul":
@@ -106,12 +119,12 @@ class Case:
             self.x = O.gen_normal_f32(seed + 1, self.cols, sigma)
             self.y_bytes = rows * 4
         self.variant = variant
-        stride = -(-self.weight_bytes // COPY_ALIGN) * COPY_ALIGN
+        stride = -(-self.q.nbytes // COPY_ALIGN) * COPY_ALIGN
         self.n_copies = max(2, -(-COPIES_MIN_BYTES // stride))
         self.stride = stride
         self.wbuf = ctx.alloc(stride * self.n_copies)
         one = np.zeros(stride, dtype=np.uint8)
-        one[: self.weight_bytes] = self.q
+        one[: self.q.nbytes] = self.q
         ctx.upload(self.wbuf, np.tile(one, self.n_copies))
         self.dx = ctx.alloc(self.x.nbytes)
         ctx.upload(self.dx, self.x)
@@ -123,6 +136,9 @@ class Case:
             self.ctx.q4k_matvec(w, self.dx, self.dy, self.rows, self.units, self.variant)
         elif self.kind == "q4_0":
             self.ctx.q4_0_matvec(w, self.dx, self.dy, self.rows, self.units, self.variant)
+        elif self.kind == "gate_up":
+            self.ctx.q4k_gate_up(w, w + self.up_off, self.dx, self.dy, self.rows, self.units,
+                                 self.variant)
         else:
             self.ctx.q4k_matmul(w, self.dx, self.dy, self.rows, self.units, self.batch,
                                 self.variant)
@@ -132,6 +148,8 @@ class Case:
             return self.pkg.q4k_matvec_kernel_name(self.rows, self.units, self.variant)
         if self.kind == "q4_0":
             return self.pkg.q4_0_matvec_kernel_name(self.rows, self.units, self.variant)
+        if self.kind == "gate_up":
+            return self.pkg.q4k_gate_up_kernel_name(self.rows, self.units, self.variant)
         return self.pkg.q4k_matmul_kernel_name(self.rows, self.batch, self.variant)
 
     def parity(self) -> dict:
@@ -152,6 +170,10 @@ class Case:
             rep = O.matvec_tolerance_report(y, ref, yf, ad, self.cols)
             return {k: rep[k] for k in ("ok", "rows_failed", "norm_rel_err",
                                         "gpu_err_vs_f64_norm", "cpu_err_vs_f64_norm")}
+        if self.kind == "gate_up":
+            _, g, ag, u, au = O.q4k_gate_up_f64(self.qg, self.qu, self.x, self.rows, self.units)
+            rep = O.gate_up_tolerance_report(y, g, ag, u, au, self.cols)
+            return {k: rep[k] for k in ("ok", "rows_failed", "worst_over_bound", "norm_rel_err")}
         # batched: against the f64 product of the same RN_f16 weights
         w16 = O.q4k_dequant(self.q, self.rows * self.units).reshape(self.rows, self.cols)
         w16 = w16.astype(np.float16).astype(np.float64)
@@ -175,6 +197,15 @@ class Case:
             one = lambda: O.q4k_matvec_single(self.q, self.x, self.rows, self.units)
             many = lambda: O.q4k_matvec(self.q, self.x, self.rows, self.units, threads=threads)
             frac, what = 1.0, f"full {self.rows}x{self.cols} Q4_K matvecs"
+        elif self.kind == "gate_up":
+            def two(threads):
+                g = O.q4k_matvec(self.qg, self.x, self.rows, self.units, threads=threads)
+                u = O.q4k_matvec(self.qu, self.x, self.rows, self.units, threads=threads)
+                return O.silu(g) * u
+
+            one = lambda: two(1)
+            many = lambda: two(threads)
+            frac, what = 1.0, f"gate+up {self.rows}x{self.cols} Q4_K matvec pairs + silu*mul"
         elif self.kind == "q4_0":
             one = lambda: O.q4_0_matvec(self.q, self.x, self.rows, self.units, threads=1)
             many = lambda: O.q4_0_matvec(self.q, self.x, self.rows, self.units, threads=threads)
@@ -300,7 +331,8 @@ def main() -> int:
     pct = {p: round(per_call[min(len(per_call) - 1, int(p / 100 * len(per_call)))], 3)
            for p in (10, 50, 90)}
     kernel = case.kernel()
-    shape = f"{case.rows}x{case.cols}" + (f"xB{case.batch}" if kind == "matmul" else "")
+    shape = (("2x" if kind == "gate_up" else "") + f"{case.rows}x{case.cols}"
+             + (f"xB{case.batch}" if kind == "matmul" else ""))
     traffic, traffic_src = profiled_traffic(kernel, shape)
 
     if args.calibrate_copy:
@@ -327,6 +359,9 @@ def main() -> int:
         if kind == "matmul":
             metric = (f"Q4_K_M x f16 matmul weight-bytes HBM GB/s at {case.rows}x{case.cols}, "
                       f"B={case.batch}; us/call")
+        elif kind == "gate_up":
+            metric = (f"Q4_K_M fused gate+up (silu(g)*u) weight-bytes HBM GB/s at {shape}; "
+                      "us/call")
         else:
             metric = f"{qname} matvec weight-bytes HBM GB/s (% of peak) at {shape}; us/call"
 

@@ -194,6 +194,24 @@ axh_status axh_q4_0_matvec(axh_context *ctx, const void *q, const float *x, floa
                            const axh_q4_variant *variant, void *stream);
 axh_status axh_q4_0_matvec_kernel_name(uint32_t n_rows, uint32_t blocks_per_row,
                                        const axh_q4_variant *variant, char *buf, size_t cap);
+/* Fused SwiGLU gate/up projection of a decode step, one pass over x:
+ *   h[r] = silu(g_r) * u_r,  g_r = dot(q_gate row r, x),  u_r = dot(q_up row r, x),
+ *   silu(g) = g / (1 + exp(-g)),
+ * for two Q4_K_M matrices of the same shape (n_rows rows of sb_per_row
+ * superblocks).  No counterpart in the reference, whose kernels stop at one
+ * matvec per dispatch (multi-row work is roadmap, ROADMAP.md:54-72); it
+ * equals two axh_q4k_matvec calls followed by silu(g) * u, with each dot
+ * product held to the matvec's tolerance.  Limits: 1 <= sb_per_row <= 128,
+ * each matrix below 4 GiB, q_gate / q_up / x 16-byte aligned.  Variant holes:
+ * rows_per_wave = output rows per lane group (each reads that many gate and
+ * up rows), waves_per_workgroup, prefetch; nontemporal 0 or 2. */
+axh_status axh_q4k_gate_up(axh_context *ctx, const void *q_gate, const void *q_up,
+                           const float *x, float *h, uint32_t n_rows, uint32_t sb_per_row,
+                           const axh_q4_variant *variant, void *stream);
+axh_status axh_q4k_gate_up_kernel_name(uint32_t n_rows, uint32_t sb_per_row,
+                                       const axh_q4_variant *variant, char *buf, size_t cap);
+uint32_t axh_q4k_gate_up_variant_count(void);
+axh_status axh_q4k_gate_up_variant_at(uint32_t i, axh_q4_variant *out);
 /* Decode-only kernels, bit-exact with the reference's CPU dequantisation
  * (common_helpers.rs:437-454; common.rs:229-253): w receives 256 (Q4_K) or
  * 32 (Q4_0) f32 per unit in the reference's element order. */

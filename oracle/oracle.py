@@ -179,6 +179,54 @@ def q4k_matmul_f16x(q, x_f16_bits, n_rows: int, sb_per_row: int, batch: int,
     return y
 
 
+# ---- SwiGLU gate/up (no reference counterpart) -------------------------------
+def silu(g) -> np.ndarray:
+    """silu(g) = g * sigmoid(g) = g / (1 + exp(-g)) in f64 (the SwiGLU gate of
+    a decode step's feed-forward block; the reference stops at one matvec,
+    ROADMAP.md:54-72).  Pinned against scipy.special.expit, the identity
+    silu(g) - silu(-g) = g and closed-form values."""
+    g = np.asarray(g, dtype=np.float64)
+    with np.errstate(over="ignore"):
+        return g / (1.0 + np.exp(-g))
+
+
+def q4k_gate_up_f64(q_gate, q_up, x, n_rows: int, sb_per_row: int):
+    """h = silu(Wg x) * (Wu x) from the f64 row dots; also returns the dots
+    (g, |g| terms, u, |u| terms) for the tolerance criterion."""
+    g, ag = q4k_matvec_f64(q_gate, x, n_rows, sb_per_row)
+    u, au = q4k_matvec_f64(q_up, x, n_rows, sb_per_row)
+    return silu(g) * u, g, ag, u, au
+
+
+def gate_up_tolerance_report(h_gpu, g, ag, u, au, n_cols: int, rel_tol: float = 1e-3,
+                             cancel_frac: float = 0.1) -> dict:
+    """Acceptance for h = silu(g) * u when each dot product may carry the
+    matvec criterion's error e = rel_tol * (|c| if |c| >= cancel_frac * s
+    else s), s = sum|w x| / sqrt(n): per row
+      |h - h_ref| <= L * e_g * (|u| + e_u) + |silu(g)| * e_u + 8 ulp(h_ref)
+    with L = 1.1 >= max |silu'|, and ||h - h_ref|| <= rel_tol * ||h_ref||."""
+    h = np.asarray(h_gpu, dtype=np.float64)
+    g, u = np.asarray(g, np.float64), np.asarray(u, np.float64)
+
+    def allowed(c, a):
+        s = np.asarray(a, np.float64) / np.sqrt(max(1, n_cols))
+        return rel_tol * np.where(np.abs(c) < cancel_frac * s, s, np.abs(c))
+
+    ref = silu(g) * u
+    e_g, e_u = allowed(g, ag), allowed(u, au)
+    bound = 1.1 * e_g * (np.abs(u) + e_u) + np.abs(silu(g)) * e_u + 8 * 2.0 ** -24 * np.abs(ref)
+    diff = np.abs(h - ref)
+    row_ok = (diff <= bound) & np.isfinite(h)
+    norm_err = float(np.linalg.norm(h - ref) / max(np.linalg.norm(ref), 1e-30))
+    return {
+        "rows": int(h.size),
+        "rows_failed": int((~row_ok).sum()),
+        "worst_over_bound": float((diff / np.maximum(bound, 1e-300)).max()) if h.size else 0.0,
+        "norm_rel_err": norm_err,
+        "ok": bool(row_ok.all() and norm_err <= rel_tol),
+    }
+
+
 # ---- generators ------------------------------------------------------------
 def generate_q4km_test_data(n_superblocks: int, seed: int):
     """generate_q4km_test_data (tests/common_helpers.rs:476-519)."""

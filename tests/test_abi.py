@@ -175,3 +175,25 @@ def test_matmul_kernel_selection(axc):
     assert {v.kind for v in vs} == {1, 2, 3}
     for v in vs:
         assert name(64, 64, v).startswith("axh_q4k_matmul_")
+
+
+def test_gate_up_kernel_selection(axc):
+    """Fused gate/up: persistent kernel only; x staging widened for long rows;
+    rows past 128 superblocks and non-temporal requests are typed errors."""
+    name = axc.q4k_gate_up_kernel_name
+    assert name(14336, 16) == "axh_q4k_gate_up_r1_w4_p2_x1"
+    assert name(14336, 56) == "axh_q4k_gate_up_r1_w8_p2_x1"
+    assert name(14336, 128) == "axh_q4k_gate_up_r1_w8_p2_x2"
+    assert name(14336, 16, axc.Variant(2, 8, 2, 0)) == "axh_q4k_gate_up_r2_w8_p2_x1"
+    assert name(14336, 56, axc.Variant(1, 4, 2, 0)) == "axh_q4k_gate_up_r1_w4_p2_x2"
+    co = axc.builtin_code_object()
+    vs = axc.compiled_variants("gate_up")
+    assert len(set(vs)) == len(vs) >= 4
+    for v in vs:
+        assert name(1000, 16, v).encode() in co
+    for sb in (1, 16, 64, 128):
+        assert name(7, sb).encode() in co
+    for bad in ((4, 0, None), (4, 129, None), (4, 16, axc.Variant(0, 0, 0, 1)),
+                (4, 16, axc.Variant(3, 4, 2, 0)), (4, 100, axc.Variant(2, 4, 2, 0))):
+        with pytest.raises(axc.DispatchError):
+            name(*bad)

@@ -1,0 +1,133 @@
+"""Fused SwiGLU gate/up projection on the GPU (marked `gpu`):
+h[r] = silu(Wg[r] . x) * (Wu[r] . x) for two Q4_K_M matrices.
+
+The reference has no such kernel (its dispatches stop at one matvec,
+ROADMAP.md:54-72); the checks hold the fused result to the matvec's own
+criterion:
+  * against the f64 oracle (oracle.gate_up_tolerance_report: each dot product
+    within the matvec tolerance, propagated through silu(g) * u, plus 1e-3
+    norm-wise);
+  * against two axh_q4k_matvec calls with the same holes, whose per-row
+    arithmetic the fused kernel shares: silu(g) * u of those outputs agrees
+    to f32 rounding of the final combination (pins the gate/up row pairing
+    and the row order).
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-3
+
+
+def _say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _dev(ctx, arr):
+    b = ctx.alloc(max(arr.nbytes, 16))
+    ctx.upload(b, arr)
+    return b
+
+
+def _inputs(seed, rows, sb, sigma=0.5):
+    qg = O.gen_q4k_weights(seed, rows * sb)
+    qu = O.gen_q4k_weights(seed + 1, rows * sb)
+    x = O.gen_normal_f32(seed + 2, sb * 256, sigma)
+    return qg, qu, x
+
+
+def _gate_up(ctx, qg, qu, x, rows, sb, variant=None):
+    dg, du, dx, dh = _dev(ctx, qg), _dev(ctx, qu), _dev(ctx, x), ctx.alloc(rows * 4)
+    ctx.q4k_gate_up(dg, du, dx, dh, rows, sb, variant)
+    ctx.synchronize()
+    h = np.frombuffer(ctx.download(dh, rows * 4), dtype=np.float32).copy()
+    for b in (dg, du, dx, dh):
+        b.close()
+    return h
+
+
+def _matvec(ctx, q, x, rows, sb, variant=None):
+    dq, dx, dy = _dev(ctx, q), _dev(ctx, x), ctx.alloc(rows * 4)
+    ctx.q4k_matvec(dq, dx, dy, rows, sb, variant)
+    ctx.synchronize()
+    y = np.frombuffer(ctx.download(dy, rows * 4), dtype=np.float32).copy()
+    for b in (dq, dx, dy):
+        b.close()
+    return y
+
+
+def _check(h, qg, qu, x, rows, sb, what):
+    _, g, ag, u, au = O.q4k_gate_up_f64(qg, qu, x, rows, sb)
+    rep = O.gate_up_tolerance_report(h, g, ag, u, au, sb * 256, REL_TOL)
+    _say(f"{what}: {rep}")
+    assert rep["ok"], f"{what}: {rep}"
+
+
+def test_llama3_8b_ffn_shape(ctx):
+    """Gate and up projections of Llama-3-8B: 14336 rows x 4096 columns each."""
+    rows, sb = 14336, 16
+    _say("gate_up 14336x4096")
+    qg, qu, x = _inputs(700, rows, sb)
+    h = _gate_up(ctx, qg, qu, x, rows, sb)
+    _check(h, qg, qu, x, rows, sb, "gate_up 14336x4096")
+
+
+@pytest.mark.parametrize("rows,sb", [(1, 1), (2, 1), (3, 5), (31, 128), (257, 16), (1000, 64),
+                                     (100, 100), (4097, 8), (64, 33)])
+def test_edge_shapes(ctx, rows, sb):
+    """Odd row counts (partial bundles and pairs), one superblock, the longest
+    staged row (128 superblocks), rows needing two staged x sub-blocks."""
+    _say(f"gate_up edge {rows}x{sb}")
+    qg, qu, x = _inputs(rows * 3 + sb, rows, sb, sigma=1.0)
+    h = _gate_up(ctx, qg, qu, x, rows, sb)
+    _check(h, qg, qu, x, rows, sb, f"edge {rows}x{sb}")
+
+
+def test_every_variant_matches_two_matvecs(ctx, axc):
+    rows, sb = 1531, 24
+    qg, qu, x = _inputs(710, rows, sb)
+    for v in axc.compiled_variants("gate_up"):
+        _say(f"gate_up variant {v}")
+        h = _gate_up(ctx, qg, qu, x, rows, sb, v)
+        _check(h, qg, qu, x, rows, sb, f"variant {v}")
+        mv = axc.Variant(v.rows_per_wave, v.waves_per_workgroup, v.prefetch, 2)
+        try:
+            g = _matvec(ctx, qg, x, rows, sb, mv)
+            u = _matvec(ctx, qu, x, rows, sb, mv)
+        except axc.DispatchError:
+            continue  # no matvec compiled with these holes
+        want = O.silu(g.astype(np.float64)) * u.astype(np.float64)
+        assert np.all(np.abs(h - want) <= 4 * 2.0 ** -24 * np.abs(want) + 1e-30), str(v)
+
+
+def test_large_gate_saturates_and_negative_gate_vanishes(ctx):
+    """Rows scaled so |g| reaches hundreds: silu(g) -> g for g >> 0 and -> 0
+    (no NaN from exp overflow) for g << 0."""
+    rows, sb = 256, 4
+    qg, qu, x = _inputs(720, rows, sb)
+    x = (x * np.float32(40.0)).astype(np.float32)
+    h = _gate_up(ctx, qg, qu, x, rows, sb)
+    assert np.all(np.isfinite(h))
+    _check(h, qg, qu, x, rows, sb, "saturating gates")
+
+
+def test_invalid_arguments_are_typed_errors(ctx, axc):
+    b = ctx.alloc(1 << 20)
+    with pytest.raises(axc.DispatchError):
+        ctx.q4k_gate_up(b, b, b, b, 4, 0)  # no superblocks
+    with pytest.raises(axc.DispatchError):
+        ctx.q4k_gate_up(b, b, b, b, 4, 129)  # row longer than the staged x
+    with pytest.raises(axc.DispatchError):
+        ctx.q4k_gate_up(b, b, b, b, 4, 1, axc.Variant(0, 0, 0, 1))  # no non-temporal kernel
+    with pytest.raises(axc.DispatchError):
+        ctx.q4k_gate_up(b, b, b, b, 4, 1, axc.Variant(3, 4, 2, 0))  # not compiled
+    ctx.q4k_gate_up(b, b, b, b, 0, 1)  # empty: nothing to do
+    b.close()

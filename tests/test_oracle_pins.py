@@ -316,3 +316,45 @@ def test_batched_oracle_is_per_column_dot():
     for b in range(batch):
         assert np.array_equal(Y[:, b].view(np.uint32),
                               O.q4k_matvec_single(q, xf[b], rows, sb).view(np.uint32))
+
+
+# ---- f3: SwiGLU gate/up ----------------------------------------------------------
+def test_silu_matches_scipy_expit_and_closed_forms():
+    from scipy.special import expit
+
+    g = np.concatenate([np.linspace(-60, 60, 2001), [0.0, 1e-30, -1e-30, 700.0, -700.0]])
+    s = O.silu(g)
+    assert np.allclose(s, g * expit(g), rtol=1e-14, atol=1e-300)
+    assert O.silu(0.0) == 0.0
+    assert O.silu(1.0) == pytest.approx(1.0 / (1.0 + np.exp(-1.0)), rel=1e-15)
+    assert O.silu(800.0) == 800.0 and O.silu(-800.0) == 0.0  # exp overflow handled
+    # silu(g) - silu(-g) = g * (sigmoid(g) + sigmoid(-g)) = g
+    assert np.allclose(O.silu(g) - O.silu(-g), g, rtol=1e-13, atol=1e-12)
+
+
+def test_gate_up_oracle_is_silu_of_rowwise_dots():
+    rows, sb = 9, 2
+    qg, qu = O.gen_q4k_weights(61, rows * sb), O.gen_q4k_weights(62, rows * sb)
+    x = O.gen_normal_f32(63, sb * 256, 0.5)
+    h, g, ag, u, au = O.q4k_gate_up_f64(qg, qu, x, rows, sb)
+    wg = O.q4k_dequant(qg, rows * sb).reshape(rows, -1).astype(np.float64)
+    wu = O.q4k_dequant(qu, rows * sb).reshape(rows, -1).astype(np.float64)
+    xd = x.astype(np.float64)
+    assert np.allclose(g, wg @ xd, rtol=1e-12) and np.allclose(u, wu @ xd, rtol=1e-12)
+    assert np.allclose(ag, np.abs(wg) @ np.abs(xd), rtol=1e-12)
+    assert np.allclose(h, (wg @ xd) / (1 + np.exp(-(wg @ xd))) * (wu @ xd), rtol=1e-12)
+
+
+def test_gate_up_tolerance_rejects_swapped_and_perturbed_rows():
+    rows, sb = 64, 16
+    qg, qu = O.gen_q4k_weights(64, rows * sb), O.gen_q4k_weights(65, rows * sb)
+    x = O.gen_normal_f32(66, sb * 256, 0.5)
+    h, g, ag, u, au = O.q4k_gate_up_f64(qg, qu, x, rows, sb)
+    assert O.gate_up_tolerance_report(h.astype(np.float32), g, ag, u, au, sb * 256)["ok"]
+    swapped = O.silu(u) * g  # gate and up exchanged
+    assert not O.gate_up_tolerance_report(swapped, g, ag, u, au, sb * 256)["ok"]
+    shifted = np.roll(h, 1)  # row r paired with row r-1
+    assert not O.gate_up_tolerance_report(shifted, g, ag, u, au, sb * 256)["ok"]
+    bad = h.copy()
+    bad[5] *= 1.01
+    assert not O.gate_up_tolerance_report(bad, g, ag, u, au, sb * 256)["ok"]
