@@ -159,6 +159,9 @@ def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
         "axh_q4k_gate_up_variant_at": (st, [u32, c.POINTER(_Variant)]),
         "axh_q4k_matmul_f16": (st, [vp, vp, vp, vp, u32, u32, u32, c.POINTER(_MatmulVariant),
                                     vp]),
+        "axh_q4k_matmul_f32": (st, [vp, vp, vp, vp, vp, u32, u32, u32,
+                                    c.POINTER(_MatmulVariant), vp]),
+        "axh_f32_to_f16": (st, [vp, vp, vp, u64, vp]),
         "axh_q4k_matmul_kernel_name": (st, [u32, u32, c.POINTER(_MatmulVariant), c.c_char_p,
                                             sz]),
         "axh_q4k_matmul_variant_count": (u32, []),
@@ -658,6 +661,19 @@ class HipContext:
         _check(self._lib.axh_q4k_matmul_f16(self._raw, _ptr(q), _ptr(x), _ptr(y), n_rows,
                                             sb_per_row, batch, ctypes.byref(v) if v else None,
                                             _stream(stream)))
+
+    def q4k_matmul_f32(self, q, x, x16, y, n_rows: int, sb_per_row: int, batch: int,
+                       variant: Optional[MatmulVariant] = None, stream=None) -> None:
+        """As q4k_matmul for f32 activations: x is rounded to f16 (RN) into
+        x16 (batch * K * 2 bytes), then the f16 matmul runs on x16."""
+        v = variant._c() if variant else None
+        _check(self._lib.axh_q4k_matmul_f32(self._raw, _ptr(q), _ptr(x), _ptr(x16), _ptr(y),
+                                            n_rows, sb_per_row, batch,
+                                            ctypes.byref(v) if v else None, _stream(stream)))
+
+    def f32_to_f16(self, x, h, n: int, stream=None) -> None:
+        """h = RN_f16(x) for n values."""
+        _check(self._lib.axh_f32_to_f16(self._raw, _ptr(x), _ptr(h), n, _stream(stream)))
 
     def q4k_dequant(self, q, w, n_superblocks: int, stream=None) -> None:
         _check(self._lib.axh_q4k_dequant(self._raw, _ptr(q), _ptr(w), n_superblocks,

@@ -1037,6 +1037,34 @@ extern "C" __global__ void __launch_bounds__(256)
   if (i < a.n_units) f[i] = f16_to_f32(h[i]);
 }
 
+// f32 -> f16, round to nearest even, of n values: the activation cast that
+// feeds the batched matmul (one pass: 6 bytes of HBM traffic per value).
+// Eight values per thread (two 16-byte loads, one 16-byte store); the thread
+// holding the last n % 8 values converts them one at a time.  The host
+// guarantees 16-byte aligned x and h and n <= 2^32 - 16.
+typedef _Float16 axh_half2_t __attribute__((ext_vector_type(2)));
+typedef float axh_float2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_rn_f16(float a, float b) {
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_convertvector((axh_float2_t){a, b}, axh_half2_t));
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    axh_f32_to_f16(const float *__restrict__ x, uint16_t *__restrict__ h, CountArgs a) {
+  const uint32_t i = (blockIdx.x * 256u + threadIdx.x) * 8u;
+  if (i + 8u <= a.n_units) {
+    const float4 lo = *reinterpret_cast<const float4 *>(x + i);
+    const float4 hi = *reinterpret_cast<const float4 *>(x + i + 4u);
+    *reinterpret_cast<uint4 *>(h + i) =
+        make_uint4(pack_rn_f16(lo.x, lo.y), pack_rn_f16(lo.z, lo.w), pack_rn_f16(hi.x, hi.y),
+                   pack_rn_f16(hi.z, hi.w));
+  } else {
+    for (uint32_t k = i; k < a.n_units; ++k)
+      h[k] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(x[k]));
+  }
+}
+
 // Bounded busy wait (runtime tests of the completion timeout): sleeps
 // a.n_units times (about 3 us each) and then writes the count.  Always ends.
 extern "C" __global__ void __launch_bounds__(64) axh_spin(uint32_t *__restrict__ out,

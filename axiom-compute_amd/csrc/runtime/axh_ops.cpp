@@ -545,9 +545,9 @@ axh_status axh_q4k_matmul_kernel_name(uint32_t n_rows, uint32_t batch,
   return ok();
 }
 
-axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x, float *y,
-                              uint32_t n_rows, uint32_t sb_per_row, uint32_t batch,
-                              const axh_q4_matmul_variant *variant, void *stream) {
+// Argument checks shared by the f16 and f32 entry points.
+static axh_status q4k_matmul_check(axh_context *ctx, const void *q, const void *x, const float *y,
+                                   uint32_t n_rows, uint32_t sb_per_row, uint32_t batch) {
   if (!ctx) return fail(AXH_ERR_INVALID_ARGUMENT, "ctx is NULL");
   if (n_rows == 0 || batch == 0) return ok();
   if (sb_per_row == 0)
@@ -557,12 +557,20 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
   if (((uintptr_t)q & 15u) || ((uintptr_t)x & 15u) || ((uintptr_t)y & 3u))
     return fail(AXH_ERR_INVALID_ARGUMENT, "q and x must be 16-byte and y 4-byte aligned");
   const uint64_t q_bytes = (uint64_t)n_rows * sb_per_row * 144u;
-  const uint64_t x_bytes = (uint64_t)batch * sb_per_row * 256u * 2u;
-  if (q_bytes >= kMatmulOob || x_bytes >= kMatmulOob)
-    return fail(AXH_ERR_INVALID_ARGUMENT, "q and x must each be below 4 GiB - 256 B");
+  const uint64_t x_f16_bytes = (uint64_t)batch * sb_per_row * 256u * 2u;
+  if (q_bytes >= kMatmulOob || x_f16_bytes >= kMatmulOob)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q and f16 x must each be below 4 GiB - 256 B");
+  return ok();
+}
+
+axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x, float *y,
+                              uint32_t n_rows, uint32_t sb_per_row, uint32_t batch,
+                              const axh_q4_matmul_variant *variant, void *stream) {
+  axh_status s = q4k_matmul_check(ctx, q, x, y, n_rows, sb_per_row, batch);
+  if (s != AXH_OK || n_rows == 0 || batch == 0) return s;
   MatmulVariant v{};
   char name[64];
-  axh_status s = plan_q4k_matmul(n_rows, batch, variant, &v, name, sizeof(name));
+  s = plan_q4k_matmul(n_rows, batch, variant, &v, name, sizeof(name));
   if (s != AXH_OK) return s;
   const uint32_t tm = v.kind == 3 ? 32u : 32u * v.w, tn = 16u * v.nt;
   const uint64_t gx = (n_rows + tm - 1) / tm, gy = (batch + tn - 1) / tn;
@@ -577,6 +585,22 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
   MatmulArgs a{n_rows, sb_per_row, batch, 0};
   s = launch_raw(k, grid, bufs, 3, &a, sizeof(a), 0, pick_stream(ctx, stream));
   return s == AXH_OK ? ok() : s;
+}
+
+axh_status axh_q4k_matmul_f32(axh_context *ctx, const void *q, const float *x, uint16_t *x16,
+                              float *y, uint32_t n_rows, uint32_t sb_per_row, uint32_t batch,
+                              const axh_q4_matmul_variant *variant, void *stream) {
+  axh_status s = q4k_matmul_check(ctx, q, x, y, n_rows, sb_per_row, batch);
+  if (s != AXH_OK || n_rows == 0 || batch == 0) return s;
+  if (!device_ptr_ok(x16) || ((uintptr_t)x16 & 15u))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "x16 must be a 16-byte aligned device pointer");
+  MatmulVariant v{};
+  char name[64];
+  s = plan_q4k_matmul(n_rows, batch, variant, &v, name, sizeof(name));
+  if (s != AXH_OK) return s; // reject a bad variant before any device work
+  s = axh_f32_to_f16(ctx, x, x16, (uint64_t)batch * sb_per_row * 256u, stream);
+  if (s != AXH_OK) return s;
+  return axh_q4k_matmul_f16(ctx, q, x16, y, n_rows, sb_per_row, batch, variant, stream);
 }
 
 static axh_status count_launch(axh_context *ctx, const char *name, const void *in, void *out,
@@ -613,6 +637,13 @@ axh_status axh_q4_0_dequant(axh_context *ctx, const void *q, float *w, uint64_t 
 
 axh_status axh_f16_widen(axh_context *ctx, const uint16_t *h, float *f, uint64_t n, void *stream) {
   return count_launch(ctx, "axh_f16_widen", h, f, n, n, stream);
+}
+
+axh_status axh_f32_to_f16(axh_context *ctx, const float *x, uint16_t *h, uint64_t n, void *stream) {
+  if (n > 0xFFFFFFF0ull) return fail(AXH_ERR_INVALID_ARGUMENT, "n too large for one launch");
+  if (((uintptr_t)x & 15u) || ((uintptr_t)h & 15u))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "x and h must be 16-byte aligned");
+  return count_launch(ctx, "axh_f32_to_f16", x, h, (n + 7u) / 8u, n, stream);
 }
 
 } // extern "C"

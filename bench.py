@@ -38,16 +38,16 @@ COPY_ALIGN = 256
 
 # name: (kind, rows, units per row, x sigma, config label)
 WORKLOADS = {
-    "c1": ("q4_0", 256, 128, 1.0, "config 1"),
-    "c2": ("q4k", 1, 128, 1.0, "config 2"),
-    "c3": ("q4k", 4096, 16, 1.0, "config 3"),
-    "c3b": ("q4k", 14336, 16, 1.0, "config 3"),
-    "c4": ("q4k", 4096, 56, 0.5, "config 4, down-projection"),
-    "head": ("q4k", 128256, 16, 1.0, "config 4, output head"),
-    "c5": ("matmul", 14336, 16, 1.0, "config 5"),
+    "c1": ("q4_0", 256, 128, 1.0, "BASELINE config 1"),
+    "c2": ("q4k", 1, 128, 1.0, "BASELINE config 2"),
+    "c3": ("q4k", 4096, 16, 1.0, "BASELINE config 3"),
+    "c3b": ("q4k", 14336, 16, 1.0, "BASELINE config 3"),
+    "c4": ("q4k", 4096, 56, 0.5, "BASELINE config 4, down-projection"),
+    "head": ("q4k", 128256, 16, 1.0, "BASELINE config 4, output head"),
+    "c5": ("matmul", 14336, 16, 1.0, "BASELINE config 5"),
     # fused SwiGLU gate/up projections of a Llama-3-8B decode step (two
     # 14336 x 4096 Q4_K_M matrices against one x)
-    "ffn": ("gate_up", 14336, 16, 0.5, "gate/up, fused"),
+    "ffn": ("gate_up", 14336, 16, 0.5, "Llama-3-8B gate/up, not a BASELINE config"),
 }
 
 
@@ -89,7 +89,7 @@ def profiled_traffic(kernel: str, workload: str):
 class Case:
     """One workload: device buffers, the launch of step i, parity, CPU baseline."""
 
-    def __init__(self, pkg, O, np, ctx, name, batch, variant):
+    def __init__(self, pkg, O, np, ctx, name, batch, variant, x_f32=False):
         kind, rows, units, sigma, label = WORKLOADS[name]
         self.kind, self.rows, self.units, self.label = kind, rows, units, label
         self.ctx, self.O, self.np, self.pkg = ctx, O, np, pkg
@@ -112,8 +112,11 @@ class Case:
             self.weight_bytes *= 2
         else:
             self.q = O.gen_q4k_weights(seed, rows * units)
+        self.x_f32 = kind == "matmul" and x_f32
         if kind == "matmul":
-            self.x = O.gen_normal_f32(seed + 1, self.cols * self.batch, sigma).astype(np.float16)
+            self.x = O.gen_normal_f32(seed + 1, self.cols * self.batch, sigma)
+            if not self.x_f32:
+                self.x = self.x.astype(np.float16)
             self.y_bytes = self.batch * rows * 4
         else:
             self.x = O.gen_normal_f32(seed + 1, self.cols, sigma)
@@ -129,6 +132,7 @@ class Case:
         self.dx = ctx.alloc(self.x.nbytes)
         ctx.upload(self.dx, self.x)
         self.dy = ctx.alloc(self.y_bytes)
+        self.dx16 = ctx.alloc(self.x.size * 2) if self.x_f32 else None
 
     def launch(self, i: int) -> None:
         w = self.wbuf.ptr + (i % self.n_copies) * self.stride
@@ -139,6 +143,9 @@ class Case:
         elif self.kind == "gate_up":
             self.ctx.q4k_gate_up(w, w + self.up_off, self.dx, self.dy, self.rows, self.units,
                                  self.variant)
+        elif self.x_f32:
+            self.ctx.q4k_matmul_f32(w, self.dx, self.dx16, self.dy, self.rows, self.units,
+                                    self.batch, self.variant)
         else:
             self.ctx.q4k_matmul(w, self.dx, self.dy, self.rows, self.units, self.batch,
                                 self.variant)
@@ -177,7 +184,7 @@ class Case:
         # batched: against the f64 product of the same RN_f16 weights
         w16 = O.q4k_dequant(self.q, self.rows * self.units).reshape(self.rows, self.cols)
         w16 = w16.astype(np.float16).astype(np.float64)
-        xf = self.x.astype(np.float64).reshape(self.batch, self.cols)
+        xf = self.x.astype(np.float16).astype(np.float64).reshape(self.batch, self.cols)
         ref = xf @ w16.T
         yy = y.reshape(self.batch, self.rows)
         err = float(np.linalg.norm(yy - ref) / max(np.linalg.norm(ref), 1e-30))
@@ -213,7 +220,7 @@ class Case:
         else:
             sl = max(1, min(self.rows, 16384 // self.batch))
             qs = self.q[: sl * self.units * 144]
-            xb = self.x.view(self.np.uint16)
+            xb = self.x.astype(self.np.float16).view(self.np.uint16)
             one = lambda: O.q4k_matmul_f16x(qs, xb, sl, self.units, self.batch, threads=1)
             many = lambda: O.q4k_matmul_f16x(qs, xb, sl, self.units, self.batch,
                                              threads=threads)
@@ -240,8 +247,9 @@ class Case:
         }
 
     def close(self) -> None:
-        for b in (self.wbuf, self.dx, self.dy):
-            b.close()
+        for b in (self.wbuf, self.dx, self.dy, self.dx16):
+            if b is not None:
+                b.close()
 
 
 def parse_variant(pkg, kind: str, text: str):
@@ -258,6 +266,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c4", choices=sorted(WORKLOADS))
     ap.add_argument("--batch", type=int, default=128, help="activation vectors (c5 only)")
+    ap.add_argument("--x-f32", action="store_true",
+                    help="c5 only: f32 activations (cast to f16 by a separate pass, then the "
+                         "f16 matmul; both timed)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--variant", default="",
                     help="matvec: rows_per_wave,waves,prefetch[,nontemporal]; "
@@ -280,7 +291,7 @@ def main() -> int:
     kind = WORKLOADS[args.workload][0]
     variant = parse_variant(pkg, kind, args.variant)
     ctx = pkg.HipContext.new()
-    case = Case(pkg, O, np, ctx, args.workload, args.batch, variant)
+    case = Case(pkg, O, np, ctx, args.workload, args.batch, variant, args.x_f32)
 
     par = case.parity()
     if not par["ok"]:
@@ -383,10 +394,11 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16 in, f32 accumulate" if kind == "matmul" else "f32",
+        "dtype": ("f32 in (cast to f16, RN), f32 accumulate" if case.x_f32
+                  else "f16 in, f32 accumulate") if kind == "matmul" else "f32",
         "data": "synthetic",
         "config": {
-            "workload": f"{args.workload}: {kind} {shape} (BASELINE {case.label})",
+            "workload": f"{args.workload}: {kind} {shape} ({case.label})",
             "rows": case.rows,
             "cols": case.cols,
             "batch": case.batch,

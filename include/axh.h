@@ -222,11 +222,16 @@ axh_status axh_q4_0_dequant(axh_context *ctx, const void *q, float *w, uint64_t 
 /* IEEE binary16 -> binary32 widening of n raw patterns (the ptr_read_u16_zext +
  * f16_bits_to_f32 builtins, crates/axc-codegen/src/q4_0.rs:86-171). */
 axh_status axh_f16_widen(axh_context *ctx, const uint16_t *h, float *f, uint64_t n, void *stream);
+/* binary32 -> binary16, round to nearest even, of n values (NaN stays NaN,
+ * values beyond the f16 range become infinities): the activation cast that
+ * feeds the f16 matmul.  No counterpart in the reference.  x and h 16-byte
+ * aligned; n < 2^32 - 16. */
+axh_status axh_f32_to_f16(axh_context *ctx, const float *x, uint16_t *h, uint64_t n, void *stream);
 
 /* ---- graph capture -----------------------------------------------------------
  * Records the launches issued on the context stream between begin and end
- * (axh_q4k_matvec, axh_q4_0_matvec, axh_q4k_matmul_f16, axh_launch with a NULL
- * stream) into a graph that replays them in order with no host work per
+ * (axh_q4k_matvec, axh_q4_0_matvec, axh_q4k_gate_up, axh_q4k_matmul_f16/_f32,
+ * axh_launch with a NULL stream) into a graph that replays them in order with no host work per
  * kernel: the HIP counterpart of recording a Vulkan command buffer once and
  * resubmitting it.  Launch each operation once before capturing it (its
  * kernel is then prepared and cached).  No event, copy or synchronisation
@@ -260,6 +265,15 @@ typedef struct axh_q4_matmul_variant {
 } axh_q4_matmul_variant;
 axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x, float *y,
                               uint32_t n_rows, uint32_t sb_per_row, uint32_t batch,
+                              const axh_q4_matmul_variant *variant, void *stream);
+/* The same product for f32 activations: x (batch x K f32) is first rounded
+ * to f16 (RN, ties to even) into the caller's buffer x16 (batch x K f16) by
+ * axh_f32_to_f16, then axh_q4k_matmul_f16 runs on x16; both launches go to
+ * `stream` in that order.  A separate cast pass is cheaper than converting
+ * inside the matmul's loads, because every row tile re-reads X.  x and x16
+ * 16-byte aligned.  No counterpart in the reference (see axh_q4k_matmul_f16). */
+axh_status axh_q4k_matmul_f32(axh_context *ctx, const void *q, const float *x, uint16_t *x16,
+                              float *y, uint32_t n_rows, uint32_t sb_per_row, uint32_t batch,
                               const axh_q4_matmul_variant *variant, void *stream);
 axh_status axh_q4k_matmul_kernel_name(uint32_t n_rows, uint32_t batch,
                                       const axh_q4_matmul_variant *variant, char *buf,

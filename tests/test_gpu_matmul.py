@@ -154,3 +154,88 @@ def test_invalid_arguments_are_typed_errors(ctx, axc):
         ctx.q4k_matmul(b, b, b, 4, 1, 2, axc.MatmulVariant(1, 3, 3, 1))  # not compiled
     ctx.q4k_matmul(b, b, b, 0, 1, 2)  # empty: nothing to do
     b.close()
+
+
+def _x32_with_ties(seed, n):
+    """N(0, 1) f32 activations plus exact f16 rounding ties (both directions of
+    ties-to-even), values in the f16 subnormal range and exact f16 values."""
+    x = O.gen_normal_f32(seed, n)
+    m = n // 8
+    k = np.arange(m, dtype=np.float32)
+    x[:m] = (1.0 + (2 * (k % 512) + 1) * 2.0 ** -11).astype(np.float32)  # halfway cases
+    x[m:2 * m] = (k % 1000 - 500).astype(np.float32) * np.float32(2.0 ** -25)  # subnormals
+    x[2 * m:3 * m] = -x[:m] * np.float32(3.0)
+    return x
+
+
+def _run_f32(ctx, q, x32, rows, sb, batch, variant=None):
+    dq, dx, dy = _dev(ctx, q), _dev(ctx, x32), ctx.alloc(batch * rows * 4)
+    dx16 = ctx.alloc(max(16, x32.size * 2))
+    ctx.q4k_matmul_f32(dq, dx, dx16, dy, rows, sb, batch, variant)
+    ctx.synchronize()
+    y = np.frombuffer(ctx.download(dy, batch * rows * 4), dtype=np.float32).reshape(batch, rows)
+    x16 = np.frombuffer(ctx.download(dx16, x32.size * 2), dtype=np.uint16)
+    for b in (dq, dx, dy, dx16):
+        b.close()
+    return y.copy(), x16.copy()
+
+
+@pytest.mark.parametrize("rows,sb,batch", [(14336, 16, 8), (14336, 16, 32), (14336, 16, 512),
+                                           (257, 2, 130), (31, 4, 1)])
+def test_f32_activations_equal_f16_kernel_on_rn_f16_x(ctx, rows, sb, batch):
+    """f32 activations: the cast buffer holds numpy's round-to-nearest-even f16
+    of x bit for bit, and Y equals the f16 entry point on it bit for bit."""
+    _say(f"matmul f32 X {rows}x{sb * 256} B={batch}")
+    q = O.gen_q4k_weights(rows + batch, rows * sb)
+    x32 = _x32_with_ties(rows + 3 * batch, sb * 256 * batch)
+    y32, x16 = _run_f32(ctx, q, x32, rows, sb, batch)
+    assert np.array_equal(x16, x32.astype(np.float16).view(np.uint16))
+    y16 = _run(ctx, q, x32.astype(np.float16), rows, sb, batch)
+    assert np.array_equal(y32.view(np.uint32), y16.view(np.uint32))
+
+
+def test_f32_activations_every_variant(ctx, axc):
+    rows, sb, batch = 200, 3, 40
+    q = O.gen_q4k_weights(95, rows * sb)
+    x32 = _x32_with_ties(96, sb * 256 * batch)
+    xh = x32.astype(np.float16)
+    for v in axc.compiled_matmul_variants():
+        _say(f"matmul f32 X variant {v}")
+        y32, _ = _run_f32(ctx, q, x32, rows, sb, batch, v)
+        y16 = _run(ctx, q, xh, rows, sb, batch, v)
+        assert np.array_equal(y32.view(np.uint32), y16.view(np.uint32)), str(v)
+        _check(y32, q, xh, rows, sb, batch, f"f32 X variant {v}")
+
+
+def _cast(ctx, x32):
+    dx, dh = _dev(ctx, x32), ctx.alloc(max(16, x32.size * 2))
+    ctx.f32_to_f16(dx, dh, x32.size)
+    ctx.synchronize()
+    h = np.frombuffer(ctx.download(dh, x32.size * 2), dtype=np.uint16).copy()
+    for b in (dx, dh):
+        b.close()
+    return h
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 9, 15, 17, 4096 * 32 + 5])
+def test_f32_to_f16_cast_matches_numpy(ctx, n):
+    """Every class of f32 input against numpy's RNE cast, bit for bit (NaN by
+    class): ties both ways, f16 subnormals and underflow to zero, overflow to
+    infinity, signed zeros, infinities; n covers the 8-value groups and tails."""
+    rng = np.random.default_rng(n)
+    bits = rng.integers(0, 2 ** 32, size=n, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32).copy()
+    special = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 65504.0, 65520.0, 65519.99,
+                        2.0 ** -24, 2.0 ** -25, 2.0 ** -25 * 1.0000001, 3 * 2.0 ** -26,
+                        1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11, -(1 + 2.0 ** -11), 6.1e-5],
+                       dtype=np.float32)
+    m = min(n, special.size)
+    x[:m] = special[:m]
+    half = n // 2
+    x[m:half] = rng.normal(size=max(0, half - m)).astype(np.float32)
+    h = _cast(ctx, x)
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    nan = np.isnan(x)
+    assert np.array_equal(h[~nan], want[~nan])
+    assert np.all(np.isnan(h[nan].view(np.float16)))
