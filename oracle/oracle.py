@@ -18,6 +18,9 @@ LIB_PATH = HERE / "liboracle.so"
 
 Q4_0_BLOCK_BYTES, Q4_0_BLOCK_ELEMS = 18, 32
 Q4K_SB_BYTES, Q4K_SB_ELEMS = 144, 256
+# ggml type ids (GGUF) and superblock bytes of the k-quants next to Q4_K.
+GGML_Q5_K, GGML_Q6_K = 13, 14
+KQ_SB_BYTES = {GGML_Q5_K: 176, GGML_Q6_K: 210}
 
 _lib = None
 
@@ -49,6 +52,13 @@ def lib() -> ctypes.CDLL:
             "axo_gen_q4k_weights": (None, [u64, vp, sz]),
             "axo_gen_q4_0_weights": (None, [u64, vp, sz]),
             "axo_gen_normal_f32": (None, [u64, vp, sz, c.c_double]),
+            "axo_q5k_dequant": (None, [vp, vp, sz]),
+            "axo_q6k_dequant": (None, [vp, vp, sz]),
+            "axo_kq_dot": (c.c_float, [i32, vp, vp, sz]),
+            "axo_kq_matvec": (None, [i32, vp, vp, vp, sz, sz, i32]),
+            "axo_kq_matvec_f64": (None, [i32, vp, vp, vp, vp, sz, sz]),
+            "axo_gen_q5k_weights": (None, [u64, vp, sz]),
+            "axo_gen_q6k_weights": (None, [u64, vp, sz]),
         }
         for name, (res, args) in sigs.items():
             f = getattr(L, name)
@@ -177,6 +187,43 @@ def q4k_matmul_f16x(q, x_f16_bits, n_rows: int, sb_per_row: int, batch: int,
     lib().axo_q4k_matmul_f16x(_p(q), _p(xb), _p(y), n_rows, sb_per_row, batch,
                               threads or default_threads())
     return y
+
+
+# ---- Q5_K / Q6_K (ggml k-quants; restated in kq_oracle.c) ---------------------
+def kq_dequant(kind: int, q, n_superblocks: int) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    assert q.size >= n_superblocks * KQ_SB_BYTES[kind]
+    w = np.empty(n_superblocks * 256, dtype=np.float32)
+    fn = lib().axo_q5k_dequant if kind == GGML_Q5_K else lib().axo_q6k_dequant
+    fn(_p(q), _p(w), n_superblocks)
+    return w
+
+
+def kq_matvec(kind: int, q, x, n_rows: int, sb_per_row: int, threads: int = 0) -> np.ndarray:
+    """Row r: sequential f32 dot of row r's superblocks with x (element order)."""
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert q.size >= n_rows * sb_per_row * KQ_SB_BYTES[kind] and x.size >= sb_per_row * 256
+    y = np.empty(n_rows, dtype=np.float32)
+    lib().axo_kq_matvec(kind, _p(q), _p(x), _p(y), n_rows, sb_per_row,
+                        threads or default_threads())
+    return y
+
+
+def kq_matvec_f64(kind: int, q, x, n_rows: int, sb_per_row: int):
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(n_rows, dtype=np.float64)
+    a = np.empty(n_rows, dtype=np.float64)
+    lib().axo_kq_matvec_f64(kind, _p(q), _p(x), _p(y), _p(a), n_rows, sb_per_row)
+    return y, a
+
+
+def gen_kq_weights(kind: int, seed: int, n_superblocks: int) -> np.ndarray:
+    q = np.empty(n_superblocks * KQ_SB_BYTES[kind], dtype=np.uint8)
+    fn = lib().axo_gen_q5k_weights if kind == GGML_Q5_K else lib().axo_gen_q6k_weights
+    fn(seed, _p(q), n_superblocks)
+    return q
 
 
 # ---- SwiGLU gate/up (no reference counterpart) -------------------------------

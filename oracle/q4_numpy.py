@@ -65,6 +65,54 @@ def q4k_dequant(q: np.ndarray) -> np.ndarray:
     return out.reshape(-1)
 
 
+# ---- Q5_K / Q6_K (ggml k-quants), from each weight's point of view -----------
+# Element e of a superblock is traced to the byte, nibble and bit it comes
+# from (ggml block_q5_K / block_q6_K layouts), instead of looping over the
+# packed bytes as the C oracle does.
+def _q6k_sources():
+    e = np.arange(256)
+    n, r = e // 128, e % 128
+    part, l = r // 32, r % 32               # part 0..3: q1..q4 of ggml's loop
+    ql_byte = 64 * n + l + 32 * (part % 2)  # parts 1 and 3 read ql[l + 32]
+    ql_shift = 4 * (part // 2)              # parts 2 and 3 take the high nibble
+    qh_byte = 128 + 32 * n + l
+    qh_shift = 2 * part
+    sc_byte = 192 + 8 * n + l // 16 + 2 * part
+    return ql_byte, ql_shift, qh_byte, qh_shift, sc_byte
+
+
+def q6k_dequant(q: np.ndarray) -> np.ndarray:
+    """Q6_K, 210-byte superblocks: w = d * sc * (q6 - 32); every product is exact."""
+    b = np.asarray(q, dtype=np.uint8).reshape(-1, 210).astype(np.int64)
+    ql_b, ql_s, qh_b, qh_s, sc_b = _q6k_sources()
+    q6 = ((b[:, ql_b] >> ql_s) & 0xF) | (((b[:, qh_b] >> qh_s) & 3) << 4)
+    sc = b[:, sc_b]
+    sc = np.where(sc >= 128, sc - 256, sc)  # int8
+    d = b[:, 208:210].astype(np.uint8).copy().view(np.float16).astype(np.float64)
+    w = d * sc * (q6 - 32)  # exact in f64, and representable in f32
+    return w.astype(np.float32).reshape(-1)
+
+
+def q5k_dequant(q: np.ndarray) -> np.ndarray:
+    """Q5_K, 176-byte superblocks: w = RN_f32(d*sc*q5 - dmin*m), q5 = nibble + 16*qh bit."""
+    b = np.asarray(q, dtype=np.uint8).reshape(-1, 176)
+    e = np.arange(256)
+    j, hi, l = e // 64, (e % 64) // 32, e % 32
+    bi = b.astype(np.int64)
+    nib = (bi[:, 48 + 32 * j + l] >> (4 * hi)) & 0xF
+    bit = (bi[:, 16 + l] >> (2 * j + hi)) & 1
+    q5 = nib + 16 * bit
+    header = np.concatenate([b[:, :16], np.zeros((b.shape[0], 128), np.uint8)], axis=1)
+    sc_t, m_t = scale_min_table(header)       # same 12-byte scales field as Q4_K
+    sub = 2 * j + hi
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32)
+    dmin = b[:, 2:4].copy().view(np.float16).astype(np.float32)
+    d1 = d * sc_t[:, sub].astype(np.float32)          # exact
+    m1 = dmin * m_t[:, sub].astype(np.float32)        # exact
+    prod = (d1.astype(np.float64) * q5).astype(np.float32)  # exact
+    return (prod - m1).astype(np.float32).reshape(-1)  # one f32 rounding
+
+
 def q4_0_dequant(q: np.ndarray) -> np.ndarray:
     """Q4_0 blocks (n*18 bytes) -> n*32 float32 weights."""
     blk = np.asarray(q, dtype=np.uint8).reshape(-1, 18)

@@ -87,6 +87,24 @@ void axo_gen_q4_0_weights(uint64_t seed, uint8_t *q, size_t n_blocks);
 /* x ~ N(0, sigma^2): Box-Muller on SplitMix64 uniforms, computed in double. */
 void axo_gen_normal_f32(uint64_t seed, float *x, size_t n, double sigma);
 
+/* ---- ggml k-quants next to Q4_K in real checkpoints (kq_oracle.c) ---------
+ * No reference counterpart; restated from ggml's block layouts (see
+ * kq_oracle.c).  type: AXO_GGML_Q5_K or AXO_GGML_Q6_K (GGUF type ids). */
+#define AXO_GGML_Q5_K 13
+#define AXO_GGML_Q6_K 14
+#define AXO_Q5K_SB_BYTES 176u
+#define AXO_Q6K_SB_BYTES 210u
+void axo_q5k_dequant(const uint8_t *q, float *w, size_t n_superblocks);
+void axo_q6k_dequant(const uint8_t *q, float *w, size_t n_superblocks);
+/* Sequential f32 dot in element order (no FMA). */
+float axo_kq_dot(int type, const uint8_t *q, const float *x, size_t n_superblocks);
+void axo_kq_matvec(int type, const uint8_t *q, const float *x, float *y, size_t n_rows,
+                   size_t sb_per_row, int n_threads);
+void axo_kq_matvec_f64(int type, const uint8_t *q, const float *x, double *y, double *absdot,
+                       size_t n_rows, size_t sb_per_row);
+void axo_gen_q5k_weights(uint64_t seed, uint8_t *q, size_t n_superblocks);
+void axo_gen_q6k_weights(uint64_t seed, uint8_t *q, size_t n_superblocks);
+
 #ifdef __cplusplus
 }
 #endif

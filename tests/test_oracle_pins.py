@@ -358,3 +358,126 @@ def test_gate_up_tolerance_rejects_swapped_and_perturbed_rows():
     bad = h.copy()
     bad[5] *= 1.01
     assert not O.gate_up_tolerance_report(bad, g, ag, u, au, sb * 256)["ok"]
+
+
+# ---- f2: Q5_K / Q6_K (ggml k-quants; no reference counterpart) ------------------
+@pytest.mark.parametrize("kind", [O.GGML_Q5_K, O.GGML_Q6_K])
+def test_kq_dequant_matches_independent_restatement(kind):
+    q = O.gen_kq_weights(kind, 77, 500)
+    # include extreme header values: f16 subnormal and large d / dmin
+    nb = O.KQ_SB_BYTES[kind]
+    blocks = q.reshape(-1, nb)
+    d_off = 208 if kind == O.GGML_Q6_K else 0
+    blocks[0, d_off:d_off + 2] = np.array([0x0001], np.uint16).view(np.uint8)
+    blocks[1, d_off:d_off + 2] = np.array([0x7BFF], np.uint16).view(np.uint8)
+    w = O.kq_dequant(kind, q, 500)
+    ref = (N.q5k_dequant if kind == O.GGML_Q5_K else N.q6k_dequant)(q)
+    assert np.array_equal(w.view(np.uint32), ref.view(np.uint32))
+
+
+def _q6k_block(d=1.0, scales=1, ql=0, qh=0):
+    b = np.zeros(210, np.uint8)
+    b[0:128] = ql
+    b[128:192] = qh
+    b[192:208] = np.asarray(scales, np.int8).view(np.uint8) if np.ndim(scales) else np.uint8(
+        np.int8(scales).view(np.uint8))
+    b[208:210] = np.array([d], np.float16).view(np.uint8)
+    return b
+
+
+def test_q6k_closed_forms_and_bit_sources():
+    assert np.all(O.kq_dequant(O.GGML_Q6_K, _q6k_block(0.5), 1) == -16.0)  # q = 0 -> -32
+    assert np.all(O.kq_dequant(O.GGML_Q6_K, _q6k_block(0.5, 1, 0xFF, 0xFF), 1) == 15.5)
+    # scale s of sub-block t (16 weights) multiplies exactly weights 16t..16t+15
+    sc = np.arange(-8, 8, dtype=np.int8) * 3
+    w = O.kq_dequant(O.GGML_Q6_K, _q6k_block(0.25, sc, 0, 0), 1).reshape(2, 4, 2, 16)
+    for n in range(2):
+        for part in range(4):
+            for half in range(2):
+                s = int(sc[8 * n + half + 2 * part])
+                assert np.all(w[n, part, half] == 0.25 * s * -32), (n, part, half)
+    # one qh bit pair / one ql nibble at a time: exactly one weight moves
+    for byte, shift, elem, q6 in [(128 + 5, 2, 32 + 5, 16), (128 + 32 + 7, 6, 128 + 96 + 7, 16),
+                                  (128 + 0, 0, 0, 16), (40, 4, 96 + 8, 1), (64 + 3, 0, 128 + 3, 1)]:
+        b = _q6k_block(1.0)
+        b[byte] = np.uint8(1 << shift)
+        w = O.kq_dequant(O.GGML_Q6_K, b, 1)
+        moved = np.flatnonzero(w != -32.0)
+        assert moved.tolist() == [elem] and w[elem] == q6 - 32, (byte, shift)
+
+
+def test_q6k_planted_mistakes_are_rejected():
+    """A restatement with the qh bit pairs of parts 1 and 2 swapped, or with
+    ql halves exchanged, disagrees with the pinned oracle."""
+    q = O.gen_kq_weights(O.GGML_Q6_K, 78, 8)
+    w = O.kq_dequant(O.GGML_Q6_K, q, 8)
+    b = q.reshape(-1, 210).astype(np.int64)
+    e = np.arange(256)
+    n, r = e // 128, e % 128
+    part, l = r // 32, r % 32
+    bad_shift = 2 * np.array([0, 2, 1, 3])[part]
+    q6 = ((b[:, 64 * n + l + 32 * (part % 2)] >> (4 * (part // 2))) & 0xF) | \
+        (((b[:, 128 + 32 * n + l] >> bad_shift) & 3) << 4)
+    sc = b[:, 192 + 8 * n + l // 16 + 2 * part]
+    sc = np.where(sc >= 128, sc - 256, sc)
+    d = q.reshape(-1, 210)[:, 208:210].copy().view(np.float16).astype(np.float64)
+    assert not np.array_equal((d * sc * (q6 - 32)).astype(np.float32).reshape(-1), w)
+
+
+def test_q5k_with_zero_high_bits_is_q4k_and_high_bit_adds_sixteen():
+    """Q5_K = Q4_K's header and nibbles plus one high bit per weight: with qh = 0
+    it decodes exactly as the (pinned) Q4_K oracle, and with qh = 0xFF every
+    weight is RN_f32(d*sc*(q+16) - dmin*m)."""
+    q4 = O.gen_q4k_weights(79, 64).reshape(-1, 144)
+    q5 = np.zeros((64, 176), np.uint8)
+    q5[:, :16] = q4[:, :16]
+    q5[:, 48:] = q4[:, 16:]
+    w4 = O.q4k_dequant(q4.reshape(-1), 64)
+    assert np.array_equal(O.kq_dequant(O.GGML_Q5_K, q5, 64).view(np.uint32), w4.view(np.uint32))
+    q5[:, 16:48] = 0xFF
+    w5 = O.kq_dequant(O.GGML_Q5_K, q5, 64).reshape(64, 256)
+    for sb in range(3):
+        d = float(q4[sb, 0:2].copy().view(np.float16)[0])
+        dmin = float(q4[sb, 2:4].copy().view(np.float16)[0])
+        for e in (0, 31, 32, 100, 255):
+            j, hi, l = e // 64, (e % 64) // 32, e % 32
+            sc, m = N.scale_min_k4(q4[sb, 4:16], 2 * j + hi)
+            nib = (int(q4[sb, 16 + 32 * j + l]) >> (4 * hi)) & 0xF
+            exact = Fraction(d) * sc * (nib + 16) - Fraction(dmin) * m
+            assert w5[sb, e] == np.float32(float(exact)), (sb, e)
+
+
+def test_q5k_high_bit_sources():
+    for l, j, hi in [(0, 0, 0), (5, 0, 1), (31, 3, 1), (17, 2, 0)]:
+        b = np.zeros(176, np.uint8)
+        b[0:2] = np.array([1.0], np.float16).view(np.uint8)
+        b[4:8] = 1  # sc = 1 for sub-blocks 0..3
+        b[12:16] = 1  # low nibble of sc[4..7] = 1, m[4..7] = 0
+        b[16 + l] = np.uint8(1 << (2 * j + hi))
+        w = O.kq_dequant(O.GGML_Q5_K, b, 1)
+        assert np.flatnonzero(w).tolist() == [64 * j + 32 * hi + l] and w.max() == 16.0
+
+
+@pytest.mark.parametrize("kind", [O.GGML_Q5_K, O.GGML_Q6_K])
+def test_kq_dot_is_sequential_f32_in_element_order(kind):
+    q = O.gen_kq_weights(kind, 80, 2)
+    x = O.gen_normal_f32(81, 512)
+    w = O.kq_dequant(kind, q, 2)
+    s = np.float32(0)
+    for i in range(512):
+        s = np.float32(s + np.float32(w[i] * x[i]))
+    y = O.kq_matvec(kind, q, x, 1, 2, threads=1)
+    assert y[0].view(np.uint32) == s.view(np.uint32)
+    yf, ad = O.kq_matvec_f64(kind, q, x, 1, 2)
+    exact = sum(Fraction(float(a)) * Fraction(float(b)) for a, b in zip(w, x))
+    assert abs(yf[0] - float(exact)) <= 1e-12 * ad[0]
+
+
+@pytest.mark.parametrize("kind", [O.GGML_Q5_K, O.GGML_Q6_K])
+def test_kq_matvec_threads_bit_identical(kind):
+    rows, sb = 37, 3
+    q = O.gen_kq_weights(kind, 82, rows * sb)
+    x = O.gen_normal_f32(83, sb * 256)
+    a = O.kq_matvec(kind, q, x, rows, sb, threads=1)
+    b = O.kq_matvec(kind, q, x, rows, sb, threads=5)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
