@@ -5,6 +5,7 @@ The package directory name contains a hyphen, so it is loaded by path; see
 into libaxh.so (hand-written HIP kernels + C ABI runtime).
 """
 from . import axh  # noqa: F401
+from . import gguf  # noqa: F401
 from .axh import (  # noqa: F401
     BindingPlan,
     DeviceBuffer,
@@ -22,6 +23,9 @@ from .axh import (  # noqa: F401
     q4k_matmul_kernel_name,
     q4k_gate_up_kernel_name,
     q4k_matvec_kernel_name,
+    q5k_matvec_kernel_name,
+    q6k_matvec_kernel_name,
+    ggml_type_size,
     q4_0_matvec_kernel_name,
     load_library,
     validate_request,
@@ -45,6 +49,10 @@ __all__ = [
     "q4k_matmul_kernel_name",
     "q4k_gate_up_kernel_name",
     "q4k_matvec_kernel_name",
+    "q5k_matvec_kernel_name",
+    "q6k_matvec_kernel_name",
+    "ggml_type_size",
+    "gguf",
     "q4_0_matvec_kernel_name",
     "load_library",
     "validate_request",

@@ -101,6 +101,18 @@ class _MatmulVariant(ctypes.Structure):
                 ("col_tiles", ctypes.c_uint32), ("prefetch", ctypes.c_uint32)]
 
 
+class _GgufTensorInfo(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("type", ctypes.c_uint32), ("n_dims", ctypes.c_uint32),
+                ("ne", ctypes.c_uint64 * 4), ("offset", ctypes.c_uint64),
+                ("nbytes", ctypes.c_uint64)]
+
+
+class _GgufKvInfo(ctypes.Structure):
+    _fields_ = [("key", ctypes.c_char_p), ("type", ctypes.c_uint32),
+                ("item_type", ctypes.c_uint32), ("count", ctypes.c_uint64),
+                ("value", ctypes.c_void_p)]
+
+
 def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
     """Load libaxh.so (raises ImportError if it has not been built)."""
     global _lib
@@ -154,6 +166,31 @@ def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
         "axh_q4k_matvec_kernel_name": (st, [u32, u32, c.POINTER(_Variant), c.c_char_p, sz]),
         "axh_q4_0_matvec_kernel_name": (st, [u32, u32, c.POINTER(_Variant), c.c_char_p, sz]),
         "axh_q4k_gate_up": (st, [vp, vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
+        "axh_q5k_matvec": (st, [vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
+        "axh_q6k_matvec": (st, [vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
+        "axh_q5k_matvec_kernel_name": (st, [u32, u32, c.POINTER(_Variant), c.c_char_p, sz]),
+        "axh_q6k_matvec_kernel_name": (st, [u32, u32, c.POINTER(_Variant), c.c_char_p, sz]),
+        "axh_q5k_matvec_variant_count": (u32, []),
+        "axh_q5k_matvec_variant_at": (st, [u32, c.POINTER(_Variant)]),
+        "axh_q6k_matvec_variant_count": (u32, []),
+        "axh_q6k_matvec_variant_at": (st, [u32, c.POINTER(_Variant)]),
+        "axh_matvec_ggml": (st, [vp, u32, vp, vp, vp, u32, u64, vp]),
+        "axh_q5k_dequant": (st, [vp, vp, vp, u64, vp]),
+        "axh_q6k_dequant": (st, [vp, vp, vp, u64, vp]),
+        "axh_ggml_type_size": (st, [u32, c.POINTER(u32), c.POINTER(u32)]),
+        "axh_gguf_open": (st, [c.c_char_p, c.POINTER(vp)]),
+        "axh_gguf_close": (None, [vp]),
+        "axh_gguf_version": (u32, [vp]),
+        "axh_gguf_alignment": (u32, [vp]),
+        "axh_gguf_data_offset": (u64, [vp]),
+        "axh_gguf_tensor_count": (u64, [vp]),
+        "axh_gguf_kv_count": (u64, [vp]),
+        "axh_gguf_tensor_at": (st, [vp, u64, c.POINTER(_GgufTensorInfo)]),
+        "axh_gguf_find_tensor": (st, [vp, c.c_char_p, c.POINTER(u64)]),
+        "axh_gguf_tensor_data": (vp, [vp, u64]),
+        "axh_gguf_upload_tensor": (st, [vp, vp, u64, vp, u64]),
+        "axh_gguf_kv_at": (st, [vp, u64, c.POINTER(_GgufKvInfo)]),
+        "axh_gguf_find_kv": (st, [vp, c.c_char_p, c.POINTER(u64)]),
         "axh_q4k_gate_up_kernel_name": (st, [u32, u32, c.POINTER(_Variant), c.c_char_p, sz]),
         "axh_q4k_gate_up_variant_count": (u32, []),
         "axh_q4k_gate_up_variant_at": (st, [u32, c.POINTER(_Variant)]),
@@ -284,11 +321,39 @@ def q4k_gate_up_kernel_name(n_rows: int, sb_per_row: int,
     return buf.value.decode()
 
 
-def compiled_variants(kind: str = "q4k") -> list[Variant]:
-    """Compiled hole assignments of the "q4k" or "q4_0" matvec, or of the
-    fused "gate_up" kernel."""
+def _kernel_name(fn: str, n_rows: int, units: int, variant: Optional[Variant]) -> str:
     lib = load_library()
-    if kind not in ("q4k", "q4_0", "gate_up"):
+    v = variant._c() if variant else None
+    buf = ctypes.create_string_buffer(64)
+    _check(getattr(lib, fn)(n_rows, units, ctypes.byref(v) if v else None, buf, 64))
+    return buf.value.decode()
+
+
+def q5k_matvec_kernel_name(n_rows: int, sb_per_row: int,
+                           variant: Optional[Variant] = None) -> str:
+    """Entry point axh_q5k_matvec launches for this shape and variant."""
+    return _kernel_name("axh_q5k_matvec_kernel_name", n_rows, sb_per_row, variant)
+
+
+def q6k_matvec_kernel_name(n_rows: int, sb_per_row: int,
+                           variant: Optional[Variant] = None) -> str:
+    """Entry point axh_q6k_matvec launches for this shape and variant."""
+    return _kernel_name("axh_q6k_matvec_kernel_name", n_rows, sb_per_row, variant)
+
+
+def ggml_type_size(ggml_type: int) -> tuple[int, int]:
+    """(elements, bytes) per block of a ggml type."""
+    lib = load_library()
+    e, b = ctypes.c_uint32(), ctypes.c_uint32()
+    _check(lib.axh_ggml_type_size(ggml_type, ctypes.byref(e), ctypes.byref(b)))
+    return e.value, b.value
+
+
+def compiled_variants(kind: str = "q4k") -> list[Variant]:
+    """Compiled hole assignments of the "q4k", "q4_0", "q5k" or "q6k" matvec,
+    or of the fused "gate_up" kernel."""
+    lib = load_library()
+    if kind not in ("q4k", "q4_0", "q5k", "q6k", "gate_up"):
         raise ValueError(f"unknown kernel family {kind!r}")
     count = getattr(lib, f"axh_{kind}_matvec_variant_count" if kind != "gate_up"
                     else "axh_q4k_gate_up_variant_count")
@@ -645,6 +710,32 @@ class HipContext:
         v = variant._c() if variant else None
         _check(self._lib.axh_q4k_gate_up(self._raw, _ptr(q_gate), _ptr(q_up), _ptr(x), _ptr(h),
                                          n_rows, sb_per_row, ctypes.byref(v) if v else None,
+                                         _stream(stream)))
+
+    def q5k_matvec(self, q, x, y, n_rows: int, sb_per_row: int,
+                   variant: Optional[Variant] = None, stream=None) -> None:
+        v = variant._c() if variant else None
+        _check(self._lib.axh_q5k_matvec(self._raw, _ptr(q), _ptr(x), _ptr(y), n_rows, sb_per_row,
+                                        ctypes.byref(v) if v else None, _stream(stream)))
+
+    def q6k_matvec(self, q, x, y, n_rows: int, sb_per_row: int,
+                   variant: Optional[Variant] = None, stream=None) -> None:
+        v = variant._c() if variant else None
+        _check(self._lib.axh_q6k_matvec(self._raw, _ptr(q), _ptr(x), _ptr(y), n_rows, sb_per_row,
+                                        ctypes.byref(v) if v else None, _stream(stream)))
+
+    def matvec_ggml(self, ggml_type: int, q, x, y, n_rows: int, n_cols: int,
+                    stream=None) -> None:
+        """y = W x for a row-major ggml tensor (Q4_0, Q4_K, Q5_K, Q6_K)."""
+        _check(self._lib.axh_matvec_ggml(self._raw, ggml_type, _ptr(q), _ptr(x), _ptr(y), n_rows,
+                                         n_cols, _stream(stream)))
+
+    def q5k_dequant(self, q, w, n_superblocks: int, stream=None) -> None:
+        _check(self._lib.axh_q5k_dequant(self._raw, _ptr(q), _ptr(w), n_superblocks,
+                                         _stream(stream)))
+
+    def q6k_dequant(self, q, w, n_superblocks: int, stream=None) -> None:
+        _check(self._lib.axh_q6k_dequant(self._raw, _ptr(q), _ptr(w), n_superblocks,
                                          _stream(stream)))
 
     def q4_0_matvec(self, q, x, y, n_rows: int, blocks_per_row: int,

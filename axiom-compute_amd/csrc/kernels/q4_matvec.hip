@@ -350,31 +350,64 @@ __device__ __forceinline__ void q4k_flat_load_x(__amdgpu_buffer_rsrc_t xr, uint3
   for (int t = 0; t < 8; ++t) v[t] = buf_loadf4(xr, si * 128u + 16u * (uint32_t)t);
 }
 
-template <int RPW, int PF>
+// kQ5: Q5_K superblocks (the qh runs are loaded too).
+template <int RPW, int PF, bool kQ5 = false>
 struct Q4kFlatBuf {
   uint4 h[PF][RPW], a[PF][RPW], b[PF][RPW];
+  uint4 q0[kQ5 ? PF : 1][kQ5 ? RPW : 1], q1[kQ5 ? PF : 1][kQ5 ? RPW : 1];
 };
+
+// Q5_K (ggml k-quant, 176 bytes; no reference counterpart): Q4_K's header
+// and scale field, then qh[32] @16 and qs[128] @48.  Weight 64c + l (low
+// nibble of qs[32c + l]) gains 16 * bit 2c of qh[l], weight 64c + 32 + l
+// (high nibble) gains 16 * bit 2c+1.  Sub-block sums and scales are Q4_K's.
+constexpr uint32_t kQ5kSbBytes = 176;
+
+// Q4_K dword step with the fifth bits: the low-nibble value q + 16b keeps
+// its f16-subnormal encoding with b in mantissa bit 4 (16 * 2^-24), the
+// high-nibble value with b in bit 8 (16 * 2^-20).  qhs = qh dword >> 2c.
+__device__ __forceinline__ void q5k_dword(uint32_t w, uint32_t qhs, float4 xl, float4 xh,
+                                          float &alo, float &ahi) {
+  const uint32_t w8 = w >> 8, q8 = qhs >> 8;
+  const uint32_t a = (w & 0x000F000Fu) | ((qhs & 0x00010001u) << 4);
+  const uint32_t b = (w8 & 0x000F000Fu) | ((q8 & 0x00010001u) << 4);
+  const uint32_t ch = (w & 0x00F000F0u) | ((qhs & 0x00020002u) << 7);
+  const uint32_t dh = (w8 & 0x00F000F0u) | ((q8 & 0x00020002u) << 7);
+  alo = __builtin_fmaf(lo_half_f16(a), xl.x, alo);
+  alo = __builtin_fmaf(lo_half_f16(b), xl.y, alo);
+  alo = __builtin_fmaf(hi_half_f16(a), xl.z, alo);
+  alo = __builtin_fmaf(hi_half_f16(b), xl.w, alo);
+  ahi = __builtin_fmaf(lo_half_f16(ch), xh.x, ahi);
+  ahi = __builtin_fmaf(lo_half_f16(dh), xh.y, ahi);
+  ahi = __builtin_fmaf(hi_half_f16(ch), xh.z, ahi);
+  ahi = __builtin_fmaf(hi_half_f16(dh), xh.w, ahi);
+}
 
 // Loads of one iteration for the RPW rows of `bundle`.  Rows past the matrix
 // read zeros (buffer range check); superblocks past the row are never used.
 // kDual (fused gate/up): a bundle is RPW/2 output rows, slots r < RPW/2 read
 // row bundle*RPW/2 + r of the first matrix and slots r >= RPW/2 the same row
 // of the second.
-template <int RPW, int PF, bool kNT, bool kDual>
-__device__ __forceinline__ void q4k_flat_load(Q4kFlatBuf<RPW, PF> &B, int p,
+template <int RPW, int PF, bool kNT, bool kDual, bool kQ5>
+__device__ __forceinline__ void q4k_flat_load(Q4kFlatBuf<RPW, PF, kQ5> &B, int p,
                                               __amdgpu_buffer_rsrc_t qr,
                                               __amdgpu_buffer_rsrc_t qr2, uint32_t row_bytes,
                                               uint32_t bundle, uint32_t it, uint32_t s,
                                               uint32_t c) {
   constexpr int kRb = kDual ? RPW / 2 : RPW;
-  const uint32_t sb_off = (it * 8u + s) * (uint32_t)kQ4kSbBytes;
+  constexpr uint32_t kQs = kQ5 ? 48u : 16u; // offset of qs in the superblock
+  const uint32_t sb_off = (it * 8u + s) * (kQ5 ? kQ5kSbBytes : (uint32_t)kQ4kSbBytes);
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
     const __amdgpu_buffer_rsrc_t src = (kDual && r >= kRb) ? qr2 : qr;
     const uint32_t off = (bundle * kRb + (uint32_t)(r % kRb)) * row_bytes + sb_off;
     B.h[p][r] = buf_load16<kNT>(src, off);
-    B.a[p][r] = buf_load16<kNT>(src, off + 16u + 32u * c);
-    B.b[p][r] = buf_load16<kNT>(src, off + 32u + 32u * c);
+    if constexpr (kQ5) {
+      B.q0[p][r] = buf_load16<kNT>(src, off + 16u);
+      B.q1[p][r] = buf_load16<kNT>(src, off + 32u);
+    }
+    B.a[p][r] = buf_load16<kNT>(src, off + kQs + 32u * c);
+    B.b[p][r] = buf_load16<kNT>(src, off + kQs + 16u + 32u * c);
   }
 }
 
@@ -384,8 +417,8 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 }
 
 // kDual: y[r] = silu(W1[r].x) * (W2[r].x) for q = W1, q2 = W2 (same shape);
-// otherwise y = W1 x and q2 is unused.
-template <int RPW, int NW, int PF, bool kNT, int XP, bool kDual = false>
+// otherwise y = W1 x and q2 is unused.  kQ5: Q5_K superblocks instead of Q4_K.
+template <int RPW, int NW, int PF, bool kNT, int XP, bool kDual = false, bool kQ5 = false>
 __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
                                                 const uint8_t *__restrict__ q2,
                                                 const float *__restrict__ x,
@@ -393,6 +426,7 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
                                                 uint32_t nsb, float *lds) {
   constexpr int kRb = kDual ? RPW / 2 : RPW; // output rows per bundle
   static_assert(!kDual || RPW % 2 == 0, "the fused kernel pairs gate and up rows");
+  static_assert(!(kDual && kQ5), "the fused gate/up kernel reads Q4_K");
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   // wave index as a scalar: every loop bound below is then wave-uniform
@@ -410,7 +444,7 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
   const uint32_t n_it = (nsb + 7u) >> 3;
   const uint32_t total = (n_my * n_it + (PF - 1)) / PF * PF;
   // The host guarantees n_rows * row_bytes < 2^32 for this kernel.
-  const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
+  const uint32_t row_bytes = nsb * (kQ5 ? kQ5kSbBytes : (uint32_t)kQ4kSbBytes);
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(q, n_rows * row_bytes);
   const __amdgpu_buffer_rsrc_t qr2 = kDual ? make_rsrc(q2, n_rows * row_bytes) : qr;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, nsb * 1024u);
@@ -437,12 +471,12 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
 
-  Q4kFlatBuf<RPW, PF> B;
+  Q4kFlatBuf<RPW, PF, kQ5> B;
   uint32_t l_pi = 0, l_it = 0; // load cursor: pair index (of this wave) and iteration
 #pragma unroll
   for (int p = 0; p < PF; ++p) {
     const uint32_t bundle = 2u * (W + l_pi * total_waves) + half;
-    q4k_flat_load<RPW, PF, kNT, kDual>(B, p, qr, qr2, row_bytes, bundle, l_it, s, c);
+    q4k_flat_load<RPW, PF, kNT, kDual, kQ5>(B, p, qr, qr2, row_bytes, bundle, l_it, s, c);
     if (++l_it == n_it) { l_it = 0; ++l_pi; }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -474,14 +508,27 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
           uint32_t scp, mp;
           q4k_scale_min_pair(hd.y, hd.z, hd.w, c, &scp, &mp);
           float alo = 0.0f, ahi = 0.0f;
-          q4k_dword(B.a[p][r].x, xl[0], xh[0], alo, ahi);
-          q4k_dword(B.a[p][r].y, xl[1], xh[1], alo, ahi);
-          q4k_dword(B.a[p][r].z, xl[2], xh[2], alo, ahi);
-          q4k_dword(B.a[p][r].w, xl[3], xh[3], alo, ahi);
-          q4k_dword(B.b[p][r].x, xl[4], xh[4], alo, ahi);
-          q4k_dword(B.b[p][r].y, xl[5], xh[5], alo, ahi);
-          q4k_dword(B.b[p][r].z, xl[6], xh[6], alo, ahi);
-          q4k_dword(B.b[p][r].w, xl[7], xh[7], alo, ahi);
+          if constexpr (kQ5) {
+            const uint4 h0 = B.q0[p][r], h1 = B.q1[p][r];
+            const uint32_t sh = 2u * c;
+            q5k_dword(B.a[p][r].x, h0.x >> sh, xl[0], xh[0], alo, ahi);
+            q5k_dword(B.a[p][r].y, h0.y >> sh, xl[1], xh[1], alo, ahi);
+            q5k_dword(B.a[p][r].z, h0.z >> sh, xl[2], xh[2], alo, ahi);
+            q5k_dword(B.a[p][r].w, h0.w >> sh, xl[3], xh[3], alo, ahi);
+            q5k_dword(B.b[p][r].x, h1.x >> sh, xl[4], xh[4], alo, ahi);
+            q5k_dword(B.b[p][r].y, h1.y >> sh, xl[5], xh[5], alo, ahi);
+            q5k_dword(B.b[p][r].z, h1.z >> sh, xl[6], xh[6], alo, ahi);
+            q5k_dword(B.b[p][r].w, h1.w >> sh, xl[7], xh[7], alo, ahi);
+          } else {
+            q4k_dword(B.a[p][r].x, xl[0], xh[0], alo, ahi);
+            q4k_dword(B.a[p][r].y, xl[1], xh[1], alo, ahi);
+            q4k_dword(B.a[p][r].z, xl[2], xh[2], alo, ahi);
+            q4k_dword(B.a[p][r].w, xl[3], xh[3], alo, ahi);
+            q4k_dword(B.b[p][r].x, xl[4], xh[4], alo, ahi);
+            q4k_dword(B.b[p][r].y, xl[5], xh[5], alo, ahi);
+            q4k_dword(B.b[p][r].z, xl[6], xh[6], alo, ahi);
+            q4k_dword(B.b[p][r].w, xl[7], xh[7], alo, ahi);
+          }
           const float dot = __builtin_fmaf((float)(scp & 0xFFu), alo, (float)(scp >> 8) * ahi);
           const float mins = __builtin_fmaf((float)(mp & 0xFFu), sub.x, (float)(mp >> 8) * sub.y);
           acc[r] = __builtin_fmaf(f16_to_f32(hd.x & 0xFFFFu), dot,
@@ -491,7 +538,7 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
       // refill this slot PF iterations ahead (unconditional)
       {
         const uint32_t bundle = 2u * (W + l_pi * total_waves) + half;
-        q4k_flat_load<RPW, PF, kNT, kDual>(B, p, qr, qr2, row_bytes, bundle, l_it, s, c);
+        q4k_flat_load<RPW, PF, kNT, kDual, kQ5>(B, p, qr, qr2, row_bytes, bundle, l_it, s, c);
         if (++l_it == n_it) { l_it = 0; ++l_pi; }
       }
       if (++c_it == n_it) { // a bundle pair is complete: reduce and store
@@ -549,6 +596,283 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
     q4k_matvec_flat<RPW, NW, PF, NT != 0, 2>(q, q, x, y, a.n_rows, a.units_per_row,             \
                                                axh_lds_dyn);                                     \
   }
+
+// ===========================================================================
+// Q6_K matvec (ggml k-quant, 210-byte superblocks; no reference counterpart).
+// Superblock: ql[128] @0, qh[64] @128, int8 scales[16] @192, f16 d @208.
+// Weight 128n + 32p + l (half n, part p = 0..3, l = 0..31) has the 6-bit
+// value q = nibble | (2 bits of qh[32n + l] at 2p) << 4, the nibble being the
+// low (p = 0, 1) or high (p = 2, 3) half of ql[64n + l + 32(p & 1)], and
+// w = d * scales[8n + 2p + l/16] * (q - 32) (exact in f32).
+//
+// Same persistent skeleton as the Q4_K flat kernel (pairs of RPW-row
+// bundles per wave, 16 superblocks per wave iteration, 4 lanes each, loads PF
+// iterations ahead).  Lane c of a superblock takes half n = c/2 and
+// l in [16(c&1), 16(c&1) + 16): 64 weights, 4 parts of 16.  Its bytes are
+// three 16-byte runs (ql for parts 0/2, ql for parts 1/3, qh), the 16 scale
+// bytes and d.  Superblocks start at 2-byte boundaries (210 = 2 mod 4), so a
+// 16-byte run is read as 5 aligned dwords and realigned with v_alignbit;
+// every aligned dword read lies inside the superblock or its predecessor.
+//
+// LDS: xs[sb*272 + 64p + 16i + 4c + e] = x[sb*256 + 128n + 32p + 16h + 4i + e] * 2^24
+//      (c = 2n + h), and ss[sb*16 + 4c + p] = sum of those 16 x (unscaled), so
+//      sum_l (q_l - 32) x_l = sum_l q_l x_l - 32 * ss.
+// ===========================================================================
+constexpr uint32_t kQ6kSbBytes = 210;
+constexpr uint32_t kQ6kSbFloats = 272;
+
+__device__ __forceinline__ void q6k_stage(float *xs, float *ss, uint32_t si,
+                                          const float4 (&v)[8]) {
+  const uint32_t sb = si >> 3, j = si & 7u, n = j >> 2, p = j & 3u;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t c = 2u * n + (uint32_t)h;
+    float *dst = xs + sb * kQ6kSbFloats + 64u * p + 4u * c;
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 a = v[4 * h + i];
+      sum += (a.x + a.y) + (a.z + a.w);
+      *reinterpret_cast<float4 *>(dst + 16u * (uint32_t)i) =
+          make_float4(a.x * 16777216.0f, a.y * 16777216.0f, a.z * 16777216.0f,
+                      a.w * 16777216.0f);
+    }
+    ss[sb * 16u + 4u * c + p] = sum;
+  }
+}
+
+// 16 bytes at byte offset `off` (2-byte aligned): raw aligned dwords.
+struct Q6kRun {
+  uint4 a;   // dwords at off & ~3
+  uint32_t e; // the dword after them
+};
+
+__device__ __forceinline__ Q6kRun q6k_load_run(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const uint32_t al = off & ~3u;
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)al, 0, 0);
+  Q6kRun out;
+  out.a = make_uint4(v.x, v.y, v.z, v.w);
+  out.e = __builtin_amdgcn_raw_buffer_load_b32(r, (int)(al + 16u), 0, 0);
+  return out;
+}
+
+// The 16 bytes of a run as 4 dwords (sh = 8 * (off & 3), 0 or 16).
+__device__ __forceinline__ uint4 q6k_align(const Q6kRun &r, uint32_t sh) {
+  return make_uint4(__builtin_amdgcn_alignbit(r.a.y, r.a.x, sh),
+                    __builtin_amdgcn_alignbit(r.a.z, r.a.y, sh),
+                    __builtin_amdgcn_alignbit(r.a.w, r.a.z, sh),
+                    __builtin_amdgcn_alignbit(r.e, r.a.w, sh));
+}
+
+template <int RPW, int PF>
+struct Q6kFlatBuf {
+  Q6kRun lo[PF][RPW], hi[PF][RPW], qh[PF][RPW], sc[PF][RPW];
+  uint32_t d[PF][RPW];
+};
+
+template <int RPW, int PF>
+__device__ __forceinline__ void q6k_flat_load(Q6kFlatBuf<RPW, PF> &B, int p,
+                                              __amdgpu_buffer_rsrc_t qr, uint32_t row_bytes,
+                                              uint32_t bundle, uint32_t it, uint32_t s,
+                                              uint32_t c) {
+  const uint32_t n = c >> 1, h = c & 1u;
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const uint32_t o = (bundle * RPW + (uint32_t)r) * row_bytes + (it * 8u + s) * kQ6kSbBytes;
+    B.lo[p][r] = q6k_load_run(qr, o + 64u * n + 16u * h);
+    B.hi[p][r] = q6k_load_run(qr, o + 64u * n + 32u + 16u * h);
+    B.qh[p][r] = q6k_load_run(qr, o + 128u + 32u * n + 16u * h);
+    // scales: when o is 4-byte aligned the 16 bytes need no fifth dword; read
+    // one inside the run instead of the dword past the superblock
+    const uint32_t sal = (o + 192u) & ~3u;
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)sal, 0, 0);
+    B.sc[p][r].a = make_uint4(v.x, v.y, v.z, v.w);
+    B.sc[p][r].e = __builtin_amdgcn_raw_buffer_load_b32(qr, (int)(sal + ((o & 3u) ? 16u : 12u)),
+                                                        0, 0);
+    B.d[p][r] = __builtin_amdgcn_raw_buffer_load_b16(qr, (int)(o + 208u), 0, 0);
+  }
+}
+
+// Four bytes of 6-bit values against four x (pre-scaled by 2^24).
+__device__ __forceinline__ float q6k_bytes(uint32_t v, float4 x, float acc) {
+  const uint32_t a = v & 0x00FF00FFu, b = (v >> 8) & 0x00FF00FFu;
+  acc = __builtin_fmaf(lo_half_f16(a), x.x, acc);
+  acc = __builtin_fmaf(lo_half_f16(b), x.y, acc);
+  acc = __builtin_fmaf(hi_half_f16(a), x.z, acc);
+  acc = __builtin_fmaf(hi_half_f16(b), x.w, acc);
+  return acc;
+}
+
+template <int RPW, int NW, int PF, int XP>
+__device__ __forceinline__ void q6k_matvec_flat(const uint8_t *__restrict__ q,
+                                                const float *__restrict__ x,
+                                                float *__restrict__ y, uint32_t n_rows,
+                                                uint32_t nsb, float *lds) {
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t G = lane >> 2, half = G >> 3, s = G & 7u, c = lane & 3u;
+  const uint32_t total_waves = gridDim.x * NW;
+  const uint32_t W = blockIdx.x * NW + wave;
+  const uint32_t n_bundles = (n_rows + RPW - 1) / RPW;
+  const uint32_t n_pairs = (n_bundles + 1u) >> 1;
+  if (nsb == 0) {
+    for (uint32_t r = W * 64u + lane; r < n_rows; r += total_waves * 64u) y[r] = 0.0f;
+    return;
+  }
+  const uint32_t n_my = W < n_pairs ? (n_pairs - 1u - W) / total_waves + 1u : 0u;
+  const uint32_t n_it = (nsb + 7u) >> 3;
+  const uint32_t total = (n_my * n_it + (PF - 1)) / PF * PF;
+  // The host guarantees n_rows * row_bytes < 2^32 for this kernel.
+  const uint32_t row_bytes = nsb * kQ6kSbBytes;
+  const __amdgpu_buffer_rsrc_t qr = make_rsrc(q, n_rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, nsb * 1024u);
+  float *xs = lds;
+  float *ss = lds + nsb * kQ6kSbFloats;
+
+  // Prologue as in the Q4_K flat kernel: x first, then (once x has arrived)
+  // the weight prefetch, then the LDS writes.
+  const uint32_t nsub = nsb * 8u;
+  uint32_t my_sub[XP];
+  float4 xv[XP][8];
+#pragma unroll
+  for (int k = 0; k < XP; ++k) {
+    my_sub[k] = min(tid + (uint32_t)k * (NW * 64u), nsub - 1u);
+    q4k_flat_load_x(xr, my_sub[k], xv[k]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+
+  Q6kFlatBuf<RPW, PF> B;
+  uint32_t l_pi = 0, l_it = 0;
+#pragma unroll
+  for (int p = 0; p < PF; ++p) {
+    const uint32_t bundle = 2u * (W + l_pi * total_waves) + half;
+    q6k_flat_load<RPW, PF>(B, p, qr, row_bytes, bundle, l_it, s, c);
+    if (++l_it == n_it) { l_it = 0; ++l_pi; }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int k = 0; k < XP; ++k) q6k_stage(xs, ss, my_sub[k], xv[k]);
+  __syncthreads();
+
+  const uint32_t n = c >> 1, hsel = (c & 1u) * 8u; // scale byte of (n, h): 8n + 2p + h
+  float acc[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
+  uint32_t c_pi = 0, c_it = 0;
+  for (uint32_t j0 = 0; j0 < total; j0 += PF) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+      const uint32_t sb = c_it * 8u + s;
+      if (c_pi < n_my && sb < nsb) {
+        const float *xb = xs + sb * kQ6kSbFloats + 4u * c;
+        const float4 sums = *reinterpret_cast<const float4 *>(ss + sb * 16u + 4u * c);
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+          const uint32_t bundle = 2u * (W + c_pi * total_waves) + half;
+          const uint32_t o = (bundle * RPW + (uint32_t)r) * row_bytes + sb * kQ6kSbBytes;
+          const uint32_t sh = (o & 3u) * 8u;
+          const uint4 lo = q6k_align(B.lo[p][r], sh);
+          const uint4 hi = q6k_align(B.hi[p][r], sh);
+          const uint4 qh = q6k_align(B.qh[p][r], sh);
+          const uint4 sc = q6k_align(B.sc[p][r], sh);
+          const uint32_t lw[4] = {lo.x, lo.y, lo.z, lo.w};
+          const uint32_t hw[4] = {hi.x, hi.y, hi.z, hi.w};
+          const uint32_t qw[4] = {qh.x, qh.y, qh.z, qh.w};
+          float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t v0 = (lw[i] & 0x0F0F0F0Fu) | ((qw[i] << 4) & 0x30303030u);
+            const uint32_t v1 = (hw[i] & 0x0F0F0F0Fu) | ((qw[i] << 2) & 0x30303030u);
+            const uint32_t v2 = ((lw[i] >> 4) & 0x0F0F0F0Fu) | (qw[i] & 0x30303030u);
+            const uint32_t v3 = ((hw[i] >> 4) & 0x0F0F0F0Fu) | ((qw[i] >> 2) & 0x30303030u);
+            d0 = q6k_bytes(v0, *reinterpret_cast<const float4 *>(xb + 16u * i), d0);
+            d1 = q6k_bytes(v1, *reinterpret_cast<const float4 *>(xb + 64u + 16u * i), d1);
+            d2 = q6k_bytes(v2, *reinterpret_cast<const float4 *>(xb + 128u + 16u * i), d2);
+            d3 = q6k_bytes(v3, *reinterpret_cast<const float4 *>(xb + 192u + 16u * i), d3);
+          }
+          // scale bytes 8n + h + {0, 2} (dword 2n) and 8n + h + {4, 6} (dword 2n + 1)
+          const uint32_t s0 = n ? sc.z : sc.x, s1 = n ? sc.w : sc.y;
+          // int8 scales (the sign-extending byte extract; a bit-field builtin
+          // returning an unsigned type would turn -1 into 2^32 - 1 here)
+          const float c0 = (float)(int8_t)(s0 >> hsel);
+          const float c1 = (float)(int8_t)(s0 >> (hsel + 16u));
+          const float c2 = (float)(int8_t)(s1 >> hsel);
+          const float c3 = (float)(int8_t)(s1 >> (hsel + 16u));
+          float t = c0 * __builtin_fmaf(-32.0f, sums.x, d0);
+          t = __builtin_fmaf(c1, __builtin_fmaf(-32.0f, sums.y, d1), t);
+          t = __builtin_fmaf(c2, __builtin_fmaf(-32.0f, sums.z, d2), t);
+          t = __builtin_fmaf(c3, __builtin_fmaf(-32.0f, sums.w, d3), t);
+          acc[r] = __builtin_fmaf(f16_to_f32(B.d[p][r]), t, acc[r]);
+        }
+      }
+      {
+        const uint32_t bundle = 2u * (W + l_pi * total_waves) + half;
+        q6k_flat_load<RPW, PF>(B, p, qr, row_bytes, bundle, l_it, s, c);
+        if (++l_it == n_it) { l_it = 0; ++l_pi; }
+      }
+      if (++c_it == n_it) {
+        if (c_pi < n_my) {
+          const uint32_t bundle0 = 2u * (W + c_pi * total_waves);
+#pragma unroll
+          for (int r = 0; r < RPW; ++r) {
+            float v = acc[r];
+            v += dpp_mov<0xB1>(v);
+            v += dpp_mov<0x4E>(v);
+            v += dpp_mov<0x141>(v);
+            v += dpp_mov<0x140>(v);
+            const int vi = __builtin_bit_cast(int, v);
+            const float h0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 0)) +
+                             __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 16));
+            const float h1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 32)) +
+                             __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 48));
+            const uint32_t r0 = bundle0 * RPW + (uint32_t)r;
+            const uint32_t r1 = (bundle0 + 1u) * RPW + (uint32_t)r;
+            if (lane == 0 && r0 < n_rows) y[r0] = h0;
+            if (lane == 0 && r1 < n_rows) y[r1] = h1;
+            acc[r] = 0.0f;
+          }
+        }
+        c_it = 0;
+        ++c_pi;
+      }
+    }
+  }
+}
+
+#define AXH_Q6K_MATVEC_FLAT(RPW, NW, PF, XP)                                                     \
+  extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
+      axh_q6k_matvec_flat_r##RPW##_w##NW##_p##PF##_x##XP(const uint8_t *__restrict__ q,          \
+                                                         const float *__restrict__ x,            \
+                                                         float *__restrict__ y, RowsArgs a) {    \
+    extern __shared__ float axh_lds_dyn[];                                                       \
+    q6k_matvec_flat<RPW, NW, PF, XP>(q, x, y, a.n_rows, a.units_per_row, axh_lds_dyn);          \
+  }
+
+#define AXH_Q5K_MATVEC_FLAT(RPW, NW, PF, XP)                                                     \
+  extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
+      axh_q5k_matvec_flat_r##RPW##_w##NW##_p##PF##_x##XP(const uint8_t *__restrict__ q,          \
+                                                         const float *__restrict__ x,            \
+                                                         float *__restrict__ y, RowsArgs a) {    \
+    extern __shared__ float axh_lds_dyn[];                                                       \
+    q4k_matvec_flat<RPW, NW, PF, false, XP, false, true>(q, q, x, y, a.n_rows,                   \
+                                                         a.units_per_row, axh_lds_dyn);          \
+  }
+
+AXH_Q5K_MATVEC_FLAT(1, 4, 2, 1)
+AXH_Q5K_MATVEC_FLAT(1, 8, 2, 1)
+AXH_Q5K_MATVEC_FLAT(2, 4, 2, 1)
+AXH_Q5K_MATVEC_FLAT(1, 4, 2, 2)
+AXH_Q5K_MATVEC_FLAT(1, 8, 2, 2)
+
+AXH_Q6K_MATVEC_FLAT(1, 4, 2, 1)
+AXH_Q6K_MATVEC_FLAT(1, 8, 2, 1)
+AXH_Q6K_MATVEC_FLAT(1, 4, 4, 1)
+AXH_Q6K_MATVEC_FLAT(2, 4, 2, 1)
+AXH_Q6K_MATVEC_FLAT(1, 4, 2, 2)
+AXH_Q6K_MATVEC_FLAT(1, 8, 2, 2)
 
 // Fused SwiGLU gate/up projection: y[r] = silu(Wg[r].x) * (Wu[r].x), ROWS
 // output rows per bundle (2 * ROWS weight rows per lane group).
@@ -976,6 +1300,60 @@ extern "C" __global__ void __launch_bounds__(64)
 // ===========================================================================
 // Decode-only kernels (bit-exact checks of the dequantised weights)
 // ===========================================================================
+// Q5_K: one thread per (superblock, 16-byte qs slice), as Q4_K plus the
+// fifth bit from qh: fma(d*sc, q, -(dmin*m)) with d*sc, dmin*m and (d*sc)*q
+// exact in f32 (q <= 31), so the one rounding is the subtraction's.
+extern "C" __global__ void __launch_bounds__(256)
+    axh_q5k_dequant(const uint8_t *__restrict__ q, float *__restrict__ w, CountArgs a) {
+  const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t sb = gid >> 3, k = gid & 7u, c = k >> 1, h = k & 1u;
+  if (sb >= a.n_units) return;
+  const uint8_t *b = q + (size_t)sb * kQ5kSbBytes;
+  const uint4 hd = *reinterpret_cast<const uint4 *>(b);
+  const uint4 qv = *reinterpret_cast<const uint4 *>(b + 48u + 16u * k);
+  const uint4 hv = *reinterpret_cast<const uint4 *>(b + 16u + 16u * h);
+  uint32_t scp, mp;
+  q4k_scale_min_pair(hd.y, hd.z, hd.w, c, &scp, &mp);
+  const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
+  const float d1 = d * (float)(scp & 0xFFu), m1f = dmin * (float)(mp & 0xFFu);
+  const float d2 = d * (float)(scp >> 8), m2f = dmin * (float)(mp >> 8);
+  float *wl = w + (size_t)sb * kQ4kSbElems + 64u * c + 16u * h;
+  float *wh = wl + 32;
+  const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
+  const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    float lo[4], hi[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t byte = (qw[t] >> (8 * e)) & 0xFFu, bits = (hw[t] >> (8 * e + 2 * c)) & 3u;
+      lo[e] = __builtin_fmaf(d1, (float)((byte & 15u) + 16u * (bits & 1u)), -m1f);
+      hi[e] = __builtin_fmaf(d2, (float)((byte >> 4) + 16u * (bits >> 1)), -m2f);
+    }
+    *reinterpret_cast<float4 *>(wl + 4 * t) = make_float4(lo[0], lo[1], lo[2], lo[3]);
+    *reinterpret_cast<float4 *>(wh + 4 * t) = make_float4(hi[0], hi[1], hi[2], hi[3]);
+  }
+}
+
+// Q6_K: one thread per (superblock, half n, part p): 32 weights
+// d * sc * (q - 32), exact in f32.  Byte reads (superblocks are 2-byte aligned).
+extern "C" __global__ void __launch_bounds__(256)
+    axh_q6k_dequant(const uint8_t *__restrict__ q, float *__restrict__ w, CountArgs a) {
+  const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t sb = gid >> 3, n = (gid >> 2) & 1u, p = gid & 3u;
+  if (sb >= a.n_units) return;
+  const uint8_t *b = q + (size_t)sb * kQ6kSbBytes;
+  const float d = f16_to_f32((uint32_t)b[208] | ((uint32_t)b[209] << 8));
+  const float s0 = d * (float)(int8_t)b[192u + 8u * n + 2u * p];
+  const float s1 = d * (float)(int8_t)b[192u + 8u * n + 2u * p + 1u];
+  const uint8_t *ql = b + 64u * n + 32u * (p & 1u), *qh = b + 128u + 32u * n;
+  float *o = w + (size_t)sb * kQ4kSbElems + 128u * n + 32u * p;
+  for (uint32_t l = 0; l < 32; ++l) {
+    const uint32_t v = ((ql[l] >> (4u * (p >> 1))) & 15u) | (((qh[l] >> (2u * p)) & 3u) << 4);
+    o[l] = (l < 16 ? s0 : s1) * (float)((int)v - 32);
+  }
+}
+
 // Q4_K: one thread per (superblock, 16-byte qs slice).  Each value is
 // fma(d*sc, nibble, -(dmin*m)): d*sc, dmin*m and (d*sc)*nibble are exact in
 // f32, so the single rounding equals the reference's d1*lo - m1f.

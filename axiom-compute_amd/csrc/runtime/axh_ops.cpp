@@ -66,6 +66,15 @@ constexpr MatvecVariant kGateUpVariants[] = {
     {1, 4, 2, 2, 1}, {1, 4, 4, 2, 1}, {1, 8, 2, 2, 1}, {2, 4, 2, 2, 1},
     {2, 8, 2, 2, 1}, {1, 4, 2, 2, 2}, {1, 8, 2, 2, 2},
 };
+// axh_q5k_matvec_flat_r{rpw}_w{nw}_p{pf}_x{xp} and axh_q6k_... (ggml k-quants
+// next to Q4_K).  Keep in sync with AXH_Q5K_MATVEC_FLAT / AXH_Q6K_MATVEC_FLAT.
+constexpr MatvecVariant kQ5kVariants[] = {
+    {1, 4, 2, 2, 1}, {1, 8, 2, 2, 1}, {2, 4, 2, 2, 1}, {1, 4, 2, 2, 2}, {1, 8, 2, 2, 2},
+};
+constexpr MatvecVariant kQ6kVariants[] = {
+    {1, 4, 2, 2, 1}, {1, 8, 2, 2, 1}, {1, 4, 4, 2, 1}, {2, 4, 2, 2, 1},
+    {1, 4, 2, 2, 2}, {1, 8, 2, 2, 2},
+};
 // axh_q4_0_matvec_r{rpw}_w{nw} (prefetch and cache policy are not holes for Q4_0).
 constexpr MatvecVariant kQ4_0Variants[] = {
     {1, 1, 1, 2, 1}, {1, 4, 1, 2, 1}, {2, 4, 1, 2, 1}, {4, 4, 1, 2, 1}};
@@ -432,6 +441,140 @@ axh_status axh_q4k_gate_up(axh_context *ctx, const void *q_gate, const void *q_u
   return s == AXH_OK ? ok() : s;
 }
 
+// ---- Q5_K / Q6_K (persistent kernel only: a row's x must fit LDS) ----------
+struct KqFormat {
+  const char *prefix;            // kernel name prefix
+  const MatvecVariant *table;
+  size_t n;
+  uint32_t sb_bytes, lds_per_sb; // superblock bytes, LDS bytes per superblock of x
+};
+
+static const KqFormat kQ5kFormat{"axh_q5k_matvec_flat", kQ5kVariants,
+                                 sizeof(kQ5kVariants) / sizeof(kQ5kVariants[0]), 176u, 1120u};
+static const KqFormat kQ6kFormat{"axh_q6k_matvec_flat", kQ6kVariants,
+                                 sizeof(kQ6kVariants) / sizeof(kQ6kVariants[0]), 210u, 1152u};
+
+static MatvecVariant kq_default(uint32_t nsb) {
+  if (nsb * 8u <= 256u) return {1, 4, 2, 2, 1};
+  return {1, 8, 2, 2, 1};
+}
+
+static axh_status plan_kq(const KqFormat &f, uint32_t n_rows, uint32_t sb_per_row,
+                          const axh_q4_variant *variant, Q4kPlan *p) {
+  if (sb_per_row == 0 || sb_per_row > kQ4kFlatMaxSb)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "sb_per_row must be 1..128 for Q5_K / Q6_K");
+  if ((uint64_t)n_rows * sb_per_row * f.sb_bytes >= 0xFFFFFFFFull)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "Q5_K / Q6_K matrices must be below 4 GiB");
+  if (variant && variant->nontemporal == 1)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "no non-temporal Q5_K / Q6_K variant is compiled");
+  const MatvecVariant dflt = kq_default(sb_per_row);
+  const uint32_t want_nw =
+      variant && variant->waves_per_workgroup ? variant->waves_per_workgroup : dflt.nw;
+  const uint32_t min_xp = (sb_per_row * 8u + want_nw * 64u - 1u) / (want_nw * 64u);
+  const MatvecVariant *v = find_variant(f.table, f.n, variant, dflt, min_xp);
+  if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q5_K / Q6_K variant matches");
+  if (sb_per_row * 8u > v->xp * v->nw * 64u)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "row too long for this variant's x staging");
+  std::snprintf(p->name, sizeof(p->name), "%s_r%u_w%u_p%u_x%u", f.prefix, v->rpw, v->nw, v->pf,
+                v->xp);
+  p->nw = v->nw;
+  p->lds = sb_per_row * f.lds_per_sb;
+  p->flat = true;
+  const uint32_t bundles = (n_rows + v->rpw - 1) / v->rpw;
+  p->units = ((bundles + 1) / 2 + v->nw - 1) / v->nw;
+  p->args = RowsArgs{n_rows, sb_per_row, sb_per_row, 0};
+  return ok();
+}
+
+static axh_status kq_kernel_name(const KqFormat &f, uint32_t n_rows, uint32_t sb_per_row,
+                                 const axh_q4_variant *variant, char *buf, size_t cap) {
+  if (!buf || cap == 0) return fail(AXH_ERR_INVALID_ARGUMENT, "buf is NULL");
+  Q4kPlan p{};
+  axh_status s = plan_kq(f, n_rows, sb_per_row, variant, &p);
+  if (s != AXH_OK) return s;
+  if (std::strlen(p.name) + 1 > cap) return fail(AXH_ERR_INVALID_ARGUMENT, "buf too small");
+  std::memcpy(buf, p.name, std::strlen(p.name) + 1);
+  return ok();
+}
+
+static axh_status kq_matvec(const KqFormat &f, axh_context *ctx, const void *q, const float *x,
+                            float *y, uint32_t n_rows, uint32_t sb_per_row,
+                            const axh_q4_variant *variant, void *stream) {
+  if (!ctx) return fail(AXH_ERR_INVALID_ARGUMENT, "ctx is NULL");
+  if (n_rows == 0) return ok();
+  if (!device_ptr_ok(y) || !device_ptr_ok(q) || !device_ptr_ok(x))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q, x and y must be device pointers");
+  if (((uintptr_t)q & 15u) || ((uintptr_t)x & 15u))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q and x must be 16-byte aligned");
+  Q4kPlan p{};
+  axh_status s = plan_kq(f, n_rows, sb_per_row, variant, &p);
+  if (s != AXH_OK) return s;
+  if (p.lds > ctx->core->max_lds)
+    return fail(AXH_ERR_PIPELINE_LAYOUT, "LDS tile exceeds the device limit");
+  hipSetDevice(ctx->core->device);
+  axh_kernel *k = nullptr;
+  s = builtin_kernel(ctx, p.name, 3, sizeof(RowsArgs), p.nw * 64u, &k);
+  if (s != AXH_OK) return s;
+  uint32_t grid[3] = {p.units, 1, 1};
+  const uint32_t resident = occupancy(ctx, k, p.lds) * ctx->core->cu_count;
+  if (resident < grid[0]) grid[0] = resident;
+  void *bufs[3] = {const_cast<void *>(q), const_cast<float *>(x), y};
+  s = launch_raw(k, grid, bufs, 3, &p.args, sizeof(p.args), p.lds, pick_stream(ctx, stream));
+  return s == AXH_OK ? ok() : s;
+}
+
+axh_status axh_q5k_matvec(axh_context *ctx, const void *q, const float *x, float *y,
+                          uint32_t n_rows, uint32_t sb_per_row, const axh_q4_variant *variant,
+                          void *stream) {
+  return kq_matvec(kQ5kFormat, ctx, q, x, y, n_rows, sb_per_row, variant, stream);
+}
+
+axh_status axh_q6k_matvec(axh_context *ctx, const void *q, const float *x, float *y,
+                          uint32_t n_rows, uint32_t sb_per_row, const axh_q4_variant *variant,
+                          void *stream) {
+  return kq_matvec(kQ6kFormat, ctx, q, x, y, n_rows, sb_per_row, variant, stream);
+}
+
+axh_status axh_q5k_matvec_kernel_name(uint32_t n_rows, uint32_t sb_per_row,
+                                      const axh_q4_variant *variant, char *buf, size_t cap) {
+  return kq_kernel_name(kQ5kFormat, n_rows, sb_per_row, variant, buf, cap);
+}
+
+axh_status axh_q6k_matvec_kernel_name(uint32_t n_rows, uint32_t sb_per_row,
+                                      const axh_q4_variant *variant, char *buf, size_t cap) {
+  return kq_kernel_name(kQ6kFormat, n_rows, sb_per_row, variant, buf, cap);
+}
+
+uint32_t axh_q5k_matvec_variant_count(void) { return count_holes(kQ5kVariants, kQ5kFormat.n); }
+axh_status axh_q5k_matvec_variant_at(uint32_t i, axh_q4_variant *out) {
+  return holes_at(kQ5kVariants, kQ5kFormat.n, i, out);
+}
+uint32_t axh_q6k_matvec_variant_count(void) { return count_holes(kQ6kVariants, kQ6kFormat.n); }
+axh_status axh_q6k_matvec_variant_at(uint32_t i, axh_q4_variant *out) {
+  return holes_at(kQ6kVariants, kQ6kFormat.n, i, out);
+}
+
+axh_status axh_matvec_ggml(axh_context *ctx, uint32_t ggml_type, const void *q, const float *x,
+                           float *y, uint32_t n_rows, uint64_t n_cols, void *stream) {
+  const uint32_t block = ggml_type == AXH_GGML_Q4_0 ? 32u : 256u;
+  if (n_cols % block != 0)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "n_cols must be a whole number of blocks");
+  if (n_cols / block > 0xFFFFFFFFull) return fail(AXH_ERR_INVALID_ARGUMENT, "n_cols too large");
+  const uint32_t units = (uint32_t)(n_cols / block);
+  switch (ggml_type) {
+  case AXH_GGML_Q4_0:
+    return axh_q4_0_matvec(ctx, q, x, y, n_rows, units, nullptr, stream);
+  case AXH_GGML_Q4_K:
+    return axh_q4k_matvec(ctx, q, x, y, n_rows, units, nullptr, stream);
+  case AXH_GGML_Q5_K:
+    return axh_q5k_matvec(ctx, q, x, y, n_rows, units, nullptr, stream);
+  case AXH_GGML_Q6_K:
+    return axh_q6k_matvec(ctx, q, x, y, n_rows, units, nullptr, stream);
+  default:
+    return fail(AXH_ERR_INVALID_ARGUMENT, "unsupported ggml type for matvec");
+  }
+}
+
 static const MatvecVariant *pick_q4_0(uint32_t n_rows, uint32_t blocks_per_row,
                                       const axh_q4_variant *variant) {
   axh_q4_variant vv{};
@@ -619,6 +762,20 @@ static axh_status count_launch(axh_context *ctx, const char *name, const void *i
   hipSetDevice(ctx->core->device);
   s = launch_raw(k, grid, bufs, 2, &a, sizeof(a), 0, pick_stream(ctx, stream));
   return s == AXH_OK ? ok() : s;
+}
+
+axh_status axh_q5k_dequant(axh_context *ctx, const void *q, float *w, uint64_t n_sb, void *stream) {
+  if (n_sb > (1ull << 28)) return fail(AXH_ERR_INVALID_ARGUMENT, "too many superblocks");
+  if (((uintptr_t)q & 15u) || ((uintptr_t)w & 15u))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q and w must be 16-byte aligned");
+  return count_launch(ctx, "axh_q5k_dequant", q, w, n_sb * 8u, n_sb, stream);
+}
+
+axh_status axh_q6k_dequant(axh_context *ctx, const void *q, float *w, uint64_t n_sb, void *stream) {
+  if (n_sb > (1ull << 28)) return fail(AXH_ERR_INVALID_ARGUMENT, "too many superblocks");
+  if ((uintptr_t)q & 1u) return fail(AXH_ERR_INVALID_ARGUMENT, "q must be 2-byte aligned");
+  if ((uintptr_t)w & 3u) return fail(AXH_ERR_INVALID_ARGUMENT, "w must be 4-byte aligned");
+  return count_launch(ctx, "axh_q6k_dequant", q, w, n_sb * 8u, n_sb, stream);
 }
 
 axh_status axh_q4k_dequant(axh_context *ctx, const void *q, float *w, uint64_t n_sb, void *stream) {

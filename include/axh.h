@@ -194,6 +194,45 @@ axh_status axh_q4_0_matvec(axh_context *ctx, const void *q, const float *x, floa
                            const axh_q4_variant *variant, void *stream);
 axh_status axh_q4_0_matvec_kernel_name(uint32_t n_rows, uint32_t blocks_per_row,
                                        const axh_q4_variant *variant, char *buf, size_t cap);
+/* ---- ggml k-quants next to Q4_K, and matvec by ggml type ---------------------
+ * ggml tensor type ids as stored in GGUF files (ggml.h enum ggml_type). */
+enum {
+    AXH_GGML_F32 = 0, AXH_GGML_F16 = 1, AXH_GGML_Q4_0 = 2, AXH_GGML_Q4_1 = 3,
+    AXH_GGML_Q5_0 = 6, AXH_GGML_Q5_1 = 7, AXH_GGML_Q8_0 = 8, AXH_GGML_Q8_1 = 9,
+    AXH_GGML_Q2_K = 10, AXH_GGML_Q3_K = 11, AXH_GGML_Q4_K = 12, AXH_GGML_Q5_K = 13,
+    AXH_GGML_Q6_K = 14, AXH_GGML_Q8_K = 15, AXH_GGML_I8 = 24, AXH_GGML_I16 = 25,
+    AXH_GGML_I32 = 26, AXH_GGML_I64 = 27, AXH_GGML_F64 = 28, AXH_GGML_BF16 = 30
+};
+/* Elements and bytes per block of a ggml type (error for unsized types). */
+axh_status axh_ggml_type_size(uint32_t type, uint32_t *block_elems, uint32_t *block_bytes);
+/* y = W x for the ggml k-quants that real Q4_K_M / Q5_K_M checkpoints mix in:
+ * Q5_K (176-byte superblocks: d, dmin, the Q4_K scale field, qh[32], qs[128])
+ * and Q6_K (210-byte superblocks: ql[128], qh[64], int8 scales[16], d).  No
+ * counterpart in the reference (it has no loader for real checkpoints,
+ * ROADMAP.md:230-234); checked against a sequential-f32 CPU restatement of
+ * ggml's dequantisation with the matvec tolerance.  Limits: 1 <= sb_per_row
+ * <= 128 (the row's x is staged in LDS), matrix below 4 GiB, q and x 16-byte
+ * aligned.  Variant holes as for Q4_K (nontemporal 0 or 2). */
+axh_status axh_q5k_matvec(axh_context *ctx, const void *q, const float *x, float *y,
+                          uint32_t n_rows, uint32_t sb_per_row, const axh_q4_variant *variant,
+                          void *stream);
+axh_status axh_q6k_matvec(axh_context *ctx, const void *q, const float *x, float *y,
+                          uint32_t n_rows, uint32_t sb_per_row, const axh_q4_variant *variant,
+                          void *stream);
+axh_status axh_q5k_matvec_kernel_name(uint32_t n_rows, uint32_t sb_per_row,
+                                      const axh_q4_variant *variant, char *buf, size_t cap);
+axh_status axh_q6k_matvec_kernel_name(uint32_t n_rows, uint32_t sb_per_row,
+                                      const axh_q4_variant *variant, char *buf, size_t cap);
+uint32_t axh_q5k_matvec_variant_count(void);
+axh_status axh_q5k_matvec_variant_at(uint32_t i, axh_q4_variant *out);
+uint32_t axh_q6k_matvec_variant_count(void);
+axh_status axh_q6k_matvec_variant_at(uint32_t i, axh_q4_variant *out);
+/* Matvec of a row-major ggml tensor of n_rows rows of n_cols elements
+ * (GGUF ne[0] = n_cols), dispatched on its type: Q4_0, Q4_K, Q5_K or Q6_K,
+ * each with its default variant. */
+axh_status axh_matvec_ggml(axh_context *ctx, uint32_t ggml_type, const void *q, const float *x,
+                           float *y, uint32_t n_rows, uint64_t n_cols, void *stream);
+
 /* Fused SwiGLU gate/up projection of a decode step, one pass over x:
  *   h[r] = silu(g_r) * u_r,  g_r = dot(q_gate row r, x),  u_r = dot(q_up row r, x),
  *   silu(g) = g / (1 + exp(-g)),
@@ -219,6 +258,14 @@ axh_status axh_q4k_dequant(axh_context *ctx, const void *q, float *w, uint64_t n
                            void *stream);
 axh_status axh_q4_0_dequant(axh_context *ctx, const void *q, float *w, uint64_t n_blocks,
                             void *stream);
+/* Q5_K / Q6_K decode (256 f32 per superblock in ggml's element order),
+ * bit-exact with the CPU restatement: Q5_K rounds once (the subtraction),
+ * Q6_K weights are exact products.  Q5_K: q and w 16-byte aligned; Q6_K:
+ * q 2-byte and w 4-byte aligned. */
+axh_status axh_q5k_dequant(axh_context *ctx, const void *q, float *w, uint64_t n_superblocks,
+                           void *stream);
+axh_status axh_q6k_dequant(axh_context *ctx, const void *q, float *w, uint64_t n_superblocks,
+                           void *stream);
 /* IEEE binary16 -> binary32 widening of n raw patterns (the ptr_read_u16_zext +
  * f16_bits_to_f32 builtins, crates/axc-codegen/src/q4_0.rs:86-171). */
 axh_status axh_f16_widen(axh_context *ctx, const uint16_t *h, float *f, uint64_t n, void *stream);

@@ -197,3 +197,24 @@ def test_gate_up_kernel_selection(axc):
                 (4, 16, axc.Variant(3, 4, 2, 0)), (4, 100, axc.Variant(2, 4, 2, 0))):
         with pytest.raises(axc.DispatchError):
             name(*bad)
+
+
+def test_kquant_kernel_selection(axc):
+    """Q5_K / Q6_K: persistent kernel only, x staging widened for long rows,
+    typed errors beyond 128 superblocks or for missing variants."""
+    co = axc.builtin_code_object()
+    for fam, name in (("q5k", axc.q5k_matvec_kernel_name), ("q6k", axc.q6k_matvec_kernel_name)):
+        assert name(128256, 16) == f"axh_{fam}_matvec_flat_r1_w4_p2_x1"
+        assert name(4096, 56) == f"axh_{fam}_matvec_flat_r1_w8_p2_x1"
+        assert name(4096, 128) == f"axh_{fam}_matvec_flat_r1_w8_p2_x2"
+        assert name(4096, 56, axc.Variant(1, 4, 2, 0)) == f"axh_{fam}_matvec_flat_r1_w4_p2_x2"
+        vs = axc.compiled_variants(fam)
+        assert len(set(vs)) == len(vs) >= 3
+        for v in vs:
+            assert name(100, 16, v).encode() in co
+        for bad in ((4, 0, None), (4, 129, None), (4, 16, axc.Variant(0, 0, 0, 1)),
+                    (4, 16, axc.Variant(3, 4, 2, 0)), (4, 100, axc.Variant(2, 4, 2, 0))):
+            with pytest.raises(axc.DispatchError):
+                name(*bad)
+    for k in ("axh_q5k_dequant", "axh_q6k_dequant", "axh_f32_to_f16"):
+        assert k.encode() in co
