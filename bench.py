@@ -48,7 +48,13 @@ WORKLOADS = {
     # fused SwiGLU gate/up projections of a Llama-3-8B decode step (two
     # 14336 x 4096 Q4_K_M matrices against one x)
     "ffn": ("gate_up", 14336, 16, 0.5, "Llama-3-8B gate/up, not a BASELINE config"),
+    # ggml k-quants that Q4_K_M / Q5_K_M checkpoints store next to Q4_K
+    "head6": ("q6k", 128256, 16, 1.0, "Llama-3-8B output head as Q4_K_M stores it (Q6_K), "
+                                        "not a BASELINE config"),
+    "down6": ("q6k", 4096, 56, 0.5, "Llama-3-8B ffn_down as Q6_K, not a BASELINE config"),
+    "up5": ("q5k", 14336, 16, 1.0, "Llama-3-8B ffn_up as Q5_K, not a BASELINE config"),
 }
+KQ_IDS = {"q5k": 13, "q6k": 14}
 
 
 def cpu_model() -> str:
@@ -94,13 +100,15 @@ class Case:
         self.kind, self.rows, self.units, self.label = kind, rows, units, label
         self.ctx, self.O, self.np, self.pkg = ctx, O, np, pkg
         self.batch = batch if kind == "matmul" else 1
-        unit_bytes = 18 if kind == "q4_0" else 144
+        unit_bytes = {"q4_0": 18, "q5k": 176, "q6k": 210}.get(kind, 144)
         self.cols = units * (32 if kind == "q4_0" else 256)
         self.weight_bytes = rows * units * unit_bytes
         seed = 20241 if name == "c4" else 30000 + rows + units
         self.up_off = 0
         if kind == "q4_0":
             self.q = O.gen_q4_0_weights(seed, rows * units)
+        elif kind in KQ_IDS:
+            self.q = O.gen_kq_weights(KQ_IDS[kind], seed, rows * units)
         elif kind == "gate_up":
             # gate rows, then the up rows at the next COPY_ALIGN boundary
             self.qg = O.gen_q4k_weights(seed, rows * units)
@@ -140,6 +148,10 @@ class Case:
             self.ctx.q4k_matvec(w, self.dx, self.dy, self.rows, self.units, self.variant)
         elif self.kind == "q4_0":
             self.ctx.q4_0_matvec(w, self.dx, self.dy, self.rows, self.units, self.variant)
+        elif self.kind == "q5k":
+            self.ctx.q5k_matvec(w, self.dx, self.dy, self.rows, self.units, self.variant)
+        elif self.kind == "q6k":
+            self.ctx.q6k_matvec(w, self.dx, self.dy, self.rows, self.units, self.variant)
         elif self.kind == "gate_up":
             self.ctx.q4k_gate_up(w, w + self.up_off, self.dx, self.dy, self.rows, self.units,
                                  self.variant)
@@ -157,6 +169,10 @@ class Case:
             return self.pkg.q4_0_matvec_kernel_name(self.rows, self.units, self.variant)
         if self.kind == "gate_up":
             return self.pkg.q4k_gate_up_kernel_name(self.rows, self.units, self.variant)
+        if self.kind == "q5k":
+            return self.pkg.q5k_matvec_kernel_name(self.rows, self.units, self.variant)
+        if self.kind == "q6k":
+            return self.pkg.q6k_matvec_kernel_name(self.rows, self.units, self.variant)
         return self.pkg.q4k_matmul_kernel_name(self.rows, self.batch, self.variant)
 
     def parity(self) -> dict:
@@ -174,6 +190,13 @@ class Case:
         if self.kind == "q4_0":
             ref = O.q4_0_matvec(self.q, self.x, self.rows, self.units)
             yf, ad = O.q4_0_matvec_f64(self.q, self.x, self.rows, self.units)
+            rep = O.matvec_tolerance_report(y, ref, yf, ad, self.cols)
+            return {k: rep[k] for k in ("ok", "rows_failed", "norm_rel_err",
+                                        "gpu_err_vs_f64_norm", "cpu_err_vs_f64_norm")}
+        if self.kind in KQ_IDS:
+            kid = KQ_IDS[self.kind]
+            ref = O.kq_matvec(kid, self.q, self.x, self.rows, self.units)
+            yf, ad = O.kq_matvec_f64(kid, self.q, self.x, self.rows, self.units)
             rep = O.matvec_tolerance_report(y, ref, yf, ad, self.cols)
             return {k: rep[k] for k in ("ok", "rows_failed", "norm_rel_err",
                                         "gpu_err_vs_f64_norm", "cpu_err_vs_f64_norm")}
@@ -204,6 +227,12 @@ class Case:
             one = lambda: O.q4k_matvec_single(self.q, self.x, self.rows, self.units)
             many = lambda: O.q4k_matvec(self.q, self.x, self.rows, self.units, threads=threads)
             frac, what = 1.0, f"full {self.rows}x{self.cols} Q4_K matvecs"
+        elif self.kind in KQ_IDS:
+            kid = KQ_IDS[self.kind]
+            one = lambda: O.kq_matvec(kid, self.q, self.x, self.rows, self.units, threads=1)
+            many = lambda: O.kq_matvec(kid, self.q, self.x, self.rows, self.units,
+                                       threads=threads)
+            frac, what = 1.0, f"full {self.rows}x{self.cols} {self.kind.upper()} matvecs"
         elif self.kind == "gate_up":
             def two(threads):
                 g = O.q4k_matvec(self.qg, self.x, self.rows, self.units, threads=threads)
@@ -366,7 +395,7 @@ def main() -> int:
         unit, peak = "GB/s", HBM_PEAK_GBS
         algo = case.weight_bytes
         value = algo / t / 1e9
-        qname = "Q4_0" if kind == "q4_0" else "Q4_K_M"
+        qname = {"q4_0": "Q4_0", "q5k": "Q5_K", "q6k": "Q6_K"}.get(kind, "Q4_K_M")
         if kind == "matmul":
             metric = (f"Q4_K_M x f16 matmul weight-bytes HBM GB/s at {case.rows}x{case.cols}, "
                       f"B={case.batch}; us/call")
