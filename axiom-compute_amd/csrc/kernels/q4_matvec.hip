@@ -327,6 +327,7 @@ AXH_Q4K_MATVEC_TILED(2, 8, 2)
 // needs no further scaling.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kQ4kFlatSbFloats = 272; // LDS floats per superblock of x (256 + pad)
+constexpr uint32_t kWaitXMinSb = 32;       // rows this long wait for x before prefetching
 
 __device__ __forceinline__ void q4k_flat_stage(const float *__restrict__ x, float *xs, float *ss,
                                                uint32_t si, const float4 (&v)[8]) {
@@ -451,8 +452,8 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
   float *xs = lds;
   float *ss = lds + nsb * kQ4kFlatSbFloats;
 
-  // Prologue: x requests first, then (once x has arrived) the weight
-  // prefetch, then the LDS writes.  XP
+  // Prologue: x requests first, then (for long rows once x has arrived) the
+  // weight prefetch, then the LDS writes.  XP
   // sub-blocks of x (32 floats each) per thread: the host launches this
   // kernel only when nsb * 8 <= XP * NW * 64.
   const uint32_t nsub = nsb * 8u;
@@ -463,12 +464,13 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
     my_sub[k] = min(tid + (uint32_t)k * (NW * 64u), nsub - 1u);
     q4k_flat_load_x(xr, my_sub[k], xv[k]);
   }
-  // Let x arrive before the weight prefetch goes out: every wave of the grid
-  // issues its prefetch at once, and x requests queued behind that traffic
-  // arrive later than the first weights would (measured: about 0.3 us per
-  // launch on 4096 x 14336).
+  // For long rows, let x arrive before the weight prefetch goes out: every
+  // wave of the grid issues its prefetch at once, and x requests queued
+  // behind that traffic arrive later than the first weights would (measured:
+  // 0.3 us less per launch on 4096 x 14336, 0.2 us more on 4096 x 4096,
+  // where x is 16 KiB).
   __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (nsb >= kWaitXMinSb) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
 
   Q4kFlatBuf<RPW, PF, kQ5> B;
@@ -730,8 +732,8 @@ __device__ __forceinline__ void q6k_matvec_flat(const uint8_t *__restrict__ q,
   float *xs = lds;
   float *ss = lds + nsb * kQ6kSbFloats;
 
-  // Prologue as in the Q4_K flat kernel: x first, then (once x has arrived)
-  // the weight prefetch, then the LDS writes.
+  // Prologue as in the Q4_K flat kernel: x first, then (for long rows once x
+  // has arrived) the weight prefetch, then the LDS writes.
   const uint32_t nsub = nsb * 8u;
   uint32_t my_sub[XP];
   float4 xv[XP][8];
@@ -741,7 +743,7 @@ __device__ __forceinline__ void q6k_matvec_flat(const uint8_t *__restrict__ q,
     q4k_flat_load_x(xr, my_sub[k], xv[k]);
   }
   __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (nsb >= kWaitXMinSb) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
 
   Q6kFlatBuf<RPW, PF> B;
