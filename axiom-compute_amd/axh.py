@@ -199,8 +199,8 @@ def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
         "axh_q4k_matmul_f32": (st, [vp, vp, vp, vp, vp, u32, u32, u32,
                                     c.POINTER(_MatmulVariant), vp]),
         "axh_f32_to_f16": (st, [vp, vp, vp, u64, vp]),
-        "axh_q4k_matmul_kernel_name": (st, [u32, u32, c.POINTER(_MatmulVariant), c.c_char_p,
-                                            sz]),
+        "axh_q4k_matmul_kernel_name": (st, [u32, u32, u32, c.POINTER(_MatmulVariant),
+                                            c.c_char_p, sz]),
         "axh_q4k_matmul_variant_count": (u32, []),
         "axh_q4k_matmul_variant_at": (st, [u32, c.POINTER(_MatmulVariant)]),
         "axh_q4_0_matvec": (st, [vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
@@ -289,13 +289,14 @@ def compiled_matmul_variants() -> list[MatmulVariant]:
     return out
 
 
-def q4k_matmul_kernel_name(n_rows: int, batch: int,
+def q4k_matmul_kernel_name(n_rows: int, sb_per_row: int, batch: int,
                            variant: Optional[MatmulVariant] = None) -> str:
     """Entry point axh_q4k_matmul_f16 launches for this shape and variant."""
     lib = load_library()
     v = variant._c() if variant else None
     buf = ctypes.create_string_buffer(64)
-    _check(lib.axh_q4k_matmul_kernel_name(n_rows, batch, ctypes.byref(v) if v else None, buf, 64))
+    _check(lib.axh_q4k_matmul_kernel_name(n_rows, sb_per_row, batch,
+                                          ctypes.byref(v) if v else None, buf, 64))
     return buf.value.decode()
 
 

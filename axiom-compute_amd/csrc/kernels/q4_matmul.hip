@@ -527,6 +527,155 @@ __device__ __forceinline__ void q4k_matmul_ks(const uint8_t *__restrict__ q,
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// Streaming variant for narrow batches (kind 4): persistent waves stream
+// 16-row tiles of W over K with PF 128-wide steps of loads in flight
+// (register A fragments as in q4k_matmul_rf), against the workgroup's 16
+// activation columns (blockIdx.y selects the column group) staged once in
+// LDS as Xs[col][k] (row stride K + 8 halves).  The KS waves of a tile slot
+// take interleaved K steps (wave w: steps (w % KS) + KS*j); at the end of a
+// tile their partial tiles are summed in LDS in wave order (deterministic)
+// and stored.  Every wave of a workgroup runs the same number of tile rounds,
+// so the two barriers per round are reached by all of them.  Loads are
+// unconditional: rows past the matrix and steps past the end read zeros
+// through the buffer range check.
+// ---------------------------------------------------------------------------
+struct StStep {
+  uint4 hd;
+  uint2 qlo, qhi;
+};
+
+template <int NW, int KS, int PF>
+__device__ __forceinline__ void q4k_matmul_st(const uint8_t *__restrict__ q,
+                                              const uint16_t *__restrict__ x,
+                                              float *__restrict__ y, const MatmulArgs a,
+                                              _Float16 *Xs) {
+  static_assert(NW % KS == 0, "KS waves per tile slot");
+  constexpr int kSlots = NW / KS;
+  __shared__ __attribute__((aligned(16))) f32x4_t red[KS > 1 ? (KS - 1) * kSlots * 64 : 1];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t slot = wave / KS, kpart = wave % KS;
+  const uint32_t fr = lane & 15u, g = lane >> 4;
+  const uint32_t n_rows = a.n_rows, nsb = a.sb_per_row, batch = a.batch;
+  const uint32_t K = nsb * 256u, ldx = K + 8u;
+  const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
+  const __amdgpu_buffer_rsrc_t qr = rsrc(q, n_rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t xr = rsrc(x, batch * K * 2u);
+  const uint32_t n0 = blockIdx.y * 16u;
+  const uint32_t slots_total = gridDim.x * kSlots;
+  const uint32_t slot_g = blockIdx.x * kSlots + slot;
+  const uint32_t n_tiles = (n_rows + 15u) >> 4;
+  const uint32_t n_rounds = (n_tiles + slots_total - 1u) / slots_total; // same for the whole grid
+  const uint32_t n_steps = 2u * nsb;
+  const uint32_t my_steps = (n_steps + KS - 1u) / KS; // per wave and tile (padded)
+  const uint32_t total = (n_rounds * my_steps + (PF - 1)) / PF * PF;
+
+  // Stage the 16 columns: 16-byte chunks (col, 8 halves of k), 8 in flight per thread.
+  const uint32_t kc_per_col = K >> 3, n_chunks = 16u * kc_per_col;
+  for (uint32_t c0 = 0; c0 < n_chunks; c0 += 8u * NW * 64u) {
+    uint4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t ch = c0 + tid + (uint32_t)i * (NW * 64u);
+      const uint32_t col = ch / kc_per_col, kc = ch - col * kc_per_col, b = n0 + col;
+      v[i] = bload16(xr, (ch < n_chunks && b < batch) ? (b * K + kc * 8u) * 2u : kOob);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t ch = c0 + tid + (uint32_t)i * (NW * 64u);
+      const uint32_t col = ch / kc_per_col, kc = ch - col * kc_per_col;
+      if (ch < n_chunks) *reinterpret_cast<uint4 *>(Xs + col * ldx + kc * 8u) = v[i];
+    }
+  }
+
+  // (round, j) -> tile slot_g + round * slots_total, K step kpart + KS * j
+  auto load_step = [&](StStep &S, uint32_t rd, uint32_t j) {
+    const uint32_t row = (slot_g + rd * slots_total) * 16u + fr;
+    const uint32_t ks = kpart + (uint32_t)KS * j;
+    const uint32_t base =
+        (row < n_rows && ks < n_steps) ? row * row_bytes + (ks >> 1) * 144u : kOob;
+    S.hd = bload16(qr, base);
+    const uint32_t qo = 16u + 64u * (ks & 1u) + 8u * g;
+    S.qlo = bload8(qr, base == kOob ? kOob : base + qo);
+    S.qhi = bload8(qr, base == kOob ? kOob : base + qo + 32u);
+  };
+  StStep S[PF];
+  uint32_t l_rd = 0, l_j = 0;
+#pragma unroll
+  for (int p = 0; p < PF; ++p) {
+    load_step(S[p], l_rd, l_j);
+    if (++l_j == my_steps) { l_j = 0; ++l_rd; }
+  }
+  __syncthreads(); // Xs complete
+
+  f32x4_t acc = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+  uint32_t c_rd = 0, c_j = 0;
+  const _Float16 *xrow = Xs + fr * ldx + 8u * g;
+  for (uint32_t j0 = 0; j0 < total; j0 += PF) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+      const uint32_t ks = kpart + (uint32_t)KS * c_j;
+      const uint32_t h = ks & 1u;
+      half8_t af[4];
+      {
+        const uint4 hd = S[p].hd;
+        const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          const uint32_t c = 2u * h + (uint32_t)cc;
+          uint32_t scp, mp;
+          q4k_scale_min_pair(hd.y, hd.z, hd.w, c, &scp, &mp);
+          const float d1s = d * (float)(scp & 0xFFu) * 16777216.0f;
+          const float d2s = d * (float)(scp >> 8) * 1048576.0f;
+          const float m1 = dmin * (float)(mp & 0xFFu), m2 = dmin * (float)(mp >> 8);
+          const uint2 qw = cc == 0 ? S[p].qlo : S[p].qhi;
+          uint32_t l0, l1, h0, h1, l2, l3, h2, h3;
+          dequant_dword(qw.x, d1s, m1, d2s, m2, l0, l1, h0, h1);
+          dequant_dword(qw.y, d1s, m1, d2s, m2, l2, l3, h2, h3);
+          af[2 * cc] = __builtin_bit_cast(half8_t, make_uint4(l0, l1, l2, l3));
+          af[2 * cc + 1] = __builtin_bit_cast(half8_t, make_uint4(h0, h1, h2, h3));
+        }
+      }
+      // steps past K (padding) read X at step 0: their A fragments are zero
+      const _Float16 *xk = xrow + (ks < n_steps ? ks : 0u) * (uint32_t)kKStep;
+      half8_t bfr[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) bfr[kk] = *reinterpret_cast<const half8_t *>(xk + 32 * kk);
+      // refill this slot PF steps ahead (unconditional; past the end: zeros)
+      load_step(S[p], l_rd, l_j);
+      if (++l_j == my_steps) { l_j = 0; ++l_rd; }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[kk], bfr[kk], acc, 0, 0, 0);
+      if (++c_j == my_steps) { // a tile round is complete: reduce across kpart, store
+        if (c_rd < n_rounds) {
+          if constexpr (KS > 1) {
+            if (kpart > 0) red[((kpart - 1u) * kSlots + slot) * 64u + lane] = acc;
+            __syncthreads();
+            if (kpart == 0) {
+#pragma unroll
+              for (uint32_t w = 1; w < (uint32_t)KS; ++w) acc += red[((w - 1u) * kSlots + slot) * 64u + lane];
+            }
+            __syncthreads();
+          }
+          const uint32_t b = n0 + fr, r0 = (slot_g + c_rd * slots_total) * 16u + 4u * g;
+          if (kpart == 0 && b < batch) {
+            float *dst = y + (size_t)b * n_rows + r0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (r0 + e < n_rows) dst[e] = acc[e];
+          }
+        }
+        acc = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+        c_j = 0;
+        ++c_rd;
+      }
+    }
+  }
+}
+
 } // namespace
 
 #define AXH_Q4K_MATMUL(W, NT)                                                                    \
@@ -564,3 +713,18 @@ AXH_Q4K_MATMUL_KS(4, 1, 2)
 AXH_Q4K_MATMUL_KS(8, 1, 1)
 AXH_Q4K_MATMUL_KS(4, 2, 2)
 AXH_Q4K_MATMUL_KS(8, 2, 1)
+
+#define AXH_Q4K_MATMUL_ST(NW, KS, PF)                                                            \
+  extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
+      axh_q4k_matmul_st_w##NW##_k##KS##_p##PF(const uint8_t *__restrict__ q,                     \
+                                              const uint16_t *__restrict__ x,                    \
+                                              float *__restrict__ y, MatmulArgs a) {             \
+    extern __shared__ _Float16 axh_xs_dyn[];                                                     \
+    q4k_matmul_st<NW, KS, PF>(q, x, y, a, axh_xs_dyn);                                           \
+  }
+
+AXH_Q4K_MATMUL_ST(4, 1, 4)
+AXH_Q4K_MATMUL_ST(8, 2, 4)
+AXH_Q4K_MATMUL_ST(8, 2, 2)
+AXH_Q4K_MATMUL_ST(16, 4, 2)
+AXH_Q4K_MATMUL_ST(16, 4, 4)

@@ -36,13 +36,17 @@ struct MatmulArgs {
 // Compiled batched-matmul kernels (keep in sync with q4_matmul.hip):
 //   kind 1 (LDS-tiled)  axh_q4k_matmul_w{W}_n{NT}: W waves x 32 rows, NT 16-column tiles;
 //   kind 2 (register A) axh_q4k_matmul_rf_w{W}_n{NT}_p{PF}_x1;
-//   kind 3 (K-split)    axh_q4k_matmul_ks_k{W}_n{NT}_p{PF}: W waves split K of one 32-row tile.
+//   kind 3 (K-split)    axh_q4k_matmul_ks_k{W}_n{NT}_p{PF}: W waves split K of one 32-row tile;
+//   kind 4 (streaming)  axh_q4k_matmul_st_w{W}_k{W/4}_p{PF}: persistent waves stream 16-row
+//                       tiles against 16 columns staged in LDS, W/4 waves splitting each
+//                       tile's K (col_tiles is 1).
 struct MatmulVariant {
   uint32_t kind, w, nt, pf;
 };
 constexpr MatmulVariant kQ4kMatmulVariants[] = {
     {1, 1, 1, 1}, {1, 2, 2, 1}, {1, 4, 4, 1}, {1, 4, 8, 1}, {2, 4, 4, 2},
-    {2, 4, 8, 1}, {3, 4, 1, 2}, {3, 8, 1, 1}, {3, 4, 2, 2}, {3, 8, 2, 1}};
+    {2, 4, 8, 1}, {3, 4, 1, 2}, {3, 8, 1, 1}, {3, 4, 2, 2}, {3, 8, 2, 1},
+    {4, 4, 1, 4}, {4, 8, 1, 4}, {4, 8, 1, 2}, {4, 16, 1, 2}, {4, 16, 1, 4}};
 constexpr uint32_t kMatmulOob = 0xFFFFFF00u; // the kernels' out-of-range offset
 
 struct MatvecVariant {
@@ -629,8 +633,12 @@ axh_status axh_q4_0_matvec(axh_context *ctx, const void *q, const float *x, floa
 // Defaults from on-device sweeps at 14336 x 4096 (K-split while the batch
 // fits one or two 16-column tiles, LDS tiles in the middle, register A for
 // large batches).
-static MatmulVariant q4k_matmul_default(uint32_t n_rows, uint32_t batch) {
+// Kind 4 stages 16 activation columns of the whole K in LDS.
+constexpr uint32_t kStreamMaxSb = 18; // 16 x (18*256 + 8) halves = 147,712 B
+
+static MatmulVariant q4k_matmul_default(uint32_t n_rows, uint32_t batch, uint32_t nsb) {
   (void)n_rows;
+  if (batch <= 16 && nsb <= kStreamMaxSb) return {4, 16, 1, 2};
   if (batch <= 16) return {3, 8, 1, 1};
   if (batch <= 32) return {3, 8, 2, 1};
   if (batch <= 128) return {1, 4, 4, 1};
@@ -651,10 +659,10 @@ axh_status axh_q4k_matmul_variant_at(uint32_t i, axh_q4_matmul_variant *out) {
   return ok();
 }
 
-static axh_status plan_q4k_matmul(uint32_t n_rows, uint32_t batch,
+static axh_status plan_q4k_matmul(uint32_t n_rows, uint32_t sb_per_row, uint32_t batch,
                                   const axh_q4_matmul_variant *variant, MatmulVariant *out,
                                   char *name, size_t cap) {
-  MatmulVariant want = q4k_matmul_default(n_rows, batch);
+  MatmulVariant want = q4k_matmul_default(n_rows, batch, sb_per_row);
   if (variant) {
     if (variant->kind) want.kind = variant->kind;
     if (variant->waves_per_workgroup) want.w = variant->waves_per_workgroup;
@@ -668,20 +676,22 @@ static axh_status plan_q4k_matmul(uint32_t n_rows, uint32_t batch,
         std::snprintf(name, cap, "axh_q4k_matmul_w%u_n%u", v.w, v.nt);
       else if (v.kind == 2)
         std::snprintf(name, cap, "axh_q4k_matmul_rf_w%u_n%u_p%u_x1", v.w, v.nt, v.pf);
-      else
+      else if (v.kind == 3)
         std::snprintf(name, cap, "axh_q4k_matmul_ks_k%u_n%u_p%u", v.w, v.nt, v.pf);
+      else
+        std::snprintf(name, cap, "axh_q4k_matmul_st_w%u_k%u_p%u", v.w, v.w / 4u, v.pf);
       return ok();
     }
   return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_K matmul variant matches");
 }
 
-axh_status axh_q4k_matmul_kernel_name(uint32_t n_rows, uint32_t batch,
+axh_status axh_q4k_matmul_kernel_name(uint32_t n_rows, uint32_t sb_per_row, uint32_t batch,
                                       const axh_q4_matmul_variant *variant, char *buf,
                                       size_t cap) {
   if (!buf || cap == 0) return fail(AXH_ERR_INVALID_ARGUMENT, "buf is NULL");
   MatmulVariant v{};
   char name[64];
-  axh_status s = plan_q4k_matmul(n_rows, batch, variant, &v, name, sizeof(name));
+  axh_status s = plan_q4k_matmul(n_rows, sb_per_row, batch, variant, &v, name, sizeof(name));
   if (s != AXH_OK) return s;
   if (std::strlen(name) + 1 > cap) return fail(AXH_ERR_INVALID_ARGUMENT, "buf too small");
   std::memcpy(buf, name, std::strlen(name) + 1);
@@ -713,20 +723,30 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
   if (s != AXH_OK || n_rows == 0 || batch == 0) return s;
   MatmulVariant v{};
   char name[64];
-  s = plan_q4k_matmul(n_rows, batch, variant, &v, name, sizeof(name));
+  s = plan_q4k_matmul(n_rows, sb_per_row, batch, variant, &v, name, sizeof(name));
   if (s != AXH_OK) return s;
-  const uint32_t tm = v.kind == 3 ? 32u : 32u * v.w, tn = 16u * v.nt;
-  const uint64_t gx = (n_rows + tm - 1) / tm, gy = (batch + tn - 1) / tn;
+  // kind 4 stages 16 activation columns of the whole K in LDS
+  const uint32_t lds = v.kind == 4 ? 16u * (sb_per_row * 256u + 8u) * 2u : 0u;
+  if (lds > ctx->core->max_lds)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "streaming matmul: 16 columns of K do not fit LDS");
+  const uint32_t tm = v.kind == 3 ? 32u : v.kind == 4 ? 64u : 32u * v.w; // kind 4: 4 tile slots
+  const uint32_t tn = 16u * v.nt;
+  uint64_t gx = (n_rows + tm - 1) / tm;
+  const uint64_t gy = (batch + tn - 1) / tn;
   if (gx > ctx->core->max_wg[0] || gy > ctx->core->max_wg[1])
     return fail(AXH_ERR_WORKGROUP_COUNT_EXCEEDS_LIMIT, "matmul grid exceeds the device limit");
   hipSetDevice(ctx->core->device);
   axh_kernel *k = nullptr;
   s = builtin_kernel(ctx, name, 3, sizeof(MatmulArgs), v.w * 64u, &k);
   if (s != AXH_OK) return s;
+  if (v.kind == 4) { // persistent: at most one resident wave of workgroups per column group
+    const uint64_t resident = (uint64_t)occupancy(ctx, k, lds) * ctx->core->cu_count;
+    if (resident < gx) gx = resident;
+  }
   const uint32_t grid[3] = {(uint32_t)gx, (uint32_t)gy, 1};
   void *bufs[3] = {const_cast<void *>(q), const_cast<uint16_t *>(x), y};
   MatmulArgs a{n_rows, sb_per_row, batch, 0};
-  s = launch_raw(k, grid, bufs, 3, &a, sizeof(a), 0, pick_stream(ctx, stream));
+  s = launch_raw(k, grid, bufs, 3, &a, sizeof(a), lds, pick_stream(ctx, stream));
   return s == AXH_OK ? ok() : s;
 }
 
@@ -739,7 +759,7 @@ axh_status axh_q4k_matmul_f32(axh_context *ctx, const void *q, const float *x, u
     return fail(AXH_ERR_INVALID_ARGUMENT, "x16 must be a 16-byte aligned device pointer");
   MatmulVariant v{};
   char name[64];
-  s = plan_q4k_matmul(n_rows, batch, variant, &v, name, sizeof(name));
+  s = plan_q4k_matmul(n_rows, sb_per_row, batch, variant, &v, name, sizeof(name));
   if (s != AXH_OK) return s; // reject a bad variant before any device work
   s = axh_f32_to_f16(ctx, x, x16, (uint64_t)batch * sb_per_row * 256u, stream);
   if (s != AXH_OK) return s;

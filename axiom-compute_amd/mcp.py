@@ -376,7 +376,8 @@ def bench_variant(params: dict, ctx: McpContext) -> dict:
                       f"worst output {rep['worst_row']} at {rep['worst_over_allowed']:.3g} x allowed; "
                       f"norm error {rep['norm_rel_err']:.3g}"}
     srt = sorted(samples)
-    name = (_axh.q4k_matmul_kernel_name(rows, batch, variant) if kernel == "q4k_matmul_f16" else
+    name = (_axh.q4k_matmul_kernel_name(rows, units, batch, variant)
+            if kernel == "q4k_matmul_f16" else
             _axh.q4k_matvec_kernel_name(rows, units, variant)
             if kernel == "q4km_dequant_matvec" else
             _axh.q4_0_matvec_kernel_name(rows, units, variant))

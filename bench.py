@@ -173,7 +173,7 @@ class Case:
             return self.pkg.q5k_matvec_kernel_name(self.rows, self.units, self.variant)
         if self.kind == "q6k":
             return self.pkg.q6k_matvec_kernel_name(self.rows, self.units, self.variant)
-        return self.pkg.q4k_matmul_kernel_name(self.rows, self.batch, self.variant)
+        return self.pkg.q4k_matmul_kernel_name(self.rows, self.units, self.batch, self.variant)
 
     def parity(self) -> dict:
         """Checks this exact workload against the oracle before timing."""

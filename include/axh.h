@@ -305,8 +305,8 @@ axh_status axh_q4_0_matvec_variant_at(uint32_t i, axh_q4_variant *out);
  * batch = 1 case with f32 weights); multi-row matmul is roadmap there
  * (ROADMAP.md:54-72).  q and x 16-byte aligned, each below 4 GiB. */
 typedef struct axh_q4_matmul_variant {
-    uint32_t kind;                /* 1 LDS-tiled, 2 register A, 3 K-split; 0 = default */
-    uint32_t waves_per_workgroup; /* kinds 1-2: 32 rows per wave; kind 3: waves splitting K */
+    uint32_t kind;                /* 1 LDS-tiled, 2 register A, 3 K-split, 4 streaming; 0 = default */
+    uint32_t waves_per_workgroup; /* kinds 1-2: 32 rows per wave; 3: waves splitting K; 4: waves */
     uint32_t col_tiles;           /* 16-column MFMA tiles per workgroup */
     uint32_t prefetch;            /* K steps in flight (kinds 2-3) */
 } axh_q4_matmul_variant;
@@ -322,7 +322,7 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
 axh_status axh_q4k_matmul_f32(axh_context *ctx, const void *q, const float *x, uint16_t *x16,
                               float *y, uint32_t n_rows, uint32_t sb_per_row, uint32_t batch,
                               const axh_q4_matmul_variant *variant, void *stream);
-axh_status axh_q4k_matmul_kernel_name(uint32_t n_rows, uint32_t batch,
+axh_status axh_q4k_matmul_kernel_name(uint32_t n_rows, uint32_t sb_per_row, uint32_t batch,
                                       const axh_q4_matmul_variant *variant, char *buf,
                                       size_t cap);
 uint32_t axh_q4k_matmul_variant_count(void);
