@@ -1108,6 +1108,118 @@ __device__ __forceinline__ void q4k_matvec_cols(const uint8_t *__restrict__ q,
   } while (i < n_pad);
 }
 
+// ---------------------------------------------------------------------------
+// Split-K for few long rows (fewer than 32 rows of 64..256 superblocks):
+// workgroup g (one wave) takes superblocks [g*SPW, g*SPW + SPW) of every row,
+// four lanes per superblock (as the column kernel), with its x slice in
+// VGPRs.  Lane 63 stores the per-row partial sums to
+// ws[kSkPartials + g*32 + row] and counts the workgroup with a device-scope
+// release increment of ws[0]; the workgroup that sees G - 1 (all others
+// done) takes an acquire fence, adds the partials in workgroup order
+// (deterministic), writes y and resets the counter to zero for the next
+// call.  The host allocates the workspace once per stream (counter zeroed
+// then); calls on one stream never overlap.  Each release writes back the
+// L2 of its XCD, so the split is kept to at most 16 workgroups (measured:
+// 8 workgroups 7.2 us, 32 workgroups 14 us for 1 x 32768).
+// ---------------------------------------------------------------------------
+constexpr uint32_t kSkPartials = 64; // floats before the partials (the counter is word 0)
+constexpr uint32_t kSkMaxRows = 32;
+
+template <int SPW>
+__device__ __forceinline__ void q4k_matvec_sk(const uint8_t *__restrict__ q,
+                                              const float *__restrict__ x,
+                                              float *__restrict__ y, float *ws, uint32_t n_rows,
+                                              uint32_t nsb) {
+  constexpr int RB = 4;
+  const uint32_t tid = threadIdx.x, g = blockIdx.x, G = gridDim.x;
+  const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
+  const __amdgpu_buffer_rsrc_t qr = make_rsrc(q, n_rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, nsb * 1024u);
+  const uint32_t sb = g * SPW + (tid >> 2), c = tid & 3u;
+  const bool live = tid < 4u * SPW && sb < nsb;
+  const uint32_t lane_off = live ? sb * (uint32_t)kQ4kSbBytes : kQ4kColsOob;
+  const uint32_t x_off = live ? (sb * 4u + c) * 256u : nsb * 1024u; // idle lanes read zeros
+  const uint32_t n_batches = (n_rows + RB - 1) / RB;
+
+  float4 xl[8], xh[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    xl[t] = buf_loadf4(xr, x_off + 16u * (uint32_t)t);
+    xh[t] = buf_loadf4(xr, x_off + 128u + 16u * (uint32_t)t);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  Q4kColsBuf<RB> B0, B1;
+  q4k_cols_load<RB, false>(B0, qr, 0u, n_rows, row_bytes, lane_off, c);
+  __builtin_amdgcn_sched_barrier(0);
+  q4k_cols_load<RB, false>(B1, qr, 1u, n_rows, row_bytes, lane_off, c);
+  __builtin_amdgcn_sched_barrier(0);
+  float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    s0 += (xl[t].x + xl[t].y) + (xl[t].z + xl[t].w);
+    s1 += (xh[t].x + xh[t].y) + (xh[t].z + xh[t].w);
+    xl[t] = make_float4(xl[t].x * 16777216.0f, xl[t].y * 16777216.0f, xl[t].z * 16777216.0f,
+                        xl[t].w * 16777216.0f);
+    xh[t] = make_float4(xh[t].x * 1048576.0f, xh[t].y * 1048576.0f, xh[t].z * 1048576.0f,
+                        xh[t].w * 1048576.0f);
+  }
+  float *part = ws + kSkPartials + g * kSkMaxRows;
+  const uint32_t n_pad = (n_batches + 1u) & ~1u; // >= 2; padding batches store nothing
+  float v[RB];
+  uint32_t b = 0;
+  do {
+    q4k_cols_compute<RB>(B0, xl, xh, s0, s1, c, v);
+    q4k_cols_load<RB, false>(B0, qr, b + 2u, n_rows, row_bytes, lane_off, c);
+#pragma unroll
+    for (int r = 0; r < RB; ++r) v[r] = wave_sum_to_lane63(v[r]);
+    if (tid == 63u) {
+#pragma unroll
+      for (int r = 0; r < RB; ++r)
+        if (b * RB + r < n_rows) part[b * RB + r] = v[r];
+    }
+    q4k_cols_compute<RB>(B1, xl, xh, s0, s1, c, v);
+    q4k_cols_load<RB, false>(B1, qr, b + 3u, n_rows, row_bytes, lane_off, c);
+#pragma unroll
+    for (int r = 0; r < RB; ++r) v[r] = wave_sum_to_lane63(v[r]);
+    if (tid == 63u) {
+#pragma unroll
+      for (int r = 0; r < RB; ++r)
+        if ((b + 1u) * RB + r < n_rows) part[(b + 1u) * RB + r] = v[r];
+    }
+    b += 2u;
+  } while (b < n_pad);
+
+  // Lane 63 stored the partials: its release increment orders them before the count.
+  uint32_t last = 0;
+  if (tid == 63u) {
+    const uint32_t prev = __hip_atomic_fetch_add(reinterpret_cast<uint32_t *>(ws), 1u,
+                                                 __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    last = prev == G - 1u ? 1u : 0u;
+  }
+  last = __builtin_amdgcn_readlane(last, 63);
+  if (!last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  if (tid < n_rows) {
+    float s = 0.0f;
+    for (uint32_t k = 0; k < G; ++k)
+      s += __hip_atomic_load(ws + kSkPartials + k * kSkMaxRows + tid, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    y[tid] = s;
+  }
+  if (tid == 0u)
+    __hip_atomic_store(reinterpret_cast<uint32_t *>(ws), 0u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+#define AXH_Q4K_MATVEC_SK(SPW)                                                                   \
+  extern "C" __global__ void __launch_bounds__(64)                                               \
+      axh_q4k_matvec_sk_s##SPW(const uint8_t *__restrict__ q, const float *__restrict__ x,      \
+                               float *__restrict__ y, float *ws, RowsArgs a) {                   \
+    q4k_matvec_sk<SPW>(q, x, y, ws, a.n_rows, a.units_per_row);                                  \
+  }
+
+AXH_Q4K_MATVEC_SK(16)
+
 #define AXH_Q4K_MATVEC_COLS(RB, NW, NT, XF)                                                       \
   extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
       axh_q4k_matvec_cols_r##RB##_w##NW##_n##NT##_x##XF(const uint8_t *__restrict__ q,           \

@@ -71,6 +71,9 @@ struct axh_context {
   std::mutex ops_mu;
   std::unordered_map<std::string, axh_kernel *> ops; // builtin kernels by entry name
   std::unordered_map<uint64_t, uint32_t> occupancy;  // (kernel, lds) -> workgroups per CU
+  // Per-stream device workspaces of the kernels that reduce across
+  // workgroups (split-K matvec): calls on one stream never overlap.
+  std::unordered_map<void *, void *> workspaces;
 };
 
 namespace axh {

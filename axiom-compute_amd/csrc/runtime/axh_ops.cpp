@@ -176,7 +176,41 @@ constexpr uint32_t kQ4kColsMaxRows = 32;
 constexpr uint32_t kQ4kColsMaxSb = 128; // 4 * 128 lanes = 8 waves
 constexpr uint32_t kQ4kColsRb = 4;      // rows per batch of the compiled cols kernels
 
+// Few long rows: K split across one-wave workgroups of kSkSpw superblocks,
+// reduced by the last workgroup through a per-stream workspace (counter and
+// partials).  Every workgroup's device-scope release writes back its XCD's
+// L2, so the split stays at 4..16 workgroups.
+constexpr uint32_t kSkMinSb = 64;  // shorter rows stay on the cols kernel
+constexpr uint32_t kSkMaxSb = 256; // longer rows: more workgroups than pay
+constexpr uint32_t kSkSpw = 16;    // superblocks per workgroup
+constexpr uint32_t kSkMaxGroups = kSkMaxSb / kSkSpw;
+constexpr size_t kSkWorkspaceBytes = (64u + kSkMaxGroups * 32u) * 4u;
+
 static bool device_ptr_ok(const void *p) { return p != nullptr; }
+
+// The workspace of `stream`: allocated and zeroed on first use (which must
+// not be inside a graph capture); the kernels leave its counter at zero.
+// Calls on one stream run in order, so they share it safely.
+static axh_status stream_workspace(axh_context *ctx, hipStream_t stream, void **out) {
+  std::lock_guard<std::mutex> lk(ctx->ops_mu);
+  auto it = ctx->workspaces.find(stream);
+  if (it != ctx->workspaces.end()) {
+    *out = it->second;
+    return ok();
+  }
+  void *p = nullptr;
+  hipError_t e = hipMalloc(&p, kSkWorkspaceBytes);
+  if (e != hipSuccess) return fail(AXH_ERR_BUFFER_ALLOCATION, "workspace hipMalloc failed");
+  e = hipMemset(p, 0, kSkWorkspaceBytes);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    hipFree(p);
+    return fail(AXH_ERR_STAGING_COPY, "workspace initialisation failed");
+  }
+  ctx->workspaces.emplace(stream, p);
+  *out = p;
+  return ok();
+}
 
 } // namespace axh
 
@@ -282,6 +316,16 @@ struct Q4kPlan {
 static axh_status plan_q4k(uint32_t n_rows, uint32_t sb_per_row, const axh_q4_variant *variant,
                            Q4kPlan *p) {
   const uint64_t q_bytes = (uint64_t)n_rows * sb_per_row * 144u;
+  if (!variant && n_rows < kQ4kColsMaxRows && sb_per_row >= kSkMinSb &&
+      sb_per_row <= kSkMaxSb && q_bytes < 0xFFFFFF00ull) {
+    std::snprintf(p->name, sizeof(p->name), "axh_q4k_matvec_sk_s%u", kSkSpw);
+    p->nw = 1;
+    p->lds = 0;
+    p->flat = false;
+    p->units = (sb_per_row + kSkSpw - 1) / kSkSpw;
+    p->args = RowsArgs{n_rows, sb_per_row, kSkSpw, 0};
+    return ok();
+  }
   if (!variant && n_rows < kQ4kColsMaxRows && sb_per_row >= 1 &&
       sb_per_row <= kQ4kColsMaxSb) {
     // Few rows: each row is split across NW waves (4 lanes per superblock).
@@ -359,15 +403,25 @@ axh_status axh_q4k_matvec(axh_context *ctx, const void *q, const float *x, float
     return fail(AXH_ERR_PIPELINE_LAYOUT, "LDS tile exceeds the device limit");
   hipSetDevice(ctx->core->device);
   axh_kernel *k = nullptr;
-  s = builtin_kernel(ctx, p.name, 3, sizeof(RowsArgs), p.nw * 64u, &k);
+  const bool split_k = std::strncmp(p.name, "axh_q4k_matvec_sk_", 18) == 0;
+  s = builtin_kernel(ctx, p.name, split_k ? 4 : 3, sizeof(RowsArgs), p.nw * 64u, &k);
   if (s != AXH_OK) return s;
   uint32_t grid[3] = {p.units, 1, 1};
   if (p.flat) {
     const uint32_t resident = occupancy(ctx, k, p.lds) * ctx->core->cu_count;
     if (resident < grid[0]) grid[0] = resident;
   }
+  const hipStream_t st = pick_stream(ctx, stream);
+  if (split_k) {
+    void *ws = nullptr;
+    s = stream_workspace(ctx, st, &ws);
+    if (s != AXH_OK) return s;
+    void *bufs4[4] = {const_cast<void *>(q), const_cast<float *>(x), y, ws};
+    s = launch_raw(k, grid, bufs4, 4, &p.args, sizeof(p.args), 0, st);
+    return s == AXH_OK ? ok() : s;
+  }
   void *bufs[3] = {const_cast<void *>(q), const_cast<float *>(x), y};
-  s = launch_raw(k, grid, bufs, 3, &p.args, sizeof(p.args), p.lds, pick_stream(ctx, stream));
+  s = launch_raw(k, grid, bufs, 3, &p.args, sizeof(p.args), p.lds, st);
   return s == AXH_OK ? ok() : s;
 }
 

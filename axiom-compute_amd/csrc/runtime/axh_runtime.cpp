@@ -298,6 +298,11 @@ void axh_context_destroy(axh_context *ctx) {
     hipSetDevice(ctx->core->device);
     hipStreamSynchronize(ctx->core->stream);
   }
+  if (!ctx->workspaces.empty()) {
+    hipSetDevice(ctx->core->device);
+    hipDeviceSynchronize(); // workspaces may be in use on caller streams
+    for (auto &kv : ctx->workspaces) hipFree(kv.second);
+  }
   delete ctx; // Core lives on while handles hold it
 }
 

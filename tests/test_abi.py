@@ -112,6 +112,7 @@ def test_kernel_selection_by_shape_and_variant(axc):
     assert name(4096, 56) == "axh_q4k_matvec_flat_r1_w8_p2_n0"
     assert name(4096, 16) == "axh_q4k_matvec_flat_r2_w4_p2_n0"
     assert name(4096, 128) == "axh_q4k_matvec_flat_r1_w16_p2_n0"
+    assert name(1, 256) == "axh_q4k_matvec_sk_s16"  # few long rows: split-K
     assert name(1, 1024) == "axh_q4k_matvec_tiled_r1_w4_p2"
     assert name(4096, 1024) == "axh_q4k_matvec_tiled_r2_w8_p2"
     assert name(4096, 56, axc.Variant(2, 4, 4, 1)) == "axh_q4k_matvec_tiled_r2_w8_p2"  # 56*8 > 4*64
@@ -120,7 +121,9 @@ def test_kernel_selection_by_shape_and_variant(axc):
     assert name(4096, 56, axc.Variant(2, 4, 2, 2)) == "axh_q4k_matvec_flat_r2_w4_p2_n0_x2"
     assert name(4096, 16, axc.Variant(2, 4, 2, 2)) == "axh_q4k_matvec_flat_r2_w4_p2_n0"
     # few rows: the row is split across the workgroup's waves
-    assert name(1, 128) == "axh_q4k_matvec_cols_r4_w8_n0_x1"
+    assert name(1, 128) == "axh_q4k_matvec_sk_s16"
+    assert name(31, 64) == "axh_q4k_matvec_sk_s16"
+    assert name(1, 63) == "axh_q4k_matvec_cols_r4_w4_n0_x1"
     assert name(8, 56) == "axh_q4k_matvec_cols_r4_w4_n0_x1"
     assert name(31, 1) == "axh_q4k_matvec_cols_r4_w1_n0_x1"
     assert name(32, 1) == "axh_q4k_matvec_flat_r2_w4_p2_n0"

@@ -272,3 +272,40 @@ def test_q4km_reference_kernel_many_superblocks(ctx, axc, n):
                               struct.pack("<I", n))
     gpu = struct.unpack("<f", out[2])[0]
     assert O.reference_rel_err(gpu, cpu) < REL_TOL, (n, gpu, float(cpu))
+
+
+# ---- few long rows: split-K across workgroups with a last-workgroup reduction --
+@pytest.mark.parametrize("rows,sb", [(1, 64), (1, 65), (1, 128), (3, 71), (31, 128), (2, 255),
+                                     (1, 256), (31, 200)])
+def test_q4k_split_k_shapes(ctx, axc, rows, sb):
+    """Few rows of 64..256 superblocks take the split-K kernel: ragged last
+    slices, the 16-workgroup limit, and row counts up to 31."""
+    assert axc.q4k_matvec_kernel_name(rows, sb).startswith("axh_q4k_matvec_sk_")
+    _say(f"q4k split-K {rows}x{sb}")
+    q = O.gen_q4k_weights(rows * 17 + sb, rows * sb)
+    x = O.gen_normal_f32(rows + 3 * sb, sb * 256)
+    y = _run_q4k(ctx, q, x, rows, sb)
+    _check_q4k(y, q, x, rows, sb, f"q4k split-K {rows}x{sb}")
+
+
+def test_q4k_split_k_back_to_back_calls_reset_the_counter(ctx):
+    """Consecutive split-K calls with different grids on one stream, without
+    synchronising in between: each must see a zero counter (the last
+    workgroup of the previous call resets it)."""
+    shapes = [(1, 128), (5, 250), (1, 64), (31, 128), (1, 128)]
+    cases = []
+    for i, (rows, sb) in enumerate(shapes):
+        q = O.gen_q4k_weights(900 + i, rows * sb)
+        x = O.gen_normal_f32(950 + i, sb * 256)
+        dq, dx, dy = _to_dev(ctx, q), _to_dev(ctx, x), ctx.alloc(rows * 4)
+        cases.append((rows, sb, q, x, dq, dx, dy))
+    _say("split-K back-to-back")
+    for _ in range(3):
+        for rows, sb, q, x, dq, dx, dy in cases:
+            ctx.q4k_matvec(dq, dx, dy, rows, sb)
+    ctx.synchronize()
+    for rows, sb, q, x, dq, dx, dy in cases:
+        y = np.frombuffer(ctx.download(dy, rows * 4), dtype=np.float32).copy()
+        _check_q4k(y, q, x, rows, sb, f"back-to-back {rows}x{sb}")
+        for b in (dq, dx, dy):
+            b.close()
