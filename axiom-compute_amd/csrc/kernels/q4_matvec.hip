@@ -1381,6 +1381,130 @@ __device__ __forceinline__ void q4_0_matvec_body(const uint8_t *__restrict__ q,
   }
 }
 
+// ---------------------------------------------------------------------------
+// Q4_0 rows of at most 128 blocks (an even count, so every block pair starts
+// 4-byte aligned): lane l owns the block pair [2l, 2l + 2) of every row, with
+// its 64 x values in VGPRs (no LDS staging, no barrier).  A wave takes RB
+// rows at a time (batches strided over the grid), with the next batch's nine
+// dwords per row in flight, and reduces each row with DPP.  Rows past the
+// matrix and idle lanes read zeros through the buffer range check.
+// ---------------------------------------------------------------------------
+template <int RB>
+struct Q4_0ColsBuf {
+  uint4 a[RB], b[RB];
+  uint32_t c[RB];
+};
+
+template <int RB>
+__device__ __forceinline__ void q4_0_cols_load(Q4_0ColsBuf<RB> &B, __amdgpu_buffer_rsrc_t qr,
+                                               uint32_t batch, uint32_t n_rows,
+                                               uint32_t row_bytes, uint32_t lane_off) {
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const uint32_t row = batch * RB + (uint32_t)r;
+    const uint32_t off =
+        (row < n_rows && lane_off != kQ4kColsOob) ? row * row_bytes + lane_off : kQ4kColsOob;
+    B.a[r] = buf_load16<false>(qr, off);
+    B.b[r] = buf_load16<false>(qr, off + 16u);
+    B.c[r] = __builtin_amdgcn_raw_buffer_load_b32(qr, (int)(off + 32u), 0, 0);
+  }
+}
+
+template <int RB>
+__device__ __forceinline__ void q4_0_cols_compute(const Q4_0ColsBuf<RB> &B,
+                                                  const float4 (&x)[2][8], float sa, float sb,
+                                                  float (&v)[RB]) {
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const uint32_t D[9] = {B.a[r].x, B.a[r].y, B.a[r].z, B.a[r].w, B.b[r].x,
+                           B.b[r].y, B.b[r].z, B.b[r].w, B.c[r]};
+    // block A: d = bytes 0-1, qs = bytes 2-17; block B: d = bytes 18-19, qs = bytes 20-35
+    const uint32_t qa[4] = {__builtin_amdgcn_alignbit(D[1], D[0], 16),
+                            __builtin_amdgcn_alignbit(D[2], D[1], 16),
+                            __builtin_amdgcn_alignbit(D[3], D[2], 16),
+                            __builtin_amdgcn_alignbit(D[4], D[3], 16)};
+    float alo = 0.0f, ahi = 0.0f, blo = 0.0f, bhi = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      q4k_dword(qa[t], x[0][t], x[0][4 + t], alo, ahi);
+      q4k_dword(D[5 + t], x[1][t], x[1][4 + t], blo, bhi);
+    }
+    v[r] = __builtin_fmaf(f16_to_f32(D[0] & 0xFFFFu), __builtin_fmaf(-8.0f, sa, alo + ahi),
+                          f16_to_f32(D[4] >> 16) * __builtin_fmaf(-8.0f, sb, blo + bhi));
+  }
+}
+
+template <int RB>
+__device__ __forceinline__ void q4_0_matvec_cols(const uint8_t *__restrict__ q,
+                                                 const float *__restrict__ x,
+                                                 float *__restrict__ y, uint32_t n_rows,
+                                                 uint32_t nb) {
+  const uint32_t lane = threadIdx.x, G = gridDim.x;
+  const uint32_t n_batches = (n_rows + RB - 1) / RB;
+  uint32_t b = blockIdx.x;
+  if (b >= n_batches) return;
+  // The host guarantees n_rows * row_bytes < 2^32 - 256 for this kernel.
+  const uint32_t row_bytes = nb * (uint32_t)kQ4_0BlockBytes;
+  const __amdgpu_buffer_rsrc_t qr = make_rsrc(q, n_rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, nb * 128u);
+  const bool live = 2u * lane < nb;
+  const uint32_t lane_off = live ? lane * 36u : kQ4kColsOob;
+  const uint32_t x_off = live ? lane * 256u : nb * 128u; // idle lanes read zeros
+
+  float4 xv[2][8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) xv[h][t] = buf_loadf4(xr, x_off + 128u * h + 16u * (uint32_t)t);
+  __builtin_amdgcn_sched_barrier(0);
+  Q4_0ColsBuf<RB> B0, B1;
+  q4_0_cols_load<RB>(B0, qr, b, n_rows, row_bytes, lane_off);
+  __builtin_amdgcn_sched_barrier(0);
+  q4_0_cols_load<RB>(B1, qr, b + G, n_rows, row_bytes, lane_off);
+  __builtin_amdgcn_sched_barrier(0);
+  // low nibbles (elements 0..15 of a block) against x * 2^24, high against x * 2^20
+  float sa = 0.0f, sb = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const float f = t < 4 ? 16777216.0f : 1048576.0f;
+    sa += (xv[0][t].x + xv[0][t].y) + (xv[0][t].z + xv[0][t].w);
+    sb += (xv[1][t].x + xv[1][t].y) + (xv[1][t].z + xv[1][t].w);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      xv[h][t] = make_float4(xv[h][t].x * f, xv[h][t].y * f, xv[h][t].z * f, xv[h][t].w * f);
+  }
+  const uint32_t n_mine = (n_batches - b + G - 1u) / G;
+  const uint32_t n_pad = (n_mine + 1u) & ~1u;
+  float v[RB];
+  uint32_t i = 0;
+  do { // n_pad >= 2: this workgroup has at least one batch
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      Q4_0ColsBuf<RB> &B = half ? B1 : B0;
+      q4_0_cols_compute<RB>(B, xv, sa, sb, v);
+      const uint32_t cur = b + (uint32_t)half * G;
+      q4_0_cols_load<RB>(B, qr, b + (2u + (uint32_t)half) * G, n_rows, row_bytes, lane_off);
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const float sres = wave_sum_to_lane63(v[r]);
+        const uint32_t row = cur * RB + (uint32_t)r;
+        if (lane == 63u && row < n_rows) y[row] = sres;
+      }
+    }
+    b += 2u * G;
+    i += 2u;
+  } while (i < n_pad);
+}
+
+#define AXH_Q4_0_MATVEC_COLS(RB)                                                                 \
+  extern "C" __global__ void __launch_bounds__(64)                                               \
+      axh_q4_0_matvec_cols_r##RB(const uint8_t *__restrict__ q, const float *__restrict__ x,     \
+                                 float *__restrict__ y, RowsArgs a) {                            \
+    q4_0_matvec_cols<RB>(q, x, y, a.n_rows, a.units_per_row);                                    \
+  }
+
+AXH_Q4_0_MATVEC_COLS(1)
+
 #define AXH_Q4_0_MATVEC(RPW, NW)                                                                 \
   extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
       axh_q4_0_matvec_r##RPW##_w##NW(const uint8_t *__restrict__ q,                              \

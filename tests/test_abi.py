@@ -227,3 +227,15 @@ def test_kquant_kernel_selection(axc):
                 name(*bad)
     for k in ("axh_q5k_dequant", "axh_q6k_dequant", "axh_f32_to_f16"):
         assert k.encode() in co
+
+
+def test_q4_0_kernel_selection(axc):
+    """Q4_0: the column kernel for rows of at most 128 blocks (even count) by
+    default; the LDS-staged kernels for odd or longer rows and on request."""
+    name = axc.q4_0_matvec_kernel_name
+    assert name(256, 128) == "axh_q4_0_matvec_cols_r1"
+    assert name(4096, 2) == "axh_q4_0_matvec_cols_r1"
+    assert name(256, 127).startswith("axh_q4_0_matvec_r")
+    assert name(256, 130).startswith("axh_q4_0_matvec_r")
+    assert name(256, 128, axc.Variant(1, 1, 0, 0)) == "axh_q4_0_matvec_r1_w1"
+    assert b"axh_q4_0_matvec_cols_r1" in axc.builtin_code_object()
