@@ -98,7 +98,8 @@ _lib: Optional[ctypes.CDLL] = None
 
 class _MatmulVariant(ctypes.Structure):
     _fields_ = [("kind", ctypes.c_uint32), ("waves_per_workgroup", ctypes.c_uint32),
-                ("col_tiles", ctypes.c_uint32), ("prefetch", ctypes.c_uint32)]
+                ("col_tiles", ctypes.c_uint32), ("prefetch", ctypes.c_uint32),
+                ("row_tiles", ctypes.c_uint32)]
 
 
 class _GgufTensorInfo(ctypes.Structure):
@@ -268,15 +269,18 @@ def q4k_matvec_kernel_name(n_rows: int, sb_per_row: int,
 @dataclass(frozen=True)
 class MatmulVariant:
     """Strategy holes of the batched matmul kernels (0 = default).  kind: 1
-    LDS-tiled, 2 register A, 3 K-split."""
+    LDS-tiled, 2 register A, 3 K-split, 4 streaming, 5 K-split tile
+    (row_tiles is kind 5's only)."""
 
     kind: int = 0
     waves_per_workgroup: int = 0
     col_tiles: int = 0
     prefetch: int = 0
+    row_tiles: int = 0
 
     def _c(self) -> _MatmulVariant:
-        return _MatmulVariant(self.kind, self.waves_per_workgroup, self.col_tiles, self.prefetch)
+        return _MatmulVariant(self.kind, self.waves_per_workgroup, self.col_tiles, self.prefetch,
+                              self.row_tiles)
 
 
 def compiled_matmul_variants() -> list[MatmulVariant]:
@@ -285,7 +289,8 @@ def compiled_matmul_variants() -> list[MatmulVariant]:
     for i in range(lib.axh_q4k_matmul_variant_count()):
         v = _MatmulVariant()
         _check(lib.axh_q4k_matmul_variant_at(i, ctypes.byref(v)))
-        out.append(MatmulVariant(v.kind, v.waves_per_workgroup, v.col_tiles, v.prefetch))
+        out.append(MatmulVariant(v.kind, v.waves_per_workgroup, v.col_tiles, v.prefetch,
+                                 v.row_tiles))
     return out
 
 

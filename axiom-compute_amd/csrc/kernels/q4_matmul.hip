@@ -12,7 +12,12 @@
 // common_helpers.rs:437-454) and then rounded once to f16 (RN_f16(w32)).
 // f16 x f16 products are exact in the f32 accumulators of the MFMA.
 //
-// Three kernel kinds (selected per batch size by the runtime):
+// Five kernel kinds (the runtime picks per batch size; the others stay
+// reachable as strategy variants):
+//   * K-split tile (axh_q4k_matmul_kx_...; the default up to 128 columns):
+//     the waves of a workgroup split K, each streaming raw weight bytes and
+//     X through a private LDS ring filled by coalesced direct-to-LDS loads;
+//     see q4k_matmul_kx;
 //   * LDS-tiled (axh_q4k_matmul_w{W}_n{NT}): a workgroup of W waves owns
 //     TM = 32*W rows and TN = 16*NT columns of Y; per 128-wide K step (half a
 //     superblock) every thread dequantises one quarter superblock (32 qs
@@ -20,10 +25,13 @@
 //     threads copy the X tile [TN][128] into LDS, and each wave runs
 //     v_mfma_f32_16x16x32_f16 over its 32 x TN sub-tile while the next
 //     step's global loads are in flight;
-//   * register-A (axh_q4k_matmul_rf_...): each lane dequantises exactly the
-//     A fragments it feeds the MFMA, X is double-buffered in LDS;
-//   * K-split (axh_q4k_matmul_ks_...): for small batches, the waves of a
-//     workgroup share one 32-row tile and split K, summing in LDS.
+//   * register-A (axh_q4k_matmul_rf_...; the default beyond 128 columns):
+//     each lane dequantises exactly the A fragments it feeds the MFMA, X is
+//     double-buffered in LDS;
+//   * K-split (axh_q4k_matmul_ks_...): the waves of a workgroup share one
+//     32-row tile and split K, summing in LDS;
+//   * streaming (axh_q4k_matmul_st_...): persistent, 16 columns of the whole
+//     K staged once in LDS.
 // LDS rows are padded to 136 halves (272 bytes) so that 16 lanes reading
 // 16-byte fragments of 16 consecutive rows hit 64 distinct banks.
 #include "q4_common.h"
@@ -676,9 +684,203 @@ __device__ __forceinline__ void q4k_matmul_st(const uint8_t *__restrict__ q,
   }
 }
 
+// ---------------------------------------------------------------------------
+// K-split tile variant (kind 5): a workgroup of KS waves owns a TM = 16*RT
+// by TN = 16*NT tile of Y, and every wave runs the whole tile over its share
+// of K: wave w takes the 64-wide chunk c = w % 4 of superblocks w/4, w/4 +
+// KS/4, ... (from a per-workgroup start, see below).  Each lane dequantises
+// exactly the A fragments it feeds (row lane%16 of each of the RT row tiles;
+// the 8 qs bytes [32c + 8g, 32c + 8g + 8), g = lane/16, hold the fragment of
+// sub-block 2c in their low nibbles and that of 2c+1 in their high nibbles),
+// so one dequantised fragment feeds NT MFMAs.
+//
+// Operands reach the wave through a private ring of PF LDS buffers filled by
+// direct-to-LDS buffer loads (16 bytes per lane, no VGPRs), laid out so that
+// the global reads are coalesced: a fragment's 16 lanes read 16 different
+// rows (weights) or columns (X), which as direct loads would touch 4 cache
+// lines per 4 lanes.  X instruction (kk, t) covers columns 16t..16t+15 and
+// k = 32kk..32kk+31 of the chunk: lane 4c' + j loads 16 bytes (8 k) of column
+// c' (64 contiguous bytes per lane quad), with the piece rotated by c'/4 so
+// that the fragment reads (lane (n, g): column n, piece g) hit distinct
+// banks.  Weight piece 3r + {0, 1, 2} is row r's header or its two 16-byte
+// halves of the chunk's 32 qs bytes.  A wave waits only for its own loads
+// (the load counter), so there is no barrier until the end, when all KS
+// partial tiles go to LDS and wave w sums tiles w, w + KS, ... in wave order
+// (deterministic) and stores them.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <int RT, int NT>
+struct KxLayout {
+  static constexpr int kX = 2 * NT;                  // X instructions per superblock step
+  static constexpr int kW = (48 * RT + 63) / 64;     // weight instructions per step
+  static constexpr int kPerStep = kX + kW;           // 16-byte-per-lane loads (1 KiB each)
+};
+
+__device__ __forceinline__ uint32_t kx_xrot(uint32_t col) { return (col >> 2) & 3u; }
+
+template <int RT, int NT, int KS, int PF>
+__device__ __forceinline__ void q4k_matmul_kx(const uint8_t *__restrict__ q,
+                                              const uint16_t *__restrict__ x,
+                                              float *__restrict__ y, const MatmulArgs a,
+                                              f32x4_t *lds) {
+  static_assert(KS % 4 == 0, "each wave keeps one 64-wide chunk of the superblocks it visits");
+  using L = KxLayout<RT, NT>;
+  static_assert(L::kPerStep * (PF - 1) <= 63, "loads in flight must fit the load counter");
+  constexpr uint32_t kSbStride = KS / 4;
+  constexpr int kTiles = RT * NT;
+  constexpr uint32_t kBufSlots = 64u * L::kPerStep; // 16-byte slots per ring buffer
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t c = wave & 3u, sb0 = wave >> 2;
+  const uint32_t fr = lane & 15u, g = lane >> 4;
+  const uint32_t n_rows = a.n_rows, nsb = a.sb_per_row, batch = a.batch;
+  const uint32_t K = nsb * 256u;
+  const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
+  const __amdgpu_buffer_rsrc_t qr = rsrc(q, n_rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t xr = rsrc(x, batch * K * 2u);
+  const uint32_t m0 = blockIdx.x * (16u * RT), n0 = blockIdx.y * (16u * NT);
+  f32x4_t *ring = lds + wave * (uint32_t)PF * kBufSlots;
+
+  // The wave's superblocks sb0 + kSbStride * t, t < n_my, are visited from a
+  // per-workgroup start, so that the workgroups of an XCD (dealt round-robin
+  // to the 8 XCDs) do not all read the same stretch of X at once.
+  const uint32_t n_my = sb0 < nsb ? (nsb - sb0 + kSbStride - 1u) / kSbStride : 0u;
+  const uint32_t rot = n_my ? ((blockIdx.x >> 3) + blockIdx.y) % n_my : 0u;
+
+  // Load roles (fixed per lane).  X: column n0 + 16t + (lane >> 2), piece
+  // (lane - rot(col)) & 3 of the 32-k half kk.  Weights: piece P = 64m + lane
+  // -> row P / 3, part P % 3 (0 header, 1-2 qs halves of the chunk).
+  const uint32_t xc = lane >> 2, xp = ((lane & 3u) - kx_xrot(lane >> 2)) & 3u;
+  uint32_t xoff0[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const uint32_t b = n0 + 16u * (uint32_t)t + xc;
+    xoff0[t] = b < batch ? (b * K + 64u * c + 8u * xp) * 2u : kOob;
+  }
+  uint32_t woff0[L::kW];
+#pragma unroll
+  for (int m = 0; m < L::kW; ++m) {
+    const uint32_t P = 64u * (uint32_t)m + lane, r = P / 3u, part = P - 3u * r;
+    const uint32_t row = m0 + r;
+    woff0[m] = (r < 16u * RT && row < n_rows)
+                   ? row * row_bytes + (part == 0u ? 0u : 16u + 32u * c + 16u * (part - 1u))
+                   : kOob;
+  }
+
+  auto issue = [&](uint32_t j) { // step j -> ring buffer j % PF
+    const bool live = j < n_my;
+    const uint32_t tt = j + rot;
+    const uint32_t sb = sb0 + kSbStride * (tt >= n_my ? tt - n_my : tt);
+    f32x4_t *buf = ring + (j % (uint32_t)PF) * kBufSlots;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const uint32_t off =
+            (xoff0[t] == kOob || !live) ? kOob : xoff0[t] + sb * 512u + 64u * (uint32_t)kk;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void_t *)(buf + (kk * NT + t) * 64), 16,
+                                                 off, 0, 0, 0);
+      }
+#pragma unroll
+    for (int m = 0; m < L::kW; ++m) {
+      const uint32_t off = (woff0[m] == kOob || !live) ? kOob : woff0[m] + sb * 144u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(qr, (lds_void_t *)(buf + (L::kX + m) * 64), 16,
+                                               off, 0, 0, 0);
+    }
+  };
+
+  f32x4_t acc[RT][NT];
+#pragma unroll
+  for (int i = 0; i < RT; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[i][j] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+
+#pragma unroll
+  for (int p = 0; p < PF; ++p) issue((uint32_t)p);
+
+  // Fragment read slots (fixed per lane).
+  const uint32_t xslot = 4u * fr + ((g + kx_xrot(fr)) & 3u);
+  for (uint32_t j = 0; j < n_my; ++j) {
+    // this step's loads are done when at most (PF - 1) steps' loads remain
+    if constexpr (PF == 2)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(L::kPerStep) : "memory");
+    else if constexpr (PF == 3)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * L::kPerStep) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const f32x4_t *buf = ring + (j % (uint32_t)PF) * kBufSlots;
+    uint4 hd[RT];
+    uint2 qw[RT];
+    half8_t xf[2][NT];
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+      const uint32_t r3 = 3u * (16u * (uint32_t)i + fr);
+      const f32x4_t *wp = buf + L::kX * 64 + r3;
+      hd[i] = __builtin_bit_cast(uint4, wp[0]);
+      qw[i] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint8_t *>(wp + 1 + (g >> 1)) +
+                                               8u * (g & 1u));
+    }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) xf[kk][t] = __builtin_bit_cast(half8_t, buf[(kk * NT + t) * 64 + xslot]);
+    // the buffer is refilled only after every read of it has returned
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    issue(j + (uint32_t)PF);
+
+    half8_t af[RT][2];
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+      const float d = f16_to_f32(hd[i].x & 0xFFFFu), dmin = f16_to_f32(hd[i].x >> 16);
+      uint32_t scp, mp;
+      q4k_scale_min_pair(hd[i].y, hd[i].z, hd[i].w, c, &scp, &mp);
+      const float d1s = d * (float)(scp & 0xFFu) * 16777216.0f;
+      const float d2s = d * (float)(scp >> 8) * 1048576.0f;
+      const float m1 = dmin * (float)(mp & 0xFFu), m2 = dmin * (float)(mp >> 8);
+      uint32_t l0, l1, h0, h1, l2, l3, h2, h3;
+      dequant_dword(qw[i].x, d1s, m1, d2s, m2, l0, l1, h0, h1);
+      dequant_dword(qw[i].y, d1s, m1, d2s, m2, l2, l3, h2, h3);
+      af[i][0] = __builtin_bit_cast(half8_t, make_uint4(l0, l1, l2, l3));
+      af[i][1] = __builtin_bit_cast(half8_t, make_uint4(h0, h1, h2, h3));
+    }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+          acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i][kk], xf[kk][t], acc[i][t], 0, 0, 0);
+  }
+
+  // Ring loads past the wave's last step are still landing: drain them, and
+  // let every wave finish with its ring before the LDS is reused.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  // Partial tiles -> LDS as red[wave][tile][lane]; wave w then owns tiles w, w + KS, ...
+#pragma unroll
+  for (int i = 0; i < RT; ++i)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) lds[(wave * kTiles + (uint32_t)(i * NT + t)) * 64u + lane] = acc[i][t];
+  __syncthreads();
+  for (uint32_t tt = wave; tt < (uint32_t)kTiles; tt += KS) {
+    f32x4_t s = lds[tt * 64u + lane];
+#pragma unroll
+    for (uint32_t w = 1; w < (uint32_t)KS; ++w) s += lds[(w * kTiles + tt) * 64u + lane];
+    const uint32_t i = tt / NT, t = tt - i * NT;
+    const uint32_t b = n0 + 16u * t + fr;
+    const uint32_t r0 = m0 + 16u * i + 4u * g;
+    if (b >= batch) continue;
+    float *dst = y + (size_t)b * n_rows + r0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (r0 + e < n_rows) dst[e] = s[e];
+  }
+}
+
 } // namespace
 
-#define AXH_Q4K_MATMUL(W, NT)                                                                    \
+#define AXH_Q4K_MATMUL(W, NT)                                                              \
   extern "C" __global__ void __launch_bounds__(W * 64)                                           \
       axh_q4k_matmul_w##W##_n##NT(const uint8_t *__restrict__ q, const uint16_t *__restrict__ x, \
                                   float *__restrict__ y, MatmulArgs a) {                         \
@@ -728,3 +930,21 @@ AXH_Q4K_MATMUL_ST(8, 2, 4)
 AXH_Q4K_MATMUL_ST(8, 2, 2)
 AXH_Q4K_MATMUL_ST(16, 4, 2)
 AXH_Q4K_MATMUL_ST(16, 4, 4)
+
+#define AXH_Q4K_MATMUL_KX(RT, NT, KS, PF)                                                        \
+  extern "C" __global__ void __launch_bounds__(KS * 64)                                          \
+      axh_q4k_matmul_kx_r##RT##_n##NT##_k##KS##_p##PF(const uint8_t *__restrict__ q,             \
+                                                      const uint16_t *__restrict__ x,            \
+                                                      float *__restrict__ y, MatmulArgs a) {     \
+    extern __shared__ f32x4_t axh_red_dyn[];                                                     \
+    q4k_matmul_kx<RT, NT, KS, PF>(q, x, y, a, axh_red_dyn);                                      \
+  }
+
+AXH_Q4K_MATMUL_KX(4, 8, 4, 2)
+AXH_Q4K_MATMUL_KX(2, 8, 4, 2)
+AXH_Q4K_MATMUL_KX(4, 4, 4, 2)
+AXH_Q4K_MATMUL_KX(4, 4, 4, 3)
+AXH_Q4K_MATMUL_KX(8, 4, 4, 2)
+AXH_Q4K_MATMUL_KX(4, 2, 4, 2)
+AXH_Q4K_MATMUL_KX(4, 2, 4, 3)
+AXH_Q4K_MATMUL_KX(4, 1, 4, 3)

@@ -40,13 +40,18 @@ struct MatmulArgs {
 //   kind 4 (streaming)  axh_q4k_matmul_st_w{W}_k{W/4}_p{PF}: persistent waves stream 16-row
 //                       tiles against 16 columns staged in LDS, W/4 waves splitting each
 //                       tile's K (col_tiles is 1).
+//   kind 5 (K-split tile) axh_q4k_matmul_kx_r{RT}_n{NT}_k{W}_p{PF}: a 16*RT x 16*NT tile per
+//                       workgroup, its W waves splitting K by 64-wide superblock chunks,
+//                       register A, X straight from global memory, PF superblocks in flight.
 struct MatmulVariant {
-  uint32_t kind, w, nt, pf;
+  uint32_t kind, w, nt, pf, rt; // rt: row tiles (kind 5 only)
 };
 constexpr MatmulVariant kQ4kMatmulVariants[] = {
-    {1, 1, 1, 1}, {1, 2, 2, 1}, {1, 4, 4, 1}, {1, 4, 8, 1}, {2, 4, 4, 2},
-    {2, 4, 8, 1}, {3, 4, 1, 2}, {3, 8, 1, 1}, {3, 4, 2, 2}, {3, 8, 2, 1},
-    {4, 4, 1, 4}, {4, 8, 1, 4}, {4, 8, 1, 2}, {4, 16, 1, 2}, {4, 16, 1, 4}};
+    {1, 1, 1, 1, 0},  {1, 2, 2, 1, 0},  {1, 4, 4, 1, 0},  {1, 4, 8, 1, 0},  {2, 4, 4, 2, 0},
+    {2, 4, 8, 1, 0},  {3, 4, 1, 2, 0},  {3, 8, 1, 1, 0},  {3, 4, 2, 2, 0},  {3, 8, 2, 1, 0},
+    {4, 4, 1, 4, 0},  {4, 8, 1, 4, 0},  {4, 8, 1, 2, 0},  {4, 16, 1, 2, 0}, {4, 16, 1, 4, 0},
+    {5, 4, 8, 2, 4},  {5, 4, 8, 2, 2},  {5, 4, 4, 2, 4},  {5, 4, 4, 3, 4},  {5, 4, 4, 2, 8},
+    {5, 4, 2, 2, 4},  {5, 4, 2, 3, 4},  {5, 4, 1, 3, 4}};
 constexpr uint32_t kMatmulOob = 0xFFFFFF00u; // the kernels' out-of-range offset
 
 struct MatvecVariant {
@@ -716,19 +721,26 @@ axh_status axh_q4_0_matvec(axh_context *ctx, const void *q, const float *x, floa
   return s == AXH_OK ? ok() : s;
 }
 
-// Defaults from on-device sweeps at 14336 x 4096 (K-split while the batch
-// fits one or two 16-column tiles, LDS tiles in the middle, register A for
-// large batches).
-// Kind 4 stages 16 activation columns of the whole K in LDS.
-constexpr uint32_t kStreamMaxSb = 18; // 16 x (18*256 + 8) halves = 147,712 B
+// Defaults from on-device sweeps at 14336 x 4096: the K-split tile kind with
+// the batch in one column group up to 128 columns, register A beyond.
+
+// Kind 5 LDS: each wave's ring of `pf` buffers, one 1 KiB slot row per
+// 16-byte-per-lane load of a step (2*nt for X, ceil(48*rt/64) for the
+// weights), reused at the end for the waves' partial tiles (1 KiB per tile).
+static uint32_t kx_lds_bytes(const MatmulVariant &v) {
+  const uint32_t ring = v.w * v.pf * (2u * v.nt + (48u * v.rt + 63u) / 64u);
+  const uint32_t red = v.w * v.rt * v.nt;
+  return (ring > red ? ring : red) * 1024u;
+}
 
 static MatmulVariant q4k_matmul_default(uint32_t n_rows, uint32_t batch, uint32_t nsb) {
   (void)n_rows;
-  if (batch <= 16 && nsb <= kStreamMaxSb) return {4, 16, 1, 2};
-  if (batch <= 16) return {3, 8, 1, 1};
-  if (batch <= 32) return {3, 8, 2, 1};
-  if (batch <= 128) return {1, 4, 4, 1};
-  return {2, 4, 8, 1};
+  (void)nsb;
+  if (batch <= 16) return {5, 4, 1, 3, 4};
+  if (batch <= 32) return {5, 4, 2, 2, 4};
+  if (batch <= 64) return {5, 4, 4, 2, 4};
+  if (batch <= 128) return {5, 4, 8, 2, 4};
+  return {2, 4, 8, 1, 0};
 }
 
 uint32_t axh_q4k_matmul_variant_count(void) {
@@ -742,6 +754,7 @@ axh_status axh_q4k_matmul_variant_at(uint32_t i, axh_q4_matmul_variant *out) {
   out->waves_per_workgroup = kQ4kMatmulVariants[i].w;
   out->col_tiles = kQ4kMatmulVariants[i].nt;
   out->prefetch = kQ4kMatmulVariants[i].pf;
+  out->row_tiles = kQ4kMatmulVariants[i].rt;
   return ok();
 }
 
@@ -754,9 +767,17 @@ static axh_status plan_q4k_matmul(uint32_t n_rows, uint32_t sb_per_row, uint32_t
     if (variant->waves_per_workgroup) want.w = variant->waves_per_workgroup;
     if (variant->col_tiles) want.nt = variant->col_tiles;
     if (variant->prefetch) want.pf = variant->prefetch;
+    if (variant->row_tiles) {
+      if (want.kind != 5)
+        return fail(AXH_ERR_INVALID_ARGUMENT, "row_tiles is a hole of matmul kind 5 only");
+      want.rt = variant->row_tiles;
+    }
   }
+  if (want.kind != 5) want.rt = 0;
+  else if (want.rt == 0) want.rt = 4;
   for (const MatmulVariant &v : kQ4kMatmulVariants)
-    if (v.kind == want.kind && v.w == want.w && v.nt == want.nt && v.pf == want.pf) {
+    if (v.kind == want.kind && v.w == want.w && v.nt == want.nt && v.pf == want.pf &&
+        v.rt == want.rt) {
       *out = v;
       if (v.kind == 1)
         std::snprintf(name, cap, "axh_q4k_matmul_w%u_n%u", v.w, v.nt);
@@ -764,8 +785,10 @@ static axh_status plan_q4k_matmul(uint32_t n_rows, uint32_t sb_per_row, uint32_t
         std::snprintf(name, cap, "axh_q4k_matmul_rf_w%u_n%u_p%u_x1", v.w, v.nt, v.pf);
       else if (v.kind == 3)
         std::snprintf(name, cap, "axh_q4k_matmul_ks_k%u_n%u_p%u", v.w, v.nt, v.pf);
-      else
+      else if (v.kind == 4)
         std::snprintf(name, cap, "axh_q4k_matmul_st_w%u_k%u_p%u", v.w, v.w / 4u, v.pf);
+      else
+        std::snprintf(name, cap, "axh_q4k_matmul_kx_r%u_n%u_k%u_p%u", v.rt, v.nt, v.w, v.pf);
       return ok();
     }
   return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_K matmul variant matches");
@@ -811,11 +834,17 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
   char name[64];
   s = plan_q4k_matmul(n_rows, sb_per_row, batch, variant, &v, name, sizeof(name));
   if (s != AXH_OK) return s;
-  // kind 4 stages 16 activation columns of the whole K in LDS
-  const uint32_t lds = v.kind == 4 ? 16u * (sb_per_row * 256u + 8u) * 2u : 0u;
+  // kind 4 stages 16 activation columns of the whole K in LDS; kind 5 sums the
+  // partial tiles of its waves there (one 16x16 f32 tile = 1 KiB per wave)
+  const uint32_t lds = v.kind == 4 ? 16u * (sb_per_row * 256u + 8u) * 2u
+                       : v.kind == 5 ? kx_lds_bytes(v)
+                                     : 0u;
   if (lds > ctx->core->max_lds)
-    return fail(AXH_ERR_INVALID_ARGUMENT, "streaming matmul: 16 columns of K do not fit LDS");
-  const uint32_t tm = v.kind == 3 ? 32u : v.kind == 4 ? 64u : 32u * v.w; // kind 4: 4 tile slots
+    return fail(AXH_ERR_INVALID_ARGUMENT, "matmul variant needs more LDS than the device has");
+  const uint32_t tm = v.kind == 3   ? 32u
+                      : v.kind == 4 ? 64u // 4 tile slots
+                      : v.kind == 5 ? 16u * v.rt
+                                    : 32u * v.w;
   const uint32_t tn = 16u * v.nt;
   uint64_t gx = (n_rows + tm - 1) / tm;
   const uint64_t gy = (batch + tn - 1) / tn;

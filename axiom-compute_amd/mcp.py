@@ -9,7 +9,7 @@ library's compiled Q4 operations, named like the reference kernels:
 
   q4km_dequant_matvec  holes rows_per_wave, waves_per_workgroup, prefetch, nontemporal
   q4_0_dequant_matvec  holes rows_per_wave, waves_per_workgroup
-  q4k_matmul_f16       holes kind, waves_per_workgroup, col_tiles, prefetch
+  q4k_matmul_f16       holes kind, waves_per_workgroup, col_tiles, prefetch, row_tiles
 
 and a request names a shape ({"n_rows", "units_per_row", "batch"}) instead of
 input byte sizes.  Correctness is a real verdict for every kernel (the
@@ -222,9 +222,9 @@ def check_result(kernel: str, shape: dict, q, x, y, rel_tol: float = DEFAULT_REL
 def default_holes(kernel: str) -> dict:
     """Candidate values of every hole, from the compiled variants (sorted)."""
     if kernel == "q4k_matmul_f16":
-        vs = [(v.kind, v.waves_per_workgroup, v.col_tiles, v.prefetch)
+        vs = [(v.kind, v.waves_per_workgroup, v.col_tiles, v.prefetch, v.row_tiles)
               for v in _axh.compiled_matmul_variants()]
-        names = ("kind", "waves_per_workgroup", "col_tiles", "prefetch")
+        names = ("kind", "waves_per_workgroup", "col_tiles", "prefetch", "row_tiles")
     else:
         kind = "q4k" if kernel == "q4km_dequant_matvec" else "q4_0"
         vs = [(v.rows_per_wave, v.waves_per_workgroup, v.prefetch, v.nontemporal)
@@ -239,7 +239,7 @@ def _variant_obj(kernel: str, a: dict):
     g = lambda k: int(a.get(k, 0))
     if kernel == "q4k_matmul_f16":
         return _axh.MatmulVariant(g("kind"), g("waves_per_workgroup"), g("col_tiles"),
-                                  g("prefetch"))
+                                  g("prefetch"), g("row_tiles"))
     return _axh.Variant(g("rows_per_wave"), g("waves_per_workgroup"), g("prefetch"),
                         g("nontemporal"))
 

@@ -305,10 +305,13 @@ axh_status axh_q4_0_matvec_variant_at(uint32_t i, axh_q4_variant *out);
  * batch = 1 case with f32 weights); multi-row matmul is roadmap there
  * (ROADMAP.md:54-72).  q and x 16-byte aligned, each below 4 GiB. */
 typedef struct axh_q4_matmul_variant {
-    uint32_t kind;                /* 1 LDS-tiled, 2 register A, 3 K-split, 4 streaming; 0 = default */
-    uint32_t waves_per_workgroup; /* kinds 1-2: 32 rows per wave; 3: waves splitting K; 4: waves */
+    uint32_t kind;                /* 1 LDS-tiled, 2 register A, 3 K-split, 4 streaming,
+                                     5 K-split tile; 0 = default */
+    uint32_t waves_per_workgroup; /* kinds 1-2: 32 rows per wave; 3, 5: waves splitting K;
+                                     4: waves */
     uint32_t col_tiles;           /* 16-column MFMA tiles per workgroup */
-    uint32_t prefetch;            /* K steps in flight (kinds 2-3) */
+    uint32_t prefetch;            /* K steps (kind 5: superblocks) in flight (kinds 2-5) */
+    uint32_t row_tiles;           /* kind 5: 16-row MFMA tiles per workgroup; 0 otherwise */
 } axh_q4_matmul_variant;
 axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x, float *y,
                               uint32_t n_rows, uint32_t sb_per_row, uint32_t batch,

@@ -164,14 +164,15 @@ def test_context_without_gpu_reports_typed_error(axc):
 
 
 def test_matmul_kernel_selection(axc):
-    """Defaults per batch (and K: the streaming kind stages 16 columns of the
-    whole K in LDS, up to 18 superblocks per row)."""
+    """Defaults per batch: the K-split tile kind (its LDS ring does not grow
+    with K) with all columns in one group up to 128, register A beyond."""
     name = axc.q4k_matmul_kernel_name
-    assert name(14336, 16, 8) == "axh_q4k_matmul_st_w16_k4_p2"
-    assert name(14336, 16, 16) == "axh_q4k_matmul_st_w16_k4_p2"
-    assert name(4096, 56, 8) == "axh_q4k_matmul_ks_k8_n1_p1"  # K = 14336: no LDS room
-    assert name(14336, 16, 32) == "axh_q4k_matmul_ks_k8_n2_p1"
-    assert name(14336, 16, 128) == "axh_q4k_matmul_w4_n4"
+    assert name(14336, 16, 8) == "axh_q4k_matmul_kx_r4_n1_k4_p3"
+    assert name(14336, 16, 16) == "axh_q4k_matmul_kx_r4_n1_k4_p3"
+    assert name(4096, 56, 8) == "axh_q4k_matmul_kx_r4_n1_k4_p3"
+    assert name(14336, 16, 32) == "axh_q4k_matmul_kx_r4_n2_k4_p2"
+    assert name(14336, 16, 64) == "axh_q4k_matmul_kx_r4_n4_k4_p2"
+    assert name(14336, 16, 128) == "axh_q4k_matmul_kx_r4_n8_k4_p2"
     assert name(14336, 16, 512) == "axh_q4k_matmul_rf_w4_n8_p1_x1"
     assert name(14336, 16, 512, axc.MatmulVariant(1, 2, 2, 1)) == "axh_q4k_matmul_w2_n2"
     assert name(14336, 16, 8, axc.MatmulVariant(3, 4, 1, 2)) == "axh_q4k_matmul_ks_k4_n1_p2"
@@ -179,8 +180,13 @@ def test_matmul_kernel_selection(axc):
         name(14336, 16, 8, axc.MatmulVariant(1, 3, 1, 1))
     vs = axc.compiled_matmul_variants()
     assert len(set(vs)) == len(vs) >= 6
-    assert {v.kind for v in vs} == {1, 2, 3, 4}
+    assert {v.kind for v in vs} == {1, 2, 3, 4, 5}
     assert name(14336, 16, 8, axc.MatmulVariant(4, 4, 1, 4)) == "axh_q4k_matmul_st_w4_k1_p4"
+    assert name(14336, 16, 128, axc.MatmulVariant(5, 4, 8, 2, 4)) == \
+        "axh_q4k_matmul_kx_r4_n8_k4_p2"
+    assert all((v.row_tiles > 0) == (v.kind == 5) for v in vs)
+    with pytest.raises(axc.DispatchError):  # row tiles are kind 5's only
+        name(14336, 16, 8, axc.MatmulVariant(4, 4, 1, 4, 2))
     co = axc.builtin_code_object()
     for v in vs:
         assert name(64, 16, 64, v).startswith("axh_q4k_matmul_")
