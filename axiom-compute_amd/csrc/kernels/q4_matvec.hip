@@ -329,26 +329,41 @@ AXH_Q4K_MATVEC_TILED(2, 8, 2)
 constexpr uint32_t kQ4kFlatSbFloats = 272; // LDS floats per superblock of x (256 + pad)
 constexpr uint32_t kWaitXMinSb = 32;       // rows this long wait for x before prefetching
 
-__device__ __forceinline__ void q4k_flat_stage(const float *__restrict__ x, float *xs, float *ss,
-                                               uint32_t si, const float4 (&v)[8]) {
-  const uint32_t sb = si >> 3, j = si & 7u, c = j >> 1, part = j & 1u;
-  const float scale = part ? 1048576.0f : 16777216.0f;
-  float *dst = xs + sb * kQ4kFlatSbFloats + part * 128u + 4u * c;
-  float sum = 0.0f;
+// Coalesced x staging for the persistent kernels: float4 f = tid + i * NT
+// (NT threads, i < 8 * XP) of x, so consecutive lanes read consecutive 16
+// bytes.  (One 32-float sub-block per thread instead puts every lane of a
+// load on its own cache line, 4x the address-unit work of a coalesced load,
+// and the 8 loads of a lane revisit each line after the wave's other lanes
+// have filled L1.)  Float4 f is element 4w of superblock f / 64, w = f % 64:
+// chunk c = w / 16, part (high nibbles) = (w / 8) & 1, group t = w & 7, and
+// the 8 lanes 8m..8m+7 of a load hold one whole sub-block (f / 8), whose sum
+// they form with DPP inside their half-row.
+template <int NT, int XP>
+__device__ __forceinline__ void q4k_flat_load_xc(__amdgpu_buffer_rsrc_t xr, uint32_t tid,
+                                                 float4 (&v)[8 * XP]) {
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const float4 a = v[t];
-    sum += (a.x + a.y) + (a.z + a.w);
-    *reinterpret_cast<float4 *>(dst + (uint32_t)t * 16u) =
-        make_float4(a.x * scale, a.y * scale, a.z * scale, a.w * scale);
-  }
-  ss[si] = sum;
+  for (int i = 0; i < 8 * XP; ++i) v[i] = buf_loadf4(xr, (tid + (uint32_t)i * NT) * 16u);
 }
 
-__device__ __forceinline__ void q4k_flat_load_x(__amdgpu_buffer_rsrc_t xr, uint32_t si,
-                                                float4 (&v)[8]) {
+template <int NT, int XP>
+__device__ __forceinline__ void q4k_flat_stage_xc(float *xs, float *ss, uint32_t tid, uint32_t nsb,
+                                                  const float4 (&v)[8 * XP]) {
 #pragma unroll
-  for (int t = 0; t < 8; ++t) v[t] = buf_loadf4(xr, si * 128u + 16u * (uint32_t)t);
+  for (int i = 0; i < 8 * XP; ++i) {
+    const uint32_t f = tid + (uint32_t)i * NT;
+    const float4 a = v[i];
+    float s = (a.x + a.y) + (a.z + a.w);
+    s += dpp_mov<0xB1>(s);  // quad_perm [1,0,3,2]
+    s += dpp_mov<0x4E>(s);  // quad_perm [2,3,0,1]
+    s += dpp_mov<0x141>(s); // row_half_mirror: the 8-lane sum in every lane
+    if (f < nsb * 64u) {    // whole 8-lane groups: NT and 64 * nsb are multiples of 8
+      const uint32_t sb = f >> 6, w = f & 63u, c = w >> 4, part = (w >> 3) & 1u, t = w & 7u;
+      const float scale = part ? 1048576.0f : 16777216.0f;
+      *reinterpret_cast<float4 *>(xs + sb * kQ4kFlatSbFloats + part * 128u + 16u * t + 4u * c) =
+          make_float4(a.x * scale, a.y * scale, a.z * scale, a.w * scale);
+      if ((f & 7u) == 0u) ss[f >> 3] = s;
+    }
+  }
 }
 
 // kQ5: Q5_K superblocks (the qh runs are loaded too).
@@ -453,17 +468,11 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
   float *ss = lds + nsb * kQ4kFlatSbFloats;
 
   // Prologue: x requests first, then (for long rows once x has arrived) the
-  // weight prefetch, then the LDS writes.  XP
-  // sub-blocks of x (32 floats each) per thread: the host launches this
-  // kernel only when nsb * 8 <= XP * NW * 64.
-  const uint32_t nsub = nsb * 8u;
-  uint32_t my_sub[XP];
-  float4 xv[XP][8];
-#pragma unroll
-  for (int k = 0; k < XP; ++k) {
-    my_sub[k] = min(tid + (uint32_t)k * (NW * 64u), nsub - 1u);
-    q4k_flat_load_x(xr, my_sub[k], xv[k]);
-  }
+  // weight prefetch, then the LDS writes.  8 * XP float4 of x per thread (a
+  // sub-block's worth per XP): the host launches this kernel only when
+  // nsb * 8 <= XP * NW * 64.
+  float4 xv[8 * XP];
+  q4k_flat_load_xc<NW * 64, XP>(xr, tid, xv);
   // For long rows, let x arrive before the weight prefetch goes out: every
   // wave of the grid issues its prefetch at once, and x requests queued
   // behind that traffic arrive later than the first weights would (measured:
@@ -482,9 +491,7 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
     if (++l_it == n_it) { l_it = 0; ++l_pi; }
   }
   __builtin_amdgcn_sched_barrier(0);
-  // Threads beyond nsub rewrite the last sub-block with the same values.
-#pragma unroll
-  for (int k = 0; k < XP; ++k) q4k_flat_stage(x, xs, ss, my_sub[k], xv[k]);
+  q4k_flat_stage_xc<NW * 64, XP>(xs, ss, tid, nsb, xv);
   __syncthreads();
 
   float acc[RPW];
@@ -623,23 +630,29 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
 constexpr uint32_t kQ6kSbBytes = 210;
 constexpr uint32_t kQ6kSbFloats = 272;
 
-__device__ __forceinline__ void q6k_stage(float *xs, float *ss, uint32_t si,
-                                          const float4 (&v)[8]) {
-  const uint32_t sb = si >> 3, j = si & 7u, n = j >> 2, p = j & 3u;
+// Coalesced as q4k_flat_stage_xc: float4 f holds elements 4w..4w+3 of
+// superblock f / 64 (w = f % 64), i.e. 128n + 32p + 16h + 4i with n = w / 32,
+// p = (w / 8) & 3, h = (w / 4) & 1, i = w & 3; a lane quad holds one
+// 16-element group (n, p, h), summed with DPP.
+template <int NT, int XP>
+__device__ __forceinline__ void q6k_stage_xc(float *xs, float *ss, uint32_t tid, uint32_t nsb,
+                                             const float4 (&v)[8 * XP]) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const uint32_t c = 2u * n + (uint32_t)h;
-    float *dst = xs + sb * kQ6kSbFloats + 64u * p + 4u * c;
-    float sum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float4 a = v[4 * h + i];
-      sum += (a.x + a.y) + (a.z + a.w);
-      *reinterpret_cast<float4 *>(dst + 16u * (uint32_t)i) =
+  for (int k = 0; k < 8 * XP; ++k) {
+    const uint32_t f = tid + (uint32_t)k * NT;
+    const float4 a = v[k];
+    float s = (a.x + a.y) + (a.z + a.w);
+    s += dpp_mov<0xB1>(s); // quad_perm [1,0,3,2]
+    s += dpp_mov<0x4E>(s); // quad_perm [2,3,0,1]: the quad's sum in every lane
+    if (f < nsb * 64u) {
+      const uint32_t sb = f >> 6, w = f & 63u;
+      const uint32_t n = w >> 5, p = (w >> 3) & 3u, h = (w >> 2) & 1u, i = w & 3u;
+      const uint32_t c = 2u * n + h;
+      *reinterpret_cast<float4 *>(xs + sb * kQ6kSbFloats + 64u * p + 4u * c + 16u * i) =
           make_float4(a.x * 16777216.0f, a.y * 16777216.0f, a.z * 16777216.0f,
                       a.w * 16777216.0f);
+      if (i == 0u) ss[sb * 16u + 4u * c + p] = s;
     }
-    ss[sb * 16u + 4u * c + p] = sum;
   }
 }
 
@@ -734,14 +747,8 @@ __device__ __forceinline__ void q6k_matvec_flat(const uint8_t *__restrict__ q,
 
   // Prologue as in the Q4_K flat kernel: x first, then (for long rows once x
   // has arrived) the weight prefetch, then the LDS writes.
-  const uint32_t nsub = nsb * 8u;
-  uint32_t my_sub[XP];
-  float4 xv[XP][8];
-#pragma unroll
-  for (int k = 0; k < XP; ++k) {
-    my_sub[k] = min(tid + (uint32_t)k * (NW * 64u), nsub - 1u);
-    q4k_flat_load_x(xr, my_sub[k], xv[k]);
-  }
+  float4 xv[8 * XP];
+  q4k_flat_load_xc<NW * 64, XP>(xr, tid, xv);
   __builtin_amdgcn_sched_barrier(0);
   if (nsb >= kWaitXMinSb) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
@@ -755,8 +762,7 @@ __device__ __forceinline__ void q6k_matvec_flat(const uint8_t *__restrict__ q,
     if (++l_it == n_it) { l_it = 0; ++l_pi; }
   }
   __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int k = 0; k < XP; ++k) q6k_stage(xs, ss, my_sub[k], xv[k]);
+  q6k_stage_xc<NW * 64, XP>(xs, ss, tid, nsb, xv);
   __syncthreads();
 
   const uint32_t n = c >> 1, hsel = (c & 1u) * 8u; // scale byte of (n, h): 8n + 2p + h
