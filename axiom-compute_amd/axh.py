@@ -269,8 +269,8 @@ def q4k_matvec_kernel_name(n_rows: int, sb_per_row: int,
 @dataclass(frozen=True)
 class MatmulVariant:
     """Strategy holes of the batched matmul kernels (0 = default).  kind: 1
-    LDS-tiled, 2 register A, 3 K-split, 4 streaming, 5 K-split tile
-    (row_tiles is kind 5's only)."""
+    LDS-tiled, 2 register A, 3 K-split, 4 streaming, 5 K-split tile, 6
+    row-split tile (row_tiles is kinds 5 and 6's only)."""
 
     kind: int = 0
     waves_per_workgroup: int = 0

@@ -100,6 +100,22 @@ __device__ __forceinline__ void dequant_dword(uint32_t w, float d1s, float m1, f
   hi23 = pack_f16(h2, h3);
 }
 
+// Four consecutive rows r0..r0+3 of one output column (the lane's part of a
+// 16x16 MFMA tile): one 16-byte store when all four exist and the address is
+// aligned (y is only required to be 4-byte aligned), else scalar stores.
+// Scalar stores put every lane of a store on its own 4-byte word, 4x the
+// store instructions.
+__device__ __forceinline__ void store_col4(float *ycol, uint32_t r0, uint32_t n_rows, f32x4_t v) {
+  float *dst = ycol + r0;
+  if (r0 + 4u <= n_rows && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0u) {
+    *reinterpret_cast<f32x4_t *>(dst) = v;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (r0 + (uint32_t)e < n_rows) dst[e] = v[e];
+  }
+}
+
 template <int W, int NT>
 __device__ __forceinline__ void q4k_matmul(const uint8_t *__restrict__ q,
                                            const uint16_t *__restrict__ x,
@@ -205,10 +221,7 @@ __device__ __forceinline__ void q4k_matmul(const uint8_t *__restrict__ q,
       const uint32_t b = n0 + 16u * j + (lane & 15u);
       const uint32_t r0 = m0 + wave * 32u + 16u * i + 4u * (lane >> 4);
       if (b >= batch) continue;
-      float *dst = y + (size_t)b * n_rows + r0;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (r0 + e < n_rows) dst[e] = acc[i][j][e];
+      store_col4(y + (size_t)b * n_rows, r0, n_rows, acc[i][j]);
     }
 }
 
@@ -386,10 +399,7 @@ __device__ __forceinline__ void q4k_matmul_rf(const uint8_t *__restrict__ q,
       const uint32_t b = n0 + 16u * j + fr;
       const uint32_t r0 = m0 + wave * 32u + 16u * i + 4u * g;
       if (b >= batch) continue;
-      float *dst = y + (size_t)b * n_rows + r0;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (r0 + e < n_rows) dst[e] = acc[i][j][e];
+      store_col4(y + (size_t)b * n_rows, r0, n_rows, acc[i][j]);
     }
 }
 
@@ -528,10 +538,7 @@ __device__ __forceinline__ void q4k_matmul_ks(const uint8_t *__restrict__ q,
       const uint32_t b = n0 + 16u * j + fr;
       const uint32_t r0 = m0 + 16u * i + 4u * g;
       if (b >= batch) continue;
-      float *dst = y + (size_t)b * n_rows + r0;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (r0 + e < n_rows) dst[e] = acc[i][j][e];
+      store_col4(y + (size_t)b * n_rows, r0, n_rows, acc[i][j]);
     }
 }
 
@@ -670,10 +677,7 @@ __device__ __forceinline__ void q4k_matmul_st(const uint8_t *__restrict__ q,
           }
           const uint32_t b = n0 + fr, r0 = (slot_g + c_rd * slots_total) * 16u + 4u * g;
           if (kpart == 0 && b < batch) {
-            float *dst = y + (size_t)b * n_rows + r0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (r0 + e < n_rows) dst[e] = acc[e];
+            store_col4(y + (size_t)b * n_rows, r0, n_rows, acc);
           }
         }
         acc = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
@@ -871,11 +875,165 @@ __device__ __forceinline__ void q4k_matmul_kx(const uint8_t *__restrict__ q,
     const uint32_t b = n0 + 16u * t + fr;
     const uint32_t r0 = m0 + 16u * i + 4u * g;
     if (b >= batch) continue;
-    float *dst = y + (size_t)b * n_rows + r0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (r0 + e < n_rows) dst[e] = s[e];
+    store_col4(y + (size_t)b * n_rows, r0, n_rows, s);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Row-split tile variant for wide batches (kind 6): a workgroup of W waves
+// owns a TM = 16*RT*W by TN = 16*NT tile of Y; wave w owns rows 16*RT*w ..
+// +16*RT (RT row tiles: every X fragment it reads feeds RT MFMAs) and walks
+// all of K in 64-wide steps (one chunk of a superblock), so no partial sums
+// cross waves.  W = 8 puts two waves on every SIMD, which lets one wave's
+// dequantisation run while the other's MFMAs issue (with a single wave per
+// SIMD the two serialise).  A ring of PF LDS buffers holds, per step, the X
+// tile [TN x 64] (filled cooperatively: wave w issues X instructions w,
+// w + W, ...) and each wave's private weight pieces (per row: the header
+// and the chunk's 32 qs bytes, three 16-byte pieces), all by direct-to-LDS
+// loads laid out as in q4k_matmul_kx (quads read 64 contiguous bytes; X
+// pieces rotated by column/4 so the fragment reads hit distinct banks).  One
+// barrier per step: after it every wave's loads of the step have landed and
+// every wave is done with the buffer of step j - 1, which the loads of step
+// j + PF - 1 refill.
+// ---------------------------------------------------------------------------
+template <int W, int RT, int NT>
+struct RsLayout {
+  static constexpr int kX = 2 * NT;                    // X instructions per step (workgroup)
+  static constexpr int kXPer = kX / W;                 // ... issued by each wave
+  static constexpr int kW = (48 * RT + 63) / 64;       // weight instructions per wave
+  static constexpr int kPerStep = kXPer + kW;          // loads per wave per step
+  static constexpr int kBufSlots = 64 * (kX + W * kW); // 16-byte slots per ring buffer
+};
+
+template <int W, int RT, int NT, int PF>
+__device__ __forceinline__ void q4k_matmul_rs(const uint8_t *__restrict__ q,
+                                              const uint16_t *__restrict__ x,
+                                              float *__restrict__ y, const MatmulArgs a,
+                                              f32x4_t *lds) {
+  using L = RsLayout<W, RT, NT>;
+  static_assert(L::kX % W == 0, "X instructions split evenly over the waves");
+  static_assert(PF >= 2 && PF <= 5 && L::kPerStep * (PF - 1) <= 63,
+                "loads in flight must fit the load counter");
+  constexpr uint32_t TM = 16u * RT * W, TN = 16u * NT;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t fr = lane & 15u, g = lane >> 4;
+  const uint32_t n_rows = a.n_rows, nsb = a.sb_per_row, batch = a.batch;
+  const uint32_t K = nsb * 256u, n_steps = 4u * nsb;
+  const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
+  const __amdgpu_buffer_rsrc_t qr = rsrc(q, n_rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t xr = rsrc(x, batch * K * 2u);
+  const uint32_t m0 = blockIdx.x * TM + wave * (16u * RT), n0 = blockIdx.y * TN;
+
+  // X load role: instruction i = wave + W * u covers k-half kk = i / NT and
+  // column tile t = i % NT; lane 4c' + j loads column 16t + c', piece (j - rot) & 3.
+  const uint32_t xc = lane >> 2, xp = ((lane & 3u) - kx_xrot(lane >> 2)) & 3u;
+  uint32_t xoff0[L::kXPer];
+#pragma unroll
+  for (int u = 0; u < L::kXPer; ++u) {
+    const uint32_t i = wave + (uint32_t)(W * u), kk = i / NT, t = i - kk * NT;
+    const uint32_t b = n0 + 16u * t + xc;
+    xoff0[u] = b < batch ? (b * K + 32u * kk + 8u * xp) * 2u : kOob;
+  }
+  // Weight load role: piece P = 64m + lane -> row P / 3, part P % 3 (0 the
+  // header, 1-2 the 16-byte halves of the chunk's 32 qs bytes).
+  uint32_t woff0[L::kW], wpart[L::kW];
+#pragma unroll
+  for (int m = 0; m < L::kW; ++m) {
+    const uint32_t P = 64u * (uint32_t)m + lane, r = P / 3u;
+    const uint32_t row = m0 + r;
+    wpart[m] = P - 3u * r;
+    woff0[m] = (r < 16u * RT && row < n_rows) ? row * row_bytes : kOob;
+  }
+
+  auto issue = [&](uint32_t j) { // step j -> ring buffer j % PF
+    const bool live = j < n_steps;
+    const uint32_t sb = j >> 2, c = j & 3u;
+    f32x4_t *buf = lds + (j % (uint32_t)PF) * (uint32_t)L::kBufSlots;
+#pragma unroll
+    for (int u = 0; u < L::kXPer; ++u) {
+      const uint32_t i = wave + (uint32_t)(W * u);
+      const uint32_t off = (xoff0[u] == kOob || !live) ? kOob : xoff0[u] + 128u * j;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void_t *)(buf + i * 64u), 16, off, 0, 0, 0);
+    }
+    f32x4_t *wb = buf + (L::kX + wave * L::kW) * 64;
+#pragma unroll
+    for (int m = 0; m < L::kW; ++m) {
+      const uint32_t off =
+          (woff0[m] == kOob || !live)
+              ? kOob
+              : woff0[m] + sb * 144u + (wpart[m] == 0u ? 0u : 16u * wpart[m] + 32u * c);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(qr, (lds_void_t *)(wb + m * 64), 16, off, 0, 0, 0);
+    }
+  };
+
+  f32x4_t acc[RT][NT];
+#pragma unroll
+  for (int i = 0; i < RT; ++i)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[i][t] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+
+#pragma unroll
+  for (int p = 0; p < PF - 1; ++p) issue((uint32_t)p);
+
+  const uint32_t xslot = 4u * fr + ((g + kx_xrot(fr)) & 3u);
+  for (uint32_t j = 0; j < n_steps; ++j) {
+    // own loads of step j landed (PF - 2 later steps may be in flight), then
+    // the barrier: everyone's loads of step j landed, step j - 1 is consumed
+    if constexpr (PF == 2)
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    else if constexpr (PF == 3)
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(L::kPerStep) : "memory");
+    else if constexpr (PF == 4)
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * L::kPerStep) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(3 * L::kPerStep) : "memory");
+    issue(j + (uint32_t)(PF - 1));
+    const f32x4_t *buf = lds + (j % (uint32_t)PF) * (uint32_t)L::kBufSlots;
+    const f32x4_t *wb = buf + (L::kX + wave * L::kW) * 64;
+    half8_t af[RT][2];
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+      const f32x4_t *wp = wb + 3u * (16u * (uint32_t)i + fr);
+      const uint4 hd = __builtin_bit_cast(uint4, wp[0]);
+      const uint2 qw = *reinterpret_cast<const uint2 *>(
+          reinterpret_cast<const uint8_t *>(wp + 1 + (g >> 1)) + 8u * (g & 1u));
+      const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
+      uint32_t scp, mp;
+      q4k_scale_min_pair(hd.y, hd.z, hd.w, j & 3u, &scp, &mp);
+      const float d1s = d * (float)(scp & 0xFFu) * 16777216.0f;
+      const float d2s = d * (float)(scp >> 8) * 1048576.0f;
+      const float m1 = dmin * (float)(mp & 0xFFu), m2 = dmin * (float)(mp >> 8);
+      uint32_t l0, l1, h0, h1, l2, l3, h2, h3;
+      dequant_dword(qw.x, d1s, m1, d2s, m2, l0, l1, h0, h1);
+      dequant_dword(qw.y, d1s, m1, d2s, m2, l2, l3, h2, h3);
+      af[i][0] = __builtin_bit_cast(half8_t, make_uint4(l0, l1, l2, l3));
+      af[i][1] = __builtin_bit_cast(half8_t, make_uint4(h0, h1, h2, h3));
+    }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      half8_t xf[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        xf[t] = __builtin_bit_cast(half8_t, buf[((uint32_t)kk * NT + (uint32_t)t) * 64u + xslot]);
+#pragma unroll
+      for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+          acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i][kk], xf[t], acc[i][t], 0, 0, 0);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // ring loads past the last step
+
+#pragma unroll
+  for (int i = 0; i < RT; ++i)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const uint32_t b = n0 + 16u * t + fr;
+      const uint32_t r0 = m0 + 16u * i + 4u * g;
+      if (b >= batch) continue;
+      store_col4(y + (size_t)b * n_rows, r0, n_rows, acc[i][t]);
+    }
 }
 
 } // namespace
@@ -948,3 +1106,18 @@ AXH_Q4K_MATMUL_KX(8, 4, 4, 2)
 AXH_Q4K_MATMUL_KX(4, 2, 4, 2)
 AXH_Q4K_MATMUL_KX(4, 2, 4, 3)
 AXH_Q4K_MATMUL_KX(4, 1, 4, 3)
+
+#define AXH_Q4K_MATMUL_RS(W, RT, NT, PF)                                                         \
+  extern "C" __global__ void __launch_bounds__(W * 64)                                           \
+      axh_q4k_matmul_rs_w##W##_r##RT##_n##NT##_p##PF(const uint8_t *__restrict__ q,              \
+                                                     const uint16_t *__restrict__ x,             \
+                                                     float *__restrict__ y, MatmulArgs a) {      \
+    extern __shared__ f32x4_t axh_rs_dyn[];                                                      \
+    q4k_matmul_rs<W, RT, NT, PF>(q, x, y, a, axh_rs_dyn);                                        \
+  }
+
+AXH_Q4K_MATMUL_RS(8, 2, 8, 4)
+AXH_Q4K_MATMUL_RS(8, 2, 8, 3)
+AXH_Q4K_MATMUL_RS(4, 4, 8, 4)
+AXH_Q4K_MATMUL_RS(8, 2, 4, 4)
+AXH_Q4K_MATMUL_RS(8, 1, 8, 4)

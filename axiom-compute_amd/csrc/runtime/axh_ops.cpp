@@ -42,7 +42,11 @@ struct MatmulArgs {
 //                       tile's K (col_tiles is 1).
 //   kind 5 (K-split tile) axh_q4k_matmul_kx_r{RT}_n{NT}_k{W}_p{PF}: a 16*RT x 16*NT tile per
 //                       workgroup, its W waves splitting K by 64-wide superblock chunks,
-//                       register A, X straight from global memory, PF superblocks in flight.
+//                       register A, operands through per-wave LDS rings, PF superblocks in
+//                       flight.
+//   kind 6 (row-split tile) axh_q4k_matmul_rs_w{W}_r{RT}_n{NT}_p{PF}: W waves of RT row tiles
+//                       each share an X tile [16*NT x 64] in a PF-deep LDS ring (one barrier
+//                       per 64-wide K step).
 struct MatmulVariant {
   uint32_t kind, w, nt, pf, rt; // rt: row tiles (kind 5 only)
 };
@@ -51,7 +55,8 @@ constexpr MatmulVariant kQ4kMatmulVariants[] = {
     {2, 4, 8, 1, 0},  {3, 4, 1, 2, 0},  {3, 8, 1, 1, 0},  {3, 4, 2, 2, 0},  {3, 8, 2, 1, 0},
     {4, 4, 1, 4, 0},  {4, 8, 1, 4, 0},  {4, 8, 1, 2, 0},  {4, 16, 1, 2, 0}, {4, 16, 1, 4, 0},
     {5, 4, 8, 2, 4},  {5, 4, 8, 2, 2},  {5, 4, 4, 2, 4},  {5, 4, 4, 3, 4},  {5, 4, 4, 2, 8},
-    {5, 4, 2, 2, 4},  {5, 4, 2, 3, 4},  {5, 4, 1, 3, 4}};
+    {5, 4, 2, 2, 4},  {5, 4, 2, 3, 4},  {5, 4, 1, 3, 4},  {6, 8, 8, 4, 2},  {6, 8, 8, 3, 2},
+    {6, 4, 8, 4, 4},  {6, 8, 4, 4, 2},  {6, 8, 8, 4, 1}};
 constexpr uint32_t kMatmulOob = 0xFFFFFF00u; // the kernels' out-of-range offset
 
 struct MatvecVariant {
@@ -722,7 +727,8 @@ axh_status axh_q4_0_matvec(axh_context *ctx, const void *q, const float *x, floa
 }
 
 // Defaults from on-device sweeps at 14336 x 4096: the K-split tile kind with
-// the batch in one column group up to 128 columns, register A beyond.
+// the batch in one column group up to 128 columns; beyond, the row-split kind
+// with the row tile chosen to keep about 224 workgroups (one per CU).
 
 // Kind 5 LDS: each wave's ring of `pf` buffers, one 1 KiB slot row per
 // 16-byte-per-lane load of a step (2*nt for X, ceil(48*rt/64) for the
@@ -733,6 +739,12 @@ static uint32_t kx_lds_bytes(const MatmulVariant &v) {
   return (ring > red ? ring : red) * 1024u;
 }
 
+// Kind 6 LDS: a ring of `pf` buffers, each the X tile (2 * nt instructions of
+// 1 KiB) and every wave's weight pieces (16 * rt rows x 3 pieces of 16 bytes).
+static uint32_t rs_lds_bytes(const MatmulVariant &v) {
+  return v.pf * (2u * v.nt + v.w * ((48u * v.rt + 63u) / 64u)) * 1024u;
+}
+
 static MatmulVariant q4k_matmul_default(uint32_t n_rows, uint32_t batch, uint32_t nsb) {
   (void)n_rows;
   (void)nsb;
@@ -740,7 +752,8 @@ static MatmulVariant q4k_matmul_default(uint32_t n_rows, uint32_t batch, uint32_
   if (batch <= 32) return {5, 4, 2, 2, 4};
   if (batch <= 64) return {5, 4, 4, 2, 4};
   if (batch <= 128) return {5, 4, 8, 2, 4};
-  return {2, 4, 8, 1, 0};
+  if (batch <= 256) return {6, 8, 8, 4, 1};
+  return {6, 8, 8, 3, 2};
 }
 
 uint32_t axh_q4k_matmul_variant_count(void) {
@@ -768,13 +781,13 @@ static axh_status plan_q4k_matmul(uint32_t n_rows, uint32_t sb_per_row, uint32_t
     if (variant->col_tiles) want.nt = variant->col_tiles;
     if (variant->prefetch) want.pf = variant->prefetch;
     if (variant->row_tiles) {
-      if (want.kind != 5)
-        return fail(AXH_ERR_INVALID_ARGUMENT, "row_tiles is a hole of matmul kind 5 only");
+      if (want.kind != 5 && want.kind != 6)
+        return fail(AXH_ERR_INVALID_ARGUMENT, "row_tiles is a hole of matmul kinds 5 and 6 only");
       want.rt = variant->row_tiles;
     }
   }
-  if (want.kind != 5) want.rt = 0;
-  else if (want.rt == 0) want.rt = 4;
+  if (want.kind != 5 && want.kind != 6) want.rt = 0;
+  else if (want.rt == 0) want.rt = want.kind == 5 ? 4u : 2u;
   for (const MatmulVariant &v : kQ4kMatmulVariants)
     if (v.kind == want.kind && v.w == want.w && v.nt == want.nt && v.pf == want.pf &&
         v.rt == want.rt) {
@@ -787,8 +800,10 @@ static axh_status plan_q4k_matmul(uint32_t n_rows, uint32_t sb_per_row, uint32_t
         std::snprintf(name, cap, "axh_q4k_matmul_ks_k%u_n%u_p%u", v.w, v.nt, v.pf);
       else if (v.kind == 4)
         std::snprintf(name, cap, "axh_q4k_matmul_st_w%u_k%u_p%u", v.w, v.w / 4u, v.pf);
-      else
+      else if (v.kind == 5)
         std::snprintf(name, cap, "axh_q4k_matmul_kx_r%u_n%u_k%u_p%u", v.rt, v.nt, v.w, v.pf);
+      else
+        std::snprintf(name, cap, "axh_q4k_matmul_rs_w%u_r%u_n%u_p%u", v.w, v.rt, v.nt, v.pf);
       return ok();
     }
   return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_K matmul variant matches");
@@ -838,12 +853,14 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
   // partial tiles of its waves there (one 16x16 f32 tile = 1 KiB per wave)
   const uint32_t lds = v.kind == 4 ? 16u * (sb_per_row * 256u + 8u) * 2u
                        : v.kind == 5 ? kx_lds_bytes(v)
+                       : v.kind == 6 ? rs_lds_bytes(v)
                                      : 0u;
   if (lds > ctx->core->max_lds)
     return fail(AXH_ERR_INVALID_ARGUMENT, "matmul variant needs more LDS than the device has");
   const uint32_t tm = v.kind == 3   ? 32u
                       : v.kind == 4 ? 64u // 4 tile slots
                       : v.kind == 5 ? 16u * v.rt
+                      : v.kind == 6 ? 16u * v.rt * v.w
                                     : 32u * v.w;
   const uint32_t tn = 16u * v.nt;
   uint64_t gx = (n_rows + tm - 1) / tm;
