@@ -132,6 +132,43 @@ def test_every_variant(ctx, axc):
         _check(y, q, xh, rows, sb, batch, f"variant {v}")
 
 
+@pytest.mark.parametrize("rows,sb,batch", [(1, 1, 1), (37, 7, 129), (130, 2, 15)])
+def test_tile_kinds_on_odd_shapes(ctx, axc, rows, sb, batch):
+    """The K-split and row-split tile kinds (5, 6) at shapes none of their
+    tiles divide: a single row, superblock and column; more superblocks than
+    a wave's ring holds, a column group of 129; rows past one row tile."""
+    q, xh = _inputs(rows * 11 + sb + batch, rows, sb, batch)
+    for v in axc.compiled_matmul_variants():
+        if v.kind not in (5, 6):
+            continue
+        _say(f"matmul odd shape {rows}x{sb} B={batch} variant {v}")
+        y = _run(ctx, q, xh, rows, sb, batch, v)
+        _check(y, q, xh, rows, sb, batch, f"odd {rows}x{sb} B={batch} {v}")
+
+
+@pytest.mark.parametrize("batch", [8, 40, 200])
+def test_output_only_4_byte_aligned(ctx, batch):
+    """y 4 bytes past a 16-byte boundary: the tile stores fall back to single
+    words (the API asks y for 4-byte alignment only); nothing outside y is
+    written."""
+    rows, sb = 70, 2
+    q, xh = _inputs(900 + batch, rows, sb, batch)
+    dq, dx = _dev(ctx, q), _dev(ctx, xh)
+    n = batch * rows
+    dy = ctx.alloc(n * 4 + 32)
+    guard = np.full(n + 8, -7.0, dtype=np.float32)
+    ctx.upload(dy, guard)
+    _say(f"matmul unaligned y B={batch}")
+    ctx.q4k_matmul(dq, dx, dy.ptr + 4, rows, sb, batch)
+    ctx.synchronize()
+    out = np.frombuffer(ctx.download(dy, (n + 8) * 4), dtype=np.float32)
+    for b in (dq, dx, dy):
+        b.close()
+    assert out[0] == -7.0 and np.all(out[n + 1:] == -7.0)
+    y = out[1:n + 1].reshape(batch, rows).copy()
+    _check(y, q, xh, rows, sb, batch, f"unaligned y B={batch}")
+
+
 def test_batch_one_matches_the_matvec_within_f16_weight_rounding(ctx):
     rows, sb = 512, 16
     q, xh = _inputs(93, rows, sb, 1)
