@@ -619,9 +619,9 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
 // iterations ahead).  Lane c of a superblock takes half n = c/2 and
 // l in [16(c&1), 16(c&1) + 16): 64 weights, 4 parts of 16.  Its bytes are
 // three 16-byte runs (ql for parts 0/2, ql for parts 1/3, qh), the 16 scale
-// bytes and d.  Superblocks start at 2-byte boundaries (210 = 2 mod 4), so a
-// 16-byte run is read as 5 aligned dwords and realigned with v_alignbit;
-// every aligned dword read lies inside the superblock or its predecessor.
+// bytes and d.  Superblocks start at 2-byte boundaries (210 = 2 mod 4); each
+// 16-byte run is one 16-byte load at its own (possibly 2-byte-aligned)
+// address, and every read lies inside the superblock.
 //
 // LDS: xs[sb*272 + 64p + 16i + 4c + e] = x[sb*256 + 128n + 32p + 16h + 4i + e] * 2^24
 //      (c = 2n + h), and ss[sb*16 + 4c + p] = sum of those 16 x (unscaled), so
@@ -656,32 +656,19 @@ __device__ __forceinline__ void q6k_stage_xc(float *xs, float *ss, uint32_t tid,
   }
 }
 
-// 16 bytes at byte offset `off` (2-byte aligned): raw aligned dwords.
-struct Q6kRun {
-  uint4 a;   // dwords at off & ~3
-  uint32_t e; // the dword after them
-};
-
-__device__ __forceinline__ Q6kRun q6k_load_run(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  const uint32_t al = off & ~3u;
-  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)al, 0, 0);
-  Q6kRun out;
-  out.a = make_uint4(v.x, v.y, v.z, v.w);
-  out.e = __builtin_amdgcn_raw_buffer_load_b32(r, (int)(al + 16u), 0, 0);
-  return out;
-}
-
-// The 16 bytes of a run as 4 dwords (sh = 8 * (off & 3), 0 or 16).
-__device__ __forceinline__ uint4 q6k_align(const Q6kRun &r, uint32_t sh) {
-  return make_uint4(__builtin_amdgcn_alignbit(r.a.y, r.a.x, sh),
-                    __builtin_amdgcn_alignbit(r.a.z, r.a.y, sh),
-                    __builtin_amdgcn_alignbit(r.a.w, r.a.z, sh),
-                    __builtin_amdgcn_alignbit(r.e, r.a.w, sh));
+// 16 bytes at byte offset `off`, which is only 2-byte aligned when the
+// superblock starts at 2 mod 4: one 16-byte load.  gfx950 code objects for
+// amdhsa run in unaligned-access mode (the compiler itself emits
+// global_load_dwordx4 at 2-byte-aligned addresses for such data), so this
+// replaces an aligned 16-byte load, a fifth dword and four v_alignbit.
+__device__ __forceinline__ uint4 q6k_load_run(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 template <int RPW, int PF>
 struct Q6kFlatBuf {
-  Q6kRun lo[PF][RPW], hi[PF][RPW], qh[PF][RPW], sc[PF][RPW];
+  uint4 lo[PF][RPW], hi[PF][RPW], qh[PF][RPW], sc[PF][RPW];
   uint32_t d[PF][RPW];
 };
 
@@ -697,13 +684,7 @@ __device__ __forceinline__ void q6k_flat_load(Q6kFlatBuf<RPW, PF> &B, int p,
     B.lo[p][r] = q6k_load_run(qr, o + 64u * n + 16u * h);
     B.hi[p][r] = q6k_load_run(qr, o + 64u * n + 32u + 16u * h);
     B.qh[p][r] = q6k_load_run(qr, o + 128u + 32u * n + 16u * h);
-    // scales: when o is 4-byte aligned the 16 bytes need no fifth dword; read
-    // one inside the run instead of the dword past the superblock
-    const uint32_t sal = (o + 192u) & ~3u;
-    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)sal, 0, 0);
-    B.sc[p][r].a = make_uint4(v.x, v.y, v.z, v.w);
-    B.sc[p][r].e = __builtin_amdgcn_raw_buffer_load_b32(qr, (int)(sal + ((o & 3u) ? 16u : 12u)),
-                                                        0, 0);
+    B.sc[p][r] = q6k_load_run(qr, o + 192u);
     B.d[p][r] = __builtin_amdgcn_raw_buffer_load_b16(qr, (int)(o + 208u), 0, 0);
   }
 }
@@ -779,13 +760,7 @@ __device__ __forceinline__ void q6k_matvec_flat(const uint8_t *__restrict__ q,
         const float4 sums = *reinterpret_cast<const float4 *>(ss + sb * 16u + 4u * c);
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {
-          const uint32_t bundle = 2u * (W + c_pi * total_waves) + half;
-          const uint32_t o = (bundle * RPW + (uint32_t)r) * row_bytes + sb * kQ6kSbBytes;
-          const uint32_t sh = (o & 3u) * 8u;
-          const uint4 lo = q6k_align(B.lo[p][r], sh);
-          const uint4 hi = q6k_align(B.hi[p][r], sh);
-          const uint4 qh = q6k_align(B.qh[p][r], sh);
-          const uint4 sc = q6k_align(B.sc[p][r], sh);
+          const uint4 lo = B.lo[p][r], hi = B.hi[p][r], qh = B.qh[p][r], sc = B.sc[p][r];
           const uint32_t lw[4] = {lo.x, lo.y, lo.z, lo.w};
           const uint32_t hw[4] = {hi.x, hi.y, hi.z, hi.w};
           const uint32_t qw[4] = {qh.x, qh.y, qh.z, qh.w};
