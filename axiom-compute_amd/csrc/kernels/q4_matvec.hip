@@ -1090,7 +1090,78 @@ __device__ __forceinline__ void q4k_matvec_cols(const uint8_t *__restrict__ q,
 }
 
 // ---------------------------------------------------------------------------
-// Split-K for few long rows (fewer than 32 rows of 64..256 superblocks):
+// One workgroup for up to RB long rows (the single row of config 2): all
+// NW*64 lanes work on the same rows, four lanes per superblock (lane t:
+// superblock t / 4, quarter t % 4, as the column kernel), with x staged once
+// in LDS by the coalesced loads of the persistent kernel (the same layout,
+// pre-scaled, with sub-block sums) instead of 64 contiguous floats per lane.
+// All rows are requested at once; each lane's partial sums are reduced with
+// DPP and the NW wave sums are added in wave order in LDS: no atomics and
+// no ordering between workgroups.
+// ---------------------------------------------------------------------------
+template <int NW, int XP, int RB>
+__device__ __forceinline__ void q4k_matvec_wg(const uint8_t *__restrict__ q,
+                                              const float *__restrict__ x,
+                                              float *__restrict__ y, uint32_t n_rows,
+                                              uint32_t nsb, float *lds) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
+  const __amdgpu_buffer_rsrc_t qr = make_rsrc(q, n_rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, nsb * 1024u);
+  float *xs = lds, *ss = lds + nsb * kQ4kFlatSbFloats, *red = ss + nsb * 8u;
+  float4 xv[8 * XP];
+  q4k_flat_load_xc<NW * 64, XP>(xr, tid, xv);
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t sbi = tid >> 2, c = tid & 3u;
+  const uint32_t lane_off = sbi < nsb ? sbi * (uint32_t)kQ4kSbBytes : kQ4kColsOob;
+  Q4kColsBuf<RB> B;
+  q4k_cols_load<RB, false>(B, qr, 0u, n_rows, row_bytes, lane_off, c);
+  __builtin_amdgcn_sched_barrier(0);
+  q4k_flat_stage_xc<NW * 64, XP>(xs, ss, tid, nsb, xv);
+  __syncthreads();
+  // idle lanes (superblock past the row) read superblock 0's x; their weights are zero
+  const uint32_t sbx = sbi < nsb ? sbi : 0u;
+  const float *xb = xs + sbx * kQ4kFlatSbFloats + 4u * c;
+  float4 xl[8], xh[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    xl[t] = *reinterpret_cast<const float4 *>(xb + (uint32_t)t * 16u);
+    xh[t] = *reinterpret_cast<const float4 *>(xb + 128u + (uint32_t)t * 16u);
+  }
+  const float2 sub = *reinterpret_cast<const float2 *>(ss + sbx * 8u + 2u * c);
+  float v[RB];
+  q4k_cols_compute<RB>(B, xl, xh, sub.x, sub.y, c, v);
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    v[r] = wave_sum_to_lane63(v[r]);
+    if (lane == 63u) red[r * NW + wave] = v[r];
+  }
+  __syncthreads();
+  if (tid < (uint32_t)RB && tid < n_rows) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) sum += red[tid * NW + (uint32_t)w];
+    y[tid] = sum;
+  }
+}
+
+#define AXH_Q4K_MATVEC_WG(NW, XP, RB)                                                            \
+  extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
+      axh_q4k_matvec_wg_w##NW##_x##XP##_r##RB(const uint8_t *__restrict__ q,                     \
+                                              const float *__restrict__ x,                       \
+                                              float *__restrict__ y, RowsArgs a) {               \
+    extern __shared__ float axh_wg_dyn[];                                                        \
+    q4k_matvec_wg<NW, XP, RB>(q, x, y, a.n_rows, a.units_per_row, axh_wg_dyn);                   \
+  }
+
+AXH_Q4K_MATVEC_WG(8, 2, 1)
+AXH_Q4K_MATVEC_WG(8, 2, 2)
+AXH_Q4K_MATVEC_WG(8, 2, 4)
+
+// ---------------------------------------------------------------------------
+// Split-K for few long rows (fewer than 32 rows of 64..256 superblocks that
+// the one-workgroup kernel does not take):
 // workgroup g (one wave) takes superblocks [g*SPW, g*SPW + SPW) of every row,
 // four lanes per superblock (as the column kernel), with its x slice in
 // VGPRs.  Lane 63 stores the per-row partial sums to

@@ -277,12 +277,27 @@ def test_q4km_reference_kernel_many_superblocks(ctx, axc, n):
     assert O.reference_rel_err(gpu, cpu) < REL_TOL, (n, gpu, float(cpu))
 
 
+# ---- few long rows: one workgroup (1-4 rows of up to 128 superblocks) ----------
+@pytest.mark.parametrize("rows,sb", [(1, 33), (1, 64), (1, 65), (1, 127), (1, 128), (2, 33),
+                                     (2, 100), (3, 64), (3, 71), (4, 128)])
+def test_q4k_one_workgroup_shapes(ctx, axc, rows, sb):
+    """1-4 rows of 33..128 superblocks take the one-workgroup kernel: idle
+    lanes past the row, odd superblock counts, every row-batch size."""
+    assert axc.q4k_matvec_kernel_name(rows, sb).startswith("axh_q4k_matvec_wg_")
+    _say(f"q4k one-workgroup {rows}x{sb}")
+    q = O.gen_q4k_weights(rows * 19 + sb, rows * sb)
+    x = O.gen_normal_f32(rows + 5 * sb, sb * 256)
+    y = _run_q4k(ctx, q, x, rows, sb)
+    _check_q4k(y, q, x, rows, sb, f"q4k one-workgroup {rows}x{sb}")
+
+
 # ---- few long rows: split-K across workgroups with a last-workgroup reduction --
-@pytest.mark.parametrize("rows,sb", [(1, 64), (1, 65), (1, 128), (3, 71), (31, 128), (2, 255),
-                                     (1, 256), (31, 200)])
+@pytest.mark.parametrize("rows,sb", [(5, 64), (5, 65), (8, 128), (31, 128), (2, 255),
+                                     (1, 256), (31, 200), (4, 129)])
 def test_q4k_split_k_shapes(ctx, axc, rows, sb):
-    """Few rows of 64..256 superblocks take the split-K kernel: ragged last
-    slices, the 16-workgroup limit, and row counts up to 31."""
+    """Few rows of 64..256 superblocks the one-workgroup kernel does not take
+    go to the split-K kernel: ragged last slices, the 16-workgroup limit, and
+    row counts up to 31."""
     assert axc.q4k_matvec_kernel_name(rows, sb).startswith("axh_q4k_matvec_sk_")
     _say(f"q4k split-K {rows}x{sb}")
     q = O.gen_q4k_weights(rows * 17 + sb, rows * sb)

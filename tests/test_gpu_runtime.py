@@ -210,8 +210,10 @@ def test_graph_replays_match_eager_results(ctx, axc):
     q0 = O.gen_q4_0_weights(83, rows * nb)
     x0 = O.gen_normal_f32(84, nb * 32)
     xh = O.gen_normal_f32(85, sb * 256 * batch).astype(np.float16)
-    ksb = 128  # one row of 128 superblocks: the split-K kernel and its workspace counter
-    qk = O.gen_q4k_weights(86, ksb)
+    # 5 rows of 128 superblocks: the split-K kernel and its workspace counter;
+    # the first of them alone: the one-workgroup kernel
+    ksb, krows = 128, 5
+    qk = O.gen_q4k_weights(86, krows * ksb)
     xk = O.gen_normal_f32(87, ksb * 256)
     bufs = {}
     for name, arr in (("q", q), ("x", x), ("q0", q0), ("x0", x0), ("xh", xh), ("qk", qk),
@@ -219,25 +221,28 @@ def test_graph_replays_match_eager_results(ctx, axc):
         bufs[name] = ctx.alloc(arr.nbytes)
         ctx.upload(bufs[name], arr)
     y1, y2, y3 = ctx.alloc(rows * 4), ctx.alloc(rows * 4), ctx.alloc(rows * batch * 4)
-    y4 = ctx.alloc(16)
-    outs = ((y1, rows * 4), (y2, rows * 4), (y3, rows * batch * 4), (y4, 4))
+    y4, y5 = ctx.alloc(32), ctx.alloc(16)
+    outs = ((y1, rows * 4), (y2, rows * 4), (y3, rows * batch * 4), (y4, krows * 4), (y5, 4))
 
     def ops():
         ctx.q4k_matvec(bufs["q"], bufs["x"], y1, rows, sb)
         ctx.q4_0_matvec(bufs["q0"], bufs["x0"], y2, rows, nb)
         ctx.q4k_matmul(bufs["q"], bufs["xh"], y3, rows, sb, batch)
-        ctx.q4k_matvec(bufs["qk"], bufs["xk"], y4, 1, ksb)
+        ctx.q4k_matvec(bufs["qk"], bufs["xk"], y4, krows, ksb)
+        ctx.q4k_matvec(bufs["qk"], bufs["xk"], y5, 1, ksb)
 
+    assert axc.q4k_matvec_kernel_name(krows, ksb).startswith("axh_q4k_matvec_sk_")
+    assert axc.q4k_matvec_kernel_name(1, ksb).startswith("axh_q4k_matvec_wg_")
     ops()  # eager (also prepares every kernel and the workspace before capture)
     ctx.synchronize()
     eager = [ctx.download(b, n) for b, n in outs]
     g = ctx.capture(ops)
-    assert g.node_count == 4
+    assert g.node_count == 5
     for rep in range(4):
         for b, n in outs:
             ctx.upload(b, np.full(n // 4, np.nan, dtype=np.float32))  # poison between replays
         ctx.q4k_matvec(bufs["q"], bufs["x"], y1, rows, sb)  # eager work between replays
-        ctx.q4k_matvec(bufs["qk"], bufs["xk"], y4, 1, ksb)
+        ctx.q4k_matvec(bufs["qk"], bufs["xk"], y4, krows, ksb)
         ctx.synchronize()
         g.launch()
         ctx.synchronize()
