@@ -432,8 +432,133 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g / (1.0f + expf(-g)) * u;
 }
 
+// One iteration of the flat kernels for the RPW rows of slot p: lane group s
+// holds superblock sb, quarter c.  acc[r] += this quarter's share of row r.
+template <int RPW, int NS, bool kQ5>
+__device__ __forceinline__ void q4k_flat_compute(const Q4kFlatBuf<RPW, NS, kQ5> &B, int p,
+                                                 const float *xs, const float *ss, uint32_t sb,
+                                                 uint32_t c, float (&acc)[RPW]) {
+  const float *xb = xs + sb * kQ4kFlatSbFloats + 4u * c;
+  float4 xl[8], xh[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    xl[t] = *reinterpret_cast<const float4 *>(xb + (uint32_t)t * 16u);
+    xh[t] = *reinterpret_cast<const float4 *>(xb + 128u + (uint32_t)t * 16u);
+  }
+  const float2 sub = *reinterpret_cast<const float2 *>(ss + sb * 8u + 2u * c);
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const uint4 hd = B.h[p][r];
+    uint32_t scp, mp;
+    q4k_scale_min_pair(hd.y, hd.z, hd.w, c, &scp, &mp);
+    float alo = 0.0f, ahi = 0.0f;
+    if constexpr (kQ5) {
+      const uint4 h0 = B.q0[p][r], h1 = B.q1[p][r];
+      const uint32_t sh = 2u * c;
+      q5k_dword(B.a[p][r].x, h0.x >> sh, xl[0], xh[0], alo, ahi);
+      q5k_dword(B.a[p][r].y, h0.y >> sh, xl[1], xh[1], alo, ahi);
+      q5k_dword(B.a[p][r].z, h0.z >> sh, xl[2], xh[2], alo, ahi);
+      q5k_dword(B.a[p][r].w, h0.w >> sh, xl[3], xh[3], alo, ahi);
+      q5k_dword(B.b[p][r].x, h1.x >> sh, xl[4], xh[4], alo, ahi);
+      q5k_dword(B.b[p][r].y, h1.y >> sh, xl[5], xh[5], alo, ahi);
+      q5k_dword(B.b[p][r].z, h1.z >> sh, xl[6], xh[6], alo, ahi);
+      q5k_dword(B.b[p][r].w, h1.w >> sh, xl[7], xh[7], alo, ahi);
+    } else {
+      q4k_dword(B.a[p][r].x, xl[0], xh[0], alo, ahi);
+      q4k_dword(B.a[p][r].y, xl[1], xh[1], alo, ahi);
+      q4k_dword(B.a[p][r].z, xl[2], xh[2], alo, ahi);
+      q4k_dword(B.a[p][r].w, xl[3], xh[3], alo, ahi);
+      q4k_dword(B.b[p][r].x, xl[4], xh[4], alo, ahi);
+      q4k_dword(B.b[p][r].y, xl[5], xh[5], alo, ahi);
+      q4k_dword(B.b[p][r].z, xl[6], xh[6], alo, ahi);
+      q4k_dword(B.b[p][r].w, xl[7], xh[7], alo, ahi);
+    }
+    const float dot = __builtin_fmaf((float)(scp & 0xFFu), alo, (float)(scp >> 8) * ahi);
+    const float mins = __builtin_fmaf((float)(mp & 0xFFu), sub.x, (float)(mp >> 8) * sub.y);
+    acc[r] = __builtin_fmaf(f16_to_f32(hd.x & 0xFFFFu), dot,
+                            __builtin_fmaf(-f16_to_f32(hd.x >> 16), mins, acc[r]));
+  }
+}
+
+// Reduce the pair of bundles (bundle0, bundle0 + 1) that a wave finished and
+// store it: each half-wave's lanes hold one bundle's partial sums.
+template <int RPW, bool kDual>
+__device__ __forceinline__ void q4k_flat_store(float (&acc)[RPW], uint32_t bundle0, uint32_t lane,
+                                               uint32_t n_rows, float *__restrict__ y) {
+  constexpr int kRb = kDual ? RPW / 2 : RPW;
+  float h0[RPW], h1[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    float v = acc[r];
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x141>(v);
+    v += dpp_mov<0x140>(v);
+    const int vi = __builtin_bit_cast(int, v);
+    h0[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 0)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 16));
+    h1[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 32)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 48));
+    acc[r] = 0.0f;
+  }
+#pragma unroll
+  for (int r = 0; r < kRb; ++r) {
+    const uint32_t r0 = bundle0 * kRb + (uint32_t)r;
+    const uint32_t r1 = (bundle0 + 1u) * kRb + (uint32_t)r;
+    const float o0 = kDual ? silu_mul(h0[r], h0[(r + kRb) % RPW]) : h0[r];
+    const float o1 = kDual ? silu_mul(h1[r], h1[(r + kRb) % RPW]) : h1[r];
+    if (lane == 0 && r0 < n_rows) y[r0] = o0;
+    if (lane == 0 && r1 < n_rows) y[r1] = o1;
+  }
+}
+
+// x chunk j of the early-refill kernels: superblocks [8j, 8j + 8), 512
+// float4 staged by NT threads with the coalesced mapping and layout of
+// q4k_flat_stage_xc (float4 f = 512j + tid + i*NT).  Chunks past the row read
+// zeros and stage nothing.
+template <int NT>
+__device__ __forceinline__ void q4k_flat_load_chunk(__amdgpu_buffer_rsrc_t xr, uint32_t tid,
+                                                    uint32_t j, float4 (&v)[512 / NT]) {
+#pragma unroll
+  for (int i = 0; i < 512 / NT; ++i)
+    v[i] = buf_loadf4(xr, (j * 512u + tid + (uint32_t)i * NT) * 16u);
+}
+
+template <int NT>
+__device__ __forceinline__ void q4k_flat_stage_chunk(float *xs, float *ss, uint32_t tid, uint32_t j,
+                                                     uint32_t nsb, const float4 (&v)[512 / NT]) {
+#pragma unroll
+  for (int i = 0; i < 512 / NT; ++i) {
+    const uint32_t f = j * 512u + tid + (uint32_t)i * NT;
+    const float4 a = v[i];
+    float sm = (a.x + a.y) + (a.z + a.w);
+    sm += dpp_mov<0xB1>(sm);
+    sm += dpp_mov<0x4E>(sm);
+    sm += dpp_mov<0x141>(sm);
+    if (f < nsb * 64u) {
+      const uint32_t sb = f >> 6, w = f & 63u, c = w >> 4, part = (w >> 3) & 1u, t = w & 7u;
+      const float scale = part ? 1048576.0f : 16777216.0f;
+      *reinterpret_cast<float4 *>(xs + sb * kQ4kFlatSbFloats + part * 128u + 16u * t + 4u * c) =
+          make_float4(a.x * scale, a.y * scale, a.z * scale, a.w * scale);
+      if ((f & 7u) == 0u) ss[f >> 3] = sm;
+    }
+  }
+}
+
 // kDual: y[r] = silu(W1[r].x) * (W2[r].x) for q = W1, q2 = W2 (same shape);
 // otherwise y = W1 x and q2 is unused.  kQ5: Q5_K superblocks instead of Q4_K.
+//
+// PF >= 2: x is staged whole first; PF register slots, slot p refilled PF
+// iterations ahead right after it is computed.
+// PF == 1 (early refill): two slots, and the next iteration's loads are
+// issued before the current one is computed, so one iteration is in flight
+// at every point of the loop.  x is staged chunk by chunk during the first
+// pass over a row (chunk j right before iteration j, requested with the
+// weights of iteration j), so the weight stream starts with the first 8 KiB
+// of x instead of after all of it.  On 4096 x 14336 this is the fastest
+// order measured (8.13 vs 8.5 us per back-to-back call): every variant with
+// more loads in flight was slower on this machine, while a refill that waits
+// for the compute leaves the memory pipe idle during it.
 template <int RPW, int NW, int PF, bool kNT, int XP, bool kDual = false, bool kQ5 = false>
 __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
                                                 const uint8_t *__restrict__ q2,
@@ -443,6 +568,10 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
   constexpr int kRb = kDual ? RPW / 2 : RPW; // output rows per bundle
   static_assert(!kDual || RPW % 2 == 0, "the fused kernel pairs gate and up rows");
   static_assert(!(kDual && kQ5), "the fused gate/up kernel reads Q4_K");
+  constexpr bool kEarly = PF == 1;        // refill before the compute, chunked x
+  constexpr int kSlots = kEarly ? 2 : PF; // register slots
+  constexpr int NT = NW * 64;
+  static_assert(!kEarly || NT <= 512, "an x chunk is 512 float4");
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   // wave index as a scalar: every loop bound below is then wave-uniform
@@ -458,7 +587,7 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
   }
   const uint32_t n_my = W < n_pairs ? (n_pairs - 1u - W) / total_waves + 1u : 0u;
   const uint32_t n_it = (nsb + 7u) >> 3;
-  const uint32_t total = (n_my * n_it + (PF - 1)) / PF * PF;
+  const uint32_t total = (n_my * n_it + (kSlots - 1)) / kSlots * kSlots;
   // The host guarantees n_rows * row_bytes < 2^32 for this kernel.
   const uint32_t row_bytes = nsb * (kQ5 ? kQ5kSbBytes : (uint32_t)kQ4kSbBytes);
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(q, n_rows * row_bytes);
@@ -467,123 +596,173 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
   float *xs = lds;
   float *ss = lds + nsb * kQ4kFlatSbFloats;
 
-  // Prologue: x requests first, then (for long rows once x has arrived) the
-  // weight prefetch, then the LDS writes.  8 * XP float4 of x per thread (a
-  // sub-block's worth per XP): the host launches this kernel only when
-  // nsb * 8 <= XP * NW * 64.
-  float4 xv[8 * XP];
-  q4k_flat_load_xc<NW * 64, XP>(xr, tid, xv);
-  // For long rows, let x arrive before the weight prefetch goes out: every
-  // wave of the grid issues its prefetch at once, and x requests queued
-  // behind that traffic arrive later than the first weights would (measured:
-  // 0.3 us less per launch on 4096 x 14336, 0.2 us more on 4096 x 4096,
-  // where x is 16 KiB).
-  __builtin_amdgcn_sched_barrier(0);
-  if (nsb >= kWaitXMinSb) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-
-  Q4kFlatBuf<RPW, PF, kQ5> B;
+  Q4kFlatBuf<RPW, kSlots, kQ5> B;
   uint32_t l_pi = 0, l_it = 0; // load cursor: pair index (of this wave) and iteration
-#pragma unroll
-  for (int p = 0; p < PF; ++p) {
-    const uint32_t bundle = 2u * (W + l_pi * total_waves) + half;
-    q4k_flat_load<RPW, PF, kNT, kDual, kQ5>(B, p, qr, qr2, row_bytes, bundle, l_it, s, c);
-    if (++l_it == n_it) { l_it = 0; ++l_pi; }
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  q4k_flat_stage_xc<NW * 64, XP>(xs, ss, tid, nsb, xv);
-  __syncthreads();
-
+  uint32_t c_pi = 0, c_it = 0; // compute cursor
   float acc[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
-  uint32_t c_pi = 0, c_it = 0; // compute cursor
-  for (uint32_t j0 = 0; j0 < total; j0 += PF) {
-#pragma unroll
-    for (int p = 0; p < PF; ++p) {
-      const uint32_t sb = c_it * 8u + s;
-      if (c_pi < n_my && sb < nsb) {
-        const float *xb = xs + sb * kQ4kFlatSbFloats + 4u * c;
-        float4 xl[8], xh[8];
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          xl[t] = *reinterpret_cast<const float4 *>(xb + (uint32_t)t * 16u);
-          xh[t] = *reinterpret_cast<const float4 *>(xb + 128u + (uint32_t)t * 16u);
-        }
-        const float2 sub = *reinterpret_cast<const float2 *>(ss + sb * 8u + 2u * c);
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-          const uint4 hd = B.h[p][r];
-          uint32_t scp, mp;
-          q4k_scale_min_pair(hd.y, hd.z, hd.w, c, &scp, &mp);
-          float alo = 0.0f, ahi = 0.0f;
-          if constexpr (kQ5) {
-            const uint4 h0 = B.q0[p][r], h1 = B.q1[p][r];
-            const uint32_t sh = 2u * c;
-            q5k_dword(B.a[p][r].x, h0.x >> sh, xl[0], xh[0], alo, ahi);
-            q5k_dword(B.a[p][r].y, h0.y >> sh, xl[1], xh[1], alo, ahi);
-            q5k_dword(B.a[p][r].z, h0.z >> sh, xl[2], xh[2], alo, ahi);
-            q5k_dword(B.a[p][r].w, h0.w >> sh, xl[3], xh[3], alo, ahi);
-            q5k_dword(B.b[p][r].x, h1.x >> sh, xl[4], xh[4], alo, ahi);
-            q5k_dword(B.b[p][r].y, h1.y >> sh, xl[5], xh[5], alo, ahi);
-            q5k_dword(B.b[p][r].z, h1.z >> sh, xl[6], xh[6], alo, ahi);
-            q5k_dword(B.b[p][r].w, h1.w >> sh, xl[7], xh[7], alo, ahi);
-          } else {
-            q4k_dword(B.a[p][r].x, xl[0], xh[0], alo, ahi);
-            q4k_dword(B.a[p][r].y, xl[1], xh[1], alo, ahi);
-            q4k_dword(B.a[p][r].z, xl[2], xh[2], alo, ahi);
-            q4k_dword(B.a[p][r].w, xl[3], xh[3], alo, ahi);
-            q4k_dword(B.b[p][r].x, xl[4], xh[4], alo, ahi);
-            q4k_dword(B.b[p][r].y, xl[5], xh[5], alo, ahi);
-            q4k_dword(B.b[p][r].z, xl[6], xh[6], alo, ahi);
-            q4k_dword(B.b[p][r].w, xl[7], xh[7], alo, ahi);
-          }
-          const float dot = __builtin_fmaf((float)(scp & 0xFFu), alo, (float)(scp >> 8) * ahi);
-          const float mins = __builtin_fmaf((float)(mp & 0xFFu), sub.x, (float)(mp >> 8) * sub.y);
-          acc[r] = __builtin_fmaf(f16_to_f32(hd.x & 0xFFFFu), dot,
-                                  __builtin_fmaf(-f16_to_f32(hd.x >> 16), mins, acc[r]));
-        }
+  // Loads of the next iteration into slot p (unconditional: past the last
+  // pair they read zeros or bytes whose results are never used).
+  auto load_next = [&](int p) {
+    const uint32_t bundle = 2u * (W + l_pi * total_waves) + half;
+    q4k_flat_load<RPW, kSlots, kNT, kDual, kQ5>(B, p, qr, qr2, row_bytes, bundle, l_it, s, c);
+    if (++l_it == n_it) { l_it = 0; ++l_pi; }
+  };
+  // Compute the current iteration from slot p and advance the compute cursor.
+  auto compute = [&](int p) {
+    const uint32_t sb = c_it * 8u + s;
+    if (c_pi < n_my && sb < nsb) q4k_flat_compute<RPW, kSlots, kQ5>(B, p, xs, ss, sb, c, acc);
+    if (++c_it == n_it) { // a bundle pair is complete: reduce and store
+      if (c_pi < n_my)
+        q4k_flat_store<RPW, kDual>(acc, 2u * (W + c_pi * total_waves), lane, n_rows, y);
+      c_it = 0;
+      ++c_pi;
+    }
+  };
+
+  if constexpr (kEarly) {
+    // First pass: the wave's first bundle pair, iteration j with x chunk j
+    // staged right before it (every wave, uniform trip count padded to even).
+    // Loads past the row go through an empty resource (zero records): they
+    // return zeros without a memory request.
+    const uint32_t bundle0 = 2u * W + half;
+    const __amdgpu_buffer_rsrc_t none = make_rsrc(q, 0u);
+    auto load_first = [&](int p, uint32_t it) {
+      const bool in = it < n_it;
+      q4k_flat_load<RPW, kSlots, kNT, kDual, kQ5>(B, p, in ? qr : none, in ? qr2 : none,
+                                                  row_bytes, bundle0, it, s, c);
+    };
+    float4 xv[2][512 / NT];
+    q4k_flat_load_chunk<NT>(xr, tid, 0u, xv[0]);
+    load_first(0, 0u);
+    const uint32_t n1 = (n_it + 1u) & ~1u;
+    uint32_t j = 0;
+    do {
+      q4k_flat_stage_chunk<NT>(xs, ss, tid, j, nsb, xv[0]);
+      q4k_flat_load_chunk<NT>(xr, tid, j + 1u, xv[1]);
+      load_first(1, j + 1u);
+      __syncthreads();
+      if (n_my > 0 && j * 8u + s < nsb)
+        q4k_flat_compute<RPW, kSlots, kQ5>(B, 0, xs, ss, j * 8u + s, c, acc);
+      q4k_flat_stage_chunk<NT>(xs, ss, tid, j + 1u, nsb, xv[1]);
+      q4k_flat_load_chunk<NT>(xr, tid, j + 2u, xv[0]);
+      load_first(0, j + 2u);
+      __syncthreads();
+      if (n_my > 0 && (j + 1u) * 8u + s < nsb)
+        q4k_flat_compute<RPW, kSlots, kQ5>(B, 1, xs, ss, (j + 1u) * 8u + s, c, acc);
+      j += 2u;
+    } while (j < n1);
+    if (n_my > 0) q4k_flat_store<RPW, kDual>(acc, 2u * W, lane, n_rows, y);
+    // The wave's other pairs: x is resident, no barriers.
+    if (n_my > 1) {
+      l_pi = 1;
+      c_pi = 1;
+      const uint32_t total2 = ((n_my - 1u) * n_it + 1u) & ~1u;
+      load_next(0);
+      for (uint32_t k = 0; k < total2; k += 2u) {
+        load_next(1);
+        compute(0);
+        load_next(0);
+        compute(1);
       }
-      // refill this slot PF iterations ahead (unconditional)
-      {
-        const uint32_t bundle = 2u * (W + l_pi * total_waves) + half;
-        q4k_flat_load<RPW, PF, kNT, kDual, kQ5>(B, p, qr, qr2, row_bytes, bundle, l_it, s, c);
-        if (++l_it == n_it) { l_it = 0; ++l_pi; }
-      }
-      if (++c_it == n_it) { // a bundle pair is complete: reduce and store
-        if (c_pi < n_my) {
-          const uint32_t bundle0 = 2u * (W + c_pi * total_waves);
-          float h0[RPW], h1[RPW];
+    }
+  } else {
+    // Prologue: x requests first, then (for long rows once x has arrived) the
+    // weight prefetch, then the LDS writes.  8 * XP float4 of x per thread (a
+    // sub-block's worth per XP): the host launches this kernel only when
+    // nsb * 8 <= XP * NW * 64.
+    float4 xv[8 * XP];
+    q4k_flat_load_xc<NT, XP>(xr, tid, xv);
+    // For long rows, let x arrive before the weight prefetch goes out: every
+    // wave of the grid issues its prefetch at once, and x requests queued
+    // behind that traffic arrive later than the first weights would (measured:
+    // 0.3 us less per launch on 4096 x 14336, 0.2 us more on 4096 x 4096,
+    // where x is 16 KiB).
+    __builtin_amdgcn_sched_barrier(0);
+    if (nsb >= kWaitXMinSb) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int r = 0; r < RPW; ++r) {
-            float v = acc[r];
-            v += dpp_mov<0xB1>(v);
-            v += dpp_mov<0x4E>(v);
-            v += dpp_mov<0x141>(v);
-            v += dpp_mov<0x140>(v);
-            const int vi = __builtin_bit_cast(int, v);
-            h0[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 0)) +
-                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 16));
-            h1[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 32)) +
-                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 48));
-            acc[r] = 0.0f;
-          }
+    for (int p = 0; p < PF; ++p) load_next(p);
+    __builtin_amdgcn_sched_barrier(0);
+    q4k_flat_stage_xc<NT, XP>(xs, ss, tid, nsb, xv);
+    __syncthreads();
+    for (uint32_t j0 = 0; j0 < total; j0 += PF) {
 #pragma unroll
-          for (int r = 0; r < kRb; ++r) {
-            const uint32_t r0 = bundle0 * kRb + (uint32_t)r;
-            const uint32_t r1 = (bundle0 + 1u) * kRb + (uint32_t)r;
-            const float o0 = kDual ? silu_mul(h0[r], h0[(r + kRb) % RPW]) : h0[r];
-            const float o1 = kDual ? silu_mul(h1[r], h1[(r + kRb) % RPW]) : h1[r];
-            if (lane == 0 && r0 < n_rows) y[r0] = o0;
-            if (lane == 0 && r1 < n_rows) y[r1] = o1;
-          }
-        }
-        c_it = 0;
-        ++c_pi;
+      for (int p = 0; p < PF; ++p) {
+        compute(p);
+        load_next(p); // refill this slot PF iterations ahead
       }
     }
   }
 }
+
+// One pass, one bundle pair per wave (axh_q4k_matvec_one_i{NIT}): rows of
+// 8 * (NIT - 1) < nsb <= 8 * NIT superblocks, 8 waves per workgroup, wave W
+// takes rows 2W and 2W + 1 and the grid covers all pairs.  The persistent
+// kernel's early-refill order (one iteration in flight, x staged chunk by
+// chunk with the weights), fully unrolled over the NIT iterations so that no
+// load, barrier or bookkeeping is spent past the row.  On 4096 x 14336 (one
+// pair per wave either way) this measured 8.13-8.36 us per back-to-back call
+// against 8.62-8.76 us for the persistent early-refill kernel, whose first
+// pass loops over an even trip count.
+template <int NIT>
+__device__ __forceinline__ void q4k_matvec_one(const uint8_t *__restrict__ q,
+                                               const float *__restrict__ x, float *__restrict__ y,
+                                               uint32_t n_rows, uint32_t nsb, float *lds) {
+  constexpr int NW = 8, NT = NW * 64;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t G = lane >> 2, half = G >> 3, s = G & 7u, c = lane & 3u;
+  const uint32_t W = blockIdx.x * NW + wave;
+  const bool mine = W < (n_rows + 1u) >> 1; // this wave has a pair of rows
+  const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
+  const __amdgpu_buffer_rsrc_t qr = make_rsrc(q, n_rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, nsb * 1024u);
+  float *xs = lds;
+  float *ss = lds + nsb * kQ4kFlatSbFloats;
+  const uint32_t bundle = 2u * W + half;
+  Q4kFlatBuf<1, 2, false> B;
+  float4 xv[2][512 / NT];
+  float acc[1] = {0.0f};
+  q4k_flat_load_chunk<NT>(xr, tid, 0u, xv[0]);
+  q4k_flat_load<1, 2, false, false, false>(B, 0, qr, qr, row_bytes, bundle, 0u, s, c);
+#pragma unroll
+  for (int j = 0; j < NIT; ++j) {
+    const int p = j & 1;
+    q4k_flat_stage_chunk<NT>(xs, ss, tid, (uint32_t)j, nsb, xv[p]);
+    if (j + 1 < NIT) { // next iteration's x chunk and weights, before the compute
+      q4k_flat_load_chunk<NT>(xr, tid, (uint32_t)(j + 1), xv[p ^ 1]);
+      q4k_flat_load<1, 2, false, false, false>(B, p ^ 1, qr, qr, row_bytes, bundle,
+                                               (uint32_t)(j + 1), s, c);
+    }
+    __syncthreads();
+    const uint32_t sb = (uint32_t)j * 8u + s;
+    if (mine && sb < nsb) q4k_flat_compute<1, 2, false>(B, p, xs, ss, sb, c, acc);
+  }
+  if (mine) q4k_flat_store<1, false>(acc, 2u * W, lane, n_rows, y);
+}
+
+#define AXH_Q4K_MATVEC_ONE(NIT)                                                                  \
+  extern "C" __global__ void __launch_bounds__(512)                                              \
+      axh_q4k_matvec_one_i##NIT(const uint8_t *__restrict__ q, const float *__restrict__ x,      \
+                                float *__restrict__ y, RowsArgs a) {                             \
+    extern __shared__ float axh_lds_dyn[];                                                       \
+    q4k_matvec_one<NIT>(q, x, y, a.n_rows, a.units_per_row, axh_lds_dyn);                        \
+  }
+AXH_Q4K_MATVEC_ONE(5)
+AXH_Q4K_MATVEC_ONE(6)
+AXH_Q4K_MATVEC_ONE(7)
+AXH_Q4K_MATVEC_ONE(8)
+AXH_Q4K_MATVEC_ONE(9)
+AXH_Q4K_MATVEC_ONE(10)
+AXH_Q4K_MATVEC_ONE(11)
+AXH_Q4K_MATVEC_ONE(12)
+AXH_Q4K_MATVEC_ONE(13)
+AXH_Q4K_MATVEC_ONE(14)
+AXH_Q4K_MATVEC_ONE(15)
+AXH_Q4K_MATVEC_ONE(16)
 
 #define AXH_Q4K_MATVEC_FLAT(RPW, NW, PF, NT)                                                     \
   extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
@@ -717,8 +896,10 @@ __device__ __forceinline__ void q6k_matvec_flat(const uint8_t *__restrict__ q,
     return;
   }
   const uint32_t n_my = W < n_pairs ? (n_pairs - 1u - W) / total_waves + 1u : 0u;
+  constexpr bool kEarly = PF == 1;        // refill before the compute
+  constexpr int kSlots = kEarly ? 2 : PF; // register slots
   const uint32_t n_it = (nsb + 7u) >> 3;
-  const uint32_t total = (n_my * n_it + (PF - 1)) / PF * PF;
+  const uint32_t total = (n_my * n_it + (kSlots - 1)) / kSlots * kSlots;
   // The host guarantees n_rows * row_bytes < 2^32 for this kernel.
   const uint32_t row_bytes = nsb * kQ6kSbBytes;
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(q, n_rows * row_bytes);
@@ -734,12 +915,12 @@ __device__ __forceinline__ void q6k_matvec_flat(const uint8_t *__restrict__ q,
   if (nsb >= kWaitXMinSb) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
 
-  Q6kFlatBuf<RPW, PF> B;
+  Q6kFlatBuf<RPW, kSlots> B;
   uint32_t l_pi = 0, l_it = 0;
 #pragma unroll
   for (int p = 0; p < PF; ++p) {
     const uint32_t bundle = 2u * (W + l_pi * total_waves) + half;
-    q6k_flat_load<RPW, PF>(B, p, qr, row_bytes, bundle, l_it, s, c);
+    q6k_flat_load<RPW, kSlots>(B, p, qr, row_bytes, bundle, l_it, s, c);
     if (++l_it == n_it) { l_it = 0; ++l_pi; }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -751,9 +932,14 @@ __device__ __forceinline__ void q6k_matvec_flat(const uint8_t *__restrict__ q,
 #pragma unroll
   for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
   uint32_t c_pi = 0, c_it = 0;
-  for (uint32_t j0 = 0; j0 < total; j0 += PF) {
+  for (uint32_t j0 = 0; j0 < total; j0 += kSlots) {
 #pragma unroll
-    for (int p = 0; p < PF; ++p) {
+    for (int p = 0; p < kSlots; ++p) {
+      if constexpr (kEarly) { // the other slot: the next iteration (unconditional)
+        const uint32_t bundle = 2u * (W + l_pi * total_waves) + half;
+        q6k_flat_load<RPW, kSlots>(B, (p + 1) % kSlots, qr, row_bytes, bundle, l_it, s, c);
+        if (++l_it == n_it) { l_it = 0; ++l_pi; }
+      }
       const uint32_t sb = c_it * 8u + s;
       if (c_pi < n_my && sb < nsb) {
         const float *xb = xs + sb * kQ6kSbFloats + 4u * c;
@@ -791,9 +977,9 @@ __device__ __forceinline__ void q6k_matvec_flat(const uint8_t *__restrict__ q,
           acc[r] = __builtin_fmaf(f16_to_f32(B.d[p][r]), t, acc[r]);
         }
       }
-      {
+      if constexpr (!kEarly) {
         const uint32_t bundle = 2u * (W + l_pi * total_waves) + half;
-        q6k_flat_load<RPW, PF>(B, p, qr, row_bytes, bundle, l_it, s, c);
+        q6k_flat_load<RPW, kSlots>(B, p, qr, row_bytes, bundle, l_it, s, c);
         if (++l_it == n_it) { l_it = 0; ++l_pi; }
       }
       if (++c_it == n_it) {
@@ -845,12 +1031,16 @@ __device__ __forceinline__ void q6k_matvec_flat(const uint8_t *__restrict__ q,
   }
 
 AXH_Q5K_MATVEC_FLAT(1, 4, 2, 1)
+AXH_Q5K_MATVEC_FLAT(1, 4, 1, 1)
+AXH_Q5K_MATVEC_FLAT(1, 8, 1, 1)
 AXH_Q5K_MATVEC_FLAT(1, 8, 2, 1)
 AXH_Q5K_MATVEC_FLAT(2, 4, 2, 1)
 AXH_Q5K_MATVEC_FLAT(1, 4, 2, 2)
 AXH_Q5K_MATVEC_FLAT(1, 8, 2, 2)
 
 AXH_Q6K_MATVEC_FLAT(1, 4, 2, 1)
+AXH_Q6K_MATVEC_FLAT(1, 4, 1, 1)
+AXH_Q6K_MATVEC_FLAT(1, 8, 1, 1)
 AXH_Q6K_MATVEC_FLAT(1, 8, 2, 1)
 AXH_Q6K_MATVEC_FLAT(1, 4, 4, 1)
 AXH_Q6K_MATVEC_FLAT(2, 4, 2, 1)
@@ -870,6 +1060,8 @@ AXH_Q6K_MATVEC_FLAT(1, 8, 2, 2)
   }
 
 AXH_Q4K_GATE_UP(1, 4, 2, 1)
+AXH_Q4K_GATE_UP(1, 4, 1, 1)
+AXH_Q4K_GATE_UP(1, 8, 1, 1)
 AXH_Q4K_GATE_UP(1, 4, 4, 1)
 AXH_Q4K_GATE_UP(1, 8, 2, 1)
 AXH_Q4K_GATE_UP(2, 4, 2, 1)
@@ -878,6 +1070,10 @@ AXH_Q4K_GATE_UP(1, 4, 2, 2)
 AXH_Q4K_GATE_UP(1, 8, 2, 2)
 
 AXH_Q4K_MATVEC_FLAT(1, 8, 2, 0)
+AXH_Q4K_MATVEC_FLAT(1, 8, 1, 0)
+AXH_Q4K_MATVEC_FLAT(1, 4, 1, 0)
+AXH_Q4K_MATVEC_FLAT(2, 4, 1, 0)
+AXH_Q4K_MATVEC_FLAT(2, 8, 1, 0)
 AXH_Q4K_MATVEC_FLAT(1, 8, 4, 0)
 AXH_Q4K_MATVEC_FLAT(1, 8, 7, 0)
 AXH_Q4K_MATVEC_FLAT(1, 16, 2, 0)

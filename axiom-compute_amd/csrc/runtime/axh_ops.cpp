@@ -71,23 +71,26 @@ constexpr MatvecVariant kQ4kVariants[] = {
     {1, 8, 2, 2, 1}, {1, 8, 4, 2, 1}, {1, 8, 7, 2, 1}, {1, 16, 2, 2, 1}, {1, 4, 7, 2, 1},
     {2, 4, 2, 2, 1}, {2, 4, 4, 2, 1}, {2, 8, 2, 2, 1}, {2, 8, 4, 2, 1},  {4, 4, 2, 2, 1},
     {1, 8, 7, 1, 1}, {2, 4, 2, 1, 1}, {2, 4, 4, 1, 1}, {1, 4, 2, 2, 2},  {1, 4, 4, 2, 2},
-    {2, 4, 2, 2, 2}, {2, 4, 4, 2, 2},
+    {2, 4, 2, 2, 2}, {2, 4, 4, 2, 2}, {1, 8, 1, 2, 1}, {1, 4, 1, 2, 1}, {2, 4, 1, 2, 1},
+    {2, 8, 1, 2, 1},
 };
 // axh_q4k_gate_up_r{rpw}_w{nw}_p{pf}_x{xp}: fused SwiGLU gate/up kernels, rpw
 // output rows per bundle (each lane group reads rpw gate and rpw up rows).
 // Keep in sync with the AXH_Q4K_GATE_UP list in q4_matvec.hip.
 constexpr MatvecVariant kGateUpVariants[] = {
     {1, 4, 2, 2, 1}, {1, 4, 4, 2, 1}, {1, 8, 2, 2, 1}, {2, 4, 2, 2, 1},
-    {2, 8, 2, 2, 1}, {1, 4, 2, 2, 2}, {1, 8, 2, 2, 2},
+    {2, 8, 2, 2, 1}, {1, 4, 2, 2, 2}, {1, 8, 2, 2, 2}, {1, 4, 1, 2, 1},
+    {1, 8, 1, 2, 1},
 };
 // axh_q5k_matvec_flat_r{rpw}_w{nw}_p{pf}_x{xp} and axh_q6k_... (ggml k-quants
 // next to Q4_K).  Keep in sync with AXH_Q5K_MATVEC_FLAT / AXH_Q6K_MATVEC_FLAT.
 constexpr MatvecVariant kQ5kVariants[] = {
     {1, 4, 2, 2, 1}, {1, 8, 2, 2, 1}, {2, 4, 2, 2, 1}, {1, 4, 2, 2, 2}, {1, 8, 2, 2, 2},
+    {1, 4, 1, 2, 1}, {1, 8, 1, 2, 1},
 };
 constexpr MatvecVariant kQ6kVariants[] = {
     {1, 4, 2, 2, 1}, {1, 8, 2, 2, 1}, {1, 4, 4, 2, 1}, {2, 4, 2, 2, 1},
-    {1, 4, 2, 2, 2}, {1, 8, 2, 2, 2},
+    {1, 4, 2, 2, 2}, {1, 8, 2, 2, 2}, {1, 4, 1, 2, 1}, {1, 8, 1, 2, 1},
 };
 // axh_q4_0_matvec_r{rpw}_w{nw} (prefetch and cache policy are not holes for Q4_0).
 constexpr MatvecVariant kQ4_0Variants[] = {
@@ -162,13 +165,20 @@ static const MatvecVariant *find_variant(const MatvecVariant *table, size_t n,
   return best;
 }
 
+// Prefetch 1 (early refill) kernels stage x chunk by chunk during the first
+// pass, so any row of up to 128 superblocks fits their x staging; the others
+// stage XP sub-blocks per thread before the first iteration.
+static bool staged_in_chunks(const MatvecVariant &v) { return v.pf == 1; }
+
 // Default strategy per shape (chosen from on-device sweeps; any compiled
 // variant can be forced through axh_q4_variant).
 static MatvecVariant q4k_default(uint32_t n_rows, uint32_t nsb) {
   (void)n_rows;
   // The persistent kernel stages 32-element sub-blocks of x, one (or two for
   // the _x2 kernels) per thread.
-  if (nsb * 8u <= 256u) return {2, 4, 2, 2, 1};
+  // Early refill (prefetch 1) for short rows: 14336 x 4096 9.9 vs 10.5 us,
+  // neutral on 4096 x 4096 and the 128256 x 4096 head.
+  if (nsb * 8u <= 256u) return {2, 4, 1, 2, 1};
   if (nsb * 8u <= 512u) return {1, 8, 2, 2, 1};
   return {1, 16, 2, 2, 1};
 }
@@ -334,6 +344,19 @@ static bool q4k_use_wg(uint32_t n_rows, uint32_t nsb) {
   return nsb <= kWgMaxSb && ((n_rows <= 2u && nsb >= 33u) || (n_rows <= 4u && nsb >= 64u));
 }
 
+// One pass with one pair of rows per wave (axh_q4k_matvec_one_i{NIT}, NIT =
+// ceil(nsb / 8) in 5..16) for long rows, when the 8-wave workgroups for all
+// rows (16 rows each) fit the 256 CUs of an MI355X at once: each workgroup
+// then stages x once for its 16 rows either way, and the one-pass kernel
+// skips the persistent kernel's bookkeeping (4096 x 14336: 8.1-8.4 vs 8.5-8.7
+// us per call).
+constexpr uint32_t kOneMinSb = 33, kOneMaxSb = 128, kOneMaxRows = 16u * 256u;
+
+static bool q4k_use_one(uint32_t n_rows, uint32_t nsb) {
+  return nsb >= kOneMinSb && nsb <= kOneMaxSb && n_rows >= kQ4kColsMaxRows &&
+         n_rows <= kOneMaxRows;
+}
+
 static axh_status plan_q4k(uint32_t n_rows, uint32_t sb_per_row, const axh_q4_variant *variant,
                            Q4kPlan *p) {
   const uint64_t q_bytes = (uint64_t)n_rows * sb_per_row * 144u;
@@ -369,6 +392,15 @@ static axh_status plan_q4k(uint32_t n_rows, uint32_t sb_per_row, const axh_q4_va
     p->args = RowsArgs{n_rows, sb_per_row, sb_per_row, 0};
     return ok();
   }
+  if (!variant && q4k_use_one(n_rows, sb_per_row)) {
+    std::snprintf(p->name, sizeof(p->name), "axh_q4k_matvec_one_i%u", (sb_per_row + 7u) / 8u);
+    p->nw = 8;
+    p->lds = sb_per_row * 1120u;
+    p->flat = false; // one workgroup per 16 rows, all of them launched
+    p->units = (n_rows + 15u) / 16u;
+    p->args = RowsArgs{n_rows, sb_per_row, sb_per_row, 0};
+    return ok();
+  }
   const MatvecVariant dflt = q4k_default(n_rows, sb_per_row);
   const uint32_t want_nw =
       variant && variant->waves_per_workgroup ? variant->waves_per_workgroup : dflt.nw;
@@ -376,8 +408,8 @@ static axh_status plan_q4k(uint32_t n_rows, uint32_t sb_per_row, const axh_q4_va
   const MatvecVariant *v = find_variant(
       kQ4kVariants, sizeof(kQ4kVariants) / sizeof(kQ4kVariants[0]), variant, dflt, min_xp);
   if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_K matvec variant matches");
-  p->flat = sb_per_row >= 1 && sb_per_row <= kQ4kFlatMaxSb &&
-            sb_per_row * 8u <= v->xp * v->nw * 64u && q_bytes < 0xFFFFFFFFull;
+  p->flat = sb_per_row >= 1 && sb_per_row <= kQ4kFlatMaxSb && q_bytes < 0xFFFFFFFFull &&
+            (staged_in_chunks(*v) || sb_per_row * 8u <= v->xp * v->nw * 64u);
   if (p->flat) {
     std::snprintf(p->name, sizeof(p->name), "axh_q4k_matvec_flat_r%u_w%u_p%u_n%u%s", v->rpw,
                   v->nw, v->pf, v->nt == 1 ? 1u : 0u, v->xp == 2 ? "_x2" : "");
@@ -459,7 +491,8 @@ axh_status axh_q4k_matvec(axh_context *ctx, const void *q, const float *x, float
 // Fused gate/up: the persistent kernel only (x of a row fits LDS).
 static MatvecVariant gate_up_default(uint32_t n_rows, uint32_t nsb) {
   (void)n_rows;
-  if (nsb * 8u <= 256u) return {1, 4, 2, 2, 1};
+  // early refill: 2 x 14336 x 4096 15.1-15.6 vs 15.7-16.4 us
+  if (nsb * 8u <= 256u) return {1, 4, 1, 2, 1};
   return {1, 8, 2, 2, 1};
 }
 
@@ -479,7 +512,7 @@ static axh_status plan_gate_up(uint32_t n_rows, uint32_t sb_per_row,
       find_variant(kGateUpVariants, sizeof(kGateUpVariants) / sizeof(kGateUpVariants[0]),
                    variant, dflt, min_xp);
   if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled gate/up variant matches");
-  if (sb_per_row * 8u > v->xp * v->nw * 64u)
+  if (!staged_in_chunks(*v) && sb_per_row * 8u > v->xp * v->nw * 64u)
     return fail(AXH_ERR_INVALID_ARGUMENT, "gate/up: row too long for this variant's x staging");
   std::snprintf(p->name, sizeof(p->name), "axh_q4k_gate_up_r%u_w%u_p%u_x%u", v->rpw, v->nw,
                 v->pf, v->xp);
@@ -536,16 +569,24 @@ struct KqFormat {
   const MatvecVariant *table;
   size_t n;
   uint32_t sb_bytes, lds_per_sb; // superblock bytes, LDS bytes per superblock of x
+  bool chunked_early;            // prefetch-1 kernels stage x in chunks (any row fits)
 };
 
 static const KqFormat kQ5kFormat{"axh_q5k_matvec_flat", kQ5kVariants,
-                                 sizeof(kQ5kVariants) / sizeof(kQ5kVariants[0]), 176u, 1120u};
+                                 sizeof(kQ5kVariants) / sizeof(kQ5kVariants[0]), 176u, 1120u,
+                                 true};
 static const KqFormat kQ6kFormat{"axh_q6k_matvec_flat", kQ6kVariants,
-                                 sizeof(kQ6kVariants) / sizeof(kQ6kVariants[0]), 210u, 1152u};
+                                 sizeof(kQ6kVariants) / sizeof(kQ6kVariants[0]), 210u, 1152u,
+                                 false};
 
-static MatvecVariant kq_default(uint32_t nsb) {
-  if (nsb * 8u <= 256u) return {1, 4, 2, 2, 1};
-  return {1, 8, 2, 2, 1};
+// Early refill (prefetch 1) where the format's kernel can stage the row's x:
+// Q5_K 14336 x 4096 10.6-10.9 vs 11.3-11.4 us; Q6_K 4096 x 14336 12.5 vs
+// 13.4-13.9 us, 128256 x 4096 90.0-90.6 vs 90.9-92.0 us.  The Q6_K kernel
+// stages x whole, one sub-block per thread with its prefetch-1 variants.
+static MatvecVariant kq_default(const KqFormat &f, uint32_t nsb) {
+  const uint32_t nw = nsb * 8u <= 256u ? 4u : 8u;
+  const bool early = f.chunked_early || nsb * 8u <= nw * 64u;
+  return {1, nw, early ? 1u : 2u, 2, 1};
 }
 
 static axh_status plan_kq(const KqFormat &f, uint32_t n_rows, uint32_t sb_per_row,
@@ -556,13 +597,13 @@ static axh_status plan_kq(const KqFormat &f, uint32_t n_rows, uint32_t sb_per_ro
     return fail(AXH_ERR_INVALID_ARGUMENT, "Q5_K / Q6_K matrices must be below 4 GiB");
   if (variant && variant->nontemporal == 1)
     return fail(AXH_ERR_INVALID_ARGUMENT, "no non-temporal Q5_K / Q6_K variant is compiled");
-  const MatvecVariant dflt = kq_default(sb_per_row);
+  const MatvecVariant dflt = kq_default(f, sb_per_row);
   const uint32_t want_nw =
       variant && variant->waves_per_workgroup ? variant->waves_per_workgroup : dflt.nw;
   const uint32_t min_xp = (sb_per_row * 8u + want_nw * 64u - 1u) / (want_nw * 64u);
   const MatvecVariant *v = find_variant(f.table, f.n, variant, dflt, min_xp);
   if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q5_K / Q6_K variant matches");
-  if (sb_per_row * 8u > v->xp * v->nw * 64u)
+  if (!(f.chunked_early && staged_in_chunks(*v)) && sb_per_row * 8u > v->xp * v->nw * 64u)
     return fail(AXH_ERR_INVALID_ARGUMENT, "row too long for this variant's x staging");
   std::snprintf(p->name, sizeof(p->name), "%s_r%u_w%u_p%u_x%u", f.prefix, v->rpw, v->nw, v->pf,
                 v->xp);

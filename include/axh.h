@@ -163,8 +163,12 @@ void axh_event_destroy(axh_event *ev);
 /* ---- Q4 dequant-matvec operations ------------------------------------------
  * Strategy holes of the matvec kernels (the reference's @strategy surface,
  * crates/axc-hir/src/hir.rs:62-68): rows_per_wave, waves_per_workgroup,
- * prefetch (superblock iterations loaded ahead) and nontemporal (weight-load
- * cache policy).  Zero fields pick the defaults for the shape. */
+ * prefetch (superblock iterations loaded ahead: 1 issues the next iteration's
+ * loads before the current one is computed and stages x chunk by chunk; P >= 2
+ * keeps P iterations loaded and refills a slot after computing it) and
+ * nontemporal (weight-load cache policy).  Zero fields pick the defaults for
+ * the shape; with no variant, long rows (33-128 superblocks, up to 4096 rows)
+ * take a one-pass kernel that is not a hole assignment. */
 typedef struct axh_q4_variant {
     uint32_t rows_per_wave;
     uint32_t waves_per_workgroup;

@@ -108,6 +108,18 @@ def test_every_variant_matches_two_matvecs(ctx, axc):
         assert np.all(np.abs(h - want) <= 4 * 2.0 ** -24 * np.abs(want) + 1e-30), str(v)
 
 
+def test_early_refill_several_pairs_per_wave(ctx, axc):
+    """Prefetch-1 variants with more rows than the persistent grid holds."""
+    rows, sb = 20011, 9
+    qg, qu, x = _inputs(711, rows, sb)
+    vs = [v for v in axc.compiled_variants("gate_up") if v.prefetch == 1]
+    assert vs
+    for v in vs:
+        _say(f"gate_up early refill {v}")
+        h = _gate_up(ctx, qg, qu, x, rows, sb, v)
+        _check(h, qg, qu, x, rows, sb, f"early refill {v}")
+
+
 def test_large_gate_saturates_and_negative_gate_vanishes(ctx):
     """Rows scaled so |g| reaches hundreds: silu(g) -> g for g >> 0 and -> 0
     (no NaN from exp overflow) for g << 0."""

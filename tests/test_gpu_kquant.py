@@ -111,6 +111,20 @@ def test_every_variant(ctx, axc, kind):
         _check(y, kind, q, x, rows, sb, f"variant {v}")
 
 
+@pytest.mark.parametrize("kind", [Q5, Q6])
+def test_early_refill_several_pairs_per_wave(ctx, axc, kind):
+    """Prefetch-1 variants with more rows than the persistent grid holds."""
+    rows, sb = 20011, 9
+    q = O.gen_kq_weights(kind, 79, rows * sb)
+    x = O.gen_normal_f32(80, sb * 256)
+    vs = [v for v in axc.compiled_variants("q5k" if kind == Q5 else "q6k") if v.prefetch == 1]
+    assert vs
+    for v in vs:
+        _say(f"kquant {kind} early refill {v}")
+        y = _matvec(ctx, kind, q, x, rows, sb, v)
+        _check(y, kind, q, x, rows, sb, f"early refill {v}")
+
+
 def test_one_hot_x_reads_single_weights(ctx):
     """x = e_k picks column k: y = W[:, k] exactly (exact products, one term;
     compared as values: a zero Q6_K weight with a negative scale is -0.0 in

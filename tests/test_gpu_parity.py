@@ -277,6 +277,36 @@ def test_q4km_reference_kernel_many_superblocks(ctx, axc, n):
     assert O.reference_rel_err(gpu, cpu) < REL_TOL, (n, gpu, float(cpu))
 
 
+# ---- long rows, up to 4096 of them: one pass, one pair of rows per wave ---------
+@pytest.mark.parametrize("rows,sb", [(32, 33), (33, 40), (47, 41), (100, 56), (4095, 57),
+                                     (1000, 127), (64, 128)])
+def test_q4k_one_pass_shapes(ctx, axc, rows, sb):
+    """Rows of 33..128 superblocks, 32..4096 rows: every unrolled trip count's
+    boundary (8k and 8k + 1 superblocks), an odd row count (a half-empty last
+    pair) and workgroups past the last pair."""
+    assert axc.q4k_matvec_kernel_name(rows, sb).startswith("axh_q4k_matvec_one_i")
+    _say(f"q4k one pass {rows}x{sb}")
+    q = O.gen_q4k_weights(rows * 23 + sb, rows * sb)
+    x = O.gen_normal_f32(rows + 7 * sb, sb * 256)
+    y = _run_q4k(ctx, q, x, rows, sb)
+    _check_q4k(y, q, x, rows, sb, f"q4k one pass {rows}x{sb}")
+
+
+@pytest.mark.parametrize("sb", [9, 40])
+def test_q4k_early_refill_several_pairs_per_wave(ctx, axc, sb):
+    """Prefetch-1 variants on more rows than the persistent grid holds, so
+    each wave walks several bundle pairs after its chunk-staged first pass."""
+    rows = 20011
+    q = O.gen_q4k_weights(sb + 5, rows * sb)
+    x = O.gen_normal_f32(sb + 6, sb * 256)
+    vs = [v for v in axc.compiled_variants("q4k") if v.prefetch == 1]
+    assert vs
+    for v in vs:
+        _say(f"q4k early refill {rows}x{sb} {v}")
+        y = _run_q4k(ctx, q, x, rows, sb, v)
+        _check_q4k(y, q, x, rows, sb, f"early refill {rows}x{sb} {v}")
+
+
 # ---- few long rows: one workgroup (1-4 rows of up to 128 superblocks) ----------
 @pytest.mark.parametrize("rows,sb", [(1, 33), (1, 64), (1, 65), (1, 127), (1, 128), (2, 33),
                                      (2, 100), (3, 64), (3, 71), (4, 128)])
