@@ -173,12 +173,12 @@ static bool staged_in_chunks(const MatvecVariant &v) { return v.pf == 1; }
 // Default strategy per shape (chosen from on-device sweeps; any compiled
 // variant can be forced through axh_q4_variant).
 static MatvecVariant q4k_default(uint32_t n_rows, uint32_t nsb) {
-  (void)n_rows;
   // The persistent kernel stages 32-element sub-blocks of x, one (or two for
   // the _x2 kernels) per thread.
   // Early refill (prefetch 1) for short rows: 14336 x 4096 9.9 vs 10.5 us,
-  // neutral on 4096 x 4096 and the 128256 x 4096 head.
-  if (nsb * 8u <= 256u) return {2, 4, 1, 2, 1};
+  // neutral on 4096 x 4096.  On the 128256 x 4096 head prefetch 2 stays
+  // ahead by 1-2 % (58.1-59.0 vs 59.4 us in one run).
+  if (nsb * 8u <= 256u) return {2, 4, n_rows >= 65536u ? 2u : 1u, 2, 1};
   if (nsb * 8u <= 512u) return {1, 8, 2, 2, 1};
   return {1, 16, 2, 2, 1};
 }

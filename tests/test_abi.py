@@ -118,6 +118,7 @@ def test_kernel_selection_by_shape_and_variant(axc):
     assert name(4097, 56) == "axh_q4k_matvec_flat_r1_w8_p2_n0"
     assert name(4096, 32) == "axh_q4k_matvec_flat_r2_w4_p1_n0"
     assert name(4096, 16) == "axh_q4k_matvec_flat_r2_w4_p1_n0"
+    assert name(128256, 16) == "axh_q4k_matvec_flat_r2_w4_p2_n0"  # the head keeps prefetch 2
     assert name(8192, 128) == "axh_q4k_matvec_flat_r1_w16_p2_n0"
     # the early-refill (prefetch 1) kernels stage x in chunks: any row fits
     assert name(4096, 56, axc.Variant(2, 4, 1, 2)) == "axh_q4k_matvec_flat_r2_w4_p1_n0"
