@@ -56,7 +56,7 @@ constexpr MatmulVariant kQ4kMatmulVariants[] = {
     {4, 4, 1, 4, 0},  {4, 8, 1, 4, 0},  {4, 8, 1, 2, 0},  {4, 16, 1, 2, 0}, {4, 16, 1, 4, 0},
     {5, 4, 8, 2, 4},  {5, 4, 8, 2, 2},  {5, 4, 4, 2, 4},  {5, 4, 4, 3, 4},  {5, 4, 4, 2, 8},
     {5, 4, 2, 2, 4},  {5, 4, 2, 3, 4},  {5, 4, 1, 3, 4},  {6, 8, 8, 4, 2},  {6, 8, 8, 3, 2},
-    {6, 4, 8, 4, 4},  {6, 8, 4, 4, 2},  {6, 8, 8, 4, 1}};
+    {6, 4, 8, 4, 4},  {6, 8, 4, 4, 2},  {6, 8, 8, 4, 1},  {7, 8, 1, 1, 0}};
 constexpr uint32_t kMatmulOob = 0xFFFFFF00u; // the kernels' out-of-range offset
 
 struct MatvecVariant {
@@ -807,9 +807,13 @@ static uint32_t rs_lds_bytes(const MatmulVariant &v) {
   return v.pf * (2u * v.nt + v.w * ((48u * v.rt + 63u) / 64u)) * 1024u;
 }
 
+// Kind 7 (streaming rows) keeps each wave's X fragments in VGPRs after
+// staging them through 128 KiB of LDS: K up to 16 superblocks (8 waves x 2).
+constexpr uint32_t kSrMaxSb = 16;
+
 static MatmulVariant q4k_matmul_default(uint32_t n_rows, uint32_t batch, uint32_t nsb) {
   (void)n_rows;
-  (void)nsb;
+  if (batch <= 16 && nsb <= kSrMaxSb) return {7, 8, 1, 1, 0};
   if (batch <= 16) return {5, 4, 1, 3, 4};
   if (batch <= 32) return {5, 4, 2, 2, 4};
   if (batch <= 64) return {5, 4, 4, 2, 4};
@@ -864,6 +868,12 @@ static axh_status plan_q4k_matmul(uint32_t n_rows, uint32_t sb_per_row, uint32_t
         std::snprintf(name, cap, "axh_q4k_matmul_st_w%u_k%u_p%u", v.w, v.w / 4u, v.pf);
       else if (v.kind == 5)
         std::snprintf(name, cap, "axh_q4k_matmul_kx_r%u_n%u_k%u_p%u", v.rt, v.nt, v.w, v.pf);
+      else if (v.kind == 7) {
+        if (sb_per_row > kSrMaxSb)
+          return fail(AXH_ERR_INVALID_ARGUMENT,
+                      "matmul kind 7 takes rows of at most 16 superblocks (K <= 4096)");
+        std::snprintf(name, cap, "axh_q4k_matmul_sr_w%u_s2", v.w);
+      }
       else
         std::snprintf(name, cap, "axh_q4k_matmul_rs_w%u_r%u_n%u_p%u", v.w, v.rt, v.nt, v.pf);
       return ok();
@@ -913,9 +923,11 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
   if (s != AXH_OK) return s;
   // kind 4 stages 16 activation columns of the whole K in LDS; kind 5 sums the
   // partial tiles of its waves there (one 16x16 f32 tile = 1 KiB per wave)
+  // kind 7: 128 KiB of X staging, then two buffers of the waves' partial tiles
   const uint32_t lds = v.kind == 4 ? 16u * (sb_per_row * 256u + 8u) * 2u
                        : v.kind == 5 ? kx_lds_bytes(v)
                        : v.kind == 6 ? rs_lds_bytes(v)
+                       : v.kind == 7 ? 131072u + 2u * v.w * 1024u
                                      : 0u;
   if (lds > ctx->core->max_lds)
     return fail(AXH_ERR_INVALID_ARGUMENT, "matmul variant needs more LDS than the device has");
@@ -923,6 +935,7 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
                       : v.kind == 4 ? 64u // 4 tile slots
                       : v.kind == 5 ? 16u * v.rt
                       : v.kind == 6 ? 16u * v.rt * v.w
+                      : v.kind == 7 ? 16u
                                     : 32u * v.w;
   const uint32_t tn = 16u * v.nt;
   uint64_t gx = (n_rows + tm - 1) / tm;
@@ -933,7 +946,7 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
   axh_kernel *k = nullptr;
   s = builtin_kernel(ctx, name, 3, sizeof(MatmulArgs), v.w * 64u, &k);
   if (s != AXH_OK) return s;
-  if (v.kind == 4) { // persistent: at most one resident wave of workgroups per column group
+  if (v.kind == 4 || v.kind == 7) { // persistent: one resident wave of workgroups per column group
     const uint64_t resident = (uint64_t)occupancy(ctx, k, lds) * ctx->core->cu_count;
     if (resident < gx) gx = resident;
   }

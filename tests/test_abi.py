@@ -183,9 +183,14 @@ def test_matmul_kernel_selection(axc):
     """Defaults per batch: the K-split tile kind (its LDS ring does not grow
     with K) with all columns in one group up to 128, register A beyond."""
     name = axc.q4k_matmul_kernel_name
-    assert name(14336, 16, 8) == "axh_q4k_matmul_kx_r4_n1_k4_p3"
-    assert name(14336, 16, 16) == "axh_q4k_matmul_kx_r4_n1_k4_p3"
+    # up to 16 columns and K <= 4096: streaming rows; longer rows: the K-split tile
+    assert name(14336, 16, 8) == "axh_q4k_matmul_sr_w8_s2"
+    assert name(14336, 16, 16) == "axh_q4k_matmul_sr_w8_s2"
+    assert name(14336, 1, 1) == "axh_q4k_matmul_sr_w8_s2"
     assert name(4096, 56, 8) == "axh_q4k_matmul_kx_r4_n1_k4_p3"
+    assert name(4096, 17, 16) == "axh_q4k_matmul_kx_r4_n1_k4_p3"
+    with pytest.raises(axc.DispatchError):  # kind 7 keeps K <= 4096 of X in registers
+        name(4096, 17, 16, axc.MatmulVariant(7, 8, 1, 1))
     assert name(14336, 16, 32) == "axh_q4k_matmul_kx_r4_n2_k4_p2"
     assert name(14336, 16, 64) == "axh_q4k_matmul_kx_r4_n4_k4_p2"
     assert name(14336, 16, 128) == "axh_q4k_matmul_kx_r4_n8_k4_p2"
@@ -197,7 +202,7 @@ def test_matmul_kernel_selection(axc):
         name(14336, 16, 8, axc.MatmulVariant(1, 3, 1, 1))
     vs = axc.compiled_matmul_variants()
     assert len(set(vs)) == len(vs) >= 6
-    assert {v.kind for v in vs} == {1, 2, 3, 4, 5, 6}
+    assert {v.kind for v in vs} == {1, 2, 3, 4, 5, 6, 7}
     assert name(14336, 16, 8, axc.MatmulVariant(4, 4, 1, 4)) == "axh_q4k_matmul_st_w4_k1_p4"
     assert name(14336, 16, 128, axc.MatmulVariant(5, 4, 8, 2, 4)) == \
         "axh_q4k_matmul_kx_r4_n8_k4_p2"

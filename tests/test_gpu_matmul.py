@@ -146,6 +146,20 @@ def test_tile_kinds_on_odd_shapes(ctx, axc, rows, sb, batch):
         _check(y, q, xh, rows, sb, batch, f"odd {rows}x{sb} B={batch} {v}")
 
 
+@pytest.mark.parametrize("rows,sb,batch", [(5000, 13, 13), (4097, 16, 16), (17, 7, 1),
+                                           (1000, 16, 3), (70000, 2, 9)])
+def test_streaming_rows_kind(ctx, axc, rows, sb, batch):
+    """Kind 7 (the default up to 16 columns and K <= 4096): more 16-row blocks
+    than workgroups (several per workgroup), a partial last block, rows not a
+    multiple of 4 (scalar stores), waves whose superblocks lie past the row
+    (K < 4096), a single column."""
+    assert axc.q4k_matmul_kernel_name(rows, sb, batch) == "axh_q4k_matmul_sr_w8_s2"
+    _say(f"matmul streaming rows {rows}x{sb * 256} B={batch}")
+    q, xh = _inputs(rows + sb * 5 + batch, rows, sb, batch)
+    y = _run(ctx, q, xh, rows, sb, batch)
+    _check(y, q, xh, rows, sb, batch, f"streaming rows {rows}x{sb} B={batch}")
+
+
 @pytest.mark.parametrize("batch", [8, 40, 200])
 def test_output_only_4_byte_aligned(ctx, batch):
     """y 4 bytes past a 16-byte boundary: the tile stores fall back to single
