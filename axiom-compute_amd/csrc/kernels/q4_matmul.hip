@@ -35,7 +35,7 @@
 //     32-row tile and split K, summing in LDS;
 //   * streaming (axh_q4k_matmul_st_...): persistent, 16 columns of the whole
 //     K staged once in LDS;
-//   * streaming rows (axh_q4k_matmul_sr_...; the default up to 16 columns
+//   * streaming rows (axh_q4k_matmul_sr_...; the default up to 32 columns
 //     and K <= 4096): persistent, K split across the waves, X fragments kept
 //     in VGPRs, weights streamed like the matvec; see q4k_matmul_sr.
 // LDS rows are padded to 136 halves (272 bytes) so that 16 lanes reading
@@ -1043,9 +1043,9 @@ __device__ __forceinline__ void q4k_matmul_rs(const uint8_t *__restrict__ q,
 }
 
 // ---------------------------------------------------------------------------
-// Streaming rows (kind 7, the default up to 16 columns and K <= 4096): a
+// Streaming rows (kind 7, the default up to 32 columns and K <= 4096): a
 // persistent workgroup of NW waves walks 16-row blocks b = blockIdx.x +
-// k * gridDim.x for the 16 columns n0 = 16 * blockIdx.y ..; wave w owns
+// k * gridDim.x for the 16 * NC columns n0 = 16 * NC * blockIdx.y ..; wave w owns
 // superblocks [w*SPW, w*SPW + SPW) of every row (K split NW ways), so its X
 // fragments for those superblocks stay in VGPRs for the whole kernel and
 // only weights stream.  Per superblock a lane (row r = lane % 16, k-block
@@ -1057,8 +1057,9 @@ __device__ __forceinline__ void q4k_matmul_rs(const uint8_t *__restrict__ q,
 // 8t .., sub-block 2g + 1); the X fragment of step t holds the same k.  The
 // NW partial 16x16 tiles of a block are summed in LDS in wave order
 // (deterministic) by wave k % NW, which stores them.  Against the K-split
-// tile kind at 14336 x 4096: 11.2 vs 14.2 us at 8 columns, 11.8 vs 14.6 at 16.
-template <int NW, int SPW>
+// tile kind at 14336 x 4096: 11.2 vs 14.2 us at 8 columns, 11.8 vs 14.6 at 16,
+// 15.0 vs 16.0 at 32 (NC = 2: every A fragment feeds two MFMAs).
+template <int NW, int SPW, int NC>
 __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
                                               const uint16_t *__restrict__ x,
                                               float *__restrict__ y, const MatmulArgs a,
@@ -1073,7 +1074,7 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
   const __amdgpu_buffer_rsrc_t xr = rsrc(x, batch * K * 2u);
   const uint32_t n_blocks = (n_rows + 15u) >> 4;
   const uint32_t n_myb = blockIdx.x < n_blocks ? (n_blocks - 1u - blockIdx.x) / gridDim.x + 1u : 0u;
-  const uint32_t n0 = 16u * blockIdx.y; // this workgroup's 16 columns
+  const uint32_t n0 = 16u * NC * blockIdx.y; // this workgroup's 16 * NC columns
 
   // Weight loads of step (k, j): row 16 b + r, superblock wave*SPW + j: header
   // and the 32 qs bytes of chunk g.
@@ -1085,42 +1086,51 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
     QA[slot] = bload16(qr, off == kOob ? kOob : off + 16u + 32u * g);
     QB[slot] = bload16(qr, off == kOob ? kOob : off + 32u + 32u * g);
   };
-  // X fragments of the wave's superblocks (column r, k-block g of step t),
-  // staged through a wave-private LDS region by coalesced direct-to-LDS loads
-  // (all below 128 KiB of LDS): instruction (pc, n) copies 1 KiB of column n
-  // (two superblocks of k), lane l taking 16-byte piece l ^ n, so that the
+  // X fragments of the wave's superblocks (column group c, column r, k-block g
+  // of step t), staged per column group through a wave-private LDS region of
+  // 16 * 512 * SPW bytes (all regions within the first 128 KiB of LDS) by
+  // coalesced direct-to-LDS loads: instruction (pc, n) copies 1 KiB of column
+  // n (two superblocks of k), lane l taking 16-byte piece l ^ n, so that the
   // 16 lanes of a fragment read (columns 0..15, same piece) hit 16 different
   // bank groups.  Then each lane reads its 8 * SPW fragments into VGPRs.
   static_assert(NW * SPW <= 16, "X staging: NW * SPW * 8 KiB must fit 128 KiB");
-  half8_t xf[SPW][8];
+  half8_t xf[NC][SPW][8];
   {
     typedef __attribute__((address_space(3))) void lds_void_t;
-    constexpr uint32_t kColB = 512u * SPW;                // staged bytes per column
+    constexpr uint32_t kColB = 512u * SPW; // staged bytes per column
     uint8_t *xs = reinterpret_cast<uint8_t *>(red) + wave * 16u * kColB;
     issue(0u, 0, 0); // the first step's weights, in flight during the X staging
 #pragma unroll
-    for (int pc = 0; pc < SPW / 2; ++pc)
+    for (int c = 0; c < NC; ++c) {
+      // the previous group's fragment reads are done before the region is refilled
+      if (c > 0) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-      for (int n = 0; n < 16; ++n) {
-        const uint32_t s0 = wave * SPW + 2u * (uint32_t)pc;
-        const uint32_t piece = lane ^ (uint32_t)n, sl = s0 + (piece >> 5);
-        const uint32_t off = (n0 + (uint32_t)n < batch && sl < nsb)
-                                 ? ((n0 + (uint32_t)n) * K + 256u * s0) * 2u + 16u * piece
-                                 : kOob;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            xr, (lds_void_t *)(xs + (uint32_t)n * kColB + 1024u * (uint32_t)pc), 16, off, 0, 0, 0);
-      }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // every X piece is in LDS
+      for (int pc = 0; pc < SPW / 2; ++pc)
 #pragma unroll
-    for (int j = 0; j < SPW; ++j)
+        for (int n = 0; n < 16; ++n) {
+          const uint32_t col = n0 + 16u * (uint32_t)c + (uint32_t)n;
+          const uint32_t s0 = wave * SPW + 2u * (uint32_t)pc;
+          const uint32_t piece = lane ^ (uint32_t)n, sl = s0 + (piece >> 5);
+          const uint32_t off =
+              (col < batch && sl < nsb) ? (col * K + 256u * s0) * 2u + 16u * piece : kOob;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              xr, (lds_void_t *)(xs + (uint32_t)n * kColB + 1024u * (uint32_t)pc), 16, off, 0, 0,
+              0);
+        }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // every X piece is in LDS
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const uint32_t P = 32u * (uint32_t)j + 8u * g + (uint32_t)t; // 16-byte piece of the wave's k
-        const uint32_t addr = r * kColB + 1024u * (P >> 6) + 16u * ((P & 63u) ^ r);
-        xf[j][t] = *reinterpret_cast<const half8_t *>(xs + addr);
-      }
+      for (int j = 0; j < SPW; ++j)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const uint32_t P = 32u * (uint32_t)j + 8u * g + (uint32_t)t; // 16-byte piece of the wave's k
+          const uint32_t addr = r * kColB + 1024u * (P >> 6) + 16u * ((P & 63u) ^ r);
+          xf[c][j][t] = *reinterpret_cast<const half8_t *>(xs + addr);
+        }
+    }
   }
-  f32x4_t acc = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4_t acc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) acc[c] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
   for (uint32_t k = 0; k < n_myb; ++k) {
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
@@ -1143,25 +1153,36 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
         uint32_t l0, l1, h0, h1, l2, l3, h2, h3;
         dequant_dword(w[2 * t], d1s, m1, d2s, m2, l0, l1, h0, h1);
         dequant_dword(w[2 * t + 1], d1s, m1, d2s, m2, l2, l3, h2, h3);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            __builtin_bit_cast(half8_t, make_uint4(l0, l1, l2, l3)), xf[j][t], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            __builtin_bit_cast(half8_t, make_uint4(h0, h1, h2, h3)), xf[j][t + 4], acc, 0, 0, 0);
+        const half8_t alo = __builtin_bit_cast(half8_t, make_uint4(l0, l1, l2, l3));
+        const half8_t ahi = __builtin_bit_cast(half8_t, make_uint4(h0, h1, h2, h3));
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, xf[c][j][t], acc[c], 0, 0, 0);
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, xf[c][j][t + 4], acc[c], 0, 0, 0);
+        }
       }
     }
-    // partial tiles of block k -> LDS (double buffer by block parity)
-    f32x4_t *buf = red + 8192u + (k & 1u) * (NW * 64u); // after the 128 KiB of X staging
-    buf[wave * 64u + lane] = acc;
-    acc = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+    // partial tiles of block k -> LDS (double buffer by block parity), after
+    // the 128 KiB of X staging
+    f32x4_t *buf = red + 8192u + (k & 1u) * (NW * NC * 64u);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      buf[(wave * NC + (uint32_t)c) * 64u + lane] = acc[c];
+      acc[c] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+    }
     // LDS-only barrier: the partial tiles must be written, while the weight
     // loads in flight and the previous block's y stores need not be waited for
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     if (wave == k % NW) {
-      f32x4_t sum = buf[lane];
-#pragma unroll
-      for (int w2 = 1; w2 < NW; ++w2) sum += buf[w2 * 64u + lane];
       const uint32_t b = blockIdx.x + k * gridDim.x;
-      if (n0 + r < batch) store_col4(y + (size_t)(n0 + r) * n_rows, 16u * b + 4u * g, n_rows, sum);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        f32x4_t sum = buf[(uint32_t)c * 64u + lane];
+#pragma unroll
+        for (int w2 = 1; w2 < NW; ++w2) sum += buf[((uint32_t)w2 * NC + (uint32_t)c) * 64u + lane];
+        const uint32_t col = n0 + 16u * (uint32_t)c + r;
+        if (col < batch) store_col4(y + (size_t)col * n_rows, 16u * b + 4u * g, n_rows, sum);
+      }
     }
   }
 }
@@ -1252,13 +1273,14 @@ AXH_Q4K_MATMUL_RS(4, 4, 8, 4)
 AXH_Q4K_MATMUL_RS(8, 2, 4, 4)
 AXH_Q4K_MATMUL_RS(8, 1, 8, 4)
 
-#define AXH_Q4K_MATMUL_SR(NW, SPW)                                                               \
+#define AXH_Q4K_MATMUL_SR(NW, SPW, NC, SUFFIX)                                                   \
   extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
-      axh_q4k_matmul_sr_w##NW##_s##SPW(const uint8_t *__restrict__ q,                            \
-                                       const uint16_t *__restrict__ x, float *__restrict__ y,    \
-                                       MatmulArgs a) {                                           \
+      axh_q4k_matmul_sr_w##NW##_s##SPW##SUFFIX(const uint8_t *__restrict__ q,                    \
+                                               const uint16_t *__restrict__ x,                   \
+                                               float *__restrict__ y, MatmulArgs a) {            \
     extern __shared__ f32x4_t axh_sr_dyn[];                                                      \
-    q4k_matmul_sr<NW, SPW>(q, x, y, a, axh_sr_dyn);                                              \
+    q4k_matmul_sr<NW, SPW, NC>(q, x, y, a, axh_sr_dyn);                                          \
   }
 
-AXH_Q4K_MATMUL_SR(8, 2)
+AXH_Q4K_MATMUL_SR(8, 2, 1, )
+AXH_Q4K_MATMUL_SR(8, 2, 2, _n2)

@@ -56,7 +56,7 @@ constexpr MatmulVariant kQ4kMatmulVariants[] = {
     {4, 4, 1, 4, 0},  {4, 8, 1, 4, 0},  {4, 8, 1, 2, 0},  {4, 16, 1, 2, 0}, {4, 16, 1, 4, 0},
     {5, 4, 8, 2, 4},  {5, 4, 8, 2, 2},  {5, 4, 4, 2, 4},  {5, 4, 4, 3, 4},  {5, 4, 4, 2, 8},
     {5, 4, 2, 2, 4},  {5, 4, 2, 3, 4},  {5, 4, 1, 3, 4},  {6, 8, 8, 4, 2},  {6, 8, 8, 3, 2},
-    {6, 4, 8, 4, 4},  {6, 8, 4, 4, 2},  {6, 8, 8, 4, 1},  {7, 8, 1, 1, 0}};
+    {6, 4, 8, 4, 4},  {6, 8, 4, 4, 2},  {6, 8, 8, 4, 1},  {7, 8, 1, 1, 0},  {7, 8, 2, 1, 0}};
 constexpr uint32_t kMatmulOob = 0xFFFFFF00u; // the kernels' out-of-range offset
 
 struct MatvecVariant {
@@ -813,7 +813,11 @@ constexpr uint32_t kSrMaxSb = 16;
 
 static MatmulVariant q4k_matmul_default(uint32_t n_rows, uint32_t batch, uint32_t nsb) {
   (void)n_rows;
+  // kind 7 against the K-split tile kind at 14336 x 4096 (A/B in one run):
+  // B = 8 11.2 vs 14.2 us, B = 16 11.8 vs 14.6, B = 32 (two column groups per
+  // workgroup) 15.0 vs 16.0; at B = 64 the K-split tile kind stays ahead.
   if (batch <= 16 && nsb <= kSrMaxSb) return {7, 8, 1, 1, 0};
+  if (batch <= 32 && nsb <= kSrMaxSb) return {7, 8, 2, 1, 0};
   if (batch <= 16) return {5, 4, 1, 3, 4};
   if (batch <= 32) return {5, 4, 2, 2, 4};
   if (batch <= 64) return {5, 4, 4, 2, 4};
@@ -872,7 +876,7 @@ static axh_status plan_q4k_matmul(uint32_t n_rows, uint32_t sb_per_row, uint32_t
         if (sb_per_row > kSrMaxSb)
           return fail(AXH_ERR_INVALID_ARGUMENT,
                       "matmul kind 7 takes rows of at most 16 superblocks (K <= 4096)");
-        std::snprintf(name, cap, "axh_q4k_matmul_sr_w%u_s2", v.w);
+        std::snprintf(name, cap, "axh_q4k_matmul_sr_w%u_s2%s", v.w, v.nt == 2 ? "_n2" : "");
       }
       else
         std::snprintf(name, cap, "axh_q4k_matmul_rs_w%u_r%u_n%u_p%u", v.w, v.rt, v.nt, v.pf);
@@ -927,7 +931,7 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
   const uint32_t lds = v.kind == 4 ? 16u * (sb_per_row * 256u + 8u) * 2u
                        : v.kind == 5 ? kx_lds_bytes(v)
                        : v.kind == 6 ? rs_lds_bytes(v)
-                       : v.kind == 7 ? 131072u + 2u * v.w * 1024u
+                       : v.kind == 7 ? 131072u + 2u * v.w * v.nt * 1024u
                                      : 0u;
   if (lds > ctx->core->max_lds)
     return fail(AXH_ERR_INVALID_ARGUMENT, "matmul variant needs more LDS than the device has");

@@ -187,11 +187,13 @@ def test_matmul_kernel_selection(axc):
     assert name(14336, 16, 8) == "axh_q4k_matmul_sr_w8_s2"
     assert name(14336, 16, 16) == "axh_q4k_matmul_sr_w8_s2"
     assert name(14336, 1, 1) == "axh_q4k_matmul_sr_w8_s2"
+    assert name(14336, 16, 32) == "axh_q4k_matmul_sr_w8_s2_n2"  # two column groups
+    assert name(14336, 16, 17) == "axh_q4k_matmul_sr_w8_s2_n2"
     assert name(4096, 56, 8) == "axh_q4k_matmul_kx_r4_n1_k4_p3"
     assert name(4096, 17, 16) == "axh_q4k_matmul_kx_r4_n1_k4_p3"
     with pytest.raises(axc.DispatchError):  # kind 7 keeps K <= 4096 of X in registers
         name(4096, 17, 16, axc.MatmulVariant(7, 8, 1, 1))
-    assert name(14336, 16, 32) == "axh_q4k_matmul_kx_r4_n2_k4_p2"
+    assert name(4096, 56, 32) == "axh_q4k_matmul_kx_r4_n2_k4_p2"
     assert name(14336, 16, 64) == "axh_q4k_matmul_kx_r4_n4_k4_p2"
     assert name(14336, 16, 128) == "axh_q4k_matmul_kx_r4_n8_k4_p2"
     assert name(14336, 16, 256) == "axh_q4k_matmul_rs_w8_r1_n8_p4"

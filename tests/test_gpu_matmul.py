@@ -147,13 +147,15 @@ def test_tile_kinds_on_odd_shapes(ctx, axc, rows, sb, batch):
 
 
 @pytest.mark.parametrize("rows,sb,batch", [(5000, 13, 13), (4097, 16, 16), (17, 7, 1),
-                                           (1000, 16, 3), (70000, 2, 9)])
+                                           (1000, 16, 3), (70000, 2, 9), (4097, 16, 32),
+                                           (333, 11, 19), (70000, 3, 25)])
 def test_streaming_rows_kind(ctx, axc, rows, sb, batch):
-    """Kind 7 (the default up to 16 columns and K <= 4096): more 16-row blocks
+    """Kind 7 (the default up to 32 columns and K <= 4096; two column groups
+    per workgroup beyond 16 columns): more 16-row blocks
     than workgroups (several per workgroup), a partial last block, rows not a
     multiple of 4 (scalar stores), waves whose superblocks lie past the row
     (K < 4096), a single column."""
-    assert axc.q4k_matmul_kernel_name(rows, sb, batch) == "axh_q4k_matmul_sr_w8_s2"
+    assert axc.q4k_matmul_kernel_name(rows, sb, batch).startswith("axh_q4k_matmul_sr_w8_s2")
     _say(f"matmul streaming rows {rows}x{sb * 256} B={batch}")
     q, xh = _inputs(rows + sb * 5 + batch, rows, sb, batch)
     y = _run(ctx, q, xh, rows, sb, batch)
