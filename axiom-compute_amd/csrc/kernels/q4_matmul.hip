@@ -14,8 +14,8 @@
 //
 // Seven kernel kinds (the runtime picks per batch size; the others stay
 // reachable as strategy variants):
-//   * K-split tile (axh_q4k_matmul_kx_...; the default from 17 to 128
-//     columns, and up to 16 columns when K > 4096):
+//   * K-split tile (axh_q4k_matmul_kx_...; the default from 33 to 128
+//     columns, and up to 32 columns when K > 4096):
 //     the waves of a workgroup split K, each streaming raw weight bytes and
 //     X through a private LDS ring filled by coalesced direct-to-LDS loads;
 //     see q4k_matmul_kx;
