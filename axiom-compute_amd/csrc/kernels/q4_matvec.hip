@@ -699,49 +699,60 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
 
 // One pass, one bundle pair per wave (axh_q4k_matvec_one_i{NIT}): rows of
 // 8 * (NIT - 1) < nsb <= 8 * NIT superblocks, 8 waves per workgroup, wave W
-// takes rows 2W and 2W + 1 and the grid covers all pairs.  The persistent
-// kernel's early-refill order (one iteration in flight, x staged chunk by
-// chunk with the weights), fully unrolled over the NIT iterations so that no
-// load, barrier or bookkeeping is spent past the row.  On 4096 x 14336 (one
-// pair per wave either way) this measured 8.13-8.36 us per back-to-back call
-// against 8.62-8.76 us for the persistent early-refill kernel, whose first
-// pass loops over an even trip count.
-template <int NIT>
+// takes rows 2W and 2W + 1 and the grid covers all of them, one workgroup per
+// 16 rows.  The persistent kernel's early-refill order (one iteration in
+// flight, x staged chunk by chunk with the weights), fully unrolled over the
+// NIT iterations, so no load, barrier or bookkeeping is spent past the row.
+// Every row group stages x itself (nsb KiB per 16 rows), which costs more
+// than it saves only for very tall matrices.  Measured against the persistent
+// kernels (A/B in one run): 4096 x 14336 8.13-8.36 vs 8.62-8.76 us, 4096 x
+// 4096 4.06 vs 4.62-4.92, 14336 x 4096 8.9-9.1 vs 9.9-10.5, 32768 x 4096 17.0
+// vs 18.6; the 128256-row head 56.8 vs 53.5 (persistent prefetch 2) stays
+// persistent.  The template also covers the fused gate/up (kDual) and Q5_K
+// (kQ5) layouts, but there it measured no faster than the persistent kernels
+// (2 x 14336 x 4096: 16.8 vs 16.8 us; Q5_K 14336 x 4096: 11.7 vs 11.3), so
+// only the Q4_K instances are built.
+template <int NIT, bool kDual = false, bool kQ5 = false>
 __device__ __forceinline__ void q4k_matvec_one(const uint8_t *__restrict__ q,
+                                               const uint8_t *__restrict__ q2,
                                                const float *__restrict__ x, float *__restrict__ y,
                                                uint32_t n_rows, uint32_t nsb, float *lds) {
   constexpr int NW = 8, NT = NW * 64;
+  constexpr int RPW = kDual ? 2 : 1; // row slots per lane: (gate, up) or one row
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t G = lane >> 2, half = G >> 3, s = G & 7u, c = lane & 3u;
   const uint32_t W = blockIdx.x * NW + wave;
   const bool mine = W < (n_rows + 1u) >> 1; // this wave has a pair of rows
-  const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
+  const uint32_t row_bytes = nsb * (kQ5 ? kQ5kSbBytes : (uint32_t)kQ4kSbBytes);
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(q, n_rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t qr2 = kDual ? make_rsrc(q2, n_rows * row_bytes) : qr;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, nsb * 1024u);
   float *xs = lds;
   float *ss = lds + nsb * kQ4kFlatSbFloats;
   const uint32_t bundle = 2u * W + half;
-  Q4kFlatBuf<1, 2, false> B;
+  Q4kFlatBuf<RPW, 2, kQ5> B;
   float4 xv[2][512 / NT];
-  float acc[1] = {0.0f};
+  float acc[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
   q4k_flat_load_chunk<NT>(xr, tid, 0u, xv[0]);
-  q4k_flat_load<1, 2, false, false, false>(B, 0, qr, qr, row_bytes, bundle, 0u, s, c);
+  q4k_flat_load<RPW, 2, false, kDual, kQ5>(B, 0, qr, qr2, row_bytes, bundle, 0u, s, c);
 #pragma unroll
   for (int j = 0; j < NIT; ++j) {
     const int p = j & 1;
     q4k_flat_stage_chunk<NT>(xs, ss, tid, (uint32_t)j, nsb, xv[p]);
     if (j + 1 < NIT) { // next iteration's x chunk and weights, before the compute
       q4k_flat_load_chunk<NT>(xr, tid, (uint32_t)(j + 1), xv[p ^ 1]);
-      q4k_flat_load<1, 2, false, false, false>(B, p ^ 1, qr, qr, row_bytes, bundle,
+      q4k_flat_load<RPW, 2, false, kDual, kQ5>(B, p ^ 1, qr, qr2, row_bytes, bundle,
                                                (uint32_t)(j + 1), s, c);
     }
     __syncthreads();
     const uint32_t sb = (uint32_t)j * 8u + s;
-    if (mine && sb < nsb) q4k_flat_compute<1, 2, false>(B, p, xs, ss, sb, c, acc);
+    if (mine && sb < nsb) q4k_flat_compute<RPW, 2, kQ5>(B, p, xs, ss, sb, c, acc);
   }
-  if (mine) q4k_flat_store<1, false>(acc, 2u * W, lane, n_rows, y);
+  if (mine) q4k_flat_store<RPW, kDual>(acc, 2u * W, lane, n_rows, y);
 }
 
 #define AXH_Q4K_MATVEC_ONE(NIT)                                                                  \
@@ -749,8 +760,12 @@ __device__ __forceinline__ void q4k_matvec_one(const uint8_t *__restrict__ q,
       axh_q4k_matvec_one_i##NIT(const uint8_t *__restrict__ q, const float *__restrict__ x,      \
                                 float *__restrict__ y, RowsArgs a) {                             \
     extern __shared__ float axh_lds_dyn[];                                                       \
-    q4k_matvec_one<NIT>(q, x, y, a.n_rows, a.units_per_row, axh_lds_dyn);                        \
+    q4k_matvec_one<NIT>(q, q, x, y, a.n_rows, a.units_per_row, axh_lds_dyn);                     \
   }
+AXH_Q4K_MATVEC_ONE(1)
+AXH_Q4K_MATVEC_ONE(2)
+AXH_Q4K_MATVEC_ONE(3)
+AXH_Q4K_MATVEC_ONE(4)
 AXH_Q4K_MATVEC_ONE(5)
 AXH_Q4K_MATVEC_ONE(6)
 AXH_Q4K_MATVEC_ONE(7)

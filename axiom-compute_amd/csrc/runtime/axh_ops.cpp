@@ -345,16 +345,27 @@ static bool q4k_use_wg(uint32_t n_rows, uint32_t nsb) {
 }
 
 // One pass with one pair of rows per wave (axh_q4k_matvec_one_i{NIT}, NIT =
-// ceil(nsb / 8) in 5..16) for long rows, when the 8-wave workgroups for all
-// rows (16 rows each) fit the 256 CUs of an MI355X at once: each workgroup
-// then stages x once for its 16 rows either way, and the one-pass kernel
-// skips the persistent kernel's bookkeeping (4096 x 14336: 8.1-8.4 vs 8.5-8.7
-// us per call).
-constexpr uint32_t kOneMinSb = 33, kOneMaxSb = 128, kOneMaxRows = 16u * 256u;
+// ceil(nsb / 8)): one 8-wave workgroup per 16 rows, all launched, each
+// staging x for its own rows.  Faster than the persistent kernels from 32 up
+// to 32768 rows (A/B in one run: 4096 x 14336 8.1-8.4 vs 8.5-8.7 us, 4096 x
+// 4096 4.06 vs 4.6-4.9, 14336 x 4096 8.9-9.1 vs 9.9-10.5, 32768 x 4096 17.0
+// vs 18.6); on the 128256-row head (8016 workgroups) the persistent kernel
+// stays ahead (53.5 vs 56.8 us).
+constexpr uint32_t kOneMinRows = 32, kOneMaxRows = 32768, kOneMaxSb = 128;
 
-static bool q4k_use_one(uint32_t n_rows, uint32_t nsb) {
-  return nsb >= kOneMinSb && nsb <= kOneMaxSb && n_rows >= kQ4kColsMaxRows &&
-         n_rows <= kOneMaxRows;
+static bool use_one_pass(uint32_t n_rows, uint32_t nsb) {
+  return nsb >= 1 && nsb <= kOneMaxSb && n_rows >= kOneMinRows && n_rows <= kOneMaxRows;
+}
+
+// Fills a one-pass plan for kernel family `prefix` (LDS: lds_per_sb per superblock of x).
+static void plan_one_pass(const char *prefix, uint32_t n_rows, uint32_t nsb, uint32_t lds_per_sb,
+                          Q4kPlan *p) {
+  std::snprintf(p->name, sizeof(p->name), "%s_one_i%u", prefix, (nsb + 7u) / 8u);
+  p->nw = 8;
+  p->lds = nsb * lds_per_sb;
+  p->flat = false; // one workgroup per 16 rows, all of them launched
+  p->units = (n_rows + 15u) / 16u;
+  p->args = RowsArgs{n_rows, nsb, nsb, 0};
 }
 
 static axh_status plan_q4k(uint32_t n_rows, uint32_t sb_per_row, const axh_q4_variant *variant,
@@ -392,13 +403,8 @@ static axh_status plan_q4k(uint32_t n_rows, uint32_t sb_per_row, const axh_q4_va
     p->args = RowsArgs{n_rows, sb_per_row, sb_per_row, 0};
     return ok();
   }
-  if (!variant && q4k_use_one(n_rows, sb_per_row)) {
-    std::snprintf(p->name, sizeof(p->name), "axh_q4k_matvec_one_i%u", (sb_per_row + 7u) / 8u);
-    p->nw = 8;
-    p->lds = sb_per_row * 1120u;
-    p->flat = false; // one workgroup per 16 rows, all of them launched
-    p->units = (n_rows + 15u) / 16u;
-    p->args = RowsArgs{n_rows, sb_per_row, sb_per_row, 0};
+  if (!variant && use_one_pass(n_rows, sb_per_row) && q_bytes < 0xFFFFFFFFull) {
+    plan_one_pass("axh_q4k_matvec", n_rows, sb_per_row, 1120u, p);
     return ok();
   }
   const MatvecVariant dflt = q4k_default(n_rows, sb_per_row);
@@ -555,8 +561,10 @@ axh_status axh_q4k_gate_up(axh_context *ctx, const void *q_gate, const void *q_u
   s = builtin_kernel(ctx, p.name, 4, sizeof(RowsArgs), p.nw * 64u, &k);
   if (s != AXH_OK) return s;
   uint32_t grid[3] = {p.units, 1, 1};
-  const uint32_t resident = occupancy(ctx, k, p.lds) * ctx->core->cu_count;
-  if (resident < grid[0]) grid[0] = resident;
+  if (p.flat) { // persistent: at most one resident round of workgroups
+    const uint32_t resident = occupancy(ctx, k, p.lds) * ctx->core->cu_count;
+    if (resident < grid[0]) grid[0] = resident;
+  }
   void *bufs[4] = {const_cast<void *>(q_gate), const_cast<void *>(q_up), const_cast<float *>(x),
                    h};
   s = launch_raw(k, grid, bufs, 4, &p.args, sizeof(p.args), p.lds, pick_stream(ctx, stream));
@@ -646,8 +654,10 @@ static axh_status kq_matvec(const KqFormat &f, axh_context *ctx, const void *q, 
   s = builtin_kernel(ctx, p.name, 3, sizeof(RowsArgs), p.nw * 64u, &k);
   if (s != AXH_OK) return s;
   uint32_t grid[3] = {p.units, 1, 1};
-  const uint32_t resident = occupancy(ctx, k, p.lds) * ctx->core->cu_count;
-  if (resident < grid[0]) grid[0] = resident;
+  if (p.flat) { // persistent: at most one resident round of workgroups
+    const uint32_t resident = occupancy(ctx, k, p.lds) * ctx->core->cu_count;
+    if (resident < grid[0]) grid[0] = resident;
+  }
   void *bufs[3] = {const_cast<void *>(q), const_cast<float *>(x), y};
   s = launch_raw(k, grid, bufs, 3, &p.args, sizeof(p.args), p.lds, pick_stream(ctx, stream));
   return s == AXH_OK ? ok() : s;

@@ -99,7 +99,7 @@ def test_builtin_code_object_holds_every_variant_kernel(axc):
     for v in axc.compiled_variants("q4_0"):
         name = f"axh_q4_0_matvec_r{v.rows_per_wave}_w{v.waves_per_workgroup}"
         assert name.encode() in co, name
-    for nit in range(5, 17):  # one-pass kernels for rows of 33..128 superblocks
+    for nit in range(1, 17):  # one-pass kernels for rows of 1..128 superblocks
         assert f"axh_q4k_matvec_one_i{nit}".encode() in co
     for name in ("q4km_dequant_matvec", "q4_0_dequant_matvec", "axh_q4k_dequant",
                  "axh_q4_0_dequant", "axh_f16_widen", "axh_q4k_matvec_tiled_r2_w8_p2",
@@ -111,15 +111,19 @@ def test_kernel_selection_by_shape_and_variant(axc):
     """The entry point axh_q4k_matvec launches (no device work): persistent
     kernel while a row's x fits one workgroup's LDS, tiled kernel beyond."""
     name = axc.q4k_matvec_kernel_name
-    # long rows, up to 16 rows per CU: one pass, one pair of rows per wave
+    # 32..32768 rows: one pass, one pair of rows per wave, a workgroup per 16 rows
     assert name(4096, 56) == "axh_q4k_matvec_one_i7"
     assert name(32, 33) == "axh_q4k_matvec_one_i5"
     assert name(4096, 128) == "axh_q4k_matvec_one_i16"
-    assert name(4097, 56) == "axh_q4k_matvec_flat_r1_w8_p2_n0"
-    assert name(4096, 32) == "axh_q4k_matvec_flat_r2_w4_p1_n0"
-    assert name(4096, 16) == "axh_q4k_matvec_flat_r2_w4_p1_n0"
+    assert name(4097, 56) == "axh_q4k_matvec_one_i7"
+    assert name(4096, 32) == "axh_q4k_matvec_one_i4"
+    assert name(4096, 16) == "axh_q4k_matvec_one_i2"
+    assert name(32768, 1) == "axh_q4k_matvec_one_i1"
+    # taller matrices: the persistent kernels
+    assert name(32769, 16) == "axh_q4k_matvec_flat_r2_w4_p1_n0"
     assert name(128256, 16) == "axh_q4k_matvec_flat_r2_w4_p2_n0"  # the head keeps prefetch 2
-    assert name(8192, 128) == "axh_q4k_matvec_flat_r1_w16_p2_n0"
+    assert name(65536, 56) == "axh_q4k_matvec_flat_r1_w8_p2_n0"
+    assert name(65536, 128) == "axh_q4k_matvec_flat_r1_w16_p2_n0"
     # the early-refill (prefetch 1) kernels stage x in chunks: any row fits
     assert name(4096, 56, axc.Variant(2, 4, 1, 2)) == "axh_q4k_matvec_flat_r2_w4_p1_n0"
     assert name(1, 256) == "axh_q4k_matvec_sk_s16"  # few long rows: split-K
@@ -142,7 +146,7 @@ def test_kernel_selection_by_shape_and_variant(axc):
     assert name(8, 63) == "axh_q4k_matvec_cols_r4_w4_n0_x1"
     assert name(8, 56) == "axh_q4k_matvec_cols_r4_w4_n0_x1"
     assert name(31, 1) == "axh_q4k_matvec_cols_r4_w1_n0_x1"
-    assert name(32, 1) == "axh_q4k_matvec_flat_r2_w4_p1_n0"
+    assert name(32, 1) == "axh_q4k_matvec_one_i1"
     co = axc.builtin_code_object()
     for rows in (1, 31, 64):
         for sb in (1, 16, 56, 128, 129, 4096):
@@ -248,8 +252,8 @@ def test_kquant_kernel_selection(axc):
         assert name(128256, 16) == f"axh_{fam}_matvec_flat_r1_w4_p1_x1"
         assert name(4096, 56) == f"axh_{fam}_matvec_flat_r1_w8_p1_x1"
         # Q5_K's prefetch-1 kernel stages x in chunks; Q6_K's stages it whole
-        assert name(4096, 128) == ("axh_q5k_matvec_flat_r1_w8_p1_x1" if fam == "q5k"
-                                   else "axh_q6k_matvec_flat_r1_w8_p2_x2")
+        assert name(65536, 128) == ("axh_q5k_matvec_flat_r1_w8_p1_x1" if fam == "q5k"
+                                    else "axh_q6k_matvec_flat_r1_w8_p2_x2")
         assert name(4096, 56, axc.Variant(1, 4, 2, 0)) == f"axh_{fam}_matvec_flat_r1_w4_p2_x2"
         vs = axc.compiled_variants(fam)
         assert len(set(vs)) == len(vs) >= 3

@@ -279,10 +279,11 @@ def test_q4km_reference_kernel_many_superblocks(ctx, axc, n):
 
 # ---- long rows, up to 4096 of them: one pass, one pair of rows per wave ---------
 @pytest.mark.parametrize("rows,sb", [(32, 33), (33, 40), (47, 41), (100, 56), (4095, 57),
-                                     (1000, 127), (64, 128)])
+                                     (1000, 127), (64, 128), (32, 1), (33, 9), (4096, 16),
+                                     (30001, 3), (777, 24)])
 def test_q4k_one_pass_shapes(ctx, axc, rows, sb):
-    """Rows of 33..128 superblocks, 32..4096 rows: every unrolled trip count's
-    boundary (8k and 8k + 1 superblocks), an odd row count (a half-empty last
+    """32..32768 rows of 1..128 superblocks: trip counts 1..16 and their
+    boundaries (8k and 8k + 1 superblocks), odd row counts (a half-empty last
     pair) and workgroups past the last pair."""
     assert axc.q4k_matvec_kernel_name(rows, sb).startswith("axh_q4k_matvec_one_i")
     _say(f"q4k one pass {rows}x{sb}")
