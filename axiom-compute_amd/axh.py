@@ -208,6 +208,9 @@ def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
         "axh_q4k_dequant": (st, [vp, vp, vp, u64, vp]),
         "axh_q4_0_dequant": (st, [vp, vp, vp, u64, vp]),
         "axh_f16_widen": (st, [vp, vp, vp, u64, vp]),
+        "axh_read_floor": (st, [vp, vp, u64, vp, u32, vp]),
+        "axh_launch_empty": (st, [vp, vp, u32, vp]),
+        "axh_cu_count": (u32, [vp]),
         "axh_q4k_matvec_variant_count": (u32, []),
         "axh_q4k_matvec_variant_at": (st, [u32, c.POINTER(_Variant)]),
         "axh_q4_0_matvec_variant_count": (u32, []),
@@ -781,6 +784,18 @@ class HipContext:
 
     def f16_widen(self, h, f, n: int, stream=None) -> None:
         _check(self._lib.axh_f16_widen(self._raw, _ptr(h), _ptr(f), n, _stream(stream)))
+
+    def cu_count(self) -> int:
+        return int(self._lib.axh_cu_count(self._raw))
+
+    def read_floor(self, q, nbytes: int, out, out_words: int, stream=None) -> None:
+        """Stream nbytes of q with the matvec's launch shape (measurement helper)."""
+        _check(self._lib.axh_read_floor(self._raw, _ptr(q), nbytes, _ptr(out), out_words,
+                                        _stream(stream)))
+
+    def launch_empty(self, out, out_words: int, stream=None) -> None:
+        """An empty kernel with the matvec's launch shape (measurement helper)."""
+        _check(self._lib.axh_launch_empty(self._raw, _ptr(out), out_words, _stream(stream)))
 
 
 def header_functions(header: Path = HEADER_PATH) -> list[str]:

@@ -1944,6 +1944,39 @@ extern "C" __global__ void __launch_bounds__(256)
   }
 }
 
+// Measurement helpers for the floor that one launch per call puts under a
+// matvec (no counterpart in the reference).  axh_read_floor streams
+// a.n_units 16-byte pieces of q with the matvec's launch shape (one 8-wave
+// workgroup per CU, 16-byte buffer loads, four in flight per lane) and
+// writes, per wave, the XOR of every dword it read to out[wave], so the loads
+// cannot be dropped and each wave ends with one store, as a matvec wave does.
+extern "C" __global__ void __launch_bounds__(512) axh_read_floor(const uint8_t *__restrict__ q,
+                                                                 uint32_t *__restrict__ out,
+                                                                 CountArgs a) {
+  const uint32_t n = a.n_units, nt = gridDim.x * 512u;
+  const uint32_t gtid = blockIdx.x * 512u + threadIdx.x;
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(q, n * 16u);
+  uint32_t acc = 0;
+  for (uint32_t i = gtid; i < n; i += 4u * nt) {
+    uint4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = buf_load16<false>(r, (i + (uint32_t)u * nt) * 16u);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  for (int off = 32; off >= 1; off >>= 1) // XOR across the wave
+
+    acc ^= (uint32_t)__shfl_xor((int)acc, off, 64);
+  if ((threadIdx.x & 63u) == 0u) out[gtid >> 6] = acc;
+}
+
+// The same launch shape doing nothing: the per-launch cost alone.
+extern "C" __global__ void __launch_bounds__(512) axh_launch_empty(const uint8_t *__restrict__ q,
+                                                                   uint32_t *__restrict__ out,
+                                                                   CountArgs a) {
+  if (a.n_units == 0xFFFFFFFFu && threadIdx.x == 0) out[0] = (uint32_t)(uintptr_t)q;
+}
+
 // Bounded busy wait (runtime tests of the completion timeout): sleeps
 // a.n_units times (about 3 us each) and then writes the count.  Always ends.
 extern "C" __global__ void __launch_bounds__(64) axh_spin(uint32_t *__restrict__ out,

@@ -1033,6 +1033,40 @@ axh_status axh_q4_0_dequant(axh_context *ctx, const void *q, float *w, uint64_t 
   return count_launch(ctx, "axh_q4_0_dequant", q, w, n_blocks, n_blocks, stream);
 }
 
+// Measurement helpers: the matvec's launch shape (one 512-thread workgroup
+// per CU) reading `bytes` or doing nothing.
+static axh_status floor_launch(axh_context *ctx, const char *name, const void *q, uint64_t pieces,
+                               uint32_t *out, uint32_t out_words, void *stream) {
+  if (!ctx) return fail(AXH_ERR_INVALID_ARGUMENT, "ctx is NULL");
+  if (!device_ptr_ok(out) || (pieces && !device_ptr_ok(q)))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q and out must be device pointers");
+  if (((uintptr_t)q & 15u) || pieces > 0xFFFFFFFFull / 16u)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q must be 16-byte aligned and below 4 GiB");
+  const uint32_t grid[3] = {ctx->core->cu_count, 1, 1};
+  if (out_words < 8u * grid[0])
+    return fail(AXH_ERR_INVALID_ARGUMENT, "out needs 8 words per compute unit");
+  hipSetDevice(ctx->core->device);
+  axh_kernel *k = nullptr;
+  axh_status s = builtin_kernel(ctx, name, 2, sizeof(CountArgs), 512, &k);
+  if (s != AXH_OK) return s;
+  CountArgs a{(uint32_t)pieces};
+  void *bufs[2] = {const_cast<void *>(q), out};
+  s = launch_raw(k, grid, bufs, 2, &a, sizeof(a), 0, pick_stream(ctx, stream));
+  return s == AXH_OK ? ok() : s;
+}
+
+axh_status axh_read_floor(axh_context *ctx, const void *q, uint64_t bytes, uint32_t *out,
+                          uint32_t out_words, void *stream) {
+  if (bytes % 16u) return fail(AXH_ERR_INVALID_ARGUMENT, "bytes must be a multiple of 16");
+  return floor_launch(ctx, "axh_read_floor", q, bytes / 16u, out, out_words, stream);
+}
+
+axh_status axh_launch_empty(axh_context *ctx, uint32_t *out, uint32_t out_words, void *stream) {
+  return floor_launch(ctx, "axh_launch_empty", out, 0, out, out_words, stream);
+}
+
+uint32_t axh_cu_count(axh_context *ctx) { return ctx ? ctx->core->cu_count : 0u; }
+
 axh_status axh_f16_widen(axh_context *ctx, const uint16_t *h, float *f, uint64_t n, void *stream) {
   return count_launch(ctx, "axh_f16_widen", h, f, n, n, stream);
 }

@@ -370,6 +370,42 @@ def main() -> int:
     per_call = sorted(evs[g].elapsed_ms(evs[g + 1]) * 1000.0 / group for g in range(n_groups))
     pct = {p: round(per_call[min(len(per_call) - 1, int(p / 100 * len(per_call)))], 3)
            for p in (10, 50, 90)}
+    # The floor of the launch-per-call protocol on this box, for matvec
+    # workloads: the same number of bytes read from the same rotated copies by
+    # a kernel of the same launch shape that only reads (one store per wave),
+    # and an empty kernel of that shape, both launched back to back like the
+    # timed calls.
+    floor = None
+    if kind != "matmul":
+        words = 8 * ctx.cu_count()
+        fout = ctx.alloc(words * 4)
+        nb = case.weight_bytes // 16 * 16
+
+        def floor_us(fn):
+            for i in range(args.warmup):
+                fn(i)
+            ctx.device_synchronize()
+            ev0.record()
+            for i in range(args.steps):
+                fn(i)
+            ev1.record()
+            ev1.synchronize()
+            return ev0.elapsed_ms(ev1) * 1000.0 / args.steps
+
+        read_us = floor_us(lambda i: ctx.read_floor(case.wbuf.ptr + (i % case.n_copies) * case.stride,
+                                                    nb, fout, words))
+        empty_us = floor_us(lambda i: ctx.launch_empty(fout, words))
+        fout.close()
+        floor = {
+            "read_same_bytes_us": round(read_us, 3),
+            "read_same_bytes_GBps": round(nb / read_us / 1e3, 1),
+            "empty_launch_us": round(empty_us, 3),
+            "kernel_vs_read_floor": round(read_us / us_per_call, 4),
+            "what": "back-to-back launches of the matvec's launch shape (one 512-thread "
+                    "workgroup per CU) that only read the same bytes from the same rotated "
+                    "copies (one store per wave), and that do nothing (the empty launch is "
+                    "bounded by this host path's launch rate)",
+        }
     kernel = case.kernel()
     shape = (("2x" if kind == "gate_up" else "") + f"{case.rows}x{case.cols}"
              + (f"xB{case.batch}" if kind == "matmul" else ""))
@@ -450,6 +486,7 @@ def main() -> int:
             "algorithmic_bytes" if not mfma_bound else "algorithmic_flops": algo,
         },
         "cpu_baseline": cpu,
+        "launch_floor": floor,
     }
     print(json.dumps(out), flush=True)
     case.close()

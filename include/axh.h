@@ -273,6 +273,18 @@ axh_status axh_q6k_dequant(axh_context *ctx, const void *q, float *w, uint64_t n
 /* IEEE binary16 -> binary32 widening of n raw patterns (the ptr_read_u16_zext +
  * f16_bits_to_f32 builtins, crates/axc-codegen/src/q4_0.rs:86-171). */
 axh_status axh_f16_widen(axh_context *ctx, const uint16_t *h, float *f, uint64_t n, void *stream);
+
+/* Measurement helpers (no counterpart in the reference): the floor that one
+ * kernel launch per call puts under a matvec on this device.  Both use the
+ * matvec's launch shape, one 512-thread workgroup per compute unit.
+ * axh_read_floor streams `bytes` (a multiple of 16, below 4 GiB) from q with
+ * 16-byte loads and writes, per wave, the XOR of every dword it read to
+ * out[wave]; axh_launch_empty does nothing.  out holds out_words >= 8 *
+ * axh_cu_count(ctx) words. */
+axh_status axh_read_floor(axh_context *ctx, const void *q, uint64_t bytes, uint32_t *out,
+                          uint32_t out_words, void *stream);
+axh_status axh_launch_empty(axh_context *ctx, uint32_t *out, uint32_t out_words, void *stream);
+uint32_t axh_cu_count(axh_context *ctx);
 /* binary32 -> binary16, round to nearest even, of n values (NaN stays NaN,
  * values beyond the f16 range become infinities): the activation cast that
  * feeds the f16 matmul.  No counterpart in the reference.  x and h 16-byte

@@ -251,3 +251,25 @@ def test_graph_replays_match_eager_results(ctx, axc):
     g.close()
     for b in list(bufs.values()) + [y1, y2, y3, y4]:
         b.close()
+
+
+@pytest.mark.parametrize("nbytes", [16, 1 << 20, (1 << 20) + 48, 33030144])
+def test_read_floor_reads_every_byte(ctx, axc, nbytes):
+    """The bench's launch-floor helper reads exactly the bytes it is given:
+    the XOR of its per-wave results equals the XOR of every dword."""
+    words = 8 * ctx.cu_count()
+    assert words >= 8
+    data = np.random.default_rng(nbytes).integers(0, 2**32, nbytes // 4, dtype=np.uint32)
+    dq, dout = ctx.alloc(nbytes), ctx.alloc(words * 4)
+    ctx.upload(dq, data)
+    ctx.read_floor(dq, nbytes, dout, words)
+    ctx.launch_empty(dout, words)  # writes nothing
+    ctx.synchronize()
+    got = np.frombuffer(ctx.download(dout, words * 4), dtype=np.uint32)
+    assert int(np.bitwise_xor.reduce(got)) == int(np.bitwise_xor.reduce(data))
+    with pytest.raises(axc.DispatchError):
+        ctx.read_floor(dq, 15, dout, words)  # not a multiple of 16
+    with pytest.raises(axc.DispatchError):
+        ctx.read_floor(dq, 16, dout, words - 1)  # out too small
+    for b in (dq, dout):
+        b.close()
