@@ -555,10 +555,11 @@ __device__ __forceinline__ void q4k_flat_stage_chunk(float *xs, float *ss, uint3
 // at every point of the loop.  x is staged chunk by chunk during the first
 // pass over a row (chunk j right before iteration j, requested with the
 // weights of iteration j), so the weight stream starts with the first 8 KiB
-// of x instead of after all of it.  On 4096 x 14336 this is the fastest
-// order measured (8.13 vs 8.5 us per back-to-back call): every variant with
-// more loads in flight was slower on this machine, while a refill that waits
-// for the compute leaves the memory pipe idle during it.
+// of x instead of after all of it.  Every variant with more loads in flight
+// was slower on this machine, while a refill that waits for the compute
+// leaves the memory pipe idle during it (A/B in one run, 14336 x 4096: 9.9
+// vs 10.5 us; Q6_K 4096 x 14336: 12.5 vs 13.4-13.9 us).  The one-pass kernel
+// below is this order unrolled over a compile-time trip count.
 template <int RPW, int NW, int PF, bool kNT, int XP, bool kDual = false, bool kQ5 = false>
 __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
                                                 const uint8_t *__restrict__ q2,
