@@ -98,6 +98,7 @@ constexpr MatvecVariant kQ4_0Variants[] = {
 
 constexpr uint32_t kQ4kMaxTileSb = 128;   // tiled kernel: 128 * 1088 B = 136 KiB of LDS
 constexpr uint32_t kQ4kFlatMaxSb = 128;   // persistent kernel: 128 * 1120 B = 140 KiB of LDS
+constexpr uint32_t kQ4kFlatRounds = 2;    // persistent Q4_K grid: resident workgroups x 2
 constexpr uint32_t kQ4_0MaxTileB = 1024; // 1024 * 132 B = 132 KiB of LDS
 
 } // namespace
@@ -477,7 +478,12 @@ axh_status axh_q4k_matvec(axh_context *ctx, const void *q, const float *x, float
   if (s != AXH_OK) return s;
   uint32_t grid[3] = {p.units, 1, 1};
   if (p.flat) {
-    const uint32_t resident = occupancy(ctx, k, p.lds) * ctx->core->cu_count;
+    // Two rounds of resident workgroups (the bundle loop is grid-stride):
+    // the tall matrices this kernel is the default for end with less tail
+    // (128256 x 4096, prefetch 2, A/B in one run: 51.3-52.7 vs 52.2-54.1 us;
+    // four rounds 51.4, one workgroup per bundle pair group 57.0).  The Q5_K,
+    // Q6_K and gate/up launches stay at one round, where more was slower.
+    const uint32_t resident = kQ4kFlatRounds * occupancy(ctx, k, p.lds) * ctx->core->cu_count;
     if (resident < grid[0]) grid[0] = resident;
   }
   const hipStream_t st = pick_stream(ctx, stream);
