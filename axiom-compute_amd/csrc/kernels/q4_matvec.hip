@@ -713,7 +713,16 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
 // (kQ5) layouts, but there it measured no faster than the persistent kernels
 // (2 x 14336 x 4096: 16.8 vs 16.8 us; Q5_K 14336 x 4096: 11.7 vs 11.3), so
 // only the Q4_K instances are built.
-template <int NIT, bool kDual = false, bool kQ5 = false>
+//
+// kWhole (axh_q4k_matvec_onex_i{NIT}): x is staged whole first, behind one
+// barrier, with the first iteration's weights already requested, and the
+// early-refill loop then runs without barriers, so the waves of a workgroup
+// drift apart and one wave's dot overlaps another's loads.  It pays where
+// several workgroups share a CU and the staging of one overlaps the weight
+// stream of another (A/B in one run, 14336 x 4096: 8.27-8.40 vs 8.78-9.00
+// us), and costs where one workgroup per CU waits for all of x (4096 x 14336:
+// 8.64-8.70 vs 8.12-8.22 us).
+template <int NIT, bool kDual = false, bool kQ5 = false, bool kWhole = false>
 __device__ __forceinline__ void q4k_matvec_one(const uint8_t *__restrict__ q,
                                                const uint8_t *__restrict__ q2,
                                                const float *__restrict__ x, float *__restrict__ y,
@@ -738,6 +747,31 @@ __device__ __forceinline__ void q4k_matvec_one(const uint8_t *__restrict__ q,
   float acc[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
+  if constexpr (kWhole) {
+    q4k_flat_load<RPW, 2, false, kDual, kQ5>(B, 0, qr, qr2, row_bytes, bundle, 0u, s, c);
+#pragma unroll
+    for (int g = 0; g < NIT; g += 4) { // x chunks in groups of 4 (16 VGPRs)
+      float4 xg[4][512 / NT];
+#pragma unroll
+      for (int j = g; j < g + 4 && j < NIT; ++j)
+        q4k_flat_load_chunk<NT>(xr, tid, (uint32_t)j, xg[j - g]);
+#pragma unroll
+      for (int j = g; j < g + 4 && j < NIT; ++j)
+        q4k_flat_stage_chunk<NT>(xs, ss, tid, (uint32_t)j, nsb, xg[j - g]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NIT; ++j) {
+      const int p = j & 1;
+      if (j + 1 < NIT)
+        q4k_flat_load<RPW, 2, false, kDual, kQ5>(B, p ^ 1, qr, qr2, row_bytes, bundle,
+                                                 (uint32_t)(j + 1), s, c);
+      const uint32_t sb = (uint32_t)j * 8u + s;
+      if (mine && sb < nsb) q4k_flat_compute<RPW, 2, kQ5>(B, p, xs, ss, sb, c, acc);
+    }
+    if (mine) q4k_flat_store<RPW, kDual>(acc, 2u * W, lane, n_rows, y);
+    return;
+  }
   q4k_flat_load_chunk<NT>(xr, tid, 0u, xv[0]);
   q4k_flat_load<RPW, 2, false, kDual, kQ5>(B, 0, qr, qr2, row_bytes, bundle, 0u, s, c);
 #pragma unroll
@@ -762,6 +796,12 @@ __device__ __forceinline__ void q4k_matvec_one(const uint8_t *__restrict__ q,
                                 float *__restrict__ y, RowsArgs a) {                             \
     extern __shared__ float axh_lds_dyn[];                                                       \
     q4k_matvec_one<NIT>(q, q, x, y, a.n_rows, a.units_per_row, axh_lds_dyn);                     \
+  }                                                                                              \
+  extern "C" __global__ void __launch_bounds__(512)                                              \
+      axh_q4k_matvec_onex_i##NIT(const uint8_t *__restrict__ q, const float *__restrict__ x,     \
+                                 float *__restrict__ y, RowsArgs a) {                            \
+    extern __shared__ float axh_lds_dyn[];                                                       \
+    q4k_matvec_one<NIT, false, false, true>(q, q, x, y, a.n_rows, a.units_per_row, axh_lds_dyn); \
   }
 AXH_Q4K_MATVEC_ONE(1)
 AXH_Q4K_MATVEC_ONE(2)

@@ -353,6 +353,16 @@ static bool q4k_use_wg(uint32_t n_rows, uint32_t nsb) {
 // vs 18.6); on the 128256-row head (8016 workgroups) the persistent kernel
 // stays ahead (53.5 vs 56.8 us).
 constexpr uint32_t kOneMinRows = 32, kOneMaxRows = 32768, kOneMaxSb = 128;
+// From 6144 rows of at most 32 superblocks (two or more workgroups per CU,
+// and LDS for three or more) the one-pass kernel that stages x whole behind
+// one barrier (axh_q4k_matvec_onex_i{NIT}) is used: A/B in one run, 6144 x
+// 4096 5.31 vs 5.77 us, 8192 x 4096 5.63 vs 6.24, 11008 x 4096 7.10 vs 7.53,
+// 14336 x 4096 8.39-8.47 vs 8.90-8.97, 14336 x 8192 15.7-16.0 vs 16.1-16.4,
+// 32768 x 4096 even.  4096 rows (one workgroup per CU) and longer rows (LDS
+// for one or two) measured slower or even: 4096 x 4096 4.21 vs 4.08, 4096 x
+// 14336 8.84-8.93 vs 8.42-8.55, 8192 x 14336 even, 8192 x 32768 32.5-32.8 vs
+// 31.5-32.2.
+constexpr uint32_t kOneWholeMinRows = 6144, kOneWholeMaxSb = 32;
 
 static bool use_one_pass(uint32_t n_rows, uint32_t nsb) {
   return nsb >= 1 && nsb <= kOneMaxSb && n_rows >= kOneMinRows && n_rows <= kOneMaxRows;
@@ -361,7 +371,8 @@ static bool use_one_pass(uint32_t n_rows, uint32_t nsb) {
 // Fills a one-pass plan for kernel family `prefix` (LDS: lds_per_sb per superblock of x).
 static void plan_one_pass(const char *prefix, uint32_t n_rows, uint32_t nsb, uint32_t lds_per_sb,
                           Q4kPlan *p) {
-  std::snprintf(p->name, sizeof(p->name), "%s_one_i%u", prefix, (nsb + 7u) / 8u);
+  std::snprintf(p->name, sizeof(p->name), "%s_one%s_i%u", prefix,
+                n_rows >= kOneWholeMinRows && nsb <= kOneWholeMaxSb ? "x" : "", (nsb + 7u) / 8u);
   p->nw = 8;
   p->lds = nsb * lds_per_sb;
   p->flat = false; // one workgroup per 16 rows, all of them launched

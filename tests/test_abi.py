@@ -101,6 +101,7 @@ def test_builtin_code_object_holds_every_variant_kernel(axc):
         assert name.encode() in co, name
     for nit in range(1, 17):  # one-pass kernels for rows of 1..128 superblocks
         assert f"axh_q4k_matvec_one_i{nit}".encode() in co
+        assert f"axh_q4k_matvec_onex_i{nit}".encode() in co
     for name in ("q4km_dequant_matvec", "q4_0_dequant_matvec", "axh_q4k_dequant",
                  "axh_q4_0_dequant", "axh_f16_widen", "axh_q4k_matvec_tiled_r2_w8_p2",
                  "axh_q4k_matvec_tiled_r1_w4_p2"):
@@ -118,7 +119,14 @@ def test_kernel_selection_by_shape_and_variant(axc):
     assert name(4097, 56) == "axh_q4k_matvec_one_i7"
     assert name(4096, 32) == "axh_q4k_matvec_one_i4"
     assert name(4096, 16) == "axh_q4k_matvec_one_i2"
-    assert name(32768, 1) == "axh_q4k_matvec_one_i1"
+    assert name(6143, 16) == "axh_q4k_matvec_one_i2"
+    # from 6144 rows of at most 32 superblocks: x staged whole behind one barrier
+    assert name(32768, 1) == "axh_q4k_matvec_onex_i1"
+    assert name(6144, 16) == "axh_q4k_matvec_onex_i2"
+    assert name(14336, 16) == "axh_q4k_matvec_onex_i2"
+    assert name(14336, 32) == "axh_q4k_matvec_onex_i4"
+    assert name(14336, 33) == "axh_q4k_matvec_one_i5"
+    assert name(8192, 56) == "axh_q4k_matvec_one_i7"
     # taller matrices: the persistent kernels
     assert name(32769, 16) == "axh_q4k_matvec_flat_r2_w4_p1_n0"
     assert name(128256, 16) == "axh_q4k_matvec_flat_r2_w4_p2_n0"  # the head keeps prefetch 2

@@ -285,12 +285,27 @@ def test_q4k_one_pass_shapes(ctx, axc, rows, sb):
     """32..32768 rows of 1..128 superblocks: trip counts 1..16 and their
     boundaries (8k and 8k + 1 superblocks), odd row counts (a half-empty last
     pair) and workgroups past the last pair."""
-    assert axc.q4k_matvec_kernel_name(rows, sb).startswith("axh_q4k_matvec_one_i")
+    assert axc.q4k_matvec_kernel_name(rows, sb).startswith("axh_q4k_matvec_one")
     _say(f"q4k one pass {rows}x{sb}")
     q = O.gen_q4k_weights(rows * 23 + sb, rows * sb)
     x = O.gen_normal_f32(rows + 7 * sb, sb * 256)
     y = _run_q4k(ctx, q, x, rows, sb)
     _check_q4k(y, q, x, rows, sb, f"q4k one pass {rows}x{sb}")
+
+
+@pytest.mark.parametrize("rows,sb", [(6144, 1), (6145, 8), (6151, 9), (8192, 17), (11008, 16),
+                                     (14336, 16), (9999, 24), (6200, 25), (7001, 32),
+                                     (32768, 2)])
+def test_q4k_one_pass_whole_x_shapes(ctx, axc, rows, sb):
+    """The one-pass kernel that stages x whole (6144+ rows of at most 32
+    superblocks): trip counts 1..4 and their boundaries, odd row counts and
+    partial last workgroups."""
+    assert axc.q4k_matvec_kernel_name(rows, sb) == f"axh_q4k_matvec_onex_i{(sb + 7) // 8}"
+    _say(f"q4k one pass whole x {rows}x{sb}")
+    q = O.gen_q4k_weights(rows * 29 + sb, rows * sb)
+    x = O.gen_normal_f32(rows + 11 * sb, sb * 256)
+    y = _run_q4k(ctx, q, x, rows, sb)
+    _check_q4k(y, q, x, rows, sb, f"q4k one pass whole x {rows}x{sb}")
 
 
 @pytest.mark.parametrize("sb", [9, 40])
