@@ -307,8 +307,9 @@ def main() -> int:
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU only: this build runs the matvec on one MI355X; "
-              "see DESIGN.md for how the path shards across GPUs.", file=sys.stderr)
+        print("bench.py measures one GPU only: this build runs the matvec on one MI355X "
+              "(across GPUs the rows would be split into contiguous blocks, one per GPU, with "
+              "x replicated and no collective until the consumer of y).", file=sys.stderr)
         return 2
 
     import numpy as np
