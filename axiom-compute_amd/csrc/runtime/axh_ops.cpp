@@ -364,8 +364,16 @@ constexpr uint32_t kOneMinRows = 32, kOneMaxRows = 32768, kOneMaxSb = 128;
 // 31.5-32.2.
 constexpr uint32_t kOneWholeMinRows = 6144, kOneWholeMaxSb = 32;
 
+// The whole-x kernel also takes 32769-65535 rows of at most 16 superblocks
+// (A/B in one run against the persistent kernel: 40000 x 4096 18.5-18.8 vs
+// 20.5-21.7 us, 65536 x 4096 29.1 vs 29.8-30.1), but not longer rows (50000 x
+// 8192: 46.3-46.6 vs 43.4-44.1); the 128256-row head stays persistent
+// (51.6-51.8 vs 53.5-54.3 us).
+constexpr uint32_t kOneTallMaxRows = 65535, kOneTallMaxSb = 16;
+
 static bool use_one_pass(uint32_t n_rows, uint32_t nsb) {
-  return nsb >= 1 && nsb <= kOneMaxSb && n_rows >= kOneMinRows && n_rows <= kOneMaxRows;
+  if (nsb < 1 || nsb > kOneMaxSb || n_rows < kOneMinRows) return false;
+  return n_rows <= kOneMaxRows || (nsb <= kOneTallMaxSb && n_rows <= kOneTallMaxRows);
 }
 
 // Fills a one-pass plan for kernel family `prefix` (LDS: lds_per_sb per superblock of x).

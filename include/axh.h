@@ -167,9 +167,10 @@ void axh_event_destroy(axh_event *ev);
  * loads before the current one is computed and stages x chunk by chunk; P >= 2
  * keeps P iterations loaded and refills a slot after computing it) and
  * nontemporal (weight-load cache policy).  Zero fields pick the defaults for
- * the shape; with no variant, 32-32768 rows of 1-128 superblocks take a
- * one-pass kernel (one workgroup per 16 rows; from 6144 rows of at most 32
- * superblocks x is staged whole first), which is not a hole assignment. */
+ * the shape; with no variant, 32-32768 rows of 1-128 superblocks (and up to
+ * 65535 rows of at most 16) take a one-pass kernel (one workgroup per 16
+ * rows; from 6144 rows of at most 32 superblocks x is staged whole first),
+ * which is not a hole assignment. */
 typedef struct axh_q4_variant {
     uint32_t rows_per_wave;
     uint32_t waves_per_workgroup;
