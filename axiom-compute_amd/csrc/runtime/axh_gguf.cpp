@@ -241,7 +241,12 @@ static axh_status parse(axh_gguf *g) {
       if (t.ne[0] % ts.elems != 0)
         return fail(AXH_ERR_METADATA_PARSE,
                     "GGUF tensor " + t.name + ": row length is not a whole number of blocks");
-      t.nbytes = n_elems / ts.elems * ts.bytes;
+      // Element counts reach 2^62, so blocks * block bytes can wrap in 64
+      // bits: such a tensor cannot lie inside any file.
+      if (__builtin_mul_overflow(n_elems / ts.elems, (uint64_t)ts.bytes, &t.nbytes) ||
+          t.nbytes > g->size)
+        return fail(AXH_ERR_METADATA_PARSE,
+                    "GGUF tensor " + t.name + ": byte size exceeds the file");
     }
     if (t.rel_off % g->alignment != 0)
       return fail(AXH_ERR_METADATA_PARSE, "GGUF tensor " + t.name + ": misaligned offset");

@@ -40,6 +40,8 @@ struct Core {
   std::mutex staging_mu;
   void *staging = nullptr; // pinned host memory
   size_t staging_bytes = 0;
+  // Staging buffers whose copy outlived a fence timeout (freed at teardown).
+  std::vector<void *> retired_staging;
 
   std::mutex cache_mu; // guards modules and kernels
   std::unordered_map<uint64_t, LoadedModule> modules;
@@ -74,6 +76,9 @@ struct axh_context {
   // Per-stream device workspaces of the kernels that reduce across
   // workgroups (split-K matvec): calls on one stream never overlap.
   std::unordered_map<void *, void *> workspaces;
+  // Set when a capture on the context stream records a launch that uses the
+  // context stream's workspace (the graph then replays on that stream only).
+  std::atomic<bool> capture_uses_workspace{false};
 };
 
 namespace axh {

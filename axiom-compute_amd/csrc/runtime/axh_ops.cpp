@@ -364,12 +364,12 @@ constexpr uint32_t kOneMinRows = 32, kOneMaxRows = 32768, kOneMaxSb = 128;
 // 31.5-32.2.
 constexpr uint32_t kOneWholeMinRows = 6144, kOneWholeMaxSb = 32;
 
-// The whole-x kernel also takes 32769-65535 rows of at most 16 superblocks
+// The whole-x kernel also takes 32769-65536 rows of at most 16 superblocks
 // (A/B in one run against the persistent kernel: 40000 x 4096 18.5-18.8 vs
 // 20.5-21.7 us, 65536 x 4096 29.1 vs 29.8-30.1), but not longer rows (50000 x
 // 8192: 46.3-46.6 vs 43.4-44.1); the 128256-row head stays persistent
 // (51.6-51.8 vs 53.5-54.3 us).
-constexpr uint32_t kOneTallMaxRows = 65535, kOneTallMaxSb = 16;
+constexpr uint32_t kOneTallMaxRows = 65536, kOneTallMaxSb = 16;
 
 static bool use_one_pass(uint32_t n_rows, uint32_t nsb) {
   if (nsb < 1 || nsb > kOneMaxSb || n_rows < kOneMinRows) return false;
@@ -510,6 +510,10 @@ axh_status axh_q4k_matvec(axh_context *ctx, const void *q, const float *x, float
     void *ws = nullptr;
     s = stream_workspace(ctx, st, &ws);
     if (s != AXH_OK) return s;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (st == ctx->core->stream && hipStreamIsCapturing(st, &cs) == hipSuccess &&
+        cs == hipStreamCaptureStatusActive)
+      ctx->capture_uses_workspace = true;
     void *bufs4[4] = {const_cast<void *>(q), const_cast<float *>(x), y, ws};
     s = launch_raw(k, grid, bufs4, 4, &p.args, sizeof(p.args), 0, st);
     return s == AXH_OK ? ok() : s;
@@ -963,7 +967,8 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
   // kind 4 stages 16 activation columns of the whole K in LDS; kind 5 sums the
   // partial tiles of its waves there (one 16x16 f32 tile = 1 KiB per wave)
   // kind 7: 128 KiB of X staging, then two buffers of the waves' partial tiles
-  const uint32_t lds = v.kind == 4 ? 16u * (sb_per_row * 256u + 8u) * 2u
+  // (64-bit: kind 4's size grows with K and would wrap in 32 bits)
+  const uint64_t lds = v.kind == 4 ? 16ull * ((uint64_t)sb_per_row * 256u + 8u) * 2u
                        : v.kind == 5 ? kx_lds_bytes(v)
                        : v.kind == 6 ? rs_lds_bytes(v)
                        : v.kind == 7 ? 131072u + 2u * v.w * v.nt * 1024u
@@ -986,13 +991,13 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
   s = builtin_kernel(ctx, name, 3, sizeof(MatmulArgs), v.w * 64u, &k);
   if (s != AXH_OK) return s;
   if (v.kind == 4 || v.kind == 7) { // persistent: one resident wave of workgroups per column group
-    const uint64_t resident = (uint64_t)occupancy(ctx, k, lds) * ctx->core->cu_count;
+    const uint64_t resident = (uint64_t)occupancy(ctx, k, (uint32_t)lds) * ctx->core->cu_count;
     if (resident < gx) gx = resident;
   }
   const uint32_t grid[3] = {(uint32_t)gx, (uint32_t)gy, 1};
   void *bufs[3] = {const_cast<void *>(q), const_cast<uint16_t *>(x), y};
   MatmulArgs a{n_rows, sb_per_row, batch, 0};
-  s = launch_raw(k, grid, bufs, 3, &a, sizeof(a), lds, pick_stream(ctx, stream));
+  s = launch_raw(k, grid, bufs, 3, &a, sizeof(a), (uint32_t)lds, pick_stream(ctx, stream));
   return s == AXH_OK ? ok() : s;
 }
 

@@ -48,7 +48,9 @@ Core::~Core() {
   if (device >= 0) hipSetDevice(device);
   for (auto &kv : modules)
     if (kv.second.module) hipModuleUnload(kv.second.module);
+  if (stream) hipStreamSynchronize(stream); // retired staging buffers may still be in use
   if (staging) hipHostFree(staging);
+  for (void *p : retired_staging) hipHostFree(p);
   if (stream) hipStreamDestroy(stream);
 }
 
@@ -112,6 +114,20 @@ static axh_status ensure_staging(Core &core, size_t bytes) {
 
 static constexpr size_t kStagingChunk = size_t(32) << 20;
 
+// A wait that timed out leaves its copy queued on the stream, still reading
+// or writing the staging buffer.  The buffer is retired (freed when the core
+// goes away) so the next staged copy fills a fresh one instead of handing
+// the queued transfer the wrong bytes.
+static axh_status staging_wait(Core &core) {
+  const axh_status s = wait_stream(core, core.stream);
+  if (s == AXH_ERR_FENCE_TIMEOUT && core.staging) {
+    core.retired_staging.push_back(core.staging);
+    core.staging = nullptr;
+    core.staging_bytes = 0;
+  }
+  return s;
+}
+
 // Host -> device through the pinned staging buffer, in chunks.
 static axh_status staged_upload(Core &core, void *dst, const void *src, size_t bytes,
                                 uint32_t binding) {
@@ -126,7 +142,7 @@ static axh_status staged_upload(Core &core, void *dst, const void *src, size_t b
     if (e != hipSuccess)
       return fail(AXH_ERR_STAGING_COPY, "binding #" + std::to_string(binding) +
                                             " (HostToDevice): " + hip_msg("hipMemcpyAsync", e));
-    s = wait_stream(core, core.stream);
+    s = staging_wait(core);
     if (s != AXH_OK) return s;
   }
   return AXH_OK;
@@ -144,7 +160,7 @@ static axh_status staged_download(Core &core, void *dst, const void *src, size_t
     if (e != hipSuccess)
       return fail(AXH_ERR_READBACK, "readback of binding #" + std::to_string(binding) +
                                         " failed: " + hip_msg("hipMemcpyAsync", e));
-    s = wait_stream(core, core.stream);
+    s = staging_wait(core);
     if (s != AXH_OK) return s;
     std::memcpy(static_cast<uint8_t *>(dst) + off, core.staging, n);
   }
@@ -668,11 +684,16 @@ struct axh_graph {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   uint64_t n_nodes = 0;
+  // Holds a split-K launch bound to the context stream's workspace: replays
+  // on another stream could overlap calls that share that workspace.
+  bool uses_workspace = false;
+  hipStream_t home = nullptr;
 };
 
 axh_status axh_capture_begin(axh_context *ctx) {
   if (!ctx) return fail(AXH_ERR_INVALID_ARGUMENT, "ctx is NULL");
   hipSetDevice(ctx->core->device);
+  ctx->capture_uses_workspace = false;
   hipError_t e = hipStreamBeginCapture(ctx->core->stream, hipStreamCaptureModeThreadLocal);
   if (e != hipSuccess) return fail(AXH_ERR_COMMAND_RECORD, hip_msg("hipStreamBeginCapture", e));
   return ok();
@@ -698,14 +719,21 @@ axh_status axh_capture_end(axh_context *ctx, axh_graph **out) {
   G->graph = g;
   G->exec = exec;
   G->n_nodes = n;
+  G->uses_workspace = ctx->capture_uses_workspace.exchange(false);
+  G->home = ctx->core->stream;
   *out = G;
   return ok();
 }
 
 axh_status axh_graph_launch(axh_context *ctx, axh_graph *g, void *stream) {
   if (!ctx || !g) return fail(AXH_ERR_INVALID_ARGUMENT, "NULL argument");
+  const hipStream_t st = pick_stream(ctx, stream);
+  if (g->uses_workspace && st != g->home)
+    return fail(AXH_ERR_INVALID_ARGUMENT,
+                "this graph holds a split-K matvec bound to the context stream's workspace; "
+                "replay it on the context stream (NULL)");
   hipSetDevice(ctx->core->device);
-  hipError_t e = hipGraphLaunch(g->exec, pick_stream(ctx, stream));
+  hipError_t e = hipGraphLaunch(g->exec, st);
   if (e != hipSuccess) return fail(AXH_ERR_QUEUE_SUBMIT, hip_msg("hipGraphLaunch", e));
   return ok();
 }

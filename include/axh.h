@@ -168,7 +168,7 @@ void axh_event_destroy(axh_event *ev);
  * keeps P iterations loaded and refills a slot after computing it) and
  * nontemporal (weight-load cache policy).  Zero fields pick the defaults for
  * the shape; with no variant, 32-32768 rows of 1-128 superblocks (and up to
- * 65535 rows of at most 16) take a one-pass kernel (one workgroup per 16
+ * 65536 rows of at most 16) take a one-pass kernel (one workgroup per 16
  * rows; from 6144 rows of at most 32 superblocks x is staged whole first),
  * which is not a hole assignment. */
 typedef struct axh_q4_variant {
@@ -300,7 +300,10 @@ axh_status axh_f32_to_f16(axh_context *ctx, const float *x, uint16_t *h, uint64_
  * kernel: the HIP counterpart of recording a Vulkan command buffer once and
  * resubmitting it.  Launch each operation once before capturing it (its
  * kernel is then prepared and cached).  No event, copy or synchronisation
- * call may be made on the context stream while capturing. */
+ * call may be made on the context stream while capturing.  A graph that holds
+ * a split-K matvec (fewer than 32 rows of 64-256 superblocks) uses the
+ * context stream's workspace and replays only on the context stream: another
+ * stream gets AXH_ERR_INVALID_ARGUMENT. */
 typedef struct axh_graph axh_graph;
 axh_status axh_capture_begin(axh_context *ctx);
 axh_status axh_capture_end(axh_context *ctx, axh_graph **out);

@@ -128,11 +128,11 @@ def test_kernel_selection_by_shape_and_variant(axc):
     assert name(14336, 33) == "axh_q4k_matvec_one_i5"
     assert name(8192, 56) == "axh_q4k_matvec_one_i7"
     # taller matrices: the persistent kernels
-    assert name(32769, 16) == "axh_q4k_matvec_onex_i2"  # whole-x one pass up to 65535 rows
-    assert name(65535, 16) == "axh_q4k_matvec_onex_i2"
+    assert name(32769, 16) == "axh_q4k_matvec_onex_i2"  # whole-x one pass up to 65536 rows
+    assert name(65536, 16) == "axh_q4k_matvec_onex_i2"
     assert name(40000, 17).startswith("axh_q4k_matvec_flat_")
     assert name(40000, 33).startswith("axh_q4k_matvec_flat_")
-    assert name(65536, 16).startswith("axh_q4k_matvec_flat_")
+    assert name(65537, 16).startswith("axh_q4k_matvec_flat_")
     assert name(128256, 16) == "axh_q4k_matvec_flat_r2_w4_p2_n0"  # the head keeps prefetch 2
     assert name(65536, 56) == "axh_q4k_matvec_flat_r1_w8_p2_n0"
     assert name(65536, 128) == "axh_q4k_matvec_flat_r1_w16_p2_n0"

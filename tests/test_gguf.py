@@ -118,7 +118,7 @@ def _file(head: bytes, data: bytes = b"", align: int = 32) -> bytes:
 @pytest.mark.parametrize("case", [
     "magic", "v1", "v4", "dims0", "dims5", "misaligned", "partial_block", "dup_tensor",
     "dup_key", "align_not_pow2", "align_wrong_type", "huge_string", "huge_counts",
-    "bad_value_type", "past_end", "zero_dim",
+    "bad_value_type", "past_end", "zero_dim", "f32_size_wraps", "f64_size_wraps",
 ])
 def test_malformed_files_are_typed_errors(gg, axc, tmp_path, case):
     q = b"\1" * 144
@@ -140,6 +140,9 @@ def test_malformed_files_are_typed_errors(gg, axc, tmp_path, case):
         "bad_value_type": _header(0, 1) + _s("k") + struct.pack("<II", 13, 0),
         "past_end": _header(1, 0) + _tensor("w", (512,), 12, 0),
         "zero_dim": _header(1, 0) + _tensor("w", (256, 0), 12, 0),
+        # element count * element bytes wraps in 64 bits (to 0 and to 8 bytes)
+        "f32_size_wraps": _header(1, 0) + _tensor("w", (2 ** 62,), 0, 0),
+        "f64_size_wraps": _header(1, 0) + _tensor("w", (2 ** 61 + 1,), 28, 0),
     }
     p = tmp_path / f"{case}.gguf"
     p.write_bytes(_file(blobs[case], q))

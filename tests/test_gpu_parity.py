@@ -295,10 +295,10 @@ def test_q4k_one_pass_shapes(ctx, axc, rows, sb):
 
 @pytest.mark.parametrize("rows,sb", [(6144, 1), (6145, 8), (6151, 9), (8192, 17), (11008, 16),
                                      (14336, 16), (9999, 24), (6200, 25), (7001, 32),
-                                     (32768, 2), (40001, 16), (65535, 3)])
+                                     (32768, 2), (40001, 16), (65535, 3), (65536, 5)])
 def test_q4k_one_pass_whole_x_shapes(ctx, axc, rows, sb):
     """The one-pass kernel that stages x whole (6144-32768 rows of at most 32
-    superblocks, up to 65535 rows of at most 16): trip counts 1..4 and their
+    superblocks, up to 65536 rows of at most 16): trip counts 1..4 and their
     boundaries, odd row counts and partial last workgroups."""
     assert axc.q4k_matvec_kernel_name(rows, sb) == f"axh_q4k_matvec_onex_i{(sb + 7) // 8}"
     _say(f"q4k one pass whole x {rows}x{sb}")

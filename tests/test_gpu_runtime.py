@@ -248,9 +248,53 @@ def test_graph_replays_match_eager_results(ctx, axc):
         ctx.synchronize()
         got = [ctx.download(b, n) for b, n in outs]
         assert got == eager, f"replay {rep}"
+    # The split-K launch is bound to the context stream's workspace: a replay
+    # on another stream is refused before any work is queued.  A graph
+    # without it replays anywhere.
+    other = axc.HipContext.new()
+    with pytest.raises(axc.DispatchError) as e:
+        g.launch(stream=other.stream)
+    assert e.value.variant == "InvalidArgument"
     g.close()
-    for b in list(bufs.values()) + [y1, y2, y3, y4]:
+    g2 = ctx.capture(lambda: ctx.q4k_matvec(bufs["q"], bufs["x"], y1, rows, sb))
+    ctx.upload(y1, np.full(rows, np.nan, dtype=np.float32))
+    g2.launch(stream=other.stream)
+    other.synchronize(other.stream)
+    assert ctx.download(y1, rows * 4) == eager[0]
+    g2.close()
+    other.close()
+    for b in list(bufs.values()) + [y1, y2, y3, y4, y5]:
         b.close()
+
+
+def test_staged_upload_after_a_timed_out_upload(axc, ctx):
+    """An upload whose copy waits behind a ~10 ms kernel times out (1 ms
+    fence); a second upload to another buffer follows at once.  Once the
+    device drains, each buffer holds its own bytes: the queued first copy
+    still reads the staging memory it was given."""
+    c = axc.HipContext.new_with_options(axc.HipContextOptions(fence_timeout_ms=1))
+    h = c.prepare_kernel(axc.builtin_code_object(),
+                         axc.BindingPlan([axc.axh.ACCESS_READ_WRITE], 4, (64, 1, 1)), 4, "axh_spin")
+    flag = c.alloc(4)
+    n = 4096
+    a, b = c.alloc(n), c.alloc(n)
+    da = np.full(n, 0xA5, dtype=np.uint8)
+    db = np.full(n, 0x3C, dtype=np.uint8)
+    c.launch(h, (1, 1, 1), [flag], struct.pack("<I", 3000))  # bounded: ends by itself
+    with pytest.raises(axc.DispatchError) as e:
+        c.upload(a, da)
+    assert e.value.variant == "FenceTimeout"
+    try:
+        c.upload(b, db)
+    except axc.DispatchError as e2:  # may also wait behind the kernel
+        assert e2.variant == "FenceTimeout"
+    c.device_synchronize()  # unbounded wait
+    assert ctx.download(a, n) == da.tobytes()
+    assert ctx.download(b, n) == db.tobytes()
+    for buf in (flag, a, b):
+        buf.close()
+    h.release()
+    c.close()
 
 
 @pytest.mark.parametrize("nbytes", [16, 1 << 20, (1 << 20) + 48, 33030144])
