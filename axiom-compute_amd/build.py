@@ -30,6 +30,10 @@ HIP_FLAGS = [
     "-std=c++17",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
+# Kernel code objects: every kernel argument (pointers and 32-bit shape
+# words) is preloaded into SGPRs at wave launch, so no wave waits for a
+# kernarg load before its first memory request.
+KERNEL_FLAGS = ["-mllvm", "-amdgpu-kernarg-preload-count=16"]
 
 KERNELS = ["q4_matvec", "q4_matmul"]
 
@@ -49,7 +53,7 @@ def build_kernels() -> dict[str, Path]:
     for name in KERNELS:
         src = PKG / "csrc" / "kernels" / f"{name}.hip"
         out = BUILD / f"{name}.co"
-        _run([HIPCC, *HIP_FLAGS, "--offload-device-only", "--no-gpu-bundle-output",
+        _run([HIPCC, *HIP_FLAGS, *KERNEL_FLAGS, "--offload-device-only", "--no-gpu-bundle-output",
               "-I", str(PKG / "csrc" / "kernels"), "-o", str(out), str(src)])
         cos[name] = out
     return cos
@@ -58,6 +62,7 @@ def build_kernels() -> dict[str, Path]:
 def build_runtime(cos: dict[str, Path]) -> Path:
     rt = PKG / "csrc" / "runtime"
     embed_o = BUILD / "axh_embed.o"
+
     _run(["gcc", "-c", f'-DAXH_Q4_MATVEC_CO="{cos["q4_matvec"]}"',
           f'-DAXH_Q4_MATMUL_CO="{cos["q4_matmul"]}"', "-o", str(embed_o),
           str(rt / "axh_embed.S")])

@@ -56,6 +56,10 @@ struct MatmulArgs {
   uint32_t batch;
   uint32_t pad;
 };
+// The shape as separate 32-bit kernel arguments (the struct's kernarg
+// layout), so that all arguments are preloaded into SGPRs at wave launch.
+#define AXH_MATMUL_ARGS uint32_t a_n_rows, uint32_t a_sb_per_row, uint32_t a_batch, uint32_t a_pad
+#define AXH_MATMUL_UNPACK const MatmulArgs a{a_n_rows, a_sb_per_row, a_batch, a_pad}
 
 namespace {
 
@@ -1192,7 +1196,7 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
 #define AXH_Q4K_MATMUL(W, NT)                                                              \
   extern "C" __global__ void __launch_bounds__(W * 64)                                           \
       axh_q4k_matmul_w##W##_n##NT(const uint8_t *__restrict__ q, const uint16_t *__restrict__ x, \
-                                  float *__restrict__ y, MatmulArgs a) {                         \
+                                  float *__restrict__ y, AXH_MATMUL_ARGS) { AXH_MATMUL_UNPACK; \
     q4k_matmul<W, NT>(q, x, y, a);                                                               \
   }
 
@@ -1205,7 +1209,7 @@ AXH_Q4K_MATMUL(4, 8)
   extern "C" __global__ void __launch_bounds__(W * 64)                                           \
       axh_q4k_matmul_rf_w##W##_n##NT##_p##PF##_x##XL(const uint8_t *__restrict__ q,             \
                                                       const uint16_t *__restrict__ x,            \
-                                                      float *__restrict__ y, MatmulArgs a) {     \
+                                                      float *__restrict__ y, AXH_MATMUL_ARGS) { AXH_MATMUL_UNPACK; \
     q4k_matmul_rf<W, NT, PF, XL != 0>(q, x, y, a);                                               \
   }
 
@@ -1216,7 +1220,7 @@ AXH_Q4K_MATMUL_RF(4, 8, 1, 1)
   extern "C" __global__ void __launch_bounds__(KS * 64)                                          \
       axh_q4k_matmul_ks_k##KS##_n##NT##_p##PF(const uint8_t *__restrict__ q,                     \
                                               const uint16_t *__restrict__ x,                    \
-                                              float *__restrict__ y, MatmulArgs a) {             \
+                                              float *__restrict__ y, AXH_MATMUL_ARGS) { AXH_MATMUL_UNPACK; \
     q4k_matmul_ks<KS, NT, PF>(q, x, y, a);                                                       \
   }
 
@@ -1229,7 +1233,7 @@ AXH_Q4K_MATMUL_KS(8, 2, 1)
   extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
       axh_q4k_matmul_st_w##NW##_k##KS##_p##PF(const uint8_t *__restrict__ q,                     \
                                               const uint16_t *__restrict__ x,                    \
-                                              float *__restrict__ y, MatmulArgs a) {             \
+                                              float *__restrict__ y, AXH_MATMUL_ARGS) { AXH_MATMUL_UNPACK; \
     extern __shared__ _Float16 axh_xs_dyn[];                                                     \
     q4k_matmul_st<NW, KS, PF>(q, x, y, a, axh_xs_dyn);                                           \
   }
@@ -1244,7 +1248,7 @@ AXH_Q4K_MATMUL_ST(16, 4, 4)
   extern "C" __global__ void __launch_bounds__(KS * 64)                                          \
       axh_q4k_matmul_kx_r##RT##_n##NT##_k##KS##_p##PF(const uint8_t *__restrict__ q,             \
                                                       const uint16_t *__restrict__ x,            \
-                                                      float *__restrict__ y, MatmulArgs a) {     \
+                                                      float *__restrict__ y, AXH_MATMUL_ARGS) { AXH_MATMUL_UNPACK; \
     extern __shared__ f32x4_t axh_red_dyn[];                                                     \
     q4k_matmul_kx<RT, NT, KS, PF>(q, x, y, a, axh_red_dyn);                                      \
   }
@@ -1262,7 +1266,7 @@ AXH_Q4K_MATMUL_KX(4, 1, 4, 3)
   extern "C" __global__ void __launch_bounds__(W * 64)                                           \
       axh_q4k_matmul_rs_w##W##_r##RT##_n##NT##_p##PF(const uint8_t *__restrict__ q,              \
                                                      const uint16_t *__restrict__ x,             \
-                                                     float *__restrict__ y, MatmulArgs a) {      \
+                                                     float *__restrict__ y, AXH_MATMUL_ARGS) { AXH_MATMUL_UNPACK; \
     extern __shared__ f32x4_t axh_rs_dyn[];                                                      \
     q4k_matmul_rs<W, RT, NT, PF>(q, x, y, a, axh_rs_dyn);                                        \
   }
@@ -1277,7 +1281,7 @@ AXH_Q4K_MATMUL_RS(8, 1, 8, 4)
   extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
       axh_q4k_matmul_sr_w##NW##_s##SPW##SUFFIX(const uint8_t *__restrict__ q,                    \
                                                const uint16_t *__restrict__ x,                   \
-                                               float *__restrict__ y, MatmulArgs a) {            \
+                                               float *__restrict__ y, AXH_MATMUL_ARGS) { AXH_MATMUL_UNPACK; \
     extern __shared__ f32x4_t axh_sr_dyn[];                                                      \
     q4k_matmul_sr<NW, SPW, NC>(q, x, y, a, axh_sr_dyn);                                          \
   }

@@ -25,6 +25,16 @@ struct CountArgs {
   uint32_t n_units; // n_superblocks (Q4_K) or n_blocks (Q4_0)
 };
 
+// Kernels take the shape as separate 32-bit arguments (the same kernarg
+// layout as the structs above) so that every argument is preloaded into
+// SGPRs at wave launch (-amdgpu-kernarg-preload-count): no wave waits for a
+// kernarg load before its first memory request (north star 8.44 -> 8.07 us
+// per call, A/B in one run).
+#define AXH_ROWS_ARGS uint32_t a_n_rows, uint32_t a_units_per_row, uint32_t a_tile_units, uint32_t a_pad
+#define AXH_ROWS_UNPACK const RowsArgs a{a_n_rows, a_units_per_row, a_tile_units, a_pad}
+#define AXH_COUNT_ARGS uint32_t a_n_units
+#define AXH_COUNT_UNPACK const CountArgs a{a_n_units}
+
 // ===========================================================================
 // Q4_K_M matvec
 // ===========================================================================
@@ -287,7 +297,7 @@ __device__ __forceinline__ void q4k_matvec_body(const uint8_t *__restrict__ q,
   extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
       axh_q4k_matvec_tiled_r##RPW##_w##NW##_p##PF(const uint8_t *__restrict__ q,                 \
                                                   const float *__restrict__ x,                   \
-                                                  float *__restrict__ y, RowsArgs a) {           \
+                                                  float *__restrict__ y, AXH_ROWS_ARGS) { AXH_ROWS_UNPACK; \
     extern __shared__ float axh_lds_dyn[];                                                       \
     if (a.units_per_row <= a.tile_units)                                                         \
       q4k_matvec_body<RPW, NW, PF, false, false>(q, x, y, a.n_rows, a.units_per_row,             \
@@ -793,13 +803,13 @@ __device__ __forceinline__ void q4k_matvec_one(const uint8_t *__restrict__ q,
 #define AXH_Q4K_MATVEC_ONE(NIT)                                                                  \
   extern "C" __global__ void __launch_bounds__(512)                                              \
       axh_q4k_matvec_one_i##NIT(const uint8_t *__restrict__ q, const float *__restrict__ x,      \
-                                float *__restrict__ y, RowsArgs a) {                             \
+                                float *__restrict__ y, AXH_ROWS_ARGS) { AXH_ROWS_UNPACK; \
     extern __shared__ float axh_lds_dyn[];                                                       \
     q4k_matvec_one<NIT>(q, q, x, y, a.n_rows, a.units_per_row, axh_lds_dyn);                     \
   }                                                                                              \
   extern "C" __global__ void __launch_bounds__(512)                                              \
       axh_q4k_matvec_onex_i##NIT(const uint8_t *__restrict__ q, const float *__restrict__ x,     \
-                                 float *__restrict__ y, RowsArgs a) {                            \
+                                 float *__restrict__ y, AXH_ROWS_ARGS) { AXH_ROWS_UNPACK; \
     extern __shared__ float axh_lds_dyn[];                                                       \
     q4k_matvec_one<NIT, false, false, true>(q, q, x, y, a.n_rows, a.units_per_row, axh_lds_dyn); \
   }
@@ -824,7 +834,7 @@ AXH_Q4K_MATVEC_ONE(16)
   extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
       axh_q4k_matvec_flat_r##RPW##_w##NW##_p##PF##_n##NT(const uint8_t *__restrict__ q,          \
                                                          const float *__restrict__ x,            \
-                                                         float *__restrict__ y, RowsArgs a) {    \
+                                                         float *__restrict__ y, AXH_ROWS_ARGS) { AXH_ROWS_UNPACK; \
     extern __shared__ float axh_lds_dyn[];                                                       \
     q4k_matvec_flat<RPW, NW, PF, NT != 0, 1>(q, q, x, y, a.n_rows, a.units_per_row,             \
                                                axh_lds_dyn);                                     \
@@ -835,7 +845,7 @@ AXH_Q4K_MATVEC_ONE(16)
       axh_q4k_matvec_flat_r##RPW##_w##NW##_p##PF##_n##NT##_x2(const uint8_t *__restrict__ q,     \
                                                               const float *__restrict__ x,       \
                                                               float *__restrict__ y,             \
-                                                              RowsArgs a) {                      \
+                                                              AXH_ROWS_ARGS) { AXH_ROWS_UNPACK; \
     extern __shared__ float axh_lds_dyn[];                                                       \
     q4k_matvec_flat<RPW, NW, PF, NT != 0, 2>(q, q, x, y, a.n_rows, a.units_per_row,             \
                                                axh_lds_dyn);                                     \
@@ -1071,7 +1081,7 @@ __device__ __forceinline__ void q6k_matvec_flat(const uint8_t *__restrict__ q,
   extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
       axh_q6k_matvec_flat_r##RPW##_w##NW##_p##PF##_x##XP(const uint8_t *__restrict__ q,          \
                                                          const float *__restrict__ x,            \
-                                                         float *__restrict__ y, RowsArgs a) {    \
+                                                         float *__restrict__ y, AXH_ROWS_ARGS) { AXH_ROWS_UNPACK; \
     extern __shared__ float axh_lds_dyn[];                                                       \
     q6k_matvec_flat<RPW, NW, PF, XP>(q, x, y, a.n_rows, a.units_per_row, axh_lds_dyn);          \
   }
@@ -1080,7 +1090,7 @@ __device__ __forceinline__ void q6k_matvec_flat(const uint8_t *__restrict__ q,
   extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
       axh_q5k_matvec_flat_r##RPW##_w##NW##_p##PF##_x##XP(const uint8_t *__restrict__ q,          \
                                                          const float *__restrict__ x,            \
-                                                         float *__restrict__ y, RowsArgs a) {    \
+                                                         float *__restrict__ y, AXH_ROWS_ARGS) { AXH_ROWS_UNPACK; \
     extern __shared__ float axh_lds_dyn[];                                                       \
     q4k_matvec_flat<RPW, NW, PF, false, XP, false, true>(q, q, x, y, a.n_rows,                   \
                                                          a.units_per_row, axh_lds_dyn);          \
@@ -1109,7 +1119,7 @@ AXH_Q6K_MATVEC_FLAT(1, 8, 2, 2)
   extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
       axh_q4k_gate_up_r##ROWS##_w##NW##_p##PF##_x##XP(                                           \
           const uint8_t *__restrict__ qg, const uint8_t *__restrict__ qu,                        \
-          const float *__restrict__ x, float *__restrict__ y, RowsArgs a) {                      \
+          const float *__restrict__ x, float *__restrict__ y, AXH_ROWS_ARGS) { AXH_ROWS_UNPACK; \
     extern __shared__ float axh_lds_dyn[];                                                       \
     q4k_matvec_flat<2 * ROWS, NW, PF, false, XP, true>(qg, qu, x, y, a.n_rows, a.units_per_row,  \
                                                        axh_lds_dyn);                             \
@@ -1402,7 +1412,7 @@ __device__ __forceinline__ void q4k_matvec_wg(const uint8_t *__restrict__ q,
   extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
       axh_q4k_matvec_wg_w##NW##_x##XP##_r##RB(const uint8_t *__restrict__ q,                     \
                                               const float *__restrict__ x,                       \
-                                              float *__restrict__ y, RowsArgs a) {               \
+                                              float *__restrict__ y, AXH_ROWS_ARGS) { AXH_ROWS_UNPACK; \
     extern __shared__ float axh_wg_dyn[];                                                        \
     q4k_matvec_wg<NW, XP, RB>(q, x, y, a.n_rows, a.units_per_row, axh_wg_dyn);                   \
   }
@@ -1518,7 +1528,7 @@ __device__ __forceinline__ void q4k_matvec_sk(const uint8_t *__restrict__ q,
 #define AXH_Q4K_MATVEC_SK(SPW)                                                                   \
   extern "C" __global__ void __launch_bounds__(64)                                               \
       axh_q4k_matvec_sk_s##SPW(const uint8_t *__restrict__ q, const float *__restrict__ x,      \
-                               float *__restrict__ y, float *ws, RowsArgs a) {                   \
+                               float *__restrict__ y, float *ws, AXH_ROWS_ARGS) { AXH_ROWS_UNPACK; \
     q4k_matvec_sk<SPW>(q, x, y, ws, a.n_rows, a.units_per_row);                                  \
   }
 
@@ -1528,7 +1538,7 @@ AXH_Q4K_MATVEC_SK(16)
   extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
       axh_q4k_matvec_cols_r##RB##_w##NW##_n##NT##_x##XF(const uint8_t *__restrict__ q,           \
                                                          const float *__restrict__ x,            \
-                                                         float *__restrict__ y, RowsArgs a) {    \
+                                                         float *__restrict__ y, AXH_ROWS_ARGS) { AXH_ROWS_UNPACK; \
     __shared__ float red[2 * RB * NW];                                                           \
     q4k_matvec_cols<RB, NW, NT != 0, XF != 0>(q, x, y, a.n_rows, a.units_per_row, red);         \
   }
@@ -1550,7 +1560,7 @@ AXH_Q4K_MATVEC_COLS(4, 8, 0, 1)
 constexpr uint32_t kRefTileSb = 16; // 17 KiB static LDS tile
 extern "C" __global__ void __launch_bounds__(64)
     q4km_dequant_matvec(const uint8_t *__restrict__ q, const float *__restrict__ x,
-                        float *__restrict__ y, CountArgs a) {
+                        float *__restrict__ y, AXH_COUNT_ARGS) { AXH_COUNT_UNPACK;
   __shared__ float lds[kRefTileSb * 256 + kRefTileSb * 16];
   if (blockIdx.x != 0 || blockIdx.y != 0 || blockIdx.z != 0) return;
   if (a.n_units <= kRefTileSb)
@@ -1803,7 +1813,7 @@ __device__ __forceinline__ void q4_0_matvec_cols(const uint8_t *__restrict__ q,
 #define AXH_Q4_0_MATVEC_COLS(RB)                                                                 \
   extern "C" __global__ void __launch_bounds__(64)                                               \
       axh_q4_0_matvec_cols_r##RB(const uint8_t *__restrict__ q, const float *__restrict__ x,     \
-                                 float *__restrict__ y, RowsArgs a) {                            \
+                                 float *__restrict__ y, AXH_ROWS_ARGS) { AXH_ROWS_UNPACK; \
     q4_0_matvec_cols<RB>(q, x, y, a.n_rows, a.units_per_row);                                    \
   }
 
@@ -1813,7 +1823,7 @@ AXH_Q4_0_MATVEC_COLS(1)
   extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
       axh_q4_0_matvec_r##RPW##_w##NW(const uint8_t *__restrict__ q,                              \
                                      const float *__restrict__ x, float *__restrict__ y,         \
-                                     RowsArgs a) {                                               \
+                                     AXH_ROWS_ARGS) { AXH_ROWS_UNPACK;                   \
     extern __shared__ float axh_lds_dyn[];                                                       \
     q4_0_matvec_body<RPW, NW>(q, x, y, a.n_rows, a.units_per_row, a.tile_units, blockIdx.x,      \
                               axh_lds_dyn);                                                      \
@@ -1829,7 +1839,7 @@ AXH_Q4_0_MATVEC(4, 4)
 constexpr uint32_t kRefTileB = 128; // 17 KiB static LDS tile
 extern "C" __global__ void __launch_bounds__(64)
     q4_0_dequant_matvec(const uint8_t *__restrict__ q, const float *__restrict__ x,
-                        float *__restrict__ y, CountArgs a) {
+                        float *__restrict__ y, AXH_COUNT_ARGS) { AXH_COUNT_UNPACK;
   __shared__ float lds[(kRefTileB / 2) * 64 + kRefTileB];
   if (blockIdx.x != 0 || blockIdx.y != 0 || blockIdx.z != 0) return;
   if (a.n_units == 0) {
@@ -1846,7 +1856,7 @@ extern "C" __global__ void __launch_bounds__(64)
 // fifth bit from qh: fma(d*sc, q, -(dmin*m)) with d*sc, dmin*m and (d*sc)*q
 // exact in f32 (q <= 31), so the one rounding is the subtraction's.
 extern "C" __global__ void __launch_bounds__(256)
-    axh_q5k_dequant(const uint8_t *__restrict__ q, float *__restrict__ w, CountArgs a) {
+    axh_q5k_dequant(const uint8_t *__restrict__ q, float *__restrict__ w, AXH_COUNT_ARGS) { AXH_COUNT_UNPACK;
   const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
   const uint32_t sb = gid >> 3, k = gid & 7u, c = k >> 1, h = k & 1u;
   if (sb >= a.n_units) return;
@@ -1880,7 +1890,7 @@ extern "C" __global__ void __launch_bounds__(256)
 // Q6_K: one thread per (superblock, half n, part p): 32 weights
 // d * sc * (q - 32), exact in f32.  Byte reads (superblocks are 2-byte aligned).
 extern "C" __global__ void __launch_bounds__(256)
-    axh_q6k_dequant(const uint8_t *__restrict__ q, float *__restrict__ w, CountArgs a) {
+    axh_q6k_dequant(const uint8_t *__restrict__ q, float *__restrict__ w, AXH_COUNT_ARGS) { AXH_COUNT_UNPACK;
   const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
   const uint32_t sb = gid >> 3, n = (gid >> 2) & 1u, p = gid & 3u;
   if (sb >= a.n_units) return;
@@ -1900,7 +1910,7 @@ extern "C" __global__ void __launch_bounds__(256)
 // fma(d*sc, nibble, -(dmin*m)): d*sc, dmin*m and (d*sc)*nibble are exact in
 // f32, so the single rounding equals the reference's d1*lo - m1f.
 extern "C" __global__ void __launch_bounds__(256)
-    axh_q4k_dequant(const uint8_t *__restrict__ q, float *__restrict__ w, CountArgs a) {
+    axh_q4k_dequant(const uint8_t *__restrict__ q, float *__restrict__ w, AXH_COUNT_ARGS) { AXH_COUNT_UNPACK;
   const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
   const uint32_t sb = gid >> 3, k = gid & 7u, c = k >> 1, h = k & 1u;
   if (sb >= a.n_units) return;
@@ -1933,7 +1943,7 @@ extern "C" __global__ void __launch_bounds__(256)
 
 // Q4_0: one thread per block; (nibble - 8) * d is exact in f32.
 extern "C" __global__ void __launch_bounds__(256)
-    axh_q4_0_dequant(const uint8_t *__restrict__ q, float *__restrict__ w, CountArgs a) {
+    axh_q4_0_dequant(const uint8_t *__restrict__ q, float *__restrict__ w, AXH_COUNT_ARGS) { AXH_COUNT_UNPACK;
   const uint32_t blk = blockIdx.x * 256u + threadIdx.x;
   if (blk >= a.n_units) return;
   const uint16_t *p16 = reinterpret_cast<const uint16_t *>(q + (size_t)blk * kQ4_0BlockBytes);
@@ -1952,7 +1962,7 @@ extern "C" __global__ void __launch_bounds__(256)
 // f16 -> f32 widening of raw 16-bit patterns (pins v_cvt_f32_f16 against the
 // oracle's exhaustive table).
 extern "C" __global__ void __launch_bounds__(256)
-    axh_f16_widen(const uint16_t *__restrict__ h, float *__restrict__ f, CountArgs a) {
+    axh_f16_widen(const uint16_t *__restrict__ h, float *__restrict__ f, AXH_COUNT_ARGS) { AXH_COUNT_UNPACK;
   const uint32_t i = blockIdx.x * 256u + threadIdx.x;
   if (i < a.n_units) f[i] = f16_to_f32(h[i]);
 }
@@ -1971,7 +1981,7 @@ __device__ __forceinline__ uint32_t pack_rn_f16(float a, float b) {
 }
 
 extern "C" __global__ void __launch_bounds__(256)
-    axh_f32_to_f16(const float *__restrict__ x, uint16_t *__restrict__ h, CountArgs a) {
+    axh_f32_to_f16(const float *__restrict__ x, uint16_t *__restrict__ h, AXH_COUNT_ARGS) { AXH_COUNT_UNPACK;
   const uint32_t i = (blockIdx.x * 256u + threadIdx.x) * 8u;
   if (i + 8u <= a.n_units) {
     const float4 lo = *reinterpret_cast<const float4 *>(x + i);
@@ -1993,7 +2003,7 @@ extern "C" __global__ void __launch_bounds__(256)
 // cannot be dropped and each wave ends with one store, as a matvec wave does.
 extern "C" __global__ void __launch_bounds__(512) axh_read_floor(const uint8_t *__restrict__ q,
                                                                  uint32_t *__restrict__ out,
-                                                                 CountArgs a) {
+                                                                 AXH_COUNT_ARGS) { AXH_COUNT_UNPACK;
   const uint32_t n = a.n_units, nt = gridDim.x * 512u;
   const uint32_t gtid = blockIdx.x * 512u + threadIdx.x;
   const __amdgpu_buffer_rsrc_t r = make_rsrc(q, n * 16u);
@@ -2014,14 +2024,14 @@ extern "C" __global__ void __launch_bounds__(512) axh_read_floor(const uint8_t *
 // The same launch shape doing nothing: the per-launch cost alone.
 extern "C" __global__ void __launch_bounds__(512) axh_launch_empty(const uint8_t *__restrict__ q,
                                                                    uint32_t *__restrict__ out,
-                                                                   CountArgs a) {
+                                                                   AXH_COUNT_ARGS) { AXH_COUNT_UNPACK;
   if (a.n_units == 0xFFFFFFFFu && threadIdx.x == 0) out[0] = (uint32_t)(uintptr_t)q;
 }
 
 // Bounded busy wait (runtime tests of the completion timeout): sleeps
 // a.n_units times (about 3 us each) and then writes the count.  Always ends.
 extern "C" __global__ void __launch_bounds__(64) axh_spin(uint32_t *__restrict__ out,
-                                                          CountArgs a) {
+                                                          AXH_COUNT_ARGS) { AXH_COUNT_UNPACK;
   for (uint32_t i = 0; i < a.n_units; ++i) __builtin_amdgcn_s_sleep(127);
   if (threadIdx.x == 0 && blockIdx.x == 0) out[0] = a.n_units;
 }

@@ -63,6 +63,10 @@ struct axh_kernel {
   uint32_t pc_bytes = 0;
   uint32_t wg[3] = {1, 1, 1};
   uint32_t lds = 0;
+  // Kernels of this library's own code objects take their push constants as
+  // separate 32-bit arguments (preloaded into SGPRs): launches pass one
+  // kernel parameter per word.  Other code objects take one by-value block.
+  bool scalar_pc = false;
   std::mutex mu;              // serialises dispatch_handle on this handle
   std::vector<void *> pool;   // per-binding device buffers
   std::vector<size_t> pool_bytes;
@@ -86,6 +90,9 @@ namespace axh {
 // dynamic LDS when non-zero.
 axh_status launch_raw(axh_kernel *k, const uint32_t grid[3], void *const *buffers, size_t n_buffers,
                       const void *pc, size_t pc_bytes, uint32_t lds, hipStream_t stream);
+// True for the code objects embedded in this library (their kernels take
+// push constants as separate 32-bit arguments).
+bool is_builtin_code_object(const void *co, size_t bytes);
 // Builtin kernel by entry name, prepared once per context.
 axh_status builtin_kernel(axh_context *ctx, const char *entry, uint32_t n_buffers,
                           uint32_t pc_bytes, uint32_t wg_x, axh_kernel **out);

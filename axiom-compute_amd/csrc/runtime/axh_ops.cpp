@@ -103,6 +103,16 @@ constexpr uint32_t kQ4_0MaxTileB = 1024; // 1024 * 132 B = 132 KiB of LDS
 
 } // namespace
 
+bool is_builtin_code_object(const void *co, size_t bytes) {
+  const unsigned char *objs[2][2] = {{axh_q4_matvec_co_begin, axh_q4_matvec_co_end},
+                                     {axh_q4_matmul_co_begin, axh_q4_matmul_co_end}};
+  for (const auto &o : objs) {
+    const size_t n = (size_t)(o[1] - o[0]);
+    if (bytes == n && (co == o[0] || std::memcmp(co, o[0], n) == 0)) return true;
+  }
+  return false;
+}
+
 axh_status builtin_kernel(axh_context *ctx, const char *entry, uint32_t n_buffers,
                           uint32_t pc_bytes, uint32_t wg_x, axh_kernel **out) {
   std::lock_guard<std::mutex> lk(ctx->ops_mu);

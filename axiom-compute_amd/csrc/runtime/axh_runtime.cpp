@@ -171,9 +171,10 @@ axh_status launch_raw(axh_kernel *k, const uint32_t grid[3], void *const *buffer
                       size_t n_buffers, const void *pc, size_t pc_bytes, uint32_t lds,
                       hipStream_t stream) {
   // Kernel arguments: buffer pointers in binding order, then the push
-  // constants as one by-value struct (16-byte aligned local copy).
+  // constants as one by-value struct (16-byte aligned local copy), or as
+  // one argument per 32-bit word for this library's own kernels.
   void *ptrs[64];
-  void *params[65];
+  void *params[64 + 64];
   alignas(16) uint8_t pcbuf[256];
   if (n_buffers > 64 || pc_bytes > sizeof(pcbuf))
     return fail(AXH_ERR_DESCRIPTOR_POOL, "too many kernel arguments");
@@ -182,7 +183,13 @@ axh_status launch_raw(axh_kernel *k, const uint32_t grid[3], void *const *buffer
     ptrs[i] = buffers[i];
     params[np++] = &ptrs[i];
   }
-  if (pc_bytes) {
+  if (pc_bytes && k->scalar_pc) { // one 32-bit argument per word
+    if (pc_bytes % 4u || np + pc_bytes / 4u > sizeof(params) / sizeof(params[0]))
+      return fail(AXH_ERR_PUSH_CONSTANT_SIZE_MISMATCH,
+                  "builtin kernels take push constants as whole 32-bit words");
+    std::memcpy(pcbuf, pc, pc_bytes);
+    for (size_t w = 0; w < pc_bytes / 4u; ++w) params[np++] = pcbuf + 4u * w;
+  } else if (pc_bytes) {
     std::memcpy(pcbuf, pc, pc_bytes);
     params[np++] = pcbuf;
   }
@@ -446,6 +453,7 @@ axh_status axh_prepare_kernel(axh_context *ctx, const void *code_object, size_t 
   k->wg[1] = w[1];
   k->wg[2] = w[2];
   k->lds = plan->dynamic_lds_bytes;
+  k->scalar_pc = is_builtin_code_object(code_object, co_bytes);
   core.kernels[key] = k;
   *out = k;
   return ok();
