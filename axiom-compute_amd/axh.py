@@ -159,6 +159,7 @@ def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
         "axh_event_elapsed_ms": (st, [vp, vp, c.POINTER(c.c_float)]),
         "axh_event_destroy": (None, [vp]),
         "axh_q4k_matvec": (st, [vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
+        "axh_q4k_matvec_noalloc": (st, [vp, vp, vp, vp, u32, u32, vp]),
         "axh_capture_begin": (st, [vp]),
         "axh_capture_end": (st, [vp, c.POINTER(vp)]),
         "axh_graph_launch": (st, [vp, vp, vp]),
@@ -712,6 +713,11 @@ class HipContext:
         v = variant._c() if variant else None
         _check(self._lib.axh_q4k_matvec(self._raw, _ptr(q), _ptr(x), _ptr(y), n_rows, sb_per_row,
                                         ctypes.byref(v) if v else None, _stream(stream)))
+
+    def q4k_matvec_noalloc(self, q, x, y, n_rows: int, sb_per_row: int, stream=None) -> None:
+        """Allocation-free matvec (1-32 rows of 1-256 superblocks, per-device scratch)."""
+        _check(self._lib.axh_q4k_matvec_noalloc(self._raw, _ptr(q), _ptr(x), _ptr(y), n_rows,
+                                                sb_per_row, _stream(stream)))
 
     def q4k_gate_up(self, q_gate, q_up, x, h, n_rows: int, sb_per_row: int,
                     variant: Optional[Variant] = None, stream=None) -> None:

@@ -62,7 +62,11 @@ def build_kernels() -> dict[str, Path]:
 def build_runtime(cos: dict[str, Path]) -> Path:
     rt = PKG / "csrc" / "runtime"
     embed_o = BUILD / "axh_embed.o"
-
+    # The allocation-free entry point keeps its scratch in a __device__ array,
+    # so its file is HIP (host code plus that array's device image).
+    noalloc_o = BUILD / "axh_noalloc.o"
+    _run([HIPCC, *HIP_FLAGS, "-fPIC", "-c", "-I", str(ROOT / "include"), "-I", str(rt),
+          "-o", str(noalloc_o), str(rt / "axh_noalloc.hip")])
     _run(["gcc", "-c", f'-DAXH_Q4_MATVEC_CO="{cos["q4_matvec"]}"',
           f'-DAXH_Q4_MATMUL_CO="{cos["q4_matmul"]}"', "-o", str(embed_o),
           str(rt / "axh_embed.S")])
@@ -73,7 +77,7 @@ def build_runtime(cos: dict[str, Path]) -> Path:
         "-I", str(rt),
         str(rt / "axh_runtime.cpp"), str(rt / "axh_ops.cpp"), str(rt / "axh_gguf.cpp"),
         str(PKG / "csrc" / "tune" / "axh_tune.cpp"), str(PKG / "csrc" / "check" / "axh_check.cpp"),
-        str(embed_o),
+        str(embed_o), str(noalloc_o),
         "-L", str(ROCM / "lib"), "-Wl,-rpath," + str(ROCM / "lib"), "-lamdhip64", "-pthread",
         "-o", str(tmp),
     ])

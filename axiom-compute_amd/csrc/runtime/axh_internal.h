@@ -97,5 +97,8 @@ bool is_builtin_code_object(const void *co, size_t bytes);
 axh_status builtin_kernel(axh_context *ctx, const char *entry, uint32_t n_buffers,
                           uint32_t pc_bytes, uint32_t wg_x, axh_kernel **out);
 hipStream_t pick_stream(axh_context *ctx, void *stream);
+// Set-up of the allocation-free matvec (axh_noalloc.hip): resolves this
+// device's scratch array and prepares its kernel.  Run by axh_context_create.
+void noalloc_setup(axh_context *ctx);
 uint64_t hash_bytes(const void *data, size_t n, uint64_t seed);
 } // namespace axh

@@ -306,6 +306,7 @@ axh_status axh_context_create(const axh_context_options *opts, axh_context **out
   }
   axh_context *ctx = new axh_context();
   ctx->core = core;
+  noalloc_setup(ctx); // a failure there is reported by axh_q4k_matvec_noalloc
   *out = ctx;
   return ok();
 }

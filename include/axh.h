@@ -186,6 +186,20 @@ typedef struct axh_q4_variant {
 axh_status axh_q4k_matvec(axh_context *ctx, const void *q, const float *x, float *y,
                           uint32_t n_rows, uint32_t sb_per_row, const axh_q4_variant *variant,
                           void *stream);
+/* Allocation-free variant of axh_q4k_matvec.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory during a
+ * call (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Computes the same y for 1-32 rows of 1-256 superblocks
+ * with the split-K kernel, whose workgroup counter and partial sums live in
+ * a fixed 2304-byte per-device scratch array that axh_context_create sets up;
+ * a call allocates nothing and calls no allocating routine.  Larger shapes
+ * (and sb_per_row = 0) return AXH_ERR_INVALID_ARGUMENT.  Every call on a
+ * device shares that device's scratch, which keeps the last call's partial
+ * sums (the counter is back at zero after each call): calls that overlap on
+ * one GPU (two streams, two host threads, two contexts) race, so order them.
+ * q and x 16-byte aligned. */
+axh_status axh_q4k_matvec_noalloc(axh_context *ctx, const void *q, const float *x, float *y,
+                                  uint32_t n_rows, uint32_t sb_per_row, void *stream);
 /* Name of the kernel axh_q4k_matvec launches for this shape and variant (the
  * entry point profilers report), NUL-terminated into buf[cap].  No device
  * work.  Counterpart of the kernel name the reference's BenchFn receives in
