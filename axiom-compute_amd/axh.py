@@ -55,6 +55,9 @@ VARIANTS = {
 }
 
 ACCESS_READ_ONLY, ACCESS_WRITE_ONLY, ACCESS_READ_WRITE = 0, 1, 2
+# Q4_K matvec kernel families (the `family` hole, include/axh.h AXH_Q4K_FAMILY_*).
+(FAMILY_DEFAULT, FAMILY_PERSISTENT, FAMILY_ONE_PASS, FAMILY_ONE_PASS_X, FAMILY_WORKGROUP,
+ FAMILY_SPLIT_K, FAMILY_COLUMNS, FAMILY_TILED) = range(8)
 
 
 class DispatchError(RuntimeError):
@@ -90,6 +93,8 @@ class _Variant(ctypes.Structure):
         ("waves_per_workgroup", ctypes.c_uint32),
         ("prefetch", ctypes.c_uint32),
         ("nontemporal", ctypes.c_uint32),
+        ("family", ctypes.c_uint32),
+        ("sb_per_lane", ctypes.c_uint32),
     ]
 
 
@@ -100,6 +105,20 @@ class _MatmulVariant(ctypes.Structure):
     _fields_ = [("kind", ctypes.c_uint32), ("waves_per_workgroup", ctypes.c_uint32),
                 ("col_tiles", ctypes.c_uint32), ("prefetch", ctypes.c_uint32),
                 ("row_tiles", ctypes.c_uint32)]
+
+
+class _BenchOp(ctypes.Structure):
+    _fields_ = [
+        ("op", ctypes.c_uint32), ("q", ctypes.c_void_p), ("q_stride", ctypes.c_uint64),
+        ("n_copies", ctypes.c_uint32), ("q2_offset", ctypes.c_uint64), ("x", ctypes.c_void_p),
+        ("x16", ctypes.c_void_p), ("y", ctypes.c_void_p), ("n_rows", ctypes.c_uint32),
+        ("units", ctypes.c_uint32), ("batch", ctypes.c_uint32),
+        ("variant", ctypes.c_void_p), ("matmul_variant", ctypes.c_void_p),
+    ]
+
+
+BENCH_OPS = {"q4k": 1, "q4_0": 2, "q5k": 3, "q6k": 4, "gate_up": 5, "matmul_f16": 6,
+             "matmul_f32": 7, "read_floor": 8, "launch_empty": 9}
 
 
 class _GgufTensorInfo(ctypes.Structure):
@@ -166,6 +185,7 @@ def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
         "axh_graph_node_count": (u64, [vp]),
         "axh_graph_destroy": (None, [vp]),
         "axh_q4k_matvec_kernel_name": (st, [u32, u32, c.POINTER(_Variant), c.c_char_p, sz]),
+        "axh_q4k_matvec_default_variant": (st, [u32, u32, c.POINTER(_Variant)]),
         "axh_q4_0_matvec_kernel_name": (st, [u32, u32, c.POINTER(_Variant), c.c_char_p, sz]),
         "axh_q4k_gate_up": (st, [vp, vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
         "axh_q5k_matvec": (st, [vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
@@ -217,6 +237,7 @@ def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
         "axh_q4_0_matvec_variant_count": (u32, []),
         "axh_q4_0_matvec_variant_at": (st, [u32, c.POINTER(_Variant)]),
         "axh_builtin_code_object": (vp, [c.POINTER(sz)]),
+        "axh_bench_loop": (st, [vp, c.POINTER(_BenchOp), u32, u32, u32, c.POINTER(c.c_float)]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -253,10 +274,24 @@ class Variant:
     waves_per_workgroup: int = 0
     prefetch: int = 0
     nontemporal: int = 0
+    family: int = 0       # FAMILY_* (Q4_K matvec only); 0 = the shape's choice
+    sb_per_lane: int = 0  # one-pass families: superblocks a lane walks per row
 
     def _c(self) -> _Variant:
         return _Variant(self.rows_per_wave, self.waves_per_workgroup, self.prefetch,
-                        self.nontemporal)
+                        self.nontemporal, self.family, self.sb_per_lane)
+
+
+def _variant_from_c(v: "_Variant") -> "Variant":
+    return Variant(v.rows_per_wave, v.waves_per_workgroup, v.prefetch, v.nontemporal, v.family,
+                   v.sb_per_lane)
+
+
+def q4k_matvec_default_variant(n_rows: int, sb_per_row: int) -> "Variant":
+    """The hole assignment axh_q4k_matvec uses for this shape with no variant."""
+    v = _Variant()
+    _check(load_library().axh_q4k_matvec_default_variant(n_rows, sb_per_row, ctypes.byref(v)))
+    return _variant_from_c(v)
 
 
 def q4k_matvec_kernel_name(n_rows: int, sb_per_row: int,
@@ -798,6 +833,26 @@ class HipContext:
         """Stream nbytes of q with the matvec's launch shape (measurement helper)."""
         _check(self._lib.axh_read_floor(self._raw, _ptr(q), nbytes, _ptr(out), out_words,
                                         _stream(stream)))
+
+    def bench_loop(self, op: str, q, q_stride: int, n_copies: int, x, y, n_rows: int = 0,
+                   units: int = 0, batch: int = 0, variant=None, q2_offset: int = 0, x16=None,
+                   warmup: int = 20, groups: int = 10, calls_per_group: int = 20) -> list:
+        """Times `groups` x `calls_per_group` back-to-back calls of one operation
+        launched from the library's own loop (axh_bench_loop); returns the
+        per-group times in ms."""
+        v = variant._c() if variant is not None else None
+        o = _BenchOp(BENCH_OPS[op], _ptr(q), q_stride, n_copies, q2_offset, _ptr(x),
+                     _ptr(x16) if x16 is not None else None, _ptr(y), n_rows, units, batch,
+                     None, None)
+        if v is not None:
+            if isinstance(variant, MatmulVariant):
+                o.matmul_variant = ctypes.cast(ctypes.byref(v), ctypes.c_void_p)
+            else:
+                o.variant = ctypes.cast(ctypes.byref(v), ctypes.c_void_p)
+        out = (ctypes.c_float * groups)()
+        _check(self._lib.axh_bench_loop(self._raw, ctypes.byref(o), warmup, groups,
+                                        calls_per_group, out))
+        return [float(t) for t in out]
 
     def launch_empty(self, out, out_words: int, stream=None) -> None:
         """An empty kernel with the matvec's launch shape (measurement helper)."""

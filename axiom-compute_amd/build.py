@@ -76,7 +76,8 @@ def build_runtime(cos: dict[str, Path]) -> Path:
         "-D__HIP_PLATFORM_AMD__", "-I", str(ROCM / "include"), "-I", str(ROOT / "include"),
         "-I", str(rt),
         str(rt / "axh_runtime.cpp"), str(rt / "axh_ops.cpp"), str(rt / "axh_gguf.cpp"),
-        str(PKG / "csrc" / "tune" / "axh_tune.cpp"), str(PKG / "csrc" / "check" / "axh_check.cpp"),
+        str(PKG / "csrc" / "tune" / "axh_tune.cpp"), str(PKG / "csrc" / "tune" / "axh_winners.cpp"),
+        str(PKG / "csrc" / "check" / "axh_check.cpp"),
         str(embed_o), str(noalloc_o),
         "-L", str(ROCM / "lib"), "-Wl,-rpath," + str(ROCM / "lib"), "-lamdhip64", "-pthread",
         "-o", str(tmp),

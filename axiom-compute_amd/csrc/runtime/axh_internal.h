@@ -13,6 +13,7 @@
 #include <vector>
 
 #include "axh.h"
+#include "axh_tune.h"
 
 namespace axh {
 
@@ -83,6 +84,12 @@ struct axh_context {
   // Set when a capture on the context stream records a launch that uses the
   // context stream's workspace (the graph then replays on that stream only).
   std::atomic<bool> capture_uses_workspace{false};
+  // Tuned winners consulted when a call passes no variant; loaded from and
+  // saved to winners_path (empty: in memory only).
+  std::mutex winners_mu;
+  axh_winner_table *winners = nullptr;
+  std::atomic<bool> has_winners{false};
+  std::string winners_path;
 };
 
 namespace axh {
@@ -100,5 +107,11 @@ hipStream_t pick_stream(axh_context *ctx, void *stream);
 // Set-up of the allocation-free matvec (axh_noalloc.hip): resolves this
 // device's scratch array and prepares its kernel.  Run by axh_context_create.
 void noalloc_setup(axh_context *ctx);
+// The tuned winner for (op, n_rows, units), if the context has one.
+bool lookup_winner(axh_context *ctx, const char *op, uint32_t n_rows, uint32_t units,
+                   axh_q4_variant *out);
+// Loads (or starts) the context's winner table from `dir`; frees it.
+void winners_attach(axh_context *ctx, const std::string &dir);
+void winners_detach(axh_context *ctx);
 uint64_t hash_bytes(const void *data, size_t n, uint64_t seed);
 } // namespace axh

@@ -4,6 +4,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "axh_internal.h"
 
@@ -176,6 +177,14 @@ static const MatvecVariant *find_variant(const MatvecVariant *table, size_t n,
   return best;
 }
 
+// The family and sb_per_lane holes belong to the Q4_K matvec only.
+static axh_status reject_family(const axh_q4_variant *v) {
+  if (v && (v->family || v->sb_per_lane))
+    return fail(AXH_ERR_INVALID_ARGUMENT,
+                "family and sb_per_lane are holes of the Q4_K matvec only");
+  return AXH_OK;
+}
+
 // Prefetch 1 (early refill) kernels stage x chunk by chunk during the first
 // pass, so any row of up to 128 superblocks fits their x staging; the others
 // stage XP sub-blocks per thread before the first iteration.
@@ -215,6 +224,7 @@ constexpr uint32_t kSkMinSb = 64;  // shorter rows stay on the cols kernel
 constexpr uint32_t kSkMaxSb = 256; // longer rows: more workgroups than pay
 constexpr uint32_t kSkSpw = 16;    // superblocks per workgroup
 constexpr uint32_t kSkMaxGroups = kSkMaxSb / kSkSpw;
+constexpr uint32_t kSkMaxGroupRows = 32; // partial-sum rows per workgroup
 constexpr size_t kSkWorkspaceBytes = (64u + kSkMaxGroups * 32u) * 4u;
 
 static bool device_ptr_ok(const void *p) { return p != nullptr; }
@@ -386,90 +396,218 @@ static bool use_one_pass(uint32_t n_rows, uint32_t nsb) {
   return n_rows <= kOneMaxRows || (nsb <= kOneTallMaxSb && n_rows <= kOneTallMaxRows);
 }
 
-// Fills a one-pass plan for kernel family `prefix` (LDS: lds_per_sb per superblock of x).
-static void plan_one_pass(const char *prefix, uint32_t n_rows, uint32_t nsb, uint32_t lds_per_sb,
-                          Q4kPlan *p) {
-  std::snprintf(p->name, sizeof(p->name), "%s_one%s_i%u", prefix,
-                n_rows >= kOneWholeMinRows && nsb <= kOneWholeMaxSb ? "x" : "", (nsb + 7u) / 8u);
-  p->nw = 8;
-  p->lds = nsb * lds_per_sb;
-  p->flat = false; // one workgroup per 16 rows, all of them launched
-  p->units = (n_rows + 15u) / 16u;
-  p->args = RowsArgs{n_rows, nsb, nsb, 0};
+
+// Tiled kernel plan (rows longer than one LDS tile, or matrices >= 4 GiB).
+static void plan_tiled(uint32_t n_rows, uint32_t nsb, const MatvecVariant &tv, Q4kPlan *p) {
+  std::snprintf(p->name, sizeof(p->name), "axh_q4k_matvec_tiled_r%u_w%u_p%u", tv.rpw, tv.nw, tv.pf);
+  uint32_t tile = (nsb + 7u) & ~7u;
+  if (tile == 0) tile = 8;
+  if (tile > kQ4kMaxTileSb) tile = kQ4kMaxTileSb;
+  p->nw = tv.nw;
+  p->lds = tile * 1088u;
+  p->flat = false;
+  const uint32_t rows_per_wg = tv.rpw * tv.nw;
+  p->units = (n_rows + rows_per_wg - 1) / rows_per_wg;
+  p->args = RowsArgs{n_rows, nsb, tile, 0};
+}
+
+// Which holes a family reads; the others must stay zero.
+static bool q4k_persistent_holes(const axh_q4_variant *v) {
+  return v && (v->rows_per_wave || v->waves_per_workgroup || v->prefetch || v->nontemporal);
+}
+
+// The default family for a shape (the sweeps quoted above each kernel).
+static uint32_t q4k_default_family(uint32_t n_rows, uint32_t nsb, uint64_t q_bytes) {
+  if (q4k_use_wg(n_rows, nsb)) return AXH_Q4K_FAMILY_WORKGROUP;
+  if (n_rows < kQ4kColsMaxRows && nsb >= kSkMinSb && nsb <= kSkMaxSb && q_bytes < 0xFFFFFF00ull)
+    return AXH_Q4K_FAMILY_SPLIT_K;
+  if (n_rows < kQ4kColsMaxRows && nsb >= 1 && nsb <= kQ4kColsMaxSb) return AXH_Q4K_FAMILY_COLUMNS;
+  if (use_one_pass(n_rows, nsb) && q_bytes < 0xFFFFFFFFull)
+    return n_rows >= kOneWholeMinRows && nsb <= kOneWholeMaxSb ? AXH_Q4K_FAMILY_ONE_PASS_X
+                                                               : AXH_Q4K_FAMILY_ONE_PASS;
+  return AXH_Q4K_FAMILY_PERSISTENT; // falls back to tiled for rows it cannot stage
 }
 
 static axh_status plan_q4k(uint32_t n_rows, uint32_t sb_per_row, const axh_q4_variant *variant,
                            Q4kPlan *p) {
   const uint64_t q_bytes = (uint64_t)n_rows * sb_per_row * 144u;
-  if (!variant && q4k_use_wg(n_rows, sb_per_row)) {
-    const uint32_t rb = n_rows == 1u ? 1u : n_rows == 2u ? 2u : 4u;
+  const uint32_t nsb = sb_per_row;
+  uint32_t fam = variant ? variant->family : 0u;
+  if (fam > AXH_Q4K_FAMILY_TILED) return fail(AXH_ERR_INVALID_ARGUMENT, "unknown kernel family");
+  const bool explicit_family = fam != AXH_Q4K_FAMILY_DEFAULT;
+  if (!explicit_family)
+    fam = q4k_persistent_holes(variant) ? (uint32_t)AXH_Q4K_FAMILY_PERSISTENT
+                                        : q4k_default_family(n_rows, nsb, q_bytes);
+  if (variant && variant->sb_per_lane && fam != AXH_Q4K_FAMILY_ONE_PASS &&
+      fam != AXH_Q4K_FAMILY_ONE_PASS_X)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "sb_per_lane is a hole of the one-pass families only");
+  const bool other_holes = q4k_persistent_holes(variant);
+  switch (fam) {
+  case AXH_Q4K_FAMILY_WORKGROUP: {
+    if (variant && (variant->waves_per_workgroup || variant->prefetch || variant->nontemporal))
+      return fail(AXH_ERR_INVALID_ARGUMENT, "the one-workgroup family's only hole is rows_per_wave");
+    if (n_rows > 4u || nsb < 1u || nsb > kWgMaxSb)
+      return fail(AXH_ERR_INVALID_ARGUMENT,
+                  "the one-workgroup family takes 1-4 rows of 1-128 superblocks");
+    uint32_t rb = variant && variant->rows_per_wave ? variant->rows_per_wave
+                  : n_rows == 1u                    ? 1u
+                  : n_rows == 2u                    ? 2u
+                                                    : 4u;
+    if ((rb != 1u && rb != 2u && rb != 4u) || rb < n_rows)
+      return fail(AXH_ERR_INVALID_ARGUMENT,
+                  "one-workgroup rows_per_wave must be 1, 2 or 4 and cover n_rows");
     std::snprintf(p->name, sizeof(p->name), "axh_q4k_matvec_wg_w%u_x2_r%u", kWgNw, rb);
     p->nw = kWgNw;
-    p->lds = sb_per_row * (272u + 8u) * 4u + rb * kWgNw * 4u;
+    p->lds = nsb * (272u + 8u) * 4u + rb * kWgNw * 4u;
     p->flat = false;
     p->units = 1;
-    p->args = RowsArgs{n_rows, sb_per_row, sb_per_row, 0};
+    p->args = RowsArgs{n_rows, nsb, nsb, 0};
     return ok();
   }
-  if (!variant && n_rows < kQ4kColsMaxRows && sb_per_row >= kSkMinSb &&
-      sb_per_row <= kSkMaxSb && q_bytes < 0xFFFFFF00ull) {
+  case AXH_Q4K_FAMILY_SPLIT_K:
+    if (other_holes) return fail(AXH_ERR_INVALID_ARGUMENT, "the split-K family has no holes");
+    if (n_rows > kSkMaxGroupRows || nsb < 1u || nsb > kSkMaxSb || q_bytes >= 0xFFFFFF00ull)
+      return fail(AXH_ERR_INVALID_ARGUMENT,
+                  "the split-K family takes 1-32 rows of 1-256 superblocks");
     std::snprintf(p->name, sizeof(p->name), "axh_q4k_matvec_sk_s%u", kSkSpw);
     p->nw = 1;
     p->lds = 0;
     p->flat = false;
-    p->units = (sb_per_row + kSkSpw - 1) / kSkSpw;
-    p->args = RowsArgs{n_rows, sb_per_row, kSkSpw, 0};
+    p->units = (nsb + kSkSpw - 1) / kSkSpw;
+    p->args = RowsArgs{n_rows, nsb, kSkSpw, 0};
     return ok();
-  }
-  if (!variant && n_rows < kQ4kColsMaxRows && sb_per_row >= 1 &&
-      sb_per_row <= kQ4kColsMaxSb) {
-    // Few rows: each row is split across NW waves (4 lanes per superblock).
-    const uint32_t nw = (sb_per_row * 4u + 63u) / 64u;
+  case AXH_Q4K_FAMILY_COLUMNS: {
+    if (other_holes) return fail(AXH_ERR_INVALID_ARGUMENT, "the column family has no holes");
+    if (nsb < 1u || nsb > kQ4kColsMaxSb || q_bytes >= 0xFFFFFF00ull)
+      return fail(AXH_ERR_INVALID_ARGUMENT, "the column family takes rows of 1-128 superblocks");
+    // Each row is split across NW waves (4 lanes per superblock).
+    const uint32_t nw = (nsb * 4u + 63u) / 64u;
     std::snprintf(p->name, sizeof(p->name), "axh_q4k_matvec_cols_r%u_w%u_n0_x1", kQ4kColsRb, nw);
     p->nw = nw;
     p->lds = 0;
     p->flat = false;
     p->units = (n_rows + kQ4kColsRb - 1) / kQ4kColsRb;
-    p->args = RowsArgs{n_rows, sb_per_row, sb_per_row, 0};
+    p->args = RowsArgs{n_rows, nsb, nsb, 0};
     return ok();
   }
-  if (!variant && use_one_pass(n_rows, sb_per_row) && q_bytes < 0xFFFFFFFFull) {
-    plan_one_pass("axh_q4k_matvec", n_rows, sb_per_row, 1120u, p);
+  case AXH_Q4K_FAMILY_ONE_PASS:
+  case AXH_Q4K_FAMILY_ONE_PASS_X: {
+    if (other_holes)
+      return fail(AXH_ERR_INVALID_ARGUMENT, "the one-pass families' only hole is sb_per_lane");
+    if (nsb < 1u || nsb > kOneMaxSb || q_bytes >= 0xFFFFFFFFull)
+      return fail(AXH_ERR_INVALID_ARGUMENT,
+                  "the one-pass families take rows of 1-128 superblocks below 4 GiB");
+    const uint32_t need = (nsb + 7u) / 8u;
+    const uint32_t nit = variant && variant->sb_per_lane ? variant->sb_per_lane : need;
+    if (nit < need || nit > 16u)
+      return fail(AXH_ERR_INVALID_ARGUMENT,
+                  "sb_per_lane must cover the row (ceil(sb_per_row / 8)) and be at most 16");
+    std::snprintf(p->name, sizeof(p->name), "axh_q4k_matvec_one%s_i%u",
+                  fam == AXH_Q4K_FAMILY_ONE_PASS_X ? "x" : "", nit);
+    p->nw = 8;
+    p->lds = nsb * 1120u;
+    p->flat = false; // one workgroup per 16 rows, all of them launched
+    p->units = (n_rows + 15u) / 16u;
+    p->args = RowsArgs{n_rows, nsb, nsb, 0};
     return ok();
   }
-  const MatvecVariant dflt = q4k_default(n_rows, sb_per_row);
+  case AXH_Q4K_FAMILY_TILED: {
+    if (variant && variant->nontemporal)
+      return fail(AXH_ERR_INVALID_ARGUMENT, "the tiled family has no nontemporal hole");
+    MatvecVariant tv = n_rows >= 2048 ? MatvecVariant{2, 8, 2, 2, 1} : MatvecVariant{1, 4, 2, 2, 1};
+    if (variant && variant->rows_per_wave) tv.rpw = variant->rows_per_wave;
+    if (variant && variant->waves_per_workgroup) tv.nw = variant->waves_per_workgroup;
+    if (variant && variant->prefetch) tv.pf = variant->prefetch;
+    if (!((tv.rpw == 2 && tv.nw == 8 && tv.pf == 2) || (tv.rpw == 1 && tv.nw == 4 && tv.pf == 2)))
+      return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled tiled Q4_K matvec variant matches");
+    plan_tiled(n_rows, nsb, tv, p);
+    return ok();
+  }
+  default:
+    break;
+  }
+  // Persistent family (explicitly, or from its holes, or by default).
+  const MatvecVariant dflt = q4k_default(n_rows, nsb);
   const uint32_t want_nw =
       variant && variant->waves_per_workgroup ? variant->waves_per_workgroup : dflt.nw;
-  const uint32_t min_xp = (sb_per_row * 8u + want_nw * 64u - 1u) / (want_nw * 64u);
+  const uint32_t min_xp = (nsb * 8u + want_nw * 64u - 1u) / (want_nw * 64u);
   const MatvecVariant *v = find_variant(
       kQ4kVariants, sizeof(kQ4kVariants) / sizeof(kQ4kVariants[0]), variant, dflt, min_xp);
   if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_K matvec variant matches");
-  p->flat = sb_per_row >= 1 && sb_per_row <= kQ4kFlatMaxSb && q_bytes < 0xFFFFFFFFull &&
-            (staged_in_chunks(*v) || sb_per_row * 8u <= v->xp * v->nw * 64u);
+  p->flat = nsb >= 1 && nsb <= kQ4kFlatMaxSb && q_bytes < 0xFFFFFFFFull &&
+            (staged_in_chunks(*v) || nsb * 8u <= v->xp * v->nw * 64u);
   if (p->flat) {
     std::snprintf(p->name, sizeof(p->name), "axh_q4k_matvec_flat_r%u_w%u_p%u_n%u%s", v->rpw,
                   v->nw, v->pf, v->nt == 1 ? 1u : 0u, v->xp == 2 ? "_x2" : "");
     p->nw = v->nw;
-    p->lds = sb_per_row * 1120u; // 272 floats of x + 8 sums per superblock
+    p->lds = nsb * 1120u; // 272 floats of x + 8 sums per superblock
     // Each wave handles pairs of RPW-row bundles; the grid is persistent.
     const uint32_t bundles = (n_rows + v->rpw - 1) / v->rpw;
     const uint32_t pairs = (bundles + 1) / 2;
     p->units = (pairs + v->nw - 1) / v->nw;
-    p->args = RowsArgs{n_rows, sb_per_row, sb_per_row, 0};
+    p->args = RowsArgs{n_rows, nsb, nsb, 0};
     return ok();
   }
+  if (explicit_family)
+    return fail(AXH_ERR_INVALID_ARGUMENT,
+                "the persistent family takes rows of 1-128 superblocks below 4 GiB whose x "
+                "this variant can stage");
   // Rows longer than one LDS tile, or matrices of 4 GiB and more.
-  const MatvecVariant tv =
-      n_rows >= 2048 ? MatvecVariant{2, 8, 2, 2, 1} : MatvecVariant{1, 4, 2, 2, 1};
-  std::snprintf(p->name, sizeof(p->name), "axh_q4k_matvec_tiled_r%u_w%u_p%u", tv.rpw, tv.nw, tv.pf);
-  uint32_t tile = (sb_per_row + 7u) & ~7u;
-  if (tile == 0) tile = 8;
-  if (tile > kQ4kMaxTileSb) tile = kQ4kMaxTileSb;
-  p->nw = tv.nw;
-  p->lds = tile * 1088u;
-  const uint32_t rows_per_wg = tv.rpw * tv.nw;
-  p->units = (n_rows + rows_per_wg - 1) / rows_per_wg;
-  p->args = RowsArgs{n_rows, sb_per_row, tile, 0};
+  plan_tiled(n_rows, nsb,
+             n_rows >= 2048 ? MatvecVariant{2, 8, 2, 2, 1} : MatvecVariant{1, 4, 2, 2, 1}, p);
+  return ok();
+}
+
+// A call with no variant takes the context's tuned winner for the shape when
+// it plans (a stale entry that no longer fits falls back to the default).
+static axh_status plan_q4k_ctx(axh_context *ctx, uint32_t n_rows, uint32_t sb_per_row,
+                               const axh_q4_variant *variant, Q4kPlan *p) {
+  axh_q4_variant tuned{};
+  if (!variant && lookup_winner(ctx, "q4k_matvec", n_rows, sb_per_row, &tuned) &&
+      plan_q4k(n_rows, sb_per_row, &tuned, p) == AXH_OK)
+    return ok();
+  return plan_q4k(n_rows, sb_per_row, variant, p);
+}
+
+axh_status axh_context_q4k_matvec_kernel_name(axh_context *ctx, uint32_t n_rows,
+                                              uint32_t sb_per_row, const axh_q4_variant *variant,
+                                              char *buf, size_t cap) {
+  if (!ctx) return fail(AXH_ERR_INVALID_ARGUMENT, "ctx is NULL");
+  if (!buf || cap == 0) return fail(AXH_ERR_INVALID_ARGUMENT, "buf is NULL");
+  Q4kPlan p{};
+  axh_status s = plan_q4k_ctx(ctx, n_rows, sb_per_row, variant, &p);
+  if (s != AXH_OK) return s;
+  if (std::strlen(p.name) + 1 > cap) return fail(AXH_ERR_INVALID_ARGUMENT, "buf too small");
+  std::memcpy(buf, p.name, std::strlen(p.name) + 1);
+  return ok();
+}
+
+axh_status axh_q4k_matvec_default_variant(uint32_t n_rows, uint32_t sb_per_row,
+                                         axh_q4_variant *out) {
+  if (!out) return fail(AXH_ERR_INVALID_ARGUMENT, "out is NULL");
+  *out = axh_q4_variant{};
+  const uint64_t q_bytes = (uint64_t)n_rows * sb_per_row * 144u;
+  const uint32_t fam = q4k_default_family(n_rows, sb_per_row, q_bytes);
+  Q4kPlan p{};
+  axh_status s = plan_q4k(n_rows, sb_per_row, nullptr, &p);
+  if (s != AXH_OK) return s;
+  out->family = fam;
+  unsigned a = 0, b = 0, c = 0, d = 0;
+  if (fam == AXH_Q4K_FAMILY_ONE_PASS || fam == AXH_Q4K_FAMILY_ONE_PASS_X) {
+    out->sb_per_lane = (sb_per_row + 7u) / 8u;
+  } else if (fam == AXH_Q4K_FAMILY_WORKGROUP) {
+    if (std::sscanf(p.name, "axh_q4k_matvec_wg_w%u_x2_r%u", &a, &b) == 2) out->rows_per_wave = b;
+  } else if (std::sscanf(p.name, "axh_q4k_matvec_flat_r%u_w%u_p%u_n%u", &a, &b, &c, &d) == 4) {
+    out->rows_per_wave = a;
+    out->waves_per_workgroup = b;
+    out->prefetch = c;
+    out->nontemporal = d == 1u ? 1u : 2u;
+  } else if (std::sscanf(p.name, "axh_q4k_matvec_tiled_r%u_w%u_p%u", &a, &b, &c) == 3) {
+    out->family = AXH_Q4K_FAMILY_TILED;
+    out->rows_per_wave = a;
+    out->waves_per_workgroup = b;
+    out->prefetch = c;
+  }
   return ok();
 }
 
@@ -496,7 +634,7 @@ axh_status axh_q4k_matvec(axh_context *ctx, const void *q, const float *x, float
   if (((uintptr_t)q & 15u) || ((uintptr_t)x & 15u))
     return fail(AXH_ERR_INVALID_ARGUMENT, "q and x must be 16-byte aligned");
   Q4kPlan p{};
-  axh_status s = plan_q4k(n_rows, sb_per_row, variant, &p);
+  axh_status s = plan_q4k_ctx(ctx, n_rows, sb_per_row, variant, &p);
   if (s != AXH_OK) return s;
   if (p.lds > ctx->core->max_lds)
     return fail(AXH_ERR_PIPELINE_LAYOUT, "LDS tile exceeds the device limit");
@@ -543,6 +681,7 @@ static MatvecVariant gate_up_default(uint32_t n_rows, uint32_t nsb) {
 
 static axh_status plan_gate_up(uint32_t n_rows, uint32_t sb_per_row,
                                const axh_q4_variant *variant, Q4kPlan *p) {
+  if (reject_family(variant) != AXH_OK) return AXH_ERR_INVALID_ARGUMENT;
   if (sb_per_row == 0 || sb_per_row > kQ4kFlatMaxSb)
     return fail(AXH_ERR_INVALID_ARGUMENT, "gate/up: sb_per_row must be 1..128");
   if ((uint64_t)n_rows * sb_per_row * 144u >= 0xFFFFFFFFull)
@@ -638,6 +777,7 @@ static MatvecVariant kq_default(const KqFormat &f, uint32_t nsb) {
 
 static axh_status plan_kq(const KqFormat &f, uint32_t n_rows, uint32_t sb_per_row,
                           const axh_q4_variant *variant, Q4kPlan *p) {
+  if (reject_family(variant) != AXH_OK) return AXH_ERR_INVALID_ARGUMENT;
   if (sb_per_row == 0 || sb_per_row > kQ4kFlatMaxSb)
     return fail(AXH_ERR_INVALID_ARGUMENT, "sb_per_row must be 1..128 for Q5_K / Q6_K");
   if ((uint64_t)n_rows * sb_per_row * f.sb_bytes >= 0xFFFFFFFFull)
@@ -779,6 +919,7 @@ static const MatvecVariant *pick_q4_0(uint32_t n_rows, uint32_t blocks_per_row,
 axh_status axh_q4_0_matvec_kernel_name(uint32_t n_rows, uint32_t blocks_per_row,
                                        const axh_q4_variant *variant, char *buf, size_t cap) {
   if (!buf || cap == 0) return fail(AXH_ERR_INVALID_ARGUMENT, "buf is NULL");
+  if (reject_family(variant) != AXH_OK) return AXH_ERR_INVALID_ARGUMENT;
   if (q4_0_use_cols(n_rows, blocks_per_row, variant)) {
     const int n = std::snprintf(buf, cap, "axh_q4_0_matvec_cols_r%u", kQ4_0ColsRb);
     if (n < 0 || (size_t)n >= cap) return fail(AXH_ERR_INVALID_ARGUMENT, "buf too small");
@@ -802,6 +943,7 @@ axh_status axh_q4_0_matvec(axh_context *ctx, const void *q, const float *x, floa
     return fail(AXH_ERR_INVALID_ARGUMENT, "blocks_per_row too large");
   if (((uintptr_t)q & 3u) || ((uintptr_t)x & 15u))
     return fail(AXH_ERR_INVALID_ARGUMENT, "q must be 4-byte and x 16-byte aligned");
+  if (reject_family(variant) != AXH_OK) return AXH_ERR_INVALID_ARGUMENT;
   if (q4_0_use_cols(n_rows, blocks_per_row, variant)) {
     const uint32_t rb = kQ4_0ColsRb;
     char cname[64];
@@ -1119,3 +1261,74 @@ axh_status axh_f32_to_f16(axh_context *ctx, const float *x, uint16_t *h, uint64_
 }
 
 } // extern "C"
+
+// ---- measurement loop ---------------------------------------------------------
+static axh_status bench_call(axh_context *ctx, const axh_bench_op *o, uint32_t i) {
+  const uint8_t *q = static_cast<const uint8_t *>(o->q) + (uint64_t)(i % o->n_copies) * o->q_stride;
+  switch (o->op) {
+  case AXH_BENCH_Q4K_MATVEC:
+    return axh_q4k_matvec(ctx, q, static_cast<const float *>(o->x), static_cast<float *>(o->y),
+                          o->n_rows, o->units, o->variant, nullptr);
+  case AXH_BENCH_Q4_0_MATVEC:
+    return axh_q4_0_matvec(ctx, q, static_cast<const float *>(o->x), static_cast<float *>(o->y),
+                           o->n_rows, o->units, o->variant, nullptr);
+  case AXH_BENCH_Q5K_MATVEC:
+    return axh_q5k_matvec(ctx, q, static_cast<const float *>(o->x), static_cast<float *>(o->y),
+                          o->n_rows, o->units, o->variant, nullptr);
+  case AXH_BENCH_Q6K_MATVEC:
+    return axh_q6k_matvec(ctx, q, static_cast<const float *>(o->x), static_cast<float *>(o->y),
+                          o->n_rows, o->units, o->variant, nullptr);
+  case AXH_BENCH_Q4K_GATE_UP:
+    return axh_q4k_gate_up(ctx, q, q + o->q2_offset, static_cast<const float *>(o->x),
+                           static_cast<float *>(o->y), o->n_rows, o->units, o->variant, nullptr);
+  case AXH_BENCH_Q4K_MATMUL_F16:
+    return axh_q4k_matmul_f16(ctx, q, static_cast<const uint16_t *>(o->x),
+                              static_cast<float *>(o->y), o->n_rows, o->units, o->batch,
+                              o->matmul_variant, nullptr);
+  case AXH_BENCH_Q4K_MATMUL_F32:
+    return axh_q4k_matmul_f32(ctx, q, static_cast<const float *>(o->x),
+                              static_cast<uint16_t *>(o->x16), static_cast<float *>(o->y),
+                              o->n_rows, o->units, o->batch, o->matmul_variant, nullptr);
+  case AXH_BENCH_READ_FLOOR:
+    return axh_read_floor(ctx, q, (uint64_t)o->units * 16u, static_cast<uint32_t *>(o->y),
+                          o->batch, nullptr);
+  case AXH_BENCH_LAUNCH_EMPTY:
+    return axh_launch_empty(ctx, static_cast<uint32_t *>(o->y), o->batch, nullptr);
+  default:
+    return fail(AXH_ERR_INVALID_ARGUMENT, "unknown bench operation");
+  }
+}
+
+extern "C" axh_status axh_bench_loop(axh_context *ctx, const axh_bench_op *op, uint32_t warmup,
+                                     uint32_t groups, uint32_t calls_per_group, float *group_ms) {
+  if (!ctx || !op || !group_ms || groups == 0 || calls_per_group == 0 || op->n_copies == 0)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "bench loop: bad arguments");
+  if (groups > 100000) return fail(AXH_ERR_INVALID_ARGUMENT, "bench loop: too many groups");
+  hipSetDevice(ctx->core->device);
+  const hipStream_t st = ctx->core->stream;
+  uint32_t i = 0;
+  for (; i < warmup; ++i) {
+    const axh_status s = bench_call(ctx, op, i);
+    if (s != AXH_OK) return s;
+  }
+  axh_status s = axh_device_synchronize(ctx);
+  if (s != AXH_OK) return s;
+  std::vector<hipEvent_t> ev(groups + 1u, nullptr);
+  for (auto &e : ev)
+    if (hipEventCreate(&e) != hipSuccess) {
+      for (auto &f : ev)
+        if (f) hipEventDestroy(f);
+      return fail(AXH_ERR_QUEUE_SUBMIT, "hipEventCreate failed");
+    }
+  hipEventRecord(ev[0], st);
+  for (uint32_t g = 0; g < groups && s == AXH_OK; ++g) {
+    for (uint32_t c = 0; c < calls_per_group && s == AXH_OK; ++c) s = bench_call(ctx, op, i++);
+    hipEventRecord(ev[g + 1u], st);
+  }
+  if (s == AXH_OK) s = axh_synchronize(ctx, nullptr);
+  for (uint32_t g = 0; g < groups && s == AXH_OK; ++g)
+    if (hipEventElapsedTime(&group_ms[g], ev[g], ev[g + 1u]) != hipSuccess)
+      s = fail(AXH_ERR_QUEUE_SUBMIT, "hipEventElapsedTime failed");
+  for (auto &e : ev) hipEventDestroy(e);
+  return s == AXH_OK ? ok() : s;
+}

@@ -306,6 +306,7 @@ axh_status axh_context_create(const axh_context_options *opts, axh_context **out
   }
   axh_context *ctx = new axh_context();
   ctx->core = core;
+  winners_attach(ctx, core->cache_dir);
   noalloc_setup(ctx); // a failure there is reported by axh_q4k_matvec_noalloc
   *out = ctx;
   return ok();
@@ -327,6 +328,7 @@ void axh_context_destroy(axh_context *ctx) {
     hipDeviceSynchronize(); // workspaces may be in use on caller streams
     for (auto &kv : ctx->workspaces) hipFree(kv.second);
   }
+  winners_detach(ctx);
   delete ctx; // Core lives on while handles hold it
 }
 

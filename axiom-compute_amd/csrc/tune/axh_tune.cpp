@@ -12,6 +12,7 @@
 #include <string>
 #include <vector>
 
+#include "axh_check.h"
 #include "axh_internal.h"
 #include "axh_tune.h"
 
@@ -321,75 +322,70 @@ axh_status axh_grid_search(const axh_strategy_hole *holes, uint32_t n_holes,
   return ok();
 }
 
-// ---- HIP-timed sweep of the compiled Q4_K matvec variants ------------------
+// ---- Q4_K matvec autotuner: every kernel family, judged by the checker ------
 namespace {
 struct Q4kTuneCtx {
   axh_context *ctx;
   const void *q;
   const float *x;
   float *y;
-  float *y_ref; // device scratch for the reference output
   uint32_t n_rows, sb;
   uint32_t samples;
   double tol;
-  std::vector<float> ref_host;
+  std::vector<uint8_t> q_host; // checker inputs
+  std::vector<float> x_host, y_host;
+  // hole names of the current family's search, in the enumerator's key order
+  std::vector<std::string> keys;
 };
 
-// values in sorted key order: nontemporal, prefetch, rows_per_wave, waves_per_workgroup
-axh_q4_variant to_variant(const int64_t *v) {
+// The assignment of one enumerated variant (values in sorted key order).
+axh_q4_variant assignment(const Q4kTuneCtx &t, const int64_t *v) {
   axh_q4_variant r{};
-  r.nontemporal = (uint32_t)v[0];
-  r.prefetch = (uint32_t)v[1];
-  r.rows_per_wave = (uint32_t)v[2];
-  r.waves_per_workgroup = (uint32_t)v[3];
+  for (size_t k = 0; k < t.keys.size(); ++k) {
+    const uint32_t val = (uint32_t)v[k];
+    const std::string &n = t.keys[k];
+    if (n == "family") r.family = val;
+    else if (n == "nontemporal") r.nontemporal = val;
+    else if (n == "prefetch") r.prefetch = val;
+    else if (n == "rows_per_wave") r.rows_per_wave = val;
+    else if (n == "sb_per_lane") r.sb_per_lane = val;
+    else if (n == "waves_per_workgroup") r.waves_per_workgroup = val;
+  }
   return r;
 }
 
-bool compiled(const axh_q4_variant &v) {
-  const uint32_t n = axh_q4k_matvec_variant_count();
-  for (uint32_t i = 0; i < n; ++i) {
-    axh_q4_variant c{};
-    axh_q4k_matvec_variant_at(i, &c);
-    if (c.rows_per_wave == v.rows_per_wave && c.waves_per_workgroup == v.waves_per_workgroup &&
-        c.prefetch == v.prefetch && c.nontemporal == v.nontemporal)
-      return true;
+// A variant is valid for the shape when it plans to a compiled kernel.
+bool plans(const Q4kTuneCtx &t, const axh_q4_variant &v, char *err, size_t cap) {
+  char name[64];
+  if (axh_q4k_matvec_kernel_name(t.n_rows, t.sb, &v, name, sizeof(name)) != AXH_OK) {
+    std::snprintf(err, cap, "%s", axh_last_error());
+    return false;
   }
-  return false;
+  return true;
 }
 
 int tune_correct(void *user, uint64_t, const int64_t *vals, uint32_t, char *err, size_t cap) {
   Q4kTuneCtx &t = *static_cast<Q4kTuneCtx *>(user);
-  const axh_q4_variant v = to_variant(vals);
-  if (!compiled(v)) {
-    std::snprintf(err, cap, "variant not compiled");
-    return 1;
-  }
+  const axh_q4_variant v = assignment(t, vals);
+  // An assignment with no kernel for the shape is not judged here: the bench
+  // then reports it Failed (grid_search.rs:93-101), not CorrectnessRejected.
+  if (!plans(t, v, err, cap)) return 0;
   if (axh_q4k_matvec(t.ctx, t.q, t.x, t.y, t.n_rows, t.sb, &v, nullptr) != AXH_OK ||
-      axh_synchronize(t.ctx, nullptr) != AXH_OK) {
+      axh_synchronize(t.ctx, nullptr) != AXH_OK ||
+      axh_download(t.ctx, t.y_host.data(), t.y, 4u * t.n_rows) != AXH_OK) {
     std::snprintf(err, cap, "%s", axh_last_error());
     return 1;
   }
-  std::vector<float> got(t.n_rows);
-  if (axh_download(t.ctx, got.data(), t.y, 4u * t.n_rows) != AXH_OK) {
-    std::snprintf(err, cap, "%s", axh_last_error());
+  axh_check_report rep{};
+  if (axh_check_q4k_matvec(t.q_host.data(), t.x_host.data(), t.y_host.data(), t.n_rows, t.sb,
+                           t.tol, &rep) != AXH_OK) {
+    std::snprintf(err, cap, "%s", axh_check_last_error());
     return 1;
   }
-  if (t.tol == 0.0) {
-    if (std::memcmp(got.data(), t.ref_host.data(), 4u * t.n_rows) != 0) {
-      std::snprintf(err, cap, "output differs bitwise from the default variant");
-      return 1;
-    }
-    return 0;
-  }
-  double num = 0, den = 0;
-  for (uint32_t i = 0; i < t.n_rows; ++i) {
-    const double d = (double)got[i] - (double)t.ref_host[i];
-    num += d * d;
-    den += (double)t.ref_host[i] * t.ref_host[i];
-  }
-  if (std::sqrt(num) > t.tol * std::sqrt(den) + 1e-30) {
-    std::snprintf(err, cap, "norm-wise relative error %.3g > %.3g", std::sqrt(num / (den + 1e-300)),
-                  t.tol);
+  if (!rep.ok) {
+    std::snprintf(err, cap, "checker: %llu of %llu rows beyond %.3g (worst %.3g x allowed)",
+                  (unsigned long long)rep.rows_failed, (unsigned long long)rep.rows_checked,
+                  t.tol, rep.worst_over_allowed);
     return 1;
   }
   return 0;
@@ -398,11 +394,8 @@ int tune_correct(void *user, uint64_t, const int64_t *vals, uint32_t, char *err,
 int tune_bench(void *user, uint64_t, const int64_t *vals, uint32_t, axh_sample_stats *out,
                char *err, size_t cap) {
   Q4kTuneCtx &t = *static_cast<Q4kTuneCtx *>(user);
-  const axh_q4_variant v = to_variant(vals);
-  if (!compiled(v)) {
-    std::snprintf(err, cap, "variant not compiled");
-    return 1;
-  }
+  const axh_q4_variant v = assignment(t, vals);
+  if (!plans(t, v, err, cap)) return 1;
   hipStream_t s = t.ctx->core->stream;
   std::vector<uint64_t> ns;
   hipEvent_t e0, e1;
@@ -441,38 +434,119 @@ int tune_bench(void *user, uint64_t, const int64_t *vals, uint32_t, axh_sample_s
   out->n_samples = (uint32_t)ns.size();
   return 0;
 }
+
+// One family's hole space (candidate lists; the family itself is a
+// one-candidate hole so every variant id names its family).
+struct Hole {
+  const char *name;
+  std::vector<int64_t> cand;
+};
+
+std::vector<Hole> family_holes(uint32_t fam, uint32_t n_rows, uint32_t nsb) {
+  std::vector<Hole> h{{"family", {(int64_t)fam}}};
+  switch (fam) {
+  case AXH_Q4K_FAMILY_PERSISTENT:
+    h.push_back({"nontemporal", {2, 1}});
+    h.push_back({"prefetch", {1, 2, 4, 7}});
+    h.push_back({"rows_per_wave", {1, 2, 4}});
+    h.push_back({"waves_per_workgroup", {4, 8, 16}});
+    break;
+  case AXH_Q4K_FAMILY_ONE_PASS:
+  case AXH_Q4K_FAMILY_ONE_PASS_X: {
+    const int64_t need = (nsb + 7) / 8;
+    std::vector<int64_t> c{need};
+    if (need < 16) c.push_back(need + 1); // a longer trip count than the row needs
+    h.push_back({"sb_per_lane", c});
+    break;
+  }
+  case AXH_Q4K_FAMILY_WORKGROUP:
+    h.push_back({"rows_per_wave", {1, 2, 4}});
+    break;
+  case AXH_Q4K_FAMILY_TILED:
+    h.push_back({"prefetch", {2}});
+    h.push_back({"rows_per_wave", {1, 2}});
+    h.push_back({"waves_per_workgroup", {4, 8}});
+    break;
+  default: // split-K, columns: no holes beyond the family
+    break;
+  }
+  (void)n_rows;
+  return h;
+}
 } // namespace
 
 axh_status axh_q4k_matvec_autotune(axh_context *ctx, const void *q, const float *x, float *y,
                                    uint32_t n_rows, uint32_t sb_per_row, uint32_t samples,
-                                   double tol, axh_q4_variant *best, uint64_t *best_median_ns) {
-  if (!ctx || !best || n_rows == 0 || sb_per_row == 0)
+                                   double tol, axh_autotune_report *out) {
+  if (!ctx || !out || n_rows == 0 || sb_per_row == 0)
     return fail(AXH_ERR_INVALID_ARGUMENT, "autotune needs a context, a shape and an output");
-  // reference output from the default variant
-  axh_status st = axh_q4k_matvec(ctx, q, x, y, n_rows, sb_per_row, nullptr, nullptr);
+  std::memset(out, 0, sizeof(*out));
+  Q4kTuneCtx t{ctx, q, x, y, n_rows, sb_per_row, samples ? samples : 5, tol > 0 ? tol : 1e-3,
+               {}, {}, {}, {}};
+  const uint64_t q_bytes = (uint64_t)n_rows * sb_per_row * 144u;
+  if (q_bytes > (uint64_t)4 << 30)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "autotune: the checker copy is limited to 4 GiB");
+  t.q_host.resize(q_bytes);
+  t.x_host.resize((size_t)sb_per_row * 256u);
+  t.y_host.resize(n_rows);
+  axh_status st = axh_download(ctx, t.q_host.data(), q, q_bytes);
+  if (st == AXH_OK) st = axh_download(ctx, t.x_host.data(), x, 4u * t.x_host.size());
   if (st != AXH_OK) return st;
-  if ((st = axh_synchronize(ctx, nullptr)) != AXH_OK) return st;
-  Q4kTuneCtx t{ctx, q, x, y, nullptr, n_rows, sb_per_row, samples ? samples : 5, tol, {}};
-  t.ref_host.resize(n_rows);
-  if ((st = axh_download(ctx, t.ref_host.data(), y, 4u * n_rows)) != AXH_OK) return st;
-  const int64_t rpw[] = {1, 2, 4}, nw[] = {4, 8, 16}, pf[] = {2, 4, 7}, nt[] = {2, 1};
-  const axh_strategy_hole holes[] = {{"rows_per_wave", rpw, 3},
-                                     {"waves_per_workgroup", nw, 3},
-                                     {"prefetch", pf, 3},
-                                     {"nontemporal", nt, 2}};
-  uint64_t n = 0;
-  if ((st = axh_enumerate_strategy(holes, 4, &n, nullptr, nullptr, nullptr, 0)) != AXH_OK) return st;
-  std::vector<axh_variant_result> res(n);
-  axh_correctness_policy pol{AXH_POLICY_EQUIV_FP_TOL, 0};
-  axh_grid_search_result out{};
-  st = axh_grid_search(holes, 4, &pol, tune_correct, tune_bench, &t, res.data(), n, &out);
-  if (st != AXH_OK) return st;
-  if (out.fallback_used) return fail((axh_status)AXH_ERR_NO_SUCCESSFUL_VARIANTS, "no variant ran");
-  std::vector<int64_t> vals(4 * n);
-  axh_enumerate_strategy(holes, 4, &n, nullptr, vals.data(), nullptr, n);
-  *best = to_variant(&vals[4 * out.winner_ordinal]);
-  if (best_median_ns) *best_median_ns = res[out.winner_ordinal].stats.median_ns;
-  return ok();
+  if ((st = axh_q4k_matvec_default_variant(n_rows, sb_per_row, &out->dflt)) != AXH_OK) return st;
+
+  bool have = false;
+  for (uint32_t fam = AXH_Q4K_FAMILY_PERSISTENT; fam <= AXH_Q4K_FAMILY_TILED; ++fam) {
+    // families that cannot take the shape are skipped whole
+    axh_q4_variant probe{};
+    probe.family = fam;
+    char name[64];
+    if (fam != AXH_Q4K_FAMILY_PERSISTENT &&
+        axh_q4k_matvec_kernel_name(n_rows, sb_per_row, &probe, name, sizeof(name)) != AXH_OK)
+      continue;
+    const std::vector<Hole> hs = family_holes(fam, n_rows, sb_per_row);
+    std::vector<axh_strategy_hole> holes;
+    for (const Hole &h : hs)
+      holes.push_back({h.name, h.cand.data(), (uint32_t)h.cand.size()});
+    uint64_t n = 0;
+    std::vector<uint32_t> order(holes.size());
+    if ((st = axh_enumerate_strategy(holes.data(), (uint32_t)holes.size(), &n, order.data(),
+                                     nullptr, nullptr, 0)) != AXH_OK)
+      return st;
+    t.keys.clear();
+    for (uint32_t k : order) t.keys.push_back(holes[k].name);
+    std::vector<axh_variant_result> res(n);
+    axh_correctness_policy pol{AXH_POLICY_EQUIV_FP_TOL, 0};
+    axh_grid_search_result gs{};
+    if ((st = axh_grid_search(holes.data(), (uint32_t)holes.size(), &pol, tune_correct,
+                              tune_bench, &t, res.data(), n, &gs)) != AXH_OK)
+      return st;
+    std::vector<int64_t> vals(holes.size() * n);
+    axh_enumerate_strategy(holes.data(), (uint32_t)holes.size(), &n, nullptr, vals.data(),
+                           nullptr, n);
+    out->variants += (uint32_t)n;
+    for (uint64_t v = 0; v < n; ++v) {
+      const axh_variant_result &r = res[v];
+      if (r.outcome == AXH_OUTCOME_OK) ++out->accepted;
+      else if (r.outcome == AXH_OUTCOME_CORRECTNESS_REJECTED) ++out->rejected;
+      else ++out->failed;
+      if (r.outcome != AXH_OUTCOME_OK) continue;
+      const axh_q4_variant a = assignment(t, &vals[holes.size() * v]);
+      if (std::memcmp(&a, &out->dflt, sizeof(a)) == 0) out->default_median_ns = r.stats.median_ns;
+      if (!have || r.stats.median_ns < out->best_median_ns) {
+        have = true;
+        out->best = a;
+        out->best_median_ns = r.stats.median_ns;
+      }
+    }
+  }
+  if (!have) return fail((axh_status)AXH_ERR_NO_SUCCESSFUL_VARIANTS, "no variant ran");
+  if ((st = axh_q4k_matvec_kernel_name(n_rows, sb_per_row, &out->best, out->best_kernel,
+                                       sizeof(out->best_kernel))) != AXH_OK)
+    return st;
+  if ((st = axh_context_winner_put(ctx, "q4k_matvec", n_rows, sb_per_row, &out->best,
+                                   out->best_median_ns)) != AXH_OK)
+    return st;
+  return axh_context_winners_save(ctx);
 }
 
 } // extern "C"

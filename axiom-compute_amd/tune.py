@@ -2,7 +2,8 @@
 
   enumerate_strategy(holes) -> list[StrategyVariant]        (enumerator.rs:68-129)
   grid_search(holes, policy, correctness_fn, bench_fn)       (grid_search.rs:158-283)
-  q4k_matvec_autotune(ctx, q, x, y, n_rows, sb_per_row)      (HIP-timed variant sweep)
+  q4k_matvec_autotune(ctx, q, x, y, n_rows, sb_per_row)      (every Q4_K family, checked)
+  WinnerTable / load_winners(path)                           (per-shape winners, JSON)
 
 `holes` is a mapping name -> candidate list (source order; index 0 is the
 baseline), like StrategyHoles.map.  bench_fn(assignments) returns SampleStats
@@ -44,6 +45,14 @@ class _Summary(ctypes.Structure):
                 ("n_results", ctypes.c_uint64)]
 
 
+class _Report(ctypes.Structure):
+    _fields_ = [("best", _axh._Variant), ("best_median_ns", ctypes.c_uint64),
+                ("dflt", _axh._Variant), ("default_median_ns", ctypes.c_uint64),
+                ("variants", ctypes.c_uint32), ("accepted", ctypes.c_uint32),
+                ("rejected", ctypes.c_uint32), ("failed", ctypes.c_uint32),
+                ("best_kernel", ctypes.c_char * 64)]
+
+
 _BENCH = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64,
                           ctypes.POINTER(ctypes.c_int64), ctypes.c_uint32,
                           ctypes.POINTER(_Stats), ctypes.c_void_p, ctypes.c_size_t)
@@ -73,8 +82,26 @@ def _lib():
         lib.axh_q4k_matvec_autotune.restype = c.c_int
         lib.axh_q4k_matvec_autotune.argtypes = [c.c_void_p, c.c_void_p, c.c_void_p, c.c_void_p,
                                                 c.c_uint32, c.c_uint32, c.c_uint32, c.c_double,
-                                                c.POINTER(_axh._Variant),
-                                                c.POINTER(c.c_uint64)]
+                                                c.POINTER(_Report)]
+        vp, u32, u64 = c.c_void_p, c.c_uint32, c.c_uint64
+        V = c.POINTER(_axh._Variant)
+        for name, res, args in (
+                ("axh_winners_new", vp, []), ("axh_winners_free", None, [vp]),
+                ("axh_winners_count", u64, [vp]),
+                ("axh_winners_load", c.c_int, [c.c_char_p, c.POINTER(vp)]),
+                ("axh_winners_save", c.c_int, [vp, c.c_char_p]),
+                ("axh_winners_put", c.c_int, [vp, c.c_char_p, u32, u32, V, u64]),
+                ("axh_winners_get", c.c_int, [vp, c.c_char_p, u32, u32, c.POINTER(u32), V,
+                                              c.POINTER(u64)]),
+                ("axh_context_winner_put", c.c_int, [vp, c.c_char_p, u32, u32, V, u64]),
+                ("axh_context_winner_get", c.c_int, [vp, c.c_char_p, u32, u32, c.POINTER(u32),
+                                                     V, c.POINTER(u64)]),
+                ("axh_context_winners_save", c.c_int, [vp]),
+                ("axh_context_winners_path", c.c_char_p, [vp]),
+                ("axh_context_q4k_matvec_kernel_name", c.c_int, [vp, u32, u32, V, c.c_char_p,
+                                                                 c.c_size_t])):
+            fn = getattr(lib, name)
+            fn.restype, fn.argtypes = res, args
         _configured = True
     return lib
 
@@ -236,13 +263,99 @@ def grid_search(holes: Mapping[str, Sequence[int]], policy: CorrectnessPolicy,
                             bool(summ.fallback_used), warnings)
 
 
+@dataclass
+class AutotuneReport:
+    best: "_axh.Variant"
+    best_median_ns: int
+    default: "_axh.Variant"
+    default_median_ns: int
+    variants: int
+    accepted: int
+    rejected: int
+    failed: int
+    best_kernel: str
+
+
 def q4k_matvec_autotune(ctx, q, x, y, n_rows: int, sb_per_row: int, samples: int = 5,
-                        tol: float = 1e-3):
-    """Sweep the compiled Q4_K matvec variants on resident buffers; returns
-    (Variant, median ns per call)."""
-    v = _axh._Variant()
-    ns = ctypes.c_uint64()
+                        tol: float = 1e-3) -> AutotuneReport:
+    """Grid search over every Q4_K matvec kernel family on resident buffers; each
+    variant is judged by the f64 host checker (relative `tol`) and timed.  The
+    winner is stored in the context's table (and its file, if it has one)."""
+    r = _Report()
     _check(_lib().axh_q4k_matvec_autotune(ctx.raw, _axh._ptr(q), _axh._ptr(x), _axh._ptr(y),
-                                          n_rows, sb_per_row, samples, tol, ctypes.byref(v),
-                                          ctypes.byref(ns)))
-    return _axh.Variant(v.rows_per_wave, v.waves_per_workgroup, v.prefetch, v.nontemporal), int(ns.value)
+                                          n_rows, sb_per_row, samples, tol, ctypes.byref(r)))
+    return AutotuneReport(_axh._variant_from_c(r.best), int(r.best_median_ns),
+                          _axh._variant_from_c(r.dflt), int(r.default_median_ns),
+                          r.variants, r.accepted, r.rejected, r.failed, r.best_kernel.decode())
+
+
+class WinnerTable:
+    """Per-shape tuned winners (axh_winners_*): op, n_rows, units -> (Variant, median_ns)."""
+
+    def __init__(self, raw: Optional[int] = None):
+        self._raw = raw if raw is not None else _lib().axh_winners_new()
+
+    @classmethod
+    def load(cls, path) -> "WinnerTable":
+        raw = ctypes.c_void_p()
+        _check(_lib().axh_winners_load(str(path).encode(), ctypes.byref(raw)))
+        return cls(raw.value)
+
+    def save(self, path) -> None:
+        _check(_lib().axh_winners_save(self._raw, str(path).encode()))
+
+    def __len__(self) -> int:
+        return int(_lib().axh_winners_count(self._raw))
+
+    def put(self, op: str, n_rows: int, units: int, v: "_axh.Variant", median_ns: int) -> None:
+        c = v._c()
+        _check(_lib().axh_winners_put(self._raw, op.encode(), n_rows, units, ctypes.byref(c),
+                                      median_ns))
+
+    def get(self, op: str, n_rows: int, units: int):
+        found, c, ns = ctypes.c_uint32(), _axh._Variant(), ctypes.c_uint64()
+        _check(_lib().axh_winners_get(self._raw, op.encode(), n_rows, units, ctypes.byref(found),
+                                      ctypes.byref(c), ctypes.byref(ns)))
+        return (_axh._variant_from_c(c), int(ns.value)) if found.value else None
+
+    def close(self) -> None:
+        if self._raw:
+            _lib().axh_winners_free(self._raw)
+            self._raw = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def context_winner_put(ctx, op: str, n_rows: int, units: int, v: "_axh.Variant",
+                       median_ns: int = 0) -> None:
+    c = v._c()
+    _check(_lib().axh_context_winner_put(ctx.raw, op.encode(), n_rows, units, ctypes.byref(c),
+                                         median_ns))
+
+
+def context_winner_get(ctx, op: str, n_rows: int, units: int):
+    found, c, ns = ctypes.c_uint32(), _axh._Variant(), ctypes.c_uint64()
+    _check(_lib().axh_context_winner_get(ctx.raw, op.encode(), n_rows, units,
+                                         ctypes.byref(found), ctypes.byref(c), ctypes.byref(ns)))
+    return (_axh._variant_from_c(c), int(ns.value)) if found.value else None
+
+
+def context_winners_save(ctx) -> None:
+    _check(_lib().axh_context_winners_save(ctx.raw))
+
+
+def context_winners_path(ctx) -> str:
+    return _lib().axh_context_winners_path(ctx.raw).decode()
+
+
+def context_q4k_matvec_kernel_name(ctx, n_rows: int, sb_per_row: int, variant=None) -> str:
+    """Kernel axh_q4k_matvec launches on this context (consults its winner table)."""
+    v = variant._c() if variant else None
+    buf = ctypes.create_string_buffer(64)
+    _check(_lib().axh_context_q4k_matvec_kernel_name(ctx.raw, n_rows, sb_per_row,
+                                                     ctypes.byref(v) if v else None, buf, 64))
+    return buf.value.decode()

@@ -162,6 +162,16 @@ class Case:
             self.ctx.q4k_matmul(w, self.dx, self.dy, self.rows, self.units, self.batch,
                                 self.variant)
 
+    def bench_op(self) -> dict:
+        """Arguments of ctx.bench_loop for this workload (call i reads copy i)."""
+        op = {"q4k": "q4k", "q4_0": "q4_0", "q5k": "q5k", "q6k": "q6k",
+              "gate_up": "gate_up"}.get(self.kind)
+        if op is None:
+            op = "matmul_f32" if self.x_f32 else "matmul_f16"
+        return dict(op=op, q=self.wbuf, q_stride=self.stride, n_copies=self.n_copies, x=self.dx,
+                    y=self.dy, n_rows=self.rows, units=self.units, batch=self.batch,
+                    variant=self.variant, q2_offset=self.up_off, x16=self.dx16)
+
     def kernel(self) -> str:
         if self.kind == "q4k":
             return self.pkg.q4k_matvec_kernel_name(self.rows, self.units, self.variant)
@@ -300,7 +310,7 @@ def main() -> int:
                          "f16 matmul; both timed)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--variant", default="",
-                    help="matvec: rows_per_wave,waves,prefetch[,nontemporal]; "
+                    help="matvec: rows_per_wave,waves,prefetch[,nontemporal[,family,sb_per_lane]]; "
                          "c5: kind,waves,col_tiles,prefetch")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run device-to-device copies of the weight size (counter calibration)")
@@ -328,23 +338,45 @@ def main() -> int:
         print(json.dumps({"error": "parity failure", "report": par}), file=sys.stderr)
         return 1
 
-    # Timed region: K back-to-back calls launched from the host on the context
-    # stream, bracketed by device synchronisation and HIP events recorded on
-    # that same stream (the reported value).  The same K calls are then
-    # captured once into a HIP graph and replayed, for comparison.
+    # Timed region (the reported value): K back-to-back calls of the operation
+    # launched by the library's own loop (axh_bench_loop) on the context
+    # stream through the public entry point, after W untimed calls, with HIP
+    # events on that stream before the first call and after each of 10 groups
+    # of K / 10 calls (K calls in groups of one when K is not a multiple of
+    # 10); device synchronisation on both sides.  The groups give p10/p50/p90.
+    # The same K calls launched from this Python loop through ctypes, and
+    # replayed from one captured HIP graph, are reported next to it.
+    groups, per_group = (10, args.steps // 10) if args.steps % 10 == 0 else (args.steps, 1)
+    # Pre-warm, untimed: the same calls for at least 100 ms, so the clocks have
+    # ramped up under load (a few warmup calls are a fraction of a millisecond,
+    # and the first group of a cold start runs ~10 % slower).
+    prewarm_ms, n = 0.0, 20
+    while prewarm_ms < 100.0 and n <= (1 << 20):
+        prewarm_ms += sum(ctx.bench_loop(**case.bench_op(), warmup=0, groups=1,
+                                         calls_per_group=n))
+        n *= 2
+    ctx.device_synchronize()
+    group_ms = ctx.bench_loop(**case.bench_op(), warmup=args.warmup, groups=groups,
+                              calls_per_group=per_group)
+    ctx.device_synchronize()
+    total_ms = sum(group_ms)
+    us_per_call = total_ms * 1000.0 / args.steps
+    t = us_per_call * 1e-6
+    per_call = sorted(g * 1000.0 / per_group for g in group_ms)
+    pct = {p: round(per_call[min(len(per_call) - 1, int(p / 100 * len(per_call)))], 3)
+           for p in (10, 50, 90)}
+
+    ev0, ev1 = ctx.event(), ctx.event()
     for i in range(args.warmup):
         case.launch(i)
     ctx.device_synchronize()
-    ev0, ev1 = ctx.event(), ctx.event()
     ev0.record()
     for i in range(args.steps):
         case.launch(i)
     ev1.record()
     ev1.synchronize()
     ctx.device_synchronize()
-    total_ms = ev0.elapsed_ms(ev1)
-    us_per_call = total_ms * 1000.0 / args.steps
-    t = us_per_call * 1e-6
+    us_python = ev0.elapsed_ms(ev1) * 1000.0 / args.steps
 
     graph = ctx.capture(lambda: [case.launch(i) for i in range(args.steps)])
     graph.launch()  # warm replay
@@ -357,56 +389,33 @@ def main() -> int:
     us_graph = ev0.elapsed_ms(ev1) * 1000.0 / args.steps
     graph.close()
 
-    # Distribution: the same back-to-back stream cut by events into at least
-    # 10 groups of max(1, steps // 10) calls (an event between every call
-    # would add its own gap), so p10/p50/p90 are distinct at any step count.
-    group = max(1, args.steps // 10)
-    n_groups = max(10, args.steps // group)
-    evs = [ctx.event() for _ in range(n_groups + 1)]
-    evs[0].record()
-    for g in range(n_groups):
-        for i in range(group):
-            case.launch(g * group + i)
-        evs[g + 1].record()
-    evs[-1].synchronize()
-    per_call = sorted(evs[g].elapsed_ms(evs[g + 1]) * 1000.0 / group for g in range(n_groups))
-    pct = {p: round(per_call[min(len(per_call) - 1, int(p / 100 * len(per_call)))], 3)
-           for p in (10, 50, 90)}
     # The floor of the launch-per-call protocol on this box, for matvec
     # workloads: the same number of bytes read from the same rotated copies by
     # a kernel of the same launch shape that only reads (one store per wave),
-    # and an empty kernel of that shape, both launched back to back like the
-    # timed calls.
+    # and an empty kernel of that shape, launched by the same loop.
     floor = None
     if kind != "matmul":
         words = 8 * ctx.cu_count()
         fout = ctx.alloc(words * 4)
         nb = case.weight_bytes // 16 * 16
 
-        def floor_us(fn):
-            for i in range(args.warmup):
-                fn(i)
-            ctx.device_synchronize()
-            ev0.record()
-            for i in range(args.steps):
-                fn(i)
-            ev1.record()
-            ev1.synchronize()
-            return ev0.elapsed_ms(ev1) * 1000.0 / args.steps
+        def floor_us(op):
+            ms = ctx.bench_loop(op, case.wbuf, case.stride, case.n_copies, None, fout,
+                                units=nb // 16, batch=words, warmup=args.warmup, groups=groups,
+                                calls_per_group=per_group)
+            return sum(ms) * 1000.0 / args.steps
 
-        read_us = floor_us(lambda i: ctx.read_floor(case.wbuf.ptr + (i % case.n_copies) * case.stride,
-                                                    nb, fout, words))
-        empty_us = floor_us(lambda i: ctx.launch_empty(fout, words))
+        read_us = floor_us("read_floor")
+        empty_us = floor_us("launch_empty")
         fout.close()
         floor = {
             "read_same_bytes_us": round(read_us, 3),
             "read_same_bytes_GBps": round(nb / read_us / 1e3, 1),
             "empty_launch_us": round(empty_us, 3),
             "kernel_vs_read_floor": round(read_us / us_per_call, 4),
-            "what": "back-to-back launches of the matvec's launch shape (one 512-thread "
-                    "workgroup per CU) that only read the same bytes from the same rotated "
-                    "copies (one store per wave), and that do nothing (the empty launch is "
-                    "bounded by this host path's launch rate)",
+            "what": "back-to-back launches, by the same loop, of the matvec's launch shape "
+                    "(one 512-thread workgroup per CU) that only read the same bytes from the "
+                    "same rotated copies (one store per wave), and that do nothing",
         }
     kernel = case.kernel()
     shape = (("2x" if kind == "gate_up" else "") + f"{case.rows}x{case.cols}"
@@ -453,10 +462,13 @@ def main() -> int:
         "warmup": args.warmup,
         "ms_per_step": round(total_ms / args.steps, 6),
         "us_per_call": round(us_per_call, 3),
-        "timing": f"{args.steps} back-to-back calls launched from the host; the same calls "
-                  f"replayed from one HIP graph: {us_graph:.3f} us/call",
+        "timing": f"{args.steps} back-to-back calls launched by the library's loop "
+                  f"(axh_bench_loop, {groups} event-timed groups) after an untimed pre-warm of "
+                  f"{prewarm_ms:.0f} ms and {args.warmup} warmup calls; the same calls launched "
+                  f"from Python through ctypes: {us_python:.3f} us/call; replayed from one "
+                  f"HIP graph: {us_graph:.3f} us/call",
         "us_per_call_p10_p50_p90": [pct[10], pct[50], pct[90]],
-        "distribution": f"{n_groups} event-timed groups of {group} back-to-back calls",
+        "distribution": f"{groups} event-timed groups of {per_group} back-to-back calls",
         "kernel": kernel,
         "pct_of_peak": round(100.0 * value / peak, 2),
         "higher_is_better": True,

@@ -61,7 +61,12 @@ const char *axh_status_name(int status);
  * Replaces VulkanContextOptions / VulkanContext::new_with_options
  * (crates/axc-runtime/src/context.rs:76-109,175). */
 typedef struct axh_context_options {
-    const char *code_object_cache_dir; /* pipeline_cache_path; NULL = none         */
+    /* pipeline_cache_path: directory of the tuned-winner table
+     * (axh_winners.json, see axh_tune.h), loaded at creation and consulted by
+     * calls that pass no variant; NULL, or AXH_DISABLE_CODE_OBJECT_CACHE=1
+     * (as AXC_DISABLE_PIPELINE_CACHE, pipeline_cache.rs:153-170), = none.
+     * Kernels are embedded code objects, so nothing else is cached. */
+    const char *code_object_cache_dir;
     int32_t device_index;              /* physical_device_index; -1 = AXH_DEVICE_INDEX env or 0 */
     uint64_t fence_timeout_ms;         /* 0 = AXH_FENCE_TIMEOUT_MS env or 10000 (dispatch.rs:26) */
 } axh_context_options;
@@ -162,20 +167,44 @@ void axh_event_destroy(axh_event *ev);
 
 /* ---- Q4 dequant-matvec operations ------------------------------------------
  * Strategy holes of the matvec kernels (the reference's @strategy surface,
- * crates/axc-hir/src/hir.rs:62-68): rows_per_wave, waves_per_workgroup,
- * prefetch (superblock iterations loaded ahead: 1 issues the next iteration's
- * loads before the current one is computed and stages x chunk by chunk; P >= 2
- * keeps P iterations loaded and refills a slot after computing it) and
- * nontemporal (weight-load cache policy).  Zero fields pick the defaults for
- * the shape; with no variant, 32-32768 rows of 1-128 superblocks (and up to
- * 65536 rows of at most 16) take a one-pass kernel (one workgroup per 16
- * rows; from 6144 rows of at most 32 superblocks x is staged whole first),
- * which is not a hole assignment. */
+ * crates/axc-hir/src/hir.rs:62-68).  `family` picks the Q4_K kernel family
+ * (AXH_Q4K_FAMILY_*); the other holes are that family's:
+ *   persistent: rows_per_wave, waves_per_workgroup, prefetch (superblock
+ *     iterations loaded ahead: 1 issues the next iteration's loads before the
+ *     current one is computed and stages x chunk by chunk; P >= 2 keeps P
+ *     iterations loaded and refills a slot after computing it) and nontemporal
+ *     (weight-load cache policy);
+ *   one pass (x staged chunk by chunk, or whole): sb_per_lane, the superblocks
+ *     a lane walks per row (the kernel's trip count, eight superblocks per
+ *     half-wave per step: from ceil(sb_per_row / 8) to 16);
+ *   one workgroup: rows_per_wave = rows per workgroup (1, 2 or 4, at least
+ *     n_rows);
+ *   tiled: rows_per_wave, waves_per_workgroup, prefetch.
+ * Zero fields take the shape's choice.  family = 0 selects the persistent
+ * family when any of its four holes is set, else the default family for the
+ * shape: one workgroup for 1-4 long rows, split-K or column slices for fewer
+ * than 32 rows, one pass for 32-32768 rows of 1-128 superblocks (and up to
+ * 65536 rows of at most 16; x staged whole from 6144 rows of at most 32
+ * superblocks), persistent beyond, tiled for rows of more than 128
+ * superblocks.  Every default is a hole assignment.  The Q4_0, Q5_K, Q6_K and
+ * gate/up operations take the persistent holes only (family = sb_per_lane = 0). */
+enum {
+    AXH_Q4K_FAMILY_DEFAULT = 0,
+    AXH_Q4K_FAMILY_PERSISTENT = 1, /* axh_q4k_matvec_flat_r*_w*_p*_n*[_x2]            */
+    AXH_Q4K_FAMILY_ONE_PASS = 2,   /* axh_q4k_matvec_one_i{sb_per_lane}              */
+    AXH_Q4K_FAMILY_ONE_PASS_X = 3, /* axh_q4k_matvec_onex_i{sb_per_lane}: x whole    */
+    AXH_Q4K_FAMILY_WORKGROUP = 4,  /* axh_q4k_matvec_wg_w8_x2_r{1,2,4}: 1-4 rows     */
+    AXH_Q4K_FAMILY_SPLIT_K = 5,    /* axh_q4k_matvec_sk_s16: <= 32 rows, <= 256 SB   */
+    AXH_Q4K_FAMILY_COLUMNS = 6,    /* axh_q4k_matvec_cols_r4_w*: rows of <= 128 SB   */
+    AXH_Q4K_FAMILY_TILED = 7       /* axh_q4k_matvec_tiled_r*_w*_p*: any row length  */
+};
 typedef struct axh_q4_variant {
     uint32_t rows_per_wave;
     uint32_t waves_per_workgroup;
     uint32_t prefetch;
     uint32_t nontemporal; /* 1: weight loads bypass cache allocation; 2: force normal loads */
+    uint32_t family;      /* AXH_Q4K_FAMILY_* */
+    uint32_t sb_per_lane; /* one-pass families: superblocks a lane walks per row */
 } axh_q4_variant;
 
 /* y[r] = dot(row r of Q4_K_M matrix q, x) for r < n_rows, where each row is
@@ -200,6 +229,11 @@ axh_status axh_q4k_matvec(axh_context *ctx, const void *q, const float *x, float
  * q and x 16-byte aligned. */
 axh_status axh_q4k_matvec_noalloc(axh_context *ctx, const void *q, const float *x, float *y,
                                   uint32_t n_rows, uint32_t sb_per_row, void *stream);
+/* The hole assignment (family and that family's holes, no zero left to the
+ * shape) that axh_q4k_matvec uses for this shape when given no variant:
+ * passing it as the variant launches the same kernel.  No device work. */
+axh_status axh_q4k_matvec_default_variant(uint32_t n_rows, uint32_t sb_per_row,
+                                         axh_q4_variant *out);
 /* Name of the kernel axh_q4k_matvec launches for this shape and variant (the
  * entry point profilers report), NUL-terminated into buf[cap].  No device
  * work.  Counterpart of the kernel name the reference's BenchFn receives in
@@ -367,6 +401,37 @@ axh_status axh_q4k_matmul_kernel_name(uint32_t n_rows, uint32_t sb_per_row, uint
                                       size_t cap);
 uint32_t axh_q4k_matmul_variant_count(void);
 axh_status axh_q4k_matmul_variant_at(uint32_t i, axh_q4_matmul_variant *out);
+
+/* ---- measurement loop ------------------------------------------------------
+ * `groups` x `calls_per_group` back-to-back calls of one operation, launched
+ * by this library's own loop on the context stream through the public entry
+ * points above (each call a full dispatch: validation, kernel choice, one
+ * kernel launch), after `warmup` untimed calls.  Call i reads the weights at
+ * q + (i % n_copies) * q_stride.  A HIP event is recorded before the first
+ * timed call and after every group; group_ms[g] receives group g's time.  The
+ * bench's counterpart of the reference's compiled benchmark loops
+ * (crates/axc-driver/benches/dispatch_q4km.rs:101-124): no interpreter
+ * between launches.  No counterpart in the reference's C surface. */
+enum {
+    AXH_BENCH_Q4K_MATVEC = 1, AXH_BENCH_Q4_0_MATVEC = 2, AXH_BENCH_Q5K_MATVEC = 3,
+    AXH_BENCH_Q6K_MATVEC = 4, AXH_BENCH_Q4K_GATE_UP = 5, AXH_BENCH_Q4K_MATMUL_F16 = 6,
+    AXH_BENCH_Q4K_MATMUL_F32 = 7, AXH_BENCH_READ_FLOOR = 8, AXH_BENCH_LAUNCH_EMPTY = 9
+};
+typedef struct axh_bench_op {
+    uint32_t op;                   /* AXH_BENCH_* */
+    const void *q;                 /* first weight copy */
+    uint64_t q_stride;             /* bytes between copies */
+    uint32_t n_copies;             /* >= 1 */
+    uint64_t q2_offset;            /* gate/up: the up matrix at q + q2_offset in a copy */
+    const void *x;                 /* activations (f32, or f16 for MATMUL_F16) */
+    void *x16;                     /* MATMUL_F32: the f16 staging buffer */
+    void *y;                       /* output; READ_FLOOR / LAUNCH_EMPTY: the out words */
+    uint32_t n_rows, units, batch; /* READ_FLOOR: units = bytes / 16; y holds batch words */
+    const axh_q4_variant *variant;
+    const axh_q4_matmul_variant *matmul_variant;
+} axh_bench_op;
+axh_status axh_bench_loop(axh_context *ctx, const axh_bench_op *op, uint32_t warmup,
+                          uint32_t groups, uint32_t calls_per_group, float *group_ms);
 
 /* The built-in code object holding every kernel above, for callers that drive
  * the generic prepare/dispatch API (e.g. the reference-contract kernels

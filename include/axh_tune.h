@@ -100,15 +100,72 @@ axh_status axh_grid_search(const axh_strategy_hole *holes, uint32_t n_holes,
                            axh_bench_fn bench, void *user, axh_variant_result *results,
                            uint64_t capacity, axh_grid_search_result *out);
 
-/* Timed sweep of the compiled Q4_K matvec variants on resident buffers:
- * each variant is checked against the default variant's output (relative
- * 1e-3 norm-wise, or bit-exact when tol == 0) and timed over `samples`
- * back-to-back calls with HIP events; the fastest passing variant is
- * written to *best.  A wrapper of axh_grid_search whose holes are
- * rows_per_wave, waves_per_workgroup, prefetch and nontemporal. */
+/* ---- Tuned-winner table ---------------------------------------------------
+ * The persistent artefact of a search, one hole assignment per (op, n_rows,
+ * units): the counterpart of the reference's strategy sidecar
+ * (crates/axc-driver/src/optimize.rs:103-128) and, as a file a context loads
+ * at creation, of its pipeline cache (crates/axc-runtime/src/pipeline_cache.rs).
+ * JSON, schema "axh-winners-1".  A missing file loads as an empty table; an
+ * unreadable or malformed one is AXH_ERR_CODE_OBJECT_CACHE_LOAD
+ * (PipelineCacheLoadFailed).  Saving is atomic (temporary file + rename).
+ * A table is not thread-safe; a context guards its own. */
+typedef struct axh_winner_table axh_winner_table;
+axh_winner_table *axh_winners_new(void);
+void axh_winners_free(axh_winner_table *t);
+uint64_t axh_winners_count(const axh_winner_table *t);
+axh_status axh_winners_load(const char *path, axh_winner_table **out);
+axh_status axh_winners_save(const axh_winner_table *t, const char *path);
+axh_status axh_winners_put(axh_winner_table *t, const char *op, uint32_t n_rows, uint32_t units,
+                           const axh_q4_variant *v, uint64_t median_ns);
+/* *found = 1 and the entry, or *found = 0. */
+axh_status axh_winners_get(const axh_winner_table *t, const char *op, uint32_t n_rows,
+                           uint32_t units, uint32_t *found, axh_q4_variant *v,
+                           uint64_t *median_ns);
+
+/* The context's table (owned by the context).  axh_context_create loads it
+ * from <code_object_cache_dir>/axh_winners.json unless the option is NULL or
+ * AXH_DISABLE_CODE_OBJECT_CACHE=1; a file that fails to load is reported on
+ * stderr and the context starts with an empty table (as the reference treats
+ * its pipeline cache, pipeline_cache.rs:45-100).  axh_q4k_matvec called with
+ * no variant uses the table's "q4k_matvec" entry for its shape, if any. */
+axh_status axh_context_winner_put(axh_context *ctx, const char *op, uint32_t n_rows,
+                                  uint32_t units, const axh_q4_variant *v, uint64_t median_ns);
+axh_status axh_context_winner_get(axh_context *ctx, const char *op, uint32_t n_rows,
+                                  uint32_t units, uint32_t *found, axh_q4_variant *v,
+                                  uint64_t *median_ns);
+/* Writes the context's table to its file (no-op without one). */
+axh_status axh_context_winners_save(axh_context *ctx);
+/* Path of the context's table file, "" when it has none. */
+const char *axh_context_winners_path(const axh_context *ctx);
+/* The kernel axh_q4k_matvec launches on this context for the shape and
+ * variant (a NULL variant consults the context's table). */
+axh_status axh_context_q4k_matvec_kernel_name(axh_context *ctx, uint32_t n_rows,
+                                              uint32_t sb_per_row, const axh_q4_variant *variant,
+                                              char *buf, size_t cap);
+
+/* ---- Q4_K matvec autotuner ---------------------------------------------------
+ * Grid search over the whole Q4_K matvec kernel space on resident buffers,
+ * one axh_grid_search per kernel family that takes the shape (family plus that
+ * family's holes; every default is among the assignments).  Each variant runs
+ * once and its output is judged by axh_check_q4k_matvec (f64 accumulation of
+ * the reference's dequantised weights, relative tolerance `tol`, 1e-3 when 0)
+ * on host copies of q and x, then it is timed over `samples` groups of 20
+ * back-to-back calls with HIP events.  The fastest accepted variant is stored
+ * in the context's table (and its file, if any). */
+typedef struct axh_autotune_report {
+    axh_q4_variant best;          /* winner */
+    uint64_t best_median_ns;      /* its median per call */
+    axh_q4_variant dflt;          /* the shape's default assignment */
+    uint64_t default_median_ns;   /* its median in the same sweep */
+    uint32_t variants;            /* assignments enumerated over all families */
+    uint32_t accepted;            /* passed the checker and timed */
+    uint32_t rejected;            /* failed the checker */
+    uint32_t failed;              /* not compiled, not valid for the shape, or launch error */
+    char best_kernel[64];         /* entry point of the winner */
+} axh_autotune_report;
 axh_status axh_q4k_matvec_autotune(axh_context *ctx, const void *q, const float *x, float *y,
                                    uint32_t n_rows, uint32_t sb_per_row, uint32_t samples,
-                                   double tol, axh_q4_variant *best, uint64_t *best_median_ns);
+                                   double tol, axh_autotune_report *out);
 
 #ifdef __cplusplus
 }

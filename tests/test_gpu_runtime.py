@@ -161,29 +161,6 @@ def test_concurrent_dispatch_on_two_handles(ctx, axc):
     h2.release()
 
 
-def test_autotune_picks_a_compiled_variant(ctx, axc):
-    import importlib
-    tune = importlib.import_module("axiom_compute_amd.tune")
-    rows, sb = 2048, 16
-    _say("autotune 2048x4096")
-    q = O.gen_q4k_weights(61, rows * sb)
-    x = O.gen_normal_f32(62, sb * 256)
-    dq, dx, dy = ctx.alloc(q.nbytes), ctx.alloc(x.nbytes), ctx.alloc(rows * 4)
-    ctx.upload(dq, q)
-    ctx.upload(dx, x)
-    v, ns = tune.q4k_matvec_autotune(ctx, dq, dx, dy, rows, sb, samples=3)
-    assert ns > 0
-    assert v in axc.compiled_variants("q4k")
-    ctx.q4k_matvec(dq, dx, dy, rows, sb, v)
-    ctx.synchronize()
-    y = np.frombuffer(ctx.download(dy, rows * 4), dtype=np.float32)
-    ref = O.q4k_matvec(q, x, rows, sb)
-    yf, ad = O.q4k_matvec_f64(q, x, rows, sb)
-    assert O.matvec_tolerance_report(y, ref, yf, ad, sb * 256)["ok"]
-    for b in (dq, dx, dy):
-        b.close()
-
-
 def test_events_time_launches_on_the_context_stream(ctx, axc):
     h = ctx.prepare_kernel(axc.builtin_code_object(),
                            axc.BindingPlan([axc.axh.ACCESS_READ_WRITE], 4, (64, 1, 1)), 4, "axh_spin")

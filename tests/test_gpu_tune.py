@@ -1,0 +1,164 @@
+"""The Q4_K matvec autotuner over the whole kernel space and the tuned-winner
+table on the GPU (marked `gpu`).
+
+The search is the reference's grid search (crates/axc-optimize/src/
+grid_search.rs:158-283) with every kernel family as a hole assignment and the
+verdict of the f64 host checker (crates/axc-driver/src/mcp/tools/
+bench_variant.rs:395-400 has none for Q4); the winner is persisted like the
+reference's strategy sidecar (crates/axc-driver/src/optimize.rs:103-128).
+"""
+from __future__ import annotations
+
+import importlib
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def tune(axc):
+    return importlib.import_module("axiom_compute_amd.tune")
+
+
+def _dev(ctx, arr):
+    b = ctx.alloc(arr.nbytes)
+    ctx.upload(b, arr)
+    return b
+
+
+def _median_us(ctx, fn, calls=50, rounds=7):
+    ev0, ev1 = ctx.event(), ctx.event()
+    out = []
+    for _ in range(rounds):
+        for _ in range(5):
+            fn()
+        ctx.device_synchronize()
+        ev0.record()
+        for _ in range(calls):
+            fn()
+        ev1.record()
+        ev1.synchronize()
+        out.append(ev0.elapsed_ms(ev1) * 1000.0 / calls)
+    return sorted(out)[len(out) // 2]
+
+
+def test_grid_search_over_every_family_at_c4(axc, tune):
+    """4096 x 14336: the search spans every family that
+    takes the shape, accepts only checker-approved variants, and its winner,
+    timed again afterwards against the default, is within 2 % of it."""
+    rows, sb = 4096, 56
+    _say(f"autotune {rows}x{sb * 256} over every family")
+    c = axc.HipContext.new()  # its own context: the winner goes into this one's table
+    q = O.gen_q4k_weights(20241, rows * sb)
+    x = O.gen_normal_f32(20242, sb * 256, 0.5)
+    dq, dx, dy = _dev(c, q), _dev(c, x), c.alloc(rows * 4)
+    rep = tune.q4k_matvec_autotune(c, dq, dx, dy, rows, sb, samples=5)
+    _say(f"autotune report: {rep}")
+    assert rep.default == axc.q4k_matvec_default_variant(rows, sb)
+    assert rep.default_median_ns > 0  # the default was among the accepted variants
+    assert rep.accepted >= 15 and rep.rejected == 0
+    assert rep.variants == rep.accepted + rep.rejected + rep.failed
+    assert rep.best_kernel == axc.q4k_matvec_kernel_name(rows, sb, rep.best)
+    assert rep.best_median_ns <= rep.default_median_ns
+    fams = {v.family for v in [rep.best, rep.default]}
+    assert fams <= set(range(1, 8))
+    # stored in the context's table: a call without a variant now runs the winner
+    assert tune.context_winner_get(c, "q4k_matvec", rows, sb)[0] == rep.best
+    assert tune.context_q4k_matvec_kernel_name(c, rows, sb) == rep.best_kernel
+    assert tune.context_winners_path(c) == ""  # no cache directory: in memory only
+    # the winner's output passes the oracle's tolerance
+    c.q4k_matvec(dq, dx, dy, rows, sb, rep.best)
+    c.synchronize()
+    y = np.frombuffer(c.download(dy, rows * 4), dtype=np.float32)
+    ref = O.q4k_matvec(q, x, rows, sb)
+    yf, ad = O.q4k_matvec_f64(q, x, rows, sb)
+    assert O.matvec_tolerance_report(y, ref, yf, ad, sb * 256)["ok"]
+    # timed again, independently of the search: no slower than the default by > 2 %
+    t_best = _median_us(c, lambda: c.q4k_matvec(dq, dx, dy, rows, sb, rep.best))
+    t_dflt = _median_us(c, lambda: c.q4k_matvec(dq, dx, dy, rows, sb, rep.default))
+    _say(f"re-timed: winner {rep.best_kernel} {t_best:.3f} us, default {t_dflt:.3f} us")
+    assert t_best <= 1.02 * t_dflt
+    for b in (dq, dx, dy):
+        b.close()
+    c.close()
+
+
+def test_autotune_small_shape_every_family(axc, tune):
+    """3 rows of 100 superblocks: one workgroup, split-K, columns, persistent
+    and tiled families all take the shape and are all searched."""
+    rows, sb = 3, 100
+    c = axc.HipContext.new()
+    q = O.gen_q4k_weights(71, rows * sb)
+    x = O.gen_normal_f32(72, sb * 256)
+    dq, dx, dy = _dev(c, q), _dev(c, x), c.alloc(rows * 4)
+    rep = tune.q4k_matvec_autotune(c, dq, dx, dy, rows, sb, samples=3)
+    _say(f"autotune 3x100 report: {rep}")
+    assert rep.rejected == 0 and rep.default_median_ns > 0
+    assert rep.accepted >= 8  # wg r4, split-K, columns, one pass x2, tiled, persistent ...
+    for b in (dq, dx, dy):
+        b.close()
+    c.close()
+
+
+def test_dispatch_uses_the_stored_winner(axc, tune, tmp_path):
+    """A winner stored for a shape is used by calls that pass no variant, is
+    saved under the cache directory and loaded by the next context; the
+    AXH_DISABLE_CODE_OBJECT_CACHE=1 override and a corrupt file both leave
+    the default in place."""
+    rows, sb = 1000, 16
+    dflt = axc.q4k_matvec_kernel_name(rows, sb)
+    won = axc.Variant(2, 4, 1, 2, axc.FAMILY_PERSISTENT)
+    won_name = axc.q4k_matvec_kernel_name(rows, sb, won)
+    assert won_name != dflt
+    opts = axc.HipContextOptions(code_object_cache_dir=str(tmp_path / "cache"))
+    q = O.gen_q4k_weights(91, rows * sb)
+    x = O.gen_normal_f32(92, sb * 256)
+    ref = O.q4k_matvec(q, x, rows, sb)
+    yf, ad = O.q4k_matvec_f64(q, x, rows, sb)
+
+    c = axc.HipContext.new_with_options(opts)
+    assert tune.context_q4k_matvec_kernel_name(c, rows, sb) == dflt
+    tune.context_winner_put(c, "q4k_matvec", rows, sb, won, 1234)
+    assert tune.context_q4k_matvec_kernel_name(c, rows, sb) == won_name
+    dq, dx, dy = _dev(c, q), _dev(c, x), c.alloc(rows * 4)
+    c.q4k_matvec(dq, dx, dy, rows, sb)  # no variant: the stored winner runs
+    c.synchronize()
+    y = np.frombuffer(c.download(dy, rows * 4), dtype=np.float32)
+    assert O.matvec_tolerance_report(y, ref, yf, ad, sb * 256)["ok"]
+    tune.context_winners_save(c)
+    path = tune.context_winners_path(c)
+    assert path.endswith("cache/axh_winners.json") and os.path.exists(path)
+    for b in (dq, dx, dy):
+        b.close()
+    c.close()
+
+    c2 = axc.HipContext.new_with_options(opts)  # loads the saved table
+    assert tune.context_winner_get(c2, "q4k_matvec", rows, sb) == (won, 1234)
+    assert tune.context_q4k_matvec_kernel_name(c2, rows, sb) == won_name
+    c2.close()
+
+    os.environ["AXH_DISABLE_CODE_OBJECT_CACHE"] = "1"
+    try:
+        c3 = axc.HipContext.new_with_options(opts)
+        assert tune.context_q4k_matvec_kernel_name(c3, rows, sb) == dflt
+        assert tune.context_winners_path(c3) == ""
+        c3.close()
+    finally:
+        del os.environ["AXH_DISABLE_CODE_OBJECT_CACHE"]
+
+    with open(path, "w") as f:
+        f.write('{"schema": "axh-winners-1", "entries": [')  # truncated
+    c4 = axc.HipContext.new_with_options(opts)  # non-fatal: empty table, default kernel
+    assert tune.context_q4k_matvec_kernel_name(c4, rows, sb) == dflt
+    c4.close()
