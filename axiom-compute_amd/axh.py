@@ -118,7 +118,7 @@ class _BenchOp(ctypes.Structure):
 
 
 BENCH_OPS = {"q4k": 1, "q4_0": 2, "q5k": 3, "q6k": 4, "gate_up": 5, "matmul_f16": 6,
-             "matmul_f32": 7, "read_floor": 8, "launch_empty": 9}
+             "matmul_f32": 7, "read_floor": 8, "launch_empty": 9, "read_shape": 10}
 
 
 class _GgufTensorInfo(ctypes.Structure):
@@ -231,6 +231,7 @@ def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
         "axh_f16_widen": (st, [vp, vp, vp, u64, vp]),
         "axh_read_floor": (st, [vp, vp, u64, vp, u32, vp]),
         "axh_launch_empty": (st, [vp, vp, u32, vp]),
+        "axh_read_floor_shape": (st, [vp, vp, u64, u32, u32, u32, vp, u32, vp]),
         "axh_cu_count": (u32, [vp]),
         "axh_q4k_matvec_variant_count": (u32, []),
         "axh_q4k_matvec_variant_at": (st, [u32, c.POINTER(_Variant)]),
@@ -853,6 +854,12 @@ class HipContext:
         _check(self._lib.axh_bench_loop(self._raw, ctypes.byref(o), warmup, groups,
                                         calls_per_group, out))
         return [float(t) for t in out]
+
+    def read_floor_shape(self, q, nbytes: int, threads: int, loads: int, grid: int, out,
+                         out_words: int, stream=None) -> None:
+        """The read floor at another launch shape (measurement helper)."""
+        _check(self._lib.axh_read_floor_shape(self._raw, _ptr(q), nbytes, threads, loads, grid,
+                                              _ptr(out), out_words, _stream(stream)))
 
     def launch_empty(self, out, out_words: int, stream=None) -> None:
         """An empty kernel with the matvec's launch shape (measurement helper)."""

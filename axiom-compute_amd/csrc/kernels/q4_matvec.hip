@@ -2001,25 +2001,51 @@ extern "C" __global__ void __launch_bounds__(256)
 // workgroup per CU, 16-byte buffer loads, four in flight per lane) and
 // writes, per wave, the XOR of every dword it read to out[wave], so the loads
 // cannot be dropped and each wave ends with one store, as a matvec wave does.
-extern "C" __global__ void __launch_bounds__(512) axh_read_floor(const uint8_t *__restrict__ q,
-                                                                 uint32_t *__restrict__ out,
-                                                                 AXH_COUNT_ARGS) { AXH_COUNT_UNPACK;
-  const uint32_t n = a.n_units, nt = gridDim.x * 512u;
-  const uint32_t gtid = blockIdx.x * 512u + threadIdx.x;
+// T threads per workgroup, U loads of 16 bytes in flight per lane, a
+// grid-stride walk over the whole buffer (consecutive lanes read consecutive
+// pieces); the grid is the caller's.
+template <int T, int U>
+__device__ __forceinline__ void read_floor(const uint8_t *__restrict__ q, uint32_t *__restrict__ out,
+                                           uint32_t n) {
+  const uint32_t nt = gridDim.x * (uint32_t)T;
+  const uint32_t gtid = blockIdx.x * (uint32_t)T + threadIdx.x;
   const __amdgpu_buffer_rsrc_t r = make_rsrc(q, n * 16u);
   uint32_t acc = 0;
-  for (uint32_t i = gtid; i < n; i += 4u * nt) {
-    uint4 v[4];
+  for (uint32_t i = gtid; i < n; i += (uint32_t)U * nt) {
+    uint4 v[U];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = buf_load16<false>(r, (i + (uint32_t)u * nt) * 16u);
+    for (int u = 0; u < U; ++u) v[u] = buf_load16<false>(r, (i + (uint32_t)u * nt) * 16u);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
   }
   for (int off = 32; off >= 1; off >>= 1) // XOR across the wave
-
     acc ^= (uint32_t)__shfl_xor((int)acc, off, 64);
   if ((threadIdx.x & 63u) == 0u) out[gtid >> 6] = acc;
 }
+
+extern "C" __global__ void __launch_bounds__(512) axh_read_floor(const uint8_t *__restrict__ q,
+                                                                 uint32_t *__restrict__ out,
+                                                                 AXH_COUNT_ARGS) { AXH_COUNT_UNPACK;
+  read_floor<512, 4>(q, out, a.n_units);
+}
+
+// The same read at other launch shapes (axh_read_floor_shape: the sweep for
+// the best single-launch read of a buffer).
+#define AXH_READ_FLOOR_SHAPE(T, U)                                                               \
+  extern "C" __global__ void __launch_bounds__(T) axh_read_floor_t##T##_u##U(                    \
+      const uint8_t *__restrict__ q, uint32_t *__restrict__ out, AXH_COUNT_ARGS) {               \
+    AXH_COUNT_UNPACK;                                                                            \
+    read_floor<T, U>(q, out, a.n_units);                                                         \
+  }
+AXH_READ_FLOOR_SHAPE(256, 2)
+AXH_READ_FLOOR_SHAPE(256, 4)
+AXH_READ_FLOOR_SHAPE(256, 8)
+AXH_READ_FLOOR_SHAPE(512, 2)
+AXH_READ_FLOOR_SHAPE(512, 4)
+AXH_READ_FLOOR_SHAPE(512, 8)
+AXH_READ_FLOOR_SHAPE(1024, 2)
+AXH_READ_FLOOR_SHAPE(1024, 4)
+AXH_READ_FLOOR_SHAPE(1024, 8)
 
 // The same launch shape doing nothing: the per-launch cost alone.
 extern "C" __global__ void __launch_bounds__(512) axh_launch_empty(const uint8_t *__restrict__ q,

@@ -1222,9 +1222,10 @@ static axh_status floor_launch(axh_context *ctx, const char *name, const void *q
   if (!ctx) return fail(AXH_ERR_INVALID_ARGUMENT, "ctx is NULL");
   if (!device_ptr_ok(out) || (pieces && !device_ptr_ok(q)))
     return fail(AXH_ERR_INVALID_ARGUMENT, "q and out must be device pointers");
-  if (((uintptr_t)q & 15u) || pieces > 0xFFFFFFFFull / 16u)
-    return fail(AXH_ERR_INVALID_ARGUMENT, "q must be 16-byte aligned and below 4 GiB");
   const uint32_t grid[3] = {ctx->core->cu_count, 1, 1};
+  // The kernel's 32-bit byte offsets reach (pieces + 4 * threads in the grid) * 16.
+  if (((uintptr_t)q & 15u) || pieces + 4ull * 512u * grid[0] > 0xFFFFFFFFull / 16u)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q must be 16-byte aligned and below 4 GiB");
   if (out_words < 8u * grid[0])
     return fail(AXH_ERR_INVALID_ARGUMENT, "out needs 8 words per compute unit");
   hipSetDevice(ctx->core->device);
@@ -1241,6 +1242,34 @@ axh_status axh_read_floor(axh_context *ctx, const void *q, uint64_t bytes, uint3
                           uint32_t out_words, void *stream) {
   if (bytes % 16u) return fail(AXH_ERR_INVALID_ARGUMENT, "bytes must be a multiple of 16");
   return floor_launch(ctx, "axh_read_floor", q, bytes / 16u, out, out_words, stream);
+}
+
+axh_status axh_read_floor_shape(axh_context *ctx, const void *q, uint64_t bytes, uint32_t threads,
+                                uint32_t loads, uint32_t grid, uint32_t *out, uint32_t out_words,
+                                void *stream) {
+  if (!ctx) return fail(AXH_ERR_INVALID_ARGUMENT, "ctx is NULL");
+  if ((threads != 256 && threads != 512 && threads != 1024) ||
+      (loads != 2 && loads != 4 && loads != 8) || grid == 0 || grid > 65536)
+    return fail(AXH_ERR_INVALID_ARGUMENT,
+                "read floor shapes: 256/512/1024 threads, 2/4/8 loads, 1..65536 workgroups");
+  // The kernel's 32-bit byte offsets reach (pieces + loads * threads in the grid) * 16.
+  if (bytes % 16u || bytes / 16u + (uint64_t)loads * threads * grid > 0xFFFFFFFFull / 16u)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "bytes must be a multiple of 16 below 4 GiB");
+  if (!device_ptr_ok(out) || (bytes && !device_ptr_ok(q)) || ((uintptr_t)q & 15u))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q (16-byte aligned) and out must be device pointers");
+  if ((uint64_t)out_words < (uint64_t)grid * threads / 64u)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "out needs one word per wave of the grid");
+  char name[48];
+  std::snprintf(name, sizeof(name), "axh_read_floor_t%u_u%u", threads, loads);
+  hipSetDevice(ctx->core->device);
+  axh_kernel *k = nullptr;
+  axh_status s = builtin_kernel(ctx, name, 2, sizeof(CountArgs), threads, &k);
+  if (s != AXH_OK) return s;
+  CountArgs a{(uint32_t)(bytes / 16u)};
+  const uint32_t g[3] = {grid, 1, 1};
+  void *bufs[2] = {const_cast<void *>(q), out};
+  s = launch_raw(k, g, bufs, 2, &a, sizeof(a), 0, pick_stream(ctx, stream));
+  return s == AXH_OK ? ok() : s;
 }
 
 axh_status axh_launch_empty(axh_context *ctx, uint32_t *out, uint32_t out_words, void *stream) {
@@ -1294,6 +1323,11 @@ static axh_status bench_call(axh_context *ctx, const axh_bench_op *o, uint32_t i
                           o->batch, nullptr);
   case AXH_BENCH_LAUNCH_EMPTY:
     return axh_launch_empty(ctx, static_cast<uint32_t *>(o->y), o->batch, nullptr);
+  case AXH_BENCH_READ_SHAPE:
+    if (!o->variant) return fail(AXH_ERR_INVALID_ARGUMENT, "read shape needs a variant");
+    return axh_read_floor_shape(ctx, q, (uint64_t)o->units * 16u, o->variant->waves_per_workgroup * 64u,
+                                o->variant->prefetch, o->n_rows, static_cast<uint32_t *>(o->y),
+                                o->batch, nullptr);
   default:
     return fail(AXH_ERR_INVALID_ARGUMENT, "unknown bench operation");
   }

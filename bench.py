@@ -92,6 +92,19 @@ def profiled_traffic(kernel: str, workload: str):
     return None, None
 
 
+def profiled_mfma_busy(kernel: str, workload: str):
+    """Fraction of the dispatch's cycles the MFMA units were busy, summed over
+    every SIMD (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs)), as
+    recorded by the counter summary under profiles/ (None if absent)."""
+    pat = re.compile(r"^mfma_busy kernel=(\S+) workload=(\S+) frac=([0-9.]+) source=(\S+)")
+    for f in sorted((ROOT / "profiles").glob("*.md")):
+        for ln in f.read_text().splitlines():
+            m = pat.match(ln.strip().strip("`"))
+            if m and m.group(1) == kernel and m.group(2) == workload:
+                return float(m.group(3)), f"profiles/{f.name}"
+    return None, None
+
+
 class Case:
     """One workload: device buffers, the launch of step i, parity, CPU baseline."""
 
@@ -408,14 +421,39 @@ def main() -> int:
         read_us = floor_us("read_floor")
         empty_us = floor_us("launch_empty")
         fout.close()
+        # The best single-launch read of the same bytes: the read kernel at
+        # every shape of 256/512/1024 threads, 2/4/8 16-byte loads in flight per
+        # lane and 256-2048 workgroups, launched by the same loop.
+        sweep = []
+        sout = ctx.alloc(2048 * 1024 // 64 * 4)
+        for threads in (256, 512, 1024):
+            for loads in (2, 4, 8):
+                for grid in (256, 512, 1024, 2048):
+                    ms = ctx.bench_loop("read_shape", case.wbuf, case.stride, case.n_copies, None,
+                                        sout, n_rows=grid, units=nb // 16,
+                                        batch=grid * threads // 64,
+                                        variant=pkg.Variant(0, threads // 64, loads),
+                                        warmup=args.warmup, groups=groups,
+                                        calls_per_group=per_group)
+                    sweep.append((sum(ms) * 1000.0 / args.steps, threads, loads, grid))
+        sout.close()
+        sweep.sort()
+        best_us, bt, bl, bg = sweep[0]
         floor = {
             "read_same_bytes_us": round(read_us, 3),
             "read_same_bytes_GBps": round(nb / read_us / 1e3, 1),
             "empty_launch_us": round(empty_us, 3),
             "kernel_vs_read_floor": round(read_us / us_per_call, 4),
+            "best_read_us": round(best_us, 3),
+            "best_read_GBps": round(nb / best_us / 1e3, 1),
+            "best_read_shape": f"axh_read_floor_t{bt}_u{bl}, {bg} workgroups",
+            "kernel_vs_best_read": round(best_us / us_per_call, 4),
+            "read_sweep_us": [[t_, l_, g_, round(u_, 3)] for u_, t_, l_, g_ in sweep],
             "what": "back-to-back launches, by the same loop, of the matvec's launch shape "
                     "(one 512-thread workgroup per CU) that only read the same bytes from the "
-                    "same rotated copies (one store per wave), and that do nothing",
+                    "same rotated copies (one store per wave), and that do nothing; "
+                    "best_read: the fastest of the read kernel's 36 launch shapes "
+                    "(read_sweep_us rows: threads, loads in flight per lane, workgroups, us)",
         }
     kernel = case.kernel()
     shape = (("2x" if kind == "gate_up" else "") + f"{case.rows}x{case.cols}"
@@ -503,6 +541,10 @@ def main() -> int:
         "cpu_baseline": cpu,
         "launch_floor": floor,
     }
+    if mfma_bound:
+        busy, busy_src = profiled_mfma_busy(kernel, shape)
+        out["roofline"]["mfma_busy"] = busy
+        out["roofline"]["mfma_busy_source"] = busy_src
     print(json.dumps(out), flush=True)
     case.close()
     ctx.close()

@@ -334,6 +334,13 @@ axh_status axh_f16_widen(axh_context *ctx, const uint16_t *h, float *f, uint64_t
 axh_status axh_read_floor(axh_context *ctx, const void *q, uint64_t bytes, uint32_t *out,
                           uint32_t out_words, void *stream);
 axh_status axh_launch_empty(axh_context *ctx, uint32_t *out, uint32_t out_words, void *stream);
+/* The same read at another launch shape: `grid` workgroups of `threads`
+ * (256, 512 or 1024) lanes with `loads` (2, 4 or 8) 16-byte loads in flight
+ * per lane, walking the buffer grid-stride; out holds one word per wave.
+ * For the sweep that finds the best single-launch read of a buffer. */
+axh_status axh_read_floor_shape(axh_context *ctx, const void *q, uint64_t bytes, uint32_t threads,
+                                uint32_t loads, uint32_t grid, uint32_t *out, uint32_t out_words,
+                                void *stream);
 uint32_t axh_cu_count(axh_context *ctx);
 /* binary32 -> binary16, round to nearest even, of n values (NaN stays NaN,
  * values beyond the f16 range become infinities): the activation cast that
@@ -415,7 +422,9 @@ axh_status axh_q4k_matmul_variant_at(uint32_t i, axh_q4_matmul_variant *out);
 enum {
     AXH_BENCH_Q4K_MATVEC = 1, AXH_BENCH_Q4_0_MATVEC = 2, AXH_BENCH_Q5K_MATVEC = 3,
     AXH_BENCH_Q6K_MATVEC = 4, AXH_BENCH_Q4K_GATE_UP = 5, AXH_BENCH_Q4K_MATMUL_F16 = 6,
-    AXH_BENCH_Q4K_MATMUL_F32 = 7, AXH_BENCH_READ_FLOOR = 8, AXH_BENCH_LAUNCH_EMPTY = 9
+    AXH_BENCH_Q4K_MATMUL_F32 = 7, AXH_BENCH_READ_FLOOR = 8, AXH_BENCH_LAUNCH_EMPTY = 9,
+    AXH_BENCH_READ_SHAPE = 10 /* axh_read_floor_shape: n_rows = workgroups, variant->
+                                 waves_per_workgroup = threads / 64, variant->prefetch = loads */
 };
 typedef struct axh_bench_op {
     uint32_t op;                   /* AXH_BENCH_* */

@@ -294,3 +294,30 @@ def test_read_floor_reads_every_byte(ctx, axc, nbytes):
         ctx.read_floor(dq, 16, dout, words - 1)  # out too small
     for b in (dq, dout):
         b.close()
+
+
+@pytest.mark.parametrize("threads", [256, 512, 1024])
+@pytest.mark.parametrize("loads", [2, 4, 8])
+def test_read_floor_shapes_read_every_byte(ctx, axc, threads, loads):
+    """Each launch shape of the read sweep reads exactly the bytes it is given."""
+    nbytes = (3 << 20) + 80
+    data = np.random.default_rng(threads + loads).integers(0, 2**32, nbytes // 4, dtype=np.uint32)
+    dq = ctx.alloc(nbytes)
+    ctx.upload(dq, data)
+    for grid in (1, 256, 2048):
+        words = grid * threads // 64
+        dout = ctx.alloc(words * 4)
+        ctx.read_floor_shape(dq, nbytes, threads, loads, grid, dout, words)
+        ctx.synchronize()
+        got = np.frombuffer(ctx.download(dout, words * 4), dtype=np.uint32)
+        assert int(np.bitwise_xor.reduce(got)) == int(np.bitwise_xor.reduce(data)), grid
+        with pytest.raises(axc.DispatchError):
+            ctx.read_floor_shape(dq, nbytes, threads, loads, grid, dout, words - 1)
+        dout.close()
+    with pytest.raises(axc.DispatchError):
+        ctx.read_floor_shape(dq, nbytes, 128, loads, 1, dq, 1 << 18)
+    with pytest.raises(axc.DispatchError):
+        ctx.read_floor_shape(dq, nbytes, threads, 3, 1, dq, 1 << 18)
+    with pytest.raises(axc.DispatchError):
+        ctx.read_floor_shape(dq, 1 << 32, threads, loads, 1, dq, 1 << 18)
+    dq.close()
