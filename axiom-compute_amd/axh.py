@@ -16,12 +16,14 @@ this module fails loudly when it has not been built; there is no fallback.
 from __future__ import annotations
 
 import ctypes
+import os
 from dataclasses import dataclass, field
 from pathlib import Path
 from typing import Iterable, Optional, Sequence
 
 _HERE = Path(__file__).resolve().parent
-LIB_PATH = _HERE / "libaxh.so"
+# AXH_LIBRARY selects another build of the library (e.g. the sanitizer build).
+LIB_PATH = Path(os.environ["AXH_LIBRARY"]) if os.environ.get("AXH_LIBRARY") else _HERE / "libaxh.so"
 HEADER_PATH = _HERE.parent / "include" / "axh.h"
 
 # status code -> reference DispatchError variant name (error.rs:27-195)

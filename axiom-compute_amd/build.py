@@ -7,6 +7,14 @@
 
 Every step runs on a machine without a GPU.  Outputs stay in the source
 tree (libaxh.so next to this file, intermediates in _build/).
+
+`python axiom-compute_amd/build.py --sanitize` also builds the host code
+(runtime, GGUF reader, checker, autotuner, winner table) and the oracle with
+AddressSanitizer and UndefinedBehaviorSanitizer into separate outputs,
+_build/san/libaxh.so and oracle/_san/liboracle.so, for the CPU test suite
+(AXH_LIBRARY / AXH_ORACLE_LIBRARY select them; the sanitizer runtimes are
+preloaded into the interpreter).  Device code is never built with a
+sanitizer.
 """
 from __future__ import annotations
 
@@ -37,6 +45,11 @@ KERNEL_FLAGS = ["-mllvm", "-amdgpu-kernarg-preload-count=16"]
 
 KERNELS = ["q4_matvec", "q4_matmul"]
 
+# Host-only sanitizer build (g++ lines only).
+SAN_FLAGS = ["-fsanitize=address,undefined", "-fno-omit-frame-pointer",
+             "-fno-sanitize-recover=undefined", "-g"]
+SAN_LIB = BUILD / "san" / "libaxh.so"
+
 
 def _run(cmd: list[str]) -> None:
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
@@ -59,7 +72,7 @@ def build_kernels() -> dict[str, Path]:
     return cos
 
 
-def build_runtime(cos: dict[str, Path]) -> Path:
+def build_runtime(cos: dict[str, Path], sanitize: bool = False) -> Path:
     rt = PKG / "csrc" / "runtime"
     embed_o = BUILD / "axh_embed.o"
     # The allocation-free entry point keeps its scratch in a __device__ array,
@@ -70,9 +83,12 @@ def build_runtime(cos: dict[str, Path]) -> Path:
     _run(["gcc", "-c", f'-DAXH_Q4_MATVEC_CO="{cos["q4_matvec"]}"',
           f'-DAXH_Q4_MATMUL_CO="{cos["q4_matmul"]}"', "-o", str(embed_o),
           str(rt / "axh_embed.S")])
-    tmp = LIB.with_suffix(".so.tmp")
+    out = SAN_LIB if sanitize else LIB
+    out.parent.mkdir(parents=True, exist_ok=True)
+    tmp = out.with_suffix(".so.tmp")
     _run([
         "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
+        *(SAN_FLAGS if sanitize else []),
         "-D__HIP_PLATFORM_AMD__", "-I", str(ROCM / "include"), "-I", str(ROOT / "include"),
         "-I", str(rt),
         str(rt / "axh_runtime.cpp"), str(rt / "axh_ops.cpp"), str(rt / "axh_gguf.cpp"),
@@ -82,13 +98,13 @@ def build_runtime(cos: dict[str, Path]) -> Path:
         "-L", str(ROCM / "lib"), "-Wl,-rpath," + str(ROCM / "lib"), "-lamdhip64", "-pthread",
         "-o", str(tmp),
     ])
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, out)
+    return out
 
 
-def build_oracle() -> Path:
-    _run(["make", "-s", "-C", str(ROOT / "oracle")])
-    return ROOT / "oracle" / "liboracle.so"
+def build_oracle(sanitize: bool = False) -> Path:
+    _run(["make", "-s", "-C", str(ROOT / "oracle"), *(["san"] if sanitize else [])])
+    return ROOT / "oracle" / ("_san/liboracle.so" if sanitize else "liboracle.so")
 
 
 def build_all() -> None:
@@ -97,7 +113,17 @@ def build_all() -> None:
     build_oracle()
 
 
+def build_sanitized() -> tuple[Path, Path]:
+    """The host code and the oracle with ASan + UBSan (separate outputs)."""
+    cos = build_kernels()
+    return build_runtime(cos, sanitize=True), build_oracle(sanitize=True)
+
+
 if __name__ == "__main__":
-    build_all()
-    print(f"built {LIB}")
+    if "--sanitize" in sys.argv[1:]:
+        lib, orc = build_sanitized()
+        print(f"built {lib} and {orc}")
+    else:
+        build_all()
+        print(f"built {LIB}")
     sys.exit(0)

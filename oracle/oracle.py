@@ -14,7 +14,9 @@ from pathlib import Path
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB_PATH = HERE / "liboracle.so"
+# AXH_ORACLE_LIBRARY selects another build (e.g. the sanitizer build).
+LIB_PATH = (Path(os.environ["AXH_ORACLE_LIBRARY"]) if os.environ.get("AXH_ORACLE_LIBRARY")
+            else HERE / "liboracle.so")
 
 Q4_0_BLOCK_BYTES, Q4_0_BLOCK_ELEMS = 18, 32
 Q4K_SB_BYTES, Q4K_SB_ELEMS = 144, 256
