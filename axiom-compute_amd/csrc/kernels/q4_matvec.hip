@@ -732,7 +732,7 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
 // stream of another (A/B in one run, 14336 x 4096: 8.27-8.40 vs 8.78-9.00
 // us), and costs where one workgroup per CU waits for all of x (4096 x 14336:
 // 8.64-8.70 vs 8.12-8.22 us).
-template <int NIT, bool kDual = false, bool kQ5 = false, bool kWhole = false>
+template <int NIT, bool kDual = false, bool kQ5 = false, bool kWhole = false, int XD = 1>
 __device__ __forceinline__ void q4k_matvec_one(const uint8_t *__restrict__ q,
                                                const uint8_t *__restrict__ q2,
                                                const float *__restrict__ x, float *__restrict__ y,
@@ -753,7 +753,6 @@ __device__ __forceinline__ void q4k_matvec_one(const uint8_t *__restrict__ q,
   float *ss = lds + nsb * kQ4kFlatSbFloats;
   const uint32_t bundle = 2u * W + half;
   Q4kFlatBuf<RPW, 2, kQ5> B;
-  float4 xv[2][512 / NT];
   float acc[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
@@ -782,17 +781,30 @@ __device__ __forceinline__ void q4k_matvec_one(const uint8_t *__restrict__ q,
     if (mine) q4k_flat_store<RPW, kDual>(acc, 2u * W, lane, n_rows, y);
     return;
   }
-  q4k_flat_load_chunk<NT>(xr, tid, 0u, xv[0]);
+  // x chunks are requested XD iterations ahead of their staging (issued
+  // before the weights of the next iteration), the weights one iteration
+  // ahead.  The load counter is in order, so with XD = 1 the staging of chunk
+  // j + 1 waits behind the weights requested with it; XD = 2
+  // (axh_q4k_matvec_onep_i{NIT}) takes that wait off the critical path where
+  // nothing else on the CU hides it: one workgroup per CU (A/B in one run,
+  // 4096 x 14336: 7.55-7.87 vs 7.88-8.01 us, 4096 x 8192 5.42 vs 5.58), but
+  // not with two (8192 x 14336: 14.7 vs 13.8) or at three iterations (4096 x
+  // 6144: 4.78 vs 4.70).  Three weight slots, or x three ahead, were slower.
+  static_assert(XD == 1 || XD == 2, "x one or two chunks ahead");
+  constexpr int XB = XD + 1;
+  float4 xq[XB][512 / NT];
+  q4k_flat_load_chunk<NT>(xr, tid, 0u, xq[0]);
   q4k_flat_load<RPW, 2, false, kDual, kQ5>(B, 0, qr, qr2, row_bytes, bundle, 0u, s, c);
+#pragma unroll
+  for (int k = 1; k < XD; ++k) q4k_flat_load_chunk<NT>(xr, tid, (uint32_t)k, xq[k]);
 #pragma unroll
   for (int j = 0; j < NIT; ++j) {
     const int p = j & 1;
-    q4k_flat_stage_chunk<NT>(xs, ss, tid, (uint32_t)j, nsb, xv[p]);
-    if (j + 1 < NIT) { // next iteration's x chunk and weights, before the compute
-      q4k_flat_load_chunk<NT>(xr, tid, (uint32_t)(j + 1), xv[p ^ 1]);
+    q4k_flat_stage_chunk<NT>(xs, ss, tid, (uint32_t)j, nsb, xq[j % XB]);
+    if (j + XD < NIT) q4k_flat_load_chunk<NT>(xr, tid, (uint32_t)(j + XD), xq[(j + XD) % XB]);
+    if (j + 1 < NIT) // next iteration's weights, before the compute
       q4k_flat_load<RPW, 2, false, kDual, kQ5>(B, p ^ 1, qr, qr2, row_bytes, bundle,
                                                (uint32_t)(j + 1), s, c);
-    }
     __syncthreads();
     const uint32_t sb = (uint32_t)j * 8u + s;
     if (mine && sb < nsb) q4k_flat_compute<RPW, 2, kQ5>(B, p, xs, ss, sb, c, acc);
@@ -829,6 +841,29 @@ AXH_Q4K_MATVEC_ONE(13)
 AXH_Q4K_MATVEC_ONE(14)
 AXH_Q4K_MATVEC_ONE(15)
 AXH_Q4K_MATVEC_ONE(16)
+
+#define AXH_Q4K_MATVEC_ONEP(NIT)                                                                 \
+  extern "C" __global__ void __launch_bounds__(512)                                              \
+      axh_q4k_matvec_onep_i##NIT(const uint8_t *__restrict__ q, const float *__restrict__ x,     \
+                                 float *__restrict__ y, AXH_ROWS_ARGS) { AXH_ROWS_UNPACK; \
+    extern __shared__ float axh_lds_dyn[];                                                       \
+    q4k_matvec_one<NIT, false, false, false, 2>(q, q, x, y, a.n_rows, a.units_per_row,           \
+                                                axh_lds_dyn);                                    \
+  }
+AXH_Q4K_MATVEC_ONEP(3)
+AXH_Q4K_MATVEC_ONEP(4)
+AXH_Q4K_MATVEC_ONEP(5)
+AXH_Q4K_MATVEC_ONEP(6)
+AXH_Q4K_MATVEC_ONEP(7)
+AXH_Q4K_MATVEC_ONEP(8)
+AXH_Q4K_MATVEC_ONEP(9)
+AXH_Q4K_MATVEC_ONEP(10)
+AXH_Q4K_MATVEC_ONEP(11)
+AXH_Q4K_MATVEC_ONEP(12)
+AXH_Q4K_MATVEC_ONEP(13)
+AXH_Q4K_MATVEC_ONEP(14)
+AXH_Q4K_MATVEC_ONEP(15)
+AXH_Q4K_MATVEC_ONEP(16)
 
 #define AXH_Q4K_MATVEC_FLAT(RPW, NW, PF, NT)                                                     \
   extern "C" __global__ void __launch_bounds__(NW * 64)                                          \

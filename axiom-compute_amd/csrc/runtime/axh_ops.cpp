@@ -391,6 +391,15 @@ constexpr uint32_t kOneWholeMinRows = 6144, kOneWholeMaxSb = 32;
 // (51.6-51.8 vs 53.5-54.3 us).
 constexpr uint32_t kOneTallMaxRows = 65536, kOneTallMaxSb = 16;
 
+// x two chunks ahead (axh_q4k_matvec_onep_i{NIT}) from four iterations on, up
+// to one workgroup per CU (A/B in one run, GB/s at the median, one vs onep:
+// 4096 rows x 8192 3411-3420 vs 3526-3531, x 14336 4114-4169 vs 4254-4277, x
+// 32768 4767-4832 vs 4870-4974, 3072 x 14336 3315-3323 vs 3376-3381; even at
+// 1024-2048 rows; slower at three iterations, 4096 x 6144 3008-3020 vs
+// 2965-2974, and with two workgroups per CU, 6144 x 14336 3982-4015 vs
+// 3912-3925).  The prefetch hole of the one-pass family picks either.
+constexpr uint32_t kOnePMinIt = 4, kOnePMaxRows = 4096;
+
 static bool use_one_pass(uint32_t n_rows, uint32_t nsb) {
   if (nsb < 1 || nsb > kOneMaxSb || n_rows < kOneMinRows) return false;
   return n_rows <= kOneMaxRows || (nsb <= kOneTallMaxSb && n_rows <= kOneTallMaxRows);
@@ -492,8 +501,13 @@ static axh_status plan_q4k(uint32_t n_rows, uint32_t sb_per_row, const axh_q4_va
   }
   case AXH_Q4K_FAMILY_ONE_PASS:
   case AXH_Q4K_FAMILY_ONE_PASS_X: {
-    if (other_holes)
-      return fail(AXH_ERR_INVALID_ARGUMENT, "the one-pass families' only hole is sb_per_lane");
+    const uint32_t xd = variant ? variant->prefetch : 0u;
+    if (variant && (variant->rows_per_wave || variant->waves_per_workgroup || variant->nontemporal))
+      return fail(AXH_ERR_INVALID_ARGUMENT,
+                  "the one-pass families' holes are sb_per_lane and (one pass) prefetch");
+    if (xd && (fam == AXH_Q4K_FAMILY_ONE_PASS_X || xd > 2u))
+      return fail(AXH_ERR_INVALID_ARGUMENT,
+                  "one-pass prefetch is 1 or 2 x chunks ahead (none for the whole-x kernel)");
     if (nsb < 1u || nsb > kOneMaxSb || q_bytes >= 0xFFFFFFFFull)
       return fail(AXH_ERR_INVALID_ARGUMENT,
                   "the one-pass families take rows of 1-128 superblocks below 4 GiB");
@@ -502,8 +516,12 @@ static axh_status plan_q4k(uint32_t n_rows, uint32_t sb_per_row, const axh_q4_va
     if (nit < need || nit > 16u)
       return fail(AXH_ERR_INVALID_ARGUMENT,
                   "sb_per_lane must cover the row (ceil(sb_per_row / 8)) and be at most 16");
+    if (xd == 2u && nit < 3u)
+      return fail(AXH_ERR_INVALID_ARGUMENT, "x two chunks ahead needs three or more iterations");
+    const bool two_ahead = fam == AXH_Q4K_FAMILY_ONE_PASS &&
+                           (xd == 2u || (xd == 0u && nit >= kOnePMinIt && n_rows <= kOnePMaxRows));
     std::snprintf(p->name, sizeof(p->name), "axh_q4k_matvec_one%s_i%u",
-                  fam == AXH_Q4K_FAMILY_ONE_PASS_X ? "x" : "", nit);
+                  fam == AXH_Q4K_FAMILY_ONE_PASS_X ? "x" : two_ahead ? "p" : "", nit);
     p->nw = 8;
     p->lds = nsb * 1120u;
     p->flat = false; // one workgroup per 16 rows, all of them launched
@@ -595,6 +613,8 @@ axh_status axh_q4k_matvec_default_variant(uint32_t n_rows, uint32_t sb_per_row,
   unsigned a = 0, b = 0, c = 0, d = 0;
   if (fam == AXH_Q4K_FAMILY_ONE_PASS || fam == AXH_Q4K_FAMILY_ONE_PASS_X) {
     out->sb_per_lane = (sb_per_row + 7u) / 8u;
+    if (fam == AXH_Q4K_FAMILY_ONE_PASS)
+      out->prefetch = std::strncmp(p.name, "axh_q4k_matvec_onep_", 20) == 0 ? 2u : 1u;
   } else if (fam == AXH_Q4K_FAMILY_WORKGROUP) {
     if (std::sscanf(p.name, "axh_q4k_matvec_wg_w%u_x2_r%u", &a, &b) == 2) out->rows_per_wave = b;
   } else if (std::sscanf(p.name, "axh_q4k_matvec_flat_r%u_w%u_p%u_n%u", &a, &b, &c, &d) == 4) {

@@ -457,6 +457,8 @@ std::vector<Hole> family_holes(uint32_t fam, uint32_t n_rows, uint32_t nsb) {
     std::vector<int64_t> c{need};
     if (need < 16) c.push_back(need + 1); // a longer trip count than the row needs
     h.push_back({"sb_per_lane", c});
+    // x one or two chunks ahead (variants that cannot take it fail to plan)
+    if (fam == AXH_Q4K_FAMILY_ONE_PASS) h.push_back({"prefetch", {1, 2}});
     break;
   }
   case AXH_Q4K_FAMILY_WORKGROUP:

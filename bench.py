@@ -405,55 +405,65 @@ def main() -> int:
     # The floor of the launch-per-call protocol on this box, for matvec
     # workloads: the same number of bytes read from the same rotated copies by
     # a kernel of the same launch shape that only reads (one store per wave),
-    # and an empty kernel of that shape, launched by the same loop.
+    # the best of the read kernel's launch shapes, and an empty kernel, all
+    # launched by the same loop.
     floor = None
     if kind != "matmul":
-        words = 8 * ctx.cu_count()
-        fout = ctx.alloc(words * 4)
         nb = case.weight_bytes // 16 * 16
+        fout = ctx.alloc(2048 * 1024 // 64 * 4)
+        words = 8 * ctx.cu_count()
+        per_round = max(20, per_group)
 
-        def floor_us(op):
-            ms = ctx.bench_loop(op, case.wbuf, case.stride, case.n_copies, None, fout,
-                                units=nb // 16, batch=words, warmup=args.warmup, groups=groups,
-                                calls_per_group=per_group)
-            return sum(ms) * 1000.0 / args.steps
+        def floor_op(op, **kw):
+            return dict(op=op, q=case.wbuf, q_stride=case.stride, n_copies=case.n_copies, x=None,
+                        y=fout, units=nb // 16, **kw)
 
-        read_us = floor_us("read_floor")
-        empty_us = floor_us("launch_empty")
-        fout.close()
-        # The best single-launch read of the same bytes: the read kernel at
-        # every shape of 256/512/1024 threads, 2/4/8 16-byte loads in flight per
-        # lane and 256-2048 workgroups, launched by the same loop.
+        def shape_op(threads, loads, grid):
+            return floor_op("read_shape", n_rows=grid, batch=grid * threads // 64,
+                            variant=pkg.Variant(0, threads // 64, loads))
+
+        def us(op, calls):
+            return sum(ctx.bench_loop(**op, warmup=2, groups=1, calls_per_group=calls)) * 1e3 / calls
+
+        # The read kernel at every shape of 256/512/1024 threads, 2/4/8 16-byte
+        # loads in flight per lane and 256-2048 workgroups.
         sweep = []
-        sout = ctx.alloc(2048 * 1024 // 64 * 4)
         for threads in (256, 512, 1024):
             for loads in (2, 4, 8):
                 for grid in (256, 512, 1024, 2048):
-                    ms = ctx.bench_loop("read_shape", case.wbuf, case.stride, case.n_copies, None,
-                                        sout, n_rows=grid, units=nb // 16,
-                                        batch=grid * threads // 64,
-                                        variant=pkg.Variant(0, threads // 64, loads),
-                                        warmup=args.warmup, groups=groups,
-                                        calls_per_group=per_group)
-                    sweep.append((sum(ms) * 1000.0 / args.steps, threads, loads, grid))
-        sout.close()
+                    sweep.append((us(shape_op(threads, loads, grid), args.steps), threads, loads,
+                                  grid))
         sweep.sort()
-        best_us, bt, bl, bg = sweep[0]
+        _, bt, bl, bg = sweep[0]
+        # Ratios from interleaved rounds (the matvec, the read of its launch
+        # shape, the best read shape, the empty kernel, one after another,
+        # 10 rounds), so that clock drift between runs cancels.
+        ops = {"matvec": case.bench_op(), "read": floor_op("read_floor", batch=words),
+               "best": shape_op(bt, bl, bg), "empty": floor_op("launch_empty", batch=words)}
+        rounds = {k: [] for k in ops}
+        for _ in range(10):
+            for k, op in ops.items():
+                rounds[k].append(us(op, per_round))
+        med = {k: sorted(v)[len(v) // 2] for k, v in rounds.items()}
+        fout.close()
+        read_us, best_us, empty_us = med["read"], med["best"], med["empty"]
         floor = {
             "read_same_bytes_us": round(read_us, 3),
             "read_same_bytes_GBps": round(nb / read_us / 1e3, 1),
             "empty_launch_us": round(empty_us, 3),
-            "kernel_vs_read_floor": round(read_us / us_per_call, 4),
+            "kernel_interleaved_us": round(med["matvec"], 3),
+            "kernel_vs_read_floor": round(read_us / med["matvec"], 4),
             "best_read_us": round(best_us, 3),
             "best_read_GBps": round(nb / best_us / 1e3, 1),
             "best_read_shape": f"axh_read_floor_t{bt}_u{bl}, {bg} workgroups",
-            "kernel_vs_best_read": round(best_us / us_per_call, 4),
+            "kernel_vs_best_read": round(best_us / med["matvec"], 4),
             "read_sweep_us": [[t_, l_, g_, round(u_, 3)] for u_, t_, l_, g_ in sweep],
-            "what": "back-to-back launches, by the same loop, of the matvec's launch shape "
-                    "(one 512-thread workgroup per CU) that only read the same bytes from the "
-                    "same rotated copies (one store per wave), and that do nothing; "
-                    "best_read: the fastest of the read kernel's 36 launch shapes "
-                    "(read_sweep_us rows: threads, loads in flight per lane, workgroups, us)",
+            "what": "back-to-back launches, by the same loop, of a kernel of the matvec's "
+                    "launch shape (one 512-thread workgroup per CU) that only reads the same "
+                    "bytes from the same rotated copies (one store per wave), of the fastest of "
+                    "that read kernel's 36 launch shapes (read_sweep_us rows: threads, loads "
+                    "in flight per lane, workgroups, us per call), and of an empty kernel; the "
+                    "ratios are medians of 10 interleaved rounds of the matvec and each floor",
         }
     kernel = case.kernel()
     shape = (("2x" if kind == "gate_up" else "") + f"{case.rows}x{case.cols}"

@@ -176,7 +176,10 @@ void axh_event_destroy(axh_event *ev);
  *     (weight-load cache policy);
  *   one pass (x staged chunk by chunk, or whole): sb_per_lane, the superblocks
  *     a lane walks per row (the kernel's trip count, eight superblocks per
- *     half-wave per step: from ceil(sb_per_row / 8) to 16);
+ *     half-wave per step: from ceil(sb_per_row / 8) to 16); chunk by chunk
+ *     also prefetch, the x chunks requested ahead of their staging (1, or 2
+ *     from three steps: axh_q4k_matvec_onep_i*; the default is 2 from four
+ *     steps up to 4096 rows);
  *   one workgroup: rows_per_wave = rows per workgroup (1, 2 or 4, at least
  *     n_rows);
  *   tiled: rows_per_wave, waves_per_workgroup, prefetch.
@@ -191,7 +194,7 @@ void axh_event_destroy(axh_event *ev);
 enum {
     AXH_Q4K_FAMILY_DEFAULT = 0,
     AXH_Q4K_FAMILY_PERSISTENT = 1, /* axh_q4k_matvec_flat_r*_w*_p*_n*[_x2]            */
-    AXH_Q4K_FAMILY_ONE_PASS = 2,   /* axh_q4k_matvec_one_i{sb_per_lane}              */
+    AXH_Q4K_FAMILY_ONE_PASS = 2,   /* axh_q4k_matvec_one[p]_i{sb_per_lane}           */
     AXH_Q4K_FAMILY_ONE_PASS_X = 3, /* axh_q4k_matvec_onex_i{sb_per_lane}: x whole    */
     AXH_Q4K_FAMILY_WORKGROUP = 4,  /* axh_q4k_matvec_wg_w8_x2_r{1,2,4}: 1-4 rows     */
     AXH_Q4K_FAMILY_SPLIT_K = 5,    /* axh_q4k_matvec_sk_s16: <= 32 rows, <= 256 SB   */

@@ -102,6 +102,8 @@ def test_builtin_code_object_holds_every_variant_kernel(axc):
     for nit in range(1, 17):  # one-pass kernels for rows of 1..128 superblocks
         assert f"axh_q4k_matvec_one_i{nit}".encode() in co
         assert f"axh_q4k_matvec_onex_i{nit}".encode() in co
+        if nit >= 3:  # x two chunks ahead
+            assert f"axh_q4k_matvec_onep_i{nit}".encode() in co
     for name in ("q4km_dequant_matvec", "q4_0_dequant_matvec", "axh_q4k_dequant",
                  "axh_q4_0_dequant", "axh_f16_widen", "axh_q4k_matvec_tiled_r2_w8_p2",
                  "axh_q4k_matvec_tiled_r1_w4_p2"):
@@ -112,12 +114,14 @@ def test_kernel_selection_by_shape_and_variant(axc):
     """The entry point axh_q4k_matvec launches (no device work): persistent
     kernel while a row's x fits one workgroup's LDS, tiled kernel beyond."""
     name = axc.q4k_matvec_kernel_name
-    # 32..32768 rows: one pass, one pair of rows per wave, a workgroup per 16 rows
-    assert name(4096, 56) == "axh_q4k_matvec_one_i7"
-    assert name(32, 33) == "axh_q4k_matvec_one_i5"
-    assert name(4096, 128) == "axh_q4k_matvec_one_i16"
+    # 32..32768 rows: one pass, one pair of rows per wave, a workgroup per 16 rows;
+    # x two chunks ahead from four steps up to one workgroup per CU (4096 rows)
+    assert name(4096, 56) == "axh_q4k_matvec_onep_i7"
+    assert name(32, 33) == "axh_q4k_matvec_onep_i5"
+    assert name(4096, 128) == "axh_q4k_matvec_onep_i16"
     assert name(4097, 56) == "axh_q4k_matvec_one_i7"
-    assert name(4096, 32) == "axh_q4k_matvec_one_i4"
+    assert name(4096, 32) == "axh_q4k_matvec_onep_i4"
+    assert name(4096, 24) == "axh_q4k_matvec_one_i3"
     assert name(4096, 16) == "axh_q4k_matvec_one_i2"
     assert name(6143, 16) == "axh_q4k_matvec_one_i2"
     # from 6144 rows of at most 32 superblocks: x staged whole behind one barrier

@@ -293,6 +293,23 @@ def test_q4k_one_pass_shapes(ctx, axc, rows, sb):
     _check_q4k(y, q, x, rows, sb, f"q4k one pass {rows}x{sb}")
 
 
+@pytest.mark.parametrize("rows,sb,xd", [(32, 17, 2), (33, 24, 2), (4096, 25, 2), (4095, 56, 2),
+                                        (4096, 56, 1), (2047, 128, 2), (100, 113, 2),
+                                        (5000, 40, 2), (4096, 40, 1), (64, 121, 2)])
+def test_q4k_one_pass_x_ahead(ctx, axc, rows, sb, xd):
+    """Both x prefetch distances of the chunked one-pass kernel (the prefetch
+    hole: one_i* one chunk ahead, onep_i* two), at trip counts 3..16 with a
+    partial last chunk, odd row counts and partial last workgroups."""
+    v = axc.Variant(prefetch=xd, family=axc.FAMILY_ONE_PASS)
+    want = f"axh_q4k_matvec_one{'p' if xd == 2 else ''}_i{(sb + 7) // 8}"
+    assert axc.q4k_matvec_kernel_name(rows, sb, v) == want
+    _say(f"q4k one pass x {xd} ahead {rows}x{sb}")
+    q = O.gen_q4k_weights(rows * 31 + sb + xd, rows * sb)
+    x = O.gen_normal_f32(rows + 13 * sb, sb * 256)
+    y = _run_q4k(ctx, q, x, rows, sb, v)
+    _check_q4k(y, q, x, rows, sb, f"q4k one pass x {xd} ahead {rows}x{sb}")
+
+
 @pytest.mark.parametrize("rows,sb", [(6144, 1), (6145, 8), (6151, 9), (8192, 17), (11008, 16),
                                      (14336, 16), (9999, 24), (6200, 25), (7001, 32),
                                      (32768, 2), (40001, 16), (65535, 3), (65536, 5)])

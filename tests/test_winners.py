@@ -32,6 +32,8 @@ def test_every_default_is_a_hole_assignment(axc, rows, sb):
     assert axc.q4k_matvec_kernel_name(rows, sb, d) == axc.q4k_matvec_kernel_name(rows, sb)
     if d.family in (axc.FAMILY_ONE_PASS, axc.FAMILY_ONE_PASS_X):
         assert d.sb_per_lane == (sb + 7) // 8
+        assert d.prefetch == (0 if d.family == axc.FAMILY_ONE_PASS_X else
+                              2 if (sb + 7) // 8 >= 4 and rows <= 4096 else 1)
     if d.family == axc.FAMILY_PERSISTENT:
         assert 0 not in (d.rows_per_wave, d.waves_per_workgroup, d.prefetch, d.nontemporal)
 
@@ -51,8 +53,12 @@ def test_family_defaults_by_shape(axc):
 def test_each_family_names_its_kernel(axc):
     V, F = axc.Variant, axc
     n = axc.q4k_matvec_kernel_name
-    assert n(4096, 56, V(family=F.FAMILY_ONE_PASS)) == "axh_q4k_matvec_one_i7"
-    assert n(4096, 56, V(family=F.FAMILY_ONE_PASS, sb_per_lane=9)) == "axh_q4k_matvec_one_i9"
+    assert n(4096, 56, V(family=F.FAMILY_ONE_PASS)) == "axh_q4k_matvec_onep_i7"
+    assert n(4096, 56, V(family=F.FAMILY_ONE_PASS, sb_per_lane=9)) == "axh_q4k_matvec_onep_i9"
+    assert n(4096, 56, V(prefetch=1, family=F.FAMILY_ONE_PASS)) == "axh_q4k_matvec_one_i7"
+    assert n(8192, 56, V(family=F.FAMILY_ONE_PASS)) == "axh_q4k_matvec_one_i7"
+    assert n(8192, 56, V(prefetch=2, family=F.FAMILY_ONE_PASS)) == "axh_q4k_matvec_onep_i7"
+    assert n(4096, 24, V(prefetch=2, family=F.FAMILY_ONE_PASS)) == "axh_q4k_matvec_onep_i3"
     assert n(4096, 56, V(family=F.FAMILY_ONE_PASS_X)) == "axh_q4k_matvec_onex_i7"
     assert n(4096, 56, V(family=F.FAMILY_PERSISTENT)) == "axh_q4k_matvec_flat_r1_w8_p2_n0"
     assert n(4096, 56, V(2, 8, 1, 2, F.FAMILY_PERSISTENT)) == "axh_q4k_matvec_flat_r2_w8_p1_n0"
@@ -72,6 +78,9 @@ def test_each_family_names_its_kernel(axc):
     (4096, 56, dict(family=2, sb_per_lane=17), "no one-pass kernel beyond 16 steps"),
     (4096, 56, dict(family=1, sb_per_lane=7), "sb_per_lane outside the one-pass families"),
     (4096, 56, dict(family=2, rows_per_wave=2), "one pass has no rows_per_wave hole"),
+    (4096, 56, dict(family=2, prefetch=3), "x at most two chunks ahead"),
+    (4096, 16, dict(family=2, prefetch=2), "two ahead needs three steps"),
+    (14336, 16, dict(family=3, prefetch=1), "whole x has no prefetch hole"),
     (5, 56, dict(family=4), "one workgroup takes at most 4 rows"),
     (3, 56, dict(family=4, rows_per_wave=2), "rows_per_wave below n_rows"),
     (33, 56, dict(family=5), "split-K takes at most 32 rows"),
