@@ -412,7 +412,7 @@ def main() -> int:
         nb = case.weight_bytes // 16 * 16
         fout = ctx.alloc(2048 * 1024 // 64 * 4)
         words = 8 * ctx.cu_count()
-        per_round = max(20, per_group)
+        per_round = max(100, args.steps)
 
         def floor_op(op, **kw):
             return dict(op=op, q=case.wbuf, q_stride=case.stride, n_copies=case.n_copies, x=None,
@@ -423,7 +423,7 @@ def main() -> int:
                             variant=pkg.Variant(0, threads // 64, loads))
 
         def us(op, calls):
-            return sum(ctx.bench_loop(**op, warmup=2, groups=1, calls_per_group=calls)) * 1e3 / calls
+            return sum(ctx.bench_loop(**op, warmup=20, groups=1, calls_per_group=calls)) * 1e3 / calls
 
         # The read kernel at every shape of 256/512/1024 threads, 2/4/8 16-byte
         # loads in flight per lane and 256-2048 workgroups.
@@ -436,12 +436,13 @@ def main() -> int:
         sweep.sort()
         _, bt, bl, bg = sweep[0]
         # Ratios from interleaved rounds (the matvec, the read of its launch
-        # shape, the best read shape, the empty kernel, one after another,
-        # 10 rounds), so that clock drift between runs cancels.
+        # shape, the best read shape, the empty kernel, one after another, each
+        # max(100, K) back-to-back calls, 5 rounds), so that clock drift
+        # between runs cancels.
         ops = {"matvec": case.bench_op(), "read": floor_op("read_floor", batch=words),
                "best": shape_op(bt, bl, bg), "empty": floor_op("launch_empty", batch=words)}
         rounds = {k: [] for k in ops}
-        for _ in range(10):
+        for _ in range(5):
             for k, op in ops.items():
                 rounds[k].append(us(op, per_round))
         med = {k: sorted(v)[len(v) // 2] for k, v in rounds.items()}
@@ -463,7 +464,8 @@ def main() -> int:
                     "bytes from the same rotated copies (one store per wave), of the fastest of "
                     "that read kernel's 36 launch shapes (read_sweep_us rows: threads, loads "
                     "in flight per lane, workgroups, us per call), and of an empty kernel; the "
-                    "ratios are medians of 10 interleaved rounds of the matvec and each floor",
+                    "ratios are medians of 5 interleaved rounds of max(100, K) calls of the "
+                    "matvec and of each floor",
         }
     kernel = case.kernel()
     shape = (("2x" if kind == "gate_up" else "") + f"{case.rows}x{case.cols}"
