@@ -1063,7 +1063,11 @@ __device__ __forceinline__ void q4k_matmul_rs(const uint8_t *__restrict__ q,
 // (deterministic) by wave k % NW, which stores them.  Against the K-split
 // tile kind at 14336 x 4096: 11.2 vs 14.2 us at 8 columns, 11.8 vs 14.6 at 16,
 // 15.0 vs 16.0 at 32 (NC = 2: every A fragment feeds two MFMAs).
-template <int NW, int SPW, int NC>
+// XH (axh_q4k_matmul_sr_w*_s*_h): column groups of 8 (lanes of MFMA columns
+// 8..15 hold zero X fragments and store nothing), staged through 64 KiB, so
+// the kernel needs 80 KiB of LDS and two workgroups share a CU; for at most 8
+// columns, where a 16-column group would carry 8 empty ones.
+template <int NW, int SPW, int NC, bool XH = false>
 __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
                                               const uint16_t *__restrict__ x,
                                               float *__restrict__ y, const MatmulArgs a,
@@ -1076,9 +1080,14 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
   const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
   const __amdgpu_buffer_rsrc_t qr = rsrc(q, n_rows * row_bytes);
   const __amdgpu_buffer_rsrc_t xr = rsrc(x, batch * K * 2u);
+  // 16-row blocks b = blockIdx.x + k * gridDim.x.  (Contiguous row ranges
+  // per workgroup, and the last round's blocks split in 8-row halves over
+  // twice the workgroups, both measured slower: 14336 x 4096 x 8, 11.4-12.1
+  // vs 10.9-11.5 us.)
   const uint32_t n_blocks = (n_rows + 15u) >> 4;
   const uint32_t n_myb = blockIdx.x < n_blocks ? (n_blocks - 1u - blockIdx.x) / gridDim.x + 1u : 0u;
-  const uint32_t n0 = 16u * NC * blockIdx.y; // this workgroup's 16 * NC columns
+  constexpr uint32_t kXc = XH ? 8u : 16u;    // columns of a group
+  const uint32_t n0 = kXc * NC * blockIdx.y; // this workgroup's kXc * NC columns
 
   // Weight loads of step (k, j): row 16 b + r, superblock wave*SPW + j: header
   // and the 32 qs bytes of chunk g.
@@ -1102,7 +1111,8 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
   {
     typedef __attribute__((address_space(3))) void lds_void_t;
     constexpr uint32_t kColB = 512u * SPW; // staged bytes per column
-    uint8_t *xs = reinterpret_cast<uint8_t *>(red) + wave * 16u * kColB;
+    uint8_t *xs = reinterpret_cast<uint8_t *>(red) + wave * kXc * kColB;
+    const uint32_t rr = r & (kXc - 1u);   // the lane's column within its group
     issue(0u, 0, 0); // the first step's weights, in flight during the X staging
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -1111,8 +1121,8 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
 #pragma unroll
       for (int pc = 0; pc < SPW / 2; ++pc)
 #pragma unroll
-        for (int n = 0; n < 16; ++n) {
-          const uint32_t col = n0 + 16u * (uint32_t)c + (uint32_t)n;
+        for (int n = 0; n < (int)kXc; ++n) {
+          const uint32_t col = n0 + kXc * (uint32_t)c + (uint32_t)n;
           const uint32_t s0 = wave * SPW + 2u * (uint32_t)pc;
           const uint32_t piece = lane ^ (uint32_t)n, sl = s0 + (piece >> 5);
           const uint32_t off =
@@ -1127,8 +1137,9 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
           const uint32_t P = 32u * (uint32_t)j + 8u * g + (uint32_t)t; // 16-byte piece of the wave's k
-          const uint32_t addr = r * kColB + 1024u * (P >> 6) + 16u * ((P & 63u) ^ r);
-          xf[c][j][t] = *reinterpret_cast<const half8_t *>(xs + addr);
+          const uint32_t addr = rr * kColB + 1024u * (P >> 6) + 16u * ((P & 63u) ^ rr);
+          const half8_t v = *reinterpret_cast<const half8_t *>(xs + addr);
+          xf[c][j][t] = (!XH || r < 8u) ? v : (half8_t){};
         }
     }
   }
@@ -1167,8 +1178,8 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
       }
     }
     // partial tiles of block k -> LDS (double buffer by block parity), after
-    // the 128 KiB of X staging
-    f32x4_t *buf = red + 8192u + (k & 1u) * (NW * NC * 64u);
+    // the 128 (XH: 64) KiB of X staging
+    f32x4_t *buf = red + (XH ? 4096u : 8192u) + (k & 1u) * (NW * NC * 64u);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       buf[(wave * NC + (uint32_t)c) * 64u + lane] = acc[c];
@@ -1184,8 +1195,9 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
         f32x4_t sum = buf[(uint32_t)c * 64u + lane];
 #pragma unroll
         for (int w2 = 1; w2 < NW; ++w2) sum += buf[((uint32_t)w2 * NC + (uint32_t)c) * 64u + lane];
-        const uint32_t col = n0 + 16u * (uint32_t)c + r;
-        if (col < batch) store_col4(y + (size_t)col * n_rows, 16u * b + 4u * g, n_rows, sum);
+        const uint32_t col = n0 + kXc * (uint32_t)c + r;
+        if ((!XH || r < 8u) && col < batch)
+          store_col4(y + (size_t)col * n_rows, 16u * b + 4u * g, n_rows, sum);
       }
     }
   }
@@ -1277,14 +1289,15 @@ AXH_Q4K_MATMUL_RS(4, 4, 8, 4)
 AXH_Q4K_MATMUL_RS(8, 2, 4, 4)
 AXH_Q4K_MATMUL_RS(8, 1, 8, 4)
 
-#define AXH_Q4K_MATMUL_SR(NW, SPW, NC, SUFFIX)                                                   \
+#define AXH_Q4K_MATMUL_SR(NW, SPW, NC, XH, SUFFIX)                                               \
   extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
       axh_q4k_matmul_sr_w##NW##_s##SPW##SUFFIX(const uint8_t *__restrict__ q,                    \
                                                const uint16_t *__restrict__ x,                   \
                                                float *__restrict__ y, AXH_MATMUL_ARGS) { AXH_MATMUL_UNPACK; \
     extern __shared__ f32x4_t axh_sr_dyn[];                                                      \
-    q4k_matmul_sr<NW, SPW, NC>(q, x, y, a, axh_sr_dyn);                                          \
+    q4k_matmul_sr<NW, SPW, NC, XH>(q, x, y, a, axh_sr_dyn);                                      \
   }
 
-AXH_Q4K_MATMUL_SR(8, 2, 1, )
-AXH_Q4K_MATMUL_SR(8, 2, 2, _n2)
+AXH_Q4K_MATMUL_SR(8, 2, 1, false, )
+AXH_Q4K_MATMUL_SR(8, 2, 2, false, _n2)
+AXH_Q4K_MATMUL_SR(8, 2, 1, true, _h)

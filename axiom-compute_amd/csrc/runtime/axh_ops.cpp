@@ -57,7 +57,8 @@ constexpr MatmulVariant kQ4kMatmulVariants[] = {
     {4, 4, 1, 4, 0},  {4, 8, 1, 4, 0},  {4, 8, 1, 2, 0},  {4, 16, 1, 2, 0}, {4, 16, 1, 4, 0},
     {5, 4, 8, 2, 4},  {5, 4, 8, 2, 2},  {5, 4, 4, 2, 4},  {5, 4, 4, 3, 4},  {5, 4, 4, 2, 8},
     {5, 4, 2, 2, 4},  {5, 4, 2, 3, 4},  {5, 4, 1, 3, 4},  {6, 8, 8, 4, 2},  {6, 8, 8, 3, 2},
-    {6, 4, 8, 4, 4},  {6, 8, 4, 4, 2},  {6, 8, 8, 4, 1},  {7, 8, 1, 1, 0},  {7, 8, 2, 1, 0}};
+    {6, 4, 8, 4, 4},  {6, 8, 4, 4, 2},  {6, 8, 8, 4, 1},  {7, 8, 1, 1, 0},  {7, 8, 2, 1, 0},
+    {7, 8, 1, 2, 0}};
 constexpr uint32_t kMatmulOob = 0xFFFFFF00u; // the kernels' out-of-range offset
 
 struct MatvecVariant {
@@ -1026,7 +1027,12 @@ static MatmulVariant q4k_matmul_default(uint32_t n_rows, uint32_t batch, uint32_
   (void)n_rows;
   // kind 7 against the K-split tile kind at 14336 x 4096 (A/B in one run):
   // B = 8 11.2 vs 14.2 us, B = 16 11.8 vs 14.6, B = 32 (two column groups per
-  // workgroup) 15.0 vs 16.0; at B = 64 the K-split tile kind stays ahead.
+  // workgroup) 15.0 vs 16.0; at B = 64 the K-split tile kind stays ahead.  Up
+  // to 8 columns its 8-column groups (prefetch 2: X staged through 64 KiB)
+  // are faster still, one workgroup per CU (A/B in one run: B = 8 10.93 vs
+  // 11.50 us, B = 4 10.70 vs 11.11, B = 1 10.64 vs 11.01; two workgroups per
+  // CU 12.6, 12.1 and 11.6).
+  if (batch <= 8 && nsb <= kSrMaxSb) return {7, 8, 1, 2, 0};
   if (batch <= 16 && nsb <= kSrMaxSb) return {7, 8, 1, 1, 0};
   if (batch <= 32 && nsb <= kSrMaxSb) return {7, 8, 2, 1, 0};
   if (batch <= 16) return {5, 4, 1, 3, 4};
@@ -1087,7 +1093,9 @@ static axh_status plan_q4k_matmul(uint32_t n_rows, uint32_t sb_per_row, uint32_t
         if (sb_per_row > kSrMaxSb)
           return fail(AXH_ERR_INVALID_ARGUMENT,
                       "matmul kind 7 takes rows of at most 16 superblocks (K <= 4096)");
-        std::snprintf(name, cap, "axh_q4k_matmul_sr_w%u_s2%s", v.w, v.nt == 2 ? "_n2" : "");
+        // prefetch 2: 8-column groups staged through 64 KiB (two workgroups per CU)
+        std::snprintf(name, cap, "axh_q4k_matmul_sr_w%u_s2%s%s", v.w, v.nt == 2 ? "_n2" : "",
+                      v.pf == 2 ? "_h" : "");
       }
       else
         std::snprintf(name, cap, "axh_q4k_matmul_rs_w%u_r%u_n%u_p%u", v.w, v.rt, v.nt, v.pf);
@@ -1143,7 +1151,7 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
   const uint64_t lds = v.kind == 4 ? 16ull * ((uint64_t)sb_per_row * 256u + 8u) * 2u
                        : v.kind == 5 ? kx_lds_bytes(v)
                        : v.kind == 6 ? rs_lds_bytes(v)
-                       : v.kind == 7 ? 131072u + 2u * v.w * v.nt * 1024u
+                       : v.kind == 7 ? (v.pf == 2 ? 65536u : 131072u) + 2u * v.w * v.nt * 1024u
                                      : 0u;
   if (lds > ctx->core->max_lds)
     return fail(AXH_ERR_INVALID_ARGUMENT, "matmul variant needs more LDS than the device has");
@@ -1153,7 +1161,7 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
                       : v.kind == 6 ? 16u * v.rt * v.w
                       : v.kind == 7 ? 16u
                                     : 32u * v.w;
-  const uint32_t tn = 16u * v.nt;
+  const uint32_t tn = (v.kind == 7 && v.pf == 2 ? 8u : 16u) * v.nt;
   uint64_t gx = (n_rows + tm - 1) / tm;
   const uint64_t gy = (batch + tn - 1) / tn;
   if (gx > ctx->core->max_wg[0] || gy > ctx->core->max_wg[1])
@@ -1163,7 +1171,9 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
   s = builtin_kernel(ctx, name, 3, sizeof(MatmulArgs), v.w * 64u, &k);
   if (s != AXH_OK) return s;
   if (v.kind == 4 || v.kind == 7) { // persistent: one resident wave of workgroups per column group
-    const uint64_t resident = (uint64_t)occupancy(ctx, k, (uint32_t)lds) * ctx->core->cu_count;
+    // (kind 7: one workgroup per CU even where two would fit)
+    const uint64_t resident =
+        (uint64_t)(v.kind == 7 ? 1u : occupancy(ctx, k, (uint32_t)lds)) * ctx->core->cu_count;
     if (resident < gx) gx = resident;
   }
   const uint32_t grid[3] = {(uint32_t)gx, (uint32_t)gy, 1};

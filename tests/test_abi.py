@@ -204,9 +204,13 @@ def test_matmul_kernel_selection(axc):
     with K) with all columns in one group up to 128, register A beyond."""
     name = axc.q4k_matmul_kernel_name
     # up to 16 columns and K <= 4096: streaming rows; longer rows: the K-split tile
-    assert name(14336, 16, 8) == "axh_q4k_matmul_sr_w8_s2"
+    # up to 8 columns in 8-column groups (X staged through 64 KiB)
+    assert name(14336, 16, 8) == "axh_q4k_matmul_sr_w8_s2_h"
+    assert name(14336, 1, 1) == "axh_q4k_matmul_sr_w8_s2_h"
+    assert name(14336, 16, 8, axc.MatmulVariant(7, 8, 1, 1)) == "axh_q4k_matmul_sr_w8_s2"
+    assert name(14336, 16, 9) == "axh_q4k_matmul_sr_w8_s2"
     assert name(14336, 16, 16) == "axh_q4k_matmul_sr_w8_s2"
-    assert name(14336, 1, 1) == "axh_q4k_matmul_sr_w8_s2"
+    assert name(14336, 16, 16, axc.MatmulVariant(7, 8, 1, 2)) == "axh_q4k_matmul_sr_w8_s2_h"
     assert name(14336, 16, 32) == "axh_q4k_matmul_sr_w8_s2_n2"  # two column groups
     assert name(14336, 16, 17) == "axh_q4k_matmul_sr_w8_s2_n2"
     assert name(4096, 56, 8) == "axh_q4k_matmul_kx_r4_n1_k4_p3"

@@ -148,18 +148,34 @@ def test_tile_kinds_on_odd_shapes(ctx, axc, rows, sb, batch):
 
 @pytest.mark.parametrize("rows,sb,batch", [(5000, 13, 13), (4097, 16, 16), (17, 7, 1),
                                            (1000, 16, 3), (70000, 2, 9), (4097, 16, 32),
-                                           (333, 11, 19), (70000, 3, 25)])
+                                           (333, 11, 19), (70000, 3, 25), (14336, 16, 8),
+                                           (4099, 5, 7)])
 def test_streaming_rows_kind(ctx, axc, rows, sb, batch):
-    """Kind 7 (the default up to 32 columns and K <= 4096; two column groups
-    per workgroup beyond 16 columns): more 16-row blocks
-    than workgroups (several per workgroup), a partial last block, rows not a
-    multiple of 4 (scalar stores), waves whose superblocks lie past the row
-    (K < 4096), a single column."""
+    """Kind 7 (the default up to 32 columns and K <= 4096; 8-column groups up
+    to 8 columns, two column groups per workgroup beyond 16 columns): more
+    16-row blocks than workgroups (several per workgroup), a partial last
+    block, rows not a multiple of 4 (scalar stores), waves whose superblocks
+    lie past the row (K < 4096), a single column."""
     assert axc.q4k_matmul_kernel_name(rows, sb, batch).startswith("axh_q4k_matmul_sr_w8_s2")
     _say(f"matmul streaming rows {rows}x{sb * 256} B={batch}")
     q, xh = _inputs(rows + sb * 5 + batch, rows, sb, batch)
     y = _run(ctx, q, xh, rows, sb, batch)
     _check(y, q, xh, rows, sb, batch, f"streaming rows {rows}x{sb} B={batch}")
+
+
+@pytest.mark.parametrize("rows,sb,batch,pf", [(1000, 16, 3, 1), (4097, 16, 8, 1),
+                                              (5000, 13, 13, 2), (70000, 3, 25, 2),
+                                              (333, 11, 16, 2)])
+def test_streaming_rows_group_widths(ctx, axc, rows, sb, batch, pf):
+    """Both column-group widths of kind 7 away from their defaults: 16-column
+    groups at <= 8 columns, 8-column groups (two or more per matrix) beyond."""
+    v = axc.MatmulVariant(7, 8, 1, pf)
+    want = "axh_q4k_matmul_sr_w8_s2" + ("_h" if pf == 2 else "")
+    assert axc.q4k_matmul_kernel_name(rows, sb, batch, v) == want
+    _say(f"matmul streaming rows {rows}x{sb * 256} B={batch} prefetch {pf}")
+    q, xh = _inputs(rows + sb * 7 + batch + pf, rows, sb, batch)
+    y = _run(ctx, q, xh, rows, sb, batch, v)
+    _check(y, q, xh, rows, sb, batch, f"streaming rows {rows}x{sb} B={batch} pf {pf}")
 
 
 @pytest.mark.parametrize("batch", [8, 40, 200])
