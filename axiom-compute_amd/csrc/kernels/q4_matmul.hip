@@ -1047,6 +1047,200 @@ __device__ __forceinline__ void q4k_matmul_rs(const uint8_t *__restrict__ q,
 }
 
 // ---------------------------------------------------------------------------
+// 32 x 32 tiles with wide waves (kind 8, axh_q4k_matmul_rm_w{W}_p4): a
+// workgroup of W waves (one per SIMD) owns 64 * W rows x 128 columns of Y;
+// wave w owns 64 rows (two 32-row MFMA tiles) x 128 columns (four 32-column
+// tiles) and walks all of K in 64-wide steps (one chunk of a superblock) with
+// v_mfma_f32_32x32x16_f16, so each X fragment read from LDS feeds two MFMAs
+// (64 rows, twice the row-split kind's reuse) and each dequantised A fragment
+// four (128 columns).  A ring of 4 LDS buffers, each the step's X tile (128
+// columns x 64 k, 16 KiB) and every wave's weight pieces (per row: header and
+// the chunk's 32 qs bytes), is filled by direct-to-LDS loads three steps
+// ahead; each step's fragments (X read from LDS, A dequantised) are prepared
+// during the previous step's MFMAs.  Lane l (row l % 32 of a row tile, half h
+// = l / 32) dequantises the
+// qs bytes [16h, 16h + 16) of the chunk: their low nibbles are the A
+// fragments of k-steps 0-1 (k = 16h + 0..15), their high nibbles those of
+// k-steps 2-3 (k = 32 + 16h + ..), each 8 consecutive k, so the X fragment of
+// the same (k-step, half) is one 16-byte piece.  X piece p of column n sits
+// in slot p ^ (n & 7) of the column's 128 bytes, so 8 lanes reading one piece
+// of 8 consecutive columns hit distinct banks.  One barrier per step makes
+// every wave's X of step j + 1 visible and frees the buffer the next loads
+// refill.
+// ---------------------------------------------------------------------------
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+template <int W, int RT>
+__device__ __forceinline__ void q4k_matmul_rm(const uint8_t *__restrict__ q,
+                                              const uint16_t *__restrict__ x,
+                                              float *__restrict__ y, const MatmulArgs a,
+                                              f32x4_t *lds) {
+  static_assert(W == 1 || W == 2 || W == 4 || W == 8, "16 X instructions per step over the waves");
+  static_assert(RT == 1 || RT == 2, "32 or 64 rows per wave");
+  constexpr int kXPer = 16 / W;                   // X instructions per wave per step
+  constexpr int kWI = (96 * RT + 63) / 64;        // weight instructions (32 RT rows x 48 B)
+  constexpr int kPerStep = kXPer + kWI;
+  constexpr uint32_t kWs = 64u * kWI;             // f32x4 slots of a wave's weight pieces
+  constexpr uint32_t kBuf = 16u * 64u + W * kWs;  // f32x4 slots per ring buffer
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t r = lane & 31u, h = lane >> 5;
+  const uint32_t n_rows = a.n_rows, nsb = a.sb_per_row, batch = a.batch;
+  const uint32_t K = nsb * 256u, n_steps = 4u * nsb;
+  const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
+  const __amdgpu_buffer_rsrc_t qr = rsrc(q, n_rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t xr = rsrc(x, batch * K * 2u);
+  const uint32_t m0 = blockIdx.x * (32u * RT * W) + 32u * RT * wave, n0 = blockIdx.y * 128u;
+
+  // X load role: instruction i = wave + W * u covers columns 8i .. 8i + 7;
+  // lane L loads piece (L & 7) ^ (col & 7) of column 8i + L / 8.
+  uint32_t xoff0[kXPer];
+#pragma unroll
+  for (int u = 0; u < kXPer; ++u) {
+    const uint32_t i = wave + (uint32_t)(W * u), col = 8u * i + (lane >> 3);
+    const uint32_t p = (lane & 7u) ^ (col & 7u), b = n0 + col;
+    xoff0[u] = b < batch ? (b * K + 8u * p) * 2u : kOob;
+  }
+  // Weight load role: piece P = 64m + lane -> row P / 3 of the wave's 64,
+  // part P % 3 (0 the header, 1-2 the 16-byte halves of the chunk's qs).
+  uint32_t woff0[kWI], wpart[kWI];
+#pragma unroll
+  for (int m = 0; m < kWI; ++m) {
+    const uint32_t P = 64u * (uint32_t)m + lane, rr = P / 3u, row = m0 + rr;
+    wpart[m] = P - 3u * rr;
+    woff0[m] = (rr < 32u * RT && row < n_rows) ? row * row_bytes : kOob;
+  }
+  auto issue = [&](uint32_t j) { // step j -> ring buffer j % 4
+    const bool live = j < n_steps;
+    const uint32_t sb = j >> 2, c = j & 3u;
+    f32x4_t *buf = lds + (j & 3u) * kBuf;
+#pragma unroll
+    for (int u = 0; u < kXPer; ++u) {
+      const uint32_t i = wave + (uint32_t)(W * u);
+      const uint32_t off = (xoff0[u] == kOob || !live) ? kOob : xoff0[u] + 128u * j;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void_t *)(buf + i * 64u), 16, off, 0, 0, 0);
+    }
+    f32x4_t *wb = buf + 16u * 64u + wave * kWs;
+#pragma unroll
+    for (int m = 0; m < kWI; ++m) {
+      const uint32_t off =
+          (woff0[m] == kOob || !live)
+              ? kOob
+              : woff0[m] + sb * 144u + (wpart[m] == 0u ? 0u : 16u * wpart[m] + 32u * c);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(qr, (lds_void_t *)(wb + m * 64), 16, off, 0, 0, 0);
+    }
+  };
+  // A fragments of step j from its ring buffer: af[i][s], s the k-step.
+  auto dequant = [&](uint32_t j, half8_t (&af)[RT][4]) {
+    const f32x4_t *wb = lds + (j & 3u) * kBuf + 16u * 64u + wave * kWs;
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+      const uint32_t pr = 3u * (32u * (uint32_t)i + r); // the row's three pieces
+      const uint4 hd = __builtin_bit_cast(uint4, wb[pr]);
+      const uint4 qv = __builtin_bit_cast(uint4, wb[pr + 1u + h]);
+      const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
+      uint32_t scp, mp;
+      q4k_scale_min_pair(hd.y, hd.z, hd.w, j & 3u, &scp, &mp);
+      const float d1s = d * (float)(scp & 0xFFu) * 16777216.0f;
+      const float d2s = d * (float)(scp >> 8) * 1048576.0f;
+      const float m1 = dmin * (float)(mp & 0xFFu), m2 = dmin * (float)(mp >> 8);
+      uint32_t l[4][2], hh[4][2];
+      dequant_dword(qv.x, d1s, m1, d2s, m2, l[0][0], l[0][1], hh[0][0], hh[0][1]);
+      dequant_dword(qv.y, d1s, m1, d2s, m2, l[1][0], l[1][1], hh[1][0], hh[1][1]);
+      dequant_dword(qv.z, d1s, m1, d2s, m2, l[2][0], l[2][1], hh[2][0], hh[2][1]);
+      dequant_dword(qv.w, d1s, m1, d2s, m2, l[3][0], l[3][1], hh[3][0], hh[3][1]);
+      af[i][0] = __builtin_bit_cast(half8_t, make_uint4(l[0][0], l[0][1], l[1][0], l[1][1]));
+      af[i][1] = __builtin_bit_cast(half8_t, make_uint4(l[2][0], l[2][1], l[3][0], l[3][1]));
+      af[i][2] = __builtin_bit_cast(half8_t, make_uint4(hh[0][0], hh[0][1], hh[1][0], hh[1][1]));
+      af[i][3] = __builtin_bit_cast(half8_t, make_uint4(hh[2][0], hh[2][1], hh[3][0], hh[3][1]));
+    }
+  };
+
+  f32x16_t acc[RT][4];
+#pragma unroll
+  for (int i = 0; i < RT; ++i)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[i][t] = (f32x16_t){};
+
+  // fragment slots of this lane: X piece p(s) = (s & 1) + 2h + 4 (s >> 1) of column 32t + r
+  uint32_t xaddr[4][4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const uint32_t col = 32u * (uint32_t)t + r;
+      const uint32_t p = ((uint32_t)s & 1u) + 2u * h + 4u * ((uint32_t)s >> 1);
+      xaddr[t][s] = col * 8u + (p ^ (col & 7u)); // f32x4 slot in a buffer
+    }
+
+  // Every fragment of step j + 1 (X from LDS, A dequantised from the
+  // weight pieces) is prepared while step j's MFMAs issue.
+  auto read_x = [&](uint32_t j, half8_t (&bf)[4][4]) {
+    const f32x4_t *buf = lds + (j & 3u) * kBuf;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) bf[s][t] = __builtin_bit_cast(half8_t, buf[xaddr[t][s]]);
+  };
+  issue(0u);
+  issue(1u);
+  issue(2u);
+  half8_t af[2][RT][4]; // A fragments of steps j and j + 1
+  half8_t bf[2][4][4]; // X fragments of steps j and j + 1
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * kPerStep) : "memory"); // step 0 landed
+  read_x(0u, bf[0]);
+  dequant(0u, af[0]);
+  // Two steps per trip (n_steps is a multiple of 4): fragment indices are
+  // compile-time constants.
+  for (uint32_t j = 0; j < n_steps; j += 2) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint32_t jj = j + (uint32_t)e;
+      // own loads of step jj + 1 landed (jj + 2 in flight); after the barrier
+      // every wave's X of step jj + 1 is in LDS and step jj is read
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kPerStep) : "memory");
+      issue(jj + 3u); // refills the buffer of step jj - 1
+      dequant(jj + 1u, af[e ^ 1]); // past the last step: zeros, unused
+      read_x(jj + 1u, bf[e ^ 1]);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < RT; ++i)
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[e][i][s], bf[e][s][t], acc[i][t], 0, 0, 0);
+      // the next step's weight pieces first (the dequantisation waits for
+      // them; LDS returns in order), then its X fragments and dequantisation
+      // between this step's MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * RT, 0); // DS read: weight pieces
+#pragma unroll
+      for (int k = 0; k < 16 * RT; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
+        if (k >= RT && k < RT + 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read: X
+        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0); // VALU
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // ring loads past the last step
+
+#pragma unroll
+  for (int i = 0; i < RT; ++i)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t b = n0 + 32u * (uint32_t)t + r;
+      if (b >= batch) continue;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const f32x4_t v = {acc[i][t][4 * q4], acc[i][t][4 * q4 + 1], acc[i][t][4 * q4 + 2],
+                           acc[i][t][4 * q4 + 3]};
+        store_col4(y + (size_t)b * n_rows, m0 + 32u * (uint32_t)i + 8u * (uint32_t)q4 + 4u * h,
+                   n_rows, v);
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Streaming rows (kind 7, the default up to 32 columns and K <= 4096): a
 // persistent workgroup of NW waves walks 16-row blocks b = blockIdx.x +
 // k * gridDim.x for the 16 * NC columns n0 = 16 * NC * blockIdx.y ..; wave w owns
@@ -1288,6 +1482,20 @@ AXH_Q4K_MATMUL_RS(8, 2, 8, 3)
 AXH_Q4K_MATMUL_RS(4, 4, 8, 4)
 AXH_Q4K_MATMUL_RS(8, 2, 4, 4)
 AXH_Q4K_MATMUL_RS(8, 1, 8, 4)
+
+#define AXH_Q4K_MATMUL_RM(W, RT)                                                                 \
+  extern "C" __global__ void __launch_bounds__(W * 64)                                           \
+      axh_q4k_matmul_rm_w##W##_r##RT##_p4(const uint8_t *__restrict__ q,                         \
+                                          const uint16_t *__restrict__ x, float *__restrict__ y,  \
+                                          AXH_MATMUL_ARGS) { AXH_MATMUL_UNPACK;                   \
+    extern __shared__ f32x4_t axh_rm_dyn[];                                                      \
+    q4k_matmul_rm<W, RT>(q, x, y, a, axh_rm_dyn);                                                \
+  }
+
+AXH_Q4K_MATMUL_RM(4, 2)
+AXH_Q4K_MATMUL_RM(8, 1)
+AXH_Q4K_MATMUL_RM(4, 1)
+AXH_Q4K_MATMUL_RM(2, 2)
 
 #define AXH_Q4K_MATMUL_SR(NW, SPW, NC, XH, SUFFIX)                                               \
   extern "C" __global__ void __launch_bounds__(NW * 64)                                          \

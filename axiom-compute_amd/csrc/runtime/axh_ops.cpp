@@ -58,7 +58,7 @@ constexpr MatmulVariant kQ4kMatmulVariants[] = {
     {5, 4, 8, 2, 4},  {5, 4, 8, 2, 2},  {5, 4, 4, 2, 4},  {5, 4, 4, 3, 4},  {5, 4, 4, 2, 8},
     {5, 4, 2, 2, 4},  {5, 4, 2, 3, 4},  {5, 4, 1, 3, 4},  {6, 8, 8, 4, 2},  {6, 8, 8, 3, 2},
     {6, 4, 8, 4, 4},  {6, 8, 4, 4, 2},  {6, 8, 8, 4, 1},  {7, 8, 1, 1, 0},  {7, 8, 2, 1, 0},
-    {7, 8, 1, 2, 0}};
+    {7, 8, 1, 2, 0},  {8, 8, 8, 4, 1},  {8, 4, 8, 4, 2},  {8, 4, 8, 4, 1},  {8, 2, 8, 4, 2}};
 constexpr uint32_t kMatmulOob = 0xFFFFFF00u; // the kernels' out-of-range offset
 
 struct MatvecVariant {
@@ -1019,6 +1019,12 @@ static uint32_t rs_lds_bytes(const MatmulVariant &v) {
   return v.pf * (2u * v.nt + v.w * ((48u * v.rt + 63u) / 64u)) * 1024u;
 }
 
+// Kind 8 LDS: a ring of 4 buffers, each the X tile (16 KiB) and every wave's
+// weight pieces (32 * rt rows x 48 bytes, in 1 KiB load instructions).
+static uint32_t rm_lds_bytes(const MatmulVariant &v) {
+  return 4u * (16u + v.w * ((96u * v.rt + 63u) / 64u)) * 1024u;
+}
+
 // Kind 7 (streaming rows) keeps each wave's X fragments in VGPRs after
 // staging them through 128 KiB of LDS: K up to 16 superblocks (8 waves x 2).
 constexpr uint32_t kSrMaxSb = 16;
@@ -1039,8 +1045,12 @@ static MatmulVariant q4k_matmul_default(uint32_t n_rows, uint32_t batch, uint32_
   if (batch <= 32) return {5, 4, 2, 2, 4};
   if (batch <= 64) return {5, 4, 4, 2, 4};
   if (batch <= 128) return {5, 4, 8, 2, 4};
-  if (batch <= 256) return {6, 8, 8, 4, 1};
-  return {6, 8, 8, 3, 2};
+  // kind 8 (32 x 32 MFMA tiles) against the row-split kind at 14336 x 4096
+  // (A/B in one run): B = 512 74.1 us (8 waves of 32 rows) vs 83-94, B = 256
+  // 49.3 (4 waves of 32 rows) vs 52.1; at B = 128 the K-split tile kind stays
+  // ahead (31.3 vs 46.8).
+  if (batch <= 256) return {8, 4, 8, 4, 1};
+  return {8, 8, 8, 4, 1};
 }
 
 uint32_t axh_q4k_matmul_variant_count(void) {
@@ -1063,18 +1073,22 @@ static axh_status plan_q4k_matmul(uint32_t n_rows, uint32_t sb_per_row, uint32_t
                                   char *name, size_t cap) {
   MatmulVariant want = q4k_matmul_default(n_rows, batch, sb_per_row);
   if (variant) {
-    if (variant->kind) want.kind = variant->kind;
+    if (variant->kind && variant->kind != want.kind) {
+      want.kind = variant->kind;
+      want.rt = 0; // the row tiles of the requested kind's default
+    }
     if (variant->waves_per_workgroup) want.w = variant->waves_per_workgroup;
     if (variant->col_tiles) want.nt = variant->col_tiles;
     if (variant->prefetch) want.pf = variant->prefetch;
     if (variant->row_tiles) {
-      if (want.kind != 5 && want.kind != 6)
-        return fail(AXH_ERR_INVALID_ARGUMENT, "row_tiles is a hole of matmul kinds 5 and 6 only");
+      if (want.kind != 5 && want.kind != 6 && want.kind != 8)
+        return fail(AXH_ERR_INVALID_ARGUMENT,
+                    "row_tiles is a hole of matmul kinds 5, 6 and 8 only");
       want.rt = variant->row_tiles;
     }
   }
-  if (want.kind != 5 && want.kind != 6) want.rt = 0;
-  else if (want.rt == 0) want.rt = want.kind == 5 ? 4u : 2u;
+  if (want.kind != 5 && want.kind != 6 && want.kind != 8) want.rt = 0;
+  else if (want.rt == 0) want.rt = want.kind == 5 ? 4u : want.kind == 6 ? 2u : 1u;
   for (const MatmulVariant &v : kQ4kMatmulVariants)
     if (v.kind == want.kind && v.w == want.w && v.nt == want.nt && v.pf == want.pf &&
         v.rt == want.rt) {
@@ -1089,6 +1103,8 @@ static axh_status plan_q4k_matmul(uint32_t n_rows, uint32_t sb_per_row, uint32_t
         std::snprintf(name, cap, "axh_q4k_matmul_st_w%u_k%u_p%u", v.w, v.w / 4u, v.pf);
       else if (v.kind == 5)
         std::snprintf(name, cap, "axh_q4k_matmul_kx_r%u_n%u_k%u_p%u", v.rt, v.nt, v.w, v.pf);
+      else if (v.kind == 8)
+        std::snprintf(name, cap, "axh_q4k_matmul_rm_w%u_r%u_p4", v.w, v.rt);
       else if (v.kind == 7) {
         if (sb_per_row > kSrMaxSb)
           return fail(AXH_ERR_INVALID_ARGUMENT,
@@ -1152,6 +1168,7 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
                        : v.kind == 5 ? kx_lds_bytes(v)
                        : v.kind == 6 ? rs_lds_bytes(v)
                        : v.kind == 7 ? (v.pf == 2 ? 65536u : 131072u) + 2u * v.w * v.nt * 1024u
+                       : v.kind == 8 ? rm_lds_bytes(v)
                                      : 0u;
   if (lds > ctx->core->max_lds)
     return fail(AXH_ERR_INVALID_ARGUMENT, "matmul variant needs more LDS than the device has");
@@ -1160,6 +1177,7 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
                       : v.kind == 5 ? 16u * v.rt
                       : v.kind == 6 ? 16u * v.rt * v.w
                       : v.kind == 7 ? 16u
+                      : v.kind == 8 ? 32u * v.rt * v.w
                                     : 32u * v.w;
   const uint32_t tn = (v.kind == 7 && v.pf == 2 ? 8u : 16u) * v.nt;
   uint64_t gx = (n_rows + tm - 1) / tm;

@@ -103,7 +103,7 @@ def test_one_hot_lcg_fixture_weights(ctx):
         assert np.array_equal(y[:, 0].astype(np.float16).view(np.uint16), w16.view(np.uint16))
 
 
-@pytest.mark.parametrize("batch", [8, 32, 128, 512])
+@pytest.mark.parametrize("batch", [8, 32, 128, 256, 512])
 def test_c5_down_projection_shapes(ctx, batch):
     """14336 x 4096 weights, B f16 activations ~ N(0, 1)."""
     rows, sb = 14336, 16
@@ -132,14 +132,16 @@ def test_every_variant(ctx, axc):
         _check(y, q, xh, rows, sb, batch, f"variant {v}")
 
 
-@pytest.mark.parametrize("rows,sb,batch", [(1, 1, 1), (37, 7, 129), (130, 2, 15)])
+@pytest.mark.parametrize("rows,sb,batch", [(1, 1, 1), (37, 7, 129), (130, 2, 15),
+                                           (300, 3, 260), (1000, 1, 33)])
 def test_tile_kinds_on_odd_shapes(ctx, axc, rows, sb, batch):
-    """The K-split and row-split tile kinds (5, 6) at shapes none of their
-    tiles divide: a single row, superblock and column; more superblocks than
-    a wave's ring holds, a column group of 129; rows past one row tile."""
+    """The K-split, row-split and 32x32 tile kinds (5, 6, 8) at shapes none of
+    their tiles divide: a single row, superblock and column; more superblocks
+    than a wave's ring holds, column groups of 129 and 260; rows past one row
+    tile; a single superblock (four K steps)."""
     q, xh = _inputs(rows * 11 + sb + batch, rows, sb, batch)
     for v in axc.compiled_matmul_variants():
-        if v.kind not in (5, 6):
+        if v.kind not in (5, 6, 8):
             continue
         _say(f"matmul odd shape {rows}x{sb} B={batch} variant {v}")
         y = _run(ctx, q, xh, rows, sb, batch, v)
