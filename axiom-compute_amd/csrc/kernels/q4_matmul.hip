@@ -1047,13 +1047,13 @@ __device__ __forceinline__ void q4k_matmul_rs(const uint8_t *__restrict__ q,
 }
 
 // ---------------------------------------------------------------------------
-// 32 x 32 tiles with wide waves (kind 8, axh_q4k_matmul_rm_w{W}_p4): a
-// workgroup of W waves (one per SIMD) owns 64 * W rows x 128 columns of Y;
-// wave w owns 64 rows (two 32-row MFMA tiles) x 128 columns (four 32-column
-// tiles) and walks all of K in 64-wide steps (one chunk of a superblock) with
-// v_mfma_f32_32x32x16_f16, so each X fragment read from LDS feeds two MFMAs
-// (64 rows, twice the row-split kind's reuse) and each dequantised A fragment
-// four (128 columns).  A ring of 4 LDS buffers, each the step's X tile (128
+// 32 x 32 tiles with wide waves (kind 8, axh_q4k_matmul_rm_w{W}_r{RT}_p4): a
+// workgroup of W waves owns 32 * RT * W rows x 128 columns of Y; wave w owns
+// 32 * RT rows (RT 32-row MFMA tiles) x 128 columns (four 32-column tiles) and
+// walks all of K in 64-wide steps (one chunk of a superblock) with
+// v_mfma_f32_32x32x16_f16, so each X fragment read from LDS feeds RT MFMAs of
+// 32 rows (the row-split kind's 16x16 tiles: 16 rows) and each dequantised A
+// fragment four (128 columns).  A ring of 4 LDS buffers, each the step's X tile (128
 // columns x 64 k, 16 KiB) and every wave's weight pieces (per row: header and
 // the chunk's 32 qs bytes), is filled by direct-to-LDS loads three steps
 // ahead; each step's fragments (X read from LDS, A dequantised) are prepared
