@@ -1053,21 +1053,32 @@ __device__ __forceinline__ void q4k_matmul_rs(const uint8_t *__restrict__ q,
 // walks all of K in 64-wide steps (one chunk of a superblock) with
 // v_mfma_f32_32x32x16_f16, so each X fragment read from LDS feeds RT MFMAs of
 // 32 rows (the row-split kind's 16x16 tiles: 16 rows) and each dequantised A
-// fragment four (128 columns).  A ring of 4 LDS buffers, each the step's X tile (128
-// columns x 64 k, 16 KiB) and every wave's weight pieces (per row: header and
-// the chunk's 32 qs bytes), is filled by direct-to-LDS loads three steps
-// ahead; each step's fragments (X read from LDS, A dequantised) are prepared
-// during the previous step's MFMAs.  Lane l (row l % 32 of a row tile, half h
-// = l / 32) dequantises the
-// qs bytes [16h, 16h + 16) of the chunk: their low nibbles are the A
-// fragments of k-steps 0-1 (k = 16h + 0..15), their high nibbles those of
-// k-steps 2-3 (k = 32 + 16h + ..), each 8 consecutive k, so the X fragment of
-// the same (k-step, half) is one 16-byte piece.  X piece p of column n sits
-// in slot p ^ (n & 7) of the column's 128 bytes, so 8 lanes reading one piece
-// of 8 consecutive columns hit distinct banks.  One barrier per step makes
-// every wave's X of step j + 1 visible and frees the buffer the next loads
-// refill.
-// ---------------------------------------------------------------------------
+// fragment four (128 columns).  A ring of 4 LDS buffers, each the step's X
+// tile (128 columns x 64 k, 16 KiB) and every wave's weight pieces (per row:
+// header and the chunk's 32 qs bytes), is filled by direct-to-LDS loads three
+// steps ahead; each step's fragments (X read from LDS, A dequantised) are
+// prepared during the previous step's MFMAs.  Lane l (row l % 32 of a row
+// tile, half h = l / 32) dequantises the qs bytes [16h, 16h + 16) of the
+// chunk: their low nibbles are the A fragments of k-steps 0-1 (k = 16h +
+// 0..15), their high nibbles those of k-steps 2-3 (k = 32 + 16h + ..), each 8
+// consecutive k, so the X fragment of the same (k-step, half) is one 16-byte
+// piece.  X piece p of column n sits in slot p ^ (n & 7) of the column's 128
+// bytes, so 8 lanes reading one piece of 8 consecutive columns hit distinct
+// banks.  One barrier per step makes every wave's X of step j + 1 visible and
+// frees the buffer the next loads refill.
+// The step loop is unrolled by the ring depth, so a step's ring slot and
+// chunk are compile-time constants: the LDS addresses of the fragment reads
+// are a per-lane base plus immediates, the scale decode of a chunk is
+// specialised, and the direct-to-LDS loads take the step's offset in an SGPR
+// (X: 128 bytes per step, weights: 144 bytes per superblock) over per-lane
+// offsets prepared once.  Each X fragment is refilled for the next step right
+// after the step's last MFMA that reads it, and the next step's
+// dequantisation is written between the MFMAs.  That takes the VALU work per
+// step from 111 to 86 instructions (32 rows) and measured, A/B in one run at
+// 14336 x 4096: B = 256 (4 waves) 44.8 vs 52.8 us, B = 512 (8 waves) 78.5 vs
+// 79.1.  (The compiler's own schedule is kept: a fixed MFMA / LDS read / VALU
+// pattern through sched_group_barrier put dependent MFMAs back to back, and
+// sched_barrier fences between the groups measured even.)
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 template <int W, int RT>
@@ -1082,6 +1093,9 @@ __device__ __forceinline__ void q4k_matmul_rm(const uint8_t *__restrict__ q,
   constexpr int kPerStep = kXPer + kWI;
   constexpr uint32_t kWs = 64u * kWI;             // f32x4 slots of a wave's weight pieces
   constexpr uint32_t kBuf = 16u * 64u + W * kWs;  // f32x4 slots per ring buffer
+  // Offset of loads that must read zeros: past any buffer the runtime passes
+  // (below 4 GiB - 1 MiB), with room for the SGPR step offsets on top.
+  constexpr uint32_t kFar = 0xFFF00000u;
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t r = lane & 31u, h = lane >> 5;
@@ -1093,46 +1107,47 @@ __device__ __forceinline__ void q4k_matmul_rm(const uint8_t *__restrict__ q,
   const uint32_t m0 = blockIdx.x * (32u * RT * W) + 32u * RT * wave, n0 = blockIdx.y * 128u;
 
   // X load role: instruction i = wave + W * u covers columns 8i .. 8i + 7;
-  // lane L loads piece (L & 7) ^ (col & 7) of column 8i + L / 8.
-  uint32_t xoff0[kXPer];
+  // lane L loads piece (L & 7) ^ (col & 7) of column 8i + L / 8.  Step j
+  // adds 128 j bytes (SGPR offset).
+  uint32_t xv0[kXPer];
 #pragma unroll
   for (int u = 0; u < kXPer; ++u) {
     const uint32_t i = wave + (uint32_t)(W * u), col = 8u * i + (lane >> 3);
     const uint32_t p = (lane & 7u) ^ (col & 7u), b = n0 + col;
-    xoff0[u] = b < batch ? (b * K + 8u * p) * 2u : kOob;
+    xv0[u] = b < batch ? (b * K + 8u * p) * 2u : kFar;
   }
-  // Weight load role: piece P = 64m + lane -> row P / 3 of the wave's 64,
-  // part P % 3 (0 the header, 1-2 the 16-byte halves of the chunk's qs).
-  uint32_t woff0[kWI], wpart[kWI];
+  // Weight load role: piece P = 64m + lane -> row P / 3 of the wave's 32 RT,
+  // part P % 3 (0 the header, 1-2 the 16-byte halves of the chunk's qs), one
+  // per-lane offset for each chunk c; superblock j / 4 adds 144 (j / 4) bytes.
+  uint32_t wv0[kWI][4];
 #pragma unroll
   for (int m = 0; m < kWI; ++m) {
-    const uint32_t P = 64u * (uint32_t)m + lane, rr = P / 3u, row = m0 + rr;
-    wpart[m] = P - 3u * rr;
-    woff0[m] = (rr < 32u * RT && row < n_rows) ? row * row_bytes : kOob;
+    const uint32_t P = 64u * (uint32_t)m + lane, rr = P / 3u, part = P - 3u * rr, row = m0 + rr;
+    const uint32_t base = (rr < 32u * RT && row < n_rows) ? row * row_bytes : kFar;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      wv0[m][c] = base == kFar ? kFar : base + (part == 0u ? 0u : 16u * part + 32u * (uint32_t)c);
   }
-  auto issue = [&](uint32_t j) { // step j -> ring buffer j % 4
-    const bool live = j < n_steps;
-    const uint32_t sb = j >> 2, c = j & 3u;
-    f32x4_t *buf = lds + (j & 3u) * kBuf;
+  // step j -> ring buffer j % 4 (a compile-time slot); past the last step the
+  // loads read bytes that are never used, or zeros past the buffers
+  auto issue = [&](uint32_t j, auto slot_c) {
+    constexpr int sl = decltype(slot_c)::value;
+    f32x4_t *buf = lds + sl * kBuf;
 #pragma unroll
     for (int u = 0; u < kXPer; ++u) {
       const uint32_t i = wave + (uint32_t)(W * u);
-      const uint32_t off = (xoff0[u] == kOob || !live) ? kOob : xoff0[u] + 128u * j;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void_t *)(buf + i * 64u), 16, off, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void_t *)(buf + i * 64u), 16, xv0[u],
+                                               128u * j, 0, 0);
     }
     f32x4_t *wb = buf + 16u * 64u + wave * kWs;
 #pragma unroll
-    for (int m = 0; m < kWI; ++m) {
-      const uint32_t off =
-          (woff0[m] == kOob || !live)
-              ? kOob
-              : woff0[m] + sb * 144u + (wpart[m] == 0u ? 0u : 16u * wpart[m] + 32u * c);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(qr, (lds_void_t *)(wb + m * 64), 16, off, 0, 0, 0);
-    }
+    for (int m = 0; m < kWI; ++m)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(qr, (lds_void_t *)(wb + m * 64), 16, wv0[m][sl],
+                                               (j >> 2) * 144u, 0, 0);
   };
-  // A fragments of step j from its ring buffer: af[i][s], s the k-step.
-  auto dequant = [&](uint32_t j, half8_t (&af)[RT][4]) {
-    const f32x4_t *wb = lds + (j & 3u) * kBuf + 16u * 64u + wave * kWs;
+  // A fragments of a step from its ring buffer: af[i][s], s the k-step.
+  auto dequant = [&](const f32x4_t *buf, uint32_t c, half8_t (&af)[RT][4]) {
+    const f32x4_t *wb = buf + 16u * 64u + wave * kWs;
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
       const uint32_t pr = 3u * (32u * (uint32_t)i + r); // the row's three pieces
@@ -1140,7 +1155,7 @@ __device__ __forceinline__ void q4k_matmul_rm(const uint8_t *__restrict__ q,
       const uint4 qv = __builtin_bit_cast(uint4, wb[pr + 1u + h]);
       const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
       uint32_t scp, mp;
-      q4k_scale_min_pair(hd.y, hd.z, hd.w, j & 3u, &scp, &mp);
+      q4k_scale_min_pair(hd.y, hd.z, hd.w, c, &scp, &mp);
       const float d1s = d * (float)(scp & 0xFFu) * 16777216.0f;
       const float d2s = d * (float)(scp >> 8) * 1048576.0f;
       const float m1 = dmin * (float)(mp & 0xFFu), m2 = dmin * (float)(mp >> 8);
@@ -1155,72 +1170,100 @@ __device__ __forceinline__ void q4k_matmul_rm(const uint8_t *__restrict__ q,
       af[i][3] = __builtin_bit_cast(half8_t, make_uint4(hh[2][0], hh[2][1], hh[3][0], hh[3][1]));
     }
   };
-
+  // X fragment (k-step s, column tile t) of this lane: piece p(s) = (s & 1) +
+  // 2h + 4 (s >> 1) of column 32t + r, at f32x4 slot xl[s] + 256 t of a buffer.
+  uint32_t xl[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const uint32_t p = ((uint32_t)s & 1u) + 2u * h + 4u * ((uint32_t)s >> 1);
+    xl[s] = 8u * r + (p ^ (r & 7u));
+  }
   f32x16_t acc[RT][4];
 #pragma unroll
   for (int i = 0; i < RT; ++i)
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[i][t] = (f32x16_t){};
-
-  // fragment slots of this lane: X piece p(s) = (s & 1) + 2h + 4 (s >> 1) of column 32t + r
-  uint32_t xaddr[4][4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const uint32_t col = 32u * (uint32_t)t + r;
-      const uint32_t p = ((uint32_t)s & 1u) + 2u * h + 4u * ((uint32_t)s >> 1);
-      xaddr[t][s] = col * 8u + (p ^ (col & 7u)); // f32x4 slot in a buffer
-    }
-
-  // Every fragment of step j + 1 (X from LDS, A dequantised from the
-  // weight pieces) is prepared while step j's MFMAs issue.
-  auto read_x = [&](uint32_t j, half8_t (&bf)[4][4]) {
-    const f32x4_t *buf = lds + (j & 3u) * kBuf;
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int t = 0; t < 4; ++t) bf[s][t] = __builtin_bit_cast(half8_t, buf[xaddr[t][s]]);
-  };
-  issue(0u);
-  issue(1u);
-  issue(2u);
-  half8_t af[2][RT][4]; // A fragments of steps j and j + 1
-  half8_t bf[2][4][4]; // X fragments of steps j and j + 1
+  issue(0u, std::integral_constant<int, 0>{});
+  issue(1u, std::integral_constant<int, 1>{});
+  issue(2u, std::integral_constant<int, 2>{});
+  half8_t af[2][RT][4]; // A fragments of steps jj and jj + 1
+  half8_t bf[4][4];     // X fragments, each refilled for step jj + 1 once step jj's MFMAs read it
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * kPerStep) : "memory"); // step 0 landed
-  read_x(0u, bf[0]);
-  dequant(0u, af[0]);
-  // Two steps per trip (n_steps is a multiple of 4): fragment indices are
-  // compile-time constants.
-  for (uint32_t j = 0; j < n_steps; j += 2) {
+  dequant(lds, 0u, af[0]);
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const uint32_t jj = j + (uint32_t)e;
-      // own loads of step jj + 1 landed (jj + 2 in flight); after the barrier
-      // every wave's X of step jj + 1 is in LDS and step jj is read
-      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kPerStep) : "memory");
-      issue(jj + 3u); // refills the buffer of step jj - 1
-      dequant(jj + 1u, af[e ^ 1]); // past the last step: zeros, unused
-      read_x(jj + 1u, bf[e ^ 1]);
+  for (int s = 0; s < 4; ++s)
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
+    for (int t = 0; t < 4; ++t) bf[s][t] = __builtin_bit_cast(half8_t, lds[xl[s] + 256u * (uint32_t)t]);
+  // Step jj's MFMAs, with step jj + 1's X fragments read and its A fragments
+  // dequantised between them (per row tile: the scale decode, then the four
+  // qs dwords in low and high halves).
+  auto step = [&](uint32_t jj, auto e_c) {
+    constexpr int e = decltype(e_c)::value; // jj % 4: the ring slot
+    constexpr int sn = (e + 1) & 3;         // slot and chunk of step jj + 1
+    // own loads of step jj + 1 landed (jj + 2 in flight); after the barrier
+    // every wave's X of step jj + 1 is in LDS and step jj - 1's buffer is free
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kPerStep) : "memory");
+    issue(jj + 3u, std::integral_constant<int, (e + 3) & 3>{});
+    const f32x4_t *bufn = lds + sn * kBuf; // past the last step: read, never used
+    const f32x4_t *wb = bufn + 16u * 64u + wave * kWs;
+    uint4 hd[RT], qv[RT];
 #pragma unroll
-        for (int i = 0; i < RT; ++i)
-#pragma unroll
-          for (int t = 0; t < 4; ++t)
-            acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[e][i][s], bf[e][s][t], acc[i][t], 0, 0, 0);
-      // the next step's weight pieces first (the dequantisation waits for
-      // them; LDS returns in order), then its X fragments and dequantisation
-      // between this step's MFMAs
-      __builtin_amdgcn_sched_group_barrier(0x100, 2 * RT, 0); // DS read: weight pieces
-#pragma unroll
-      for (int k = 0; k < 16 * RT; ++k) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // MFMA
-        if (k >= RT && k < RT + 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // DS read: X
-        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0); // VALU
-      }
-      __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < RT; ++i) {
+      const uint32_t pr = 3u * (32u * (uint32_t)i + r); // the row's three pieces
+      hd[i] = __builtin_bit_cast(uint4, wb[pr]);
+      qv[i] = __builtin_bit_cast(uint4, wb[pr + 1u + h]);
     }
+    float dd[RT], dm[RT], d1s[RT], d2s[RT], m1[RT], m2[RT];
+    uint32_t scp[RT], mp[RT], lo[RT][4][2], hi[RT][4][2];
+#pragma unroll
+    for (int k = 0; k < 16 * RT; ++k) {
+      const int s = k / (4 * RT), i = (k >> 2) % RT, t = k & 3;
+      acc[i][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[e & 1][i][s], bf[s][t], acc[i][t], 0, 0, 0);
+      if (i == RT - 1)
+        bf[s][t] = __builtin_bit_cast(half8_t, bufn[xl[s] + 256u * (uint32_t)t]);
+      const int ii = k >> 4, kk = k & 15; // dequantisation work of row tile ii
+      if (kk == 2) {
+        dd[ii] = f16_to_f32(hd[ii].x & 0xFFFFu);
+        dm[ii] = f16_to_f32(hd[ii].x >> 16);
+        q4k_scale_min_pair(hd[ii].y, hd[ii].z, hd[ii].w, (uint32_t)sn, &scp[ii], &mp[ii]);
+      } else if (kk == 3) {
+        d1s[ii] = dd[ii] * (float)(scp[ii] & 0xFFu) * 16777216.0f;
+        d2s[ii] = dd[ii] * (float)(scp[ii] >> 8) * 1048576.0f;
+        m1[ii] = dm[ii] * (float)(mp[ii] & 0xFFu);
+        m2[ii] = dm[ii] * (float)(mp[ii] >> 8);
+      } else if (kk >= 4 && kk < 12) {
+        const int dw = (kk - 4) >> 1;
+        const uint32_t w = dw == 0 ? qv[ii].x : dw == 1 ? qv[ii].y : dw == 2 ? qv[ii].z : qv[ii].w;
+        const uint32_t w8 = w >> 8;
+        if (((kk - 4) & 1) == 0) { // low nibbles: bytes 0, 2 and 1, 3 of the dword
+          const uint32_t lb = w & 0x000F000Fu, hb = w8 & 0x000F000Fu;
+          lo[ii][dw][0] = pack_f16(__builtin_fmaf(lo_half_f16(lb), d1s[ii], -m1[ii]),
+                                   __builtin_fmaf(lo_half_f16(hb), d1s[ii], -m1[ii]));
+          lo[ii][dw][1] = pack_f16(__builtin_fmaf(hi_half_f16(lb), d1s[ii], -m1[ii]),
+                                   __builtin_fmaf(hi_half_f16(hb), d1s[ii], -m1[ii]));
+        } else { // high nibbles
+          const uint32_t lb = w & 0x00F000F0u, hb = w8 & 0x00F000F0u;
+          hi[ii][dw][0] = pack_f16(__builtin_fmaf(lo_half_f16(lb), d2s[ii], -m2[ii]),
+                                   __builtin_fmaf(lo_half_f16(hb), d2s[ii], -m2[ii]));
+          hi[ii][dw][1] = pack_f16(__builtin_fmaf(hi_half_f16(lb), d2s[ii], -m2[ii]),
+                                   __builtin_fmaf(hi_half_f16(hb), d2s[ii], -m2[ii]));
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+      half8_t(&o)[4] = af[(e & 1) ^ 1][i];
+      o[0] = __builtin_bit_cast(half8_t, make_uint4(lo[i][0][0], lo[i][0][1], lo[i][1][0], lo[i][1][1]));
+      o[1] = __builtin_bit_cast(half8_t, make_uint4(lo[i][2][0], lo[i][2][1], lo[i][3][0], lo[i][3][1]));
+      o[2] = __builtin_bit_cast(half8_t, make_uint4(hi[i][0][0], hi[i][0][1], hi[i][1][0], hi[i][1][1]));
+      o[3] = __builtin_bit_cast(half8_t, make_uint4(hi[i][2][0], hi[i][2][1], hi[i][3][0], hi[i][3][1]));
+    }
+  };
+  for (uint32_t j = 0; j < n_steps; j += 4) { // n_steps is a multiple of 4
+    step(j, std::integral_constant<int, 0>{});
+    step(j + 1u, std::integral_constant<int, 1>{});
+    step(j + 2u, std::integral_constant<int, 2>{});
+    step(j + 3u, std::integral_constant<int, 3>{});
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // ring loads past the last step
 
