@@ -764,13 +764,19 @@ __device__ __forceinline__ void q4k_matmul_kx(const uint8_t *__restrict__ q,
 
   // Load roles (fixed per lane).  X: column n0 + 16t + (lane >> 2), piece
   // (lane - rot(col)) & 3 of the 32-k half kk.  Weights: piece P = 64m + lane
-  // -> row P / 3, part P % 3 (0 header, 1-2 qs halves of the chunk).
+  // -> row P / 3, part P % 3 (0 header, 1-2 qs halves of the chunk).  The
+  // step's superblock enters as an SGPR offset (X: 512 bytes, weights: 144
+  // per superblock) over these per-lane offsets; lanes past the matrix or the
+  // batch start far past any buffer, so they read zeros whatever the step.
+  // (A/B in one run, 14336 x 4096: B = 128 28.8-29.4 vs 30.5-31.2 us, B = 64
+  // 22.2 vs 23.6, against per-lane offsets recomputed every step.)
+  constexpr uint32_t kFar = 0xFFF00000u;
   const uint32_t xc = lane >> 2, xp = ((lane & 3u) - kx_xrot(lane >> 2)) & 3u;
   uint32_t xoff0[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const uint32_t b = n0 + 16u * (uint32_t)t + xc;
-    xoff0[t] = b < batch ? (b * K + 64u * c + 8u * xp) * 2u : kOob;
+    xoff0[t] = b < batch ? (b * K + 64u * c + 8u * xp) * 2u : kFar;
   }
   uint32_t woff0[L::kW];
 #pragma unroll
@@ -779,29 +785,26 @@ __device__ __forceinline__ void q4k_matmul_kx(const uint8_t *__restrict__ q,
     const uint32_t row = m0 + r;
     woff0[m] = (r < 16u * RT && row < n_rows)
                    ? row * row_bytes + (part == 0u ? 0u : 16u + 32u * c + 16u * (part - 1u))
-                   : kOob;
+                   : kFar;
   }
 
-  auto issue = [&](uint32_t j) { // step j -> ring buffer j % PF
-    const bool live = j < n_my;
-    const uint32_t tt = j + rot;
-    const uint32_t sb = sb0 + kSbStride * (tt >= n_my ? tt - n_my : tt);
+  // step j -> ring buffer j % PF (steps are issued in order); past the wave's
+  // last step the loads read superblocks of its own range again, never used
+  uint32_t it = rot; // the wave's superblock index of the next step issued
+  auto issue = [&](uint32_t j) {
+    const uint32_t sb = sb0 + kSbStride * it;
+    it = it + 1u == n_my ? 0u : it + 1u;
     f32x4_t *buf = ring + (j % (uint32_t)PF) * kBufSlots;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const uint32_t off =
-            (xoff0[t] == kOob || !live) ? kOob : xoff0[t] + sb * 512u + 64u * (uint32_t)kk;
+      for (int t = 0; t < NT; ++t)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void_t *)(buf + (kk * NT + t) * 64), 16,
-                                                 off, 0, 0, 0);
-      }
+                                                 xoff0[t], sb * 512u + 64u * (uint32_t)kk, 0, 0);
 #pragma unroll
-    for (int m = 0; m < L::kW; ++m) {
-      const uint32_t off = (woff0[m] == kOob || !live) ? kOob : woff0[m] + sb * 144u;
+    for (int m = 0; m < L::kW; ++m)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(qr, (lds_void_t *)(buf + (L::kX + m) * 64), 16,
-                                               off, 0, 0, 0);
-    }
+                                               woff0[m], sb * 144u, 0, 0);
   };
 
   f32x4_t acc[RT][NT];
