@@ -1320,21 +1320,44 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
   const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
   const __amdgpu_buffer_rsrc_t qr = rsrc(q, n_rows * row_bytes);
   const __amdgpu_buffer_rsrc_t xr = rsrc(x, batch * K * 2u);
-  // 16-row blocks b = blockIdx.x + k * gridDim.x.  (Contiguous row ranges
-  // per workgroup, and the last round's blocks split in 8-row halves over
-  // twice the workgroups, both measured slower: 14336 x 4096 x 8, 11.4-12.1
-  // vs 10.9-11.5 us.)
-  const uint32_t n_blocks = (n_rows + 15u) >> 4;
-  const uint32_t n_myb = blockIdx.x < n_blocks ? (n_blocks - 1u - blockIdx.x) / gridDim.x + 1u : 0u;
+  // 16-row blocks b = blockIdx.x + k * gridDim.x.  When the last round's T
+  // blocks would leave half the grid idle (2T <= grid), they are split into
+  // 2T half blocks of 8 rows, one per workgroup: a half block's lane (r, g)
+  // takes row r & 7 and superblock wave * SPW + (r >> 3), so every lane
+  // dequantises one superblock instead of two, and the MFMAs against the X
+  // fragments of the wave's first and second superblock give rows 0..7 and
+  // 8..15 of two tiles whose matching halves are the row's two parts.  At
+  // 14336 rows (896 blocks over 256 workgroups) every workgroup then does 3.5
+  // blocks of work instead of 4 or 3: A/B in one run, 14336 x 4096 x 8 10.23-
+  // 10.30 vs 10.56-10.64 us, x 16 11.43-11.61 vs 11.57-11.64, x 32 13.84-14.03
+  // vs 14.06-14.37.  (Contiguous row ranges per workgroup, and 8-row halves
+  // that kept two superblocks per lane, both measured slower.)
+  const uint32_t n_blocks = (n_rows + 15u) >> 4, G = gridDim.x;
+  const uint32_t n_full = n_blocks / G, n_tail = n_blocks - n_full * G;
+  const bool split = SPW == 2 && n_tail != 0u && 2u * n_tail <= G;
+  const uint32_t n_myb =
+      split ? n_full : (blockIdx.x < n_blocks ? (n_blocks - 1u - blockIdx.x) / G + 1u : 0u);
+  const bool half = split && blockIdx.x < 2u * n_tail;
+  const uint32_t hrow0 = 16u * n_full * G + 8u * blockIdx.x; // the half block's first row
   constexpr uint32_t kXc = XH ? 8u : 16u;    // columns of a group
   const uint32_t n0 = kXc * NC * blockIdx.y; // this workgroup's kXc * NC columns
 
   // Weight loads of step (k, j): row 16 b + r, superblock wave*SPW + j: header
-  // and the 32 qs bytes of chunk g.
+  // and the 32 qs bytes of chunk g.  k == n_myb is the half block (one step).
   uint4 H[2], QA[2], QB[2];
   auto issue = [&](uint32_t k, int j, int slot) {
-    const uint32_t b = blockIdx.x + k * gridDim.x, s = wave * SPW + (uint32_t)j;
-    const uint32_t off = (k < n_myb && s < nsb) ? (16u * b + r) * row_bytes + s * 144u : kOob;
+    uint32_t row, s;
+    bool ok;
+    if (k < n_myb) {
+      row = 16u * (blockIdx.x + k * G) + r;
+      s = wave * SPW + (uint32_t)j;
+      ok = s < nsb;
+    } else {
+      row = hrow0 + (r & 7u);
+      s = wave * SPW + (r >> 3);
+      ok = half && k == n_myb && j == 0 && s < nsb;
+    }
+    const uint32_t off = ok ? row * row_bytes + s * 144u : kOob;
     H[slot] = bload16(qr, off);
     QA[slot] = bload16(qr, off == kOob ? kOob : off + 16u + 32u * g);
     QB[slot] = bload16(qr, off == kOob ? kOob : off + 32u + 32u * g);
@@ -1438,6 +1461,54 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
         const uint32_t col = n0 + kXc * (uint32_t)c + r;
         if ((!XH || r < 8u) && col < batch)
           store_col4(y + (size_t)col * n_rows, 16u * b + 4u * g, n_rows, sum);
+      }
+    }
+  }
+  if (half) { // its loads were issued into slot 0 with the last full block's
+    const uint32_t k = n_myb;
+    f32x4_t acc1[NC]; // tiles against the second superblock's X (rows 8..15 valid)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc1[c] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+    const uint4 hd = H[0];
+    const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
+    uint32_t scp, mp;
+    q4k_scale_min_pair(hd.y, hd.z, hd.w, g, &scp, &mp);
+    const float d1s = d * (float)(scp & 0xFFu) * 16777216.0f;
+    const float d2s = d * (float)(scp >> 8) * 1048576.0f;
+    const float m1 = dmin * (float)(mp & 0xFFu), m2 = dmin * (float)(mp >> 8);
+    const uint32_t w[8] = {QA[0].x, QA[0].y, QA[0].z, QA[0].w, QB[0].x, QB[0].y, QB[0].z, QB[0].w};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      uint32_t l0, l1, h0, h1, l2, l3, h2, h3;
+      dequant_dword(w[2 * t], d1s, m1, d2s, m2, l0, l1, h0, h1);
+      dequant_dword(w[2 * t + 1], d1s, m1, d2s, m2, l2, l3, h2, h3);
+      const half8_t alo = __builtin_bit_cast(half8_t, make_uint4(l0, l1, l2, l3));
+      const half8_t ahi = __builtin_bit_cast(half8_t, make_uint4(h0, h1, h2, h3));
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, xf[c][0][t], acc[c], 0, 0, 0);
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, xf[c][0][t + 4], acc[c], 0, 0, 0);
+        acc1[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, xf[c][1][t], acc1[c], 0, 0, 0);
+        acc1[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, xf[c][1][t + 4], acc1[c], 0, 0, 0);
+      }
+    }
+    // lanes 0..31 hold rows 0..7 of the first tile, lanes 32..63 rows 8..15
+    // of the second: the same output rows, the row's two superblock parts
+    f32x4_t *buf = red + (XH ? 4096u : 8192u) + (k & 1u) * (NW * NC * 64u);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) buf[(wave * NC + (uint32_t)c) * 64u + lane] = lane < 32u ? acc[c] : acc1[c];
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (wave == k % NW && lane < 32u) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        f32x4_t sum = buf[(uint32_t)c * 64u + lane] + buf[(uint32_t)c * 64u + lane + 32u];
+#pragma unroll
+        for (int w2 = 1; w2 < NW; ++w2)
+          sum += buf[((uint32_t)w2 * NC + (uint32_t)c) * 64u + lane] +
+                 buf[((uint32_t)w2 * NC + (uint32_t)c) * 64u + lane + 32u];
+        const uint32_t col = n0 + kXc * (uint32_t)c + r;
+        if ((!XH || r < 8u) && col < batch)
+          store_col4(y + (size_t)col * n_rows, hrow0 + 4u * g, n_rows, sum);
       }
     }
   }

@@ -59,7 +59,10 @@ constexpr MatmulVariant kQ4kMatmulVariants[] = {
     {5, 4, 2, 2, 4},  {5, 4, 2, 3, 4},  {5, 4, 1, 3, 4},  {6, 8, 8, 4, 2},  {6, 8, 8, 3, 2},
     {6, 4, 8, 4, 4},  {6, 8, 4, 4, 2},  {6, 8, 8, 4, 1},  {7, 8, 1, 1, 0},  {7, 8, 2, 1, 0},
     {7, 8, 1, 2, 0},  {8, 8, 8, 4, 1},  {8, 4, 8, 4, 2},  {8, 4, 8, 4, 1},  {8, 2, 8, 4, 2}};
-constexpr uint32_t kMatmulOob = 0xFFFFFF00u; // the kernels' out-of-range offset
+// The matmul kernels read zeros through offsets at or past 0xFFF00000 (with
+// the step offsets on top), and address rows up to 16 past the matrix: q and
+// x must stay below that, with 16 rows to spare.
+constexpr uint64_t kMatmulOob = 0xFFF00000u;
 
 struct MatvecVariant {
   uint32_t rpw, nw, pf, nt;
@@ -1146,8 +1149,8 @@ static axh_status q4k_matmul_check(axh_context *ctx, const void *q, const void *
     return fail(AXH_ERR_INVALID_ARGUMENT, "q and x must be 16-byte and y 4-byte aligned");
   const uint64_t q_bytes = (uint64_t)n_rows * sb_per_row * 144u;
   const uint64_t x_f16_bytes = (uint64_t)batch * sb_per_row * 256u * 2u;
-  if (q_bytes >= kMatmulOob || x_f16_bytes >= kMatmulOob)
-    return fail(AXH_ERR_INVALID_ARGUMENT, "q and f16 x must each be below 4 GiB - 256 B");
+  if (q_bytes + 16ull * sb_per_row * 144u >= kMatmulOob || x_f16_bytes >= kMatmulOob)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q (with 16 rows to spare) and f16 x must each be below 4 GiB - 1 MiB");
   return ok();
 }
 
