@@ -151,13 +151,17 @@ def test_tile_kinds_on_odd_shapes(ctx, axc, rows, sb, batch):
 @pytest.mark.parametrize("rows,sb,batch", [(5000, 13, 13), (4097, 16, 16), (17, 7, 1),
                                            (1000, 16, 3), (70000, 2, 9), (4097, 16, 32),
                                            (333, 11, 19), (70000, 3, 25), (14336, 16, 8),
-                                           (4099, 5, 7)])
+                                           (4099, 5, 7), (7296, 16, 16), (14331, 16, 32)])
 def test_streaming_rows_kind(ctx, axc, rows, sb, batch):
     """Kind 7 (the default up to 32 columns and K <= 4096; 8-column groups up
     to 8 columns, two column groups per workgroup beyond 16 columns): more
     16-row blocks than workgroups (several per workgroup), a partial last
     block, rows not a multiple of 4 (scalar stores), waves whose superblocks
-    lie past the row (K < 4096), a single column."""
+    lie past the row (K < 4096), a single column.  On a 256-CU grid the last
+    round's blocks become 8-row half blocks where they fill at most half of it
+    (14336 rows: exactly half; 4097, 5000, 70000: fewer; 14331 and 5000: the
+    last half block partly past the matrix) and stay whole where they fill
+    more (7296 rows: 200 of 256)."""
     assert axc.q4k_matmul_kernel_name(rows, sb, batch).startswith("axh_q4k_matmul_sr_w8_s2")
     _say(f"matmul streaming rows {rows}x{sb * 256} B={batch}")
     q, xh = _inputs(rows + sb * 5 + batch, rows, sb, batch)
