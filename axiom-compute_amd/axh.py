@@ -312,7 +312,9 @@ def q4k_matvec_kernel_name(n_rows: int, sb_per_row: int,
 class MatmulVariant:
     """Strategy holes of the batched matmul kernels (0 = default).  kind: 1
     LDS-tiled, 2 register A, 3 K-split, 4 streaming, 5 K-split tile, 6
-    row-split tile (row_tiles is kinds 5 and 6's only)."""
+    row-split tile, 7 streaming rows (K <= 4096), 8 32x32 tiles; row_tiles
+    is kinds 5, 6 and 8's only.  The default kind follows the grid each kind
+    would launch on 256 CUs (q4k_matmul_kernel_name names the choice)."""
 
     kind: int = 0
     waves_per_workgroup: int = 0

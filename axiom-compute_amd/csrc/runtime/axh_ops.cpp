@@ -1,6 +1,7 @@
 // Q4_0 / Q4_K_M operations over resident device buffers: variant selection
 // (the strategy holes), LDS tile sizing, grid shape and launch of the
 // builtin gfx950 kernels in q4_matvec.hip.
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -1032,28 +1033,57 @@ static uint32_t rm_lds_bytes(const MatmulVariant &v) {
 // staging them through 128 KiB of LDS: K up to 16 superblocks (8 waves x 2).
 constexpr uint32_t kSrMaxSb = 16;
 
+// The default matmul kind follows the grid each kind would launch, counted in
+// MI355X's 256 CUs (a constant, so that the choice and its kernel name do not
+// depend on the device a query runs on).  Measured over 60 shapes (1024 to
+// 14336 rows, K = 4096 and 14336, 8 to 512 columns, every compiled variant):
+// the choice below is the fastest variant at 59 and within 2% at the last.
+constexpr uint64_t kMatmulCus = 256;
+// Workgroups the tile kinds (5 and 8) need before their tile size matters
+// less than filling the chip: 5/8 of the CUs.  Below it, more and smaller
+// tiles win (4096 x 4096 x 256: 16-row x 64-column K-split tiles in 256
+// workgroups 21.5 us, 32 x 32 MFMA tiles in 64 workgroups 37.6).
+constexpr uint64_t kMatmulFill = 160;
+
 static MatmulVariant q4k_matmul_default(uint32_t n_rows, uint32_t batch, uint32_t nsb) {
-  (void)n_rows;
-  // kind 7 against the K-split tile kind at 14336 x 4096 (A/B in one run):
-  // B = 8 11.2 vs 14.2 us, B = 16 11.8 vs 14.6, B = 32 (two column groups per
-  // workgroup) 15.0 vs 16.0; at B = 64 the K-split tile kind stays ahead.  Up
-  // to 8 columns its 8-column groups (prefetch 2: X staged through 64 KiB)
-  // are faster still, one workgroup per CU (A/B in one run: B = 8 10.93 vs
-  // 11.50 us, B = 4 10.70 vs 11.11, B = 1 10.64 vs 11.01; two workgroups per
-  // CU 12.6, 12.1 and 11.6).
-  if (batch <= 8 && nsb <= kSrMaxSb) return {7, 8, 1, 2, 0};
-  if (batch <= 16 && nsb <= kSrMaxSb) return {7, 8, 1, 1, 0};
-  if (batch <= 32 && nsb <= kSrMaxSb) return {7, 8, 2, 1, 0};
-  if (batch <= 16) return {5, 4, 1, 3, 4};
-  if (batch <= 32) return {5, 4, 2, 2, 4};
-  if (batch <= 64) return {5, 4, 4, 2, 4};
-  if (batch <= 128) return {5, 4, 8, 2, 4};
-  // kind 8 (32 x 32 MFMA tiles) against the row-split kind at 14336 x 4096
-  // (A/B in one run): B = 512 74.1 us (8 waves of 32 rows) vs 83-94, B = 256
-  // 49.3 (4 waves of 32 rows) vs 52.1; at B = 128 the K-split tile kind stays
-  // ahead (31.3 vs 46.8).
-  if (batch <= 256) return {8, 4, 8, 4, 1};
-  return {8, 8, 8, 4, 1};
+  const auto groups = [&](uint32_t rows_per_wg, uint32_t cols_per_wg) {
+    return (uint64_t)((n_rows + rows_per_wg - 1) / rows_per_wg) *
+           ((batch + cols_per_wg - 1) / cols_per_wg);
+  };
+  if (nsb <= kSrMaxSb) {
+    // Kind 7 runs one workgroup per CU over the 16-row blocks of each column
+    // group.  The narrowest group (8, 16 or 32 columns) whose grid is one
+    // resident wave wins: 14336 x 4096 at B = 8 10.9 us, 16 11.8 and 32 15.0
+    // against the K-split tile kind's 14.2, 14.6 and 16.0; 1024 x 4096 x 64
+    // 5.5 us with 16-column groups against 6.9 with 32 and 13.2 as tiles.
+    const uint64_t per_group = std::min<uint64_t>(kMatmulCus, (n_rows + 15u) / 16u);
+    if (per_group * ((batch + 7u) / 8u) <= kMatmulCus) return {7, 8, 1, 2, 0};
+    if (per_group * ((batch + 15u) / 16u) <= kMatmulCus) return {7, 8, 1, 1, 0};
+    if (per_group * ((batch + 31u) / 32u) <= kMatmulCus) return {7, 8, 2, 1, 0};
+    // Up to two blocks of 32 columns per CU it still beats the tiles (4096 x
+    // 4096 x 64 13.8 us against 14.7; 2048 x 4096 x 128 13.5 against 14.9),
+    // not at four (8192 x 4096 x 64 18.6 against 16.3).
+    if (groups(16, 32) <= 2 * kMatmulCus) return {7, 8, 2, 1, 0};
+  }
+  // The K-split kind (32-row tiles, K over 8 waves) wherever its grid is one
+  // wave: long rows over few of them (4096 x 14336 at B = 8 28.9 us and 32
+  // 35.2 against the K-split tile kind's 39.4 and 40.7; 1024 x 14336 x 128
+  // 34.8 against 40.2).
+  if (groups(32, 16) <= kMatmulCus) return {3, 8, 1, 1, 0};
+  // kind 8 (32 x 32 MFMA tiles) where its rows fill the chip: 14336 x 4096 x
+  // 512 74.1 us (8 waves of 32 rows) against 83-94 for the row-split kind,
+  // B = 256 49.3 (4 waves of 32 rows) against 52.1; 8192 x 4096 x 512 46.0 us
+  // with 4 waves against 60.7 as K-split tiles.
+  if (batch > 256 && groups(256, 128) >= kMatmulFill) return {8, 8, 8, 4, 1};
+  if (batch > 128 && groups(128, 128) >= kMatmulFill) return {8, 4, 8, 4, 1};
+  // The K-split tile kind: up to 128 columns per workgroup, halved until the
+  // grid fills (4096 x 14336 x 64: one column tile 41.3 us against four
+  // 58.8; 4096 x 11008 x 128: two 37.9 against eight 76.5).  Two column
+  // tiles prefetch 3 steps at K > 4096 (4096 x 14336 x 128 45.8 us against
+  // 47.6), 2 at K <= 4096 (4096 x 4096 x 128 16.0 against 16.3).
+  uint32_t nt = batch <= 16 ? 1u : batch <= 32 ? 2u : batch <= 64 ? 4u : 8u;
+  while (nt > 1 && groups(64, 16 * nt) < kMatmulFill) nt /= 2;
+  return {5, 4, nt, nt == 1 || (nt == 2 && nsb > kSrMaxSb) ? 3u : 2u, 4};
 }
 
 uint32_t axh_q4k_matmul_variant_count(void) {

@@ -387,7 +387,8 @@ typedef struct axh_q4_matmul_variant {
     uint32_t kind;                /* 1 LDS-tiled, 2 register A, 3 K-split, 4 streaming,
                                      5 K-split tile, 6 row-split tile, 7 streaming rows
                                      (K <= 4096), 8 32x32 tiles (128 columns per
-                                     workgroup); 0 = default */
+                                     workgroup); 0 = default, chosen by the grid
+                                     each kind launches on 256 CUs */
     uint32_t waves_per_workgroup; /* kinds 1-2: 32 rows per wave; 3, 5, 7: waves splitting K;
                                      4: waves; 6, 8: waves of row_tiles row tiles each */
     uint32_t col_tiles;           /* 16-column MFMA tiles per workgroup (kind 8: 8) */

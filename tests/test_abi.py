@@ -200,11 +200,13 @@ def test_context_without_gpu_reports_typed_error(axc):
 
 
 def test_matmul_kernel_selection(axc):
-    """Defaults per batch: the K-split tile kind (its LDS ring does not grow
-    with K) with all columns in one group up to 128, register A beyond."""
+    """Defaults by the grid each kind would launch on 256 CUs: streaming rows
+    (kind 7) in the narrowest column groups that keep its grid one resident
+    wave, the K-split kind where its grid is one wave, 32 x 32 MFMA tiles where
+    their rows fill 160 workgroups, else K-split tiles with their columns
+    halved until the grid fills."""
     name = axc.q4k_matmul_kernel_name
-    # up to 16 columns and K <= 4096: streaming rows; longer rows: the K-split tile
-    # up to 8 columns in 8-column groups (X staged through 64 KiB)
+    # K <= 4096, up to 8 columns of 14336 rows: 8-column groups (X staged through 64 KiB)
     assert name(14336, 16, 8) == "axh_q4k_matmul_sr_w8_s2_h"
     assert name(14336, 1, 1) == "axh_q4k_matmul_sr_w8_s2_h"
     assert name(14336, 16, 8, axc.MatmulVariant(7, 8, 1, 1)) == "axh_q4k_matmul_sr_w8_s2"
@@ -213,15 +215,34 @@ def test_matmul_kernel_selection(axc):
     assert name(14336, 16, 16, axc.MatmulVariant(7, 8, 1, 2)) == "axh_q4k_matmul_sr_w8_s2_h"
     assert name(14336, 16, 32) == "axh_q4k_matmul_sr_w8_s2_n2"  # two column groups
     assert name(14336, 16, 17) == "axh_q4k_matmul_sr_w8_s2_n2"
-    assert name(4096, 56, 8) == "axh_q4k_matmul_kx_r4_n1_k4_p3"
-    assert name(4096, 17, 16) == "axh_q4k_matmul_kx_r4_n1_k4_p3"
+    # fewer rows: narrower groups still fit one wave, and kind 7 goes past 32 columns
+    assert name(1024, 16, 32) == "axh_q4k_matmul_sr_w8_s2_h"  # 64 blocks x 4 groups
+    assert name(2048, 16, 32) == "axh_q4k_matmul_sr_w8_s2"
+    assert name(1024, 16, 64) == "axh_q4k_matmul_sr_w8_s2"
+    assert name(4096, 16, 64) == "axh_q4k_matmul_sr_w8_s2_n2"  # two blocks of 32 columns per CU
+    assert name(8192, 16, 64) == "axh_q4k_matmul_kx_r4_n2_k4_p2"  # four: K-split tiles
+    # K > 4096 over few rows: the K-split kind while its grid is one wave
+    assert name(4096, 56, 8) == "axh_q4k_matmul_ks_k8_n1_p1"
+    assert name(4096, 17, 16) == "axh_q4k_matmul_ks_k8_n1_p1"
     with pytest.raises(axc.DispatchError):  # kind 7 keeps K <= 4096 of X in registers
         name(4096, 17, 16, axc.MatmulVariant(7, 8, 1, 1))
-    assert name(4096, 56, 32) == "axh_q4k_matmul_kx_r4_n2_k4_p2"
+    assert name(4096, 56, 32) == "axh_q4k_matmul_ks_k8_n1_p1"  # 128 x 2 workgroups
+    assert name(1024, 56, 128) == "axh_q4k_matmul_ks_k8_n1_p1"
+    assert name(8192, 56, 32) == "axh_q4k_matmul_kx_r4_n1_k4_p3"  # 256 x 2: K-split tiles
+    assert name(14336, 56, 8) == "axh_q4k_matmul_kx_r4_n1_k4_p3"
+    assert name(14336, 56, 32) == "axh_q4k_matmul_kx_r4_n2_k4_p3"  # prefetch 3 at K > 4096
+    # K-split tiles, columns halved until 160 workgroups
     assert name(14336, 16, 64) == "axh_q4k_matmul_kx_r4_n4_k4_p2"
     assert name(14336, 16, 128) == "axh_q4k_matmul_kx_r4_n8_k4_p2"
+    assert name(4096, 16, 128) == "axh_q4k_matmul_kx_r4_n2_k4_p2"
+    assert name(4096, 56, 128) == "axh_q4k_matmul_kx_r4_n2_k4_p3"
+    assert name(4096, 56, 64) == "axh_q4k_matmul_kx_r4_n1_k4_p3"
+    # 32 x 32 MFMA tiles where their rows fill the grid
     assert name(14336, 16, 256) == "axh_q4k_matmul_rm_w4_r1_p4"
     assert name(14336, 16, 512) == "axh_q4k_matmul_rm_w8_r1_p4"
+    assert name(8192, 16, 512) == "axh_q4k_matmul_rm_w4_r1_p4"  # 8 waves: 128 workgroups
+    assert name(4096, 16, 512) == "axh_q4k_matmul_kx_r4_n8_k4_p2"
+    assert name(4096, 16, 256) == "axh_q4k_matmul_kx_r4_n4_k4_p2"
     assert name(14336, 16, 512, axc.MatmulVariant(6, 8, 8, 3, 2)) == "axh_q4k_matmul_rs_w8_r2_n8_p3"
     assert name(14336, 16, 512, axc.MatmulVariant(8, 4, 8, 4, 2)) == "axh_q4k_matmul_rm_w4_r2_p4"
     assert name(14336, 16, 512, axc.MatmulVariant(1, 2, 2, 1)) == "axh_q4k_matmul_w2_n2"

@@ -123,6 +123,23 @@ def test_edge_shapes(ctx, rows, sb, batch):
     _check(y, q, xh, rows, sb, batch, f"edge {rows}x{sb} B={batch}")
 
 
+@pytest.mark.parametrize("rows,sb,batch,kernel", [(1024, 16, 250, "sr_w8_s2_n2"),
+                                                  (2000, 16, 100, "sr_w8_s2_n2"),
+                                                  (1000, 16, 60, "sr_w8_s2"),
+                                                  (1024, 56, 128, "ks_k8_n1_p1"),
+                                                  (4000, 56, 30, "ks_k8_n1_p1"),
+                                                  (4096, 56, 100, "kx_r4_n2_k4_p3")])
+def test_grid_fill_defaults(ctx, axc, rows, sb, batch, kernel):
+    """The defaults that follow from the grid on few rows: streaming rows past
+    32 columns (several column groups, the last one partial), the K-split kind
+    at K > 4096 up to 128 columns, K-split tiles with their columns halved."""
+    assert axc.q4k_matmul_kernel_name(rows, sb, batch) == "axh_q4k_matmul_" + kernel
+    _say(f"matmul default {kernel} {rows}x{sb * 256} B={batch}")
+    q, xh = _inputs(rows + 3 * sb + 5 * batch, rows, sb, batch)
+    y = _run(ctx, q, xh, rows, sb, batch)
+    _check(y, q, xh, rows, sb, batch, f"default {kernel} {rows}x{sb} B={batch}")
+
+
 def test_every_variant(ctx, axc):
     rows, sb, batch = 200, 3, 40
     q, xh = _inputs(91, rows, sb, batch)
