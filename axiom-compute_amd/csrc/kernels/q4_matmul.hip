@@ -12,34 +12,19 @@
 // common_helpers.rs:437-454) and then rounded once to f16 (RN_f16(w32)).
 // f16 x f16 products are exact in the f32 accumulators of the MFMA.
 //
-// Seven kernel kinds (the runtime picks per batch size; the others stay
-// reachable as strategy variants):
-//   * K-split tile (axh_q4k_matmul_kx_...; the default from 33 to 128
-//     columns, and up to 32 columns when K > 4096):
-//     the waves of a workgroup split K, each streaming raw weight bytes and
-//     X through a private LDS ring filled by coalesced direct-to-LDS loads;
-//     see q4k_matmul_kx;
-//   * LDS-tiled (axh_q4k_matmul_w{W}_n{NT}): a workgroup of W waves owns
-//     TM = 32*W rows and TN = 16*NT columns of Y; per 128-wide K step (half a
-//     superblock) every thread dequantises one quarter superblock (32 qs
-//     bytes = 64 weights) of one row into the LDS tile As[TM][128], the
-//     threads copy the X tile [TN][128] into LDS, and each wave runs
-//     v_mfma_f32_16x16x32_f16 over its 32 x TN sub-tile while the next
-//     step's global loads are in flight;
-//   * register-A (axh_q4k_matmul_rf_...): each lane dequantises exactly the
-//     A fragments it feeds the MFMA, X is double-buffered in LDS;
-//   * row-split tile (axh_q4k_matmul_rs_...; the default beyond 128 columns):
-//     eight waves each own their rows of a wide tile and walk all of K, the X
-//     tile shared through an LDS ring; see q4k_matmul_rs;
-//   * K-split (axh_q4k_matmul_ks_...): the waves of a workgroup share one
-//     32-row tile and split K, summing in LDS;
-//   * streaming (axh_q4k_matmul_st_...): persistent, 16 columns of the whole
-//     K staged once in LDS;
-//   * streaming rows (axh_q4k_matmul_sr_...; the default up to 32 columns
-//     and K <= 4096): persistent, K split across the waves, X fragments kept
-//     in VGPRs, weights streamed like the matvec; see q4k_matmul_sr.
-// LDS rows are padded to 136 halves (272 bytes) so that 16 lanes reading
-// 16-byte fragments of 16 consecutive rows hit 64 distinct banks.
+// Four kernel kinds; the runtime picks one by the grid each would launch
+// (the others stay reachable as strategy variants):
+//   * streaming rows (axh_q4k_matmul_sr_..., kind 7; K <= 4096): persistent,
+//     K split across the waves, X fragments kept in VGPRs, weights streamed
+//     like the matvec; see q4k_matmul_sr;
+//   * K-split (axh_q4k_matmul_ks_..., kind 3): the waves of a workgroup share
+//     one 32-row tile and split K, summing in LDS; see q4k_matmul_ks;
+//   * K-split tile (axh_q4k_matmul_kx_..., kind 5): the waves of a workgroup
+//     split K, each streaming raw weight bytes and X through a private LDS
+//     ring filled by coalesced direct-to-LDS loads; see q4k_matmul_kx;
+//   * 32 x 32 tiles (axh_q4k_matmul_rm_..., kind 8): waves of 32-row MFMA
+//     tiles over 128 columns, X and weights through a 4-deep LDS ring; see
+//     q4k_matmul_rm.
 #include "q4_common.h"
 
 using namespace axh;
@@ -63,8 +48,6 @@ struct MatmulArgs {
 
 namespace {
 
-constexpr int kKStep = 128;   // K per LDS step (half a superblock)
-constexpr int kLd = 136;      // LDS row stride in halves (128 + 8 pad)
 constexpr uint32_t kOob = 0xFFFFFF00u; // out-of-range buffer offset: loads return zeros
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_t bytes) {
@@ -126,115 +109,6 @@ __device__ __forceinline__ void store_col4(float *ycol, uint32_t r0, uint32_t n_
   }
 }
 
-template <int W, int NT>
-__device__ __forceinline__ void q4k_matmul(const uint8_t *__restrict__ q,
-                                           const uint16_t *__restrict__ x,
-                                           float *__restrict__ y, const MatmulArgs a) {
-  constexpr int TM = 32 * W, TN = 16 * NT;
-  constexpr int kXChunks = TN * (kKStep / 8);        // 16-byte chunks of the X tile
-  constexpr int kXPer = (kXChunks + 64 * W - 1) / (64 * W);
-  __shared__ __attribute__((aligned(16))) _Float16 As[TM * kLd];
-  __shared__ __attribute__((aligned(16))) _Float16 Xs[TN * kLd];
-
-  const uint32_t tid = threadIdx.x, lane = tid & 63u;
-  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t n_rows = a.n_rows, nsb = a.sb_per_row, batch = a.batch;
-  const uint32_t m0 = blockIdx.x * TM, n0 = blockIdx.y * TN;
-  const uint32_t K = nsb * 256u;
-  const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
-  const __amdgpu_buffer_rsrc_t qr = rsrc(q, n_rows * row_bytes);
-  const __amdgpu_buffer_rsrc_t xr = rsrc(x, batch * K * 2u);
-
-  // Dequantisation role: row m0 + drow, quarter dq of each 128-wide K step.
-  const uint32_t drow = tid >> 1, dq = tid & 1u;
-  const uint32_t grow = m0 + drow;
-  const uint32_t row_off = grow < n_rows ? grow * row_bytes : kOob;
-
-  f32x4_t acc[2][NT];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < NT; ++j) acc[i][j] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
-
-  uint4 hd, qa, qb, xv[kXPer];
-  auto load_step = [&](uint32_t ks) {
-    const uint32_t sb = ks >> 1, c = 2u * (ks & 1u) + dq;
-    const uint32_t off = row_off == kOob ? kOob : row_off + sb * (uint32_t)kQ4kSbBytes;
-    hd = bload16(qr, off);
-    qa = bload16(qr, off == kOob ? kOob : off + 16u + 32u * c);
-    qb = bload16(qr, off == kOob ? kOob : off + 32u + 32u * c);
-#pragma unroll
-    for (int i = 0; i < kXPer; ++i) {
-      const uint32_t chunk = tid + (uint32_t)i * (64u * W);
-      const uint32_t n = chunk >> 4, kc = chunk & 15u, b = n0 + n;
-      const uint32_t xoff =
-          (chunk < (uint32_t)kXChunks && b < batch) ? (b * K + ks * kKStep + kc * 8u) * 2u : kOob;
-      xv[i] = bload16(xr, xoff);
-    }
-  };
-
-  const uint32_t n_steps = nsb * 2u;
-  load_step(0);
-  for (uint32_t ks = 0; ks < n_steps; ++ks) {
-    __syncthreads(); // the previous step's fragment reads are done
-    {
-      const uint32_t c = 2u * (ks & 1u) + dq;
-      uint32_t scp, mp;
-      q4k_scale_min_pair(hd.y, hd.z, hd.w, c, &scp, &mp);
-      const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
-      const float d1s = d * (float)(scp & 0xFFu) * 16777216.0f; // low nibbles: q * 2^-24
-      const float d2s = d * (float)(scp >> 8) * 1048576.0f;     // high nibbles: q * 2^-20
-      const float m1 = dmin * (float)(mp & 0xFFu), m2 = dmin * (float)(mp >> 8);
-      const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-      _Float16 *dst = As + drow * kLd + 64u * dq;
-#pragma unroll
-      for (int t = 0; t < 8; t += 2) {
-        uint32_t l0, l1, h0, h1, l2, l3, h2, h3;
-        dequant_dword(w[t], d1s, m1, d2s, m2, l0, l1, h0, h1);
-        dequant_dword(w[t + 1], d1s, m1, d2s, m2, l2, l3, h2, h3);
-        *reinterpret_cast<uint4 *>(dst + 4 * t) = make_uint4(l0, l1, l2, l3);
-        *reinterpret_cast<uint4 *>(dst + 32 + 4 * t) = make_uint4(h0, h1, h2, h3);
-      }
-#pragma unroll
-      for (int i = 0; i < kXPer; ++i) {
-        const uint32_t chunk = tid + (uint32_t)i * (64u * W);
-        if (chunk < (uint32_t)kXChunks)
-          *reinterpret_cast<uint4 *>(Xs + (chunk >> 4) * kLd + (chunk & 15u) * 8u) = xv[i];
-      }
-    }
-    __syncthreads();
-    if (ks + 1u < n_steps) load_step(ks + 1u); // in flight during the MFMAs
-    const uint32_t fr = lane & 15u, fk = 8u * (lane >> 4);
-#pragma unroll
-    for (int kk = 0; kk < kKStep / 32; ++kk) {
-      half8_t af[2], bf[NT];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        af[i] = *reinterpret_cast<const half8_t *>(As + (wave * 32u + 16u * i + fr) * kLd +
-                                                   32u * kk + fk);
-#pragma unroll
-      for (int j = 0; j < NT; ++j)
-        bf[j] = *reinterpret_cast<const half8_t *>(Xs + (16u * j + fr) * kLd + 32u * kk + fk);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < NT; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-  }
-
-  // C fragment: lane holds column (lane % 16) and rows 4 * (lane / 16) + 0..3.
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const uint32_t b = n0 + 16u * j + (lane & 15u);
-      const uint32_t r0 = m0 + wave * 32u + 16u * i + 4u * (lane >> 4);
-      if (b >= batch) continue;
-      store_col4(y + (size_t)b * n_rows, r0, n_rows, acc[i][j]);
-    }
-}
-
 __device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
   const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b32(r, (int)off + 4, 0, 0);
@@ -242,184 +116,26 @@ __device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 }
 
 // ---------------------------------------------------------------------------
-// Register-fragment variant.  Each lane dequantises exactly the A fragments
-// it feeds to v_mfma_f32_16x16x32_f16 (row lane%16 of a 16-row tile,
-// k = 32*kk + 8*(lane/16) + 0..7), so A never goes through LDS.  In a
-// 128-wide K step of superblock sb (half h = step%2) the lane reads, per
-// 16-row tile, the row's 16-byte header and the 8 qs bytes
-// [32c + 8g, 32c + 8g + 8) for c = 2h and 2h+1: low nibbles feed the
-// fragments of sub-blocks 2c (kk = 2(c-2h)), high nibbles those of 2c+1.
-// X fragments come straight from global memory (kXLds = false; every wave
-// reads the same lines through L1) or from a double-buffered LDS tile
-// filled by the whole workgroup (kXLds = true).  Loads run PF steps ahead
-// in a register ring.
+// K-split variant for small batches (memory- and dequant-bound): the KS waves
+// of a workgroup share one 32 x TN output tile and take interleaved 128-wide
+// K steps (half a superblock; wave w: steps w, w + KS, ...).  Each lane
+// dequantises exactly the A fragments it feeds to v_mfma_f32_16x16x32_f16
+// (row lane%16 of a 16-row tile, k = 32*kk + 8*(lane/16) + 0..7), so A never
+// goes through LDS: in step ks of superblock sb (half h = ks%2) the lane
+// reads, per 16-row tile, the row's 16-byte header and the 8 qs bytes
+// [32c + 8g, 32c + 8g + 8) for c = 2h and 2h+1, whose low nibbles feed the
+// fragments of sub-block 2c and high nibbles those of 2c+1.  X fragments
+// come straight from global memory.  Loads run PF steps ahead in a register
+// ring.  The KS partial tiles are summed in LDS in wave order
+// (deterministic) by wave 0.
 // ---------------------------------------------------------------------------
-template <int NT, int XPER, bool kXLds>
-struct RfStep {
+template <int NT>
+struct KsStep {
   uint4 hd[2];
   uint2 qlo[2], qhi[2];
-  uint4 xv[kXLds ? XPER : 4 * NT];
+  uint4 xv[4 * NT];
 };
 
-template <int W, int NT, int PF, bool kXLds>
-__device__ __forceinline__ void q4k_matmul_rf(const uint8_t *__restrict__ q,
-                                              const uint16_t *__restrict__ x,
-                                              float *__restrict__ y, const MatmulArgs a) {
-  constexpr int TM = 32 * W, TN = 16 * NT;
-  constexpr int kXChunks = TN * (kKStep / 8);
-  constexpr int kXPer = (kXChunks + 64 * W - 1) / (64 * W);
-  __shared__ __attribute__((aligned(16))) _Float16 Xs[kXLds ? 2 * TN * kLd : 8];
-
-  const uint32_t tid = threadIdx.x, lane = tid & 63u;
-  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t n_rows = a.n_rows, nsb = a.sb_per_row, batch = a.batch;
-  const uint32_t m0 = blockIdx.x * TM, n0 = blockIdx.y * TN;
-  const uint32_t K = nsb * 256u;
-  const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
-  const __amdgpu_buffer_rsrc_t qr = rsrc(q, n_rows * row_bytes);
-  const __amdgpu_buffer_rsrc_t xr = rsrc(x, batch * K * 2u);
-  const uint32_t fr = lane & 15u, g = lane >> 4;
-
-  uint32_t row_off[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const uint32_t row = m0 + wave * 32u + 16u * (uint32_t)i + fr;
-    row_off[i] = row < n_rows ? row * row_bytes : kOob;
-  }
-  // X fragment / chunk offsets of step 0 (step ks adds ks * 256 bytes)
-  uint32_t xoff0[kXLds ? kXPer : NT];
-  if constexpr (kXLds) {
-#pragma unroll
-    for (int i = 0; i < kXPer; ++i) {
-      const uint32_t chunk = tid + (uint32_t)i * (64u * W);
-      const uint32_t n = chunk >> 4, kc = chunk & 15u, b = n0 + n;
-      xoff0[i] = (chunk < (uint32_t)kXChunks && b < batch) ? (b * K + kc * 8u) * 2u : kOob;
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const uint32_t b = n0 + 16u * (uint32_t)j + fr;
-      xoff0[j] = b < batch ? (b * K + 8u * g) * 2u : kOob;
-    }
-  }
-
-  auto load_step = [&](RfStep<NT, kXPer, kXLds> &S, uint32_t ks) {
-    const uint32_t sb = ks >> 1, h = ks & 1u;
-    const bool live = ks < 2u * nsb;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t base = (row_off[i] == kOob || !live) ? kOob : row_off[i] + sb * 144u;
-      S.hd[i] = bload16(qr, base);
-      const uint32_t qo = 16u + 64u * h + 8u * g;
-      S.qlo[i] = bload8(qr, base == kOob ? kOob : base + qo);
-      S.qhi[i] = bload8(qr, base == kOob ? kOob : base + qo + 32u);
-    }
-    if constexpr (kXLds) {
-#pragma unroll
-      for (int i = 0; i < kXPer; ++i)
-        S.xv[i] = bload16(xr, (xoff0[i] == kOob || !live) ? kOob : xoff0[i] + ks * 256u);
-    } else {
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-        for (int j = 0; j < NT; ++j)
-          S.xv[kk * NT + j] =
-              bload16(xr, (xoff0[j] == kOob || !live) ? kOob : xoff0[j] + ks * 256u + 64u * kk);
-    }
-  };
-
-  f32x4_t acc[2][NT];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < NT; ++j) acc[i][j] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
-
-  RfStep<NT, kXPer, kXLds> S[PF];
-#pragma unroll
-  for (int p = 0; p < PF; ++p) load_step(S[p], (uint32_t)p);
-
-  const uint32_t n_steps = (2u * nsb + PF - 1) / PF * PF;
-  for (uint32_t ks0 = 0; ks0 < n_steps; ks0 += PF) {
-#pragma unroll
-    for (int p = 0; p < PF; ++p) {
-      const uint32_t ks = ks0 + (uint32_t)p;
-      const uint32_t h = ks & 1u;
-      // A fragments of this step: [tile][kk]
-      half8_t af[2][4];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const uint4 hd = S[p].hd[i];
-        const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-          const uint32_t c = 2u * h + (uint32_t)cc;
-          uint32_t scp, mp;
-          q4k_scale_min_pair(hd.y, hd.z, hd.w, c, &scp, &mp);
-          const float d1s = d * (float)(scp & 0xFFu) * 16777216.0f;
-          const float d2s = d * (float)(scp >> 8) * 1048576.0f;
-          const float m1 = dmin * (float)(mp & 0xFFu), m2 = dmin * (float)(mp >> 8);
-          const uint2 qw = cc == 0 ? S[p].qlo[i] : S[p].qhi[i];
-          uint32_t l0, l1, h0, h1, l2, l3, h2, h3;
-          dequant_dword(qw.x, d1s, m1, d2s, m2, l0, l1, h0, h1);
-          dequant_dword(qw.y, d1s, m1, d2s, m2, l2, l3, h2, h3);
-          af[i][2 * cc] = __builtin_bit_cast(half8_t, make_uint4(l0, l1, l2, l3));
-          af[i][2 * cc + 1] = __builtin_bit_cast(half8_t, make_uint4(h0, h1, h2, h3));
-        }
-      }
-      half8_t bfr[4][NT];
-      if constexpr (kXLds) {
-        _Float16 *xb = Xs + (ks & 1u) * (TN * kLd);
-#pragma unroll
-        for (int i = 0; i < kXPer; ++i) {
-          const uint32_t chunk = tid + (uint32_t)i * (64u * W);
-          if (chunk < (uint32_t)kXChunks)
-            *reinterpret_cast<uint4 *>(xb + (chunk >> 4) * kLd + (chunk & 15u) * 8u) = S[p].xv[i];
-        }
-        __syncthreads();
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-          for (int j = 0; j < NT; ++j)
-            bfr[kk][j] = *reinterpret_cast<const half8_t *>(xb + (16u * j + fr) * kLd +
-                                                             32u * kk + 8u * g);
-      } else {
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-          for (int j = 0; j < NT; ++j)
-            bfr[kk][j] = __builtin_bit_cast(half8_t, S[p].xv[kk * NT + j]);
-      }
-      // refill this slot PF steps ahead (unconditional; past the end: zeros)
-      load_step(S[p], ks + (uint32_t)PF);
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < NT; ++j)
-            acc[i][j] =
-                __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i][kk], bfr[kk][j], acc[i][j], 0, 0, 0);
-    }
-  }
-
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const uint32_t b = n0 + 16u * j + fr;
-      const uint32_t r0 = m0 + wave * 32u + 16u * i + 4u * g;
-      if (b >= batch) continue;
-      store_col4(y + (size_t)b * n_rows, r0, n_rows, acc[i][j]);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// K-split variant for small batches (memory- and dequant-bound): the KS waves
-// of a workgroup share one 32 x TN output tile and take interleaved K steps
-// (wave w: steps w, w + KS, ...), with register A fragments and X fragments
-// from global memory as in q4k_matmul_rf.  The KS partial tiles are summed in
-// LDS in wave order (deterministic) by wave 0.
-// ---------------------------------------------------------------------------
 template <int KS, int NT, int PF>
 __device__ __forceinline__ void q4k_matmul_ks(const uint8_t *__restrict__ q,
                                               const uint16_t *__restrict__ x,
@@ -451,7 +167,7 @@ __device__ __forceinline__ void q4k_matmul_ks(const uint8_t *__restrict__ q,
     xoff0[j] = b < batch ? (b * K + 8u * g) * 2u : kOob;
   }
 
-  auto load_step = [&](RfStep<NT, 1, false> &S, uint32_t ks) {
+  auto load_step = [&](KsStep<NT> &S, uint32_t ks) {
     const uint32_t sb = ks >> 1, h = ks & 1u;
     const bool live = ks < n_steps;
 #pragma unroll
@@ -476,7 +192,7 @@ __device__ __forceinline__ void q4k_matmul_ks(const uint8_t *__restrict__ q,
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[i][j] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
 
-  RfStep<NT, 1, false> S[PF];
+  KsStep<NT> S[PF];
 #pragma unroll
   for (int p = 0; p < PF; ++p) load_step(S[p], wave + (uint32_t)(p * KS));
 
@@ -552,151 +268,6 @@ __device__ __forceinline__ void q4k_matmul_ks(const uint8_t *__restrict__ q,
     }
 }
 
-
-// ---------------------------------------------------------------------------
-// Streaming variant for narrow batches (kind 4): persistent waves stream
-// 16-row tiles of W over K with PF 128-wide steps of loads in flight
-// (register A fragments as in q4k_matmul_rf), against the workgroup's 16
-// activation columns (blockIdx.y selects the column group) staged once in
-// LDS as Xs[col][k] (row stride K + 8 halves).  The KS waves of a tile slot
-// take interleaved K steps (wave w: steps (w % KS) + KS*j); at the end of a
-// tile their partial tiles are summed in LDS in wave order (deterministic)
-// and stored.  Every wave of a workgroup runs the same number of tile rounds,
-// so the two barriers per round are reached by all of them.  Loads are
-// unconditional: rows past the matrix and steps past the end read zeros
-// through the buffer range check.
-// ---------------------------------------------------------------------------
-struct StStep {
-  uint4 hd;
-  uint2 qlo, qhi;
-};
-
-template <int NW, int KS, int PF>
-__device__ __forceinline__ void q4k_matmul_st(const uint8_t *__restrict__ q,
-                                              const uint16_t *__restrict__ x,
-                                              float *__restrict__ y, const MatmulArgs a,
-                                              _Float16 *Xs) {
-  static_assert(NW % KS == 0, "KS waves per tile slot");
-  constexpr int kSlots = NW / KS;
-  __shared__ __attribute__((aligned(16))) f32x4_t red[KS > 1 ? (KS - 1) * kSlots * 64 : 1];
-  const uint32_t tid = threadIdx.x, lane = tid & 63u;
-  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t slot = wave / KS, kpart = wave % KS;
-  const uint32_t fr = lane & 15u, g = lane >> 4;
-  const uint32_t n_rows = a.n_rows, nsb = a.sb_per_row, batch = a.batch;
-  const uint32_t K = nsb * 256u, ldx = K + 8u;
-  const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
-  const __amdgpu_buffer_rsrc_t qr = rsrc(q, n_rows * row_bytes);
-  const __amdgpu_buffer_rsrc_t xr = rsrc(x, batch * K * 2u);
-  const uint32_t n0 = blockIdx.y * 16u;
-  const uint32_t slots_total = gridDim.x * kSlots;
-  const uint32_t slot_g = blockIdx.x * kSlots + slot;
-  const uint32_t n_tiles = (n_rows + 15u) >> 4;
-  const uint32_t n_rounds = (n_tiles + slots_total - 1u) / slots_total; // same for the whole grid
-  const uint32_t n_steps = 2u * nsb;
-  const uint32_t my_steps = (n_steps + KS - 1u) / KS; // per wave and tile (padded)
-  const uint32_t total = (n_rounds * my_steps + (PF - 1)) / PF * PF;
-
-  // Stage the 16 columns: 16-byte chunks (col, 8 halves of k), 8 in flight per thread.
-  const uint32_t kc_per_col = K >> 3, n_chunks = 16u * kc_per_col;
-  for (uint32_t c0 = 0; c0 < n_chunks; c0 += 8u * NW * 64u) {
-    uint4 v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t ch = c0 + tid + (uint32_t)i * (NW * 64u);
-      const uint32_t col = ch / kc_per_col, kc = ch - col * kc_per_col, b = n0 + col;
-      v[i] = bload16(xr, (ch < n_chunks && b < batch) ? (b * K + kc * 8u) * 2u : kOob);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t ch = c0 + tid + (uint32_t)i * (NW * 64u);
-      const uint32_t col = ch / kc_per_col, kc = ch - col * kc_per_col;
-      if (ch < n_chunks) *reinterpret_cast<uint4 *>(Xs + col * ldx + kc * 8u) = v[i];
-    }
-  }
-
-  // (round, j) -> tile slot_g + round * slots_total, K step kpart + KS * j
-  auto load_step = [&](StStep &S, uint32_t rd, uint32_t j) {
-    const uint32_t row = (slot_g + rd * slots_total) * 16u + fr;
-    const uint32_t ks = kpart + (uint32_t)KS * j;
-    const uint32_t base =
-        (row < n_rows && ks < n_steps) ? row * row_bytes + (ks >> 1) * 144u : kOob;
-    S.hd = bload16(qr, base);
-    const uint32_t qo = 16u + 64u * (ks & 1u) + 8u * g;
-    S.qlo = bload8(qr, base == kOob ? kOob : base + qo);
-    S.qhi = bload8(qr, base == kOob ? kOob : base + qo + 32u);
-  };
-  StStep S[PF];
-  uint32_t l_rd = 0, l_j = 0;
-#pragma unroll
-  for (int p = 0; p < PF; ++p) {
-    load_step(S[p], l_rd, l_j);
-    if (++l_j == my_steps) { l_j = 0; ++l_rd; }
-  }
-  __syncthreads(); // Xs complete
-
-  f32x4_t acc = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
-  uint32_t c_rd = 0, c_j = 0;
-  const _Float16 *xrow = Xs + fr * ldx + 8u * g;
-  for (uint32_t j0 = 0; j0 < total; j0 += PF) {
-#pragma unroll
-    for (int p = 0; p < PF; ++p) {
-      const uint32_t ks = kpart + (uint32_t)KS * c_j;
-      const uint32_t h = ks & 1u;
-      half8_t af[4];
-      {
-        const uint4 hd = S[p].hd;
-        const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-          const uint32_t c = 2u * h + (uint32_t)cc;
-          uint32_t scp, mp;
-          q4k_scale_min_pair(hd.y, hd.z, hd.w, c, &scp, &mp);
-          const float d1s = d * (float)(scp & 0xFFu) * 16777216.0f;
-          const float d2s = d * (float)(scp >> 8) * 1048576.0f;
-          const float m1 = dmin * (float)(mp & 0xFFu), m2 = dmin * (float)(mp >> 8);
-          const uint2 qw = cc == 0 ? S[p].qlo : S[p].qhi;
-          uint32_t l0, l1, h0, h1, l2, l3, h2, h3;
-          dequant_dword(qw.x, d1s, m1, d2s, m2, l0, l1, h0, h1);
-          dequant_dword(qw.y, d1s, m1, d2s, m2, l2, l3, h2, h3);
-          af[2 * cc] = __builtin_bit_cast(half8_t, make_uint4(l0, l1, l2, l3));
-          af[2 * cc + 1] = __builtin_bit_cast(half8_t, make_uint4(h0, h1, h2, h3));
-        }
-      }
-      // steps past K (padding) read X at step 0: their A fragments are zero
-      const _Float16 *xk = xrow + (ks < n_steps ? ks : 0u) * (uint32_t)kKStep;
-      half8_t bfr[4];
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) bfr[kk] = *reinterpret_cast<const half8_t *>(xk + 32 * kk);
-      // refill this slot PF steps ahead (unconditional; past the end: zeros)
-      load_step(S[p], l_rd, l_j);
-      if (++l_j == my_steps) { l_j = 0; ++l_rd; }
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[kk], bfr[kk], acc, 0, 0, 0);
-      if (++c_j == my_steps) { // a tile round is complete: reduce across kpart, store
-        if (c_rd < n_rounds) {
-          if constexpr (KS > 1) {
-            if (kpart > 0) red[((kpart - 1u) * kSlots + slot) * 64u + lane] = acc;
-            __syncthreads();
-            if (kpart == 0) {
-#pragma unroll
-              for (uint32_t w = 1; w < (uint32_t)KS; ++w) acc += red[((w - 1u) * kSlots + slot) * 64u + lane];
-            }
-            __syncthreads();
-          }
-          const uint32_t b = n0 + fr, r0 = (slot_g + c_rd * slots_total) * 16u + 4u * g;
-          if (kpart == 0 && b < batch) {
-            store_col4(y + (size_t)b * n_rows, r0, n_rows, acc);
-          }
-        }
-        acc = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
-        c_j = 0;
-        ++c_rd;
-      }
-    }
-  }
-}
 
 // ---------------------------------------------------------------------------
 // K-split tile variant (kind 5): a workgroup of KS waves owns a TM = 16*RT
@@ -893,169 +464,12 @@ __device__ __forceinline__ void q4k_matmul_kx(const uint8_t *__restrict__ q,
 }
 
 // ---------------------------------------------------------------------------
-// Row-split tile variant for wide batches (kind 6): a workgroup of W waves
-// owns a TM = 16*RT*W by TN = 16*NT tile of Y; wave w owns rows 16*RT*w ..
-// +16*RT (RT row tiles: every X fragment it reads feeds RT MFMAs) and walks
-// all of K in 64-wide steps (one chunk of a superblock), so no partial sums
-// cross waves.  W = 8 puts two waves on every SIMD, which lets one wave's
-// dequantisation run while the other's MFMAs issue (with a single wave per
-// SIMD the two serialise).  A ring of PF LDS buffers holds, per step, the X
-// tile [TN x 64] (filled cooperatively: wave w issues X instructions w,
-// w + W, ...) and each wave's private weight pieces (per row: the header
-// and the chunk's 32 qs bytes, three 16-byte pieces), all by direct-to-LDS
-// loads laid out as in q4k_matmul_kx (quads read 64 contiguous bytes; X
-// pieces rotated by column/4 so the fragment reads hit distinct banks).  One
-// barrier per step: after it every wave's loads of the step have landed and
-// every wave is done with the buffer of step j - 1, which the loads of step
-// j + PF - 1 refill.
-// ---------------------------------------------------------------------------
-template <int W, int RT, int NT>
-struct RsLayout {
-  static constexpr int kX = 2 * NT;                    // X instructions per step (workgroup)
-  static constexpr int kXPer = kX / W;                 // ... issued by each wave
-  static constexpr int kW = (48 * RT + 63) / 64;       // weight instructions per wave
-  static constexpr int kPerStep = kXPer + kW;          // loads per wave per step
-  static constexpr int kBufSlots = 64 * (kX + W * kW); // 16-byte slots per ring buffer
-};
-
-template <int W, int RT, int NT, int PF>
-__device__ __forceinline__ void q4k_matmul_rs(const uint8_t *__restrict__ q,
-                                              const uint16_t *__restrict__ x,
-                                              float *__restrict__ y, const MatmulArgs a,
-                                              f32x4_t *lds) {
-  using L = RsLayout<W, RT, NT>;
-  static_assert(L::kX % W == 0, "X instructions split evenly over the waves");
-  static_assert(PF >= 2 && PF <= 5 && L::kPerStep * (PF - 1) <= 63,
-                "loads in flight must fit the load counter");
-  constexpr uint32_t TM = 16u * RT * W, TN = 16u * NT;
-  const uint32_t tid = threadIdx.x, lane = tid & 63u;
-  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t fr = lane & 15u, g = lane >> 4;
-  const uint32_t n_rows = a.n_rows, nsb = a.sb_per_row, batch = a.batch;
-  const uint32_t K = nsb * 256u, n_steps = 4u * nsb;
-  const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
-  const __amdgpu_buffer_rsrc_t qr = rsrc(q, n_rows * row_bytes);
-  const __amdgpu_buffer_rsrc_t xr = rsrc(x, batch * K * 2u);
-  const uint32_t m0 = blockIdx.x * TM + wave * (16u * RT), n0 = blockIdx.y * TN;
-
-  // X load role: instruction i = wave + W * u covers k-half kk = i / NT and
-  // column tile t = i % NT; lane 4c' + j loads column 16t + c', piece (j - rot) & 3.
-  const uint32_t xc = lane >> 2, xp = ((lane & 3u) - kx_xrot(lane >> 2)) & 3u;
-  uint32_t xoff0[L::kXPer];
-#pragma unroll
-  for (int u = 0; u < L::kXPer; ++u) {
-    const uint32_t i = wave + (uint32_t)(W * u), kk = i / NT, t = i - kk * NT;
-    const uint32_t b = n0 + 16u * t + xc;
-    xoff0[u] = b < batch ? (b * K + 32u * kk + 8u * xp) * 2u : kOob;
-  }
-  // Weight load role: piece P = 64m + lane -> row P / 3, part P % 3 (0 the
-  // header, 1-2 the 16-byte halves of the chunk's 32 qs bytes).
-  uint32_t woff0[L::kW], wpart[L::kW];
-#pragma unroll
-  for (int m = 0; m < L::kW; ++m) {
-    const uint32_t P = 64u * (uint32_t)m + lane, r = P / 3u;
-    const uint32_t row = m0 + r;
-    wpart[m] = P - 3u * r;
-    woff0[m] = (r < 16u * RT && row < n_rows) ? row * row_bytes : kOob;
-  }
-
-  auto issue = [&](uint32_t j) { // step j -> ring buffer j % PF
-    const bool live = j < n_steps;
-    const uint32_t sb = j >> 2, c = j & 3u;
-    f32x4_t *buf = lds + (j % (uint32_t)PF) * (uint32_t)L::kBufSlots;
-#pragma unroll
-    for (int u = 0; u < L::kXPer; ++u) {
-      const uint32_t i = wave + (uint32_t)(W * u);
-      const uint32_t off = (xoff0[u] == kOob || !live) ? kOob : xoff0[u] + 128u * j;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void_t *)(buf + i * 64u), 16, off, 0, 0, 0);
-    }
-    f32x4_t *wb = buf + (L::kX + wave * L::kW) * 64;
-#pragma unroll
-    for (int m = 0; m < L::kW; ++m) {
-      const uint32_t off =
-          (woff0[m] == kOob || !live)
-              ? kOob
-              : woff0[m] + sb * 144u + (wpart[m] == 0u ? 0u : 16u * wpart[m] + 32u * c);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(qr, (lds_void_t *)(wb + m * 64), 16, off, 0, 0, 0);
-    }
-  };
-
-  f32x4_t acc[RT][NT];
-#pragma unroll
-  for (int i = 0; i < RT; ++i)
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[i][t] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
-
-#pragma unroll
-  for (int p = 0; p < PF - 1; ++p) issue((uint32_t)p);
-
-  const uint32_t xslot = 4u * fr + ((g + kx_xrot(fr)) & 3u);
-  for (uint32_t j = 0; j < n_steps; ++j) {
-    // own loads of step j landed (PF - 2 later steps may be in flight), then
-    // the barrier: everyone's loads of step j landed, step j - 1 is consumed
-    if constexpr (PF == 2)
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    else if constexpr (PF == 3)
-      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(L::kPerStep) : "memory");
-    else if constexpr (PF == 4)
-      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * L::kPerStep) : "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(3 * L::kPerStep) : "memory");
-    issue(j + (uint32_t)(PF - 1));
-    const f32x4_t *buf = lds + (j % (uint32_t)PF) * (uint32_t)L::kBufSlots;
-    const f32x4_t *wb = buf + (L::kX + wave * L::kW) * 64;
-    half8_t af[RT][2];
-#pragma unroll
-    for (int i = 0; i < RT; ++i) {
-      const f32x4_t *wp = wb + 3u * (16u * (uint32_t)i + fr);
-      const uint4 hd = __builtin_bit_cast(uint4, wp[0]);
-      const uint2 qw = *reinterpret_cast<const uint2 *>(
-          reinterpret_cast<const uint8_t *>(wp + 1 + (g >> 1)) + 8u * (g & 1u));
-      const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
-      uint32_t scp, mp;
-      q4k_scale_min_pair(hd.y, hd.z, hd.w, j & 3u, &scp, &mp);
-      const float d1s = d * (float)(scp & 0xFFu) * 16777216.0f;
-      const float d2s = d * (float)(scp >> 8) * 1048576.0f;
-      const float m1 = dmin * (float)(mp & 0xFFu), m2 = dmin * (float)(mp >> 8);
-      uint32_t l0, l1, h0, h1, l2, l3, h2, h3;
-      dequant_dword(qw.x, d1s, m1, d2s, m2, l0, l1, h0, h1);
-      dequant_dword(qw.y, d1s, m1, d2s, m2, l2, l3, h2, h3);
-      af[i][0] = __builtin_bit_cast(half8_t, make_uint4(l0, l1, l2, l3));
-      af[i][1] = __builtin_bit_cast(half8_t, make_uint4(h0, h1, h2, h3));
-    }
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      half8_t xf[NT];
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-        xf[t] = __builtin_bit_cast(half8_t, buf[((uint32_t)kk * NT + (uint32_t)t) * 64u + xslot]);
-#pragma unroll
-      for (int i = 0; i < RT; ++i)
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-          acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i][kk], xf[t], acc[i][t], 0, 0, 0);
-    }
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // ring loads past the last step
-
-#pragma unroll
-  for (int i = 0; i < RT; ++i)
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const uint32_t b = n0 + 16u * t + fr;
-      const uint32_t r0 = m0 + 16u * i + 4u * g;
-      if (b >= batch) continue;
-      store_col4(y + (size_t)b * n_rows, r0, n_rows, acc[i][t]);
-    }
-}
-
-// ---------------------------------------------------------------------------
 // 32 x 32 tiles with wide waves (kind 8, axh_q4k_matmul_rm_w{W}_r{RT}_p4): a
 // workgroup of W waves owns 32 * RT * W rows x 128 columns of Y; wave w owns
 // 32 * RT rows (RT 32-row MFMA tiles) x 128 columns (four 32-column tiles) and
 // walks all of K in 64-wide steps (one chunk of a superblock) with
 // v_mfma_f32_32x32x16_f16, so each X fragment read from LDS feeds RT MFMAs of
-// 32 rows (the row-split kind's 16x16 tiles: 16 rows) and each dequantised A
+// 32 rows (16x16 tiles: 16 rows) and each dequantised A
 // fragment four (128 columns).  A ring of 4 LDS buffers, each the step's X
 // tile (128 columns x 64 k, 16 KiB) and every wave's weight pieces (per row:
 // header and the chunk's 32 qs bytes), is filled by direct-to-LDS loads three
@@ -1516,29 +930,6 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
 
 } // namespace
 
-#define AXH_Q4K_MATMUL(W, NT)                                                              \
-  extern "C" __global__ void __launch_bounds__(W * 64)                                           \
-      axh_q4k_matmul_w##W##_n##NT(const uint8_t *__restrict__ q, const uint16_t *__restrict__ x, \
-                                  float *__restrict__ y, AXH_MATMUL_ARGS) { AXH_MATMUL_UNPACK; \
-    q4k_matmul<W, NT>(q, x, y, a);                                                               \
-  }
-
-AXH_Q4K_MATMUL(1, 1)
-AXH_Q4K_MATMUL(2, 2)
-AXH_Q4K_MATMUL(4, 4)
-AXH_Q4K_MATMUL(4, 8)
-
-#define AXH_Q4K_MATMUL_RF(W, NT, PF, XL)                                                         \
-  extern "C" __global__ void __launch_bounds__(W * 64)                                           \
-      axh_q4k_matmul_rf_w##W##_n##NT##_p##PF##_x##XL(const uint8_t *__restrict__ q,             \
-                                                      const uint16_t *__restrict__ x,            \
-                                                      float *__restrict__ y, AXH_MATMUL_ARGS) { AXH_MATMUL_UNPACK; \
-    q4k_matmul_rf<W, NT, PF, XL != 0>(q, x, y, a);                                               \
-  }
-
-AXH_Q4K_MATMUL_RF(4, 4, 2, 1)
-AXH_Q4K_MATMUL_RF(4, 8, 1, 1)
-
 #define AXH_Q4K_MATMUL_KS(KS, NT, PF)                                                            \
   extern "C" __global__ void __launch_bounds__(KS * 64)                                          \
       axh_q4k_matmul_ks_k##KS##_n##NT##_p##PF(const uint8_t *__restrict__ q,                     \
@@ -1551,21 +942,6 @@ AXH_Q4K_MATMUL_KS(4, 1, 2)
 AXH_Q4K_MATMUL_KS(8, 1, 1)
 AXH_Q4K_MATMUL_KS(4, 2, 2)
 AXH_Q4K_MATMUL_KS(8, 2, 1)
-
-#define AXH_Q4K_MATMUL_ST(NW, KS, PF)                                                            \
-  extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
-      axh_q4k_matmul_st_w##NW##_k##KS##_p##PF(const uint8_t *__restrict__ q,                     \
-                                              const uint16_t *__restrict__ x,                    \
-                                              float *__restrict__ y, AXH_MATMUL_ARGS) { AXH_MATMUL_UNPACK; \
-    extern __shared__ _Float16 axh_xs_dyn[];                                                     \
-    q4k_matmul_st<NW, KS, PF>(q, x, y, a, axh_xs_dyn);                                           \
-  }
-
-AXH_Q4K_MATMUL_ST(4, 1, 4)
-AXH_Q4K_MATMUL_ST(8, 2, 4)
-AXH_Q4K_MATMUL_ST(8, 2, 2)
-AXH_Q4K_MATMUL_ST(16, 4, 2)
-AXH_Q4K_MATMUL_ST(16, 4, 4)
 
 #define AXH_Q4K_MATMUL_KX(RT, NT, KS, PF)                                                        \
   extern "C" __global__ void __launch_bounds__(KS * 64)                                          \
@@ -1584,21 +960,6 @@ AXH_Q4K_MATMUL_KX(8, 4, 4, 2)
 AXH_Q4K_MATMUL_KX(4, 2, 4, 2)
 AXH_Q4K_MATMUL_KX(4, 2, 4, 3)
 AXH_Q4K_MATMUL_KX(4, 1, 4, 3)
-
-#define AXH_Q4K_MATMUL_RS(W, RT, NT, PF)                                                         \
-  extern "C" __global__ void __launch_bounds__(W * 64)                                           \
-      axh_q4k_matmul_rs_w##W##_r##RT##_n##NT##_p##PF(const uint8_t *__restrict__ q,              \
-                                                     const uint16_t *__restrict__ x,             \
-                                                     float *__restrict__ y, AXH_MATMUL_ARGS) { AXH_MATMUL_UNPACK; \
-    extern __shared__ f32x4_t axh_rs_dyn[];                                                      \
-    q4k_matmul_rs<W, RT, NT, PF>(q, x, y, a, axh_rs_dyn);                                        \
-  }
-
-AXH_Q4K_MATMUL_RS(8, 2, 8, 4)
-AXH_Q4K_MATMUL_RS(8, 2, 8, 3)
-AXH_Q4K_MATMUL_RS(4, 4, 8, 4)
-AXH_Q4K_MATMUL_RS(8, 2, 4, 4)
-AXH_Q4K_MATMUL_RS(8, 1, 8, 4)
 
 #define AXH_Q4K_MATMUL_RM(W, RT)                                                                 \
   extern "C" __global__ void __launch_bounds__(W * 64)                                           \

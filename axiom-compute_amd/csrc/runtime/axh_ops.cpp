@@ -35,31 +35,27 @@ struct MatmulArgs {
   uint32_t pad;
 };
 
-// Compiled batched-matmul kernels (keep in sync with q4_matmul.hip):
-//   kind 1 (LDS-tiled)  axh_q4k_matmul_w{W}_n{NT}: W waves x 32 rows, NT 16-column tiles;
-//   kind 2 (register A) axh_q4k_matmul_rf_w{W}_n{NT}_p{PF}_x1;
+// Compiled batched-matmul kernels (keep in sync with q4_matmul.hip).  Kinds 1
+// (LDS-tiled), 2 (register A), 4 (streaming) and 6 (row-split tile) were
+// removed: none was the fastest variant at any shape measured; their numbers
+// stay unused so that a request for one fails as an unknown variant.
 //   kind 3 (K-split)    axh_q4k_matmul_ks_k{W}_n{NT}_p{PF}: W waves split K of one 32-row tile;
-//   kind 4 (streaming)  axh_q4k_matmul_st_w{W}_k{W/4}_p{PF}: persistent waves stream 16-row
-//                       tiles against 16 columns staged in LDS, W/4 waves splitting each
-//                       tile's K (col_tiles is 1).
 //   kind 5 (K-split tile) axh_q4k_matmul_kx_r{RT}_n{NT}_k{W}_p{PF}: a 16*RT x 16*NT tile per
 //                       workgroup, its W waves splitting K by 64-wide superblock chunks,
 //                       register A, operands through per-wave LDS rings, PF superblocks in
 //                       flight.
-//   kind 6 (row-split tile) axh_q4k_matmul_rs_w{W}_r{RT}_n{NT}_p{PF}: W waves of RT row tiles
-//                       each share an X tile [16*NT x 64] in a PF-deep LDS ring (one barrier
-//                       per 64-wide K step).
+//   kind 7 (streaming rows) axh_q4k_matmul_sr_w{W}_s2[_n2|_h]: persistent, one workgroup per
+//                       CU over 16-row blocks, K <= 4096 (pf 2: 8-column groups).
+//   kind 8 (32x32 tiles) axh_q4k_matmul_rm_w{W}_r{RT}_p4: W waves of RT 32-row MFMA tiles
+//                       over 128 columns, a 4-deep LDS ring.
 struct MatmulVariant {
-  uint32_t kind, w, nt, pf, rt; // rt: row tiles (kind 5 only)
+  uint32_t kind, w, nt, pf, rt; // rt: row tiles (kinds 5 and 8)
 };
 constexpr MatmulVariant kQ4kMatmulVariants[] = {
-    {1, 1, 1, 1, 0},  {1, 2, 2, 1, 0},  {1, 4, 4, 1, 0},  {1, 4, 8, 1, 0},  {2, 4, 4, 2, 0},
-    {2, 4, 8, 1, 0},  {3, 4, 1, 2, 0},  {3, 8, 1, 1, 0},  {3, 4, 2, 2, 0},  {3, 8, 2, 1, 0},
-    {4, 4, 1, 4, 0},  {4, 8, 1, 4, 0},  {4, 8, 1, 2, 0},  {4, 16, 1, 2, 0}, {4, 16, 1, 4, 0},
-    {5, 4, 8, 2, 4},  {5, 4, 8, 2, 2},  {5, 4, 4, 2, 4},  {5, 4, 4, 3, 4},  {5, 4, 4, 2, 8},
-    {5, 4, 2, 2, 4},  {5, 4, 2, 3, 4},  {5, 4, 1, 3, 4},  {6, 8, 8, 4, 2},  {6, 8, 8, 3, 2},
-    {6, 4, 8, 4, 4},  {6, 8, 4, 4, 2},  {6, 8, 8, 4, 1},  {7, 8, 1, 1, 0},  {7, 8, 2, 1, 0},
-    {7, 8, 1, 2, 0},  {8, 8, 8, 4, 1},  {8, 4, 8, 4, 2},  {8, 4, 8, 4, 1},  {8, 2, 8, 4, 2}};
+    {3, 4, 1, 2, 0}, {3, 8, 1, 1, 0}, {3, 4, 2, 2, 0}, {3, 8, 2, 1, 0}, {5, 4, 8, 2, 4},
+    {5, 4, 8, 2, 2}, {5, 4, 4, 2, 4}, {5, 4, 4, 3, 4}, {5, 4, 4, 2, 8}, {5, 4, 2, 2, 4},
+    {5, 4, 2, 3, 4}, {5, 4, 1, 3, 4}, {7, 8, 1, 1, 0}, {7, 8, 2, 1, 0}, {7, 8, 1, 2, 0},
+    {8, 8, 8, 4, 1}, {8, 4, 8, 4, 2}, {8, 4, 8, 4, 1}, {8, 2, 8, 4, 2}};
 // The matmul kernels read zeros through offsets at or past 0xFFF00000 (with
 // the step offsets on top), and address rows up to 16 past the matrix: q and
 // x must stay below that, with 16 rows to spare.
@@ -1004,10 +1000,6 @@ axh_status axh_q4_0_matvec(axh_context *ctx, const void *q, const float *x, floa
   return s == AXH_OK ? ok() : s;
 }
 
-// Defaults from on-device sweeps at 14336 x 4096: the K-split tile kind with
-// the batch in one column group up to 128 columns; beyond, the row-split kind
-// with the row tile chosen to keep about 224 workgroups (one per CU).
-
 // Kind 5 LDS: each wave's ring of `pf` buffers, one 1 KiB slot row per
 // 16-byte-per-lane load of a step (2*nt for X, ceil(48*rt/64) for the
 // weights), reused at the end for the waves' partial tiles (1 KiB per tile).
@@ -1015,12 +1007,6 @@ static uint32_t kx_lds_bytes(const MatmulVariant &v) {
   const uint32_t ring = v.w * v.pf * (2u * v.nt + (48u * v.rt + 63u) / 64u);
   const uint32_t red = v.w * v.rt * v.nt;
   return (ring > red ? ring : red) * 1024u;
-}
-
-// Kind 6 LDS: a ring of `pf` buffers, each the X tile (2 * nt instructions of
-// 1 KiB) and every wave's weight pieces (16 * rt rows x 3 pieces of 16 bytes).
-static uint32_t rs_lds_bytes(const MatmulVariant &v) {
-  return v.pf * (2u * v.nt + v.w * ((48u * v.rt + 63u) / 64u)) * 1024u;
 }
 
 // Kind 8 LDS: a ring of 4 buffers, each the X tile (16 KiB) and every wave's
@@ -1071,7 +1057,7 @@ static MatmulVariant q4k_matmul_default(uint32_t n_rows, uint32_t batch, uint32_
   // 34.8 against 40.2).
   if (groups(32, 16) <= kMatmulCus) return {3, 8, 1, 1, 0};
   // kind 8 (32 x 32 MFMA tiles) where its rows fill the chip: 14336 x 4096 x
-  // 512 74.1 us (8 waves of 32 rows) against 83-94 for the row-split kind,
+  // 512 74.1 us (8 waves of 32 rows) against 83-94 for a row-split kind,
   // B = 256 49.3 (4 waves of 32 rows) against 52.1; 8192 x 4096 x 512 46.0 us
   // with 4 waves against 60.7 as K-split tiles.
   if (batch > 256 && groups(256, 128) >= kMatmulFill) return {8, 8, 8, 4, 1};
@@ -1114,40 +1100,31 @@ static axh_status plan_q4k_matmul(uint32_t n_rows, uint32_t sb_per_row, uint32_t
     if (variant->col_tiles) want.nt = variant->col_tiles;
     if (variant->prefetch) want.pf = variant->prefetch;
     if (variant->row_tiles) {
-      if (want.kind != 5 && want.kind != 6 && want.kind != 8)
-        return fail(AXH_ERR_INVALID_ARGUMENT,
-                    "row_tiles is a hole of matmul kinds 5, 6 and 8 only");
+      if (want.kind != 5 && want.kind != 8)
+        return fail(AXH_ERR_INVALID_ARGUMENT, "row_tiles is a hole of matmul kinds 5 and 8 only");
       want.rt = variant->row_tiles;
     }
   }
-  if (want.kind != 5 && want.kind != 6 && want.kind != 8) want.rt = 0;
-  else if (want.rt == 0) want.rt = want.kind == 5 ? 4u : want.kind == 6 ? 2u : 1u;
+  if (want.kind != 5 && want.kind != 8) want.rt = 0;
+  else if (want.rt == 0) want.rt = want.kind == 5 ? 4u : 1u;
   for (const MatmulVariant &v : kQ4kMatmulVariants)
     if (v.kind == want.kind && v.w == want.w && v.nt == want.nt && v.pf == want.pf &&
         v.rt == want.rt) {
       *out = v;
-      if (v.kind == 1)
-        std::snprintf(name, cap, "axh_q4k_matmul_w%u_n%u", v.w, v.nt);
-      else if (v.kind == 2)
-        std::snprintf(name, cap, "axh_q4k_matmul_rf_w%u_n%u_p%u_x1", v.w, v.nt, v.pf);
-      else if (v.kind == 3)
+      if (v.kind == 3)
         std::snprintf(name, cap, "axh_q4k_matmul_ks_k%u_n%u_p%u", v.w, v.nt, v.pf);
-      else if (v.kind == 4)
-        std::snprintf(name, cap, "axh_q4k_matmul_st_w%u_k%u_p%u", v.w, v.w / 4u, v.pf);
       else if (v.kind == 5)
         std::snprintf(name, cap, "axh_q4k_matmul_kx_r%u_n%u_k%u_p%u", v.rt, v.nt, v.w, v.pf);
       else if (v.kind == 8)
         std::snprintf(name, cap, "axh_q4k_matmul_rm_w%u_r%u_p4", v.w, v.rt);
-      else if (v.kind == 7) {
+      else {
         if (sb_per_row > kSrMaxSb)
           return fail(AXH_ERR_INVALID_ARGUMENT,
                       "matmul kind 7 takes rows of at most 16 superblocks (K <= 4096)");
-        // prefetch 2: 8-column groups staged through 64 KiB (two workgroups per CU)
+        // prefetch 2: 8-column groups, X staged through 64 KiB
         std::snprintf(name, cap, "axh_q4k_matmul_sr_w%u_s2%s%s", v.w, v.nt == 2 ? "_n2" : "",
                       v.pf == 2 ? "_h" : "");
       }
-      else
-        std::snprintf(name, cap, "axh_q4k_matmul_rs_w%u_r%u_n%u_p%u", v.w, v.rt, v.nt, v.pf);
       return ok();
     }
   return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_K matmul variant matches");
@@ -1193,25 +1170,19 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
   char name[64];
   s = plan_q4k_matmul(n_rows, sb_per_row, batch, variant, &v, name, sizeof(name));
   if (s != AXH_OK) return s;
-  // kind 4 stages 16 activation columns of the whole K in LDS; kind 5 sums the
-  // partial tiles of its waves there (one 16x16 f32 tile = 1 KiB per wave)
-  // kind 7: 128 KiB of X staging, then two buffers of the waves' partial tiles
-  // (64-bit: kind 4's size grows with K and would wrap in 32 bits)
-  const uint64_t lds = v.kind == 4 ? 16ull * ((uint64_t)sb_per_row * 256u + 8u) * 2u
-                       : v.kind == 5 ? kx_lds_bytes(v)
-                       : v.kind == 6 ? rs_lds_bytes(v)
+  // kind 5 sums the partial tiles of its waves in LDS (one 16x16 f32 tile =
+  // 1 KiB per wave); kind 7: 128 KiB of X staging, then two buffers of the
+  // waves' partial tiles
+  const uint32_t lds = v.kind == 5   ? kx_lds_bytes(v)
                        : v.kind == 7 ? (v.pf == 2 ? 65536u : 131072u) + 2u * v.w * v.nt * 1024u
                        : v.kind == 8 ? rm_lds_bytes(v)
                                      : 0u;
   if (lds > ctx->core->max_lds)
     return fail(AXH_ERR_INVALID_ARGUMENT, "matmul variant needs more LDS than the device has");
   const uint32_t tm = v.kind == 3   ? 32u
-                      : v.kind == 4 ? 64u // 4 tile slots
                       : v.kind == 5 ? 16u * v.rt
-                      : v.kind == 6 ? 16u * v.rt * v.w
                       : v.kind == 7 ? 16u
-                      : v.kind == 8 ? 32u * v.rt * v.w
-                                    : 32u * v.w;
+                                    : 32u * v.rt * v.w;
   const uint32_t tn = (v.kind == 7 && v.pf == 2 ? 8u : 16u) * v.nt;
   uint64_t gx = (n_rows + tm - 1) / tm;
   const uint64_t gy = (batch + tn - 1) / tn;
@@ -1221,12 +1192,8 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
   axh_kernel *k = nullptr;
   s = builtin_kernel(ctx, name, 3, sizeof(MatmulArgs), v.w * 64u, &k);
   if (s != AXH_OK) return s;
-  if (v.kind == 4 || v.kind == 7) { // persistent: one resident wave of workgroups per column group
-    // (kind 7: one workgroup per CU even where two would fit)
-    const uint64_t resident =
-        (uint64_t)(v.kind == 7 ? 1u : occupancy(ctx, k, (uint32_t)lds)) * ctx->core->cu_count;
-    if (resident < gx) gx = resident;
-  }
+  // kind 7 is persistent: one workgroup per CU per column group, even where two would fit
+  if (v.kind == 7 && ctx->core->cu_count < gx) gx = ctx->core->cu_count;
   const uint32_t grid[3] = {(uint32_t)gx, (uint32_t)gy, 1};
   void *bufs[3] = {const_cast<void *>(q), const_cast<uint16_t *>(x), y};
   MatmulArgs a{n_rows, sb_per_row, batch, 0};

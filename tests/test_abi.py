@@ -243,22 +243,20 @@ def test_matmul_kernel_selection(axc):
     assert name(8192, 16, 512) == "axh_q4k_matmul_rm_w4_r1_p4"  # 8 waves: 128 workgroups
     assert name(4096, 16, 512) == "axh_q4k_matmul_kx_r4_n8_k4_p2"
     assert name(4096, 16, 256) == "axh_q4k_matmul_kx_r4_n4_k4_p2"
-    assert name(14336, 16, 512, axc.MatmulVariant(6, 8, 8, 3, 2)) == "axh_q4k_matmul_rs_w8_r2_n8_p3"
     assert name(14336, 16, 512, axc.MatmulVariant(8, 4, 8, 4, 2)) == "axh_q4k_matmul_rm_w4_r2_p4"
-    assert name(14336, 16, 512, axc.MatmulVariant(1, 2, 2, 1)) == "axh_q4k_matmul_w2_n2"
     assert name(14336, 16, 8, axc.MatmulVariant(3, 4, 1, 2)) == "axh_q4k_matmul_ks_k4_n1_p2"
-    with pytest.raises(axc.DispatchError):
-        name(14336, 16, 8, axc.MatmulVariant(1, 3, 1, 1))
+    # kinds 1, 2, 4 and 6 (LDS-tiled, register A, streaming, row-split) were removed
+    for kind, w, nt, pf, rt in ((1, 2, 2, 1, 0), (2, 4, 4, 2, 0), (4, 4, 1, 4, 0), (6, 8, 8, 3, 2)):
+        with pytest.raises(axc.DispatchError):
+            name(14336, 16, 512, axc.MatmulVariant(kind, w, nt, pf, rt))
     vs = axc.compiled_matmul_variants()
     assert len(set(vs)) == len(vs) >= 6
-    assert {v.kind for v in vs} == {1, 2, 3, 4, 5, 6, 7, 8}
-    assert name(14336, 16, 8, axc.MatmulVariant(4, 4, 1, 4)) == "axh_q4k_matmul_st_w4_k1_p4"
+    assert {v.kind for v in vs} == {3, 5, 7, 8}
     assert name(14336, 16, 128, axc.MatmulVariant(5, 4, 8, 2, 4)) == \
         "axh_q4k_matmul_kx_r4_n8_k4_p2"
-    assert all((v.row_tiles > 0) == (v.kind in (5, 6, 8)) for v in vs)
-    assert name(14336, 16, 512, axc.MatmulVariant(6, 8, 8, 4)) == "axh_q4k_matmul_rs_w8_r2_n8_p4"
-    with pytest.raises(axc.DispatchError):  # row tiles are kinds 5 and 6 only
-        name(14336, 16, 8, axc.MatmulVariant(4, 4, 1, 4, 2))
+    assert all((v.row_tiles > 0) == (v.kind in (5, 8)) for v in vs)
+    with pytest.raises(axc.DispatchError):  # row tiles are kinds 5 and 8 only
+        name(14336, 16, 8, axc.MatmulVariant(3, 4, 1, 2, 2))
     co = axc.builtin_code_object()
     for v in vs:
         assert name(64, 16, 64, v).startswith("axh_q4k_matmul_")
