@@ -117,7 +117,7 @@ __device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 
 // ---------------------------------------------------------------------------
 // K-split variant for small batches (memory- and dequant-bound): the KS waves
-// of a workgroup share one 32 x TN output tile and take interleaved 128-wide
+// of a workgroup share one 16*RT x TN output tile and take interleaved 128-wide
 // K steps (half a superblock; wave w: steps w, w + KS, ...).  Each lane
 // dequantises exactly the A fragments it feeds to v_mfma_f32_16x16x32_f16
 // (row lane%16 of a 16-row tile, k = 32*kk + 8*(lane/16) + 0..7), so A never
@@ -129,24 +129,24 @@ __device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 // ring.  The KS partial tiles are summed in LDS in wave order
 // (deterministic) by wave 0.
 // ---------------------------------------------------------------------------
-template <int NT>
+template <int NT, int RT>
 struct KsStep {
-  uint4 hd[2];
-  uint2 qlo[2], qhi[2];
+  uint4 hd[RT];
+  uint2 qlo[RT], qhi[RT];
   uint4 xv[4 * NT];
 };
 
-template <int KS, int NT, int PF>
+template <int KS, int NT, int PF, int RT>
 __device__ __forceinline__ void q4k_matmul_ks(const uint8_t *__restrict__ q,
                                               const uint16_t *__restrict__ x,
                                               float *__restrict__ y, const MatmulArgs a) {
   constexpr int TN = 16 * NT;
-  __shared__ __attribute__((aligned(16))) f32x4_t red[KS > 1 ? (KS - 1) * 2 * NT * 64 : 1];
+  __shared__ __attribute__((aligned(16))) f32x4_t red[KS > 1 ? (KS - 1) * RT * NT * 64 : 1];
 
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t n_rows = a.n_rows, nsb = a.sb_per_row, batch = a.batch;
-  const uint32_t m0 = blockIdx.x * 32u, n0 = blockIdx.y * TN;
+  const uint32_t m0 = blockIdx.x * (16u * RT), n0 = blockIdx.y * TN;
   const uint32_t K = nsb * 256u;
   const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
   const __amdgpu_buffer_rsrc_t qr = rsrc(q, n_rows * row_bytes);
@@ -154,9 +154,9 @@ __device__ __forceinline__ void q4k_matmul_ks(const uint8_t *__restrict__ q,
   const uint32_t fr = lane & 15u, g = lane >> 4;
   const uint32_t n_steps = 2u * nsb;
 
-  uint32_t row_off[2];
+  uint32_t row_off[RT];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < RT; ++i) {
     const uint32_t row = m0 + 16u * (uint32_t)i + fr;
     row_off[i] = row < n_rows ? row * row_bytes : kOob;
   }
@@ -167,11 +167,11 @@ __device__ __forceinline__ void q4k_matmul_ks(const uint8_t *__restrict__ q,
     xoff0[j] = b < batch ? (b * K + 8u * g) * 2u : kOob;
   }
 
-  auto load_step = [&](KsStep<NT> &S, uint32_t ks) {
+  auto load_step = [&](KsStep<NT, RT> &S, uint32_t ks) {
     const uint32_t sb = ks >> 1, h = ks & 1u;
     const bool live = ks < n_steps;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < RT; ++i) {
       const uint32_t base = (row_off[i] == kOob || !live) ? kOob : row_off[i] + sb * 144u;
       S.hd[i] = bload16(qr, base);
       const uint32_t qo = 16u + 64u * h + 8u * g;
@@ -186,13 +186,13 @@ __device__ __forceinline__ void q4k_matmul_ks(const uint8_t *__restrict__ q,
             bload16(xr, (xoff0[j] == kOob || !live) ? kOob : xoff0[j] + ks * 256u + 64u * kk);
   };
 
-  f32x4_t acc[2][NT];
+  f32x4_t acc[RT][NT];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < RT; ++i)
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[i][j] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
 
-  KsStep<NT> S[PF];
+  KsStep<NT, RT> S[PF];
 #pragma unroll
   for (int p = 0; p < PF; ++p) load_step(S[p], wave + (uint32_t)(p * KS));
 
@@ -203,9 +203,9 @@ __device__ __forceinline__ void q4k_matmul_ks(const uint8_t *__restrict__ q,
     for (int p = 0; p < PF; ++p) {
       const uint32_t ks = wave + (j0 + (uint32_t)p) * KS;
       const uint32_t h = ks & 1u;
-      half8_t af[2][4];
+      half8_t af[RT][4];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < RT; ++i) {
         const uint4 hd = S[p].hd[i];
         const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
 #pragma unroll
@@ -233,7 +233,7 @@ __device__ __forceinline__ void q4k_matmul_ks(const uint8_t *__restrict__ q,
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < RT; ++i)
 #pragma unroll
           for (int j = 0; j < NT; ++j)
             acc[i][j] =
@@ -244,21 +244,21 @@ __device__ __forceinline__ void q4k_matmul_ks(const uint8_t *__restrict__ q,
   if constexpr (KS > 1) {
     if (wave > 0) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < RT; ++i)
 #pragma unroll
-        for (int j = 0; j < NT; ++j) red[(((wave - 1u) * 2u + i) * NT + j) * 64u + lane] = acc[i][j];
+        for (int j = 0; j < NT; ++j) red[(((wave - 1u) * RT + i) * NT + j) * 64u + lane] = acc[i][j];
     }
     __syncthreads();
     if (wave != 0) return;
 #pragma unroll
     for (uint32_t w = 1; w < (uint32_t)KS; ++w)
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < RT; ++i)
 #pragma unroll
-        for (int j = 0; j < NT; ++j) acc[i][j] += red[(((w - 1u) * 2u + i) * NT + j) * 64u + lane];
+        for (int j = 0; j < NT; ++j) acc[i][j] += red[(((w - 1u) * RT + i) * NT + j) * 64u + lane];
   }
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < RT; ++i)
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       const uint32_t b = n0 + 16u * j + fr;
@@ -930,18 +930,20 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
 
 } // namespace
 
-#define AXH_Q4K_MATMUL_KS(KS, NT, PF)                                                            \
+#define AXH_Q4K_MATMUL_KS(KS, NT, PF, RT, SUFFIX)                                                \
   extern "C" __global__ void __launch_bounds__(KS * 64)                                          \
-      axh_q4k_matmul_ks_k##KS##_n##NT##_p##PF(const uint8_t *__restrict__ q,                     \
-                                              const uint16_t *__restrict__ x,                    \
-                                              float *__restrict__ y, AXH_MATMUL_ARGS) { AXH_MATMUL_UNPACK; \
-    q4k_matmul_ks<KS, NT, PF>(q, x, y, a);                                                       \
+      axh_q4k_matmul_ks_k##KS##_n##NT##_p##PF##SUFFIX(const uint8_t *__restrict__ q,             \
+                                                      const uint16_t *__restrict__ x,            \
+                                                      float *__restrict__ y, AXH_MATMUL_ARGS) { AXH_MATMUL_UNPACK; \
+    q4k_matmul_ks<KS, NT, PF, RT>(q, x, y, a);                                                   \
   }
 
-AXH_Q4K_MATMUL_KS(4, 1, 2)
-AXH_Q4K_MATMUL_KS(8, 1, 1)
-AXH_Q4K_MATMUL_KS(4, 2, 2)
-AXH_Q4K_MATMUL_KS(8, 2, 1)
+AXH_Q4K_MATMUL_KS(4, 1, 2, 2, )
+AXH_Q4K_MATMUL_KS(8, 1, 1, 2, )
+AXH_Q4K_MATMUL_KS(4, 2, 2, 2, )
+AXH_Q4K_MATMUL_KS(8, 2, 1, 2, )
+AXH_Q4K_MATMUL_KS(8, 1, 1, 1, _r1)
+AXH_Q4K_MATMUL_KS(8, 1, 2, 1, _r1)
 
 #define AXH_Q4K_MATMUL_KX(RT, NT, KS, PF)                                                        \
   extern "C" __global__ void __launch_bounds__(KS * 64)                                          \

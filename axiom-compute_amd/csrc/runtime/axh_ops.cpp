@@ -39,7 +39,8 @@ struct MatmulArgs {
 // (LDS-tiled), 2 (register A), 4 (streaming) and 6 (row-split tile) were
 // removed: none was the fastest variant at any shape measured; their numbers
 // stay unused so that a request for one fails as an unknown variant.
-//   kind 3 (K-split)    axh_q4k_matmul_ks_k{W}_n{NT}_p{PF}: W waves split K of one 32-row tile;
+//   kind 3 (K-split)    axh_q4k_matmul_ks_k{W}_n{NT}_p{PF}[_r1]: W waves split K of one tile of
+//                       16 * RT rows (RT = 2, or 1 with _r1);
 //   kind 5 (K-split tile) axh_q4k_matmul_kx_r{RT}_n{NT}_k{W}_p{PF}: a 16*RT x 16*NT tile per
 //                       workgroup, its W waves splitting K by 64-wide superblock chunks,
 //                       register A, operands through per-wave LDS rings, PF superblocks in
@@ -49,10 +50,11 @@ struct MatmulArgs {
 //   kind 8 (32x32 tiles) axh_q4k_matmul_rm_w{W}_r{RT}_p4: W waves of RT 32-row MFMA tiles
 //                       over 128 columns, a 4-deep LDS ring.
 struct MatmulVariant {
-  uint32_t kind, w, nt, pf, rt; // rt: row tiles (kinds 5 and 8)
+  uint32_t kind, w, nt, pf, rt; // rt: row tiles (kinds 3, 5 and 8)
 };
 constexpr MatmulVariant kQ4kMatmulVariants[] = {
-    {3, 4, 1, 2, 0}, {3, 8, 1, 1, 0}, {3, 4, 2, 2, 0}, {3, 8, 2, 1, 0}, {5, 4, 8, 2, 4},
+    {3, 4, 1, 2, 2}, {3, 8, 1, 1, 2}, {3, 4, 2, 2, 2}, {3, 8, 2, 1, 2}, {3, 8, 1, 1, 1},
+    {3, 8, 1, 2, 1}, {5, 4, 8, 2, 4},
     {5, 4, 8, 2, 2}, {5, 4, 4, 2, 4}, {5, 4, 4, 3, 4}, {5, 4, 4, 2, 8}, {5, 4, 2, 2, 4},
     {5, 4, 2, 3, 4}, {5, 4, 1, 3, 4}, {7, 8, 1, 1, 0}, {7, 8, 2, 1, 0}, {7, 8, 1, 2, 0},
     {8, 8, 8, 4, 1}, {8, 4, 8, 4, 2}, {8, 4, 8, 4, 1}, {8, 2, 8, 4, 2}};
@@ -1051,11 +1053,13 @@ static MatmulVariant q4k_matmul_default(uint32_t n_rows, uint32_t batch, uint32_
     // not at four (8192 x 4096 x 64 18.6 against 16.3).
     if (groups(16, 32) <= 2 * kMatmulCus) return {7, 8, 2, 1, 0};
   }
-  // The K-split kind (32-row tiles, K over 8 waves) wherever its grid is one
-  // wave: long rows over few of them (4096 x 14336 at B = 8 28.9 us and 32
-  // 35.2 against the K-split tile kind's 39.4 and 40.7; 1024 x 14336 x 128
-  // 34.8 against 40.2).
-  if (groups(32, 16) <= kMatmulCus) return {3, 8, 1, 1, 0};
+  // The K-split kind (K over 8 waves) wherever its grid is one wave: long
+  // rows over few of them.  16-row tiles first (4096 x 14336 at B = 8 19.8
+  // us, B = 16 24.3, against 28.9 and 34.5 with 32-row tiles and 39.3 and
+  // 39.8 for the K-split tile kind), then 32-row tiles (4096 x 14336 x 32
+  // 35.4 against 40.2; 1024 x 14336 x 128 35.1 against 40.1).
+  if (groups(16, 16) <= kMatmulCus) return {3, 8, 1, 1, 1};
+  if (groups(32, 16) <= kMatmulCus) return {3, 8, 1, 1, 2};
   // kind 8 (32 x 32 MFMA tiles) where its rows fill the chip: 14336 x 4096 x
   // 512 74.1 us (8 waves of 32 rows) against 83-94 for a row-split kind,
   // B = 256 49.3 (4 waves of 32 rows) against 52.1; 8192 x 4096 x 512 46.0 us
@@ -1100,19 +1104,21 @@ static axh_status plan_q4k_matmul(uint32_t n_rows, uint32_t sb_per_row, uint32_t
     if (variant->col_tiles) want.nt = variant->col_tiles;
     if (variant->prefetch) want.pf = variant->prefetch;
     if (variant->row_tiles) {
-      if (want.kind != 5 && want.kind != 8)
-        return fail(AXH_ERR_INVALID_ARGUMENT, "row_tiles is a hole of matmul kinds 5 and 8 only");
+      if (want.kind != 3 && want.kind != 5 && want.kind != 8)
+        return fail(AXH_ERR_INVALID_ARGUMENT,
+                    "row_tiles is a hole of matmul kinds 3, 5 and 8 only");
       want.rt = variant->row_tiles;
     }
   }
-  if (want.kind != 5 && want.kind != 8) want.rt = 0;
-  else if (want.rt == 0) want.rt = want.kind == 5 ? 4u : 1u;
+  if (want.kind != 3 && want.kind != 5 && want.kind != 8) want.rt = 0;
+  else if (want.rt == 0) want.rt = want.kind == 5 ? 4u : want.kind == 3 ? 2u : 1u;
   for (const MatmulVariant &v : kQ4kMatmulVariants)
     if (v.kind == want.kind && v.w == want.w && v.nt == want.nt && v.pf == want.pf &&
         v.rt == want.rt) {
       *out = v;
       if (v.kind == 3)
-        std::snprintf(name, cap, "axh_q4k_matmul_ks_k%u_n%u_p%u", v.w, v.nt, v.pf);
+        std::snprintf(name, cap, "axh_q4k_matmul_ks_k%u_n%u_p%u%s", v.w, v.nt, v.pf,
+                      v.rt == 1 ? "_r1" : "");
       else if (v.kind == 5)
         std::snprintf(name, cap, "axh_q4k_matmul_kx_r%u_n%u_k%u_p%u", v.rt, v.nt, v.w, v.pf);
       else if (v.kind == 8)
@@ -1179,7 +1185,7 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
                                      : 0u;
   if (lds > ctx->core->max_lds)
     return fail(AXH_ERR_INVALID_ARGUMENT, "matmul variant needs more LDS than the device has");
-  const uint32_t tm = v.kind == 3   ? 32u
+  const uint32_t tm = v.kind == 3   ? 16u * v.rt
                       : v.kind == 5 ? 16u * v.rt
                       : v.kind == 7 ? 16u
                                     : 32u * v.rt * v.w;

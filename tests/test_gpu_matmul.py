@@ -128,6 +128,8 @@ def test_edge_shapes(ctx, rows, sb, batch):
                                                   (1000, 16, 60, "sr_w8_s2"),
                                                   (1024, 56, 128, "ks_k8_n1_p1"),
                                                   (4000, 56, 30, "ks_k8_n1_p1"),
+                                                  (4000, 56, 9, "ks_k8_n1_p1_r1"),
+                                                  (1000, 43, 31, "ks_k8_n1_p1_r1"),
                                                   (4096, 56, 100, "kx_r4_n2_k4_p3")])
 def test_grid_fill_defaults(ctx, axc, rows, sb, batch, kernel):
     """The defaults that follow from the grid on few rows: streaming rows past
