@@ -464,6 +464,195 @@ __device__ __forceinline__ void q4k_matmul_kx(const uint8_t *__restrict__ q,
 }
 
 // ---------------------------------------------------------------------------
+// Long rows over few of them (kind 9, axh_q4k_matmul_lk_c{XC}_x{XD}_w{WD}): a
+// workgroup of 8 waves owns one 16-row block and XC = 8 or 16 columns and
+// walks K in chunks of 8 superblocks, wave w taking superblock w of every
+// chunk.  A lane (row r = lane % 16, k-block g = lane / 16) loads the row's
+// header and the 32 qs bytes of chunk g of that superblock into registers,
+// WD chunks ahead, and dequantises them into the A fragments of 8 MFMA steps,
+// as q4k_matmul_sr does.  X for a chunk (XC columns x 2048 k, 4 KiB per
+// column) is staged in a ring of XD + 1 LDS buffers by coalesced direct-to-LDS
+// loads shared by the waves, XD chunks ahead: instruction (n, pc) copies 1 KiB
+// of column n (superblocks 2pc and 2pc + 1 of the chunk), lane l taking
+// 16-byte piece l ^ n, so that the 16 lanes of a fragment read (columns
+// 0..15, same piece) hit distinct banks.  One barrier per chunk.  Unlike
+// q4k_matmul_sr, which keeps X fragments in VGPRs and so stops at K = 4096,
+// any K fits; each workgroup reads X once, from L2.  At the end the 8 partial
+// 16x16 tiles are summed in LDS in wave order (deterministic).  For XC = 8
+// the lanes of MFMA columns 8..15 hold zero X fragments and store nothing.
+// ---------------------------------------------------------------------------
+template <int XC, int XD, int WD>
+__device__ __forceinline__ void q4k_matmul_lk(const uint8_t *__restrict__ q,
+                                              const uint16_t *__restrict__ x,
+                                              float *__restrict__ y, const MatmulArgs a,
+                                              f32x4_t *lds) {
+  static_assert(XC == 8 || XC == 16, "8 or 16 columns per workgroup");
+  constexpr int NW = 8, XR = XD + 1, WR = WD + 1; // ring slots of X (LDS) and weights (VGPRs)
+  static_assert(XD >= 1 && WD >= XD && WR % XR == 0 && WR <= 8,
+                "the weights run at least as far ahead as X, in a ring of whole X rings");
+  constexpr uint32_t kColB = 4096u;            // staged bytes of one column per chunk
+  constexpr uint32_t kSlot = XC * kColB / 16u; // f32x4 slots of an X buffer
+  constexpr int kXL = XC * 4 / NW;             // X instructions per wave per chunk
+  constexpr int kPer = kXL + 3;                // loads per wave per chunk
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t r = lane & 15u, g = lane >> 4;
+  const uint32_t n_rows = a.n_rows, nsb = a.sb_per_row, batch = a.batch;
+  const uint32_t K = nsb * 256u;
+  const uint32_t row_bytes = nsb * (uint32_t)kQ4kSbBytes;
+  const __amdgpu_buffer_rsrc_t qr = rsrc(q, n_rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t xr = rsrc(x, batch * K * 2u);
+  const uint32_t n_ch = (nsb + 7u) >> 3;
+  const uint32_t row = 16u * blockIdx.x + r, n0 = XC * blockIdx.y;
+  const uint32_t rr = r & (uint32_t)(XC - 1); // the lane's column within the group
+
+  // Per-lane offsets are prepared once and the chunk enters as an SGPR
+  // offset; loads past the last superblock or column read zeros (kFar, with
+  // room for the SGPR offset on top).
+  constexpr uint32_t kFar = 0xFFF00000u;
+  uint32_t xv0[kXL];
+#pragma unroll
+  for (int m = 0; m < kXL; ++m) {
+    const uint32_t qi = wave + (uint32_t)(NW * m), n = qi >> 2, col = n0 + n;
+    xv0[m] = col < batch ? col * K * 2u + 16u * (lane ^ n) : kFar;
+  }
+  const uint32_t xhalf = lane >> 5; // superblock of the lane's piece within the pair
+  const uint32_t wv0 = row < n_rows ? row * row_bytes : kFar;
+  // X of chunk c into X slot xs (this wave's instructions)
+  auto issue_x = [&](uint32_t c, auto xs_c) {
+    constexpr int xs = decltype(xs_c)::value;
+    f32x4_t *buf = lds + xs * kSlot;
+#pragma unroll
+    for (int m = 0; m < kXL; ++m) {
+      const uint32_t qi = wave + (uint32_t)(NW * m), n = qi >> 2, pc = qi & 3u;
+      const uint32_t s0 = 8u * c + 2u * pc;
+      const uint32_t v = s0 + xhalf < nsb ? xv0[m] : kFar;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void_t *)(buf + n * (kColB / 16u) + pc * 64u),
+                                               16, v, 512u * s0, 0, 0);
+    }
+  };
+  // weights of superblock 8c + wave into register slot ws
+  uint4 H[WR], QA[WR], QB[WR];
+  auto issue_w = [&](uint32_t c, auto ws_c) {
+    constexpr int ws = decltype(ws_c)::value;
+    const uint32_t sb = 8u * c + wave;
+    const uint32_t v = sb < nsb ? wv0 : kFar;
+    const u32x4_t h = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)v, (int)(sb * 144u), 0);
+    const u32x4_t qa =
+        __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(v + 16u + 32u * g), (int)(sb * 144u), 0);
+    const u32x4_t qb =
+        __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(v + 32u + 32u * g), (int)(sb * 144u), 0);
+    H[ws] = make_uint4(h.x, h.y, h.z, h.w);
+    QA[ws] = make_uint4(qa.x, qa.y, qa.z, qa.w);
+    QB[ws] = make_uint4(qb.x, qb.y, qb.z, qb.w);
+  };
+  // X fragment of step t: piece P = 32 (wave & 1) + 8g + t of the wave's
+  // superblock pair wave >> 1 in column rr.
+  uint32_t xa[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const uint32_t P = 32u * (wave & 1u) + 8u * g + (uint32_t)t;
+    xa[t] = rr * (kColB / 16u) + 64u * (wave >> 1) + (P ^ rr);
+  }
+  f32x4_t acc = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+  // Chunk c (c % WR = e) issues X of chunk c + XD, then the weights of chunk
+  // c + WD.  The issue order is fixed, so the loads issued after X of chunk c
+  // are always the 3 weight loads of its group and the XD - 1 groups in
+  // between: waiting for that many leaves the weights ahead in flight.
+  auto step = [&](uint32_t c, auto e_c) {
+    constexpr int e = decltype(e_c)::value;
+    // own X of chunk c landed; after the barrier every wave's X of chunk c is
+    // in LDS and chunk c - 1's X buffer is free
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((XD - 1) * kPer + 3) : "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    issue_x(c + (uint32_t)XD, std::integral_constant<int, (e + XD) % XR>{});
+    issue_w(c + (uint32_t)WD, std::integral_constant<int, (e + WD) % WR>{});
+    __builtin_amdgcn_sched_barrier(0);
+    const f32x4_t *buf = lds + (e % XR) * kSlot;
+    half8_t xf[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const half8_t v = __builtin_bit_cast(half8_t, buf[xa[t]]);
+      xf[t] = (XC == 16 || r < 8u) ? v : (half8_t){};
+    }
+    const uint4 hd = H[e];
+    const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
+    uint32_t scp, mp;
+    q4k_scale_min_pair(hd.y, hd.z, hd.w, g, &scp, &mp);
+    const float d1s = d * (float)(scp & 0xFFu) * 16777216.0f;
+    const float d2s = d * (float)(scp >> 8) * 1048576.0f;
+    const float m1 = dmin * (float)(mp & 0xFFu), m2 = dmin * (float)(mp >> 8);
+    const uint32_t w[8] = {QA[e].x, QA[e].y, QA[e].z, QA[e].w, QB[e].x, QB[e].y, QB[e].z, QB[e].w};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      uint32_t l0, l1, h0, h1, l2, l3, h2, h3;
+      dequant_dword(w[2 * t], d1s, m1, d2s, m2, l0, l1, h0, h1);
+      dequant_dword(w[2 * t + 1], d1s, m1, d2s, m2, l2, l3, h2, h3);
+      const half8_t alo = __builtin_bit_cast(half8_t, make_uint4(l0, l1, l2, l3));
+      const half8_t ahi = __builtin_bit_cast(half8_t, make_uint4(h0, h1, h2, h3));
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, xf[t], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, xf[t + 4], acc, 0, 0, 0);
+    }
+  };
+  // Prologue: the groups chunks -WD .. -1 would have issued (weights of
+  // chunks 0 .. WD - 1, X of chunks 0 .. XD - 1), in the same order.
+  auto pro = [&](auto i_c) {
+    constexpr int i = decltype(i_c)::value; // the group of chunk i - WD
+    if constexpr (i < WD) {
+      if constexpr (i - WD + XD >= 0)
+        issue_x((uint32_t)(i - WD + XD), std::integral_constant<int, (i - WD + XD) % XR>{});
+      issue_w((uint32_t)i, std::integral_constant<int, i>{});
+    }
+  };
+  pro(std::integral_constant<int, 0>{});
+  pro(std::integral_constant<int, 1>{});
+  pro(std::integral_constant<int, 2>{});
+  pro(std::integral_constant<int, 3>{});
+  pro(std::integral_constant<int, 4>{});
+  pro(std::integral_constant<int, 5>{});
+  pro(std::integral_constant<int, 6>{});
+  // Whole rounds of WR chunks, then the rest: no step of the loop body is
+  // conditional, so no load is left in flight on a path around the back edge
+  // (which made the compiler wait for every load at the loop head).
+  auto round = [&](uint32_t c0, auto e_c, bool guard) {
+    constexpr int e = decltype(e_c)::value;
+    if constexpr (e < WR)
+      if (!guard || c0 + (uint32_t)e < n_ch) step(c0 + (uint32_t)e, e_c);
+  };
+  uint32_t c0 = 0;
+  for (; c0 + (uint32_t)WR <= n_ch; c0 += (uint32_t)WR) {
+    round(c0, std::integral_constant<int, 0>{}, false);
+    round(c0, std::integral_constant<int, 1>{}, false);
+    round(c0, std::integral_constant<int, 2>{}, false);
+    round(c0, std::integral_constant<int, 3>{}, false);
+    round(c0, std::integral_constant<int, 4>{}, false);
+    round(c0, std::integral_constant<int, 5>{}, false);
+    round(c0, std::integral_constant<int, 6>{}, false);
+    round(c0, std::integral_constant<int, 7>{}, false);
+  }
+  round(c0, std::integral_constant<int, 0>{}, true);
+  round(c0, std::integral_constant<int, 1>{}, true);
+  round(c0, std::integral_constant<int, 2>{}, true);
+  round(c0, std::integral_constant<int, 3>{}, true);
+  round(c0, std::integral_constant<int, 4>{}, true);
+  round(c0, std::integral_constant<int, 5>{}, true);
+  round(c0, std::integral_constant<int, 6>{}, true);
+  // every load (the ones past the last chunk too) has landed before the LDS
+  // is reused and before the waves end
+  f32x4_t *red = lds + XR * kSlot;
+  red[wave * 64u + lane] = acc;
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if (wave == 0u) {
+    f32x4_t sum = red[lane];
+#pragma unroll
+    for (uint32_t w2 = 1; w2 < (uint32_t)NW; ++w2) sum += red[w2 * 64u + lane];
+    const uint32_t col = n0 + r;
+    if ((XC == 16 || r < 8u) && col < batch)
+      store_col4(y + (size_t)col * n_rows, 16u * blockIdx.x + 4u * g, n_rows, sum);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // 32 x 32 tiles with wide waves (kind 8, axh_q4k_matmul_rm_w{W}_r{RT}_p4): a
 // workgroup of W waves owns 32 * RT * W rows x 128 columns of Y; wave w owns
 // 32 * RT rows (RT 32-row MFMA tiles) x 128 columns (four 32-column tiles) and
@@ -989,3 +1178,17 @@ AXH_Q4K_MATMUL_RM(2, 2)
 AXH_Q4K_MATMUL_SR(8, 2, 1, false, )
 AXH_Q4K_MATMUL_SR(8, 2, 2, false, _n2)
 AXH_Q4K_MATMUL_SR(8, 2, 1, true, _h)
+
+#define AXH_Q4K_MATMUL_LK(XC, XD, WD)                                                            \
+  extern "C" __global__ void __launch_bounds__(512)                                              \
+      axh_q4k_matmul_lk_c##XC##_x##XD##_w##WD(const uint8_t *__restrict__ q,                     \
+                                              const uint16_t *__restrict__ x,                    \
+                                              float *__restrict__ y, AXH_MATMUL_ARGS) {          \
+    AXH_MATMUL_UNPACK;                                                                           \
+    extern __shared__ f32x4_t axh_lk_dyn[];                                                      \
+    q4k_matmul_lk<XC, XD, WD>(q, x, y, a, axh_lk_dyn);                                           \
+  }
+
+AXH_Q4K_MATMUL_LK(8, 2, 2)
+AXH_Q4K_MATMUL_LK(8, 1, 3)
+AXH_Q4K_MATMUL_LK(16, 1, 3)

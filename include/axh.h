@@ -386,16 +386,21 @@ axh_status axh_q4_0_matvec_variant_at(uint32_t i, axh_q4_variant *out);
 typedef struct axh_q4_matmul_variant {
     uint32_t kind;                /* 3 K-split, 5 K-split tile, 7 streaming rows
                                      (K <= 4096), 8 32x32 tiles (128 columns per
-                                     workgroup); 0 = default, chosen by the grid
+                                     workgroup), 9 long rows (K < 262144, X in
+                                     chunks through LDS); 0 = default, chosen by the grid
                                      each kind launches on 256 CUs.  Kinds 1, 2, 4
                                      and 6 were removed (no shape where they won) */
-    uint32_t waves_per_workgroup; /* 3, 5, 7: waves splitting K; 8: waves of row_tiles
+    uint32_t waves_per_workgroup; /* 3, 5, 7, 9: waves splitting K; 8: waves of row_tiles
                                      row tiles each */
-    uint32_t col_tiles;           /* 16-column MFMA tiles per workgroup (kind 8: 8) */
+    uint32_t col_tiles;           /* 16-column MFMA tiles per workgroup (kind 8: 8;
+                                     kind 9: 8-column groups, 1 or 2) */
     uint32_t prefetch;            /* K steps in flight (kinds 3, 7; kind 7 prefetch 2:
-                                     8-column groups), LDS ring depth (5, 8: 4) */
-    uint32_t row_tiles;           /* kind 5: 16-row MFMA tiles per wave (0: 4); kind 8:
-                                     32-row tiles per wave (0: 1); 0 otherwise */
+                                     8-column groups), LDS ring depth (5, 8: 4), X
+                                     chunks in flight (9) */
+    uint32_t row_tiles;           /* kind 3: 16-row MFMA tiles (0: 2); kind 5: 16-row
+                                     MFMA tiles per wave (0: 4); kind 8: 32-row tiles
+                                     per wave (0: 1); kind 9: weight chunks in flight
+                                     (0: 3); 0 otherwise */
 } axh_q4_matmul_variant;
 axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x, float *y,
                               uint32_t n_rows, uint32_t sb_per_row, uint32_t batch,

@@ -127,14 +127,17 @@ def test_edge_shapes(ctx, rows, sb, batch):
                                                   (2000, 16, 100, "sr_w8_s2_n2"),
                                                   (1000, 16, 60, "sr_w8_s2"),
                                                   (1024, 56, 128, "ks_k8_n1_p1"),
-                                                  (4000, 56, 30, "ks_k8_n1_p1"),
-                                                  (4000, 56, 9, "ks_k8_n1_p1_r1"),
-                                                  (1000, 43, 31, "ks_k8_n1_p1_r1"),
+                                                  (1000, 56, 60, "ks_k8_n1_p1_r1"),
+                                                  (4000, 56, 30, "lk_c16_x1_w3"),
+                                                  (4000, 56, 7, "lk_c8_x2_w2"),
+                                                  (8100, 43, 5, "lk_c8_x1_w3"),
+                                                  (1000, 43, 31, "lk_c16_x1_w3"),
                                                   (4096, 56, 100, "kx_r4_n2_k4_p3")])
 def test_grid_fill_defaults(ctx, axc, rows, sb, batch, kernel):
     """The defaults that follow from the grid on few rows: streaming rows past
-    32 columns (several column groups, the last one partial), the K-split kind
-    at K > 4096 up to 128 columns, K-split tiles with their columns halved."""
+    32 columns (several column groups, the last one partial), kind 9 at K >
+    4096 up to 32 columns, the K-split kind up to 128, K-split tiles with
+    their columns halved."""
     assert axc.q4k_matmul_kernel_name(rows, sb, batch) == "axh_q4k_matmul_" + kernel
     _say(f"matmul default {kernel} {rows}x{sb * 256} B={batch}")
     q, xh = _inputs(rows + 3 * sb + 5 * batch, rows, sb, batch)
@@ -165,6 +168,24 @@ def test_tile_kinds_on_odd_shapes(ctx, axc, rows, sb, batch):
         _say(f"matmul odd shape {rows}x{sb} B={batch} variant {v}")
         y = _run(ctx, q, xh, rows, sb, batch, v)
         _check(y, q, xh, rows, sb, batch, f"odd {rows}x{sb} B={batch} {v}")
+
+
+@pytest.mark.parametrize("rows,sb,batch", [(4096, 56, 8), (1000, 43, 5), (37, 9, 16), (130, 1, 1),
+                                           (300, 17, 20), (64, 64, 3), (20, 8, 9)])
+def test_long_rows_kind(ctx, axc, rows, sb, batch):
+    """Kind 9 (8 waves over one 16-row block, K in chunks of 8 superblocks,
+    X through an LDS ring) in every compiled form: whole and partial chunks
+    (56, 43, 9, 1, 17 superblocks; 64 and 8 fill the ring rounds exactly),
+    more chunks than the ring holds, rows past the last block, 8- and
+    16-column groups with partial ones (5, 9, 16, 20 columns)."""
+    q, xh = _inputs(rows * 5 + sb * 7 + batch, rows, sb, batch)
+    for v in axc.compiled_matmul_variants():
+        if v.kind != 9:
+            continue
+        _say(f"matmul long rows {rows}x{sb * 256} B={batch} "
+             f"{axc.q4k_matmul_kernel_name(rows, sb, batch, v)}")
+        y = _run(ctx, q, xh, rows, sb, batch, v)
+        _check(y, q, xh, rows, sb, batch, f"long rows {rows}x{sb} B={batch} {v}")
 
 
 @pytest.mark.parametrize("rows,sb,batch", [(5000, 13, 13), (4097, 16, 16), (17, 7, 1),

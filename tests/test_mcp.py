@@ -87,7 +87,7 @@ def test_variant_id_matches_the_enumerator(mcp, tune):
 
 def test_default_hole_spaces_come_from_compiled_variants(mcp, axc):
     h = mcp.default_holes("q4k_matmul_f16")
-    assert set(h["kind"]) == {3, 5, 7, 8}
+    assert set(h["kind"]) == {3, 5, 7, 8, 9}
     assert 0 in h["row_tiles"] and 4 in h["row_tiles"]
     assert mcp.default_holes("q4_0_dequant_matvec")["waves_per_workgroup"] == [1, 4]
 
