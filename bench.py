@@ -14,6 +14,8 @@ JSON line.  Other BASELINE configs are measured with --workload:
   head  Q4_K matvec 128256 x 4096              (output head)
   c5    Q4_K matmul 14336 x 4096, --batch B    (f16 activations; GB/s for B <= 32,
                                                 TFLOP/s for larger B)
+  down  Q4_K matmul 4096 x 14336, --batch B    (the c4 weights against B activation
+                                                vectors: batched decode; not a config)
 
   python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--workload c4] [--batch 128]
 """
@@ -45,6 +47,8 @@ WORKLOADS = {
     "c4": ("q4k", 4096, 56, 0.5, "BASELINE config 4, down-projection"),
     "head": ("q4k", 128256, 16, 1.0, "BASELINE config 4, output head"),
     "c5": ("matmul", 14336, 16, 1.0, "BASELINE config 5"),
+    # the c4 down-projection against several activation vectors (batched decode)
+    "down": ("matmul", 4096, 56, 1.0, "Llama-3-8B ffn_down batched, not a BASELINE config"),
     # fused SwiGLU gate/up projections of a Llama-3-8B decode step (two
     # 14336 x 4096 Q4_K_M matrices against one x)
     "ffn": ("gate_up", 14336, 16, 0.5, "Llama-3-8B gate/up, not a BASELINE config"),
@@ -317,7 +321,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c4", choices=sorted(WORKLOADS))
-    ap.add_argument("--batch", type=int, default=128, help="activation vectors (c5 only)")
+    ap.add_argument("--batch", type=int, default=128, help="activation vectors (c5 and down only)")
     ap.add_argument("--x-f32", action="store_true",
                     help="c5 only: f32 activations (cast to f16 by a separate pass, then the "
                          "f16 matmul; both timed)")
