@@ -464,8 +464,9 @@ __device__ __forceinline__ void q4k_matmul_kx(const uint8_t *__restrict__ q,
 }
 
 // ---------------------------------------------------------------------------
-// Long rows over few of them (kind 9, axh_q4k_matmul_lk_c{XC}_x{XD}_w{WD}): a
-// workgroup of 8 waves owns one 16-row block and XC = 8 or 16 columns and
+// Long rows over few of them (kind 9, axh_q4k_matmul_lk_c{XC}_x{XD}_w{WD}[_r2]):
+// a workgroup of 8 waves owns 16 * RT rows (RT = 1, or 2 with _r2: each wave
+// then works on two 16-row tiles) and XC = 8 or 16 columns and
 // walks K in chunks of 8 superblocks, wave w taking superblock w of every
 // chunk.  A lane (row r = lane % 16, k-block g = lane / 16) loads the row's
 // header and the 32 qs bytes of chunk g of that superblock into registers,
@@ -481,19 +482,20 @@ __device__ __forceinline__ void q4k_matmul_kx(const uint8_t *__restrict__ q,
 // 16x16 tiles are summed in LDS in wave order (deterministic).  For XC = 8
 // the lanes of MFMA columns 8..15 hold zero X fragments and store nothing.
 // ---------------------------------------------------------------------------
-template <int XC, int XD, int WD>
+template <int XC, int XD, int WD, int RT = 1>
 __device__ __forceinline__ void q4k_matmul_lk(const uint8_t *__restrict__ q,
                                               const uint16_t *__restrict__ x,
                                               float *__restrict__ y, const MatmulArgs a,
                                               f32x4_t *lds) {
   static_assert(XC == 8 || XC == 16, "8 or 16 columns per workgroup");
+  static_assert(RT == 1 || RT == 2, "16 or 32 rows per workgroup");
   constexpr int NW = 8, XR = XD + 1, WR = WD + 1; // ring slots of X (LDS) and weights (VGPRs)
   static_assert(XD >= 1 && WD >= XD && WR % XR == 0 && WR <= 8,
                 "the weights run at least as far ahead as X, in a ring of whole X rings");
   constexpr uint32_t kColB = 4096u;            // staged bytes of one column per chunk
   constexpr uint32_t kSlot = XC * kColB / 16u; // f32x4 slots of an X buffer
   constexpr int kXL = XC * 4 / NW;             // X instructions per wave per chunk
-  constexpr int kPer = kXL + 3;                // loads per wave per chunk
+  constexpr int kPer = kXL + 3 * RT;           // loads per wave per chunk
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t r = lane & 15u, g = lane >> 4;
@@ -503,7 +505,7 @@ __device__ __forceinline__ void q4k_matmul_lk(const uint8_t *__restrict__ q,
   const __amdgpu_buffer_rsrc_t qr = rsrc(q, n_rows * row_bytes);
   const __amdgpu_buffer_rsrc_t xr = rsrc(x, batch * K * 2u);
   const uint32_t n_ch = (nsb + 7u) >> 3;
-  const uint32_t row = 16u * blockIdx.x + r, n0 = XC * blockIdx.y;
+  const uint32_t m0 = 16u * RT * blockIdx.x, n0 = XC * blockIdx.y;
   const uint32_t rr = r & (uint32_t)(XC - 1); // the lane's column within the group
 
   // Per-lane offsets are prepared once and the chunk enters as an SGPR
@@ -517,7 +519,12 @@ __device__ __forceinline__ void q4k_matmul_lk(const uint8_t *__restrict__ q,
     xv0[m] = col < batch ? col * K * 2u + 16u * (lane ^ n) : kFar;
   }
   const uint32_t xhalf = lane >> 5; // superblock of the lane's piece within the pair
-  const uint32_t wv0 = row < n_rows ? row * row_bytes : kFar;
+  uint32_t wv0[RT];
+#pragma unroll
+  for (int i = 0; i < RT; ++i) {
+    const uint32_t row = m0 + 16u * (uint32_t)i + r;
+    wv0[i] = row < n_rows ? row * row_bytes : kFar;
+  }
   // X of chunk c into X slot xs (this wave's instructions)
   auto issue_x = [&](uint32_t c, auto xs_c) {
     constexpr int xs = decltype(xs_c)::value;
@@ -531,20 +538,23 @@ __device__ __forceinline__ void q4k_matmul_lk(const uint8_t *__restrict__ q,
                                                16, v, 512u * s0, 0, 0);
     }
   };
-  // weights of superblock 8c + wave into register slot ws
-  uint4 H[WR], QA[WR], QB[WR];
+  // weights of superblock 8c + wave (each row tile) into register slot ws
+  uint4 H[WR][RT], QA[WR][RT], QB[WR][RT];
   auto issue_w = [&](uint32_t c, auto ws_c) {
     constexpr int ws = decltype(ws_c)::value;
     const uint32_t sb = 8u * c + wave;
-    const uint32_t v = sb < nsb ? wv0 : kFar;
-    const u32x4_t h = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)v, (int)(sb * 144u), 0);
-    const u32x4_t qa =
-        __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(v + 16u + 32u * g), (int)(sb * 144u), 0);
-    const u32x4_t qb =
-        __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(v + 32u + 32u * g), (int)(sb * 144u), 0);
-    H[ws] = make_uint4(h.x, h.y, h.z, h.w);
-    QA[ws] = make_uint4(qa.x, qa.y, qa.z, qa.w);
-    QB[ws] = make_uint4(qb.x, qb.y, qb.z, qb.w);
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+      const uint32_t v = sb < nsb ? wv0[i] : kFar;
+      const u32x4_t h = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)v, (int)(sb * 144u), 0);
+      const u32x4_t qa =
+          __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(v + 16u + 32u * g), (int)(sb * 144u), 0);
+      const u32x4_t qb =
+          __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(v + 32u + 32u * g), (int)(sb * 144u), 0);
+      H[ws][i] = make_uint4(h.x, h.y, h.z, h.w);
+      QA[ws][i] = make_uint4(qa.x, qa.y, qa.z, qa.w);
+      QB[ws][i] = make_uint4(qb.x, qb.y, qb.z, qb.w);
+    }
   };
   // X fragment of step t: piece P = 32 (wave & 1) + 8g + t of the wave's
   // superblock pair wave >> 1 in column rr.
@@ -554,7 +564,9 @@ __device__ __forceinline__ void q4k_matmul_lk(const uint8_t *__restrict__ q,
     const uint32_t P = 32u * (wave & 1u) + 8u * g + (uint32_t)t;
     xa[t] = rr * (kColB / 16u) + 64u * (wave >> 1) + (P ^ rr);
   }
-  f32x4_t acc = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4_t acc[RT];
+#pragma unroll
+  for (int i = 0; i < RT; ++i) acc[i] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
   // Chunk c (c % WR = e) issues X of chunk c + XD, then the weights of chunk
   // c + WD.  The issue order is fixed, so the loads issued after X of chunk c
   // are always the 3 weight loads of its group and the XD - 1 groups in
@@ -575,23 +587,27 @@ __device__ __forceinline__ void q4k_matmul_lk(const uint8_t *__restrict__ q,
       const half8_t v = __builtin_bit_cast(half8_t, buf[xa[t]]);
       xf[t] = (XC == 16 || r < 8u) ? v : (half8_t){};
     }
-    const uint4 hd = H[e];
-    const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
-    uint32_t scp, mp;
-    q4k_scale_min_pair(hd.y, hd.z, hd.w, g, &scp, &mp);
-    const float d1s = d * (float)(scp & 0xFFu) * 16777216.0f;
-    const float d2s = d * (float)(scp >> 8) * 1048576.0f;
-    const float m1 = dmin * (float)(mp & 0xFFu), m2 = dmin * (float)(mp >> 8);
-    const uint32_t w[8] = {QA[e].x, QA[e].y, QA[e].z, QA[e].w, QB[e].x, QB[e].y, QB[e].z, QB[e].w};
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      uint32_t l0, l1, h0, h1, l2, l3, h2, h3;
-      dequant_dword(w[2 * t], d1s, m1, d2s, m2, l0, l1, h0, h1);
-      dequant_dword(w[2 * t + 1], d1s, m1, d2s, m2, l2, l3, h2, h3);
-      const half8_t alo = __builtin_bit_cast(half8_t, make_uint4(l0, l1, l2, l3));
-      const half8_t ahi = __builtin_bit_cast(half8_t, make_uint4(h0, h1, h2, h3));
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, xf[t], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, xf[t + 4], acc, 0, 0, 0);
+    for (int i = 0; i < RT; ++i) {
+      const uint4 hd = H[e][i];
+      const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
+      uint32_t scp, mp;
+      q4k_scale_min_pair(hd.y, hd.z, hd.w, g, &scp, &mp);
+      const float d1s = d * (float)(scp & 0xFFu) * 16777216.0f;
+      const float d2s = d * (float)(scp >> 8) * 1048576.0f;
+      const float m1 = dmin * (float)(mp & 0xFFu), m2 = dmin * (float)(mp >> 8);
+      const uint32_t w[8] = {QA[e][i].x, QA[e][i].y, QA[e][i].z, QA[e][i].w,
+                             QB[e][i].x, QB[e][i].y, QB[e][i].z, QB[e][i].w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        uint32_t l0, l1, h0, h1, l2, l3, h2, h3;
+        dequant_dword(w[2 * t], d1s, m1, d2s, m2, l0, l1, h0, h1);
+        dequant_dword(w[2 * t + 1], d1s, m1, d2s, m2, l2, l3, h2, h3);
+        const half8_t alo = __builtin_bit_cast(half8_t, make_uint4(l0, l1, l2, l3));
+        const half8_t ahi = __builtin_bit_cast(half8_t, make_uint4(h0, h1, h2, h3));
+        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, xf[t], acc[i], 0, 0, 0);
+        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, xf[t + 4], acc[i], 0, 0, 0);
+      }
     }
   };
   // Prologue: the groups chunks -WD .. -1 would have issued (weights of
@@ -640,15 +656,16 @@ __device__ __forceinline__ void q4k_matmul_lk(const uint8_t *__restrict__ q,
   // every load (the ones past the last chunk too) has landed before the LDS
   // is reused and before the waves end
   f32x4_t *red = lds + XR * kSlot;
-  red[wave * 64u + lane] = acc;
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  if (wave == 0u) {
-    f32x4_t sum = red[lane];
 #pragma unroll
-    for (uint32_t w2 = 1; w2 < (uint32_t)NW; ++w2) sum += red[w2 * 64u + lane];
+  for (int i = 0; i < RT; ++i) red[(wave * RT + (uint32_t)i) * 64u + lane] = acc[i];
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if (wave < (uint32_t)RT) { // wave i sums and stores row tile i
+    f32x4_t sum = red[wave * 64u + lane];
+#pragma unroll
+    for (uint32_t w2 = 1; w2 < (uint32_t)NW; ++w2) sum += red[(w2 * RT + wave) * 64u + lane];
     const uint32_t col = n0 + r;
     if ((XC == 16 || r < 8u) && col < batch)
-      store_col4(y + (size_t)col * n_rows, 16u * blockIdx.x + 4u * g, n_rows, sum);
+      store_col4(y + (size_t)col * n_rows, m0 + 16u * wave + 4u * g, n_rows, sum);
   }
 }
 
@@ -1179,16 +1196,18 @@ AXH_Q4K_MATMUL_SR(8, 2, 1, false, )
 AXH_Q4K_MATMUL_SR(8, 2, 2, false, _n2)
 AXH_Q4K_MATMUL_SR(8, 2, 1, true, _h)
 
-#define AXH_Q4K_MATMUL_LK(XC, XD, WD)                                                            \
+#define AXH_Q4K_MATMUL_LK(XC, XD, WD, RT, SUFFIX)                                               \
   extern "C" __global__ void __launch_bounds__(512)                                              \
-      axh_q4k_matmul_lk_c##XC##_x##XD##_w##WD(const uint8_t *__restrict__ q,                     \
-                                              const uint16_t *__restrict__ x,                    \
-                                              float *__restrict__ y, AXH_MATMUL_ARGS) {          \
+      axh_q4k_matmul_lk_c##XC##_x##XD##_w##WD##SUFFIX(const uint8_t *__restrict__ q,             \
+                                                      const uint16_t *__restrict__ x,            \
+                                                      float *__restrict__ y, AXH_MATMUL_ARGS) {  \
     AXH_MATMUL_UNPACK;                                                                           \
     extern __shared__ f32x4_t axh_lk_dyn[];                                                      \
-    q4k_matmul_lk<XC, XD, WD>(q, x, y, a, axh_lk_dyn);                                           \
+    q4k_matmul_lk<XC, XD, WD, RT>(q, x, y, a, axh_lk_dyn);                                       \
   }
 
-AXH_Q4K_MATMUL_LK(8, 2, 2)
-AXH_Q4K_MATMUL_LK(8, 1, 3)
-AXH_Q4K_MATMUL_LK(16, 1, 3)
+AXH_Q4K_MATMUL_LK(8, 2, 2, 1, )
+AXH_Q4K_MATMUL_LK(8, 1, 3, 1, )
+AXH_Q4K_MATMUL_LK(16, 1, 3, 1, )
+AXH_Q4K_MATMUL_LK(8, 2, 2, 2, _r2)
+AXH_Q4K_MATMUL_LK(16, 1, 3, 2, _r2)

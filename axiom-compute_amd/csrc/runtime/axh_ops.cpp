@@ -49,20 +49,20 @@ struct MatmulArgs {
 //                       CU over 16-row blocks, K <= 4096 (pf 2: 8-column groups).
 //   kind 8 (32x32 tiles) axh_q4k_matmul_rm_w{W}_r{RT}_p4: W waves of RT 32-row MFMA tiles
 //                       over 128 columns, a 4-deep LDS ring.
-//   kind 9 (long rows)  axh_q4k_matmul_lk_c{8*NT}_x{PF}_w{RT}: 8 waves over one 16-row block
-//                       and 8 * NT columns (col_tiles counts 8-column groups), K in chunks of
-//                       8 superblocks, X through an LDS ring PF chunks ahead, the weights in
-//                       registers RT chunks ahead (row_tiles counts chunks here).
+//   kind 9 (long rows)  axh_q4k_matmul_lk_c{8*NT}_x{PF}_w{WD}[_r2]: 8 waves over RT 16-row
+//                       tiles and 8 * NT columns (col_tiles counts 8-column groups), K in
+//                       chunks of 8 superblocks, X through an LDS ring PF chunks ahead, the
+//                       weights in registers WD chunks ahead (3 for PF 1, else PF).
 struct MatmulVariant {
-  uint32_t kind, w, nt, pf, rt; // rt: row tiles (kinds 3, 5 and 8), weight chunks ahead (9)
+  uint32_t kind, w, nt, pf, rt; // rt: row tiles (kinds 3, 5, 8 and 9)
 };
 constexpr MatmulVariant kQ4kMatmulVariants[] = {
     {3, 4, 1, 2, 2}, {3, 8, 1, 1, 2}, {3, 4, 2, 2, 2}, {3, 8, 2, 1, 2}, {3, 8, 1, 1, 1},
     {3, 8, 1, 2, 1}, {5, 4, 8, 2, 4},
     {5, 4, 8, 2, 2}, {5, 4, 4, 2, 4}, {5, 4, 4, 3, 4}, {5, 4, 4, 2, 8}, {5, 4, 2, 2, 4},
     {5, 4, 2, 3, 4}, {5, 4, 1, 3, 4}, {7, 8, 1, 1, 0}, {7, 8, 2, 1, 0}, {7, 8, 1, 2, 0},
-    {8, 8, 8, 4, 1}, {8, 4, 8, 4, 2}, {8, 4, 8, 4, 1}, {8, 2, 8, 4, 2}, {9, 8, 1, 2, 2},
-    {9, 8, 1, 1, 3}, {9, 8, 2, 1, 3}};
+    {8, 8, 8, 4, 1}, {8, 4, 8, 4, 2}, {8, 4, 8, 4, 1}, {8, 2, 8, 4, 2}, {9, 8, 1, 2, 1},
+    {9, 8, 1, 1, 1}, {9, 8, 2, 1, 1}, {9, 8, 1, 2, 2}, {9, 8, 2, 1, 2}};
 // The matmul kernels read zeros through offsets at or past 0xFFF00000 (with
 // the step offsets on top), and address rows up to 16 past the matrix: q and
 // x must stay below that, with 16 rows to spare.
@@ -1023,12 +1023,12 @@ static uint32_t rm_lds_bytes(const MatmulVariant &v) {
 }
 
 // Kind 9 LDS: a ring of pf + 1 buffers of the X chunk (8 * nt columns x 4
-// KiB), then the waves' partial tiles (1 KiB each).  Its loads take the
+// KiB), then the waves' partial tiles (1 KiB each, rt per wave).  Its loads take the
 // chunk as an SGPR offset of 512 bytes per superblock (X), up to 3 chunks
 // past the row, over the zero-reading offset 0xFFF00000, which leaves 1 MiB:
 // rows of fewer than 1024 superblocks keep it below 2^32.
 static uint32_t lk_lds_bytes(const MatmulVariant &v) {
-  return (v.pf + 1u) * 8u * v.nt * 4096u + 8u * 1024u;
+  return (v.pf + 1u) * 8u * v.nt * 4096u + 8u * v.rt * 1024u;
 }
 constexpr uint32_t kLkMaxSb = 1024;
 
@@ -1068,19 +1068,26 @@ static MatmulVariant q4k_matmul_default(uint32_t n_rows, uint32_t batch, uint32_
     // not at four (8192 x 4096 x 64 18.6 against 16.3).
     if (groups(16, 32) <= 2 * kMatmulCus) return {7, 8, 2, 1, 0};
   }
-  // Long rows (K > 4096) over few of them, up to 32 columns: kind 9 (one
-  // 16-row block per workgroup, K in chunks of 8 superblocks, X through an
-  // LDS ring) while its grid is at most two waves.  4096 x 14336: B = 1 11.0
-  // us, B = 8 13.6, B = 16 16.1, B = 32 27.7, against 16.3, 19.8, 24.4 and
-  // 35.1 for the K-split kind; 8192 x 14336 x 8 25.0 (two workgroups per CU,
-  // X one chunk ahead) against 29.8.  At 14336 x 14336 x 8 (896 workgroups)
-  // the K-split tile kind stays ahead (40.2 against 42.6).
+  // Long rows (K > 4096) over few of them, up to 32 columns: kind 9 (8 waves
+  // over 16 or 32 rows and 8 or 16 columns, K in chunks of 8 superblocks, X
+  // through an LDS ring).  Every workgroup reads all of X for its columns, so
+  // the largest tile whose grid still fills the chip wins: 4096 x 14336 x 32
+  // 23.4 us with 32 x 16 tiles against 28.2 with 16 x 16 and 35.7 for the
+  // K-split kind; B = 16 16.5 with 16 x 16 (32 x 16: 128 workgroups, 23.5);
+  // B = 8 13.6 with 16 x 8 against 19.9 for the K-split kind; 8192 x 14336 x
+  // 8 22.5 with 32 x 8 against 30.5.  Only while the grid is one wave (one
+  // workgroup per CU): with more, the K-split tile kind is ahead (8192 x
+  // 14336 x 32 42.4 against 45.0; 14336 x 14336 x 8 40.1 against 41.5).
   if (nsb > kSrMaxSb && batch <= 32) {
-    const uint32_t xc = batch <= 8 ? 8u : 16u;
-    const uint64_t lk = groups(16, xc);
-    if (lk <= kMatmulCus) return xc == 8 ? MatmulVariant{9, 8, 1, 2, 2} : MatmulVariant{9, 8, 2, 1, 3};
-    if (lk <= 2 * kMatmulCus)
-      return xc == 8 ? MatmulVariant{9, 8, 1, 1, 3} : MatmulVariant{9, 8, 2, 1, 3};
+    constexpr uint32_t cand[4][2] = {{16, 2}, {16, 1}, {8, 2}, {8, 1}}; // columns, row tiles
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t xc = cand[i][0], rt = cand[i][1];
+      if (batch <= 8 && xc == 16) continue;
+      const uint64_t g = groups(16 * rt, xc);
+      if (g < kMatmulFill && i < 3) continue;
+      if (g <= kMatmulCus) return xc == 16 ? MatmulVariant{9, 8, 2, 1, rt} : MatmulVariant{9, 8, 1, 2, rt};
+      break;
+    }
   }
   // The K-split kind (K over 8 waves) wherever its grid is one wave: long
   // rows over few of them.  16-row tiles first (4096 x 14336 at B = 8 19.8
@@ -1141,7 +1148,7 @@ static axh_status plan_q4k_matmul(uint32_t n_rows, uint32_t sb_per_row, uint32_t
   }
   if (want.kind != 3 && want.kind != 5 && want.kind != 8 && want.kind != 9) want.rt = 0;
   else if (want.rt == 0)
-    want.rt = want.kind == 5 ? 4u : want.kind == 3 ? 2u : want.kind == 9 ? 3u : 1u;
+    want.rt = want.kind == 5 ? 4u : want.kind == 3 ? 2u : 1u;
   for (const MatmulVariant &v : kQ4kMatmulVariants)
     if (v.kind == want.kind && v.w == want.w && v.nt == want.nt && v.pf == want.pf &&
         v.rt == want.rt) {
@@ -1157,7 +1164,8 @@ static axh_status plan_q4k_matmul(uint32_t n_rows, uint32_t sb_per_row, uint32_t
         if (sb_per_row >= kLkMaxSb)
           return fail(AXH_ERR_INVALID_ARGUMENT,
                       "matmul kind 9 takes rows of fewer than 1024 superblocks");
-        std::snprintf(name, cap, "axh_q4k_matmul_lk_c%u_x%u_w%u", 8u * v.nt, v.pf, v.rt);
+        std::snprintf(name, cap, "axh_q4k_matmul_lk_c%u_x%u_w%u%s", 8u * v.nt, v.pf,
+                      v.pf == 1u ? 3u : v.pf, v.rt == 2u ? "_r2" : "");
       }
       else {
         if (sb_per_row > kSrMaxSb)
@@ -1224,7 +1232,8 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
     return fail(AXH_ERR_INVALID_ARGUMENT, "matmul variant needs more LDS than the device has");
   const uint32_t tm = v.kind == 3   ? 16u * v.rt
                       : v.kind == 5 ? 16u * v.rt
-                      : v.kind == 7 || v.kind == 9 ? 16u
+                      : v.kind == 7 ? 16u
+                      : v.kind == 9 ? 16u * v.rt
                                     : 32u * v.rt * v.w;
   const uint32_t tn = (v.kind == 7 && v.pf == 2) || v.kind == 9 ? 8u * v.nt : 16u * v.nt;
   uint64_t gx = (n_rows + tm - 1) / tm;

@@ -399,8 +399,8 @@ typedef struct axh_q4_matmul_variant {
                                      chunks in flight (9) */
     uint32_t row_tiles;           /* kind 3: 16-row MFMA tiles (0: 2); kind 5: 16-row
                                      MFMA tiles per wave (0: 4); kind 8: 32-row tiles
-                                     per wave (0: 1); kind 9: weight chunks in flight
-                                     (0: 3); 0 otherwise */
+                                     per wave (0: 1); kind 9: 16-row tiles per
+                                     workgroup (0: 1); 0 otherwise */
 } axh_q4_matmul_variant;
 axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x, float *y,
                               uint32_t n_rows, uint32_t sb_per_row, uint32_t batch,

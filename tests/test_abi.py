@@ -221,19 +221,20 @@ def test_matmul_kernel_selection(axc):
     assert name(1024, 16, 64) == "axh_q4k_matmul_sr_w8_s2"
     assert name(4096, 16, 64) == "axh_q4k_matmul_sr_w8_s2_n2"  # two blocks of 32 columns per CU
     assert name(8192, 16, 64) == "axh_q4k_matmul_kx_r4_n2_k4_p2"  # four: K-split tiles
-    # K > 4096 over few rows: kind 9 (one 16-row block per workgroup) up to 32
-    # columns while its grid is at most two waves, then the K-split kind while
-    # its grid is one wave
+    # K > 4096 over few rows: kind 9 up to 32 columns, its largest tile (32 or
+    # 16 rows x 16 or 8 columns) whose grid fills 160 workgroups, at most two
+    # waves of them; then the K-split kind while its grid is one wave
     assert name(4096, 56, 8) == "axh_q4k_matmul_lk_c8_x2_w2"
     assert name(4096, 17, 16) == "axh_q4k_matmul_lk_c16_x1_w3"
     with pytest.raises(axc.DispatchError):  # kind 7 keeps K <= 4096 of X in registers
         name(4096, 17, 16, axc.MatmulVariant(7, 8, 1, 1))
-    assert name(4096, 56, 32) == "axh_q4k_matmul_lk_c16_x1_w3"  # 256 x 2 workgroups
-    assert name(8192, 56, 8) == "axh_q4k_matmul_lk_c8_x1_w3"  # two waves: X one chunk ahead
+    assert name(4096, 56, 32) == "axh_q4k_matmul_lk_c16_x1_w3_r2"  # 128 x 2 workgroups
+    assert name(1024, 56, 32) == "axh_q4k_matmul_lk_c8_x2_w2"  # 64 x 4
+    assert name(8192, 56, 8) == "axh_q4k_matmul_lk_c8_x2_w2_r2"  # 256 x 1
+    assert name(14336, 56, 8) == "axh_q4k_matmul_kx_r4_n1_k4_p3"  # 448 x 1: K-split tiles
+    assert name(8192, 56, 32) == "axh_q4k_matmul_kx_r4_n1_k4_p3"  # 256 x 2
     assert name(1024, 56, 64) == "axh_q4k_matmul_ks_k8_n1_p1_r1"  # 16-row tiles: 64 x 4
     assert name(1024, 56, 128) == "axh_q4k_matmul_ks_k8_n1_p1"  # 32-row tiles: 32 x 8
-    assert name(8192, 56, 32) == "axh_q4k_matmul_kx_r4_n1_k4_p3"  # 512 x 2: K-split tiles
-    assert name(14336, 56, 8) == "axh_q4k_matmul_kx_r4_n1_k4_p3"
     assert name(14336, 56, 32) == "axh_q4k_matmul_kx_r4_n2_k4_p3"  # prefetch 3 at K > 4096
     assert name(4096, 56, 8, axc.MatmulVariant(3, 8, 1, 2, 1)) == "axh_q4k_matmul_ks_k8_n1_p2_r1"
     with pytest.raises(axc.DispatchError):  # kind 9 keeps the chunk offsets below 1 MiB
@@ -262,6 +263,7 @@ def test_matmul_kernel_selection(axc):
     assert name(14336, 16, 128, axc.MatmulVariant(5, 4, 8, 2, 4)) == \
         "axh_q4k_matmul_kx_r4_n8_k4_p2"
     assert all((v.row_tiles > 0) == (v.kind in (3, 5, 8, 9)) for v in vs)
+    assert name(4096, 56, 32, axc.MatmulVariant(9, 8, 2, 1, 2)) == "axh_q4k_matmul_lk_c16_x1_w3_r2"
     with pytest.raises(axc.DispatchError):  # row tiles are kinds 3, 5, 8 and 9 only
         name(14336, 16, 8, axc.MatmulVariant(7, 8, 1, 1, 1))
     co = axc.builtin_code_object()

@@ -128,10 +128,12 @@ def test_edge_shapes(ctx, rows, sb, batch):
                                                   (1000, 16, 60, "sr_w8_s2"),
                                                   (1024, 56, 128, "ks_k8_n1_p1"),
                                                   (1000, 56, 60, "ks_k8_n1_p1_r1"),
-                                                  (4000, 56, 30, "lk_c16_x1_w3"),
+                                                  (4000, 56, 30, "lk_c16_x1_w3_r2"),
+                                                  (4000, 56, 16, "lk_c16_x1_w3"),
                                                   (4000, 56, 7, "lk_c8_x2_w2"),
-                                                  (8100, 43, 5, "lk_c8_x1_w3"),
-                                                  (1000, 43, 31, "lk_c16_x1_w3"),
+                                                  (8100, 43, 5, "lk_c8_x2_w2_r2"),
+                                                  (11000, 43, 5, "kx_r4_n1_k4_p3"),
+                                                  (1000, 43, 31, "lk_c8_x2_w2"),
                                                   (4096, 56, 100, "kx_r4_n2_k4_p3")])
 def test_grid_fill_defaults(ctx, axc, rows, sb, batch, kernel):
     """The defaults that follow from the grid on few rows: streaming rows past
