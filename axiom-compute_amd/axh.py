@@ -314,7 +314,7 @@ class MatmulVariant:
     K-split, 5 K-split tile, 7 streaming rows (K <= 4096), 8 32x32 tiles, 9
     long rows (kinds 1, 2, 4 and 6 were removed); row_tiles is kinds 3, 5, 8
     and 9's only (kind 9: 16-row tiles per workgroup; its col_tiles counts
-    8-column groups).  The default kind follows the grid each kind
+    4-column groups).  The default kind follows the grid each kind
     would launch on 256 CUs (q4k_matmul_kernel_name names the choice)."""
 
     kind: int = 0

@@ -487,7 +487,7 @@ __device__ __forceinline__ void q4k_matmul_lk(const uint8_t *__restrict__ q,
                                               const uint16_t *__restrict__ x,
                                               float *__restrict__ y, const MatmulArgs a,
                                               f32x4_t *lds) {
-  static_assert(XC == 8 || XC == 16, "8 or 16 columns per workgroup");
+  static_assert(XC == 4 || XC == 8 || XC == 16, "4, 8 or 16 columns per workgroup");
   static_assert(RT == 1 || RT == 2, "16 or 32 rows per workgroup");
   constexpr int NW = 8, XR = XD + 1, WR = WD + 1; // ring slots of X (LDS) and weights (VGPRs)
   static_assert(XD >= 1 && WD >= XD && WR % XR == 0 && WR <= 8,
@@ -585,7 +585,7 @@ __device__ __forceinline__ void q4k_matmul_lk(const uint8_t *__restrict__ q,
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       const half8_t v = __builtin_bit_cast(half8_t, buf[xa[t]]);
-      xf[t] = (XC == 16 || r < 8u) ? v : (half8_t){};
+      xf[t] = r < (uint32_t)XC ? v : (half8_t){};
     }
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
@@ -664,7 +664,7 @@ __device__ __forceinline__ void q4k_matmul_lk(const uint8_t *__restrict__ q,
 #pragma unroll
     for (uint32_t w2 = 1; w2 < (uint32_t)NW; ++w2) sum += red[(w2 * RT + wave) * 64u + lane];
     const uint32_t col = n0 + r;
-    if ((XC == 16 || r < 8u) && col < batch)
+    if (r < (uint32_t)XC && col < batch)
       store_col4(y + (size_t)col * n_rows, m0 + 16u * wave + 4u * g, n_rows, sum);
   }
 }
@@ -1210,4 +1210,5 @@ AXH_Q4K_MATMUL_LK(8, 2, 2, 1, )
 AXH_Q4K_MATMUL_LK(8, 1, 3, 1, )
 AXH_Q4K_MATMUL_LK(16, 1, 3, 1, )
 AXH_Q4K_MATMUL_LK(8, 2, 2, 2, _r2)
+AXH_Q4K_MATMUL_LK(4, 2, 2, 1, )
 AXH_Q4K_MATMUL_LK(16, 1, 3, 2, _r2)

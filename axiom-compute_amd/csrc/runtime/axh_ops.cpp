@@ -49,8 +49,8 @@ struct MatmulArgs {
 //                       CU over 16-row blocks, K <= 4096 (pf 2: 8-column groups).
 //   kind 8 (32x32 tiles) axh_q4k_matmul_rm_w{W}_r{RT}_p4: W waves of RT 32-row MFMA tiles
 //                       over 128 columns, a 4-deep LDS ring.
-//   kind 9 (long rows)  axh_q4k_matmul_lk_c{8*NT}_x{PF}_w{WD}[_r2]: 8 waves over RT 16-row
-//                       tiles and 8 * NT columns (col_tiles counts 8-column groups), K in
+//   kind 9 (long rows)  axh_q4k_matmul_lk_c{4*NT}_x{PF}_w{WD}[_r2]: 8 waves over RT 16-row
+//                       tiles and 4 * NT columns (col_tiles counts 4-column groups), K in
 //                       chunks of 8 superblocks, X through an LDS ring PF chunks ahead, the
 //                       weights in registers WD chunks ahead (3 for PF 1, else PF).
 struct MatmulVariant {
@@ -61,8 +61,8 @@ constexpr MatmulVariant kQ4kMatmulVariants[] = {
     {3, 8, 1, 2, 1}, {5, 4, 8, 2, 4},
     {5, 4, 8, 2, 2}, {5, 4, 4, 2, 4}, {5, 4, 4, 3, 4}, {5, 4, 4, 2, 8}, {5, 4, 2, 2, 4},
     {5, 4, 2, 3, 4}, {5, 4, 1, 3, 4}, {7, 8, 1, 1, 0}, {7, 8, 2, 1, 0}, {7, 8, 1, 2, 0},
-    {8, 8, 8, 4, 1}, {8, 4, 8, 4, 2}, {8, 4, 8, 4, 1}, {8, 2, 8, 4, 2}, {9, 8, 1, 2, 1},
-    {9, 8, 1, 1, 1}, {9, 8, 2, 1, 1}, {9, 8, 1, 2, 2}, {9, 8, 2, 1, 2}};
+    {8, 8, 8, 4, 1}, {8, 4, 8, 4, 2}, {8, 4, 8, 4, 1}, {8, 2, 8, 4, 2}, {9, 8, 2, 2, 1},
+    {9, 8, 2, 1, 1}, {9, 8, 4, 1, 1}, {9, 8, 2, 2, 2}, {9, 8, 4, 1, 2}, {9, 8, 1, 2, 1}};
 // The matmul kernels read zeros through offsets at or past 0xFFF00000 (with
 // the step offsets on top), and address rows up to 16 past the matrix: q and
 // x must stay below that, with 16 rows to spare.
@@ -1022,13 +1022,13 @@ static uint32_t rm_lds_bytes(const MatmulVariant &v) {
   return 4u * (16u + v.w * ((96u * v.rt + 63u) / 64u)) * 1024u;
 }
 
-// Kind 9 LDS: a ring of pf + 1 buffers of the X chunk (8 * nt columns x 4
+// Kind 9 LDS: a ring of pf + 1 buffers of the X chunk (4 * nt columns x 4
 // KiB), then the waves' partial tiles (1 KiB each, rt per wave).  Its loads take the
 // chunk as an SGPR offset of 512 bytes per superblock (X), up to 3 chunks
 // past the row, over the zero-reading offset 0xFFF00000, which leaves 1 MiB:
 // rows of fewer than 1024 superblocks keep it below 2^32.
 static uint32_t lk_lds_bytes(const MatmulVariant &v) {
-  return (v.pf + 1u) * 8u * v.nt * 4096u + 8u * v.rt * 1024u;
+  return (v.pf + 1u) * 4u * v.nt * 4096u + 8u * v.rt * 1024u;
 }
 constexpr uint32_t kLkMaxSb = 1024;
 
@@ -1079,13 +1079,17 @@ static MatmulVariant q4k_matmul_default(uint32_t n_rows, uint32_t batch, uint32_
   // workgroup per CU): with more, the K-split tile kind is ahead (8192 x
   // 14336 x 32 42.4 against 45.0; 14336 x 14336 x 8 40.1 against 41.5).
   if (nsb > kSrMaxSb && batch <= 32) {
+    // up to 4 columns: 4-column tiles (X loads halved; 56 KiB of LDS, so two
+    // workgroups per CU): 4096 x 14336 x 4 10.8 us against 11.7 with 8
+    // columns, 8192 x 14336 x 4 (512 workgroups) 20.0 against 21.9
+    if (batch <= 4 && groups(16, 4) <= 2 * kMatmulCus) return {9, 8, 1, 2, 1};
     constexpr uint32_t cand[4][2] = {{16, 2}, {16, 1}, {8, 2}, {8, 1}}; // columns, row tiles
     for (int i = 0; i < 4; ++i) {
       const uint32_t xc = cand[i][0], rt = cand[i][1];
       if (batch <= 8 && xc == 16) continue;
       const uint64_t g = groups(16 * rt, xc);
       if (g < kMatmulFill && i < 3) continue;
-      if (g <= kMatmulCus) return xc == 16 ? MatmulVariant{9, 8, 2, 1, rt} : MatmulVariant{9, 8, 1, 2, rt};
+      if (g <= kMatmulCus) return xc == 16 ? MatmulVariant{9, 8, 4, 1, rt} : MatmulVariant{9, 8, 2, 2, rt};
       break;
     }
   }
@@ -1164,7 +1168,7 @@ static axh_status plan_q4k_matmul(uint32_t n_rows, uint32_t sb_per_row, uint32_t
         if (sb_per_row >= kLkMaxSb)
           return fail(AXH_ERR_INVALID_ARGUMENT,
                       "matmul kind 9 takes rows of fewer than 1024 superblocks");
-        std::snprintf(name, cap, "axh_q4k_matmul_lk_c%u_x%u_w%u%s", 8u * v.nt, v.pf,
+        std::snprintf(name, cap, "axh_q4k_matmul_lk_c%u_x%u_w%u%s", 4u * v.nt, v.pf,
                       v.pf == 1u ? 3u : v.pf, v.rt == 2u ? "_r2" : "");
       }
       else {
@@ -1235,7 +1239,7 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
                       : v.kind == 7 ? 16u
                       : v.kind == 9 ? 16u * v.rt
                                     : 32u * v.rt * v.w;
-  const uint32_t tn = (v.kind == 7 && v.pf == 2) || v.kind == 9 ? 8u * v.nt : 16u * v.nt;
+  const uint32_t tn = v.kind == 9 ? 4u * v.nt : (v.kind == 7 && v.pf == 2 ? 8u : 16u) * v.nt;
   uint64_t gx = (n_rows + tm - 1) / tm;
   const uint64_t gy = (batch + tn - 1) / tn;
   if (gx > ctx->core->max_wg[0] || gy > ctx->core->max_wg[1])

@@ -393,7 +393,7 @@ typedef struct axh_q4_matmul_variant {
     uint32_t waves_per_workgroup; /* 3, 5, 7, 9: waves splitting K; 8: waves of row_tiles
                                      row tiles each */
     uint32_t col_tiles;           /* 16-column MFMA tiles per workgroup (kind 8: 8;
-                                     kind 9: 8-column groups, 1 or 2) */
+                                     kind 9: 4-column groups, 1, 2 or 4) */
     uint32_t prefetch;            /* K steps in flight (kinds 3, 7; kind 7 prefetch 2:
                                      8-column groups), LDS ring depth (5, 8: 4), X
                                      chunks in flight (9) */

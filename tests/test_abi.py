@@ -230,6 +230,8 @@ def test_matmul_kernel_selection(axc):
         name(4096, 17, 16, axc.MatmulVariant(7, 8, 1, 1))
     assert name(4096, 56, 32) == "axh_q4k_matmul_lk_c16_x1_w3_r2"  # 128 x 2 workgroups
     assert name(1024, 56, 32) == "axh_q4k_matmul_lk_c8_x2_w2"  # 64 x 4
+    assert name(4096, 56, 4) == "axh_q4k_matmul_lk_c4_x2_w2"  # up to 4 columns
+    assert name(8192, 56, 3) == "axh_q4k_matmul_lk_c4_x2_w2"  # 512: two per CU
     assert name(8192, 56, 8) == "axh_q4k_matmul_lk_c8_x2_w2_r2"  # 256 x 1
     assert name(14336, 56, 8) == "axh_q4k_matmul_kx_r4_n1_k4_p3"  # 448 x 1: K-split tiles
     assert name(8192, 56, 32) == "axh_q4k_matmul_kx_r4_n1_k4_p3"  # 256 x 2
@@ -263,7 +265,7 @@ def test_matmul_kernel_selection(axc):
     assert name(14336, 16, 128, axc.MatmulVariant(5, 4, 8, 2, 4)) == \
         "axh_q4k_matmul_kx_r4_n8_k4_p2"
     assert all((v.row_tiles > 0) == (v.kind in (3, 5, 8, 9)) for v in vs)
-    assert name(4096, 56, 32, axc.MatmulVariant(9, 8, 2, 1, 2)) == "axh_q4k_matmul_lk_c16_x1_w3_r2"
+    assert name(4096, 56, 32, axc.MatmulVariant(9, 8, 4, 1, 2)) == "axh_q4k_matmul_lk_c16_x1_w3_r2"
     with pytest.raises(axc.DispatchError):  # row tiles are kinds 3, 5, 8 and 9 only
         name(14336, 16, 8, axc.MatmulVariant(7, 8, 1, 1, 1))
     co = axc.builtin_code_object()

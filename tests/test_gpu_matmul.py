@@ -131,6 +131,7 @@ def test_edge_shapes(ctx, rows, sb, batch):
                                                   (4000, 56, 30, "lk_c16_x1_w3_r2"),
                                                   (4000, 56, 16, "lk_c16_x1_w3"),
                                                   (4000, 56, 7, "lk_c8_x2_w2"),
+                                                  (4000, 43, 3, "lk_c4_x2_w2"),
                                                   (8100, 43, 5, "lk_c8_x2_w2_r2"),
                                                   (11000, 43, 5, "kx_r4_n1_k4_p3"),
                                                   (1000, 43, 31, "lk_c8_x2_w2"),
@@ -173,13 +174,13 @@ def test_tile_kinds_on_odd_shapes(ctx, axc, rows, sb, batch):
 
 
 @pytest.mark.parametrize("rows,sb,batch", [(4096, 56, 8), (1000, 43, 5), (37, 9, 16), (130, 1, 1),
-                                           (300, 17, 20), (64, 64, 3), (20, 8, 9)])
+                                           (300, 17, 20), (64, 64, 3), (20, 8, 9), (100, 20, 2)])
 def test_long_rows_kind(ctx, axc, rows, sb, batch):
     """Kind 9 (8 waves over one 16-row block, K in chunks of 8 superblocks,
     X through an LDS ring) in every compiled form: whole and partial chunks
     (56, 43, 9, 1, 17 superblocks; 64 and 8 fill the ring rounds exactly),
-    more chunks than the ring holds, rows past the last block, 8- and
-    16-column groups with partial ones (5, 9, 16, 20 columns)."""
+    more chunks than the ring holds, rows past the last block, 4-, 8- and
+    16-column groups with partial ones (2, 3, 5, 9, 16, 20 columns)."""
     q, xh = _inputs(rows * 5 + sb * 7 + batch, rows, sb, batch)
     for v in axc.compiled_matmul_variants():
         if v.kind != 9:
