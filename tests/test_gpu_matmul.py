@@ -264,6 +264,42 @@ def test_batch_one_matches_the_matvec_within_f16_weight_rounding(ctx):
     assert np.all(np.abs(y.astype(np.float64) - ymv) <= (2.0 ** -11 + 2e-5) * absd)
 
 
+@pytest.mark.parametrize("batch", [4, 8, 16, 32])
+def test_long_rows_columns_are_independent_at_full_size(ctx, axc, batch):
+    """The batched down-projection (4096 x 14336, the north star's weights) at
+    its defaults: every column of a batched call equals, bit for bit, the same
+    column run alone in the first column slot of the same kernel (the column
+    tiles sum the same products in the same order whichever slot a column
+    takes), and the whole result meets the f16-weight product check."""
+    rows, sb = 4096, 56
+    name = axc.q4k_matmul_kernel_name(rows, sb, batch)
+    assert name.startswith("axh_q4k_matmul_lk_")
+    _say(f"matmul long rows columns {rows}x{sb * 256} B={batch} {name}")
+    q, xh = _inputs(700 + batch, rows, sb, batch)
+    dq = _dev(ctx, q)
+    dx, dy = _dev(ctx, xh), ctx.alloc(batch * rows * 4)
+    def named(u):
+        try:
+            return axc.q4k_matmul_kernel_name(rows, sb, batch, u)
+        except axc.DispatchError:  # kinds that do not take this shape
+            return None
+    v = next(u for u in axc.compiled_matmul_variants() if named(u) == name)
+    ctx.q4k_matmul(dq, dx, dy, rows, sb, batch, v)
+    ctx.synchronize()
+    y = np.frombuffer(ctx.download(dy, batch * rows * 4), dtype=np.float32).reshape(batch, rows)
+    x2 = xh.reshape(batch, sb * 256)
+    d1, o1 = ctx.alloc(sb * 256 * 2), ctx.alloc(rows * 4)
+    for b in range(batch):
+        ctx.upload(d1, np.ascontiguousarray(x2[b]))
+        ctx.q4k_matmul(dq, d1, o1, rows, sb, 1, v)
+        ctx.synchronize()
+        y1 = np.frombuffer(ctx.download(o1, rows * 4), dtype=np.float32)
+        assert np.array_equal(y1.view(np.uint32), y[b].view(np.uint32)), f"column {b}"
+    for buf in (dq, dx, dy, d1, o1):
+        buf.close()
+    _check(y.copy(), q, xh, rows, sb, batch, f"long rows full size B={batch}", oracle_f32=False)
+
+
 def test_invalid_arguments_are_typed_errors(ctx, axc):
     b = ctx.alloc(64)
     with pytest.raises(axc.DispatchError):
