@@ -685,9 +685,11 @@ __device__ __forceinline__ void q4k_matmul_lk(const uint8_t *__restrict__ q,
 // chunk: their low nibbles are the A fragments of k-steps 0-1 (k = 16h +
 // 0..15), their high nibbles those of k-steps 2-3 (k = 32 + 16h + ..), each 8
 // consecutive k, so the X fragment of the same (k-step, half) is one 16-byte
-// piece.  X piece p of column n sits in slot p ^ (n & 7) of the column's 128
-// bytes, so 8 lanes reading one piece of 8 consecutive columns hit distinct
-// banks.  One barrier per step makes every wave's X of step j + 1 visible and
+// piece.  X piece p of column n sits in slot p ^ ((n >> 1) & 7) of the
+// column's 128 bytes: columns n and n + 1 lie in the two 128-byte halves of
+// the 64 banks, so 16 lanes reading one piece of 16 consecutive columns hit
+// 16 distinct 16-byte bank groups (with p ^ (n & 7), columns n and n + 8
+// collided).  One barrier per step makes every wave's X of step j + 1 visible and
 // frees the buffer the next loads refill.
 // The step loop is unrolled by the ring depth, so a step's ring slot and
 // chunk are compile-time constants: the LDS addresses of the fragment reads
@@ -730,13 +732,13 @@ __device__ __forceinline__ void q4k_matmul_rm(const uint8_t *__restrict__ q,
   const uint32_t m0 = blockIdx.x * (32u * RT * W) + 32u * RT * wave, n0 = blockIdx.y * 128u;
 
   // X load role: instruction i = wave + W * u covers columns 8i .. 8i + 7;
-  // lane L loads piece (L & 7) ^ (col & 7) of column 8i + L / 8.  Step j
+  // lane L loads piece (L & 7) ^ ((col >> 1) & 7) of column 8i + L / 8.  Step j
   // adds 128 j bytes (SGPR offset).
   uint32_t xv0[kXPer];
 #pragma unroll
   for (int u = 0; u < kXPer; ++u) {
     const uint32_t i = wave + (uint32_t)(W * u), col = 8u * i + (lane >> 3);
-    const uint32_t p = (lane & 7u) ^ (col & 7u), b = n0 + col;
+    const uint32_t p = (lane & 7u) ^ ((col >> 1) & 7u), b = n0 + col;
     xv0[u] = b < batch ? (b * K + 8u * p) * 2u : kFar;
   }
   // Weight load role: piece P = 64m + lane -> row P / 3 of the wave's 32 RT,
@@ -799,7 +801,7 @@ __device__ __forceinline__ void q4k_matmul_rm(const uint8_t *__restrict__ q,
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     const uint32_t p = ((uint32_t)s & 1u) + 2u * h + 4u * ((uint32_t)s >> 1);
-    xl[s] = 8u * r + (p ^ (r & 7u));
+    xl[s] = 8u * r + (p ^ ((r >> 1) & 7u));
   }
   f32x16_t acc[RT][4];
 #pragma unroll
