@@ -283,11 +283,13 @@ __device__ __forceinline__ void q4k_matmul_ks(const uint8_t *__restrict__ q,
 // direct-to-LDS buffer loads (16 bytes per lane, no VGPRs), laid out so that
 // the global reads are coalesced: a fragment's 16 lanes read 16 different
 // rows (weights) or columns (X), which as direct loads would touch 4 cache
-// lines per 4 lanes.  X instruction (kk, t) covers columns 16t..16t+15 and
-// k = 32kk..32kk+31 of the chunk: lane 4c' + j loads 16 bytes (8 k) of column
-// c' (64 contiguous bytes per lane quad), with the piece rotated by c'/4 so
-// that the fragment reads (lane (n, g): column n, piece g) hit distinct
-// banks.  Weight piece 3r + {0, 1, 2} is row r's header or its two 16-byte
+// lines per 4 lanes.  X instruction u covers columns 8u..8u+7 and the whole
+// 64-k chunk, one 128-byte line per column: lane 8b + s loads 16-byte piece
+// s ^ f of column 8u + b, f = (b >> 1) | ((u & 1) << 2), so that the fragment
+// reads (16 lanes: columns 16t..16t+15, one piece) hit 16 distinct 16-byte
+// bank groups.  (Two instructions per line, 64 bytes of 16 columns each,
+// measured 3 % slower, A/B in one run at 14336 x 4096: B = 128 28.97 vs
+// 28.09 us, B = 64 20.86 vs 20.45, B = 32 16.17 vs 15.78.)  Weight piece 3r + {0, 1, 2} is row r's header or its two 16-byte
 // halves of the chunk's 32 qs bytes.  A wave waits only for its own loads
 // (the load counter), so there is no barrier until the end, when all KS
 // partial tiles go to LDS and wave w sums tiles w, w + KS, ... in wave order
@@ -302,7 +304,11 @@ struct KxLayout {
   static constexpr int kPerStep = kX + kW;           // 16-byte-per-lane loads (1 KiB each)
 };
 
-__device__ __forceinline__ uint32_t kx_xrot(uint32_t col) { return (col >> 2) & 3u; }
+// The slot of X piece p (0..7, 8 k each) of tile column n in a ring buffer.
+__device__ __forceinline__ uint32_t kx_xslot(uint32_t n, uint32_t p) {
+  const uint32_t b = n & 7u, f = (b >> 1) | (((n >> 3) & 1u) << 2);
+  return 64u * (n >> 3) + 8u * b + (p ^ f);
+}
 
 template <int RT, int NT, int KS, int PF>
 __device__ __forceinline__ void q4k_matmul_kx(const uint8_t *__restrict__ q,
@@ -333,8 +339,8 @@ __device__ __forceinline__ void q4k_matmul_kx(const uint8_t *__restrict__ q,
   const uint32_t n_my = sb0 < nsb ? (nsb - sb0 + kSbStride - 1u) / kSbStride : 0u;
   const uint32_t rot = n_my ? ((blockIdx.x >> 3) + blockIdx.y) % n_my : 0u;
 
-  // Load roles (fixed per lane).  X: column n0 + 16t + (lane >> 2), piece
-  // (lane - rot(col)) & 3 of the 32-k half kk.  Weights: piece P = 64m + lane
+  // Load roles (fixed per lane).  X instruction u: lane l takes the piece
+  // whose slot is 64u + l (kx_xslot).  Weights: piece P = 64m + lane
   // -> row P / 3, part P % 3 (0 header, 1-2 qs halves of the chunk).  The
   // step's superblock enters as an SGPR offset (X: 512 bytes, weights: 144
   // per superblock) over these per-lane offsets; lanes past the matrix or the
@@ -342,12 +348,12 @@ __device__ __forceinline__ void q4k_matmul_kx(const uint8_t *__restrict__ q,
   // (A/B in one run, 14336 x 4096: B = 128 28.8-29.4 vs 30.5-31.2 us, B = 64
   // 22.2 vs 23.6, against per-lane offsets recomputed every step.)
   constexpr uint32_t kFar = 0xFFF00000u;
-  const uint32_t xc = lane >> 2, xp = ((lane & 3u) - kx_xrot(lane >> 2)) & 3u;
-  uint32_t xoff0[NT];
+  uint32_t xoff0[2 * NT];
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const uint32_t b = n0 + 16u * (uint32_t)t + xc;
-    xoff0[t] = b < batch ? (b * K + 64u * c + 8u * xp) * 2u : kFar;
+  for (int u = 0; u < 2 * NT; ++u) {
+    const uint32_t b = n0 + 8u * (uint32_t)u + (lane >> 3);
+    const uint32_t p = (lane & 7u) ^ ((lane >> 4) | (((uint32_t)u & 1u) << 2));
+    xoff0[u] = b < batch ? (b * K + 64u * c + 8u * p) * 2u : kFar;
   }
   uint32_t woff0[L::kW];
 #pragma unroll
@@ -367,11 +373,9 @@ __device__ __forceinline__ void q4k_matmul_kx(const uint8_t *__restrict__ q,
     it = it + 1u == n_my ? 0u : it + 1u;
     f32x4_t *buf = ring + (j % (uint32_t)PF) * kBufSlots;
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void_t *)(buf + (kk * NT + t) * 64), 16,
-                                                 xoff0[t], sb * 512u + 64u * (uint32_t)kk, 0, 0);
+    for (int u = 0; u < 2 * NT; ++u)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void_t *)(buf + u * 64), 16, xoff0[u],
+                                               sb * 512u, 0, 0);
 #pragma unroll
     for (int m = 0; m < L::kW; ++m)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(qr, (lds_void_t *)(buf + (L::kX + m) * 64), 16,
@@ -388,7 +392,7 @@ __device__ __forceinline__ void q4k_matmul_kx(const uint8_t *__restrict__ q,
   for (int p = 0; p < PF; ++p) issue((uint32_t)p);
 
   // Fragment read slots (fixed per lane).
-  const uint32_t xslot = 4u * fr + ((g + kx_xrot(fr)) & 3u);
+  const uint32_t xs0 = kx_xslot(fr, g), xs1 = kx_xslot(fr, 4u + g);
   for (uint32_t j = 0; j < n_my; ++j) {
     // this step's loads are done when at most (PF - 1) steps' loads remain
     if constexpr (PF == 2)
@@ -410,9 +414,10 @@ __device__ __forceinline__ void q4k_matmul_kx(const uint8_t *__restrict__ q,
                                                8u * (g & 1u));
     }
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int t = 0; t < NT; ++t) xf[kk][t] = __builtin_bit_cast(half8_t, buf[(kk * NT + t) * 64 + xslot]);
+    for (int t = 0; t < NT; ++t) {
+      xf[0][t] = __builtin_bit_cast(half8_t, buf[128 * t + xs0]);
+      xf[1][t] = __builtin_bit_cast(half8_t, buf[128 * t + xs1]);
+    }
     // the buffer is refilled only after every read of it has returned
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     issue(j + (uint32_t)PF);
