@@ -925,9 +925,14 @@ __device__ __forceinline__ void q4k_matmul_rm(const uint8_t *__restrict__ q,
 // and dequantises them into the A fragments of 8 MFMA steps: step t < 4 takes
 // the low nibbles of qs bytes [32g + 8t, 32g + 8t + 8) (weights 64g + 8t ..
 // of the superblock, sub-block 2g), step t + 4 their high nibbles (64g + 32 +
-// 8t .., sub-block 2g + 1); the X fragment of step t holds the same k.  The
-// NW partial 16x16 tiles of a block are summed in LDS in wave order
-// (deterministic) by wave k % NW, which stores them.  Against the K-split
+// 8t .., sub-block 2g + 1); the X fragment of step t holds the same k.  Each
+// wave writes its partial 16x16 tiles of every block into its own X staging
+// region, free once its fragments are in VGPRs, and after one barrier at the
+// end (or when the regions fill: 16 blocks, 8 with two column groups or
+// 8-column groups) the waves sum the blocks' tiles in wave order
+// (deterministic) and store them.  A barrier and a sum after every block cost
+// 6-10 %, A/B in one run at 14336 x 4096: B = 8 11.01 vs 10.35 us, B = 16
+// 12.00 vs 11.21, B = 32 14.68 vs 13.23.  Against the K-split
 // tile kind at 14336 x 4096: 11.2 vs 14.2 us at 8 columns, 11.8 vs 14.6 at 16,
 // 15.0 vs 16.0 at 32 (NC = 2: every A fragment feeds two MFMAs).
 // XH (axh_q4k_matmul_sr_w*_s*_h): column groups of 8 (lanes of MFMA columns
@@ -968,6 +973,10 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
   const uint32_t hrow0 = 16u * n_full * G + 8u * blockIdx.x; // the half block's first row
   constexpr uint32_t kXc = XH ? 8u : 16u;    // columns of a group
   const uint32_t n0 = kXc * NC * blockIdx.y; // this workgroup's kXc * NC columns
+  // A wave's X staging region (f32x4 slots), free once its fragments are in
+  // VGPRs; it then holds the wave's partial tiles of up to kGroup blocks.
+  constexpr uint32_t kRegion = kXc * 512u * SPW / 16u;
+  constexpr uint32_t kGroup = kRegion / 64u / NC;
 
   // Weight loads of step (k, j): row 16 b + r, superblock wave*SPW + j: header
   // and the 32 qs bytes of chunk g.  k == n_myb is the half block (one step).
@@ -1033,9 +1042,37 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
         }
     }
   }
+  // Sums the partial tiles of blocks kb .. kb + nb - 1 (and of the half
+  // block after them) over the waves, in wave order, and stores them; slot tt
+  // of every region (block kb + tt / NC, column group tt % NC) is summed by
+  // wave tt % NW.  Lanes 0..31 of a half block's slot hold rows 0..7 against
+  // the first superblock's X, lanes 32..63 the same rows against the second.
+  auto flush = [&](uint32_t kb, uint32_t nb, bool with_half) {
+    const uint32_t n_t = (nb + (with_half ? 1u : 0u)) * NC;
+    for (uint32_t tt = wave; tt < n_t; tt += NW) {
+      const uint32_t sblk = tt / NC, c = tt - sblk * NC;
+      const f32x4_t *sl = red + tt * 64u;
+      const uint32_t col = n0 + kXc * c + r;
+      const bool ok = (!XH || r < 8u) && col < batch;
+      if (sblk < nb) {
+        f32x4_t sum = sl[lane];
+#pragma unroll
+        for (int w2 = 1; w2 < NW; ++w2) sum += sl[(uint32_t)w2 * kRegion + lane];
+        const uint32_t b = blockIdx.x + (kb + sblk) * G;
+        if (ok) store_col4(y + (size_t)col * n_rows, 16u * b + 4u * g, n_rows, sum);
+      } else if (lane < 32u) {
+        f32x4_t sum = sl[lane] + sl[lane + 32u];
+#pragma unroll
+        for (int w2 = 1; w2 < NW; ++w2)
+          sum += sl[(uint32_t)w2 * kRegion + lane] + sl[(uint32_t)w2 * kRegion + lane + 32u];
+        if (ok) store_col4(y + (size_t)col * n_rows, hrow0 + 4u * g, n_rows, sum);
+      }
+    }
+  };
   f32x4_t acc[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) acc[c] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+  uint32_t kb = 0; // first block whose partial tiles are not yet summed
   for (uint32_t k = 0; k < n_myb; ++k) {
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
@@ -1067,28 +1104,17 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
         }
       }
     }
-    // partial tiles of block k -> LDS (double buffer by block parity), after
-    // the 128 (XH: 64) KiB of X staging
-    f32x4_t *buf = red + (XH ? 4096u : 8192u) + (k & 1u) * (NW * NC * 64u);
+    // partial tiles of block k -> the wave's region, slot (k - kb) * NC + c
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      buf[(wave * NC + (uint32_t)c) * 64u + lane] = acc[c];
+      red[wave * kRegion + ((k - kb) * NC + (uint32_t)c) * 64u + lane] = acc[c];
       acc[c] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
     }
-    // LDS-only barrier: the partial tiles must be written, while the weight
-    // loads in flight and the previous block's y stores need not be waited for
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (wave == k % NW) {
-      const uint32_t b = blockIdx.x + k * gridDim.x;
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        f32x4_t sum = buf[(uint32_t)c * 64u + lane];
-#pragma unroll
-        for (int w2 = 1; w2 < NW; ++w2) sum += buf[((uint32_t)w2 * NC + (uint32_t)c) * 64u + lane];
-        const uint32_t col = n0 + kXc * (uint32_t)c + r;
-        if ((!XH || r < 8u) && col < batch)
-          store_col4(y + (size_t)col * n_rows, 16u * b + 4u * g, n_rows, sum);
-      }
+    if (k + 1u - kb == kGroup && (k + 1u < n_myb || half)) { // the regions are full
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      flush(kb, kGroup, false);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); // slots read before reuse
+      kb = k + 1u;
     }
   }
   if (half) { // its loads were issued into slot 0 with the last full block's
@@ -1121,24 +1147,12 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
     }
     // lanes 0..31 hold rows 0..7 of the first tile, lanes 32..63 rows 8..15
     // of the second: the same output rows, the row's two superblock parts
-    f32x4_t *buf = red + (XH ? 4096u : 8192u) + (k & 1u) * (NW * NC * 64u);
 #pragma unroll
-    for (int c = 0; c < NC; ++c) buf[(wave * NC + (uint32_t)c) * 64u + lane] = lane < 32u ? acc[c] : acc1[c];
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (wave == k % NW && lane < 32u) {
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        f32x4_t sum = buf[(uint32_t)c * 64u + lane] + buf[(uint32_t)c * 64u + lane + 32u];
-#pragma unroll
-        for (int w2 = 1; w2 < NW; ++w2)
-          sum += buf[((uint32_t)w2 * NC + (uint32_t)c) * 64u + lane] +
-                 buf[((uint32_t)w2 * NC + (uint32_t)c) * 64u + lane + 32u];
-        const uint32_t col = n0 + kXc * (uint32_t)c + r;
-        if ((!XH || r < 8u) && col < batch)
-          store_col4(y + (size_t)col * n_rows, hrow0 + 4u * g, n_rows, sum);
-      }
-    }
+    for (int c = 0; c < NC; ++c)
+      red[wave * kRegion + ((k - kb) * NC + (uint32_t)c) * 64u + lane] = lane < 32u ? acc[c] : acc1[c];
   }
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  flush(kb, n_myb - kb, half);
 }
 
 } // namespace

@@ -1225,10 +1225,10 @@ axh_status axh_q4k_matmul_f16(axh_context *ctx, const void *q, const uint16_t *x
   s = plan_q4k_matmul(n_rows, sb_per_row, batch, variant, &v, name, sizeof(name));
   if (s != AXH_OK) return s;
   // kind 5 sums the partial tiles of its waves in LDS (one 16x16 f32 tile =
-  // 1 KiB per wave); kind 7: 128 KiB of X staging, then two buffers of the
-  // waves' partial tiles
+  // 1 KiB per wave); kind 7: 128 KiB of X staging (64 KiB with 8-column
+  // groups), whose wave regions then hold the waves' partial tiles
   const uint32_t lds = v.kind == 5   ? kx_lds_bytes(v)
-                       : v.kind == 7 ? (v.pf == 2 ? 65536u : 131072u) + 2u * v.w * v.nt * 1024u
+                       : v.kind == 7 ? (v.pf == 2 ? 65536u : 131072u)
                        : v.kind == 8 ? rm_lds_bytes(v)
                        : v.kind == 9 ? lk_lds_bytes(v)
                                      : 0u;

@@ -194,7 +194,9 @@ def test_long_rows_kind(ctx, axc, rows, sb, batch):
 @pytest.mark.parametrize("rows,sb,batch", [(5000, 13, 13), (4097, 16, 16), (17, 7, 1),
                                            (1000, 16, 3), (70000, 2, 9), (4097, 16, 32),
                                            (333, 11, 19), (70000, 3, 25), (14336, 16, 8),
-                                           (4099, 5, 7), (7296, 16, 16), (14331, 16, 32)])
+                                           (4099, 5, 7), (7296, 16, 16), (14331, 16, 32),
+                                           (34368, 4, 5), (32768, 2, 8), (34368, 2, 30),
+                                           (66336, 2, 12), (65536, 2, 16)])
 def test_streaming_rows_kind(ctx, axc, rows, sb, batch):
     """Kind 7 (the default up to 32 columns and K <= 4096; 8-column groups up
     to 8 columns, two column groups per workgroup beyond 16 columns): more
@@ -204,7 +206,11 @@ def test_streaming_rows_kind(ctx, axc, rows, sb, batch):
     round's blocks become 8-row half blocks where they fill at most half of it
     (14336 rows: exactly half; 4097, 5000, 70000: fewer; 14331 and 5000: the
     last half block partly past the matrix) and stay whole where they fill
-    more (7296 rows: 200 of 256)."""
+    more (7296 rows: 200 of 256).  The waves' partial tiles are summed when
+    their LDS regions fill (16 blocks with one 16-column group, 8 with two or
+    with 8-column groups) and at the end: 70000 and 66336 rows sum a full
+    group and then the rest; 34368 rows fill a group exactly before the half
+    block; 32768 and 65536 rows end on a full group."""
     assert axc.q4k_matmul_kernel_name(rows, sb, batch).startswith("axh_q4k_matmul_sr_w8_s2")
     _say(f"matmul streaming rows {rows}x{sb * 256} B={batch}")
     q, xh = _inputs(rows + sb * 5 + batch, rows, sb, batch)
