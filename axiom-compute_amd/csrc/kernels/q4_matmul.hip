@@ -321,6 +321,7 @@ __device__ __forceinline__ void q4k_matmul_kx(const uint8_t *__restrict__ q,
   constexpr uint32_t kSbStride = KS / 4;
   constexpr int kTiles = RT * NT;
   constexpr uint32_t kBufSlots = 64u * L::kPerStep; // 16-byte slots per ring buffer
+  constexpr bool kTileOuter = NT == 4;
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t c = wave & 3u, sb0 = wave >> 2;
@@ -420,7 +421,6 @@ __device__ __forceinline__ void q4k_matmul_kx(const uint8_t *__restrict__ q,
     }
     // the buffer is refilled only after every read of it has returned
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    issue(j + (uint32_t)PF);
 
     half8_t af[RT][2];
 #pragma unroll
@@ -437,13 +437,49 @@ __device__ __forceinline__ void q4k_matmul_kx(const uint8_t *__restrict__ q,
       af[i][0] = __builtin_bit_cast(half8_t, make_uint4(l0, l1, l2, l3));
       af[i][1] = __builtin_bit_cast(half8_t, make_uint4(h0, h1, h2, h3));
     }
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+    // The refill loads go out among the MFMAs instead of as one burst, which
+    // filled the load unit's queue and held the wave.  With 4 column tiles
+    // the MFMAs run tile by tile, so that row tile i + 1's dequantisation
+    // sits among row tile i's MFMAs (a first tile's worth of VALU, then
+    // MFMA, 3 VALU, MFMA, 3 VALU, load, MFMA per load); otherwise the
+    // dequantisation comes first and every load sits between MFMAs.
+    if constexpr (kTileOuter) {
+      issue(j + (uint32_t)PF);
 #pragma unroll
       for (int i = 0; i < RT; ++i)
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
-          acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i][kk], xf[kk][t], acc[i][t], 0, 0, 0);
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+            acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i][kk], xf[kk][t], acc[i][t], 0, 0, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 40, 0);
+#pragma unroll
+      for (int k = 0; k < L::kPerStep; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+    } else {
+      __builtin_amdgcn_sched_barrier(0);
+      issue(j + (uint32_t)PF);
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int i = 0; i < RT; ++i)
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+            acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i][kk], xf[kk][t], acc[i][t], 0, 0, 0);
+      constexpr int kPer = (2 * RT * NT) / L::kPerStep > 0 ? (2 * RT * NT) / L::kPerStep : 1;
+#pragma unroll
+      for (int k = 0; k < L::kPerStep; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, kPer, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   // Ring loads past the wave's last step are still landing: drain them, and
