@@ -608,10 +608,14 @@ __device__ __forceinline__ void q4k_matmul_lk(const uint8_t *__restrict__ q,
   f32x4_t acc[RT];
 #pragma unroll
   for (int i = 0; i < RT; ++i) acc[i] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
-  // Chunk c (c % WR = e) issues X of chunk c + XD, then the weights of chunk
-  // c + WD.  The issue order is fixed, so the loads issued after X of chunk c
-  // are always the 3 weight loads of its group and the XD - 1 groups in
-  // between: waiting for that many leaves the weights ahead in flight.
+  // Chunk c (c % WR = e) issues X of chunk c + XD after its barrier, then
+  // the weights of chunk c + WD halfway through its MFMAs (issued with the X
+  // loads, the burst filled the load unit's queue and held the waves: A/B in
+  // one run at 4096 x 14336, B = 8 13.31 vs 12.39 us, B = 16 15.92 vs 15.32,
+  // B = 32 23.21 vs 22.17; at the end of the step, B = 32 took 23.05).  The
+  // issue order is fixed, so the loads issued after X of chunk c are always
+  // the 3 weight loads of its group and the XD - 1 groups in between: waiting
+  // for that many leaves the weights ahead in flight.
   auto step = [&](uint32_t c, auto e_c) {
     constexpr int e = decltype(e_c)::value;
     // own X of chunk c landed; after the barrier every wave's X of chunk c is
@@ -619,7 +623,6 @@ __device__ __forceinline__ void q4k_matmul_lk(const uint8_t *__restrict__ q,
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((XD - 1) * kPer + 3) : "memory");
     __builtin_amdgcn_sched_barrier(0);
     issue_x(c + (uint32_t)XD, std::integral_constant<int, (e + XD) % XR>{});
-    issue_w(c + (uint32_t)WD, std::integral_constant<int, (e + WD) % WR>{});
     __builtin_amdgcn_sched_barrier(0);
     const f32x4_t *buf = lds + (e % XR) * kSlot;
     half8_t xf[8];
@@ -648,6 +651,11 @@ __device__ __forceinline__ void q4k_matmul_lk(const uint8_t *__restrict__ q,
         const half8_t ahi = __builtin_bit_cast(half8_t, make_uint4(h0, h1, h2, h3));
         acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, xf[t], acc[i], 0, 0, 0);
         acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, xf[t + 4], acc[i], 0, 0, 0);
+        if (4 * i + t == 2 * RT - 1) { // halfway
+          __builtin_amdgcn_sched_barrier(0);
+          issue_w(c + (uint32_t)WD, std::integral_constant<int, (e + WD) % WR>{});
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     }
   };
