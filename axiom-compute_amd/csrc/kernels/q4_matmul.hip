@@ -289,8 +289,9 @@ __device__ __forceinline__ void q4k_matmul_ks(const uint8_t *__restrict__ q,
 // reads (16 lanes: columns 16t..16t+15, one piece) hit 16 distinct 16-byte
 // bank groups.  (Two instructions per line, 64 bytes of 16 columns each,
 // measured 3 % slower, A/B in one run at 14336 x 4096: B = 128 28.97 vs
-// 28.09 us, B = 64 20.86 vs 20.45, B = 32 16.17 vs 15.78.)  Weight piece 3r + {0, 1, 2} is row r's header or its two 16-byte
-// halves of the chunk's 32 qs bytes.  A wave waits only for its own loads
+// 28.09 us, B = 64 20.86 vs 20.45, B = 32 16.17 vs 15.78.)  Weight piece
+// 3r + {0, 1, 2} is row r's header or its two 16-byte halves of the chunk's
+// 32 qs bytes.  A wave waits only for its own loads
 // (the load counter), so there is no barrier until the end, when all KS
 // partial tiles go to LDS and wave w sums tiles w, w + KS, ... in wave order
 // (deterministic) and stores them.
