@@ -149,6 +149,7 @@ def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
     sigs = {
         "axh_last_error": (c.c_char_p, []),
         "axh_status_name": (c.c_char_p, [c.c_int]),
+        "axh_abi_version": (u32, []),
         "axh_context_create": (st, [c.POINTER(_Options), c.POINTER(vp)]),
         "axh_context_destroy": (None, [vp]),
         "axh_context_device_name": (c.c_char_p, [vp]),

@@ -615,13 +615,14 @@ __device__ __forceinline__ void q4k_matmul_lk(const uint8_t *__restrict__ q,
   // one run at 4096 x 14336, B = 8 13.31 vs 12.39 us, B = 16 15.92 vs 15.32,
   // B = 32 23.21 vs 22.17; at the end of the step, B = 32 took 23.05).  The
   // issue order is fixed, so the loads issued after X of chunk c are always
-  // the 3 weight loads of its group and the XD - 1 groups in between: waiting
-  // for that many leaves the weights ahead in flight.
+  // the 3 * RT weight loads of its group and the XD - 1 groups in between:
+  // waiting for that many leaves the weights ahead in flight.
   auto step = [&](uint32_t c, auto e_c) {
     constexpr int e = decltype(e_c)::value;
     // own X of chunk c landed; after the barrier every wave's X of chunk c is
     // in LDS and chunk c - 1's X buffer is free
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((XD - 1) * kPer + 3) : "memory");
+    static_assert((XD - 1) * kPer + 3 * RT <= 63, "vmcnt holds 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((XD - 1) * kPer + 3 * RT) : "memory");
     __builtin_amdgcn_sched_barrier(0);
     issue_x(c + (uint32_t)XD, std::integral_constant<int, (e + XD) % XR>{});
     __builtin_amdgcn_sched_barrier(0);

@@ -90,6 +90,11 @@ struct axh_context {
   axh_winner_table *winners = nullptr;
   std::atomic<bool> has_winners{false};
   std::string winners_path;
+  // The allocation-free matvec's kernel and this device's scratch address,
+  // both resolved once at context creation (null if that set-up failed), so
+  // its calls look nothing up and allocate nothing on the host either.
+  axh_kernel *noalloc_kernel = nullptr;
+  void *noalloc_scratch = nullptr;
 };
 
 namespace axh {

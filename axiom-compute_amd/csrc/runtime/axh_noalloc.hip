@@ -80,7 +80,9 @@ void noalloc_setup(axh_context *ctx) {
   void *p = nullptr;
   if (resolve_scratch(ctx->core->device, &p) != AXH_OK) return;
   axh_kernel *k = nullptr;
-  (void)builtin_kernel(ctx, kKernel, 4, sizeof(RowsArgs), 64u, &k);
+  if (builtin_kernel(ctx, kKernel, 4, sizeof(RowsArgs), 64u, &k) != AXH_OK || !k) return;
+  ctx->noalloc_kernel = k; // owned by ctx->ops until the context is destroyed
+  ctx->noalloc_scratch = p;
 }
 
 } // namespace axh
@@ -98,23 +100,22 @@ extern "C" axh_status axh_q4k_matvec_noalloc(axh_context *ctx, const void *q, co
   if (!q || !x || !y) return fail(AXH_ERR_INVALID_ARGUMENT, "q, x and y must be device pointers");
   if (((uintptr_t)q & 15u) || ((uintptr_t)x & 15u))
     return fail(AXH_ERR_INVALID_ARGUMENT, "q and x must be 16-byte aligned");
-  void *ws = nullptr;
-  axh_status s = resolve_scratch(ctx->core->device, &ws);
-  if (s != AXH_OK) return s;
-  axh_kernel *k = nullptr;
-  {
-    std::lock_guard<std::mutex> lk(ctx->ops_mu);
-    auto it = ctx->ops.find(kKernel);
-    if (it != ctx->ops.end()) k = it->second;
-  }
-  if (!k)
+  // Both resolved at context creation: no lookup, no host allocation here.
+  axh_kernel *const k = ctx->noalloc_kernel;
+  void *const ws = ctx->noalloc_scratch;
+  if (!k || !ws) {
+    void *p = nullptr;
+    const axh_status s = resolve_scratch(ctx->core->device, &p); // reports a scratch failure
+    if (s != AXH_OK) return s;
     return fail(AXH_ERR_PIPELINE_CREATION,
                 "the split-K kernel was not prepared at context creation (see the last error of "
                 "axh_context_create)");
+  }
   hipSetDevice(ctx->core->device);
   const uint32_t grid[3] = {(sb_per_row + kSpw - 1) / kSpw, 1, 1};
   RowsArgs a{n_rows, sb_per_row, kSpw, 0};
   void *bufs[4] = {const_cast<void *>(q), const_cast<float *>(x), y, ws};
-  s = axh::launch_raw(k, grid, bufs, 4, &a, sizeof(a), 0, axh::pick_stream(ctx, stream));
+  const axh_status s =
+      axh::launch_raw(k, grid, bufs, 4, &a, sizeof(a), 0, axh::pick_stream(ctx, stream));
   return s == AXH_OK ? axh::ok() : s;
 }

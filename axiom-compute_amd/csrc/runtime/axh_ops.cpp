@@ -1078,7 +1078,9 @@ static MatmulVariant q4k_matmul_default(uint32_t n_rows, uint32_t batch, uint32_
   // 8 22.5 with 32 x 8 against 30.5.  Only while the grid is one wave (one
   // workgroup per CU): with more, the K-split tile kind is ahead (8192 x
   // 14336 x 32 42.4 against 45.0; 14336 x 14336 x 8 40.1 against 41.5).
-  if (nsb > kSrMaxSb && batch <= 32) {
+  // Kind 9 keeps a row's superblock offsets below kLkMaxSb; longer rows fall
+  // through to the K-split kinds.
+  if (nsb > kSrMaxSb && nsb < kLkMaxSb && batch <= 32) {
     // up to 4 columns: 4-column tiles (X loads halved; 56 KiB of LDS, so two
     // workgroups per CU): 4096 x 14336 x 4 10.8 us against 11.7 with 8
     // columns, 8192 x 14336 x 4 (512 workgroups) 20.0 against 21.9
@@ -1444,11 +1446,6 @@ extern "C" axh_status axh_bench_loop(axh_context *ctx, const axh_bench_op *op, u
   if (groups > 100000) return fail(AXH_ERR_INVALID_ARGUMENT, "bench loop: too many groups");
   hipSetDevice(ctx->core->device);
   const hipStream_t st = ctx->core->stream;
-  uint32_t i = 0;
-  for (; i < warmup; ++i) {
-    const axh_status s = bench_call(ctx, op, i);
-    if (s != AXH_OK) return s;
-  }
   axh_status s = axh_device_synchronize(ctx);
   if (s != AXH_OK) return s;
   std::vector<hipEvent_t> ev(groups + 1u, nullptr);
@@ -1458,6 +1455,15 @@ extern "C" axh_status axh_bench_loop(axh_context *ctx, const axh_bench_op *op, u
         if (f) hipEventDestroy(f);
       return fail(AXH_ERR_QUEUE_SUBMIT, "hipEventCreate failed");
     }
+  // The warmup calls prime the queue: the first event follows them with no
+  // synchronisation in between, so the first timed call starts behind queued
+  // work, as every later one does, instead of on an idle device.
+  uint32_t i = 0;
+  for (; i < warmup && s == AXH_OK; ++i) s = bench_call(ctx, op, i);
+  if (s != AXH_OK) {
+    for (auto &e : ev) hipEventDestroy(e);
+    return s;
+  }
   hipEventRecord(ev[0], st);
   for (uint32_t g = 0; g < groups && s == AXH_OK; ++g) {
     for (uint32_t c = 0; c < calls_per_group && s == AXH_OK; ++c) s = bench_call(ctx, op, i++);

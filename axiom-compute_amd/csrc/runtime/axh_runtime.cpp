@@ -220,6 +220,8 @@ extern "C" {
 
 const char *axh_last_error(void) { return t_last_error.c_str(); }
 
+uint32_t axh_abi_version(void) { return AXH_ABI_VERSION; }
+
 const char *axh_status_name(int s) {
   switch (s) {
   case AXH_OK: return "Ok";

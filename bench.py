@@ -357,29 +357,33 @@ def main() -> int:
 
     # Timed region (the reported value): K back-to-back calls of the operation
     # launched by the library's own loop (axh_bench_loop) on the context
-    # stream through the public entry point, after W untimed calls, with HIP
-    # events on that stream before the first call and after each of 10 groups
-    # of K / 10 calls (K calls in groups of one when K is not a multiple of
-    # 10); device synchronisation on both sides.  The groups give p10/p50/p90.
-    # The same K calls launched from this Python loop through ctypes, and
-    # replayed from one captured HIP graph, are reported next to it.
-    groups, per_group = (10, args.steps // 10) if args.steps % 10 == 0 else (args.steps, 1)
+    # stream through the public entry point, between exactly two HIP events on
+    # that stream, with device synchronisation on both sides.  The W warmup
+    # calls are queued right before the first event (no synchronisation in
+    # between), so the first timed call starts behind queued work like the
+    # others.  The spread (p10/p50/p90) comes from REPEATS more runs of the
+    # same W + K loop, each between its own two events.  The same K calls
+    # launched from this Python loop through ctypes, and replayed from one
+    # captured HIP graph, are reported next to it.
+    REPEATS = 11
     # Pre-warm, untimed: the same calls for at least 100 ms, so the clocks have
     # ramped up under load (a few warmup calls are a fraction of a millisecond,
-    # and the first group of a cold start runs ~10 % slower).
+    # and the first loop of a cold start runs ~10 % slower).
     prewarm_ms, n = 0.0, 20
     while prewarm_ms < 100.0 and n <= (1 << 20):
         prewarm_ms += sum(ctx.bench_loop(**case.bench_op(), warmup=0, groups=1,
                                          calls_per_group=n))
         n *= 2
     ctx.device_synchronize()
-    group_ms = ctx.bench_loop(**case.bench_op(), warmup=args.warmup, groups=groups,
-                              calls_per_group=per_group)
+    total_ms = ctx.bench_loop(**case.bench_op(), warmup=args.warmup, groups=1,
+                              calls_per_group=args.steps)[0]
     ctx.device_synchronize()
-    total_ms = sum(group_ms)
     us_per_call = total_ms * 1000.0 / args.steps
     t = us_per_call * 1e-6
-    per_call = sorted(g * 1000.0 / per_group for g in group_ms)
+    per_call = sorted(ctx.bench_loop(**case.bench_op(), warmup=args.warmup, groups=1,
+                                     calls_per_group=args.steps)[0] * 1000.0 / args.steps
+                      for _ in range(REPEATS))
+    ctx.device_synchronize()
     pct = {p: round(per_call[min(len(per_call) - 1, int(p / 100 * len(per_call)))], 3)
            for p in (10, 50, 90)}
 
@@ -517,12 +521,13 @@ def main() -> int:
         "ms_per_step": round(total_ms / args.steps, 6),
         "us_per_call": round(us_per_call, 3),
         "timing": f"{args.steps} back-to-back calls launched by the library's loop "
-                  f"(axh_bench_loop, {groups} event-timed groups) after an untimed pre-warm of "
-                  f"{prewarm_ms:.0f} ms and {args.warmup} warmup calls; the same calls launched "
-                  f"from Python through ctypes: {us_python:.3f} us/call; replayed from one "
-                  f"HIP graph: {us_graph:.3f} us/call",
+                  f"(axh_bench_loop) between two HIP events, behind {args.warmup} queued warmup "
+                  f"calls, after an untimed pre-warm of {prewarm_ms:.0f} ms; the same calls "
+                  f"launched from Python through ctypes: {us_python:.3f} us/call; replayed from "
+                  f"one HIP graph: {us_graph:.3f} us/call",
         "us_per_call_p10_p50_p90": [pct[10], pct[50], pct[90]],
-        "distribution": f"{groups} event-timed groups of {per_group} back-to-back calls",
+        "distribution": f"{REPEATS} more runs of the same {args.warmup} warmup + {args.steps} "
+                        f"timed calls, each between its own two events",
         "kernel": kernel,
         "pct_of_peak": round(100.0 * value / peak, 2),
         "higher_is_better": True,

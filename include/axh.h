@@ -18,6 +18,15 @@
 extern "C" {
 #endif
 
+/* Layout version of the structs below, raised whenever one of them changes
+ * size or field order.  2: axh_q4_variant grew from 4 to 6 fields (16 to 24
+ * bytes: family, sb_per_lane appended).  A binding written against an older
+ * header compares axh_abi_version() with the AXH_ABI_VERSION it was written
+ * for and refuses to run on a mismatch.  No counterpart in the reference
+ * (its runtime is linked as one Rust crate graph). */
+#define AXH_ABI_VERSION 2u
+uint32_t axh_abi_version(void);
+
 /* One code per DispatchError variant (crates/axc-runtime/src/error.rs:27-195),
  * in the reference's order, with the HIP failure each one stands for. */
 typedef enum axh_status {
@@ -425,8 +434,11 @@ axh_status axh_q4k_matmul_variant_at(uint32_t i, axh_q4_matmul_variant *out);
  * by this library's own loop on the context stream through the public entry
  * points above (each call a full dispatch: validation, kernel choice, one
  * kernel launch), after `warmup` untimed calls.  Call i reads the weights at
- * q + (i % n_copies) * q_stride.  A HIP event is recorded before the first
- * timed call and after every group; group_ms[g] receives group g's time.  The
+ * q + (i % n_copies) * q_stride.  The device is synchronised before the
+ * warmup calls, not after them: they prime the queue, so the first timed call
+ * starts behind queued work like every later one.  A HIP event is recorded
+ * before the first timed call and after every group; group_ms[g] receives
+ * group g's time (groups = 1 times all the calls between two events).  The
  * bench's counterpart of the reference's compiled benchmark loops
  * (crates/axc-driver/benches/dispatch_q4km.rs:101-124): no interpreter
  * between launches.  No counterpart in the reference's C surface. */

@@ -241,6 +241,12 @@ def test_matmul_kernel_selection(axc):
     assert name(4096, 56, 8, axc.MatmulVariant(3, 8, 1, 2, 1)) == "axh_q4k_matmul_ks_k8_n1_p2_r1"
     with pytest.raises(axc.DispatchError):  # kind 9 keeps the chunk offsets below 1 MiB
         name(16, 1024, 8, axc.MatmulVariant(9))
+    # ... so a call without a variant never picks it there: rows of 1024 or
+    # more superblocks fall through to the K-split kinds
+    assert name(64, 1024, 1) == "axh_q4k_matmul_ks_k8_n1_p1_r1"
+    assert name(4096, 1200, 8).startswith("axh_q4k_matmul_k")
+    assert name(4096, 2048, 2).startswith("axh_q4k_matmul_k")
+    assert name(16, 1023, 8).startswith("axh_q4k_matmul_lk_")
     # K-split tiles, columns halved until 160 workgroups
     assert name(14336, 16, 64) == "axh_q4k_matmul_kx_r4_n4_k4_p2"
     assert name(14336, 16, 128) == "axh_q4k_matmul_kx_r4_n8_k4_p2"
