@@ -324,6 +324,17 @@ axh_status axh_grid_search(const axh_strategy_hole *holes, uint32_t n_holes,
 
 // ---- Q4_K matvec autotuner: every kernel family, judged by the checker ------
 namespace {
+// Weight copies the timing rotates through: more bytes than the 256 MiB
+// Infinity Cache, so every timed call streams its weights from HBM, as the
+// bench and a model's decode step do (a single 33 MB matrix stays cache-hot).
+constexpr uint64_t kRotateBytes = 512ull << 20;
+constexpr uint32_t kMaxCopies = 64;
+// Interleaved confirmation of the sweep's winner against the default: rounds
+// of calls of each, alternating; the default is kept unless the winner's
+// median is below it by more than the run-to-run spread of these boxes.
+constexpr uint32_t kConfirmRounds = 9, kConfirmCalls = 50;
+constexpr double kConfirmSpread = 0.02;
+
 struct Q4kTuneCtx {
   axh_context *ctx;
   const void *q;
@@ -336,7 +347,40 @@ struct Q4kTuneCtx {
   std::vector<float> x_host, y_host;
   // hole names of the current family's search, in the enumerator's key order
   std::vector<std::string> keys;
+  // rotated weight copies (copy 0 is the caller's q)
+  uint8_t *copies = nullptr;
+  uint64_t stride = 0;
+  uint32_t n_copies = 1;
+  uint32_t next = 0;
+  const void *weights() {
+    const uint32_t i = next++ % n_copies;
+    return i == 0 ? q : copies + (uint64_t)(i - 1) * stride;
+  }
 };
+
+// Median ns per call of `calls` back-to-back calls of v over the rotated
+// copies (one group between two events).
+axh_status time_calls(Q4kTuneCtx &t, const axh_q4_variant &v, uint32_t calls, hipEvent_t e0,
+                      hipEvent_t e1, uint64_t *ns) {
+  hipStream_t s = t.ctx->core->stream;
+  for (uint32_t i = 0; i < 3; ++i) {
+    const axh_status st = axh_q4k_matvec(t.ctx, t.weights(), t.x, t.y, t.n_rows, t.sb, &v, s);
+    if (st != AXH_OK) return st;
+  }
+  hipEventRecord(e0, s);
+  for (uint32_t i = 0; i < calls; ++i) {
+    const axh_status st = axh_q4k_matvec(t.ctx, t.weights(), t.x, t.y, t.n_rows, t.sb, &v, s);
+    if (st != AXH_OK) return st;
+  }
+  hipEventRecord(e1, s);
+  const axh_status st = axh_synchronize(t.ctx, nullptr);
+  if (st != AXH_OK) return st;
+  float ms = 0;
+  if (hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+    return fail(AXH_ERR_QUEUE_SUBMIT, "hipEventElapsedTime failed");
+  *ns = (uint64_t)((double)ms * 1e6 / calls);
+  return AXH_OK;
+}
 
 // The assignment of one enumerated variant (values in sorted key order).
 axh_q4_variant assignment(const Q4kTuneCtx &t, const int64_t *v) {
@@ -396,37 +440,21 @@ int tune_bench(void *user, uint64_t, const int64_t *vals, uint32_t, axh_sample_s
   Q4kTuneCtx &t = *static_cast<Q4kTuneCtx *>(user);
   const axh_q4_variant v = assignment(t, vals);
   if (!plans(t, v, err, cap)) return 1;
-  hipStream_t s = t.ctx->core->stream;
-  std::vector<uint64_t> ns;
   hipEvent_t e0, e1;
   if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
     std::snprintf(err, cap, "hipEventCreate failed");
     return 1;
   }
-  for (uint32_t i = 0; i < 3; ++i) axh_q4k_matvec(t.ctx, t.q, t.x, t.y, t.n_rows, t.sb, &v, s);
-  const uint32_t reps = 20;
-  for (uint32_t smp = 0; smp < t.samples; ++smp) {
-    hipEventRecord(e0, s);
-    for (uint32_t i = 0; i < reps; ++i)
-      if (axh_q4k_matvec(t.ctx, t.q, t.x, t.y, t.n_rows, t.sb, &v, s) != AXH_OK) {
-        std::snprintf(err, cap, "%s", axh_last_error());
-        hipEventDestroy(e0);
-        hipEventDestroy(e1);
-        return 1;
-      }
-    hipEventRecord(e1, s);
-    if (axh_synchronize(t.ctx, nullptr) != AXH_OK) {
-      std::snprintf(err, cap, "%s", axh_last_error());
-      hipEventDestroy(e0);
-      hipEventDestroy(e1);
-      return 1;
-    }
-    float ms = 0;
-    hipEventElapsedTime(&ms, e0, e1);
-    ns.push_back((uint64_t)((double)ms * 1e6 / reps));
-  }
+  std::vector<uint64_t> ns(t.samples);
+  axh_status st = AXH_OK;
+  for (uint32_t smp = 0; smp < t.samples && st == AXH_OK; ++smp)
+    st = time_calls(t, v, 20, e0, e1, &ns[smp]);
   hipEventDestroy(e0);
   hipEventDestroy(e1);
+  if (st != AXH_OK) {
+    std::snprintf(err, cap, "%s", axh_last_error());
+    return 1;
+  }
   std::sort(ns.begin(), ns.end());
   out->median_ns = ns[ns.size() / 2];
   out->min_ns = ns.front();
@@ -477,6 +505,41 @@ std::vector<Hole> family_holes(uint32_t fam, uint32_t n_rows, uint32_t nsb) {
 }
 } // namespace
 
+// A family takes the shape when its probe assignment plans to a kernel (the
+// persistent family takes every shape).
+static bool family_takes(uint32_t fam, uint32_t n_rows, uint32_t nsb) {
+  axh_q4_variant probe{};
+  probe.family = fam;
+  char name[64];
+  return fam == AXH_Q4K_FAMILY_PERSISTENT ||
+         axh_q4k_matvec_kernel_name(n_rows, nsb, &probe, name, sizeof(name)) == AXH_OK;
+}
+
+axh_status axh_q4k_matvec_family_holes(uint32_t family, uint32_t n_rows, uint32_t sb_per_row,
+                                       const char **names, uint32_t *n_candidates,
+                                       int64_t *candidates, uint32_t cap_holes,
+                                       uint32_t cap_candidates, uint32_t *n_holes) {
+  if (!n_holes || n_rows == 0 || sb_per_row == 0 || family < AXH_Q4K_FAMILY_PERSISTENT ||
+      family > AXH_Q4K_FAMILY_TILED)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "family holes: a family 1-7, a shape and n_holes");
+  if (!family_takes(family, n_rows, sb_per_row))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "the family has no kernel for this shape");
+  const std::vector<Hole> hs = family_holes(family, n_rows, sb_per_row);
+  *n_holes = (uint32_t)hs.size();
+  if (!names) return ok(); // size query
+  uint32_t used = 0;
+  if (hs.size() > cap_holes || !n_candidates || !candidates)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "family holes: arrays too small");
+  for (size_t h = 0; h < hs.size(); ++h) {
+    if (used + hs[h].cand.size() > cap_candidates)
+      return fail(AXH_ERR_INVALID_ARGUMENT, "family holes: candidate array too small");
+    names[h] = hs[h].name;
+    n_candidates[h] = (uint32_t)hs[h].cand.size();
+    for (int64_t c : hs[h].cand) candidates[used++] = c;
+  }
+  return ok();
+}
+
 axh_status axh_q4k_matvec_autotune(axh_context *ctx, const void *q, const float *x, float *y,
                                    uint32_t n_rows, uint32_t sb_per_row, uint32_t samples,
                                    double tol, axh_autotune_report *out) {
@@ -495,16 +558,30 @@ axh_status axh_q4k_matvec_autotune(axh_context *ctx, const void *q, const float 
   if (st == AXH_OK) st = axh_download(ctx, t.x_host.data(), x, 4u * t.x_host.size());
   if (st != AXH_OK) return st;
   if ((st = axh_q4k_matvec_default_variant(n_rows, sb_per_row, &out->dflt)) != AXH_OK) return st;
+  // Rotated copies of q (device to device), released on every return below.
+  t.stride = (q_bytes + 255u) / 256u * 256u;
+  t.n_copies = (uint32_t)std::min<uint64_t>(kMaxCopies, std::max<uint64_t>(
+                                                            1, (kRotateBytes + t.stride - 1) / t.stride));
+  if (t.n_copies > 1) {
+    void *p = nullptr;
+    if ((st = axh_buffer_alloc(ctx, t.stride * (t.n_copies - 1), &p)) != AXH_OK) return st;
+    t.copies = static_cast<uint8_t *>(p);
+    for (uint32_t c = 1; c < t.n_copies && st == AXH_OK; ++c)
+      st = axh_copy_device(ctx, t.copies + (uint64_t)(c - 1) * t.stride, q, q_bytes);
+    if (st == AXH_OK) st = axh_synchronize(ctx, nullptr);
+  }
+  struct Release {
+    Q4kTuneCtx &t;
+    ~Release() {
+      if (t.copies) axh_buffer_free(t.ctx, t.copies);
+    }
+  } release{t};
+  if (st != AXH_OK) return st;
+  out->weight_copies = t.n_copies;
 
   bool have = false;
   for (uint32_t fam = AXH_Q4K_FAMILY_PERSISTENT; fam <= AXH_Q4K_FAMILY_TILED; ++fam) {
-    // families that cannot take the shape are skipped whole
-    axh_q4_variant probe{};
-    probe.family = fam;
-    char name[64];
-    if (fam != AXH_Q4K_FAMILY_PERSISTENT &&
-        axh_q4k_matvec_kernel_name(n_rows, sb_per_row, &probe, name, sizeof(name)) != AXH_OK)
-      continue;
+    if (!family_takes(fam, n_rows, sb_per_row)) continue; // families without a kernel: skipped
     const std::vector<Hole> hs = family_holes(fam, n_rows, sb_per_row);
     std::vector<axh_strategy_hole> holes;
     for (const Hole &h : hs)
@@ -542,6 +619,34 @@ axh_status axh_q4k_matvec_autotune(axh_context *ctx, const void *q, const float 
     }
   }
   if (!have) return fail((axh_status)AXH_ERR_NO_SUCCESSFUL_VARIANTS, "no variant ran");
+  // Confirmation: the sweep's winner against the default in interleaved
+  // rounds; a winner that does not beat the default by more than the spread
+  // leaves the default in place.
+  if (std::memcmp(&out->best, &out->dflt, sizeof(out->best)) != 0 && out->default_median_ns) {
+    hipEvent_t e0, e1;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+      return fail(AXH_ERR_QUEUE_SUBMIT, "hipEventCreate failed");
+    std::vector<uint64_t> tb(kConfirmRounds), td(kConfirmRounds);
+    for (uint32_t r = 0; r < kConfirmRounds && st == AXH_OK; ++r) {
+      st = time_calls(t, out->best, kConfirmCalls, e0, e1, &tb[r]);
+      if (st == AXH_OK) st = time_calls(t, out->dflt, kConfirmCalls, e0, e1, &td[r]);
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (st != AXH_OK) return st;
+    std::sort(tb.begin(), tb.end());
+    std::sort(td.begin(), td.end());
+    out->confirm_best_ns = tb[kConfirmRounds / 2];
+    out->confirm_default_ns = td[kConfirmRounds / 2];
+    if ((double)out->confirm_best_ns > (1.0 - kConfirmSpread) * (double)out->confirm_default_ns) {
+      out->kept_default = 1;
+      out->best = out->dflt;
+      out->best_median_ns = out->default_median_ns;
+    }
+  } else {
+    out->confirm_best_ns = out->confirm_default_ns = out->best_median_ns;
+    out->kept_default = std::memcmp(&out->best, &out->dflt, sizeof(out->best)) == 0;
+  }
   if ((st = axh_q4k_matvec_kernel_name(n_rows, sb_per_row, &out->best, out->best_kernel,
                                        sizeof(out->best_kernel))) != AXH_OK)
     return st;

@@ -7,18 +7,30 @@ JSONL optimisation history, and `optimization_history`.  Where the reference
 compiles `.axc` source with `@strategy` holes, the kernels here are the
 library's compiled Q4 operations, named like the reference kernels:
 
-  q4km_dequant_matvec  holes rows_per_wave, waves_per_workgroup, prefetch, nontemporal
+  q4km_dequant_matvec  one hole map per kernel family that takes the shape
+                       (family, then that family's holes among rows_per_wave,
+                       waves_per_workgroup, prefetch, nontemporal, sb_per_lane):
+                       the space of the library's autotuner, default kernels
+                       included
   q4_0_dequant_matvec  holes rows_per_wave, waves_per_workgroup
   q4k_matmul_f16       holes kind, waves_per_workgroup, col_tiles, prefetch, row_tiles
 
 and a request names a shape ({"n_rows", "units_per_row", "batch"}) instead of
-input byte sizes.  Correctness is a real verdict for every kernel (the
+input byte sizes.  A search over several hole maps enumerates each map as the
+reference enumerates one (keys sorted, last key fastest) and numbers the
+variants on across the maps.  Correctness is a real verdict for every kernel (the
 reference reports its Q4 kernel "not_checked", bench_variant.rs:395-400):
 the device result is compared with an f64 accumulation of the reference's
 dequantised weights by the library's host checker (include/axh_check.h).
 
 Timing samples are HIP-event times on resident buffers (each sample the mean
-of `launches_per_sample` back-to-back launches), not host round trips.
+of `launches_per_sample` back-to-back launches), not host round trips.  The
+weights are copied on the device until the copies pass 512 MiB and the
+launches rotate through them, so each launch reads HBM rather than the
+256 MiB Infinity Cache.  grid_search runs one set of inputs for the whole
+search and times the variants in interleaved rounds (one sample of every
+variant per round), so drift of the clocks over a search falls on all
+variants alike.
 """
 from __future__ import annotations
 
@@ -219,20 +231,23 @@ def check_result(kernel: str, shape: dict, q, x, y, rel_tol: float = DEFAULT_REL
 
 
 # ---- hole spaces ----------------------------------------------------------------
-def default_holes(kernel: str) -> dict:
-    """Candidate values of every hole, from the compiled variants (sorted)."""
+def default_holes(kernel: str, shape: Optional[dict] = None) -> list:
+    """The kernel's hole space as a list of hole maps.  q4km_dequant_matvec:
+    one map per kernel family that takes the shape (the autotuner's space,
+    tune.q4k_matvec_hole_spaces); the other kernels: one map of the candidate
+    values of every hole among the compiled variants (sorted)."""
+    if kernel == "q4km_dequant_matvec":
+        from . import tune
+        shape = shape or {"n_rows": 1, "units_per_row": 1}
+        return tune.q4k_matvec_hole_spaces(int(shape["n_rows"]), int(shape["units_per_row"]))
     if kernel == "q4k_matmul_f16":
         vs = [(v.kind, v.waves_per_workgroup, v.col_tiles, v.prefetch, v.row_tiles)
               for v in _axh.compiled_matmul_variants()]
         names = ("kind", "waves_per_workgroup", "col_tiles", "prefetch", "row_tiles")
     else:
-        kind = "q4k" if kernel == "q4km_dequant_matvec" else "q4_0"
-        vs = [(v.rows_per_wave, v.waves_per_workgroup, v.prefetch, v.nontemporal)
-              for v in _axh.compiled_variants(kind)]
-        names = ("rows_per_wave", "waves_per_workgroup", "prefetch", "nontemporal")
-        if kind == "q4_0":
-            names, vs = names[:2], [v[:2] for v in vs]
-    return {n: sorted({v[i] for v in vs}) for i, n in enumerate(names)}
+        vs = [(v.rows_per_wave, v.waves_per_workgroup) for v in _axh.compiled_variants("q4_0")]
+        names = ("rows_per_wave", "waves_per_workgroup")
+    return [{n: sorted({v[i] for v in vs}) for i, n in enumerate(names)}]
 
 
 def _variant_obj(kernel: str, a: dict):
@@ -241,7 +256,17 @@ def _variant_obj(kernel: str, a: dict):
         return _axh.MatmulVariant(g("kind"), g("waves_per_workgroup"), g("col_tiles"),
                                   g("prefetch"), g("row_tiles"))
     return _axh.Variant(g("rows_per_wave"), g("waves_per_workgroup"), g("prefetch"),
-                        g("nontemporal"))
+                        g("nontemporal"), g("family"), g("sb_per_lane"))
+
+
+def _enumerate_spaces(spaces: list) -> list:
+    """Variants of every map in turn; ordinals continue across the maps."""
+    from . import tune
+    out = []
+    for holes in spaces:
+        for v in tune.enumerate_strategy(holes):
+            out.append(tune.StrategyVariant(len(out), v.variant_id, v.assignments))
+    return out
 
 
 # ---- context ---------------------------------------------------------------------
@@ -295,29 +320,112 @@ def _kernel_and_shape(params: dict):
     return kernel, out
 
 
-def _holes(params: dict, kernel: str) -> dict:
-    """`holes_override` REPLACES the kernel's hole map when present, even if
-    empty (grid_search.rs:268-272); otherwise the compiled hole space."""
+def _holes(params: dict, kernel: str, shape: Optional[dict] = None) -> list:
+    """`holes_override` REPLACES the kernel's hole space when present, even if
+    empty (grid_search.rs:268-272): one map, or a list of maps; otherwise the
+    kernel's default space."""
     h = params.get("holes_override")
     if h is None:
-        return default_holes(kernel)
-    if not isinstance(h, dict) or not all(isinstance(v, list) for v in h.values()):
-        raise invalid("holes_override must map hole names to lists of integers")
-    return {k: [int(x) for x in v] for k, v in h.items()}
+        return default_holes(kernel, shape)
+    maps = h if isinstance(h, list) else [h]
+    for m in maps:
+        if not isinstance(m, dict) or not all(isinstance(v, list) for v in m.values()):
+            raise invalid("holes_override must map hole names to lists of integers "
+                          "(or be a list of such maps)")
+    return [{k: [int(x) for x in v] for k, v in m.items()} for m in maps]
 
 
 def enumerate_variants(params: dict, ctx: McpContext) -> dict:
     from . import tune
-    kernel, _ = _kernel_and_shape({**params, "shape": params.get("shape") or
-                                   {"n_rows": 1, "units_per_row": 1}})
-    holes = _holes(params, kernel)
+    kernel, shape = _kernel_and_shape({**params, "shape": params.get("shape") or
+                                       {"n_rows": 1, "units_per_row": 1}})
+    spaces = _holes(params, kernel, shape)
     try:
-        vs = tune.enumerate_strategy(holes)
+        vs = _enumerate_spaces(spaces)
     except tune.TuneError as e:
         raise McpToolError(ENUMERATE_ERROR, "enumerate_error", str(e))
     return {"variants": [{"ordinal": v.ordinal, "variant_id": v.variant_id,
                           "assignments": v.assignments} for v in vs],
             "count": len(vs)}
+
+
+ROTATE_BYTES = 512 << 20
+
+
+class _Workload:
+    """One set of inputs on the device, the weights copied until the copies
+    pass ROTATE_BYTES; launch(variant, i) runs call i on copy i mod n."""
+
+    def __init__(self, hip, kernel: str, shape: dict, q, x):
+        self.hip, self.kernel, self.shape, self.q, self.x = hip, kernel, shape, q, x
+        self.rows, self.units = shape["n_rows"], shape["units_per_row"]
+        self.batch = shape.get("batch", 1)
+        self.stride = -(-max(q.nbytes, 16) // 256) * 256
+        self.n = max(1, min(64, -(-ROTATE_BYTES // self.stride)))
+        self.y_bytes = self.rows * self.batch * 4
+        self.bufs = []
+        try:
+            self.w = hip.alloc(self.stride * self.n)
+            self.bufs.append(self.w)
+            for c in range(self.n):
+                hip.upload(self.w.ptr + c * self.stride, q)
+            self.dx = hip.alloc(max(x.nbytes, 16))
+            self.bufs.append(self.dx)
+            hip.upload(self.dx, x)
+            self.dy = hip.alloc(self.y_bytes)
+            self.bufs.append(self.dy)
+        except Exception:
+            self.close()
+            raise
+
+    def launch(self, variant, i: int = 0) -> None:
+        w = self.w.ptr + (i % self.n) * self.stride
+        if self.kernel == "q4km_dequant_matvec":
+            self.hip.q4k_matvec(w, self.dx, self.dy, self.rows, self.units, variant)
+        elif self.kernel == "q4_0_dequant_matvec":
+            self.hip.q4_0_matvec(w, self.dx, self.dy, self.rows, self.units, variant)
+        else:
+            self.hip.q4k_matmul(w, self.dx, self.dy, self.rows, self.units, self.batch, variant)
+
+    def run_once(self, variant) -> np.ndarray:
+        """One call on copy 0 and its output (DispatchError if it cannot run)."""
+        self.launch(variant, 0)
+        self.hip.synchronize()
+        return np.frombuffer(self.hip.download(self.dy, self.y_bytes), dtype=np.float32).copy()
+
+    def sample_ns(self, variant, per: int, e0, e1) -> int:
+        """Mean ns per call of `per` back-to-back calls over the copies."""
+        for i in range(3):
+            self.launch(variant, i)
+        e0.record()
+        for i in range(per):
+            self.launch(variant, i)
+        e1.record()
+        e1.synchronize()
+        return int(round(e0.elapsed_ms(e1) * 1e6 / per))
+
+    def verdict(self, y, params: dict) -> dict:
+        if params.get("correctness", "check") == "none":
+            return {"status": "not_checked", "reason": "correctness policy `none`"}
+        rep = check_result(self.kernel, self.shape, self.q, self.x, y,
+                           float(params.get("rel_tol", DEFAULT_REL_TOL)))
+        return {"status": "ok"} if rep["ok"] else {
+            "status": "failed",
+            "reason": f"{rep['rows_failed']} of {rep['rows_checked']} outputs outside tolerance; "
+                      f"worst output {rep['worst_row']} at {rep['worst_over_allowed']:.3g} x "
+                      f"allowed; norm error {rep['norm_rel_err']:.3g}"}
+
+    def kernel_entry(self, variant) -> str:
+        if self.kernel == "q4k_matmul_f16":
+            return _axh.q4k_matmul_kernel_name(self.rows, self.units, self.batch, variant)
+        if self.kernel == "q4km_dequant_matvec":
+            return _axh.q4k_matvec_kernel_name(self.rows, self.units, variant)
+        return _axh.q4_0_matvec_kernel_name(self.rows, self.units, variant)
+
+    def close(self) -> None:
+        for b in self.bufs:
+            b.close()
+        self.bufs = []
 
 
 def bench_variant(params: dict, ctx: McpContext) -> dict:
@@ -330,100 +438,89 @@ def bench_variant(params: dict, ctx: McpContext) -> dict:
     vid = variant_id(assignments)
     hip = ctx.hip()
     q, x = seeded_inputs(kernel, shape, vid)
-    rows, units = shape["n_rows"], shape["units_per_row"]
-    batch = shape.get("batch", 1)
     variant = _variant_obj(kernel, assignments)
-    y_bytes = rows * batch * 4
-    bufs = [hip.alloc(max(q.nbytes, 16)), hip.alloc(max(x.nbytes, 16)), hip.alloc(y_bytes)]
+    wl = _Workload(hip, kernel, shape, q, x)
     try:
-        hip.upload(bufs[0], q)
-        hip.upload(bufs[1], x)
-
-        def launch():
-            if kernel == "q4km_dequant_matvec":
-                hip.q4k_matvec(bufs[0], bufs[1], bufs[2], rows, units, variant)
-            elif kernel == "q4_0_dequant_matvec":
-                hip.q4_0_matvec(bufs[0], bufs[1], bufs[2], rows, units, variant)
-            else:
-                hip.q4k_matmul(bufs[0], bufs[1], bufs[2], rows, units, batch, variant)
-
         try:
-            launch()
-            hip.synchronize()
+            y = wl.run_once(variant)
         except _axh.DispatchError as e:
-            raise McpToolError(DEVICE_UNAVAILABLE, "dispatch_failed",
-                               f"{e.variant}: {e}")
-        y = np.frombuffer(hip.download(bufs[2], y_bytes), dtype=np.float32).copy()
-        samples = []
+            raise McpToolError(DEVICE_UNAVAILABLE, "dispatch_failed", f"{e.variant}: {e}")
         e0, e1 = hip.event(), hip.event()
-        for _ in range(samples_n):
-            e0.record()
-            for _ in range(per):
-                launch()
-            e1.record()
-            e1.synchronize()
-            samples.append(int(round(e0.elapsed_ms(e1) * 1e6 / per)))
+        samples = [wl.sample_ns(variant, per, e0, e1) for _ in range(samples_n)]
+        verdict = wl.verdict(y, params)
+        name = wl.kernel_entry(variant)
+        copies = wl.n
     finally:
-        for b in bufs:
-            b.close()
-    if params.get("correctness", "check") == "none":
-        verdict = {"status": "not_checked", "reason": "correctness policy `none`"}
-    else:
-        rep = check_result(kernel, shape, q, x, y, float(params.get("rel_tol", DEFAULT_REL_TOL)))
-        verdict = {"status": "ok"} if rep["ok"] else {
-            "status": "failed",
-            "reason": f"{rep['rows_failed']} of {rep['rows_checked']} outputs outside tolerance; "
-                      f"worst output {rep['worst_row']} at {rep['worst_over_allowed']:.3g} x allowed; "
-                      f"norm error {rep['norm_rel_err']:.3g}"}
+        wl.close()
     srt = sorted(samples)
-    name = (_axh.q4k_matmul_kernel_name(rows, units, batch, variant)
-            if kernel == "q4k_matmul_f16" else
-            _axh.q4k_matvec_kernel_name(rows, units, variant)
-            if kernel == "q4km_dequant_matvec" else
-            _axh.q4_0_matvec_kernel_name(rows, units, variant))
     return {"median_ns": srt[len(srt) // 2], "samples": samples, "correctness": verdict,
-            "machine": ctx.machine(), "kernel_entry": name, "variant_id": vid}
+            "machine": ctx.machine(), "kernel_entry": name, "variant_id": vid,
+            "weight_copies": copies}
 
 
 def grid_search(params: dict, ctx: McpContext) -> dict:
+    """The reference's grid search (grid_search.rs:158-283) over the kernel's
+    hole space: every variant runs once and is judged, then the accepted ones
+    are timed in `sample_count` interleaved rounds of `launches_per_sample`
+    calls each; the winner has the lowest median (ties: lowest ordinal)."""
     from . import tune
     kernel, shape = _kernel_and_shape(params)
     sample_count = int(params.get("sample_count", 5))
     if sample_count < 1:
         raise invalid("sample_count must be >= 1")
-    holes = _holes(params, kernel)
+    per = max(1, int(params.get("launches_per_sample", 10)))
+    spaces = _holes(params, kernel, shape)
     try:
-        variants = tune.enumerate_strategy(holes)
+        variants = _enumerate_spaces(spaces)
     except tune.TuneError as e:
         raise McpToolError(ENUMERATE_ERROR, "enumerate_error", str(e))
+    if not variants:
+        raise McpToolError(ENUMERATE_ERROR, "enumerate_error", "the hole space is empty")
     warnings = []
     if len(variants) > CARTESIAN_WARN_THRESHOLD:
         warnings.append(f"Cartesian product ({len(variants)}) exceeds CARTESIAN_WARN_THRESHOLD "
                         f"({CARTESIAN_WARN_THRESHOLD}); search may take a long time")
-    ctx.hip()
-    ranked = []
-    for v in variants:
-        req = {"kernel": kernel, "shape": shape, "assignments": v.assignments,
-               "sample_count": sample_count, "correctness": params.get("correctness", "check"),
-               "launches_per_sample": params.get("launches_per_sample", 10)}
-        try:
-            r = bench_variant(req, ctx)
-            st = r["correctness"]["status"]
-            outcome = ("ok" if st == "ok" else "not_checked" if st == "not_checked" else
-                       f"correctness_rejected: {r['correctness']['reason']}")
-            median = None if st == "failed" else r["median_ns"]
-            ranked.append({"ordinal": v.ordinal, "variant_id": v.variant_id,
-                           "assignments": v.assignments, "median_ns": median,
-                           "correctness": r["correctness"], "outcome": outcome})
-        except McpToolError as e:
-            ranked.append({"ordinal": v.ordinal, "variant_id": v.variant_id,
-                           "assignments": v.assignments, "median_ns": None,
-                           "correctness": {"status": "not_checked", "reason": e.message},
-                           "outcome": f"failed: {e.message}"})
+    hip = ctx.hip()
+    key = source_key(kernel, shape)
+    # one input set for the whole search, seeded by the source key
+    q, x = seeded_inputs(kernel, shape, tune.xxh3_64(key.encode()))
+    wl = _Workload(hip, kernel, shape, q, x)
+    ranked, timed = [], []
+    try:
+        for v in variants:
+            variant = _variant_obj(kernel, v.assignments)
+            row = {"ordinal": v.ordinal, "variant_id": v.variant_id,
+                   "assignments": v.assignments, "median_ns": None}
+            try:
+                y = wl.run_once(variant)
+            except _axh.DispatchError as e:
+                row.update(correctness={"status": "not_checked", "reason": str(e)},
+                           outcome=f"failed: {e.variant}: {e}")
+                ranked.append(row)
+                continue
+            verdict = wl.verdict(y, params)
+            row["correctness"] = verdict
+            row["kernel_entry"] = wl.kernel_entry(variant)
+            if verdict["status"] == "failed":
+                row["outcome"] = f"correctness_rejected: {verdict['reason']}"
+            else:
+                row["outcome"] = "ok" if verdict["status"] == "ok" else "not_checked"
+                row["samples"] = []
+                timed.append((row, variant))
+            ranked.append(row)
+        e0, e1 = hip.event(), hip.event()
+        for _ in range(sample_count):  # interleaved rounds
+            for row, variant in timed:
+                row["samples"].append(wl.sample_ns(variant, per, e0, e1))
+        for row, _ in timed:
+            srt = sorted(row["samples"])
+            row["median_ns"] = srt[len(srt) // 2]
+        copies = wl.n
+    finally:
+        wl.close()
     ranked.sort(key=lambda r: (r["median_ns"] is None, r["median_ns"] or 0, r["ordinal"]))
     win = next((r for r in ranked if r["median_ns"] is not None), ranked[0])
     fallback = win["median_ns"] is None
-    key = source_key(kernel, shape)
     from . import tune as _t
     path = history_path(ctx.history_dir, key)
     win_ns = win["median_ns"] if win["median_ns"] is not None else 2 ** 64 - 1
@@ -438,9 +535,11 @@ def grid_search(params: dict, ctx: McpContext) -> dict:
     except OSError as e:
         raise McpToolError(IO_ERROR, "io_error", str(e))
     return {"winner": {"ordinal": win["ordinal"], "variant_id": win["variant_id"],
-                       "assignments": win["assignments"]},
+                       "assignments": win["assignments"],
+                       "kernel_entry": win.get("kernel_entry")},
             "winner_median_ns": win_ns, "ranked": ranked, "fallback_used": fallback,
-            "warnings": warnings, "history_path": str(path), "machine": ctx.machine()}
+            "warnings": warnings, "history_path": str(path), "machine": ctx.machine(),
+            "weight_copies": copies}
 
 
 def optimization_history(params: dict, ctx: McpContext) -> dict:

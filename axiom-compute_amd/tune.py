@@ -50,7 +50,9 @@ class _Report(ctypes.Structure):
                 ("dflt", _axh._Variant), ("default_median_ns", ctypes.c_uint64),
                 ("variants", ctypes.c_uint32), ("accepted", ctypes.c_uint32),
                 ("rejected", ctypes.c_uint32), ("failed", ctypes.c_uint32),
-                ("best_kernel", ctypes.c_char * 64)]
+                ("best_kernel", ctypes.c_char * 64), ("confirm_best_ns", ctypes.c_uint64),
+                ("confirm_default_ns", ctypes.c_uint64), ("kept_default", ctypes.c_uint32),
+                ("weight_copies", ctypes.c_uint32)]
 
 
 _BENCH = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64,
@@ -79,6 +81,12 @@ def _lib():
         lib.axh_grid_search.argtypes = [c.POINTER(_Hole), c.c_uint32, c.POINTER(_Policy),
                                         _CORRECT, _BENCH, c.c_void_p, c.POINTER(_Result),
                                         c.c_uint64, c.POINTER(_Summary)]
+        lib.axh_q4k_matvec_family_holes.restype = c.c_int
+        lib.axh_q4k_matvec_family_holes.argtypes = [c.c_uint32, c.c_uint32, c.c_uint32,
+                                                    c.POINTER(c.c_char_p),
+                                                    c.POINTER(c.c_uint32),
+                                                    c.POINTER(c.c_int64), c.c_uint32,
+                                                    c.c_uint32, c.POINTER(c.c_uint32)]
         lib.axh_q4k_matvec_autotune.restype = c.c_int
         lib.axh_q4k_matvec_autotune.argtypes = [c.c_void_p, c.c_void_p, c.c_void_p, c.c_void_p,
                                                 c.c_uint32, c.c_uint32, c.c_uint32, c.c_double,
@@ -274,6 +282,37 @@ class AutotuneReport:
     rejected: int
     failed: int
     best_kernel: str
+    confirm_best_ns: int = 0
+    confirm_default_ns: int = 0
+    kept_default: bool = False
+    weight_copies: int = 1
+
+
+def q4k_matvec_family_holes(family: int, n_rows: int, sb_per_row: int) -> Optional[dict]:
+    """The hole space the autotuner searches for `family` at this shape
+    ({hole: [candidates]}, the family hole included), or None when the family
+    has no kernel for the shape."""
+    lib = _lib()
+    n = ctypes.c_uint32()
+    if lib.axh_q4k_matvec_family_holes(family, n_rows, sb_per_row, None, None, None, 0, 0,
+                                       ctypes.byref(n)) != 0:
+        return None
+    names = (ctypes.c_char_p * n.value)()
+    counts = (ctypes.c_uint32 * n.value)()
+    cands = (ctypes.c_int64 * 256)()
+    _check(lib.axh_q4k_matvec_family_holes(family, n_rows, sb_per_row, names, counts, cands,
+                                           n.value, 256, ctypes.byref(n)))
+    out, k = {}, 0
+    for h in range(n.value):
+        out[names[h].decode()] = [int(cands[k + i]) for i in range(counts[h])]
+        k += counts[h]
+    return out
+
+
+def q4k_matvec_hole_spaces(n_rows: int, sb_per_row: int) -> list:
+    """One hole map per Q4_K matvec family that takes the shape, in family
+    order: the space axh_q4k_matvec_autotune searches."""
+    return [h for f in range(1, 8) if (h := q4k_matvec_family_holes(f, n_rows, sb_per_row))]
 
 
 def q4k_matvec_autotune(ctx, q, x, y, n_rows: int, sb_per_row: int, samples: int = 5,
@@ -286,7 +325,9 @@ def q4k_matvec_autotune(ctx, q, x, y, n_rows: int, sb_per_row: int, samples: int
                                           n_rows, sb_per_row, samples, tol, ctypes.byref(r)))
     return AutotuneReport(_axh._variant_from_c(r.best), int(r.best_median_ns),
                           _axh._variant_from_c(r.dflt), int(r.default_median_ns),
-                          r.variants, r.accepted, r.rejected, r.failed, r.best_kernel.decode())
+                          r.variants, r.accepted, r.rejected, r.failed, r.best_kernel.decode(),
+                          int(r.confirm_best_ns), int(r.confirm_default_ns),
+                          bool(r.kept_default), int(r.weight_copies))
 
 
 class WinnerTable:

@@ -20,11 +20,13 @@ extern "C" {
 
 /* Layout version of the structs below, raised whenever one of them changes
  * size or field order.  2: axh_q4_variant grew from 4 to 6 fields (16 to 24
- * bytes: family, sb_per_lane appended).  A binding written against an older
+ * bytes: family, sb_per_lane appended).  3: axh_autotune_report (axh_tune.h)
+ * gained confirm_best_ns, confirm_default_ns, kept_default and
+ * weight_copies at its end.  A binding written against an older
  * header compares axh_abi_version() with the AXH_ABI_VERSION it was written
  * for and refuses to run on a mismatch.  No counterpart in the reference
  * (its runtime is linked as one Rust crate graph). */
-#define AXH_ABI_VERSION 2u
+#define AXH_ABI_VERSION 3u
 uint32_t axh_abi_version(void);
 
 /* One code per DispatchError variant (crates/axc-runtime/src/error.rs:27-195),

@@ -150,11 +150,16 @@ axh_status axh_context_q4k_matvec_kernel_name(axh_context *ctx, uint32_t n_rows,
  * once and its output is judged by axh_check_q4k_matvec (f64 accumulation of
  * the reference's dequantised weights, relative tolerance `tol`, 1e-3 when 0)
  * on host copies of q and x, then it is timed over `samples` groups of 20
- * back-to-back calls with HIP events.  The fastest accepted variant is stored
- * in the context's table (and its file, if any). */
+ * back-to-back calls with HIP events.  Timed calls rotate through device
+ * copies of q totalling more than 512 MiB (up to 64 copies), so each call
+ * reads its weights from HBM rather than the 256 MiB Infinity Cache.  The
+ * fastest accepted variant is then timed again against the default in 9
+ * interleaved rounds of 50 calls each; unless its median is more than 2 %
+ * below the default's (the run-to-run spread), the default is kept.  The
+ * result is stored in the context's table (and its file, if any). */
 typedef struct axh_autotune_report {
-    axh_q4_variant best;          /* winner */
-    uint64_t best_median_ns;      /* its median per call */
+    axh_q4_variant best;          /* winner (the default when kept_default) */
+    uint64_t best_median_ns;      /* its median per call in the sweep */
     axh_q4_variant dflt;          /* the shape's default assignment */
     uint64_t default_median_ns;   /* its median in the same sweep */
     uint32_t variants;            /* assignments enumerated over all families */
@@ -162,10 +167,29 @@ typedef struct axh_autotune_report {
     uint32_t rejected;            /* failed the checker */
     uint32_t failed;              /* not compiled, not valid for the shape, or launch error */
     char best_kernel[64];         /* entry point of the winner */
+    uint64_t confirm_best_ns;     /* the sweep's fastest, interleaved re-timing (median) */
+    uint64_t confirm_default_ns;  /* the default in the same rounds */
+    uint32_t kept_default;        /* 1: the result is the default (the sweep's fastest,
+                                     or a variant that did not beat it by more than 2 %) */
+    uint32_t weight_copies;       /* copies of q the timing rotated through */
 } axh_autotune_report;
 axh_status axh_q4k_matvec_autotune(axh_context *ctx, const void *q, const float *x, float *y,
                                    uint32_t n_rows, uint32_t sb_per_row, uint32_t samples,
                                    double tol, axh_autotune_report *out);
+
+/* The hole space the autotuner searches for one kernel family at a shape (the
+ * family hole first, with the family as its one candidate, then that family's
+ * holes), for callers that run their own search over the same space, such as
+ * the JSON-RPC tuning tools.  names[h] (static strings) and n_candidates[h]
+ * for h < *n_holes; the candidates of all holes concatenated in `candidates`.
+ * With names == NULL only *n_holes is set.  InvalidArgument when the family
+ * has no kernel for the shape or an array is too small.  No counterpart in
+ * the reference (its holes come from the kernel source's @strategy block,
+ * crates/axc-hir/src/hir.rs:62-68). */
+axh_status axh_q4k_matvec_family_holes(uint32_t family, uint32_t n_rows, uint32_t sb_per_row,
+                                       const char **names, uint32_t *n_candidates,
+                                       int64_t *candidates, uint32_t cap_holes,
+                                       uint32_t cap_candidates, uint32_t *n_holes);
 
 #ifdef __cplusplus
 }

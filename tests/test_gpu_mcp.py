@@ -79,3 +79,51 @@ def test_grid_search_over_the_stdio_server(mcp, tmp_path):
     assert len(entries) == 1
     assert entries[0]["grid_search"]["winner_variant_id"] == res["winner"]["variant_id"]
     assert entries[0]["source_xxh3"] == r2["result"]["history_path"].split("/")[-1][:16]
+
+
+def test_grid_search_over_the_default_space_at_c4(mcp, axc, tmp_path):
+    """4096 x 14336 over the tool's default hole space
+    (every family the autotuner searches): the default kernel is among the
+    accepted variants, and the winner, timed again against the default on
+    rotated copies in interleaved rounds, is no slower than it beyond the
+    run-to-run spread (grid_search.rs:265-276 searches the kernel's own
+    holes)."""
+    rows, sb = 4096, 56
+    shape = {"n_rows": rows, "units_per_row": sb}
+    _say(f"grid_search q4km_dequant_matvec {shape} over the default space")
+    ctx = mcp.McpContext(history_dir=tmp_path)
+    res = mcp.grid_search({"kernel": "q4km_dequant_matvec", "shape": shape, "sample_count": 5,
+                           "launches_per_sample": 20}, ctx)
+    assert not res["fallback_used"] and res["weight_copies"] >= 9
+    dflt = axc.q4k_matvec_kernel_name(rows, sb)
+    ok = [r for r in res["ranked"] if r["median_ns"] is not None]
+    assert all(r["correctness"]["status"] == "ok" for r in ok)
+    assert dflt in {r["kernel_entry"] for r in ok}
+    win = res["winner"]
+    _say(f"  winner {win['kernel_entry']} {res['winner_median_ns']} ns "
+         f"({len(ok)} of {len(res['ranked'])} variants timed); default {dflt}")
+    # re-time the winner and the default
+    import numpy as np
+    from oracle import oracle as O
+    hip = ctx.hip()
+    q = O.gen_q4k_weights(20241, rows * sb)
+    x = O.gen_normal_f32(20242, sb * 256, 0.5)
+    stride = (q.nbytes + 255) // 256 * 256
+    n = -(-(600 << 20) // stride)
+    wbuf = hip.alloc(stride * n)
+    for c in range(n):
+        hip.upload(wbuf.ptr + c * stride, q)
+    dx, dy = hip.alloc(x.nbytes), hip.alloc(rows * 4)
+    hip.upload(dx, x)
+    base = dict(op="q4k", q=wbuf, q_stride=stride, n_copies=n, x=dx, y=dy, n_rows=rows, units=sb)
+    wv = mcp._variant_obj("q4km_dequant_matvec", win["assignments"])
+    t = {"winner": [], "default": []}
+    for _ in range(9):
+        for k, v in (("winner", wv), ("default", None)):
+            t[k].append(sum(hip.bench_loop(**base, variant=v, warmup=5, groups=1,
+                                           calls_per_group=50)) * 1e3 / 50)
+    med = {k: sorted(v)[len(v) // 2] for k, v in t.items()}
+    _say(f"  re-timed: winner {med['winner']:.3f} us, default {med['default']:.3f} us")
+    for b in (wbuf, dx, dy):
+        b.close()
+    assert med["winner"] <= 1.03 * med["default"], med

@@ -37,20 +37,29 @@ def _dev(ctx, arr):
     return b
 
 
-def _median_us(ctx, fn, calls=50, rounds=7):
-    ev0, ev1 = ctx.event(), ctx.event()
-    out = []
+def _rotated(ctx, q, min_total=600 << 20):
+    """Device copies of q (256-byte aligned) totalling more than min_total."""
+    stride = (q.nbytes + 255) // 256 * 256
+    n = max(2, -(-min_total // stride))
+    buf = ctx.alloc(stride * n)
+    for c in range(n):
+        ctx.upload(buf.ptr + c * stride, q)
+    return buf, stride, n
+
+
+def _interleaved_us(ctx, ops: dict, rounds=9, calls=50) -> dict:
+    """Median us per call of each bench-loop op, timed in interleaved rounds."""
+    t = {k: [] for k in ops}
     for _ in range(rounds):
-        for _ in range(5):
-            fn()
-        ctx.device_synchronize()
-        ev0.record()
-        for _ in range(calls):
-            fn()
-        ev1.record()
-        ev1.synchronize()
-        out.append(ev0.elapsed_ms(ev1) * 1000.0 / calls)
-    return sorted(out)[len(out) // 2]
+        for k, op in ops.items():
+            t[k].append(sum(ctx.bench_loop(**op, warmup=5, groups=1, calls_per_group=calls))
+                        * 1e3 / calls)
+    return {k: sorted(v)[len(v) // 2] for k, v in t.items()}
+
+
+# Run-to-run spread of one kernel timed in interleaved rounds on these boxes
+# (the same binary measured up to ~2 % apart); the margin sits above it.
+SPREAD_MARGIN = 1.03
 
 
 def test_grid_search_over_every_family_at_c4(axc, tune):
@@ -65,12 +74,17 @@ def test_grid_search_over_every_family_at_c4(axc, tune):
     dq, dx, dy = _dev(c, q), _dev(c, x), c.alloc(rows * 4)
     rep = tune.q4k_matvec_autotune(c, dq, dx, dy, rows, sb, samples=5)
     _say(f"autotune report: {rep}")
+    assert rep.weight_copies >= 9  # timed over > 512 MiB of copies: HBM, not the cache
     assert rep.default == axc.q4k_matvec_default_variant(rows, sb)
     assert rep.default_median_ns > 0  # the default was among the accepted variants
     assert rep.accepted >= 15 and rep.rejected == 0
     assert rep.variants == rep.accepted + rep.rejected + rep.failed
     assert rep.best_kernel == axc.q4k_matvec_kernel_name(rows, sb, rep.best)
-    assert rep.best_median_ns <= rep.default_median_ns
+    assert rep.confirm_best_ns > 0 and rep.confirm_default_ns > 0
+    if rep.kept_default:  # the default was fastest, or not beaten by more than 2 %
+        assert rep.best == rep.default
+    else:
+        assert rep.confirm_best_ns < 0.98 * rep.confirm_default_ns
     fams = {v.family for v in [rep.best, rep.default]}
     assert fams <= set(range(1, 8))
     # stored in the context's table: a call without a variant now runs the winner
@@ -84,12 +98,17 @@ def test_grid_search_over_every_family_at_c4(axc, tune):
     ref = O.q4k_matvec(q, x, rows, sb)
     yf, ad = O.q4k_matvec_f64(q, x, rows, sb)
     assert O.matvec_tolerance_report(y, ref, yf, ad, sb * 256)["ok"]
-    # timed again, independently of the search: no slower than the default by > 2 %
-    t_best = _median_us(c, lambda: c.q4k_matvec(dq, dx, dy, rows, sb, rep.best))
-    t_dflt = _median_us(c, lambda: c.q4k_matvec(dq, dx, dy, rows, sb, rep.default))
-    _say(f"re-timed: winner {rep.best_kernel} {t_best:.3f} us, default {t_dflt:.3f} us")
-    assert t_best <= 1.02 * t_dflt
-    for b in (dq, dx, dy):
+    # timed again, independently of the search, on rotated copies in interleaved
+    # rounds: no slower than the default beyond the run-to-run spread
+    wbuf, stride, n = _rotated(c, q)
+    base = dict(op="q4k", q=wbuf, q_stride=stride, n_copies=n, x=dx, y=dy, n_rows=rows,
+                units=sb)
+    med = _interleaved_us(c, {"best": dict(base, variant=rep.best),
+                              "default": dict(base, variant=rep.default)})
+    _say(f"re-timed: winner {rep.best_kernel} {med['best']:.3f} us, default "
+         f"{axc.q4k_matvec_kernel_name(rows, sb, rep.default)} {med['default']:.3f} us")
+    assert med["best"] <= SPREAD_MARGIN * med["default"], med
+    for b in (dq, dx, dy, wbuf):
         b.close()
     c.close()
 

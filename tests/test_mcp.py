@@ -78,18 +78,56 @@ def test_at_1119b_concurrent_writers_do_not_interleave(mcp, tmp_path):
 
 
 def test_variant_id_matches_the_enumerator(mcp, tune):
-    holes = mcp.default_holes("q4km_dequant_matvec")
-    assert set(holes) == {"rows_per_wave", "waves_per_workgroup", "prefetch", "nontemporal"}
-    for v in tune.enumerate_strategy(holes):
-        assert mcp.variant_id(v.assignments) == v.variant_id
+    spaces = mcp.default_holes("q4km_dequant_matvec", {"n_rows": 4096, "units_per_row": 56})
+    assert len(spaces) >= 3
+    for holes in spaces:
+        assert "family" in holes and len(holes["family"]) == 1
+        for v in tune.enumerate_strategy(holes):
+            assert mcp.variant_id(v.assignments) == v.variant_id
     assert mcp.variant_id({}) == 0
 
 
+def test_matvec_hole_space_is_the_autotuners_and_reaches_the_default(mcp, tune, axc):
+    """The tool searches the autotuner's per-family space (every family that
+    takes the shape, in family order), so the shipped default kernel of each
+    shape is one of its variants (a space of the persistent family's holes
+    alone cannot reach it)."""
+    for rows, sb in ((4096, 56), (4096, 16), (14336, 16), (1, 128), (3, 100), (128256, 16)):
+        shape = {"n_rows": rows, "units_per_row": sb}
+        spaces = mcp.default_holes("q4km_dequant_matvec", shape)
+        assert spaces == tune.q4k_matvec_hole_spaces(rows, sb)
+        fams = [h["family"][0] for h in spaces]
+        assert fams == sorted(fams) and axc.FAMILY_PERSISTENT in fams
+        vs = mcp._enumerate_spaces(spaces)
+        assert [v.ordinal for v in vs] == list(range(len(vs)))
+        d = axc.q4k_matvec_default_variant(rows, sb)
+        names = {axc.q4k_matvec_kernel_name(rows, sb, mcp._variant_obj("q4km_dequant_matvec",
+                                                                         v.assignments))
+                 for v in vs
+                 if _plans(axc, rows, sb, mcp._variant_obj("q4km_dequant_matvec", v.assignments))}
+        assert axc.q4k_matvec_kernel_name(rows, sb, d) in names, (rows, sb)
+        assert axc.q4k_matvec_kernel_name(rows, sb) in names
+
+
+def _plans(axc, rows, sb, v):
+    try:
+        axc.q4k_matvec_kernel_name(rows, sb, v)
+        return True
+    except axc.DispatchError:
+        return False
+
+
+def test_variant_objects_carry_every_hole(mcp, axc):
+    v = mcp._variant_obj("q4km_dequant_matvec", {"family": 2, "prefetch": 2, "sb_per_lane": 7})
+    assert v == axc.Variant(0, 0, 2, 0, 2, 7)
+    assert axc.q4k_matvec_kernel_name(4096, 56, v) == "axh_q4k_matvec_onep_i7"
+
+
 def test_default_hole_spaces_come_from_compiled_variants(mcp, axc):
-    h = mcp.default_holes("q4k_matmul_f16")
+    (h,) = mcp.default_holes("q4k_matmul_f16")
     assert set(h["kind"]) == {3, 5, 7, 8, 9}
     assert 0 in h["row_tiles"] and 4 in h["row_tiles"]
-    assert mcp.default_holes("q4_0_dequant_matvec")["waves_per_workgroup"] == [1, 4]
+    assert mcp.default_holes("q4_0_dequant_matvec")[0]["waves_per_workgroup"] == [1, 4]
 
 
 def test_seeded_inputs_are_deterministic_and_well_formed(mcp):
@@ -171,7 +209,7 @@ def test_jsonrpc_envelopes(mcp, tmp_path):
     assert r["error"]["code"] == mcp.INVALID_PARAMS
     r = mcp.handle_line(json.dumps({"jsonrpc": "2.0", "id": 5, "method": "enumerate_variants",
                                     "params": {"kernel": "q4_0_dequant_matvec"}}), ctx)
-    h = mcp.default_holes("q4_0_dequant_matvec")
+    (h,) = mcp.default_holes("q4_0_dequant_matvec")
     assert r["result"]["count"] == len(h["rows_per_wave"]) * len(h["waves_per_workgroup"])
     r = mcp.handle_line(json.dumps({"jsonrpc": "2.0", "id": 6, "method": "enumerate_variants",
                                     "params": {"kernel": "q4_0_dequant_matvec",
