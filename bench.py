@@ -150,7 +150,9 @@ class Case:
         stride = -(-self.q.nbytes // COPY_ALIGN) * COPY_ALIGN
         self.n_copies = max(2, -(-COPIES_MIN_BYTES // stride))
         self.stride = stride
-        self.wbuf = ctx.alloc(stride * self.n_copies)
+        # tail room of x's size: the weights-and-x read floor reads weight + x
+        # bytes from the last copy
+        self.wbuf = ctx.alloc(stride * self.n_copies + self.x.nbytes + COPY_ALIGN)
         one = np.zeros(stride, dtype=np.uint8)
         one[: self.q.nbytes] = self.q
         ctx.upload(self.wbuf, np.tile(one, self.n_copies))
@@ -368,6 +370,39 @@ def main() -> int:
     # loop right after the pre-warm's long burst runs a few % slower than the
     # loops that follow (clocks), and the timed loop is meant to be a typical one.
     REPEATS = 11
+    # Matvec workloads: the read kernel's launch-shape sweep that names the
+    # best single-launch read of the weights (for the floors below).  It runs
+    # before the pre-warm: after a burst of pure-read launches the matvec runs
+    # ~5 % slower until some milliseconds of matvec load have passed (measured:
+    # 7.73 -> 8.08-8.15 us per call at C4, back to 7.70 after ~5000 calls, not
+    # after 0.5 s idle), and the pre-warm supplies that load.
+    if kind != "matmul":
+        nb = case.weight_bytes // 16 * 16
+        fout = ctx.alloc(2048 * 1024 // 64 * 4)
+        words = 8 * ctx.cu_count()
+        per_round = max(20, args.steps)  # the headline's loop length
+
+        def floor_op(op, **kw):
+            return dict(op=op, q=case.wbuf, q_stride=case.stride, n_copies=case.n_copies, x=None,
+                        y=fout, units=nb // 16, **kw)
+
+        def shape_op(threads, loads, grid):
+            return floor_op("read_shape", n_rows=grid, batch=grid * threads // 64,
+                            variant=pkg.Variant(0, threads // 64, loads))
+
+        def us(op, calls):
+            return sum(ctx.bench_loop(**op, warmup=20, groups=1, calls_per_group=calls)) * 1e3 / calls
+
+        # The read kernel at every shape of 256/512/1024 threads, 2/4/8 16-byte
+        # loads in flight per lane and 256-2048 workgroups.
+        sweep = []
+        for threads in (256, 512, 1024):
+            for loads in (2, 4, 8):
+                for grid in (256, 512, 1024, 2048):
+                    sweep.append((us(shape_op(threads, loads, grid), args.steps), threads, loads,
+                                  grid))
+        sweep.sort()
+        _, bt, bl, bg = sweep[0]
     # Pre-warm, untimed: the same calls for at least 100 ms, so the clocks have
     # ramped up under load (a few warmup calls are a fraction of a millisecond,
     # and the first loop of a cold start runs ~10 % slower).
@@ -421,36 +456,10 @@ def main() -> int:
     # The floor of the launch-per-call protocol on this box, for matvec
     # workloads: the same number of bytes read from the same rotated copies by
     # a kernel of the same launch shape that only reads (one store per wave),
-    # the best of the read kernel's launch shapes, and an empty kernel, all
-    # launched by the same loop.
+    # the best of the read kernel's launch shapes (swept above), and an empty
+    # kernel, all launched by the same loop.
     floor = None
     if kind != "matmul":
-        nb = case.weight_bytes // 16 * 16
-        fout = ctx.alloc(2048 * 1024 // 64 * 4)
-        words = 8 * ctx.cu_count()
-        per_round = max(20, args.steps)  # the headline's loop length
-
-        def floor_op(op, **kw):
-            return dict(op=op, q=case.wbuf, q_stride=case.stride, n_copies=case.n_copies, x=None,
-                        y=fout, units=nb // 16, **kw)
-
-        def shape_op(threads, loads, grid):
-            return floor_op("read_shape", n_rows=grid, batch=grid * threads // 64,
-                            variant=pkg.Variant(0, threads // 64, loads))
-
-        def us(op, calls):
-            return sum(ctx.bench_loop(**op, warmup=20, groups=1, calls_per_group=calls)) * 1e3 / calls
-
-        # The read kernel at every shape of 256/512/1024 threads, 2/4/8 16-byte
-        # loads in flight per lane and 256-2048 workgroups.
-        sweep = []
-        for threads in (256, 512, 1024):
-            for loads in (2, 4, 8):
-                for grid in (256, 512, 1024, 2048):
-                    sweep.append((us(shape_op(threads, loads, grid), args.steps), threads, loads,
-                                  grid))
-        sweep.sort()
-        _, bt, bl, bg = sweep[0]
         # Ratios from interleaved rounds (the matvec, the read of its launch
         # shape, the best read shape, the empty kernel, one after another, each
         # max(20, K) back-to-back calls, the headline's loop length, 5 rounds),
@@ -458,24 +467,20 @@ def main() -> int:
         # between runs cancels.
         ops = {"matvec": case.bench_op(), "read": floor_op("read_floor", batch=words),
                "best": shape_op(bt, bl, bg), "empty": floor_op("launch_empty", batch=words)}
-        # The bytes a call cannot avoid are the weights and x: a read of both
-        # (weights + x contiguous per copy, copies rotated past 512 MiB; the
-        # contents do not matter to a read) at the best read shape.  For C1 and
-        # C2 x outweighs the weights (C2: 128 KiB of x, 18 KiB of weights).
+        # The bytes a call cannot avoid are the weights and x: a read of as
+        # many bytes (from the same rotated copies, starting at each copy; the
+        # contents do not matter to a read) at the best read shape.  For C1
+        # and C2 x outweighs the weights (C2: 128 KiB of x, 18 KiB of weights).
         nbx = (case.weight_bytes + case.x.nbytes + 15) // 16 * 16
-        xstride = -(-nbx // COPY_ALIGN) * COPY_ALIGN
-        xcopies = max(2, -(-COPIES_MIN_BYTES // xstride))
-        xbuf = ctx.alloc(xstride * xcopies)
-        ops["read_wx"] = dict(op="read_shape", q=xbuf, q_stride=xstride, n_copies=xcopies,
-                              x=None, y=fout, units=nbx // 16, n_rows=bg, batch=bg * bt // 64,
-                              variant=pkg.Variant(0, bt // 64, bl))
+        ops["read_wx"] = dict(op="read_shape", q=case.wbuf, q_stride=case.stride,
+                              n_copies=case.n_copies, x=None, y=fout, units=nbx // 16, n_rows=bg,
+                              batch=bg * bt // 64, variant=pkg.Variant(0, bt // 64, bl))
         rounds = {k: [] for k in ops}
         for _ in range(5):
             for k, op in ops.items():
                 rounds[k].append(us(op, per_round))
         med = {k: sorted(v)[len(v) // 2] for k, v in rounds.items()}
         fout.close()
-        xbuf.close()
         read_us, best_us, empty_us = med["read"], med["best"], med["empty"]
         floor = {
             "read_same_bytes_us": round(read_us, 3),
