@@ -936,20 +936,29 @@ __device__ __forceinline__ void q6k_stage_xc(float *xs, float *ss, uint32_t tid,
   }
 }
 
-// 16 bytes at byte offset `off`, which is only 2-byte aligned when the
-// superblock starts at 2 mod 4: one 16-byte load.  gfx950 code objects for
-// amdhsa run in unaligned-access mode (the compiler itself emits
-// global_load_dwordx4 at 2-byte-aligned addresses for such data), so this
-// replaces an aligned 16-byte load, a fifth dword and four v_alignbit.
-__device__ __forceinline__ uint4 q6k_load_run(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-
+// Dword-aligned loads of a superblock's runs.  A superblock starts at 0 or 2
+// mod 4 (210 = 2 mod 4), and every run starts at a multiple of 16 from it,
+// so all of a superblock's runs share one misalignment sh = start & 3 (0 or
+// 2).  A 16-byte load at a 2-mod-4 address is split by the memory pipeline:
+// with the decode and x reads taken out (timing-only copies), the 128256 x
+// 4096 head took 78.0 us with the runs loaded as they lie and 71.0 us with
+// their addresses rounded down to 4 bytes.  So each lane loads its three
+// 16-byte runs (ql low, ql high, qh) from run start - sh, and the dword that
+// completes a run is the first dword of another run of the same superblock:
+// with lane c = 2n + h of a lane quad holding half n, l in [16h, 16h + 16),
+//   ql low  (n, 0) <- ql low  (n, 1);  ql low  (n, 1) <- ql high (n, 0)
+//   ql high (n, 0) <- ql high (n, 1);  ql high (0, 1) <- ql low (1, 0);
+//   ql high (1, 1) <- qh (0, 0);       qh (n, h) <- qh of the next lane,
+//   qh (1, 1) <- the scale run's first dword (bytes 190..193),
+// fetched with a quad permute, and v_alignbyte shifts each run into place.
+// The lanes of half 0 load the 16 scale bytes from 192 - sh; the lanes of
+// half 1 need scale bytes 200..207, loaded from 192 (sh = 0) or 194 (sh = 2),
+// so that no load leaves the superblock (the d load stays a 2-byte load at
+// 208: a dword there would reach past the last superblock of the matrix).
 template <int RPW, int PF>
 struct Q6kFlatBuf {
   uint4 lo[PF][RPW], hi[PF][RPW], qh[PF][RPW], sc[PF][RPW];
-  uint32_t d[PF][RPW];
+  uint32_t d[PF][RPW], sh[PF][RPW]; // sh: the superblock's start & 3
 };
 
 template <int RPW, int PF>
@@ -961,12 +970,37 @@ __device__ __forceinline__ void q6k_flat_load(Q6kFlatBuf<RPW, PF> &B, int p,
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
     const uint32_t o = (bundle * RPW + (uint32_t)r) * row_bytes + (it * 8u + s) * kQ6kSbBytes;
-    B.lo[p][r] = q6k_load_run(qr, o + 64u * n + 16u * h);
-    B.hi[p][r] = q6k_load_run(qr, o + 64u * n + 32u + 16u * h);
-    B.qh[p][r] = q6k_load_run(qr, o + 128u + 32u * n + 16u * h);
-    B.sc[p][r] = q6k_load_run(qr, o + 192u);
+    const uint32_t sh = o & 3u, a = o - sh; // a: the dword-aligned start
+    const uint32_t sc_off = a + 192u + (n != 0u && sh != 0u ? 4u : 0u);
+    const u32x4_t lo = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(a + 64u * n + 16u * h), 0, 0);
+    const u32x4_t hi =
+        __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(a + 64u * n + 32u + 16u * h), 0, 0);
+    const u32x4_t qh =
+        __builtin_amdgcn_raw_buffer_load_b128(qr, (int)(a + 128u + 32u * n + 16u * h), 0, 0);
+    const u32x4_t sc = __builtin_amdgcn_raw_buffer_load_b128(qr, (int)sc_off, 0, 0);
+    B.lo[p][r] = make_uint4(lo.x, lo.y, lo.z, lo.w);
+    B.hi[p][r] = make_uint4(hi.x, hi.y, hi.z, hi.w);
+    B.qh[p][r] = make_uint4(qh.x, qh.y, qh.z, qh.w);
+    B.sc[p][r] = make_uint4(sc.x, sc.y, sc.z, sc.w);
     B.d[p][r] = __builtin_amdgcn_raw_buffer_load_b16(qr, (int)(o + 208u), 0, 0);
+    B.sh[p][r] = sh;
   }
+}
+
+__device__ __forceinline__ uint32_t quad_perm_u32_b1(uint32_t v) { // quad_perm [1,0,3,2]
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t quad_perm_u32_39(uint32_t v) { // quad_perm [1,2,3,0]
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x39, 0xF, 0xF, false);
+}
+
+// A run's four dwords from its dword-aligned load v and the next dword e,
+// shifted by sh bytes (sh = 0 returns v).
+__device__ __forceinline__ void q6k_align_run(uint4 v, uint32_t e, uint32_t sh, uint32_t (&w)[4]) {
+  w[0] = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
+  w[1] = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
+  w[2] = __builtin_amdgcn_alignbyte(v.w, v.z, sh);
+  w[3] = __builtin_amdgcn_alignbyte(e, v.w, sh);
 }
 
 // Four bytes of 6-bit values against four x (pre-scaled by 2^24).
@@ -1048,9 +1082,15 @@ __device__ __forceinline__ void q6k_matvec_flat(const uint8_t *__restrict__ q,
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {
           const uint4 lo = B.lo[p][r], hi = B.hi[p][r], qh = B.qh[p][r], sc = B.sc[p][r];
-          const uint32_t lw[4] = {lo.x, lo.y, lo.z, lo.w};
-          const uint32_t hw[4] = {hi.x, hi.y, hi.z, hi.w};
-          const uint32_t qw[4] = {qh.x, qh.y, qh.z, qh.w};
+          const uint32_t sh = B.sh[p][r];
+          // the dword after each run, from the lane of the quad that loaded it
+          const uint32_t lo_e = quad_perm_u32_b1((c & 1u) ? lo.x : hi.x);
+          const uint32_t hi_e = quad_perm_u32_39(c == 0u ? qh.x : c == 2u ? lo.x : hi.x);
+          const uint32_t qh_e = quad_perm_u32_39(c == 0u ? sc.x : qh.x);
+          uint32_t lw[4], hw[4], qw[4];
+          q6k_align_run(lo, lo_e, sh, lw);
+          q6k_align_run(hi, hi_e, sh, hw);
+          q6k_align_run(qh, qh_e, sh, qw);
           float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -1063,8 +1103,14 @@ __device__ __forceinline__ void q6k_matvec_flat(const uint8_t *__restrict__ q,
             d2 = q6k_bytes(v2, *reinterpret_cast<const float4 *>(xb + 128u + 16u * i), d2);
             d3 = q6k_bytes(v3, *reinterpret_cast<const float4 *>(xb + 192u + 16u * i), d3);
           }
-          // scale bytes 8n + h + {0, 2} (dword 2n) and 8n + h + {4, 6} (dword 2n + 1)
-          const uint32_t s0 = n ? sc.z : sc.x, s1 = n ? sc.w : sc.y;
+          // scale bytes 8n + h + {0, 2} (dword 2n) and 8n + h + {4, 6} (dword 2n + 1):
+          // dwords k, k + 1 of the scale load shifted by sh, k = 0 for half 0,
+          // 2 for half 1 at sh = 0 (loaded from 192), 1 at sh = 2 (from 194)
+          const uint32_t k0 = n ? (sh ? sc.y : sc.z) : sc.x;
+          const uint32_t k1 = n ? (sh ? sc.z : sc.w) : sc.y;
+          const uint32_t k2 = n ? sc.w : sc.z;
+          const uint32_t s0 = __builtin_amdgcn_alignbyte(k1, k0, sh);
+          const uint32_t s1 = __builtin_amdgcn_alignbyte(k2, k1, sh);
           // int8 scales (the sign-extending byte extract; a bit-field builtin
           // returning an unsigned type would turn -1 into 2^32 - 1 here)
           const float c0 = (float)(int8_t)(s0 >> hsel);
