@@ -720,9 +720,10 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
 // 4096 4.06 vs 4.62-4.92, 14336 x 4096 8.9-9.1 vs 9.9-10.5, 32768 x 4096 17.0
 // vs 18.6; the 128256-row head 56.8 vs 53.5 (persistent prefetch 2) stays
 // persistent.  The template also covers the fused gate/up (kDual) and Q5_K
-// (kQ5) layouts, but there it measured no faster than the persistent kernels
-// (2 x 14336 x 4096: 16.8 vs 16.8 us; Q5_K 14336 x 4096: 11.7 vs 11.3), so
-// only the Q4_K instances are built.
+// (kQ5) layouts.  The fused gate/up measured no faster than its persistent
+// kernel (2 x 14336 x 4096: 16.8 vs 16.8 us) and is not built; the Q5_K
+// instances for rows of up to 16 superblocks are (axh_q5k_matvec_one_i{NIT},
+// see the runtime's Q5_K kernel choice).
 //
 // kWhole (axh_q4k_matvec_onex_i{NIT}): x is staged whole first, behind one
 // barrier, with the first iteration's weights already requested, and the
@@ -841,6 +842,16 @@ AXH_Q4K_MATVEC_ONE(13)
 AXH_Q4K_MATVEC_ONE(14)
 AXH_Q4K_MATVEC_ONE(15)
 AXH_Q4K_MATVEC_ONE(16)
+
+#define AXH_Q5K_MATVEC_ONE(NIT)                                                                  \
+  extern "C" __global__ void __launch_bounds__(512)                                              \
+      axh_q5k_matvec_one_i##NIT(const uint8_t *__restrict__ q, const float *__restrict__ x,      \
+                                float *__restrict__ y, AXH_ROWS_ARGS) { AXH_ROWS_UNPACK; \
+    extern __shared__ float axh_lds_dyn[];                                                       \
+    q4k_matvec_one<NIT, false, true>(q, q, x, y, a.n_rows, a.units_per_row, axh_lds_dyn);        \
+  }
+AXH_Q5K_MATVEC_ONE(1)
+AXH_Q5K_MATVEC_ONE(2)
 
 #define AXH_Q4K_MATVEC_ONEP(NIT)                                                                 \
   extern "C" __global__ void __launch_bounds__(512)                                              \

@@ -189,7 +189,8 @@ static const MatvecVariant *find_variant(const MatvecVariant *table, size_t n,
 static axh_status reject_family(const axh_q4_variant *v) {
   if (v && (v->family || v->sb_per_lane))
     return fail(AXH_ERR_INVALID_ARGUMENT,
-                "family and sb_per_lane are holes of the Q4_K matvec only");
+                "family and sb_per_lane are holes of the Q4_K matvec (and sb_per_lane of the "
+                "Q5_K one-pass family) only");
   return AXH_OK;
 }
 
@@ -803,13 +804,48 @@ static MatvecVariant kq_default(const KqFormat &f, uint32_t nsb) {
   return {1, nw, early ? 1u : 2u, 2, 1};
 }
 
+// Q5_K rows of up to 16 superblocks over 2048 to 32768 rows take the
+// one-pass kernel (axh_q5k_matvec_one_i{NIT}: one workgroup per 16 rows, x
+// staged chunk by chunk, fully unrolled).  A/B in one run, 14336 x 4096:
+// 10.02-10.08 vs 10.56-10.70 us (plain launches, one weight copy per call
+// from 14 rotated copies), 10.71 vs 11.05 on another box, and 10.79-10.88 vs
+// 10.92-10.96 through the library's launch loop on a third; 4096 x 4096
+// 4.60 vs 4.70.  Not below 2048 rows (1024 x 4096: 3.95 vs 3.49) nor for
+// longer rows (4096 x 14336: even).  The family is also reachable as
+// variant->family = AXH_Q4K_FAMILY_ONE_PASS (hole: sb_per_lane, 1 or 2).
+constexpr uint32_t kQ5OneMinRows = 2048, kQ5OneMaxRows = 32768, kQ5OneMaxSb = 16;
+
 static axh_status plan_kq(const KqFormat &f, uint32_t n_rows, uint32_t sb_per_row,
                           const axh_q4_variant *variant, Q4kPlan *p) {
-  if (reject_family(variant) != AXH_OK) return AXH_ERR_INVALID_ARGUMENT;
+  const bool q5 = &f == &kQ5kFormat;
+  const uint32_t fam = variant ? variant->family : 0u;
+  const bool flat_holes = variant && (variant->rows_per_wave || variant->waves_per_workgroup ||
+                                      variant->prefetch || variant->nontemporal);
+  if (!(q5 && fam == AXH_Q4K_FAMILY_ONE_PASS) && reject_family(variant) != AXH_OK)
+    return AXH_ERR_INVALID_ARGUMENT;
   if (sb_per_row == 0 || sb_per_row > kQ4kFlatMaxSb)
     return fail(AXH_ERR_INVALID_ARGUMENT, "sb_per_row must be 1..128 for Q5_K / Q6_K");
   if ((uint64_t)n_rows * sb_per_row * f.sb_bytes >= 0xFFFFFFFFull)
     return fail(AXH_ERR_INVALID_ARGUMENT, "Q5_K / Q6_K matrices must be below 4 GiB");
+  if (q5 && (fam == AXH_Q4K_FAMILY_ONE_PASS ||
+             (!flat_holes && n_rows >= kQ5OneMinRows && n_rows <= kQ5OneMaxRows &&
+              sb_per_row <= kQ5OneMaxSb))) {
+    if (flat_holes)
+      return fail(AXH_ERR_INVALID_ARGUMENT, "the Q5_K one-pass family's only hole is sb_per_lane");
+    const uint32_t need = (sb_per_row + 7u) / 8u;
+    const uint32_t nit = variant && variant->sb_per_lane ? variant->sb_per_lane : need;
+    if (nit < need || nit > 2u)
+      return fail(AXH_ERR_INVALID_ARGUMENT,
+                  "Q5_K one-pass: sb_per_lane must cover the row and be 1 or 2 (rows of up to "
+                  "16 superblocks)");
+    std::snprintf(p->name, sizeof(p->name), "axh_q5k_matvec_one_i%u", nit);
+    p->nw = 8;
+    p->lds = sb_per_row * f.lds_per_sb;
+    p->flat = false; // one workgroup per 16 rows, all of them launched
+    p->units = (n_rows + 15u) / 16u;
+    p->args = RowsArgs{n_rows, sb_per_row, sb_per_row, 0};
+    return ok();
+  }
   if (variant && variant->nontemporal == 1)
     return fail(AXH_ERR_INVALID_ARGUMENT, "no non-temporal Q5_K / Q6_K variant is compiled");
   const MatvecVariant dflt = kq_default(f, sb_per_row);

@@ -200,8 +200,12 @@ void axh_event_destroy(axh_event *ev);
  * than 32 rows, one pass for 32-32768 rows of 1-128 superblocks (and up to
  * 65536 rows of at most 16; x staged whole from 6144 rows of at most 32
  * superblocks), persistent beyond, tiled for rows of more than 128
- * superblocks.  Every default is a hole assignment.  The Q4_0, Q5_K, Q6_K and
- * gate/up operations take the persistent holes only (family = sb_per_lane = 0). */
+ * superblocks.  Every default is a hole assignment.  The Q4_0, Q6_K and
+ * gate/up operations take the persistent holes only (family = sb_per_lane =
+ * 0).  Q5_K takes the persistent holes or family = AXH_Q4K_FAMILY_ONE_PASS
+ * with sb_per_lane 1 or 2 (rows of up to 16 superblocks); with no hole set it
+ * runs one pass for 2048-32768 rows of up to 16 superblocks, else the
+ * persistent family. */
 enum {
     AXH_Q4K_FAMILY_DEFAULT = 0,
     AXH_Q4K_FAMILY_PERSISTENT = 1, /* axh_q4k_matvec_flat_r*_w*_p*_n*[_x2]            */

@@ -125,6 +125,19 @@ def test_early_refill_several_pairs_per_wave(ctx, axc, kind):
         _check(y, kind, q, x, rows, sb, f"early refill {v}")
 
 
+@pytest.mark.parametrize("rows,sb,nit", [(1, 1, 1), (7, 3, 1), (33, 8, 2), (17, 9, 2),
+                                         (4097, 16, 2), (2048, 8, 1), (100, 16, 2)])
+def test_q5k_one_pass_family(ctx, axc, rows, sb, nit):
+    """The Q5_K one-pass kernel (the default for 2048-32768 rows of up to 16
+    superblocks) at ragged row counts, requested explicitly."""
+    q = O.gen_kq_weights(Q5, rows * 5 + sb, rows * sb)
+    x = O.gen_normal_f32(rows + 2 * sb, sb * 256)
+    v = axc.Variant(0, 0, 0, 0, axc.FAMILY_ONE_PASS, nit)
+    _say(f"kquant Q5_K one-pass {rows}x{sb} i{nit}")
+    y = _matvec(ctx, Q5, q, x, rows, sb, v)
+    _check(y, Q5, q, x, rows, sb, f"one-pass {rows}x{sb} i{nit}")
+
+
 def test_one_hot_x_reads_single_weights(ctx):
     """x = e_k picks column k: y = W[:, k] exactly (exact products, one term;
     compared as values: a zero Q6_K weight with a negative scale is -0.0 in
