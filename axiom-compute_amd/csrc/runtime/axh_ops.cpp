@@ -809,8 +809,9 @@ static MatvecVariant kq_default(const KqFormat &f, uint32_t nsb) {
 // staged chunk by chunk, fully unrolled).  A/B in one run, 14336 x 4096:
 // 10.02-10.08 vs 10.56-10.70 us (plain launches, one weight copy per call
 // from 14 rotated copies), 10.71 vs 11.05 on another box, and 10.79-10.88 vs
-// 10.92-10.96 through the library's launch loop on a third; 4096 x 4096
-// 4.60 vs 4.70.  Not below 2048 rows (1024 x 4096: 3.95 vs 3.49) nor for
+// 10.92-10.96 through the library's launch loop on a third, and even in the
+// kernel trace on a fourth (10.85-10.90 vs 10.84-10.88); 4096 x 4096 4.60 vs
+// 4.70.  Not below 2048 rows (1024 x 4096: 3.95 vs 3.49) nor for
 // longer rows (4096 x 14336: even).  The family is also reachable as
 // variant->family = AXH_Q4K_FAMILY_ONE_PASS (hole: sb_per_lane, 1 or 2).
 constexpr uint32_t kQ5OneMinRows = 2048, kQ5OneMaxRows = 32768, kQ5OneMaxSb = 16;
