@@ -1045,49 +1045,56 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
     QB[slot] = bload16(qr, off == kOob ? kOob : off + 32u + 32u * g);
   };
   // X fragments of the wave's superblocks (column group c, column r, k-block g
-  // of step t), staged per column group through a wave-private LDS region of
-  // 16 * 512 * SPW bytes (all regions within the first 128 KiB of LDS) by
-  // coalesced direct-to-LDS loads: instruction (pc, n) copies 1 KiB of column
-  // n (two superblocks of k), lane l taking 16-byte piece l ^ n, so that the
-  // 16 lanes of a fragment read (columns 0..15, same piece) hit 16 different
-  // bank groups.  Then each lane reads its 8 * SPW fragments into VGPRs.
-  static_assert(NW * SPW <= 16, "X staging: NW * SPW * 8 KiB must fit 128 KiB");
+  // of step t), staged one superblock at a time through the wave-private LDS
+  // region (all regions within the first 128 KiB of LDS) by coalesced
+  // direct-to-LDS loads: instruction (c, m) copies superblock j's 512 bytes of
+  // columns n = 2m and 2m + 1 of group c, lane l taking 16-byte piece
+  // (l & 31) ^ n of column 2m + l / 32, so that the 16 lanes of a fragment
+  // (columns 0..15, same piece) hit 16 different bank groups.  Superblock 0's
+  // X is requested first and the first step's weights after it, so that the
+  // X wait does not queue behind the weights (loads return in order); its
+  // fragments go to VGPRs, then superblock 1's X is requested and lands
+  // during the first step, and its fragments are read before the first step
+  // that needs them (the half block reads them too).
+  static_assert(SPW == 2, "X staged one superblock at a time, two per wave");
+  static_assert(NW * NC * kXc * 512u <= 131072u, "X staging fits 128 KiB");
   half8_t xf[NC][SPW][8];
-  {
-    typedef __attribute__((address_space(3))) void lds_void_t;
-    constexpr uint32_t kColB = 512u * SPW; // staged bytes per column
-    uint8_t *xs = reinterpret_cast<uint8_t *>(red) + wave * kXc * kColB;
-    const uint32_t rr = r & (kXc - 1u);   // the lane's column within its group
-    issue(0u, 0, 0); // the first step's weights, in flight during the X staging
+  typedef __attribute__((address_space(3))) void lds_void_t;
+  uint8_t *const xs = reinterpret_cast<uint8_t *>(red) + wave * (kRegion * 16u);
+  const uint32_t rr = r & (kXc - 1u); // the lane's column within its group
+  auto stage = [&](int j) {
+    const uint32_t sj = wave * SPW + (uint32_t)j;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      // the previous group's fragment reads are done before the region is refilled
-      if (c > 0) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
-      for (int pc = 0; pc < SPW / 2; ++pc)
+      for (int m = 0; m < (int)kXc / 2; ++m) {
+        const uint32_t n = 2u * (uint32_t)m + (lane >> 5), col = n0 + kXc * (uint32_t)c + n;
+        const uint32_t piece = (lane & 31u) ^ n;
+        const uint32_t off = (col < batch && sj < nsb) ? (col * K + 256u * sj) * 2u + 16u * piece : kOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            xr, (lds_void_t *)(xs + (kXc * (uint32_t)c + 2u * (uint32_t)m) * 512u), 16, off, 0, 0, 0);
+      }
+  };
+  auto read_frags = [&](int j) {
 #pragma unroll
-        for (int n = 0; n < (int)kXc; ++n) {
-          const uint32_t col = n0 + kXc * (uint32_t)c + (uint32_t)n;
-          const uint32_t s0 = wave * SPW + 2u * (uint32_t)pc;
-          const uint32_t piece = lane ^ (uint32_t)n, sl = s0 + (piece >> 5);
-          const uint32_t off =
-              (col < batch && sl < nsb) ? (col * K + 256u * s0) * 2u + 16u * piece : kOob;
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              xr, (lds_void_t *)(xs + (uint32_t)n * kColB + 1024u * (uint32_t)pc), 16, off, 0, 0,
-              0);
-        }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // every X piece is in LDS
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
-      for (int j = 0; j < SPW; ++j)
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          const uint32_t P = 32u * (uint32_t)j + 8u * g + (uint32_t)t; // 16-byte piece of the wave's k
-          const uint32_t addr = rr * kColB + 1024u * (P >> 6) + 16u * ((P & 63u) ^ rr);
-          const half8_t v = *reinterpret_cast<const half8_t *>(xs + addr);
-          xf[c][j][t] = (!XH || r < 8u) ? v : (half8_t){};
-        }
-    }
-  }
+      for (int t = 0; t < 8; ++t) {
+        const uint32_t P = 8u * g + (uint32_t)t; // 16-byte piece of the superblock
+        const uint32_t addr = (kXc * (uint32_t)c + rr) * 512u + 16u * (P ^ rr);
+        const half8_t v = *reinterpret_cast<const half8_t *>(xs + addr);
+        xf[c][j][t] = (!XH || r < 8u) ? v : (half8_t){};
+      }
+  };
+  stage(0);
+  __builtin_amdgcn_sched_barrier(0);
+  issue(0u, 0, 0); // the first step's weights
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); // superblock 0's X is in LDS
+  read_frags(0);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); // read before the region is refilled
+  stage(1);
+  bool x1_pending = true; // superblock 1's fragments not yet in VGPRs
   // Sums the partial tiles of blocks kb .. kb + nb - 1 (and of the half
   // block after them) over the waves, in wave order, and stores them; slot tt
   // of every region (block kb + tt / NC, column group tt % NC) is summed by
@@ -1127,6 +1134,13 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
       if (j + 1 < SPW) issue(k, j + 1, slot ^ 1);
       else issue(k + 1u, 0, slot ^ 1);
       __builtin_amdgcn_sched_barrier(0);
+      if (j == 1 && x1_pending) {
+        // superblock 1's X landed: at most the 3 weight loads just issued
+        // remain (this step's own weights, issued before them, are needed now)
+        asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+        read_frags(1);
+        x1_pending = false;
+      }
       const uint4 hd = H[slot];
       const float d = f16_to_f32(hd.x & 0xFFFFu), dmin = f16_to_f32(hd.x >> 16);
       uint32_t scp, mp;
@@ -1162,6 +1176,10 @@ __device__ __forceinline__ void q4k_matmul_sr(const uint8_t *__restrict__ q,
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); // slots read before reuse
       kb = k + 1u;
     }
+  }
+  if (x1_pending) { // no full block: superblock 1's X for the half block (or nothing)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    read_frags(1);
   }
   if (half) { // its loads were issued into slot 0 with the last full block's
     const uint32_t k = n_myb;
