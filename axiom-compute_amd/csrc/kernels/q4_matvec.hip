@@ -1024,6 +1024,88 @@ __device__ __forceinline__ float q6k_bytes(uint32_t v, float4 x, float acc) {
   return acc;
 }
 
+// One iteration of the Q6_K kernels for the RPW rows of slot p: lane quad s
+// holds superblock sb, lane c of it half n = c / 2 and l in [16(c & 1),
+// 16(c & 1) + 16).  acc[r] += this lane's share of row r.  The quad permutes
+// read the other lanes of the quad, which take the same branch (same sb).
+template <int RPW, int NS>
+__device__ __forceinline__ void q6k_flat_compute(const Q6kFlatBuf<RPW, NS> &B, int p,
+                                                 const float *xs, const float *ss, uint32_t sb,
+                                                 uint32_t c, float (&acc)[RPW]) {
+  const uint32_t n = c >> 1, hsel = (c & 1u) * 8u; // scale byte of (n, h): 8n + 2p + h
+  const float *xb = xs + sb * kQ6kSbFloats + 4u * c;
+  const float4 sums = *reinterpret_cast<const float4 *>(ss + sb * 16u + 4u * c);
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const uint4 lo = B.lo[p][r], hi = B.hi[p][r], qh = B.qh[p][r], sc = B.sc[p][r];
+    const uint32_t sh = B.sh[p][r];
+    // the dword after each run, from the lane of the quad that loaded it
+    const uint32_t lo_e = quad_perm_u32_b1((c & 1u) ? lo.x : hi.x);
+    const uint32_t hi_e = quad_perm_u32_39(c == 0u ? qh.x : c == 2u ? lo.x : hi.x);
+    const uint32_t qh_e = quad_perm_u32_39(c == 0u ? sc.x : qh.x);
+    uint32_t lw[4], hw[4], qw[4];
+    q6k_align_run(lo, lo_e, sh, lw);
+    q6k_align_run(hi, hi_e, sh, hw);
+    q6k_align_run(qh, qh_e, sh, qw);
+    float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t v0 = (lw[i] & 0x0F0F0F0Fu) | ((qw[i] << 4) & 0x30303030u);
+      const uint32_t v1 = (hw[i] & 0x0F0F0F0Fu) | ((qw[i] << 2) & 0x30303030u);
+      const uint32_t v2 = ((lw[i] >> 4) & 0x0F0F0F0Fu) | (qw[i] & 0x30303030u);
+      const uint32_t v3 = ((hw[i] >> 4) & 0x0F0F0F0Fu) | ((qw[i] >> 2) & 0x30303030u);
+      d0 = q6k_bytes(v0, *reinterpret_cast<const float4 *>(xb + 16u * i), d0);
+      d1 = q6k_bytes(v1, *reinterpret_cast<const float4 *>(xb + 64u + 16u * i), d1);
+      d2 = q6k_bytes(v2, *reinterpret_cast<const float4 *>(xb + 128u + 16u * i), d2);
+      d3 = q6k_bytes(v3, *reinterpret_cast<const float4 *>(xb + 192u + 16u * i), d3);
+    }
+    // scale bytes 8n + h + {0, 2} (dword 2n) and 8n + h + {4, 6} (dword 2n + 1):
+    // dwords k, k + 1 of the scale load shifted by sh, k = 0 for half 0,
+    // 2 for half 1 at sh = 0 (loaded from 192), 1 at sh = 2 (from 194)
+    const uint32_t k0 = n ? (sh ? sc.y : sc.z) : sc.x;
+    const uint32_t k1 = n ? (sh ? sc.z : sc.w) : sc.y;
+    const uint32_t k2 = n ? sc.w : sc.z;
+    const uint32_t s0 = __builtin_amdgcn_alignbyte(k1, k0, sh);
+    const uint32_t s1 = __builtin_amdgcn_alignbyte(k2, k1, sh);
+    // int8 scales (the sign-extending byte extract; a bit-field builtin
+    // returning an unsigned type would turn -1 into 2^32 - 1 here)
+    const float c0 = (float)(int8_t)(s0 >> hsel);
+    const float c1 = (float)(int8_t)(s0 >> (hsel + 16u));
+    const float c2 = (float)(int8_t)(s1 >> hsel);
+    const float c3 = (float)(int8_t)(s1 >> (hsel + 16u));
+    float t = c0 * __builtin_fmaf(-32.0f, sums.x, d0);
+    t = __builtin_fmaf(c1, __builtin_fmaf(-32.0f, sums.y, d1), t);
+    t = __builtin_fmaf(c2, __builtin_fmaf(-32.0f, sums.z, d2), t);
+    t = __builtin_fmaf(c3, __builtin_fmaf(-32.0f, sums.w, d3), t);
+    acc[r] = __builtin_fmaf(f16_to_f32(B.d[p][r]), t, acc[r]);
+  }
+}
+
+// Reduce the pair of bundles (bundle0, bundle0 + 1) a wave finished (each
+// half-wave's lanes hold one bundle's partial sums) and store it.
+template <int RPW>
+__device__ __forceinline__ void q6k_flat_store(float (&acc)[RPW], uint32_t bundle0, uint32_t lane,
+                                               uint32_t n_rows, float *__restrict__ y) {
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    float v = acc[r];
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x141>(v);
+    v += dpp_mov<0x140>(v);
+    const int vi = __builtin_bit_cast(int, v);
+    const float h0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 0)) +
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 16));
+    const float h1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 32)) +
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 48));
+    const uint32_t r0 = bundle0 * RPW + (uint32_t)r;
+    const uint32_t r1 = (bundle0 + 1u) * RPW + (uint32_t)r;
+    if (lane == 0 && r0 < n_rows) y[r0] = h0;
+    if (lane == 0 && r1 < n_rows) y[r1] = h1;
+    acc[r] = 0.0f;
+  }
+}
+
 template <int RPW, int NW, int PF, int XP>
 __device__ __forceinline__ void q6k_matvec_flat(const uint8_t *__restrict__ q,
                                                 const float *__restrict__ x,
@@ -1073,7 +1155,6 @@ __device__ __forceinline__ void q6k_matvec_flat(const uint8_t *__restrict__ q,
   q6k_stage_xc<NW * 64, XP>(xs, ss, tid, nsb, xv);
   __syncthreads();
 
-  const uint32_t n = c >> 1, hsel = (c & 1u) * 8u; // scale byte of (n, h): 8n + 2p + h
   float acc[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
@@ -1087,81 +1168,14 @@ __device__ __forceinline__ void q6k_matvec_flat(const uint8_t *__restrict__ q,
         if (++l_it == n_it) { l_it = 0; ++l_pi; }
       }
       const uint32_t sb = c_it * 8u + s;
-      if (c_pi < n_my && sb < nsb) {
-        const float *xb = xs + sb * kQ6kSbFloats + 4u * c;
-        const float4 sums = *reinterpret_cast<const float4 *>(ss + sb * 16u + 4u * c);
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-          const uint4 lo = B.lo[p][r], hi = B.hi[p][r], qh = B.qh[p][r], sc = B.sc[p][r];
-          const uint32_t sh = B.sh[p][r];
-          // the dword after each run, from the lane of the quad that loaded it
-          const uint32_t lo_e = quad_perm_u32_b1((c & 1u) ? lo.x : hi.x);
-          const uint32_t hi_e = quad_perm_u32_39(c == 0u ? qh.x : c == 2u ? lo.x : hi.x);
-          const uint32_t qh_e = quad_perm_u32_39(c == 0u ? sc.x : qh.x);
-          uint32_t lw[4], hw[4], qw[4];
-          q6k_align_run(lo, lo_e, sh, lw);
-          q6k_align_run(hi, hi_e, sh, hw);
-          q6k_align_run(qh, qh_e, sh, qw);
-          float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint32_t v0 = (lw[i] & 0x0F0F0F0Fu) | ((qw[i] << 4) & 0x30303030u);
-            const uint32_t v1 = (hw[i] & 0x0F0F0F0Fu) | ((qw[i] << 2) & 0x30303030u);
-            const uint32_t v2 = ((lw[i] >> 4) & 0x0F0F0F0Fu) | (qw[i] & 0x30303030u);
-            const uint32_t v3 = ((hw[i] >> 4) & 0x0F0F0F0Fu) | ((qw[i] >> 2) & 0x30303030u);
-            d0 = q6k_bytes(v0, *reinterpret_cast<const float4 *>(xb + 16u * i), d0);
-            d1 = q6k_bytes(v1, *reinterpret_cast<const float4 *>(xb + 64u + 16u * i), d1);
-            d2 = q6k_bytes(v2, *reinterpret_cast<const float4 *>(xb + 128u + 16u * i), d2);
-            d3 = q6k_bytes(v3, *reinterpret_cast<const float4 *>(xb + 192u + 16u * i), d3);
-          }
-          // scale bytes 8n + h + {0, 2} (dword 2n) and 8n + h + {4, 6} (dword 2n + 1):
-          // dwords k, k + 1 of the scale load shifted by sh, k = 0 for half 0,
-          // 2 for half 1 at sh = 0 (loaded from 192), 1 at sh = 2 (from 194)
-          const uint32_t k0 = n ? (sh ? sc.y : sc.z) : sc.x;
-          const uint32_t k1 = n ? (sh ? sc.z : sc.w) : sc.y;
-          const uint32_t k2 = n ? sc.w : sc.z;
-          const uint32_t s0 = __builtin_amdgcn_alignbyte(k1, k0, sh);
-          const uint32_t s1 = __builtin_amdgcn_alignbyte(k2, k1, sh);
-          // int8 scales (the sign-extending byte extract; a bit-field builtin
-          // returning an unsigned type would turn -1 into 2^32 - 1 here)
-          const float c0 = (float)(int8_t)(s0 >> hsel);
-          const float c1 = (float)(int8_t)(s0 >> (hsel + 16u));
-          const float c2 = (float)(int8_t)(s1 >> hsel);
-          const float c3 = (float)(int8_t)(s1 >> (hsel + 16u));
-          float t = c0 * __builtin_fmaf(-32.0f, sums.x, d0);
-          t = __builtin_fmaf(c1, __builtin_fmaf(-32.0f, sums.y, d1), t);
-          t = __builtin_fmaf(c2, __builtin_fmaf(-32.0f, sums.z, d2), t);
-          t = __builtin_fmaf(c3, __builtin_fmaf(-32.0f, sums.w, d3), t);
-          acc[r] = __builtin_fmaf(f16_to_f32(B.d[p][r]), t, acc[r]);
-        }
-      }
+      if (c_pi < n_my && sb < nsb) q6k_flat_compute<RPW, kSlots>(B, p, xs, ss, sb, c, acc);
       if constexpr (!kEarly) {
         const uint32_t bundle = 2u * (W + l_pi * total_waves) + half;
         q6k_flat_load<RPW, kSlots>(B, p, qr, row_bytes, bundle, l_it, s, c);
         if (++l_it == n_it) { l_it = 0; ++l_pi; }
       }
       if (++c_it == n_it) {
-        if (c_pi < n_my) {
-          const uint32_t bundle0 = 2u * (W + c_pi * total_waves);
-#pragma unroll
-          for (int r = 0; r < RPW; ++r) {
-            float v = acc[r];
-            v += dpp_mov<0xB1>(v);
-            v += dpp_mov<0x4E>(v);
-            v += dpp_mov<0x141>(v);
-            v += dpp_mov<0x140>(v);
-            const int vi = __builtin_bit_cast(int, v);
-            const float h0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 0)) +
-                             __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 16));
-            const float h1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 32)) +
-                             __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 48));
-            const uint32_t r0 = bundle0 * RPW + (uint32_t)r;
-            const uint32_t r1 = (bundle0 + 1u) * RPW + (uint32_t)r;
-            if (lane == 0 && r0 < n_rows) y[r0] = h0;
-            if (lane == 0 && r1 < n_rows) y[r1] = h1;
-            acc[r] = 0.0f;
-          }
-        }
+        if (c_pi < n_my) q6k_flat_store<RPW>(acc, 2u * (W + c_pi * total_waves), lane, n_rows, y);
         c_it = 0;
         ++c_pi;
       }
@@ -1204,6 +1218,94 @@ AXH_Q6K_MATVEC_FLAT(1, 4, 4, 1)
 AXH_Q6K_MATVEC_FLAT(2, 4, 2, 1)
 AXH_Q6K_MATVEC_FLAT(1, 4, 2, 2)
 AXH_Q6K_MATVEC_FLAT(1, 8, 2, 2)
+
+// x chunk j of the Q6_K one-pass kernel: superblocks [8j, 8j + 8), float4 f
+// = 512j + tid + i*NT, staged with the mapping and layout of q6k_stage_xc.
+// Chunks past the row read zeros (buffer range) and stage nothing.
+template <int NT>
+__device__ __forceinline__ void q6k_stage_chunk(float *xs, float *ss, uint32_t tid, uint32_t j,
+                                                uint32_t nsb, const float4 (&v)[512 / NT]) {
+#pragma unroll
+  for (int i = 0; i < 512 / NT; ++i) {
+    const uint32_t f = j * 512u + tid + (uint32_t)i * NT;
+    const float4 a = v[i];
+    float sm = (a.x + a.y) + (a.z + a.w);
+    sm += dpp_mov<0xB1>(sm);
+    sm += dpp_mov<0x4E>(sm);
+    if (f < nsb * 64u) {
+      const uint32_t sb = f >> 6, w = f & 63u;
+      const uint32_t n = w >> 5, p = (w >> 3) & 3u, h = (w >> 2) & 1u, i4 = w & 3u;
+      const uint32_t c = 2u * n + h;
+      *reinterpret_cast<float4 *>(xs + sb * kQ6kSbFloats + 64u * p + 4u * c + 16u * i4) =
+          make_float4(a.x * 16777216.0f, a.y * 16777216.0f, a.z * 16777216.0f,
+                      a.w * 16777216.0f);
+      if (i4 == 0u) ss[sb * 16u + 4u * c + p] = sm;
+    }
+  }
+}
+
+// Q6_K one pass, one pair of rows per wave (axh_q6k_matvec_one_i{NIT}): rows
+// of 8 * (NIT - 1) < nsb <= 8 * NIT superblocks, 8 waves per workgroup, wave
+// W takes rows 2W and 2W + 1, one workgroup per 16 rows, all launched.  The
+// Q4_K one-pass order (q4k_matvec_one) with the Q6_K loads and decode of the
+// persistent kernel, so its output equals the persistent kernel's bit for
+// bit: x staged chunk by chunk (8 superblocks, 8 KiB) with the next
+// iteration's weights in flight, fully unrolled, one barrier per iteration.
+// Every chunk has its own LDS region (nsb * 1152 bytes in all), so a chunk is
+// never overwritten while a wave still reads it.  XD = 2 (x two chunks
+// ahead) and longer rows measured even with the persistent kernel (4096 x
+// 14336, seven iterations: 11.80-11.85 vs 11.87 us) and are not built.
+template <int NIT, int XD>
+__device__ __forceinline__ void q6k_matvec_one(const uint8_t *__restrict__ q,
+                                               const float *__restrict__ x, float *__restrict__ y,
+                                               uint32_t n_rows, uint32_t nsb, float *lds) {
+  constexpr int NW = 8, NT = NW * 64;
+  static_assert(XD == 1 || XD == 2, "x one or two chunks ahead");
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t G = lane >> 2, half = G >> 3, s = G & 7u, c = lane & 3u;
+  const uint32_t W = blockIdx.x * NW + wave;
+  const bool mine = W < (n_rows + 1u) >> 1; // this wave has a pair of rows
+  // The host guarantees n_rows * row_bytes < 2^32 for this kernel.
+  const uint32_t row_bytes = nsb * kQ6kSbBytes;
+  const __amdgpu_buffer_rsrc_t qr = make_rsrc(q, n_rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, nsb * 1024u);
+  float *xs = lds;
+  float *ss = lds + nsb * kQ6kSbFloats;
+  const uint32_t bundle = 2u * W + half;
+  Q6kFlatBuf<1, 2> B;
+  float acc[1] = {0.0f};
+  constexpr int XB = XD + 1;
+  float4 xq[XB][512 / NT];
+  q4k_flat_load_chunk<NT>(xr, tid, 0u, xq[0]);
+  q6k_flat_load<1, 2>(B, 0, qr, row_bytes, bundle, 0u, s, c);
+#pragma unroll
+  for (int k = 1; k < XD; ++k) q4k_flat_load_chunk<NT>(xr, tid, (uint32_t)k, xq[k]);
+#pragma unroll
+  for (int j = 0; j < NIT; ++j) {
+    const int p = j & 1;
+    q6k_stage_chunk<NT>(xs, ss, tid, (uint32_t)j, nsb, xq[j % XB]);
+    if (j + XD < NIT) q4k_flat_load_chunk<NT>(xr, tid, (uint32_t)(j + XD), xq[(j + XD) % XB]);
+    if (j + 1 < NIT) // next iteration's weights, before the compute
+      q6k_flat_load<1, 2>(B, p ^ 1, qr, row_bytes, bundle, (uint32_t)(j + 1), s, c);
+    __syncthreads();
+    const uint32_t sb = (uint32_t)j * 8u + s;
+    if (mine && sb < nsb) q6k_flat_compute<1, 2>(B, p, xs, ss, sb, c, acc);
+  }
+  if (mine) q6k_flat_store<1>(acc, 2u * W, lane, n_rows, y);
+}
+
+#define AXH_Q6K_MATVEC_ONE(NIT, XD, TAG)                                                         \
+  extern "C" __global__ void __launch_bounds__(512)                                              \
+      axh_q6k_matvec_one##TAG##_i##NIT(const uint8_t *__restrict__ q,                            \
+                                       const float *__restrict__ x, float *__restrict__ y,       \
+                                       AXH_ROWS_ARGS) { AXH_ROWS_UNPACK;                         \
+    extern __shared__ float axh_lds_dyn[];                                                       \
+    q6k_matvec_one<NIT, XD>(q, x, y, a.n_rows, a.units_per_row, axh_lds_dyn);                    \
+  }
+AXH_Q6K_MATVEC_ONE(1, 1, )
+AXH_Q6K_MATVEC_ONE(2, 1, )
 
 // Fused SwiGLU gate/up projection: y[r] = silu(Wg[r].x) * (Wu[r].x), ROWS
 // output rows per bundle (2 * ROWS weight rows per lane group).

@@ -190,7 +190,7 @@ static axh_status reject_family(const axh_q4_variant *v) {
   if (v && (v->family || v->sb_per_lane))
     return fail(AXH_ERR_INVALID_ARGUMENT,
                 "family and sb_per_lane are holes of the Q4_K matvec (and sb_per_lane of the "
-                "Q5_K one-pass family) only");
+                "Q5_K / Q6_K one-pass family) only");
   return AXH_OK;
 }
 
@@ -778,19 +778,20 @@ axh_status axh_q4k_gate_up(axh_context *ctx, const void *q_gate, const void *q_u
   return s == AXH_OK ? ok() : s;
 }
 
-// ---- Q5_K / Q6_K (persistent kernel only: a row's x must fit LDS) ----------
+// ---- Q5_K / Q6_K (persistent kernels; one-pass kernels for short rows) -----
 struct KqFormat {
   const char *prefix;            // kernel name prefix
+  const char *one_prefix;        // the one-pass kernels' name prefix
   const MatvecVariant *table;
   size_t n;
   uint32_t sb_bytes, lds_per_sb; // superblock bytes, LDS bytes per superblock of x
   bool chunked_early;            // prefetch-1 kernels stage x in chunks (any row fits)
 };
 
-static const KqFormat kQ5kFormat{"axh_q5k_matvec_flat", kQ5kVariants,
+static const KqFormat kQ5kFormat{"axh_q5k_matvec_flat", "axh_q5k_matvec_one", kQ5kVariants,
                                  sizeof(kQ5kVariants) / sizeof(kQ5kVariants[0]), 176u, 1120u,
                                  true};
-static const KqFormat kQ6kFormat{"axh_q6k_matvec_flat", kQ6kVariants,
+static const KqFormat kQ6kFormat{"axh_q6k_matvec_flat", "axh_q6k_matvec_one", kQ6kVariants,
                                  sizeof(kQ6kVariants) / sizeof(kQ6kVariants[0]), 210u, 1152u,
                                  false};
 
@@ -814,7 +815,16 @@ static MatvecVariant kq_default(const KqFormat &f, uint32_t nsb) {
 // 4.70.  Not below 2048 rows (1024 x 4096: 3.95 vs 3.49) nor for
 // longer rows (4096 x 14336: even).  The family is also reachable as
 // variant->family = AXH_Q4K_FAMILY_ONE_PASS (hole: sb_per_lane, 1 or 2).
-constexpr uint32_t kQ5OneMinRows = 2048, kQ5OneMaxRows = 32768, kQ5OneMaxSb = 16;
+constexpr uint32_t kQ5OneMinRows = 2048, kQ5OneMaxRows = 32768, kKqOneMaxSb = 16;
+
+// Q6_K rows of up to 16 superblocks over 256 to 4096 rows (at most one
+// workgroup per CU) take the one-pass kernel too (axh_q6k_matvec_one_i{NIT}).
+// A/B in one run, us per call through the library's launch loop, one-pass vs
+// persistent: 256 x 4096 4.05 vs 4.74, 512 x 4096 4.56 vs 4.65, 1024 x 4096
+// 4.62 vs 4.85, 2048 x 4096 4.85 vs 5.00, 4096 x 4096 5.44 vs 5.90, 4096 x
+// 3072 5.21 vs 5.38, 4096 x 2048 3.72 vs 4.30, 1024 x 2048 3.24 vs 4.08; but
+// 6144 x 4096 7.28 vs 6.91 and 14336 x 4096 12.08 vs 11.95.
+constexpr uint32_t kQ6OneMinRows = 256, kQ6OneMaxRows = 4096;
 
 static axh_status plan_kq(const KqFormat &f, uint32_t n_rows, uint32_t sb_per_row,
                           const axh_q4_variant *variant, Q4kPlan *p) {
@@ -822,24 +832,26 @@ static axh_status plan_kq(const KqFormat &f, uint32_t n_rows, uint32_t sb_per_ro
   const uint32_t fam = variant ? variant->family : 0u;
   const bool flat_holes = variant && (variant->rows_per_wave || variant->waves_per_workgroup ||
                                       variant->prefetch || variant->nontemporal);
-  if (!(q5 && fam == AXH_Q4K_FAMILY_ONE_PASS) && reject_family(variant) != AXH_OK)
+  if (fam != AXH_Q4K_FAMILY_ONE_PASS && reject_family(variant) != AXH_OK)
     return AXH_ERR_INVALID_ARGUMENT;
   if (sb_per_row == 0 || sb_per_row > kQ4kFlatMaxSb)
     return fail(AXH_ERR_INVALID_ARGUMENT, "sb_per_row must be 1..128 for Q5_K / Q6_K");
   if ((uint64_t)n_rows * sb_per_row * f.sb_bytes >= 0xFFFFFFFFull)
     return fail(AXH_ERR_INVALID_ARGUMENT, "Q5_K / Q6_K matrices must be below 4 GiB");
-  if (q5 && (fam == AXH_Q4K_FAMILY_ONE_PASS ||
-             (!flat_holes && n_rows >= kQ5OneMinRows && n_rows <= kQ5OneMaxRows &&
-              sb_per_row <= kQ5OneMaxSb))) {
+  const uint32_t one_min = q5 ? kQ5OneMinRows : kQ6OneMinRows;
+  const uint32_t one_max = q5 ? kQ5OneMaxRows : kQ6OneMaxRows;
+  if (fam == AXH_Q4K_FAMILY_ONE_PASS ||
+      (!flat_holes && n_rows >= one_min && n_rows <= one_max && sb_per_row <= kKqOneMaxSb)) {
     if (flat_holes)
-      return fail(AXH_ERR_INVALID_ARGUMENT, "the Q5_K one-pass family's only hole is sb_per_lane");
+      return fail(AXH_ERR_INVALID_ARGUMENT,
+                  "the Q5_K / Q6_K one-pass family's only hole is sb_per_lane");
     const uint32_t need = (sb_per_row + 7u) / 8u;
     const uint32_t nit = variant && variant->sb_per_lane ? variant->sb_per_lane : need;
     if (nit < need || nit > 2u)
       return fail(AXH_ERR_INVALID_ARGUMENT,
-                  "Q5_K one-pass: sb_per_lane must cover the row and be 1 or 2 (rows of up to "
-                  "16 superblocks)");
-    std::snprintf(p->name, sizeof(p->name), "axh_q5k_matvec_one_i%u", nit);
+                  "Q5_K / Q6_K one-pass: sb_per_lane must cover the row and be 1 or 2 (rows of "
+                  "up to 16 superblocks)");
+    std::snprintf(p->name, sizeof(p->name), "%s_i%u", f.one_prefix, nit);
     p->nw = 8;
     p->lds = sb_per_row * f.lds_per_sb;
     p->flat = false; // one workgroup per 16 rows, all of them launched

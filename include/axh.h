@@ -200,11 +200,12 @@ void axh_event_destroy(axh_event *ev);
  * than 32 rows, one pass for 32-32768 rows of 1-128 superblocks (and up to
  * 65536 rows of at most 16; x staged whole from 6144 rows of at most 32
  * superblocks), persistent beyond, tiled for rows of more than 128
- * superblocks.  Every default is a hole assignment.  The Q4_0, Q6_K and
- * gate/up operations take the persistent holes only (family = sb_per_lane =
- * 0).  Q5_K takes the persistent holes or family = AXH_Q4K_FAMILY_ONE_PASS
- * with sb_per_lane 1 or 2 (rows of up to 16 superblocks); with no hole set it
- * runs one pass for 2048-32768 rows of up to 16 superblocks, else the
+ * superblocks.  Every default is a hole assignment.  The Q4_0 and gate/up
+ * operations take the persistent holes only (family = sb_per_lane = 0).
+ * Q5_K and Q6_K take the persistent holes or family =
+ * AXH_Q4K_FAMILY_ONE_PASS with sb_per_lane 1 or 2 (rows of up to 16
+ * superblocks); with no hole set they run one pass for rows of up to 16
+ * superblocks over 2048-32768 rows (Q5_K) or 256-4096 rows (Q6_K), else the
  * persistent family. */
 enum {
     AXH_Q4K_FAMILY_DEFAULT = 0,

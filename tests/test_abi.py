@@ -346,8 +346,29 @@ def test_q5k_one_pass_family(axc):
                 (100, 16, V(0, 0, 0, 0, 0, 2))):
         with pytest.raises(axc.DispatchError):
             name(*bad)
-    with pytest.raises(axc.DispatchError):
-        axc.q6k_matvec_kernel_name(100, 16, V(0, 0, 0, 0, one, 0))
+
+
+def test_q6k_one_pass_family(axc):
+    """Q6_K rows of up to 16 superblocks over 256-4096 rows take the one-pass
+    kernel by default; the family is reachable by request with the same hole
+    (sb_per_lane 1 or 2) and otherwise the persistent kernels run."""
+    co = axc.builtin_code_object()
+    name, V, one = axc.q6k_matvec_kernel_name, axc.Variant, axc.FAMILY_ONE_PASS
+    assert name(1024, 16) == "axh_q6k_matvec_one_i2"  # Llama-3-8B attn_v (GQA)
+    assert name(4096, 16) == "axh_q6k_matvec_one_i2"
+    assert name(256, 8) == "axh_q6k_matvec_one_i1"
+    for rows, sb in ((255, 16), (4097, 16), (14336, 16), (128256, 16), (4096, 17), (4096, 56)):
+        assert name(rows, sb).startswith("axh_q6k_matvec_flat_"), (rows, sb)
+    assert name(4096, 16, V(1, 4, 1, 0)) == "axh_q6k_matvec_flat_r1_w4_p1_x1"  # flat holes
+    assert name(7, 3, V(0, 0, 0, 0, one, 0)) == "axh_q6k_matvec_one_i1"
+    assert name(7, 3, V(0, 0, 0, 0, one, 2)) == "axh_q6k_matvec_one_i2"
+    for k in ("axh_q6k_matvec_one_i1", "axh_q6k_matvec_one_i2"):
+        assert k.encode() in co
+    for bad in ((100, 17, V(0, 0, 0, 0, one, 0)), (100, 16, V(0, 0, 0, 0, one, 1)),
+                (100, 16, V(0, 0, 0, 0, one, 3)), (100, 16, V(0, 0, 2, 0, one, 0)),
+                (100, 16, V(0, 0, 0, 0, 0, 2)), (100, 16, V(0, 0, 0, 0, 3, 0))):
+        with pytest.raises(axc.DispatchError):
+            name(*bad)
 
 
 def test_q4_0_kernel_selection(axc):

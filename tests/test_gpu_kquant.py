@@ -138,6 +138,23 @@ def test_q5k_one_pass_family(ctx, axc, rows, sb, nit):
     _check(y, Q5, q, x, rows, sb, f"one-pass {rows}x{sb} i{nit}")
 
 
+@pytest.mark.parametrize("rows,sb,nit", [(1, 1, 1), (7, 3, 1), (33, 8, 2), (17, 9, 2),
+                                         (4097, 16, 2), (1024, 16, 2), (100, 16, 2), (256, 8, 1)])
+def test_q6k_one_pass_family(ctx, axc, rows, sb, nit):
+    """The Q6_K one-pass kernel (the default for 256-4096 rows of up to 16
+    superblocks) at ragged row counts, requested explicitly: within the
+    oracle's tolerance, and bit for bit the persistent kernel's output (the
+    same per-lane loads, decode and reduction order)."""
+    q = O.gen_kq_weights(Q6, rows * 7 + sb, rows * sb)
+    x = O.gen_normal_f32(rows + 3 * sb, sb * 256)
+    v = axc.Variant(0, 0, 0, 0, axc.FAMILY_ONE_PASS, nit)
+    _say(f"kquant Q6_K one-pass {rows}x{sb} i{nit}")
+    y = _matvec(ctx, Q6, q, x, rows, sb, v)
+    _check(y, Q6, q, x, rows, sb, f"one-pass {rows}x{sb} i{nit}")
+    flat = _matvec(ctx, Q6, q, x, rows, sb, axc.Variant(1, 4, 1, 0))
+    assert np.array_equal(y.view(np.uint32), flat.view(np.uint32))
+
+
 def test_one_hot_x_reads_single_weights(ctx):
     """x = e_k picks column k: y = W[:, k] exactly (exact products, one term;
     compared as values: a zero Q6_K weight with a negative scale is -0.0 in
