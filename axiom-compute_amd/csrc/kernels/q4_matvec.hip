@@ -1014,9 +1014,21 @@ __device__ __forceinline__ void q6k_align_run(uint4 v, uint32_t e, uint32_t sh, 
   w[3] = __builtin_amdgcn_alignbyte(e, v.w, sh);
 }
 
-// Four bytes of 6-bit values against four x (pre-scaled by 2^24).
+// (a & m) | c as one v_and_or_b32 whose result the caller then masks and
+// permutes: written out, the compiler forms the masked half with a v_bitop3
+// of a & m and c, and the full value with a separate v_or for the permute.
+__device__ __forceinline__ uint32_t q6k_and_or(uint32_t a, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(c));
+  return r;
+}
+
+// Four bytes of 6-bit values (bits 6-7 clear) against four x (pre-scaled by
+// 2^24): bytes 0 and 2 are the f16 halves of v & 0x00FF00FF, and one byte
+// permute (v_perm_b32, selector 0x0C030C01: byte 1, zero, byte 3, zero) puts
+// bytes 1 and 3 in the same places, where a shift and a mask took two.
 __device__ __forceinline__ float q6k_bytes(uint32_t v, float4 x, float acc) {
-  const uint32_t a = v & 0x00FF00FFu, b = (v >> 8) & 0x00FF00FFu;
+  const uint32_t a = v & 0x00FF00FFu, b = __builtin_amdgcn_perm(v, v, 0x0C030C01u);
   acc = __builtin_fmaf(lo_half_f16(a), x.x, acc);
   acc = __builtin_fmaf(lo_half_f16(b), x.y, acc);
   acc = __builtin_fmaf(hi_half_f16(a), x.z, acc);
@@ -1050,10 +1062,10 @@ __device__ __forceinline__ void q6k_flat_compute(const Q6kFlatBuf<RPW, NS> &B, i
     float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t v0 = (lw[i] & 0x0F0F0F0Fu) | ((qw[i] << 4) & 0x30303030u);
-      const uint32_t v1 = (hw[i] & 0x0F0F0F0Fu) | ((qw[i] << 2) & 0x30303030u);
-      const uint32_t v2 = ((lw[i] >> 4) & 0x0F0F0F0Fu) | (qw[i] & 0x30303030u);
-      const uint32_t v3 = ((hw[i] >> 4) & 0x0F0F0F0Fu) | ((qw[i] >> 2) & 0x30303030u);
+      const uint32_t v0 = q6k_and_or(lw[i], 0x0F0F0F0Fu, (qw[i] << 4) & 0x30303030u);
+      const uint32_t v1 = q6k_and_or(hw[i], 0x0F0F0F0Fu, (qw[i] << 2) & 0x30303030u);
+      const uint32_t v2 = q6k_and_or(lw[i] >> 4, 0x0F0F0F0Fu, qw[i] & 0x30303030u);
+      const uint32_t v3 = q6k_and_or(hw[i] >> 4, 0x0F0F0F0Fu, (qw[i] >> 2) & 0x30303030u);
       d0 = q6k_bytes(v0, *reinterpret_cast<const float4 *>(xb + 16u * i), d0);
       d1 = q6k_bytes(v1, *reinterpret_cast<const float4 *>(xb + 64u + 16u * i), d1);
       d2 = q6k_bytes(v2, *reinterpret_cast<const float4 *>(xb + 128u + 16u * i), d2);
