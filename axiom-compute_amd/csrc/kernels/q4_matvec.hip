@@ -720,8 +720,10 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
 // 4096 4.06 vs 4.62-4.92, 14336 x 4096 8.9-9.1 vs 9.9-10.5, 32768 x 4096 17.0
 // vs 18.6; the 128256-row head 56.8 vs 53.5 (persistent prefetch 2) stays
 // persistent.  The template also covers the fused gate/up (kDual) and Q5_K
-// (kQ5) layouts.  The fused gate/up measured no faster than its persistent
-// kernel (2 x 14336 x 4096: 16.8 vs 16.8 us) and is not built; the Q5_K
+// (kQ5) layouts.  The fused gate/up measured slower than its persistent
+// kernel (2 x 14336 x 4096, A/B in one run, alternating order: x chunk by
+// chunk 15.12 us, x whole 14.97, persistent 14.53; identical output) and is
+// not built; the Q5_K
 // instances for rows of up to 16 superblocks are (axh_q5k_matvec_one_i{NIT},
 // see the runtime's Q5_K kernel choice).
 //
