@@ -37,10 +37,12 @@ def ratio_gate(floor_us: float, candidate_us: float, min_ratio: float) -> GateRe
 
 
 def interleaved_medians(measure: Callable[[str], float], names, rounds: int) -> dict:
-    """Median of `rounds` measurements of each name, one of each per round."""
+    """Median of `rounds` measurements of each name, one of each per round, the
+    order reversed every other round (ABBA), so that no name always runs first."""
+    names = list(names)
     t = {k: [] for k in names}
-    for _ in range(rounds):
-        for k in names:
+    for i in range(rounds):
+        for k in (names if i % 2 == 0 else names[::-1]):
             t[k].append(measure(k))
     return {k: sorted(v)[len(v) // 2] for k, v in t.items()}
 
