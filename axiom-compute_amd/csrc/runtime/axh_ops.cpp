@@ -201,12 +201,32 @@ static bool staged_in_chunks(const MatvecVariant &v) { return v.pf == 1; }
 
 // Default strategy per shape (chosen from on-device sweeps; any compiled
 // variant can be forced through axh_q4_variant).
+// Between 4097 and 6143 rows (more one-pass workgroups than CUs, fewer than
+// two per CU) the one-pass kernels' default gives way: rows of up to 24
+// superblocks take the whole-x kernel, rows of 25-32 the persistent kernel
+// with one row per lane group.  A/B in one run each, us per call, default
+// then the replacement: 4160 x 4096 5.12 vs 4.71, 5120 x 6144 6.87 vs 6.55,
+// 5632 x 3072 5.10 vs 4.87 (and the autotuner's re-timed winners at
+// 4352-5632 x 4096: 6-9 % faster, 4608 x 5120 6 %); 4608 x 8192 8.14 vs 7.41,
+// 5120 x 8192 8.24 vs 7.54, 5632 x 8192 8.38 vs 7.66, 6000 x 7168 8.49 vs
+// 7.76, 4352 x 7680 8.16 vs 7.43, where the persistent kernel with two rows
+// per lane group (its default for short rows) took 9.2-9.7 and the whole-x
+// kernel 8.3-8.5; 4097 x 6400 even (6.15 vs 6.25), 4608 x 2048 even.
+constexpr uint32_t kOneWholeMinRows = 6144, kOneWholeMaxSb = 32; // x whole from here on
+constexpr uint32_t kOneMidMinRows = 4097, kOneMidWholeMaxSb = 24;
+
+static bool q4k_mid_band_persistent(uint32_t n_rows, uint32_t nsb) {
+  return n_rows >= kOneMidMinRows && n_rows < kOneWholeMinRows && nsb > kOneMidWholeMaxSb &&
+         nsb <= kOneWholeMaxSb;
+}
+
 static MatvecVariant q4k_default(uint32_t n_rows, uint32_t nsb) {
   // The persistent kernel stages 32-element sub-blocks of x, one (or two for
   // the _x2 kernels) per thread.
   // Early refill (prefetch 1) for short rows: 14336 x 4096 9.9 vs 10.5 us,
   // neutral on 4096 x 4096.  On the 128256 x 4096 head prefetch 2 stays
   // ahead by 1-2 % (58.1-59.0 vs 59.4 us in one run).
+  if (q4k_mid_band_persistent(n_rows, nsb)) return {1, 4, 1, 2, 1};
   if (nsb * 8u <= 256u) return {2, 4, n_rows >= 65536u ? 2u : 1u, 2, 1};
   if (nsb * 8u <= 512u) return {1, 8, 2, 2, 1};
   return {1, 16, 2, 2, 1};
@@ -390,8 +410,8 @@ constexpr uint32_t kOneMinRows = 32, kOneMaxRows = 32768, kOneMaxSb = 128;
 // 32768 x 4096 even.  4096 rows (one workgroup per CU) and longer rows (LDS
 // for one or two) measured slower or even: 4096 x 4096 4.21 vs 4.08, 4096 x
 // 14336 8.84-8.93 vs 8.42-8.55, 8192 x 14336 even, 8192 x 32768 32.5-32.8 vs
-// 31.5-32.2.
-constexpr uint32_t kOneWholeMinRows = 6144, kOneWholeMaxSb = 32;
+// 31.5-32.2.  (kOneWholeMinRows and kOneWholeMaxSb are defined with the
+// 4097-6143-row band above.)
 
 // The whole-x kernel also takes 32769-65536 rows of at most 16 superblocks
 // (A/B in one run against the persistent kernel: 40000 x 4096 18.5-18.8 vs
@@ -440,9 +460,13 @@ static uint32_t q4k_default_family(uint32_t n_rows, uint32_t nsb, uint64_t q_byt
   if (n_rows < kQ4kColsMaxRows && nsb >= kSkMinSb && nsb <= kSkMaxSb && q_bytes < 0xFFFFFF00ull)
     return AXH_Q4K_FAMILY_SPLIT_K;
   if (n_rows < kQ4kColsMaxRows && nsb >= 1 && nsb <= kQ4kColsMaxSb) return AXH_Q4K_FAMILY_COLUMNS;
-  if (use_one_pass(n_rows, nsb) && q_bytes < 0xFFFFFFFFull)
-    return n_rows >= kOneWholeMinRows && nsb <= kOneWholeMaxSb ? AXH_Q4K_FAMILY_ONE_PASS_X
-                                                               : AXH_Q4K_FAMILY_ONE_PASS;
+  if (use_one_pass(n_rows, nsb) && q_bytes < 0xFFFFFFFFull) {
+    if (n_rows >= kOneWholeMinRows && nsb <= kOneWholeMaxSb) return AXH_Q4K_FAMILY_ONE_PASS_X;
+    if (n_rows >= kOneMidMinRows && n_rows < kOneWholeMinRows && nsb <= kOneMidWholeMaxSb)
+      return AXH_Q4K_FAMILY_ONE_PASS_X;
+    if (q4k_mid_band_persistent(n_rows, nsb)) return AXH_Q4K_FAMILY_PERSISTENT;
+    return AXH_Q4K_FAMILY_ONE_PASS;
+  }
   return AXH_Q4K_FAMILY_PERSISTENT; // falls back to tiled for rows it cannot stage
 }
 

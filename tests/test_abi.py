@@ -123,7 +123,14 @@ def test_kernel_selection_by_shape_and_variant(axc):
     assert name(4096, 32) == "axh_q4k_matvec_onep_i4"
     assert name(4096, 24) == "axh_q4k_matvec_one_i3"
     assert name(4096, 16) == "axh_q4k_matvec_one_i2"
-    assert name(6143, 16) == "axh_q4k_matvec_one_i2"
+    # 4097-6143 rows: x staged whole up to 24 superblocks, the persistent kernel
+    # with one row per lane group for 25-32, one pass again beyond
+    assert name(4097, 24) == "axh_q4k_matvec_onex_i3"
+    assert name(6143, 16) == "axh_q4k_matvec_onex_i2"
+    assert name(5120, 8) == "axh_q4k_matvec_onex_i1"
+    assert name(4097, 25) == "axh_q4k_matvec_flat_r1_w4_p1_n0"
+    assert name(6143, 32) == "axh_q4k_matvec_flat_r1_w4_p1_n0"
+    assert name(5120, 33) == "axh_q4k_matvec_one_i5"
     # from 6144 rows of at most 32 superblocks: x staged whole behind one barrier
     assert name(32768, 1) == "axh_q4k_matvec_onex_i1"
     assert name(6144, 16) == "axh_q4k_matvec_onex_i2"

@@ -325,6 +325,23 @@ def test_q4k_one_pass_whole_x_shapes(ctx, axc, rows, sb):
     _check_q4k(y, q, x, rows, sb, f"q4k one pass whole x {rows}x{sb}")
 
 
+@pytest.mark.parametrize("rows,sb,kernel", [(4097, 1, "onex_i1"), (4160, 16, "onex_i2"),
+                                            (5121, 24, "onex_i3"), (6143, 9, "onex_i2"),
+                                            (4097, 25, "flat_r1_w4_p1_n0"),
+                                            (4608, 32, "flat_r1_w4_p1_n0"),
+                                            (6143, 31, "flat_r1_w4_p1_n0")])
+def test_q4k_defaults_between_4097_and_6143_rows(ctx, axc, rows, sb, kernel):
+    """The default between 4097 and 6143 rows: x staged whole for rows of up
+    to 24 superblocks, the persistent kernel with one row per lane group for
+    25-32, at both ends of the band and with odd row counts."""
+    assert axc.q4k_matvec_kernel_name(rows, sb) == f"axh_q4k_matvec_{kernel}"
+    _say(f"q4k default {rows}x{sb} ({kernel})")
+    q = O.gen_q4k_weights(rows * 37 + sb, rows * sb)
+    x = O.gen_normal_f32(rows + 17 * sb, sb * 256)
+    y = _run_q4k(ctx, q, x, rows, sb)
+    _check_q4k(y, q, x, rows, sb, f"q4k default {rows}x{sb}")
+
+
 @pytest.mark.parametrize("sb", [9, 40])
 def test_q4k_early_refill_several_pairs_per_wave(ctx, axc, sb):
     """Prefetch-1 variants on more rows than the persistent grid holds, so
