@@ -215,7 +215,21 @@ static bool staged_in_chunks(const MatvecVariant &v) { return v.pf == 1; }
 constexpr uint32_t kOneWholeMinRows = 6144, kOneWholeMaxSb = 32; // x whole from here on
 constexpr uint32_t kOneMidMinRows = 4097, kOneMidWholeMaxSb = 24;
 
+// Rows of 74 or more superblocks leave LDS for one one-pass workgroup per CU
+// (nsb * 1120 bytes each, 160 KiB per CU), so the one-pass grid balances only
+// at whole multiples of 4096 rows;
+// the persistent kernel's 4096 waves (16 per workgroup, one row pair each)
+// balance up to 8192 rows.  Between 4097 and 8191 rows the persistent kernel
+// is ahead (A/B in one run, us per call, one pass vs persistent: 4352 x
+// 28672 24.17 vs 18.95, 5120 x 28672 24.25 vs 19.48, 6144 x 28672 24.78 vs
+// 21.03, 7168 x 28672 25.72 vs 24.24, 5120 x 20480 18.70 vs 15.42, 6144 x
+// 20480 18.66 vs 16.52, 7168 x 20480 20.06 vs 18.24, 6144 x 32768 28.00 vs
+// 23.81); at 8192 rows they are even (27.34 vs 27.01) and at 10240 the one
+// pass is ahead (37.38 vs 42.37).
+constexpr uint32_t kLongMinSb = 74, kLongMaxRows = 8191;
+
 static bool q4k_mid_band_persistent(uint32_t n_rows, uint32_t nsb) {
+  if (n_rows >= kOneMidMinRows && n_rows <= kLongMaxRows && nsb >= kLongMinSb) return true;
   return n_rows >= kOneMidMinRows && n_rows < kOneWholeMinRows && nsb > kOneMidWholeMaxSb &&
          nsb <= kOneWholeMaxSb;
 }
@@ -226,7 +240,7 @@ static MatvecVariant q4k_default(uint32_t n_rows, uint32_t nsb) {
   // Early refill (prefetch 1) for short rows: 14336 x 4096 9.9 vs 10.5 us,
   // neutral on 4096 x 4096.  On the 128256 x 4096 head prefetch 2 stays
   // ahead by 1-2 % (58.1-59.0 vs 59.4 us in one run).
-  if (q4k_mid_band_persistent(n_rows, nsb)) return {1, 4, 1, 2, 1};
+  if (q4k_mid_band_persistent(n_rows, nsb) && nsb <= kOneWholeMaxSb) return {1, 4, 1, 2, 1};
   if (nsb * 8u <= 256u) return {2, 4, n_rows >= 65536u ? 2u : 1u, 2, 1};
   if (nsb * 8u <= 512u) return {1, 8, 2, 2, 1};
   return {1, 16, 2, 2, 1};

@@ -200,7 +200,8 @@ void axh_event_destroy(axh_event *ev);
  * than 32 rows, one pass for 32-32768 rows of 1-128 superblocks (and up to
  * 65536 rows of at most 16; x staged whole from 6144 rows of at most 32
  * superblocks and from 4097 rows of at most 24), except 4097-6143 rows of
- * 25-32 superblocks, which take the persistent family; persistent beyond,
+ * 25-32 superblocks and 4097-8191 rows of 74 or more, which take the
+ * persistent family; persistent beyond,
  * tiled for rows of more than 128 superblocks.  Every default is a hole
  * assignment.  The Q4_0 and gate/up
  * operations take the persistent holes only (family = sb_per_lane = 0).

@@ -131,6 +131,11 @@ def test_kernel_selection_by_shape_and_variant(axc):
     assert name(4097, 25) == "axh_q4k_matvec_flat_r1_w4_p1_n0"
     assert name(6143, 32) == "axh_q4k_matvec_flat_r1_w4_p1_n0"
     assert name(5120, 33) == "axh_q4k_matvec_one_i5"
+    # 4097-8191 rows of 74+ superblocks (one one-pass workgroup per CU): persistent
+    assert name(4097, 74) == "axh_q4k_matvec_flat_r1_w16_p2_n0"
+    assert name(8191, 128) == "axh_q4k_matvec_flat_r1_w16_p2_n0"
+    assert name(5000, 73) == "axh_q4k_matvec_one_i10"
+    assert name(8192, 112) == "axh_q4k_matvec_one_i14"
     # from 6144 rows of at most 32 superblocks: x staged whole behind one barrier
     assert name(32768, 1) == "axh_q4k_matvec_onex_i1"
     assert name(6144, 16) == "axh_q4k_matvec_onex_i2"

@@ -329,11 +329,14 @@ def test_q4k_one_pass_whole_x_shapes(ctx, axc, rows, sb):
                                             (5121, 24, "onex_i3"), (6143, 9, "onex_i2"),
                                             (4097, 25, "flat_r1_w4_p1_n0"),
                                             (4608, 32, "flat_r1_w4_p1_n0"),
-                                            (6143, 31, "flat_r1_w4_p1_n0")])
+                                            (6143, 31, "flat_r1_w4_p1_n0"),
+                                            (4097, 74, "flat_r1_w16_p2_n0"),
+                                            (8191, 128, "flat_r1_w16_p2_n0")])
 def test_q4k_defaults_between_4097_and_6143_rows(ctx, axc, rows, sb, kernel):
     """The default between 4097 and 6143 rows: x staged whole for rows of up
     to 24 superblocks, the persistent kernel with one row per lane group for
-    25-32, at both ends of the band and with odd row counts."""
+    25-32, at both ends of the band and with odd row counts; and the
+    persistent kernel for 4097-8191 rows of 74 or more superblocks."""
     assert axc.q4k_matvec_kernel_name(rows, sb) == f"axh_q4k_matvec_{kernel}"
     _say(f"q4k default {rows}x{sb} ({kernel})")
     q = O.gen_q4k_weights(rows * 37 + sb, rows * sb)
