@@ -837,9 +837,19 @@ static const KqFormat kQ6kFormat{"axh_q6k_matvec_flat", "axh_q6k_matvec_one", kQ
 // Q5_K 14336 x 4096 10.6-10.9 vs 11.3-11.4 us; Q6_K 4096 x 14336 12.5 vs
 // 13.4-13.9 us, 128256 x 4096 90.0-90.6 vs 90.9-92.0 us.  The Q6_K kernel
 // stages x whole, one sub-block per thread with its prefetch-1 variants.
-static MatvecVariant kq_default(const KqFormat &f, uint32_t nsb) {
+//
+// Q6_K rows of 17-32 superblocks on at most 1024 rows (at most half the CUs
+// get a workgroup) keep x staged whole and two iterations in flight instead:
+// A/B in one run, us per call, prefetch 2 vs early refill: 512 x 8192 5.87
+// vs 6.21, 1024 x 8192 (Llama-2-70B attn_v) 5.81 vs 6.13, 1024 x 6144 5.03
+// vs 5.57; from 2048 rows early refill stays ahead (early refill vs
+// prefetch 2: 2048 x 8192 6.39 vs 6.45, 4096 x 8192 7.87 vs 8.16).
+constexpr uint32_t kQ6FewRows = 1024;
+
+static MatvecVariant kq_default(const KqFormat &f, uint32_t n_rows, uint32_t nsb) {
   const uint32_t nw = nsb * 8u <= 256u ? 4u : 8u;
   const bool early = f.chunked_early || nsb * 8u <= nw * 64u;
+  if (&f == &kQ6kFormat && n_rows <= kQ6FewRows && nsb > 16u && nsb <= 32u) return {1, 4, 2, 2, 1};
   return {1, nw, early ? 1u : 2u, 2, 1};
 }
 
@@ -899,7 +909,7 @@ static axh_status plan_kq(const KqFormat &f, uint32_t n_rows, uint32_t sb_per_ro
   }
   if (variant && variant->nontemporal == 1)
     return fail(AXH_ERR_INVALID_ARGUMENT, "no non-temporal Q5_K / Q6_K variant is compiled");
-  const MatvecVariant dflt = kq_default(f, sb_per_row);
+  const MatvecVariant dflt = kq_default(f, n_rows, sb_per_row);
   const uint32_t want_nw =
       variant && variant->waves_per_workgroup ? variant->waves_per_workgroup : dflt.nw;
   const uint32_t min_xp = (sb_per_row * 8u + want_nw * 64u - 1u) / (want_nw * 64u);

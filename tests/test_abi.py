@@ -372,6 +372,11 @@ def test_q6k_one_pass_family(axc):
     for rows, sb in ((255, 16), (4097, 16), (14336, 16), (128256, 16), (4096, 17), (4096, 56)):
         assert name(rows, sb).startswith("axh_q6k_matvec_flat_"), (rows, sb)
     assert name(4096, 16, V(1, 4, 1, 0)) == "axh_q6k_matvec_flat_r1_w4_p1_x1"  # flat holes
+    # up to 1024 rows of 17-32 superblocks: prefetch 2 (Llama-2-70B attn_v is 1024 x 8192)
+    assert name(1024, 32) == "axh_q6k_matvec_flat_r1_w4_p2_x1"
+    assert name(1, 17) == "axh_q6k_matvec_flat_r1_w4_p2_x1"
+    assert name(1025, 32) == "axh_q6k_matvec_flat_r1_w4_p1_x1"
+    assert name(1024, 33) == "axh_q6k_matvec_flat_r1_w8_p1_x1"
     assert name(7, 3, V(0, 0, 0, 0, one, 0)) == "axh_q6k_matvec_one_i1"
     assert name(7, 3, V(0, 0, 0, 0, one, 2)) == "axh_q6k_matvec_one_i2"
     for k in ("axh_q6k_matvec_one_i1", "axh_q6k_matvec_one_i2"):
