@@ -1138,6 +1138,9 @@ constexpr uint32_t kSrMaxSb = 16;
 // depend on the device a query runs on).  Measured over 60 shapes (1024 to
 // 14336 rows, K = 4096 and 14336, 8 to 512 columns, every compiled variant):
 // the choice below is the fastest variant at 59 and within 2% at the last.
+// A later sweep of 22 shapes (up to 28672 rows, K up to 14336) moved two
+// regions: 128 columns on enough rows (32 x 32 tiles) and more than 32
+// columns on few long rows (the long-rows kind).
 constexpr uint64_t kMatmulCus = 256;
 // Workgroups the tile kinds (5 and 8) need before their tile size matters
 // less than filling the chip: 5/8 of the CUs.  Below it, more and smaller
@@ -1192,19 +1195,29 @@ static MatmulVariant q4k_matmul_default(uint32_t n_rows, uint32_t batch, uint32_
       break;
     }
   }
-  // The K-split kind (K over 8 waves) wherever its grid is one wave: long
-  // rows over few of them.  16-row tiles first (4096 x 14336 at B = 8 19.8
-  // us, B = 16 24.3, against 28.9 and 34.5 with 32-row tiles and 39.3 and
-  // 39.8 for the K-split tile kind), then 32-row tiles (4096 x 14336 x 32
+  // Long rows over few of them, more than 32 columns, where one wave of
+  // 16 x 16 or 32 x 16 tiles fills the chip: the long-rows kind with 16-column
+  // tiles (A/B in one run, against the K-split kind with the same tiles:
+  // 1024 x 8192 x 64 9.08 vs 14.79 us, 1024 x 8192 x 128 13.69 vs 20.61, 1024
+  // x 14336 x 128 21.19 vs 34.85, 2048 x 14336 x 64 21.88 vs 35.04, 512 x
+  // 14336 x 128 13.01 vs 24.41).  The K-split kind (K over 8 waves) keeps
+  // rows the long-rows kind cannot index (kLkMaxSb superblocks and more):
+  // 16-row tiles first (4096 x 14336 at B = 8 19.8 us, B = 16 24.3, against
+  // 28.9 and 34.5 with 32-row tiles), then 32-row tiles (4096 x 14336 x 32
   // 35.4 against 40.2; 1024 x 14336 x 128 35.1 against 40.1).
-  if (groups(16, 16) <= kMatmulCus) return {3, 8, 1, 1, 1};
-  if (groups(32, 16) <= kMatmulCus) return {3, 8, 1, 1, 2};
+  const bool lk_ok = nsb > kSrMaxSb && nsb < kLkMaxSb;
+  if (groups(16, 16) <= kMatmulCus) return lk_ok ? MatmulVariant{9, 8, 4, 1, 1} : MatmulVariant{3, 8, 1, 1, 1};
+  if (groups(32, 16) <= kMatmulCus) return lk_ok ? MatmulVariant{9, 8, 4, 1, 2} : MatmulVariant{3, 8, 1, 1, 2};
   // kind 8 (32 x 32 MFMA tiles) where its rows fill the chip: 14336 x 4096 x
   // 512 74.1 us (8 waves of 32 rows) against 83-94 for a row-split kind,
   // B = 256 49.3 (4 waves of 32 rows) against 52.1; 8192 x 4096 x 512 46.0 us
   // with 4 waves against 60.7 as K-split tiles.
   if (batch > 256 && groups(256, 128) >= kMatmulFill) return {8, 8, 8, 4, 1};
-  if (batch > 128 && groups(128, 128) >= kMatmulFill) return {8, 4, 8, 4, 1};
+  // from 128 columns (A/B in one run against the K-split tile kind at 128
+  // columns: 20480 x 4096 40.35 vs 51.0 us, 28672 x 4096 43.95 vs 53.0, 28672
+  // x 8192 78.45 vs 94.92, 24576 x 14336 136.0 vs 156.2; below the fill
+  // 16384 x 8192 and 11008 x 4096 stay on the K-split tile kind)
+  if (batch >= 128 && groups(128, 128) >= kMatmulFill) return {8, 4, 8, 4, 1};
   // The K-split tile kind: up to 128 columns per workgroup, halved until the
   // grid fills (4096 x 14336 x 64: one column tile 41.3 us against four
   // 58.8; 4096 x 11008 x 128: two 37.9 against eight 76.5).  Two column

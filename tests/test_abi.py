@@ -233,6 +233,10 @@ def test_matmul_kernel_selection(axc):
     assert name(1024, 16, 64) == "axh_q4k_matmul_sr_w8_s2"
     assert name(4096, 16, 64) == "axh_q4k_matmul_sr_w8_s2_n2"  # two blocks of 32 columns per CU
     assert name(8192, 16, 64) == "axh_q4k_matmul_kx_r4_n2_k4_p2"  # four: K-split tiles
+    # 128 columns: 32 x 32 tiles once 128 x 128 of them fill 160 workgroups
+    assert name(14336, 16, 128) == "axh_q4k_matmul_kx_r4_n8_k4_p2"  # 112: K-split tiles
+    assert name(20480, 16, 128) == "axh_q4k_matmul_rm_w4_r1_p4"  # 160
+    assert name(28672, 32, 128) == "axh_q4k_matmul_rm_w4_r1_p4"
     # K > 4096 over few rows: kind 9 up to 32 columns, its largest tile (32 or
     # 16 rows x 16 or 8 columns) whose grid fills 160 workgroups, at most two
     # waves of them; then the K-split kind while its grid is one wave
@@ -247,8 +251,12 @@ def test_matmul_kernel_selection(axc):
     assert name(8192, 56, 8) == "axh_q4k_matmul_lk_c8_x2_w2_r2"  # 256 x 1
     assert name(14336, 56, 8) == "axh_q4k_matmul_kx_r4_n1_k4_p3"  # 448 x 1: K-split tiles
     assert name(8192, 56, 32) == "axh_q4k_matmul_kx_r4_n1_k4_p3"  # 256 x 2
-    assert name(1024, 56, 64) == "axh_q4k_matmul_ks_k8_n1_p1_r1"  # 16-row tiles: 64 x 4
-    assert name(1024, 56, 128) == "axh_q4k_matmul_ks_k8_n1_p1"  # 32-row tiles: 32 x 8
+    # past 32 columns, where one wave of 16 x 16 or 32 x 16 tiles fills the
+    # chip: kind 9 with 16-column tiles (the K-split kind with the same tiles
+    # for rows too long for kind 9)
+    assert name(1024, 56, 64) == "axh_q4k_matmul_lk_c16_x1_w3"  # 16-row tiles: 64 x 4
+    assert name(1024, 56, 128) == "axh_q4k_matmul_lk_c16_x1_w3_r2"  # 32-row tiles: 32 x 8
+    assert name(64, 1100, 64) == "axh_q4k_matmul_ks_k8_n1_p1_r1"
     assert name(14336, 56, 32) == "axh_q4k_matmul_kx_r4_n2_k4_p3"  # prefetch 3 at K > 4096
     assert name(4096, 56, 8, axc.MatmulVariant(3, 8, 1, 2, 1)) == "axh_q4k_matmul_ks_k8_n1_p2_r1"
     with pytest.raises(axc.DispatchError):  # kind 9 keeps the chunk offsets below 1 MiB

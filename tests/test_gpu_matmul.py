@@ -126,8 +126,11 @@ def test_edge_shapes(ctx, rows, sb, batch):
 @pytest.mark.parametrize("rows,sb,batch,kernel", [(1024, 16, 250, "sr_w8_s2_n2"),
                                                   (2000, 16, 100, "sr_w8_s2_n2"),
                                                   (1000, 16, 60, "sr_w8_s2"),
-                                                  (1024, 56, 128, "ks_k8_n1_p1"),
-                                                  (1000, 56, 60, "ks_k8_n1_p1_r1"),
+                                                  (1024, 56, 128, "lk_c16_x1_w3_r2"),
+                                                  (1000, 56, 60, "lk_c16_x1_w3"),
+                                                  (500, 33, 127, "lk_c16_x1_w3"),
+                                                  (64, 1100, 64, "ks_k8_n1_p1_r1"),
+                                                  (20480, 16, 128, "rm_w4_r1_p4"),
                                                   (4000, 56, 30, "lk_c16_x1_w3_r2"),
                                                   (4000, 56, 16, "lk_c16_x1_w3"),
                                                   (4000, 56, 7, "lk_c8_x2_w2"),
@@ -139,8 +142,10 @@ def test_edge_shapes(ctx, rows, sb, batch):
 def test_grid_fill_defaults(ctx, axc, rows, sb, batch, kernel):
     """The defaults that follow from the grid on few rows: streaming rows past
     32 columns (several column groups, the last one partial), kind 9 at K >
-    4096 up to 32 columns, the K-split kind up to 128, K-split tiles with
-    their columns halved."""
+    4096 up to 32 columns and, where one wave of its 16-column tiles fills
+    the chip, beyond (partial last column group), the K-split kind for rows
+    too long for kind 9, K-split tiles with their columns halved, and 32 x 32
+    tiles at 128 columns on enough rows."""
     assert axc.q4k_matmul_kernel_name(rows, sb, batch) == "axh_q4k_matmul_" + kernel
     _say(f"matmul default {kernel} {rows}x{sb * 256} B={batch}")
     q, xh = _inputs(rows + 3 * sb + 5 * batch, rows, sb, batch)
