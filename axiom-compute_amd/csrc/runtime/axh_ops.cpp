@@ -1183,8 +1183,14 @@ static MatmulVariant q4k_matmul_default(uint32_t n_rows, uint32_t batch, uint32_
   if (nsb > kSrMaxSb && nsb < kLkMaxSb && batch <= 32) {
     // up to 4 columns: 4-column tiles (X loads halved; 56 KiB of LDS, so two
     // workgroups per CU): 4096 x 14336 x 4 10.8 us against 11.7 with 8
-    // columns, 8192 x 14336 x 4 (512 workgroups) 20.0 against 21.9
-    if (batch <= 4 && groups(16, 4) <= 2 * kMatmulCus) return {9, 8, 1, 2, 1};
+    // columns, 8192 x 14336 x 4 (512 workgroups) 20.0 against 21.9.  Also up
+    // to 8 columns where 8-column tiles would leave half the CUs or more idle
+    // (A/B in one run: 512 x 14336 x 8 8.65 vs 9.69 us, 1024 x 14336 x 8 9.53
+    // vs 11.13, 2048 x 14336 x 6 9.94 vs 11.61, 1024 x 8192 x 8 6.34 vs 6.90,
+    // 2048 x 8192 x 8 7.28 vs 8.46, 1024 x 8192 x 5 6.30 vs 6.71; at 4096 x
+    // 14336 x 8 the 8-column tiles stay ahead).
+    const bool narrow = batch <= 4 || (batch <= 8 && groups(16, 8) <= kMatmulCus / 2);
+    if (narrow && groups(16, 4) <= 2 * kMatmulCus) return {9, 8, 1, 2, 1};
     constexpr uint32_t cand[4][2] = {{16, 2}, {16, 1}, {8, 2}, {8, 1}}; // columns, row tiles
     for (int i = 0; i < 4; ++i) {
       const uint32_t xc = cand[i][0], rt = cand[i][1];

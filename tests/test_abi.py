@@ -247,6 +247,8 @@ def test_matmul_kernel_selection(axc):
     assert name(4096, 56, 32) == "axh_q4k_matmul_lk_c16_x1_w3_r2"  # 128 x 2 workgroups
     assert name(1024, 56, 32) == "axh_q4k_matmul_lk_c8_x2_w2"  # 64 x 4
     assert name(4096, 56, 4) == "axh_q4k_matmul_lk_c4_x2_w2"  # up to 4 columns
+    assert name(2048, 56, 8) == "axh_q4k_matmul_lk_c4_x2_w2"  # 8 columns on 128 tiles of 8
+    assert name(2049, 56, 8) == "axh_q4k_matmul_lk_c8_x2_w2"
     assert name(8192, 56, 3) == "axh_q4k_matmul_lk_c4_x2_w2"  # 512: two per CU
     assert name(8192, 56, 8) == "axh_q4k_matmul_lk_c8_x2_w2_r2"  # 256 x 1
     assert name(14336, 56, 8) == "axh_q4k_matmul_kx_r4_n1_k4_p3"  # 448 x 1: K-split tiles

@@ -135,6 +135,7 @@ def test_edge_shapes(ctx, rows, sb, batch):
                                                   (4000, 56, 16, "lk_c16_x1_w3"),
                                                   (4000, 56, 7, "lk_c8_x2_w2"),
                                                   (4000, 43, 3, "lk_c4_x2_w2"),
+                                                  (1024, 32, 7, "lk_c4_x2_w2"),
                                                   (8100, 43, 5, "lk_c8_x2_w2_r2"),
                                                   (11000, 43, 5, "kx_r4_n1_k4_p3"),
                                                   (1000, 43, 31, "lk_c8_x2_w2"),
