@@ -843,13 +843,16 @@ static const KqFormat kQ6kFormat{"axh_q6k_matvec_flat", "axh_q6k_matvec_one", kQ
 // A/B in one run, us per call, prefetch 2 vs early refill: 512 x 8192 5.87
 // vs 6.21, 1024 x 8192 (Llama-2-70B attn_v) 5.81 vs 6.13, 1024 x 6144 5.03
 // vs 5.57; from 2048 rows early refill stays ahead (early refill vs
-// prefetch 2: 2048 x 8192 6.39 vs 6.45, 4096 x 8192 7.87 vs 8.16).
-constexpr uint32_t kQ6FewRows = 1024;
+// prefetch 2: 2048 x 8192 6.39 vs 6.45, 4096 x 8192 7.87 vs 8.16).  The same
+// holds for Q5_K rows of up to 32 superblocks (its one-pass kernel starts at
+// 2048 rows): 1024 x 4096 3.46 vs 3.57 us, 1024 x 8192 5.10 vs 5.38.
+constexpr uint32_t kKqFewRows = 1024;
 
 static MatvecVariant kq_default(const KqFormat &f, uint32_t n_rows, uint32_t nsb) {
   const uint32_t nw = nsb * 8u <= 256u ? 4u : 8u;
   const bool early = f.chunked_early || nsb * 8u <= nw * 64u;
-  if (&f == &kQ6kFormat && n_rows <= kQ6FewRows && nsb > 16u && nsb <= 32u) return {1, 4, 2, 2, 1};
+  const bool few = n_rows <= kKqFewRows && nsb <= 32u && (&f == &kQ5kFormat || nsb > 16u);
+  if (few) return {1, 4, 2, 2, 1};
   return {1, nw, early ? 1u : 2u, 2, 1};
 }
 

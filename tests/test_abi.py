@@ -387,6 +387,12 @@ def test_q6k_one_pass_family(axc):
     assert name(1, 17) == "axh_q6k_matvec_flat_r1_w4_p2_x1"
     assert name(1025, 32) == "axh_q6k_matvec_flat_r1_w4_p1_x1"
     assert name(1024, 33) == "axh_q6k_matvec_flat_r1_w8_p1_x1"
+    # Q5_K: the same up to 1024 rows of up to 32 superblocks
+    q5 = axc.q5k_matvec_kernel_name
+    assert q5(1024, 16) == "axh_q5k_matvec_flat_r1_w4_p2_x1"
+    assert q5(1024, 32) == "axh_q5k_matvec_flat_r1_w4_p2_x1"
+    assert q5(1025, 32) == "axh_q5k_matvec_flat_r1_w4_p1_x1"
+    assert q5(4096, 16) == "axh_q5k_matvec_one_i2"
     assert name(7, 3, V(0, 0, 0, 0, one, 0)) == "axh_q6k_matvec_one_i1"
     assert name(7, 3, V(0, 0, 0, 0, one, 2)) == "axh_q6k_matvec_one_i2"
     for k in ("axh_q6k_matvec_one_i1", "axh_q6k_matvec_one_i2"):
