@@ -443,6 +443,18 @@ constexpr uint32_t kOneTallMaxRows = 65536, kOneTallMaxSb = 16;
 // 3912-3925).  The prefetch hole of the one-pass family picks either.
 constexpr uint32_t kOnePMinIt = 4, kOnePMaxRows = 4096;
 
+// Up to 1024 rows the one-pass kernels' 16 rows per workgroup leave CUs idle
+// (64 workgroups at 1024 rows); the tiled kernel with one row per wave (4
+// rows per workgroup) fills 4x as many, and from 24 superblocks per row that
+// pays.  A/B in one run, us per call, one pass vs tiled r1 w4 p2: 128 x 8192
+// 4.38 vs 3.41, 128 x 28672 11.94 vs 7.43, 256 x 6144 3.70 vs 3.29, 256 x
+// 14336 6.88 vs 4.98, 512 x 14336 6.90 vs 5.57, 512 x 28672 12.06 vs 8.61,
+// 1024 x 6144 4.00 vs 3.87, 1024 x 28672 12.13 vs 9.43 (and the autotuner's
+// re-timed winners: 1024 x 8192 -12 %, 1024 x 14336 -19 %, 512 x 8192 -13 %);
+// at 16 superblocks at most 6 % (128 rows), and from 2048 rows the one pass
+// is ahead (2048 x 8192 4.98 vs 5.14, 2048 x 28672 12.33 vs 16.91).
+constexpr uint32_t kTiledFewMaxRows = 1024, kTiledFewMinSb = 24;
+
 static bool use_one_pass(uint32_t n_rows, uint32_t nsb) {
   if (nsb < 1 || nsb > kOneMaxSb || n_rows < kOneMinRows) return false;
   return n_rows <= kOneMaxRows || (nsb <= kOneTallMaxSb && n_rows <= kOneTallMaxRows);
@@ -475,6 +487,7 @@ static uint32_t q4k_default_family(uint32_t n_rows, uint32_t nsb, uint64_t q_byt
     return AXH_Q4K_FAMILY_SPLIT_K;
   if (n_rows < kQ4kColsMaxRows && nsb >= 1 && nsb <= kQ4kColsMaxSb) return AXH_Q4K_FAMILY_COLUMNS;
   if (use_one_pass(n_rows, nsb) && q_bytes < 0xFFFFFFFFull) {
+    if (n_rows <= kTiledFewMaxRows && nsb >= kTiledFewMinSb) return AXH_Q4K_FAMILY_TILED;
     if (n_rows >= kOneWholeMinRows && nsb <= kOneWholeMaxSb) return AXH_Q4K_FAMILY_ONE_PASS_X;
     if (n_rows >= kOneMidMinRows && n_rows < kOneWholeMinRows && nsb <= kOneMidWholeMaxSb)
       return AXH_Q4K_FAMILY_ONE_PASS_X;

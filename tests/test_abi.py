@@ -117,8 +117,13 @@ def test_kernel_selection_by_shape_and_variant(axc):
     # 32..32768 rows: one pass, one pair of rows per wave, a workgroup per 16 rows;
     # x two chunks ahead from four steps up to one workgroup per CU (4096 rows)
     assert name(4096, 56) == "axh_q4k_matvec_onep_i7"
-    assert name(32, 33) == "axh_q4k_matvec_onep_i5"
+    assert name(2048, 33) == "axh_q4k_matvec_onep_i5"
     assert name(4096, 128) == "axh_q4k_matvec_onep_i16"
+    # up to 1024 rows of 24+ superblocks: the tiled kernel, one row per wave
+    assert name(32, 33) == "axh_q4k_matvec_tiled_r1_w4_p2"
+    assert name(1024, 24) == "axh_q4k_matvec_tiled_r1_w4_p2"
+    assert name(1024, 23) == "axh_q4k_matvec_one_i3"
+    assert name(1025, 24) == "axh_q4k_matvec_one_i3"
     assert name(4097, 56) == "axh_q4k_matvec_one_i7"
     assert name(4096, 32) == "axh_q4k_matvec_onep_i4"
     assert name(4096, 24) == "axh_q4k_matvec_one_i3"

@@ -284,13 +284,28 @@ def test_q4km_reference_kernel_many_superblocks(ctx, axc, n):
 def test_q4k_one_pass_shapes(ctx, axc, rows, sb):
     """32..32768 rows of 1..128 superblocks: trip counts 1..16 and their
     boundaries (8k and 8k + 1 superblocks), odd row counts (a half-empty last
-    pair) and workgroups past the last pair."""
-    assert axc.q4k_matvec_kernel_name(rows, sb).startswith("axh_q4k_matvec_one")
+    pair) and workgroups past the last pair.  The one-pass family is requested
+    (up to 1024 rows of 24+ superblocks the default is the tiled kernel)."""
+    v = axc.Variant(family=axc.FAMILY_ONE_PASS)
+    assert axc.q4k_matvec_kernel_name(rows, sb, v).startswith("axh_q4k_matvec_one")
     _say(f"q4k one pass {rows}x{sb}")
     q = O.gen_q4k_weights(rows * 23 + sb, rows * sb)
     x = O.gen_normal_f32(rows + 7 * sb, sb * 256)
-    y = _run_q4k(ctx, q, x, rows, sb)
+    y = _run_q4k(ctx, q, x, rows, sb, v)
     _check_q4k(y, q, x, rows, sb, f"q4k one pass {rows}x{sb}")
+
+
+@pytest.mark.parametrize("rows,sb", [(32, 24), (33, 40), (100, 56), (777, 24), (1000, 127),
+                                     (1024, 128), (64, 113)])
+def test_q4k_tiled_default_on_few_long_rows(ctx, axc, rows, sb):
+    """32..1024 rows of 24..128 superblocks default to the tiled kernel with
+    one row per wave: odd row counts, partial last workgroups and tiles."""
+    assert axc.q4k_matvec_kernel_name(rows, sb) == "axh_q4k_matvec_tiled_r1_w4_p2"
+    _say(f"q4k tiled default {rows}x{sb}")
+    q = O.gen_q4k_weights(rows * 41 + sb, rows * sb)
+    x = O.gen_normal_f32(rows + 19 * sb, sb * 256)
+    y = _run_q4k(ctx, q, x, rows, sb)
+    _check_q4k(y, q, x, rows, sb, f"q4k tiled default {rows}x{sb}")
 
 
 @pytest.mark.parametrize("rows,sb,xd", [(32, 17, 2), (33, 24, 2), (4096, 25, 2), (4095, 56, 2),

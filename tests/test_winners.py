@@ -17,7 +17,7 @@ SHAPES = [(1, 1), (1, 16), (1, 33), (1, 128), (2, 40), (3, 64), (4, 128), (5, 12
           (31, 16), (32, 16), (256, 16), (4096, 56), (4096, 16), (14336, 16), (6144, 32),
           (6144, 33), (32768, 16), (32769, 17), (40000, 16), (65536, 16), (65537, 16),
           (128256, 16), (4096, 129), (100, 300), (3000, 200), (4160, 16), (5120, 24),
-          (5120, 32), (6143, 25), (6144, 112), (8191, 74)]
+          (5120, 32), (6143, 25), (6144, 112), (8191, 74), (777, 24), (32, 56)]
 
 
 @pytest.fixture(scope="module")
@@ -51,6 +51,7 @@ def test_family_defaults_by_shape(axc):
     assert fam(5120, 16) == F.FAMILY_ONE_PASS_X  # 4097-6143 rows, up to 24 superblocks
     assert fam(5120, 32) == F.FAMILY_PERSISTENT  # 4097-6143 rows, 25-32 superblocks
     assert fam(6144, 112) == F.FAMILY_PERSISTENT  # 4097-8191 rows, 74+ superblocks
+    assert fam(1024, 32) == F.FAMILY_TILED  # up to 1024 rows of 24+ superblocks
     assert fam(4096, 129) == F.FAMILY_TILED
 
 
