@@ -278,8 +278,8 @@ class Variant:
     waves_per_workgroup: int = 0
     prefetch: int = 0
     nontemporal: int = 0
-    family: int = 0       # FAMILY_* (Q4_K matvec only); 0 = the shape's choice
-    sb_per_lane: int = 0  # one-pass families: superblocks a lane walks per row
+    family: int = 0       # FAMILY_* (Q4_K and Q4_0 matvec); 0 = the shape's choice
+    sb_per_lane: int = 0  # one-pass families: superblocks (Q4_0: octets) a lane walks per row
 
     def _c(self) -> _Variant:
         return _Variant(self.rows_per_wave, self.waves_per_workgroup, self.prefetch,

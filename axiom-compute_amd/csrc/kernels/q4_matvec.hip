@@ -355,9 +355,15 @@ __device__ __forceinline__ void q4k_flat_load_xc(__amdgpu_buffer_rsrc_t xr, uint
   for (int i = 0; i < 8 * XP; ++i) v[i] = buf_loadf4(xr, (tid + (uint32_t)i * NT) * 16u);
 }
 
-template <int NT, int XP>
-__device__ __forceinline__ void q4k_flat_stage_xc(float *xs, float *ss, uint32_t tid, uint32_t nsb,
-                                                  const float4 (&v)[8 * XP]) {
+// kQ40: `units` is the row's Q4_0 block count (8 float4 each), else its
+// superblock count (64 float4 each).  Q4_0 layout: the 256 elements of a unit
+// are an octet of 8 blocks, quarter c = w / 16 holds blocks 2c and 2c + 1, and
+// float4 i = w & 15 of the quarter (natural order: block 2c's low-nibble
+// elements, its high-nibble elements, then block 2c + 1's) goes to 16i + 4c
+// of the octet's slot; it meets high nibbles (scale 2^20) where i & 4.
+template <int NT, int XP, bool kQ40 = false>
+__device__ __forceinline__ void q4k_flat_stage_xc(float *xs, float *ss, uint32_t tid,
+                                                  uint32_t units, const float4 (&v)[8 * XP]) {
 #pragma unroll
   for (int i = 0; i < 8 * XP; ++i) {
     const uint32_t f = tid + (uint32_t)i * NT;
@@ -366,11 +372,19 @@ __device__ __forceinline__ void q4k_flat_stage_xc(float *xs, float *ss, uint32_t
     s += dpp_mov<0xB1>(s);  // quad_perm [1,0,3,2]
     s += dpp_mov<0x4E>(s);  // quad_perm [2,3,0,1]
     s += dpp_mov<0x141>(s); // row_half_mirror: the 8-lane sum in every lane
-    if (f < nsb * 64u) {    // whole 8-lane groups: NT and 64 * nsb are multiples of 8
-      const uint32_t sb = f >> 6, w = f & 63u, c = w >> 4, part = (w >> 3) & 1u, t = w & 7u;
-      const float scale = part ? 1048576.0f : 16777216.0f;
-      *reinterpret_cast<float4 *>(xs + sb * kQ4kFlatSbFloats + part * 128u + 16u * t + 4u * c) =
-          make_float4(a.x * scale, a.y * scale, a.z * scale, a.w * scale);
+    // whole 8-lane groups: NT and the row's float4 count are multiples of 8
+    if (f < (kQ40 ? units * 8u : units * 64u)) {
+      if constexpr (kQ40) {
+        const uint32_t sb = f >> 6, w = f & 63u, c = w >> 4, i4 = w & 15u;
+        const float scale = (i4 & 4u) ? 1048576.0f : 16777216.0f;
+        *reinterpret_cast<float4 *>(xs + sb * kQ4kFlatSbFloats + 16u * i4 + 4u * c) =
+            make_float4(a.x * scale, a.y * scale, a.z * scale, a.w * scale);
+      } else {
+        const uint32_t sb = f >> 6, w = f & 63u, c = w >> 4, part = (w >> 3) & 1u, t = w & 7u;
+        const float scale = part ? 1048576.0f : 16777216.0f;
+        *reinterpret_cast<float4 *>(xs + sb * kQ4kFlatSbFloats + part * 128u + 16u * t + 4u * c) =
+            make_float4(a.x * scale, a.y * scale, a.z * scale, a.w * scale);
+      }
       if ((f & 7u) == 0u) ss[f >> 3] = s;
     }
   }
@@ -490,6 +504,99 @@ __device__ __forceinline__ void q4k_flat_compute(const Q4kFlatBuf<RPW, NS, kQ5> 
   }
 }
 
+// Q4_0 rows in the persistent and one-pass kernels: a row is read as octets
+// of 8 blocks (144 bytes and 256 weights, a Q4_K superblock's footprint), one
+// octet per lane group s, and quarter c of the group owns blocks 2c and
+// 2c + 1 (36 bytes at 36c: two 16-byte loads and a dword).  Rows of an even
+// block count keep every quarter 4-byte aligned; a quarter past the row's
+// last block computes nothing.
+template <int RPW, int PF>
+struct Q40FlatBuf {
+  uint4 a[PF][RPW], b[PF][RPW];
+  uint32_t c[PF][RPW];
+};
+
+template <int RPW, int PF, bool kNT>
+__device__ __forceinline__ void q4_0_flat_load(Q40FlatBuf<RPW, PF> &B, int p,
+                                               __amdgpu_buffer_rsrc_t qr, uint32_t row_bytes,
+                                               uint32_t bundle, uint32_t it, uint32_t s,
+                                               uint32_t c) {
+  const uint32_t q_off = (it * 8u + s) * (uint32_t)kQ4kSbBytes + 36u * c;
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const uint32_t off = (bundle * RPW + (uint32_t)r) * row_bytes + q_off;
+    B.a[p][r] = buf_load16<kNT>(qr, off);
+    B.b[p][r] = buf_load16<kNT>(qr, off + 16u);
+    B.c[p][r] = __builtin_amdgcn_raw_buffer_load_b32(qr, (int)(off + 32u), 0, kNT ? 2 : 0);
+  }
+}
+
+// Blocks 2c and 2c + 1 of octet sb for the RPW rows of slot p (live: the
+// quarter lies inside the row).  Block A is d = bytes 0-1 and qs = bytes
+// 2-17, block B d = bytes 18-19 and qs = bytes 20-35; each block adds
+// d * (sum q * x - 8 * sum x), its x staged pre-scaled for the
+// f16-subnormal nibbles and its plain sum in ss.
+template <int RPW, int NS>
+__device__ __forceinline__ void q4_0_flat_compute(const Q40FlatBuf<RPW, NS> &B, int p,
+                                                  const float *xs, const float *ss, uint32_t sb,
+                                                  uint32_t c, bool live, float (&acc)[RPW]) {
+  const float *xb = xs + sb * kQ4kFlatSbFloats + 4u * c;
+  float4 xv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) xv[i] = *reinterpret_cast<const float4 *>(xb + 16u * (uint32_t)i);
+  const float2 bsum = *reinterpret_cast<const float2 *>(ss + sb * 8u + 2u * c);
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const uint4 a = B.a[p][r], b = B.b[p][r];
+    const uint32_t qa[4] = {__builtin_amdgcn_alignbit(a.y, a.x, 16),
+                            __builtin_amdgcn_alignbit(a.z, a.y, 16),
+                            __builtin_amdgcn_alignbit(a.w, a.z, 16),
+                            __builtin_amdgcn_alignbit(b.x, a.w, 16)};
+    const uint32_t qb[4] = {b.y, b.z, b.w, B.c[p][r]};
+    float alo = 0.0f, ahi = 0.0f, blo = 0.0f, bhi = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      q4k_dword(qa[t], xv[t], xv[4 + t], alo, ahi);
+      q4k_dword(qb[t], xv[8 + t], xv[12 + t], blo, bhi);
+    }
+    const float v = __builtin_fmaf(f16_to_f32(a.x & 0xFFFFu), __builtin_fmaf(-8.0f, bsum.x, alo + ahi),
+                                   f16_to_f32(b.x >> 16) * __builtin_fmaf(-8.0f, bsum.y, blo + bhi));
+    acc[r] = live ? acc[r] + v : acc[r];
+  }
+}
+
+// The register slots, loads and compute of the flat layouts: Q4_K / Q5_K
+// superblocks, or Q4_0 octets (kQ40; `units` is then the row's block count).
+template <int RPW, int PF, bool kQ5, bool kQ40>
+struct FlatBufSel {
+  using type = Q4kFlatBuf<RPW, PF, kQ5>;
+};
+template <int RPW, int PF, bool kQ5>
+struct FlatBufSel<RPW, PF, kQ5, true> {
+  using type = Q40FlatBuf<RPW, PF>;
+};
+
+template <int RPW, int PF, bool kNT, bool kDual, bool kQ5, bool kQ40>
+__device__ __forceinline__ void flat_load(typename FlatBufSel<RPW, PF, kQ5, kQ40>::type &B, int p,
+                                          __amdgpu_buffer_rsrc_t qr, __amdgpu_buffer_rsrc_t qr2,
+                                          uint32_t row_bytes, uint32_t bundle, uint32_t it,
+                                          uint32_t s, uint32_t c) {
+  if constexpr (kQ40)
+    q4_0_flat_load<RPW, PF, kNT>(B, p, qr, row_bytes, bundle, it, s, c);
+  else
+    q4k_flat_load<RPW, PF, kNT, kDual, kQ5>(B, p, qr, qr2, row_bytes, bundle, it, s, c);
+}
+
+template <int RPW, int PF, bool kQ5, bool kQ40>
+__device__ __forceinline__ void flat_compute(const typename FlatBufSel<RPW, PF, kQ5, kQ40>::type &B,
+                                             int p, const float *xs, const float *ss, uint32_t sb,
+                                             uint32_t c, uint32_t units, float (&acc)[RPW]) {
+  if constexpr (kQ40)
+    q4_0_flat_compute<RPW, PF>(B, p, xs, ss, sb, c, sb * 8u + 2u * c < units, acc);
+  else
+    q4k_flat_compute<RPW, PF, kQ5>(B, p, xs, ss, sb, c, acc);
+}
+
 // Reduce the pair of bundles (bundle0, bundle0 + 1) that a wave finished and
 // store it: each half-wave's lanes hold one bundle's partial sums.
 template <int RPW, bool kDual>
@@ -534,9 +641,9 @@ __device__ __forceinline__ void q4k_flat_load_chunk(__amdgpu_buffer_rsrc_t xr, u
     v[i] = buf_loadf4(xr, (j * 512u + tid + (uint32_t)i * NT) * 16u);
 }
 
-template <int NT>
+template <int NT, bool kQ40 = false>
 __device__ __forceinline__ void q4k_flat_stage_chunk(float *xs, float *ss, uint32_t tid, uint32_t j,
-                                                     uint32_t nsb, const float4 (&v)[512 / NT]) {
+                                                     uint32_t units, const float4 (&v)[512 / NT]) {
 #pragma unroll
   for (int i = 0; i < 512 / NT; ++i) {
     const uint32_t f = j * 512u + tid + (uint32_t)i * NT;
@@ -545,11 +652,18 @@ __device__ __forceinline__ void q4k_flat_stage_chunk(float *xs, float *ss, uint3
     sm += dpp_mov<0xB1>(sm);
     sm += dpp_mov<0x4E>(sm);
     sm += dpp_mov<0x141>(sm);
-    if (f < nsb * 64u) {
-      const uint32_t sb = f >> 6, w = f & 63u, c = w >> 4, part = (w >> 3) & 1u, t = w & 7u;
-      const float scale = part ? 1048576.0f : 16777216.0f;
-      *reinterpret_cast<float4 *>(xs + sb * kQ4kFlatSbFloats + part * 128u + 16u * t + 4u * c) =
-          make_float4(a.x * scale, a.y * scale, a.z * scale, a.w * scale);
+    if (f < (kQ40 ? units * 8u : units * 64u)) {
+      if constexpr (kQ40) {
+        const uint32_t sb = f >> 6, w = f & 63u, c = w >> 4, i4 = w & 15u;
+        const float scale = (i4 & 4u) ? 1048576.0f : 16777216.0f;
+        *reinterpret_cast<float4 *>(xs + sb * kQ4kFlatSbFloats + 16u * i4 + 4u * c) =
+            make_float4(a.x * scale, a.y * scale, a.z * scale, a.w * scale);
+      } else {
+        const uint32_t sb = f >> 6, w = f & 63u, c = w >> 4, part = (w >> 3) & 1u, t = w & 7u;
+        const float scale = part ? 1048576.0f : 16777216.0f;
+        *reinterpret_cast<float4 *>(xs + sb * kQ4kFlatSbFloats + part * 128u + 16u * t + 4u * c) =
+            make_float4(a.x * scale, a.y * scale, a.z * scale, a.w * scale);
+      }
       if ((f & 7u) == 0u) ss[f >> 3] = sm;
     }
   }
@@ -570,7 +684,8 @@ __device__ __forceinline__ void q4k_flat_stage_chunk(float *xs, float *ss, uint3
 // leaves the memory pipe idle during it (A/B in one run, 14336 x 4096: 9.9
 // vs 10.5 us; Q6_K 4096 x 14336: 12.5 vs 13.4-13.9 us).  The one-pass kernel
 // below is this order unrolled over a compile-time trip count.
-template <int RPW, int NW, int PF, bool kNT, int XP, bool kDual = false, bool kQ5 = false>
+template <int RPW, int NW, int PF, bool kNT, int XP, bool kDual = false, bool kQ5 = false,
+          bool kQ40 = false>
 __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
                                                 const uint8_t *__restrict__ q2,
                                                 const float *__restrict__ x,
@@ -579,6 +694,7 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
   constexpr int kRb = kDual ? RPW / 2 : RPW; // output rows per bundle
   static_assert(!kDual || RPW % 2 == 0, "the fused kernel pairs gate and up rows");
   static_assert(!(kDual && kQ5), "the fused gate/up kernel reads Q4_K");
+  static_assert(!(kQ40 && (kDual || kQ5)), "Q4_0 rows are a layout of their own");
   constexpr bool kEarly = PF == 1;        // refill before the compute, chunked x
   constexpr int kSlots = kEarly ? 2 : PF; // register slots
   constexpr int NT = NW * 64;
@@ -597,17 +713,21 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
     return;
   }
   const uint32_t n_my = W < n_pairs ? (n_pairs - 1u - W) / total_waves + 1u : 0u;
-  const uint32_t n_it = (nsb + 7u) >> 3;
+  // kQ40: nsb is the row's Q4_0 block count and the 256-weight units are
+  // its octets of 8 blocks.
+  const uint32_t n_units = kQ40 ? (nsb + 7u) >> 3 : nsb;
+  const uint32_t n_it = (n_units + 7u) >> 3;
   const uint32_t total = (n_my * n_it + (kSlots - 1)) / kSlots * kSlots;
   // The host guarantees n_rows * row_bytes < 2^32 for this kernel.
-  const uint32_t row_bytes = nsb * (kQ5 ? kQ5kSbBytes : (uint32_t)kQ4kSbBytes);
+  const uint32_t row_bytes =
+      nsb * (kQ40 ? (uint32_t)kQ4_0BlockBytes : kQ5 ? kQ5kSbBytes : (uint32_t)kQ4kSbBytes);
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(q, n_rows * row_bytes);
   const __amdgpu_buffer_rsrc_t qr2 = kDual ? make_rsrc(q2, n_rows * row_bytes) : qr;
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, nsb * 1024u);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, nsb * (kQ40 ? 128u : 1024u));
   float *xs = lds;
-  float *ss = lds + nsb * kQ4kFlatSbFloats;
+  float *ss = lds + n_units * kQ4kFlatSbFloats;
 
-  Q4kFlatBuf<RPW, kSlots, kQ5> B;
+  typename FlatBufSel<RPW, kSlots, kQ5, kQ40>::type B;
   uint32_t l_pi = 0, l_it = 0; // load cursor: pair index (of this wave) and iteration
   uint32_t c_pi = 0, c_it = 0; // compute cursor
   float acc[RPW];
@@ -617,13 +737,14 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
   // pair they read zeros or bytes whose results are never used).
   auto load_next = [&](int p) {
     const uint32_t bundle = 2u * (W + l_pi * total_waves) + half;
-    q4k_flat_load<RPW, kSlots, kNT, kDual, kQ5>(B, p, qr, qr2, row_bytes, bundle, l_it, s, c);
+    flat_load<RPW, kSlots, kNT, kDual, kQ5, kQ40>(B, p, qr, qr2, row_bytes, bundle, l_it, s, c);
     if (++l_it == n_it) { l_it = 0; ++l_pi; }
   };
   // Compute the current iteration from slot p and advance the compute cursor.
   auto compute = [&](int p) {
     const uint32_t sb = c_it * 8u + s;
-    if (c_pi < n_my && sb < nsb) q4k_flat_compute<RPW, kSlots, kQ5>(B, p, xs, ss, sb, c, acc);
+    if (c_pi < n_my && sb < n_units)
+      flat_compute<RPW, kSlots, kQ5, kQ40>(B, p, xs, ss, sb, c, nsb, acc);
     if (++c_it == n_it) { // a bundle pair is complete: reduce and store
       if (c_pi < n_my)
         q4k_flat_store<RPW, kDual>(acc, 2u * (W + c_pi * total_waves), lane, n_rows, y);
@@ -641,8 +762,8 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
     const __amdgpu_buffer_rsrc_t none = make_rsrc(q, 0u);
     auto load_first = [&](int p, uint32_t it) {
       const bool in = it < n_it;
-      q4k_flat_load<RPW, kSlots, kNT, kDual, kQ5>(B, p, in ? qr : none, in ? qr2 : none,
-                                                  row_bytes, bundle0, it, s, c);
+      flat_load<RPW, kSlots, kNT, kDual, kQ5, kQ40>(B, p, in ? qr : none, in ? qr2 : none,
+                                                    row_bytes, bundle0, it, s, c);
     };
     float4 xv[2][512 / NT];
     q4k_flat_load_chunk<NT>(xr, tid, 0u, xv[0]);
@@ -650,18 +771,18 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
     const uint32_t n1 = (n_it + 1u) & ~1u;
     uint32_t j = 0;
     do {
-      q4k_flat_stage_chunk<NT>(xs, ss, tid, j, nsb, xv[0]);
+      q4k_flat_stage_chunk<NT, kQ40>(xs, ss, tid, j, nsb, xv[0]);
       q4k_flat_load_chunk<NT>(xr, tid, j + 1u, xv[1]);
       load_first(1, j + 1u);
       __syncthreads();
-      if (n_my > 0 && j * 8u + s < nsb)
-        q4k_flat_compute<RPW, kSlots, kQ5>(B, 0, xs, ss, j * 8u + s, c, acc);
-      q4k_flat_stage_chunk<NT>(xs, ss, tid, j + 1u, nsb, xv[1]);
+      if (n_my > 0 && j * 8u + s < n_units)
+        flat_compute<RPW, kSlots, kQ5, kQ40>(B, 0, xs, ss, j * 8u + s, c, nsb, acc);
+      q4k_flat_stage_chunk<NT, kQ40>(xs, ss, tid, j + 1u, nsb, xv[1]);
       q4k_flat_load_chunk<NT>(xr, tid, j + 2u, xv[0]);
       load_first(0, j + 2u);
       __syncthreads();
-      if (n_my > 0 && (j + 1u) * 8u + s < nsb)
-        q4k_flat_compute<RPW, kSlots, kQ5>(B, 1, xs, ss, (j + 1u) * 8u + s, c, acc);
+      if (n_my > 0 && (j + 1u) * 8u + s < n_units)
+        flat_compute<RPW, kSlots, kQ5, kQ40>(B, 1, xs, ss, (j + 1u) * 8u + s, c, nsb, acc);
       j += 2u;
     } while (j < n1);
     if (n_my > 0) q4k_flat_store<RPW, kDual>(acc, 2u * W, lane, n_rows, y);
@@ -682,7 +803,7 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
     // Prologue: x requests first, then (for long rows once x has arrived) the
     // weight prefetch, then the LDS writes.  8 * XP float4 of x per thread (a
     // sub-block's worth per XP): the host launches this kernel only when
-    // nsb * 8 <= XP * NW * 64.
+    // nsb * 8 <= XP * NW * 64 (Q4_0: nsb <= XP * NW * 64 blocks).
     float4 xv[8 * XP];
     q4k_flat_load_xc<NT, XP>(xr, tid, xv);
     // For long rows, let x arrive before the weight prefetch goes out: every
@@ -691,12 +812,12 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
     // 0.3 us less per launch on 4096 x 14336, 0.2 us more on 4096 x 4096,
     // where x is 16 KiB).
     __builtin_amdgcn_sched_barrier(0);
-    if (nsb >= kWaitXMinSb) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (n_units >= kWaitXMinSb) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int p = 0; p < PF; ++p) load_next(p);
     __builtin_amdgcn_sched_barrier(0);
-    q4k_flat_stage_xc<NT, XP>(xs, ss, tid, nsb, xv);
+    q4k_flat_stage_xc<NT, XP, kQ40>(xs, ss, tid, nsb, xv);
     __syncthreads();
     for (uint32_t j0 = 0; j0 < total; j0 += PF) {
 #pragma unroll
@@ -735,7 +856,8 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
 // stream of another (A/B in one run, 14336 x 4096: 8.27-8.40 vs 8.78-9.00
 // us), and costs where one workgroup per CU waits for all of x (4096 x 14336:
 // 8.64-8.70 vs 8.12-8.22 us).
-template <int NIT, bool kDual = false, bool kQ5 = false, bool kWhole = false, int XD = 1>
+template <int NIT, bool kDual = false, bool kQ5 = false, bool kWhole = false, int XD = 1,
+          bool kQ40 = false>
 __device__ __forceinline__ void q4k_matvec_one(const uint8_t *__restrict__ q,
                                                const uint8_t *__restrict__ q2,
                                                const float *__restrict__ x, float *__restrict__ y,
@@ -748,19 +870,23 @@ __device__ __forceinline__ void q4k_matvec_one(const uint8_t *__restrict__ q,
   const uint32_t G = lane >> 2, half = G >> 3, s = G & 7u, c = lane & 3u;
   const uint32_t W = blockIdx.x * NW + wave;
   const bool mine = W < (n_rows + 1u) >> 1; // this wave has a pair of rows
-  const uint32_t row_bytes = nsb * (kQ5 ? kQ5kSbBytes : (uint32_t)kQ4kSbBytes);
+  static_assert(!(kQ40 && (kDual || kQ5)), "Q4_0 rows are a layout of their own");
+  // kQ40: nsb is the row's Q4_0 block count, read as octets of 8 blocks.
+  const uint32_t n_units = kQ40 ? (nsb + 7u) >> 3 : nsb;
+  const uint32_t row_bytes =
+      nsb * (kQ40 ? (uint32_t)kQ4_0BlockBytes : kQ5 ? kQ5kSbBytes : (uint32_t)kQ4kSbBytes);
   const __amdgpu_buffer_rsrc_t qr = make_rsrc(q, n_rows * row_bytes);
   const __amdgpu_buffer_rsrc_t qr2 = kDual ? make_rsrc(q2, n_rows * row_bytes) : qr;
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, nsb * 1024u);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, nsb * (kQ40 ? 128u : 1024u));
   float *xs = lds;
-  float *ss = lds + nsb * kQ4kFlatSbFloats;
+  float *ss = lds + n_units * kQ4kFlatSbFloats;
   const uint32_t bundle = 2u * W + half;
-  Q4kFlatBuf<RPW, 2, kQ5> B;
+  typename FlatBufSel<RPW, 2, kQ5, kQ40>::type B;
   float acc[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
   if constexpr (kWhole) {
-    q4k_flat_load<RPW, 2, false, kDual, kQ5>(B, 0, qr, qr2, row_bytes, bundle, 0u, s, c);
+    flat_load<RPW, 2, false, kDual, kQ5, kQ40>(B, 0, qr, qr2, row_bytes, bundle, 0u, s, c);
 #pragma unroll
     for (int g = 0; g < NIT; g += 4) { // x chunks in groups of 4 (16 VGPRs)
       float4 xg[4][512 / NT];
@@ -769,17 +895,17 @@ __device__ __forceinline__ void q4k_matvec_one(const uint8_t *__restrict__ q,
         q4k_flat_load_chunk<NT>(xr, tid, (uint32_t)j, xg[j - g]);
 #pragma unroll
       for (int j = g; j < g + 4 && j < NIT; ++j)
-        q4k_flat_stage_chunk<NT>(xs, ss, tid, (uint32_t)j, nsb, xg[j - g]);
+        q4k_flat_stage_chunk<NT, kQ40>(xs, ss, tid, (uint32_t)j, nsb, xg[j - g]);
     }
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < NIT; ++j) {
       const int p = j & 1;
       if (j + 1 < NIT)
-        q4k_flat_load<RPW, 2, false, kDual, kQ5>(B, p ^ 1, qr, qr2, row_bytes, bundle,
-                                                 (uint32_t)(j + 1), s, c);
+        flat_load<RPW, 2, false, kDual, kQ5, kQ40>(B, p ^ 1, qr, qr2, row_bytes, bundle,
+                                                   (uint32_t)(j + 1), s, c);
       const uint32_t sb = (uint32_t)j * 8u + s;
-      if (mine && sb < nsb) q4k_flat_compute<RPW, 2, kQ5>(B, p, xs, ss, sb, c, acc);
+      if (mine && sb < n_units) flat_compute<RPW, 2, kQ5, kQ40>(B, p, xs, ss, sb, c, nsb, acc);
     }
     if (mine) q4k_flat_store<RPW, kDual>(acc, 2u * W, lane, n_rows, y);
     return;
@@ -797,20 +923,20 @@ __device__ __forceinline__ void q4k_matvec_one(const uint8_t *__restrict__ q,
   constexpr int XB = XD + 1;
   float4 xq[XB][512 / NT];
   q4k_flat_load_chunk<NT>(xr, tid, 0u, xq[0]);
-  q4k_flat_load<RPW, 2, false, kDual, kQ5>(B, 0, qr, qr2, row_bytes, bundle, 0u, s, c);
+  flat_load<RPW, 2, false, kDual, kQ5, kQ40>(B, 0, qr, qr2, row_bytes, bundle, 0u, s, c);
 #pragma unroll
   for (int k = 1; k < XD; ++k) q4k_flat_load_chunk<NT>(xr, tid, (uint32_t)k, xq[k]);
 #pragma unroll
   for (int j = 0; j < NIT; ++j) {
     const int p = j & 1;
-    q4k_flat_stage_chunk<NT>(xs, ss, tid, (uint32_t)j, nsb, xq[j % XB]);
+    q4k_flat_stage_chunk<NT, kQ40>(xs, ss, tid, (uint32_t)j, nsb, xq[j % XB]);
     if (j + XD < NIT) q4k_flat_load_chunk<NT>(xr, tid, (uint32_t)(j + XD), xq[(j + XD) % XB]);
     if (j + 1 < NIT) // next iteration's weights, before the compute
-      q4k_flat_load<RPW, 2, false, kDual, kQ5>(B, p ^ 1, qr, qr2, row_bytes, bundle,
-                                               (uint32_t)(j + 1), s, c);
+      flat_load<RPW, 2, false, kDual, kQ5, kQ40>(B, p ^ 1, qr, qr2, row_bytes, bundle,
+                                                 (uint32_t)(j + 1), s, c);
     __syncthreads();
     const uint32_t sb = (uint32_t)j * 8u + s;
-    if (mine && sb < nsb) q4k_flat_compute<RPW, 2, kQ5>(B, p, xs, ss, sb, c, acc);
+    if (mine && sb < n_units) flat_compute<RPW, 2, kQ5, kQ40>(B, p, xs, ss, sb, c, nsb, acc);
   }
   if (mine) q4k_flat_store<RPW, kDual>(acc, 2u * W, lane, n_rows, y);
 }
@@ -2041,6 +2167,86 @@ AXH_Q4_0_MATVEC(1, 1)
 AXH_Q4_0_MATVEC(1, 4)
 AXH_Q4_0_MATVEC(2, 4)
 AXH_Q4_0_MATVEC(4, 4)
+
+// Q4_0 through the Q4_K persistent and one-pass kernels (kQ40: octets of 8
+// blocks in place of superblocks, 64 blocks per iteration).
+// axh_q4_0_matvec_flat_r{RPW}_w{NW}_p{PF}: persistent, grid-strided pairs of
+// RPW-row bundles; PF 1 stages x chunk by chunk with early refill, PF 2 stages
+// it whole first (XP * NW * 64 blocks at most).
+#define AXH_Q4_0_MATVEC_FLAT(RPW, NW, PF, XP)                                                    \
+  extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
+      axh_q4_0_matvec_flat_r##RPW##_w##NW##_p##PF##_x##XP(const uint8_t *__restrict__ q,         \
+                                                          const float *__restrict__ x,           \
+                                                          float *__restrict__ y,                 \
+                                                          AXH_ROWS_ARGS) { AXH_ROWS_UNPACK;      \
+    extern __shared__ float axh_lds_dyn[];                                                       \
+    q4k_matvec_flat<RPW, NW, PF, false, XP, false, false, true>(q, q, x, y, a.n_rows,            \
+                                                                a.units_per_row, axh_lds_dyn);   \
+  }
+AXH_Q4_0_MATVEC_FLAT(1, 4, 1, 1)
+AXH_Q4_0_MATVEC_FLAT(1, 8, 1, 1)
+AXH_Q4_0_MATVEC_FLAT(2, 4, 1, 1)
+AXH_Q4_0_MATVEC_FLAT(2, 8, 1, 1)
+AXH_Q4_0_MATVEC_FLAT(1, 8, 2, 1)
+AXH_Q4_0_MATVEC_FLAT(2, 4, 2, 2)
+AXH_Q4_0_MATVEC_FLAT(1, 16, 2, 1)
+
+// axh_q4_0_matvec_one{,x,p}_i{NIT}: one workgroup of 8 waves per 16 rows of
+// 64 * (NIT - 1) < nb <= 64 * NIT blocks (x chunk by chunk, x whole, x two
+// chunks ahead).
+#define AXH_Q4_0_MATVEC_ONE(NIT)                                                                 \
+  extern "C" __global__ void __launch_bounds__(512)                                              \
+      axh_q4_0_matvec_one_i##NIT(const uint8_t *__restrict__ q, const float *__restrict__ x,     \
+                                 float *__restrict__ y, AXH_ROWS_ARGS) { AXH_ROWS_UNPACK;        \
+    extern __shared__ float axh_lds_dyn[];                                                       \
+    q4k_matvec_one<NIT, false, false, false, 1, true>(q, q, x, y, a.n_rows, a.units_per_row,     \
+                                                      axh_lds_dyn);                              \
+  }                                                                                              \
+  extern "C" __global__ void __launch_bounds__(512)                                              \
+      axh_q4_0_matvec_onex_i##NIT(const uint8_t *__restrict__ q, const float *__restrict__ x,    \
+                                  float *__restrict__ y, AXH_ROWS_ARGS) { AXH_ROWS_UNPACK;       \
+    extern __shared__ float axh_lds_dyn[];                                                       \
+    q4k_matvec_one<NIT, false, false, true, 1, true>(q, q, x, y, a.n_rows, a.units_per_row,      \
+                                                     axh_lds_dyn);                               \
+  }
+#define AXH_Q4_0_MATVEC_ONEP(NIT)                                                                \
+  extern "C" __global__ void __launch_bounds__(512)                                              \
+      axh_q4_0_matvec_onep_i##NIT(const uint8_t *__restrict__ q, const float *__restrict__ x,    \
+                                  float *__restrict__ y, AXH_ROWS_ARGS) { AXH_ROWS_UNPACK;       \
+    extern __shared__ float axh_lds_dyn[];                                                       \
+    q4k_matvec_one<NIT, false, false, false, 2, true>(q, q, x, y, a.n_rows, a.units_per_row,     \
+                                                      axh_lds_dyn);                              \
+  }
+AXH_Q4_0_MATVEC_ONE(1)
+AXH_Q4_0_MATVEC_ONE(2)
+AXH_Q4_0_MATVEC_ONE(3)
+AXH_Q4_0_MATVEC_ONE(4)
+AXH_Q4_0_MATVEC_ONE(5)
+AXH_Q4_0_MATVEC_ONE(6)
+AXH_Q4_0_MATVEC_ONE(7)
+AXH_Q4_0_MATVEC_ONE(8)
+AXH_Q4_0_MATVEC_ONE(9)
+AXH_Q4_0_MATVEC_ONE(10)
+AXH_Q4_0_MATVEC_ONE(11)
+AXH_Q4_0_MATVEC_ONE(12)
+AXH_Q4_0_MATVEC_ONE(13)
+AXH_Q4_0_MATVEC_ONE(14)
+AXH_Q4_0_MATVEC_ONE(15)
+AXH_Q4_0_MATVEC_ONE(16)
+AXH_Q4_0_MATVEC_ONEP(3)
+AXH_Q4_0_MATVEC_ONEP(4)
+AXH_Q4_0_MATVEC_ONEP(5)
+AXH_Q4_0_MATVEC_ONEP(6)
+AXH_Q4_0_MATVEC_ONEP(7)
+AXH_Q4_0_MATVEC_ONEP(8)
+AXH_Q4_0_MATVEC_ONEP(9)
+AXH_Q4_0_MATVEC_ONEP(10)
+AXH_Q4_0_MATVEC_ONEP(11)
+AXH_Q4_0_MATVEC_ONEP(12)
+AXH_Q4_0_MATVEC_ONEP(13)
+AXH_Q4_0_MATVEC_ONEP(14)
+AXH_Q4_0_MATVEC_ONEP(15)
+AXH_Q4_0_MATVEC_ONEP(16)
 
 // Reference-compatible entry point for examples/q4_0_dequant_matvec.axc
 // (bindings q=0, x=1, y=2; push constant n_blocks: u32 @0; 1x1x1 of 64).

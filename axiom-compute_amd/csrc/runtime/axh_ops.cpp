@@ -104,6 +104,13 @@ constexpr MatvecVariant kQ6kVariants[] = {
 // axh_q4_0_matvec_r{rpw}_w{nw} (prefetch and cache policy are not holes for Q4_0).
 constexpr MatvecVariant kQ4_0Variants[] = {
     {1, 1, 1, 2, 1}, {1, 4, 1, 2, 1}, {2, 4, 1, 2, 1}, {4, 4, 1, 2, 1}};
+// axh_q4_0_matvec_flat_r{rpw}_w{nw}_p{pf}_x{xp}: the Q4_K persistent kernel
+// over octets of 8 Q4_0 blocks (normal loads only).  Keep in sync with the
+// AXH_Q4_0_MATVEC_FLAT list in q4_matvec.hip.
+constexpr MatvecVariant kQ4_0FlatVariants[] = {
+    {1, 4, 1, 2, 1}, {1, 8, 1, 2, 1}, {2, 4, 1, 2, 1}, {2, 8, 1, 2, 1},
+    {1, 8, 2, 2, 1}, {2, 4, 2, 2, 2}, {1, 16, 2, 2, 1}};
+constexpr uint32_t kQ4_0FlatRounds = 2; // persistent Q4_0 grid: resident workgroups x 2
 
 constexpr uint32_t kQ4kMaxTileSb = 128;   // tiled kernel: 128 * 1088 B = 136 KiB of LDS
 constexpr uint32_t kQ4kFlatMaxSb = 128;   // persistent kernel: 128 * 1120 B = 140 KiB of LDS
@@ -246,10 +253,18 @@ static MatvecVariant q4k_default(uint32_t n_rows, uint32_t nsb) {
   return {1, 16, 2, 2, 1};
 }
 
+// The LDS-tiled Q4_0 kernel's rows per wave (4 waves per workgroup), for the
+// rows the octet kernels do not take (odd block counts, rows of more than
+// 1024 blocks, fewer than 32 rows).  A/B in one run, us per call through the
+// library's launch loop (one wave per workgroup was the default below 4096
+// rows): 2048 x 448 blocks r1 w4 9.68 vs r1 w1 32.27, 256 x 160 3.99 vs 4.61;
+// 4096 x 160 r1 6.98 vs r2 7.31, 4096 x 448 r2 13.82 vs r1 17.70; 8192 x 128
+// r2 6.34 vs r4 7.35, 8192 x 448 r4 21.77 vs r2 25.71; 14336 x 256 r4 17.57
+// vs r2 20.18.
 static MatvecVariant q4_0_default(uint32_t n_rows, uint32_t nb) {
-  (void)nb;
-  if (n_rows >= 4096) return {2, 4, 1, 2, 1};
-  return {1, 1, 1, 2, 1};
+  if (n_rows < 4096) return {1, 4, 1, 2, 1};
+  if (n_rows < 8192 || (n_rows < 14336 && nb <= 256)) return {2, 4, 1, 2, 1};
+  return {4, 4, 1, 2, 1};
 }
 
 // Rows below this count (with at most kQ4kColsMaxSb superblocks) go to the
@@ -1035,41 +1050,192 @@ axh_status axh_matvec_ggml(axh_context *ctx, uint32_t ggml_type, const void *q, 
   }
 }
 
-// Q4_0 rows of at most 128 blocks, an even count: the column kernel (lane =
-// block pair, x in VGPRs, one row per batch: measured 2.7 us at 256 x 4096
-// against 3.3 us for two or four rows per batch and for the LDS-staged
-// kernel) unless a variant is requested.
+// The Q4_0 column kernel takes rows of at most 128 blocks, an even count
+// (lane = block pair, x in VGPRs, one row per batch: measured 2.7 us at 256 x
+// 4096 against 3.3 us for two or four rows per batch).
 constexpr uint32_t kQ4_0ColsMaxB = 128;
 constexpr uint32_t kQ4_0ColsRb = 1;
 
-static bool q4_0_use_cols(uint32_t n_rows, uint32_t nb, const axh_q4_variant *variant) {
-  return !variant && nb >= 2 && nb <= kQ4_0ColsMaxB && (nb & 1u) == 0 &&
+static bool q4_0_cols_fit(uint32_t n_rows, uint32_t nb) {
+  return nb >= 2 && nb <= kQ4_0ColsMaxB && (nb & 1u) == 0 &&
          (uint64_t)n_rows * nb * 18u < 0xFFFFFF00ull;
 }
 
-static const MatvecVariant *pick_q4_0(uint32_t n_rows, uint32_t blocks_per_row,
-                                      const axh_q4_variant *variant) {
-  axh_q4_variant vv{};
-  if (variant) vv = *variant;
-  vv.prefetch = 1;
-  vv.nontemporal = 2;
-  return find_variant(kQ4_0Variants, axh_q4_0_matvec_variant_count(), &vv,
-                      q4_0_default(n_rows, blocks_per_row));
+// The persistent and one-pass kernels read a row as octets of 8 blocks (the
+// Q4_K kernels' layout, 1120 bytes of LDS per octet of x): rows of an even
+// block count (every quarter-octet 4-byte aligned), at most 1024 blocks,
+// matrices below 4 GiB.
+constexpr uint32_t kQ4_0MaxOctets = 128;
+constexpr uint32_t kQ4_0OneMaxIt = 16; // one-pass kernels: 1-16 steps of 64 blocks
+
+static bool q4_0_octets_fit(uint32_t n_rows, uint32_t nb) {
+  return nb >= 2 && (nb & 1u) == 0 && (nb + 7u) / 8u <= kQ4_0MaxOctets &&
+         (uint64_t)n_rows * nb * 18u < 0xFFFFFFFFull;
+}
+
+// Persistent Q4_0 default: one row per bundle, 8 waves, early refill (A/B in
+// one run, us per call: 28672 x 448 blocks 42.5 vs 47.8 for 4 waves and 42.9
+// for prefetch 2; 4096 x 1024 16.1 vs 27.4 for 4 waves).
+static MatvecVariant q4_0_flat_default(uint32_t n_rows, uint32_t nb) {
+  (void)n_rows;
+  (void)nb;
+  return {1, 8, 1, 2, 1};
+}
+
+// Default Q4_0 family per shape, from A/B runs (interleaved launch loops, us
+// per call, rotated weights; the LDS-tiled kernel's figures are its best row
+// count):
+// - at most 512 rows of at most 128 blocks: the column kernel, ahead in the
+//   kernel trace (256 x 128 blocks 2.79 us against 3.50 tiled and 3.64 one
+//   pass) and over 1000 sustained calls (2.88 vs 3.01 and 3.16), though not
+//   in 20-call loops (3.55 vs 3.01 and 3.04);
+// - fewer than 32 rows otherwise: tiled (16 x 1024 blocks 11.4 vs 12.3 one
+//   pass, 8 x 344 4.90 vs 4.91);
+// - one pass from 32 rows (the Q4_K one-pass kernel over octets): 4096 x 448
+//   8.1 vs 13.7 tiled, 14336 x 448 24.0 vs 40.8, 4096 x 128 3.9 vs 4.7 tiled
+//   and 6.0 column, 1024 x 1024 13.5 vs 14.0, 256 x 160 3.8 vs 4.3; x staged
+//   whole for rows of 65-128 blocks from 6144 rows (8192 x 128 5.22 vs 5.53,
+//   14336 x 128 8.34 vs 8.71, 128256 x 128 49.7 vs 50.8; 4096 x 128 4.01 vs
+//   3.93), x two chunks ahead for 14-16 steps from 4096 rows (4096 x 1024
+//   15.9 vs 16.5, 8192 x 1024 31.3 vs 31.6);
+// - persistent for more than 16384 rows of more than 256 blocks (28672 x 448
+//   42.5 vs 44.1-44.7 one pass; 28672 x 256 25.3 vs 24.7 stays one pass).
+constexpr uint32_t kQ4_0ColsMaxRows = 512, kQ4_0FewRows = 32;
+constexpr uint32_t kQ4_0OneXMinRows = 6144;
+constexpr uint32_t kQ4_0OnePMinIt = 14, kQ4_0OnePMinRows = 4096;
+constexpr uint32_t kQ4_0FlatMinRows = 16385, kQ4_0FlatMinB = 257;
+
+static uint32_t q4_0_default_family(uint32_t n_rows, uint32_t nb) {
+  if (n_rows <= kQ4_0ColsMaxRows && q4_0_cols_fit(n_rows, nb)) return AXH_Q4K_FAMILY_COLUMNS;
+  if (n_rows < kQ4_0FewRows || !q4_0_octets_fit(n_rows, nb)) return AXH_Q4K_FAMILY_TILED;
+  if (n_rows >= kQ4_0FlatMinRows && nb >= kQ4_0FlatMinB) return AXH_Q4K_FAMILY_PERSISTENT;
+  if ((nb + 63u) / 64u == 2u && n_rows >= kQ4_0OneXMinRows) return AXH_Q4K_FAMILY_ONE_PASS_X;
+  return AXH_Q4K_FAMILY_ONE_PASS;
+}
+
+// Kernel, LDS and grid of one Q4_0 matvec call.  family 0 with a hole set
+// means the LDS-tiled kernel (axh_q4_0_matvec_r*_w*), the only family with
+// holes before the others were built; with no hole set, the shape's default.
+static axh_status plan_q4_0(uint32_t n_rows, uint32_t nb, const axh_q4_variant *variant,
+                            Q4kPlan *p) {
+  const bool holes = variant && (variant->rows_per_wave || variant->waves_per_workgroup ||
+                                 variant->prefetch || variant->nontemporal);
+  uint32_t fam = variant ? variant->family : 0u;
+  if (variant && variant->sb_per_lane && fam != AXH_Q4K_FAMILY_ONE_PASS &&
+      fam != AXH_Q4K_FAMILY_ONE_PASS_X)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "sb_per_lane is a hole of the one-pass families only");
+  if (fam == AXH_Q4K_FAMILY_DEFAULT)
+    fam = holes ? AXH_Q4K_FAMILY_TILED : q4_0_default_family(n_rows, nb);
+  const uint32_t n_oct = (nb + 7u) / 8u;
+  switch (fam) {
+  case AXH_Q4K_FAMILY_COLUMNS: {
+    if (holes) return fail(AXH_ERR_INVALID_ARGUMENT, "the column family has no holes");
+    if (!q4_0_cols_fit(n_rows, nb))
+      return fail(AXH_ERR_INVALID_ARGUMENT,
+                  "the Q4_0 column family takes rows of 2-128 blocks, an even count");
+    std::snprintf(p->name, sizeof(p->name), "axh_q4_0_matvec_cols_r%u", kQ4_0ColsRb);
+    const uint32_t n_batches = (n_rows + kQ4_0ColsRb - 1) / kQ4_0ColsRb;
+    p->nw = 1;
+    p->lds = 0;
+    p->flat = false;
+    p->units = n_batches < 2048u ? n_batches : 2048u;
+    p->args = RowsArgs{n_rows, nb, 0, 0};
+    return ok();
+  }
+  case AXH_Q4K_FAMILY_PERSISTENT: {
+    if (variant && variant->nontemporal == 1)
+      return fail(AXH_ERR_INVALID_ARGUMENT, "no non-temporal Q4_0 variant is compiled");
+    if (!q4_0_octets_fit(n_rows, nb))
+      return fail(AXH_ERR_INVALID_ARGUMENT,
+                  "the Q4_0 persistent family takes rows of 2-1024 blocks, an even count, "
+                  "below 4 GiB");
+    const MatvecVariant dflt = q4_0_flat_default(n_rows, nb);
+    const uint32_t want_nw =
+        variant && variant->waves_per_workgroup ? variant->waves_per_workgroup : dflt.nw;
+    const uint32_t min_xp = (nb + want_nw * 64u - 1u) / (want_nw * 64u);
+    const MatvecVariant *v =
+        find_variant(kQ4_0FlatVariants, sizeof(kQ4_0FlatVariants) / sizeof(kQ4_0FlatVariants[0]),
+                     variant, dflt, min_xp);
+    if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_0 persistent variant matches");
+    if (!staged_in_chunks(*v) && nb > v->xp * v->nw * 64u)
+      return fail(AXH_ERR_INVALID_ARGUMENT, "row too long for this variant's x staging");
+    std::snprintf(p->name, sizeof(p->name), "axh_q4_0_matvec_flat_r%u_w%u_p%u_x%u", v->rpw,
+                  v->nw, v->pf, v->xp);
+    p->nw = v->nw;
+    p->lds = n_oct * 1120u;
+    p->flat = true;
+    const uint32_t bundles = (n_rows + v->rpw - 1) / v->rpw;
+    p->units = ((bundles + 1) / 2 + v->nw - 1) / v->nw;
+    p->args = RowsArgs{n_rows, nb, nb, 0};
+    return ok();
+  }
+  case AXH_Q4K_FAMILY_ONE_PASS:
+  case AXH_Q4K_FAMILY_ONE_PASS_X: {
+    const uint32_t xd = variant ? variant->prefetch : 0u;
+    if (variant && (variant->rows_per_wave || variant->waves_per_workgroup || variant->nontemporal))
+      return fail(AXH_ERR_INVALID_ARGUMENT,
+                  "the one-pass families' holes are sb_per_lane and (one pass) prefetch");
+    if (xd && (fam == AXH_Q4K_FAMILY_ONE_PASS_X || xd > 2u))
+      return fail(AXH_ERR_INVALID_ARGUMENT,
+                  "one-pass prefetch is 1 or 2 x chunks ahead (none for the whole-x kernel)");
+    if (!q4_0_octets_fit(n_rows, nb))
+      return fail(AXH_ERR_INVALID_ARGUMENT,
+                  "the Q4_0 one-pass families take rows of 2-1024 blocks, an even count, "
+                  "below 4 GiB");
+    const uint32_t need = (nb + 63u) / 64u;
+    const uint32_t nit = variant && variant->sb_per_lane ? variant->sb_per_lane : need;
+    if (nit < need || nit > kQ4_0OneMaxIt)
+      return fail(AXH_ERR_INVALID_ARGUMENT,
+                  "Q4_0 one pass: sb_per_lane (steps of 64 blocks) must cover the row and be at "
+                  "most 16");
+    if (xd == 2u && nit < 3u)
+      return fail(AXH_ERR_INVALID_ARGUMENT, "x two chunks ahead needs three or more steps");
+    const bool two_ahead = fam == AXH_Q4K_FAMILY_ONE_PASS &&
+                           (xd == 2u || (xd == 0u && nit >= kQ4_0OnePMinIt &&
+                                         n_rows >= kQ4_0OnePMinRows));
+    std::snprintf(p->name, sizeof(p->name), "axh_q4_0_matvec_one%s_i%u",
+                  fam == AXH_Q4K_FAMILY_ONE_PASS_X ? "x" : two_ahead ? "p" : "", nit);
+    p->nw = 8;
+    p->lds = n_oct * 1120u;
+    p->flat = false; // one workgroup per 16 rows, all of them launched
+    p->units = (n_rows + 15u) / 16u;
+    p->args = RowsArgs{n_rows, nb, nb, 0};
+    return ok();
+  }
+  case AXH_Q4K_FAMILY_TILED: {
+    axh_q4_variant vv{};
+    if (variant) vv = *variant;
+    vv.prefetch = 1; // prefetch and cache policy are not holes of this kernel
+    vv.nontemporal = 2;
+    const MatvecVariant *v = find_variant(kQ4_0Variants, axh_q4_0_matvec_variant_count(), &vv,
+                                          q4_0_default(n_rows, nb));
+    if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_0 matvec variant matches");
+    std::snprintf(p->name, sizeof(p->name), "axh_q4_0_matvec_r%u_w%u", v->rpw, v->nw);
+    uint32_t tile = (nb + 127u) & ~127u;
+    if (tile == 0) tile = 128;
+    if (tile > kQ4_0MaxTileB) tile = kQ4_0MaxTileB;
+    p->nw = v->nw;
+    p->lds = tile * 132u;
+    p->flat = false;
+    const uint32_t rows_per_wg = v->rpw * v->nw;
+    p->units = (n_rows + rows_per_wg - 1) / rows_per_wg;
+    p->args = RowsArgs{n_rows, nb, tile, 0};
+    return ok();
+  }
+  default:
+    return fail(AXH_ERR_INVALID_ARGUMENT,
+                "Q4_0 takes the persistent, one-pass, column and tiled families");
+  }
 }
 
 axh_status axh_q4_0_matvec_kernel_name(uint32_t n_rows, uint32_t blocks_per_row,
                                        const axh_q4_variant *variant, char *buf, size_t cap) {
   if (!buf || cap == 0) return fail(AXH_ERR_INVALID_ARGUMENT, "buf is NULL");
-  if (reject_family(variant) != AXH_OK) return AXH_ERR_INVALID_ARGUMENT;
-  if (q4_0_use_cols(n_rows, blocks_per_row, variant)) {
-    const int n = std::snprintf(buf, cap, "axh_q4_0_matvec_cols_r%u", kQ4_0ColsRb);
-    if (n < 0 || (size_t)n >= cap) return fail(AXH_ERR_INVALID_ARGUMENT, "buf too small");
-    return ok();
-  }
-  const MatvecVariant *v = pick_q4_0(n_rows, blocks_per_row, variant);
-  if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_0 matvec variant matches");
-  const int n = std::snprintf(buf, cap, "axh_q4_0_matvec_r%u_w%u", v->rpw, v->nw);
-  if (n < 0 || (size_t)n >= cap) return fail(AXH_ERR_INVALID_ARGUMENT, "buf too small");
+  Q4kPlan p{};
+  axh_status s = plan_q4_0(n_rows, blocks_per_row, variant, &p);
+  if (s != AXH_OK) return s;
+  if (std::strlen(p.name) + 1 > cap) return fail(AXH_ERR_INVALID_ARGUMENT, "buf too small");
+  std::memcpy(buf, p.name, std::strlen(p.name) + 1);
   return ok();
 }
 
@@ -1084,39 +1250,22 @@ axh_status axh_q4_0_matvec(axh_context *ctx, const void *q, const float *x, floa
     return fail(AXH_ERR_INVALID_ARGUMENT, "blocks_per_row too large");
   if (((uintptr_t)q & 3u) || ((uintptr_t)x & 15u))
     return fail(AXH_ERR_INVALID_ARGUMENT, "q must be 4-byte and x 16-byte aligned");
-  if (reject_family(variant) != AXH_OK) return AXH_ERR_INVALID_ARGUMENT;
-  if (q4_0_use_cols(n_rows, blocks_per_row, variant)) {
-    const uint32_t rb = kQ4_0ColsRb;
-    char cname[64];
-    std::snprintf(cname, sizeof(cname), "axh_q4_0_matvec_cols_r%u", rb);
-    axh_kernel *k = nullptr;
-    axh_status s = builtin_kernel(ctx, cname, 3, sizeof(RowsArgs), 64u, &k);
-    if (s != AXH_OK) return s;
-    const uint32_t n_batches = (n_rows + rb - 1) / rb;
-    const uint32_t grid[3] = {n_batches < 2048u ? n_batches : 2048u, 1, 1};
-    RowsArgs a{n_rows, blocks_per_row, 0, 0};
-    void *bufs[3] = {const_cast<void *>(q), const_cast<float *>(x), y};
-    hipSetDevice(ctx->core->device);
-    s = launch_raw(k, grid, bufs, 3, &a, sizeof(a), 0, pick_stream(ctx, stream));
-    return s == AXH_OK ? ok() : s;
-  }
-  const MatvecVariant *v = pick_q4_0(n_rows, blocks_per_row, variant);
-  if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_0 matvec variant matches");
-  char name[64];
-  std::snprintf(name, sizeof(name), "axh_q4_0_matvec_r%u_w%u", v->rpw, v->nw);
-  axh_kernel *k = nullptr;
-  axh_status s = builtin_kernel(ctx, name, 3, sizeof(RowsArgs), v->nw * 64u, &k);
+  Q4kPlan p{};
+  axh_status s = plan_q4_0(n_rows, blocks_per_row, variant, &p);
   if (s != AXH_OK) return s;
-  uint32_t tile = (blocks_per_row + 127u) & ~127u;
-  if (tile == 0) tile = 128;
-  if (tile > kQ4_0MaxTileB) tile = kQ4_0MaxTileB;
-  const uint32_t lds = tile * 132u;
-  RowsArgs a{n_rows, blocks_per_row, tile, 0};
-  const uint32_t rows_per_wg = v->rpw * v->nw;
-  const uint32_t grid[3] = {(n_rows + rows_per_wg - 1) / rows_per_wg, 1, 1};
-  void *bufs[3] = {const_cast<void *>(q), const_cast<float *>(x), y};
+  if (p.lds > ctx->core->max_lds)
+    return fail(AXH_ERR_PIPELINE_LAYOUT, "LDS tile exceeds the device limit");
   hipSetDevice(ctx->core->device);
-  s = launch_raw(k, grid, bufs, 3, &a, sizeof(a), lds, pick_stream(ctx, stream));
+  axh_kernel *k = nullptr;
+  s = builtin_kernel(ctx, p.name, 3, sizeof(RowsArgs), p.nw * 64u, &k);
+  if (s != AXH_OK) return s;
+  uint32_t grid[3] = {p.units, 1, 1};
+  if (p.flat) { // persistent: at most kQ4_0FlatRounds rounds of resident workgroups
+    const uint32_t resident = kQ4_0FlatRounds * occupancy(ctx, k, p.lds) * ctx->core->cu_count;
+    if (resident < grid[0]) grid[0] = resident;
+  }
+  void *bufs[3] = {const_cast<void *>(q), const_cast<float *>(x), y};
+  s = launch_raw(k, grid, bufs, 3, &p.args, sizeof(p.args), p.lds, pick_stream(ctx, stream));
   return s == AXH_OK ? ok() : s;
 }
 

@@ -58,6 +58,9 @@ WORKLOADS = {
     "down6": ("q6k", 4096, 56, 0.5, "Llama-3-8B ffn_down as Q6_K, not a BASELINE config"),
     "v6": ("q6k", 1024, 16, 1.0, "Llama-3-8B attn_v (8 KV heads) as Q6_K, not a BASELINE config"),
     "up5": ("q5k", 14336, 16, 1.0, "Llama-3-8B ffn_up as Q5_K, not a BASELINE config"),
+    # Q4_0 checkpoints store every projection in it: the same shapes as Q4_0
+    "down0": ("q4_0", 4096, 448, 0.5, "Llama-3-8B ffn_down as Q4_0, not a BASELINE config"),
+    "head0": ("q4_0", 128256, 128, 1.0, "Llama-3-8B output head as Q4_0, not a BASELINE config"),
 }
 KQ_IDS = {"q5k": 13, "q6k": 14}
 

@@ -204,8 +204,22 @@ void axh_event_destroy(axh_event *ev);
  * 25-32 superblocks and 4097-8191 rows of 74 or more, which take the
  * persistent family; persistent beyond,
  * tiled for rows of more than 128 superblocks.  Every default is a hole
- * assignment.  The Q4_0 and gate/up
- * operations take the persistent holes only (family = sb_per_lane = 0).
+ * assignment.  The gate/up operation
+ * takes the persistent holes only (family = sb_per_lane = 0).
+ * Q4_0 takes family PERSISTENT (axh_q4_0_matvec_flat_r*_w*_p*_x*: the Q4_K
+ * persistent kernel over octets of 8 blocks; holes rows_per_wave,
+ * waves_per_workgroup, prefetch), ONE_PASS / ONE_PASS_X
+ * (axh_q4_0_matvec_one{,p,x}_i{sb_per_lane}, sb_per_lane the octets a lane
+ * walks per row, each step covering 64 blocks: ceil(blocks / 64) to 16;
+ * prefetch as for Q4_K), COLUMNS (axh_q4_0_matvec_cols_r1, rows
+ * of 2-128 blocks) and TILED (axh_q4_0_matvec_r*_w*: rows_per_wave,
+ * waves_per_workgroup; also what family 0 with a hole set selects).  The
+ * octet families take rows of an even block count up to 1024 blocks, below
+ * 4 GiB.  With no hole set: columns for up to 512 rows of up to 128 blocks,
+ * tiled for fewer than 32 rows, odd block counts and longer rows, persistent
+ * for more than 16384 rows of more than 256 blocks, else one pass (x whole
+ * for rows of 65-128 blocks from 6144 rows, x two chunks ahead for 14-16 steps
+ * from 4096 rows).
  * Q5_K and Q6_K take the persistent holes or family =
  * AXH_Q4K_FAMILY_ONE_PASS with sb_per_lane 1 or 2 (rows of up to 16
  * superblocks); with no hole set they run one pass for rows of up to 16

@@ -410,12 +410,75 @@ def test_q6k_one_pass_family(axc):
 
 
 def test_q4_0_kernel_selection(axc):
-    """Q4_0: the column kernel for rows of at most 128 blocks (even count) by
-    default; the LDS-staged kernels for odd or longer rows and on request."""
+    """Q4_0 defaults: the column kernel for at most 512 rows of at most 128
+    blocks (even count); the LDS-tiled kernel for fewer than 32 rows, odd
+    block counts and rows of more than 1024 blocks; otherwise the one-pass
+    kernel over octets of 8 blocks (x whole for 65-128 blocks from 6144 rows,
+    x two chunks ahead for 14-16 steps from 4096 rows), persistent for more
+    than 16384 rows of more than 256 blocks."""
     name = axc.q4_0_matvec_kernel_name
     assert name(256, 128) == "axh_q4_0_matvec_cols_r1"
-    assert name(4096, 2) == "axh_q4_0_matvec_cols_r1"
-    assert name(256, 127).startswith("axh_q4_0_matvec_r")
-    assert name(256, 130).startswith("axh_q4_0_matvec_r")
+    assert name(512, 128) == name(1, 2) == name(300, 2) == "axh_q4_0_matvec_cols_r1"
+    assert name(513, 128) == "axh_q4_0_matvec_one_i2"
+    assert name(4096, 2) == "axh_q4_0_matvec_one_i1"
+    assert name(256, 130) == "axh_q4_0_matvec_one_i3"
+    assert name(32, 448) == "axh_q4_0_matvec_one_i7"
+    assert name(31, 448) == name(16, 1024) == "axh_q4_0_matvec_r1_w4"
+    assert name(6143, 128) == "axh_q4_0_matvec_one_i2"
+    assert name(6144, 128) == name(128256, 128) == "axh_q4_0_matvec_onex_i2"
+    assert name(6144, 64) == "axh_q4_0_matvec_one_i1"
+    assert name(6144, 130) == "axh_q4_0_matvec_one_i3"
+    assert name(4096, 896) == "axh_q4_0_matvec_onep_i14"
+    assert name(4096, 1024) == "axh_q4_0_matvec_onep_i16"
+    assert name(4095, 1024) == "axh_q4_0_matvec_one_i16"
+    assert name(4096, 832) == "axh_q4_0_matvec_one_i13"
+    assert name(16384, 448) == "axh_q4_0_matvec_one_i7"
+    assert name(16385, 256) == "axh_q4_0_matvec_one_i4"
+    assert name(16385, 258) == name(28672, 448) == "axh_q4_0_matvec_flat_r1_w8_p1_x1"
+    # odd block counts and rows past 1024 blocks: the LDS-tiled kernel
+    assert name(256, 127) == name(4095, 1026) == "axh_q4_0_matvec_r1_w4"
+    assert name(4096, 127) == name(8191, 1100) == name(8192, 255) == "axh_q4_0_matvec_r2_w4"
+    assert name(8192, 257) == name(14336, 127) == "axh_q4_0_matvec_r4_w4"
     assert name(256, 128, axc.Variant(1, 1, 0, 0)) == "axh_q4_0_matvec_r1_w1"
-    assert b"axh_q4_0_matvec_cols_r1" in axc.builtin_code_object()
+    assert name(256, 128, axc.Variant(family=axc.FAMILY_TILED)) == "axh_q4_0_matvec_r1_w4"
+    co = axc.builtin_code_object()
+    assert b"axh_q4_0_matvec_cols_r1" in co
+    for nit in range(1, 17):
+        assert f"axh_q4_0_matvec_one_i{nit}".encode() in co
+        assert f"axh_q4_0_matvec_onex_i{nit}".encode() in co
+        if nit >= 3:
+            assert f"axh_q4_0_matvec_onep_i{nit}".encode() in co
+
+
+def test_q4_0_family_holes(axc):
+    """The Q4_0 families and their holes: persistent (rows_per_wave,
+    waves_per_workgroup, prefetch), one pass (sb_per_lane = steps of 64 blocks,
+    prefetch = x chunks ahead), one pass with x whole, column, tiled."""
+    name, V = axc.q4_0_matvec_kernel_name, axc.Variant
+    P, O1, OX = axc.FAMILY_PERSISTENT, axc.FAMILY_ONE_PASS, axc.FAMILY_ONE_PASS_X
+    co = axc.builtin_code_object()
+    assert name(4096, 128, V(family=P)) == "axh_q4_0_matvec_flat_r1_w8_p1_x1"
+    for (r, w, pf), want in (((1, 4, 1), "r1_w4_p1_x1"), ((2, 4, 1), "r2_w4_p1_x1"),
+                             ((2, 8, 1), "r2_w8_p1_x1"), ((1, 8, 2), "r1_w8_p2_x1"),
+                             ((2, 4, 2), "r2_w4_p2_x2"), ((1, 16, 2), "r1_w16_p2_x1")):
+        got = name(4096, 448, V(r, w, pf, 0, P))
+        assert got == f"axh_q4_0_matvec_flat_{want}" and got.encode() in co
+    assert name(4096, 1024, V(1, 16, 2, 0, P)) == "axh_q4_0_matvec_flat_r1_w16_p2_x1"
+    assert name(4096, 128, V(family=O1)) == "axh_q4_0_matvec_one_i2"
+    assert name(4096, 128, V(family=O1, sb_per_lane=5)) == "axh_q4_0_matvec_one_i5"
+    assert name(4096, 128, V(prefetch=2, family=O1, sb_per_lane=3)) == "axh_q4_0_matvec_onep_i3"
+    assert name(4096, 1024, V(prefetch=1, family=O1)) == "axh_q4_0_matvec_one_i16"
+    assert name(4096, 128, V(family=OX)) == "axh_q4_0_matvec_onex_i2"
+    assert name(4096, 128, V(family=axc.FAMILY_COLUMNS)) == "axh_q4_0_matvec_cols_r1"
+    assert name(4096, 448, V(2, 4, 0, 0, axc.FAMILY_TILED)) == "axh_q4_0_matvec_r2_w4"
+    for bad in ((4096, 127, V(family=P)), (4096, 1026, V(family=P)), (4096, 127, V(family=O1)),
+                (4096, 1026, V(family=OX)), (4096, 130, V(family=O1, sb_per_lane=2)),
+                (4096, 128, V(family=O1, sb_per_lane=17)), (4096, 128, V(prefetch=2, family=O1)),
+                (4096, 448, V(prefetch=2, family=OX)), (4096, 448, V(prefetch=3, family=O1)),
+                (4096, 448, V(1, 0, 0, 0, O1)), (4096, 448, V(0, 0, 0, 1, P)),
+                (4096, 448, V(3, 4, 1, 0, P)), (4096, 1024, V(1, 8, 2, 0, P)),
+                (4096, 130, V(family=axc.FAMILY_COLUMNS)), (4096, 128, V(1, 4, 0, 0, 6)),
+                (4096, 128, V(family=axc.FAMILY_WORKGROUP)), (4096, 128, V(family=5)),
+                (4096, 128, V(1, 4, 0, 0, 0, 2)), (119304648, 2, V(family=P))):
+        with pytest.raises(axc.DispatchError):
+            name(*bad)

@@ -227,6 +227,66 @@ def test_q4_0_matvec_edge_shapes(ctx, rows, nb):
     _check_q4_0(y, q, x, rows, nb, f"q4_0 edge {rows}x{nb}")
 
 
+def _q4_0_octet_variants(axc, rows, nb):
+    """Every octet-kernel variant that takes this shape: each compiled
+    persistent variant, one pass with x one and two chunks ahead, with x whole,
+    and a trip count one past the row's."""
+    V = axc.Variant
+    need = (nb + 63) // 64
+    cands = [V(r, w, pf, 0, axc.FAMILY_PERSISTENT)
+             for r, w, pf in ((1, 4, 1), (1, 8, 1), (2, 4, 1), (2, 8, 1), (1, 8, 2), (2, 4, 2),
+                              (1, 16, 2))]
+    cands += [V(prefetch=1, family=axc.FAMILY_ONE_PASS), V(family=axc.FAMILY_ONE_PASS_X),
+              V(prefetch=2, family=axc.FAMILY_ONE_PASS, sb_per_lane=max(need, 3)),
+              V(prefetch=1, family=axc.FAMILY_ONE_PASS, sb_per_lane=need + 1)]
+    out = []
+    for v in cands:
+        try:
+            out.append((v, axc.q4_0_matvec_kernel_name(rows, nb, v)))
+        except axc.DispatchError:
+            pass  # row too long for this variant's x staging, or past 16 steps
+    return out
+
+
+@pytest.mark.parametrize("rows,nb", [(1, 2), (2, 66), (3, 130), (33, 130), (5, 8), (100, 446),
+                                     (257, 1022), (31, 1024), (1000, 64), (64, 960),
+                                     (4097, 128), (47, 512)])
+def test_q4_0_octet_kernels_bit_exact(ctx, axc, rows, nb):
+    """Q4_0 through the persistent and one-pass kernels (rows read as octets of
+    8 blocks): partial last octets (a quarter of 2 blocks live, or 3), odd row
+    counts, one row, trip counts 1..16.  Every variant runs the same per-lane
+    order and reduction, so all of them agree bit for bit, and with the oracle
+    to its tolerance."""
+    q = O.gen_q4_0_weights(rows * 17 + nb, rows * nb)
+    x = O.gen_normal_f32(rows * 3 + nb, nb * 32)
+    got = {}
+    for v, kname in _q4_0_octet_variants(axc, rows, nb):
+        _say(f"q4_0 octets {rows}x{nb} {kname}")
+        y = _run_q4_0(ctx, q, x, rows, nb, v)
+        _check_q4_0(y, q, x, rows, nb, f"q4_0 octets {rows}x{nb} {kname}")
+        got[kname] = y
+    assert len(got) >= 6, sorted(got)
+    first = next(iter(got.values()))
+    for kname, y in got.items():
+        assert np.array_equal(y.view(np.uint32), first.view(np.uint32)), kname
+
+
+@pytest.mark.parametrize("rows,nb,kernel", [(4096, 448, "one_i7"), (6144, 128, "onex_i2"),
+                                            (16385, 258, "flat_r1_w8_p1_x1"),
+                                            (4096, 1024, "onep_i16"), (513, 128, "one_i2"),
+                                            (14336, 127, "r4_w4"), (20, 1024, "r1_w4")])
+def test_q4_0_defaults_by_shape(ctx, axc, rows, nb, kernel):
+    """The default Q4_0 kernel of each shape band (one pass, x whole, x two
+    chunks ahead, persistent, LDS-tiled for odd and few rows) against the
+    oracle."""
+    assert axc.q4_0_matvec_kernel_name(rows, nb) == f"axh_q4_0_matvec_{kernel}"
+    _say(f"q4_0 default {rows}x{nb} {kernel}")
+    q = O.gen_q4_0_weights(rows + 5 * nb, rows * nb)
+    x = O.gen_normal_f32(rows + 11 * nb, nb * 32)
+    y = _run_q4_0(ctx, q, x, rows, nb)
+    _check_q4_0(y, q, x, rows, nb, f"q4_0 default {rows}x{nb}")
+
+
 # ---- the reference kernel contract through prepare_kernel / dispatch_handle --
 def _plan(axc, pc):
     return axc.BindingPlan(

@@ -102,12 +102,20 @@ def test_invalid_family_assignments_are_typed_errors(axc, rows, sb, v, what):
     assert e.value.variant == "InvalidArgument", what
 
 
-def test_family_holes_belong_to_the_q4k_matvec_only(axc):
-    for fn in (axc.q4_0_matvec_kernel_name, axc.q4k_gate_up_kernel_name,
-               axc.q5k_matvec_kernel_name, axc.q6k_matvec_kernel_name):
+def test_family_holes_belong_to_the_matvec_families(axc):
+    """The family hole belongs to the Q4_K and Q4_0 matvecs (Q5_K / Q6_K take
+    only their one-pass family); sb_per_lane only with a one-pass family."""
+    for fn in (axc.q4k_gate_up_kernel_name, axc.q5k_matvec_kernel_name,
+               axc.q6k_matvec_kernel_name):
         for v in (axc.Variant(family=1), axc.Variant(sb_per_lane=2)):
             with pytest.raises(axc.DispatchError):
                 fn(4096, 16, v)
+    q40 = axc.q4_0_matvec_kernel_name
+    assert q40(4096, 16, axc.Variant(family=1)) == "axh_q4_0_matvec_flat_r1_w8_p1_x1"
+    for v in (axc.Variant(sb_per_lane=2), axc.Variant(family=axc.FAMILY_WORKGROUP),
+              axc.Variant(family=axc.FAMILY_SPLIT_K)):
+        with pytest.raises(axc.DispatchError):
+            q40(4096, 16, v)
 
 
 # ---- the winner table -----------------------------------------------------------
