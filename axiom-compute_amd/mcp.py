@@ -12,7 +12,10 @@ library's compiled Q4 operations, named like the reference kernels:
                        waves_per_workgroup, prefetch, nontemporal, sb_per_lane):
                        the space of the library's autotuner, default kernels
                        included
-  q4_0_dequant_matvec  holes rows_per_wave, waves_per_workgroup
+  q4_0_dequant_matvec  holes rows_per_wave, waves_per_workgroup (the LDS-tiled
+                       kernel), and with a shape one map per other kernel
+                       family that takes it (persistent, one pass, one pass
+                       with x whole, columns)
   q4k_matmul_f16       holes kind, waves_per_workgroup, col_tiles, prefetch, row_tiles
 
 and a request names a shape ({"n_rows", "units_per_row", "batch"}) instead of
@@ -234,12 +237,17 @@ def check_result(kernel: str, shape: dict, q, x, y, rel_tol: float = DEFAULT_REL
 def default_holes(kernel: str, shape: Optional[dict] = None) -> list:
     """The kernel's hole space as a list of hole maps.  q4km_dequant_matvec:
     one map per kernel family that takes the shape (the autotuner's space,
-    tune.q4k_matvec_hole_spaces); the other kernels: one map of the candidate
-    values of every hole among the compiled variants (sorted)."""
+    tune.q4k_matvec_hole_spaces); q4_0_dequant_matvec with a shape: the
+    LDS-tiled kernel's map, then one map per other family that takes the shape
+    (tune.q4_0_matvec_hole_spaces); otherwise one map of the candidate values
+    of every hole among the compiled variants (sorted)."""
     if kernel == "q4km_dequant_matvec":
         from . import tune
         shape = shape or {"n_rows": 1, "units_per_row": 1}
         return tune.q4k_matvec_hole_spaces(int(shape["n_rows"]), int(shape["units_per_row"]))
+    if kernel == "q4_0_dequant_matvec" and shape:
+        from . import tune
+        return tune.q4_0_matvec_hole_spaces(int(shape["n_rows"]), int(shape["units_per_row"]))
     if kernel == "q4k_matmul_f16":
         vs = [(v.kind, v.waves_per_workgroup, v.col_tiles, v.prefetch, v.row_tiles)
               for v in _axh.compiled_matmul_variants()]

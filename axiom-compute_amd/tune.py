@@ -315,6 +315,38 @@ def q4k_matvec_hole_spaces(n_rows: int, sb_per_row: int) -> list:
     return [h for f in range(1, 8) if (h := q4k_matvec_family_holes(f, n_rows, sb_per_row))]
 
 
+def q4_0_matvec_hole_spaces(n_rows: int, blocks_per_row: int) -> list:
+    """One hole map per Q4_0 matvec family that takes the shape: the LDS-tiled
+    kernel's holes first (family 0 with rows_per_wave / waves_per_workgroup),
+    then the persistent, one-pass, one-pass-with-x-whole and column families
+    (the family hole first, with the family as its one candidate).  A family
+    takes the shape when its plain assignment plans to a kernel; assignments
+    of a map that name no compiled kernel fail to plan and rank as failures."""
+    V = _axh.Variant
+
+    def takes(v):
+        try:
+            _axh.q4_0_matvec_kernel_name(n_rows, blocks_per_row, v)
+            return True
+        except _axh.DispatchError:
+            return False
+
+    vs = _axh.compiled_variants("q4_0")
+    out = [{"rows_per_wave": sorted({v.rows_per_wave for v in vs}),
+            "waves_per_workgroup": sorted({v.waves_per_workgroup for v in vs})}]
+    need = (blocks_per_row + 63) // 64
+    steps = [need] + ([need + 1] if need < 16 else [])
+    if takes(V(family=_axh.FAMILY_PERSISTENT)):
+        out.append({"family": [_axh.FAMILY_PERSISTENT], "prefetch": [1, 2],
+                    "rows_per_wave": [1, 2], "waves_per_workgroup": [4, 8, 16]})
+    if takes(V(prefetch=1, family=_axh.FAMILY_ONE_PASS)):
+        out.append({"family": [_axh.FAMILY_ONE_PASS], "prefetch": [1, 2], "sb_per_lane": steps})
+        out.append({"family": [_axh.FAMILY_ONE_PASS_X], "sb_per_lane": steps})
+    if takes(V(family=_axh.FAMILY_COLUMNS)):
+        out.append({"family": [_axh.FAMILY_COLUMNS]})
+    return out
+
+
 def q4k_matvec_autotune(ctx, q, x, y, n_rows: int, sb_per_row: int, samples: int = 5,
                         tol: float = 1e-3) -> AutotuneReport:
     """Grid search over every Q4_K matvec kernel family on resident buffers; each

@@ -50,6 +50,25 @@ def test_bench_variant_uncompiled_assignment_is_an_error(mcp, tmp_path):
     assert e.value.code == mcp.DEVICE_UNAVAILABLE and e.value.category == "dispatch_failed"
 
 
+def test_q4_0_grid_search_over_every_family(mcp, tmp_path, axc):
+    """grid_search over the Q4_0 families that take 2048 x 128 blocks: every
+    assignment that names a compiled kernel runs and passes the host checker,
+    the rest fail to plan and rank last."""
+    _say("grid_search q4_0 2048x128 every family")
+    ctx = mcp.McpContext(history_dir=tmp_path)
+    shape = {"n_rows": 2048, "units_per_row": 128}
+    res = mcp.grid_search({"kernel": "q4_0_dequant_matvec", "shape": shape,
+                           "sample_count": 2}, ctx)
+    ranked = res["ranked"]
+    ok = [r for r in ranked if r["outcome"] == "ok"]
+    assert ok and all(r["median_ns"] for r in ok)
+    fams = {int(r["assignments"].get("family", 0)) for r in ok}
+    assert fams == {0, axc.FAMILY_PERSISTENT, axc.FAMILY_ONE_PASS, axc.FAMILY_ONE_PASS_X,
+                    axc.FAMILY_COLUMNS}, fams
+    assert not [r for r in ranked if r["outcome"].startswith("correctness_rejected")]
+    assert all(r["median_ns"] is None for r in ranked[len(ok):])
+
+
 def test_grid_search_over_the_stdio_server(mcp, tmp_path):
     """Two JSON-RPC calls through serve(): a grid search (some assignments are
     not compiled and rank last as failures) and the history it appended."""

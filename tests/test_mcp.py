@@ -130,6 +130,30 @@ def test_default_hole_spaces_come_from_compiled_variants(mcp, axc):
     assert mcp.default_holes("q4_0_dequant_matvec")[0]["waves_per_workgroup"] == [1, 4]
 
 
+def test_q4_0_hole_spaces_follow_the_shape(mcp, axc):
+    """With a shape, the Q4_0 space is the LDS-tiled kernel's map and one map
+    per other family that takes the shape; each family's plain assignment
+    plans to that family's kernel."""
+    sp = mcp.default_holes("q4_0_dequant_matvec", {"n_rows": 256, "units_per_row": 128})
+    assert sp[0] == mcp.default_holes("q4_0_dequant_matvec")[0]
+    fams = [m["family"][0] for m in sp[1:]]
+    assert fams == [axc.FAMILY_PERSISTENT, axc.FAMILY_ONE_PASS, axc.FAMILY_ONE_PASS_X,
+                    axc.FAMILY_COLUMNS]
+    one = sp[2]
+    assert one["sb_per_lane"] == [2, 3] and one["prefetch"] == [1, 2]
+    # odd block counts take only the tiled kernel; 130 blocks no column kernel
+    assert len(mcp.default_holes("q4_0_dequant_matvec", {"n_rows": 64, "units_per_row": 127})) == 1
+    sp = mcp.default_holes("q4_0_dequant_matvec", {"n_rows": 64, "units_per_row": 130})
+    assert [m["family"][0] for m in sp[1:]] == [axc.FAMILY_PERSISTENT, axc.FAMILY_ONE_PASS,
+                                                 axc.FAMILY_ONE_PASS_X]
+    sp = mcp.default_holes("q4_0_dequant_matvec", {"n_rows": 64, "units_per_row": 1024})
+    assert sp[2]["sb_per_lane"] == [16]
+    for m in sp[1:]:
+        a = {k: v[0] for k, v in m.items()}
+        name = axc.q4_0_matvec_kernel_name(64, 1024, mcp._variant_obj("q4_0_dequant_matvec", a))
+        assert name.startswith("axh_q4_0_matvec_" + {1: "flat", 2: "one", 3: "onex"}[a["family"]])
+
+
 def test_seeded_inputs_are_deterministic_and_well_formed(mcp):
     shape = {"n_rows": 3, "units_per_row": 2}
     q1, x1 = mcp.seeded_inputs("q4km_dequant_matvec", shape, 77)
