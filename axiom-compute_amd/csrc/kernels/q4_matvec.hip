@@ -978,8 +978,28 @@ AXH_Q4K_MATVEC_ONE(16)
     extern __shared__ float axh_lds_dyn[];                                                       \
     q4k_matvec_one<NIT, false, true>(q, q, x, y, a.n_rows, a.units_per_row, axh_lds_dyn);        \
   }
+#define AXH_Q5K_MATVEC_ONEP(NIT)                                                                 \
+  extern "C" __global__ void __launch_bounds__(512)                                              \
+      axh_q5k_matvec_onep_i##NIT(const uint8_t *__restrict__ q, const float *__restrict__ x,     \
+                                 float *__restrict__ y, AXH_ROWS_ARGS) { AXH_ROWS_UNPACK;        \
+    extern __shared__ float axh_lds_dyn[];                                                       \
+    q4k_matvec_one<NIT, false, true, false, 2>(q, q, x, y, a.n_rows, a.units_per_row,            \
+                                               axh_lds_dyn);                                     \
+  }
 AXH_Q5K_MATVEC_ONE(1)
 AXH_Q5K_MATVEC_ONE(2)
+AXH_Q5K_MATVEC_ONE(3)
+AXH_Q5K_MATVEC_ONEP(3)
+AXH_Q5K_MATVEC_ONE(4)
+AXH_Q5K_MATVEC_ONEP(4)
+AXH_Q5K_MATVEC_ONE(5)
+AXH_Q5K_MATVEC_ONEP(5)
+AXH_Q5K_MATVEC_ONE(6)
+AXH_Q5K_MATVEC_ONEP(6)
+AXH_Q5K_MATVEC_ONE(7)
+AXH_Q5K_MATVEC_ONEP(7)
+AXH_Q5K_MATVEC_ONE(8)
+AXH_Q5K_MATVEC_ONEP(8)
 
 #define AXH_Q4K_MATVEC_ONEP(NIT)                                                                 \
   extern "C" __global__ void __launch_bounds__(512)                                              \
@@ -1446,6 +1466,18 @@ __device__ __forceinline__ void q6k_matvec_one(const uint8_t *__restrict__ q,
   }
 AXH_Q6K_MATVEC_ONE(1, 1, )
 AXH_Q6K_MATVEC_ONE(2, 1, )
+AXH_Q6K_MATVEC_ONE(3, 1, )
+AXH_Q6K_MATVEC_ONE(3, 2, p)
+AXH_Q6K_MATVEC_ONE(4, 1, )
+AXH_Q6K_MATVEC_ONE(4, 2, p)
+AXH_Q6K_MATVEC_ONE(5, 1, )
+AXH_Q6K_MATVEC_ONE(5, 2, p)
+AXH_Q6K_MATVEC_ONE(6, 1, )
+AXH_Q6K_MATVEC_ONE(6, 2, p)
+AXH_Q6K_MATVEC_ONE(7, 1, )
+AXH_Q6K_MATVEC_ONE(7, 2, p)
+AXH_Q6K_MATVEC_ONE(8, 1, )
+AXH_Q6K_MATVEC_ONE(8, 2, p)
 
 // Fused SwiGLU gate/up projection: y[r] = silu(Wg[r].x) * (Wu[r].x), ROWS
 // output rows per bundle (2 * ROWS weight rows per lane group).

@@ -876,11 +876,24 @@ static const KqFormat kQ6kFormat{"axh_q6k_matvec_flat", "axh_q6k_matvec_one", kQ
 // 2048 rows): 1024 x 4096 3.46 vs 3.57 us, 1024 x 8192 5.10 vs 5.38.
 constexpr uint32_t kKqFewRows = 1024;
 
+// Rows of 17-64 superblocks on at most 2048 rows, and of 33-64 on 14336 rows
+// and more, take 4 waves with x staged whole and two iterations in flight
+// (the _x2 kernels past 32 superblocks).  A/B in one run, us per call, Q5_K /
+// Q6_K, against 8 waves with early refill: 1024 x 14336 7.32 vs 9.51 / 9.10
+// vs 10.71, 2048 x 10240 6.41 vs 7.60 / 7.51 vs 8.69, 2048 x 6144 4.71 vs
+// 5.06 (early refill, 4 waves) / 5.39 vs 5.66, 14336 x 14336 27.7 vs 31.3 /
+// 34.7 vs 37.6, 14336 x 10240 21.7 vs 23.5 / 24.8 vs 25.6; not at 4096 rows
+// (Q6_K 4096 x 14336 13.1 vs 11.5) nor on 14336 rows of 24 superblocks (Q6_K
+// 16.8 vs 16.3).
+constexpr uint32_t kKqW4MaxRows = 2048, kKqW4TallMinRows = 14336;
+
 static MatvecVariant kq_default(const KqFormat &f, uint32_t n_rows, uint32_t nsb) {
   const uint32_t nw = nsb * 8u <= 256u ? 4u : 8u;
   const bool early = f.chunked_early || nsb * 8u <= nw * 64u;
   const bool few = n_rows <= kKqFewRows && nsb <= 32u && (&f == &kQ5kFormat || nsb > 16u);
-  if (few) return {1, 4, 2, 2, 1};
+  const bool w4 = nsb > 16u && nsb <= 64u &&
+                  (n_rows <= kKqW4MaxRows || (n_rows >= kKqW4TallMinRows && nsb > 32u));
+  if (few || w4) return {1, 4, 2, 2, 1}; // the _x2 kernel where the row needs it
   return {1, nw, early ? 1u : 2u, 2, 1};
 }
 
@@ -895,6 +908,7 @@ static MatvecVariant kq_default(const KqFormat &f, uint32_t n_rows, uint32_t nsb
 // longer rows (4096 x 14336: even).  The family is also reachable as
 // variant->family = AXH_Q4K_FAMILY_ONE_PASS (hole: sb_per_lane, 1 or 2).
 constexpr uint32_t kQ5OneMinRows = 2048, kQ5OneMaxRows = 32768, kKqOneMaxSb = 16;
+constexpr uint32_t kKqOneMaxIt = 8; // one-pass kernels compiled for 1-8 steps
 
 // Q6_K rows of up to 16 superblocks over 256 to 4096 rows (at most one
 // workgroup per CU) take the one-pass kernel too (axh_q6k_matvec_one_i{NIT}).
@@ -904,6 +918,24 @@ constexpr uint32_t kQ5OneMinRows = 2048, kQ5OneMaxRows = 32768, kKqOneMaxSb = 16
 // 3072 5.21 vs 5.38, 4096 x 2048 3.72 vs 4.30, 1024 x 2048 3.24 vs 4.08; but
 // 6144 x 4096 7.28 vs 6.91 and 14336 x 4096 12.08 vs 11.95.
 constexpr uint32_t kQ6OneMinRows = 256, kQ6OneMaxRows = 4096;
+
+// Longer rows take the one-pass kernel past 2048 rows too: Q5_K 2049-4096
+// rows of 17-64 superblocks (4096 x 6144 5.67 vs 6.49 us, 4096 x 10240 7.84 vs
+// 8.18, 4096 x 14336 10.10 vs 10.46, 4096 x 16384 11.03 vs 11.55; 8192 x
+// 10240 14.8 vs 14.6 stays persistent), Q6_K 2049-8192 rows of 17-40 (4096 x
+// 6144 6.59 vs 7.26, 4096 x 10240 9.15 vs 9.49, 8192 x 6144 10.52 vs 11.06,
+// 8192 x 10240 15.24 vs 15.71; 4096 x 14336 11.79 vs 11.52 stays persistent).
+// At 2048 rows the 4-wave persistent kernel stays ahead (Q5_K 2048 x 14336
+// 7.64 vs 9.18).
+constexpr uint32_t kKqOneLongMinRows = 2049, kQ5OneLongMaxRows = 4096, kQ6OneLongMaxRows = 8192;
+constexpr uint32_t kQ5OneLongMaxSb = 64, kQ6OneLongMaxSb = 40;
+
+static bool kq_one_long(const KqFormat &f, uint32_t n_rows, uint32_t nsb) {
+  const bool q5 = &f == &kQ5kFormat;
+  return n_rows >= kKqOneLongMinRows && nsb > kKqOneMaxSb &&
+         n_rows <= (q5 ? kQ5OneLongMaxRows : kQ6OneLongMaxRows) &&
+         nsb <= (q5 ? kQ5OneLongMaxSb : kQ6OneLongMaxSb);
+}
 
 static axh_status plan_kq(const KqFormat &f, uint32_t n_rows, uint32_t sb_per_row,
                           const axh_q4_variant *variant, Q4kPlan *p) {
@@ -920,17 +952,23 @@ static axh_status plan_kq(const KqFormat &f, uint32_t n_rows, uint32_t sb_per_ro
   const uint32_t one_min = q5 ? kQ5OneMinRows : kQ6OneMinRows;
   const uint32_t one_max = q5 ? kQ5OneMaxRows : kQ6OneMaxRows;
   if (fam == AXH_Q4K_FAMILY_ONE_PASS ||
-      (!flat_holes && n_rows >= one_min && n_rows <= one_max && sb_per_row <= kKqOneMaxSb)) {
-    if (flat_holes)
+      (!flat_holes && ((n_rows >= one_min && n_rows <= one_max && sb_per_row <= kKqOneMaxSb) ||
+                       kq_one_long(f, n_rows, sb_per_row)))) {
+    const uint32_t xd = variant ? variant->prefetch : 0u;
+    if (variant && (variant->rows_per_wave || variant->waves_per_workgroup ||
+                    variant->nontemporal || xd > 2u))
       return fail(AXH_ERR_INVALID_ARGUMENT,
-                  "the Q5_K / Q6_K one-pass family's only hole is sb_per_lane");
+                  "the Q5_K / Q6_K one-pass family's holes are sb_per_lane and prefetch (x one "
+                  "or two chunks ahead)");
     const uint32_t need = (sb_per_row + 7u) / 8u;
     const uint32_t nit = variant && variant->sb_per_lane ? variant->sb_per_lane : need;
-    if (nit < need || nit > 2u)
+    if (nit < need || nit > kKqOneMaxIt)
       return fail(AXH_ERR_INVALID_ARGUMENT,
-                  "Q5_K / Q6_K one-pass: sb_per_lane must cover the row and be 1 or 2 (rows of "
-                  "up to 16 superblocks)");
-    std::snprintf(p->name, sizeof(p->name), "%s_i%u", f.one_prefix, nit);
+                  "Q5_K / Q6_K one-pass: sb_per_lane must cover the row and be at most 8 (rows "
+                  "of up to 64 superblocks)");
+    if (xd == 2u && nit < 3u)
+      return fail(AXH_ERR_INVALID_ARGUMENT, "x two chunks ahead needs three or more steps");
+    std::snprintf(p->name, sizeof(p->name), "%s%s_i%u", f.one_prefix, xd == 2u ? "p" : "", nit);
     p->nw = 8;
     p->lds = sb_per_row * f.lds_per_sb;
     p->flat = false; // one workgroup per 16 rows, all of them launched

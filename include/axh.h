@@ -221,10 +221,13 @@ void axh_event_destroy(axh_event *ev);
  * for rows of 65-128 blocks from 6144 rows, x two chunks ahead for 14-16 steps
  * from 4096 rows).
  * Q5_K and Q6_K take the persistent holes or family =
- * AXH_Q4K_FAMILY_ONE_PASS with sb_per_lane 1 or 2 (rows of up to 16
- * superblocks); with no hole set they run one pass for rows of up to 16
- * superblocks over 2048-32768 rows (Q5_K) or 256-4096 rows (Q6_K), else the
- * persistent family. */
+ * AXH_Q4K_FAMILY_ONE_PASS with sb_per_lane 1-8 (rows of up to 64
+ * superblocks) and prefetch (x one or two chunks ahead, two from three
+ * steps); with no hole set they run one pass for rows of up to 16
+ * superblocks over 2048-32768 rows (Q5_K) or 256-4096 rows (Q6_K), and for
+ * 2049-4096 rows of up to 64 superblocks (Q5_K) or 2049-8192 rows of up to 40
+ * (Q6_K), else the persistent family (4 waves with x staged whole for up to
+ * 2048 rows of 17-64 superblocks and for 14336 rows and more of 33-64). */
 enum {
     AXH_Q4K_FAMILY_DEFAULT = 0,
     AXH_Q4K_FAMILY_PERSISTENT = 1, /* axh_q4k_matvec_flat_r*_w*_p*_n*[_x2]            */

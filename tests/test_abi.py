@@ -335,7 +335,9 @@ def test_kquant_kernel_selection(axc):
     co = axc.builtin_code_object()
     for fam, name in (("q5k", axc.q5k_matvec_kernel_name), ("q6k", axc.q6k_matvec_kernel_name)):
         assert name(128256, 16) == f"axh_{fam}_matvec_flat_r1_w4_p1_x1"
-        assert name(4096, 56) == f"axh_{fam}_matvec_flat_r1_w8_p1_x1"
+        assert name(4096, 56) == ("axh_q5k_matvec_one_i7" if fam == "q5k"
+                                  else "axh_q6k_matvec_flat_r1_w8_p1_x1")
+        assert name(8192, 56) == f"axh_{fam}_matvec_flat_r1_w8_p1_x1"
         # Q5_K's prefetch-1 kernel stages x in chunks; Q6_K's stages it whole
         assert name(65536, 128) == ("axh_q5k_matvec_flat_r1_w8_p1_x1" if fam == "q5k"
                                     else "axh_q6k_matvec_flat_r1_w8_p2_x2")
@@ -361,16 +363,24 @@ def test_q5k_one_pass_family(axc):
     assert name(14336, 16) == "axh_q5k_matvec_one_i2"
     assert name(4096, 16) == "axh_q5k_matvec_one_i2"
     assert name(2048, 8) == "axh_q5k_matvec_one_i1"
-    for rows, sb in ((1024, 16), (32769, 16), (4096, 17), (4096, 56)):
+    for rows, sb in ((1024, 16), (32769, 16), (2048, 17), (4097, 17), (4096, 65), (8192, 56)):
         assert name(rows, sb).startswith("axh_q5k_matvec_flat_"), (rows, sb)
+    # 2049-4096 rows of 17-64 superblocks: one pass too
+    assert name(2049, 17) == "axh_q5k_matvec_one_i3"
+    assert name(4096, 56) == "axh_q5k_matvec_one_i7"
+    assert name(4096, 64) == "axh_q5k_matvec_one_i8"
     assert name(4096, 16, V(1, 4, 1, 0)) == "axh_q5k_matvec_flat_r1_w4_p1_x1"  # flat holes
     assert name(7, 3, V(0, 0, 0, 0, one, 0)) == "axh_q5k_matvec_one_i1"
     assert name(7, 3, V(0, 0, 0, 0, one, 2)) == "axh_q5k_matvec_one_i2"
-    for k in ("axh_q5k_matvec_one_i1", "axh_q5k_matvec_one_i2"):
-        assert k.encode() in co
-    for bad in ((100, 17, V(0, 0, 0, 0, one, 0)), (100, 16, V(0, 0, 0, 0, one, 1)),
-                (100, 16, V(0, 0, 0, 0, one, 3)), (100, 16, V(1, 0, 0, 0, one, 0)),
-                (100, 16, V(0, 0, 0, 0, 0, 2))):
+    assert name(7, 3, V(0, 0, 2, 0, one, 3)) == "axh_q5k_matvec_onep_i3"
+    assert name(100, 64, V(0, 0, 1, 0, one, 8)) == "axh_q5k_matvec_one_i8"
+    for i in range(1, 9):
+        assert f"axh_q5k_matvec_one_i{i}".encode() in co
+        assert i < 3 or f"axh_q5k_matvec_onep_i{i}".encode() in co
+    for bad in ((100, 65, V(0, 0, 0, 0, one, 0)), (100, 16, V(0, 0, 0, 0, one, 1)),
+                (100, 16, V(0, 0, 0, 0, one, 9)), (100, 16, V(1, 0, 0, 0, one, 0)),
+                (100, 16, V(0, 0, 2, 0, one, 0)), (100, 16, V(0, 0, 3, 0, one, 3)),
+                (100, 16, V(0, 0, 0, 1, one, 0)), (100, 16, V(0, 0, 0, 0, 0, 2))):
         with pytest.raises(axc.DispatchError):
             name(*bad)
 
@@ -384,26 +394,40 @@ def test_q6k_one_pass_family(axc):
     assert name(1024, 16) == "axh_q6k_matvec_one_i2"  # Llama-3-8B attn_v (GQA)
     assert name(4096, 16) == "axh_q6k_matvec_one_i2"
     assert name(256, 8) == "axh_q6k_matvec_one_i1"
-    for rows, sb in ((255, 16), (4097, 16), (14336, 16), (128256, 16), (4096, 17), (4096, 56)):
+    for rows, sb in ((255, 16), (4097, 16), (14336, 16), (128256, 16), (2048, 17), (4096, 41),
+                     (4096, 56), (8193, 24)):
         assert name(rows, sb).startswith("axh_q6k_matvec_flat_"), (rows, sb)
+    # 2049-8192 rows of 17-40 superblocks: one pass too
+    assert name(2049, 17) == "axh_q6k_matvec_one_i3"
+    assert name(4096, 40) == "axh_q6k_matvec_one_i5"
+    assert name(8192, 24) == "axh_q6k_matvec_one_i3"
+    # at most 2048 rows of 17-64 superblocks, and 14336 rows and more of 33-64:
+    # 4 waves, x whole, prefetch 2
+    assert name(2048, 24) == "axh_q6k_matvec_flat_r1_w4_p2_x1"
+    assert name(1024, 56) == name(14336, 56) == "axh_q6k_matvec_flat_r1_w4_p2_x2"
+    assert name(14336, 24) == "axh_q6k_matvec_flat_r1_w4_p1_x1"
+    assert axc.q5k_matvec_kernel_name(14336, 40) == "axh_q5k_matvec_flat_r1_w4_p2_x2"
     assert name(4096, 16, V(1, 4, 1, 0)) == "axh_q6k_matvec_flat_r1_w4_p1_x1"  # flat holes
     # up to 1024 rows of 17-32 superblocks: prefetch 2 (Llama-2-70B attn_v is 1024 x 8192)
     assert name(1024, 32) == "axh_q6k_matvec_flat_r1_w4_p2_x1"
     assert name(1, 17) == "axh_q6k_matvec_flat_r1_w4_p2_x1"
-    assert name(1025, 32) == "axh_q6k_matvec_flat_r1_w4_p1_x1"
-    assert name(1024, 33) == "axh_q6k_matvec_flat_r1_w8_p1_x1"
+    assert name(1025, 32) == "axh_q6k_matvec_flat_r1_w4_p2_x1"
+    assert name(1024, 33) == "axh_q6k_matvec_flat_r1_w4_p2_x2"
+    assert name(1024, 65) == "axh_q6k_matvec_flat_r1_w8_p2_x2"
     # Q5_K: the same up to 1024 rows of up to 32 superblocks
     q5 = axc.q5k_matvec_kernel_name
     assert q5(1024, 16) == "axh_q5k_matvec_flat_r1_w4_p2_x1"
     assert q5(1024, 32) == "axh_q5k_matvec_flat_r1_w4_p2_x1"
-    assert q5(1025, 32) == "axh_q5k_matvec_flat_r1_w4_p1_x1"
+    assert q5(1025, 16) == "axh_q5k_matvec_flat_r1_w4_p1_x1"
     assert q5(4096, 16) == "axh_q5k_matvec_one_i2"
     assert name(7, 3, V(0, 0, 0, 0, one, 0)) == "axh_q6k_matvec_one_i1"
     assert name(7, 3, V(0, 0, 0, 0, one, 2)) == "axh_q6k_matvec_one_i2"
-    for k in ("axh_q6k_matvec_one_i1", "axh_q6k_matvec_one_i2"):
-        assert k.encode() in co
-    for bad in ((100, 17, V(0, 0, 0, 0, one, 0)), (100, 16, V(0, 0, 0, 0, one, 1)),
-                (100, 16, V(0, 0, 0, 0, one, 3)), (100, 16, V(0, 0, 2, 0, one, 0)),
+    assert name(100, 56, V(0, 0, 2, 0, one, 0)) == "axh_q6k_matvec_onep_i7"
+    for i in range(1, 9):
+        assert f"axh_q6k_matvec_one_i{i}".encode() in co
+        assert i < 3 or f"axh_q6k_matvec_onep_i{i}".encode() in co
+    for bad in ((100, 65, V(0, 0, 0, 0, one, 0)), (100, 16, V(0, 0, 0, 0, one, 1)),
+                (100, 16, V(0, 0, 0, 0, one, 9)), (100, 16, V(0, 0, 2, 0, one, 0)),
                 (100, 16, V(0, 0, 0, 0, 0, 2)), (100, 16, V(0, 0, 0, 0, 3, 0))):
         with pytest.raises(axc.DispatchError):
             name(*bad)

@@ -125,34 +125,68 @@ def test_early_refill_several_pairs_per_wave(ctx, axc, kind):
         _check(y, kind, q, x, rows, sb, f"early refill {v}")
 
 
-@pytest.mark.parametrize("rows,sb,nit", [(1, 1, 1), (7, 3, 1), (33, 8, 2), (17, 9, 2),
-                                         (4097, 16, 2), (2048, 8, 1), (100, 16, 2)])
-def test_q5k_one_pass_family(ctx, axc, rows, sb, nit):
+def _flat_for(axc, sb):
+    """A persistent variant that stages a row of `sb` superblocks."""
+    return axc.Variant(1, 4, 1, 0) if sb <= 32 else axc.Variant(1, 8, 1, 0)
+
+
+@pytest.mark.parametrize("rows,sb,nit,xd", [(1, 1, 1, 1), (7, 3, 1, 1), (33, 8, 2, 1),
+                                            (17, 9, 2, 1), (4097, 16, 2, 1), (2048, 8, 1, 1),
+                                            (100, 16, 2, 1), (4096, 56, 7, 1), (2049, 17, 3, 1),
+                                            (33, 64, 8, 1), (50, 40, 5, 2), (4095, 56, 7, 2),
+                                            (9, 24, 4, 2)])
+def test_q5k_one_pass_family(ctx, axc, rows, sb, nit, xd):
     """The Q5_K one-pass kernel (the default for 2048-32768 rows of up to 16
-    superblocks) at ragged row counts, requested explicitly."""
+    superblocks and 2049-4096 rows of up to 64) at ragged row counts, trip
+    counts 1-8 (one past the row's too), x one or two chunks ahead, requested
+    explicitly: within the oracle's tolerance, and bit for bit the persistent
+    kernel's output (the same per-lane loads, decode and reduction order)."""
     q = O.gen_kq_weights(Q5, rows * 5 + sb, rows * sb)
     x = O.gen_normal_f32(rows + 2 * sb, sb * 256)
-    v = axc.Variant(0, 0, 0, 0, axc.FAMILY_ONE_PASS, nit)
-    _say(f"kquant Q5_K one-pass {rows}x{sb} i{nit}")
+    v = axc.Variant(0, 0, xd, 0, axc.FAMILY_ONE_PASS, nit)
+    _say(f"kquant Q5_K one-pass {rows}x{sb} i{nit} x{xd}")
     y = _matvec(ctx, Q5, q, x, rows, sb, v)
-    _check(y, Q5, q, x, rows, sb, f"one-pass {rows}x{sb} i{nit}")
+    _check(y, Q5, q, x, rows, sb, f"one-pass {rows}x{sb} i{nit} x{xd}")
+    flat = _matvec(ctx, Q5, q, x, rows, sb, _flat_for(axc, sb))
+    assert np.array_equal(y.view(np.uint32), flat.view(np.uint32))
 
 
-@pytest.mark.parametrize("rows,sb,nit", [(1, 1, 1), (7, 3, 1), (33, 8, 2), (17, 9, 2),
-                                         (4097, 16, 2), (1024, 16, 2), (100, 16, 2), (256, 8, 1)])
-def test_q6k_one_pass_family(ctx, axc, rows, sb, nit):
+@pytest.mark.parametrize("rows,sb,nit,xd", [(1, 1, 1, 1), (7, 3, 1, 1), (33, 8, 2, 1),
+                                            (17, 9, 2, 1), (4097, 16, 2, 1), (1024, 16, 2, 1),
+                                            (100, 16, 2, 1), (256, 8, 1, 1), (4096, 40, 5, 1),
+                                            (8192, 24, 3, 1), (2049, 17, 3, 1), (33, 64, 8, 1),
+                                            (50, 56, 7, 2), (4095, 24, 3, 2), (9, 33, 6, 2)])
+def test_q6k_one_pass_family(ctx, axc, rows, sb, nit, xd):
     """The Q6_K one-pass kernel (the default for 256-4096 rows of up to 16
-    superblocks) at ragged row counts, requested explicitly: within the
+    superblocks and 2049-8192 rows of up to 40) at ragged row counts, trip
+    counts 1-8, x one or two chunks ahead, requested explicitly: within the
     oracle's tolerance, and bit for bit the persistent kernel's output (the
     same per-lane loads, decode and reduction order)."""
     q = O.gen_kq_weights(Q6, rows * 7 + sb, rows * sb)
     x = O.gen_normal_f32(rows + 3 * sb, sb * 256)
-    v = axc.Variant(0, 0, 0, 0, axc.FAMILY_ONE_PASS, nit)
-    _say(f"kquant Q6_K one-pass {rows}x{sb} i{nit}")
+    v = axc.Variant(0, 0, xd, 0, axc.FAMILY_ONE_PASS, nit)
+    _say(f"kquant Q6_K one-pass {rows}x{sb} i{nit} x{xd}")
     y = _matvec(ctx, Q6, q, x, rows, sb, v)
-    _check(y, Q6, q, x, rows, sb, f"one-pass {rows}x{sb} i{nit}")
-    flat = _matvec(ctx, Q6, q, x, rows, sb, axc.Variant(1, 4, 1, 0))
+    _check(y, Q6, q, x, rows, sb, f"one-pass {rows}x{sb} i{nit} x{xd}")
+    flat = _matvec(ctx, Q6, q, x, rows, sb, _flat_for(axc, sb))
     assert np.array_equal(y.view(np.uint32), flat.view(np.uint32))
+
+
+@pytest.mark.parametrize("kind,rows,sb,kernel", [
+    (Q5, 1024, 56, "flat_r1_w4_p2_x2"), (Q5, 14336, 40, "flat_r1_w4_p2_x2"),
+    (Q5, 4096, 40, "one_i5"), (Q6, 2048, 24, "flat_r1_w4_p2_x1"),
+    (Q6, 14336, 56, "flat_r1_w4_p2_x2"), (Q6, 8192, 40, "one_i5")])
+def test_kquant_defaults_by_shape(ctx, axc, kind, rows, sb, kernel):
+    """The Q5_K / Q6_K default of each band that takes 4 waves with x whole
+    or the one-pass kernel on longer rows, against the oracle."""
+    fam = "q5k" if kind == Q5 else "q6k"
+    name = getattr(axc, f"{fam}_matvec_kernel_name")
+    assert name(rows, sb) == f"axh_{fam}_matvec_{kernel}"
+    q = O.gen_kq_weights(kind, rows + 3 * sb, rows * sb)
+    x = O.gen_normal_f32(rows + 5 * sb, sb * 256)
+    _say(f"kquant {fam} default {rows}x{sb} {kernel}")
+    y = _matvec(ctx, kind, q, x, rows, sb)
+    _check(y, kind, q, x, rows, sb, f"{fam} default {rows}x{sb}")
 
 
 def test_one_hot_x_reads_single_weights(ctx):
