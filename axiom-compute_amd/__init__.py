@@ -10,6 +10,6 @@ from .axh import (  # noqa: F401
     FAMILY_SPLIT_K, FAMILY_TILED, FAMILY_WORKGROUP, BindingPlan, DeviceBuffer, DispatchError,
     DispatchRequest, Graph, HipContext, HipContextOptions, KernelHandle, MatmulVariant, Variant,
     builtin_code_object, compiled_matmul_variants, compiled_variants, ggml_type_size,
-    load_library, q4_0_matvec_kernel_name, q4k_gate_up_kernel_name, q4k_matmul_kernel_name,
-    q4k_matvec_default_variant, q4k_matvec_kernel_name, q5k_matvec_kernel_name,
-    q6k_matvec_kernel_name, validate_request)
+    load_library, q4_0_gate_up_kernel_name, q4_0_matvec_kernel_name, q4k_gate_up_kernel_name,
+    q4k_matmul_kernel_name, q4k_matvec_default_variant, q4k_matvec_kernel_name,
+    q5k_matvec_kernel_name, q6k_matvec_kernel_name, validate_request)

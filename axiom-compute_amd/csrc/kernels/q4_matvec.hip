@@ -516,18 +516,23 @@ struct Q40FlatBuf {
   uint32_t c[PF][RPW];
 };
 
-template <int RPW, int PF, bool kNT>
+// kDual (fused gate/up): slots r < RPW/2 read row bundle*RPW/2 + r of the
+// first matrix, slots r >= RPW/2 the same row of the second.
+template <int RPW, int PF, bool kNT, bool kDual>
 __device__ __forceinline__ void q4_0_flat_load(Q40FlatBuf<RPW, PF> &B, int p,
-                                               __amdgpu_buffer_rsrc_t qr, uint32_t row_bytes,
+                                               __amdgpu_buffer_rsrc_t qr,
+                                               __amdgpu_buffer_rsrc_t qr2, uint32_t row_bytes,
                                                uint32_t bundle, uint32_t it, uint32_t s,
                                                uint32_t c) {
+  constexpr int kRb = kDual ? RPW / 2 : RPW;
   const uint32_t q_off = (it * 8u + s) * (uint32_t)kQ4kSbBytes + 36u * c;
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
-    const uint32_t off = (bundle * RPW + (uint32_t)r) * row_bytes + q_off;
-    B.a[p][r] = buf_load16<kNT>(qr, off);
-    B.b[p][r] = buf_load16<kNT>(qr, off + 16u);
-    B.c[p][r] = __builtin_amdgcn_raw_buffer_load_b32(qr, (int)(off + 32u), 0, kNT ? 2 : 0);
+    const __amdgpu_buffer_rsrc_t src = (kDual && r >= kRb) ? qr2 : qr;
+    const uint32_t off = (bundle * kRb + (uint32_t)(r % kRb)) * row_bytes + q_off;
+    B.a[p][r] = buf_load16<kNT>(src, off);
+    B.b[p][r] = buf_load16<kNT>(src, off + 16u);
+    B.c[p][r] = __builtin_amdgcn_raw_buffer_load_b32(src, (int)(off + 32u), 0, kNT ? 2 : 0);
   }
 }
 
@@ -582,7 +587,7 @@ __device__ __forceinline__ void flat_load(typename FlatBufSel<RPW, PF, kQ5, kQ40
                                           uint32_t row_bytes, uint32_t bundle, uint32_t it,
                                           uint32_t s, uint32_t c) {
   if constexpr (kQ40)
-    q4_0_flat_load<RPW, PF, kNT>(B, p, qr, row_bytes, bundle, it, s, c);
+    q4_0_flat_load<RPW, PF, kNT, kDual>(B, p, qr, qr2, row_bytes, bundle, it, s, c);
   else
     q4k_flat_load<RPW, PF, kNT, kDual, kQ5>(B, p, qr, qr2, row_bytes, bundle, it, s, c);
 }
@@ -694,7 +699,7 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
   constexpr int kRb = kDual ? RPW / 2 : RPW; // output rows per bundle
   static_assert(!kDual || RPW % 2 == 0, "the fused kernel pairs gate and up rows");
   static_assert(!(kDual && kQ5), "the fused gate/up kernel reads Q4_K");
-  static_assert(!(kQ40 && (kDual || kQ5)), "Q4_0 rows are a layout of their own");
+  static_assert(!(kQ40 && kQ5), "Q4_0 rows are a layout of their own");
   constexpr bool kEarly = PF == 1;        // refill before the compute, chunked x
   constexpr int kSlots = kEarly ? 2 : PF; // register slots
   constexpr int NT = NW * 64;
@@ -1491,6 +1496,17 @@ AXH_Q6K_MATVEC_ONE(8, 2, p)
                                                        axh_lds_dyn);                             \
   }
 
+// The same fusion over two Q4_0 matrices (rows read as octets of 8 blocks).
+#define AXH_Q4_0_GATE_UP(ROWS, NW, PF, XP)                                                       \
+  extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
+      axh_q4_0_gate_up_r##ROWS##_w##NW##_p##PF##_x##XP(                                          \
+          const uint8_t *__restrict__ qg, const uint8_t *__restrict__ qu,                        \
+          const float *__restrict__ x, float *__restrict__ y, AXH_ROWS_ARGS) { AXH_ROWS_UNPACK; \
+    extern __shared__ float axh_lds_dyn[];                                                       \
+    q4k_matvec_flat<2 * ROWS, NW, PF, false, XP, true, false, true>(                             \
+        qg, qu, x, y, a.n_rows, a.units_per_row, axh_lds_dyn);                                   \
+  }
+
 AXH_Q4K_GATE_UP(1, 4, 2, 1)
 AXH_Q4K_GATE_UP(1, 4, 1, 1)
 AXH_Q4K_GATE_UP(1, 8, 1, 1)
@@ -1500,6 +1516,12 @@ AXH_Q4K_GATE_UP(2, 4, 2, 1)
 AXH_Q4K_GATE_UP(2, 8, 2, 1)
 AXH_Q4K_GATE_UP(1, 4, 2, 2)
 AXH_Q4K_GATE_UP(1, 8, 2, 2)
+AXH_Q4_0_GATE_UP(1, 4, 1, 1)
+AXH_Q4_0_GATE_UP(1, 8, 1, 1)
+AXH_Q4_0_GATE_UP(2, 4, 1, 1)
+AXH_Q4_0_GATE_UP(1, 4, 2, 1)
+AXH_Q4_0_GATE_UP(1, 8, 2, 1)
+AXH_Q4_0_GATE_UP(1, 4, 2, 2)
 
 AXH_Q4K_MATVEC_FLAT(1, 8, 2, 0)
 AXH_Q4K_MATVEC_FLAT(1, 8, 1, 0)

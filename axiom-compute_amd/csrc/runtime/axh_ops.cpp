@@ -111,6 +111,11 @@ constexpr MatvecVariant kQ4_0FlatVariants[] = {
     {1, 4, 1, 2, 1}, {1, 8, 1, 2, 1}, {2, 4, 1, 2, 1}, {2, 8, 1, 2, 1},
     {1, 8, 2, 2, 1}, {2, 4, 2, 2, 2}, {1, 16, 2, 2, 1}};
 constexpr uint32_t kQ4_0FlatRounds = 2; // persistent Q4_0 grid: resident workgroups x 2
+// axh_q4_0_gate_up_r{rpw}_w{nw}_p{pf}_x{xp}: the fused gate/up kernel over two
+// Q4_0 matrices.  Keep in sync with the AXH_Q4_0_GATE_UP list in q4_matvec.hip.
+constexpr MatvecVariant kQ4_0GateUpVariants[] = {
+    {1, 4, 1, 2, 1}, {1, 8, 1, 2, 1}, {2, 4, 1, 2, 1},
+    {1, 4, 2, 2, 1}, {1, 8, 2, 2, 1}, {1, 4, 2, 2, 2}};
 
 constexpr uint32_t kQ4kMaxTileSb = 128;   // tiled kernel: 128 * 1088 B = 136 KiB of LDS
 constexpr uint32_t kQ4kFlatMaxSb = 128;   // persistent kernel: 128 * 1120 B = 140 KiB of LDS
@@ -196,7 +201,7 @@ static const MatvecVariant *find_variant(const MatvecVariant *table, size_t n,
 static axh_status reject_family(const axh_q4_variant *v) {
   if (v && (v->family || v->sb_per_lane))
     return fail(AXH_ERR_INVALID_ARGUMENT,
-                "family and sb_per_lane are holes of the Q4_K matvec (and sb_per_lane of the "
+                "family and sb_per_lane are holes of the Q4_K and Q4_0 matvecs (and of the "
                 "Q5_K / Q6_K one-pass family) only");
   return AXH_OK;
 }
@@ -1307,6 +1312,83 @@ axh_status axh_q4_0_matvec(axh_context *ctx, const void *q, const float *x, floa
   return s == AXH_OK ? ok() : s;
 }
 
+// Fused gate/up over two Q4_0 matrices: the persistent kernel over octets of
+// 8 blocks (rows of an even block count up to 1024 blocks).
+static MatvecVariant q4_0_gate_up_default(uint32_t n_rows, uint32_t nb) {
+  (void)n_rows;
+  (void)nb;
+  return {1, 4, 1, 2, 1};
+}
+
+static axh_status plan_q4_0_gate_up(uint32_t n_rows, uint32_t nb, const axh_q4_variant *variant,
+                                    Q4kPlan *p) {
+  if (reject_family(variant) != AXH_OK) return AXH_ERR_INVALID_ARGUMENT;
+  if (!q4_0_octets_fit(n_rows, nb))
+    return fail(AXH_ERR_INVALID_ARGUMENT,
+                "Q4_0 gate/up: rows of 2-1024 blocks, an even count, each matrix below 4 GiB");
+  if (variant && variant->nontemporal == 1)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "Q4_0 gate/up: no non-temporal variant is compiled");
+  const MatvecVariant dflt = q4_0_gate_up_default(n_rows, nb);
+  const uint32_t want_nw =
+      variant && variant->waves_per_workgroup ? variant->waves_per_workgroup : dflt.nw;
+  const uint32_t min_xp = (nb + want_nw * 64u - 1u) / (want_nw * 64u);
+  const MatvecVariant *v = find_variant(
+      kQ4_0GateUpVariants, sizeof(kQ4_0GateUpVariants) / sizeof(kQ4_0GateUpVariants[0]), variant,
+      dflt, min_xp);
+  if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q4_0 gate/up variant matches");
+  if (!staged_in_chunks(*v) && nb > v->xp * v->nw * 64u)
+    return fail(AXH_ERR_INVALID_ARGUMENT,
+                "Q4_0 gate/up: row too long for this variant's x staging");
+  std::snprintf(p->name, sizeof(p->name), "axh_q4_0_gate_up_r%u_w%u_p%u_x%u", v->rpw, v->nw,
+                v->pf, v->xp);
+  p->nw = v->nw;
+  p->lds = (nb + 7u) / 8u * 1120u;
+  p->flat = true;
+  const uint32_t bundles = (n_rows + v->rpw - 1) / v->rpw;
+  p->units = ((bundles + 1) / 2 + v->nw - 1) / v->nw;
+  p->args = RowsArgs{n_rows, nb, nb, 0};
+  return ok();
+}
+
+axh_status axh_q4_0_gate_up_kernel_name(uint32_t n_rows, uint32_t blocks_per_row,
+                                        const axh_q4_variant *variant, char *buf, size_t cap) {
+  if (!buf || cap == 0) return fail(AXH_ERR_INVALID_ARGUMENT, "buf is NULL");
+  Q4kPlan p{};
+  axh_status s = plan_q4_0_gate_up(n_rows, blocks_per_row, variant, &p);
+  if (s != AXH_OK) return s;
+  if (std::strlen(p.name) + 1 > cap) return fail(AXH_ERR_INVALID_ARGUMENT, "buf too small");
+  std::memcpy(buf, p.name, std::strlen(p.name) + 1);
+  return ok();
+}
+
+axh_status axh_q4_0_gate_up(axh_context *ctx, const void *q_gate, const void *q_up,
+                            const float *x, float *h, uint32_t n_rows, uint32_t blocks_per_row,
+                            const axh_q4_variant *variant, void *stream) {
+  if (!ctx) return fail(AXH_ERR_INVALID_ARGUMENT, "ctx is NULL");
+  if (n_rows == 0) return ok();
+  if (!device_ptr_ok(h) || !device_ptr_ok(q_gate) || !device_ptr_ok(q_up) || !device_ptr_ok(x))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q_gate, q_up, x and h must be device pointers");
+  if (((uintptr_t)q_gate & 3u) || ((uintptr_t)q_up & 3u) || ((uintptr_t)x & 15u))
+    return fail(AXH_ERR_INVALID_ARGUMENT,
+                "q_gate and q_up must be 4-byte and x 16-byte aligned");
+  Q4kPlan p{};
+  axh_status s = plan_q4_0_gate_up(n_rows, blocks_per_row, variant, &p);
+  if (s != AXH_OK) return s;
+  if (p.lds > ctx->core->max_lds)
+    return fail(AXH_ERR_PIPELINE_LAYOUT, "LDS tile exceeds the device limit");
+  hipSetDevice(ctx->core->device);
+  axh_kernel *k = nullptr;
+  s = builtin_kernel(ctx, p.name, 4, sizeof(RowsArgs), p.nw * 64u, &k);
+  if (s != AXH_OK) return s;
+  uint32_t grid[3] = {p.units, 1, 1};
+  const uint32_t resident = occupancy(ctx, k, p.lds) * ctx->core->cu_count;
+  if (resident < grid[0]) grid[0] = resident; // persistent: one resident round
+  void *bufs[4] = {const_cast<void *>(q_gate), const_cast<void *>(q_up), const_cast<float *>(x),
+                   h};
+  s = launch_raw(k, grid, bufs, 4, &p.args, sizeof(p.args), p.lds, pick_stream(ctx, stream));
+  return s == AXH_OK ? ok() : s;
+}
+
 // Kind 5 LDS: each wave's ring of `pf` buffers, one 1 KiB slot row per
 // 16-byte-per-lane load of a step (2*nt for X, ceil(48*rt/64) for the
 // weights), reused at the end for the waves' partial tiles (1 KiB per tile).
@@ -1735,6 +1817,9 @@ static axh_status bench_call(axh_context *ctx, const axh_bench_op *o, uint32_t i
   case AXH_BENCH_Q4K_GATE_UP:
     return axh_q4k_gate_up(ctx, q, q + o->q2_offset, static_cast<const float *>(o->x),
                            static_cast<float *>(o->y), o->n_rows, o->units, o->variant, nullptr);
+  case AXH_BENCH_Q4_0_GATE_UP:
+    return axh_q4_0_gate_up(ctx, q, q + o->q2_offset, static_cast<const float *>(o->x),
+                            static_cast<float *>(o->y), o->n_rows, o->units, o->variant, nullptr);
   case AXH_BENCH_Q4K_MATMUL_F16:
     return axh_q4k_matmul_f16(ctx, q, static_cast<const uint16_t *>(o->x),
                               static_cast<float *>(o->y), o->n_rows, o->units, o->batch,

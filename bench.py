@@ -61,6 +61,7 @@ WORKLOADS = {
     # Q4_0 checkpoints store every projection in it: the same shapes as Q4_0
     "down0": ("q4_0", 4096, 448, 0.5, "Llama-3-8B ffn_down as Q4_0, not a BASELINE config"),
     "head0": ("q4_0", 128256, 128, 1.0, "Llama-3-8B output head as Q4_0, not a BASELINE config"),
+    "ffn0": ("gate_up0", 14336, 128, 0.5, "Llama-3-8B gate/up as Q4_0, not a BASELINE config"),
 }
 KQ_IDS = {"q5k": 13, "q6k": 14}
 
@@ -121,8 +122,8 @@ class Case:
         self.kind, self.rows, self.units, self.label = kind, rows, units, label
         self.ctx, self.O, self.np, self.pkg = ctx, O, np, pkg
         self.batch = batch if kind == "matmul" else 1
-        unit_bytes = {"q4_0": 18, "q5k": 176, "q6k": 210}.get(kind, 144)
-        self.cols = units * (32 if kind == "q4_0" else 256)
+        unit_bytes = {"q4_0": 18, "gate_up0": 18, "q5k": 176, "q6k": 210}.get(kind, 144)
+        self.cols = units * (32 if kind in ("q4_0", "gate_up0") else 256)
         self.weight_bytes = rows * units * unit_bytes
         seed = 20241 if name == "c4" else 30000 + rows + units
         self.up_off = 0
@@ -130,10 +131,11 @@ class Case:
             self.q = O.gen_q4_0_weights(seed, rows * units)
         elif kind in KQ_IDS:
             self.q = O.gen_kq_weights(KQ_IDS[kind], seed, rows * units)
-        elif kind == "gate_up":
+        elif kind in ("gate_up", "gate_up0"):
             # gate rows, then the up rows at the next COPY_ALIGN boundary
-            self.qg = O.gen_q4k_weights(seed, rows * units)
-            self.qu = O.gen_q4k_weights(seed + 7, rows * units)
+            gen = O.gen_q4k_weights if kind == "gate_up" else O.gen_q4_0_weights
+            self.qg = gen(seed, rows * units)
+            self.qu = gen(seed + 7, rows * units)
             self.up_off = -(-self.weight_bytes // COPY_ALIGN) * COPY_ALIGN
             self.q = np.zeros(self.up_off + self.weight_bytes, dtype=np.uint8)
             self.q[: self.weight_bytes] = self.qg
@@ -178,6 +180,9 @@ class Case:
         elif self.kind == "gate_up":
             self.ctx.q4k_gate_up(w, w + self.up_off, self.dx, self.dy, self.rows, self.units,
                                  self.variant)
+        elif self.kind == "gate_up0":
+            self.ctx.q4_0_gate_up(w, w + self.up_off, self.dx, self.dy, self.rows, self.units,
+                                  self.variant)
         elif self.x_f32:
             self.ctx.q4k_matmul_f32(w, self.dx, self.dx16, self.dy, self.rows, self.units,
                                     self.batch, self.variant)
@@ -188,7 +193,7 @@ class Case:
     def bench_op(self) -> dict:
         """Arguments of ctx.bench_loop for this workload (call i reads copy i)."""
         op = {"q4k": "q4k", "q4_0": "q4_0", "q5k": "q5k", "q6k": "q6k",
-              "gate_up": "gate_up"}.get(self.kind)
+              "gate_up": "gate_up", "gate_up0": "gate_up_q4_0"}.get(self.kind)
         if op is None:
             op = "matmul_f32" if self.x_f32 else "matmul_f16"
         return dict(op=op, q=self.wbuf, q_stride=self.stride, n_copies=self.n_copies, x=self.dx,
@@ -202,6 +207,8 @@ class Case:
             return self.pkg.q4_0_matvec_kernel_name(self.rows, self.units, self.variant)
         if self.kind == "gate_up":
             return self.pkg.q4k_gate_up_kernel_name(self.rows, self.units, self.variant)
+        if self.kind == "gate_up0":
+            return self.pkg.q4_0_gate_up_kernel_name(self.rows, self.units, self.variant)
         if self.kind == "q5k":
             return self.pkg.q5k_matvec_kernel_name(self.rows, self.units, self.variant)
         if self.kind == "q6k":
@@ -233,8 +240,9 @@ class Case:
             rep = O.matvec_tolerance_report(y, ref, yf, ad, self.cols)
             return {k: rep[k] for k in ("ok", "rows_failed", "norm_rel_err",
                                         "gpu_err_vs_f64_norm", "cpu_err_vs_f64_norm")}
-        if self.kind == "gate_up":
-            _, g, ag, u, au = O.q4k_gate_up_f64(self.qg, self.qu, self.x, self.rows, self.units)
+        if self.kind in ("gate_up", "gate_up0"):
+            f64 = O.q4k_gate_up_f64 if self.kind == "gate_up" else O.q4_0_gate_up_f64
+            _, g, ag, u, au = f64(self.qg, self.qu, self.x, self.rows, self.units)
             rep = O.gate_up_tolerance_report(y, g, ag, u, au, self.cols)
             return {k: rep[k] for k in ("ok", "rows_failed", "worst_over_bound", "norm_rel_err")}
         # batched: against the f64 product of the same RN_f16 weights
@@ -266,15 +274,18 @@ class Case:
             many = lambda: O.kq_matvec(kid, self.q, self.x, self.rows, self.units,
                                        threads=threads)
             frac, what = 1.0, f"full {self.rows}x{self.cols} {self.kind.upper()} matvecs"
-        elif self.kind == "gate_up":
+        elif self.kind in ("gate_up", "gate_up0"):
+            mv = O.q4k_matvec if self.kind == "gate_up" else O.q4_0_matvec
+            fmt = "Q4_K" if self.kind == "gate_up" else "Q4_0"
+
             def two(threads):
-                g = O.q4k_matvec(self.qg, self.x, self.rows, self.units, threads=threads)
-                u = O.q4k_matvec(self.qu, self.x, self.rows, self.units, threads=threads)
+                g = mv(self.qg, self.x, self.rows, self.units, threads=threads)
+                u = mv(self.qu, self.x, self.rows, self.units, threads=threads)
                 return O.silu(g) * u
 
             one = lambda: two(1)
             many = lambda: two(threads)
-            frac, what = 1.0, f"gate+up {self.rows}x{self.cols} Q4_K matvec pairs + silu*mul"
+            frac, what = 1.0, f"gate+up {self.rows}x{self.cols} {fmt} matvec pairs + silu*mul"
         elif self.kind == "q4_0":
             one = lambda: O.q4_0_matvec(self.q, self.x, self.rows, self.units, threads=1)
             many = lambda: O.q4_0_matvec(self.q, self.x, self.rows, self.units, threads=threads)
@@ -510,7 +521,7 @@ def main() -> int:
                     "calls of the matvec and of each floor",
         }
     kernel = case.kernel()
-    shape = (("2x" if kind == "gate_up" else "") + f"{case.rows}x{case.cols}"
+    shape = (("2x" if kind in ("gate_up", "gate_up0") else "") + f"{case.rows}x{case.cols}"
              + (f"xB{case.batch}" if kind == "matmul" else ""))
     traffic, traffic_src = profiled_traffic(kernel, shape)
 
@@ -538,8 +549,9 @@ def main() -> int:
         if kind == "matmul":
             metric = (f"Q4_K_M x f16 matmul weight-bytes HBM GB/s at {case.rows}x{case.cols}, "
                       f"B={case.batch}; us/call")
-        elif kind == "gate_up":
-            metric = (f"Q4_K_M fused gate+up (silu(g)*u) weight-bytes HBM GB/s at {shape}; "
+        elif kind in ("gate_up", "gate_up0"):
+            fmt = "Q4_K_M" if kind == "gate_up" else "Q4_0"
+            metric = (f"{fmt} fused gate+up (silu(g)*u) weight-bytes HBM GB/s at {shape}; "
                       "us/call")
         else:
             metric = f"{qname} matvec weight-bytes HBM GB/s (% of peak) at {shape}; us/call"

@@ -345,6 +345,18 @@ axh_status axh_q4k_gate_up_kernel_name(uint32_t n_rows, uint32_t sb_per_row,
                                        const axh_q4_variant *variant, char *buf, size_t cap);
 uint32_t axh_q4k_gate_up_variant_count(void);
 axh_status axh_q4k_gate_up_variant_at(uint32_t i, axh_q4_variant *out);
+/* The same fusion over two Q4_0 matrices (n_rows rows of blocks_per_row
+ * 18-byte blocks each; x holds blocks_per_row * 32 f32): equals two
+ * axh_q4_0_matvec calls followed by silu(g) * u.  No counterpart in the
+ * reference (see axh_q4k_gate_up).  Limits: blocks_per_row even, 2-1024;
+ * each matrix below 4 GiB; q_gate / q_up 4-byte and x 16-byte aligned.
+ * Variant holes as for axh_q4k_gate_up (the persistent kernel over octets of
+ * 8 blocks). */
+axh_status axh_q4_0_gate_up(axh_context *ctx, const void *q_gate, const void *q_up,
+                            const float *x, float *h, uint32_t n_rows, uint32_t blocks_per_row,
+                            const axh_q4_variant *variant, void *stream);
+axh_status axh_q4_0_gate_up_kernel_name(uint32_t n_rows, uint32_t blocks_per_row,
+                                        const axh_q4_variant *variant, char *buf, size_t cap);
 /* Decode-only kernels, bit-exact with the reference's CPU dequantisation
  * (common_helpers.rs:437-454; common.rs:229-253): w receives 256 (Q4_K) or
  * 32 (Q4_0) f32 per unit in the reference's element order. */
@@ -474,8 +486,9 @@ enum {
     AXH_BENCH_Q4K_MATVEC = 1, AXH_BENCH_Q4_0_MATVEC = 2, AXH_BENCH_Q5K_MATVEC = 3,
     AXH_BENCH_Q6K_MATVEC = 4, AXH_BENCH_Q4K_GATE_UP = 5, AXH_BENCH_Q4K_MATMUL_F16 = 6,
     AXH_BENCH_Q4K_MATMUL_F32 = 7, AXH_BENCH_READ_FLOOR = 8, AXH_BENCH_LAUNCH_EMPTY = 9,
-    AXH_BENCH_READ_SHAPE = 10 /* axh_read_floor_shape: n_rows = workgroups, variant->
-                                 waves_per_workgroup = threads / 64, variant->prefetch = loads */
+    AXH_BENCH_READ_SHAPE = 10, /* axh_read_floor_shape: n_rows = workgroups, variant->
+                                  waves_per_workgroup = threads / 64, variant->prefetch = loads */
+    AXH_BENCH_Q4_0_GATE_UP = 11
 };
 typedef struct axh_bench_op {
     uint32_t op;                   /* AXH_BENCH_* */

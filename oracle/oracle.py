@@ -247,6 +247,13 @@ def q4k_gate_up_f64(q_gate, q_up, x, n_rows: int, sb_per_row: int):
     return silu(g) * u, g, ag, u, au
 
 
+def q4_0_gate_up_f64(q_gate, q_up, x, n_rows: int, blocks_per_row: int):
+    """The same for two Q4_0 matrices (q4_0_matvec_f64 row dots)."""
+    g, ag = q4_0_matvec_f64(q_gate, x, n_rows, blocks_per_row)
+    u, au = q4_0_matvec_f64(q_up, x, n_rows, blocks_per_row)
+    return silu(g) * u, g, ag, u, au
+
+
 def gate_up_tolerance_report(h_gpu, g, ag, u, au, n_cols: int, rel_tol: float = 1e-3,
                              cancel_frac: float = 0.1) -> dict:
     """Acceptance for h = silu(g) * u when each dot product may carry the

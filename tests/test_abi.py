@@ -474,6 +474,24 @@ def test_q4_0_kernel_selection(axc):
             assert f"axh_q4_0_matvec_onep_i{nit}".encode() in co
 
 
+def test_q4_0_gate_up_selection(axc):
+    """Fused Q4_0 gate/up: the persistent kernel over octets (4 waves, early
+    refill by default), its holes, and typed errors for odd or long rows."""
+    name, V = axc.q4_0_gate_up_kernel_name, axc.Variant
+    co = axc.builtin_code_object()
+    assert name(14336, 128) == name(1, 2) == name(100, 1024) == "axh_q4_0_gate_up_r1_w4_p1_x1"
+    for (r, w, pf), want in (((1, 8, 1), "r1_w8_p1_x1"), ((2, 4, 1), "r2_w4_p1_x1"),
+                             ((1, 4, 2), "r1_w4_p2_x1"), ((1, 8, 2), "r1_w8_p2_x1")):
+        got = name(14336, 128, V(r, w, pf, 0))
+        assert got == f"axh_q4_0_gate_up_{want}" and got.encode() in co
+    assert name(14336, 448, V(1, 4, 2, 0)) == "axh_q4_0_gate_up_r1_w4_p2_x2"
+    for bad in ((4, 127, None), (4, 1026, None), (4, 0, None), (4, 2, V(0, 0, 0, 1)),
+                (4, 2, V(4, 4, 1, 0)), (4, 2, V(family=1)), (4, 600, V(1, 8, 2, 0)),
+                (4, 600, V(1, 4, 2, 0))):
+        with pytest.raises(axc.DispatchError):
+            name(*bad)
+
+
 def test_q4_0_family_holes(axc):
     """The Q4_0 families and their holes: persistent (rows_per_wave,
     waves_per_workgroup, prefetch), one pass (sb_per_lane = steps of 64 blocks,

@@ -143,3 +143,90 @@ def test_invalid_arguments_are_typed_errors(ctx, axc):
         ctx.q4k_gate_up(b, b, b, b, 4, 1, axc.Variant(3, 4, 2, 0))  # not compiled
     ctx.q4k_gate_up(b, b, b, b, 0, 1)  # empty: nothing to do
     b.close()
+
+
+# ---- the same fusion over two Q4_0 matrices ---------------------------------------
+def _inputs0(seed, rows, nb, sigma=0.5):
+    qg = O.gen_q4_0_weights(seed, rows * nb)
+    qu = O.gen_q4_0_weights(seed + 1, rows * nb)
+    x = O.gen_normal_f32(seed + 2, nb * 32, sigma)
+    return qg, qu, x
+
+
+def _gate_up0(ctx, qg, qu, x, rows, nb, variant=None):
+    dg, du, dx, dh = _dev(ctx, qg), _dev(ctx, qu), _dev(ctx, x), ctx.alloc(rows * 4)
+    ctx.q4_0_gate_up(dg, du, dx, dh, rows, nb, variant)
+    ctx.synchronize()
+    h = np.frombuffer(ctx.download(dh, rows * 4), dtype=np.float32).copy()
+    for b in (dg, du, dx, dh):
+        b.close()
+    return h
+
+
+def _matvec0(ctx, q, x, rows, nb, variant=None):
+    dq, dx, dy = _dev(ctx, q), _dev(ctx, x), ctx.alloc(rows * 4)
+    ctx.q4_0_matvec(dq, dx, dy, rows, nb, variant)
+    ctx.synchronize()
+    y = np.frombuffer(ctx.download(dy, rows * 4), dtype=np.float32).copy()
+    for b in (dq, dx, dy):
+        b.close()
+    return y
+
+
+def _check0(h, qg, qu, x, rows, nb, what):
+    _, g, ag, u, au = O.q4_0_gate_up_f64(qg, qu, x, rows, nb)
+    rep = O.gate_up_tolerance_report(h, g, ag, u, au, nb * 32, REL_TOL)
+    _say(f"{what}: {rep}")
+    assert rep["ok"], f"{what}: {rep}"
+
+
+def test_q4_0_llama3_8b_ffn_shape(ctx):
+    """Gate and up projections of a Q4_0 Llama-3-8B: 14336 rows x 4096 columns."""
+    rows, nb = 14336, 128
+    _say("q4_0 gate_up 14336x4096")
+    qg, qu, x = _inputs0(730, rows, nb)
+    h = _gate_up0(ctx, qg, qu, x, rows, nb)
+    _check0(h, qg, qu, x, rows, nb, "q4_0 gate_up 14336x4096")
+
+
+@pytest.mark.parametrize("rows,nb", [(1, 2), (3, 66), (31, 1024), (257, 130), (1000, 64),
+                                     (4097, 8), (64, 446), (20011, 18)])
+def test_q4_0_edge_shapes(ctx, rows, nb):
+    """Odd row counts, one block pair, partial last octets (a quarter of 2
+    blocks live, or 3), the longest row (1024 blocks), more rows than the
+    persistent grid holds."""
+    _say(f"q4_0 gate_up edge {rows}x{nb}")
+    qg, qu, x = _inputs0(rows * 3 + nb, rows, nb, sigma=1.0)
+    h = _gate_up0(ctx, qg, qu, x, rows, nb)
+    _check0(h, qg, qu, x, rows, nb, f"q4_0 edge {rows}x{nb}")
+
+
+@pytest.mark.parametrize("holes", [(1, 4, 1), (1, 8, 1), (2, 4, 1), (1, 4, 2), (1, 8, 2)])
+def test_q4_0_every_variant_matches_two_matvecs(ctx, axc, holes):
+    """Each compiled Q4_0 gate/up variant against the oracle, and against two
+    persistent Q4_0 matvecs with the same holes where one is compiled:
+    silu(g) * u of their outputs agrees to f32 rounding of the combination."""
+    rows, nb = 1531, 194
+    qg, qu, x = _inputs0(740, rows, nb)
+    v = axc.Variant(*holes, 0)
+    _say(f"q4_0 gate_up variant {holes}: {axc.q4_0_gate_up_kernel_name(rows, nb, v)}")
+    h = _gate_up0(ctx, qg, qu, x, rows, nb, v)
+    _check0(h, qg, qu, x, rows, nb, f"q4_0 variant {holes}")
+    mv = axc.Variant(*holes, 2, axc.FAMILY_PERSISTENT)
+    try:
+        g = _matvec0(ctx, qg, x, rows, nb, mv)
+        u = _matvec0(ctx, qu, x, rows, nb, mv)
+    except axc.DispatchError:
+        return  # no matvec compiled with these holes
+    want = O.silu(g.astype(np.float64)) * u.astype(np.float64)
+    assert np.all(np.abs(h - want) <= 4 * 2.0 ** -24 * np.abs(want) + 1e-30), str(holes)
+
+
+def test_q4_0_invalid_arguments_are_typed_errors(ctx, axc):
+    b = ctx.alloc(1 << 20)
+    for bad in ((4, 0, None), (4, 127, None), (4, 1026, None), (4, 2, axc.Variant(0, 0, 0, 1)),
+                (4, 2, axc.Variant(4, 4, 1, 0)), (4, 2, axc.Variant(family=1))):
+        with pytest.raises(axc.DispatchError):
+            ctx.q4_0_gate_up(b, b, b, b, *bad)
+    ctx.q4_0_gate_up(b, b, b, b, 0, 2)  # empty: nothing to do
+    b.close()
