@@ -180,7 +180,8 @@ def test_events_time_launches_on_the_context_stream(ctx, axc):
 def test_graph_replays_match_eager_results(ctx, axc):
     """Captured matvec / Q4_0 / matmul launches replayed several times, with
     eager work and synchronisation between replays; every replay is compared
-    bit for bit with the eager result."""
+    bit for bit with the eager result.  The Q4_0 launches cover the column,
+    one-pass and persistent kernels and the fused gate/up."""
     rows, sb, nb, batch = 300, 16, 128, 24
     q = O.gen_q4k_weights(81, rows * sb)
     x = O.gen_normal_f32(82, sb * 256)
@@ -192,14 +193,19 @@ def test_graph_replays_match_eager_results(ctx, axc):
     ksb, krows = 128, 5
     qk = O.gen_q4k_weights(86, krows * ksb)
     xk = O.gen_normal_f32(87, ksb * 256)
+    rows0b = 600  # Q4_0 past 512 rows: the one-pass kernel
+    q0b = O.gen_q4_0_weights(88, rows0b * nb)
     bufs = {}
     for name, arr in (("q", q), ("x", x), ("q0", q0), ("x0", x0), ("xh", xh), ("qk", qk),
-                      ("xk", xk)):
+                      ("xk", xk), ("q0b", q0b)):
         bufs[name] = ctx.alloc(arr.nbytes)
         ctx.upload(bufs[name], arr)
     y1, y2, y3 = ctx.alloc(rows * 4), ctx.alloc(rows * 4), ctx.alloc(rows * batch * 4)
     y4, y5 = ctx.alloc(32), ctx.alloc(16)
-    outs = ((y1, rows * 4), (y2, rows * 4), (y3, rows * batch * 4), (y4, krows * 4), (y5, 4))
+    y6, y7, y8 = ctx.alloc(rows0b * 4), ctx.alloc(rows * 4), ctx.alloc(rows * 4)
+    outs = ((y1, rows * 4), (y2, rows * 4), (y3, rows * batch * 4), (y4, krows * 4), (y5, 4),
+            (y6, rows0b * 4), (y7, rows * 4), (y8, rows * 4))
+    persistent = axc.Variant(family=axc.FAMILY_PERSISTENT)
 
     def ops():
         ctx.q4k_matvec(bufs["q"], bufs["x"], y1, rows, sb)
@@ -207,14 +213,18 @@ def test_graph_replays_match_eager_results(ctx, axc):
         ctx.q4k_matmul(bufs["q"], bufs["xh"], y3, rows, sb, batch)
         ctx.q4k_matvec(bufs["qk"], bufs["xk"], y4, krows, ksb)
         ctx.q4k_matvec(bufs["qk"], bufs["xk"], y5, 1, ksb)
+        ctx.q4_0_matvec(bufs["q0b"], bufs["x0"], y6, rows0b, nb)
+        ctx.q4_0_gate_up(bufs["q0"], bufs["q0b"], bufs["x0"], y7, rows, nb)
+        ctx.q4_0_matvec(bufs["q0"], bufs["x0"], y8, rows, nb, persistent)
 
     assert axc.q4k_matvec_kernel_name(krows, ksb).startswith("axh_q4k_matvec_sk_")
+    assert axc.q4_0_matvec_kernel_name(rows0b, nb) == "axh_q4_0_matvec_one_i2"
     assert axc.q4k_matvec_kernel_name(1, ksb).startswith("axh_q4k_matvec_wg_")
     ops()  # eager (also prepares every kernel and the workspace before capture)
     ctx.synchronize()
     eager = [ctx.download(b, n) for b, n in outs]
     g = ctx.capture(ops)
-    assert g.node_count == 5
+    assert g.node_count == 8
     for rep in range(4):
         for b, n in outs:
             ctx.upload(b, np.full(n // 4, np.nan, dtype=np.float32))  # poison between replays
@@ -240,7 +250,7 @@ def test_graph_replays_match_eager_results(ctx, axc):
     assert ctx.download(y1, rows * 4) == eager[0]
     g2.close()
     other.close()
-    for b in list(bufs.values()) + [y1, y2, y3, y4, y5]:
+    for b in list(bufs.values()) + [y1, y2, y3, y4, y5, y6, y7, y8]:
         b.close()
 
 
