@@ -861,8 +861,37 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
 // stream of another (A/B in one run, 14336 x 4096: 8.27-8.40 vs 8.78-9.00
 // us), and costs where one workgroup per CU waits for all of x (4096 x 14336:
 // 8.64-8.70 vs 8.12-8.22 us).
+// The store of the wave-paired gate/up kernels: each wave reduces its two
+// rows (lanes 0-31 and 32-63); the odd wave of a pair (the second matrix)
+// leaves its sums in LDS, and after a barrier of the whole workgroup the even
+// wave stores silu(g) * u for both rows.  xch holds 2 floats per wave pair.
+__device__ __forceinline__ void gate_up_pair_store(float v, uint32_t pair, uint32_t wave,
+                                                   uint32_t lane, bool mine, uint32_t n_rows,
+                                                   float *__restrict__ y, float *xch) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x141>(v);
+  v += dpp_mov<0x140>(v);
+  const int vi = __builtin_bit_cast(int, v);
+  const float h0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 0)) +
+                   __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 16));
+  const float h1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 32)) +
+                   __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 48));
+  float *slot = xch + 2u * (wave >> 1);
+  if ((wave & 1u) && lane == 0) {
+    slot[0] = h0;
+    slot[1] = h1;
+  }
+  __syncthreads();
+  if (!(wave & 1u) && mine && lane == 0) {
+    const uint32_t r0 = 2u * pair, r1 = r0 + 1u;
+    if (r0 < n_rows) y[r0] = silu_mul(h0, slot[0]);
+    if (r1 < n_rows) y[r1] = silu_mul(h1, slot[1]);
+  }
+}
+
 template <int NIT, bool kDual = false, bool kQ5 = false, bool kWhole = false, int XD = 1,
-          bool kQ40 = false>
+          bool kQ40 = false, bool kPair = false>
 __device__ __forceinline__ void q4k_matvec_one(const uint8_t *__restrict__ q,
                                                const uint8_t *__restrict__ q2,
                                                const float *__restrict__ x, float *__restrict__ y,
@@ -873,15 +902,21 @@ __device__ __forceinline__ void q4k_matvec_one(const uint8_t *__restrict__ q,
   const uint32_t lane = tid & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t G = lane >> 2, half = G >> 3, s = G & 7u, c = lane & 3u;
-  const uint32_t W = blockIdx.x * NW + wave;
+  // kPair (fused gate/up): waves 2P and 2P + 1 take rows 2P and 2P + 1 of
+  // the first and of the second matrix, one row per lane slot, so the pair's
+  // loads go through one wave-uniform resource each; W is the pair index.
+  static_assert(!(kPair && kDual), "one pairing of gate and up rows");
+  const uint32_t W = kPair ? (blockIdx.x * NW + wave) >> 1 : blockIdx.x * NW + wave;
   const bool mine = W < (n_rows + 1u) >> 1; // this wave has a pair of rows
   static_assert(!(kQ40 && (kDual || kQ5)), "Q4_0 rows are a layout of their own");
   // kQ40: nsb is the row's Q4_0 block count, read as octets of 8 blocks.
   const uint32_t n_units = kQ40 ? (nsb + 7u) >> 3 : nsb;
   const uint32_t row_bytes =
       nsb * (kQ40 ? (uint32_t)kQ4_0BlockBytes : kQ5 ? kQ5kSbBytes : (uint32_t)kQ4kSbBytes);
-  const __amdgpu_buffer_rsrc_t qr = make_rsrc(q, n_rows * row_bytes);
-  const __amdgpu_buffer_rsrc_t qr2 = kDual ? make_rsrc(q2, n_rows * row_bytes) : qr;
+  const __amdgpu_buffer_rsrc_t q1r = make_rsrc(q, n_rows * row_bytes);
+  const __amdgpu_buffer_rsrc_t q2r = (kDual || kPair) ? make_rsrc(q2, n_rows * row_bytes) : q1r;
+  const __amdgpu_buffer_rsrc_t qr = (kPair && (wave & 1u)) ? q2r : q1r;
+  const __amdgpu_buffer_rsrc_t qr2 = kPair ? qr : q2r;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, nsb * (kQ40 ? 128u : 1024u));
   float *xs = lds;
   float *ss = lds + n_units * kQ4kFlatSbFloats;
@@ -912,7 +947,10 @@ __device__ __forceinline__ void q4k_matvec_one(const uint8_t *__restrict__ q,
       const uint32_t sb = (uint32_t)j * 8u + s;
       if (mine && sb < n_units) flat_compute<RPW, 2, kQ5, kQ40>(B, p, xs, ss, sb, c, nsb, acc);
     }
-    if (mine) q4k_flat_store<RPW, kDual>(acc, 2u * W, lane, n_rows, y);
+    if constexpr (kPair)
+      gate_up_pair_store(acc[0], W, wave, lane, mine, n_rows, y, ss + n_units * 8u);
+    else if (mine)
+      q4k_flat_store<RPW, kDual>(acc, 2u * W, lane, n_rows, y);
     return;
   }
   // x chunks are requested XD iterations ahead of their staging (issued
@@ -943,7 +981,10 @@ __device__ __forceinline__ void q4k_matvec_one(const uint8_t *__restrict__ q,
     const uint32_t sb = (uint32_t)j * 8u + s;
     if (mine && sb < n_units) flat_compute<RPW, 2, kQ5, kQ40>(B, p, xs, ss, sb, c, nsb, acc);
   }
-  if (mine) q4k_flat_store<RPW, kDual>(acc, 2u * W, lane, n_rows, y);
+  if constexpr (kPair)
+    gate_up_pair_store(acc[0], W, wave, lane, mine, n_rows, y, ss + n_units * 8u);
+  else if (mine)
+    q4k_flat_store<RPW, kDual>(acc, 2u * W, lane, n_rows, y);
 }
 
 #define AXH_Q4K_MATVEC_ONE(NIT)                                                                  \
@@ -1506,6 +1547,46 @@ AXH_Q6K_MATVEC_ONE(8, 2, p)
     q4k_matvec_flat<2 * ROWS, NW, PF, false, XP, true, false, true>(                             \
         qg, qu, x, y, a.n_rows, a.units_per_row, axh_lds_dyn);                                   \
   }
+
+// Wave-paired one-pass gate/up (axh_q4k_gate_up_one{,x}_i{NIT} and the Q4_0
+// axh_q4_0_gate_up_one{,x}_i{NIT}): one workgroup of 8 waves per 8 output
+// rows, the even wave of a pair reading gate rows and the odd wave the same
+// up rows, x staged chunk by chunk (one) or whole (onex).
+#define AXH_GATE_UP_ONE(FMT, Q40, NIT)                                                           \
+  extern "C" __global__ void __launch_bounds__(512)                                              \
+      axh_##FMT##_gate_up_one_i##NIT(const uint8_t *__restrict__ qg,                             \
+                                     const uint8_t *__restrict__ qu,                             \
+                                     const float *__restrict__ x, float *__restrict__ y,         \
+                                     AXH_ROWS_ARGS) { AXH_ROWS_UNPACK;                           \
+    extern __shared__ float axh_lds_dyn[];                                                       \
+    q4k_matvec_one<NIT, false, false, false, 1, Q40, true>(qg, qu, x, y, a.n_rows,               \
+                                                           a.units_per_row, axh_lds_dyn);       \
+  }                                                                                              \
+  extern "C" __global__ void __launch_bounds__(512)                                              \
+      axh_##FMT##_gate_up_onex_i##NIT(const uint8_t *__restrict__ qg,                            \
+                                      const uint8_t *__restrict__ qu,                            \
+                                      const float *__restrict__ x, float *__restrict__ y,        \
+                                      AXH_ROWS_ARGS) { AXH_ROWS_UNPACK;                          \
+    extern __shared__ float axh_lds_dyn[];                                                       \
+    q4k_matvec_one<NIT, false, false, true, 1, Q40, true>(qg, qu, x, y, a.n_rows,                \
+                                                          a.units_per_row, axh_lds_dyn);        \
+  }
+AXH_GATE_UP_ONE(q4k, false, 1)
+AXH_GATE_UP_ONE(q4_0, true, 1)
+AXH_GATE_UP_ONE(q4k, false, 2)
+AXH_GATE_UP_ONE(q4_0, true, 2)
+AXH_GATE_UP_ONE(q4k, false, 3)
+AXH_GATE_UP_ONE(q4_0, true, 3)
+AXH_GATE_UP_ONE(q4k, false, 4)
+AXH_GATE_UP_ONE(q4_0, true, 4)
+AXH_GATE_UP_ONE(q4k, false, 5)
+AXH_GATE_UP_ONE(q4_0, true, 5)
+AXH_GATE_UP_ONE(q4k, false, 6)
+AXH_GATE_UP_ONE(q4_0, true, 6)
+AXH_GATE_UP_ONE(q4k, false, 7)
+AXH_GATE_UP_ONE(q4_0, true, 7)
+AXH_GATE_UP_ONE(q4k, false, 8)
+AXH_GATE_UP_ONE(q4_0, true, 8)
 
 AXH_Q4K_GATE_UP(1, 4, 2, 1)
 AXH_Q4K_GATE_UP(1, 4, 1, 1)

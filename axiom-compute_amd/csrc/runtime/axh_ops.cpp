@@ -202,7 +202,7 @@ static axh_status reject_family(const axh_q4_variant *v) {
   if (v && (v->family || v->sb_per_lane))
     return fail(AXH_ERR_INVALID_ARGUMENT,
                 "family and sb_per_lane are holes of the Q4_K and Q4_0 matvecs (and of the "
-                "Q5_K / Q6_K one-pass family) only");
+                "one-pass families of Q5_K / Q6_K and of the gate/up operations) only");
   return AXH_OK;
 }
 
@@ -779,13 +779,75 @@ static MatvecVariant gate_up_default(uint32_t n_rows, uint32_t nsb) {
   return {1, 8, 2, 2, 1};
 }
 
+// The wave-paired one-pass gate/up kernels (axh_{q4k,q4_0}_gate_up_one{,x}_i*):
+// one workgroup of 8 waves per 8 output rows, the even wave of a pair on the
+// gate rows and the odd wave on the same up rows, rows of up to 8 steps (64
+// superblocks or 512 Q4_0 blocks).  Family ONE_PASS (x chunk by chunk) or
+// ONE_PASS_X (x whole); the only hole is sb_per_lane.  The shape's limits
+// are checked by the caller.
+constexpr uint32_t kGateUpOneMaxIt = 8;
+
+static axh_status plan_gate_up_one(bool q40, uint32_t n_rows, uint32_t units,
+                                   const axh_q4_variant *variant, Q4kPlan *p) {
+  if (variant->rows_per_wave || variant->waves_per_workgroup || variant->prefetch ||
+      variant->nontemporal)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "the gate/up one-pass families' only hole is sb_per_lane");
+  const uint32_t per_step = q40 ? 64u : 8u; // blocks or superblocks per step
+  const uint32_t need = (units + per_step - 1u) / per_step;
+  const uint32_t nit = variant->sb_per_lane ? variant->sb_per_lane : need;
+  if (nit < need || nit > kGateUpOneMaxIt)
+    return fail(AXH_ERR_INVALID_ARGUMENT,
+                "gate/up one pass: sb_per_lane must cover the row and be at most 8");
+  std::snprintf(p->name, sizeof(p->name), "axh_%s_gate_up_one%s_i%u", q40 ? "q4_0" : "q4k",
+                variant->family == AXH_Q4K_FAMILY_ONE_PASS_X ? "x" : "", nit);
+  const uint32_t n_units = q40 ? (units + 7u) / 8u : units;
+  p->nw = 8;
+  p->lds = n_units * 1120u + 32u; // x, its sums, and 2 floats per wave pair
+  p->flat = false;                // one workgroup per 8 output rows, all launched
+  p->units = (n_rows + 7u) / 8u;
+  p->args = RowsArgs{n_rows, units, units, 0};
+  return ok();
+}
+
+static bool gate_up_one_family(const axh_q4_variant *v) {
+  return v && (v->family == AXH_Q4K_FAMILY_ONE_PASS || v->family == AXH_Q4K_FAMILY_ONE_PASS_X);
+}
+
+// With no hole set, up to 12288 rows of up to 8 steps take the wave-paired
+// one-pass kernel (x chunk by chunk up to 2048 rows, whole beyond), larger
+// matrices the persistent one.  A/B in one run, us per call, Q4_K / Q4_0
+// against the persistent default: 1024 x 4096 4.02 / 3.99 vs 4.88 / 4.92,
+// 4096 x 4096 (x whole) 5.95 / 5.92 vs 6.91 / 6.80, 11008 x 4096 12.85 /
+// 12.49 vs 13.43 / 13.13; but 14336 x 4096 15.32 / 14.78 vs 14.82 / 14.61
+// and 28672 x 8192 52.3 / 47.6 vs 46.7 / 46.3 (the pair's closing barrier
+// keeps a workgroup's waves from retiring on their own).
+constexpr uint32_t kGateUpOneMaxRows = 12288, kGateUpOneChunkMaxRows = 2048;
+
+static bool gate_up_default_one(const axh_q4_variant *variant, uint32_t n_rows, uint32_t nit,
+                                axh_q4_variant *out) {
+  if (variant && (variant->rows_per_wave || variant->waves_per_workgroup ||
+                  variant->prefetch || variant->nontemporal || variant->family ||
+                  variant->sb_per_lane))
+    return false;
+  if (n_rows > kGateUpOneMaxRows || nit > kGateUpOneMaxIt) return false;
+  *out = axh_q4_variant{};
+  out->family = n_rows <= kGateUpOneChunkMaxRows ? AXH_Q4K_FAMILY_ONE_PASS
+                                                 : AXH_Q4K_FAMILY_ONE_PASS_X;
+  return true;
+}
+
 static axh_status plan_gate_up(uint32_t n_rows, uint32_t sb_per_row,
                                const axh_q4_variant *variant, Q4kPlan *p) {
-  if (reject_family(variant) != AXH_OK) return AXH_ERR_INVALID_ARGUMENT;
+  if (!gate_up_one_family(variant) && reject_family(variant) != AXH_OK)
+    return AXH_ERR_INVALID_ARGUMENT;
   if (sb_per_row == 0 || sb_per_row > kQ4kFlatMaxSb)
     return fail(AXH_ERR_INVALID_ARGUMENT, "gate/up: sb_per_row must be 1..128");
   if ((uint64_t)n_rows * sb_per_row * 144u >= 0xFFFFFFFFull)
     return fail(AXH_ERR_INVALID_ARGUMENT, "gate/up: each matrix must be below 4 GiB");
+  if (gate_up_one_family(variant)) return plan_gate_up_one(false, n_rows, sb_per_row, variant, p);
+  axh_q4_variant one{};
+  if (gate_up_default_one(variant, n_rows, (sb_per_row + 7u) / 8u, &one))
+    return plan_gate_up_one(false, n_rows, sb_per_row, &one, p);
   if (variant && variant->nontemporal == 1)
     return fail(AXH_ERR_INVALID_ARGUMENT, "gate/up: no non-temporal variant is compiled");
   const MatvecVariant dflt = gate_up_default(n_rows, sb_per_row);
@@ -1322,10 +1384,15 @@ static MatvecVariant q4_0_gate_up_default(uint32_t n_rows, uint32_t nb) {
 
 static axh_status plan_q4_0_gate_up(uint32_t n_rows, uint32_t nb, const axh_q4_variant *variant,
                                     Q4kPlan *p) {
-  if (reject_family(variant) != AXH_OK) return AXH_ERR_INVALID_ARGUMENT;
+  if (!gate_up_one_family(variant) && reject_family(variant) != AXH_OK)
+    return AXH_ERR_INVALID_ARGUMENT;
   if (!q4_0_octets_fit(n_rows, nb))
     return fail(AXH_ERR_INVALID_ARGUMENT,
                 "Q4_0 gate/up: rows of 2-1024 blocks, an even count, each matrix below 4 GiB");
+  if (gate_up_one_family(variant)) return plan_gate_up_one(true, n_rows, nb, variant, p);
+  axh_q4_variant one{};
+  if (gate_up_default_one(variant, n_rows, (nb + 63u) / 64u, &one))
+    return plan_gate_up_one(true, n_rows, nb, &one, p);
   if (variant && variant->nontemporal == 1)
     return fail(AXH_ERR_INVALID_ARGUMENT, "Q4_0 gate/up: no non-temporal variant is compiled");
   const MatvecVariant dflt = q4_0_gate_up_default(n_rows, nb);
@@ -1381,8 +1448,10 @@ axh_status axh_q4_0_gate_up(axh_context *ctx, const void *q_gate, const void *q_
   s = builtin_kernel(ctx, p.name, 4, sizeof(RowsArgs), p.nw * 64u, &k);
   if (s != AXH_OK) return s;
   uint32_t grid[3] = {p.units, 1, 1};
-  const uint32_t resident = occupancy(ctx, k, p.lds) * ctx->core->cu_count;
-  if (resident < grid[0]) grid[0] = resident; // persistent: one resident round
+  if (p.flat) { // persistent: at most one resident round of workgroups
+    const uint32_t resident = occupancy(ctx, k, p.lds) * ctx->core->cu_count;
+    if (resident < grid[0]) grid[0] = resident;
+  }
   void *bufs[4] = {const_cast<void *>(q_gate), const_cast<void *>(q_up), const_cast<float *>(x),
                    h};
   s = launch_raw(k, grid, bufs, 4, &p.args, sizeof(p.args), p.lds, pick_stream(ctx, stream));

@@ -204,8 +204,8 @@ void axh_event_destroy(axh_event *ev);
  * 25-32 superblocks and 4097-8191 rows of 74 or more, which take the
  * persistent family; persistent beyond,
  * tiled for rows of more than 128 superblocks.  Every default is a hole
- * assignment.  The gate/up operation
- * takes the persistent holes only (family = sb_per_lane = 0).
+ * assignment.  The gate/up operations
+ * take the persistent holes, or their one-pass families (see axh_q4k_gate_up).
  * Q4_0 takes family PERSISTENT (axh_q4_0_matvec_flat_r*_w*_p*_x*: the Q4_K
  * persistent kernel over octets of 8 blocks; holes rows_per_wave,
  * waves_per_workgroup, prefetch), ONE_PASS / ONE_PASS_X
@@ -335,9 +335,16 @@ axh_status axh_matvec_ggml(axh_context *ctx, uint32_t ggml_type, const void *q, 
  * matvec per dispatch (multi-row work is roadmap, ROADMAP.md:54-72); it
  * equals two axh_q4k_matvec calls followed by silu(g) * u, with each dot
  * product held to the matvec's tolerance.  Limits: 1 <= sb_per_row <= 128,
- * each matrix below 4 GiB, q_gate / q_up / x 16-byte aligned.  Variant holes:
- * rows_per_wave = output rows per lane group (each reads that many gate and
- * up rows), waves_per_workgroup, prefetch; nontemporal 0 or 2. */
+ * each matrix below 4 GiB, q_gate / q_up / x 16-byte aligned.  Variant holes
+ * (the persistent kernel): rows_per_wave = output rows per lane group (each
+ * reads that many gate and up rows), waves_per_workgroup, prefetch;
+ * nontemporal 0 or 2.  Or family = AXH_Q4K_FAMILY_ONE_PASS / _ONE_PASS_X
+ * (x chunk by chunk / whole) with sb_per_lane 1-8 (rows of up to 64
+ * superblocks): the wave-paired one-pass kernels, one workgroup per 8 output
+ * rows, the even wave of a pair on gate rows and the odd wave on up rows.
+ * With no hole set, up to 12288 rows of up to 64 superblocks take the
+ * one-pass kernel (x whole from 2049 rows), larger matrices the persistent
+ * one. */
 axh_status axh_q4k_gate_up(axh_context *ctx, const void *q_gate, const void *q_up,
                            const float *x, float *h, uint32_t n_rows, uint32_t sb_per_row,
                            const axh_q4_variant *variant, void *stream);
@@ -350,8 +357,8 @@ axh_status axh_q4k_gate_up_variant_at(uint32_t i, axh_q4_variant *out);
  * axh_q4_0_matvec calls followed by silu(g) * u.  No counterpart in the
  * reference (see axh_q4k_gate_up).  Limits: blocks_per_row even, 2-1024;
  * each matrix below 4 GiB; q_gate / q_up 4-byte and x 16-byte aligned.
- * Variant holes as for axh_q4k_gate_up (the persistent kernel over octets of
- * 8 blocks). */
+ * Variant holes and defaults as for axh_q4k_gate_up (the kernels over octets of
+ * 8 blocks; one-pass rows of up to 512 blocks). */
 axh_status axh_q4_0_gate_up(axh_context *ctx, const void *q_gate, const void *q_up,
                             const float *x, float *h, uint32_t n_rows, uint32_t blocks_per_row,
                             const axh_q4_variant *variant, void *stream);

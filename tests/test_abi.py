@@ -316,7 +316,25 @@ def test_gate_up_kernel_selection(axc):
     assert name(14336, 128) == "axh_q4k_gate_up_r1_w8_p2_x2"
     assert name(14336, 16, axc.Variant(2, 8, 2, 0)) == "axh_q4k_gate_up_r2_w8_p2_x1"
     assert name(14336, 56, axc.Variant(1, 4, 2, 0)) == "axh_q4k_gate_up_r1_w4_p2_x2"
+    # up to 12288 rows of up to 64 superblocks: the wave-paired one-pass kernel
+    assert name(1024, 16) == name(2048, 16) == "axh_q4k_gate_up_one_i2"
+    assert name(2049, 16) == "axh_q4k_gate_up_onex_i2"
+    assert name(12288, 64) == "axh_q4k_gate_up_onex_i8"
+    assert name(12289, 16) == "axh_q4k_gate_up_r1_w4_p1_x1"
+    assert name(4096, 65) == "axh_q4k_gate_up_r1_w8_p2_x2"
+    V, one, onex = axc.Variant, axc.FAMILY_ONE_PASS, axc.FAMILY_ONE_PASS_X
+    assert name(14336, 16, V(family=onex)) == "axh_q4k_gate_up_onex_i2"
+    assert name(14336, 16, V(family=one, sb_per_lane=5)) == "axh_q4k_gate_up_one_i5"
+    for bad in ((4, 16, V(family=one, sb_per_lane=1)), (4, 16, V(family=one, sb_per_lane=9)),
+                (4, 65, V(family=one)), (4, 16, V(1, 0, 0, 0, one)), (4, 16, V(family=1)),
+                (4, 16, V(sb_per_lane=2))):
+        with pytest.raises(axc.DispatchError):
+            name(*bad)
     co = axc.builtin_code_object()
+    for nit in range(1, 9):
+        for fmt in ("q4k", "q4_0"):
+            assert f"axh_{fmt}_gate_up_one_i{nit}".encode() in co
+            assert f"axh_{fmt}_gate_up_onex_i{nit}".encode() in co
     vs = axc.compiled_variants("gate_up")
     assert len(set(vs)) == len(vs) >= 4
     for v in vs:
@@ -479,7 +497,12 @@ def test_q4_0_gate_up_selection(axc):
     refill by default), its holes, and typed errors for odd or long rows."""
     name, V = axc.q4_0_gate_up_kernel_name, axc.Variant
     co = axc.builtin_code_object()
-    assert name(14336, 128) == name(1, 2) == name(100, 1024) == "axh_q4_0_gate_up_r1_w4_p1_x1"
+    assert name(14336, 128) == name(100, 1024) == "axh_q4_0_gate_up_r1_w4_p1_x1"
+    assert name(1, 2) == "axh_q4_0_gate_up_one_i1"
+    assert name(4096, 128) == name(12288, 128) == "axh_q4_0_gate_up_onex_i2"
+    assert name(2048, 512) == "axh_q4_0_gate_up_one_i8"
+    assert name(2048, 514) == "axh_q4_0_gate_up_r1_w4_p1_x1"
+    assert name(14336, 128, V(family=axc.FAMILY_ONE_PASS)) == "axh_q4_0_gate_up_one_i2"
     for (r, w, pf), want in (((1, 8, 1), "r1_w8_p1_x1"), ((2, 4, 1), "r2_w4_p1_x1"),
                              ((1, 4, 2), "r1_w4_p2_x1"), ((1, 8, 2), "r1_w8_p2_x1")):
         got = name(14336, 128, V(r, w, pf, 0))

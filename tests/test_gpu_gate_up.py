@@ -230,3 +230,42 @@ def test_q4_0_invalid_arguments_are_typed_errors(ctx, axc):
             ctx.q4_0_gate_up(b, b, b, b, *bad)
     ctx.q4_0_gate_up(b, b, b, b, 0, 2)  # empty: nothing to do
     b.close()
+
+
+# ---- wave-paired one-pass gate/up kernels (both formats) ------------------------
+@pytest.mark.parametrize("fam,nit_extra", [(2, 0), (3, 0), (2, 1), (3, 1)])
+@pytest.mark.parametrize("rows,units,q40", [(1, 1, False), (7, 3, False), (14336, 16, False),
+                                           (1531, 24, False), (33, 64, False), (9, 2, True),
+                                           (1531, 194, True), (14336, 128, True),
+                                           (100, 512, True), (17, 66, True)])
+def test_paired_one_pass_kernels(ctx, axc, rows, units, q40, fam, nit_extra):
+    """One workgroup per 8 output rows, gate rows on the even wave of a pair
+    and up rows on the odd one, x chunk by chunk (family 2) or whole (3), the
+    row's trip count and one past it: odd row counts (a pair with one row),
+    partial last workgroups and octets, the longest rows (8 steps), against
+    the f64 oracle and, for the Q4_K kernels, within 4 ulp of two one-pass
+    matvecs with the same trip count."""
+    per = 64 if q40 else 8
+    nit = (units + per - 1) // per + nit_extra
+    if nit > 8:
+        pytest.skip("8 steps at most")
+    v = axc.Variant(family=fam, sb_per_lane=nit)
+    name = (axc.q4_0_gate_up_kernel_name if q40 else axc.q4k_gate_up_kernel_name)(rows, units, v)
+    assert name == f"axh_{'q4_0' if q40 else 'q4k'}_gate_up_one{'x' if fam == 3 else ''}_i{nit}"
+    _say(f"paired gate_up {rows}x{units} {name}")
+    if q40:
+        qg, qu, x = _inputs0(rows * 11 + units, rows, units)
+        h = _gate_up0(ctx, qg, qu, x, rows, units, v)
+        _check0(h, qg, qu, x, rows, units, f"paired {name} {rows}x{units}")
+        mv = axc.Variant(prefetch=1 if fam == 2 else 0, family=fam, sb_per_lane=nit)
+        g = _matvec0(ctx, qg, x, rows, units, mv)
+        u = _matvec0(ctx, qu, x, rows, units, mv)
+    else:
+        qg, qu, x = _inputs(rows * 11 + units, rows, units)
+        h = _gate_up(ctx, qg, qu, x, rows, units, v)
+        _check(h, qg, qu, x, rows, units, f"paired {name} {rows}x{units}")
+        mv = axc.Variant(prefetch=1 if fam == 2 else 0, family=fam, sb_per_lane=nit)
+        g = _matvec(ctx, qg, x, rows, units, mv)
+        u = _matvec(ctx, qu, x, rows, units, mv)
+    want = O.silu(g.astype(np.float64)) * u.astype(np.float64)
+    assert np.all(np.abs(h - want) <= 4 * 2.0 ** -24 * np.abs(want) + 1e-30), name
