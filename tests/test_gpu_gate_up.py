@@ -233,11 +233,24 @@ def test_q4_0_invalid_arguments_are_typed_errors(ctx, axc):
 
 
 # ---- wave-paired one-pass gate/up kernels (both formats) ------------------------
-@pytest.mark.parametrize("fam,nit_extra", [(2, 0), (3, 0), (2, 1), (3, 1)])
-@pytest.mark.parametrize("rows,units,q40", [(1, 1, False), (7, 3, False), (14336, 16, False),
-                                           (1531, 24, False), (33, 64, False), (9, 2, True),
-                                           (1531, 194, True), (14336, 128, True),
-                                           (100, 512, True), (17, 66, True)])
+_PAIRED_SHAPES = [(1, 1, False), (7, 3, False), (14336, 16, False), (1531, 24, False),
+                  (33, 64, False), (9, 2, True), (1531, 194, True), (14336, 128, True),
+                  (100, 512, True), (17, 66, True)]
+
+
+def _paired_cases():
+    """Every shape with family 2 and 3, at the row's trip count and one past
+    it where that is still at most 8 steps."""
+    out = []
+    for rows, units, q40 in _PAIRED_SHAPES:
+        need = (units + (64 if q40 else 8) - 1) // (64 if q40 else 8)
+        for extra in (0, 1):
+            if need + extra <= 8:
+                out += [(rows, units, q40, fam, extra) for fam in (2, 3)]
+    return out
+
+
+@pytest.mark.parametrize("rows,units,q40,fam,nit_extra", _paired_cases())
 def test_paired_one_pass_kernels(ctx, axc, rows, units, q40, fam, nit_extra):
     """One workgroup per 8 output rows, gate rows on the even wave of a pair
     and up rows on the odd one, x chunk by chunk (family 2) or whole (3), the
@@ -247,8 +260,6 @@ def test_paired_one_pass_kernels(ctx, axc, rows, units, q40, fam, nit_extra):
     matvecs with the same trip count."""
     per = 64 if q40 else 8
     nit = (units + per - 1) // per + nit_extra
-    if nit > 8:
-        pytest.skip("8 steps at most")
     v = axc.Variant(family=fam, sb_per_lane=nit)
     name = (axc.q4_0_gate_up_kernel_name if q40 else axc.q4k_gate_up_kernel_name)(rows, units, v)
     assert name == f"axh_{'q4_0' if q40 else 'q4k'}_gate_up_one{'x' if fam == 3 else ''}_i{nit}"
