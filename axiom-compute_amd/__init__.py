@@ -12,4 +12,4 @@ from .axh import (  # noqa: F401
     builtin_code_object, compiled_matmul_variants, compiled_variants, ggml_type_size,
     load_library, q4_0_gate_up_kernel_name, q4_0_matvec_kernel_name, q4k_gate_up_kernel_name,
     q4k_matmul_kernel_name, q4k_matvec_default_variant, q4k_matvec_kernel_name,
-    q5k_matvec_kernel_name, q6k_matvec_kernel_name, validate_request)
+    q5k_gate_up_kernel_name, q5k_matvec_kernel_name, q6k_matvec_kernel_name, validate_request)

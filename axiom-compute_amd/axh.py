@@ -121,7 +121,7 @@ class _BenchOp(ctypes.Structure):
 
 BENCH_OPS = {"q4k": 1, "q4_0": 2, "q5k": 3, "q6k": 4, "gate_up": 5, "matmul_f16": 6,
              "matmul_f32": 7, "read_floor": 8, "launch_empty": 9, "read_shape": 10,
-             "gate_up_q4_0": 11}
+             "gate_up_q4_0": 11, "gate_up_q5k": 12}
 
 
 class _GgufTensorInfo(ctypes.Structure):
@@ -193,6 +193,7 @@ def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
         "axh_q4_0_matvec_kernel_name": (st, [u32, u32, c.POINTER(_Variant), c.c_char_p, sz]),
         "axh_q4k_gate_up": (st, [vp, vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
         "axh_q4_0_gate_up": (st, [vp, vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
+        "axh_q5k_gate_up": (st, [vp, vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
         "axh_q5k_matvec": (st, [vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
         "axh_q6k_matvec": (st, [vp, vp, vp, vp, u32, u32, c.POINTER(_Variant), vp]),
         "axh_q5k_matvec_kernel_name": (st, [u32, u32, c.POINTER(_Variant), c.c_char_p, sz]),
@@ -220,6 +221,7 @@ def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
         "axh_gguf_find_kv": (st, [vp, c.c_char_p, c.POINTER(u64)]),
         "axh_q4k_gate_up_kernel_name": (st, [u32, u32, c.POINTER(_Variant), c.c_char_p, sz]),
         "axh_q4_0_gate_up_kernel_name": (st, [u32, u32, c.POINTER(_Variant), c.c_char_p, sz]),
+        "axh_q5k_gate_up_kernel_name": (st, [u32, u32, c.POINTER(_Variant), c.c_char_p, sz]),
         "axh_q4k_gate_up_variant_count": (u32, []),
         "axh_q4k_gate_up_variant_at": (st, [u32, c.POINTER(_Variant)]),
         "axh_q4k_matmul_f16": (st, [vp, vp, vp, vp, u32, u32, u32, c.POINTER(_MatmulVariant),
@@ -384,6 +386,17 @@ def q4_0_gate_up_kernel_name(n_rows: int, blocks_per_row: int,
     buf = ctypes.create_string_buffer(64)
     _check(lib.axh_q4_0_gate_up_kernel_name(n_rows, blocks_per_row,
                                             ctypes.byref(v) if v else None, buf, 64))
+    return buf.value.decode()
+
+
+def q5k_gate_up_kernel_name(n_rows: int, sb_per_row: int,
+                            variant: Optional[Variant] = None) -> str:
+    """Entry point axh_q5k_gate_up launches for this shape and variant."""
+    lib = load_library()
+    v = variant._c() if variant else None
+    buf = ctypes.create_string_buffer(64)
+    _check(lib.axh_q5k_gate_up_kernel_name(n_rows, sb_per_row, ctypes.byref(v) if v else None,
+                                           buf, 64))
     return buf.value.decode()
 
 
@@ -790,6 +803,14 @@ class HipContext:
         _check(self._lib.axh_q4_0_gate_up(self._raw, _ptr(q_gate), _ptr(q_up), _ptr(x), _ptr(h),
                                           n_rows, blocks_per_row, ctypes.byref(v) if v else None,
                                           _stream(stream)))
+
+    def q5k_gate_up(self, q_gate, q_up, x, h, n_rows: int, sb_per_row: int,
+                    variant: Optional[Variant] = None, stream=None) -> None:
+        """The same fusion over two Q5_K matrices (the one-pass kernels)."""
+        v = variant._c() if variant else None
+        _check(self._lib.axh_q5k_gate_up(self._raw, _ptr(q_gate), _ptr(q_up), _ptr(x), _ptr(h),
+                                         n_rows, sb_per_row, ctypes.byref(v) if v else None,
+                                         _stream(stream)))
 
     def q5k_matvec(self, q, x, y, n_rows: int, sb_per_row: int,
                    variant: Optional[Variant] = None, stream=None) -> None:

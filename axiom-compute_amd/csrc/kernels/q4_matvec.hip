@@ -698,7 +698,6 @@ __device__ __forceinline__ void q4k_matvec_flat(const uint8_t *__restrict__ q,
                                                 uint32_t nsb, float *lds) {
   constexpr int kRb = kDual ? RPW / 2 : RPW; // output rows per bundle
   static_assert(!kDual || RPW % 2 == 0, "the fused kernel pairs gate and up rows");
-  static_assert(!(kDual && kQ5), "the fused gate/up kernel reads Q4_K");
   static_assert(!(kQ40 && kQ5), "Q4_0 rows are a layout of their own");
   constexpr bool kEarly = PF == 1;        // refill before the compute, chunked x
   constexpr int kSlots = kEarly ? 2 : PF; // register slots
@@ -1549,18 +1548,18 @@ AXH_Q6K_MATVEC_ONE(8, 2, p)
   }
 
 // Wave-paired one-pass gate/up (axh_q4k_gate_up_one{,x}_i{NIT} and the Q4_0
-// axh_q4_0_gate_up_one{,x}_i{NIT}): one workgroup of 8 waves per 8 output
-// rows, the even wave of a pair reading gate rows and the odd wave the same
-// up rows, x staged chunk by chunk (one) or whole (onex).
-#define AXH_GATE_UP_ONE(FMT, Q40, NIT)                                                           \
+// and Q5_K axh_{q4_0,q5k}_gate_up_one{,x}_i{NIT}): one workgroup of 8 waves
+// per 8 output rows, the even wave of a pair reading gate rows and the odd
+// wave the same up rows, x staged chunk by chunk (one) or whole (onex).
+#define AXH_GATE_UP_ONE(FMT, Q5, Q40, NIT)                                                       \
   extern "C" __global__ void __launch_bounds__(512)                                              \
       axh_##FMT##_gate_up_one_i##NIT(const uint8_t *__restrict__ qg,                             \
                                      const uint8_t *__restrict__ qu,                             \
                                      const float *__restrict__ x, float *__restrict__ y,         \
                                      AXH_ROWS_ARGS) { AXH_ROWS_UNPACK;                           \
     extern __shared__ float axh_lds_dyn[];                                                       \
-    q4k_matvec_one<NIT, false, false, false, 1, Q40, true>(qg, qu, x, y, a.n_rows,               \
-                                                           a.units_per_row, axh_lds_dyn);       \
+    q4k_matvec_one<NIT, false, Q5, false, 1, Q40, true>(qg, qu, x, y, a.n_rows,                  \
+                                                        a.units_per_row, axh_lds_dyn);          \
   }                                                                                              \
   extern "C" __global__ void __launch_bounds__(512)                                              \
       axh_##FMT##_gate_up_onex_i##NIT(const uint8_t *__restrict__ qg,                            \
@@ -1568,25 +1567,33 @@ AXH_Q6K_MATVEC_ONE(8, 2, p)
                                       const float *__restrict__ x, float *__restrict__ y,        \
                                       AXH_ROWS_ARGS) { AXH_ROWS_UNPACK;                          \
     extern __shared__ float axh_lds_dyn[];                                                       \
-    q4k_matvec_one<NIT, false, false, true, 1, Q40, true>(qg, qu, x, y, a.n_rows,                \
-                                                          a.units_per_row, axh_lds_dyn);        \
+    q4k_matvec_one<NIT, false, Q5, true, 1, Q40, true>(qg, qu, x, y, a.n_rows,                   \
+                                                       a.units_per_row, axh_lds_dyn);           \
   }
-AXH_GATE_UP_ONE(q4k, false, 1)
-AXH_GATE_UP_ONE(q4_0, true, 1)
-AXH_GATE_UP_ONE(q4k, false, 2)
-AXH_GATE_UP_ONE(q4_0, true, 2)
-AXH_GATE_UP_ONE(q4k, false, 3)
-AXH_GATE_UP_ONE(q4_0, true, 3)
-AXH_GATE_UP_ONE(q4k, false, 4)
-AXH_GATE_UP_ONE(q4_0, true, 4)
-AXH_GATE_UP_ONE(q4k, false, 5)
-AXH_GATE_UP_ONE(q4_0, true, 5)
-AXH_GATE_UP_ONE(q4k, false, 6)
-AXH_GATE_UP_ONE(q4_0, true, 6)
-AXH_GATE_UP_ONE(q4k, false, 7)
-AXH_GATE_UP_ONE(q4_0, true, 7)
-AXH_GATE_UP_ONE(q4k, false, 8)
-AXH_GATE_UP_ONE(q4_0, true, 8)
+AXH_GATE_UP_ONE(q4k, false, false, 1)
+AXH_GATE_UP_ONE(q4_0, false, true, 1)
+AXH_GATE_UP_ONE(q5k, true, false, 1)
+AXH_GATE_UP_ONE(q4k, false, false, 2)
+AXH_GATE_UP_ONE(q4_0, false, true, 2)
+AXH_GATE_UP_ONE(q5k, true, false, 2)
+AXH_GATE_UP_ONE(q4k, false, false, 3)
+AXH_GATE_UP_ONE(q4_0, false, true, 3)
+AXH_GATE_UP_ONE(q5k, true, false, 3)
+AXH_GATE_UP_ONE(q4k, false, false, 4)
+AXH_GATE_UP_ONE(q4_0, false, true, 4)
+AXH_GATE_UP_ONE(q5k, true, false, 4)
+AXH_GATE_UP_ONE(q4k, false, false, 5)
+AXH_GATE_UP_ONE(q4_0, false, true, 5)
+AXH_GATE_UP_ONE(q5k, true, false, 5)
+AXH_GATE_UP_ONE(q4k, false, false, 6)
+AXH_GATE_UP_ONE(q4_0, false, true, 6)
+AXH_GATE_UP_ONE(q5k, true, false, 6)
+AXH_GATE_UP_ONE(q4k, false, false, 7)
+AXH_GATE_UP_ONE(q4_0, false, true, 7)
+AXH_GATE_UP_ONE(q5k, true, false, 7)
+AXH_GATE_UP_ONE(q4k, false, false, 8)
+AXH_GATE_UP_ONE(q4_0, false, true, 8)
+AXH_GATE_UP_ONE(q5k, true, false, 8)
 
 AXH_Q4K_GATE_UP(1, 4, 2, 1)
 AXH_Q4K_GATE_UP(1, 4, 1, 1)
@@ -1597,6 +1604,20 @@ AXH_Q4K_GATE_UP(2, 4, 2, 1)
 AXH_Q4K_GATE_UP(2, 8, 2, 1)
 AXH_Q4K_GATE_UP(1, 4, 2, 2)
 AXH_Q4K_GATE_UP(1, 8, 2, 2)
+// ... and over two Q5_K matrices (the persistent kernel with both flags).
+#define AXH_Q5K_GATE_UP(ROWS, NW, PF, XP)                                                        \
+  extern "C" __global__ void __launch_bounds__(NW * 64)                                          \
+      axh_q5k_gate_up_r##ROWS##_w##NW##_p##PF##_x##XP(                                           \
+          const uint8_t *__restrict__ qg, const uint8_t *__restrict__ qu,                        \
+          const float *__restrict__ x, float *__restrict__ y, AXH_ROWS_ARGS) { AXH_ROWS_UNPACK; \
+    extern __shared__ float axh_lds_dyn[];                                                       \
+    q4k_matvec_flat<2 * ROWS, NW, PF, false, XP, true, true>(qg, qu, x, y, a.n_rows,             \
+                                                             a.units_per_row, axh_lds_dyn);      \
+  }
+AXH_Q5K_GATE_UP(1, 4, 1, 1)
+AXH_Q5K_GATE_UP(1, 8, 1, 1)
+AXH_Q5K_GATE_UP(1, 4, 2, 1)
+AXH_Q5K_GATE_UP(1, 4, 2, 2)
 AXH_Q4_0_GATE_UP(1, 4, 1, 1)
 AXH_Q4_0_GATE_UP(1, 8, 1, 1)
 AXH_Q4_0_GATE_UP(2, 4, 1, 1)

@@ -787,7 +787,7 @@ static MatvecVariant gate_up_default(uint32_t n_rows, uint32_t nsb) {
 // are checked by the caller.
 constexpr uint32_t kGateUpOneMaxIt = 8;
 
-static axh_status plan_gate_up_one(bool q40, uint32_t n_rows, uint32_t units,
+static axh_status plan_gate_up_one(const char *fmt, bool q40, uint32_t n_rows, uint32_t units,
                                    const axh_q4_variant *variant, Q4kPlan *p) {
   if (variant->rows_per_wave || variant->waves_per_workgroup || variant->prefetch ||
       variant->nontemporal)
@@ -798,7 +798,7 @@ static axh_status plan_gate_up_one(bool q40, uint32_t n_rows, uint32_t units,
   if (nit < need || nit > kGateUpOneMaxIt)
     return fail(AXH_ERR_INVALID_ARGUMENT,
                 "gate/up one pass: sb_per_lane must cover the row and be at most 8");
-  std::snprintf(p->name, sizeof(p->name), "axh_%s_gate_up_one%s_i%u", q40 ? "q4_0" : "q4k",
+  std::snprintf(p->name, sizeof(p->name), "axh_%s_gate_up_one%s_i%u", fmt,
                 variant->family == AXH_Q4K_FAMILY_ONE_PASS_X ? "x" : "", nit);
   const uint32_t n_units = q40 ? (units + 7u) / 8u : units;
   p->nw = 8;
@@ -844,10 +844,11 @@ static axh_status plan_gate_up(uint32_t n_rows, uint32_t sb_per_row,
     return fail(AXH_ERR_INVALID_ARGUMENT, "gate/up: sb_per_row must be 1..128");
   if ((uint64_t)n_rows * sb_per_row * 144u >= 0xFFFFFFFFull)
     return fail(AXH_ERR_INVALID_ARGUMENT, "gate/up: each matrix must be below 4 GiB");
-  if (gate_up_one_family(variant)) return plan_gate_up_one(false, n_rows, sb_per_row, variant, p);
+  if (gate_up_one_family(variant))
+    return plan_gate_up_one("q4k", false, n_rows, sb_per_row, variant, p);
   axh_q4_variant one{};
   if (gate_up_default_one(variant, n_rows, (sb_per_row + 7u) / 8u, &one))
-    return plan_gate_up_one(false, n_rows, sb_per_row, &one, p);
+    return plan_gate_up_one("q4k", false, n_rows, sb_per_row, &one, p);
   if (variant && variant->nontemporal == 1)
     return fail(AXH_ERR_INVALID_ARGUMENT, "gate/up: no non-temporal variant is compiled");
   const MatvecVariant dflt = gate_up_default(n_rows, sb_per_row);
@@ -893,6 +894,98 @@ axh_status axh_q4k_gate_up(axh_context *ctx, const void *q_gate, const void *q_u
     return fail(AXH_ERR_INVALID_ARGUMENT, "q_gate, q_up and x must be 16-byte aligned");
   Q4kPlan p{};
   axh_status s = plan_gate_up(n_rows, sb_per_row, variant, &p);
+  if (s != AXH_OK) return s;
+  if (p.lds > ctx->core->max_lds)
+    return fail(AXH_ERR_PIPELINE_LAYOUT, "LDS tile exceeds the device limit");
+  hipSetDevice(ctx->core->device);
+  axh_kernel *k = nullptr;
+  s = builtin_kernel(ctx, p.name, 4, sizeof(RowsArgs), p.nw * 64u, &k);
+  if (s != AXH_OK) return s;
+  uint32_t grid[3] = {p.units, 1, 1};
+  if (p.flat) { // persistent: at most one resident round of workgroups
+    const uint32_t resident = occupancy(ctx, k, p.lds) * ctx->core->cu_count;
+    if (resident < grid[0]) grid[0] = resident;
+  }
+  void *bufs[4] = {const_cast<void *>(q_gate), const_cast<void *>(q_up), const_cast<float *>(x),
+                   h};
+  s = launch_raw(k, grid, bufs, 4, &p.args, sizeof(p.args), p.lds, pick_stream(ctx, stream));
+  return s == AXH_OK ? ok() : s;
+}
+
+// Fused gate/up over two Q5_K matrices.  With no hole set: the wave-paired
+// one-pass kernel with x chunk by chunk up to 12288 rows of up to 8 steps
+// (ahead of x staged whole at every size measured: 14336 x 4096 18.9 vs
+// 20.1 us, 11008 x 4096 16.1 vs 16.7), else the persistent kernel with 4
+// waves, x whole and two iterations in flight (28672 x 8192 58.4 us against
+// 81.7 for the one-pass kernel and 2 x 32.7 for two Q5_K matvec calls;
+// 13824 x 5120 23.7 against 24.8 and 2 x 14.5), early refill past 64
+// superblocks.  The persistent holes and the one-pass families (family,
+// sb_per_lane) select the others.
+constexpr MatvecVariant kQ5GateUpVariants[] = {
+    {1, 4, 1, 2, 1}, {1, 8, 1, 2, 1}, {1, 4, 2, 2, 1}, {1, 4, 2, 2, 2}};
+
+static axh_status plan_q5k_gate_up(uint32_t n_rows, uint32_t sb_per_row,
+                                   const axh_q4_variant *variant, Q4kPlan *p) {
+  if (!gate_up_one_family(variant) && reject_family(variant) != AXH_OK)
+    return AXH_ERR_INVALID_ARGUMENT;
+  if (sb_per_row == 0 || sb_per_row > kQ4kFlatMaxSb)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "Q5_K gate/up: sb_per_row must be 1..128");
+  if ((uint64_t)n_rows * sb_per_row * 176u >= 0xFFFFFFFFull)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "Q5_K gate/up: each matrix must be below 4 GiB");
+  if (gate_up_one_family(variant))
+    return plan_gate_up_one("q5k", false, n_rows, sb_per_row, variant, p);
+  axh_q4_variant one{};
+  if (gate_up_default_one(variant, n_rows, (sb_per_row + 7u) / 8u, &one)) {
+    one.family = AXH_Q4K_FAMILY_ONE_PASS;
+    return plan_gate_up_one("q5k", false, n_rows, sb_per_row, &one, p);
+  }
+  if (variant && variant->nontemporal == 1)
+    return fail(AXH_ERR_INVALID_ARGUMENT, "Q5_K gate/up: no non-temporal variant is compiled");
+  const MatvecVariant dflt =
+      sb_per_row <= 64u ? MatvecVariant{1, 4, 2, 2, 1} : MatvecVariant{1, 4, 1, 2, 1};
+  const uint32_t want_nw =
+      variant && variant->waves_per_workgroup ? variant->waves_per_workgroup : dflt.nw;
+  const uint32_t min_xp = (sb_per_row * 8u + want_nw * 64u - 1u) / (want_nw * 64u);
+  const MatvecVariant *v = find_variant(
+      kQ5GateUpVariants, sizeof(kQ5GateUpVariants) / sizeof(kQ5GateUpVariants[0]), variant, dflt,
+      min_xp);
+  if (!v) return fail(AXH_ERR_INVALID_ARGUMENT, "no compiled Q5_K gate/up variant matches");
+  if (!staged_in_chunks(*v) && sb_per_row * 8u > v->xp * v->nw * 64u)
+    return fail(AXH_ERR_INVALID_ARGUMENT,
+                "Q5_K gate/up: row too long for this variant's x staging");
+  std::snprintf(p->name, sizeof(p->name), "axh_q5k_gate_up_r%u_w%u_p%u_x%u", v->rpw, v->nw,
+                v->pf, v->xp);
+  p->nw = v->nw;
+  p->lds = sb_per_row * 1120u;
+  p->flat = true;
+  const uint32_t bundles = (n_rows + v->rpw - 1) / v->rpw;
+  p->units = ((bundles + 1) / 2 + v->nw - 1) / v->nw;
+  p->args = RowsArgs{n_rows, sb_per_row, sb_per_row, 0};
+  return ok();
+}
+
+axh_status axh_q5k_gate_up_kernel_name(uint32_t n_rows, uint32_t sb_per_row,
+                                       const axh_q4_variant *variant, char *buf, size_t cap) {
+  if (!buf || cap == 0) return fail(AXH_ERR_INVALID_ARGUMENT, "buf is NULL");
+  Q4kPlan p{};
+  axh_status s = plan_q5k_gate_up(n_rows, sb_per_row, variant, &p);
+  if (s != AXH_OK) return s;
+  if (std::strlen(p.name) + 1 > cap) return fail(AXH_ERR_INVALID_ARGUMENT, "buf too small");
+  std::memcpy(buf, p.name, std::strlen(p.name) + 1);
+  return ok();
+}
+
+axh_status axh_q5k_gate_up(axh_context *ctx, const void *q_gate, const void *q_up,
+                           const float *x, float *h, uint32_t n_rows, uint32_t sb_per_row,
+                           const axh_q4_variant *variant, void *stream) {
+  if (!ctx) return fail(AXH_ERR_INVALID_ARGUMENT, "ctx is NULL");
+  if (n_rows == 0) return ok();
+  if (!device_ptr_ok(h) || !device_ptr_ok(q_gate) || !device_ptr_ok(q_up) || !device_ptr_ok(x))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q_gate, q_up, x and h must be device pointers");
+  if (((uintptr_t)q_gate & 15u) || ((uintptr_t)q_up & 15u) || ((uintptr_t)x & 15u))
+    return fail(AXH_ERR_INVALID_ARGUMENT, "q_gate, q_up and x must be 16-byte aligned");
+  Q4kPlan p{};
+  axh_status s = plan_q5k_gate_up(n_rows, sb_per_row, variant, &p);
   if (s != AXH_OK) return s;
   if (p.lds > ctx->core->max_lds)
     return fail(AXH_ERR_PIPELINE_LAYOUT, "LDS tile exceeds the device limit");
@@ -1389,10 +1482,10 @@ static axh_status plan_q4_0_gate_up(uint32_t n_rows, uint32_t nb, const axh_q4_v
   if (!q4_0_octets_fit(n_rows, nb))
     return fail(AXH_ERR_INVALID_ARGUMENT,
                 "Q4_0 gate/up: rows of 2-1024 blocks, an even count, each matrix below 4 GiB");
-  if (gate_up_one_family(variant)) return plan_gate_up_one(true, n_rows, nb, variant, p);
+  if (gate_up_one_family(variant)) return plan_gate_up_one("q4_0", true, n_rows, nb, variant, p);
   axh_q4_variant one{};
   if (gate_up_default_one(variant, n_rows, (nb + 63u) / 64u, &one))
-    return plan_gate_up_one(true, n_rows, nb, &one, p);
+    return plan_gate_up_one("q4_0", true, n_rows, nb, &one, p);
   if (variant && variant->nontemporal == 1)
     return fail(AXH_ERR_INVALID_ARGUMENT, "Q4_0 gate/up: no non-temporal variant is compiled");
   const MatvecVariant dflt = q4_0_gate_up_default(n_rows, nb);
@@ -1889,6 +1982,9 @@ static axh_status bench_call(axh_context *ctx, const axh_bench_op *o, uint32_t i
   case AXH_BENCH_Q4_0_GATE_UP:
     return axh_q4_0_gate_up(ctx, q, q + o->q2_offset, static_cast<const float *>(o->x),
                             static_cast<float *>(o->y), o->n_rows, o->units, o->variant, nullptr);
+  case AXH_BENCH_Q5K_GATE_UP:
+    return axh_q5k_gate_up(ctx, q, q + o->q2_offset, static_cast<const float *>(o->x),
+                           static_cast<float *>(o->y), o->n_rows, o->units, o->variant, nullptr);
   case AXH_BENCH_Q4K_MATMUL_F16:
     return axh_q4k_matmul_f16(ctx, q, static_cast<const uint16_t *>(o->x),
                               static_cast<float *>(o->y), o->n_rows, o->units, o->batch,

@@ -62,7 +62,9 @@ WORKLOADS = {
     "down0": ("q4_0", 4096, 448, 0.5, "Llama-3-8B ffn_down as Q4_0, not a BASELINE config"),
     "head0": ("q4_0", 128256, 128, 1.0, "Llama-3-8B output head as Q4_0, not a BASELINE config"),
     "ffn0": ("gate_up0", 14336, 128, 0.5, "Llama-3-8B gate/up as Q4_0, not a BASELINE config"),
+    "ffn5": ("gate_up5", 14336, 16, 0.5, "Llama-3-8B gate/up as Q5_K, not a BASELINE config"),
 }
+GATE_UP_KINDS = ("gate_up", "gate_up0", "gate_up5")
 KQ_IDS = {"q5k": 13, "q6k": 14}
 
 
@@ -122,7 +124,8 @@ class Case:
         self.kind, self.rows, self.units, self.label = kind, rows, units, label
         self.ctx, self.O, self.np, self.pkg = ctx, O, np, pkg
         self.batch = batch if kind == "matmul" else 1
-        unit_bytes = {"q4_0": 18, "gate_up0": 18, "q5k": 176, "q6k": 210}.get(kind, 144)
+        unit_bytes = {"q4_0": 18, "gate_up0": 18, "q5k": 176, "gate_up5": 176,
+                      "q6k": 210}.get(kind, 144)
         self.cols = units * (32 if kind in ("q4_0", "gate_up0") else 256)
         self.weight_bytes = rows * units * unit_bytes
         seed = 20241 if name == "c4" else 30000 + rows + units
@@ -131,9 +134,10 @@ class Case:
             self.q = O.gen_q4_0_weights(seed, rows * units)
         elif kind in KQ_IDS:
             self.q = O.gen_kq_weights(KQ_IDS[kind], seed, rows * units)
-        elif kind in ("gate_up", "gate_up0"):
+        elif kind in GATE_UP_KINDS:
             # gate rows, then the up rows at the next COPY_ALIGN boundary
-            gen = O.gen_q4k_weights if kind == "gate_up" else O.gen_q4_0_weights
+            gen = {"gate_up": O.gen_q4k_weights, "gate_up0": O.gen_q4_0_weights,
+                   "gate_up5": lambda sd, n: O.gen_kq_weights(KQ_IDS["q5k"], sd, n)}[kind]
             self.qg = gen(seed, rows * units)
             self.qu = gen(seed + 7, rows * units)
             self.up_off = -(-self.weight_bytes // COPY_ALIGN) * COPY_ALIGN
@@ -183,6 +187,9 @@ class Case:
         elif self.kind == "gate_up0":
             self.ctx.q4_0_gate_up(w, w + self.up_off, self.dx, self.dy, self.rows, self.units,
                                   self.variant)
+        elif self.kind == "gate_up5":
+            self.ctx.q5k_gate_up(w, w + self.up_off, self.dx, self.dy, self.rows, self.units,
+                                 self.variant)
         elif self.x_f32:
             self.ctx.q4k_matmul_f32(w, self.dx, self.dx16, self.dy, self.rows, self.units,
                                     self.batch, self.variant)
@@ -193,7 +200,8 @@ class Case:
     def bench_op(self) -> dict:
         """Arguments of ctx.bench_loop for this workload (call i reads copy i)."""
         op = {"q4k": "q4k", "q4_0": "q4_0", "q5k": "q5k", "q6k": "q6k",
-              "gate_up": "gate_up", "gate_up0": "gate_up_q4_0"}.get(self.kind)
+              "gate_up": "gate_up", "gate_up0": "gate_up_q4_0",
+              "gate_up5": "gate_up_q5k"}.get(self.kind)
         if op is None:
             op = "matmul_f32" if self.x_f32 else "matmul_f16"
         return dict(op=op, q=self.wbuf, q_stride=self.stride, n_copies=self.n_copies, x=self.dx,
@@ -209,6 +217,8 @@ class Case:
             return self.pkg.q4k_gate_up_kernel_name(self.rows, self.units, self.variant)
         if self.kind == "gate_up0":
             return self.pkg.q4_0_gate_up_kernel_name(self.rows, self.units, self.variant)
+        if self.kind == "gate_up5":
+            return self.pkg.q5k_gate_up_kernel_name(self.rows, self.units, self.variant)
         if self.kind == "q5k":
             return self.pkg.q5k_matvec_kernel_name(self.rows, self.units, self.variant)
         if self.kind == "q6k":
@@ -240,8 +250,9 @@ class Case:
             rep = O.matvec_tolerance_report(y, ref, yf, ad, self.cols)
             return {k: rep[k] for k in ("ok", "rows_failed", "norm_rel_err",
                                         "gpu_err_vs_f64_norm", "cpu_err_vs_f64_norm")}
-        if self.kind in ("gate_up", "gate_up0"):
-            f64 = O.q4k_gate_up_f64 if self.kind == "gate_up" else O.q4_0_gate_up_f64
+        if self.kind in GATE_UP_KINDS:
+            f64 = {"gate_up": O.q4k_gate_up_f64, "gate_up0": O.q4_0_gate_up_f64,
+                   "gate_up5": lambda *a: O.kq_gate_up_f64(KQ_IDS["q5k"], *a)}[self.kind]
             _, g, ag, u, au = f64(self.qg, self.qu, self.x, self.rows, self.units)
             rep = O.gate_up_tolerance_report(y, g, ag, u, au, self.cols)
             return {k: rep[k] for k in ("ok", "rows_failed", "worst_over_bound", "norm_rel_err")}
@@ -274,9 +285,10 @@ class Case:
             many = lambda: O.kq_matvec(kid, self.q, self.x, self.rows, self.units,
                                        threads=threads)
             frac, what = 1.0, f"full {self.rows}x{self.cols} {self.kind.upper()} matvecs"
-        elif self.kind in ("gate_up", "gate_up0"):
-            mv = O.q4k_matvec if self.kind == "gate_up" else O.q4_0_matvec
-            fmt = "Q4_K" if self.kind == "gate_up" else "Q4_0"
+        elif self.kind in GATE_UP_KINDS:
+            mv = {"gate_up": O.q4k_matvec, "gate_up0": O.q4_0_matvec,
+                  "gate_up5": lambda *a, **k: O.kq_matvec(KQ_IDS["q5k"], *a, **k)}[self.kind]
+            fmt = {"gate_up": "Q4_K", "gate_up0": "Q4_0", "gate_up5": "Q5_K"}[self.kind]
 
             def two(threads):
                 g = mv(self.qg, self.x, self.rows, self.units, threads=threads)
@@ -521,7 +533,7 @@ def main() -> int:
                     "calls of the matvec and of each floor",
         }
     kernel = case.kernel()
-    shape = (("2x" if kind in ("gate_up", "gate_up0") else "") + f"{case.rows}x{case.cols}"
+    shape = (("2x" if kind in GATE_UP_KINDS else "") + f"{case.rows}x{case.cols}"
              + (f"xB{case.batch}" if kind == "matmul" else ""))
     traffic, traffic_src = profiled_traffic(kernel, shape)
 
@@ -549,8 +561,8 @@ def main() -> int:
         if kind == "matmul":
             metric = (f"Q4_K_M x f16 matmul weight-bytes HBM GB/s at {case.rows}x{case.cols}, "
                       f"B={case.batch}; us/call")
-        elif kind in ("gate_up", "gate_up0"):
-            fmt = "Q4_K_M" if kind == "gate_up" else "Q4_0"
+        elif kind in GATE_UP_KINDS:
+            fmt = {"gate_up": "Q4_K_M", "gate_up0": "Q4_0", "gate_up5": "Q5_K"}[kind]
             metric = (f"{fmt} fused gate+up (silu(g)*u) weight-bytes HBM GB/s at {shape}; "
                       "us/call")
         else:

@@ -364,6 +364,18 @@ axh_status axh_q4_0_gate_up(axh_context *ctx, const void *q_gate, const void *q_
                             const axh_q4_variant *variant, void *stream);
 axh_status axh_q4_0_gate_up_kernel_name(uint32_t n_rows, uint32_t blocks_per_row,
                                         const axh_q4_variant *variant, char *buf, size_t cap);
+/* The same fusion over two Q5_K matrices (n_rows rows of sb_per_row 176-byte
+ * superblocks; x holds sb_per_row * 256 f32): equals two axh_q5k_matvec calls
+ * followed by silu(g) * u.  No counterpart in the reference.  Limits: 1 <=
+ * sb_per_row <= 128, each matrix below 4 GiB, q_gate / q_up / x 16-byte
+ * aligned.  Holes as for axh_q4k_gate_up; with none set, the wave-paired
+ * one-pass kernel (x chunk by chunk) up to 12288 rows of up to 64
+ * superblocks, else the persistent kernel. */
+axh_status axh_q5k_gate_up(axh_context *ctx, const void *q_gate, const void *q_up,
+                           const float *x, float *h, uint32_t n_rows, uint32_t sb_per_row,
+                           const axh_q4_variant *variant, void *stream);
+axh_status axh_q5k_gate_up_kernel_name(uint32_t n_rows, uint32_t sb_per_row,
+                                       const axh_q4_variant *variant, char *buf, size_t cap);
 /* Decode-only kernels, bit-exact with the reference's CPU dequantisation
  * (common_helpers.rs:437-454; common.rs:229-253): w receives 256 (Q4_K) or
  * 32 (Q4_0) f32 per unit in the reference's element order. */
@@ -495,7 +507,7 @@ enum {
     AXH_BENCH_Q4K_MATMUL_F32 = 7, AXH_BENCH_READ_FLOOR = 8, AXH_BENCH_LAUNCH_EMPTY = 9,
     AXH_BENCH_READ_SHAPE = 10, /* axh_read_floor_shape: n_rows = workgroups, variant->
                                   waves_per_workgroup = threads / 64, variant->prefetch = loads */
-    AXH_BENCH_Q4_0_GATE_UP = 11
+    AXH_BENCH_Q4_0_GATE_UP = 11, AXH_BENCH_Q5K_GATE_UP = 12
 };
 typedef struct axh_bench_op {
     uint32_t op;                   /* AXH_BENCH_* */

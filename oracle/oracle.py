@@ -254,6 +254,13 @@ def q4_0_gate_up_f64(q_gate, q_up, x, n_rows: int, blocks_per_row: int):
     return silu(g) * u, g, ag, u, au
 
 
+def kq_gate_up_f64(kind: int, q_gate, q_up, x, n_rows: int, sb_per_row: int):
+    """The same for two Q5_K / Q6_K matrices (kq_matvec_f64 row dots)."""
+    g, ag = kq_matvec_f64(kind, q_gate, x, n_rows, sb_per_row)
+    u, au = kq_matvec_f64(kind, q_up, x, n_rows, sb_per_row)
+    return silu(g) * u, g, ag, u, au
+
+
 def gate_up_tolerance_report(h_gpu, g, ag, u, au, n_cols: int, rel_tol: float = 1e-3,
                              cancel_frac: float = 0.1) -> dict:
     """Acceptance for h = silu(g) * u when each dot product may carry the

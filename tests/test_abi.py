@@ -515,6 +515,36 @@ def test_q4_0_gate_up_selection(axc):
             name(*bad)
 
 
+def test_q5k_gate_up_selection(axc):
+    """Fused Q5_K gate/up: the wave-paired one-pass kernel (x chunk by chunk)
+    up to 12288 rows of up to 64 superblocks, else the persistent kernel (4
+    waves, x whole, prefetch 2; early refill past 64 superblocks); both
+    reachable through their holes."""
+    name, V = axc.q5k_gate_up_kernel_name, axc.Variant
+    co = axc.builtin_code_object()
+    assert name(1, 1) == "axh_q5k_gate_up_one_i1"
+    assert name(2048, 16) == name(14336 - 2048, 16) == "axh_q5k_gate_up_one_i2"
+    assert name(100, 64) == "axh_q5k_gate_up_one_i8"
+    assert name(12289, 16) == name(28672, 32) == "axh_q5k_gate_up_r1_w4_p2_x1"
+    assert name(28672, 64) == "axh_q5k_gate_up_r1_w4_p2_x2"
+    assert name(100, 65) == name(28672, 128) == "axh_q5k_gate_up_r1_w4_p1_x1"
+    assert name(14336, 16, V(1, 8, 1, 0)) == "axh_q5k_gate_up_r1_w8_p1_x1"
+    assert name(14336, 16, V(family=axc.FAMILY_ONE_PASS)) == "axh_q5k_gate_up_one_i2"
+    assert name(14336, 16, V(family=axc.FAMILY_ONE_PASS_X, sb_per_lane=5)) == \
+        "axh_q5k_gate_up_onex_i5"
+    for nit in range(1, 9):
+        assert f"axh_q5k_gate_up_one_i{nit}".encode() in co
+        assert f"axh_q5k_gate_up_onex_i{nit}".encode() in co
+    for k in ("r1_w4_p1_x1", "r1_w8_p1_x1", "r1_w4_p2_x1", "r1_w4_p2_x2"):
+        assert f"axh_q5k_gate_up_{k}".encode() in co
+    for bad in ((4, 0, None), (4, 129, None), (4, 16, V(1, 4, 3, 0)), (4, 16, V(family=1)),
+                (4, 16, V(family=2, sb_per_lane=9)), (4, 16, V(family=2, sb_per_lane=1)),
+                (4, 16, V(sb_per_lane=2)), (4, 70, V(1, 4, 2, 0)), (4, 65, V(family=2)),
+                (4, 16, V(0, 0, 0, 1))):
+        with pytest.raises(axc.DispatchError):
+            name(*bad)
+
+
 def test_q4_0_family_holes(axc):
     """The Q4_0 families and their holes: persistent (rows_per_wave,
     waves_per_workgroup, prefetch), one pass (sb_per_lane = steps of 64 blocks,

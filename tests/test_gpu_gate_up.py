@@ -280,3 +280,78 @@ def test_paired_one_pass_kernels(ctx, axc, rows, units, q40, fam, nit_extra):
         u = _matvec(ctx, qu, x, rows, units, mv)
     want = O.silu(g.astype(np.float64)) * u.astype(np.float64)
     assert np.all(np.abs(h - want) <= 4 * 2.0 ** -24 * np.abs(want) + 1e-30), name
+
+
+# ---- the fusion over two Q5_K matrices (one-pass kernels only) -------------------
+Q5 = O.GGML_Q5_K
+
+
+def _gate_up5(ctx, qg, qu, x, rows, sb, variant=None):
+    dg, du, dx, dh = _dev(ctx, qg), _dev(ctx, qu), _dev(ctx, x), ctx.alloc(rows * 4)
+    ctx.q5k_gate_up(dg, du, dx, dh, rows, sb, variant)
+    ctx.synchronize()
+    h = np.frombuffer(ctx.download(dh, rows * 4), dtype=np.float32).copy()
+    for b in (dg, du, dx, dh):
+        b.close()
+    return h
+
+
+def _matvec5(ctx, q, x, rows, sb, variant=None):
+    dq, dx, dy = _dev(ctx, q), _dev(ctx, x), ctx.alloc(rows * 4)
+    ctx.q5k_matvec(dq, dx, dy, rows, sb, variant)
+    ctx.synchronize()
+    y = np.frombuffer(ctx.download(dy, rows * 4), dtype=np.float32).copy()
+    for b in (dq, dx, dy):
+        b.close()
+    return y
+
+
+@pytest.mark.parametrize("rows,sb,fam,nit", [(12288, 16, 0, 2), (1, 1, 0, 1), (7, 3, 2, 1),
+                                             (1531, 24, 3, 3), (33, 64, 2, 8), (2049, 17, 3, 4),
+                                             (100, 40, 2, 5), (4097, 8, 3, 1)])
+def test_q5k_gate_up(ctx, axc, rows, sb, fam, nit):
+    """Q5_K gate/up through the one-pass kernels (family 0 = the default)
+    against the f64 oracle, and within 4 ulp of silu(g) * u of two Q5_K
+    one-pass matvecs with the same trip count (the same per-row
+    arithmetic)."""
+    qg = O.gen_kq_weights(Q5, rows * 5 + sb, rows * sb)
+    qu = O.gen_kq_weights(Q5, rows * 5 + sb + 1, rows * sb)
+    x = O.gen_normal_f32(rows + 3 * sb, sb * 256, 0.5)
+    v = axc.Variant(family=fam, sb_per_lane=nit) if fam else None
+    name = axc.q5k_gate_up_kernel_name(rows, sb, v)
+    _say(f"q5k gate_up {rows}x{sb} {name}")
+    h = _gate_up5(ctx, qg, qu, x, rows, sb, v)
+    _, g, ag, u, au = O.kq_gate_up_f64(Q5, qg, qu, x, rows, sb)
+    rep = O.gate_up_tolerance_report(h, g, ag, u, au, sb * 256, REL_TOL)
+    _say(f"q5k gate_up {rows}x{sb}: {rep}")
+    assert rep["ok"], rep
+    ffam = fam or (axc.FAMILY_ONE_PASS_X if "onex" in name else axc.FAMILY_ONE_PASS)
+    mv = axc.Variant(prefetch=1 if ffam == 2 else 0, family=axc.FAMILY_ONE_PASS,
+                     sb_per_lane=int(name.rsplit("_i", 1)[1]))
+    gm = _matvec5(ctx, qg, x, rows, sb, mv)
+    um = _matvec5(ctx, qu, x, rows, sb, mv)
+    want = O.silu(gm.astype(np.float64)) * um.astype(np.float64)
+    assert np.all(np.abs(h - want) <= 4 * 2.0 ** -24 * np.abs(want) + 1e-30), name
+
+
+@pytest.mark.parametrize("rows,sb,holes", [(12289, 16, None), (1531, 24, (1, 4, 1)),
+                                           (1531, 24, (1, 8, 1)), (1531, 24, (1, 4, 2)),
+                                           (333, 64, (1, 4, 2)), (257, 100, None),
+                                           (20011, 9, (1, 4, 1))])
+def test_q5k_gate_up_persistent(ctx, axc, rows, sb, holes):
+    """The persistent Q5_K gate/up (the default past 12288 rows or 64
+    superblocks; every compiled variant): x whole in one and two staged
+    sub-blocks per thread, early refill, more rows than the grid holds,
+    against the f64 oracle."""
+    v = axc.Variant(*holes, 0) if holes else None
+    name = axc.q5k_gate_up_kernel_name(rows, sb, v)
+    assert name.startswith("axh_q5k_gate_up_r"), name
+    _say(f"q5k gate_up persistent {rows}x{sb} {name}")
+    qg = O.gen_kq_weights(Q5, rows * 7 + sb, rows * sb)
+    qu = O.gen_kq_weights(Q5, rows * 7 + sb + 1, rows * sb)
+    x = O.gen_normal_f32(rows + 5 * sb, sb * 256, 0.5)
+    h = _gate_up5(ctx, qg, qu, x, rows, sb, v)
+    _, g, ag, u, au = O.kq_gate_up_f64(Q5, qg, qu, x, rows, sb)
+    rep = O.gate_up_tolerance_report(h, g, ag, u, au, sb * 256, REL_TOL)
+    _say(f"q5k gate_up persistent {rows}x{sb}: {rep}")
+    assert rep["ok"], rep
