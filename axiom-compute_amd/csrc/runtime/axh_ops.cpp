@@ -1295,7 +1295,9 @@ static MatvecVariant q4_0_flat_default(uint32_t n_rows, uint32_t nb) {
 //   whole for rows of 65-128 blocks from 6144 rows (8192 x 128 5.22 vs 5.53,
 //   14336 x 128 8.34 vs 8.71, 128256 x 128 49.7 vs 50.8; 4096 x 128 4.01 vs
 //   3.93), x two chunks ahead for 14-16 steps from 4096 rows (4096 x 1024
-//   15.9 vs 16.5, 8192 x 1024 31.3 vs 31.6);
+//   15.9 vs 16.5, 8192 x 1024 31.3 vs 31.6; below 14 steps it runs even:
+//   4096 x 14336 8.19 vs 8.21, 4096 x 12288 7.63 vs 7.39, 4096 x 26624 13.67
+//   vs 13.70);
 // - persistent for more than 16384 rows of more than 256 blocks (28672 x 448
 //   42.5 vs 44.1-44.7 one pass; 28672 x 256 25.3 vs 24.7 stays one pass).
 constexpr uint32_t kQ4_0ColsMaxRows = 512, kQ4_0FewRows = 32;
