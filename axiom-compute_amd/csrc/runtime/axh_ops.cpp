@@ -471,9 +471,21 @@ constexpr uint32_t kOnePMinIt = 4, kOnePMaxRows = 4096;
 // 14336 6.88 vs 4.98, 512 x 14336 6.90 vs 5.57, 512 x 28672 12.06 vs 8.61,
 // 1024 x 6144 4.00 vs 3.87, 1024 x 28672 12.13 vs 9.43 (and the autotuner's
 // re-timed winners: 1024 x 8192 -12 %, 1024 x 14336 -19 %, 512 x 8192 -13 %);
-// at 16 superblocks at most 6 % (128 rows), and from 2048 rows the one pass
-// is ahead (2048 x 8192 4.98 vs 5.14, 2048 x 28672 12.33 vs 16.91).
+// from 2048 rows the one pass is ahead (2048 x 8192 4.98 vs 5.14, 2048 x
+// 28672 12.33 vs 16.91).  Shorter rows pay on fewer rows: up to 512 rows from
+// 13 superblocks (512 x 3584 2.78 vs 3.02-3.15, 512 x 4096 2.84 vs 3.10-3.19,
+// 256 x 3584 2.75 vs 2.91, 512 x 5120 3.61 vs 3.78-3.90), 513-1024 rows from
+// 17 (1024 x 5120 3.88 vs 4.04-4.08; 1024 x 4096 3.25 vs 3.27-3.29 and 1024 x
+// 3584 even), and not below 13 (512 x 3072 3.19 vs 3.24-3.30, 512 x 2048
+// even).
 constexpr uint32_t kTiledFewMaxRows = 1024, kTiledFewMinSb = 24;
+constexpr uint32_t kTiledFewShortMaxRows = 512, kTiledFewShortMinSb = 13, kTiledFewMidMinSb = 17;
+
+static bool q4k_tiled_few(uint32_t n_rows, uint32_t nsb) {
+  if (n_rows > kTiledFewMaxRows) return false;
+  if (nsb >= kTiledFewMinSb) return true;
+  return nsb >= (n_rows <= kTiledFewShortMaxRows ? kTiledFewShortMinSb : kTiledFewMidMinSb);
+}
 
 static bool use_one_pass(uint32_t n_rows, uint32_t nsb) {
   if (nsb < 1 || nsb > kOneMaxSb || n_rows < kOneMinRows) return false;
@@ -507,7 +519,7 @@ static uint32_t q4k_default_family(uint32_t n_rows, uint32_t nsb, uint64_t q_byt
     return AXH_Q4K_FAMILY_SPLIT_K;
   if (n_rows < kQ4kColsMaxRows && nsb >= 1 && nsb <= kQ4kColsMaxSb) return AXH_Q4K_FAMILY_COLUMNS;
   if (use_one_pass(n_rows, nsb) && q_bytes < 0xFFFFFFFFull) {
-    if (n_rows <= kTiledFewMaxRows && nsb >= kTiledFewMinSb) return AXH_Q4K_FAMILY_TILED;
+    if (q4k_tiled_few(n_rows, nsb)) return AXH_Q4K_FAMILY_TILED;
     if (n_rows >= kOneWholeMinRows && nsb <= kOneWholeMaxSb) return AXH_Q4K_FAMILY_ONE_PASS_X;
     if (n_rows >= kOneMidMinRows && n_rows < kOneWholeMinRows && nsb <= kOneMidWholeMaxSb)
       return AXH_Q4K_FAMILY_ONE_PASS_X;

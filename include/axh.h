@@ -197,7 +197,8 @@ void axh_event_destroy(axh_event *ev);
  * Zero fields take the shape's choice.  family = 0 selects the persistent
  * family when any of its four holes is set, else the default family for the
  * shape: one workgroup for 1-4 long rows, split-K or column slices for fewer
- * than 32 rows, tiled for 32-1024 rows of 24-128 superblocks, one pass for
+ * than 32 rows, tiled for 32-512 rows of 13-128 superblocks and 513-1024
+ * rows of 17-128, one pass for
  * 32-32768 rows of 1-128 superblocks otherwise (and up to
  * 65536 rows of at most 16; x staged whole from 6144 rows of at most 32
  * superblocks and from 4097 rows of at most 24), except 4097-6143 rows of

@@ -119,10 +119,14 @@ def test_kernel_selection_by_shape_and_variant(axc):
     assert name(4096, 56) == "axh_q4k_matvec_onep_i7"
     assert name(2048, 33) == "axh_q4k_matvec_onep_i5"
     assert name(4096, 128) == "axh_q4k_matvec_onep_i16"
-    # up to 1024 rows of 24+ superblocks: the tiled kernel, one row per wave
+    # up to 1024 rows of 24+ superblocks (17+ from 513 rows, 13+ up to 512
+    # rows): the tiled kernel, one row per wave
     assert name(32, 33) == "axh_q4k_matvec_tiled_r1_w4_p2"
-    assert name(1024, 24) == "axh_q4k_matvec_tiled_r1_w4_p2"
-    assert name(1024, 23) == "axh_q4k_matvec_one_i3"
+    assert name(1024, 24) == name(1024, 17) == "axh_q4k_matvec_tiled_r1_w4_p2"
+    assert name(512, 13) == name(32, 13) == "axh_q4k_matvec_tiled_r1_w4_p2"
+    assert name(1024, 16) == name(513, 16) == "axh_q4k_matvec_one_i2"
+    assert name(512, 12) == "axh_q4k_matvec_one_i2"
+    assert name(1025, 23) == "axh_q4k_matvec_one_i3"
     assert name(1025, 24) == "axh_q4k_matvec_one_i3"
     assert name(4097, 56) == "axh_q4k_matvec_one_i7"
     assert name(4096, 32) == "axh_q4k_matvec_onep_i4"

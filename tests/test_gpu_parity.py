@@ -356,10 +356,12 @@ def test_q4k_one_pass_shapes(ctx, axc, rows, sb):
 
 
 @pytest.mark.parametrize("rows,sb", [(32, 24), (33, 40), (100, 56), (777, 24), (1000, 127),
-                                     (1024, 128), (64, 113)])
+                                     (1024, 128), (64, 113), (512, 14), (32, 13), (999, 17),
+                                     (257, 20)])
 def test_q4k_tiled_default_on_few_long_rows(ctx, axc, rows, sb):
-    """32..1024 rows of 24..128 superblocks default to the tiled kernel with
-    one row per wave: odd row counts, partial last workgroups and tiles."""
+    """32..1024 rows of 24..128 superblocks (17+ from 513 rows, 13+ up to 512)
+    default to the tiled kernel with one row per wave: odd row counts, partial
+    last workgroups and tiles."""
     assert axc.q4k_matvec_kernel_name(rows, sb) == "axh_q4k_matvec_tiled_r1_w4_p2"
     _say(f"q4k tiled default {rows}x{sb}")
     q = O.gen_q4k_weights(rows * 41 + sb, rows * sb)
