@@ -240,8 +240,17 @@ constexpr uint32_t kOneMidMinRows = 4097, kOneMidWholeMaxSb = 24;
 // pass is ahead (37.38 vs 42.37).
 constexpr uint32_t kLongMinSb = 74, kLongMaxRows = 8191;
 
+// 24576-32768 rows of 25-32 superblocks too (A/B in one run, us per call,
+// persistent r1 w4 p1 against x staged whole: 28672 x 8192 26.18 vs 27.48,
+// 32768 x 8192 29.48 vs 31.56, 28672 x 7168 25.21 vs 26.30; even at 16384 x
+// 8192, 16.72 vs 16.87 for x whole, and 20480 x 8192, 20.73 vs 20.86).
+constexpr uint32_t kTallPersistMinRows = 24576, kTallPersistMaxRows = 32768;
+
 static bool q4k_mid_band_persistent(uint32_t n_rows, uint32_t nsb) {
   if (n_rows >= kOneMidMinRows && n_rows <= kLongMaxRows && nsb >= kLongMinSb) return true;
+  if (n_rows >= kTallPersistMinRows && n_rows <= kTallPersistMaxRows && nsb > kOneMidWholeMaxSb &&
+      nsb <= kOneWholeMaxSb)
+    return true;
   return n_rows >= kOneMidMinRows && n_rows < kOneWholeMinRows && nsb > kOneMidWholeMaxSb &&
          nsb <= kOneWholeMaxSb;
 }
@@ -520,10 +529,10 @@ static uint32_t q4k_default_family(uint32_t n_rows, uint32_t nsb, uint64_t q_byt
   if (n_rows < kQ4kColsMaxRows && nsb >= 1 && nsb <= kQ4kColsMaxSb) return AXH_Q4K_FAMILY_COLUMNS;
   if (use_one_pass(n_rows, nsb) && q_bytes < 0xFFFFFFFFull) {
     if (q4k_tiled_few(n_rows, nsb)) return AXH_Q4K_FAMILY_TILED;
+    if (q4k_mid_band_persistent(n_rows, nsb)) return AXH_Q4K_FAMILY_PERSISTENT;
     if (n_rows >= kOneWholeMinRows && nsb <= kOneWholeMaxSb) return AXH_Q4K_FAMILY_ONE_PASS_X;
     if (n_rows >= kOneMidMinRows && n_rows < kOneWholeMinRows && nsb <= kOneMidWholeMaxSb)
       return AXH_Q4K_FAMILY_ONE_PASS_X;
-    if (q4k_mid_band_persistent(n_rows, nsb)) return AXH_Q4K_FAMILY_PERSISTENT;
     return AXH_Q4K_FAMILY_ONE_PASS;
   }
   return AXH_Q4K_FAMILY_PERSISTENT; // falls back to tiled for rows it cannot stage

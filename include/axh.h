@@ -201,9 +201,9 @@ void axh_event_destroy(axh_event *ev);
  * rows of 17-128, one pass for
  * 32-32768 rows of 1-128 superblocks otherwise (and up to
  * 65536 rows of at most 16; x staged whole from 6144 rows of at most 32
- * superblocks and from 4097 rows of at most 24), except 4097-6143 rows of
- * 25-32 superblocks and 4097-8191 rows of 74 or more, which take the
- * persistent family; persistent beyond,
+ * superblocks and from 4097 rows of at most 24), except 4097-6143 and
+ * 24576-32768 rows of 25-32 superblocks and 4097-8191 rows of 74 or more,
+ * which take the persistent family; persistent beyond,
  * tiled for rows of more than 128 superblocks.  Every default is a hole
  * assignment.  The gate/up operations
  * take the persistent holes, or their one-pass families (see axh_q4k_gate_up).

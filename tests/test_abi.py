@@ -127,6 +127,11 @@ def test_kernel_selection_by_shape_and_variant(axc):
     assert name(1024, 16) == name(513, 16) == "axh_q4k_matvec_one_i2"
     assert name(512, 12) == "axh_q4k_matvec_one_i2"
     assert name(1025, 23) == "axh_q4k_matvec_one_i3"
+    # 24576-32768 rows of 25-32 superblocks: the persistent kernel, 4 waves
+    assert name(24576, 25) == name(32768, 32) == "axh_q4k_matvec_flat_r1_w4_p1_n0"
+    assert name(24575, 32) == "axh_q4k_matvec_onex_i4"
+    assert name(28672, 24) == "axh_q4k_matvec_onex_i3"
+    assert name(32769, 32) == "axh_q4k_matvec_flat_r2_w4_p1_n0"
     assert name(1025, 24) == "axh_q4k_matvec_one_i3"
     assert name(4097, 56) == "axh_q4k_matvec_one_i7"
     assert name(4096, 32) == "axh_q4k_matvec_onep_i4"

@@ -370,6 +370,18 @@ def test_q4k_tiled_default_on_few_long_rows(ctx, axc, rows, sb):
     _check_q4k(y, q, x, rows, sb, f"q4k tiled default {rows}x{sb}")
 
 
+@pytest.mark.parametrize("rows,sb", [(24576, 25), (28673, 32)])
+def test_q4k_tall_persistent_default(ctx, axc, rows, sb):
+    """24576-32768 rows of 25-32 superblocks default to the persistent kernel
+    with 4 waves and early refill (an odd row count: a half-empty last pair)."""
+    assert axc.q4k_matvec_kernel_name(rows, sb) == "axh_q4k_matvec_flat_r1_w4_p1_n0"
+    _say(f"q4k tall persistent default {rows}x{sb}")
+    q = O.gen_q4k_weights(rows + 29 * sb, rows * sb)
+    x = O.gen_normal_f32(rows + 31 * sb, sb * 256)
+    y = _run_q4k(ctx, q, x, rows, sb)
+    _check_q4k(y, q, x, rows, sb, f"q4k tall persistent {rows}x{sb}")
+
+
 @pytest.mark.parametrize("rows,sb,xd", [(32, 17, 2), (33, 24, 2), (4096, 25, 2), (4095, 56, 2),
                                         (4096, 56, 1), (2047, 128, 2), (100, 113, 2),
                                         (5000, 40, 2), (4096, 40, 1), (64, 121, 2)])
