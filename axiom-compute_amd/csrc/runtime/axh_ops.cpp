@@ -1304,12 +1304,15 @@ static MatvecVariant q4_0_flat_default(uint32_t n_rows, uint32_t nb) {
 // Default Q4_0 family per shape, from A/B runs (interleaved launch loops, us
 // per call, rotated weights; the LDS-tiled kernel's figures are its best row
 // count):
-// - at most 512 rows of at most 128 blocks: the column kernel, ahead in the
-//   kernel trace (256 x 128 blocks 2.79 us against 3.50 tiled and 3.64 one
-//   pass) and over 1000 sustained calls (2.88 vs 3.01 and 3.16), though not
-//   in 20-call loops (3.55 vs 3.01 and 3.04);
-// - fewer than 32 rows otherwise: tiled (16 x 1024 blocks 11.4 vs 12.3 one
-//   pass, 8 x 344 4.90 vs 4.91);
+// - fewer than 32 rows: the column kernel for rows of at most 128 blocks
+//   (31 x 128 2.73 vs 2.71 tiled), else tiled (16 x 1024 blocks 11.4 vs 12.3
+//   one pass, 8 x 344 4.90 vs 4.91);
+// - 32-512 rows of at most 128 blocks: tiled, one row per wave, ahead of the
+//   column kernel per call in loops of every length (interleaved in one run:
+//   256 x 128 blocks 3.11 vs 3.32 us over 1000 calls, 3.08 vs 4.07 over 100,
+//   3.32 vs 3.81 over 20; 512 x 112 3.11 vs 3.34 over 1000) and of the one
+//   pass (3.26 over 1000), though the column kernel's dispatches are shorter
+//   in the kernel trace (2.76 against 3.48 us);
 // - one pass from 32 rows (the Q4_K one-pass kernel over octets): 4096 x 448
 //   8.1 vs 13.7 tiled, 14336 x 448 24.0 vs 40.8, 4096 x 128 3.9 vs 4.7 tiled
 //   and 6.0 column, 1024 x 1024 13.5 vs 14.0, 256 x 160 3.8 vs 4.3; x staged
@@ -1321,14 +1324,16 @@ static MatvecVariant q4_0_flat_default(uint32_t n_rows, uint32_t nb) {
 //   vs 13.70);
 // - persistent for more than 16384 rows of more than 256 blocks (28672 x 448
 //   42.5 vs 44.1-44.7 one pass; 28672 x 256 25.3 vs 24.7 stays one pass).
-constexpr uint32_t kQ4_0ColsMaxRows = 512, kQ4_0FewRows = 32;
+constexpr uint32_t kQ4_0TiledShortMaxRows = 512, kQ4_0TiledShortMaxB = 128, kQ4_0FewRows = 32;
 constexpr uint32_t kQ4_0OneXMinRows = 6144;
 constexpr uint32_t kQ4_0OnePMinIt = 14, kQ4_0OnePMinRows = 4096;
 constexpr uint32_t kQ4_0FlatMinRows = 16385, kQ4_0FlatMinB = 257;
 
 static uint32_t q4_0_default_family(uint32_t n_rows, uint32_t nb) {
-  if (n_rows <= kQ4_0ColsMaxRows && q4_0_cols_fit(n_rows, nb)) return AXH_Q4K_FAMILY_COLUMNS;
-  if (n_rows < kQ4_0FewRows || !q4_0_octets_fit(n_rows, nb)) return AXH_Q4K_FAMILY_TILED;
+  if (n_rows < kQ4_0FewRows)
+    return q4_0_cols_fit(n_rows, nb) ? AXH_Q4K_FAMILY_COLUMNS : AXH_Q4K_FAMILY_TILED;
+  if (n_rows <= kQ4_0TiledShortMaxRows && nb <= kQ4_0TiledShortMaxB) return AXH_Q4K_FAMILY_TILED;
+  if (!q4_0_octets_fit(n_rows, nb)) return AXH_Q4K_FAMILY_TILED;
   if (n_rows >= kQ4_0FlatMinRows && nb >= kQ4_0FlatMinB) return AXH_Q4K_FAMILY_PERSISTENT;
   if ((nb + 63u) / 64u == 2u && n_rows >= kQ4_0OneXMinRows) return AXH_Q4K_FAMILY_ONE_PASS_X;
   return AXH_Q4K_FAMILY_ONE_PASS;

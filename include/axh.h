@@ -216,8 +216,9 @@ void axh_event_destroy(axh_event *ev);
  * of 2-128 blocks) and TILED (axh_q4_0_matvec_r*_w*: rows_per_wave,
  * waves_per_workgroup; also what family 0 with a hole set selects).  The
  * octet families take rows of an even block count up to 1024 blocks, below
- * 4 GiB.  With no hole set: columns for up to 512 rows of up to 128 blocks,
- * tiled for fewer than 32 rows, odd block counts and longer rows, persistent
+ * 4 GiB.  With no hole set: columns for fewer than 32 rows of up to 128
+ * blocks, tiled for other rows below 32, for 32-512 rows of up to 128 blocks,
+ * odd block counts and rows of more than 1024 blocks, persistent
  * for more than 16384 rows of more than 256 blocks, else one pass (x whole
  * for rows of 65-128 blocks from 6144 rows, x two chunks ahead for 14-16 steps
  * from 4096 rows).

@@ -218,8 +218,9 @@ def test_q4_0_matvec_every_variant(ctx, axc):
 @pytest.mark.parametrize("rows,nb", [(1, 1), (2, 3), (3, 127), (4, 129), (5, 1025), (17, 2048),
                                      (1, 2), (3, 2), (7, 64), (33, 126), (2049, 128), (100, 10)])
 def test_q4_0_matvec_edge_shapes(ctx, rows, nb):
-    """Odd block counts and long rows (LDS-staged kernel); even counts up to
-    128 blocks (column kernel: idle lanes, one block pair, many rows)."""
+    """Odd block counts and long rows (LDS-tiled kernel); even counts up to
+    128 blocks on fewer than 32 rows (column kernel: idle lanes, one block
+    pair) and on more rows (tiled, one pass)."""
     _say(f"q4_0 edge {rows}x{nb}")
     q = O.gen_q4_0_weights(rows * 13 + nb, rows * nb)
     x = O.gen_normal_f32(rows + nb, nb * 32)

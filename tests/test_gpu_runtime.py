@@ -206,10 +206,11 @@ def test_graph_replays_match_eager_results(ctx, axc):
     outs = ((y1, rows * 4), (y2, rows * 4), (y3, rows * batch * 4), (y4, krows * 4), (y5, 4),
             (y6, rows0b * 4), (y7, rows * 4), (y8, rows * 4))
     persistent = axc.Variant(family=axc.FAMILY_PERSISTENT)
+    columns = axc.Variant(family=axc.FAMILY_COLUMNS)
 
     def ops():
         ctx.q4k_matvec(bufs["q"], bufs["x"], y1, rows, sb)
-        ctx.q4_0_matvec(bufs["q0"], bufs["x0"], y2, rows, nb)
+        ctx.q4_0_matvec(bufs["q0"], bufs["x0"], y2, rows, nb, columns)
         ctx.q4k_matmul(bufs["q"], bufs["xh"], y3, rows, sb, batch)
         ctx.q4k_matvec(bufs["qk"], bufs["xk"], y4, krows, ksb)
         ctx.q4k_matvec(bufs["qk"], bufs["xk"], y5, 1, ksb)
