@@ -281,9 +281,16 @@ static MatvecVariant q4_0_default(uint32_t n_rows, uint32_t nb) {
   return {4, 4, 1, 2, 1};
 }
 
-// Rows below this count (with at most kQ4kColsMaxSb superblocks) go to the
-// register-resident column-slice kernel, which splits each row across the
-// workgroup's waves; it wins where a call is latency-bound (few rows).
+// The register-resident column-slice kernel (family COLUMNS) splits each of
+// up to kQ4kColsMaxSb superblocks across the workgroup's waves.  Fewer than
+// kQ4kColsMaxRows rows of at most kQ4kColsMaxSb superblocks (the one-workgroup
+// kernel's shapes aside) default to the tiled kernel, one row per wave: per
+// call, interleaved in one run, 8 x 4096 3.32 vs 4.84 us for the column
+// kernel, 31 x 4096 2.65 vs 4.13, 3 x 4096 3.31 vs 4.97, 8 x 14336 4.35 vs
+// 6.13, 31 x 14336 4.44 vs 6.15, 24 x 8192 3.44 vs 5.17; and against split-K
+// on 64-128 superblocks 16 x 32768 7.28 vs 9.64, 12 x 25600 6.36 vs 9.08, 31 x
+// 16384 4.61 vs 13.66 (8 x 32768 7.26 vs 7.27).  Split-K keeps the longer
+// rows (8 x 65536 9.42 vs 14.65 tiled, 16 x 51200 10.58 vs 12.00).
 constexpr uint32_t kQ4kColsMaxRows = 32;
 constexpr uint32_t kQ4kColsMaxSb = 128; // 4 * 128 lanes = 8 waves
 constexpr uint32_t kQ4kColsRb = 4;      // rows per batch of the compiled cols kernels
@@ -292,7 +299,7 @@ constexpr uint32_t kQ4kColsRb = 4;      // rows per batch of the compiled cols k
 // reduced by the last workgroup through a per-stream workspace (counter and
 // partials).  Every workgroup's device-scope release writes back its XCD's
 // L2, so the split stays at 4..16 workgroups.
-constexpr uint32_t kSkMinSb = 64;  // shorter rows stay on the cols kernel
+constexpr uint32_t kSkMinSb = 64;  // the split-K kernel's shortest rows (on request)
 constexpr uint32_t kSkMaxSb = 256; // longer rows: more workgroups than pay
 constexpr uint32_t kSkSpw = 16;    // superblocks per workgroup
 constexpr uint32_t kSkMaxGroups = kSkMaxSb / kSkSpw;
@@ -524,9 +531,10 @@ static bool q4k_persistent_holes(const axh_q4_variant *v) {
 // The default family for a shape (the sweeps quoted above each kernel).
 static uint32_t q4k_default_family(uint32_t n_rows, uint32_t nsb, uint64_t q_bytes) {
   if (q4k_use_wg(n_rows, nsb)) return AXH_Q4K_FAMILY_WORKGROUP;
-  if (n_rows < kQ4kColsMaxRows && nsb >= kSkMinSb && nsb <= kSkMaxSb && q_bytes < 0xFFFFFF00ull)
+  if (n_rows < kQ4kColsMaxRows && nsb > kQ4kColsMaxSb && nsb <= kSkMaxSb &&
+      q_bytes < 0xFFFFFF00ull)
     return AXH_Q4K_FAMILY_SPLIT_K;
-  if (n_rows < kQ4kColsMaxRows && nsb >= 1 && nsb <= kQ4kColsMaxSb) return AXH_Q4K_FAMILY_COLUMNS;
+  if (n_rows < kQ4kColsMaxRows && nsb >= 1 && nsb <= kQ4kColsMaxSb) return AXH_Q4K_FAMILY_TILED;
   if (use_one_pass(n_rows, nsb) && q_bytes < 0xFFFFFFFFull) {
     if (q4k_tiled_few(n_rows, nsb)) return AXH_Q4K_FAMILY_TILED;
     if (q4k_mid_band_persistent(n_rows, nsb)) return AXH_Q4K_FAMILY_PERSISTENT;

@@ -196,8 +196,8 @@ void axh_event_destroy(axh_event *ev);
  *   tiled: rows_per_wave, waves_per_workgroup, prefetch.
  * Zero fields take the shape's choice.  family = 0 selects the persistent
  * family when any of its four holes is set, else the default family for the
- * shape: one workgroup for 1-4 long rows, split-K or column slices for fewer
- * than 32 rows, tiled for 32-512 rows of 13-128 superblocks and 513-1024
+ * shape: one workgroup for 1-4 long rows, split-K for fewer than 32 rows of
+ * 129-256 superblocks, tiled for fewer than 32 rows otherwise and for 32-512 rows of 13-128 superblocks and 513-1024
  * rows of 17-128, one pass for
  * 32-32768 rows of 1-128 superblocks otherwise (and up to
  * 65536 rows of at most 16; x staged whole from 6144 rows of at most 32
@@ -429,7 +429,7 @@ axh_status axh_f32_to_f16(axh_context *ctx, const float *x, uint16_t *h, uint64_
  * resubmitting it.  Launch each operation once before capturing it (its
  * kernel is then prepared and cached).  No event, copy or synchronisation
  * call may be made on the context stream while capturing.  A graph that holds
- * a split-K matvec (fewer than 32 rows of 64-256 superblocks) uses the
+ * a split-K matvec (by default fewer than 32 rows of 129-256 superblocks) uses the
  * context stream's workspace and replays only on the context stream: another
  * stream gets AXH_ERR_INVALID_ARGUMENT. */
 typedef struct axh_graph axh_graph;

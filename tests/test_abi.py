@@ -176,18 +176,17 @@ def test_kernel_selection_by_shape_and_variant(axc):
     # two staged x sub-blocks per thread when one is not enough
     assert name(4096, 56, axc.Variant(2, 4, 2, 2)) == "axh_q4k_matvec_flat_r2_w4_p2_n0_x2"
     assert name(4096, 16, axc.Variant(2, 4, 2, 2)) == "axh_q4k_matvec_flat_r2_w4_p2_n0"
-    # few rows: one workgroup for 1-4 long rows, split-K or the column kernel otherwise
+    # few rows: one workgroup for 1-4 long rows, split-K past 128 superblocks,
+    # the tiled kernel otherwise
     assert name(1, 128) == "axh_q4k_matvec_wg_w8_x2_r1"
     assert name(2, 33) == "axh_q4k_matvec_wg_w8_x2_r2"
     assert name(3, 64) == "axh_q4k_matvec_wg_w8_x2_r4"
     assert name(4, 128) == "axh_q4k_matvec_wg_w8_x2_r4"
-    assert name(4, 63) == "axh_q4k_matvec_cols_r4_w4_n0_x1"
-    assert name(5, 128) == "axh_q4k_matvec_sk_s16"
-    assert name(31, 64) == "axh_q4k_matvec_sk_s16"
-    assert name(1, 32) == "axh_q4k_matvec_cols_r4_w2_n0_x1"
-    assert name(8, 63) == "axh_q4k_matvec_cols_r4_w4_n0_x1"
-    assert name(8, 56) == "axh_q4k_matvec_cols_r4_w4_n0_x1"
-    assert name(31, 1) == "axh_q4k_matvec_cols_r4_w1_n0_x1"
+    assert name(5, 129) == name(31, 256) == "axh_q4k_matvec_sk_s16"
+    for rows, sb in ((4, 63), (5, 128), (31, 64), (1, 32), (8, 63), (8, 56), (31, 1)):
+        assert name(rows, sb) == "axh_q4k_matvec_tiled_r1_w4_p2", (rows, sb)
+    assert name(8, 56, axc.Variant(family=axc.FAMILY_COLUMNS)) == "axh_q4k_matvec_cols_r4_w4_n0_x1"
+    assert name(31, 1, axc.Variant(family=axc.FAMILY_COLUMNS)) == "axh_q4k_matvec_cols_r4_w1_n0_x1"
     assert name(32, 1) == "axh_q4k_matvec_one_i1"
     co = axc.builtin_code_object()
     for rows in (1, 31, 64):

@@ -468,18 +468,21 @@ def test_q4k_one_workgroup_shapes(ctx, axc, rows, sb):
 @pytest.mark.parametrize("rows,sb", [(5, 64), (5, 65), (8, 128), (31, 128), (2, 255),
                                      (1, 256), (31, 200), (4, 129)])
 def test_q4k_split_k_shapes(ctx, axc, rows, sb):
-    """Few rows of 64..256 superblocks the one-workgroup kernel does not take
-    go to the split-K kernel: ragged last slices, the 16-workgroup limit, and
-    row counts up to 31."""
-    assert axc.q4k_matvec_kernel_name(rows, sb).startswith("axh_q4k_matvec_sk_")
+    """The split-K kernel (the default for fewer than 32 rows of 129-256
+    superblocks the one-workgroup kernel does not take; requested here):
+    ragged last slices, the 16-workgroup limit, and row counts up to 31."""
+    v = axc.Variant(family=axc.FAMILY_SPLIT_K)
+    assert axc.q4k_matvec_kernel_name(rows, sb, v).startswith("axh_q4k_matvec_sk_")
+    if sb > 128:
+        assert axc.q4k_matvec_kernel_name(rows, sb).startswith("axh_q4k_matvec_sk_")
     _say(f"q4k split-K {rows}x{sb}")
     q = O.gen_q4k_weights(rows * 17 + sb, rows * sb)
     x = O.gen_normal_f32(rows + 3 * sb, sb * 256)
-    y = _run_q4k(ctx, q, x, rows, sb)
+    y = _run_q4k(ctx, q, x, rows, sb, v)
     _check_q4k(y, q, x, rows, sb, f"q4k split-K {rows}x{sb}")
 
 
-def test_q4k_split_k_back_to_back_calls_reset_the_counter(ctx):
+def test_q4k_split_k_back_to_back_calls_reset_the_counter(ctx, axc):
     """Consecutive split-K calls with different grids on one stream, without
     synchronising in between: each must see a zero counter (the last
     workgroup of the previous call resets it)."""
@@ -491,9 +494,10 @@ def test_q4k_split_k_back_to_back_calls_reset_the_counter(ctx):
         dq, dx, dy = _to_dev(ctx, q), _to_dev(ctx, x), ctx.alloc(rows * 4)
         cases.append((rows, sb, q, x, dq, dx, dy))
     _say("split-K back-to-back")
+    sk = axc.Variant(family=axc.FAMILY_SPLIT_K)
     for _ in range(3):
         for rows, sb, q, x, dq, dx, dy in cases:
-            ctx.q4k_matvec(dq, dx, dy, rows, sb)
+            ctx.q4k_matvec(dq, dx, dy, rows, sb, sk)
     ctx.synchronize()
     for rows, sb, q, x, dq, dx, dy in cases:
         y = np.frombuffer(ctx.download(dy, rows * 4), dtype=np.float32).copy()

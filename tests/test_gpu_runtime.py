@@ -207,18 +207,19 @@ def test_graph_replays_match_eager_results(ctx, axc):
             (y6, rows0b * 4), (y7, rows * 4), (y8, rows * 4))
     persistent = axc.Variant(family=axc.FAMILY_PERSISTENT)
     columns = axc.Variant(family=axc.FAMILY_COLUMNS)
+    split_k = axc.Variant(family=axc.FAMILY_SPLIT_K)
 
     def ops():
         ctx.q4k_matvec(bufs["q"], bufs["x"], y1, rows, sb)
         ctx.q4_0_matvec(bufs["q0"], bufs["x0"], y2, rows, nb, columns)
         ctx.q4k_matmul(bufs["q"], bufs["xh"], y3, rows, sb, batch)
-        ctx.q4k_matvec(bufs["qk"], bufs["xk"], y4, krows, ksb)
+        ctx.q4k_matvec(bufs["qk"], bufs["xk"], y4, krows, ksb, split_k)
         ctx.q4k_matvec(bufs["qk"], bufs["xk"], y5, 1, ksb)
         ctx.q4_0_matvec(bufs["q0b"], bufs["x0"], y6, rows0b, nb)
         ctx.q4_0_gate_up(bufs["q0"], bufs["q0b"], bufs["x0"], y7, rows, nb)
         ctx.q4_0_matvec(bufs["q0"], bufs["x0"], y8, rows, nb, persistent)
 
-    assert axc.q4k_matvec_kernel_name(krows, ksb).startswith("axh_q4k_matvec_sk_")
+    assert axc.q4k_matvec_kernel_name(krows, ksb, split_k).startswith("axh_q4k_matvec_sk_")
     assert axc.q4_0_matvec_kernel_name(rows0b, nb) == "axh_q4_0_matvec_one_i2"
     assert axc.q4k_matvec_kernel_name(1, ksb).startswith("axh_q4k_matvec_wg_")
     ops()  # eager (also prepares every kernel and the workspace before capture)
@@ -230,7 +231,7 @@ def test_graph_replays_match_eager_results(ctx, axc):
         for b, n in outs:
             ctx.upload(b, np.full(n // 4, np.nan, dtype=np.float32))  # poison between replays
         ctx.q4k_matvec(bufs["q"], bufs["x"], y1, rows, sb)  # eager work between replays
-        ctx.q4k_matvec(bufs["qk"], bufs["xk"], y4, krows, ksb)
+        ctx.q4k_matvec(bufs["qk"], bufs["xk"], y4, krows, ksb, split_k)
         ctx.synchronize()
         g.launch()
         ctx.synchronize()

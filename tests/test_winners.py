@@ -43,8 +43,8 @@ def test_family_defaults_by_shape(axc):
     F = axc
     fam = lambda r, s: axc.q4k_matvec_default_variant(r, s).family
     assert fam(1, 128) == F.FAMILY_WORKGROUP
-    assert fam(5, 128) == F.FAMILY_SPLIT_K
-    assert fam(5, 16) == F.FAMILY_COLUMNS
+    assert fam(5, 129) == F.FAMILY_SPLIT_K
+    assert fam(5, 128) == fam(5, 16) == F.FAMILY_TILED
     assert fam(4096, 56) == F.FAMILY_ONE_PASS
     assert fam(14336, 16) == F.FAMILY_ONE_PASS_X
     assert fam(128256, 16) == F.FAMILY_PERSISTENT
