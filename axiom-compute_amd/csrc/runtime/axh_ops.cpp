@@ -1312,9 +1312,12 @@ static MatvecVariant q4_0_flat_default(uint32_t n_rows, uint32_t nb) {
 // Default Q4_0 family per shape, from A/B runs (interleaved launch loops, us
 // per call, rotated weights; the LDS-tiled kernel's figures are its best row
 // count):
-// - fewer than 32 rows: the column kernel for rows of at most 128 blocks
-//   (31 x 128 2.73 vs 2.71 tiled), else tiled (16 x 1024 blocks 11.4 vs 12.3
-//   one pass, 8 x 344 4.90 vs 4.91);
+// - fewer than 32 rows: tiled, one row per wave, ahead of the column kernel
+//   on every shape it takes (interleaved in one run: 1 x 128 blocks 3.33 vs
+//   4.21, 3 x 128 3.31 vs 3.91, 8 x 128 2.59 vs 2.71, 16 x 128 3.30 vs 3.87,
+//   31 x 128 3.21 vs 3.93, 31 x 32 3.16 vs 3.79, 8 x 16 3.24 vs 4.08, 24 x 100
+//   3.18 vs 3.97) and of the one pass on longer rows (16 x 1024 blocks 11.4
+//   vs 12.3, 8 x 344 4.90 vs 4.91);
 // - 32-512 rows of at most 128 blocks: tiled, one row per wave, ahead of the
 //   column kernel per call in loops of every length (interleaved in one run:
 //   256 x 128 blocks 3.11 vs 3.32 us over 1000 calls, 3.08 vs 4.07 over 100,
@@ -1338,8 +1341,7 @@ constexpr uint32_t kQ4_0OnePMinIt = 14, kQ4_0OnePMinRows = 4096;
 constexpr uint32_t kQ4_0FlatMinRows = 16385, kQ4_0FlatMinB = 257;
 
 static uint32_t q4_0_default_family(uint32_t n_rows, uint32_t nb) {
-  if (n_rows < kQ4_0FewRows)
-    return q4_0_cols_fit(n_rows, nb) ? AXH_Q4K_FAMILY_COLUMNS : AXH_Q4K_FAMILY_TILED;
+  if (n_rows < kQ4_0FewRows) return AXH_Q4K_FAMILY_TILED;
   if (n_rows <= kQ4_0TiledShortMaxRows && nb <= kQ4_0TiledShortMaxB) return AXH_Q4K_FAMILY_TILED;
   if (!q4_0_octets_fit(n_rows, nb)) return AXH_Q4K_FAMILY_TILED;
   if (n_rows >= kQ4_0FlatMinRows && nb >= kQ4_0FlatMinB) return AXH_Q4K_FAMILY_PERSISTENT;

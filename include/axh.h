@@ -197,8 +197,8 @@ void axh_event_destroy(axh_event *ev);
  * Zero fields take the shape's choice.  family = 0 selects the persistent
  * family when any of its four holes is set, else the default family for the
  * shape: one workgroup for 1-4 long rows, split-K for fewer than 32 rows of
- * 129-256 superblocks, tiled for fewer than 32 rows otherwise and for 32-512 rows of 13-128 superblocks and 513-1024
- * rows of 17-128, one pass for
+ * 129-256 superblocks, tiled for fewer than 32 rows otherwise and for 32-512
+ * rows of 13-128 superblocks and 513-1024 rows of 17-128, one pass for
  * 32-32768 rows of 1-128 superblocks otherwise (and up to
  * 65536 rows of at most 16; x staged whole from 6144 rows of at most 32
  * superblocks and from 4097 rows of at most 24), except 4097-6143 and
@@ -216,8 +216,8 @@ void axh_event_destroy(axh_event *ev);
  * of 2-128 blocks) and TILED (axh_q4_0_matvec_r*_w*: rows_per_wave,
  * waves_per_workgroup; also what family 0 with a hole set selects).  The
  * octet families take rows of an even block count up to 1024 blocks, below
- * 4 GiB.  With no hole set: columns for fewer than 32 rows of up to 128
- * blocks, tiled for other rows below 32, for 32-512 rows of up to 128 blocks,
+ * 4 GiB.  With no hole set: tiled for fewer than 32 rows, for 32-512 rows of
+ * up to 128 blocks,
  * odd block counts and rows of more than 1024 blocks, persistent
  * for more than 16384 rows of more than 256 blocks, else one pass (x whole
  * for rows of 65-128 blocks from 6144 rows, x two chunks ahead for 14-16 steps

@@ -228,6 +228,21 @@ def test_q4_0_matvec_edge_shapes(ctx, rows, nb):
     _check_q4_0(y, q, x, rows, nb, f"q4_0 edge {rows}x{nb}")
 
 
+@pytest.mark.parametrize("rows,nb", [(1, 2), (3, 2), (7, 64), (31, 128), (100, 10), (33, 126),
+                                     (2049, 128)])
+def test_q4_0_column_kernel(ctx, axc, rows, nb):
+    """The column kernel (on request; rows of an even block count up to 128):
+    one block pair per lane, one row and several, within the oracle's
+    tolerance."""
+    v = axc.Variant(family=axc.FAMILY_COLUMNS)
+    assert axc.q4_0_matvec_kernel_name(rows, nb, v) == "axh_q4_0_matvec_cols_r1"
+    _say(f"q4_0 columns {rows}x{nb}")
+    q = O.gen_q4_0_weights(rows * 11 + nb, rows * nb)
+    x = O.gen_normal_f32(rows + 2 * nb, nb * 32)
+    y = _run_q4_0(ctx, q, x, rows, nb, v)
+    _check_q4_0(y, q, x, rows, nb, f"q4_0 columns {rows}x{nb}")
+
+
 def _q4_0_octet_variants(axc, rows, nb):
     """Every octet-kernel variant that takes this shape: each compiled
     persistent variant, one pass with x one and two chunks ahead, with x whole,
@@ -275,7 +290,8 @@ def test_q4_0_octet_kernels_bit_exact(ctx, axc, rows, nb):
 @pytest.mark.parametrize("rows,nb,kernel", [(4096, 448, "one_i7"), (6144, 128, "onex_i2"),
                                             (16385, 258, "flat_r1_w8_p1_x1"),
                                             (4096, 1024, "onep_i16"), (513, 128, "one_i2"),
-                                            (14336, 127, "r4_w4"), (20, 1024, "r1_w4")])
+                                            (14336, 127, "r4_w4"), (20, 1024, "r1_w4"),
+                                            (31, 128, "r1_w4"), (1, 2, "r1_w4")])
 def test_q4_0_defaults_by_shape(ctx, axc, rows, nb, kernel):
     """The default Q4_0 kernel of each shape band (one pass, x whole, x two
     chunks ahead, persistent, LDS-tiled for odd and few rows) against the
