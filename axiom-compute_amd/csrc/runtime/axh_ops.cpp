@@ -1324,6 +1324,12 @@ static MatvecVariant q4_0_flat_default(uint32_t n_rows, uint32_t nb) {
 //   3.32 vs 3.81 over 20; 512 x 112 3.11 vs 3.34 over 1000) and of the one
 //   pass (3.26 over 1000), though the column kernel's dispatches are shorter
 //   in the kernel trace (2.76 against 3.48 us);
+// - 32-256 rows of 193-256 blocks (four one-pass steps): tiled, ahead of the
+//   one pass and of the one pass with x two chunks ahead (32 x 256 3.96 vs
+//   4.33, 128 x 256 4.04 vs 4.39, 256 x 256 4.09 vs 4.67 and 4.77, 256 x 224
+//   4.00 vs 4.60, 256 x 200 3.94 vs 5.12, 128 x 240 4.00 vs 4.37); even at 256
+//   x 192 (3.85 vs 3.86), 384 x 256 and 512 x 224, behind from 1024 rows
+//   (2048 x 256 5.87 vs 4.96) and at 256 x 320 (5.95 vs 5.40);
 // - one pass from 32 rows (the Q4_K one-pass kernel over octets): 4096 x 448
 //   8.1 vs 13.7 tiled, 14336 x 448 24.0 vs 40.8, 4096 x 128 3.9 vs 4.7 tiled
 //   and 6.0 column, 1024 x 1024 13.5 vs 14.0, 256 x 160 3.8 vs 4.3; x staged
@@ -1336,6 +1342,7 @@ static MatvecVariant q4_0_flat_default(uint32_t n_rows, uint32_t nb) {
 // - persistent for more than 16384 rows of more than 256 blocks (28672 x 448
 //   42.5 vs 44.1-44.7 one pass; 28672 x 256 25.3 vs 24.7 stays one pass).
 constexpr uint32_t kQ4_0TiledShortMaxRows = 512, kQ4_0TiledShortMaxB = 128, kQ4_0FewRows = 32;
+constexpr uint32_t kQ4_0TiledMidMaxRows = 256, kQ4_0TiledMidMinB = 193, kQ4_0TiledMidMaxB = 256;
 constexpr uint32_t kQ4_0OneXMinRows = 6144;
 constexpr uint32_t kQ4_0OnePMinIt = 14, kQ4_0OnePMinRows = 4096;
 constexpr uint32_t kQ4_0FlatMinRows = 16385, kQ4_0FlatMinB = 257;
@@ -1343,6 +1350,8 @@ constexpr uint32_t kQ4_0FlatMinRows = 16385, kQ4_0FlatMinB = 257;
 static uint32_t q4_0_default_family(uint32_t n_rows, uint32_t nb) {
   if (n_rows < kQ4_0FewRows) return AXH_Q4K_FAMILY_TILED;
   if (n_rows <= kQ4_0TiledShortMaxRows && nb <= kQ4_0TiledShortMaxB) return AXH_Q4K_FAMILY_TILED;
+  if (n_rows <= kQ4_0TiledMidMaxRows && nb >= kQ4_0TiledMidMinB && nb <= kQ4_0TiledMidMaxB)
+    return AXH_Q4K_FAMILY_TILED;
   if (!q4_0_octets_fit(n_rows, nb)) return AXH_Q4K_FAMILY_TILED;
   if (n_rows >= kQ4_0FlatMinRows && nb >= kQ4_0FlatMinB) return AXH_Q4K_FAMILY_PERSISTENT;
   if ((nb + 63u) / 64u == 2u && n_rows >= kQ4_0OneXMinRows) return AXH_Q4K_FAMILY_ONE_PASS_X;

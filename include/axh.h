@@ -217,7 +217,7 @@ void axh_event_destroy(axh_event *ev);
  * waves_per_workgroup; also what family 0 with a hole set selects).  The
  * octet families take rows of an even block count up to 1024 blocks, below
  * 4 GiB.  With no hole set: tiled for fewer than 32 rows, for 32-512 rows of
- * up to 128 blocks,
+ * up to 128 blocks and 32-256 rows of 193-256 blocks,
  * odd block counts and rows of more than 1024 blocks, persistent
  * for more than 16384 rows of more than 256 blocks, else one pass (x whole
  * for rows of 65-128 blocks from 6144 rows, x two chunks ahead for 14-16 steps

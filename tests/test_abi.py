@@ -461,13 +461,18 @@ def test_q6k_one_pass_family(axc):
 
 def test_q4_0_kernel_selection(axc):
     """Q4_0 defaults: fewer than 32 rows, 32-512 rows of at most 128 blocks,
-    odd block counts and rows of more than 1024 blocks take the LDS-tiled
-    kernel (the column kernel only on request); otherwise the one-pass kernel over octets of 8 blocks (x
-    whole for 65-128 blocks from 6144 rows, x two chunks ahead for 14-16 steps
+    32-256 rows of 193-256 blocks, odd block counts and rows of more than 1024
+    blocks take the LDS-tiled kernel (the column kernel only on request);
+    otherwise the one-pass kernel over octets of 8 blocks (x whole for 65-128 blocks from 6144 rows, x two chunks ahead for 14-16 steps
     from 4096 rows), persistent for more than 16384 rows of more than 256
     blocks."""
     name = axc.q4_0_matvec_kernel_name
     assert name(1, 2) == name(31, 128) == name(8, 16) == "axh_q4_0_matvec_r1_w4"
+    # 32-256 rows of 193-256 blocks
+    assert name(32, 193) == name(256, 256) == name(100, 200) == "axh_q4_0_matvec_r1_w4"
+    assert name(257, 256) == "axh_q4_0_matvec_one_i4"
+    assert name(256, 192) == "axh_q4_0_matvec_one_i3"
+    assert name(256, 258) == "axh_q4_0_matvec_one_i5"
     cols = axc.Variant(family=axc.FAMILY_COLUMNS)
     assert name(1, 2, cols) == name(31, 128, cols) == "axh_q4_0_matvec_cols_r1"
     assert name(256, 128) == name(512, 128) == name(300, 2) == name(32, 128) == \
