@@ -1318,12 +1318,14 @@ static MatvecVariant q4_0_flat_default(uint32_t n_rows, uint32_t nb) {
 //   31 x 128 3.21 vs 3.93, 31 x 32 3.16 vs 3.79, 8 x 16 3.24 vs 4.08, 24 x 100
 //   3.18 vs 3.97) and of the one pass on longer rows (16 x 1024 blocks 11.4
 //   vs 12.3, 8 x 344 4.90 vs 4.91);
-// - 32-512 rows of at most 128 blocks: tiled, one row per wave, ahead of the
-//   column kernel per call in loops of every length (interleaved in one run:
-//   256 x 128 blocks 3.11 vs 3.32 us over 1000 calls, 3.08 vs 4.07 over 100,
-//   3.32 vs 3.81 over 20; 512 x 112 3.11 vs 3.34 over 1000) and of the one
-//   pass (3.26 over 1000), though the column kernel's dispatches are shorter
-//   in the kernel trace (2.76 against 3.48 us);
+// - 32-1024 rows of at most 128 blocks: tiled, one row per wave, ahead of
+//   the column kernel per call in loops of every length (interleaved in one
+//   run: 256 x 128 blocks 3.11 vs 3.32 us over 1000 calls, 3.08 vs 4.07 over
+//   100, 3.32 vs 3.81 over 20; 512 x 112 3.11 vs 3.34 over 1000) and of the
+//   one pass (3.26 over 1000; 640 x 112 2.90 vs 3.08, 1024 x 128 3.22 vs
+//   3.36, 1024 x 96 3.27 vs 3.39, 513 x 128 3.21 vs 3.24, 1024 x 64 3.10 vs
+//   3.15; 2048 x 128 3.88 vs 3.69 stays one pass), though the column kernel's
+//   dispatches are shorter in the kernel trace (2.76 against 3.48 us);
 // - 32-256 rows of 193-256 blocks (four one-pass steps): tiled, ahead of the
 //   one pass and of the one pass with x two chunks ahead (32 x 256 3.96 vs
 //   4.33, 128 x 256 4.04 vs 4.39, 256 x 256 4.09 vs 4.67 and 4.77, 256 x 224
@@ -1341,7 +1343,7 @@ static MatvecVariant q4_0_flat_default(uint32_t n_rows, uint32_t nb) {
 //   vs 13.70);
 // - persistent for more than 16384 rows of more than 256 blocks (28672 x 448
 //   42.5 vs 44.1-44.7 one pass; 28672 x 256 25.3 vs 24.7 stays one pass).
-constexpr uint32_t kQ4_0TiledShortMaxRows = 512, kQ4_0TiledShortMaxB = 128, kQ4_0FewRows = 32;
+constexpr uint32_t kQ4_0TiledShortMaxRows = 1024, kQ4_0TiledShortMaxB = 128, kQ4_0FewRows = 32;
 constexpr uint32_t kQ4_0TiledMidMaxRows = 256, kQ4_0TiledMidMinB = 193, kQ4_0TiledMidMaxB = 256;
 constexpr uint32_t kQ4_0OneXMinRows = 6144;
 constexpr uint32_t kQ4_0OnePMinIt = 14, kQ4_0OnePMinRows = 4096;

@@ -216,7 +216,7 @@ void axh_event_destroy(axh_event *ev);
  * of 2-128 blocks) and TILED (axh_q4_0_matvec_r*_w*: rows_per_wave,
  * waves_per_workgroup; also what family 0 with a hole set selects).  The
  * octet families take rows of an even block count up to 1024 blocks, below
- * 4 GiB.  With no hole set: tiled for fewer than 32 rows, for 32-512 rows of
+ * 4 GiB.  With no hole set: tiled for fewer than 32 rows, for 32-1024 rows of
  * up to 128 blocks and 32-256 rows of 193-256 blocks,
  * odd block counts and rows of more than 1024 blocks, persistent
  * for more than 16384 rows of more than 256 blocks, else one pass (x whole

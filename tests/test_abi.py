@@ -460,7 +460,7 @@ def test_q6k_one_pass_family(axc):
 
 
 def test_q4_0_kernel_selection(axc):
-    """Q4_0 defaults: fewer than 32 rows, 32-512 rows of at most 128 blocks,
+    """Q4_0 defaults: fewer than 32 rows, 32-1024 rows of at most 128 blocks,
     32-256 rows of 193-256 blocks, odd block counts and rows of more than 1024
     blocks take the LDS-tiled kernel (the column kernel only on request);
     otherwise the one-pass kernel over octets of 8 blocks (x whole for 65-128 blocks from 6144 rows, x two chunks ahead for 14-16 steps
@@ -479,7 +479,8 @@ def test_q4_0_kernel_selection(axc):
         "axh_q4_0_matvec_r1_w4"
     assert name(31, 130) == "axh_q4_0_matvec_r1_w4"
     assert name(512, 130) == "axh_q4_0_matvec_one_i3"
-    assert name(513, 128) == "axh_q4_0_matvec_one_i2"
+    assert name(1024, 128) == name(513, 128) == "axh_q4_0_matvec_r1_w4"
+    assert name(1025, 128) == "axh_q4_0_matvec_one_i2"
     assert name(4096, 2) == "axh_q4_0_matvec_one_i1"
     assert name(256, 130) == "axh_q4_0_matvec_one_i3"
     assert name(32, 448) == "axh_q4_0_matvec_one_i7"

@@ -289,7 +289,7 @@ def test_q4_0_octet_kernels_bit_exact(ctx, axc, rows, nb):
 
 @pytest.mark.parametrize("rows,nb,kernel", [(4096, 448, "one_i7"), (6144, 128, "onex_i2"),
                                             (16385, 258, "flat_r1_w8_p1_x1"),
-                                            (4096, 1024, "onep_i16"), (513, 128, "one_i2"),
+                                            (4096, 1024, "onep_i16"), (1025, 128, "one_i2"),
                                             (14336, 127, "r4_w4"), (20, 1024, "r1_w4"),
                                             (31, 128, "r1_w4"), (1, 2, "r1_w4"),
                                             (200, 224, "r1_w4"), (257, 224, "one_i4")])

@@ -193,7 +193,7 @@ def test_graph_replays_match_eager_results(ctx, axc):
     ksb, krows = 128, 5
     qk = O.gen_q4k_weights(86, krows * ksb)
     xk = O.gen_normal_f32(87, ksb * 256)
-    rows0b = 600  # Q4_0 past 512 rows: the one-pass kernel
+    rows0b = 1100  # Q4_0 past 1024 rows: the one-pass kernel
     q0b = O.gen_q4_0_weights(88, rows0b * nb)
     bufs = {}
     for name, arr in (("q", q), ("x", x), ("q0", q0), ("x0", x0), ("xh", xh), ("qk", qk),
