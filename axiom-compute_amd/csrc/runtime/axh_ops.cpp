@@ -1086,17 +1086,21 @@ static MatvecVariant kq_default(const KqFormat &f, uint32_t n_rows, uint32_t nsb
   return {1, nw, early ? 1u : 2u, 2, 1};
 }
 
-// Q5_K rows of up to 16 superblocks over 2048 to 32768 rows take the
+// Q5_K rows of up to 16 superblocks over 768 to 32768 rows take the
 // one-pass kernel (axh_q5k_matvec_one_i{NIT}: one workgroup per 16 rows, x
 // staged chunk by chunk, fully unrolled).  A/B in one run, 14336 x 4096:
 // 10.02-10.08 vs 10.56-10.70 us (plain launches, one weight copy per call
 // from 14 rotated copies), 10.71 vs 11.05 on another box, and 10.79-10.88 vs
 // 10.92-10.96 through the library's launch loop on a third, and even in the
 // kernel trace on a fourth (10.85-10.90 vs 10.84-10.88); 4096 x 4096 4.60 vs
-// 4.70.  Not below 2048 rows (1024 x 4096: 3.95 vs 3.49) nor for
-// longer rows (4096 x 14336: even).  The family is also reachable as
+// 4.70; from 768 rows in two repetitions
+// in one run: 768 x 4096 3.88 / 4.01 vs 4.15 / 4.30, 1024 x 4096 4.11 / 4.13
+// vs 4.30 / 4.53, 1024 x 2048 3.19 / 3.18 vs 4.14 / 4.09, 1536 x 4096 4.10 /
+// 4.14 vs 4.35 / 4.28, 1900 x 4096 4.25 / 4.19 vs 4.53 / 4.55 (an earlier box
+// had 1024 x 4096 at 3.95 vs 3.49); not below (512 x 4096 3.72 vs 3.57, 256
+// x 4096 3.57 vs 3.36) nor for longer rows (4096 x 14336: even).  The family is also reachable as
 // variant->family = AXH_Q4K_FAMILY_ONE_PASS (hole: sb_per_lane, 1 or 2).
-constexpr uint32_t kQ5OneMinRows = 2048, kQ5OneMaxRows = 32768, kKqOneMaxSb = 16;
+constexpr uint32_t kQ5OneMinRows = 768, kQ5OneMaxRows = 32768, kKqOneMaxSb = 16;
 constexpr uint32_t kKqOneMaxIt = 8; // one-pass kernels compiled for 1-8 steps
 
 // Q6_K rows of up to 16 superblocks over 256 to 4096 rows (at most one

@@ -226,7 +226,7 @@ void axh_event_destroy(axh_event *ev);
  * AXH_Q4K_FAMILY_ONE_PASS with sb_per_lane 1-8 (rows of up to 64
  * superblocks) and prefetch (x one or two chunks ahead, two from three
  * steps); with no hole set they run one pass for rows of up to 16
- * superblocks over 2048-32768 rows (Q5_K) or 256-4096 rows (Q6_K), and for
+ * superblocks over 768-32768 rows (Q5_K) or 256-4096 rows (Q6_K), and for
  * 2049-4096 rows of up to 64 superblocks (Q5_K) or 2049-8192 rows of up to 40
  * (Q6_K), else the persistent family (4 waves with x staged whole for up to
  * 2048 rows of 17-64 superblocks and for 14336 rows and more of 33-64). */

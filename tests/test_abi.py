@@ -381,15 +381,16 @@ def test_kquant_kernel_selection(axc):
 
 
 def test_q5k_one_pass_family(axc):
-    """Q5_K rows of up to 16 superblocks over 2048-32768 rows take the
+    """Q5_K rows of up to 16 superblocks over 768-32768 rows take the
     one-pass kernel by default; the family is reachable by request (hole:
     sb_per_lane 1 or 2) and is Q5_K's only family."""
     co = axc.builtin_code_object()
     name, V, one = axc.q5k_matvec_kernel_name, axc.Variant, axc.FAMILY_ONE_PASS
     assert name(14336, 16) == "axh_q5k_matvec_one_i2"
     assert name(4096, 16) == "axh_q5k_matvec_one_i2"
-    assert name(2048, 8) == "axh_q5k_matvec_one_i1"
-    for rows, sb in ((1024, 16), (32769, 16), (2048, 17), (4097, 17), (4096, 65), (8192, 56)):
+    assert name(2048, 8) == name(768, 8) == "axh_q5k_matvec_one_i1"
+    assert name(1024, 16) == "axh_q5k_matvec_one_i2"
+    for rows, sb in ((767, 16), (32769, 16), (2048, 17), (4097, 17), (4096, 65), (8192, 56)):
         assert name(rows, sb).startswith("axh_q5k_matvec_flat_"), (rows, sb)
     # 2049-4096 rows of 17-64 superblocks: one pass too
     assert name(2049, 17) == "axh_q5k_matvec_one_i3"
@@ -440,11 +441,12 @@ def test_q6k_one_pass_family(axc):
     assert name(1025, 32) == "axh_q6k_matvec_flat_r1_w4_p2_x1"
     assert name(1024, 33) == "axh_q6k_matvec_flat_r1_w4_p2_x2"
     assert name(1024, 65) == "axh_q6k_matvec_flat_r1_w8_p2_x2"
-    # Q5_K: the same up to 1024 rows of up to 32 superblocks
+    # Q5_K: the same up to 1024 rows of up to 32 superblocks (below 768 rows
+    # of up to 16: the one pass takes 768 rows on)
     q5 = axc.q5k_matvec_kernel_name
-    assert q5(1024, 16) == "axh_q5k_matvec_flat_r1_w4_p2_x1"
+    assert q5(767, 16) == "axh_q5k_matvec_flat_r1_w4_p2_x1"
     assert q5(1024, 32) == "axh_q5k_matvec_flat_r1_w4_p2_x1"
-    assert q5(1025, 16) == "axh_q5k_matvec_flat_r1_w4_p1_x1"
+    assert q5(1025, 32) == "axh_q5k_matvec_flat_r1_w4_p2_x1"
     assert q5(4096, 16) == "axh_q5k_matvec_one_i2"
     assert name(7, 3, V(0, 0, 0, 0, one, 0)) == "axh_q6k_matvec_one_i1"
     assert name(7, 3, V(0, 0, 0, 0, one, 2)) == "axh_q6k_matvec_one_i2"

@@ -136,7 +136,7 @@ def _flat_for(axc, sb):
                                             (33, 64, 8, 1), (50, 40, 5, 2), (4095, 56, 7, 2),
                                             (9, 24, 4, 2)])
 def test_q5k_one_pass_family(ctx, axc, rows, sb, nit, xd):
-    """The Q5_K one-pass kernel (the default for 2048-32768 rows of up to 16
+    """The Q5_K one-pass kernel (the default for 768-32768 rows of up to 16
     superblocks and 2049-4096 rows of up to 64) at ragged row counts, trip
     counts 1-8 (one past the row's too), x one or two chunks ahead, requested
     explicitly: within the oracle's tolerance, and bit for bit the persistent
